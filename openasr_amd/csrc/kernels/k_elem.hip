@@ -1,0 +1,461 @@
+// k_elem.hip -- the small ops of the decoder step that keep the whole graph
+// on device (nn/decoder.rs:1850-2145 for the LLM block, whisper
+// ggml_decoder_graph.rs:3869-5392 for the seq2seq block): broadcast binary
+// ops, scale, unary activations, RMSNorm / LayerNorm (optionally fused with
+// the following weight multiply and bias add), RoPE, set_rows into the f16
+// KV cache, get_rows from quantized tables, strided copies, soft_max_ext and
+// argmax. All are HBM- or latency-bound; each is one pass over its data.
+#include "../mi355x_common.h"
+#include "../ops.h"
+
+namespace mi355x {
+
+__device__ __forceinline__ int64_t offs4(const tview & t, int64_t i0, int64_t i1, int64_t i2, int64_t i3) {
+    return i0 * t.nb[0] + i1 * t.nb[1] + i2 * t.nb[2] + i3 * t.nb[3];
+}
+
+__device__ __forceinline__ void unravel(int64_t idx, const int64_t * ne, int64_t & i0, int64_t & i1, int64_t & i2,
+                                        int64_t & i3) {
+    i0 = idx % ne[0];
+    idx /= ne[0];
+    i1 = idx % ne[1];
+    idx /= ne[1];
+    i2 = idx % ne[2];
+    i3 = idx / ne[2];
+}
+
+// ------------------------------------------------------------- binary ----
+
+template <int OP>
+__device__ __forceinline__ float bin_apply(float x, float y) {
+    if (OP == 0) return x + y;
+    if (OP == 1) return x - y;
+    if (OP == 2) return x * y;
+    return x / y;
+}
+
+template <int OP>
+__global__ void k_binary(tview d, tview a, tview b, int64_t n) {
+    for (int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(idx, d.ne, i0, i1, i2, i3);
+        const float x = *(const float *) (a.data + offs4(a, i0, i1, i2, i3));
+        const float y = *(const float *) (b.data + offs4(b, i0 % b.ne[0], i1 % b.ne[1], i2 % b.ne[2], i3 % b.ne[3]));
+        *(float *) (d.data + offs4(d, i0, i1, i2, i3)) = bin_apply<OP>(x, y);
+    }
+}
+
+static unsigned grid_for(int64_t n, int threads, int n_cu) {
+    int64_t blocks = (n + threads - 1) / threads;
+    const int64_t cap = (int64_t) n_cu * 16;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    return (unsigned) blocks;
+}
+
+void launch_binary(int op, const tview & d, const tview & a, const tview & b, hipStream_t s, int n_cu) {
+    const int64_t n = d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3];
+    const unsigned g = grid_for(n, 256, n_cu);
+    switch (op) {
+        case GGML_OP_ADD: hipLaunchKernelGGL(k_binary<0>, dim3(g), dim3(256), 0, s, d, a, b, n); break;
+        case GGML_OP_SUB: hipLaunchKernelGGL(k_binary<1>, dim3(g), dim3(256), 0, s, d, a, b, n); break;
+        case GGML_OP_MUL: hipLaunchKernelGGL(k_binary<2>, dim3(g), dim3(256), 0, s, d, a, b, n); break;
+        default: hipLaunchKernelGGL(k_binary<3>, dim3(g), dim3(256), 0, s, d, a, b, n); break;
+    }
+}
+
+// -------------------------------------------------------- scale / unary --
+
+__global__ void k_scale(tview d, tview a, float sc, float bias, int64_t n) {
+    for (int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(idx, d.ne, i0, i1, i2, i3);
+        const float x = *(const float *) (a.data + offs4(a, i0, i1, i2, i3));
+        *(float *) (d.data + offs4(d, i0, i1, i2, i3)) = x * sc + bias;
+    }
+}
+
+void launch_scale(const tview & d, const tview & a, float sc, float bias, hipStream_t s, int n_cu) {
+    const int64_t n = d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3];
+    hipLaunchKernelGGL(k_scale, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, a, sc, bias, n);
+}
+
+// ggml's gelu goes through a 64K-entry f16 table indexed by the f16 bits of
+// x (ggml_vec_gelu_f32); the table is built on the host with the same libm
+// tanhf and uploaded once, so device and host agree bit for bit.
+__device__ __forceinline__ float unary_apply(int op, float x, const uint16_t * gelu_table) {
+    switch (op) {
+        case GGML_UNARY_OP_SILU: return x / (1.0f + expf(-x));
+        case GGML_UNARY_OP_GELU: {
+            if (x <= -10.0f) return 0.0f;
+            if (x >= 10.0f) return x;
+            return half_bits_to_float(gelu_table[float_to_half_bits(x)]);
+        }
+        case GGML_UNARY_OP_GELU_ERF: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+        case GGML_UNARY_OP_RELU: return x > 0.0f ? x : 0.0f;
+        case GGML_UNARY_OP_TANH: return tanhf(x);
+        case GGML_UNARY_OP_SIGMOID: return 1.0f / (1.0f + expf(-x));
+        case GGML_UNARY_OP_EXP: return expf(x);
+        case GGML_UNARY_OP_NEG: return -x;
+        case GGML_UNARY_OP_ABS: return fabsf(x);
+        default: return x;
+    }
+}
+
+__global__ void k_unary(tview d, tview a, int op, const uint16_t * gelu_table, int64_t n) {
+    for (int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(idx, d.ne, i0, i1, i2, i3);
+        const float x = *(const float *) (a.data + offs4(a, i0, i1, i2, i3));
+        *(float *) (d.data + offs4(d, i0, i1, i2, i3)) = unary_apply(op, x, gelu_table);
+    }
+}
+
+void launch_unary(const tview & d, const tview & a, int op, const uint16_t * gelu_table, hipStream_t s, int n_cu) {
+    const int64_t n = d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3];
+    hipLaunchKernelGGL(k_unary, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, a, op, gelu_table, n);
+}
+
+// SwiGLU tail fused: d = silu(g) * u (the gate activation and gate multiply
+// of nn/ffn.rs:64-91), one pass instead of two.
+__global__ void k_silu_mul(tview d, tview g, tview u, int64_t n) {
+    for (int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(idx, d.ne, i0, i1, i2, i3);
+        const float x = *(const float *) (g.data + offs4(g, i0, i1, i2, i3));
+        const float y = *(const float *) (u.data + offs4(u, i0 % u.ne[0], i1 % u.ne[1], i2 % u.ne[2], i3 % u.ne[3]));
+        *(float *) (d.data + offs4(d, i0, i1, i2, i3)) = (x / (1.0f + expf(-x))) * y;
+    }
+}
+
+void launch_silu_mul(const tview & d, const tview & g, const tview & u, hipStream_t s, int n_cu) {
+    const int64_t n = d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3];
+    hipLaunchKernelGGL(k_silu_mul, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, g, u, n);
+}
+
+// ------------------------------------------------------------- norms -----
+
+// One wave per row. mode 0: RMSNorm, 1: LayerNorm. Optional fused weight
+// multiply (w broadcast over rows) and bias add, matching the
+// rms_norm->mul and norm->mul->add sequences of nn/norm.rs:10-56.
+__global__ __launch_bounds__(256) void k_norm(tview d, tview a, int mode, float eps, tview w, int has_w, tview bias,
+                                              int has_b, int64_t rows) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
+    const float * x = (const float *) (a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3]);
+    float * y = (float *) (d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]);
+    const int64_t n = a.ne[0];
+    float mean = 0.0f;
+    if (mode == 1) {
+        float s = 0.0f;
+        for (int64_t i = lane; i < n; i += 64) s += x[i];
+        mean = wave_sum(s) / (float) n;
+    }
+    float s2 = 0.0f;
+    for (int64_t i = lane; i < n; i += 64) {
+        const float v = x[i] - mean;
+        s2 += v * v;
+    }
+    const float var = wave_sum(s2) / (float) n;
+    const float scale = 1.0f / sqrtf(var + eps);
+    const float * wr = has_w ? (const float *) (w.data + (i1 % w.ne[1]) * w.nb[1] + (i2 % w.ne[2]) * w.nb[2] +
+                                                (i3 % w.ne[3]) * w.nb[3])
+                             : nullptr;
+    const float * br = has_b ? (const float *) (bias.data + (i1 % bias.ne[1]) * bias.nb[1] +
+                                                (i2 % bias.ne[2]) * bias.nb[2] + (i3 % bias.ne[3]) * bias.nb[3])
+                             : nullptr;
+    for (int64_t i = lane; i < n; i += 64) {
+        float v = (x[i] - mean) * scale;
+        if (has_w) v *= wr[i % w.ne[0]];
+        if (has_b) v += br[i % bias.ne[0]];
+        y[i] = v;
+    }
+}
+
+void launch_norm(const tview & d, const tview & a, int mode, float eps, const tview * w, const tview * b,
+                 hipStream_t s) {
+    const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    tview none{};
+    hipLaunchKernelGGL(k_norm, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, s, d, a, mode, eps, w ? *w : none,
+                       w ? 1 : 0, b ? *b : none, b ? 1 : 0, rows);
+}
+
+// -------------------------------------------------------------- rope -----
+
+// ggml_rope_cache_init with ext_factor 0: theta_i = p * theta_scale^i built by
+// repeated f32 multiplication, cos/sin scaled by attn_factor. NEOX rotates
+// (x[i], x[i + n_dims/2]); NORMAL rotates (x[2i], x[2i+1]). Dims past n_dims
+// pass through. One thread per rotated pair.
+__global__ void k_rope(tview d, tview a, const int32_t * pos, int n_dims, int mode, float theta_scale,
+                       float freq_scale, float attn_factor, int64_t n_pairs) {
+    const int64_t half = n_dims / 2;
+    for (int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; idx < n_pairs;
+         idx += (int64_t) gridDim.x * blockDim.x) {
+        const int64_t ic = idx % half;
+        int64_t r = idx / half;
+        const int64_t i1 = r % a.ne[1];
+        r /= a.ne[1];
+        const int64_t i2 = r % a.ne[2];
+        const int64_t i3 = r / a.ne[2];
+        float theta = (float) pos[i2];
+        for (int64_t k = 0; k < ic; k++) theta *= theta_scale;
+        const float th = freq_scale * theta;
+        const float c = cosf(th) * attn_factor, sn = sinf(th) * attn_factor;
+        const int64_t j0 = mode == GGML_ROPE_TYPE_NEOX ? ic : 2 * ic;
+        const int64_t j1 = mode == GGML_ROPE_TYPE_NEOX ? ic + half : 2 * ic + 1;
+        const char * xr = a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3];
+        char * yr = d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3];
+        const float x0 = *(const float *) (xr + j0 * a.nb[0]);
+        const float x1 = *(const float *) (xr + j1 * a.nb[0]);
+        *(float *) (yr + j0 * d.nb[0]) = x0 * c - x1 * sn;
+        *(float *) (yr + j1 * d.nb[0]) = x0 * sn + x1 * c;
+        if (ic == 0) {
+            for (int64_t i = n_dims; i < a.ne[0]; i++) *(float *) (yr + i * d.nb[0]) = *(const float *) (xr + i * a.nb[0]);
+        }
+    }
+}
+
+void launch_rope(const tview & d, const tview & a, const int32_t * pos, int n_dims, int mode, float freq_base,
+                 float freq_scale, float attn_factor, hipStream_t s, int n_cu) {
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    const int64_t n_pairs = (int64_t) (n_dims / 2) * a.ne[1] * a.ne[2] * a.ne[3];
+    hipLaunchKernelGGL(k_rope, dim3(grid_for(n_pairs, 256, n_cu)), dim3(256), 0, s, d, a, pos, n_dims, mode,
+                       theta_scale, freq_scale, attn_factor, n_pairs);
+}
+
+// ----------------------------------------------------------- set_rows ----
+
+// dst[:, idx[i, i2 % ne11, i3 % ne12], i2, i3] = src[:, i, i2, i3], with f32 ->
+// f16 round-to-nearest-even when the cache is f16 (KV write, nn/decoder.rs:2031-2036)
+__global__ void k_set_rows(tview dst, int dtype, tview src, tview idx, int idx_is_i64, int64_t n) {
+    for (int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, src.ne, i0, i1, i2, i3);
+        const char * ip = idx.data + i1 * idx.nb[0] + (i2 % idx.ne[1]) * idx.nb[1] + (i3 % idx.ne[2]) * idx.nb[2];
+        const int64_t r = idx_is_i64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
+        const float v = *(const float *) (src.data + offs4(src, i0, i1, i2, i3));
+        char * o = dst.data + i0 * dst.nb[0] + r * dst.nb[1] + i2 * dst.nb[2] + i3 * dst.nb[3];
+        if (dtype == GGML_TYPE_F16) *(uint16_t *) o = float_to_half_bits(v);
+        else *(float *) o = v;
+    }
+}
+
+void launch_set_rows(const tview & dst, int dtype, const tview & src, const tview & idx, int idx_is_i64,
+                     hipStream_t s, int n_cu) {
+    const int64_t n = src.ne[0] * src.ne[1] * src.ne[2] * src.ne[3];
+    hipLaunchKernelGGL(k_set_rows, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, dst, dtype, src, idx, idx_is_i64,
+                       n);
+}
+
+// ----------------------------------------------------------- get_rows ----
+
+__device__ __forceinline__ float dequant_elem(int type, const char * row, int64_t K, int64_t i) {
+    switch (type) {
+        case GGML_TYPE_F32: return ((const float *) row)[i];
+        case GGML_TYPE_F16: return half_bits_to_float(((const uint16_t *) row)[i]);
+        case GGML_TYPE_Q8_0: {
+            // row-split layout: quants first, then f16 scales
+            const float dd = half_bits_to_float(((const uint16_t *) (row + K))[i / 32]);
+            return dd * (float) ((const int8_t *) row)[i];
+        }
+        case GGML_TYPE_Q4_K: {
+            const char * blk = row + (i / 256) * 144;
+            const int e = (int) (i % 256);
+            const int c = e / 64, l = e % 64;
+            const int j = 2 * c + (l >= 32 ? 1 : 0);
+            const uint8_t * s = (const uint8_t *) (blk + 4);
+            int sc, m;
+            if (j < 4) {
+                sc = s[j] & 63;
+                m = s[j + 4] & 63;
+            } else {
+                sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+                m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+            }
+            const uint8_t qb = ((const uint8_t *) (blk + 16))[32 * c + (l % 32)];
+            const int q = l >= 32 ? (qb >> 4) : (qb & 0xF);
+            const float dd = half_bits_to_float(*(const uint16_t *) blk);
+            const float dm = half_bits_to_float(*(const uint16_t *) (blk + 2));
+            return dd * (float) sc * (float) q - dm * (float) m;
+        }
+        default: return 0.0f;
+    }
+}
+
+// dst[:, i10, i11, i12] = src0[:, rows[i10, i11, i12], i11, i12] as f32
+__global__ void k_get_rows(tview dst, tview src, int stype, tview idx, int64_t n) {
+    for (int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, dst.ne, i0, i1, i2, i3);
+        const int64_t r = *(const int32_t *) (idx.data + i1 * idx.nb[0] + i2 * idx.nb[1] + i3 * idx.nb[2]);
+        const char * row = src.data + r * src.nb[1] + i2 * src.nb[2] + i3 * src.nb[3];
+        float v;
+        if (stype == GGML_TYPE_I32) {
+            *(int32_t *) (dst.data + offs4(dst, i0, i1, i2, i3)) = ((const int32_t *) row)[i0];
+            continue;
+        }
+        v = dequant_elem(stype, row, src.ne[0], i0);
+        *(float *) (dst.data + offs4(dst, i0, i1, i2, i3)) = v;
+    }
+}
+
+void launch_get_rows(const tview & dst, const tview & src, int stype, const tview & idx, hipStream_t s, int n_cu) {
+    const int64_t n = dst.ne[0] * dst.ne[1] * dst.ne[2] * dst.ne[3];
+    hipLaunchKernelGGL(k_get_rows, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, dst, src, stype, idx, n);
+}
+
+// --------------------------------------------------------------- copy ----
+
+// element-order copy between any two layouts of equal element count, with
+// f32 <-> f16 conversion (CPY, CONT, DUP)
+__global__ void k_copy(tview d, int dtype, tview a, int atype, int64_t n) {
+    for (int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, a.ne, i0, i1, i2, i3);
+        const char * ip = a.data + offs4(a, i0, i1, i2, i3);
+        int64_t j0, j1, j2, j3;
+        unravel(t, d.ne, j0, j1, j2, j3);
+        char * op = d.data + offs4(d, j0, j1, j2, j3);
+        if (atype == dtype && atype == GGML_TYPE_I32) {
+            *(int32_t *) op = *(const int32_t *) ip;
+            continue;
+        }
+        const float v = atype == GGML_TYPE_F16 ? half_bits_to_float(*(const uint16_t *) ip) : *(const float *) ip;
+        if (dtype == GGML_TYPE_F16) *(uint16_t *) op = float_to_half_bits(v);
+        else *(float *) op = v;
+    }
+}
+
+void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStream_t s, int n_cu) {
+    const int64_t n = a.ne[0] * a.ne[1] * a.ne[2] * a.ne[3];
+    hipLaunchKernelGGL(k_copy, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, dtype, a, atype, n);
+}
+
+// ------------------------------------------------------------ soft_max ---
+
+// ggml_compute_forward_soft_max_f32, max_bias 0: y = softmax(x*scale + mask)
+__global__ __launch_bounds__(256) void k_soft_max(tview d, tview a, tview mask, int has_mask, float scale,
+                                                  int64_t rows) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
+    const float * x = (const float *) (a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3]);
+    float * y = (float *) (d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]);
+    const uint16_t * mp = has_mask ? (const uint16_t *) (mask.data + i1 * mask.nb[1] + (i2 % mask.ne[2]) * mask.nb[2] +
+                                                         (i3 % mask.ne[3]) * mask.nb[3])
+                                   : nullptr;
+    const int64_t n = a.ne[0];
+    float mx = -INFINITY;
+    for (int64_t i = lane; i < n; i += 64) {
+        const float v = x[i] * scale + (mp ? half_bits_to_float(mp[i]) : 0.0f);
+        mx = fmaxf(mx, v);
+    }
+    mx = wave_max(mx);
+    float sum = 0.0f;
+    for (int64_t i = lane; i < n; i += 64) {
+        const float v = x[i] * scale + (mp ? half_bits_to_float(mp[i]) : 0.0f);
+        const float e = expf(v - mx);
+        y[i] = e;
+        sum += e;
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+    for (int64_t i = lane; i < n; i += 64) y[i] *= inv;
+}
+
+void launch_soft_max(const tview & d, const tview & a, const tview * mask, float scale, hipStream_t s) {
+    const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    tview none{};
+    hipLaunchKernelGGL(k_soft_max, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, s, d, a, mask ? *mask : none,
+                       mask ? 1 : 0, scale, rows);
+}
+
+// -------------------------------------------------------------- argmax ---
+
+// one workgroup per row; first == 1 keeps the lowest index of the maximum
+// (OpenASR's first-max rule), first == 0 the highest (ggml_vec_argmax_f32)
+__global__ __launch_bounds__(256) void k_argmax(tview a, int32_t * out, int first) {
+    __shared__ float s_v[4];
+    __shared__ int s_i[4];
+    const int64_t row = blockIdx.x;
+    const float * x = (const float *) (a.data + row * a.nb[1]);
+    const int64_t n = a.ne[0];
+    float best = -INFINITY;
+    int bi = first ? 0x7fffffff : -1;
+    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
+        const float v = x[i];
+        if (v > best || (v == best && (first ? (int) i < bi : (int) i > bi))) {
+            best = v;
+            bi = (int) i;
+        }
+    }
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(best, off);
+        const int oi = __shfl_xor(bi, off);
+        if (ov > best || (ov == best && (first ? oi < bi : oi > bi))) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) {
+        s_v[wave] = best;
+        s_i[wave] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int) (blockDim.x >> 6); w++) {
+            if (s_v[w] > best || (s_v[w] == best && (first ? s_i[w] < bi : s_i[w] > bi))) {
+                best = s_v[w];
+                bi = s_i[w];
+            }
+        }
+        if (bi < 0 || bi == 0x7fffffff) bi = 0;  // all -inf / NaN row
+        out[row] = bi;
+    }
+}
+
+void launch_argmax(const tview & a, int32_t * out, int first, hipStream_t s) {
+    hipLaunchKernelGGL(k_argmax, dim3((unsigned) a.ne[1]), dim3(256), 0, s, a, out, first);
+}
+
+// ---------------------------------------------------- float mul_mat ------
+
+// dst[m, n, i2, i3] = sum_k src0[k, m, i2/r2, i3/r3] * src1[k, n, i2, i3]
+// for f16 / f32 src0 (ggml-cpu rounds src1 to f16 for an f16 src0). One wave
+// per output element; used by the non-flash attention fallback and small
+// float weights, never by the quantized hot path.
+__global__ __launch_bounds__(256) void k_mul_mat_float(tview d, tview a, int atype, tview b, int64_t total) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wid = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (wid >= total) return;
+    int64_t m, n, i2, i3;
+    unravel(wid, d.ne, m, n, i2, i3);
+    const int64_t r2 = d.ne[2] / a.ne[2], r3 = d.ne[3] / a.ne[3];
+    const char * ar = a.data + m * a.nb[1] + (i2 / r2) * a.nb[2] + (i3 / r3) * a.nb[3];
+    const char * br = b.data + n * b.nb[1] + i2 * b.nb[2] + i3 * b.nb[3];
+    float s = 0.0f;
+    for (int64_t k = lane; k < a.ne[0]; k += 64) {
+        float bv = *(const float *) (br + k * b.nb[0]);
+        float av;
+        if (atype == GGML_TYPE_F16) {
+            av = half_bits_to_float(*(const uint16_t *) (ar + k * a.nb[0]));
+            bv = round_to_half(bv);
+        } else {
+            av = *(const float *) (ar + k * a.nb[0]);
+        }
+        s += av * bv;
+    }
+    s = wave_sum(s);
+    if (lane == 0) *(float *) (d.data + m * d.nb[0] + n * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]) = s;
+}
+
+void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tview & b, hipStream_t s) {
+    const int64_t total = d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3];
+    hipLaunchKernelGGL(k_mul_mat_float, dim3((unsigned) ((total + 3) / 4)), dim3(256), 0, s, d, a, atype, b, total);
+}
+
+}  // namespace mi355x

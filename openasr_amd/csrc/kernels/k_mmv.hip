@@ -1,0 +1,193 @@
+// k_mmv.hip -- GGML_OP_MUL_MAT on block-quantized weights for a few
+// activation columns (decode, N <= 2 here; wider N goes to the MFMA path):
+// a dequant-in-register GEMV with integer dot products (v_dot4_i32_i8).
+// Call site: crates/openasr-core/src/ggml_runtime/cpu_graph.rs:3652-3686.
+//
+// Mapping: a "row team" of LPR lanes (a power of two, <= 64) owns one weight
+// row at a time; every lane streams CPL 16-byte chunks of the row with
+// 128-bit loads, the team reduces its partial sums with cross-lane shuffles,
+// and waves walk the rows grid-stride. Rows of one wave are adjacent, so a
+// wave reads one contiguous run of weight memory per step.
+#include "../mi355x_common.h"
+#include "../ops.h"
+
+namespace mi355x {
+
+__device__ __forceinline__ int dot16(const int4 & w, const int4 & a) {
+    int s = dot4_i8(w.x, a.x, 0);
+    s = dot4_i8(w.y, a.y, s);
+    s = dot4_i8(w.z, a.z, s);
+    return dot4_i8(w.w, a.w, s);
+}
+
+// Q8_0 weights in the row-split layout: [K quants][K/32 f16 scales].
+template <int NC>
+__global__ __launch_bounds__(256) void k_mmv_q8_0(const char * __restrict__ W, int64_t row_bytes, int64_t M,
+                                                  int64_t K, const int8_t * __restrict__ aq,
+                                                  const float * __restrict__ ad, char * __restrict__ dst,
+                                                  int64_t dst_nb1, int lpr_log2, int cpl) {
+    const int lane = threadIdx.x & 63;
+    const int LPR = 1 << lpr_log2;
+    const int li = lane & (LPR - 1);
+    const int teams_per_wave = 64 >> lpr_log2;
+    const int64_t team = ((int64_t) blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * teams_per_wave +
+                         (lane >> lpr_log2);
+    const int64_t team_stride = (int64_t) gridDim.x * (blockDim.x >> 6) * teams_per_wave;
+    const int64_t nblk = K / 32;
+    for (int64_t row = team; row < M; row += team_stride) {
+        const char * wr = W + row * row_bytes;
+        const uint16_t * ws = (const uint16_t *) (wr + K);
+        float acc[NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) acc[n] = 0.0f;
+        for (int c = 0; c < cpl; c++) {
+            const int64_t e = (int64_t) (li + c * LPR) * 16;
+            const int64_t b = e >> 5;
+            const int4 w = *(const int4 *) (wr + e);
+            const float dw = half_bits_to_float(ws[b]);
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                const int4 a = *(const int4 *) (aq + n * K + e);
+                const int s = dot16(w, a);
+                acc[n] += (float) s * (dw * ad[n * nblk + b]);
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            float v = acc[n];
+            for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (li == 0) *(float *) (dst + n * dst_nb1 + row * 4) = v;
+        }
+    }
+}
+
+// Q4_K weights (ggml layout, 144-byte super-blocks: f16 d, f16 dmin,
+// 12 bytes of 6-bit scales/mins, 128 bytes of nibbles) against Q8_K
+// activations. A chunk is 16 bytes of nibbles = 16 weights of sub-block 2g
+// (low nibbles) and 16 of sub-block 2g+1 (high nibbles).
+__device__ __forceinline__ void scale_min_k4(int j, const uint8_t * s, int & sc, int & m) {
+    if (j < 4) {
+        sc = s[j] & 63;
+        m = s[j + 4] & 63;
+    } else {
+        sc = (s[j + 4] & 0xF) | ((s[j - 4] >> 6) << 4);
+        m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4);
+    }
+}
+
+template <int NC>
+__global__ __launch_bounds__(256) void k_mmv_q4_K(const char * __restrict__ W, int64_t row_bytes, int64_t M,
+                                                  int64_t K, const int8_t * __restrict__ aq,
+                                                  const float * __restrict__ ad, const int16_t * __restrict__ abs_,
+                                                  char * __restrict__ dst, int64_t dst_nb1, int lpr_log2, int cpl) {
+    const int lane = threadIdx.x & 63;
+    const int LPR = 1 << lpr_log2;
+    const int li = lane & (LPR - 1);
+    const int teams_per_wave = 64 >> lpr_log2;
+    const int64_t team = ((int64_t) blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * teams_per_wave +
+                         (lane >> lpr_log2);
+    const int64_t team_stride = (int64_t) gridDim.x * (blockDim.x >> 6) * teams_per_wave;
+    const int64_t nsb = K / 256;
+    for (int64_t row = team; row < M; row += team_stride) {
+        const char * wr = W + row * row_bytes;
+        float acc[NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) acc[n] = 0.0f;
+        for (int c = 0; c < cpl; c++) {
+            const int ci = li + c * LPR;
+            const int sb = ci >> 3;
+            const int j = ci & 7;
+            const int g = j >> 1;
+            const int h = j & 1;
+            const char * blk = wr + (int64_t) sb * 144;
+            const uint4 hdr = *(const uint4 *) blk;
+            const int4 qv = *(const int4 *) (blk + 16 + 16 * j);
+            const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
+            const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
+            uint8_t sc8[12];
+            *(uint32_t *) (sc8 + 0) = hdr.y;
+            *(uint32_t *) (sc8 + 4) = hdr.z;
+            *(uint32_t *) (sc8 + 8) = hdr.w;
+            int sc_lo, m_lo, sc_hi, m_hi;
+            scale_min_k4(2 * g, sc8, sc_lo, m_lo);
+            scale_min_k4(2 * g + 1, sc8, sc_hi, m_hi);
+            const int4 lo = make_int4(qv.x & 0x0F0F0F0F, qv.y & 0x0F0F0F0F, qv.z & 0x0F0F0F0F, qv.w & 0x0F0F0F0F);
+            const int4 hi = make_int4((qv.x >> 4) & 0x0F0F0F0F, (qv.y >> 4) & 0x0F0F0F0F, (qv.z >> 4) & 0x0F0F0F0F,
+                                      (qv.w >> 4) & 0x0F0F0F0F);
+            const int64_t e_lo = (int64_t) sb * 256 + 64 * g + 16 * h;
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                const int8_t * acol = aq + n * K;
+                const int4 a_lo = *(const int4 *) (acol + e_lo);
+                const int4 a_hi = *(const int4 *) (acol + e_lo + 32);
+                const int16_t * bs = abs_ + n * (K / 16) + sb * 16;
+                const int isum = dot16(lo, a_lo) * sc_lo + dot16(hi, a_hi) * sc_hi;
+                const int msum = (int) bs[4 * g + h] * m_lo + (int) bs[4 * g + 2 + h] * m_hi;
+                const float da = ad[n * nsb + sb];
+                acc[n] += (dw * da) * (float) isum - (dmw * da) * (float) msum;
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            float v = acc[n];
+            for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (li == 0) *(float *) (dst + n * dst_nb1 + row * 4) = v;
+        }
+    }
+}
+
+// Split the row's chunks over a power-of-two team so each lane owns a whole
+// number of chunks: chunks = LPR * CPL with LPR = min(64, largest power of
+// two dividing chunks).
+static void pick_team(int64_t chunks, int & lpr_log2, int & cpl) {
+    int l2 = 0;
+    while (l2 < 6 && chunks % (2LL << l2) == 0) l2++;
+    lpr_log2 = l2;
+    cpl = (int) (chunks >> l2);
+}
+
+template <int NC>
+static void mmv_dispatch(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K,
+                         const act_buffers & act, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu) {
+    const int64_t chunks = wtype == GGML_TYPE_Q8_0 ? K / 16 : K / 32;
+    int lpr_log2, cpl;
+    pick_team(chunks, lpr_log2, cpl);
+    const int64_t teams = M;
+    const int64_t teams_per_block = 4LL * (64 >> lpr_log2);
+    int64_t blocks = (teams + teams_per_block - 1) / teams_per_block;
+    const int64_t cap = (int64_t) n_cu * 8;
+    if (blocks > cap) blocks = cap;
+    if (wtype == GGML_TYPE_Q8_0) {
+        hipLaunchKernelGGL(k_mmv_q8_0<NC>, dim3((unsigned) blocks), dim3(256), 0, stream, W, row_bytes, M, K, act.q,
+                           act.d, dst, dst_nb1, lpr_log2, cpl);
+    } else {
+        hipLaunchKernelGGL(k_mmv_q4_K<NC>, dim3((unsigned) blocks), dim3(256), 0, stream, W, row_bytes, M, K, act.q,
+                           act.d, act.bsums, dst, dst_nb1, lpr_log2, cpl);
+    }
+}
+
+void launch_mmv(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
+                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu) {
+    int64_t done = 0;
+    while (done < N) {
+        const int64_t n = N - done > 8 ? 8 : N - done;
+        act_buffers a = act;
+        a.q += done * K;
+        a.d += done * (wtype == GGML_TYPE_Q8_0 ? K / 32 : K / 256);
+        if (a.bsums) a.bsums += done * (K / 16);
+        char * d = dst + done * dst_nb1;
+        switch (n) {
+            case 1: mmv_dispatch<1>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;
+            case 2: mmv_dispatch<2>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;
+            case 3: mmv_dispatch<3>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;
+            case 4: mmv_dispatch<4>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;
+            case 5: mmv_dispatch<5>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;
+            case 6: mmv_dispatch<6>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;
+            case 7: mmv_dispatch<7>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;
+            default: mmv_dispatch<8>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;
+        }
+        done += n;
+    }
+}
+
+}  // namespace mi355x

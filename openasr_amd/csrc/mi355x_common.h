@@ -1,0 +1,91 @@
+// mi355x_common.h -- shared definitions for the gfx950 backend: error
+// handling, tensor views passed to kernels, block formats and device helpers.
+#pragma once
+
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+
+#include "ggml_abi.h"
+
+#define MI_CHECK(expr)                                                                                   \
+    do {                                                                                                 \
+        hipError_t err__ = (expr);                                                                       \
+        if (err__ != hipSuccess) {                                                                       \
+            std::fprintf(stderr, "mi355x: %s failed at %s:%d: %s\n", #expr, __FILE__, __LINE__,         \
+                         hipGetErrorString(err__));                                                      \
+            mi355x::note_hip_error(err__);                                                               \
+        }                                                                                                \
+    } while (0)
+
+namespace mi355x {
+
+void note_hip_error(hipError_t err);
+
+constexpr int kWave = 64;
+
+// A tensor as a kernel sees it: base pointer plus element counts and byte
+// strides in ggml order (dim 0 innermost).
+struct tview {
+    char * data;
+    int64_t ne[4];
+    int64_t nb[4];
+};
+
+inline tview make_view(const ggml_tensor * t) {
+    tview v;
+    v.data = (char *) t->data;
+    for (int i = 0; i < 4; i++) {
+        v.ne[i] = t->ne[i];
+        v.nb[i] = (int64_t) t->nb[i];
+    }
+    return v;
+}
+
+// Q8_0 weights are stored per row as [K int8 quants][K/32 f16 scales]
+// (same byte count as ggml's interleaved 34-byte blocks) so a lane can issue
+// aligned 16-byte loads of quants. Conversion happens in set/get_tensor.
+inline size_t q8_0_row_bytes(int64_t k) { return (size_t) (k / 32) * 34; }
+
+// Activations quantized for a Q8_0 weight: per column K int8 + K/32 f32
+// scales (the f32 value of the f16-rounded scale ggml stores).
+// Activations quantized for a Q4_K weight (ggml's Q8_K): per column K int8,
+// K/256 f32 scales and K/16 int16 partial sums.
+struct act_layout {
+    int64_t q_stride;   // bytes between columns of quants
+    int64_t d_stride;   // floats between columns of scales
+    int64_t bs_stride;  // int16 between columns of bsums (Q8_K only)
+};
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t h) {
+    return __half2float(__ushort_as_half(h));
+}
+
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+    return __half_as_ushort(__float2half_rn(f));
+}
+
+__device__ __forceinline__ float round_to_half(float f) { return __half2float(__float2half_rn(f)); }
+
+__device__ __forceinline__ int dot4_i8(int a, int b, int c) { return __builtin_amdgcn_sdot4(a, b, c, false); }
+
+template <int W>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, W);
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+    for (int off = W / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, W));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
+__device__ __forceinline__ float wave_max(float v) { return group_max<kWave>(v); }
+
+}  // namespace mi355x

@@ -1,0 +1,667 @@
+// mi355x_exec.cpp -- graph executor of the gfx950 backend.
+//
+// ggml hands the backend one graph per compute call
+// (crates/openasr-core/src/ggml_runtime/cpu_graph.rs:8007-8055 ->
+// ggml_backend_graph_compute_with_abort, ffi.rs:453-459). The executor
+//   1. plans the node stream into launches: view ops are free, RMSNorm/
+//      LayerNorm absorb their weight multiply and bias add, SiLU absorbs the
+//      gate multiply, consecutive MUL_MATs that read the same activations
+//      quantize them once;
+//   2. runs the plan eagerly the first time a graph is seen and captures it
+//      into a HIP graph the second time, replaying the captured graph for
+//      every later identical compute (the decoder step graph is persistent
+//      and only its input tensors change, llm_transformer.rs:5169-5320).
+// Scratch memory (quantized activations, attention partials) is one device
+// arena owned by the backend and addressed by offset, so a reallocation
+// only invalidates captured graphs, never the plan.
+
+#include "mi355x_exec.h"
+
+#include <cmath>
+#include <cstring>
+#include <unordered_map>
+
+#include "ops.h"
+
+namespace mi355x {
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+bool is_view_op(enum ggml_op op) {
+    return op == GGML_OP_NONE || op == GGML_OP_RESHAPE || op == GGML_OP_VIEW || op == GGML_OP_PERMUTE ||
+           op == GGML_OP_TRANSPOSE;
+}
+
+float op_f32(const ggml_tensor * t, int i) {
+    float v;
+    std::memcpy(&v, &t->op_params[i], sizeof(float));
+    return v;
+}
+
+int64_t nelem(const ggml_tensor * t) { return t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3]; }
+
+bool rows_contiguous(const ggml_tensor * t, size_t esize) { return (size_t) t->nb[0] == esize; }
+
+bool is_contiguous(const ggml_tensor * t) {
+    size_t expect = 0;
+    int64_t blck = 1;
+    switch (t->type) {
+        case GGML_TYPE_F32: expect = 4; break;
+        case GGML_TYPE_F16: expect = 2; break;
+        case GGML_TYPE_I32: expect = 4; break;
+        case GGML_TYPE_Q8_0: expect = 34; blck = 32; break;
+        case GGML_TYPE_Q4_K: expect = 144; blck = 256; break;
+        default: return false;
+    }
+    if (t->ne[0] % blck) return false;
+    size_t next = expect * (size_t) (t->ne[0] / blck);
+    if (t->ne[0] != blck && (size_t) t->nb[0] != expect) return false;
+    for (int i = 1; i < 4; i++) {
+        if (t->ne[i] != 1 && (size_t) t->nb[i] != next) return false;
+        next *= (size_t) t->ne[i];
+    }
+    return true;
+}
+
+// columns of a [K, ne1, ne2, ne3] f32 activation must be uniformly strided
+bool columns_foldable(const ggml_tensor * t) {
+    if (t->nb[0] != 4) return false;
+    if (t->ne[2] > 1 && t->nb[2] != t->nb[1] * t->ne[1]) return false;
+    if (t->ne[3] > 1 && t->nb[3] != t->nb[2] * t->ne[2]) return false;
+    return true;
+}
+
+uint64_t mix(uint64_t h, uint64_t v) {
+    h ^= v + 0x9e3779b97f4a7c15ULL + (h << 6) + (h >> 2);
+    return h;
+}
+
+uint64_t tensor_sig(uint64_t h, const ggml_tensor * t) {
+    h = mix(h, (uint64_t) (uintptr_t) t->data);
+    h = mix(h, (uint64_t) t->type | ((uint64_t) t->op << 32));
+    for (int i = 0; i < 4; i++) {
+        h = mix(h, (uint64_t) t->ne[i]);
+        h = mix(h, (uint64_t) t->nb[i]);
+    }
+    return h;
+}
+
+uint64_t graph_key(const ggml_cgraph * cg) {
+    uint64_t h = mix(0x12345678ULL, (uint64_t) cg->n_nodes);
+    for (int i = 0; i < cg->n_nodes; i++) {
+        const ggml_tensor * t = cg->nodes[i];
+        h = tensor_sig(h, t);
+        for (int p = 0; p < 16; p++) h = mix(h, (uint64_t) (uint32_t) t->op_params[p]);
+        for (int s = 0; s < GGML_MAX_SRC; s++) {
+            if (t->src[s]) h = tensor_sig(h, t->src[s]);
+        }
+    }
+    return h;
+}
+
+struct planner {
+    backend_state * be;
+    const ggml_cgraph * cg;
+    std::unordered_map<const ggml_tensor *, int> uses;
+    std::unordered_map<const ggml_tensor *, const ggml_tensor *> deferred;  // producer -> consumer it fuses into
+    std::vector<step> steps;
+    size_t act_need = 0;
+    size_t gen_need = 0;
+    const ggml_tensor * act_src = nullptr;  // activations currently quantized in the act region
+    int act_wtype = -1;
+    std::string error;
+    int n_cu;
+
+    explicit planner(backend_state * b, const ggml_cgraph * g) : be(b), cg(g), n_cu(b->dev->n_cu) {}
+
+    void count_uses() {
+        for (int i = 0; i < cg->n_nodes; i++) {
+            for (int s = 0; s < GGML_MAX_SRC; s++) {
+                if (cg->nodes[i]->src[s]) uses[cg->nodes[i]->src[s]]++;
+            }
+        }
+    }
+
+    bool single_use(const ggml_tensor * t) const {
+        auto it = uses.find(t);
+        return it != uses.end() && it->second == 1 && !(t->flags & GGML_TENSOR_FLAG_OUTPUT);
+    }
+
+    // the node (after i) consuming t, if t has exactly one consumer
+    const ggml_tensor * sole_consumer(const ggml_tensor * t, int from) const {
+        if (!single_use(t)) return nullptr;
+        for (int j = from; j < cg->n_nodes; j++) {
+            for (int s = 0; s < GGML_MAX_SRC; s++) {
+                if (cg->nodes[j]->src[s] == t) return cg->nodes[j];
+            }
+        }
+        return nullptr;
+    }
+
+    void add(std::function<void(hipStream_t)> fn, const ggml_tensor * node, const char * label) {
+        step s;
+        s.run = std::move(fn);
+        s.node = node;
+        s.label = label;
+        steps.push_back(std::move(s));
+    }
+
+    bool fail(const ggml_tensor * t, const char * why) {
+        char buf[256];
+        std::snprintf(buf, sizeof(buf), "node '%s' (op %d): %s", t->name, (int) t->op, why);
+        error = buf;
+        return false;
+    }
+
+    bool plan();
+    bool plan_mul_mat(const ggml_tensor * t);
+    bool plan_norm(int i, const ggml_tensor * t);
+    bool plan_unary(int i, const ggml_tensor * t);
+    bool plan_binary(const ggml_tensor * t);
+    bool plan_fattn(const ggml_tensor * t);
+};
+
+bool planner::plan_mul_mat(const ggml_tensor * t) {
+    const ggml_tensor * w = t->src[0];
+    const ggml_tensor * x = t->src[1];
+    const tview dv = make_view(t), xv = make_view(x);
+    if (w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K) {
+        const int wtype = w->type;
+        const int64_t K = w->ne[0], M = w->ne[1];
+        const int64_t N = x->ne[1] * x->ne[2] * x->ne[3];
+        const char * W = (const char *) w->data;
+        const int64_t row_bytes = (int64_t) w->nb[1];
+        act_need = std::max(act_need, act_bytes(wtype, K, N));
+        const bool reuse = act_src == x && act_wtype == wtype;
+        act_src = x;
+        act_wtype = wtype;
+        backend_state * b = be;
+        const int ncu = n_cu;
+        char * dst = (char *) t->data;
+        const int64_t dst_nb1 = (int64_t) t->nb[1];
+        const bool wide = mmq_supported(wtype, M, K) && N > 8;
+        add(
+            [=](hipStream_t s) {
+                act_buffers act = act_carve(wtype, b->scratch, K, N);
+                if (!reuse) launch_quantize_act(xv, wtype, act, s);
+                if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
+                else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
+            },
+            t, wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K");
+        (void) dv;
+        return true;
+    }
+    const tview wv = make_view(w);
+    const int atype = w->type;
+    act_src = nullptr;
+    add([=](hipStream_t s) { launch_mul_mat_float(dv, wv, atype, xv, s); }, t, "mul_mat_float");
+    return true;
+}
+
+bool planner::plan_norm(int i, const ggml_tensor * t) {
+    const int mode = t->op == GGML_OP_RMS_NORM ? 0 : 1;
+    const float eps = op_f32(t, 0);
+    const ggml_tensor * out = t;
+    const ggml_tensor * wt = nullptr;
+    const ggml_tensor * bt = nullptr;
+    // the fused kernel runs at the norm's position, so the weight and bias it
+    // absorbs must already exist then: leaves (weights, inputs) only
+    auto leaf = [](const ggml_tensor * x) {
+        return x->op == GGML_OP_NONE || (is_view_op(x->op) && x->view_src && x->view_src->op == GGML_OP_NONE);
+    };
+    const ggml_tensor * mul = sole_consumer(t, i + 1);
+    if (mul && mul->op == GGML_OP_MUL && mul->src[0] == t && mul->src[1]->type == GGML_TYPE_F32 &&
+        mul->src[1]->ne[0] == t->ne[0] && leaf(mul->src[1])) {
+        wt = mul->src[1];
+        out = mul;
+        deferred[mul] = mul;
+        const ggml_tensor * add = sole_consumer(mul, i + 1);
+        if (mode == 1 && add && add->op == GGML_OP_ADD && add->src[0] == mul && add->src[1]->type == GGML_TYPE_F32 &&
+            add->src[1]->ne[0] == t->ne[0] && leaf(add->src[1])) {
+            bt = add->src[1];
+            out = add;
+            deferred[add] = add;
+        }
+    }
+    const tview dv = make_view(out), av = make_view(t->src[0]);
+    const bool hw = wt != nullptr, hb = bt != nullptr;
+    const tview wv = hw ? make_view(wt) : tview{}, bv = hb ? make_view(bt) : tview{};
+    add([=](hipStream_t s) { launch_norm(dv, av, mode, eps, hw ? &wv : nullptr, hb ? &bv : nullptr, s); }, out,
+        mode == 0 ? "rms_norm" : "norm");
+    return true;
+}
+
+bool planner::plan_unary(int i, const ggml_tensor * t) {
+    const int uop = t->op_params[0];
+    const int ncu = n_cu;
+    if (uop == GGML_UNARY_OP_SILU) {
+        const ggml_tensor * mul = sole_consumer(t, i + 1);
+        if (mul && mul->op == GGML_OP_MUL && (mul->src[0] == t || mul->src[1] == t)) {
+            const ggml_tensor * other = mul->src[0] == t ? mul->src[1] : mul->src[0];
+            bool same_shape = true;
+            for (int d = 0; d < 4; d++) same_shape = same_shape && other->ne[d] == mul->ne[d];
+            if (same_shape) {
+                // the SiLU is evaluated inside the multiply, at the multiply's position
+                deferred[t] = mul;
+                return true;
+            }
+        }
+    }
+    const tview dv = make_view(t), av = make_view(t->src[0]);
+    const uint16_t * gt = be->dev->gelu_table;
+    add([=](hipStream_t s) { launch_unary(dv, av, uop, gt, s, ncu); }, t, "unary");
+    return true;
+}
+
+bool planner::plan_binary(const ggml_tensor * t) {
+    const int ncu = n_cu;
+    // SiLU(gate) * up with the SiLU deferred into this node
+    for (int k = 0; k < 2; k++) {
+        const ggml_tensor * s = t->src[k];
+        auto it = deferred.find(s);
+        if (t->op == GGML_OP_MUL && s && s->op == GGML_OP_UNARY && it != deferred.end() && it->second == t) {
+            const tview dv = make_view(t), gv = make_view(s->src[0]), uv = make_view(t->src[1 - k]);
+            add([=](hipStream_t st) { launch_silu_mul(dv, gv, uv, st, ncu); }, t, "silu_mul");
+            return true;
+        }
+    }
+    const tview dv = make_view(t), av = make_view(t->src[0]), bv = make_view(t->src[1]);
+    const int op = t->op;
+    add([=](hipStream_t s) { launch_binary(op, dv, av, bv, s, ncu); }, t, "binary");
+    return true;
+}
+
+bool planner::plan_fattn(const ggml_tensor * t) {
+    const ggml_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2], *m = t->src[3];
+    fattn_args a{};
+    a.q = (const char *) q->data;
+    a.k = (const char *) k->data;
+    a.v = (const char *) v->data;
+    a.mask = m ? (const char *) m->data : nullptr;
+    a.q_nb1 = q->nb[1];
+    a.q_nb2 = q->nb[2];
+    a.q_nb3 = q->nb[3];
+    a.k_nb1 = k->nb[1];
+    a.k_nb2 = k->nb[2];
+    a.k_nb3 = k->nb[3];
+    a.v_nb1 = v->nb[1];
+    a.v_nb2 = v->nb[2];
+    a.v_nb3 = v->nb[3];
+    if (m) {
+        a.m_nb1 = m->nb[1];
+        a.m_nb2 = m->nb[2];
+        a.m_nb3 = m->nb[3];
+        a.m_ne2 = (int) m->ne[2];
+        a.m_ne3 = (int) m->ne[3];
+    }
+    a.d = (int) q->ne[0];
+    a.n_q = (int) q->ne[1];
+    a.hq = (int) q->ne[2];
+    a.n_seq = (int) q->ne[3];
+    a.n_kv = (int) k->ne[1];
+    a.hkv = (int) k->ne[2];
+    a.rk3 = (int) (q->ne[3] / k->ne[3]);
+    a.scale = op_f32(t, 0);
+    fattn_plan(a, n_cu);
+    gen_need = std::max(gen_need, fattn_scratch_bytes(a));
+    backend_state * b = be;
+    const size_t act_off_end = 0;
+    (void) act_off_end;
+    float * out = (float *) t->data;
+    add(
+        [=](hipStream_t s) {
+            float * scratch = (float *) (b->scratch + align_up(b->scratch_cap / 2, kAlign));
+            launch_fattn(a, scratch, out, s);
+        },
+        t, "flash_attn_ext");
+    return true;
+}
+
+bool planner::plan() {
+    count_uses();
+    for (int i = 0; i < cg->n_nodes; i++) {
+        const ggml_tensor * t = cg->nodes[i];
+        if (is_view_op(t->op)) continue;
+        if (!supports_op(be->dev, t)) return fail(t, "unsupported op or layout");
+        auto dit = deferred.find(t);
+        if (dit != deferred.end() && dit->second == t) continue;  // produced by a fused predecessor
+        if (dit != deferred.end()) continue;                        // evaluated inside its consumer
+        const int ncu = n_cu;
+        switch (t->op) {
+            case GGML_OP_MUL_MAT:
+                if (!plan_mul_mat(t)) return false;
+                continue;
+            case GGML_OP_RMS_NORM:
+            case GGML_OP_NORM:
+                plan_norm(i, t);
+                break;
+            case GGML_OP_UNARY:
+                plan_unary(i, t);
+                break;
+            case GGML_OP_ADD:
+            case GGML_OP_SUB:
+            case GGML_OP_MUL:
+            case GGML_OP_DIV:
+                plan_binary(t);
+                break;
+            case GGML_OP_SCALE: {
+                const tview dv = make_view(t), av = make_view(t->src[0]);
+                const float sc = op_f32(t, 0), bias = op_f32(t, 1);
+                add([=](hipStream_t s) { launch_scale(dv, av, sc, bias, s, ncu); }, t, "scale");
+                break;
+            }
+            case GGML_OP_ROPE: {
+                const tview dv = make_view(t), av = make_view(t->src[0]);
+                const int32_t * pos = (const int32_t *) t->src[1]->data;
+                const int n_dims = t->op_params[1], mode = t->op_params[2];
+                const float fb = op_f32(t, 5), fs = op_f32(t, 6), af = op_f32(t, 8);
+                add([=](hipStream_t s) { launch_rope(dv, av, pos, n_dims, mode, fb, fs, af, s, ncu); }, t, "rope");
+                break;
+            }
+            case GGML_OP_SET_ROWS: {
+                const tview dv = make_view(t), sv = make_view(t->src[0]), iv = make_view(t->src[1]);
+                const int dtype = t->type, i64 = t->src[1]->type == GGML_TYPE_I64;
+                add([=](hipStream_t s) { launch_set_rows(dv, dtype, sv, iv, i64, s, ncu); }, t, "set_rows");
+                break;
+            }
+            case GGML_OP_GET_ROWS: {
+                const tview dv = make_view(t), sv = make_view(t->src[0]), iv = make_view(t->src[1]);
+                const int stype = t->src[0]->type;
+                add([=](hipStream_t s) { launch_get_rows(dv, sv, stype, iv, s, ncu); }, t, "get_rows");
+                break;
+            }
+            case GGML_OP_CPY:
+            case GGML_OP_CONT:
+            case GGML_OP_DUP: {
+                const ggml_tensor * dst = t->op == GGML_OP_CPY ? t : t;
+                const tview dv = make_view(dst), av = make_view(t->src[0]);
+                const int dtype = dst->type, atype = t->src[0]->type;
+                add([=](hipStream_t s) { launch_copy(dv, dtype, av, atype, s, ncu); }, t, "copy");
+                break;
+            }
+            case GGML_OP_SOFT_MAX: {
+                const tview dv = make_view(t), av = make_view(t->src[0]);
+                const bool hm = t->src[1] != nullptr;
+                const tview mv = hm ? make_view(t->src[1]) : tview{};
+                const float sc = op_f32(t, 0);
+                add([=](hipStream_t s) { launch_soft_max(dv, av, hm ? &mv : nullptr, sc, s); }, t, "soft_max");
+                break;
+            }
+            case GGML_OP_ARGMAX:
+            case GGML_OP_ARGMAX_FIRST: {
+                const tview av = make_view(t->src[0]);
+                int32_t * out = (int32_t *) t->data;
+                const int first = t->op == GGML_OP_ARGMAX_FIRST;
+                add([=](hipStream_t s) { launch_argmax(av, out, first, s); }, t, "argmax");
+                break;
+            }
+            case GGML_OP_FLASH_ATTN_EXT:
+                plan_fattn(t);
+                break;
+            default:
+                return fail(t, "no launcher");
+        }
+        // a node other than MUL_MAT may overwrite memory the act region was
+        // quantized from only through a view; be conservative for writers
+        if (t->op == GGML_OP_SET_ROWS || t->op == GGML_OP_CPY) act_src = nullptr;
+    }
+    return true;
+}
+
+bool ensure_scratch(backend_state * be, size_t act_need, size_t gen_need) {
+    const size_t half = align_up(std::max(act_need, gen_need), kAlign);
+    const size_t need = 2 * half + kAlign;
+    if (be->scratch && be->scratch_cap >= need && align_up(be->scratch_cap / 2, kAlign) >= half) return true;
+    release_graph_cache(be);
+    if (be->scratch) MI_CHECK(hipFree(be->scratch));
+    be->scratch = nullptr;
+    be->scratch_cap = 0;
+    size_t cap = need < (64u << 20) ? (64u << 20) : need;
+    if (hipMalloc((void **) &be->scratch, cap) != hipSuccess) {
+        be->scratch = nullptr;
+        return false;
+    }
+    be->scratch_cap = cap;
+    return true;
+}
+
+enum ggml_status map_error(hipError_t e) {
+    if (e == hipSuccess) return GGML_STATUS_SUCCESS;
+    if (e == hipErrorLaunchFailure || e == hipErrorIllegalAddress || e == hipErrorECCNotCorrectable ||
+        e == hipErrorNoDevice)
+        return GGML_STATUS_DEVICE_LOST;
+    return GGML_STATUS_EXECUTION_FAILED;
+}
+
+}  // namespace
+
+void release_graph_cache(backend_state * be) {
+    for (cache_entry & c : be->cache) {
+        if (c.exec) hipGraphExecDestroy(c.exec);
+        if (c.graph) hipGraphDestroy(c.graph);
+    }
+    be->cache.clear();
+}
+
+static cache_entry * find_entry(backend_state * be, uint64_t key) {
+    for (cache_entry & c : be->cache) {
+        if (c.key == key) return &c;
+    }
+    return nullptr;
+}
+
+static cache_entry * new_entry(backend_state * be, uint64_t key) {
+    const size_t kMax = 16;
+    if (be->cache.size() >= kMax) {
+        size_t victim = 0;
+        for (size_t i = 1; i < be->cache.size(); i++) {
+            if (be->cache[i].last_use < be->cache[victim].last_use) victim = i;
+        }
+        cache_entry & v = be->cache[victim];
+        if (v.exec) hipGraphExecDestroy(v.exec);
+        if (v.graph) hipGraphDestroy(v.graph);
+        be->cache.erase(be->cache.begin() + (long) victim);
+    }
+    cache_entry e;
+    e.key = key;
+    be->cache.push_back(e);
+    return &be->cache.back();
+}
+
+enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg) {
+    if (be->poisoned) return GGML_STATUS_BACKEND_POISONED;
+    MI_CHECK(hipSetDevice(be->dev->hip_id));
+    const uint64_t key = graph_key(cg);
+    cache_entry * ce = find_entry(be, key);
+    be->use_clock++;
+    if (ce && ce->exec && !be->abort_cb) {
+        ce->last_use = be->use_clock;
+        be->last_observation = GGML_BACKEND_GRAPH_CANCEL_OBSERVATION_GRAPH_COMPLETION;
+        hipError_t e = hipGraphLaunch(ce->exec, be->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
+        if (e != hipSuccess) {
+            std::fprintf(stderr, "mi355x: graph replay failed: %s\n", hipGetErrorString(e));
+            be->poisoned = map_error(e) == GGML_STATUS_DEVICE_LOST;
+        }
+        return map_error(e);
+    }
+
+    planner p(be, cg);
+    if (!p.plan()) {
+        std::fprintf(stderr, "mi355x: cannot plan graph: %s\n", p.error.c_str());
+        return GGML_STATUS_FAILED;
+    }
+    if (!ensure_scratch(be, p.act_need, p.gen_need)) return GGML_STATUS_ALLOC_FAILED;
+    ce = find_entry(be, key);  // the scratch may have been reallocated, dropping entries
+    if (!ce) ce = new_entry(be, key);
+    ce->last_use = be->use_clock;
+    ce->seen++;
+
+    const bool capture = be->use_graphs && !be->abort_cb && ce->seen >= 2;
+    if (capture) {
+        hipError_t e = hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            for (step & s : p.steps) s.run(be->stream);
+            e = hipStreamEndCapture(be->stream, &ce->graph);
+        }
+        if (e == hipSuccess) e = hipGraphInstantiate(&ce->exec, ce->graph, nullptr, nullptr, 0);
+        if (e == hipSuccess) {
+            be->last_observation = GGML_BACKEND_GRAPH_CANCEL_OBSERVATION_GRAPH_COMPLETION;
+            e = hipGraphLaunch(ce->exec, be->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
+            if (e != hipSuccess) be->poisoned = map_error(e) == GGML_STATUS_DEVICE_LOST;
+            return map_error(e);
+        }
+        std::fprintf(stderr, "mi355x: graph capture failed (%s); running eagerly\n", hipGetErrorString(e));
+        (void) hipGetLastError();
+        if (ce->graph) {
+            hipGraphDestroy(ce->graph);
+            ce->graph = nullptr;
+        }
+        ce->exec = nullptr;
+        be->use_graphs = false;
+    }
+
+    be->last_observation = GGML_BACKEND_GRAPH_CANCEL_OBSERVATION_SUBMISSION_CHECKPOINT;
+    for (step & s : p.steps) {
+        if (be->abort_cb && be->abort_cb(be->abort_data)) {
+            hipStreamSynchronize(be->stream);
+            return GGML_STATUS_ABORTED;
+        }
+        s.run(be->stream);
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
+    if (e != hipSuccess) {
+        std::fprintf(stderr, "mi355x: graph execution failed: %s\n", hipGetErrorString(e));
+        be->poisoned = map_error(e) == GGML_STATUS_DEVICE_LOST;
+    }
+    return map_error(e);
+}
+
+int profile_graph(backend_state * be, ggml_cgraph * cg, int iters, float * step_ms, int max_steps, char * labels,
+                  int label_cap) {
+    MI_CHECK(hipSetDevice(be->dev->hip_id));
+    planner p(be, cg);
+    if (!p.plan()) {
+        std::fprintf(stderr, "mi355x: cannot plan graph: %s\n", p.error.c_str());
+        return -1;
+    }
+    if (!ensure_scratch(be, p.act_need, p.gen_need)) return -1;
+    const int n = (int) p.steps.size();
+    std::vector<hipEvent_t> ev((size_t) n + 1);
+    for (auto & e : ev) MI_CHECK(hipEventCreate(&e));
+    std::vector<double> acc((size_t) n, 0.0);
+    for (int it = 0; it < iters; it++) {
+        MI_CHECK(hipEventRecord(ev[0], be->stream));
+        for (int i = 0; i < n; i++) {
+            p.steps[(size_t) i].run(be->stream);
+            MI_CHECK(hipEventRecord(ev[(size_t) i + 1], be->stream));
+        }
+        MI_CHECK(hipStreamSynchronize(be->stream));
+        for (int i = 0; i < n; i++) {
+            float ms = 0.0f;
+            MI_CHECK(hipEventElapsedTime(&ms, ev[(size_t) i], ev[(size_t) i + 1]));
+            acc[(size_t) i] += ms;
+        }
+    }
+    for (auto & e : ev) MI_CHECK(hipEventDestroy(e));
+    for (int i = 0; i < n && i < max_steps; i++) {
+        if (step_ms) step_ms[i] = (float) (acc[(size_t) i] / (iters > 0 ? iters : 1));
+        if (labels && label_cap > 0) {
+            std::snprintf(labels + (size_t) i * (size_t) label_cap, (size_t) label_cap, "%s:%s",
+                          p.steps[(size_t) i].label.c_str(), p.steps[(size_t) i].node->name);
+        }
+    }
+    return n;
+}
+
+// ------------------------------------------------------------ supports_op --
+
+bool supports_op(const device_state * dev, const ggml_tensor * t) {
+    (void) dev;
+    auto f32 = [](const ggml_tensor * x) { return x && x->type == GGML_TYPE_F32; };
+    switch (t->op) {
+        case GGML_OP_NONE:
+        case GGML_OP_RESHAPE:
+        case GGML_OP_VIEW:
+        case GGML_OP_PERMUTE:
+        case GGML_OP_TRANSPOSE:
+            return true;
+        case GGML_OP_ADD:
+        case GGML_OP_SUB:
+        case GGML_OP_MUL:
+        case GGML_OP_DIV:
+            return f32(t) && f32(t->src[0]) && f32(t->src[1]);
+        case GGML_OP_SCALE:
+            return f32(t) && f32(t->src[0]);
+        case GGML_OP_UNARY: {
+            const int u = t->op_params[0];
+            const bool op_ok = u == GGML_UNARY_OP_SILU || u == GGML_UNARY_OP_GELU || u == GGML_UNARY_OP_GELU_ERF ||
+                               u == GGML_UNARY_OP_RELU || u == GGML_UNARY_OP_TANH || u == GGML_UNARY_OP_SIGMOID ||
+                               u == GGML_UNARY_OP_EXP || u == GGML_UNARY_OP_NEG || u == GGML_UNARY_OP_ABS;
+            return op_ok && f32(t) && f32(t->src[0]);
+        }
+        case GGML_OP_RMS_NORM:
+        case GGML_OP_NORM:
+            return f32(t) && f32(t->src[0]) && rows_contiguous(t->src[0], 4) && rows_contiguous(t, 4);
+        case GGML_OP_MUL_MAT: {
+            const ggml_tensor *w = t->src[0], *x = t->src[1];
+            if (!f32(t) || !f32(x) || !is_contiguous(t)) return false;
+            if (w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K) {
+                return w->ne[2] == 1 && w->ne[3] == 1 && is_contiguous(w) && columns_foldable(x) &&
+                       (w->type != GGML_TYPE_Q4_K || w->ne[0] % 256 == 0) && w->ne[0] % 32 == 0;
+            }
+            return w->type == GGML_TYPE_F16 || w->type == GGML_TYPE_F32;
+        }
+        case GGML_OP_GET_ROWS: {
+            const ggml_tensor * s = t->src[0];
+            const bool st = s->type == GGML_TYPE_F32 || s->type == GGML_TYPE_F16 || s->type == GGML_TYPE_Q8_0 ||
+                            s->type == GGML_TYPE_Q4_K || s->type == GGML_TYPE_I32;
+            const bool rows_ok = (s->type != GGML_TYPE_Q8_0 && s->type != GGML_TYPE_Q4_K) ||
+                                 (size_t) s->nb[1] == (size_t) (s->type == GGML_TYPE_Q8_0 ? q8_0_row_bytes(s->ne[0])
+                                                                                          : (s->ne[0] / 256) * 144);
+            return st && rows_ok && t->src[1]->type == GGML_TYPE_I32;
+        }
+        case GGML_OP_SET_ROWS:
+            return (t->type == GGML_TYPE_F16 || t->type == GGML_TYPE_F32) && f32(t->src[0]) &&
+                   (t->src[1]->type == GGML_TYPE_I32 || t->src[1]->type == GGML_TYPE_I64);
+        case GGML_OP_ROPE: {
+            const int mode = t->op_params[2];
+            const float ext = op_f32(t, 7);
+            return f32(t) && f32(t->src[0]) && t->src[2] == nullptr && ext == 0.0f &&
+                   (mode == GGML_ROPE_TYPE_NEOX || mode == GGML_ROPE_TYPE_NORMAL) && t->op_params[1] % 2 == 0 &&
+                   t->op_params[1] <= t->ne[0];
+        }
+        case GGML_OP_FLASH_ATTN_EXT: {
+            const ggml_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2], *m = t->src[3];
+            if (!f32(q) || k->type != GGML_TYPE_F16 || v->type != GGML_TYPE_F16) return false;
+            if (q->nb[0] != 4 || k->nb[0] != 2 || v->nb[0] != 2) return false;
+            if (v->ne[0] != k->ne[0] || k->ne[2] != v->ne[2]) return false;
+            if (op_f32(t, 1) != 0.0f || op_f32(t, 2) != 0.0f) return false;  // max_bias, softcap
+            if (m && (m->type != GGML_TYPE_F16 || m->ne[2] != 1 || m->nb[0] != 2)) return false;
+            if (q->ne[3] % k->ne[3] != 0) return false;
+            return fattn_supported((int) q->ne[0], (int) q->ne[2], (int) k->ne[2]) && is_contiguous(t);
+        }
+        case GGML_OP_SOFT_MAX:
+            return f32(t) && f32(t->src[0]) && op_f32(t, 1) == 0.0f &&
+                   (t->src[1] == nullptr || t->src[1]->type == GGML_TYPE_F16);
+        case GGML_OP_ARGMAX:
+        case GGML_OP_ARGMAX_FIRST:
+            return f32(t->src[0]) && rows_contiguous(t->src[0], 4) && t->type == GGML_TYPE_I32;
+        case GGML_OP_CPY:
+        case GGML_OP_CONT:
+        case GGML_OP_DUP: {
+            const int a = t->src[0]->type, d = t->type;
+            auto ok = [](int ty) { return ty == GGML_TYPE_F32 || ty == GGML_TYPE_F16; };
+            return (ok(a) && ok(d)) || (a == GGML_TYPE_I32 && d == GGML_TYPE_I32);
+        }
+        default:
+            return false;
+    }
+}
+
+}  // namespace mi355x

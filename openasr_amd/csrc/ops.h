@@ -1,0 +1,72 @@
+// ops.h -- host-side launchers of the gfx950 kernels. Every launcher only
+// enqueues work on the given stream; shapes are validated by the planner
+// (mi355x_exec.cpp) before a launcher is reached.
+#pragma once
+
+#include "mi355x_common.h"
+
+namespace mi355x {
+
+struct act_buffers {
+    int8_t * q;
+    float * d;
+    int16_t * bsums;  // Q8_K only
+};
+
+// activation quantization for a quantized-weight MUL_MAT
+void launch_quantize_act(const tview & src, int wtype, const act_buffers & out, hipStream_t stream);
+size_t act_bytes(int wtype, int64_t K, int64_t ncols);
+act_buffers act_carve(int wtype, char * base, int64_t K, int64_t ncols);
+
+// GEMV on Q8_0 (row-split) / Q4_K weights for N columns, dst column stride dst_nb1 bytes
+void launch_mmv(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
+                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
+
+// MFMA int8 GEMM for wider N (prefill)
+bool mmq_supported(int wtype, int64_t M, int64_t K);
+void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
+                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
+
+// float GEMM fallback (f16 / f32 src0)
+void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tview & b, hipStream_t s);
+
+struct fattn_args {
+    const char * q;
+    const char * k;
+    const char * v;
+    const char * mask;
+    int64_t q_nb1, q_nb2, q_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t v_nb1, v_nb2, v_nb3;
+    int64_t m_nb1, m_nb2, m_nb3;
+    int m_ne2, m_ne3;
+    int d, hq, hkv, n_q, n_kv, n_seq, rk3;
+    float scale;
+    int chunk, n_chunks, q_tiles;
+};
+bool fattn_supported(int d, int hq, int hkv);
+void fattn_plan(fattn_args & a, int n_cu);
+size_t fattn_scratch_bytes(const fattn_args & a);
+void launch_fattn(const fattn_args & a, float * scratch, float * out, hipStream_t stream);
+
+void launch_binary(int op, const tview & d, const tview & a, const tview & b, hipStream_t s, int n_cu);
+void launch_scale(const tview & d, const tview & a, float sc, float bias, hipStream_t s, int n_cu);
+void launch_unary(const tview & d, const tview & a, int op, const uint16_t * gelu_table, hipStream_t s, int n_cu);
+void launch_silu_mul(const tview & d, const tview & g, const tview & u, hipStream_t s, int n_cu);
+void launch_norm(const tview & d, const tview & a, int mode, float eps, const tview * w, const tview * b,
+                 hipStream_t s);
+void launch_rope(const tview & d, const tview & a, const int32_t * pos, int n_dims, int mode, float freq_base,
+                 float freq_scale, float attn_factor, hipStream_t s, int n_cu);
+void launch_set_rows(const tview & dst, int dtype, const tview & src, const tview & idx, int idx_is_i64,
+                     hipStream_t s, int n_cu);
+void launch_get_rows(const tview & dst, const tview & src, int stype, const tview & idx, hipStream_t s, int n_cu);
+void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStream_t s, int n_cu);
+void launch_soft_max(const tview & d, const tview & a, const tview * mask, float scale, hipStream_t s);
+void launch_argmax(const tview & a, int32_t * out, int first, hipStream_t s);
+
+// Q8_0 layout conversion between ggml's interleaved blocks and the row-split
+// device layout (host side, used by set/get_tensor)
+void q8_0_to_split_rows(const uint8_t * src, uint8_t * dst, int64_t rows, int64_t k);
+void q8_0_from_split_rows(const uint8_t * src, uint8_t * dst, int64_t rows, int64_t k);
+
+}  // namespace mi355x

@@ -1,0 +1,622 @@
+/*
+ * ggml_cpu_ref.c -- CPU restatement of ggml-cpu semantics for the quantized
+ * decoder path. TEST INFRASTRUCTURE ONLY (the checker); see ggml_cpu_ref.h
+ * for the parity status of each function.
+ *
+ * The block formats, quantizers and dot products follow ggml's published
+ * ggml-common.h / ggml-quants.c / ggml-cpu algorithm descriptions (the fork
+ * that holds them, openasr-ggml @ 0db3a287, is not vendored in the
+ * reference: .gitmodules:1-3). Reference call sites are cited per function.
+ */
+#include "ggml_cpu_ref.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+/* ---------------------------------------------------------------- fp16 -- */
+
+uint16_t ref_fp32_to_fp16(float f) {
+    uint32_t x;
+    memcpy(&x, &f, 4);
+    const uint32_t sign = (x >> 16) & 0x8000u;
+    const uint32_t ax = x & 0x7fffffffu;
+    if (ax >= 0x7f800000u) {
+        return (uint16_t) (sign | 0x7c00u | (ax > 0x7f800000u ? 0x200u : 0u));
+    }
+    if (ax >= 0x477ff000u) { /* |f| >= 65520 rounds to infinity */
+        return (uint16_t) (sign | 0x7c00u);
+    }
+    if (ax < 0x38800000u) { /* below 2^-14: half subnormal, unit 2^-24 */
+        float a;
+        memcpy(&a, &ax, 4);
+        const uint32_t m = (uint32_t) rintf(a * 16777216.0f); /* exact scaling, RNE */
+        return (uint16_t) (sign | m);
+    }
+    const uint32_t e = (ax >> 23) - 112u;
+    const uint32_t mant = ax & 0x7fffffu;
+    uint32_t h = (e << 10) | (mant >> 13);
+    const uint32_t rem = mant & 0x1fffu;
+    if (rem > 0x1000u || (rem == 0x1000u && (h & 1u))) {
+        h++;
+    }
+    return (uint16_t) (sign | h);
+}
+
+float ref_fp16_to_fp32(uint16_t h) {
+    const uint32_t sign = ((uint32_t) h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1fu;
+    const uint32_t mant = h & 0x3ffu;
+    uint32_t bits;
+    if (e == 0) {
+        float v = (float) mant * 5.9604644775390625e-8f; /* 2^-24 */
+        return sign ? -v : v;
+    } else if (e == 31) {
+        bits = sign | 0x7f800000u | (mant << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (mant << 13);
+    }
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+void ref_fp32_to_fp16_row(const float * x, uint16_t * y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = ref_fp32_to_fp16(x[i]);
+}
+
+void ref_fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n) {
+    for (int64_t i = 0; i < n; i++) y[i] = ref_fp16_to_fp32(x[i]);
+}
+
+/* round half to even, as ggml's nearest_int (magic-number add) does */
+static inline int nearest_even(float v) { return (int) rintf(v); }
+
+/* ---------------------------------------------------------------- Q8_0 -- */
+
+/* ggml-base quantize_row_q8_0_ref: weights through ggml_quantize_chunk
+ * (gguf_write.rs:579-588). d = amax/127, id = 1/d, round half away. */
+void ref_quantize_row_q8_0_weights(const float * x, ref_block_q8_0 * y, int64_t k) {
+    const int64_t nb = k / REF_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < REF_QK8_0; j++) {
+            const float a = fabsf(x[i * REF_QK8_0 + j]);
+            amax = a > amax ? a : amax;
+        }
+        const float d = amax / 127.0f;
+        const float id = d != 0.0f ? 1.0f / d : 0.0f;
+        y[i].d = ref_fp32_to_fp16(d);
+        for (int j = 0; j < REF_QK8_0; j++) {
+            y[i].qs[j] = (int8_t) roundf(x[i * REF_QK8_0 + j] * id);
+        }
+    }
+}
+
+/* ggml-cpu quantize_row_q8_0 on x86 (the activation side of a Q8_0 mul_mat):
+ * d = amax/127 stored as f16, multiplier 127/amax, round half to even. */
+void ref_quantize_row_q8_0_act(const float * x, ref_block_q8_0 * y, int64_t k) {
+    const int64_t nb = k / REF_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        float amax = 0.0f;
+        for (int j = 0; j < REF_QK8_0; j++) {
+            const float a = fabsf(x[i * REF_QK8_0 + j]);
+            amax = a > amax ? a : amax;
+        }
+        const float d = amax / 127.0f;
+        y[i].d = ref_fp32_to_fp16(d);
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+        for (int j = 0; j < REF_QK8_0; j++) {
+            y[i].qs[j] = (int8_t) nearest_even(x[i * REF_QK8_0 + j] * id);
+        }
+    }
+}
+
+void ref_dequantize_row_q8_0(const ref_block_q8_0 * x, float * y, int64_t k) {
+    const int64_t nb = k / REF_QK8_0;
+    for (int64_t i = 0; i < nb; i++) {
+        const float d = ref_fp16_to_fp32(x[i].d);
+        for (int j = 0; j < REF_QK8_0; j++) y[i * REF_QK8_0 + j] = x[i].qs[j] * d;
+    }
+}
+
+/* vec_dot_q8_0_q8_0: per block an exact integer dot, scaled by d_x*d_y */
+float ref_vec_dot_q8_0_q8_0(int64_t n, const ref_block_q8_0 * x, const ref_block_q8_0 * y) {
+    const int64_t nb = n / REF_QK8_0;
+    float sumf = 0.0f;
+    for (int64_t i = 0; i < nb; i++) {
+        int sumi = 0;
+        for (int j = 0; j < REF_QK8_0; j++) sumi += (int) x[i].qs[j] * (int) y[i].qs[j];
+        sumf += (float) sumi * (ref_fp16_to_fp32(x[i].d) * ref_fp16_to_fp32(y[i].d));
+    }
+    return sumf;
+}
+
+/* ---------------------------------------------------------------- Q4_K -- */
+
+/* 6-bit scale/min unpacking of a Q4_K super-block (get_scale_min_k4) */
+void ref_get_scale_min_k4(int j, const uint8_t * q, uint8_t * d, uint8_t * m) {
+    if (j < 4) {
+        *d = q[j] & 63;
+        *m = q[j + 4] & 63;
+    } else {
+        *d = (uint8_t) ((q[j + 4] & 0x0F) | ((q[j - 4] >> 6) << 4));
+        *m = (uint8_t) ((q[j + 4] >> 4) | ((q[j] >> 6) << 4));
+    }
+}
+
+void ref_dequantize_row_q4_K(const ref_block_q4_K * x, float * y, int64_t k) {
+    const int64_t nb = k / REF_QK_K;
+    for (int64_t i = 0; i < nb; i++) {
+        const float d = ref_fp16_to_fp32(x[i].d);
+        const float dmin = ref_fp16_to_fp32(x[i].dmin);
+        const uint8_t * q = x[i].qs;
+        for (int c = 0; c < 4; c++) {
+            uint8_t sc, m;
+            ref_get_scale_min_k4(2 * c, x[i].scales, &sc, &m);
+            const float d1 = d * sc, m1 = dmin * m;
+            ref_get_scale_min_k4(2 * c + 1, x[i].scales, &sc, &m);
+            const float d2 = d * sc, m2 = dmin * m;
+            for (int l = 0; l < 32; l++) *y++ = d1 * (q[l] & 0xF) - m1;
+            for (int l = 0; l < 32; l++) *y++ = d2 * (q[l] >> 4) - m2;
+            q += 32;
+        }
+    }
+}
+
+/* Least-squares fit of x ~ s*l - mn over a small grid of candidate inverse
+ * scales (the shape of ggml's make_qkx2_quants search, restated without its
+ * importance weights). Returns s >= 0 and mn >= 0. The exact Q4_K quantizer
+ * search does not affect kernel parity: CPU and GPU consume the same bytes. */
+static void fit_subblock_q4(const float * x, int n, float * s_out, float * mn_out) {
+    float lo = x[0], hi = x[0];
+    for (int i = 1; i < n; i++) {
+        lo = x[i] < lo ? x[i] : lo;
+        hi = x[i] > hi ? x[i] : hi;
+    }
+    if (lo > 0.0f) lo = 0.0f;
+    if (hi <= lo) {
+        *s_out = 0.0f;
+        *mn_out = -lo;
+        return;
+    }
+    float best_s = (hi - lo) / 15.0f, best_min = lo, best_err = INFINITY;
+    for (int t = -10; t <= 10; t++) {
+        const float iscale = (15.0f + 0.1f * (float) t) / (hi - lo);
+        double sl = 0, sx = 0, sll = 0, slx = 0;
+        int lq[32];
+        for (int i = 0; i < n; i++) {
+            int l = nearest_even(iscale * (x[i] - lo));
+            l = l < 0 ? 0 : (l > 15 ? 15 : l);
+            lq[i] = l;
+            sl += l;
+            sx += x[i];
+            sll += (double) l * l;
+            slx += (double) l * x[i];
+        }
+        const double det = n * sll - sl * sl;
+        if (det <= 0) continue;
+        double s = (n * slx - sl * sx) / det;
+        double mn = (sx - s * sl) / n;
+        if (mn > 0) {
+            mn = 0;
+            s = sll > 0 ? slx / sll : 0;
+        }
+        if (s <= 0) continue;
+        double err = 0;
+        for (int i = 0; i < n; i++) {
+            const double e = s * lq[i] + mn - x[i];
+            err += e * e;
+        }
+        if (err < best_err) {
+            best_err = (float) err;
+            best_s = (float) s;
+            best_min = (float) mn;
+        }
+    }
+    *s_out = best_s;
+    *mn_out = -best_min;
+}
+
+void ref_quantize_row_q4_K(const float * x, ref_block_q4_K * y, int64_t k) {
+    const int64_t nb = k / REF_QK_K;
+    for (int64_t i = 0; i < nb; i++) {
+        const float * xb = x + i * REF_QK_K;
+        float scales[8], mins[8];
+        float max_scale = 0.0f, max_min = 0.0f;
+        for (int j = 0; j < 8; j++) {
+            fit_subblock_q4(xb + 32 * j, 32, &scales[j], &mins[j]);
+            max_scale = scales[j] > max_scale ? scales[j] : max_scale;
+            max_min = mins[j] > max_min ? mins[j] : max_min;
+        }
+        const float inv_scale = max_scale > 0 ? 63.0f / max_scale : 0.0f;
+        const float inv_min = max_min > 0 ? 63.0f / max_min : 0.0f;
+        uint8_t ls[8], lm[8];
+        for (int j = 0; j < 8; j++) {
+            int a = nearest_even(inv_scale * scales[j]);
+            int b = nearest_even(inv_min * mins[j]);
+            ls[j] = (uint8_t) (a > 63 ? 63 : (a < 0 ? 0 : a));
+            lm[j] = (uint8_t) (b > 63 ? 63 : (b < 0 ? 0 : b));
+        }
+        memset(y[i].scales, 0, 12);
+        for (int j = 0; j < 4; j++) {
+            y[i].scales[j] = (uint8_t) (ls[j] | ((ls[j + 4] >> 4) << 6));
+            y[i].scales[j + 4] = (uint8_t) (lm[j] | ((lm[j + 4] >> 4) << 6));
+            y[i].scales[j + 8] = (uint8_t) ((ls[j + 4] & 0xF) | ((lm[j + 4] & 0xF) << 4));
+        }
+        y[i].d = ref_fp32_to_fp16(max_scale / 63.0f);
+        y[i].dmin = ref_fp32_to_fp16(max_min / 63.0f);
+        const float d = ref_fp16_to_fp32(y[i].d);
+        const float dmin = ref_fp16_to_fp32(y[i].dmin);
+        uint8_t L[REF_QK_K];
+        for (int j = 0; j < 8; j++) {
+            uint8_t sc, m;
+            ref_get_scale_min_k4(j, y[i].scales, &sc, &m);
+            const float dd = d * sc;
+            const float dm = dmin * m;
+            for (int l = 0; l < 32; l++) {
+                int q = 0;
+                if (dd != 0.0f) {
+                    q = nearest_even((xb[32 * j + l] + dm) / dd);
+                    q = q < 0 ? 0 : (q > 15 ? 15 : q);
+                }
+                L[32 * j + l] = (uint8_t) q;
+            }
+        }
+        for (int c = 0; c < 4; c++) {
+            for (int l = 0; l < 32; l++) {
+                y[i].qs[32 * c + l] = (uint8_t) (L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+            }
+        }
+    }
+}
+
+/* ---------------------------------------------------------------- Q8_K -- */
+
+/* quantize_row_q8_K_ref: iscale = -127/max where max is the signed value of
+ * largest magnitude; d = 1/iscale; bsums over groups of 16. */
+void ref_quantize_row_q8_K(const float * x, ref_block_q8_K * y, int64_t k) {
+    const int64_t nb = k / REF_QK_K;
+    for (int64_t i = 0; i < nb; i++) {
+        const float * xb = x + i * REF_QK_K;
+        float max = 0.0f, amax = 0.0f;
+        for (int j = 0; j < REF_QK_K; j++) {
+            const float ax = fabsf(xb[j]);
+            if (ax > amax) {
+                amax = ax;
+                max = xb[j];
+            }
+        }
+        if (amax == 0.0f) {
+            y[i].d = 0.0f;
+            memset(y[i].qs, 0, REF_QK_K);
+            memset(y[i].bsums, 0, sizeof(y[i].bsums));
+            continue;
+        }
+        const float iscale = -127.0f / max;
+        for (int j = 0; j < REF_QK_K; j++) {
+            const int v = nearest_even(iscale * xb[j]);
+            y[i].qs[j] = (int8_t) (v < 127 ? v : 127);
+        }
+        for (int j = 0; j < REF_QK_K / 16; j++) {
+            int s = 0;
+            for (int l = 0; l < 16; l++) s += y[i].qs[16 * j + l];
+            y[i].bsums[j] = (int16_t) s;
+        }
+        y[i].d = 1.0f / iscale;
+    }
+}
+
+void ref_dequantize_row_q8_K(const ref_block_q8_K * x, float * y, int64_t k) {
+    const int64_t nb = k / REF_QK_K;
+    for (int64_t i = 0; i < nb; i++) {
+        for (int j = 0; j < REF_QK_K; j++) y[i * REF_QK_K + j] = x[i].d * x[i].qs[j];
+    }
+}
+
+/* vec_dot_q4_K_q8_K: per super-block the scaled integer sum and the mins
+ * correction (through the Q8_K bsums) are exact integers; the float result
+ * per super-block is d*isum - dmin*msum, accumulated in block order. */
+float ref_vec_dot_q4_K_q8_K(int64_t n, const ref_block_q4_K * x, const ref_block_q8_K * y) {
+    const int64_t nb = n / REF_QK_K;
+    float sumf = 0.0f;
+    for (int64_t i = 0; i < nb; i++) {
+        uint8_t sc[8], mn[8];
+        for (int j = 0; j < 8; j++) ref_get_scale_min_k4(j, x[i].scales, &sc[j], &mn[j]);
+        int msum = 0;
+        for (int j = 0; j < 16; j++) msum += (int) y[i].bsums[j] * (int) mn[j / 2];
+        int isum = 0;
+        const uint8_t * q4 = x[i].qs;
+        const int8_t * q8 = y[i].qs;
+        for (int c = 0; c < 4; c++) {
+            int s_lo = 0, s_hi = 0;
+            for (int l = 0; l < 32; l++) {
+                s_lo += (int) (q4[32 * c + l] & 0xF) * (int) q8[64 * c + l];
+                s_hi += (int) (q4[32 * c + l] >> 4) * (int) q8[64 * c + 32 + l];
+            }
+            isum += s_lo * sc[2 * c] + s_hi * sc[2 * c + 1];
+        }
+        const float d = ref_fp16_to_fp32(x[i].d) * y[i].d;
+        const float dmin = ref_fp16_to_fp32(x[i].dmin) * y[i].d;
+        sumf += d * (float) isum - dmin * (float) msum;
+    }
+    return sumf;
+}
+
+/* ggml_vec_dot_f16: products of two halves are exact in f32; summed wide */
+float ref_vec_dot_f16(int64_t n, const uint16_t * x, const uint16_t * y) {
+    double s = 0.0;
+    for (int64_t i = 0; i < n; i++) s += (double) (ref_fp16_to_fp32(x[i]) * ref_fp16_to_fp32(y[i]));
+    return (float) s;
+}
+
+size_t ref_row_size(int type, int64_t ne0) {
+    switch (type) {
+        case REF_F32: return (size_t) ne0 * 4;
+        case REF_F16: return (size_t) ne0 * 2;
+        case REF_Q8_0: return (size_t) (ne0 / REF_QK8_0) * sizeof(ref_block_q8_0);
+        case REF_Q4_K: return (size_t) (ne0 / REF_QK_K) * sizeof(ref_block_q4_K);
+        case REF_Q8_K: return (size_t) (ne0 / REF_QK_K) * sizeof(ref_block_q8_K);
+        default: return 0;
+    }
+}
+
+/* ------------------------------------------------------------- mul_mat -- */
+
+void ref_mul_mat(int wtype, const void * w, size_t row_bytes, int64_t m, int64_t k,
+                 const float * x, int64_t x_stride, int64_t n, float * dst, int64_t d_stride,
+                 int n_threads) {
+#ifdef _OPENMP
+    if (n_threads <= 0) n_threads = omp_get_max_threads();
+#else
+    (void) n_threads;
+#endif
+    for (int64_t col = 0; col < n; col++) {
+        const float * xc = x + col * x_stride;
+        float * dc = dst + col * d_stride;
+        if (wtype == REF_Q8_0) {
+            ref_block_q8_0 * xq = (ref_block_q8_0 *) malloc(ref_row_size(REF_Q8_0, k));
+            ref_quantize_row_q8_0_act(xc, xq, k);
+#pragma omp parallel for num_threads(n_threads) schedule(static)
+            for (int64_t r = 0; r < m; r++) {
+                dc[r] = ref_vec_dot_q8_0_q8_0(k, (const ref_block_q8_0 *) ((const char *) w + r * row_bytes), xq);
+            }
+            free(xq);
+        } else if (wtype == REF_Q4_K) {
+            ref_block_q8_K * xq = (ref_block_q8_K *) malloc(ref_row_size(REF_Q8_K, k));
+            ref_quantize_row_q8_K(xc, xq, k);
+#pragma omp parallel for num_threads(n_threads) schedule(static)
+            for (int64_t r = 0; r < m; r++) {
+                dc[r] = ref_vec_dot_q4_K_q8_K(k, (const ref_block_q4_K *) ((const char *) w + r * row_bytes), xq);
+            }
+            free(xq);
+        } else if (wtype == REF_F16) {
+            uint16_t * xh = (uint16_t *) malloc((size_t) k * 2);
+            ref_fp32_to_fp16_row(xc, xh, k);
+#pragma omp parallel for num_threads(n_threads) schedule(static)
+            for (int64_t r = 0; r < m; r++) {
+                dc[r] = ref_vec_dot_f16(k, (const uint16_t *) ((const char *) w + r * row_bytes), xh);
+            }
+            free(xh);
+        } else { /* f32 x f32: ggml_vec_dot_f32 */
+#pragma omp parallel for num_threads(n_threads) schedule(static)
+            for (int64_t r = 0; r < m; r++) {
+                const float * wr = (const float *) ((const char *) w + r * row_bytes);
+                double s = 0.0;
+                for (int64_t i = 0; i < k; i++) s += (double) (wr[i] * xc[i]);
+                dc[r] = (float) s;
+            }
+        }
+    }
+}
+
+/* ---------------------------------------------------------- row ops ---- */
+
+/* ggml_compute_forward_rms_norm_f32 (nn/norm.rs:39-56): double sum of x*x */
+void ref_rms_norm(const float * x, float * y, int64_t ne0, int64_t rows, float eps) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float * xr = x + r * ne0;
+        float * yr = y + r * ne0;
+        double sum = 0.0;
+        for (int64_t i = 0; i < ne0; i++) sum += (double) (xr[i] * xr[i]);
+        const float mean = (float) (sum / ne0);
+        const float scale = 1.0f / sqrtf(mean + eps);
+        for (int64_t i = 0; i < ne0; i++) yr[i] = xr[i] * scale;
+    }
+}
+
+/* ggml_compute_forward_norm_f32 (nn/norm.rs:10-33): mean, then variance */
+void ref_norm(const float * x, float * y, int64_t ne0, int64_t rows, float eps) {
+    for (int64_t r = 0; r < rows; r++) {
+        const float * xr = x + r * ne0;
+        float * yr = y + r * ne0;
+        double sum = 0.0;
+        for (int64_t i = 0; i < ne0; i++) sum += (double) xr[i];
+        const float mean = (float) (sum / ne0);
+        double sum2 = 0.0;
+        for (int64_t i = 0; i < ne0; i++) {
+            const float v = xr[i] - mean;
+            yr[i] = v;
+            sum2 += (double) (v * v);
+        }
+        const float variance = (float) (sum2 / ne0);
+        const float scale = 1.0f / sqrtf(variance + eps);
+        for (int64_t i = 0; i < ne0; i++) yr[i] *= scale;
+    }
+}
+
+float ref_silu(float x) { return x / (1.0f + expf(-x)); }
+
+float ref_gelu_f32(float x) {
+    const float c = 0.79788456080286535587989211986876f; /* sqrt(2/pi) */
+    return 0.5f * x * (1.0f + tanhf(c * x * (1.0f + 0.044715f * x * x)));
+}
+
+/* ggml-cpu GELU goes through a table indexed by the f16 bits of x, holding
+ * f16(gelu(f16 x)); |x| >= 10 short-circuits (ggml_vec_gelu_f32). */
+float ref_gelu(float x) {
+    if (x <= -10.0f) return 0.0f;
+    if (x >= 10.0f) return x;
+    const float xh = ref_fp16_to_fp32(ref_fp32_to_fp16(x));
+    return ref_fp16_to_fp32(ref_fp32_to_fp16(ref_gelu_f32(xh)));
+}
+
+/* ggml_compute_forward_rope_f32, NEOX mode, ext_factor 0, attn_factor 1
+ * (cpu_graph.rs:1135-1161): theta advances by repeated multiplication with
+ * theta_scale = freq_base^(-2/n_dims), as ggml_rope_cache_init does. */
+void ref_rope_neox(const float * x, float * y, int64_t head_dim, int64_t n_heads, int64_t n_tokens,
+                   const int32_t * pos, int n_dims, float freq_base, float freq_scale) {
+    const float theta_scale = powf(freq_base, -2.0f / (float) n_dims);
+    float * cache = (float *) malloc(sizeof(float) * (size_t) n_dims);
+    for (int64_t t = 0; t < n_tokens; t++) {
+        float theta = (float) pos[t];
+        for (int i0 = 0; i0 < n_dims; i0 += 2) {
+            const float th = freq_scale * theta;
+            cache[i0] = cosf(th);
+            cache[i0 + 1] = sinf(th);
+            theta *= theta_scale;
+        }
+        for (int64_t h = 0; h < n_heads; h++) {
+            const float * xr = x + (t * n_heads + h) * head_dim;
+            float * yr = y + (t * n_heads + h) * head_dim;
+            const int half = n_dims / 2;
+            for (int ic = 0; ic < half; ic++) {
+                const float c = cache[2 * ic], s = cache[2 * ic + 1];
+                const float x0 = xr[ic], x1 = xr[ic + half];
+                yr[ic] = x0 * c - x1 * s;
+                yr[ic + half] = x0 * s + x1 * c;
+            }
+            for (int64_t i = n_dims; i < head_dim; i++) yr[i] = xr[i];
+        }
+    }
+    free(cache);
+}
+
+/* ggml_compute_forward_soft_max_f32 with an f16 mask, max_bias 0 */
+void ref_soft_max_ext(const float * x, const uint16_t * mask, float * y, int64_t ne0, int64_t rows,
+                      float scale) {
+    float * wp = (float *) malloc(sizeof(float) * (size_t) ne0);
+    for (int64_t r = 0; r < rows; r++) {
+        float mx = -INFINITY;
+        for (int64_t i = 0; i < ne0; i++) {
+            wp[i] = x[r * ne0 + i] * scale + (mask ? ref_fp16_to_fp32(mask[r * ne0 + i]) : 0.0f);
+            mx = wp[i] > mx ? wp[i] : mx;
+        }
+        double sum = 0.0;
+        for (int64_t i = 0; i < ne0; i++) {
+            const float e = expf(wp[i] - mx);
+            y[r * ne0 + i] = e;
+            sum += (double) e;
+        }
+        const float inv = (float) (1.0 / sum);
+        for (int64_t i = 0; i < ne0; i++) y[r * ne0 + i] *= inv;
+    }
+    free(wp);
+}
+
+/* ggml_vec_argmax_f32 keeps the LAST index equal to the running max; the
+ * host relies on this when it reverses logits (cpu_graph.rs:3770-3772). */
+int32_t ref_argmax_last(const float * x, int64_t n) {
+    float mx = -INFINITY;
+    int32_t idx = 0;
+    for (int64_t i = 0; i < n; i++) {
+        mx = x[i] > mx ? x[i] : mx;
+        idx = x[i] == mx ? (int32_t) i : idx;
+    }
+    return idx;
+}
+
+/* first-max rule of OpenASR greedy selection (device_greedy_token.rs:44-75,
+ * whisper/ggml_decoder_graph.rs:6232-6240) */
+int32_t ref_argmax_first(const float * x, int64_t n) {
+    float mx = -INFINITY;
+    int32_t idx = 0;
+    for (int64_t i = 0; i < n; i++) {
+        if (x[i] > mx) {
+            mx = x[i];
+            idx = (int32_t) i;
+        }
+    }
+    return idx;
+}
+
+/* ----------------------------------------------------- flash attention -- */
+
+/* ggml_compute_forward_flash_attn_ext_f16_one_chunk restated: sequential
+ * online softmax over KV positions, masked (-inf) positions skipped. */
+void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_head,
+                        const uint16_t * k, const uint16_t * v, int64_t kv_stride_head,
+                        int64_t kv_stride_pos, const uint16_t * mask, int64_t mask_stride,
+                        float * out, int64_t D, int64_t n_q, int64_t Hq, int64_t Hkv, int64_t n_kv,
+                        float scale, int fidelity, int n_threads) {
+    const int64_t group = Hq / Hkv;
+#ifdef _OPENMP
+    if (n_threads <= 0) n_threads = omp_get_max_threads();
+#else
+    (void) n_threads;
+#endif
+#pragma omp parallel for collapse(2) num_threads(n_threads) schedule(static)
+    for (int64_t iq = 0; iq < n_q; iq++) {
+        for (int64_t h = 0; h < Hq; h++) {
+            const int64_t kvh = h / group;
+            const float * qr = q + iq * q_stride_tok + h * q_stride_head;
+            uint16_t qh[512];
+            float qf[512];
+            uint16_t acc16[512];
+            float acc32[512];
+            for (int64_t d = 0; d < D; d++) {
+                qh[d] = ref_fp32_to_fp16(qr[d]);
+                qf[d] = qr[d];
+                acc16[d] = 0;
+                acc32[d] = 0.0f;
+            }
+            float M = -INFINITY, S = 0.0f;
+            for (int64_t ic = 0; ic < n_kv; ic++) {
+                const float mv = mask ? ref_fp16_to_fp32(mask[iq * mask_stride + ic]) : 0.0f;
+                if (mv == -INFINITY) continue;
+                const uint16_t * kr = k + kvh * kv_stride_head + ic * kv_stride_pos;
+                const uint16_t * vr = v + kvh * kv_stride_head + ic * kv_stride_pos;
+                float s;
+                if (fidelity == 1) {
+                    s = ref_vec_dot_f16(D, kr, qh);
+                } else if (fidelity == 2) {
+                    double a = 0.0;
+                    for (int64_t d = 0; d < D; d++) a += (double) ref_fp16_to_fp32(kr[d]) * ref_fp16_to_fp32(qh[d]);
+                    s = (float) a;
+                } else {
+                    double a = 0.0;
+                    for (int64_t d = 0; d < D; d++) a += (double) ref_fp16_to_fp32(kr[d]) * qf[d];
+                    s = (float) a;
+                }
+                s = s * scale + mv;
+                const float Mold = M;
+                float ms = 1.0f, vs = 1.0f;
+                if (s > M) {
+                    M = s;
+                    ms = expf(Mold - M);
+                    for (int64_t d = 0; d < D; d++) {
+                        if (fidelity == 1) acc16[d] = ref_fp32_to_fp16(ref_fp16_to_fp32(acc16[d]) * ms);
+                        else acc32[d] *= ms;
+                    }
+                } else {
+                    vs = expf(s - M);
+                }
+                for (int64_t d = 0; d < D; d++) {
+                    if (fidelity == 1) {
+                        acc16[d] = ref_fp32_to_fp16(fmaf(ref_fp16_to_fp32(vr[d]), vs, ref_fp16_to_fp32(acc16[d])));
+                    } else {
+                        acc32[d] += ref_fp16_to_fp32(vr[d]) * vs;
+                    }
+                }
+                S = S * ms + vs;
+            }
+            const float inv = S == 0.0f ? 0.0f : 1.0f / S;
+            float * o = out + (iq * Hq + h) * D;
+            for (int64_t d = 0; d < D; d++) o[d] = (fidelity == 1 ? ref_fp16_to_fp32(acc16[d]) : acc32[d]) * inv;
+        }
+    }
+}

@@ -1,0 +1,174 @@
+"""numpy wrapper of the CPU oracle (oracle/ggml_cpu_ref.c).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker. The product never imports it.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "build" / "libggml_cpu_ref.so"
+
+F32, F16, Q8_0, Q4_K, Q8_K = 0, 1, 8, 12, 15
+BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q8_K: (256, 292)}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(f"{LIB_PATH} missing: run `python -m openasr_amd.build`")
+    L = C.CDLL(str(LIB_PATH))
+    vp, i64, f, i = C.c_void_p, C.c_int64, C.c_float, C.c_int
+
+    def s(name, res, *args):
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = list(args)
+
+    s("ref_fp32_to_fp16", C.c_uint16, f)
+    s("ref_fp16_to_fp32", f, C.c_uint16)
+    for n in ("ref_quantize_row_q8_0_weights", "ref_quantize_row_q4_K", "ref_quantize_row_q8_0_act",
+              "ref_quantize_row_q8_K", "ref_dequantize_row_q8_0", "ref_dequantize_row_q4_K",
+              "ref_dequantize_row_q8_K"):
+        s(n, None, vp, vp, i64)
+    s("ref_vec_dot_q8_0_q8_0", f, i64, vp, vp)
+    s("ref_vec_dot_q4_K_q8_K", f, i64, vp, vp)
+    s("ref_vec_dot_f16", f, i64, vp, vp)
+    s("ref_row_size", C.c_size_t, i, i64)
+    s("ref_mul_mat", None, i, vp, C.c_size_t, i64, i64, vp, i64, i64, vp, i64, i)
+    s("ref_rms_norm", None, vp, vp, i64, i64, f)
+    s("ref_norm", None, vp, vp, i64, i64, f)
+    s("ref_silu", f, f)
+    s("ref_gelu", f, f)
+    s("ref_gelu_f32", f, f)
+    s("ref_rope_neox", None, vp, vp, i64, i64, i64, vp, i, f, f)
+    s("ref_soft_max_ext", None, vp, vp, vp, i64, i64, f)
+    s("ref_argmax_last", C.c_int32, vp, i64)
+    s("ref_argmax_first", C.c_int32, vp, i64)
+    s("ref_flash_attn_ext", None, vp, i64, i64, vp, vp, i64, i64, vp, i64, vp, i64, i64, i64, i64, i64, f, i, i)
+    _lib = L
+    return L
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data
+
+
+def row_size(typ: int, k: int) -> int:
+    return int(lib().ref_row_size(typ, k))
+
+
+def quantize_weights(typ: int, x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    rows, k = x.shape
+    out = np.zeros(rows * row_size(typ, k), dtype=np.uint8)
+    fn = lib().ref_quantize_row_q8_0_weights if typ == Q8_0 else lib().ref_quantize_row_q4_K
+    fn(_p(x), _p(out), rows * k)
+    return out
+
+
+def quantize_act(typ: int, x: np.ndarray) -> np.ndarray:
+    """activation side: Q8_0 (x86 ggml-cpu rule) or Q8_K"""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1)
+    out = np.zeros(row_size(typ, x.size), dtype=np.uint8)
+    fn = lib().ref_quantize_row_q8_0_act if typ == Q8_0 else lib().ref_quantize_row_q8_K
+    fn(_p(x), _p(out), x.size)
+    return out
+
+
+def dequantize(typ: int, q: np.ndarray, n: int) -> np.ndarray:
+    out = np.zeros(n, dtype=np.float32)
+    fn = {Q8_0: lib().ref_dequantize_row_q8_0, Q4_K: lib().ref_dequantize_row_q4_K,
+          Q8_K: lib().ref_dequantize_row_q8_K}[typ]
+    q = np.ascontiguousarray(q)
+    fn(_p(q), _p(out), n)
+    return out
+
+
+def mul_mat(wtype: int, w: np.ndarray, m: int, k: int, x: np.ndarray, threads: int = 0) -> np.ndarray:
+    """x: [n, k] f32 -> [n, m] f32 (ggml dst layout ne=[m, n])"""
+    w = np.ascontiguousarray(w)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    n = x.shape[0]
+    dst = np.zeros((n, m), dtype=np.float32)
+    rb = row_size(wtype, k) if wtype in (Q8_0, Q4_K) else (2 * k if wtype == F16 else 4 * k)
+    lib().ref_mul_mat(wtype, _p(w), rb, m, k, _p(x), k, n, _p(dst), m, threads)
+    return dst
+
+
+def rms_norm(x: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().ref_rms_norm(_p(x), _p(y), x.shape[-1], x.size // x.shape[-1], eps)
+    return y
+
+
+def norm(x: np.ndarray, eps: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().ref_norm(_p(x), _p(y), x.shape[-1], x.size // x.shape[-1], eps)
+    return y
+
+
+def silu(x: np.ndarray) -> np.ndarray:
+    f = lib().ref_silu
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).reshape(-1)], np.float32).reshape(np.shape(x))
+
+
+def gelu(x: np.ndarray) -> np.ndarray:
+    f = lib().ref_gelu
+    return np.array([f(float(v)) for v in np.asarray(x, np.float32).reshape(-1)], np.float32).reshape(np.shape(x))
+
+
+def rope_neox(x: np.ndarray, pos: np.ndarray, n_dims: int, freq_base: float, freq_scale: float = 1.0):
+    """x: [tokens, heads, head_dim]"""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    t, h, d = x.shape
+    y = np.empty_like(x)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    lib().ref_rope_neox(_p(x), _p(y), d, h, t, _p(pos), n_dims, freq_base, freq_scale)
+    return y
+
+
+def soft_max_ext(x: np.ndarray, mask_f16: np.ndarray | None, scale: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    m = None if mask_f16 is None else np.ascontiguousarray(mask_f16, dtype=np.uint16)
+    lib().ref_soft_max_ext(_p(x), None if m is None else _p(m), _p(y), x.shape[-1], x.size // x.shape[-1], scale)
+    return y
+
+
+def argmax_last(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return int(lib().ref_argmax_last(_p(x), x.size))
+
+
+def argmax_first(x: np.ndarray) -> int:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    return int(lib().ref_argmax_first(_p(x), x.size))
+
+
+def flash_attn(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16: np.ndarray | None, scale: float,
+               fidelity: int = 1, threads: int = 0) -> np.ndarray:
+    """q: [n_q, Hq, D] f32; k16, v16: [Hkv, n_kv, D] f16 bits; mask16: [n_q, n_kv] f16 bits.
+    fidelity 1: ggml-cpu numerics (f16 Q, f16 V accumulator); 2: f16 Q, f32
+    accumulation; 0: f32 throughout. Returns [n_q, Hq, D] f32."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k16 = np.ascontiguousarray(k16, dtype=np.uint16)
+    v16 = np.ascontiguousarray(v16, dtype=np.uint16)
+    n_q, hq, d = q.shape
+    hkv, n_kv, _ = k16.shape
+    out = np.zeros((n_q, hq, d), dtype=np.float32)
+    m = None if mask16 is None else np.ascontiguousarray(mask16, dtype=np.uint16)
+    lib().ref_flash_attn_ext(_p(q), hq * d, d, _p(k16), _p(v16), n_kv * d, d, None if m is None else _p(m),
+                             0 if m is None else m.shape[-1], _p(out), d, n_q, hq, hkv, n_kv, scale,
+                             int(fidelity), threads)
+    return out

@@ -1,0 +1,374 @@
+"""Per-op parity of the MI355X plugin against the CPU oracle, through the C
+ABI exactly as the host drives it: a ggml graph built with libggml-base,
+allocated on the plugin's buffer type, computed by the plugin backend.
+
+Tolerances (max |gpu - oracle| / max |oracle|): the north-star bound is 2e-3
+per op; integer-dot paths are held to 1e-5 (only the float accumulation
+order differs), attention to 1e-5 against the oracle mode with the same
+rounding points and 2e-3 against the ggml-cpu-fidelity mode.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+RNG = np.random.default_rng(2024)
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def run(ggml, gpu, G, out):
+    G.build(out)
+    G.allocate(gpu.buft)
+
+
+# ------------------------------------------------------------- mul_mat --
+
+MM_CASES = [
+    ("q8_0", 64, 256), ("q8_0", 1024, 1024), ("q8_0", 3072, 1024), ("q8_0", 1024, 3072), ("q8_0", 384, 384),
+    ("q8_0", 1536, 384), ("q8_0", 384, 1536), ("q4_K", 64, 256), ("q4_K", 1024, 1024), ("q4_K", 3072, 1024),
+    ("q4_K", 1024, 3072), ("q4_K", 4096, 2048), ("q4_K", 2048, 6144),
+]
+
+
+@pytest.mark.parametrize("wname,m,k", MM_CASES)
+@pytest.mark.parametrize("n", [1, 2, 8, 13])
+def test_mul_mat_quantized(ggml, gpu, ref, wname, m, k, n):
+    wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
+    print(f"mul_mat {wname} M={m} K={k} N={n}", flush=True)
+    w = ggml.synth_normal(11, m * 7 + k, m * k, 0.0, 0.02).reshape(m, k)
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    wq = ggml.quantize(wt, w)
+    G = ggml.Graph()
+    W = G.new(wt, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    Y = G.lib.ggml_mul_mat(G.ctx, W, X)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    G.set(X, x)
+    assert G.compute(gpu.backend) == 0
+    y = G.get(Y).reshape(n, m)
+    want = ref.mul_mat(wt, wq, m, k, x)
+    assert rel_err(y, want) < 1e-5
+    # the weight round-trips through the device layout byte for byte
+    assert np.array_equal(G.get(W, np.uint8), wq)
+    G.free()
+
+
+def test_mul_mat_lm_head_full_size(ggml, gpu, ref):
+    """151936 x 1024 Q4_K at batch 8, the largest decode GEMV of the Qwen3-0.6B shape"""
+    m, k, n = 151936, 1024, 8
+    w = ggml.synth_normal(5, 99, m * k, 0.0, 0.02).reshape(m, k)
+    wq = ggml.quantize(ggml.Q4_K, w)
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    G = ggml.Graph()
+    W = G.new(ggml.Q4_K, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    Y = G.lib.ggml_mul_mat(G.ctx, W, X)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    G.set(X, x)
+    assert G.compute(gpu.backend) == 0
+    y = G.get(Y).reshape(n, m)
+    want = ref.mul_mat(ggml.Q4_K, wq, m, k, x)
+    assert rel_err(y, want) < 1e-5
+    assert np.array_equal(y.argmax(1), want.argmax(1))
+    G.free()
+
+
+def test_mul_mat_f16_weights(ggml, gpu, ref):
+    m, k, n = 96, 128, 5
+    w = RNG.standard_normal((m, k)).astype(np.float16)
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    G = ggml.Graph()
+    W = G.new(ggml.F16, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    Y = G.lib.ggml_mul_mat(G.ctx, W, X)
+    run(ggml, gpu, G, Y)
+    G.set(W, w.view(np.uint16))
+    G.set(X, x)
+    assert G.compute(gpu.backend) == 0
+    want = ref.mul_mat(ref.F16, w.view(np.uint16), m, k, x)
+    assert rel_err(G.get(Y).reshape(n, m), want) < 1e-5
+    G.free()
+
+
+# ----------------------------------------------------- flash attention --
+
+FA_CASES = [
+    # d, hq, hkv, n_kv, n_q, n_seq
+    (128, 16, 8, 512, 1, 1), (128, 16, 8, 1024, 1, 8), (128, 16, 8, 2048, 1, 1), (128, 16, 8, 8192, 1, 1),
+    (128, 16, 8, 512, 64, 1), (128, 16, 8, 2048, 64, 2), (64, 6, 6, 448, 1, 1), (64, 6, 6, 1500, 1, 1),
+    (64, 6, 6, 1500, 1, 3),
+]
+
+
+@pytest.mark.parametrize("d,hq,hkv,n_kv,n_q,n_seq", FA_CASES)
+def test_flash_attn_ext(ggml, gpu, ref, d, hq, hkv, n_kv, n_q, n_seq):
+    print(f"flash_attn D={d} Hq={hq} Hkv={hkv} kv={n_kv} nq={n_q} seq={n_seq}", flush=True)
+    q = RNG.standard_normal((n_seq, hq, n_q, d)).astype(np.float32)  # ggml [d, n_q, hq, n_seq]
+    k = RNG.standard_normal((n_seq, hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((n_seq, hkv, n_kv, d)).astype(np.float16)
+    # per sequence a different number of valid positions; the last n_q are causal
+    valid = [n_kv - 3 * s for s in range(n_seq)] if n_q == 1 else [n_kv - 64 * s for s in range(n_seq)]
+    mask = np.full((n_seq, n_q, n_kv), -np.inf, np.float16)
+    for s in range(n_seq):
+        for i in range(n_q):
+            mask[s, i, :valid[s] - n_q + i + 1] = 0
+    cross = d == 64 and n_kv == 1500  # Whisper cross attention has no mask
+    G = ggml.Graph()
+    Q = G.new(ggml.F32, d, n_q, hq, n_seq)
+    K = G.new(ggml.F16, d, n_kv, hkv, n_seq)
+    V = G.new(ggml.F16, d, n_kv, hkv, n_seq)
+    M = None if cross else G.new(ggml.F16, n_kv, n_q, 1, n_seq)
+    scale = 1.0 / math.sqrt(d)
+    O = G.lib.ggml_flash_attn_ext(G.ctx, Q, K, V, M, scale, 0.0, 0.0)
+    run(ggml, gpu, G, O)
+    G.set(Q, q)
+    G.set(K, k.view(np.uint16))
+    G.set(V, v.view(np.uint16))
+    if M is not None:
+        G.set(M, mask.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    out = G.get(O).reshape(n_seq, n_q, hq, d)
+    for s in range(n_seq):
+        qs = np.ascontiguousarray(q[s].transpose(1, 0, 2))  # [n_q, hq, d]
+        ms = None if cross else mask[s].view(np.uint16)
+        same = ref.flash_attn(qs, k[s].view(np.uint16), v[s].view(np.uint16), ms, scale, fidelity=2)
+        cpu = ref.flash_attn(qs, k[s].view(np.uint16), v[s].view(np.uint16), ms, scale, fidelity=1)
+        assert rel_err(out[s], same) < 1e-5
+        assert rel_err(out[s], cpu) < 2e-3
+    G.free()
+
+
+def test_flash_attn_fully_masked_chunks_are_skipped_exactly(ggml, gpu, ref):
+    """positions past the valid length hold garbage; results must not change"""
+    d, hq, hkv, n_kv = 128, 16, 8, 4096
+    q = RNG.standard_normal((hq, 1, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((1, n_kv), np.float16)
+    mask[0, 700:] = -np.inf
+    k[:, 700:] = np.float16(60000)
+    v[:, 700:] = np.float16(np.nan)
+    G = ggml.Graph()
+    Q = G.new(ggml.F32, d, 1, hq, 1)
+    K = G.new(ggml.F16, d, n_kv, hkv, 1)
+    V = G.new(ggml.F16, d, n_kv, hkv, 1)
+    M = G.new(ggml.F16, n_kv, 1, 1, 1)
+    O = G.lib.ggml_flash_attn_ext(G.ctx, Q, K, V, M, 1 / math.sqrt(d), 0.0, 0.0)
+    run(ggml, gpu, G, O)
+    G.set(Q, q)
+    G.set(K, k.view(np.uint16))
+    G.set(V, v.view(np.uint16))
+    G.set(M, mask.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    out = G.get(O).reshape(hq, d)
+    want = ref.flash_attn(np.ascontiguousarray(q.transpose(1, 0, 2)), k[:, :700].view(np.uint16).copy(),
+                          v[:, :700].view(np.uint16).copy(), mask[:, :700].view(np.uint16).copy(),
+                          1 / math.sqrt(d), fidelity=2)[0]
+    assert np.isfinite(out).all()
+    assert rel_err(out, want) < 1e-5
+    G.free()
+
+
+# ------------------------------------------------------------ row ops ---
+
+def test_rms_norm_mul_fused(ggml, gpu, ref):
+    x = RNG.standard_normal((8, 1024)).astype(np.float32) * 2
+    w = RNG.standard_normal(1024).astype(np.float32)
+    G = ggml.Graph()
+    X = G.new(ggml.F32, 1024, 8)
+    W = G.new(ggml.F32, 1024, weight=True)
+    Y = G.lib.ggml_mul(G.ctx, G.lib.ggml_rms_norm(G.ctx, X, 1e-6), W)
+    run(ggml, gpu, G, Y)
+    G.set(X, x)
+    G.set(W, w)
+    assert G.compute(gpu.backend) == 0
+    assert rel_err(G.get(Y).reshape(8, 1024), ref.rms_norm(x, 1e-6) * w) < 1e-6
+    G.free()
+
+
+def test_qk_norm_per_head(ggml, gpu, ref):
+    """RMSNorm over head_dim of a [128, heads, tokens] view (nn/decoder.rs:1937-1958)"""
+    x = RNG.standard_normal((4, 16, 128)).astype(np.float32)
+    w = RNG.standard_normal(128).astype(np.float32)
+    G = ggml.Graph()
+    X = G.new(ggml.F32, 128, 16, 4)
+    W = G.new(ggml.F32, 128, weight=True)
+    Y = G.lib.ggml_mul(G.ctx, G.lib.ggml_rms_norm(G.ctx, X, 1e-6), W)
+    run(ggml, gpu, G, Y)
+    G.set(X, x)
+    G.set(W, w)
+    assert G.compute(gpu.backend) == 0
+    assert rel_err(G.get(Y).reshape(4, 16, 128), ref.rms_norm(x, 1e-6) * w) < 1e-6
+    G.free()
+
+
+def test_layer_norm_affine_fused(ggml, gpu, ref):
+    x = RNG.standard_normal((3, 384)).astype(np.float32) * 3 + 1
+    w = RNG.standard_normal(384).astype(np.float32)
+    b = RNG.standard_normal(384).astype(np.float32)
+    G = ggml.Graph()
+    X = G.new(ggml.F32, 384, 3)
+    W = G.new(ggml.F32, 384, weight=True)
+    B = G.new(ggml.F32, 384, weight=True)
+    Y = G.lib.ggml_add(G.ctx, G.lib.ggml_mul(G.ctx, G.lib.ggml_norm(G.ctx, X, 1e-5), W), B)
+    run(ggml, gpu, G, Y)
+    G.set(X, x)
+    G.set(W, w)
+    G.set(B, b)
+    assert G.compute(gpu.backend) == 0
+    assert rel_err(G.get(Y).reshape(3, 384), ref.norm(x, 1e-5) * w + b) < 1e-6
+    G.free()
+
+
+def test_rope_neox_positions(ggml, gpu, ref):
+    t, h, d = 8, 16, 128
+    x = RNG.standard_normal((t, h, d)).astype(np.float32)
+    pos = np.array([0, 1, 5, 374, 383, 900, 1023, 4095], np.int32)
+    G = ggml.Graph()
+    X = G.new(ggml.F32, d, h, t)
+    P = G.new(ggml.I32, t)
+    Y = G.lib.ggml_rope_ext(G.ctx, X, P, None, d, 2, 4096, 1e6, 1.0, 0.0, 1.0, 32.0, 1.0)
+    run(ggml, gpu, G, Y)
+    G.set(X, x)
+    G.set(P, pos)
+    assert G.compute(gpu.backend) == 0
+    # same theta sequence as the oracle; sin/cos of up to ~4000 rad differ by libm ulps
+    assert rel_err(G.get(Y).reshape(t, h, d), ref.rope_neox(x, pos, d, 1e6)) < 2e-6
+    G.free()
+
+
+def test_silu_mul_and_gelu(ggml, gpu, ref):
+    g = RNG.standard_normal((4, 3072)).astype(np.float32) * 3
+    u = RNG.standard_normal((4, 3072)).astype(np.float32)
+    G = ggml.Graph()
+    Gt = G.new(ggml.F32, 3072, 4)
+    U = G.new(ggml.F32, 3072, 4)
+    Y = G.lib.ggml_mul(G.ctx, G.lib.ggml_silu(G.ctx, Gt), U)
+    Z = G.lib.ggml_gelu(G.ctx, U)
+    G.build(Y, Z)
+    G.allocate(gpu.buft)
+    G.set(Gt, g)
+    G.set(U, u)
+    assert G.compute(gpu.backend) == 0
+    assert rel_err(G.get(Y).reshape(4, 3072), ref.silu(g) * u) < 1e-6
+    assert np.array_equal(G.get(Z).reshape(4, 3072), ref.gelu(u))  # same f16 table: bit exact
+    G.free()
+
+
+def test_set_rows_batched_kv_write(ggml, gpu):
+    """f32 -> f16 rows into a [128, maxpos, 8, n_seq] cache at per-sequence rows"""
+    d, maxpos, hkv, n_seq = 128, 64, 8, 4
+    cache = RNG.standard_normal((n_seq, hkv, maxpos, d)).astype(np.float16)
+    src = RNG.standard_normal((n_seq, hkv, 1, d)).astype(np.float32)
+    rows = np.array([3, 0, 63, 17], np.int32)
+    G = ggml.Graph()
+    Cc = G.new(ggml.F16, d, maxpos, hkv, n_seq)
+    S = G.new(ggml.F32, d, 1, hkv, n_seq)
+    I = G.new(ggml.I32, 1, 1, n_seq, 1)
+    R = G.lib.ggml_set_rows(G.ctx, Cc, S, I)
+    run(ggml, gpu, G, R)
+    G.set(Cc, cache.view(np.uint16))
+    G.set(S, src)
+    G.set(I, rows)
+    assert G.compute(gpu.backend) == 0
+    got = G.get(Cc, np.uint16).reshape(n_seq, hkv, maxpos, d)
+    want = cache.copy()
+    for s in range(n_seq):
+        want[s, :, rows[s], :] = src[s, :, 0, :].astype(np.float16)
+    assert np.array_equal(got, want.view(np.uint16))
+    G.free()
+
+
+@pytest.mark.parametrize("wname", ["q8_0", "q4_K", "f32"])
+def test_get_rows_dequant(ggml, gpu, ref, wname):
+    rows, k = 300, 1024
+    w = ggml.synth_normal(3, 4, rows * k, 0.0, 0.02).reshape(rows, k)
+    ids = np.array([0, 299, 17, 17, 150], np.int32)
+    G = ggml.Graph()
+    if wname == "f32":
+        W = G.new(ggml.F32, k, rows, weight=True)
+        data, want = w, w[ids]
+    else:
+        t = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
+        W = G.new(t, k, rows, weight=True)
+        data = ggml.quantize(t, w)
+        want = ref.dequantize(t, data, rows * k).reshape(rows, k)[ids]
+    I = G.new(ggml.I32, len(ids))
+    Y = G.lib.ggml_get_rows(G.ctx, W, I)
+    run(ggml, gpu, G, Y)
+    G.set(W, data)
+    G.set(I, ids)
+    assert G.compute(gpu.backend) == 0
+    assert np.array_equal(G.get(Y).reshape(len(ids), k), want)
+    G.free()
+
+
+def test_soft_max_argmax_cpy_cont(ggml, gpu, ref):
+    x = RNG.standard_normal((6, 333)).astype(np.float32)
+    x[2, 10] = x[2, 200] = 9.0  # tie
+    mask = np.zeros((6, 333), np.float16)
+    mask[:, 300:] = -np.inf
+    G = ggml.Graph()
+    X = G.new(ggml.F32, 333, 6)
+    M = G.new(ggml.F16, 333, 6)
+    S = G.lib.ggml_soft_max_ext(G.ctx, X, M, 0.7, 0.0)
+    A = G.lib.ggml_argmax(G.ctx, X)
+    A1 = G.lib.ggml_argmax_first(G.ctx, X)
+    H = G.new(ggml.F16, 333, 6)
+    Cp = G.lib.ggml_cpy(G.ctx, X, H)
+    Tc = G.lib.ggml_cont(G.ctx, G.lib.ggml_transpose(G.ctx, X))
+    G.build(S, A, A1, Cp, Tc)
+    G.allocate(gpu.buft)
+    G.set(X, x)
+    G.set(M, mask.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    assert rel_err(G.get(S).reshape(6, 333), ref.soft_max_ext(x, mask.view(np.uint16), 0.7)) < 1e-6
+    assert list(G.get(A)) == [ref.argmax_last(r) for r in x]
+    assert list(G.get(A1)) == [ref.argmax_first(r) for r in x]
+    assert G.get(A)[2] == 200 and G.get(A1)[2] == 10
+    assert np.array_equal(G.get(H, np.uint16).reshape(6, 333), x.astype(np.float16).view(np.uint16))
+    assert np.array_equal(G.get(Tc).reshape(333, 6), x.T)
+    G.free()
+
+
+def test_abort_callback_and_graph_replay(ggml, gpu, ref):
+    """same graph computed repeatedly: eager, captured, replayed -- identical
+    results every time; an abort callback that fires stops the compute with
+    GGML_STATUS_ABORTED and reports native cancellation"""
+    import ctypes as C
+    m, k = 1024, 1024
+    wq = ggml.quantize(ggml.Q8_0, ggml.synth_normal(1, 1, m * k, 0, 0.02).reshape(m, k))
+    G = ggml.Graph()
+    W = G.new(ggml.Q8_0, k, m, weight=True)
+    X = G.new(ggml.F32, k, 1)
+    Y = G.lib.ggml_add(G.ctx, G.lib.ggml_mul_mat(G.ctx, W, X), X)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    outs = []
+    for it in range(5):
+        x = RNG.standard_normal((1, k)).astype(np.float32)
+        G.set(X, x)
+        assert G.compute(gpu.backend) == 0
+        y = G.get(Y).reshape(1, m)
+        assert rel_err(y, ref.mul_mat(ggml.Q8_0, wq, m, k, x) + x) < 1e-5
+        outs.append(y)
+    CB = C.CFUNCTYPE(C.c_bool, C.c_void_p)
+    always = CB(lambda _: True)
+    cap = ggml.cancel_capability()
+    st = G.lib.ggml_backend_graph_compute_with_abort(gpu.backend, G.gf, C.cast(always, C.c_void_p), None,
+                                                     C.byref(cap))
+    assert st == 1 and cap.mechanism == 1
+    never = CB(lambda _: False)
+    st = G.lib.ggml_backend_graph_compute_with_abort(gpu.backend, G.gf, C.cast(never, C.c_void_p), None,
+                                                     C.byref(cap))
+    assert st == 0 and cap.mechanism == 1 and cap.observation_granularity == 1
+    G.free()

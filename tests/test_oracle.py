@@ -1,0 +1,288 @@
+"""Pins the CPU oracle (oracle/ggml_cpu_ref.c) before anything is checked
+against it. Each test fixes the oracle by something other than its own
+formula: numpy's independent f16 codec, hand-packed known-answer blocks,
+f64 brute force over dequantized operands, closed forms, and invariants
+(GQA == explicit K/V repetition, masked positions contribute nothing).
+The reference holds no golden vectors for this path (its arithmetic lives
+in the un-vendored openasr-ggml fork), so these are the pins.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+RNG = np.random.default_rng(1234)
+
+
+# ------------------------------------------------------------------ f16 --
+
+def test_fp16_matches_numpy_codec(ref):
+    L = ref.lib()
+    specials = np.array([0.0, -0.0, 1.0, -1.0, 65504.0, 65519.99, 65520.0, 1e-8, 6e-8, 5.96e-8, 2.98e-8,
+                         6.1035e-5, 6.1e-5, np.inf, -np.inf, 0.1, 1.0 / 3.0, 2049.0, 2051.0, 4097.0],
+                        dtype=np.float32)
+    x = np.concatenate([specials, RNG.standard_normal(20000).astype(np.float32) * 10.0 ** RNG.integers(-8, 5, 20000)])
+    x = x.astype(np.float32)
+    got = np.array([L.ref_fp32_to_fp16(float(v)) for v in x], dtype=np.uint16)
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, want)
+    back = np.array([L.ref_fp16_to_fp32(int(h)) for h in range(0, 65536, 7)], dtype=np.float32)
+    want_back = np.arange(0, 65536, 7, dtype=np.uint16).view(np.float16).astype(np.float32)
+    assert np.array_equal(np.isnan(back), np.isnan(want_back))
+    ok = ~np.isnan(want_back)
+    assert np.array_equal(back[ok], want_back[ok])
+
+
+# ----------------------------------------------------------------- Q8_0 --
+
+def test_q8_0_weight_known_answer(ref):
+    x = (np.arange(32, dtype=np.float32) - 15.5) * 0.25  # amax = 3.875
+    q = ref.quantize_weights(ref.Q8_0, x.reshape(1, 32))
+    d = np.frombuffer(q[:2].tobytes(), dtype=np.float16)[0]
+    assert d == np.float16(3.875 / 127.0)
+    qs = q[2:34].view(np.int8)
+    # round half away from zero: x*127/3.875 for x=-3.875 -> -127
+    want = np.array([math.copysign(math.floor(abs(v * (1.0 / np.float32(3.875 / 127.0))) + 0.5), v) for v in x])
+    assert np.array_equal(qs.astype(np.int64), want.astype(np.int64))
+    z = ref.quantize_weights(ref.Q8_0, np.zeros((1, 32), np.float32))
+    assert not z.any()
+
+
+def test_q8_0_activation_rounds_half_to_even(ref):
+    # amax = 127 makes the multiplier exactly 1.0: 2.5 -> 2 (x86 ggml-cpu), 3.5 -> 4
+    x = np.zeros(32, np.float32)
+    x[0], x[1], x[2], x[3] = 127.0, 2.5, 3.5, -2.5
+    qa = ref.quantize_act(ref.Q8_0, x)[2:34].view(np.int8)
+    assert list(qa[:4]) == [127, 2, 4, -2]
+    qw = ref.quantize_weights(ref.Q8_0, x.reshape(1, 32))[2:34].view(np.int8)
+    assert list(qw[:4]) == [127, 3, 4, -3]  # weights: half away from zero
+
+
+def test_q8_0_roundtrip_error_bound(ref):
+    x = RNG.standard_normal((8, 256)).astype(np.float32)
+    q = ref.quantize_weights(ref.Q8_0, x)
+    y = ref.dequantize(ref.Q8_0, q, x.size).reshape(x.shape)
+    d = np.abs(x.reshape(-1, 32)).max(axis=1) / 127.0
+    d16 = q.reshape(-1, 34)[:, :2].copy().view(np.float16)[:, 0].astype(np.float64)
+    err = np.abs(x - y).reshape(-1, 32).max(axis=1)
+    # half a step, plus the stored scale's f16 rounding times the largest quant
+    assert np.all(err <= d * 0.5 + 127 * np.abs(d16 - d) + 1e-7)
+
+
+# ----------------------------------------------------------------- Q4_K --
+
+def pack_q4_K(d, dmin, sc, mn, q):
+    """Independent block packer from the block_q4_K spec: 6-bit scales of
+    sub-blocks 0..3 in bytes 0..3 (mins 4..7); sub-blocks 4..7 keep their
+    low nibbles in bytes 8..11 (scale low, min high) and their top two bits
+    in bits 6..7 of bytes 0..3 (scales) and 4..7 (mins)."""
+    s = np.zeros(12, np.uint8)
+    for j in range(8):
+        if j < 4:
+            s[j] |= sc[j] & 63
+            s[j + 4] |= mn[j] & 63
+        else:
+            s[j + 4] |= (sc[j] & 0xF) | ((mn[j] & 0xF) << 4)
+            s[j - 4] |= (sc[j] >> 4) << 6
+            s[j] |= (mn[j] >> 4) << 6
+    qs = np.zeros(128, np.uint8)
+    for c in range(4):
+        for l in range(32):
+            qs[32 * c + l] = q[64 * c + l] | (q[64 * c + 32 + l] << 4)
+    hdr = np.array([d, dmin], np.float16).view(np.uint8)
+    return np.concatenate([hdr, s, qs])
+
+
+def test_q4_K_dequant_known_answer(ref):
+    sc = np.array([1, 7, 13, 63, 17, 33, 48, 62])
+    mn = np.array([0, 5, 63, 9, 31, 16, 47, 2])
+    q = RNG.integers(0, 16, 256)
+    d, dmin = np.float16(0.0125), np.float16(0.0031)
+    blk = pack_q4_K(d, dmin, sc, mn, q)
+    assert blk.size == 144
+    got = ref.dequantize(ref.Q4_K, blk, 256)
+    want = np.array([np.float32(d) * np.float32(sc[i // 32]) * q[i] - np.float32(dmin) * np.float32(mn[i // 32])
+                     for i in range(256)], np.float32)
+    assert np.allclose(got, want, rtol=0, atol=1e-6)
+
+
+def test_q4_K_quantizer_roundtrip(ref):
+    x = (RNG.standard_normal((4, 512)) * 0.02).astype(np.float32)
+    q = ref.quantize_weights(ref.Q4_K, x)
+    y = ref.dequantize(ref.Q4_K, q, x.size).reshape(x.shape)
+    # 4-bit grid over each 32-weight sub-block range: error well under a step
+    rng = (x.reshape(-1, 32).max(1) - np.minimum(x.reshape(-1, 32).min(1), 0))
+    err = np.abs(x - y).reshape(-1, 32).max(1)
+    assert np.all(err <= rng / 15.0 * 0.75 + 1e-6)
+
+
+# ----------------------------------------------------------------- Q8_K --
+
+def test_q8_K_known_answer_and_invariants(ref):
+    x = RNG.standard_normal(512).astype(np.float32)
+    x[10] = 5.0
+    x[20] = -5.0  # same magnitude later: the first one (+5) sets the sign
+    blk = ref.quantize_act(ref.Q8_K, x)
+    b0 = blk[:292]
+    d = b0[:4].view(np.float32)[0]
+    qs = b0[4:260].view(np.int8).astype(np.int64)
+    bsums = b0[260:292].view(np.int16).astype(np.int64)
+    assert qs[10] == -127 and qs[20] == 127
+    assert d == pytest.approx(-5.0 / 127.0, rel=1e-6)
+    assert np.array_equal(bsums, qs.reshape(16, 16).sum(1))
+    y = ref.dequantize(ref.Q8_K, blk, 512)
+    assert np.max(np.abs(y - x)) <= 5.0 / 127.0 * 0.5 * 1.01 + np.abs(x).max() / 127 * 0.01
+
+
+# ----------------------------------------------------------- dot products --
+
+def test_vec_dot_q8_0_equals_f64_dot_of_dequantized(ref):
+    L = ref.lib()
+    for n in (32, 256, 1024):
+        w = RNG.standard_normal(n).astype(np.float32)
+        a = RNG.standard_normal(n).astype(np.float32)
+        qw = ref.quantize_weights(ref.Q8_0, w.reshape(1, -1))
+        qa = ref.quantize_act(ref.Q8_0, a)
+        got = L.ref_vec_dot_q8_0_q8_0(n, qw.ctypes.data, qa.ctypes.data)
+        want = np.dot(ref.dequantize(ref.Q8_0, qw, n).astype(np.float64), ref.dequantize(ref.Q8_0, qa, n))
+        assert got == pytest.approx(want, rel=1e-5, abs=1e-5)
+
+
+def test_vec_dot_q4_K_equals_f64_dot_of_dequantized(ref):
+    L = ref.lib()
+    for n in (256, 1024, 3072):
+        w = (RNG.standard_normal(n) * 0.02).astype(np.float32)
+        a = RNG.standard_normal(n).astype(np.float32)
+        qw = ref.quantize_weights(ref.Q4_K, w.reshape(1, -1))
+        qa = ref.quantize_act(ref.Q8_K, a)
+        got = L.ref_vec_dot_q4_K_q8_K(n, qw.ctypes.data, qa.ctypes.data)
+        want = np.dot(ref.dequantize(ref.Q4_K, qw, n).astype(np.float64),
+                      ref.dequantize(ref.Q8_K, qa, n).astype(np.float64))
+        assert got == pytest.approx(want, rel=2e-5, abs=2e-5)
+
+
+@pytest.mark.parametrize("wtype", ["q8_0", "q4_K"])
+def test_mul_mat_brute_force_and_column_invariance(ref, wtype):
+    t = ref.Q8_0 if wtype == "q8_0" else ref.Q4_K
+    m, k, n = 48, 512, 8
+    w = (RNG.standard_normal((m, k)) * 0.02).astype(np.float32)
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    qw = ref.quantize_weights(t, w)
+    y = ref.mul_mat(t, qw, m, k, x)
+    wd = ref.dequantize(t, qw, m * k).reshape(m, k).astype(np.float64)
+    at = ref.Q8_0 if t == ref.Q8_0 else ref.Q8_K
+    xd = np.stack([ref.dequantize(at, ref.quantize_act(at, x[j]), k) for j in range(n)]).astype(np.float64)
+    want = xd @ wd.T
+    assert np.allclose(y, want, rtol=1e-5, atol=1e-5)
+    for j in range(n):
+        yj = ref.mul_mat(t, qw, m, k, x[j:j + 1])
+        assert np.array_equal(yj[0], y[j])
+
+
+# ------------------------------------------------------------- row ops ---
+
+def test_norms_closed_form(ref):
+    x = RNG.standard_normal((5, 1024)).astype(np.float32) * 3 + 1
+    eps = 1e-6
+    want = x / np.sqrt((x.astype(np.float64) ** 2).mean(1, keepdims=True) + eps)
+    assert np.allclose(ref.rms_norm(x, eps), want, rtol=2e-6, atol=1e-6)
+    mu = x.astype(np.float64).mean(1, keepdims=True)
+    want = (x - mu) / np.sqrt(((x - mu) ** 2).mean(1, keepdims=True) + 1e-5)
+    assert np.allclose(ref.norm(x, 1e-5), want, rtol=2e-6, atol=1e-6)
+
+
+def test_rope_neox_closed_form(ref):
+    t, h, d = 6, 3, 128
+    x = RNG.standard_normal((t, h, d)).astype(np.float32)
+    pos = np.array([0, 1, 7, 100, 383, 1023], np.int32)
+    y = ref.rope_neox(x, pos, d, 1e6)
+    assert np.array_equal(y[0], x[0])  # position 0 is the identity
+    half = d // 2
+    inv = 1e6 ** (-2.0 * np.arange(half) / d)
+    ang = pos[:, None].astype(np.float64) * inv[None, :]
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    x0, x1 = x[..., :half].astype(np.float64), x[..., half:].astype(np.float64)
+    want = np.concatenate([x0 * c - x1 * s, x0 * s + x1 * c], -1)
+    # theta is built by repeated f32 multiplication, as ggml does: a few ulp of angle
+    assert np.allclose(y, want, rtol=1e-4, atol=1e-4)
+    y2 = ref.rope_neox(x, pos, 64, 1e6)  # partial rotation passes the tail through
+    assert np.array_equal(y2[..., 64:], x[..., 64:])
+
+
+def test_activations_closed_form(ref):
+    x = np.linspace(-12, 12, 2001).astype(np.float32)
+    assert np.allclose(ref.silu(x), x / (1 + np.exp(-x.astype(np.float64))), rtol=1e-6, atol=1e-7)
+    g = ref.gelu(x)
+    xh = x.astype(np.float16).astype(np.float64)
+    exact = 0.5 * xh * (1 + np.tanh(np.sqrt(2 / np.pi) * xh * (1 + 0.044715 * xh * xh)))
+    table = exact.astype(np.float16).astype(np.float32)
+    inner = (x > -10) & (x < 10)
+    # f16 table value: within one f16 ulp of f16(gelu(f16(x))); in the far
+    # negative tail the f32 formula's 1 + tanh cancellation adds ~|x| f32 ulps
+    ulp = np.abs(np.spacing(table.astype(np.float16))).astype(np.float32)
+    assert np.all(np.abs(g[inner] - table[inner]) <= ulp[inner] + 8 * np.abs(x[inner]) * 2.0 ** -24)
+    assert np.all(g[x <= -10] == 0) and np.array_equal(g[x >= 10], x[x >= 10])
+
+
+def test_soft_max_and_argmax(ref):
+    x = RNG.standard_normal((4, 37)).astype(np.float32)
+    mask = np.zeros((4, 37), np.float16)
+    mask[:, 30:] = -np.inf
+    y = ref.soft_max_ext(x, mask.view(np.uint16), 0.5)
+    z = x.astype(np.float64) * 0.5 + mask.astype(np.float64)
+    want = np.exp(z - z.max(1, keepdims=True))
+    want /= want.sum(1, keepdims=True)
+    assert np.allclose(y, want, rtol=1e-6, atol=1e-7)
+    v = np.array([1.0, 3.0, 2.0, 3.0, -1.0], np.float32)
+    assert ref.argmax_first(v) == 1 and ref.argmax_last(v) == 3
+
+
+# ------------------------------------------------------- flash attention --
+
+def textbook_attention(q, k, v, mask, scale, group):
+    n_q, hq, d = q.shape
+    out = np.zeros((n_q, hq, d))
+    for i in range(n_q):
+        for h in range(hq):
+            kv = h // group
+            s = (k[kv].astype(np.float64) @ q[i, h].astype(np.float64)) * scale
+            if mask is not None:
+                s = s + mask[i].astype(np.float64)
+            if np.all(np.isinf(s)):
+                continue
+            p = np.exp(s - s.max())
+            out[i, h] = (p @ v[kv].astype(np.float64)) / p.sum()
+    return out
+
+
+def test_flash_attn_textbook_gqa_and_masking(ref):
+    n_q, hq, hkv, n_kv, d = 3, 4, 2, 40, 64
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((n_q, n_kv), np.float16)
+    mask[0, 25:] = -np.inf
+    mask[1, :] = -np.inf  # fully masked row -> zeros
+    scale = 1 / math.sqrt(d)
+    qh = q.astype(np.float16).astype(np.float32)
+    want = textbook_attention(qh, k, v, mask, scale, hq // hkv)
+    exact = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, fidelity=False)
+    assert np.allclose(exact, textbook_attention(q, k, v, mask, scale, 2), rtol=1e-5, atol=1e-5)
+    fid = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, fidelity=True)
+    assert np.abs(fid - want).max() <= 2e-3 * np.abs(want).max()
+    assert not fid[1].any() and not exact[1].any()
+    # GQA == explicit repetition of each kv head over its query group
+    krep = np.repeat(k, 2, axis=0)
+    vrep = np.repeat(v, 2, axis=0)
+    rep = ref.flash_attn(q, krep.view(np.uint16), vrep.view(np.uint16), mask.view(np.uint16), scale, fidelity=False)
+    assert np.array_equal(rep, exact)
+    # masked positions contribute nothing: garbage there changes nothing
+    k2, v2 = k.copy(), v.copy()
+    k2[:, 25:] = 100
+    v2[:, 25:] = -50
+    m0 = np.zeros((1, n_kv), np.float16)
+    m0[0, 25:] = -np.inf
+    a = ref.flash_attn(q[:1], k.view(np.uint16), v.view(np.uint16), m0.view(np.uint16), scale, fidelity=False)
+    b = ref.flash_attn(q[:1], k2.view(np.uint16), v2.view(np.uint16), m0.view(np.uint16), scale, fidelity=False)
+    assert np.array_equal(a, b)
