@@ -1,0 +1,102 @@
+/*
+ * openasr_models.h -- the decoder families on the quantized decoder path, as
+ * the OpenASR host drives them through ggml (libopenasr-models.so). These are
+ * the host-side callers of the backend plugin: they build the same ggml graphs
+ * the Rust emitters build and run the same greedy step loops.
+ *
+ * Qwen3 LLM decoder: compose_llm_decoder_layer_stack / llm_layer
+ *   (crates/openasr-core/src/nn/decoder.rs:1850-2331), persistent reusable
+ *   decode graph with a resident f16 KV arena and per-step token / row /
+ *   position / mask uploads (models/qwen/llm_transformer.rs:5169-5657),
+ *   fused logits head with first-max top-1 (llm_transformer.rs:2096-2115),
+ *   prefill in chunks of at most 256 query tokens (llm_transformer.rs:60,
+ *   4016-4200).
+ * Greedy n-gram loop guard: models/seq2seq_greedy_decode.rs:19-58, 569-605.
+ *
+ * Weights are synthesised (seeded N(0, 0.02), then quantized with
+ * ggml_quantize_chunk); the host copy stays available so a CPU checker can
+ * consume exactly the bytes the device holds.
+ */
+#ifndef OPENASR_MODELS_H
+#define OPENASR_MODELS_H
+
+#include "ggml_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct {
+    int d_model;
+    int n_layers;
+    int n_head;
+    int n_kv_head;
+    int head_dim;
+    int ffn;
+    int vocab;
+    float rope_theta;
+    float rms_eps;
+    int wtype; /* GGML_TYPE_Q8_0 or GGML_TYPE_Q4_K for every matrix and the tied embedding */
+    uint64_t seed;
+} oa_qwen_config;
+
+enum oa_qwen_tensor_kind {
+    OA_QWEN_TOKEN_EMBD = 0, /* [vocab rows of d_model], wtype; tied with the lm_head */
+    OA_QWEN_OUTPUT_NORM,    /* f32 [d_model] */
+    OA_QWEN_ATTN_NORM,      /* f32 [d_model] */
+    OA_QWEN_QKV,            /* wtype, rows q|k|v of d_model: the fused projection */
+    OA_QWEN_Q_NORM,         /* f32 [head_dim] */
+    OA_QWEN_K_NORM,         /* f32 [head_dim] */
+    OA_QWEN_O,              /* wtype, d_model rows of n_head*head_dim */
+    OA_QWEN_FFN_NORM,       /* f32 [d_model] */
+    OA_QWEN_GATE,           /* wtype, ffn rows of d_model */
+    OA_QWEN_UP,             /* wtype, ffn rows of d_model */
+    OA_QWEN_DOWN            /* wtype, d_model rows of ffn */
+};
+
+typedef struct oa_qwen_weights oa_qwen_weights;
+typedef struct oa_qwen_model oa_qwen_model;
+typedef struct oa_qwen_session oa_qwen_session;
+
+oa_qwen_weights * oa_qwen_weights_synthesize(const oa_qwen_config * cfg);
+void oa_qwen_weights_free(oa_qwen_weights * w);
+/* host bytes of one tensor (layer ignored for TOKEN_EMBD / OUTPUT_NORM) */
+const void * oa_qwen_weights_tensor(const oa_qwen_weights * w, int layer, int kind, size_t * nbytes);
+
+oa_qwen_model * oa_qwen_model_create(ggml_backend_t backend, const oa_qwen_weights * w);
+void oa_qwen_model_free(oa_qwen_model * m);
+
+oa_qwen_session * oa_qwen_session_create(oa_qwen_model * m, int n_seq, int max_positions);
+void oa_qwen_session_free(oa_qwen_session * s);
+int oa_qwen_session_position(const oa_qwen_session * s, int seq);
+
+/* Prefill T positions of every sequence (chunked internally at 256) from
+ * hidden inputs [n_seq][T][d_model] (an audio-embedding prefix) or token ids
+ * [n_seq][T]. top1_out (optional, [n_seq]) gets the first-max argmax of the
+ * last position's logits. Returns a ggml_status. */
+int oa_qwen_prefill_embeddings(oa_qwen_session * s, const float * emb, int T, int32_t * top1_out);
+int oa_qwen_prefill_tokens(oa_qwen_session * s, const int32_t * tokens, int T, int32_t * top1_out);
+
+/* One decode step for every sequence: tokens [n_seq] in, top-1 [n_seq] out
+ * (lowest index on ties). logits_out (optional) gets [n_seq][vocab]. */
+int oa_qwen_decode_step(oa_qwen_session * s, const int32_t * tokens, int32_t * top1_out, float * logits_out);
+
+/* Greedy loop: feeds each step's top-1 back in for n_steps steps.
+ * out_tokens [n_steps][n_seq]; step_ms (optional) wall time per step. */
+int oa_qwen_generate(oa_qwen_session * s, const int32_t * first_tokens, int n_steps, int32_t * out_tokens,
+                     double * step_ms);
+
+/* Device KV cache of one layer for one sequence, f16 bits [n_kv_head][max_positions][head_dim] each. */
+int oa_qwen_read_kv(const oa_qwen_session * s, int layer, int seq, uint16_t * k_out, uint16_t * v_out);
+
+/* Degenerate n-gram guard (seq2seq_greedy_decode.rs:569-605): smallest n in
+ * 1..max_ngram whose trailing n-gram repeats at least 8 (n=1), 6 (n=2) or 4
+ * (n>=3) times back to back. Returns the length to keep (truncating the run
+ * to one occurrence), or -1 when no loop is detected. */
+int oa_detect_degenerate_ngram(const int32_t * tokens, int len, int max_ngram, int * ngram_len, int * repeats);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -2,6 +2,7 @@
 
   openasr_amd/lib/libggml-base.so    host-side ggml-base (g++)
   openasr_amd/lib/libggml-mi355x.so  the gfx950 backend plugin (hipcc)
+  openasr_amd/lib/libopenasr-models.so  decoder graph builders / step loops (g++)
   oracle/build/libggml_cpu_ref.so    the CPU oracle (gcc; test infrastructure)
 
 Run `python -m openasr_amd.build` (or __graft_entry__.build()). Every call
@@ -31,6 +32,9 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # results must not depend on whether the compiler fuses a*b+c: the CPU
+    # reference evaluates every expression with separate roundings
+    "-ffp-contract=off",
     "-Wno-unused-result",
 ]
 
@@ -56,6 +60,14 @@ def build_base(fp: str) -> Path:
     srcs = sorted(str(p) for p in (PKG / "host").glob("*.cpp"))
     _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", f"-I{INCLUDE}",
           f'-DOPENASR_HOST_ABI_FINGERPRINT="{fp}"', *srcs, "-o", str(out), "-ldl"])
+    return out
+
+
+def build_models() -> Path:
+    out = LIB / "libopenasr-models.so"
+    srcs = sorted(str(p) for p in (PKG / "decoders").glob("*.cpp"))
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", f"-I{INCLUDE}", *srcs, "-o", str(out),
+          f"-L{LIB}", "-lggml-base", "-Wl,-rpath,$ORIGIN"])
     return out
 
 
@@ -94,6 +106,7 @@ def build_all(plugin: bool = True) -> dict[str, Path]:
     OBJ.mkdir(parents=True, exist_ok=True)
     fp = host_abi_fingerprint()
     built = {"base": build_base(fp), "oracle": build_oracle()}
+    built["models"] = build_models()
     if plugin:
         built["plugin"] = build_plugin(fp)
     return built

@@ -85,7 +85,7 @@ void launch_scale(const tview & d, const tview & a, float sc, float bias, hipStr
 // tanhf and uploaded once, so device and host agree bit for bit.
 __device__ __forceinline__ float unary_apply(int op, float x, const uint16_t * gelu_table) {
     switch (op) {
-        case GGML_UNARY_OP_SILU: return x / (1.0f + expf(-x));
+        case GGML_UNARY_OP_SILU: return x / (1.0f + expf_det(-x));
         case GGML_UNARY_OP_GELU: {
             if (x <= -10.0f) return 0.0f;
             if (x >= 10.0f) return x;
@@ -94,8 +94,8 @@ __device__ __forceinline__ float unary_apply(int op, float x, const uint16_t * g
         case GGML_UNARY_OP_GELU_ERF: return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
         case GGML_UNARY_OP_RELU: return x > 0.0f ? x : 0.0f;
         case GGML_UNARY_OP_TANH: return tanhf(x);
-        case GGML_UNARY_OP_SIGMOID: return 1.0f / (1.0f + expf(-x));
-        case GGML_UNARY_OP_EXP: return expf(x);
+        case GGML_UNARY_OP_SIGMOID: return 1.0f / (1.0f + expf_det(-x));
+        case GGML_UNARY_OP_EXP: return expf_det(x);
         case GGML_UNARY_OP_NEG: return -x;
         case GGML_UNARY_OP_ABS: return fabsf(x);
         default: return x;
@@ -124,7 +124,7 @@ __global__ void k_silu_mul(tview d, tview g, tview u, int64_t n) {
         unravel(idx, d.ne, i0, i1, i2, i3);
         const float x = *(const float *) (g.data + offs4(g, i0, i1, i2, i3));
         const float y = *(const float *) (u.data + offs4(u, i0 % u.ne[0], i1 % u.ne[1], i2 % u.ne[2], i3 % u.ne[3]));
-        *(float *) (d.data + offs4(d, i0, i1, i2, i3)) = (x / (1.0f + expf(-x))) * y;
+        *(float *) (d.data + offs4(d, i0, i1, i2, i3)) = (x / (1.0f + expf_det(-x))) * y;
     }
 }
 
@@ -147,18 +147,19 @@ __global__ __launch_bounds__(256) void k_norm(tview d, tview a, int mode, float 
     const float * x = (const float *) (a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3]);
     float * y = (float *) (d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]);
     const int64_t n = a.ne[0];
+    // sums in f64 and one rounding, as ggml-cpu's ggml_float accumulators
     float mean = 0.0f;
     if (mode == 1) {
-        float s = 0.0f;
-        for (int64_t i = lane; i < n; i += 64) s += x[i];
-        mean = wave_sum(s) / (float) n;
+        double s = 0.0;
+        for (int64_t i = lane; i < n; i += 64) s += (double) x[i];
+        mean = (float) (wave_sum_d(s) / (double) n);
     }
-    float s2 = 0.0f;
+    double s2 = 0.0;
     for (int64_t i = lane; i < n; i += 64) {
         const float v = x[i] - mean;
-        s2 += v * v;
+        s2 += (double) (v * v);
     }
-    const float var = wave_sum(s2) / (float) n;
+    const float var = (float) (wave_sum_d(s2) / (double) n);
     const float scale = 1.0f / sqrtf(var + eps);
     const float * wr = has_w ? (const float *) (w.data + (i1 % w.ne[1]) * w.nb[1] + (i2 % w.ne[2]) * w.nb[2] +
                                                 (i3 % w.ne[3]) * w.nb[3])
@@ -202,7 +203,10 @@ __global__ void k_rope(tview d, tview a, const int32_t * pos, int n_dims, int mo
         float theta = (float) pos[i2];
         for (int64_t k = 0; k < ic; k++) theta *= theta_scale;
         const float th = freq_scale * theta;
-        const float c = cosf(th) * attn_factor, sn = sinf(th) * attn_factor;
+        float sn, c;
+        sincosf_det(th, sn, c);
+        c *= attn_factor;
+        sn *= attn_factor;
         const int64_t j0 = mode == GGML_ROPE_TYPE_NEOX ? ic : 2 * ic;
         const int64_t j1 = mode == GGML_ROPE_TYPE_NEOX ? ic + half : 2 * ic + 1;
         const char * xr = a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3];
@@ -354,15 +358,15 @@ __global__ __launch_bounds__(256) void k_soft_max(tview d, tview a, tview mask, 
         mx = fmaxf(mx, v);
     }
     mx = wave_max(mx);
-    float sum = 0.0f;
+    double sum = 0.0;
     for (int64_t i = lane; i < n; i += 64) {
         const float v = x[i] * scale + (mp ? half_bits_to_float(mp[i]) : 0.0f);
-        const float e = expf(v - mx);
+        const float e = expf_det(v - mx);
         y[i] = e;
-        sum += e;
+        sum += (double) e;
     }
-    sum = wave_sum(sum);
-    const float inv = 1.0f / sum;
+    sum = wave_sum_d(sum);
+    const float inv = (float) (1.0 / sum);
     for (int64_t i = lane; i < n; i += 64) y[i] *= inv;
 }
 

@@ -8,6 +8,11 @@
 // 128-bit loads, the team reduces its partial sums with cross-lane shuffles,
 // and waves walk the rows grid-stride. Rows of one wave are adjacent, so a
 // wave reads one contiguous run of weight memory per step.
+//
+// Block dots are exact integers; the scaled block terms are summed in f64 and
+// rounded to f32 once, so the result does not depend on the lane / team
+// split -- the CPU reference sums the same terms sequentially and gets the
+// same f32 value.
 #include "../mi355x_common.h"
 #include "../ops.h"
 
@@ -37,9 +42,9 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const char * __restrict__ W, i
     for (int64_t row = team; row < M; row += team_stride) {
         const char * wr = W + row * row_bytes;
         const uint16_t * ws = (const uint16_t *) (wr + K);
-        float acc[NC];
+        double acc[NC];
 #pragma unroll
-        for (int n = 0; n < NC; n++) acc[n] = 0.0f;
+        for (int n = 0; n < NC; n++) acc[n] = 0.0;
         for (int c = 0; c < cpl; c++) {
             const int64_t e = (int64_t) (li + c * LPR) * 16;
             const int64_t b = e >> 5;
@@ -49,14 +54,15 @@ __global__ __launch_bounds__(256) void k_mmv_q8_0(const char * __restrict__ W, i
             for (int n = 0; n < NC; n++) {
                 const int4 a = *(const int4 *) (aq + n * K + e);
                 const int s = dot16(w, a);
-                acc[n] += (float) s * (dw * ad[n * nblk + b]);
+                // d_w * d_a of two halves is exact in f32, the term exact in f64
+                acc[n] += (double) s * (double) (dw * ad[n * nblk + b]);
             }
         }
 #pragma unroll
         for (int n = 0; n < NC; n++) {
-            float v = acc[n];
+            double v = acc[n];
             for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-            if (li == 0) *(float *) (dst + n * dst_nb1 + row * 4) = v;
+            if (li == 0) *(float *) (dst + n * dst_nb1 + row * 4) = (float) v;
         }
     }
 }
@@ -90,9 +96,9 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const char * __restrict__ W, i
     const int64_t nsb = K / 256;
     for (int64_t row = team; row < M; row += team_stride) {
         const char * wr = W + row * row_bytes;
-        float acc[NC];
+        double acc[NC];
 #pragma unroll
-        for (int n = 0; n < NC; n++) acc[n] = 0.0f;
+        for (int n = 0; n < NC; n++) acc[n] = 0.0;
         for (int c = 0; c < cpl; c++) {
             const int ci = li + c * LPR;
             const int sb = ci >> 3;
@@ -123,15 +129,15 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const char * __restrict__ W, i
                 const int16_t * bs = abs_ + n * (K / 16) + sb * 16;
                 const int isum = dot16(lo, a_lo) * sc_lo + dot16(hi, a_hi) * sc_hi;
                 const int msum = (int) bs[4 * g + h] * m_lo + (int) bs[4 * g + 2 + h] * m_hi;
-                const float da = ad[n * nsb + sb];
-                acc[n] += (dw * da) * (float) isum - (dmw * da) * (float) msum;
+                const double da = (double) ad[n * nsb + sb];
+                acc[n] += ((double) dw * da) * (double) isum - ((double) dmw * da) * (double) msum;
             }
         }
 #pragma unroll
         for (int n = 0; n < NC; n++) {
-            float v = acc[n];
+            double v = acc[n];
             for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
-            if (li == 0) *(float *) (dst + n * dst_nb1 + row * 4) = v;
+            if (li == 0) *(float *) (dst + n * dst_nb1 + row * 4) = (float) v;
         }
     }
 }

@@ -88,4 +88,80 @@ __device__ __forceinline__ float group_max(float v) {
 __device__ __forceinline__ float wave_sum(float v) { return group_sum<kWave>(v); }
 __device__ __forceinline__ float wave_max(float v) { return group_max<kWave>(v); }
 
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+// exp and sin/cos as a fixed sequence of IEEE double operations rounded once
+// to f32 (the library is built without FMA contraction). The CPU reference
+// evaluates the identical sequence, so host and device agree bit for bit and
+// both are within one rounding of the exact value.
+__device__ __forceinline__ float expf_det(float x) {
+    if (x != x) return x;
+    if (x > 88.72284f) return INFINITY;
+    if (x < -103.97208f) return 0.0f;
+    const double xd = (double) x;
+    const double k = rint(xd * 1.4426950408889634074);
+    const double r = (xd - k * 0.69314718055994528623) - k * 2.3190468138462996154e-17;
+    double p = 1.0 / 479001600.0;
+    p = p * r + 1.0 / 39916800.0;
+    p = p * r + 1.0 / 3628800.0;
+    p = p * r + 1.0 / 362880.0;
+    p = p * r + 1.0 / 40320.0;
+    p = p * r + 1.0 / 5040.0;
+    p = p * r + 1.0 / 720.0;
+    p = p * r + 1.0 / 120.0;
+    p = p * r + 1.0 / 24.0;
+    p = p * r + 1.0 / 6.0;
+    p = p * r + 0.5;
+    p = p * r + 1.0;
+    p = p * r + 1.0;
+    return (float) ldexp(p, (int) k);
+}
+
+__device__ __forceinline__ void sincosf_det(float x, float & s_out, float & c_out) {
+    const double xd = (double) x;
+    const double k = rint(xd * 0.63661977236758134308);
+    const double r = (xd - k * 1.5707963267341256458) - k * 6.0771005065061922341e-11;
+    const double r2 = r * r;
+    double s = -1.0 / 355687428096000.0;
+    s = s * r2 + 1.0 / 1307674368000.0;
+    s = s * r2 - 1.0 / 6227020800.0;
+    s = s * r2 + 1.0 / 39916800.0;
+    s = s * r2 - 1.0 / 362880.0;
+    s = s * r2 + 1.0 / 5040.0;
+    s = s * r2 - 1.0 / 120.0;
+    s = s * r2 + 1.0 / 6.0;
+    s = r - (r * r2) * s;
+    double c = 1.0 / 6402373705728000.0;
+    c = c * r2 - 1.0 / 20922789888000.0;
+    c = c * r2 + 1.0 / 87178291200.0;
+    c = c * r2 - 1.0 / 479001600.0;
+    c = c * r2 + 1.0 / 3628800.0;
+    c = c * r2 - 1.0 / 40320.0;
+    c = c * r2 + 1.0 / 720.0;
+    c = c * r2 - 1.0 / 24.0;
+    c = c * r2 + 0.5;
+    c = 1.0 - r2 * c;
+    const int q = (int) (((long long) k) & 3);
+    double so, co;
+    if (q == 0) {
+        so = s;
+        co = c;
+    } else if (q == 1) {
+        so = c;
+        co = -s;
+    } else if (q == 2) {
+        so = -s;
+        co = -c;
+    } else {
+        so = -c;
+        co = s;
+    }
+    s_out = (float) so;
+    c_out = (float) co;
+}
+
 }  // namespace mi355x

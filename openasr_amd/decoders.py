@@ -1,0 +1,212 @@
+"""ctypes view of libopenasr-models.so (include/openasr_models.h): the decoder
+families' graph builders and greedy step loops, driving the backend through
+the ggml C ABI. Also the workload configurations the path is measured on.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import ggml as g
+
+MODELS_PATH = g.LIB_DIR / "libopenasr-models.so"
+
+
+class QwenConfig(C.Structure):
+    _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("n_kv_head", C.c_int),
+                ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("rope_theta", C.c_float),
+                ("rms_eps", C.c_float), ("wtype", C.c_int), ("seed", C.c_uint64)]
+
+
+# Qwen3-0.6B / 1.7B shapes (hidden, layers, heads, kv heads, head_dim, ffn, vocab)
+QWEN3_06B = dict(d_model=1024, n_layers=28, n_head=16, n_kv_head=8, head_dim=128, ffn=3072, vocab=151936)
+QWEN3_17B = dict(d_model=2048, n_layers=28, n_head=16, n_kv_head=8, head_dim=128, ffn=6144, vocab=151936)
+
+# tensor kinds (enum oa_qwen_tensor_kind)
+(TOKEN_EMBD, OUTPUT_NORM, ATTN_NORM, QKV, Q_NORM, K_NORM, O, FFN_NORM, GATE, UP, DOWN) = range(11)
+LAYER_KINDS = (ATTN_NORM, QKV, Q_NORM, K_NORM, O, FFN_NORM, GATE, UP, DOWN)
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    g.base()
+    if not MODELS_PATH.exists():
+        raise RuntimeError(f"{MODELS_PATH} is missing: run `python -m openasr_amd.build` first")
+    L = C.CDLL(str(MODELS_PATH))
+    vp, i, i32p = C.c_void_p, C.c_int, C.POINTER(C.c_int32)
+
+    def s(name, res, *args):
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = list(args)
+
+    s("oa_qwen_weights_synthesize", vp, C.POINTER(QwenConfig))
+    s("oa_qwen_weights_free", None, vp)
+    s("oa_qwen_weights_tensor", vp, vp, i, i, C.POINTER(C.c_size_t))
+    s("oa_qwen_model_create", vp, vp, vp)
+    s("oa_qwen_model_free", None, vp)
+    s("oa_qwen_session_create", vp, vp, i, i)
+    s("oa_qwen_session_free", None, vp)
+    s("oa_qwen_session_position", i, vp, i)
+    s("oa_qwen_prefill_embeddings", i, vp, vp, i, vp)
+    s("oa_qwen_prefill_tokens", i, vp, vp, i, vp)
+    s("oa_qwen_decode_step", i, vp, vp, vp, vp)
+    s("oa_qwen_generate", i, vp, vp, i, vp, vp)
+    s("oa_qwen_read_kv", i, vp, i, i, vp, vp)
+    s("oa_detect_degenerate_ngram", i, vp, i, i, vp, vp)
+    _lib = L
+    return L
+
+
+class QwenWeights:
+    """Host copy of a synthesised Qwen3-shaped decoder (quantized bytes)."""
+
+    def __init__(self, wtype: int, seed: int = 1234, rope_theta: float = 1e6, rms_eps: float = 1e-6, **shape):
+        self.cfg = QwenConfig(rope_theta=rope_theta, rms_eps=rms_eps, wtype=wtype, seed=seed, **shape)
+        self.ptr = lib().oa_qwen_weights_synthesize(C.byref(self.cfg))
+        if not self.ptr:
+            raise RuntimeError("weight synthesis failed")
+
+    def tensor(self, layer: int, kind: int) -> tuple[int, int]:
+        n = C.c_size_t(0)
+        p = lib().oa_qwen_weights_tensor(self.ptr, layer, kind, C.byref(n))
+        return p, n.value
+
+    def pointer_table(self) -> list[int]:
+        """[tok_embd, out_norm, per layer: attn_norm, qkv, q_norm, k_norm, o, ffn_norm, gate, up, down]"""
+        t = [self.tensor(-1, TOKEN_EMBD)[0], self.tensor(-1, OUTPUT_NORM)[0]]
+        for layer in range(self.cfg.n_layers):
+            t += [self.tensor(layer, k)[0] for k in LAYER_KINDS]
+        return t
+
+    def free(self):
+        if self.ptr:
+            lib().oa_qwen_weights_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class QwenModel:
+    def __init__(self, weights: QwenWeights, backend):
+        self.weights = weights
+        self.cfg = weights.cfg
+        self.ptr = lib().oa_qwen_model_create(backend, weights.ptr)
+        if not self.ptr:
+            raise RuntimeError("model upload failed")
+
+    def session(self, n_seq: int, max_positions: int) -> "QwenSession":
+        return QwenSession(self, n_seq, max_positions)
+
+    def free(self):
+        if self.ptr:
+            lib().oa_qwen_model_free(self.ptr)
+            self.ptr = None
+
+
+class QwenSession:
+    def __init__(self, model: QwenModel, n_seq: int, max_positions: int):
+        self.model = model
+        self.n_seq = n_seq
+        self.max_positions = max_positions
+        self.ptr = lib().oa_qwen_session_create(model.ptr, n_seq, max_positions)
+        if not self.ptr:
+            raise RuntimeError("session (KV arena) allocation failed")
+
+    def _check(self, st: int, what: str):
+        if st != 0:
+            raise RuntimeError(f"{what} failed with ggml status {st}")
+
+    def prefill_embeddings(self, emb: np.ndarray) -> np.ndarray:
+        emb = np.ascontiguousarray(emb, dtype=np.float32)  # [n_seq, T, d]
+        top1 = np.zeros(self.n_seq, np.int32)
+        self._check(lib().oa_qwen_prefill_embeddings(self.ptr, emb.ctypes.data, emb.shape[1], top1.ctypes.data),
+                    "prefill (embeddings)")
+        return top1
+
+    def prefill_tokens(self, tokens: np.ndarray) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)  # [n_seq, T]
+        top1 = np.zeros(self.n_seq, np.int32)
+        self._check(lib().oa_qwen_prefill_tokens(self.ptr, tokens.ctypes.data, tokens.shape[1], top1.ctypes.data),
+                    "prefill (tokens)")
+        return top1
+
+    def step(self, tokens: np.ndarray, want_logits: bool = False):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        top1 = np.zeros(self.n_seq, np.int32)
+        logits = np.zeros((self.n_seq, self.model.cfg.vocab), np.float32) if want_logits else None
+        self._check(lib().oa_qwen_decode_step(self.ptr, tokens.ctypes.data, top1.ctypes.data,
+                                              logits.ctypes.data if want_logits else None), "decode step")
+        return (top1, logits) if want_logits else top1
+
+    def generate(self, first: np.ndarray, n_steps: int):
+        first = np.ascontiguousarray(first, dtype=np.int32)
+        out = np.zeros((n_steps, self.n_seq), np.int32)
+        ms = np.zeros(n_steps, np.float64)
+        self._check(lib().oa_qwen_generate(self.ptr, first.ctypes.data, n_steps, out.ctypes.data, ms.ctypes.data),
+                    "generate")
+        return out, ms
+
+    def read_kv(self, layer: int, seq: int):
+        c = self.model.cfg
+        shape = (c.n_kv_head, self.max_positions, c.head_dim)
+        k = np.zeros(shape, np.uint16)
+        v = np.zeros(shape, np.uint16)
+        self._check(lib().oa_qwen_read_kv(self.ptr, layer, seq, k.ctypes.data, v.ctypes.data), "read_kv")
+        return k, v
+
+    def position(self, seq: int = 0) -> int:
+        return lib().oa_qwen_session_position(self.ptr, seq)
+
+    def free(self):
+        if self.ptr:
+            lib().oa_qwen_session_free(self.ptr)
+            self.ptr = None
+
+
+def detect_degenerate_ngram(tokens, max_ngram: int = 8):
+    t = np.ascontiguousarray(tokens, dtype=np.int32)
+    n, r = C.c_int(0), C.c_int(0)
+    keep = lib().oa_detect_degenerate_ngram(t.ctypes.data, len(t), max_ngram, C.byref(n), C.byref(r))
+    return None if keep < 0 else (keep, n.value, r.value)
+
+
+@dataclass
+class QwenWorkload:
+    """One of the decode configurations the path is measured on."""
+    name: str
+    shape: dict
+    wtype: int
+    n_seq: int
+    prefix: int          # audio-embedding prefix positions, N(0,1)
+    prompt: int          # prompt tokens after the prefix
+    decode: int          # greedy tokens
+    max_positions: int
+
+
+WORKLOADS = {
+    "qwen3-0.6b-q8_0-b1": QwenWorkload("qwen3-0.6b-q8_0-b1", QWEN3_06B, g.Q8_0, 1, 375, 8, 256, 1024),
+    "qwen3-0.6b-q4_K-b8": QwenWorkload("qwen3-0.6b-q4_K-b8", QWEN3_06B, g.Q4_K, 8, 375, 8, 512, 1024),
+    "qwen3-1.7b-q4_K-b8": QwenWorkload("qwen3-1.7b-q4_K-b8", QWEN3_17B, g.Q4_K, 8, 3000, 8, 1024, 4096),
+}
+
+
+def workload_inputs(w: QwenWorkload, seed: int = 77):
+    """seeded N(0,1) prefixes [n_seq, prefix, d] and prompt ids [n_seq, prompt]"""
+    d = w.shape["d_model"]
+    emb = np.stack([g.synth_normal(seed, 1000 + s, w.prefix * d).reshape(w.prefix, d) for s in range(w.n_seq)])
+    prompt = np.zeros((w.n_seq, w.prompt), np.int32)
+    for s in range(w.n_seq):
+        g.base().oa_synth_uniform_i32(seed, 2000 + s, w.prompt, w.shape["vocab"], prompt[s].ctypes.data)
+    return emb, prompt

@@ -562,6 +562,9 @@ bool ggml_gallocr_alloc_graph(ggml_gallocr_t galloc, struct ggml_cgraph * graph)
     for (int i = 0; i < graph->n_leafs; i++) consider(graph->leafs[i]);
     for (int i = 0; i < graph->n_nodes; i++) {
         for (int s = 0; s < GGML_MAX_SRC; s++) consider(graph->nodes[i]->src[s]);
+        // a view node whose base is not a graph node (set_rows into a cache
+        // tensor of the same context) still needs the base to have storage
+        consider(graph->nodes[i]->view_src);
         consider(graph->nodes[i]);
     }
     size_t total = 0;

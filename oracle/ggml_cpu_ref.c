@@ -76,6 +76,72 @@ void ref_fp16_to_fp32_row(const uint16_t * x, float * y, int64_t n) {
 /* round half to even, as ggml's nearest_int (magic-number add) does */
 static inline int nearest_even(float v) { return (int) rintf(v); }
 
+/* ------------------------------------------------- deterministic math -- */
+
+/* exp and sin/cos evaluated in double with a fixed sequence of IEEE
+ * operations (no FMA contraction: this file is built with
+ * -ffp-contract=off), then rounded once to f32. The device evaluates the
+ * identical sequence, so both sides produce the same bits; accuracy is
+ * within one rounding of the exact value (checked against libm in the
+ * oracle tests). ggml-cpu's own vectorised expf is an ISA-specific
+ * approximation of the same function. */
+float ref_expf_det(float x) {
+    if (x != x) return x;
+    if (x > 88.72284f) return INFINITY;
+    if (x < -103.97208f) return 0.0f;
+    const double xd = (double) x;
+    const double k = rint(xd * 1.4426950408889634074);
+    const double r = (xd - k * 0.69314718055994528623) - k * 2.3190468138462996154e-17;
+    double p = 1.0 / 479001600.0;
+    p = p * r + 1.0 / 39916800.0;
+    p = p * r + 1.0 / 3628800.0;
+    p = p * r + 1.0 / 362880.0;
+    p = p * r + 1.0 / 40320.0;
+    p = p * r + 1.0 / 5040.0;
+    p = p * r + 1.0 / 720.0;
+    p = p * r + 1.0 / 120.0;
+    p = p * r + 1.0 / 24.0;
+    p = p * r + 1.0 / 6.0;
+    p = p * r + 0.5;
+    p = p * r + 1.0;
+    p = p * r + 1.0;
+    return (float) ldexp(p, (int) k);
+}
+
+void ref_sincosf_det(float x, float * s_out, float * c_out) {
+    const double xd = (double) x;
+    const double k = rint(xd * 0.63661977236758134308);
+    const double r = (xd - k * 1.5707963267341256458) - k * 6.0771005065061922341e-11;
+    const double r2 = r * r;
+    double s = -1.0 / 355687428096000.0;
+    s = s * r2 + 1.0 / 1307674368000.0;
+    s = s * r2 - 1.0 / 6227020800.0;
+    s = s * r2 + 1.0 / 39916800.0;
+    s = s * r2 - 1.0 / 362880.0;
+    s = s * r2 + 1.0 / 5040.0;
+    s = s * r2 - 1.0 / 120.0;
+    s = s * r2 + 1.0 / 6.0;
+    s = r - (r * r2) * s;
+    double c = 1.0 / 6402373705728000.0;
+    c = c * r2 - 1.0 / 20922789888000.0;
+    c = c * r2 + 1.0 / 87178291200.0;
+    c = c * r2 - 1.0 / 479001600.0;
+    c = c * r2 + 1.0 / 3628800.0;
+    c = c * r2 - 1.0 / 40320.0;
+    c = c * r2 + 1.0 / 720.0;
+    c = c * r2 - 1.0 / 24.0;
+    c = c * r2 + 0.5;
+    c = 1.0 - r2 * c;
+    const int q = (int) (((long long) k) & 3);
+    double so, co;
+    if (q == 0) { so = s; co = c; }
+    else if (q == 1) { so = c; co = -s; }
+    else if (q == 2) { so = -s; co = -c; }
+    else { so = -c; co = s; }
+    *s_out = (float) so;
+    *c_out = (float) co;
+}
+
 /* ---------------------------------------------------------------- Q8_0 -- */
 
 /* ggml-base quantize_row_q8_0_ref: weights through ggml_quantize_chunk
@@ -124,16 +190,19 @@ void ref_dequantize_row_q8_0(const ref_block_q8_0 * x, float * y, int64_t k) {
     }
 }
 
-/* vec_dot_q8_0_q8_0: per block an exact integer dot, scaled by d_x*d_y */
+/* vec_dot_q8_0_q8_0: per block an exact integer dot, scaled by d_x*d_y;
+ * block terms summed in f64 and rounded once (see vec_dot_q4_K_q8_K) */
 float ref_vec_dot_q8_0_q8_0(int64_t n, const ref_block_q8_0 * x, const ref_block_q8_0 * y) {
     const int64_t nb = n / REF_QK8_0;
-    float sumf = 0.0f;
+    double sum = 0.0;
     for (int64_t i = 0; i < nb; i++) {
         int sumi = 0;
         for (int j = 0; j < REF_QK8_0; j++) sumi += (int) x[i].qs[j] * (int) y[i].qs[j];
-        sumf += (float) sumi * (ref_fp16_to_fp32(x[i].d) * ref_fp16_to_fp32(y[i].d));
+        /* d_x*d_y of two halves is exact in f32; the block term is exact in f64 */
+        const float dd = ref_fp16_to_fp32(x[i].d) * ref_fp16_to_fp32(y[i].d);
+        sum += (double) sumi * (double) dd;
     }
-    return sumf;
+    return (float) sum;
 }
 
 /* ---------------------------------------------------------------- Q4_K -- */
@@ -319,11 +388,14 @@ void ref_dequantize_row_q8_K(const ref_block_q8_K * x, float * y, int64_t k) {
 }
 
 /* vec_dot_q4_K_q8_K: per super-block the scaled integer sum and the mins
- * correction (through the Q8_K bsums) are exact integers; the float result
- * per super-block is d*isum - dmin*msum, accumulated in block order. */
+ * correction (through the Q8_K bsums) are exact integers; the super-block
+ * term d*isum - dmin*msum is formed in f64 and the terms are summed in f64,
+ * rounding to f32 once. ggml-cpu sums the same terms in f32 SIMD lanes (an
+ * ISA-dependent order); summing wide makes the result independent of order,
+ * so any correct device reduction reproduces it bit for bit. */
 float ref_vec_dot_q4_K_q8_K(int64_t n, const ref_block_q4_K * x, const ref_block_q8_K * y) {
     const int64_t nb = n / REF_QK_K;
-    float sumf = 0.0f;
+    double sum = 0.0;
     for (int64_t i = 0; i < nb; i++) {
         uint8_t sc[8], mn[8];
         for (int j = 0; j < 8; j++) ref_get_scale_min_k4(j, x[i].scales, &sc[j], &mn[j]);
@@ -340,11 +412,11 @@ float ref_vec_dot_q4_K_q8_K(int64_t n, const ref_block_q4_K * x, const ref_block
             }
             isum += s_lo * sc[2 * c] + s_hi * sc[2 * c + 1];
         }
-        const float d = ref_fp16_to_fp32(x[i].d) * y[i].d;
-        const float dmin = ref_fp16_to_fp32(x[i].dmin) * y[i].d;
-        sumf += d * (float) isum - dmin * (float) msum;
+        const double d = (double) ref_fp16_to_fp32(x[i].d) * (double) y[i].d;
+        const double dmin = (double) ref_fp16_to_fp32(x[i].dmin) * (double) y[i].d;
+        sum += d * (double) isum - dmin * (double) msum;
     }
-    return sumf;
+    return (float) sum;
 }
 
 /* ggml_vec_dot_f16: products of two halves are exact in f32; summed wide */
@@ -375,43 +447,44 @@ void ref_mul_mat(int wtype, const void * w, size_t row_bytes, int64_t m, int64_t
 #else
     (void) n_threads;
 #endif
+    /* every column is converted to the weight's vec_dot type once, then each
+     * weight row is streamed once against all columns (ggml-cpu's "convert
+     * src1 first" rule; the loop order only changes speed, not results) */
+    const int vtype = wtype == REF_Q8_0 ? REF_Q8_0 : (wtype == REF_Q4_K ? REF_Q8_K : (wtype == REF_F16 ? REF_F16 : REF_F32));
+    const size_t qrow = vtype == REF_F32 ? (size_t) k * 4 : ref_row_size(vtype, k);
+    char * xq = (char *) malloc(qrow * (size_t) (n > 0 ? n : 1));
+#pragma omp parallel for num_threads(n_threads) schedule(static)
     for (int64_t col = 0; col < n; col++) {
         const float * xc = x + col * x_stride;
-        float * dc = dst + col * d_stride;
-        if (wtype == REF_Q8_0) {
-            ref_block_q8_0 * xq = (ref_block_q8_0 *) malloc(ref_row_size(REF_Q8_0, k));
-            ref_quantize_row_q8_0_act(xc, xq, k);
-#pragma omp parallel for num_threads(n_threads) schedule(static)
-            for (int64_t r = 0; r < m; r++) {
-                dc[r] = ref_vec_dot_q8_0_q8_0(k, (const ref_block_q8_0 *) ((const char *) w + r * row_bytes), xq);
-            }
-            free(xq);
-        } else if (wtype == REF_Q4_K) {
-            ref_block_q8_K * xq = (ref_block_q8_K *) malloc(ref_row_size(REF_Q8_K, k));
-            ref_quantize_row_q8_K(xc, xq, k);
-#pragma omp parallel for num_threads(n_threads) schedule(static)
-            for (int64_t r = 0; r < m; r++) {
-                dc[r] = ref_vec_dot_q4_K_q8_K(k, (const ref_block_q4_K *) ((const char *) w + r * row_bytes), xq);
-            }
-            free(xq);
-        } else if (wtype == REF_F16) {
-            uint16_t * xh = (uint16_t *) malloc((size_t) k * 2);
-            ref_fp32_to_fp16_row(xc, xh, k);
-#pragma omp parallel for num_threads(n_threads) schedule(static)
-            for (int64_t r = 0; r < m; r++) {
-                dc[r] = ref_vec_dot_f16(k, (const uint16_t *) ((const char *) w + r * row_bytes), xh);
-            }
-            free(xh);
-        } else { /* f32 x f32: ggml_vec_dot_f32 */
-#pragma omp parallel for num_threads(n_threads) schedule(static)
-            for (int64_t r = 0; r < m; r++) {
-                const float * wr = (const float *) ((const char *) w + r * row_bytes);
+        char * o = xq + (size_t) col * qrow;
+        if (vtype == REF_Q8_0) ref_quantize_row_q8_0_act(xc, (ref_block_q8_0 *) o, k);
+        else if (vtype == REF_Q8_K) ref_quantize_row_q8_K(xc, (ref_block_q8_K *) o, k);
+        else if (vtype == REF_F16) ref_fp32_to_fp16_row(xc, (uint16_t *) o, k);
+        else memcpy(o, xc, (size_t) k * 4);
+    }
+#pragma omp parallel for num_threads(n_threads) schedule(dynamic, 16)
+    for (int64_t r = 0; r < m; r++) {
+        const char * wr = (const char *) w + r * row_bytes;
+        for (int64_t col = 0; col < n; col++) {
+            const char * xc = xq + (size_t) col * qrow;
+            float v;
+            if (vtype == REF_Q8_0) {
+                v = ref_vec_dot_q8_0_q8_0(k, (const ref_block_q8_0 *) wr, (const ref_block_q8_0 *) xc);
+            } else if (vtype == REF_Q8_K) {
+                v = ref_vec_dot_q4_K_q8_K(k, (const ref_block_q4_K *) wr, (const ref_block_q8_K *) xc);
+            } else if (vtype == REF_F16) {
+                v = ref_vec_dot_f16(k, (const uint16_t *) wr, (const uint16_t *) xc);
+            } else { /* ggml_vec_dot_f32 */
+                const float * a = (const float *) wr;
+                const float * b = (const float *) xc;
                 double s = 0.0;
-                for (int64_t i = 0; i < k; i++) s += (double) (wr[i] * xc[i]);
-                dc[r] = (float) s;
+                for (int64_t i = 0; i < k; i++) s += (double) (a[i] * b[i]);
+                v = (float) s;
             }
+            dst[col * d_stride + r] = v;
         }
     }
+    free(xq);
 }
 
 /* ---------------------------------------------------------- row ops ---- */
@@ -449,7 +522,7 @@ void ref_norm(const float * x, float * y, int64_t ne0, int64_t rows, float eps) 
     }
 }
 
-float ref_silu(float x) { return x / (1.0f + expf(-x)); }
+float ref_silu(float x) { return x / (1.0f + ref_expf_det(-x)); }
 
 float ref_gelu_f32(float x) {
     const float c = 0.79788456080286535587989211986876f; /* sqrt(2/pi) */
@@ -476,8 +549,7 @@ void ref_rope_neox(const float * x, float * y, int64_t head_dim, int64_t n_heads
         float theta = (float) pos[t];
         for (int i0 = 0; i0 < n_dims; i0 += 2) {
             const float th = freq_scale * theta;
-            cache[i0] = cosf(th);
-            cache[i0 + 1] = sinf(th);
+            ref_sincosf_det(th, &cache[i0 + 1], &cache[i0]);
             theta *= theta_scale;
         }
         for (int64_t h = 0; h < n_heads; h++) {
@@ -508,7 +580,7 @@ void ref_soft_max_ext(const float * x, const uint16_t * mask, float * y, int64_t
         }
         double sum = 0.0;
         for (int64_t i = 0; i < ne0; i++) {
-            const float e = expf(wp[i] - mx);
+            const float e = ref_expf_det(wp[i] - mx);
             y[r * ne0 + i] = e;
             sum += (double) e;
         }
@@ -574,6 +646,40 @@ void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_
                 acc16[d] = 0;
                 acc32[d] = 0.0f;
             }
+            float * o = out + (iq * Hq + h) * D;
+            if (fidelity == 3) {
+                /* two-pass: global max first, then every p = exp(s - M) and the
+                 * sums in f64, one rounding at the end */
+                float M = -INFINITY;
+                for (int64_t ic = 0; ic < n_kv; ic++) {
+                    const float mv = mask ? ref_fp16_to_fp32(mask[iq * mask_stride + ic]) : 0.0f;
+                    if (mv == -INFINITY) continue;
+                    const uint16_t * kr = k + kvh * kv_stride_head + ic * kv_stride_pos;
+                    double a = 0.0;
+                    for (int64_t d = 0; d < D; d++) a += (double) (ref_fp16_to_fp32(kr[d]) * ref_fp16_to_fp32(qh[d]));
+                    const float s = (float) a * scale + mv;
+                    M = s > M ? s : M;
+                }
+                double l = 0.0;
+                double acc[512];
+                for (int64_t d = 0; d < D; d++) acc[d] = 0.0;
+                if (M != -INFINITY) {
+                    for (int64_t ic = 0; ic < n_kv; ic++) {
+                        const float mv = mask ? ref_fp16_to_fp32(mask[iq * mask_stride + ic]) : 0.0f;
+                        if (mv == -INFINITY) continue;
+                        const uint16_t * kr = k + kvh * kv_stride_head + ic * kv_stride_pos;
+                        const uint16_t * vr = v + kvh * kv_stride_head + ic * kv_stride_pos;
+                        double a = 0.0;
+                        for (int64_t d = 0; d < D; d++) a += (double) (ref_fp16_to_fp32(kr[d]) * ref_fp16_to_fp32(qh[d]));
+                        const float s = (float) a * scale + mv;
+                        const float p = ref_expf_det(s - M);
+                        l += (double) p;
+                        for (int64_t d = 0; d < D; d++) acc[d] += (double) p * (double) ref_fp16_to_fp32(vr[d]);
+                    }
+                }
+                for (int64_t d = 0; d < D; d++) o[d] = l == 0.0 ? 0.0f : (float) (acc[d] / l);
+                continue;
+            }
             float M = -INFINITY, S = 0.0f;
             for (int64_t ic = 0; ic < n_kv; ic++) {
                 const float mv = mask ? ref_fp16_to_fp32(mask[iq * mask_stride + ic]) : 0.0f;
@@ -597,13 +703,13 @@ void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_
                 float ms = 1.0f, vs = 1.0f;
                 if (s > M) {
                     M = s;
-                    ms = expf(Mold - M);
+                    ms = ref_expf_det(Mold - M);
                     for (int64_t d = 0; d < D; d++) {
                         if (fidelity == 1) acc16[d] = ref_fp32_to_fp16(ref_fp16_to_fp32(acc16[d]) * ms);
                         else acc32[d] *= ms;
                     }
                 } else {
-                    vs = expf(s - M);
+                    vs = ref_expf_det(s - M);
                 }
                 for (int64_t d = 0; d < D; d++) {
                     if (fidelity == 1) {
@@ -615,7 +721,6 @@ void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_
                 S = S * ms + vs;
             }
             const float inv = S == 0.0f ? 0.0f : 1.0f / S;
-            float * o = out + (iq * Hq + h) * D;
             for (int64_t d = 0; d < D; d++) o[d] = (fidelity == 1 ? ref_fp16_to_fp32(acc16[d]) : acc32[d]) * inv;
         }
     }

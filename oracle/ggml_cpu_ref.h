@@ -100,6 +100,8 @@ void ref_rope_neox(const float * x, float * y, int64_t head_dim, int64_t n_heads
 void ref_soft_max_ext(const float * x, const uint16_t * mask, float * y, int64_t ne0, int64_t rows,
                       float scale);
 int32_t ref_argmax_last(const float * x, int64_t n);
+float ref_expf_det(float x);
+void ref_sincosf_det(float x, float * s_out, float * c_out);
 int32_t ref_argmax_first(const float * x, int64_t n);
 
 /*
@@ -110,7 +112,10 @@ int32_t ref_argmax_first(const float * x, int64_t n);
  *   out  f32 [n_q][Hq][D] contiguous
  * q head h reads kv head h / (Hq / Hkv). fidelity=1 reproduces ggml-cpu's
  * f16-rounded Q and f16 V accumulator; fidelity=2 rounds Q to f16 but
- * accumulates V in f32; fidelity=0 keeps Q in f32 and accumulates in f32.
+ * accumulates V in f32; fidelity=0 keeps Q in f32 and accumulates in f32;
+ * fidelity=3 (the device's canonical form) rounds Q to f16, takes the global
+ * max first and accumulates p = exp(s - max), the sum and p*V in f64,
+ * rounding once -- independent of the order positions are visited in.
  */
 void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_head,
                         const uint16_t * k, const uint16_t * v, int64_t kv_stride_head,

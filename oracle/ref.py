@@ -53,6 +53,8 @@ def lib() -> C.CDLL:
     s("ref_soft_max_ext", None, vp, vp, vp, i64, i64, f)
     s("ref_argmax_last", C.c_int32, vp, i64)
     s("ref_argmax_first", C.c_int32, vp, i64)
+    s("ref_expf_det", f, f)
+    s("ref_sincosf_det", None, f, vp, vp)
     s("ref_flash_attn_ext", None, vp, i64, i64, vp, vp, i64, i64, vp, i64, vp, i64, i64, i64, i64, i64, f, i, i)
     _lib = L
     return L
@@ -160,7 +162,8 @@ def flash_attn(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16: np.ndarr
                fidelity: int = 1, threads: int = 0) -> np.ndarray:
     """q: [n_q, Hq, D] f32; k16, v16: [Hkv, n_kv, D] f16 bits; mask16: [n_q, n_kv] f16 bits.
     fidelity 1: ggml-cpu numerics (f16 Q, f16 V accumulator); 2: f16 Q, f32
-    accumulation; 0: f32 throughout. Returns [n_q, Hq, D] f32."""
+    online accumulation; 0: f32 throughout; 3: f16 Q, two-pass f64 sums (the
+    device's order-independent form). Returns [n_q, Hq, D] f32."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     k16 = np.ascontiguousarray(k16, dtype=np.uint16)
     v16 = np.ascontiguousarray(v16, dtype=np.uint16)
@@ -172,3 +175,55 @@ def flash_attn(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16: np.ndarr
                              0 if m is None else m.shape[-1], _p(out), d, n_q, hq, hkv, n_kv, scale,
                              int(fidelity), threads)
     return out
+
+
+# ------------------------------------------------------------ decoders ---
+
+class QwenDims(C.Structure):
+    _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("n_kv_head", C.c_int),
+                ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("wtype", C.c_int),
+                ("rope_theta", C.c_float), ("rms_eps", C.c_float)]
+
+
+class QwenRef:
+    """CPU reference of one Qwen3 decoder sequence over host weight bytes
+    (a pointer table into the same buffers the device was loaded from)."""
+
+    def __init__(self, cfg, pointer_table, max_pos: int, fa_fidelity: int = 3, threads: int = 0):
+        L = lib()
+        L.ref_qwen_forward.restype = C.c_int32
+        L.ref_qwen_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                       C.c_int, C.c_int, C.c_void_p, C.c_int, C.c_int]
+        L.ref_qwen_embed.restype = None
+        L.ref_qwen_embed.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
+        self.dims = QwenDims(cfg.d_model, cfg.n_layers, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.ffn, cfg.vocab,
+                             cfg.wtype, cfg.rope_theta, cfg.rms_eps)
+        self.table = (C.c_void_p * len(pointer_table))(*pointer_table)
+        self.max_pos = max_pos
+        self.fidelity = fa_fidelity
+        self.threads = threads
+        shape = (cfg.n_kv_head, max_pos, cfg.head_dim)
+        self.k = [np.zeros(shape, np.uint16) for _ in range(cfg.n_layers)]
+        self.v = [np.zeros(shape, np.uint16) for _ in range(cfg.n_layers)]
+        self.kp = (C.c_void_p * cfg.n_layers)(*[a.ctypes.data for a in self.k])
+        self.vp = (C.c_void_p * cfg.n_layers)(*[a.ctypes.data for a in self.v])
+        self.pos = 0
+
+    def embed(self, tokens) -> np.ndarray:
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        out = np.zeros((len(tokens), self.dims.d_model), np.float32)
+        lib().ref_qwen_embed(C.byref(self.dims), self.table, tokens.ctypes.data, len(tokens), out.ctypes.data)
+        return out
+
+    def forward(self, x: np.ndarray):
+        """x [T, d] layer-0 input at the next T positions -> (top1, logits of the last position)"""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        logits = np.zeros(self.dims.vocab, np.float32)
+        top1 = lib().ref_qwen_forward(C.byref(self.dims), self.table, self.kp, self.vp, self.max_pos,
+                                      x.ctypes.data, x.shape[0], self.pos, logits.ctypes.data, self.fidelity,
+                                      self.threads)
+        self.pos += x.shape[0]
+        return int(top1), logits
+
+    def step(self, token: int):
+        return self.forward(self.embed([token]))

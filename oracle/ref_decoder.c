@@ -1,0 +1,132 @@
+/*
+ * ref_decoder.c -- CPU reference of the decoder steps, built from the
+ * restated ggml-cpu ops in ggml_cpu_ref.c. TEST INFRASTRUCTURE ONLY: the
+ * end-to-end parity tests and the benchmark's CPU-baseline leg run it as the
+ * checker.
+ *
+ * Qwen3 LLM step: the op sequence of llm_layer
+ * (crates/openasr-core/src/nn/decoder.rs:1850-2145) and the fused logits head
+ * (models/qwen/llm_transformer.rs:2096-2115), one sequence at a time (the
+ * reference's batched == serial invariant, nn/decoder.rs:3412-3520, makes the
+ * per-sequence run the definition of the batched one).
+ */
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "ggml_cpu_ref.h"
+
+typedef struct {
+    int d_model, n_layers, n_head, n_kv_head, head_dim, ffn, vocab, wtype;
+    float rope_theta, rms_eps;
+} ref_qwen_dims;
+
+/* pointer table: [tok_embd, out_norm, then per layer attn_norm, qkv, q_norm,
+ * k_norm, o, ffn_norm, gate, up, down] */
+enum { T_EMBD = 0, T_OUT_NORM = 1, T_LAYER0 = 2, T_PER_LAYER = 9 };
+
+static const void * tp(const void * const * t, int layer, int idx) { return t[T_LAYER0 + layer * T_PER_LAYER + idx]; }
+
+static void mul_row_weight(float * x, const float * w, int rows, int n) {
+    for (int r = 0; r < rows; r++)
+        for (int i = 0; i < n; i++) x[(size_t) r * n + i] *= w[i];
+}
+
+/* get_rows on the token embedding, dequantizing (cpu_graph.rs:3688-3732) */
+void ref_qwen_embed(const ref_qwen_dims * m, const void * const * t, const int32_t * tokens, int T, float * out) {
+    const size_t rs = ref_row_size(m->wtype, m->d_model);
+    for (int i = 0; i < T; i++) {
+        const void * row = (const char *) t[T_EMBD] + (size_t) tokens[i] * rs;
+        if (m->wtype == REF_Q8_0) ref_dequantize_row_q8_0((const ref_block_q8_0 *) row, out + (size_t) i * m->d_model, m->d_model);
+        else ref_dequantize_row_q4_K((const ref_block_q4_K *) row, out + (size_t) i * m->d_model, m->d_model);
+    }
+}
+
+/*
+ * T positions p0..p0+T-1 of one sequence through every layer. x [T][d] is the
+ * layer-0 input (embeddings or hidden prefix). kcache/vcache: per layer f16
+ * [n_kv_head][max_pos][head_dim]. The last position's logits go to logits
+ * ([vocab]) when non-null; returns the first-max top-1 of them (or -1).
+ */
+int32_t ref_qwen_forward(const ref_qwen_dims * m, const void * const * t, uint16_t * const * kcache,
+                         uint16_t * const * vcache, int max_pos, const float * x_in, int T, int p0, float * logits,
+                         int fa_fidelity, int threads) {
+    const int d = m->d_model, hd = m->head_dim, hq = m->n_head, hkv = m->n_kv_head;
+    const int q_w = hq * hd, kv_w = hkv * hd, qkv_w = q_w + 2 * kv_w;
+    const size_t rs_d = ref_row_size(m->wtype, d);
+    float * x = (float *) malloc(sizeof(float) * (size_t) T * d);
+    float * nrm = (float *) malloc(sizeof(float) * (size_t) T * (d > m->ffn ? d : m->ffn));
+    float * qkv = (float *) malloc(sizeof(float) * (size_t) T * qkv_w);
+    float * q = (float *) malloc(sizeof(float) * (size_t) T * q_w);
+    float * k = (float *) malloc(sizeof(float) * (size_t) T * kv_w);
+    float * att = (float *) malloc(sizeof(float) * (size_t) T * q_w);
+    float * tmp = (float *) malloc(sizeof(float) * (size_t) T * d);
+    float * g = (float *) malloc(sizeof(float) * (size_t) T * m->ffn);
+    float * u = (float *) malloc(sizeof(float) * (size_t) T * m->ffn);
+    int32_t * pos = (int32_t *) malloc(sizeof(int32_t) * (size_t) T);
+    const int n_kv = p0 + T;
+    uint16_t * mask = (uint16_t *) malloc(sizeof(uint16_t) * (size_t) T * n_kv);
+    memcpy(x, x_in, sizeof(float) * (size_t) T * d);
+    for (int i = 0; i < T; i++) {
+        pos[i] = p0 + i;
+        for (int j = 0; j < n_kv; j++) mask[(size_t) i * n_kv + j] = j <= p0 + i ? 0 : 0xFC00;
+    }
+    for (int l = 0; l < m->n_layers; l++) {
+        /* attention block */
+        ref_rms_norm(x, nrm, d, T, m->rms_eps);
+        mul_row_weight(nrm, (const float *) tp(t, l, 0), T, d);
+        ref_mul_mat(m->wtype, tp(t, l, 1), rs_d, qkv_w, d, nrm, d, T, qkv, qkv_w, threads);
+        for (int i = 0; i < T; i++) {
+            memcpy(q + (size_t) i * q_w, qkv + (size_t) i * qkv_w, sizeof(float) * q_w);
+            memcpy(k + (size_t) i * kv_w, qkv + (size_t) i * qkv_w + q_w, sizeof(float) * kv_w);
+        }
+        ref_rms_norm(q, q, hd, (int64_t) T * hq, m->rms_eps);
+        mul_row_weight(q, (const float *) tp(t, l, 2), T * hq, hd);
+        ref_rms_norm(k, k, hd, (int64_t) T * hkv, m->rms_eps);
+        mul_row_weight(k, (const float *) tp(t, l, 3), T * hkv, hd);
+        ref_rope_neox(q, q, hd, hq, T, pos, hd, m->rope_theta, 1.0f);
+        ref_rope_neox(k, k, hd, hkv, T, pos, hd, m->rope_theta, 1.0f);
+        /* set_rows f32 -> f16 into the cache (nn/decoder.rs:2031-2036) */
+        for (int i = 0; i < T; i++) {
+            for (int h = 0; h < hkv; h++) {
+                uint16_t * kd = kcache[l] + ((size_t) h * max_pos + pos[i]) * hd;
+                uint16_t * vd = vcache[l] + ((size_t) h * max_pos + pos[i]) * hd;
+                ref_fp32_to_fp16_row(k + ((size_t) i * hkv + h) * hd, kd, hd);
+                ref_fp32_to_fp16_row(qkv + (size_t) i * qkv_w + q_w + kv_w + (size_t) h * hd, vd, hd);
+            }
+        }
+        ref_flash_attn_ext(q, (int64_t) hq * hd, hd, kcache[l], vcache[l], (int64_t) max_pos * hd, hd, mask, n_kv,
+                           att, hd, T, hq, hkv, n_kv, 1.0f / sqrtf((float) hd), fa_fidelity, threads);
+        ref_mul_mat(m->wtype, tp(t, l, 4), ref_row_size(m->wtype, q_w), d, q_w, att, q_w, T, tmp, d, threads);
+        for (size_t i = 0; i < (size_t) T * d; i++) x[i] = x[i] + tmp[i];
+        /* SwiGLU block (nn/ffn.rs:64-91) */
+        ref_rms_norm(x, nrm, d, T, m->rms_eps);
+        mul_row_weight(nrm, (const float *) tp(t, l, 5), T, d);
+        ref_mul_mat(m->wtype, tp(t, l, 6), rs_d, m->ffn, d, nrm, d, T, g, m->ffn, threads);
+        ref_mul_mat(m->wtype, tp(t, l, 7), rs_d, m->ffn, d, nrm, d, T, u, m->ffn, threads);
+        for (size_t i = 0; i < (size_t) T * m->ffn; i++) g[i] = ref_silu(g[i]) * u[i];
+        ref_mul_mat(m->wtype, tp(t, l, 8), ref_row_size(m->wtype, m->ffn), d, m->ffn, g, m->ffn, T, tmp, d, threads);
+        for (size_t i = 0; i < (size_t) T * d; i++) x[i] = tmp[i] + x[i];
+    }
+    int32_t top1 = -1;
+    if (logits) {
+        /* fused logits head on the last position (llm_transformer.rs:2096-2115) */
+        float * last = x + (size_t) (T - 1) * d;
+        ref_rms_norm(last, nrm, d, 1, m->rms_eps);
+        mul_row_weight(nrm, (const float *) t[T_OUT_NORM], 1, d);
+        ref_mul_mat(m->wtype, t[T_EMBD], rs_d, m->vocab, d, nrm, d, 1, logits, m->vocab, threads);
+        top1 = ref_argmax_first(logits, m->vocab);
+    }
+    free(x);
+    free(nrm);
+    free(qkv);
+    free(q);
+    free(k);
+    free(att);
+    free(tmp);
+    free(g);
+    free(u);
+    free(pos);
+    free(mask);
+    return top1;
+}

@@ -2,10 +2,14 @@
 ABI exactly as the host drives it: a ggml graph built with libggml-base,
 allocated on the plugin's buffer type, computed by the plugin backend.
 
-Tolerances (max |gpu - oracle| / max |oracle|): the north-star bound is 2e-3
-per op; integer-dot paths are held to 1e-5 (only the float accumulation
-order differs), attention to 1e-5 against the oracle mode with the same
-rounding points and 2e-3 against the ggml-cpu-fidelity mode.
+The bar is bit-identical results (2e-3 per op). Integer
+block dots are exact and every cross-lane / cross-chunk sum is carried in f64
+and rounded once, exp / sin / cos are evaluated by the same deterministic
+sequence on both sides, and nothing is FMA-contracted, so device and oracle
+agree bit for bit except for a vanishing fraction of values whose f64 sum
+lands on an f32 rounding boundary. Attention is also held to the f64 textbook
+result and must be at least as accurate as ggml-cpu's numerics (whose V
+accumulator is f16).
 """
 
 import math
@@ -21,6 +25,16 @@ def rel_err(a, b):
     a = np.asarray(a, np.float64)
     b = np.asarray(b, np.float64)
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def assert_same_bits(a, b, max_frac=1e-5):
+    """device == reference bit for bit, allowing a vanishing fraction of
+    values that sit on an f32 rounding boundary of an f64-accumulated sum"""
+    a = np.asarray(a, np.float32)
+    b = np.asarray(b, np.float32)
+    diff = a.view(np.int32) != b.view(np.int32)
+    assert diff.mean() <= max_frac, f"{diff.sum()} of {diff.size} values differ, max rel {rel_err(a, b):.2e}"
+    assert rel_err(a, b) < 1e-6
 
 
 def run(ggml, gpu, G, out):
@@ -55,7 +69,7 @@ def test_mul_mat_quantized(ggml, gpu, ref, wname, m, k, n):
     assert G.compute(gpu.backend) == 0
     y = G.get(Y).reshape(n, m)
     want = ref.mul_mat(wt, wq, m, k, x)
-    assert rel_err(y, want) < 1e-5
+    assert_same_bits(y, want)
     # the weight round-trips through the device layout byte for byte
     assert np.array_equal(G.get(W, np.uint8), wq)
     G.free()
@@ -77,7 +91,7 @@ def test_mul_mat_lm_head_full_size(ggml, gpu, ref):
     assert G.compute(gpu.backend) == 0
     y = G.get(Y).reshape(n, m)
     want = ref.mul_mat(ggml.Q4_K, wq, m, k, x)
-    assert rel_err(y, want) < 1e-5
+    assert_same_bits(y, want)
     assert np.array_equal(y.argmax(1), want.argmax(1))
     G.free()
 
@@ -107,6 +121,19 @@ FA_CASES = [
     (128, 16, 8, 512, 64, 1), (128, 16, 8, 2048, 64, 2), (64, 6, 6, 448, 1, 1), (64, 6, 6, 1500, 1, 1),
     (64, 6, 6, 1500, 1, 3),
 ]
+
+
+def attention_f64(q, k, v, mask, scale):
+    """textbook softmax attention in f64; q [n_q, hq, d], k/v [hkv, n_kv, d]"""
+    g = q.shape[1] // k.shape[0]
+    kk = np.repeat(k.astype(np.float64), g, axis=0)  # [hq, n_kv, d]
+    vv = np.repeat(v.astype(np.float64), g, axis=0)
+    s = np.einsum("qhd,hkd->qhk", q.astype(np.float64), kk) * scale
+    if mask is not None:
+        s = s + mask.astype(np.float64)[:, None, :]
+    s = s - s.max(-1, keepdims=True)
+    p = np.exp(s)
+    return np.einsum("qhk,hkd->qhd", p, vv) / p.sum(-1)[..., None]
 
 
 @pytest.mark.parametrize("d,hq,hkv,n_kv,n_q,n_seq", FA_CASES)
@@ -140,10 +167,19 @@ def test_flash_attn_ext(ggml, gpu, ref, d, hq, hkv, n_kv, n_q, n_seq):
     for s in range(n_seq):
         qs = np.ascontiguousarray(q[s].transpose(1, 0, 2))  # [n_q, hq, d]
         ms = None if cross else mask[s].view(np.uint16)
-        same = ref.flash_attn(qs, k[s].view(np.uint16), v[s].view(np.uint16), ms, scale, fidelity=2)
+        same = ref.flash_attn(qs, k[s].view(np.uint16), v[s].view(np.uint16), ms, scale, fidelity=3)
         cpu = ref.flash_attn(qs, k[s].view(np.uint16), v[s].view(np.uint16), ms, scale, fidelity=1)
-        assert rel_err(out[s], same) < 1e-5
-        assert rel_err(out[s], cpu) < 2e-3
+        # same arithmetic (f16 Q, two-pass f64 sums): bit for bit
+        assert_same_bits(out[s], same)
+        # ggml-cpu keeps the V accumulator in f16 (fidelity 1); its error grows
+        # ~sqrt(n_kv) f16 ulps. The device is held to the f64 textbook result
+        # and must be at least as close to it as the ggml-cpu numerics are.
+        exact = attention_f64(qs.astype(np.float16).astype(np.float32), k[s], v[s],
+                              None if cross else mask[s], scale)
+        e_gpu, e_cpu = rel_err(out[s], exact), rel_err(cpu, exact)
+        print(f"  seq {s}: gpu vs f64 {e_gpu:.2e}, ggml-cpu numerics vs f64 {e_cpu:.2e}, "
+              f"gpu vs ggml-cpu numerics {rel_err(out[s], cpu):.2e}")
+        assert e_gpu < 2e-5 and e_gpu <= e_cpu
     G.free()
 
 
@@ -172,9 +208,9 @@ def test_flash_attn_fully_masked_chunks_are_skipped_exactly(ggml, gpu, ref):
     out = G.get(O).reshape(hq, d)
     want = ref.flash_attn(np.ascontiguousarray(q.transpose(1, 0, 2)), k[:, :700].view(np.uint16).copy(),
                           v[:, :700].view(np.uint16).copy(), mask[:, :700].view(np.uint16).copy(),
-                          1 / math.sqrt(d), fidelity=2)[0]
+                          1 / math.sqrt(d), fidelity=3)[0]
     assert np.isfinite(out).all()
-    assert rel_err(out, want) < 1e-5
+    assert_same_bits(out, want)
     G.free()
 
 
@@ -191,7 +227,7 @@ def test_rms_norm_mul_fused(ggml, gpu, ref):
     G.set(X, x)
     G.set(W, w)
     assert G.compute(gpu.backend) == 0
-    assert rel_err(G.get(Y).reshape(8, 1024), ref.rms_norm(x, 1e-6) * w) < 1e-6
+    assert_same_bits(G.get(Y).reshape(8, 1024), ref.rms_norm(x, 1e-6) * w)
     G.free()
 
 
@@ -207,7 +243,7 @@ def test_qk_norm_per_head(ggml, gpu, ref):
     G.set(X, x)
     G.set(W, w)
     assert G.compute(gpu.backend) == 0
-    assert rel_err(G.get(Y).reshape(4, 16, 128), ref.rms_norm(x, 1e-6) * w) < 1e-6
+    assert_same_bits(G.get(Y).reshape(4, 16, 128), ref.rms_norm(x, 1e-6) * w)
     G.free()
 
 
@@ -225,7 +261,7 @@ def test_layer_norm_affine_fused(ggml, gpu, ref):
     G.set(W, w)
     G.set(B, b)
     assert G.compute(gpu.backend) == 0
-    assert rel_err(G.get(Y).reshape(3, 384), ref.norm(x, 1e-5) * w + b) < 1e-6
+    assert_same_bits(G.get(Y).reshape(3, 384), ref.norm(x, 1e-5) * w + b)
     G.free()
 
 
@@ -241,8 +277,8 @@ def test_rope_neox_positions(ggml, gpu, ref):
     G.set(X, x)
     G.set(P, pos)
     assert G.compute(gpu.backend) == 0
-    # same theta sequence as the oracle; sin/cos of up to ~4000 rad differ by libm ulps
-    assert rel_err(G.get(Y).reshape(t, h, d), ref.rope_neox(x, pos, d, 1e6)) < 2e-6
+    # same theta sequence and the same deterministic sin/cos as the oracle
+    assert_same_bits(G.get(Y).reshape(t, h, d), ref.rope_neox(x, pos, d, 1e6))
     G.free()
 
 
@@ -259,7 +295,7 @@ def test_silu_mul_and_gelu(ggml, gpu, ref):
     G.set(Gt, g)
     G.set(U, u)
     assert G.compute(gpu.backend) == 0
-    assert rel_err(G.get(Y).reshape(4, 3072), ref.silu(g) * u) < 1e-6
+    assert_same_bits(G.get(Y).reshape(4, 3072), ref.silu(g) * u)
     assert np.array_equal(G.get(Z).reshape(4, 3072), ref.gelu(u))  # same f16 table: bit exact
     G.free()
 
@@ -331,10 +367,11 @@ def test_soft_max_argmax_cpy_cont(ggml, gpu, ref):
     G.set(X, x)
     G.set(M, mask.view(np.uint16))
     assert G.compute(gpu.backend) == 0
-    assert rel_err(G.get(S).reshape(6, 333), ref.soft_max_ext(x, mask.view(np.uint16), 0.7)) < 1e-6
-    assert list(G.get(A)) == [ref.argmax_last(r) for r in x]
-    assert list(G.get(A1)) == [ref.argmax_first(r) for r in x]
-    assert G.get(A)[2] == 200 and G.get(A1)[2] == 10
+    assert_same_bits(G.get(S).reshape(6, 333), ref.soft_max_ext(x, mask.view(np.uint16), 0.7))
+    a_last, a_first = G.get(A).reshape(-1), G.get(A1).reshape(-1)
+    assert list(a_last) == [ref.argmax_last(r) for r in x]
+    assert list(a_first) == [ref.argmax_first(r) for r in x]
+    assert a_last[2] == 200 and a_first[2] == 10
     assert np.array_equal(G.get(H, np.uint16).reshape(6, 333), x.astype(np.float16).view(np.uint16))
     assert np.array_equal(G.get(Tc).reshape(333, 6), x.T)
     G.free()
@@ -359,7 +396,7 @@ def test_abort_callback_and_graph_replay(ggml, gpu, ref):
         G.set(X, x)
         assert G.compute(gpu.backend) == 0
         y = G.get(Y).reshape(1, m)
-        assert rel_err(y, ref.mul_mat(ggml.Q8_0, wq, m, k, x) + x) < 1e-5
+        assert_same_bits(y, ref.mul_mat(ggml.Q8_0, wq, m, k, x) + x)
         outs.append(y)
     CB = C.CFUNCTYPE(C.c_bool, C.c_void_p)
     always = CB(lambda _: True)

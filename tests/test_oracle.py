@@ -286,3 +286,60 @@ def test_flash_attn_textbook_gqa_and_masking(ref):
     a = ref.flash_attn(q[:1], k.view(np.uint16), v.view(np.uint16), m0.view(np.uint16), scale, fidelity=False)
     b = ref.flash_attn(q[:1], k2.view(np.uint16), v2.view(np.uint16), m0.view(np.uint16), scale, fidelity=False)
     assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------- deterministic math --
+
+def ulp_dist(a, b):
+    """distance in f32 ulps between float32 arrays"""
+    ai = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    bi = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    ai = np.where(ai < 0, -(ai & 0x7fffffff), ai)
+    bi = np.where(bi < 0, -(bi & 0x7fffffff), bi)
+    return np.abs(ai - bi)
+
+
+def test_det_expf_correctly_rounded(ref):
+    L = ref.lib()
+    x = np.concatenate([np.linspace(-103, 88.7, 20001), RNG.standard_normal(20000) * 10,
+                        [0.0, -0.0, 1.0, -1.0, 1e-8, -1e-8, 88.72, -87.3]]).astype(np.float32)
+    got = np.array([L.ref_expf_det(float(v)) for v in x], np.float32)
+    want = np.exp(x.astype(np.float64)).astype(np.float32)  # f64 exp rounded once
+    d = ulp_dist(got, want)
+    assert d.max() <= 1 and np.mean(d == 0) > 0.999
+    assert L.ref_expf_det(-200.0) == 0.0 and math.isinf(L.ref_expf_det(100.0))
+
+
+def test_det_sincos_within_one_ulp(ref):
+    L = ref.lib()
+    x = np.concatenate([np.linspace(-5000, 5000, 40001), RNG.standard_normal(5000) * 3]).astype(np.float32)
+    s = C_float = np.zeros(1, np.float32)
+    sv = np.zeros(x.size, np.float32)
+    cv = np.zeros(x.size, np.float32)
+    for i, v in enumerate(x):
+        a = np.zeros(1, np.float32)
+        b = np.zeros(1, np.float32)
+        L.ref_sincosf_det(float(v), a.ctypes.data, b.ctypes.data)
+        sv[i], cv[i] = a[0], b[0]
+    xs = x.astype(np.float64)
+    ws, wc = np.sin(xs).astype(np.float32), np.cos(xs).astype(np.float32)
+    # absolute error bound: half an ulp of 1 plus the f32 rounding
+    assert np.abs(sv.astype(np.float64) - np.sin(xs)).max() < 1.2e-7
+    assert np.abs(cv.astype(np.float64) - np.cos(xs)).max() < 1.2e-7
+    assert np.mean(sv == ws) > 0.99 and np.mean(cv == wc) > 0.99
+
+
+def test_flash_attn_two_pass_mode(ref):
+    n_q, hq, hkv, n_kv, d = 4, 4, 2, 300, 128
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((n_q, n_kv), np.float16)
+    mask[:, 250:] = -np.inf
+    mask[3] = -np.inf
+    scale = 1 / math.sqrt(d)
+    qh = q.astype(np.float16).astype(np.float32)
+    want = textbook_attention(qh, k, v, mask, scale, 2)
+    got = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, fidelity=3)
+    assert np.abs(got - want).max() < 1e-6 * np.abs(want).max()
+    assert not got[3].any()
