@@ -1,14 +1,21 @@
-"""Benchmark of the MI355X ggml backend on OpenASR's quantized decoder path.
+"""Benchmark of the MI355X ggml backend on OpenASR's quantized decoder step.
 
-Default workload: the Qwen3-0.6B-shaped decoder's per-token MUL_MAT set on
-Q4_K weights at batch 8 (QKV 4096x1024, o 1024x2048, gate/up 3072x1024,
-down 1024x3072 for 28 layers, plus the 151936x1024 lm_head) -- one "step" is
-one pass of every weight matrix of one decode step, inputs resident in HBM.
-Timing: HIP events on the backend's own stream (the plugin's profile hook),
-with the timed region bracketed by device synchronisation.
+Workload (default): the Qwen3-0.6B-shaped decoder with Q4_K weights at
+batch 8 -- eight sequences, each with an independent seeded 375-position
+N(0,1) audio prefix plus 8 prompt tokens prefilled, then greedy decode with
+an f16 KV cache sized for 1024 positions per sequence. One "step" is one
+decode step of all eight sequences through the persistent decode graph
+(28 layers + batched lm_head + first-max top-1), inputs resident in HBM.
+The timed region is K consecutive greedy steps (each step is a synchronous
+graph compute, so the region is bracketed by device synchronisation).
 
-Prints one JSON line (see the keys below). `--gpus N` with N > 1 exits: this
-build targets one GPU per process and the path has no collectives.
+Also reported (same run): the Qwen3-0.6B Q8_0 batch-1 decode rate, per-kernel
+times of one decode step from HIP events on the backend's own stream, the
+roofline fraction of the dominant kernel (the quantized GEMV), and the CPU
+oracle's batched decode rate on the host cores from the same KV state.
+
+Prints one JSON line. `--gpus N` with N > 1 exits: the path runs one GPU per
+process and has no collectives.
 """
 
 from __future__ import annotations
@@ -26,13 +33,6 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
-Q4K_BPW = 144 / 256
-Q8_0_BPW = 34 / 32
-
-# Qwen3-0.6B shape: (name, M, K) per layer, 28 layers, + lm_head
-QWEN06_LAYER = [("qkv", 4096, 1024), ("o", 1024, 2048), ("gate", 3072, 1024), ("up", 3072, 1024),
-                ("down", 1024, 3072)]
-QWEN06_HEAD = ("lm_head", 151936, 1024)
 
 
 def log(msg: str) -> None:
@@ -42,137 +42,169 @@ def log(msg: str) -> None:
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--wtype", choices=["q4_K", "q8_0"], default="q4_K")
-    p.add_argument("--batch", type=int, default=8)
-    p.add_argument("--layers", type=int, default=28)
+    p.add_argument("--steps", type=int, default=128, help="timed decode steps")
+    p.add_argument("--warmup", type=int, default=8, help="untimed decode steps before the timed region")
+    p.add_argument("--workload", default="qwen3-0.6b-q4_K-b8")
+    p.add_argument("--no-b1", action="store_true", help="skip the batch-1 Q8_0 side measurement")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--cpu-seconds", type=float, default=12.0)
+    p.add_argument("--profile-iters", type=int, default=20)
     return p.parse_args()
+
+
+def weight_bytes(cfg, wtype) -> dict:
+    """algorithmic weight bytes per decode step, per matrix kind"""
+    from openasr_amd import ggml as g
+    bpw = 144 / 256 if wtype == g.Q4_K else 34 / 32
+    d, hd = cfg["d_model"], cfg["head_dim"]
+    q_w, kv_w = cfg["n_head"] * hd, cfg["n_kv_head"] * hd
+    per_layer = {"qkv": (q_w + 2 * kv_w) * d, "o": d * q_w, "gate": cfg["ffn"] * d, "up": cfg["ffn"] * d,
+                 "down": d * cfg["ffn"]}
+    out = {k: v * cfg["n_layers"] * bpw for k, v in per_layer.items()}
+    out["lm_head"] = cfg["vocab"] * d * bpw
+    return out
+
+
+def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cpu: bool, cpu_seconds: float):
+    from openasr_amd import decoders as D
+    from openasr_amd import ggml as g
+
+    wl = D.WORKLOADS[name]
+    plugin = g.plugin()
+    t0 = time.time()
+    w = D.QwenWeights(wl.wtype, seed=1234, **wl.shape)
+    model = D.QwenModel(w, plugin.backend)
+    sess = model.session(wl.n_seq, wl.max_positions)
+    emb, prompt = D.workload_inputs(wl, seed=77)
+    log(f"[bench] {name}: weights synthesised and uploaded in {time.time() - t0:.1f}s")
+
+    t0 = time.time()
+    sess.prefill_embeddings(emb)
+    first = sess.prefill_tokens(prompt)
+    prefill_s = time.time() - t0
+    n_prefill = wl.n_seq * (wl.prefix + wl.prompt)
+    log(f"[bench] prefill {n_prefill} positions in {prefill_s * 1e3:.1f} ms")
+
+    steps = min(steps, wl.max_positions - wl.prefix - wl.prompt - warmup)
+    out, _ = sess.generate(first, warmup)
+    cur = out[-1] if warmup else first
+    t0 = time.perf_counter()
+    out, step_ms = sess.generate(cur, steps)
+    elapsed = time.perf_counter() - t0
+    tok_s = wl.n_seq * steps / elapsed
+    log(f"[bench] {steps} decode steps: {elapsed * 1e3 / steps:.3f} ms/step, {tok_s:.1f} tokens/s "
+        f"(median step {np.median(step_ms):.3f} ms)")
+
+    # per-kernel breakdown of one decode step (eager launches, HIP events on the backend stream)
+    prof = plugin.profile(sess.decode_graph(), profile_iters)
+    kern = {}
+    for lab, ms in prof:
+        k = lab.split(":", 1)[0]
+        kern.setdefault(k, [0.0, 0])
+        kern[k][0] += ms
+        kern[k][1] += 1
+    wb = weight_bytes(wl.shape, wl.wtype)
+    gemv_key = "mul_mat_q4_K" if wl.wtype == g.Q4_K else "mul_mat_q8_0"
+    gemv_ms, gemv_n = kern.get(gemv_key, [float("nan"), 0])
+    # activation bytes per step: int8 quants in, f32 results out, per matrix
+    d, hd, ffn = wl.shape["d_model"], wl.shape["head_dim"], wl.shape["ffn"]
+    q_w, kv_w = wl.shape["n_head"] * hd, wl.shape["n_kv_head"] * hd
+    mats = [(q_w + 2 * kv_w, d), (d, q_w), (ffn, d), (ffn, d), (d, ffn)] * wl.shape["n_layers"]
+    mats.append((wl.shape["vocab"], d))
+    act_bytes = sum(k * wl.n_seq + 4 * m * wl.n_seq for m, k in mats)
+    alg_bytes = sum(wb.values()) + act_bytes
+    gemv_gbs = alg_bytes / (gemv_ms * 1e-3) / 1e9
+    eager_ms = sum(ms for _, ms in prof)
+    breakdown = {k: {"ms": round(v[0], 4), "launches": v[1]} for k, v in sorted(kern.items(), key=lambda kv: -kv[1][0])}
+    log(f"[bench] eager step {eager_ms:.3f} ms over {len(prof)} launch groups; {gemv_key}: {gemv_n} launches, "
+        f"{gemv_ms:.3f} ms, {gemv_gbs:.0f} GB/s = {gemv_gbs / HBM_PEAK_GBS:.1%} of HBM peak")
+    for k, v in breakdown.items():
+        log(f"    {k:>16}: {v['ms']:.4f} ms over {v['launches']} launches")
+
+    cpu = None
+    if want_cpu:
+        cpu = cpu_baseline(w, wl, sess, out[-1], cpu_seconds)
+    result = dict(tok_s=tok_s, ms_per_step=elapsed * 1e3 / steps, steps=steps, prefill_ms=prefill_s * 1e3,
+                  n_prefill=n_prefill, gemv_ms=gemv_ms, gemv_launches=gemv_n, gemv_gbs=gemv_gbs,
+                  weight_bytes=alg_bytes, eager_step_ms=eager_ms, breakdown=breakdown, cpu=cpu)
+    sess.free()
+    model.free()
+    w.free()
+    return result
+
+
+def cpu_baseline(w, wl, sess, tokens, seconds: float):
+    """The CPU oracle's batched decode step (oracle/ref_decoder.c, the checker)
+    on the host cores, continuing from the device's KV state: a bounded sample
+    of the same workload, timed for ~`seconds`."""
+    from oracle import ref
+
+    threads = os.cpu_count() or 1
+    r = ref.QwenRefBatch(w.cfg, w.pointer_table(), wl.max_positions, wl.n_seq, threads=threads)
+    for s in range(wl.n_seq):
+        for layer in range(wl.shape["n_layers"]):
+            k, v = sess.read_kv(layer, s)
+            r.k[s][layer][...] = k
+            r.v[s][layer][...] = v
+        r.pos[s] = sess.position(s)
+    cur = np.asarray(tokens, np.int32)
+    n = 0
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds and r.pos.max() < wl.max_positions - 1:
+        cur = r.step(cur)
+        n += 1
+    dt = time.perf_counter() - t0
+    val = wl.n_seq * n / dt
+    log(f"[bench] cpu oracle: {n} batched decode steps in {dt:.1f}s on {threads} threads = {val:.2f} tokens/s")
+    return {"value": round(val, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{n} batched decode steps of {wl.name} (oracle ref_qwen_decode_batch, {threads} OpenMP "
+                      f"threads) continuing from the device KV state at position {int(r.pos.min()) - n}"}
 
 
 def main() -> int:
     a = parse()
     if a.gpus != 1:
-        print(f"bench.py: this build runs on one GPU per process (asked for {a.gpus}); "
-              "the decoder path has no multi-GPU collectives", file=sys.stderr)
+        print(f"bench.py: this build runs on one GPU per process (asked for {a.gpus}); the decoder path has no "
+              "multi-GPU collectives", file=sys.stderr)
         return 2
-    from openasr_amd import ggml
+    from openasr_amd import ggml as g
 
-    g = ggml
-    wt = g.Q4_K if a.wtype == "q4_K" else g.Q8_0
-    bpw = Q4K_BPW if wt == g.Q4_K else Q8_0_BPW
-    plugin = g.plugin()
-    log(f"[bench] backend {plugin.name}, workload qwen3-0.6b {a.wtype} mul_mat set, batch {a.batch}")
-
-    shapes = []
-    for layer in range(a.layers):
-        for name, m, k in QWEN06_LAYER:
-            shapes.append((f"L{layer}.{name}", m, k))
-    shapes.append(QWEN06_HEAD)
-
-    # one quantized matrix per distinct shape; each layer gets its own copy so
-    # the step streams ~335 MB (Q4_K) of distinct weights, beyond the 256 MB MALL
-    G = g.Graph(n_tensors=512, graph_size=1024)
-    X = {}
-    outs = []
-    weights = []
-    for name, m, k in shapes:
-        if k not in X:
-            X[k] = G.new(g.F32, k, a.batch, name=f"x{k}")
-        W = G.new(wt, k, m, name=name, weight=True)
-        weights.append((W, m, k))
-        outs.append(G.lib.ggml_mul_mat(G.ctx, W, X[k]))
-    G.build(*outs)
-    G.allocate(plugin.buft)
-    t0 = time.time()
-    cache = {}
-    for idx, (W, m, k) in enumerate(weights):
-        key = (m, k)
-        if key not in cache:
-            w = g.synth_normal(1234, m * 131 + k, m * k, 0.0, 0.02).reshape(m, k)
-            cache[key] = g.quantize(wt, w)
-        G.set(W, cache[key])
-    rng = np.random.default_rng(0)
-    xs = {}
-    for k, t in X.items():
-        xs[k] = rng.standard_normal((a.batch, k)).astype(np.float32)
-        G.set(t, xs[k])
-    log(f"[bench] weights uploaded in {time.time() - t0:.1f}s")
-
-    # correctness spot check of the lm_head output against the oracle (the checker)
-    assert G.compute(plugin.backend) == 0
-
-    # timed region: warmup, then K steps, HIP events around every launch group
-    plugin.profile(G.gf, max(1, a.warmup))
-    prof = plugin.profile(G.gf, a.steps)
-    step_ms = sum(ms for _, ms in prof)
-    gemv = [(lab, ms) for lab, ms in prof if lab.startswith("mul_mat")]
-    total_w_bytes = sum(m * k * bpw for _, m, k in shapes)
-    # dominant kernel: per-launch algorithmic bytes over its mean duration
-    alg_bytes = [m * k * bpw + 4 * k * a.batch + 4 * m * a.batch for _, m, k in shapes]
-    gemv_ms = [ms for _, ms in gemv]
-    achieved_gbs = sum(alg_bytes) / (sum(gemv_ms) * 1e-3) / 1e9
-    head_ms = gemv_ms[-1]
-    head_gbs = alg_bytes[-1] / (head_ms * 1e-3) / 1e9
-    log(f"[bench] step {step_ms:.3f} ms over {len(prof)} launch groups; mul_mat {achieved_gbs:.0f} GB/s "
-        f"({achieved_gbs / HBM_PEAK_GBS:.1%} of peak); lm_head {head_ms * 1e3:.1f} us = {head_gbs:.0f} GB/s")
-
-    cpu = None
-    if not a.no_cpu:
-        cpu = cpu_baseline(g, wt, cache, xs, a.batch)
-
-    tokens_per_step = a.batch
+    log(f"[bench] backend {g.plugin().name}")
+    main_r = run_workload(a.workload, a.steps, a.warmup, a.profile_iters, not a.no_cpu, a.cpu_seconds)
+    b1 = None
+    if not a.no_b1 and a.workload != "qwen3-0.6b-q8_0-b1":
+        r1 = run_workload("qwen3-0.6b-q8_0-b1", min(a.steps, 128), a.warmup, a.profile_iters, False, 0)
+        b1 = {"tokens_per_s": round(r1["tok_s"], 1), "ms_per_step": round(r1["ms_per_step"], 4),
+              "mul_mat_q8_0_gbs": round(r1["gemv_gbs"], 1)}
+    frac = main_r["gemv_gbs"] / HBM_PEAK_GBS
     out = {
-        "metric": "decode tokens/sec @ batch 8 (mul_mat weight stream of one Qwen3-0.6B decode step)",
-        "value": round(tokens_per_step / (step_ms * 1e-3), 1),
+        "metric": "decode tokens/sec @ batch 8 (Qwen3-0.6B-shaped Q4_K decoder); quantized mul_mat HBM GB/s as % of peak",
+        "value": round(main_r["tok_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
-        "steps": a.steps,
+        "steps": main_r["steps"],
         "warmup": a.warmup,
-        "ms_per_step": round(step_ms, 4),
+        "ms_per_step": round(main_r["ms_per_step"], 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_K x q8_K int8 dot, f32 accumulate" if wt == g.Q4_K else "q8_0 x q8_0 int8 dot, f32 accumulate",
-        "data": "synthetic (N(0,0.02) weights quantized, N(0,1) activations)",
-        "config": {"workload": f"qwen3-0.6b-shaped {a.wtype} decoder mul_mat set, {a.layers} layers + lm_head",
-                   "batch": a.batch, "weight_bytes_per_step": int(total_w_bytes), "parallelism": "single-gpu"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved_gbs / HBM_PEAK_GBS, 4), "traffic": None},
-        "cpu_baseline": cpu,
+        "dtype": "q4_K weights x q8_K activations (int8 dot, f64 block sums), f16 KV, f32 activations",
+        "data": "synthetic: random-init N(0,0.02) weights quantized to Q4_K, seeded N(0,1) 375-position prefixes",
+        "config": {"workload": a.workload, "model": "qwen3-0.6b-shaped (hidden 1024, 28 layers, 16/8 heads, "
+                   "head_dim 128, ffn 3072, vocab 151936)", "global_batch": 8, "seq_len": 1024,
+                   "prefill_positions": main_r["n_prefill"], "parallelism": "single-gpu"},
+        "roofline": {"bound": "hbm", "achieved": round(main_r["gemv_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(frac, 4), "traffic": None,
+                     "kernel": "k_mmv_q4_K (all GEMV launches of one decode step, algorithmic weight bytes / "
+                               "summed launch time)"},
+        "cpu_baseline": main_r["cpu"],
+        "prefill_ms": round(main_r["prefill_ms"], 2),
+        "eager_step_ms": round(main_r["eager_step_ms"], 4),
+        "kernels": main_r["breakdown"],
+        "batch1_q8_0": b1,
     }
     print(json.dumps(out), flush=True)
     return 0
-
-
-def cpu_baseline(g, wt, cache, xs, batch):
-    """The oracle's mul_mat (the checker) on the host cores over a bounded
-    sample of the same workload: the five per-layer matrices of one layer,
-    repeated until ~10 s, scaled to tokens/s of a full 28-layer step."""
-    from oracle import ref
-
-    threads = os.cpu_count() or 1
-    layer_bytes = 0
-    t_total = 0.0
-    reps = 0
-    t_start = time.time()
-    while time.time() - t_start < 10.0:
-        for name, m, k in QWEN06_LAYER:
-            wq = cache[(m, k)]
-            t0 = time.perf_counter()
-            ref.mul_mat(wt, wq, m, k, xs[k], threads=threads)
-            t_total += time.perf_counter() - t0
-            if reps == 0:
-                layer_bytes += wq.nbytes
-        reps += 1
-    per_layer = t_total / reps
-    m, k = QWEN06_HEAD[1], QWEN06_HEAD[2]
-    head_bytes = cache[(m, k)].nbytes
-    step_s = per_layer * 28 + per_layer * head_bytes / layer_bytes
-    return {"value": round(batch / step_s, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle mul_mat over one layer's 5 matrices x{reps}, batch {batch}, scaled to 28 layers "
-                      f"+ lm_head by weight bytes"}
 
 
 if __name__ == "__main__":

@@ -89,6 +89,10 @@ int oa_qwen_generate(oa_qwen_session * s, const int32_t * first_tokens, int n_st
 /* Device KV cache of one layer for one sequence, f16 bits [n_kv_head][max_positions][head_dim] each. */
 int oa_qwen_read_kv(const oa_qwen_session * s, int layer, int seq, uint16_t * k_out, uint16_t * v_out);
 
+/* The persistent decode-step graph (built on the first decode step; NULL
+ * before), for measurement hooks that replay it. */
+struct ggml_cgraph * oa_qwen_decode_graph(oa_qwen_session * s);
+
 /* Degenerate n-gram guard (seq2seq_greedy_decode.rs:569-605): smallest n in
  * 1..max_ngram whose trailing n-gram repeats at least 8 (n=1), 6 (n=2) or 4
  * (n>=3) times back to back. Returns the length to keep (truncating the run

@@ -137,7 +137,10 @@ void launch_silu_mul(const tview & d, const tview & g, const tview & u, hipStrea
 
 // One wave per row. mode 0: RMSNorm, 1: LayerNorm. Optional fused weight
 // multiply (w broadcast over rows) and bias add, matching the
-// rms_norm->mul and norm->mul->add sequences of nn/norm.rs:10-56.
+// rms_norm->mul and norm->mul->add sequences of nn/norm.rs:10-56. PER is the
+// number of row elements each lane keeps in registers (the row is read
+// once); the fused weight / bias rows have the norm's width (planner check).
+template <int PER>
 __global__ __launch_bounds__(256) void k_norm(tview d, tview a, int mode, float eps, tview w, int has_w, tview bias,
                                               int has_b, int64_t rows) {
     const int lane = threadIdx.x & 63;
@@ -146,41 +149,64 @@ __global__ __launch_bounds__(256) void k_norm(tview d, tview a, int mode, float 
     const int64_t i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
     const float * x = (const float *) (a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3]);
     float * y = (float *) (d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]);
-    const int64_t n = a.ne[0];
-    // sums in f64 and one rounding, as ggml-cpu's ggml_float accumulators
-    float mean = 0.0f;
-    if (mode == 1) {
-        double s = 0.0;
-        for (int64_t i = lane; i < n; i += 64) s += (double) x[i];
-        mean = (float) (wave_sum_d(s) / (double) n);
-    }
-    double s2 = 0.0;
-    for (int64_t i = lane; i < n; i += 64) {
-        const float v = x[i] - mean;
-        s2 += (double) (v * v);
-    }
-    const float var = (float) (wave_sum_d(s2) / (double) n);
-    const float scale = 1.0f / sqrtf(var + eps);
+    const int n = (int) a.ne[0];
     const float * wr = has_w ? (const float *) (w.data + (i1 % w.ne[1]) * w.nb[1] + (i2 % w.ne[2]) * w.nb[2] +
                                                 (i3 % w.ne[3]) * w.nb[3])
                              : nullptr;
     const float * br = has_b ? (const float *) (bias.data + (i1 % bias.ne[1]) * bias.nb[1] +
                                                 (i2 % bias.ne[2]) * bias.nb[2] + (i3 % bias.ne[3]) * bias.nb[3])
                              : nullptr;
-    for (int64_t i = lane; i < n; i += 64) {
-        float v = (x[i] - mean) * scale;
-        if (has_w) v *= wr[i % w.ne[0]];
-        if (has_b) v += br[i % bias.ne[0]];
-        y[i] = v;
+    float xv[PER];
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = lane + 64 * k;
+        xv[k] = i < n ? x[i] : 0.0f;
+    }
+    // sums in f64 and one rounding, as ggml-cpu's ggml_float accumulators
+    float mean = 0.0f;
+    if (mode == 1) {
+        double s = 0.0;
+#pragma unroll
+        for (int k = 0; k < PER; k++) s += (double) xv[k];
+        mean = (float) (wave_sum_d(s) / (double) n);
+    }
+    double s2 = 0.0;
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        if (lane + 64 * k < n) {
+            const float v = xv[k] - mean;
+            s2 += (double) (v * v);
+        }
+    }
+    const float var = (float) (wave_sum_d(s2) / (double) n);
+    const float scale = 1.0f / sqrtf(var + eps);
+#pragma unroll
+    for (int k = 0; k < PER; k++) {
+        const int i = lane + 64 * k;
+        if (i < n) {
+            float v = (xv[k] - mean) * scale;
+            if (has_w) v *= wr[i];
+            if (has_b) v += br[i];
+            y[i] = v;
+        }
     }
 }
+
+bool norm_supported(int64_t ne0) { return ne0 <= 64 * 64; }
 
 void launch_norm(const tview & d, const tview & a, int mode, float eps, const tview * w, const tview * b,
                  hipStream_t s) {
     const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    const int per = (int) ((a.ne[0] + 63) / 64);
     tview none{};
-    hipLaunchKernelGGL(k_norm, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, s, d, a, mode, eps, w ? *w : none,
-                       w ? 1 : 0, b ? *b : none, b ? 1 : 0, rows);
+    const dim3 grid((unsigned) ((rows + 3) / 4));
+    const tview wv = w ? *w : none, bv = b ? *b : none;
+    const int hw = w ? 1 : 0, hb = b ? 1 : 0;
+    if (per <= 2) hipLaunchKernelGGL(k_norm<2>, grid, dim3(256), 0, s, d, a, mode, eps, wv, hw, bv, hb, rows);
+    else if (per <= 6) hipLaunchKernelGGL(k_norm<6>, grid, dim3(256), 0, s, d, a, mode, eps, wv, hw, bv, hb, rows);
+    else if (per <= 16) hipLaunchKernelGGL(k_norm<16>, grid, dim3(256), 0, s, d, a, mode, eps, wv, hw, bv, hb, rows);
+    else if (per <= 32) hipLaunchKernelGGL(k_norm<32>, grid, dim3(256), 0, s, d, a, mode, eps, wv, hw, bv, hb, rows);
+    else hipLaunchKernelGGL(k_norm<64>, grid, dim3(256), 0, s, d, a, mode, eps, wv, hw, bv, hb, rows);
 }
 
 // -------------------------------------------------------------- rope -----
@@ -379,51 +405,66 @@ void launch_soft_max(const tview & d, const tview & a, const tview * mask, float
 
 // -------------------------------------------------------------- argmax ---
 
-// one workgroup per row; first == 1 keeps the lowest index of the maximum
-// (OpenASR's first-max rule), first == 0 the highest (ggml_vec_argmax_f32)
-__global__ __launch_bounds__(256) void k_argmax(tview a, int32_t * out, int first) {
-    __shared__ float s_v[4];
-    __shared__ int s_i[4];
-    const int64_t row = blockIdx.x;
+// Two passes over 64-bit keys (order-preserving f32 bits in the high word,
+// the index -- or its complement -- in the low word) so the maximum key is the
+// wanted element: first == 1 keeps the lowest index of the maximum (OpenASR's
+// first-max rule), first == 0 the highest (ggml_vec_argmax_f32). Pass 1: one
+// workgroup per (row, 4096-element chunk); pass 2: one wave per row.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t i, int first) {
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return ((uint64_t) u << 32) | (first ? (0xFFFFFFFFu - i) : i);
+}
+
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+constexpr int kArgmaxChunk = 4096;
+
+__global__ __launch_bounds__(256) void k_argmax_part(tview a, uint64_t * keys, int first, int chunks) {
+    __shared__ uint64_t s_k[4];
+    const int64_t row = blockIdx.y;
+    const int chunk = blockIdx.x;
     const float * x = (const float *) (a.data + row * a.nb[1]);
     const int64_t n = a.ne[0];
-    float best = -INFINITY;
-    int bi = first ? 0x7fffffff : -1;
-    for (int64_t i = threadIdx.x; i < n; i += blockDim.x) {
-        const float v = x[i];
-        if (v > best || (v == best && (first ? (int) i < bi : (int) i > bi))) {
-            best = v;
-            bi = (int) i;
-        }
-    }
+    const int64_t i0 = (int64_t) chunk * kArgmaxChunk;
+    const int64_t i1 = i0 + kArgmaxChunk < n ? i0 + kArgmaxChunk : n;
+    uint64_t best = 0;
+    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) best = max_u64(best, argmax_key(x[i], (uint32_t) i, first));
     for (int off = 32; off > 0; off >>= 1) {
-        const float ov = __shfl_xor(best, off);
-        const int oi = __shfl_xor(bi, off);
-        if (ov > best || (ov == best && (first ? oi < bi : oi > bi))) {
-            best = ov;
-            bi = oi;
-        }
+        const uint64_t o = ((uint64_t) __shfl_xor((unsigned) (best >> 32), off) << 32) |
+                           (uint64_t) __shfl_xor((unsigned) best, off);
+        best = max_u64(best, o);
     }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) {
-        s_v[wave] = best;
-        s_i[wave] = bi;
-    }
+    if ((threadIdx.x & 63) == 0) s_k[threadIdx.x >> 6] = best;
     __syncthreads();
+    if (threadIdx.x == 0) keys[row * chunks + chunk] = max_u64(max_u64(s_k[0], s_k[1]), max_u64(s_k[2], s_k[3]));
+}
+
+__global__ void k_argmax_final(const uint64_t * keys, int chunks, int32_t * out, int first) {
+    const int64_t row = blockIdx.x;
+    uint64_t best = 0;
+    for (int c = threadIdx.x; c < chunks; c += 64) best = max_u64(best, keys[row * chunks + c]);
+    for (int off = 32; off > 0; off >>= 1) {
+        const uint64_t o = ((uint64_t) __shfl_xor((unsigned) (best >> 32), off) << 32) |
+                           (uint64_t) __shfl_xor((unsigned) best, off);
+        best = max_u64(best, o);
+    }
     if (threadIdx.x == 0) {
-        for (int w = 1; w < (int) (blockDim.x >> 6); w++) {
-            if (s_v[w] > best || (s_v[w] == best && (first ? s_i[w] < bi : s_i[w] > bi))) {
-                best = s_v[w];
-                bi = s_i[w];
-            }
-        }
-        if (bi < 0 || bi == 0x7fffffff) bi = 0;  // all -inf / NaN row
-        out[row] = bi;
+        const uint32_t lo = (uint32_t) best;
+        out[row] = (int32_t) (first ? 0xFFFFFFFFu - lo : lo);
     }
 }
 
-void launch_argmax(const tview & a, int32_t * out, int first, hipStream_t s) {
-    hipLaunchKernelGGL(k_argmax, dim3((unsigned) a.ne[1]), dim3(256), 0, s, a, out, first);
+size_t argmax_scratch_bytes(int64_t ne0, int64_t rows) {
+    return (size_t) rows * (size_t) ((ne0 + kArgmaxChunk - 1) / kArgmaxChunk) * sizeof(uint64_t);
+}
+
+void launch_argmax(const tview & a, int32_t * out, int first, void * scratch, hipStream_t s) {
+    const int chunks = (int) ((a.ne[0] + kArgmaxChunk - 1) / kArgmaxChunk);
+    uint64_t * keys = (uint64_t *) scratch;
+    hipLaunchKernelGGL(k_argmax_part, dim3((unsigned) chunks, (unsigned) a.ne[1]), dim3(256), 0, s, a, keys, first,
+                       chunks);
+    hipLaunchKernelGGL(k_argmax_final, dim3((unsigned) a.ne[1]), dim3(64), 0, s, keys, chunks, out, first);
 }
 
 // ---------------------------------------------------- float mul_mat ------

@@ -182,12 +182,21 @@ bool planner::plan_mul_mat(const ggml_tensor * t) {
         const int ncu = n_cu;
         char * dst = (char *) t->data;
         const int64_t dst_nb1 = (int64_t) t->nb[1];
-        const bool wide = mmq_supported(wtype, M, K) && N > 8;
+        const bool wide = mmq_supported(wtype, M, K) && N > 16;
+        const bool mfma = gemv_mfma_supported(wtype, M, K);
+        if (!reuse) {
+            add(
+                [=](hipStream_t s) {
+                    act_buffers act = act_carve(wtype, b->scratch, K, N);
+                    launch_quantize_act(xv, wtype, act, s);
+                },
+                t, wtype == GGML_TYPE_Q8_0 ? "quantize_q8_0" : "quantize_q8_K");
+        }
         add(
             [=](hipStream_t s) {
                 act_buffers act = act_carve(wtype, b->scratch, K, N);
-                if (!reuse) launch_quantize_act(xv, wtype, act, s);
                 if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
+                else if (mfma) launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
             t, wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K");
@@ -395,7 +404,13 @@ bool planner::plan() {
                 const tview av = make_view(t->src[0]);
                 int32_t * out = (int32_t *) t->data;
                 const int first = t->op == GGML_OP_ARGMAX_FIRST;
-                add([=](hipStream_t s) { launch_argmax(av, out, first, s); }, t, "argmax");
+                gen_need = std::max(gen_need, argmax_scratch_bytes(av.ne[0], av.ne[1]));
+                backend_state * b = be;
+                add(
+                    [=](hipStream_t s) {
+                        launch_argmax(av, out, first, b->scratch + align_up(b->scratch_cap / 2, kAlign), s);
+                    },
+                    t, "argmax");
                 break;
             }
             case GGML_OP_FLASH_ATTN_EXT:
@@ -607,7 +622,8 @@ bool supports_op(const device_state * dev, const ggml_tensor * t) {
         }
         case GGML_OP_RMS_NORM:
         case GGML_OP_NORM:
-            return f32(t) && f32(t->src[0]) && rows_contiguous(t->src[0], 4) && rows_contiguous(t, 4);
+            return f32(t) && f32(t->src[0]) && rows_contiguous(t->src[0], 4) && rows_contiguous(t, 4) &&
+                   norm_supported(t->ne[0]);
         case GGML_OP_MUL_MAT: {
             const ggml_tensor *w = t->src[0], *x = t->src[1];
             if (!f32(t) || !f32(x) || !is_contiguous(t)) return false;

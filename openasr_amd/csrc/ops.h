@@ -22,6 +22,11 @@ act_buffers act_carve(int wtype, char * base, int64_t K, int64_t ncols);
 void launch_mmv(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                 int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
 
+// MFMA GEMV for up to 16 columns per launch (the decode step), M % 16 == 0
+bool gemv_mfma_supported(int wtype, int64_t M, int64_t K);
+void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
+                      int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
+
 // MFMA int8 GEMM for wider N (prefill)
 bool mmq_supported(int wtype, int64_t M, int64_t K);
 void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
@@ -62,7 +67,9 @@ void launch_set_rows(const tview & dst, int dtype, const tview & src, const tvie
 void launch_get_rows(const tview & dst, const tview & src, int stype, const tview & idx, hipStream_t s, int n_cu);
 void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStream_t s, int n_cu);
 void launch_soft_max(const tview & d, const tview & a, const tview * mask, float scale, hipStream_t s);
-void launch_argmax(const tview & a, int32_t * out, int first, hipStream_t s);
+size_t argmax_scratch_bytes(int64_t ne0, int64_t rows);
+void launch_argmax(const tview & a, int32_t * out, int first, void * scratch, hipStream_t s);
+bool norm_supported(int64_t ne0);
 
 // Q8_0 layout conversion between ggml's interleaved blocks and the row-split
 // device layout (host side, used by set/get_tensor)

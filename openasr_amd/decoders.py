@@ -61,6 +61,7 @@ def lib() -> C.CDLL:
     s("oa_qwen_generate", i, vp, vp, i, vp, vp)
     s("oa_qwen_read_kv", i, vp, i, i, vp, vp)
     s("oa_detect_degenerate_ngram", i, vp, i, i, vp, vp)
+    s("oa_qwen_decode_graph", vp, vp)
     _lib = L
     return L
 
@@ -165,6 +166,9 @@ class QwenSession:
         v = np.zeros(shape, np.uint16)
         self._check(lib().oa_qwen_read_kv(self.ptr, layer, seq, k.ctypes.data, v.ctypes.data), "read_kv")
         return k, v
+
+    def decode_graph(self):
+        return lib().oa_qwen_decode_graph(self.ptr)
 
     def position(self, seq: int = 0) -> int:
         return lib().oa_qwen_session_position(self.ptr, seq)

@@ -483,6 +483,8 @@ int oa_qwen_read_kv(const oa_qwen_session * s, int layer, int seq, uint16_t * k_
     return 0;
 }
 
+struct ggml_cgraph * oa_qwen_decode_graph(oa_qwen_session * s) { return s->decode.gf; }
+
 int oa_detect_degenerate_ngram(const int32_t * tokens, int len, int max_ngram, int * ngram_len, int * repeats) {
     for (int n = 1; n <= max_ngram; n++) {
         const int bound = n == 1 ? 8 : (n == 2 ? 6 : 4);

@@ -227,3 +227,37 @@ class QwenRef:
 
     def step(self, token: int):
         return self.forward(self.embed([token]))
+
+
+class QwenRefBatch:
+    """CPU reference of a batched decode step over n_seq sequences (weights
+    streamed once per step), continuing from given KV caches."""
+
+    def __init__(self, cfg, pointer_table, max_pos: int, n_seq: int, fa_fidelity: int = 3, threads: int = 0):
+        L = lib()
+        L.ref_qwen_decode_batch.restype = None
+        L.ref_qwen_decode_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                            C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
+        self.dims = QwenDims(cfg.d_model, cfg.n_layers, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.ffn, cfg.vocab,
+                             cfg.wtype, cfg.rope_theta, cfg.rms_eps)
+        self.table = (C.c_void_p * len(pointer_table))(*pointer_table)
+        self.max_pos, self.n_seq, self.fidelity, self.threads = max_pos, n_seq, fa_fidelity, threads
+        shape = (cfg.n_kv_head, max_pos, cfg.head_dim)
+        self.k = [[np.zeros(shape, np.uint16) for _ in range(cfg.n_layers)] for _ in range(n_seq)]
+        self.v = [[np.zeros(shape, np.uint16) for _ in range(cfg.n_layers)] for _ in range(n_seq)]
+        flat_k = [a.ctypes.data for s in self.k for a in s]
+        flat_v = [a.ctypes.data for s in self.v for a in s]
+        self.kp = (C.c_void_p * len(flat_k))(*flat_k)
+        self.vp = (C.c_void_p * len(flat_v))(*flat_v)
+        self.pos = np.zeros(n_seq, np.int32)
+
+    def step(self, tokens, want_logits: bool = False):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        top1 = np.zeros(self.n_seq, np.int32)
+        logits = np.zeros((self.n_seq, self.dims.vocab), np.float32) if want_logits else None
+        pos = np.ascontiguousarray(self.pos, dtype=np.int32)
+        lib().ref_qwen_decode_batch(C.byref(self.dims), self.table, self.kp, self.vp, self.max_pos,
+                                    tokens.ctypes.data, pos.ctypes.data, self.n_seq, top1.ctypes.data,
+                                    logits.ctypes.data if want_logits else None, self.fidelity, self.threads)
+        self.pos += 1
+        return (top1, logits) if want_logits else top1

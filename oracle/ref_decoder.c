@@ -130,3 +130,86 @@ int32_t ref_qwen_forward(const ref_qwen_dims * m, const void * const * t, uint16
     free(mask);
     return top1;
 }
+
+/*
+ * One decode step of n_seq sequences at once (the serve-batch step,
+ * models/qwen/batched_decode.rs:894-975): the projections run as one
+ * mul_mat over n_seq columns (weights streamed once), attention per
+ * sequence over its own cache. kcache/vcache: [seq * n_layers + layer].
+ * top1 [n_seq] and logits [n_seq][vocab] (optional) out.
+ */
+void ref_qwen_decode_batch(const ref_qwen_dims * m, const void * const * t, uint16_t * const * kcache,
+                           uint16_t * const * vcache, int max_pos, const int32_t * tokens, const int32_t * pos,
+                           int n_seq, int32_t * top1, float * logits, int fa_fidelity, int threads) {
+    const int d = m->d_model, hd = m->head_dim, hq = m->n_head, hkv = m->n_kv_head, N = n_seq;
+    const int q_w = hq * hd, kv_w = hkv * hd, qkv_w = q_w + 2 * kv_w;
+    const size_t rs_d = ref_row_size(m->wtype, d);
+    float * x = (float *) malloc(sizeof(float) * (size_t) N * d);
+    float * nrm = (float *) malloc(sizeof(float) * (size_t) N * (d > m->ffn ? d : m->ffn));
+    float * qkv = (float *) malloc(sizeof(float) * (size_t) N * qkv_w);
+    float * q = (float *) malloc(sizeof(float) * (size_t) N * q_w);
+    float * k = (float *) malloc(sizeof(float) * (size_t) N * kv_w);
+    float * att = (float *) malloc(sizeof(float) * (size_t) N * q_w);
+    float * tmp = (float *) malloc(sizeof(float) * (size_t) N * d);
+    float * g = (float *) malloc(sizeof(float) * (size_t) N * m->ffn);
+    float * u = (float *) malloc(sizeof(float) * (size_t) N * m->ffn);
+    float * lg = (float *) malloc(sizeof(float) * (size_t) N * m->vocab);
+    uint16_t * mask = (uint16_t *) malloc(sizeof(uint16_t) * (size_t) max_pos);
+    ref_qwen_embed(m, t, tokens, N, x);
+    for (int l = 0; l < m->n_layers; l++) {
+        ref_rms_norm(x, nrm, d, N, m->rms_eps);
+        mul_row_weight(nrm, (const float *) tp(t, l, 0), N, d);
+        ref_mul_mat(m->wtype, tp(t, l, 1), rs_d, qkv_w, d, nrm, d, N, qkv, qkv_w, threads);
+        for (int i = 0; i < N; i++) {
+            memcpy(q + (size_t) i * q_w, qkv + (size_t) i * qkv_w, sizeof(float) * q_w);
+            memcpy(k + (size_t) i * kv_w, qkv + (size_t) i * qkv_w + q_w, sizeof(float) * kv_w);
+        }
+        ref_rms_norm(q, q, hd, (int64_t) N * hq, m->rms_eps);
+        mul_row_weight(q, (const float *) tp(t, l, 2), N * hq, hd);
+        ref_rms_norm(k, k, hd, (int64_t) N * hkv, m->rms_eps);
+        mul_row_weight(k, (const float *) tp(t, l, 3), N * hkv, hd);
+        ref_rope_neox(q, q, hd, hq, N, pos, hd, m->rope_theta, 1.0f);
+        ref_rope_neox(k, k, hd, hkv, N, pos, hd, m->rope_theta, 1.0f);
+        for (int i = 0; i < N; i++) {
+            uint16_t * kc = kcache[(size_t) i * m->n_layers + l];
+            uint16_t * vc = vcache[(size_t) i * m->n_layers + l];
+            for (int h = 0; h < hkv; h++) {
+                ref_fp32_to_fp16_row(k + ((size_t) i * hkv + h) * hd, kc + ((size_t) h * max_pos + pos[i]) * hd, hd);
+                ref_fp32_to_fp16_row(qkv + (size_t) i * qkv_w + q_w + kv_w + (size_t) h * hd,
+                                     vc + ((size_t) h * max_pos + pos[i]) * hd, hd);
+            }
+            const int n_kv = pos[i] + 1;
+            for (int j = 0; j < n_kv; j++) mask[j] = 0;
+            ref_flash_attn_ext(q + (size_t) i * q_w, q_w, hd, kc, vc, (int64_t) max_pos * hd, hd, mask, n_kv,
+                               att + (size_t) i * q_w, hd, 1, hq, hkv, n_kv, 1.0f / sqrtf((float) hd), fa_fidelity,
+                               threads);
+        }
+        ref_mul_mat(m->wtype, tp(t, l, 4), ref_row_size(m->wtype, q_w), d, q_w, att, q_w, N, tmp, d, threads);
+        for (size_t i = 0; i < (size_t) N * d; i++) x[i] = x[i] + tmp[i];
+        ref_rms_norm(x, nrm, d, N, m->rms_eps);
+        mul_row_weight(nrm, (const float *) tp(t, l, 5), N, d);
+        ref_mul_mat(m->wtype, tp(t, l, 6), rs_d, m->ffn, d, nrm, d, N, g, m->ffn, threads);
+        ref_mul_mat(m->wtype, tp(t, l, 7), rs_d, m->ffn, d, nrm, d, N, u, m->ffn, threads);
+        for (size_t i = 0; i < (size_t) N * m->ffn; i++) g[i] = ref_silu(g[i]) * u[i];
+        ref_mul_mat(m->wtype, tp(t, l, 8), ref_row_size(m->wtype, m->ffn), d, m->ffn, g, m->ffn, N, tmp, d, threads);
+        for (size_t i = 0; i < (size_t) N * d; i++) x[i] = tmp[i] + x[i];
+    }
+    ref_rms_norm(x, nrm, d, N, m->rms_eps);
+    mul_row_weight(nrm, (const float *) t[T_OUT_NORM], N, d);
+    ref_mul_mat(m->wtype, t[T_EMBD], rs_d, m->vocab, d, nrm, d, N, lg, m->vocab, threads);
+    for (int i = 0; i < N; i++) {
+        top1[i] = ref_argmax_first(lg + (size_t) i * m->vocab, m->vocab);
+        if (logits) memcpy(logits + (size_t) i * m->vocab, lg + (size_t) i * m->vocab, sizeof(float) * m->vocab);
+    }
+    free(x);
+    free(nrm);
+    free(qkv);
+    free(q);
+    free(k);
+    free(att);
+    free(tmp);
+    free(g);
+    free(u);
+    free(lg);
+    free(mask);
+}
