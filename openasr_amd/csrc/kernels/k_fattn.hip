@@ -2,309 +2,485 @@
 // query heads (call site crates/openasr-core/src/ggml_runtime/cpu_graph.rs:
 // 4144-4215; graph built in crates/openasr-core/src/nn/decoder.rs:2031-2105).
 //
-// Split-KV, two passes, order-independent sums:
-//   scores   one workgroup per (KV chunk, kv head, sequence, query tile)
-//            computes s = (q . k) * scale + mask for every query head that
-//            shares the kv head (K is read once per kv head) and the per-chunk
-//            row maxima. A chunk whose mask is -inf for every row of the tile
-//            is skipped without touching K (the graph always passes the full
-//            fixed span, nn/decoder.rs:1295-1301).
-//   accum    the same grid takes the row's global max M, forms
-//            p = exp(s - M), and accumulates sum(p) and sum(p * V) in f64
-//            per chunk (V read once per kv head; masked positions skipped).
-//   combine  sums the chunk partials in f64 and divides once.
-// Q is rounded to f16 before the dot with f16 K, as ggml-cpu does; products
-// of two halves are exact in f32 and every sum is carried in f64, so the
-// result does not depend on how positions are split across lanes, waves or
-// chunks -- the CPU reference computes the same value sequentially.
+// The result is defined chunk-wise over fixed 64-position KV chunks, the
+// same on every launch shape:
+//   per chunk c   s = f32(sum_f64(f16(q) * k)) * scale + mask   (masked
+//                 positions are skipped outright, as ggml-cpu does)
+//                 m_c = max s, p = exp(s - m_c), l_c = sum_f64 p,
+//                 a_c = sum_f64 p * v
+//   combine       M = max m_c; for c in order: w = exp(m_c - M),
+//                 L += w * l_c, O += w * a_c; out = f32(O / L)
+// Products of two halves are exact in f32 and of a float and a half exact in
+// f64, so the chunk sums do not depend on how positions are spread over
+// lanes; the combine runs in chunk order. The CPU reference evaluates the
+// same definition (oracle fidelity 4).
+//
+// Two launch forms compute it:
+//   split  one workgroup per (chunk, kv head, sequence, query tile): loads
+//          the chunk's mask first and skips a fully masked chunk without
+//          touching K/V (the graph always passes the full fixed span,
+//          nn/decoder.rs:1295-1301), then issues all of its K and V loads at
+//          once; partials go to scratch and a second launch combines them
+//          per tile. Used for decode, where tiles alone cannot fill the chip.
+//   full   one workgroup per (kv head, sequence, query tile) walks every
+//          chunk twice (chunk maxima, then sums). Used for prefill.
+// Both can quantize their output straight into the activation layout of the
+// MUL_MAT that consumes it (the attention output projection), since a tile
+// holds all query heads of one kv head: g*D consecutive elements of a column.
 #include "../mi355x_common.h"
 #include "../ops.h"
+#include "../quant_dev.h"
 
 namespace mi355x {
 
 constexpr int kFaThreads = 256;
-constexpr int kFaMaxChunk = 256;
-constexpr int kFaRows = 8;  // query rows (heads x positions) per workgroup
+constexpr int kFaChunk = 64;
+constexpr int kFaMaxChunks = 256;  // 16384 KV positions
+constexpr int kFaMaxRows = 8;      // query rows (positions x heads of one kv head) per tile
 
 struct fa_tile {
-    int kvh, seq, g, q0, nrows, c0, clen, kv_seq;
+    int kvh, seq, g, tq0, ntq, nrows, kv_seq, gti;
 };
 
 __device__ __forceinline__ fa_tile fa_tile_of(const fattn_args & a) {
     fa_tile t;
-    t.kvh = blockIdx.y % a.hkv;
-    t.seq = blockIdx.y / a.hkv;
+    t.kvh = (int) blockIdx.y % a.hkv;
+    t.seq = (int) blockIdx.y / a.hkv;
     t.g = a.hq / a.hkv;
-    const int tq_per_tile = kFaRows / t.g;
-    t.q0 = blockIdx.z * tq_per_tile;
-    t.nrows = min(tq_per_tile, a.n_q - t.q0) * t.g;
-    t.c0 = blockIdx.x * a.chunk;
-    t.clen = min(a.chunk, a.n_kv - t.c0);
+    t.tq0 = (int) blockIdx.z * a.tq;
+    t.ntq = min(a.tq, a.n_q - t.tq0);
+    t.nrows = t.ntq * t.g;
     t.kv_seq = t.seq / a.rk3;
+    t.gti = (int) blockIdx.y * a.q_tiles + (int) blockIdx.z;
     return t;
 }
 
-// output row index of tile row r (= query position q0 + r / g, head kvh*g + r % g)
+// output row (ggml result layout [D, hq, n_q, n_seq]) of tile row r
 __device__ __forceinline__ int64_t fa_orow(const fattn_args & a, const fa_tile & t, int r) {
-    return ((int64_t) t.seq * a.n_q + t.q0 + r / t.g) * a.hq + (int64_t) t.kvh * t.g + r % t.g;
+    return ((int64_t) t.seq * a.n_q + t.tq0 + r / t.g) * a.hq + (int64_t) t.kvh * t.g + r % t.g;
 }
 
-__device__ __forceinline__ const uint16_t * fa_mask_row(const fattn_args & a, const fa_tile & t, int tq) {
-    return (const uint16_t *) (a.mask + (int64_t) (t.q0 + tq) * a.m_nb1 + (int64_t) (t.seq % a.m_ne3) * a.m_nb3);
+template <int D, int R>
+struct alignas(16) fa_smem {
+    float q[R][D];           // f16-rounded queries; after the combine, the output rows
+    float s[R][kFaChunk];    // scores, then p
+    float mask[R][kFaChunk]; // per query position of the tile
+    float m[R];
+    double l[R];
+    double red[4][R][D];
+    float w[R];
+};
+
+__device__ __forceinline__ void unpack8(const uint4 & u, float * f) {
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        f[2 * i] = half_bits_to_float((uint16_t) (w[i] & 0xFFFF));
+        f[2 * i + 1] = half_bits_to_float((uint16_t) (w[i] >> 16));
+    }
 }
 
-__device__ __forceinline__ double dsum_group(double v, int width) {
-    for (int off = width / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, width);
-    return v;
-}
-
-template <int D>
-__global__ __launch_bounds__(kFaThreads) void k_fattn_scores(fattn_args a, float * __restrict__ S,
-                                                             float * __restrict__ cmax) {
-    constexpr int LPP = D / 8;     // lanes per key position
-    constexpr int PPW = 64 / LPP;  // positions per wave per step
-    __shared__ float s_max[4][kFaRows];
-    __shared__ int s_any;
-    const fa_tile t = fa_tile_of(a);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int chunk = blockIdx.x;
-
-    if (tid == 0) s_any = a.mask ? 0 : 1;
-    __syncthreads();
-    if (a.mask) {
-        int any = 0;
-        for (int idx = tid; idx < t.clen * (t.nrows / t.g); idx += kFaThreads) {
-            if (fa_mask_row(a, t, idx / t.clen)[t.c0 + idx % t.clen] != 0xFC00) any = 1;
-        }
-        if (any) s_any = 1;
-    }
-    __syncthreads();
-    if (!s_any) {
-        if (tid < t.nrows) cmax[fa_orow(a, t, tid) * a.n_chunks + chunk] = -INFINITY;
-        return;
-    }
-
-    const char * kbase = a.k + (int64_t) t.kvh * a.k_nb2 + (int64_t) t.kv_seq * a.k_nb3;
-    const int dl = (lane % LPP) * 8;
-    float qr[kFaRows][8];
-#pragma unroll
-    for (int r = 0; r < kFaRows; r++) {
-        const bool ok = r < t.nrows;
-        const float * qp = (const float *) (a.q + (int64_t) (t.q0 + (ok ? r / t.g : 0)) * a.q_nb1 +
-                                            (int64_t) (t.kvh * t.g + r % t.g) * a.q_nb2 + (int64_t) t.seq * a.q_nb3);
-#pragma unroll
-        for (int i = 0; i < 8; i++) qr[r][i] = ok ? round_to_half(qp[dl + i]) : 0.0f;
-    }
-    float rmax[kFaRows];
-#pragma unroll
-    for (int r = 0; r < kFaRows; r++) rmax[r] = -INFINITY;
-    for (int base = wave * PPW; base < t.clen; base += 4 * PPW) {
-        const int p = base + lane / LPP;
-        const bool valid = p < t.clen;
-        float kf[8];
-        if (valid) {
-            const uint4 kv4 = *(const uint4 *) (kbase + (int64_t) (t.c0 + p) * a.k_nb1 + dl * 2);
-            const uint32_t w[4] = {kv4.x, kv4.y, kv4.z, kv4.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                kf[2 * i] = half_bits_to_float((uint16_t) (w[i] & 0xFFFF));
-                kf[2 * i + 1] = half_bits_to_float((uint16_t) (w[i] >> 16));
+// mask of chunk c for the tile's query positions; true if any entry is live
+template <int D, int R>
+__device__ __forceinline__ bool fa_load_mask(const fattn_args & a, const fa_tile & t, int c, fa_smem<D, R> & sm) {
+    const int clen = min(kFaChunk, a.n_kv - c * kFaChunk);
+    int live = 0;
+    for (int idx = (int) threadIdx.x; idx < t.ntq * kFaChunk; idx += kFaThreads) {
+        const int tql = idx / kFaChunk, p = idx % kFaChunk;
+        float mv = -INFINITY;
+        if (p < clen) {
+            mv = 0.0f;
+            if (a.mask) {
+                const uint16_t * mr = (const uint16_t *) (a.mask + (int64_t) (t.tq0 + tql) * a.m_nb1 +
+                                                          (int64_t) (t.seq % a.m_ne3) * a.m_nb3);
+                mv = half_bits_to_float(mr[c * kFaChunk + p]);
             }
-        } else {
-#pragma unroll
-            for (int i = 0; i < 8; i++) kf[i] = 0.0f;
         }
+        sm.mask[tql][p] = mv;
+        live |= mv != -INFINITY;
+    }
+    return __syncthreads_or(live) != 0;
+}
+
+// K: thread t holds position t/4, dims (t%4)*D/4 .. +D/4
+template <int D>
+__device__ __forceinline__ void fa_load_k(const fattn_args & a, const fa_tile & t, int c, uint4 (&kr)[D / 32]) {
+    const int clen = min(kFaChunk, a.n_kv - c * kFaChunk);
+    const int p = (int) threadIdx.x >> 2, sk = (int) threadIdx.x & 3;
+    const char * kb = a.k + (int64_t) t.kvh * a.k_nb2 + (int64_t) t.kv_seq * a.k_nb3 +
+                      (int64_t) (c * kFaChunk + p) * a.k_nb1 + sk * (D / 4) * 2;
 #pragma unroll
-        for (int r = 0; r < kFaRows; r++) {
-            if (r >= t.nrows) break;
+    for (int u = 0; u < D / 32; u++) kr[u] = p < clen ? *(const uint4 *) (kb + 16 * u) : make_uint4(0, 0, 0, 0);
+}
+
+// V: thread t holds dims (t % (D/8))*8 .. +8 of positions t/(D/8) + NPG*j
+template <int D>
+__device__ __forceinline__ void fa_load_v(const fattn_args & a, const fa_tile & t, int c, uint4 (&vr)[D / 32]) {
+    constexpr int DS = D / 8, NPG = kFaThreads / DS;
+    const int clen = min(kFaChunk, a.n_kv - c * kFaChunk);
+    const int ds = (int) threadIdx.x % DS, pg = (int) threadIdx.x / DS;
+    const char * vb = a.v + (int64_t) t.kvh * a.v_nb2 + (int64_t) t.kv_seq * a.v_nb3 + ds * 16;
+#pragma unroll
+    for (int j = 0; j < D / 32; j++) {
+        const int p = pg + NPG * j;
+        vr[j] = p < clen ? *(const uint4 *) (vb + (int64_t) (c * kFaChunk + p) * a.v_nb1) : make_uint4(0, 0, 0, 0);
+    }
+}
+
+template <int D, int R>
+__device__ __forceinline__ void fa_load_q(const fattn_args & a, const fa_tile & t, fa_smem<D, R> & sm) {
+    for (int idx = (int) threadIdx.x; idx < t.nrows * D; idx += kFaThreads) {
+        const int r = idx / D, d = idx % D;
+        const float * qp = (const float *) (a.q + (int64_t) (t.tq0 + r / t.g) * a.q_nb1 +
+                                            (int64_t) (t.kvh * t.g + r % t.g) * a.q_nb2 + (int64_t) t.seq * a.q_nb3);
+        sm.q[r][d] = round_to_half(qp[d]);
+    }
+}
+
+// scores of the chunk into sm.s (needs sm.q and sm.mask; caller syncs after)
+template <int D, int R>
+__device__ __forceinline__ void fa_scores(const fattn_args & a, const fa_tile & t, const uint4 (&kr)[D / 32],
+                                          fa_smem<D, R> & sm) {
+    const int p = (int) threadIdx.x >> 2, sk = (int) threadIdx.x & 3;
+    float kf[D / 4];
+#pragma unroll
+    for (int u = 0; u < D / 32; u++) unpack8(kr[u], kf + 8 * u);
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        if (r < t.nrows) {
+            const float * qr = &sm.q[r][sk * (D / 4)];
             double acc = 0.0;
 #pragma unroll
-            for (int i = 0; i < 8; i++) acc += (double) (kf[i] * qr[r][i]);  // exact products
-            acc = dsum_group(acc, LPP);
-            if (valid && (lane % LPP) == 0) {
-                const float mv = a.mask ? half_bits_to_float(fa_mask_row(a, t, r / t.g)[t.c0 + p]) : 0.0f;
-                // a masked position is skipped outright, as ggml-cpu does, so
-                // whatever an unwritten cache slot holds never reaches the sums
-                const float s = mv == -INFINITY ? -INFINITY : (float) acc * a.scale + mv;
-                S[fa_orow(a, t, r) * a.n_kv + t.c0 + p] = s;
-                rmax[r] = fmaxf(rmax[r], s);
+            for (int i = 0; i < D / 4; i++) acc += (double) (kf[i] * qr[i]);  // exact products
+            acc += __shfl_xor(acc, 1);
+            acc += __shfl_xor(acc, 2);
+            if (sk == 0) {
+                const float mv = sm.mask[r / t.g][p];
+                sm.s[r][p] = mv == -INFINITY ? -INFINITY : (float) acc * a.scale + mv;
+            }
+        }
+    }
+}
+
+// chunk maximum m_c, p = exp(s - m_c) in place, l_c; one wave per row
+template <int D, int R>
+__device__ __forceinline__ void fa_softmax_chunk(const fa_tile & t, fa_smem<D, R> & sm) {
+    const int lane = (int) threadIdx.x & 63, wave = (int) threadIdx.x >> 6;
+    for (int r = wave; r < t.nrows; r += 4) {
+        const float s = sm.s[r][lane];
+        const float m = wave_max(s);
+        const float p = s == -INFINITY ? 0.0f : expf_det(s - m);
+        sm.s[r][lane] = p;
+        const double l = wave_sum_d((double) p);
+        if (lane == 0) {
+            sm.m[r] = m;
+            sm.l[r] = l;
+        }
+    }
+}
+
+// a_c = sum p * v into sm.red (per wave; the caller sums the four waves in
+// order); caller syncs after
+template <int D, int R>
+__device__ __forceinline__ void fa_pv(const fa_tile & t, const uint4 (&vr)[D / 32], fa_smem<D, R> & sm) {
+    constexpr int DS = D / 8, NPG = kFaThreads / DS;
+    const int lane = (int) threadIdx.x & 63, wave = (int) threadIdx.x >> 6;
+    const int ds = (int) threadIdx.x % DS, pg = (int) threadIdx.x / DS;
+    double acc[R][8];
+#pragma unroll
+    for (int r = 0; r < R; r++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc[r][i] = 0.0;
+#pragma unroll
+    for (int j = 0; j < D / 32; j++) {
+        const int p = pg + NPG * j;
+        float vf[8];
+        unpack8(vr[j], vf);
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float pr = r < t.nrows ? sm.s[r][p] : 0.0f;
+            if (pr != 0.0f) {  // masked slots may hold anything, even NaN
+#pragma unroll
+                for (int i = 0; i < 8; i++) acc[r][i] += (double) pr * (double) vf[i];  // exact products
             }
         }
     }
 #pragma unroll
-    for (int r = 0; r < kFaRows; r++) {
-        const float m = wave_max(rmax[r]);
-        if (lane == 0) s_max[wave][r] = m;
+    for (int off = DS; off < 64; off <<= 1) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) acc[r][i] += __shfl_xor(acc[r][i], off);
+    }
+    if (lane < DS) {
+#pragma unroll
+        for (int r = 0; r < R; r++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) sm.red[wave][r][ds * 8 + i] = acc[r][i];
+    }
+}
+
+template <int D, int R>
+__device__ __forceinline__ double fa_red_sum(const fa_smem<D, R> & sm, int r, int d) {
+    return ((sm.red[0][r][d] + sm.red[1][r][d]) + sm.red[2][r][d]) + sm.red[3][r][d];
+}
+
+// output rows are in sm.q; quantize the tile's column segments for the next
+// MUL_MAT (Q8_K for Q4_K weights, Q8_0 for Q8_0 weights)
+template <int D, int R>
+__device__ __forceinline__ void fa_quantize_out(const fattn_args & a, const fa_tile & t, fa_smem<D, R> & sm) {
+    const int lane = (int) threadIdx.x & 63, wave = (int) threadIdx.x >> 6;
+    const int seg = t.g * D;
+    const int64_t K = (int64_t) a.hq * D;
+    const int64_t e0 = (int64_t) t.kvh * seg;
+    for (int tql = 0; tql < t.ntq; tql++) {
+        const int64_t col = (int64_t) t.seq * a.n_q + t.tq0 + tql;
+        const float * row = &sm.q[tql * t.g][0];
+        for (int piece = wave; piece * 256 < seg; piece += 4) {
+            const int e = piece * 256 + lane * 4;
+            const float4 v = e < seg ? *(const float4 *) (row + e) : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (a.qtype == GGML_TYPE_Q4_K) {
+                const q8_K_lane o = quantize_q8_K_wave(v, lane);
+                *(char4 *) (a.act.q + col * K + e0 + e) = o.q;
+                if ((lane & 3) == 0) a.act.bsums[col * (K / 16) + (e0 + e) / 16] = (int16_t) o.bsum;
+                if (lane == 0) a.act.d[col * (K / 256) + (e0 + piece * 256) / 256] = o.d;
+            } else {
+                const q8_0_lane o = quantize_q8_0_group(v);
+                if (e < seg) {
+                    *(char4 *) (a.act.q + col * K + e0 + e) = o.q;
+                    if ((lane & 7) == 0) a.act.d[col * (K / 32) + (e0 + e) / 32] = o.d;
+                }
+            }
+        }
+    }
+}
+
+template <int D, int R>
+__global__ __launch_bounds__(kFaThreads) void k_fattn_split(fattn_args a, float * __restrict__ part_m,
+                                                            double * __restrict__ part_l,
+                                                            double * __restrict__ part_acc) {
+    __shared__ fa_smem<D, R> sm;
+    const fa_tile t = fa_tile_of(a);
+    const int c = (int) blockIdx.x, tid = (int) threadIdx.x;
+    const int64_t prow = (int64_t) t.gti * R;  // partial row of tile row 0
+
+    if (fa_load_mask<D, R>(a, t, c, sm)) {
+        uint4 kr[D / 32], vr[D / 32];
+        fa_load_k<D>(a, t, c, kr);
+        fa_load_v<D>(a, t, c, vr);
+        fa_load_q<D, R>(a, t, sm);
+        __syncthreads();
+        fa_scores<D, R>(a, t, kr, sm);
+        __syncthreads();
+        fa_softmax_chunk<D, R>(t, sm);
+        __syncthreads();
+        fa_pv<D, R>(t, vr, sm);
+        __syncthreads();
+        for (int idx = tid; idx < t.nrows * D; idx += kFaThreads) {
+            const int r = idx / D, d = idx % D;
+            part_acc[((prow + r) * a.n_chunks + c) * D + d] = fa_red_sum<D, R>(sm, r, d);
+        }
+        if (tid < t.nrows) {
+            part_m[(prow + tid) * a.n_chunks + c] = sm.m[tid];
+            part_l[(prow + tid) * a.n_chunks + c] = sm.l[tid];
+        }
+    } else if (tid < t.nrows) {
+        part_m[(prow + tid) * a.n_chunks + c] = -INFINITY;
+        part_l[(prow + tid) * a.n_chunks + c] = 0.0;
+    }
+}
+
+// combine of the split form: one workgroup per tile, chunks in order
+template <int D, int R>
+__global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, const float * __restrict__ part_m,
+                                                              const double * __restrict__ part_l,
+                                                              const double * __restrict__ part_acc,
+                                                              float * __restrict__ out) {
+    __shared__ fa_smem<D, R> sm;
+    __shared__ double s_L[R];
+    __shared__ double s_w[R][kFaMaxChunks];
+    const fa_tile t = fa_tile_of(a);
+    const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int64_t prow = (int64_t) t.gti * R;
+    for (int r = wave; r < t.nrows; r += 4) {
+        float M = -INFINITY;
+        for (int i = lane; i < a.n_chunks; i += 64) M = fmaxf(M, part_m[(prow + r) * a.n_chunks + i]);
+        M = wave_max(M);
+        for (int i = lane; i < a.n_chunks; i += 64) {
+            const float mc = part_m[(prow + r) * a.n_chunks + i];
+            s_w[r][i] = mc == -INFINITY ? 0.0 : (double) expf_det(mc - M);
+        }
     }
     __syncthreads();
     if (tid < t.nrows) {
-        const float m = fmaxf(fmaxf(s_max[0][tid], s_max[1][tid]), fmaxf(s_max[2][tid], s_max[3][tid]));
-        cmax[fa_orow(a, t, tid) * a.n_chunks + chunk] = m;
-    }
-}
-
-template <int D>
-__global__ __launch_bounds__(kFaThreads) void k_fattn_accum(fattn_args a, const float * __restrict__ S,
-                                                            const float * __restrict__ cmax,
-                                                            double * __restrict__ part_acc,
-                                                            double * __restrict__ part_l) {
-    constexpr int DPL = D / 64;                // dims per lane
-    constexpr int PG = kFaThreads / (D / DPL);  // position groups
-    __shared__ float s_p[kFaRows][kFaMaxChunk];
-    __shared__ float s_M[kFaRows];
-    __shared__ int s_live[kFaRows];
-    __shared__ double s_red[PG][kFaRows][D];
-    __shared__ double s_l[kFaRows];
-    const fa_tile t = fa_tile_of(a);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int chunk = blockIdx.x;
-
-    if (tid < kFaRows) {
-        float M = -INFINITY;
-        int live = 0;
-        if (tid < t.nrows) {
-            const float * cm = cmax + fa_orow(a, t, tid) * a.n_chunks;
-            for (int i = 0; i < a.n_chunks; i++) M = fmaxf(M, cm[i]);
-            live = cm[chunk] != -INFINITY;
+        double L = 0.0;
+        for (int i = 0; i < a.n_chunks; i++) {
+            if (s_w[tid][i] != 0.0) L += s_w[tid][i] * part_l[(prow + tid) * a.n_chunks + i];
         }
-        s_M[tid] = M;
-        s_live[tid] = live;
+        s_L[tid] = L;
     }
-    __syncthreads();
-    int any = 0;
-    for (int r = 0; r < t.nrows; r++) any |= s_live[r];
-    if (!any) {
-        for (int idx = tid; idx < t.nrows * (D + 1); idx += kFaThreads) {
-            const int r = idx / (D + 1), d = idx % (D + 1);
-            const int64_t o = fa_orow(a, t, r) * a.n_chunks + chunk;
-            if (d < D) part_acc[o * D + d] = 0.0;
-            else part_l[o] = 0.0;
-        }
-        return;
-    }
-    // p = exp(s - M) with the row's global max, one wave per row
-    for (int r = wave; r < t.nrows; r += 4) {
-        const float * sr = S + fa_orow(a, t, r) * a.n_kv + t.c0;
-        double l = 0.0;
-        for (int p = lane; p < t.clen; p += 64) {
-            float e = 0.0f;
-            if (s_live[r]) {
-                const float s = sr[p];
-                e = s == -INFINITY ? 0.0f : expf_det(s - s_M[r]);
-            }
-            s_p[r][p] = e;
-            l += (double) e;
-        }
-        l = dsum_group(l, 64);
-        if (lane == 0) s_l[r] = l;
-    }
-    __syncthreads();
-    const char * vbase = a.v + (int64_t) t.kvh * a.v_nb2 + (int64_t) t.kv_seq * a.v_nb3;
-    const int dslot = tid % (D / DPL);
-    const int pg = tid / (D / DPL);
-    double acc[kFaRows][DPL];
-#pragma unroll
-    for (int r = 0; r < kFaRows; r++)
-#pragma unroll
-        for (int i = 0; i < DPL; i++) acc[r][i] = 0.0;
-    for (int p = pg; p < t.clen; p += PG) {
-        bool need = false;
-#pragma unroll
-        for (int r = 0; r < kFaRows; r++) need |= (r < t.nrows) && s_p[r][p] != 0.0f;
-        if (!need) continue;
-        const char * vp = vbase + (int64_t) (t.c0 + p) * a.v_nb1 + dslot * DPL * 2;
-        float vf[DPL];
-        if (DPL == 2) {
-            const uint32_t w = *(const uint32_t *) vp;
-            vf[0] = half_bits_to_float((uint16_t) (w & 0xFFFF));
-            vf[DPL - 1] = half_bits_to_float((uint16_t) (w >> 16));
-        } else {
-            vf[0] = half_bits_to_float(*(const uint16_t *) vp);
-        }
-#pragma unroll
-        for (int r = 0; r < kFaRows; r++) {
-            if (r >= t.nrows) break;
-            const float pr = s_p[r][p];
-            if (pr == 0.0f) continue;
-#pragma unroll
-            for (int i = 0; i < DPL; i++) acc[r][i] += (double) pr * (double) vf[i];  // exact products
-        }
-    }
-#pragma unroll
-    for (int r = 0; r < kFaRows; r++)
-#pragma unroll
-        for (int i = 0; i < DPL; i++) s_red[pg][r][dslot * DPL + i] = acc[r][i];
     __syncthreads();
     for (int idx = tid; idx < t.nrows * D; idx += kFaThreads) {
         const int r = idx / D, d = idx % D;
-        double v = 0.0;
+        const double * pa = part_acc + (prow + r) * a.n_chunks * D + d;
+        double O = 0.0;
+        for (int i = 0; i < a.n_chunks; i++) {
+            if (s_w[r][i] != 0.0) O += s_w[r][i] * pa[(int64_t) i * D];
+        }
+        const float o = s_L[r] == 0.0 ? 0.0f : (float) (O / s_L[r]);
+        out[fa_orow(a, t, r) * D + d] = o;
+        sm.q[r][d] = o;
+    }
+    if (a.qtype >= 0) {
+        __syncthreads();
+        fa_quantize_out<D, R>(a, t, sm);
+    }
+}
+
+template <int D, int R>
+__global__ __launch_bounds__(kFaThreads) void k_fattn_full(fattn_args a, float * __restrict__ out) {
+    __shared__ fa_smem<D, R> sm;
+    __shared__ float s_mc[R][kFaMaxChunks];
+    __shared__ float s_M[R];
+    __shared__ double s_L[R];
+    constexpr int NE = (R * D + kFaThreads - 1) / kFaThreads;
+    const fa_tile t = fa_tile_of(a);
+    const int tid = (int) threadIdx.x;
+
+    fa_load_q<D, R>(a, t, sm);
+    // pass 1: chunk maxima
+    for (int c = 0; c < a.n_chunks; c++) {
+        const bool live = fa_load_mask<D, R>(a, t, c, sm);
+        if (live) {
+            uint4 kr[D / 32];
+            fa_load_k<D>(a, t, c, kr);
+            fa_scores<D, R>(a, t, kr, sm);
+            __syncthreads();
+            fa_softmax_chunk<D, R>(t, sm);
+            __syncthreads();
+        }
+        if (tid < t.nrows) s_mc[tid][c] = live ? sm.m[tid] : -INFINITY;
+        __syncthreads();
+    }
+    if (tid < t.nrows) {
+        float M = -INFINITY;
+        for (int c = 0; c < a.n_chunks; c++) M = fmaxf(M, s_mc[tid][c]);
+        s_M[tid] = M;
+        s_L[tid] = 0.0;
+    }
+    __syncthreads();
+    // pass 2: chunk sums combined in chunk order
+    double O[NE];
 #pragma unroll
-        for (int q = 0; q < PG; q++) v += s_red[q][r][d];
-        const int64_t o = fa_orow(a, t, r) * a.n_chunks + chunk;
-        part_acc[o * D + d] = v;
-        if (d == 0) part_l[o] = s_l[r];
+    for (int e = 0; e < NE; e++) O[e] = 0.0;
+    for (int c = 0; c < a.n_chunks; c++) {
+        int any = 0;
+        for (int r = 0; r < t.nrows; r++) any |= s_mc[r][c] != -INFINITY;
+        if (!any) continue;  // uniform
+        fa_load_mask<D, R>(a, t, c, sm);
+        uint4 kr[D / 32], vr[D / 32];
+        fa_load_k<D>(a, t, c, kr);
+        fa_load_v<D>(a, t, c, vr);
+        fa_scores<D, R>(a, t, kr, sm);
+        __syncthreads();
+        fa_softmax_chunk<D, R>(t, sm);
+        if (tid < t.nrows) {
+            const float mc = s_mc[tid][c];
+            sm.w[tid] = mc == -INFINITY ? 0.0f : expf_det(mc - s_M[tid]);
+        }
+        __syncthreads();
+        fa_pv<D, R>(t, vr, sm);
+        __syncthreads();
+        if (tid < t.nrows && sm.w[tid] != 0.0f) s_L[tid] += (double) sm.w[tid] * sm.l[tid];
+#pragma unroll
+        for (int e = 0; e < NE; e++) {
+            const int idx = tid + e * kFaThreads;
+            if (idx < t.nrows * D) {
+                const int r = idx / D, d = idx % D;
+                if (sm.w[r] != 0.0f) O[e] += (double) sm.w[r] * fa_red_sum<D, R>(sm, r, d);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int e = 0; e < NE; e++) {
+        const int idx = tid + e * kFaThreads;
+        if (idx < t.nrows * D) {
+            const int r = idx / D, d = idx % D;
+            const float o = s_L[r] == 0.0 ? 0.0f : (float) (O[e] / s_L[r]);
+            out[fa_orow(a, t, r) * D + d] = o;
+            sm.q[r][d] = o;
+        }
+    }
+    if (a.qtype >= 0) {
+        __syncthreads();
+        fa_quantize_out<D, R>(a, t, sm);
     }
 }
 
-template <int D>
-__global__ __launch_bounds__(D) void k_fattn_combine(const double * __restrict__ part_acc,
-                                                     const double * __restrict__ part_l, int n_chunks,
-                                                     float * __restrict__ out) {
-    const int64_t orow = blockIdx.x;
-    const int d = threadIdx.x;
-    double L = 0.0, acc = 0.0;
-    for (int i = 0; i < n_chunks; i++) {
-        L += part_l[orow * n_chunks + i];
-        acc += part_acc[(orow * n_chunks + i) * D + d];
-    }
-    out[orow * D + d] = L == 0.0 ? 0.0f : (float) (acc / L);
-}
+// ------------------------------------------------------------------ host --
 
-static int64_t fa_rows(const fattn_args & a) { return (int64_t) a.n_seq * a.n_q * a.hq; }
+static int64_t fa_tiles(const fattn_args & a) { return (int64_t) a.hkv * a.n_seq * a.q_tiles; }
 
 size_t fattn_scratch_bytes(const fattn_args & a) {
-    const int64_t rows = fa_rows(a);
-    return (size_t) rows * a.n_kv * sizeof(float) + (size_t) rows * a.n_chunks * sizeof(float) +
-           (size_t) rows * a.n_chunks * (a.d + 1) * sizeof(double) + 1024;
+    if (!a.split) return 0;
+    const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
+    return (size_t) prows * (sizeof(float) + sizeof(double) + (size_t) a.d * sizeof(double)) + 1024;
 }
 
 void fattn_plan(fattn_args & a, int n_cu) {
     const int g = a.hq / a.hkv;
-    const int tq_per_tile = kFaRows / g;
-    a.q_tiles = (a.n_q + tq_per_tile - 1) / tq_per_tile;
-    const int64_t groups = (int64_t) a.hkv * a.n_seq * a.q_tiles;
-    int chunk = kFaMaxChunk;
-    while (chunk > 32 && groups * ((a.n_kv + chunk - 1) / chunk) < 2LL * n_cu) chunk >>= 1;
-    a.chunk = chunk;
-    a.n_chunks = (a.n_kv + chunk - 1) / chunk;
+    a.tq = a.n_q == 1 ? 1 : kFaMaxRows / g;
+    a.rows = g * a.tq;
+    a.q_tiles = (a.n_q + a.tq - 1) / a.tq;
+    a.n_chunks = (a.n_kv + kFaChunk - 1) / kFaChunk;
+    const int64_t tiles = fa_tiles(a);
+    const int64_t part_bytes = tiles * a.rows * a.n_chunks * (12 + 8 * (int64_t) a.d);
+    // split the KV span over workgroups when the tiles alone leave CUs idle
+    a.split = tiles < 2LL * n_cu && a.n_chunks <= kFaMaxChunks && part_bytes <= (256LL << 20);
 }
 
 bool fattn_supported(int d, int hq, int hkv) {
     if (d != 64 && d != 128) return false;
     if (hkv <= 0 || hq % hkv != 0) return false;
-    return kFaRows % (hq / hkv) == 0;
+    const int g = hq / hkv;
+    return g == 1 || g == 2 || g == 4 || g == 8;
 }
 
-void launch_fattn(const fattn_args & a, float * scratch, float * out, hipStream_t stream) {
-    const int64_t rows = fa_rows(a);
-    float * S = scratch;
-    float * cmax = S + rows * a.n_kv;
-    char * p = (char *) (cmax + rows * a.n_chunks);
-    p = (char *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
-    double * part_acc = (double *) p;
-    double * part_l = part_acc + rows * a.n_chunks * a.d;
-    const dim3 grid((unsigned) a.n_chunks, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
-    if (a.d == 128) {
-        hipLaunchKernelGGL(k_fattn_scores<128>, grid, dim3(kFaThreads), 0, stream, a, S, cmax);
-        hipLaunchKernelGGL(k_fattn_accum<128>, grid, dim3(kFaThreads), 0, stream, a, S, cmax, part_acc, part_l);
-        hipLaunchKernelGGL(k_fattn_combine<128>, dim3((unsigned) rows), dim3(128), 0, stream, part_acc, part_l,
-                           a.n_chunks, out);
+bool fattn_fits(const fattn_args & a) { return a.n_chunks <= kFaMaxChunks; }
+
+template <int D, int R>
+static void launch_fa(const fattn_args & a, void * scratch, float * out, hipStream_t s) {
+    if (a.split) {
+        const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
+        float * pm = (float *) scratch;
+        char * p = (char *) (pm + prows);
+        p = (char *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
+        double * pl = (double *) p;
+        double * pa = pl + prows;
+        const dim3 grid((unsigned) a.n_chunks, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
+        hipLaunchKernelGGL((k_fattn_split<D, R>), grid, dim3(kFaThreads), 0, s, a, pm, pl, pa);
+        const dim3 cgrid(1u, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
+        hipLaunchKernelGGL((k_fattn_combine<D, R>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out);
     } else {
-        hipLaunchKernelGGL(k_fattn_scores<64>, grid, dim3(kFaThreads), 0, stream, a, S, cmax);
-        hipLaunchKernelGGL(k_fattn_accum<64>, grid, dim3(kFaThreads), 0, stream, a, S, cmax, part_acc, part_l);
-        hipLaunchKernelGGL(k_fattn_combine<64>, dim3((unsigned) rows), dim3(64), 0, stream, part_acc, part_l,
-                           a.n_chunks, out);
+        const dim3 grid(1u, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
+        hipLaunchKernelGGL((k_fattn_full<D, R>), grid, dim3(kFaThreads), 0, s, a, out);
     }
+}
+
+template <int D>
+static void launch_fa_d(const fattn_args & a, void * scratch, float * out, hipStream_t s) {
+    switch (a.rows) {
+        case 1: launch_fa<D, 1>(a, scratch, out, s); break;
+        case 2: launch_fa<D, 2>(a, scratch, out, s); break;
+        case 4: launch_fa<D, 4>(a, scratch, out, s); break;
+        default: launch_fa<D, 8>(a, scratch, out, s); break;
+    }
+}
+
+void launch_fattn(const fattn_args & a, void * scratch, float * out, hipStream_t stream) {
+    if (a.d == 128) launch_fa_d<128>(a, scratch, out, stream);
+    else launch_fa_d<64>(a, scratch, out, stream);
 }
 
 }  // namespace mi355x

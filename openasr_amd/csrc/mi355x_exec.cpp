@@ -30,6 +30,10 @@ namespace {
 constexpr size_t kAlign = 256;
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// scratch arena: [activation region][general region]
+char * act_base(const backend_state * be) { return be->scratch; }
+char * gen_base(const backend_state * be) { return be->scratch + be->gen_off; }
+
 bool is_view_op(enum ggml_op op) {
     return op == GGML_OP_NONE || op == GGML_OP_RESHAPE || op == GGML_OP_VIEW || op == GGML_OP_PERMUTE ||
            op == GGML_OP_TRANSPOSE;
@@ -161,7 +165,7 @@ struct planner {
     bool plan_norm(int i, const ggml_tensor * t);
     bool plan_unary(int i, const ggml_tensor * t);
     bool plan_binary(const ggml_tensor * t);
-    bool plan_fattn(const ggml_tensor * t);
+    bool plan_fattn(int i, const ggml_tensor * t);
 };
 
 bool planner::plan_mul_mat(const ggml_tensor * t) {
@@ -187,14 +191,14 @@ bool planner::plan_mul_mat(const ggml_tensor * t) {
         if (!reuse) {
             add(
                 [=](hipStream_t s) {
-                    act_buffers act = act_carve(wtype, b->scratch, K, N);
+                    act_buffers act = act_carve(wtype, act_base(b), K, N);
                     launch_quantize_act(xv, wtype, act, s);
                 },
                 t, wtype == GGML_TYPE_Q8_0 ? "quantize_q8_0" : "quantize_q8_K");
         }
         add(
             [=](hipStream_t s) {
-                act_buffers act = act_carve(wtype, b->scratch, K, N);
+                act_buffers act = act_carve(wtype, act_base(b), K, N);
                 if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
                 else if (mfma) launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
@@ -283,7 +287,7 @@ bool planner::plan_binary(const ggml_tensor * t) {
     return true;
 }
 
-bool planner::plan_fattn(const ggml_tensor * t) {
+bool planner::plan_fattn(int i, const ggml_tensor * t) {
     const ggml_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2], *m = t->src[3];
     fattn_args a{};
     a.q = (const char *) q->data;
@@ -305,6 +309,7 @@ bool planner::plan_fattn(const ggml_tensor * t) {
         a.m_nb3 = m->nb[3];
         a.m_ne2 = (int) m->ne[2];
         a.m_ne3 = (int) m->ne[3];
+        if (m->ne[0] < k->ne[1] || m->ne[1] < q->ne[1]) return fail(t, "mask smaller than the attention span");
     }
     a.d = (int) q->ne[0];
     a.n_q = (int) q->ne[1];
@@ -314,18 +319,46 @@ bool planner::plan_fattn(const ggml_tensor * t) {
     a.hkv = (int) k->ne[2];
     a.rk3 = (int) (q->ne[3] / k->ne[3]);
     a.scale = op_f32(t, 0);
+    a.qtype = -1;
+    // K and V rows are read as 16-byte vectors
+    if (((uintptr_t) a.k | (uintptr_t) a.v) % 16 != 0) return fail(t, "K/V not 16-byte aligned");
     fattn_plan(a, n_cu);
+    if (!fattn_fits(a)) return fail(t, "KV span longer than the kernel's chunk table");
+
+    // the output projection consumes the output through a contiguous reshape:
+    // let the attention kernel quantize it for that MUL_MAT
+    const int g = a.hq / a.hkv;
+    const ggml_tensor * view = sole_consumer(t, i + 1);
+    const ggml_tensor * mm = nullptr;
+    if (view && (view->op == GGML_OP_RESHAPE || view->op == GGML_OP_VIEW) && view->view_src == t &&
+        view->view_offs == 0 && is_contiguous(view) && view->ne[0] == (int64_t) a.d * a.hq) {
+        mm = sole_consumer(view, i + 1);
+    }
+    if (mm && mm->op == GGML_OP_MUL_MAT && mm->src[1] == view && mm->src[0]->ne[0] == view->ne[0] &&
+        supports_op(be->dev, mm)) {
+        const int wt = mm->src[0]->type;
+        if ((wt == GGML_TYPE_Q4_K && (g * a.d) % 256 == 0) || (wt == GGML_TYPE_Q8_0 && (g * a.d) % 32 == 0)) {
+            a.qtype = wt;
+            const int64_t K = view->ne[0], ncols = view->ne[1] * view->ne[2] * view->ne[3];
+            act_need = std::max(act_need, act_bytes(wt, K, ncols));
+            a.act = act_buffers{nullptr, nullptr, nullptr};
+        }
+    }
     gen_need = std::max(gen_need, fattn_scratch_bytes(a));
     backend_state * b = be;
-    const size_t act_off_end = 0;
-    (void) act_off_end;
     float * out = (float *) t->data;
+    const int64_t qK = (int64_t) a.d * a.hq, qN = (int64_t) a.n_q * a.n_seq;
     add(
         [=](hipStream_t s) {
-            float * scratch = (float *) (b->scratch + align_up(b->scratch_cap / 2, kAlign));
-            launch_fattn(a, scratch, out, s);
+            fattn_args la = a;
+            if (la.qtype >= 0) la.act = act_carve(la.qtype, act_base(b), qK, qN);
+            launch_fattn(la, gen_base(b), out, s);
         },
         t, "flash_attn_ext");
+    if (a.qtype >= 0) {
+        act_src = view;
+        act_wtype = a.qtype;
+    }
     return true;
 }
 
@@ -408,14 +441,14 @@ bool planner::plan() {
                 backend_state * b = be;
                 add(
                     [=](hipStream_t s) {
-                        launch_argmax(av, out, first, b->scratch + align_up(b->scratch_cap / 2, kAlign), s);
+                        launch_argmax(av, out, first, gen_base(b), s);
                     },
                     t, "argmax");
                 break;
             }
             case GGML_OP_FLASH_ATTN_EXT:
-                plan_fattn(t);
-                break;
+                if (!plan_fattn(i, t)) return false;
+                continue;
             default:
                 return fail(t, "no launcher");
         }
@@ -427,19 +460,20 @@ bool planner::plan() {
 }
 
 bool ensure_scratch(backend_state * be, size_t act_need, size_t gen_need) {
-    const size_t half = align_up(std::max(act_need, gen_need), kAlign);
-    const size_t need = 2 * half + kAlign;
-    if (be->scratch && be->scratch_cap >= need && align_up(be->scratch_cap / 2, kAlign) >= half) return true;
+    act_need = align_up(act_need, kAlign);
+    gen_need = align_up(gen_need, kAlign);
+    if (be->scratch && act_need <= be->gen_off && be->gen_off + gen_need <= be->scratch_cap) return true;
     release_graph_cache(be);
     if (be->scratch) MI_CHECK(hipFree(be->scratch));
     be->scratch = nullptr;
     be->scratch_cap = 0;
-    size_t cap = need < (64u << 20) ? (64u << 20) : need;
-    if (hipMalloc((void **) &be->scratch, cap) != hipSuccess) {
+    const size_t half = std::max<size_t>(std::max(act_need, gen_need), 32u << 20);
+    if (hipMalloc((void **) &be->scratch, 2 * half) != hipSuccess) {
         be->scratch = nullptr;
         return false;
     }
-    be->scratch_cap = cap;
+    be->scratch_cap = 2 * half;
+    be->gen_off = half;
     return true;
 }
 

@@ -43,6 +43,7 @@ struct backend_state {
     hipStream_t stream = nullptr;
     char * scratch = nullptr;
     size_t scratch_cap = 0;
+    size_t gen_off = 0;  // offset of the general region inside the arena
     std::vector<cache_entry> cache;
     uint64_t use_clock = 0;
     bool use_graphs = true;

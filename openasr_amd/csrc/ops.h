@@ -47,12 +47,22 @@ struct fattn_args {
     int m_ne2, m_ne3;
     int d, hq, hkv, n_q, n_kv, n_seq, rk3;
     float scale;
-    int chunk, n_chunks, q_tiles;
+    // launch plan (fattn_plan)
+    int tq;        // query positions per tile
+    int rows;      // tile rows = tq * (hq / hkv)
+    int q_tiles;
+    int n_chunks;  // 64-position KV chunks
+    int split;     // chunks spread over workgroups (partials, then a combine launch)
+    // optional quantization of the output for the consuming MUL_MAT:
+    // -1 none, GGML_TYPE_Q8_0 or GGML_TYPE_Q4_K (Q8_K activations)
+    int qtype;
+    act_buffers act;
 };
 bool fattn_supported(int d, int hq, int hkv);
 void fattn_plan(fattn_args & a, int n_cu);
+bool fattn_fits(const fattn_args & a);
 size_t fattn_scratch_bytes(const fattn_args & a);
-void launch_fattn(const fattn_args & a, float * scratch, float * out, hipStream_t stream);
+void launch_fattn(const fattn_args & a, void * scratch, float * out, hipStream_t stream);
 
 void launch_binary(int op, const tview & d, const tview & a, const tview & b, hipStream_t s, int n_cu);
 void launch_scale(const tview & d, const tview & a, float sc, float bias, hipStream_t s, int n_cu);

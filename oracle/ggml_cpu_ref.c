@@ -647,6 +647,56 @@ void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_
                 acc32[d] = 0.0f;
             }
             float * o = out + (iq * Hq + h) * D;
+            if (fidelity == 4) {
+                /* chunked: fixed 64-position KV chunks, each with its own max
+                 * m_c, p = exp(s - m_c), f64 sums l_c and a_c; the chunks are
+                 * combined in order with w = exp(m_c - M), M = max m_c */
+                const int64_t C = 64, n_chunks = (n_kv + C - 1) / C;
+                float mcs[1024];
+                if (n_chunks > 1024) abort(); /* spans beyond 65536 positions are not modelled */
+                float M = -INFINITY;
+                for (int64_t c = 0; c < n_chunks; c++) {
+                    float mc = -INFINITY;
+                    for (int64_t ic = c * C; ic < n_kv && ic < (c + 1) * C; ic++) {
+                        const float mv = mask ? ref_fp16_to_fp32(mask[iq * mask_stride + ic]) : 0.0f;
+                        if (mv == -INFINITY) continue;
+                        const uint16_t * kr = k + kvh * kv_stride_head + ic * kv_stride_pos;
+                        double a = 0.0;
+                        for (int64_t d = 0; d < D; d++) a += (double) (ref_fp16_to_fp32(kr[d]) * ref_fp16_to_fp32(qh[d]));
+                        const float s = (float) a * scale + mv;
+                        mc = s > mc ? s : mc;
+                    }
+                    mcs[c] = mc;
+                    M = mc > M ? mc : M;
+                }
+                double L = 0.0;
+                double O[512];
+                for (int64_t d = 0; d < D; d++) O[d] = 0.0;
+                for (int64_t c = 0; c < n_chunks && M != -INFINITY; c++) {
+                    if (mcs[c] == -INFINITY) continue;
+                    const float w = ref_expf_det(mcs[c] - M);
+                    if (w == 0.0f) continue;
+                    double l = 0.0, acc[512];
+                    for (int64_t d = 0; d < D; d++) acc[d] = 0.0;
+                    for (int64_t ic = c * C; ic < n_kv && ic < (c + 1) * C; ic++) {
+                        const float mv = mask ? ref_fp16_to_fp32(mask[iq * mask_stride + ic]) : 0.0f;
+                        if (mv == -INFINITY) continue;
+                        const uint16_t * kr = k + kvh * kv_stride_head + ic * kv_stride_pos;
+                        const uint16_t * vr = v + kvh * kv_stride_head + ic * kv_stride_pos;
+                        double a = 0.0;
+                        for (int64_t d = 0; d < D; d++) a += (double) (ref_fp16_to_fp32(kr[d]) * ref_fp16_to_fp32(qh[d]));
+                        const float s = (float) a * scale + mv;
+                        const float p = ref_expf_det(s - mcs[c]);
+                        l += (double) p;
+                        if (p == 0.0f) continue;
+                        for (int64_t d = 0; d < D; d++) acc[d] += (double) p * (double) ref_fp16_to_fp32(vr[d]);
+                    }
+                    L += (double) w * l;
+                    for (int64_t d = 0; d < D; d++) O[d] += (double) w * acc[d];
+                }
+                for (int64_t d = 0; d < D; d++) o[d] = L == 0.0 ? 0.0f : (float) (O[d] / L);
+                continue;
+            }
             if (fidelity == 3) {
                 /* two-pass: global max first, then every p = exp(s - M) and the
                  * sums in f64, one rounding at the end */

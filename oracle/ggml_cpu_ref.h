@@ -113,9 +113,14 @@ int32_t ref_argmax_first(const float * x, int64_t n);
  * q head h reads kv head h / (Hq / Hkv). fidelity=1 reproduces ggml-cpu's
  * f16-rounded Q and f16 V accumulator; fidelity=2 rounds Q to f16 but
  * accumulates V in f32; fidelity=0 keeps Q in f32 and accumulates in f32;
- * fidelity=3 (the device's canonical form) rounds Q to f16, takes the global
- * max first and accumulates p = exp(s - max), the sum and p*V in f64,
- * rounding once -- independent of the order positions are visited in.
+ * fidelity=3 rounds Q to f16, takes the global max first and accumulates
+ * p = exp(s - max), the sum and p*V in f64, rounding once.
+ * fidelity=4 (the device's definition) rounds Q to f16 and splits the span
+ * into fixed 64-position chunks: per chunk the max m_c, p = exp(s - m_c) and
+ * the f64 sums l_c = sum p, a_c = sum p*V; then M = max m_c and, in chunk
+ * order, w = exp(m_c - M), L += w*l_c, O += w*a_c; out = O/L rounded once.
+ * Chunk sums of exact products do not depend on the order positions are
+ * visited in, so any split of the chunks over workers gives these bits.
  */
 void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_head,
                         const uint16_t * k, const uint16_t * v, int64_t kv_stride_head,

@@ -162,8 +162,10 @@ def flash_attn(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16: np.ndarr
                fidelity: int = 1, threads: int = 0) -> np.ndarray:
     """q: [n_q, Hq, D] f32; k16, v16: [Hkv, n_kv, D] f16 bits; mask16: [n_q, n_kv] f16 bits.
     fidelity 1: ggml-cpu numerics (f16 Q, f16 V accumulator); 2: f16 Q, f32
-    online accumulation; 0: f32 throughout; 3: f16 Q, two-pass f64 sums (the
-    device's order-independent form). Returns [n_q, Hq, D] f32."""
+    online accumulation; 0: f32 throughout; 3: f16 Q, two-pass f64 sums over
+    the whole span; 4: f16 Q, fixed 64-position chunks with their own maxima
+    and f64 sums, combined in chunk order (the device's definition). Returns
+    [n_q, Hq, D] f32."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     k16 = np.ascontiguousarray(k16, dtype=np.uint16)
     v16 = np.ascontiguousarray(v16, dtype=np.uint16)
@@ -189,7 +191,7 @@ class QwenRef:
     """CPU reference of one Qwen3 decoder sequence over host weight bytes
     (a pointer table into the same buffers the device was loaded from)."""
 
-    def __init__(self, cfg, pointer_table, max_pos: int, fa_fidelity: int = 3, threads: int = 0):
+    def __init__(self, cfg, pointer_table, max_pos: int, fa_fidelity: int = 4, threads: int = 0):
         L = lib()
         L.ref_qwen_forward.restype = C.c_int32
         L.ref_qwen_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
@@ -233,7 +235,7 @@ class QwenRefBatch:
     """CPU reference of a batched decode step over n_seq sequences (weights
     streamed once per step), continuing from given KV caches."""
 
-    def __init__(self, cfg, pointer_table, max_pos: int, n_seq: int, fa_fidelity: int = 3, threads: int = 0):
+    def __init__(self, cfg, pointer_table, max_pos: int, n_seq: int, fa_fidelity: int = 4, threads: int = 0):
         L = lib()
         L.ref_qwen_decode_batch.restype = None
         L.ref_qwen_decode_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,

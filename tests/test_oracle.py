@@ -343,3 +343,31 @@ def test_flash_attn_two_pass_mode(ref):
     got = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, fidelity=3)
     assert np.abs(got - want).max() < 1e-6 * np.abs(want).max()
     assert not got[3].any()
+
+
+@pytest.mark.parametrize("n_kv,holes", [(1, []), (64, []), (65, []), (300, [(30, 130)]), (1000, [(0, 200), (640, 700)])])
+def test_flash_attn_chunked_mode(ref, n_kv, holes):
+    """fidelity 4 (64-position chunks with their own maxima, combined in
+    order) against the f64 textbook: chunk edges, a chunk masked out in the
+    middle, leading masked chunks, a single position"""
+    n_q, hq, hkv, d = 2, 4, 2, 128
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((n_q, n_kv), np.float16)
+    for a, b in holes:
+        mask[:, a:b] = -np.inf
+    scale = 1 / math.sqrt(d)
+    qh = q.astype(np.float16).astype(np.float32)
+    want = textbook_attention(qh, k, v, mask, scale, hq // hkv)
+    got = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, fidelity=4)
+    assert np.abs(got - want).max() < 1e-6 * max(1.0, np.abs(want).max())
+    two_pass = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, fidelity=3)
+    assert np.abs(got - two_pass).max() < 1e-6 * max(1.0, np.abs(want).max())
+    # garbage (even NaN) under the mask changes nothing
+    k2, v2 = k.copy(), v.copy()
+    for a, b in holes:
+        k2[:, a:b] = np.float16(60000)
+        v2[:, a:b] = np.float16(np.nan)
+    got2 = ref.flash_attn(q, k2.view(np.uint16), v2.view(np.uint16), mask.view(np.uint16), scale, fidelity=4)
+    assert np.array_equal(got, got2)
