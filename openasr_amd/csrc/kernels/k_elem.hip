@@ -7,6 +7,7 @@
 // argmax. All are HBM- or latency-bound; each is one pass over its data.
 #include "../mi355x_common.h"
 #include "../ops.h"
+#include "../quant_dev.h"
 
 namespace mi355x {
 
@@ -138,8 +139,9 @@ void launch_silu_mul(const tview & d, const tview & g, const tview & u, hipStrea
 // One wave per row. mode 0: RMSNorm, 1: LayerNorm. Optional fused weight
 // multiply (w broadcast over rows) and bias add, matching the
 // rms_norm->mul and norm->mul->add sequences of nn/norm.rs:10-56. PER is the
-// number of row elements each lane keeps in registers (the row is read
-// once); the fused weight / bias rows have the norm's width (planner check).
+// number of row elements each lane keeps in registers (the row, its weight
+// and bias are read once, all loads issued before the sums); the fused
+// weight / bias rows have the norm's width (planner check).
 template <int PER>
 __global__ __launch_bounds__(256) void k_norm(tview d, tview a, int mode, float eps, tview w, int has_w, tview bias,
                                               int has_b, int64_t rows) {
@@ -156,11 +158,14 @@ __global__ __launch_bounds__(256) void k_norm(tview d, tview a, int mode, float 
     const float * br = has_b ? (const float *) (bias.data + (i1 % bias.ne[1]) * bias.nb[1] +
                                                 (i2 % bias.ne[2]) * bias.nb[2] + (i3 % bias.ne[3]) * bias.nb[3])
                              : nullptr;
-    float xv[PER];
+    float xv[PER], wv[PER], bv[PER];
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const int i = lane + 64 * k;
-        xv[k] = i < n ? x[i] : 0.0f;
+        const bool ok = i < n;
+        xv[k] = ok ? x[i] : 0.0f;
+        wv[k] = ok && has_w ? wr[i] : 1.0f;
+        bv[k] = ok && has_b ? br[i] : 0.0f;
     }
     // sums in f64 and one rounding, as ggml-cpu's ggml_float accumulators
     float mean = 0.0f;
@@ -183,23 +188,126 @@ __global__ __launch_bounds__(256) void k_norm(tview d, tview a, int mode, float 
 #pragma unroll
     for (int k = 0; k < PER; k++) {
         const int i = lane + 64 * k;
-        if (i < n) {
-            float v = (xv[k] - mean) * scale;
-            if (has_w) v *= wr[i];
-            if (has_b) v += br[i];
-            y[i] = v;
+        float v = (xv[k] - mean) * scale;
+        if (has_w) v *= wv[k];
+        if (has_b) v += bv[k];
+        if (i < n) y[i] = v;
+    }
+}
+
+// Rows whose width is a multiple of 256 with contiguous elements and 1-D
+// weight / bias vectors: lane l holds elements 256c + 4l .. +3 (16-byte
+// loads), so each 256-element chunk is laid out as the activation quantizers
+// expect and the normalised row can also be written as the quantized
+// activations of the MUL_MAT that consumes it (qtype: -1 none, Q8_0 or Q4_K
+// for Q8_K). The f32 row is always written.
+template <int C>
+__global__ __launch_bounds__(256) void k_norm_rows(tview d, tview a, int mode, float eps, const float * __restrict__ wr,
+                                                   const float * __restrict__ br, int64_t rows, int qtype,
+                                                   act_buffers act) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
+    const float * x = (const float *) (a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3]);
+    float * y = (float *) (d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]);
+    constexpr int n = 256 * C;
+    float4 xv[C], wv[C], bv[C];
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const int i = 256 * c + 4 * lane;
+        xv[c] = *(const float4 *) (x + i);
+        wv[c] = wr ? *(const float4 *) (wr + i) : make_float4(1.f, 1.f, 1.f, 1.f);
+        bv[c] = br ? *(const float4 *) (br + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float mean = 0.0f;
+    if (mode == 1) {
+        double s = 0.0;
+#pragma unroll
+        for (int c = 0; c < C; c++) s += (((double) xv[c].x + (double) xv[c].y) + (double) xv[c].z) + (double) xv[c].w;
+        mean = (float) (wave_sum_d(s) / (double) n);
+    }
+    double s2 = 0.0;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        const float vx = xv[c].x - mean, vy = xv[c].y - mean, vz = xv[c].z - mean, vw = xv[c].w - mean;
+        s2 += (((double) (vx * vx) + (double) (vy * vy)) + (double) (vz * vz)) + (double) (vw * vw);
+    }
+    const float var = (float) (wave_sum_d(s2) / (double) n);
+    const float scale = 1.0f / sqrtf(var + eps);
+    const int64_t col = row;
+#pragma unroll
+    for (int c = 0; c < C; c++) {
+        float4 v;
+        v.x = (xv[c].x - mean) * scale;
+        v.y = (xv[c].y - mean) * scale;
+        v.z = (xv[c].z - mean) * scale;
+        v.w = (xv[c].w - mean) * scale;
+        if (wr) {
+            v.x *= wv[c].x;
+            v.y *= wv[c].y;
+            v.z *= wv[c].z;
+            v.w *= wv[c].w;
+        }
+        if (br) {
+            v.x += bv[c].x;
+            v.y += bv[c].y;
+            v.z += bv[c].z;
+            v.w += bv[c].w;
+        }
+        const int e = 256 * c + 4 * lane;
+        *(float4 *) (y + e) = v;
+        if (qtype == GGML_TYPE_Q4_K) {
+            const q8_K_lane o = quantize_q8_K_wave(v, lane);
+            *(char4 *) (act.q + col * n + e) = o.q;
+            if ((lane & 7) == 0) act.ssum[col * (n / 32) + e / 32] = (int16_t) o.ssum;
+            if (lane == 0) act.d[col * C + c] = o.d;
+        } else if (qtype == GGML_TYPE_Q8_0) {
+            const q8_0_lane o = quantize_q8_0_group(v);
+            *(char4 *) (act.q + col * n + e) = o.q;
+            if ((lane & 7) == 0) act.d[col * (n / 32) + e / 32] = o.d;
         }
     }
 }
 
 bool norm_supported(int64_t ne0) { return ne0 <= 64 * 64; }
 
+bool norm_rows_supported(const tview & d, const tview & a, const tview * w, const tview * b) {
+    const int64_t n = a.ne[0];
+    if (n % 256 != 0 || n / 256 > 16) return false;
+    const int c = (int) (n / 256);
+    if (c != 1 && c != 2 && c != 4 && c != 6 && c != 8 && c != 12 && c != 16) return false;
+    if (a.nb[0] != 4 || d.nb[0] != 4) return false;
+    if ((((uintptr_t) a.data) | ((uintptr_t) d.data) | a.nb[1] | a.nb[2] | a.nb[3] | d.nb[1] | d.nb[2] | d.nb[3]) % 16)
+        return false;
+    for (const tview * v : {w, b}) {
+        if (!v) continue;
+        if (v->ne[1] != 1 || v->ne[2] != 1 || v->ne[3] != 1 || v->nb[0] != 4 || ((uintptr_t) v->data) % 16) return false;
+    }
+    return true;
+}
+
 void launch_norm(const tview & d, const tview & a, int mode, float eps, const tview * w, const tview * b,
-                 hipStream_t s) {
+                 hipStream_t s, int qtype, const act_buffers * act) {
     const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    const dim3 grid((unsigned) ((rows + 3) / 4));
+    if (norm_rows_supported(d, a, w, b)) {
+        const float * wp = w ? (const float *) w->data : nullptr;
+        const float * bp = b ? (const float *) b->data : nullptr;
+        const act_buffers ab = act ? *act : act_buffers{nullptr, nullptr, nullptr};
+        const int qt = act ? qtype : -1;
+        switch (a.ne[0] / 256) {
+            case 1: hipLaunchKernelGGL(k_norm_rows<1>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
+            case 2: hipLaunchKernelGGL(k_norm_rows<2>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
+            case 4: hipLaunchKernelGGL(k_norm_rows<4>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
+            case 6: hipLaunchKernelGGL(k_norm_rows<6>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
+            case 8: hipLaunchKernelGGL(k_norm_rows<8>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
+            case 12: hipLaunchKernelGGL(k_norm_rows<12>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
+            default: hipLaunchKernelGGL(k_norm_rows<16>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
+        }
+    }
     const int per = (int) ((a.ne[0] + 63) / 64);
     tview none{};
-    const dim3 grid((unsigned) ((rows + 3) / 4));
     const tview wv = w ? *w : none, bv = b ? *b : none;
     const int hw = w ? 1 : 0, hb = b ? 1 : 0;
     if (per <= 2) hipLaunchKernelGGL(k_norm<2>, grid, dim3(256), 0, s, d, a, mode, eps, wv, hw, bv, hb, rows);

@@ -242,7 +242,7 @@ __device__ __forceinline__ void fa_quantize_out(const fattn_args & a, const fa_t
             if (a.qtype == GGML_TYPE_Q4_K) {
                 const q8_K_lane o = quantize_q8_K_wave(v, lane);
                 *(char4 *) (a.act.q + col * K + e0 + e) = o.q;
-                if ((lane & 3) == 0) a.act.bsums[col * (K / 16) + (e0 + e) / 16] = (int16_t) o.bsum;
+                if ((lane & 7) == 0) a.act.ssum[col * (K / 32) + (e0 + e) / 32] = (int16_t) o.ssum;
                 if (lane == 0) a.act.d[col * (K / 256) + (e0 + piece * 256) / 256] = o.d;
             } else {
                 const q8_0_lane o = quantize_q8_0_group(v);

@@ -81,10 +81,13 @@ __device__ __forceinline__ void scale_min_k4(int j, const uint8_t * s, int & sc,
     }
 }
 
+// Q4_K: a chunk is one sub-block pair c of a super-block (32 bytes of
+// nibbles: low nibbles = sub-block 2c, high nibbles = sub-block 2c+1), so the
+// min correction needs the activations' 32-element sums.
 template <int NC>
 __global__ __launch_bounds__(256) void k_mmv_q4_K(const char * __restrict__ W, int64_t row_bytes, int64_t M,
                                                   int64_t K, const int8_t * __restrict__ aq,
-                                                  const float * __restrict__ ad, const int16_t * __restrict__ abs_,
+                                                  const float * __restrict__ ad, const int16_t * __restrict__ ass,
                                                   char * __restrict__ dst, int64_t dst_nb1, int lpr_log2, int cpl) {
     const int lane = threadIdx.x & 63;
     const int LPR = 1 << lpr_log2;
@@ -101,13 +104,12 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const char * __restrict__ W, i
         for (int n = 0; n < NC; n++) acc[n] = 0.0;
         for (int c = 0; c < cpl; c++) {
             const int ci = li + c * LPR;
-            const int sb = ci >> 3;
-            const int j = ci & 7;
-            const int g = j >> 1;
-            const int h = j & 1;
+            const int sb = ci >> 2;
+            const int g = ci & 3;
             const char * blk = wr + (int64_t) sb * 144;
             const uint4 hdr = *(const uint4 *) blk;
-            const int4 qv = *(const int4 *) (blk + 16 + 16 * j);
+            const int4 q0 = *(const int4 *) (blk + 16 + 32 * g);
+            const int4 q1 = *(const int4 *) (blk + 32 + 32 * g);
             const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
             const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
             uint8_t sc8[12];
@@ -117,18 +119,20 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const char * __restrict__ W, i
             int sc_lo, m_lo, sc_hi, m_hi;
             scale_min_k4(2 * g, sc8, sc_lo, m_lo);
             scale_min_k4(2 * g + 1, sc8, sc_hi, m_hi);
-            const int4 lo = make_int4(qv.x & 0x0F0F0F0F, qv.y & 0x0F0F0F0F, qv.z & 0x0F0F0F0F, qv.w & 0x0F0F0F0F);
-            const int4 hi = make_int4((qv.x >> 4) & 0x0F0F0F0F, (qv.y >> 4) & 0x0F0F0F0F, (qv.z >> 4) & 0x0F0F0F0F,
-                                      (qv.w >> 4) & 0x0F0F0F0F);
-            const int64_t e_lo = (int64_t) sb * 256 + 64 * g + 16 * h;
+            const int4 lo0 = make_int4(q0.x & 0x0F0F0F0F, q0.y & 0x0F0F0F0F, q0.z & 0x0F0F0F0F, q0.w & 0x0F0F0F0F);
+            const int4 lo1 = make_int4(q1.x & 0x0F0F0F0F, q1.y & 0x0F0F0F0F, q1.z & 0x0F0F0F0F, q1.w & 0x0F0F0F0F);
+            const int4 hi0 = make_int4((q0.x >> 4) & 0x0F0F0F0F, (q0.y >> 4) & 0x0F0F0F0F, (q0.z >> 4) & 0x0F0F0F0F,
+                                       (q0.w >> 4) & 0x0F0F0F0F);
+            const int4 hi1 = make_int4((q1.x >> 4) & 0x0F0F0F0F, (q1.y >> 4) & 0x0F0F0F0F, (q1.z >> 4) & 0x0F0F0F0F,
+                                       (q1.w >> 4) & 0x0F0F0F0F);
+            const int64_t e_lo = (int64_t) sb * 256 + 64 * g;
 #pragma unroll
             for (int n = 0; n < NC; n++) {
-                const int8_t * acol = aq + n * K;
-                const int4 a_lo = *(const int4 *) (acol + e_lo);
-                const int4 a_hi = *(const int4 *) (acol + e_lo + 32);
-                const int16_t * bs = abs_ + n * (K / 16) + sb * 16;
-                const int isum = dot16(lo, a_lo) * sc_lo + dot16(hi, a_hi) * sc_hi;
-                const int msum = (int) bs[4 * g + h] * m_lo + (int) bs[4 * g + 2 + h] * m_hi;
+                const int8_t * acol = aq + n * K + e_lo;
+                const int isum = (dot16(lo0, *(const int4 *) acol) + dot16(lo1, *(const int4 *) (acol + 16))) * sc_lo +
+                                 (dot16(hi0, *(const int4 *) (acol + 32)) + dot16(hi1, *(const int4 *) (acol + 48))) * sc_hi;
+                const int16_t * ss = ass + n * (K / 32) + sb * 8 + 2 * g;
+                const int msum = (int) ss[0] * m_lo + (int) ss[1] * m_hi;
                 const double da = (double) ad[n * nsb + sb];
                 acc[n] += ((double) dw * da) * (double) isum - ((double) dmw * da) * (double) msum;
             }
@@ -155,7 +159,7 @@ static void pick_team(int64_t chunks, int & lpr_log2, int & cpl) {
 template <int NC>
 static void mmv_dispatch(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K,
                          const act_buffers & act, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu) {
-    const int64_t chunks = wtype == GGML_TYPE_Q8_0 ? K / 16 : K / 32;
+    const int64_t chunks = wtype == GGML_TYPE_Q8_0 ? K / 16 : K / 64;
     int lpr_log2, cpl;
     pick_team(chunks, lpr_log2, cpl);
     const int64_t teams = M;
@@ -168,7 +172,7 @@ static void mmv_dispatch(int wtype, const char * W, int64_t row_bytes, int64_t M
                            act.d, dst, dst_nb1, lpr_log2, cpl);
     } else {
         hipLaunchKernelGGL(k_mmv_q4_K<NC>, dim3((unsigned) blocks), dim3(256), 0, stream, W, row_bytes, M, K, act.q,
-                           act.d, act.bsums, dst, dst_nb1, lpr_log2, cpl);
+                           act.d, act.ssum, dst, dst_nb1, lpr_log2, cpl);
     }
 }
 
@@ -180,7 +184,7 @@ void launch_mmv(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t
         act_buffers a = act;
         a.q += done * K;
         a.d += done * (wtype == GGML_TYPE_Q8_0 ? K / 32 : K / 256);
-        if (a.bsums) a.bsums += done * (K / 16);
+        if (a.ssum) a.ssum += done * (K / 32);
         char * d = dst + done * dst_nb1;
         switch (n) {
             case 1: mmv_dispatch<1>(wtype, W, row_bytes, M, K, a, d, dst_nb1, stream, n_cu); break;

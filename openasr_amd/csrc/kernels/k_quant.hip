@@ -34,11 +34,11 @@ __global__ __launch_bounds__(256) void k_quantize_q8_0(const char * __restrict__
     }
 }
 
-// Q8_K: one wave per 256-element block (quantize_q8_K_wave); bsums over 16.
+// Q8_K: one wave per 256-element block (quantize_q8_K_wave); sums over 32.
 __global__ __launch_bounds__(256) void k_quantize_q8_K(const char * __restrict__ src, int64_t K, int64_t ncols,
                                                        int64_t ne1, int64_t nb1, int64_t nb2,
                                                        int8_t * __restrict__ q, float * __restrict__ d,
-                                                       int16_t * __restrict__ bsums) {
+                                                       int16_t * __restrict__ ssum) {
     const int lane = threadIdx.x & 63;
     const int64_t wave = (int64_t) blockIdx.x * (blockDim.x / 64) + (threadIdx.x >> 6);
     const int64_t chunks = K / 256;
@@ -50,7 +50,7 @@ __global__ __launch_bounds__(256) void k_quantize_q8_K(const char * __restrict__
     const float * x = (const float *) (src + i1 * nb1 + i2 * nb2);
     const q8_K_lane o = quantize_q8_K_wave(*(const float4 *) (x + e), lane);
     *(char4 *) (q + col * K + e) = o.q;
-    if ((lane & 3) == 0) bsums[col * (K / 16) + e / 16] = (int16_t) o.bsum;
+    if ((lane & 7) == 0) ssum[col * (K / 32) + e / 32] = (int16_t) o.ssum;
     if (lane == 0) d[col * chunks + blk] = o.d;
 }
 
@@ -59,7 +59,7 @@ static size_t al256(size_t v) { return (v + 255) / 256 * 256; }
 size_t act_bytes(int wtype, int64_t K, int64_t ncols) {
     const size_t q = al256((size_t) (K * ncols));
     if (wtype == GGML_TYPE_Q8_0) return q + al256((size_t) (K / 32 * ncols) * 4);
-    return q + al256((size_t) (K / 256 * ncols) * 4) + al256((size_t) (K / 16 * ncols) * 2);
+    return q + al256((size_t) (K / 256 * ncols) * 4) + al256((size_t) (K / 32 * ncols) * 2);
 }
 
 act_buffers act_carve(int wtype, char * base, int64_t K, int64_t ncols) {
@@ -68,9 +68,9 @@ act_buffers act_carve(int wtype, char * base, int64_t K, int64_t ncols) {
     a.q = (int8_t *) base;
     a.d = (float *) (base + q);
     if (wtype == GGML_TYPE_Q8_0) {
-        a.bsums = nullptr;
+        a.ssum = nullptr;
     } else {
-        a.bsums = (int16_t *) (base + q + al256((size_t) (K / 256 * ncols) * 4));
+        a.ssum = (int16_t *) (base + q + al256((size_t) (K / 256 * ncols) * 4));
     }
     return a;
 }
@@ -88,7 +88,7 @@ void launch_quantize_act(const tview & src, int wtype, const act_buffers & out, 
                            src.ne[1], src.nb[1], src.nb[2], out.q, out.d);
     } else {
         hipLaunchKernelGGL(k_quantize_q8_K, dim3((unsigned) blocks), dim3(256), 0, stream, src.data, K, ncols,
-                           src.ne[1], src.nb[1], src.nb[2], out.q, out.d, out.bsums);
+                           src.ne[1], src.nb[1], src.nb[2], out.q, out.d, out.ssum);
     }
 }
 

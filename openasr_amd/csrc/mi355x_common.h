@@ -56,7 +56,7 @@ inline size_t q8_0_row_bytes(int64_t k) { return (size_t) (k / 32) * 34; }
 struct act_layout {
     int64_t q_stride;   // bytes between columns of quants
     int64_t d_stride;   // floats between columns of scales
-    int64_t bs_stride;  // int16 between columns of bsums (Q8_K only)
+    int64_t ss_stride;  // int16 between columns of 32-element sums (Q8_K only)
 };
 
 __device__ __forceinline__ float half_bits_to_float(uint16_t h) {

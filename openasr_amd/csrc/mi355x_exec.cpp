@@ -121,8 +121,11 @@ struct planner {
 
     explicit planner(backend_state * b, const ggml_cgraph * g) : be(b), cg(g), n_cu(b->dev->n_cu) {}
 
+    std::unordered_map<const ggml_tensor *, int> index;  // node -> position in the graph
+
     void count_uses() {
         for (int i = 0; i < cg->n_nodes; i++) {
+            index[cg->nodes[i]] = i;
             for (int s = 0; s < GGML_MAX_SRC; s++) {
                 if (cg->nodes[i]->src[s]) uses[cg->nodes[i]->src[s]]++;
             }
@@ -145,7 +148,27 @@ struct planner {
         return nullptr;
     }
 
-    void add(std::function<void(hipStream_t)> fn, const ggml_tensor * node, const char * label) {
+    // the quantized weight type shared by every consumer of t after node
+    // `from`, when all of them are MUL_MATs reading t as activations; else -1
+    int quant_consumers(const ggml_tensor * t, int from) const {
+        int wt = -1;
+        for (int j = from; j < cg->n_nodes; j++) {
+            const ggml_tensor * c = cg->nodes[j];
+            bool reads = false;
+            for (int s = 0; s < GGML_MAX_SRC; s++) reads = reads || c->src[s] == t;
+            if (!reads) continue;
+            if (c->op != GGML_OP_MUL_MAT || c->src[1] != t || c->src[0] == t) return -1;
+            const int w = c->src[0]->type;
+            if ((w != GGML_TYPE_Q8_0 && w != GGML_TYPE_Q4_K) || c->src[0]->ne[0] != t->ne[0] ||
+                !supports_op(be->dev, c))
+                return -1;
+            if (wt >= 0 && w != wt) return -1;
+            wt = w;
+        }
+        return wt;
+    }
+
+    void add_step(std::function<void(hipStream_t)> fn, const ggml_tensor * node, const char * label) {
         step s;
         s.run = std::move(fn);
         s.node = node;
@@ -161,17 +184,23 @@ struct planner {
     }
 
     bool plan();
-    bool plan_mul_mat(const ggml_tensor * t);
+    bool plan_mul_mat(int i, const ggml_tensor * t);
+    // t is available before node i runs: a leaf, or a node planned earlier
+    bool ready_before(const ggml_tensor * t, int i) const {
+        while (t->view_src) t = t->view_src;
+        auto it = index.find(t);
+        return it == index.end() || it->second < i;
+    }
     bool plan_norm(int i, const ggml_tensor * t);
     bool plan_unary(int i, const ggml_tensor * t);
     bool plan_binary(const ggml_tensor * t);
     bool plan_fattn(int i, const ggml_tensor * t);
 };
 
-bool planner::plan_mul_mat(const ggml_tensor * t) {
+bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
     const ggml_tensor * w = t->src[0];
     const ggml_tensor * x = t->src[1];
-    const tview dv = make_view(t), xv = make_view(x);
+    const tview xv = make_view(x);
     if (w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K) {
         const int wtype = w->type;
         const int64_t K = w->ne[0], M = w->ne[1];
@@ -185,32 +214,48 @@ bool planner::plan_mul_mat(const ggml_tensor * t) {
         backend_state * b = be;
         const int ncu = n_cu;
         char * dst = (char *) t->data;
-        const int64_t dst_nb1 = (int64_t) t->nb[1];
+        int64_t dst_nb1 = (int64_t) t->nb[1];
         const bool wide = mmq_supported(wtype, M, K) && N > 16;
-        const bool mfma = gemv_mfma_supported(wtype, M, K);
+        const bool mfma = !wide && gemv_mfma_supported(wtype, M, K);
+        // a following residual ADD of the same shape folds into the epilogue
+        const char * res = nullptr;
+        int64_t res_nb1 = 0;
+        const ggml_tensor * add = mfma ? sole_consumer(t, i + 1) : nullptr;
+        if (add && add->op == GGML_OP_ADD && add->type == GGML_TYPE_F32 && is_contiguous(add)) {
+            const ggml_tensor * o = add->src[0] == t ? add->src[1] : add->src[0];
+            bool same = o != t && o->type == GGML_TYPE_F32 && o->nb[0] == 4 && columns_foldable(o);
+            for (int d = 0; d < 4 && same; d++) same = o->ne[d] == t->ne[d] && add->ne[d] == t->ne[d];
+            if (same && ready_before(o, i)) {
+                res = (const char *) o->data;
+                res_nb1 = (int64_t) o->nb[1];
+                dst = (char *) add->data;
+                dst_nb1 = (int64_t) add->nb[1];
+                deferred[add] = add;
+            }
+        }
         if (!reuse) {
-            add(
+            add_step(
                 [=](hipStream_t s) {
                     act_buffers act = act_carve(wtype, act_base(b), K, N);
                     launch_quantize_act(xv, wtype, act, s);
                 },
                 t, wtype == GGML_TYPE_Q8_0 ? "quantize_q8_0" : "quantize_q8_K");
         }
-        add(
+        add_step(
             [=](hipStream_t s) {
                 act_buffers act = act_carve(wtype, act_base(b), K, N);
                 if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
-                else if (mfma) launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
+                else if (mfma) launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1);
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
-            t, wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K");
-        (void) dv;
+            res ? add : t, wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K");
         return true;
     }
+    const tview dv = make_view(t);
     const tview wv = make_view(w);
     const int atype = w->type;
     act_src = nullptr;
-    add([=](hipStream_t s) { launch_mul_mat_float(dv, wv, atype, xv, s); }, t, "mul_mat_float");
+    add_step([=](hipStream_t s) { launch_mul_mat_float(dv, wv, atype, xv, s); }, t, "mul_mat_float");
     return true;
 }
 
@@ -242,8 +287,24 @@ bool planner::plan_norm(int i, const ggml_tensor * t) {
     const tview dv = make_view(out), av = make_view(t->src[0]);
     const bool hw = wt != nullptr, hb = bt != nullptr;
     const tview wv = hw ? make_view(wt) : tview{}, bv = hb ? make_view(bt) : tview{};
-    add([=](hipStream_t s) { launch_norm(dv, av, mode, eps, hw ? &wv : nullptr, hb ? &bv : nullptr, s); }, out,
-        mode == 0 ? "rms_norm" : "norm");
+    // when only quantized MUL_MATs read the result, the norm kernel also
+    // writes their quantized activations (they then skip their quantize step)
+    int qt = quant_consumers(out, i + 1);
+    if (qt >= 0 && !norm_rows_supported(dv, av, hw ? &wv : nullptr, hb ? &bv : nullptr)) qt = -1;
+    const int64_t K = out->ne[0], N = out->ne[1] * out->ne[2] * out->ne[3];
+    if (qt >= 0) act_need = std::max(act_need, act_bytes(qt, K, N));
+    backend_state * b = be;
+    add_step(
+[=](hipStream_t s) {
+            act_buffers ab{nullptr, nullptr, nullptr};
+            if (qt >= 0) ab = act_carve(qt, act_base(b), K, N);
+            launch_norm(dv, av, mode, eps, hw ? &wv : nullptr, hb ? &bv : nullptr, s, qt, qt >= 0 ? &ab : nullptr);
+        },
+        out, mode == 0 ? "rms_norm" : "norm");
+    if (qt >= 0) {
+        act_src = out;
+        act_wtype = qt;
+    }
     return true;
 }
 
@@ -265,7 +326,7 @@ bool planner::plan_unary(int i, const ggml_tensor * t) {
     }
     const tview dv = make_view(t), av = make_view(t->src[0]);
     const uint16_t * gt = be->dev->gelu_table;
-    add([=](hipStream_t s) { launch_unary(dv, av, uop, gt, s, ncu); }, t, "unary");
+    add_step([=](hipStream_t s) { launch_unary(dv, av, uop, gt, s, ncu); }, t, "unary");
     return true;
 }
 
@@ -277,13 +338,13 @@ bool planner::plan_binary(const ggml_tensor * t) {
         auto it = deferred.find(s);
         if (t->op == GGML_OP_MUL && s && s->op == GGML_OP_UNARY && it != deferred.end() && it->second == t) {
             const tview dv = make_view(t), gv = make_view(s->src[0]), uv = make_view(t->src[1 - k]);
-            add([=](hipStream_t st) { launch_silu_mul(dv, gv, uv, st, ncu); }, t, "silu_mul");
+            add_step([=](hipStream_t st) { launch_silu_mul(dv, gv, uv, st, ncu); }, t, "silu_mul");
             return true;
         }
     }
     const tview dv = make_view(t), av = make_view(t->src[0]), bv = make_view(t->src[1]);
     const int op = t->op;
-    add([=](hipStream_t s) { launch_binary(op, dv, av, bv, s, ncu); }, t, "binary");
+    add_step([=](hipStream_t s) { launch_binary(op, dv, av, bv, s, ncu); }, t, "binary");
     return true;
 }
 
@@ -348,8 +409,8 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
     backend_state * b = be;
     float * out = (float *) t->data;
     const int64_t qK = (int64_t) a.d * a.hq, qN = (int64_t) a.n_q * a.n_seq;
-    add(
-        [=](hipStream_t s) {
+    add_step(
+[=](hipStream_t s) {
             fattn_args la = a;
             if (la.qtype >= 0) la.act = act_carve(la.qtype, act_base(b), qK, qN);
             launch_fattn(la, gen_base(b), out, s);
@@ -374,7 +435,7 @@ bool planner::plan() {
         const int ncu = n_cu;
         switch (t->op) {
             case GGML_OP_MUL_MAT:
-                if (!plan_mul_mat(t)) return false;
+                if (!plan_mul_mat(i, t)) return false;
                 continue;
             case GGML_OP_RMS_NORM:
             case GGML_OP_NORM:
@@ -392,7 +453,7 @@ bool planner::plan() {
             case GGML_OP_SCALE: {
                 const tview dv = make_view(t), av = make_view(t->src[0]);
                 const float sc = op_f32(t, 0), bias = op_f32(t, 1);
-                add([=](hipStream_t s) { launch_scale(dv, av, sc, bias, s, ncu); }, t, "scale");
+                add_step([=](hipStream_t s) { launch_scale(dv, av, sc, bias, s, ncu); }, t, "scale");
                 break;
             }
             case GGML_OP_ROPE: {
@@ -400,19 +461,19 @@ bool planner::plan() {
                 const int32_t * pos = (const int32_t *) t->src[1]->data;
                 const int n_dims = t->op_params[1], mode = t->op_params[2];
                 const float fb = op_f32(t, 5), fs = op_f32(t, 6), af = op_f32(t, 8);
-                add([=](hipStream_t s) { launch_rope(dv, av, pos, n_dims, mode, fb, fs, af, s, ncu); }, t, "rope");
+                add_step([=](hipStream_t s) { launch_rope(dv, av, pos, n_dims, mode, fb, fs, af, s, ncu); }, t, "rope");
                 break;
             }
             case GGML_OP_SET_ROWS: {
                 const tview dv = make_view(t), sv = make_view(t->src[0]), iv = make_view(t->src[1]);
                 const int dtype = t->type, i64 = t->src[1]->type == GGML_TYPE_I64;
-                add([=](hipStream_t s) { launch_set_rows(dv, dtype, sv, iv, i64, s, ncu); }, t, "set_rows");
+                add_step([=](hipStream_t s) { launch_set_rows(dv, dtype, sv, iv, i64, s, ncu); }, t, "set_rows");
                 break;
             }
             case GGML_OP_GET_ROWS: {
                 const tview dv = make_view(t), sv = make_view(t->src[0]), iv = make_view(t->src[1]);
                 const int stype = t->src[0]->type;
-                add([=](hipStream_t s) { launch_get_rows(dv, sv, stype, iv, s, ncu); }, t, "get_rows");
+                add_step([=](hipStream_t s) { launch_get_rows(dv, sv, stype, iv, s, ncu); }, t, "get_rows");
                 break;
             }
             case GGML_OP_CPY:
@@ -421,7 +482,7 @@ bool planner::plan() {
                 const ggml_tensor * dst = t->op == GGML_OP_CPY ? t : t;
                 const tview dv = make_view(dst), av = make_view(t->src[0]);
                 const int dtype = dst->type, atype = t->src[0]->type;
-                add([=](hipStream_t s) { launch_copy(dv, dtype, av, atype, s, ncu); }, t, "copy");
+                add_step([=](hipStream_t s) { launch_copy(dv, dtype, av, atype, s, ncu); }, t, "copy");
                 break;
             }
             case GGML_OP_SOFT_MAX: {
@@ -429,7 +490,7 @@ bool planner::plan() {
                 const bool hm = t->src[1] != nullptr;
                 const tview mv = hm ? make_view(t->src[1]) : tview{};
                 const float sc = op_f32(t, 0);
-                add([=](hipStream_t s) { launch_soft_max(dv, av, hm ? &mv : nullptr, sc, s); }, t, "soft_max");
+                add_step([=](hipStream_t s) { launch_soft_max(dv, av, hm ? &mv : nullptr, sc, s); }, t, "soft_max");
                 break;
             }
             case GGML_OP_ARGMAX:
@@ -439,8 +500,8 @@ bool planner::plan() {
                 const int first = t->op == GGML_OP_ARGMAX_FIRST;
                 gen_need = std::max(gen_need, argmax_scratch_bytes(av.ne[0], av.ne[1]));
                 backend_state * b = be;
-                add(
-                    [=](hipStream_t s) {
+                add_step(
+[=](hipStream_t s) {
                         launch_argmax(av, out, first, gen_base(b), s);
                     },
                     t, "argmax");

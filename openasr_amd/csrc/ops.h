@@ -10,7 +10,7 @@ namespace mi355x {
 struct act_buffers {
     int8_t * q;
     float * d;
-    int16_t * bsums;  // Q8_K only
+    int16_t * ssum;  // Q8_K only: sums of each 32 consecutive quants, [col][K/32]
 };
 
 // activation quantization for a quantized-weight MUL_MAT
@@ -22,10 +22,12 @@ act_buffers act_carve(int wtype, char * base, int64_t K, int64_t ncols);
 void launch_mmv(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                 int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
 
-// MFMA GEMV for up to 16 columns per launch (the decode step), M % 16 == 0
+// MFMA GEMV for the decode step (16-column chunks), M % 16 == 0; res (same
+// column layout as dst, stride res_nb1) is added to the result when non-null
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K);
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
-                      int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
+                      int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu,
+                      const char * res = nullptr, int64_t res_nb1 = 0);
 
 // MFMA int8 GEMM for wider N (prefill)
 bool mmq_supported(int wtype, int64_t M, int64_t K);
@@ -68,8 +70,12 @@ void launch_binary(int op, const tview & d, const tview & a, const tview & b, hi
 void launch_scale(const tview & d, const tview & a, float sc, float bias, hipStream_t s, int n_cu);
 void launch_unary(const tview & d, const tview & a, int op, const uint16_t * gelu_table, hipStream_t s, int n_cu);
 void launch_silu_mul(const tview & d, const tview & g, const tview & u, hipStream_t s, int n_cu);
+// qtype/act: optionally also write the normalised rows as quantized
+// activations (rows = columns of the consuming MUL_MAT); honoured when
+// norm_rows_supported() holds, else the caller quantizes separately
 void launch_norm(const tview & d, const tview & a, int mode, float eps, const tview * w, const tview * b,
-                 hipStream_t s);
+                 hipStream_t s, int qtype = -1, const act_buffers * act = nullptr);
+bool norm_rows_supported(const tview & d, const tview & a, const tview * w, const tview * b);
 void launch_rope(const tview & d, const tview & a, const int32_t * pos, int n_dims, int mode, float freq_base,
                  float freq_scale, float attn_factor, hipStream_t s, int n_cu);
 void launch_set_rows(const tview & dst, int dtype, const tview & src, const tview & idx, int idx_is_i64,

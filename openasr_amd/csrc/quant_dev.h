@@ -33,7 +33,7 @@ __device__ __forceinline__ q8_0_lane quantize_q8_0_group(float4 v) {
 
 struct q8_K_lane {
     char4 q;
-    int bsum;  // sum of the 16 quants of this lane's 4-lane group (same in all four lanes)
+    int ssum;  // sum of the 32 quants of this lane's 8-lane group (same in all eight lanes)
     float d;   // block scale, uniform over the wave
 };
 
@@ -60,7 +60,7 @@ __device__ __forceinline__ q8_K_lane quantize_q8_K_wave(float4 v, int lane) {
     q8_K_lane o;
     if (ab == 0.0f) {
         o.q = make_char4(0, 0, 0, 0);
-        o.bsum = 0;
+        o.ssum = 0;
         o.d = 0.0f;
         return o;
     }
@@ -73,7 +73,8 @@ __device__ __forceinline__ q8_K_lane quantize_q8_K_wave(float4 v, int lane) {
     int s = a + b + c + w;
     s += __shfl_xor(s, 1);
     s += __shfl_xor(s, 2);
-    o.bsum = s;
+    s += __shfl_xor(s, 4);
+    o.ssum = s;
     o.d = 1.0f / iscale;
     return o;
 }
