@@ -317,6 +317,45 @@ void launch_norm(const tview & d, const tview & a, int mode, float eps, const tv
     else hipLaunchKernelGGL(k_norm<64>, grid, dim3(256), 0, s, d, a, mode, eps, wv, hw, bv, hb, rows);
 }
 
+// RMSNorm * w followed by RoPE NEOX over full 128-wide rows (the per-head
+// QK-norm then rotary embedding of nn/decoder.rs:1937-1968): one wave per
+// row, lane l holds elements l and l + 64 -- exactly the NEOX pair of
+// rotation index l -- so the row is normalised, scaled and rotated in
+// registers. Same arithmetic as k_norm followed by k_rope.
+__global__ __launch_bounds__(256) void k_rms_norm_rope128(tview d, tview a, float eps, const float * __restrict__ w,
+                                                          const int32_t * __restrict__ pos, float theta_scale,
+                                                          float freq_scale, float attn_factor, int64_t rows) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int64_t i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
+    const float * x = (const float *) (a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3]);
+    float * y = (float *) (d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]);
+    const float x0 = x[lane], x1 = x[lane + 64];
+    const float w0 = w[lane], w1 = w[lane + 64];
+    const float p = (float) pos[i2];
+    const double s2 = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
+    const float var = (float) (s2 / 128.0);
+    const float scale = 1.0f / sqrtf(var + eps);
+    const float v0 = (x0 * scale) * w0, v1 = (x1 * scale) * w1;
+    float theta = p;
+    for (int k = 0; k < lane; k++) theta *= theta_scale;
+    float sn, c;
+    sincosf_det(freq_scale * theta, sn, c);
+    c *= attn_factor;
+    sn *= attn_factor;
+    y[lane] = v0 * c - v1 * sn;
+    y[lane + 64] = v0 * sn + v1 * c;
+}
+
+void launch_rms_norm_rope128(const tview & d, const tview & a, float eps, const float * w, const int32_t * pos,
+                             float freq_base, float freq_scale, float attn_factor, hipStream_t s) {
+    const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
+    const float theta_scale = powf(freq_base, -2.0f / 128.0f);
+    hipLaunchKernelGGL(k_rms_norm_rope128, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, s, d, a, eps, w, pos,
+                       theta_scale, freq_scale, attn_factor, rows);
+}
+
 // -------------------------------------------------------------- rope -----
 
 // ggml_rope_cache_init with ext_factor 0: theta_i = p * theta_scale^i built by
@@ -367,24 +406,39 @@ void launch_rope(const tview & d, const tview & a, const int32_t * pos, int n_di
 
 // dst[:, idx[i, i2 % ne11, i3 % ne12], i2, i3] = src[:, i, i2, i3], with f32 ->
 // f16 round-to-nearest-even when the cache is f16 (KV write, nn/decoder.rs:2031-2036)
-__global__ void k_set_rows(tview dst, int dtype, tview src, tview idx, int idx_is_i64, int64_t n) {
-    for (int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+struct set_rows_job {
+    tview dst, src, idx;
+    int dtype, idx_is_i64;
+    int64_t n;
+};
+
+// blockIdx.y selects the job: the K and V writes of one layer share a launch
+__global__ void k_set_rows(set_rows_job j0, set_rows_job j1) {
+    const set_rows_job & j = blockIdx.y == 0 ? j0 : j1;
+    for (int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; t < j.n; t += (int64_t) gridDim.x * blockDim.x) {
         int64_t i0, i1, i2, i3;
-        unravel(t, src.ne, i0, i1, i2, i3);
-        const char * ip = idx.data + i1 * idx.nb[0] + (i2 % idx.ne[1]) * idx.nb[1] + (i3 % idx.ne[2]) * idx.nb[2];
-        const int64_t r = idx_is_i64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
-        const float v = *(const float *) (src.data + offs4(src, i0, i1, i2, i3));
-        char * o = dst.data + i0 * dst.nb[0] + r * dst.nb[1] + i2 * dst.nb[2] + i3 * dst.nb[3];
-        if (dtype == GGML_TYPE_F16) *(uint16_t *) o = float_to_half_bits(v);
+        unravel(t, j.src.ne, i0, i1, i2, i3);
+        const char * ip = j.idx.data + i1 * j.idx.nb[0] + (i2 % j.idx.ne[1]) * j.idx.nb[1] + (i3 % j.idx.ne[2]) * j.idx.nb[2];
+        const int64_t r = j.idx_is_i64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
+        const float v = *(const float *) (j.src.data + offs4(j.src, i0, i1, i2, i3));
+        char * o = j.dst.data + i0 * j.dst.nb[0] + r * j.dst.nb[1] + i2 * j.dst.nb[2] + i3 * j.dst.nb[3];
+        if (j.dtype == GGML_TYPE_F16) *(uint16_t *) o = float_to_half_bits(v);
         else *(float *) o = v;
     }
 }
 
 void launch_set_rows(const tview & dst, int dtype, const tview & src, const tview & idx, int idx_is_i64,
-                     hipStream_t s, int n_cu) {
-    const int64_t n = src.ne[0] * src.ne[1] * src.ne[2] * src.ne[3];
-    hipLaunchKernelGGL(k_set_rows, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, dst, dtype, src, idx, idx_is_i64,
-                       n);
+                     hipStream_t s, int n_cu, const tview * dst2, int dtype2, const tview * src2) {
+    set_rows_job j0{dst, src, idx, dtype, idx_is_i64, src.ne[0] * src.ne[1] * src.ne[2] * src.ne[3]};
+    set_rows_job j1 = j0;
+    if (dst2) {
+        j1.dst = *dst2;
+        j1.src = *src2;
+        j1.dtype = dtype2;
+        j1.n = src2->ne[0] * src2->ne[1] * src2->ne[2] * src2->ne[3];
+    }
+    const int64_t n = j0.n > j1.n ? j0.n : j1.n;
+    hipLaunchKernelGGL(k_set_rows, dim3(grid_for(n, 256, n_cu), dst2 ? 2 : 1), dim3(256), 0, s, j0, j1);
 }
 
 // ----------------------------------------------------------- get_rows ----

@@ -78,6 +78,33 @@ bool columns_foldable(const ggml_tensor * t) {
     return true;
 }
 
+// x is a view (or the tensor itself) of c, a contiguous f32 CONT of the 2-D
+// view s whose rows are contiguous. Express x as a strided view of s: dims
+// whose stride is a whole number of s rows move across rows, the others must
+// stay inside one row from x's starting column.
+bool remap_through_cont(const ggml_tensor * x, const ggml_tensor * c, const ggml_tensor * s, tview & out) {
+    const int64_t off = (int64_t) ((const char *) x->data - (const char *) c->data);
+    if (off < 0 || off % 4 != 0) return false;
+    const int64_t row = s->ne[0];
+    const int64_t base = off / 4;
+    int64_t reach = base % row;  // furthest column touched by in-row dims
+    out.data = (char *) s->data + (base % row) * 4 + (base / row) * (int64_t) s->nb[1];
+    for (int d = 0; d < 4; d++) {
+        out.ne[d] = x->ne[d];
+        if (x->nb[d] % 4 != 0) return false;
+        const int64_t se = (int64_t) x->nb[d] / 4;
+        if (x->ne[d] == 1) {
+            out.nb[d] = (int64_t) x->nb[d];
+        } else if (se % row == 0) {
+            out.nb[d] = (se / row) * (int64_t) s->nb[1];
+        } else {
+            out.nb[d] = se * 4;
+            reach += se * (x->ne[d] - 1);
+        }
+    }
+    return reach < row;
+}
+
 uint64_t mix(uint64_t h, uint64_t v) {
     h ^= v + 0x9e3779b97f4a7c15ULL + (h << 6) + (h >> 2);
     return h;
@@ -122,6 +149,51 @@ struct planner {
     explicit planner(backend_state * b, const ggml_cgraph * g) : be(b), cg(g), n_cu(b->dev->n_cu) {}
 
     std::unordered_map<const ggml_tensor *, int> index;  // node -> position in the graph
+    // CONT nodes whose copy is skipped: consumers read the CONT's strided
+    // source directly (CONT -> its source)
+    std::unordered_map<const ggml_tensor *, const ggml_tensor *> bypass;
+
+    static const ggml_tensor * root_of(const ggml_tensor * x) { return x->view_src ? x->view_src : x; }
+
+    // the view a kernel reads for tensor x (through a bypassed CONT if any)
+    tview view_of(const ggml_tensor * x) const {
+        auto it = bypass.find(root_of(x));
+        tview v = make_view(x);
+        if (it != bypass.end()) remap_through_cont(x, it->first, it->second, v);
+        return v;
+    }
+
+    // A CONT of a 2-D row-contiguous f32 view is not materialised when every
+    // reader is an op whose kernel takes arbitrary strides and each read view
+    // maps onto the source (the column views of the fused QKV projection,
+    // nn/decoder.rs:1722-1789, are made contiguous only to be reshaped).
+    void find_bypass() {
+        for (int i = 0; i < cg->n_nodes; i++) {
+            const ggml_tensor * c = cg->nodes[i];
+            if (c->op != GGML_OP_CONT || c->type != GGML_TYPE_F32 || (c->flags & GGML_TENSOR_FLAG_OUTPUT)) continue;
+            const ggml_tensor * s = c->src[0];
+            if (s->type != GGML_TYPE_F32 || s->nb[0] != 4 || s->ne[2] != 1 || s->ne[3] != 1) continue;
+            if (s->nb[1] % 4 != 0) continue;
+            bool ok = true, any = false;
+            for (int j = i + 1; j < cg->n_nodes && ok; j++) {
+                const ggml_tensor * n = cg->nodes[j];
+                for (int k = 0; k < GGML_MAX_SRC && ok; k++) {
+                    const ggml_tensor * x = n->src[k];
+                    if (!x || root_of(x) != c) continue;
+                    if (is_view_op(n->op)) continue;  // metadata; its readers are checked themselves
+                    any = true;
+                    const bool reader = n->op == GGML_OP_RMS_NORM || n->op == GGML_OP_NORM || n->op == GGML_OP_ROPE ||
+                                        (n->op == GGML_OP_SET_ROWS && k == 0) ||
+                                        ((n->op == GGML_OP_CPY || n->op == GGML_OP_CONT) && k == 0) ||
+                                        n->op == GGML_OP_ADD || n->op == GGML_OP_MUL || n->op == GGML_OP_SUB ||
+                                        n->op == GGML_OP_DIV;
+                    tview v;
+                    ok = reader && remap_through_cont(x, c, s, v);
+                }
+            }
+            if (ok && any) bypass[c] = s;
+        }
+    }
 
     void count_uses() {
         for (int i = 0; i < cg->n_nodes; i++) {
@@ -284,9 +356,25 @@ bool planner::plan_norm(int i, const ggml_tensor * t) {
             deferred[add] = add;
         }
     }
-    const tview dv = make_view(out), av = make_view(t->src[0]);
+    const tview dv = make_view(out), av = view_of(t->src[0]);
     const bool hw = wt != nullptr, hb = bt != nullptr;
     const tview wv = hw ? make_view(wt) : tview{}, bv = hb ? make_view(bt) : tview{};
+    // RMSNorm * w feeding a full-width NEOX RoPE over 128-element rows: one
+    // kernel normalises and rotates each row
+    const ggml_tensor * rope = (mode == 0 && hw && !hb) ? sole_consumer(out, i + 1) : nullptr;
+    if (rope && rope->op == GGML_OP_ROPE && rope->src[0] == out && supports_op(be->dev, rope) &&
+        rope->op_params[2] == GGML_ROPE_TYPE_NEOX && rope->op_params[1] == 128 && out->ne[0] == 128 &&
+        is_contiguous(wt) && wt->ne[1] == 1 && wt->ne[2] == 1 && wt->ne[3] == 1 && av.nb[0] == 4 &&
+        rope->nb[0] == 4) {
+        const tview rv = make_view(rope);
+        const float * wp = (const float *) wt->data;
+        const int32_t * pos = (const int32_t *) rope->src[1]->data;
+        const float fb = op_f32(rope, 5), fs = op_f32(rope, 6), af = op_f32(rope, 8);
+        deferred[rope] = rope;
+        add_step([=](hipStream_t s) { launch_rms_norm_rope128(rv, av, eps, wp, pos, fb, fs, af, s); }, rope,
+                 "rms_norm_rope");
+        return true;
+    }
     // when only quantized MUL_MATs read the result, the norm kernel also
     // writes their quantized activations (they then skip their quantize step)
     int qt = quant_consumers(out, i + 1);
@@ -342,7 +430,7 @@ bool planner::plan_binary(const ggml_tensor * t) {
             return true;
         }
     }
-    const tview dv = make_view(t), av = make_view(t->src[0]), bv = make_view(t->src[1]);
+    const tview dv = make_view(t), av = view_of(t->src[0]), bv = view_of(t->src[1]);
     const int op = t->op;
     add_step([=](hipStream_t s) { launch_binary(op, dv, av, bv, s, ncu); }, t, "binary");
     return true;
@@ -425,10 +513,12 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
 
 bool planner::plan() {
     count_uses();
+    find_bypass();
     for (int i = 0; i < cg->n_nodes; i++) {
         const ggml_tensor * t = cg->nodes[i];
         if (is_view_op(t->op)) continue;
         if (!supports_op(be->dev, t)) return fail(t, "unsupported op or layout");
+        if (bypass.count(t)) continue;  // readers take the CONT's source directly
         auto dit = deferred.find(t);
         if (dit != deferred.end() && dit->second == t) continue;  // produced by a fused predecessor
         if (dit != deferred.end()) continue;                        // evaluated inside its consumer
@@ -457,7 +547,7 @@ bool planner::plan() {
                 break;
             }
             case GGML_OP_ROPE: {
-                const tview dv = make_view(t), av = make_view(t->src[0]);
+                const tview dv = make_view(t), av = view_of(t->src[0]);
                 const int32_t * pos = (const int32_t *) t->src[1]->data;
                 const int n_dims = t->op_params[1], mode = t->op_params[2];
                 const float fb = op_f32(t, 5), fs = op_f32(t, 6), af = op_f32(t, 8);
@@ -465,9 +555,29 @@ bool planner::plan() {
                 break;
             }
             case GGML_OP_SET_ROWS: {
-                const tview dv = make_view(t), sv = make_view(t->src[0]), iv = make_view(t->src[1]);
+                const tview dv = make_view(t), sv = view_of(t->src[0]), iv = make_view(t->src[1]);
                 const int dtype = t->type, i64 = t->src[1]->type == GGML_TYPE_I64;
-                add_step([=](hipStream_t s) { launch_set_rows(dv, dtype, sv, iv, i64, s, ncu); }, t, "set_rows");
+                // the next planned node writing rows with the same indices
+                // (the V write after the K write) shares the launch
+                const ggml_tensor * t2 = nullptr;
+                for (int j = i + 1; j < cg->n_nodes; j++) {
+                    const ggml_tensor * n = cg->nodes[j];
+                    if (is_view_op(n->op) || bypass.count(n)) continue;
+                    if (n->op == GGML_OP_SET_ROWS && n->src[1] == t->src[1] && supports_op(be->dev, n) &&
+                        root_of(n->src[0]) != root_of(t) && n->src[0] != t) {
+                        t2 = n;
+                    }
+                    break;
+                }
+                if (t2) {
+                    const tview dv2 = make_view(t2), sv2 = view_of(t2->src[0]);
+                    const int dtype2 = t2->type;
+                    deferred[t2] = t2;
+                    add_step([=](hipStream_t s) { launch_set_rows(dv, dtype, sv, iv, i64, s, ncu, &dv2, dtype2, &sv2); },
+                             t2, "set_rows");
+                } else {
+                    add_step([=](hipStream_t s) { launch_set_rows(dv, dtype, sv, iv, i64, s, ncu); }, t, "set_rows");
+                }
                 break;
             }
             case GGML_OP_GET_ROWS: {
@@ -479,8 +589,8 @@ bool planner::plan() {
             case GGML_OP_CPY:
             case GGML_OP_CONT:
             case GGML_OP_DUP: {
-                const ggml_tensor * dst = t->op == GGML_OP_CPY ? t : t;
-                const tview dv = make_view(dst), av = make_view(t->src[0]);
+                const ggml_tensor * dst = t;
+                const tview dv = make_view(dst), av = view_of(t->src[0]);
                 const int dtype = dst->type, atype = t->src[0]->type;
                 add_step([=](hipStream_t s) { launch_copy(dv, dtype, av, atype, s, ncu); }, t, "copy");
                 break;

@@ -78,8 +78,13 @@ void launch_norm(const tview & d, const tview & a, int mode, float eps, const tv
 bool norm_rows_supported(const tview & d, const tview & a, const tview * w, const tview * b);
 void launch_rope(const tview & d, const tview & a, const int32_t * pos, int n_dims, int mode, float freq_base,
                  float freq_scale, float attn_factor, hipStream_t s, int n_cu);
+// optional second job (dst2/src2, same indices): both writes in one launch
 void launch_set_rows(const tview & dst, int dtype, const tview & src, const tview & idx, int idx_is_i64,
-                     hipStream_t s, int n_cu);
+                     hipStream_t s, int n_cu, const tview * dst2 = nullptr, int dtype2 = 0,
+                     const tview * src2 = nullptr);
+// RMSNorm * w then RoPE NEOX on rows of exactly 128 elements (n_dims 128)
+void launch_rms_norm_rope128(const tview & d, const tview & a, float eps, const float * w, const int32_t * pos,
+                             float freq_base, float freq_scale, float attn_factor, hipStream_t s);
 void launch_get_rows(const tview & dst, const tview & src, int stype, const tview & idx, hipStream_t s, int n_cu);
 void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStream_t s, int n_cu);
 void launch_soft_max(const tview & d, const tview & a, const tview * mask, float scale, hipStream_t s);
