@@ -104,8 +104,11 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
         kern[k][0] += ms
         kern[k][1] += 1
     wb = weight_bytes(wl.shape, wl.wtype)
+    # every quantized GEMV launch of the step (plain, residual-epilogue and
+    # gate+up SwiGLU launches all carry the "mul_mat" label prefix)
     gemv_key = "mul_mat_q4_K" if wl.wtype == g.Q4_K else "mul_mat_q8_0"
-    gemv_ms, gemv_n = kern.get(gemv_key, [float("nan"), 0])
+    gemv_ms = sum(v[0] for k, v in kern.items() if k.startswith("mul_mat"))
+    gemv_n = sum(v[1] for k, v in kern.items() if k.startswith("mul_mat"))
     # activation bytes per step: int8 quants in, f32 results out, per matrix
     d, hd, ffn = wl.shape["d_model"], wl.shape["head_dim"], wl.shape["ffn"]
     q_w, kv_w = wl.shape["n_head"] * hd, wl.shape["n_kv_head"] * hd

@@ -41,6 +41,7 @@ __device__ __forceinline__ v4i mfma_i8(long a, long b, v4i c) {
 
 struct gemv_args {
     const char * W;
+    const char * W2;  // optional second matrix of the same shape (gate + up)
     int64_t row_bytes, M, K;
     const int8_t * aq;
     const float * ad;
@@ -64,11 +65,16 @@ __device__ __forceinline__ void q4k_scales(const uint4 & hdr, int * sc, int * mn
     }
 }
 
-// wave partials summed in wave order by wave 0, then stored (+ residual)
+// wave partials summed in wave order by wave 0, then stored. Waves
+// [0, half) hold W's partials, waves [half, nw) W2's when there is a second
+// matrix; the epilogue then writes silu(W x) * (W2 x) -- the SwiGLU gate of
+// nn/ffn.rs:64-91 with the same roundings as MUL_MAT, SILU and MUL apart.
+// A residual, when given, is added to the rounded product.
 __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4], double (*s_red)[64][4], int64_t row,
-                                            int n0) {
+                                            int n0, int half) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int g = lane >> 4;
+    double acc2[4] = {0.0, 0.0, 0.0, 0.0};
     if (nw > 1) {
         if (wave > 0) {
 #pragma unroll
@@ -76,9 +82,13 @@ __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4
         }
         __syncthreads();
         if (wave != 0) return;
-        for (int w = 1; w < nw; w++) {
+        for (int w = 1; w < half; w++) {
 #pragma unroll
             for (int i = 0; i < 4; i++) acc[i] += s_red[w][lane][i];
+        }
+        for (int w = half; w < nw; w++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) acc2[i] += s_red[w][lane][i];
         }
     }
 #pragma unroll
@@ -86,6 +96,10 @@ __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4
         const int n = n0 + 4 * g + i;
         if (n < a.N) {
             float v = (float) acc[i];
+            if (a.W2) {
+                const float u = (float) acc2[i];
+                v = (v / (1.0f + expf_det(-v))) * u;
+            }
             if (a.res) v = *(const float *) (a.res + (int64_t) n * a.res_nb1 + row * 4) + v;
             *(float *) (a.dst + (int64_t) n * a.dst_nb1 + row * 4) = v;
         }
@@ -97,16 +111,19 @@ __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4
 __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
     __shared__ double s_red[16][64][4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int half = a.W2 ? nw / 2 : nw;
+    const int second = wave >= half;
+    const int wv = wave - (second ? half : 0);
     const int r = lane & 15, g = lane >> 4;
     const int64_t tile = blockIdx.x;
     const int n0 = (int) blockIdx.y * 16;
     const int64_t nsb = a.K / 256;
     const int64_t row = tile * 16 + r;
-    const char * wrow = a.W + row * a.row_bytes;
+    const char * wrow = (second ? a.W2 : a.W) + row * a.row_bytes;
     const bool a_ok = n0 + r < a.N;  // this lane's A-operand column
     const int8_t * acol = a.aq + (int64_t) (n0 + r) * a.K;
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int64_t sb = wave; sb < nsb; sb += nw) {
+    for (int64_t sb = wv; sb < nsb; sb += half) {
         const char * blk = wrow + sb * 144;
         const uint4 hdr = *(const uint4 *) blk;
         long q[4], af[8];
@@ -153,7 +170,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
             acc[i] += d * (double) isum[i] - dmin * (double) msum;
         }
     }
-    gemv_finish(a, acc, s_red, row, n0);
+    gemv_finish(a, acc, s_red, row, n0, half);
 }
 
 // Q8_0 weights in the row-split layout [K quants][K/32 f16 scales]; the waves
@@ -163,17 +180,20 @@ constexpr int kQ8Group = 8;
 __global__ __launch_bounds__(1024) void k_gemv_q8_0(gemv_args a) {
     __shared__ double s_red[16][64][4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int half = a.W2 ? nw / 2 : nw;
+    const int second = wave >= half;
+    const int wv = wave - (second ? half : 0);
     const int r = lane & 15, g = lane >> 4;
     const int64_t tile = blockIdx.x;
     const int n0 = (int) blockIdx.y * 16;
     const int64_t nblk = a.K / 32;
     const int64_t row = tile * 16 + r;
-    const char * wrow = a.W + row * a.row_bytes;
+    const char * wrow = (second ? a.W2 : a.W) + row * a.row_bytes;
     const uint16_t * wsc = (const uint16_t *) (wrow + a.K);
     const bool a_ok = n0 + r < a.N;
     const int8_t * acol = a.aq + (int64_t) (n0 + r) * a.K;
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int64_t b0 = (int64_t) wave * kQ8Group; b0 < nblk; b0 += (int64_t) nw * kQ8Group) {
+    for (int64_t b0 = (int64_t) wv * kQ8Group; b0 < nblk; b0 += (int64_t) half * kQ8Group) {
         long q[kQ8Group], af[kQ8Group];
         uint16_t ds[kQ8Group];
         float4 ad[4][kQ8Group / 4];
@@ -211,7 +231,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q8_0(gemv_args a) {
             }
         }
     }
-    gemv_finish(a, acc, s_red, row, n0);
+    gemv_finish(a, acc, s_red, row, n0, half);
 }
 
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K) {
@@ -223,10 +243,11 @@ bool gemv_mfma_supported(int wtype, int64_t M, int64_t K) {
 
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const char * res,
-                      int64_t res_nb1) {
+                      int64_t res_nb1, const char * W2) {
     (void) n_cu;
     gemv_args a;
     a.W = W;
+    a.W2 = W2;
     a.row_bytes = row_bytes;
     a.M = M;
     a.K = K;
@@ -240,7 +261,8 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
     a.res_nb1 = res_nb1;
     const dim3 grid((unsigned) (M / 16), (unsigned) ((N + 15) / 16));
     const int64_t units = wtype == GGML_TYPE_Q4_K ? K / 256 : (K / 32 + kQ8Group - 1) / kQ8Group;
-    const unsigned waves = (unsigned) (units < 16 ? units : 16);
+    const int64_t per = W2 ? 8 : 16;  // waves per matrix
+    const unsigned waves = (unsigned) ((units < per ? units : per) * (W2 ? 2 : 1));
     if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_gemv_q4_K, grid, dim3(64 * waves), 0, stream, a);
     else hipLaunchKernelGGL(k_gemv_q8_0, grid, dim3(64 * waves), 0, stream, a);
 }

@@ -289,10 +289,35 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         int64_t dst_nb1 = (int64_t) t->nb[1];
         const bool wide = mmq_supported(wtype, M, K) && N > 16;
         const bool mfma = !wide && gemv_mfma_supported(wtype, M, K);
+        // SwiGLU: MUL_MAT(gate, x) -> SILU -> MUL with MUL_MAT(up, x) of the
+        // same shape becomes one launch over both matrices
+        const char * W2 = nullptr;
+        const ggml_tensor * produced = t;  // the last node the GEMV step writes
+        const ggml_tensor * silu = mfma ? sole_consumer(t, i + 1) : nullptr;
+        if (silu && silu->op == GGML_OP_UNARY && silu->op_params[0] == GGML_UNARY_OP_SILU && silu->src[0] == t) {
+            const ggml_tensor * h = sole_consumer(silu, i + 1);
+            const ggml_tensor * u = nullptr;
+            if (h && h->op == GGML_OP_MUL && (h->src[0] == silu || h->src[1] == silu)) {
+                u = h->src[0] == silu ? h->src[1] : h->src[0];
+            }
+            bool ok = u && u->op == GGML_OP_MUL_MAT && u->src[1] == x && u->src[0]->type == wtype &&
+                      u->src[0]->ne[0] == K && u->src[0]->ne[1] == M && u->src[0]->nb[1] == w->nb[1] &&
+                      sole_consumer(u, i + 1) == h && supports_op(be->dev, u) && is_contiguous(h);
+            for (int d = 0; d < 4 && ok; d++) ok = h->ne[d] == t->ne[d] && u->ne[d] == t->ne[d];
+            if (ok) {
+                W2 = (const char *) u->src[0]->data;
+                dst = (char *) h->data;
+                dst_nb1 = (int64_t) h->nb[1];
+                deferred[silu] = silu;
+                deferred[u] = u;
+                deferred[h] = h;
+                produced = h;
+            }
+        }
         // a following residual ADD of the same shape folds into the epilogue
         const char * res = nullptr;
         int64_t res_nb1 = 0;
-        const ggml_tensor * add = mfma ? sole_consumer(t, i + 1) : nullptr;
+        const ggml_tensor * add = mfma && !W2 ? sole_consumer(t, i + 1) : nullptr;
         if (add && add->op == GGML_OP_ADD && add->type == GGML_TYPE_F32 && is_contiguous(add)) {
             const ggml_tensor * o = add->src[0] == t ? add->src[1] : add->src[0];
             bool same = o != t && o->type == GGML_TYPE_F32 && o->nb[0] == 4 && columns_foldable(o);
@@ -303,6 +328,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 dst = (char *) add->data;
                 dst_nb1 = (int64_t) add->nb[1];
                 deferred[add] = add;
+                produced = add;
             }
         }
         if (!reuse) {
@@ -317,10 +343,12 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             [=](hipStream_t s) {
                 act_buffers act = act_carve(wtype, act_base(b), K, N);
                 if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
-                else if (mfma) launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1);
+                else if (mfma)
+                    launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1, W2);
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
-            res ? add : t, wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K");
+            produced, W2 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")
+                             : (wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K"));
         return true;
     }
     const tview dv = make_view(t);

@@ -23,11 +23,12 @@ void launch_mmv(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t
                 int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
 
 // MFMA GEMV for the decode step (16-column chunks), M % 16 == 0; res (same
-// column layout as dst, stride res_nb1) is added to the result when non-null
+// column layout as dst, stride res_nb1) is added to the result when non-null;
+// with W2 (same shape and type as W) the result is silu(W x) * (W2 x)
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K);
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu,
-                      const char * res = nullptr, int64_t res_nb1 = 0);
+                      const char * res = nullptr, int64_t res_nb1 = 0, const char * W2 = nullptr);
 
 // MFMA int8 GEMM for wider N (prefill)
 bool mmq_supported(int wtype, int64_t M, int64_t K);
