@@ -16,6 +16,9 @@
 // same definition (oracle fidelity 4).
 //
 // Two launch forms compute it:
+//   decode one wave per (chunk, query head, sequence) for a single query
+//          position: mask first, then the chunk's K and V, no barriers;
+//          partials to scratch, combined by a second launch.
 //   split  one workgroup per (chunk, kv head, sequence, query tile): loads
 //          the chunk's mask first and skips a fully masked chunk without
 //          touching K/V (the graph always passes the full fixed span,
@@ -290,7 +293,7 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_split(fattn_args a, float 
     }
 }
 
-// combine of the split form: one workgroup per tile, chunks in order
+// combine of the split forms: one workgroup per tile, chunks in order
 template <int D, int R>
 __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, const float * __restrict__ part_m,
                                                               const double * __restrict__ part_l,
@@ -299,33 +302,42 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
     __shared__ fa_smem<D, R> sm;
     __shared__ double s_L[R];
     __shared__ double s_w[R][kFaMaxChunks];
+    __shared__ double s_l[R][kFaMaxChunks];
     const fa_tile t = fa_tile_of(a);
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t prow = (int64_t) t.gti * R;
+    const int nc = a.n_chunks;
     for (int r = wave; r < t.nrows; r += 4) {
         float M = -INFINITY;
-        for (int i = lane; i < a.n_chunks; i += 64) M = fmaxf(M, part_m[(prow + r) * a.n_chunks + i]);
+        for (int i = lane; i < nc; i += 64) M = fmaxf(M, part_m[(prow + r) * nc + i]);
         M = wave_max(M);
-        for (int i = lane; i < a.n_chunks; i += 64) {
-            const float mc = part_m[(prow + r) * a.n_chunks + i];
+        for (int i = lane; i < nc; i += 64) {
+            const float mc = part_m[(prow + r) * nc + i];
             s_w[r][i] = mc == -INFINITY ? 0.0 : (double) expf_det(mc - M);
+            s_l[r][i] = part_l[(prow + r) * nc + i];
         }
     }
     __syncthreads();
     if (tid < t.nrows) {
         double L = 0.0;
-        for (int i = 0; i < a.n_chunks; i++) {
-            if (s_w[tid][i] != 0.0) L += s_w[tid][i] * part_l[(prow + tid) * a.n_chunks + i];
+        for (int i = 0; i < nc; i++) {
+            if (s_w[tid][i] != 0.0) L += s_w[tid][i] * s_l[tid][i];
         }
         s_L[tid] = L;
     }
     __syncthreads();
     for (int idx = tid; idx < t.nrows * D; idx += kFaThreads) {
         const int r = idx / D, d = idx % D;
-        const double * pa = part_acc + (prow + r) * a.n_chunks * D + d;
+        const double * pa = part_acc + (prow + r) * nc * D + d;
         double O = 0.0;
-        for (int i = 0; i < a.n_chunks; i++) {
-            if (s_w[r][i] != 0.0) O += s_w[r][i] * pa[(int64_t) i * D];
+        for (int c0 = 0; c0 < nc; c0 += 16) {
+            double v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = c0 + k < nc ? pa[(int64_t) (c0 + k) * D] : 0.0;
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                if (c0 + k < nc && s_w[r][c0 + k] != 0.0) O += s_w[r][c0 + k] * v[k];
+            }
         }
         const float o = s_L[r] == 0.0 ? 0.0f : (float) (O / s_L[r]);
         out[fa_orow(a, t, r) * D + d] = o;
@@ -334,6 +346,111 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
     if (a.qtype >= 0) {
         __syncthreads();
         fa_quantize_out<D, R>(a, t, sm);
+    }
+}
+
+// Decode form (one query position): one wave per (chunk, query head,
+// sequence). For the scores lane p owns KV position p of the chunk (its whole
+// K row, the query broadcast from LDS); for P*V lane l owns dims D/64*l.. of
+// every position (V is loaded once the scores are done), the chunk's p
+// values broadcast lane by lane. Every sum runs in the CPU reference's order
+// (dimensions, then positions) and the p*v products are exact in f64, so
+// fused multiply-adds change nothing: the chunk partials are bit-identical. The query heads of one kv head
+// read the same K/V rows at the same time, so the second read comes from
+// cache. Waves share nothing: wave-local LDS, no workgroup barriers.
+template <int D>
+__global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __restrict__ part_m,
+                                                      double * __restrict__ part_l, double * __restrict__ part_acc) {
+    constexpr int DL = D / 64;
+    __shared__ __align__(16) float s_q[4][D];
+    const int lane = (int) threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane((int) threadIdx.x >> 6);
+    const int64_t item = (int64_t) blockIdx.x * 4 + wave;
+    const int nc = a.n_chunks;
+    if (item >= (int64_t) nc * a.hq * a.n_seq) return;
+    const int c = (int) (item % nc);
+    const int hs = (int) (item / nc);  // seq * hq + head
+    const int head = hs % a.hq, seq = hs / a.hq;
+    const int kvh = head / (a.hq / a.hkv);
+    const int kv_seq = seq / a.rk3;
+    const int clen = min(kFaChunk, a.n_kv - c * kFaChunk);
+    const int64_t prow = hs;  // partial row: tile (seq, kvh) row head % g
+    const int pos = c * kFaChunk + lane;
+
+    // the query (f16-rounded) and the mask first
+    {
+        const float * qp = (const float *) (a.q + (int64_t) head * a.q_nb2 + (int64_t) seq * a.q_nb3);
+        for (int d = lane; d < D; d += 64) s_q[wave][d] = round_to_half(qp[d]);
+    }
+    float mv = -INFINITY;
+    if (lane < clen) {
+        mv = 0.0f;
+        if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
+    }
+    const bool live = mv != -INFINITY;
+    if (__ballot(live) == 0) {
+        if (lane == 0) {
+            part_m[prow * nc + c] = -INFINITY;
+            part_l[prow * nc + c] = 0.0;
+        }
+        return;
+    }
+    // positions past the span read the chunk's last valid row (always in
+    // bounds, loads stay unconditional); they are masked
+    const int lp = min(lane, clen - 1);
+    const char * kb = a.k + (int64_t) kvh * a.k_nb2 + (int64_t) kv_seq * a.k_nb3 +
+                      (int64_t) (c * kFaChunk + lp) * a.k_nb1;
+    const char * vb = a.v + (int64_t) kvh * a.v_nb2 + (int64_t) kv_seq * a.v_nb3 + (int64_t) c * kFaChunk * a.v_nb1;
+    const int vs = (int) a.v_nb1, loff = lane * DL * 2;
+    uint4 kr[D / 8];
+#pragma unroll
+    for (int u = 0; u < D / 8; u++) kr[u] = *(const uint4 *) (kb + 16 * u);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // scores: lane = position; products of two halves are exact in f32
+    double sc = 0.0;
+#pragma unroll
+    for (int u = 0; u < D / 8; u++) {
+        float kf[8];
+        unpack8(kr[u], kf);
+        const float4 q0 = *(const float4 *) &s_q[wave][8 * u];
+        const float4 q1 = *(const float4 *) &s_q[wave][8 * u + 4];
+        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) sc += (double) (kf[i] * qv[i]);
+    }
+    // V once the scores are done; its latency overlaps the chunk softmax
+    uint32_t vr[kFaChunk];
+#pragma unroll
+    for (int j = 0; j < kFaChunk; j++) {
+        const int off = (j < clen ? j : clen - 1) * vs + loff;
+        if (DL == 2) vr[j] = *(const uint32_t *) (vb + off);
+        else vr[j] = (uint32_t) *(const uint16_t *) (vb + off);
+    }
+    const float sv = live ? (float) sc * a.scale + mv : -INFINITY;
+    const float m = wave_max(sv);
+    const float p = sv == -INFINITY ? 0.0f : expf_det(sv - m);
+    // P * V: lane = dims; the sum of p in position order alongside
+    double acc[DL], l = 0.0;
+#pragma unroll
+    for (int i = 0; i < DL; i++) acc[i] = 0.0;
+#pragma unroll
+    for (int j = 0; j < kFaChunk; j++) {
+        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
+        l += (double) pj;
+        if (pj != 0.0f) {  // masked slots may hold anything, even NaN
+            acc[0] = fma((double) pj, (double) half_bits_to_float((uint16_t) (vr[j] & 0xFFFF)), acc[0]);
+            if (DL == 2) acc[DL - 1] = fma((double) pj, (double) half_bits_to_float((uint16_t) (vr[j] >> 16)), acc[DL - 1]);
+        }
+    }
+    double * pa = part_acc + (prow * nc + c) * D + lane * DL;
+#pragma unroll
+    for (int i = 0; i < DL; i++) pa[i] = acc[i];
+    if (lane == 0) {
+        part_m[prow * nc + c] = m;
+        part_l[prow * nc + c] = l;
     }
 }
 
@@ -437,7 +554,9 @@ void fattn_plan(fattn_args & a, int n_cu) {
     const int64_t tiles = fa_tiles(a);
     const int64_t part_bytes = tiles * a.rows * a.n_chunks * (12 + 8 * (int64_t) a.d);
     // split the KV span over workgroups when the tiles alone leave CUs idle
-    a.split = tiles < 2LL * n_cu && a.n_chunks <= kFaMaxChunks && part_bytes <= (256LL << 20);
+    const bool fits = a.n_chunks <= kFaMaxChunks && part_bytes <= (256LL << 20);
+    if (fits && a.tq == 1) a.split = 2;  // wave per (chunk, query head)
+    else a.split = fits && tiles < 2LL * n_cu ? 1 : 0;
 }
 
 bool fattn_supported(int d, int hq, int hkv) {
@@ -451,6 +570,7 @@ bool fattn_fits(const fattn_args & a) { return a.n_chunks <= kFaMaxChunks; }
 
 template <int D, int R>
 static void launch_fa(const fattn_args & a, void * scratch, float * out, hipStream_t s) {
+    static_assert(R >= 1 && R <= kFaMaxRows, "tile rows");
     if (a.split) {
         const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
         float * pm = (float *) scratch;
@@ -458,8 +578,13 @@ static void launch_fa(const fattn_args & a, void * scratch, float * out, hipStre
         p = (char *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
         double * pl = (double *) p;
         double * pa = pl + prows;
-        const dim3 grid((unsigned) a.n_chunks, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
-        hipLaunchKernelGGL((k_fattn_split<D, R>), grid, dim3(kFaThreads), 0, s, a, pm, pl, pa);
+        if (a.split == 2) {
+            const int64_t items = (int64_t) a.n_chunks * a.hq * a.n_seq;
+            hipLaunchKernelGGL((k_fattn_decode<D>), dim3((unsigned) ((items + 3) / 4)), dim3(256), 0, s, a, pm, pl, pa);
+        } else {
+            const dim3 grid((unsigned) a.n_chunks, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
+            hipLaunchKernelGGL((k_fattn_split<D, R>), grid, dim3(kFaThreads), 0, s, a, pm, pl, pa);
+        }
         const dim3 cgrid(1u, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
         hipLaunchKernelGGL((k_fattn_combine<D, R>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out);
     } else {

@@ -55,7 +55,8 @@ struct fattn_args {
     int rows;      // tile rows = tq * (hq / hkv)
     int q_tiles;
     int n_chunks;  // 64-position KV chunks
-    int split;     // chunks spread over workgroups (partials, then a combine launch)
+    int split;     // 0: one workgroup per tile; 1: chunks over workgroups; 2: one wave per chunk
+                   // (1 and 2 write partials that a combine launch reduces)
     // optional quantization of the output for the consuming MUL_MAT:
     // -1 none, GGML_TYPE_Q8_0 or GGML_TYPE_Q4_K (Q8_K activations)
     int qtype;
