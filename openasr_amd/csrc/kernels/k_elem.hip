@@ -196,64 +196,78 @@ __global__ __launch_bounds__(256) void k_norm(tview d, tview a, int mode, float 
 }
 
 // Rows whose width is a multiple of 256 with contiguous elements and 1-D
-// weight / bias vectors: lane l holds elements 256c + 4l .. +3 (16-byte
-// loads), so each 256-element chunk is laid out as the activation quantizers
-// expect and the normalised row can also be written as the quantized
-// activations of the MUL_MAT that consumes it (qtype: -1 none, Q8_0 or Q4_K
-// for Q8_K). The f32 row is always written.
-template <int C>
+// weight / bias vectors: one workgroup per row, its W waves take the row's
+// 256-element chunks round-robin, lane l holding elements 256c + 4l .. +3
+// (16-byte loads) -- the layout the activation quantizers expect, so the
+// normalised row can also be written as the quantized activations of the
+// MUL_MAT that consumes it (qtype: -1 none, Q8_0, or Q4_K for Q8_K). The f32
+// row is always written. The waves' f64 partial sums are added in wave order.
+template <int C, int W>
 __global__ __launch_bounds__(256) void k_norm_rows(tview d, tview a, int mode, float eps, const float * __restrict__ wr,
-                                                   const float * __restrict__ br, int64_t rows, int qtype,
-                                                   act_buffers act) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
+                                                   const float * __restrict__ br, int qtype, act_buffers act) {
+    constexpr int CPW = C / W;  // chunks per wave
+    __shared__ double s_part[2][W];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row = blockIdx.x;
     const int64_t i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
     const float * x = (const float *) (a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3]);
     float * y = (float *) (d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]);
     constexpr int n = 256 * C;
-    float4 xv[C], wv[C], bv[C];
+    float4 xv[CPW], wv[CPW], bv[CPW];
 #pragma unroll
-    for (int c = 0; c < C; c++) {
-        const int i = 256 * c + 4 * lane;
-        xv[c] = *(const float4 *) (x + i);
-        wv[c] = wr ? *(const float4 *) (wr + i) : make_float4(1.f, 1.f, 1.f, 1.f);
-        bv[c] = br ? *(const float4 *) (br + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < CPW; k++) {
+        const int i = 256 * (wave + W * k) + 4 * lane;
+        xv[k] = *(const float4 *) (x + i);
+        wv[k] = wr ? *(const float4 *) (wr + i) : make_float4(1.f, 1.f, 1.f, 1.f);
+        bv[k] = br ? *(const float4 *) (br + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     float mean = 0.0f;
     if (mode == 1) {
         double s = 0.0;
 #pragma unroll
-        for (int c = 0; c < C; c++) s += (((double) xv[c].x + (double) xv[c].y) + (double) xv[c].z) + (double) xv[c].w;
-        mean = (float) (wave_sum_d(s) / (double) n);
+        for (int k = 0; k < CPW; k++) s += (((double) xv[k].x + (double) xv[k].y) + (double) xv[k].z) + (double) xv[k].w;
+        s = wave_sum_d(s);
+        if (lane == 0) s_part[0][wave] = s;
+        __syncthreads();
+        double t = 0.0;
+#pragma unroll
+        for (int w = 0; w < W; w++) t += s_part[0][w];
+        mean = (float) (t / (double) n);
     }
     double s2 = 0.0;
 #pragma unroll
-    for (int c = 0; c < C; c++) {
-        const float vx = xv[c].x - mean, vy = xv[c].y - mean, vz = xv[c].z - mean, vw = xv[c].w - mean;
+    for (int k = 0; k < CPW; k++) {
+        const float vx = xv[k].x - mean, vy = xv[k].y - mean, vz = xv[k].z - mean, vw = xv[k].w - mean;
         s2 += (((double) (vx * vx) + (double) (vy * vy)) + (double) (vz * vz)) + (double) (vw * vw);
     }
-    const float var = (float) (wave_sum_d(s2) / (double) n);
+    s2 = wave_sum_d(s2);
+    if (lane == 0) s_part[1][wave] = s2;
+    __syncthreads();
+    double t2 = 0.0;
+#pragma unroll
+    for (int w = 0; w < W; w++) t2 += s_part[1][w];
+    const float var = (float) (t2 / (double) n);
     const float scale = 1.0f / sqrtf(var + eps);
     const int64_t col = row;
 #pragma unroll
-    for (int c = 0; c < C; c++) {
+    for (int k = 0; k < CPW; k++) {
+        const int c = wave + W * k;
         float4 v;
-        v.x = (xv[c].x - mean) * scale;
-        v.y = (xv[c].y - mean) * scale;
-        v.z = (xv[c].z - mean) * scale;
-        v.w = (xv[c].w - mean) * scale;
+        v.x = (xv[k].x - mean) * scale;
+        v.y = (xv[k].y - mean) * scale;
+        v.z = (xv[k].z - mean) * scale;
+        v.w = (xv[k].w - mean) * scale;
         if (wr) {
-            v.x *= wv[c].x;
-            v.y *= wv[c].y;
-            v.z *= wv[c].z;
-            v.w *= wv[c].w;
+            v.x *= wv[k].x;
+            v.y *= wv[k].y;
+            v.z *= wv[k].z;
+            v.w *= wv[k].w;
         }
         if (br) {
-            v.x += bv[c].x;
-            v.y += bv[c].y;
-            v.z += bv[c].z;
-            v.w += bv[c].w;
+            v.x += bv[k].x;
+            v.y += bv[k].y;
+            v.z += bv[k].z;
+            v.w += bv[k].w;
         }
         const int e = 256 * c + 4 * lane;
         *(float4 *) (y + e) = v;
@@ -296,14 +310,15 @@ void launch_norm(const tview & d, const tview & a, int mode, float eps, const tv
         const float * bp = b ? (const float *) b->data : nullptr;
         const act_buffers ab = act ? *act : act_buffers{nullptr, nullptr, nullptr};
         const int qt = act ? qtype : -1;
+        const dim3 g1((unsigned) rows);
         switch (a.ne[0] / 256) {
-            case 1: hipLaunchKernelGGL(k_norm_rows<1>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
-            case 2: hipLaunchKernelGGL(k_norm_rows<2>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
-            case 4: hipLaunchKernelGGL(k_norm_rows<4>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
-            case 6: hipLaunchKernelGGL(k_norm_rows<6>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
-            case 8: hipLaunchKernelGGL(k_norm_rows<8>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
-            case 12: hipLaunchKernelGGL(k_norm_rows<12>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
-            default: hipLaunchKernelGGL(k_norm_rows<16>, grid, dim3(256), 0, s, d, a, mode, eps, wp, bp, rows, qt, ab); return;
+            case 1: hipLaunchKernelGGL((k_norm_rows<1, 1>), g1, dim3(64), 0, s, d, a, mode, eps, wp, bp, qt, ab); return;
+            case 2: hipLaunchKernelGGL((k_norm_rows<2, 2>), g1, dim3(128), 0, s, d, a, mode, eps, wp, bp, qt, ab); return;
+            case 4: hipLaunchKernelGGL((k_norm_rows<4, 4>), g1, dim3(256), 0, s, d, a, mode, eps, wp, bp, qt, ab); return;
+            case 6: hipLaunchKernelGGL((k_norm_rows<6, 2>), g1, dim3(128), 0, s, d, a, mode, eps, wp, bp, qt, ab); return;
+            case 8: hipLaunchKernelGGL((k_norm_rows<8, 4>), g1, dim3(256), 0, s, d, a, mode, eps, wp, bp, qt, ab); return;
+            case 12: hipLaunchKernelGGL((k_norm_rows<12, 4>), g1, dim3(256), 0, s, d, a, mode, eps, wp, bp, qt, ab); return;
+            default: hipLaunchKernelGGL((k_norm_rows<16, 4>), g1, dim3(256), 0, s, d, a, mode, eps, wp, bp, qt, ab); return;
         }
     }
     const int per = (int) ((a.ne[0] + 63) / 64);
@@ -322,38 +337,53 @@ void launch_norm(const tview & d, const tview & a, int mode, float eps, const tv
 // row, lane l holds elements l and l + 64 -- exactly the NEOX pair of
 // rotation index l -- so the row is normalised, scaled and rotated in
 // registers. Same arithmetic as k_norm followed by k_rope.
-__global__ __launch_bounds__(256) void k_rms_norm_rope128(tview d, tview a, float eps, const float * __restrict__ w,
-                                                          const int32_t * __restrict__ pos, float theta_scale,
-                                                          float freq_scale, float attn_factor, int64_t rows) {
+// blockIdx.y selects the job: the query and key rows of one layer share a
+// launch
+__global__ __launch_bounds__(256) void k_rms_norm_rope128(norm_rope_job j0, norm_rope_job j1) {
+    const norm_rope_job & j = blockIdx.y == 0 ? j0 : j1;
+    const tview & a = j.a;
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t) blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
+    if (row >= j.rows) return;
     const int64_t i1 = row % a.ne[1], i2 = (row / a.ne[1]) % a.ne[2], i3 = row / (a.ne[1] * a.ne[2]);
     const float * x = (const float *) (a.data + i1 * a.nb[1] + i2 * a.nb[2] + i3 * a.nb[3]);
-    float * y = (float *) (d.data + i1 * d.nb[1] + i2 * d.nb[2] + i3 * d.nb[3]);
+    float * y = (float *) (j.d.data + i1 * j.d.nb[1] + i2 * j.d.nb[2] + i3 * j.d.nb[3]);
     const float x0 = x[lane], x1 = x[lane + 64];
-    const float w0 = w[lane], w1 = w[lane + 64];
-    const float p = (float) pos[i2];
+    const float w0 = j.w[lane], w1 = j.w[lane + 64];
+    const float p = (float) j.pos[i2];
     const double s2 = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
     const float var = (float) (s2 / 128.0);
-    const float scale = 1.0f / sqrtf(var + eps);
+    const float scale = 1.0f / sqrtf(var + j.eps);
     const float v0 = (x0 * scale) * w0, v1 = (x1 * scale) * w1;
     float theta = p;
-    for (int k = 0; k < lane; k++) theta *= theta_scale;
+    for (int k = 0; k < lane; k++) theta *= j.theta_scale;
     float sn, c;
-    sincosf_det(freq_scale * theta, sn, c);
-    c *= attn_factor;
-    sn *= attn_factor;
+    sincosf_det(j.freq_scale * theta, sn, c);
+    c *= j.attn_factor;
+    sn *= j.attn_factor;
     y[lane] = v0 * c - v1 * sn;
     y[lane + 64] = v0 * sn + v1 * c;
 }
 
-void launch_rms_norm_rope128(const tview & d, const tview & a, float eps, const float * w, const int32_t * pos,
-                             float freq_base, float freq_scale, float attn_factor, hipStream_t s) {
-    const int64_t rows = a.ne[1] * a.ne[2] * a.ne[3];
-    const float theta_scale = powf(freq_base, -2.0f / 128.0f);
-    hipLaunchKernelGGL(k_rms_norm_rope128, dim3((unsigned) ((rows + 3) / 4)), dim3(256), 0, s, d, a, eps, w, pos,
-                       theta_scale, freq_scale, attn_factor, rows);
+void launch_rms_norm_rope128(const norm_rope_job & j0, const norm_rope_job * j1, hipStream_t s) {
+    const int64_t rows = j1 && j1->rows > j0.rows ? j1->rows : j0.rows;
+    hipLaunchKernelGGL(k_rms_norm_rope128, dim3((unsigned) ((rows + 3) / 4), j1 ? 2u : 1u), dim3(256), 0, s, j0,
+                       j1 ? *j1 : j0);
+}
+
+norm_rope_job make_norm_rope_job(const tview & d, const tview & a, float eps, const float * w, const int32_t * pos,
+                                 float freq_base, float freq_scale, float attn_factor) {
+    norm_rope_job j;
+    j.d = d;
+    j.a = a;
+    j.w = w;
+    j.pos = pos;
+    j.eps = eps;
+    j.theta_scale = powf(freq_base, -2.0f / 128.0f);
+    j.freq_scale = freq_scale;
+    j.attn_factor = attn_factor;
+    j.rows = a.ne[1] * a.ne[2] * a.ne[3];
+    return j;
 }
 
 // -------------------------------------------------------------- rope -----

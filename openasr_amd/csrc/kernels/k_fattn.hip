@@ -362,7 +362,9 @@ template <int D>
 __global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __restrict__ part_m,
                                                       double * __restrict__ part_l, double * __restrict__ part_acc) {
     constexpr int DL = D / 64;
+    constexpr int KU = D / 8;  // 16-byte pieces of a K row
     __shared__ __align__(16) float s_q[4][D];
+    __shared__ uint4 s_k[4][kFaChunk][KU + 1];  // one padded row per position: conflict-free row reads
     const int lane = (int) threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int) threadIdx.x >> 6);
     const int64_t item = (int64_t) blockIdx.x * 4 + wave;
@@ -395,19 +397,30 @@ __global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __re
         }
         return;
     }
-    // positions past the span read the chunk's last valid row (always in
-    // bounds, loads stay unconditional); they are masked
-    const int lp = min(lane, clen - 1);
-    const char * kb = a.k + (int64_t) kvh * a.k_nb2 + (int64_t) kv_seq * a.k_nb3 +
-                      (int64_t) (c * kFaChunk + lp) * a.k_nb1;
+    // K in wave-wide contiguous pieces (each load instruction covers whole
+    // rows), transposed through LDS so that lane p gets row p. Positions past
+    // the span read the chunk's last valid row (always in bounds, loads stay
+    // unconditional); they are masked.
+    const char * kc = a.k + (int64_t) kvh * a.k_nb2 + (int64_t) kv_seq * a.k_nb3 + (int64_t) c * kFaChunk * a.k_nb1;
     const char * vb = a.v + (int64_t) kvh * a.v_nb2 + (int64_t) kv_seq * a.v_nb3 + (int64_t) c * kFaChunk * a.v_nb1;
     const int vs = (int) a.v_nb1, loff = lane * DL * 2;
-    uint4 kr[D / 8];
+    uint4 kl[KU];
 #pragma unroll
-    for (int u = 0; u < D / 8; u++) kr[u] = *(const uint4 *) (kb + 16 * u);
+    for (int u = 0; u < KU; u++) {
+        const int t = u * 64 + lane, row = t / KU, col = t % KU;
+        kl[u] = *(const uint4 *) (kc + (int64_t) min(row, clen - 1) * a.k_nb1 + 16 * col);
+    }
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        const int t = u * 64 + lane;
+        s_k[wave][t / KU][t % KU] = kl[u];
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    uint4 kr[KU];
+#pragma unroll
+    for (int u = 0; u < KU; u++) kr[u] = s_k[wave][lane][u];
 
     // scores: lane = position; products of two halves are exact in f32
     double sc = 0.0;

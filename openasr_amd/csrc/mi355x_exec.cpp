@@ -264,6 +264,8 @@ struct planner {
         return it == index.end() || it->second < i;
     }
     bool plan_norm(int i, const ggml_tensor * t);
+    bool norm_rope_match(int i, const ggml_tensor * t, norm_rope_job & job, const ggml_tensor *& mul,
+                         const ggml_tensor *& rope) const;
     bool plan_unary(int i, const ggml_tensor * t);
     bool plan_binary(const ggml_tensor * t);
     bool plan_fattn(int i, const ggml_tensor * t);
@@ -359,7 +361,65 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
     return true;
 }
 
+// RMS_NORM -> MUL(w) -> full-width NEOX ROPE over 128-element rows, the
+// per-head QK-norm and rotary embedding of nn/decoder.rs:1937-1968: the job
+// and the nodes it covers (mul, rope), or false
+bool planner::norm_rope_match(int i, const ggml_tensor * t, norm_rope_job & job, const ggml_tensor *& mul,
+                              const ggml_tensor *& rope) const {
+    if (t->op != GGML_OP_RMS_NORM || t->ne[0] != 128 || !supports_op(be->dev, t)) return false;
+    mul = sole_consumer(t, i + 1);
+    if (!mul || mul->op != GGML_OP_MUL || mul->src[0] != t) return false;
+    const ggml_tensor * wt = mul->src[1];
+    if (wt->type != GGML_TYPE_F32 || wt->op != GGML_OP_NONE || !is_contiguous(wt) || wt->ne[0] != 128 ||
+        wt->ne[1] != 1 || wt->ne[2] != 1 || wt->ne[3] != 1)
+        return false;
+    rope = sole_consumer(mul, i + 1);
+    if (!rope || rope->op != GGML_OP_ROPE || rope->src[0] != mul || !supports_op(be->dev, rope) ||
+        rope->op_params[2] != GGML_ROPE_TYPE_NEOX || rope->op_params[1] != 128 || rope->nb[0] != 4)
+        return false;
+    const tview av = view_of(t->src[0]);
+    if (av.nb[0] != 4) return false;
+    job = make_norm_rope_job(make_view(rope), av, op_f32(t, 0), (const float *) wt->data,
+                             (const int32_t *) rope->src[1]->data, op_f32(rope, 5), op_f32(rope, 6), op_f32(rope, 8));
+    return true;
+}
+
 bool planner::plan_norm(int i, const ggml_tensor * t) {
+    {
+        norm_rope_job j0, j1;
+        const ggml_tensor *mul0, *rope0, *mul1, *rope1;
+        if (norm_rope_match(i, t, j0, mul0, rope0)) {
+            deferred[mul0] = mul0;
+            deferred[rope0] = rope0;
+            // the next planned node, if it is the same fusion over rows ready
+            // now (the key rows after the query rows), shares the launch
+            const ggml_tensor * t1 = nullptr;
+            int i1 = -1;
+            for (int j = i + 1; j < cg->n_nodes; j++) {
+                const ggml_tensor * n = cg->nodes[j];
+                if (is_view_op(n->op) || bypass.count(n) || deferred.count(n)) continue;
+                t1 = n;
+                i1 = j;
+                break;
+            }
+            bool pair = t1 && norm_rope_match(i1, t1, j1, mul1, rope1);
+            if (pair) {
+                const ggml_tensor * src = root_of(t1->src[0]);
+                auto bp = bypass.find(src);
+                if (bp != bypass.end()) src = root_of(bp->second);
+                pair = ready_before(src, i) && src != rope0 && src != mul0;
+            }
+            if (pair) {
+                deferred[t1] = t1;
+                deferred[mul1] = mul1;
+                deferred[rope1] = rope1;
+                add_step([=](hipStream_t s) { launch_rms_norm_rope128(j0, &j1, s); }, rope1, "rms_norm_rope");
+            } else {
+                add_step([=](hipStream_t s) { launch_rms_norm_rope128(j0, nullptr, s); }, rope0, "rms_norm_rope");
+            }
+            return true;
+        }
+    }
     const int mode = t->op == GGML_OP_RMS_NORM ? 0 : 1;
     const float eps = op_f32(t, 0);
     const ggml_tensor * out = t;
@@ -387,22 +447,6 @@ bool planner::plan_norm(int i, const ggml_tensor * t) {
     const tview dv = make_view(out), av = view_of(t->src[0]);
     const bool hw = wt != nullptr, hb = bt != nullptr;
     const tview wv = hw ? make_view(wt) : tview{}, bv = hb ? make_view(bt) : tview{};
-    // RMSNorm * w feeding a full-width NEOX RoPE over 128-element rows: one
-    // kernel normalises and rotates each row
-    const ggml_tensor * rope = (mode == 0 && hw && !hb) ? sole_consumer(out, i + 1) : nullptr;
-    if (rope && rope->op == GGML_OP_ROPE && rope->src[0] == out && supports_op(be->dev, rope) &&
-        rope->op_params[2] == GGML_ROPE_TYPE_NEOX && rope->op_params[1] == 128 && out->ne[0] == 128 &&
-        is_contiguous(wt) && wt->ne[1] == 1 && wt->ne[2] == 1 && wt->ne[3] == 1 && av.nb[0] == 4 &&
-        rope->nb[0] == 4) {
-        const tview rv = make_view(rope);
-        const float * wp = (const float *) wt->data;
-        const int32_t * pos = (const int32_t *) rope->src[1]->data;
-        const float fb = op_f32(rope, 5), fs = op_f32(rope, 6), af = op_f32(rope, 8);
-        deferred[rope] = rope;
-        add_step([=](hipStream_t s) { launch_rms_norm_rope128(rv, av, eps, wp, pos, fb, fs, af, s); }, rope,
-                 "rms_norm_rope");
-        return true;
-    }
     // when only quantized MUL_MATs read the result, the norm kernel also
     // writes their quantized activations (they then skip their quantize step)
     int qt = quant_consumers(out, i + 1);
@@ -411,7 +455,7 @@ bool planner::plan_norm(int i, const ggml_tensor * t) {
     if (qt >= 0) act_need = std::max(act_need, act_bytes(qt, K, N));
     backend_state * b = be;
     add_step(
-[=](hipStream_t s) {
+        [=](hipStream_t s) {
             act_buffers ab{nullptr, nullptr, nullptr};
             if (qt >= 0) ab = act_carve(qt, act_base(b), K, N);
             launch_norm(dv, av, mode, eps, hw ? &wv : nullptr, hb ? &bv : nullptr, s, qt, qt >= 0 ? &ab : nullptr);

@@ -84,9 +84,18 @@ void launch_rope(const tview & d, const tview & a, const int32_t * pos, int n_di
 void launch_set_rows(const tview & dst, int dtype, const tview & src, const tview & idx, int idx_is_i64,
                      hipStream_t s, int n_cu, const tview * dst2 = nullptr, int dtype2 = 0,
                      const tview * src2 = nullptr);
-// RMSNorm * w then RoPE NEOX on rows of exactly 128 elements (n_dims 128)
-void launch_rms_norm_rope128(const tview & d, const tview & a, float eps, const float * w, const int32_t * pos,
-                             float freq_base, float freq_scale, float attn_factor, hipStream_t s);
+// RMSNorm * w then RoPE NEOX on rows of exactly 128 elements (n_dims 128);
+// an optional second job (the key rows after the query rows) shares the launch
+struct norm_rope_job {
+    tview d, a;
+    const float * w;
+    const int32_t * pos;
+    float eps, theta_scale, freq_scale, attn_factor;
+    int64_t rows;
+};
+norm_rope_job make_norm_rope_job(const tview & d, const tview & a, float eps, const float * w, const int32_t * pos,
+                                 float freq_base, float freq_scale, float attn_factor);
+void launch_rms_norm_rope128(const norm_rope_job & j0, const norm_rope_job * j1, hipStream_t s);
 void launch_get_rows(const tview & dst, const tview & src, int stype, const tview & idx, hipStream_t s, int n_cu);
 void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStream_t s, int n_cu);
 void launch_soft_max(const tview & d, const tview & a, const tview * mask, float scale, hipStream_t s);
