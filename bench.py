@@ -49,6 +49,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile-iters", type=int, default=20)
+    p.add_argument("--sweep", action="store_true", help="per-kernel sweep of mul_mat and flash_attn_ext shapes")
+    p.add_argument("--sweep-reps", type=int, default=20)
     return p.parse_args()
 
 
@@ -164,8 +166,108 @@ def cpu_baseline(w, wl, sess, tokens, seconds: float):
                       f"threads) continuing from the device KV state at position {int(r.pos.min()) - n}"}
 
 
+# ------------------------------------------------------------ kernel sweep --
+
+MFMA_INT8_PEAK = 5000.0  # TFLOP/s-equivalent (int8 dense, published)
+ROTATE_BYTES = 640 << 20  # rotate operands past the 256 MB last-level cache
+
+
+def _timed_graph(G, backend, reps: int) -> float:
+    """seconds per compute of an allocated graph, after eager + capture runs"""
+    for _ in range(3):
+        if G.compute(backend) != 0:
+            raise RuntimeError("graph compute failed")
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        G.compute(backend)
+    return (time.perf_counter() - t0) / reps
+
+
+def sweep_mul_mat(plugin, g, M, K, wtype, N, reps):
+    bpw = 144 / 256 if wtype == g.Q4_K else 34 / 32
+    wbytes = M * K * bpw
+    copies = max(1, min(2048, int(ROTATE_BYTES // wbytes)))
+    copies = max(1, min(copies, int((1 << 30) // (M * N * 4))))
+    w = g.synth_normal(2024, 1, M * K, 0.0, 0.02).reshape(M, K)
+    wq = g.quantize(wtype, w)
+    x = g.synth_normal(2025, 2, K * N).reshape(N, K)
+    G = g.Graph(n_tensors=4 * copies + 16, graph_size=4 * copies + 64)
+    X = G.new(g.F32, K, N)
+    Ws = [G.new(wtype, K, M, weight=True) for _ in range(copies)]
+    outs = [G.lib.ggml_mul_mat(G.ctx, W, X) for W in Ws]
+    G.build(*outs)
+    G.allocate(plugin.buft)
+    for W in Ws:
+        G.set(W, wq)
+    G.set(X, x)
+    dt = _timed_graph(G, plugin.backend, reps) / copies
+    G.free()
+    alg = wbytes + (K * N if N <= 16 else 4 * K * N) + 4 * M * N
+    return dict(op="mul_mat", type=g.TYPE_NAMES[wtype], M=M, K=K, N=N, copies=copies, us=dt * 1e6,
+                gbs=alg / dt / 1e9, frac_hbm=alg / dt / 1e9 / HBM_PEAK_GBS,
+                tops=2.0 * M * K * N / dt / 1e12)
+
+
+def sweep_fattn(plugin, g, n_kv, n_q, reps, d=128, hq=16, hkv=8):
+    kv_bytes = 2 * n_kv * hkv * d * 2
+    copies = max(1, min(256, int(ROTATE_BYTES // kv_bytes)))
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((1, hq, n_q, d)).astype(np.float32)
+    k = rng.standard_normal((1, hkv, n_kv, d)).astype(np.float16).view(np.uint16)
+    v = rng.standard_normal((1, hkv, n_kv, d)).astype(np.float16).view(np.uint16)
+    mask = np.zeros((1, n_q, n_kv), np.float16)
+    for i in range(n_q):  # the last n_q positions are causal
+        mask[0, i, n_kv - n_q + i + 1:] = -np.inf
+    G = g.Graph(n_tensors=4 * copies + 16, graph_size=2 * copies + 64)
+    Q = G.new(g.F32, d, n_q, hq, 1)
+    Mk = G.new(g.F16, n_kv, n_q, 1, 1)
+    Ks = [G.new(g.F16, d, n_kv, hkv, 1, weight=True) for _ in range(copies)]
+    Vs = [G.new(g.F16, d, n_kv, hkv, 1, weight=True) for _ in range(copies)]
+    outs = [G.lib.ggml_flash_attn_ext(G.ctx, Q, Ks[i], Vs[i], Mk, 1.0 / np.sqrt(d), 0.0, 0.0) for i in range(copies)]
+    G.build(*outs)
+    G.allocate(plugin.buft)
+    for i in range(copies):
+        G.set(Ks[i], k)
+        G.set(Vs[i], v)
+    G.set(Q, q)
+    G.set(Mk, mask.view(np.uint16))
+    dt = _timed_graph(G, plugin.backend, reps) / copies
+    G.free()
+    alg = kv_bytes + 2 * hq * n_q * d * 4 + n_q * n_kv * 2
+    return dict(op="flash_attn_ext", D=d, hq=hq, hkv=hkv, n_kv=n_kv, n_q=n_q, copies=copies, us=dt * 1e6,
+                gbs=alg / dt / 1e9, frac_hbm=alg / dt / 1e9 / HBM_PEAK_GBS,
+                tflops=4.0 * hq * n_q * n_kv * d / dt / 1e12)
+
+
+def run_sweep(reps: int) -> int:
+    """mul_mat on Q8_0/Q4_K weights M x K in {1024^2, 3072x1024, 1024x3072,
+    151936x1024} for N in {1, 8, 64, 512}, and flash_attn_ext (16 query /
+    8 kv heads, D 128, f16 KV of {512, 2048, 8192} positions, q_len {1, 64}).
+    Operands are rotated over copies totalling more than the 256 MB cache, so
+    the rates are HBM rates. One JSON line per case."""
+    from openasr_amd import ggml as g
+
+    plugin = g.plugin()
+    for wtype in (g.Q8_0, g.Q4_K):
+        for M, K in ((1024, 1024), (3072, 1024), (1024, 3072), (151936, 1024)):
+            for N in (1, 8, 64, 512):
+                r = sweep_mul_mat(plugin, g, M, K, wtype, N, reps)
+                log(f"[sweep] mul_mat {r['type']:>4} {M:>6}x{K:<5} N={N:<4} {r['us']:9.2f} us  "
+                    f"{r['gbs']:8.1f} GB/s ({r['frac_hbm']:.1%} HBM)  {r['tops']:7.2f} TOP/s")
+                print(json.dumps(r), flush=True)
+    for n_kv in (512, 2048, 8192):
+        for n_q in (1, 64):
+            r = sweep_fattn(plugin, g, n_kv, n_q, reps)
+            log(f"[sweep] flash_attn_ext kv={n_kv:<5} q={n_q:<3} {r['us']:9.2f} us  {r['gbs']:8.1f} GB/s "
+                f"({r['frac_hbm']:.1%} HBM)  {r['tflops']:7.2f} TFLOP/s")
+            print(json.dumps(r), flush=True)
+    return 0
+
+
 def main() -> int:
     a = parse()
+    if a.sweep:
+        return run_sweep(a.sweep_reps)
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU per process (asked for {a.gpus}); the decoder path has no "
               "multi-GPU collectives", file=sys.stderr)

@@ -307,6 +307,17 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t prow = (int64_t) t.gti * R;
     const int nc = a.n_chunks;
+    // every partial is requested before any is used: one memory round trip
+    // (when each thread owns at most one output element)
+    constexpr int NE = (R * D + kFaThreads - 1) / kFaThreads;
+    double pv[16];
+    const bool small = NE == 1 && nc <= 16;
+    if (small) {
+        const int r = tid / D, d = tid % D;
+#pragma unroll
+        for (int k = 0; k < 16; k++)
+            pv[k] = tid < t.nrows * D && k < nc ? part_acc[((prow + r) * nc + k) * D + d] : 0.0;
+    }
     for (int r = wave; r < t.nrows; r += 4) {
         float M = -INFINITY;
         for (int i = lane; i < nc; i += 64) M = fmaxf(M, part_m[(prow + r) * nc + i]);
@@ -326,17 +337,27 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
         s_L[tid] = L;
     }
     __syncthreads();
-    for (int idx = tid; idx < t.nrows * D; idx += kFaThreads) {
-        const int r = idx / D, d = idx % D;
-        const double * pa = part_acc + (prow + r) * nc * D + d;
-        double O = 0.0;
-        for (int c0 = 0; c0 < nc; c0 += 16) {
-            double v[16];
 #pragma unroll
-            for (int k = 0; k < 16; k++) v[k] = c0 + k < nc ? pa[(int64_t) (c0 + k) * D] : 0.0;
+    for (int e = 0; e < NE; e++) {
+        const int idx = tid + e * kFaThreads;
+        if (idx >= t.nrows * D) continue;
+        const int r = idx / D, d = idx % D;
+        double O = 0.0;
+        if (small) {
 #pragma unroll
             for (int k = 0; k < 16; k++) {
-                if (c0 + k < nc && s_w[r][c0 + k] != 0.0) O += s_w[r][c0 + k] * v[k];
+                if (k < nc && s_w[r][k] != 0.0) O += s_w[r][k] * pv[k];
+            }
+        } else {
+            const double * pa = part_acc + (prow + r) * nc * D + d;
+            for (int c0 = 0; c0 < nc; c0 += 16) {
+                double v[16];
+#pragma unroll
+                for (int k = 0; k < 16; k++) v[k] = c0 + k < nc ? pa[(int64_t) (c0 + k) * D] : 0.0;
+#pragma unroll
+                for (int k = 0; k < 16; k++) {
+                    if (c0 + k < nc && s_w[r][c0 + k] != 0.0) O += s_w[r][c0 + k] * v[k];
+                }
             }
         }
         const float o = s_L[r] == 0.0 ? 0.0f : (float) (O / s_L[r]);
@@ -352,8 +373,8 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
 // Decode form (one query position): one wave per (chunk, query head,
 // sequence). For the scores lane p owns KV position p of the chunk (its whole
 // K row, the query broadcast from LDS); for P*V lane l owns dims D/64*l.. of
-// every position (V is loaded once the scores are done), the chunk's p
-// values broadcast lane by lane. Every sum runs in the CPU reference's order
+// every position, the chunk's p values broadcast lane by lane. After the
+// mask, K and V are requested in one burst. Every sum runs in the CPU reference's order
 // (dimensions, then positions) and the p*v products are exact in f64, so
 // fused multiply-adds change nothing: the chunk partials are bit-identical. The query heads of one kv head
 // read the same K/V rows at the same time, so the second read comes from
@@ -415,6 +436,14 @@ __global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __re
         const int t = u * 64 + lane;
         s_k[wave][t / KU][t % KU] = kl[u];
     }
+    // V in the same burst (lane = dims of every position)
+    uint32_t vr[kFaChunk];
+#pragma unroll
+    for (int j = 0; j < kFaChunk; j++) {
+        const int off = (j < clen ? j : clen - 1) * vs + loff;
+        if (DL == 2) vr[j] = *(const uint32_t *) (vb + off);
+        else vr[j] = (uint32_t) *(const uint16_t *) (vb + off);
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -433,14 +462,6 @@ __global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __re
         const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
 #pragma unroll
         for (int i = 0; i < 8; i++) sc += (double) (kf[i] * qv[i]);
-    }
-    // V once the scores are done; its latency overlaps the chunk softmax
-    uint32_t vr[kFaChunk];
-#pragma unroll
-    for (int j = 0; j < kFaChunk; j++) {
-        const int off = (j < clen ? j : clen - 1) * vs + loff;
-        if (DL == 2) vr[j] = *(const uint32_t *) (vb + off);
-        else vr[j] = (uint32_t) *(const uint16_t *) (vb + off);
     }
     const float sv = live ? (float) sc * a.scale + mv : -INFINITY;
     const float m = wave_max(sv);
