@@ -51,6 +51,8 @@ def parse():
     p.add_argument("--profile-iters", type=int, default=20)
     p.add_argument("--sweep", action="store_true", help="per-kernel sweep of mul_mat and flash_attn_ext shapes")
     p.add_argument("--sweep-reps", type=int, default=20)
+    p.add_argument("--traffic-probe", action="store_true",
+                   help="fixed short program for rocprofv3 --pmc runs (copy calibration + two decode steps)")
     return p.parse_args()
 
 
@@ -121,7 +123,7 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
     gemv_gbs = alg_bytes / (gemv_ms * 1e-3) / 1e9
     eager_ms = sum(ms for _, ms in prof)
     breakdown = {k: {"ms": round(v[0], 4), "launches": v[1]} for k, v in sorted(kern.items(), key=lambda kv: -kv[1][0])}
-    log(f"[bench] eager step {eager_ms:.3f} ms over {len(prof)} launch groups; {gemv_key}: {gemv_n} launches, "
+    log(f"[bench] profiled step {eager_ms:.3f} ms over {len(prof)} launch groups; {gemv_key}: {gemv_n} launches, "
         f"{gemv_ms:.3f} ms, {gemv_gbs:.0f} GB/s = {gemv_gbs / HBM_PEAK_GBS:.1%} of HBM peak")
     for k, v in breakdown.items():
         log(f"    {k:>16}: {v['ms']:.4f} ms over {v['launches']} launches")
@@ -264,10 +266,48 @@ def run_sweep(reps: int) -> int:
     return 0
 
 
+def run_traffic_probe(workload: str) -> int:
+    """A short fixed program for hardware-counter runs (rocprofv3 --pmc):
+    a 256 MiB f32 copy through the backend (known bytes: the counters' scale)
+    followed by two eager decode steps of the workload. Prints nothing but
+    progress; the counters come from the profiler's output."""
+    from openasr_amd import decoders as D
+    from openasr_amd import ggml as g
+
+    plugin = g.plugin()
+    n = 64 << 20  # floats
+    G = g.Graph(n_tensors=8, graph_size=16)
+    src = G.new(g.F32, n)
+    dst = G.lib.ggml_cont(G.ctx, G.lib.ggml_reshape_2d(G.ctx, src, 1 << 20, 64))
+    G.build(dst)
+    G.allocate(plugin.buft)
+    G.set(src, np.zeros(n, np.float32))
+    assert G.compute(plugin.backend) == 0
+    G.free()
+    log("[probe] copy of 256 MiB done")
+    wl = D.WORKLOADS[workload]
+    w = D.QwenWeights(wl.wtype, seed=1234, **wl.shape)
+    model = D.QwenModel(w, plugin.backend)
+    sess = model.session(wl.n_seq, wl.max_positions)
+    emb, prompt = D.workload_inputs(wl, seed=77)
+    sess.prefill_embeddings(emb)
+    cur = sess.prefill_tokens(prompt)
+    log("[probe] prefill done")
+    for _ in range(2):
+        cur = sess.step(cur)
+    log("[probe] two decode steps done")
+    sess.free()
+    model.free()
+    w.free()
+    return 0
+
+
 def main() -> int:
     a = parse()
     if a.sweep:
         return run_sweep(a.sweep_reps)
+    if a.traffic_probe:
+        return run_traffic_probe(a.workload)
     if a.gpus != 1:
         print(f"bench.py: this build runs on one GPU per process (asked for {a.gpus}); the decoder path has no "
               "multi-GPU collectives", file=sys.stderr)
@@ -282,6 +322,12 @@ def main() -> int:
         b1 = {"tokens_per_s": round(r1["tok_s"], 1), "ms_per_step": round(r1["ms_per_step"], 4),
               "mul_mat_q8_0_gbs": round(r1["gemv_gbs"], 1)}
     frac = main_r["gemv_gbs"] / HBM_PEAK_GBS
+    # measured HBM bytes per GEMV launch (rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # runs of `bench.py --traffic-probe`, summarised by openasr_amd.pmc)
+    traffic = None
+    tpath = ROOT / "profiles" / f"gemv_traffic_{a.workload}.json"
+    if tpath.exists():
+        traffic = round(json.loads(tpath.read_text())["decode_step"]["gemv_hbm_bytes_per_launch"], 1)
     out = {
         "metric": "decode tokens/sec @ batch 8 (Qwen3-0.6B-shaped Q4_K decoder); quantized mul_mat HBM GB/s as % of peak",
         "value": round(main_r["tok_s"], 1),
@@ -299,9 +345,12 @@ def main() -> int:
                    "head_dim 128, ffn 3072, vocab 151936)", "global_batch": 8, "seq_len": 1024,
                    "prefill_positions": main_r["n_prefill"], "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(main_r["gemv_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(frac, 4), "traffic": None,
-                     "kernel": "k_mmv_q4_K (all GEMV launches of one decode step, algorithmic weight bytes / "
-                               "summed launch time)"},
+                     "frac": round(frac, 4), "traffic": traffic,
+                     "alg_bytes_per_launch": round(main_r["weight_bytes"] / max(1, main_r["gemv_launches"]), 1),
+                     "launches": main_r["gemv_launches"],
+                     "kernel": "k_gemv_q4_K: the quantized GEMV launches of one decode step (per layer QKV, "
+                               "o-proj+residual, gate+up SwiGLU, down+residual; lm_head), algorithmic bytes "
+                               "(weights + int8 activations + f32 outputs) / summed launch time"},
         "cpu_baseline": main_r["cpu"],
         "prefill_ms": round(main_r["prefill_ms"], 2),
         "eager_step_ms": round(main_r["eager_step_ms"], 4),

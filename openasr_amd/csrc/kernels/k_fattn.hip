@@ -391,10 +391,15 @@ __global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __re
     const int64_t item = (int64_t) blockIdx.x * 4 + wave;
     const int nc = a.n_chunks;
     if (item >= (int64_t) nc * a.hq * a.n_seq) return;
-    const int c = (int) (item % nc);
-    const int hs = (int) (item / nc);  // seq * hq + head
-    const int head = hs % a.hq, seq = hs / a.hq;
-    const int kvh = head / (a.hq / a.hkv);
+    // the g query heads of one kv head are adjacent waves of a workgroup, so
+    // the second read of a chunk's K/V rows hits the CU's caches
+    const int g = a.hq / a.hkv;
+    const int hh = (int) (item % g);
+    const int c = (int) ((item / g) % nc);
+    const int kt = (int) (item / ((int64_t) g * nc));  // seq * hkv + kvh
+    const int kvh = kt % a.hkv, seq = kt / a.hkv;
+    const int head = kvh * g + hh;
+    const int hs = seq * a.hq + head;
     const int kv_seq = seq / a.rk3;
     const int clen = min(kFaChunk, a.n_kv - c * kFaChunk);
     const int64_t prow = hs;  // partial row: tile (seq, kvh) row head % g

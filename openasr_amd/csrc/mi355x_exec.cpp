@@ -847,19 +847,62 @@ int profile_graph(backend_state * be, ggml_cgraph * cg, int iters, float * step_
     std::vector<hipEvent_t> ev((size_t) n + 1);
     for (auto & e : ev) MI_CHECK(hipEventCreate(&e));
     std::vector<double> acc((size_t) n, 0.0);
-    for (int it = 0; it < iters; it++) {
-        MI_CHECK(hipEventRecord(ev[0], be->stream));
-        for (int i = 0; i < n; i++) {
-            p.steps[(size_t) i].run(be->stream);
-            MI_CHECK(hipEventRecord(ev[(size_t) i + 1], be->stream));
+    // Preferred: the launch groups captured into a HIP graph with an event
+    // record after each, replayed as the decode loop replays its graph, so a
+    // group's time is its kernels' run time without host launch gaps.
+    bool replayed = false;
+    if (be->use_graphs && !be->abort_cb) {
+        hipGraph_t g = nullptr;
+        hipGraphExec_t ge = nullptr;
+        hipError_t e = hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal);
+        if (e == hipSuccess) {
+            hipError_t er = hipEventRecord(ev[0], be->stream);
+            for (int i = 0; i < n && er == hipSuccess; i++) {
+                p.steps[(size_t) i].run(be->stream);
+                er = hipEventRecord(ev[(size_t) i + 1], be->stream);
+            }
+            e = hipStreamEndCapture(be->stream, &g);
+            if (er != hipSuccess) e = er;
         }
-        MI_CHECK(hipStreamSynchronize(be->stream));
-        for (int i = 0; i < n; i++) {
-            float ms = 0.0f;
-            MI_CHECK(hipEventElapsedTime(&ms, ev[(size_t) i], ev[(size_t) i + 1]));
-            acc[(size_t) i] += ms;
+        if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
+        std::vector<double> tmp((size_t) n, 0.0);
+        for (int it = 0; it < iters && e == hipSuccess; it++) {
+            e = hipGraphLaunch(ge, be->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
+            for (int i = 0; i < n && e == hipSuccess; i++) {
+                float ms = 0.0f;
+                e = hipEventElapsedTime(&ms, ev[(size_t) i], ev[(size_t) i + 1]);
+                tmp[(size_t) i] += ms;
+            }
+        }
+        if (ge) hipGraphExecDestroy(ge);
+        if (g) hipGraphDestroy(g);
+        if (e == hipSuccess) {
+            acc = tmp;
+            replayed = true;
+        } else {
+            std::fprintf(stderr, "mi355x: event timing under graph replay unavailable (%s)\n", hipGetErrorString(e));
+            (void) hipGetLastError();
+            (void) hipStreamSynchronize(be->stream);
         }
     }
+    if (!replayed) {
+        for (int it = 0; it < iters; it++) {
+            MI_CHECK(hipEventRecord(ev[0], be->stream));
+            for (int i = 0; i < n; i++) {
+                p.steps[(size_t) i].run(be->stream);
+                MI_CHECK(hipEventRecord(ev[(size_t) i + 1], be->stream));
+            }
+            MI_CHECK(hipStreamSynchronize(be->stream));
+            for (int i = 0; i < n; i++) {
+                float ms = 0.0f;
+                MI_CHECK(hipEventElapsedTime(&ms, ev[(size_t) i], ev[(size_t) i + 1]));
+                acc[(size_t) i] += ms;
+            }
+        }
+    }
+    std::fprintf(stderr, "mi355x: profiled %d launch groups x %d iterations (%s)\n", n, iters,
+                 replayed ? "HIP-graph replay with event nodes" : "eager launches");
     for (auto & e : ev) MI_CHECK(hipEventDestroy(e));
     for (int i = 0; i < n && i < max_steps; i++) {
         if (step_ms) step_ms[i] = (float) (acc[(size_t) i] / (iters > 0 ? iters : 1));
