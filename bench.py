@@ -99,7 +99,8 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
     log(f"[bench] {steps} decode steps: {elapsed * 1e3 / steps:.3f} ms/step, {tok_s:.1f} tokens/s "
         f"(median step {np.median(step_ms):.3f} ms)")
 
-    # per-kernel breakdown of one decode step (eager launches, HIP events on the backend stream)
+    # per-launch-group times of one decode step: HIP events on the backend stream around each group,
+    # the groups queued behind a short spin so they run back to back
     prof = plugin.profile(sess.decode_graph(), profile_iters)
     kern = {}
     for lab, ms in prof:

@@ -286,6 +286,18 @@ __global__ __launch_bounds__(256) void k_norm_rows(tview d, tview a, int mode, f
 
 bool norm_supported(int64_t ne0) { return ne0 <= 64 * 64; }
 
+// measurement helper: occupies the stream for a bounded time (the loop ends
+// when the constant-rate wall clock has advanced by `ticks`)
+__global__ void k_spin(uint64_t ticks) {
+    const uint64_t t0 = wall_clock64();
+    while (wall_clock64() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
+void launch_spin_us(double us, int wall_clock_khz, hipStream_t s) {
+    const uint64_t ticks = (uint64_t) (us * (double) wall_clock_khz / 1000.0);
+    hipLaunchKernelGGL(k_spin, dim3(1), dim3(64), 0, s, ticks);
+}
+
 bool norm_rows_supported(const tview & d, const tview & a, const tview * w, const tview * b) {
     const int64_t n = a.ne[0];
     if (n % 256 != 0 || n / 256 > 16) return false;

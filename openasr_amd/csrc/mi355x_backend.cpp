@@ -387,6 +387,9 @@ static void init_devices() {
         device_state * dev = new device_state;
         dev->hip_id = i;
         dev->n_cu = p.multiProcessorCount;
+        int wc = 0;
+        if (hipDeviceGetAttribute(&wc, hipDeviceAttributeWallClockRate, i) == hipSuccess && wc > 0)
+            dev->wall_clock_khz = wc;
         dev->total_mem = p.totalGlobalMem;
         dev->arch = arch;
         dev->name = "ROCm" + std::to_string(r.devices.size());

@@ -289,7 +289,8 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         const int ncu = n_cu;
         char * dst = (char *) t->data;
         int64_t dst_nb1 = (int64_t) t->nb[1];
-        const bool wide = mmq_supported(wtype, M, K) && N > 16;
+        // the tile GEMM once the columns outgrow a few GEMV chunks (earlier for tall matrices)
+        const bool wide = mmq_supported(wtype, M, K) && N > 16 && (N > 64 || M >= 8192);
         const bool mfma = !wide && gemv_mfma_supported(wtype, M, K);
         // SwiGLU: MUL_MAT(gate, x) -> SILU -> MUL with MUL_MAT(up, x) of the
         // same shape becomes one launch over both matrices
@@ -845,64 +846,33 @@ int profile_graph(backend_state * be, ggml_cgraph * cg, int iters, float * step_
     if (!ensure_scratch(be, p.act_need, p.gen_need)) return -1;
     const int n = (int) p.steps.size();
     std::vector<hipEvent_t> ev((size_t) n + 1);
-    for (auto & e : ev) MI_CHECK(hipEventCreate(&e));
+    // timing events without the system-scope fence a default event record
+    // adds (it would lengthen every measured interval)
+    for (auto & e : ev) MI_CHECK(hipEventCreateWithFlags(&e, hipEventDisableSystemFence));
     std::vector<double> acc((size_t) n, 0.0);
-    // Preferred: the launch groups captured into a HIP graph with an event
-    // record after each, replayed as the decode loop replays its graph, so a
-    // group's time is its kernels' run time without host launch gaps.
-    bool replayed = false;
-    if (be->use_graphs && !be->abort_cb) {
-        hipGraph_t g = nullptr;
-        hipGraphExec_t ge = nullptr;
-        hipError_t e = hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal);
-        if (e == hipSuccess) {
-            hipError_t er = hipEventRecord(ev[0], be->stream);
-            for (int i = 0; i < n && er == hipSuccess; i++) {
-                p.steps[(size_t) i].run(be->stream);
-                er = hipEventRecord(ev[(size_t) i + 1], be->stream);
-            }
-            e = hipStreamEndCapture(be->stream, &g);
-            if (er != hipSuccess) e = er;
+    // Each iteration first launches a bounded spin kernel (a few ms of GPU
+    // wall clock) so that the host has enqueued every launch group and its
+    // event before the GPU reaches them: the groups then run back to back as
+    // in a graph replay, and an event interval is the group's own run time
+    // plus the command processor's dispatch, without host launch gaps.
+    const double spin_us = std::min(8000.0, 20.0 * n + 200.0);
+    for (int it = 0; it < iters; it++) {
+        launch_spin_us(spin_us, be->dev->wall_clock_khz, be->stream);
+        MI_CHECK(hipEventRecord(ev[0], be->stream));
+        for (int i = 0; i < n; i++) {
+            p.steps[(size_t) i].run(be->stream);
+            MI_CHECK(hipEventRecord(ev[(size_t) i + 1], be->stream));
         }
-        if (e == hipSuccess) e = hipGraphInstantiate(&ge, g, nullptr, nullptr, 0);
-        std::vector<double> tmp((size_t) n, 0.0);
-        for (int it = 0; it < iters && e == hipSuccess; it++) {
-            e = hipGraphLaunch(ge, be->stream);
-            if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
-            for (int i = 0; i < n && e == hipSuccess; i++) {
-                float ms = 0.0f;
-                e = hipEventElapsedTime(&ms, ev[(size_t) i], ev[(size_t) i + 1]);
-                tmp[(size_t) i] += ms;
-            }
-        }
-        if (ge) hipGraphExecDestroy(ge);
-        if (g) hipGraphDestroy(g);
-        if (e == hipSuccess) {
-            acc = tmp;
-            replayed = true;
-        } else {
-            std::fprintf(stderr, "mi355x: event timing under graph replay unavailable (%s)\n", hipGetErrorString(e));
-            (void) hipGetLastError();
-            (void) hipStreamSynchronize(be->stream);
+        MI_CHECK(hipStreamSynchronize(be->stream));
+        for (int i = 0; i < n; i++) {
+            float ms = 0.0f;
+            MI_CHECK(hipEventElapsedTime(&ms, ev[(size_t) i], ev[(size_t) i + 1]));
+            acc[(size_t) i] += ms;
         }
     }
-    if (!replayed) {
-        for (int it = 0; it < iters; it++) {
-            MI_CHECK(hipEventRecord(ev[0], be->stream));
-            for (int i = 0; i < n; i++) {
-                p.steps[(size_t) i].run(be->stream);
-                MI_CHECK(hipEventRecord(ev[(size_t) i + 1], be->stream));
-            }
-            MI_CHECK(hipStreamSynchronize(be->stream));
-            for (int i = 0; i < n; i++) {
-                float ms = 0.0f;
-                MI_CHECK(hipEventElapsedTime(&ms, ev[(size_t) i], ev[(size_t) i + 1]));
-                acc[(size_t) i] += ms;
-            }
-        }
-    }
-    std::fprintf(stderr, "mi355x: profiled %d launch groups x %d iterations (%s)\n", n, iters,
-                 replayed ? "HIP-graph replay with event nodes" : "eager launches");
+    const bool replayed = false;
+    (void) replayed;
+    std::fprintf(stderr, "mi355x: profiled %d launch groups x %d iterations (queued behind a spin)\n", n, iters);
     for (auto & e : ev) MI_CHECK(hipEventDestroy(e));
     for (int i = 0; i < n && i < max_steps; i++) {
         if (step_ms) step_ms[i] = (float) (acc[(size_t) i] / (iters > 0 ? iters : 1));

@@ -19,6 +19,7 @@ struct device_state {
     std::string pci_id;
     std::string arch;
     uint16_t * gelu_table = nullptr;  // device copy of the f16 GELU table
+    int wall_clock_khz = 100000;      // constant-rate device clock (hipDeviceAttributeWallClockRate)
     ggml_backend_device dev{};
     ggml_backend_buffer_type buft{};
 };

@@ -102,6 +102,8 @@ void launch_soft_max(const tview & d, const tview & a, const tview * mask, float
 size_t argmax_scratch_bytes(int64_t ne0, int64_t rows);
 void launch_argmax(const tview & a, int32_t * out, int first, void * scratch, hipStream_t s);
 bool norm_supported(int64_t ne0);
+// a one-wave kernel that returns after `us` microseconds of device wall clock
+void launch_spin_us(double us, int wall_clock_khz, hipStream_t s);
 
 // Q8_0 layout conversion between ggml's interleaved blocks and the row-split
 // device layout (host side, used by set/get_tensor)

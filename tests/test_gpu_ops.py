@@ -52,7 +52,7 @@ MM_CASES = [
 
 
 @pytest.mark.parametrize("wname,m,k", MM_CASES)
-@pytest.mark.parametrize("n", [1, 2, 8, 13])
+@pytest.mark.parametrize("n", [1, 2, 8, 13, 64, 100])
 def test_mul_mat_quantized(ggml, gpu, ref, wname, m, k, n):
     wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
     print(f"mul_mat {wname} M={m} K={k} N={n}", flush=True)
