@@ -99,6 +99,68 @@ struct ggml_cgraph * oa_qwen_decode_graph(oa_qwen_session * s);
  * to one occurrence), or -1 when no loop is detected. */
 int oa_detect_degenerate_ngram(const int32_t * tokens, int len, int max_ngram, int * ngram_len, int * repeats);
 
+/*
+ * Whisper decoder (models/whisper/ggml_decoder_graph.rs): reusable one-token
+ * step graph (:3869-4052) -- token + learned position embedding, per layer
+ * pre-LayerNorm self attention over a resident f16 KV cache with the
+ * fixed-span mask (:4557-5044), cross attention over the precomputed f16
+ * cross K/V of the encoder frames (:5106-5340), LayerNorm -> fc1 -> GELU ->
+ * fc2 MLP (:5342-5392), each with its residual; final LayerNorm and the
+ * output projection tied to the token embedding. Cross K/V are precomputed
+ * once per utterance: K = Wk enc, V = Wv enc + bv, stored f16 (:5780-5805).
+ * Batch 1.
+ */
+typedef struct {
+    int d_model;
+    int n_layers;
+    int n_head;
+    int ffn;
+    int vocab;
+    int max_positions; /* learned positions and the self KV span */
+    int n_frames;      /* encoder frames the cross attention reads */
+    float ln_eps;
+    uint64_t seed;
+} oa_whisper_config;
+
+enum oa_whisper_tensor_kind {
+    /* per layer (layer >= 0); matrices Q8_0 rows of d_model (fc2: rows of ffn), vectors f32 */
+    OA_WH_SELF_LN_W = 0, OA_WH_SELF_LN_B, OA_WH_SELF_Q, OA_WH_SELF_Q_B, OA_WH_SELF_K, OA_WH_SELF_V,
+    OA_WH_SELF_V_B, OA_WH_SELF_O, OA_WH_SELF_O_B,
+    OA_WH_CROSS_LN_W, OA_WH_CROSS_LN_B, OA_WH_CROSS_Q, OA_WH_CROSS_Q_B, OA_WH_CROSS_K, OA_WH_CROSS_V,
+    OA_WH_CROSS_V_B, OA_WH_CROSS_O, OA_WH_CROSS_O_B,
+    OA_WH_MLP_LN_W, OA_WH_MLP_LN_B, OA_WH_FC1, OA_WH_FC1_B, OA_WH_FC2, OA_WH_FC2_B,
+    OA_WH_LAYER_KINDS,
+    /* global (layer = -1) */
+    OA_WH_TOKEN_EMBD = 100, /* Q8_0 [vocab rows of d_model], tied with the output projection */
+    OA_WH_POS_EMBD,         /* f32 [max_positions rows of d_model] */
+    OA_WH_FINAL_LN_W,
+    OA_WH_FINAL_LN_B
+};
+
+typedef struct oa_whisper_weights oa_whisper_weights;
+typedef struct oa_whisper_model oa_whisper_model;
+typedef struct oa_whisper_session oa_whisper_session;
+
+oa_whisper_weights * oa_whisper_weights_synthesize(const oa_whisper_config * cfg);
+void oa_whisper_weights_free(oa_whisper_weights * w);
+const void * oa_whisper_weights_tensor(const oa_whisper_weights * w, int layer, int kind, size_t * nbytes);
+
+oa_whisper_model * oa_whisper_model_create(ggml_backend_t backend, const oa_whisper_weights * w);
+void oa_whisper_model_free(oa_whisper_model * m);
+
+oa_whisper_session * oa_whisper_session_create(oa_whisper_model * m);
+void oa_whisper_session_free(oa_whisper_session * s);
+int oa_whisper_session_position(const oa_whisper_session * s);
+/* encoder states [n_frames][d_model] f32 -> the per-layer f16 cross K/V */
+int oa_whisper_set_encoder(oa_whisper_session * s, const float * enc);
+/* one token at the next position; top-1 (first max) and optionally the logits */
+int oa_whisper_decode_step(oa_whisper_session * s, int32_t token, int32_t * top1_out, float * logits_out);
+int oa_whisper_generate(oa_whisper_session * s, int32_t first_token, int n_steps, int32_t * out_tokens,
+                        double * step_ms);
+/* the layer's cross K / V caches, f16 [n_frames][d_model] */
+int oa_whisper_read_cross(const oa_whisper_session * s, int layer, uint16_t * k_out, uint16_t * v_out);
+struct ggml_cgraph * oa_whisper_decode_graph(oa_whisper_session * s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -21,6 +21,18 @@ class QwenConfig(C.Structure):
                 ("rms_eps", C.c_float), ("wtype", C.c_int), ("seed", C.c_uint64)]
 
 
+class WhisperConfig(C.Structure):
+    _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("ffn", C.c_int),
+                ("vocab", C.c_int), ("max_positions", C.c_int), ("n_frames", C.c_int), ("ln_eps", C.c_float),
+                ("seed", C.c_uint64)]
+
+
+# Whisper-tiny decoder shape: d_model 384, 4 layers, 6 heads of 64, FFN 1536, vocab 51865,
+# 448 learned positions, 1500 encoder frames
+WHISPER_TINY = dict(d_model=384, n_layers=4, n_head=6, ffn=1536, vocab=51865, max_positions=448, n_frames=1500)
+WH_LAYER_KINDS = 24
+WH_TOKEN_EMBD, WH_POS_EMBD, WH_FINAL_LN_W, WH_FINAL_LN_B = 100, 101, 102, 103
+
 # Qwen3-0.6B / 1.7B shapes (hidden, layers, heads, kv heads, head_dim, ffn, vocab)
 QWEN3_06B = dict(d_model=1024, n_layers=28, n_head=16, n_kv_head=8, head_dim=128, ffn=3072, vocab=151936)
 QWEN3_17B = dict(d_model=2048, n_layers=28, n_head=16, n_kv_head=8, head_dim=128, ffn=6144, vocab=151936)
@@ -58,6 +70,19 @@ def lib() -> C.CDLL:
     s("oa_qwen_prefill_embeddings", i, vp, vp, i, vp)
     s("oa_qwen_prefill_tokens", i, vp, vp, i, vp)
     s("oa_qwen_decode_step", i, vp, vp, vp, vp)
+    s("oa_whisper_weights_synthesize", vp, C.POINTER(WhisperConfig))
+    s("oa_whisper_weights_free", None, vp)
+    s("oa_whisper_weights_tensor", vp, vp, i, i, C.POINTER(C.c_size_t))
+    s("oa_whisper_model_create", vp, vp, vp)
+    s("oa_whisper_model_free", None, vp)
+    s("oa_whisper_session_create", vp, vp)
+    s("oa_whisper_session_free", None, vp)
+    s("oa_whisper_session_position", i, vp)
+    s("oa_whisper_set_encoder", i, vp, vp)
+    s("oa_whisper_decode_step", i, vp, C.c_int32, vp, vp)
+    s("oa_whisper_generate", i, vp, C.c_int32, i, vp, vp)
+    s("oa_whisper_read_cross", i, vp, i, vp, vp)
+    s("oa_whisper_decode_graph", vp, vp)
     s("oa_qwen_generate", i, vp, vp, i, vp, vp)
     s("oa_qwen_read_kv", i, vp, i, i, vp, vp)
     s("oa_detect_degenerate_ngram", i, vp, i, i, vp, vp)
@@ -177,6 +202,111 @@ class QwenSession:
         if self.ptr:
             lib().oa_qwen_session_free(self.ptr)
             self.ptr = None
+
+
+class WhisperWeights:
+    """Synthesised Whisper decoder weights (host bytes, Q8_0 matrices)."""
+
+    def __init__(self, seed: int = 1234, ln_eps: float = 1e-5, **shape):
+        self.cfg = WhisperConfig(shape["d_model"], shape["n_layers"], shape["n_head"], shape["ffn"], shape["vocab"],
+                                 shape["max_positions"], shape["n_frames"], ln_eps, seed)
+        self.ptr = lib().oa_whisper_weights_synthesize(C.byref(self.cfg))
+        if not self.ptr:
+            raise RuntimeError("whisper weight synthesis failed")
+
+    def tensor_ptr(self, layer: int, kind: int) -> int:
+        n = C.c_size_t(0)
+        p = lib().oa_whisper_weights_tensor(self.ptr, layer, kind, C.byref(n))
+        if not p:
+            raise KeyError((layer, kind))
+        return p
+
+    def pointer_table(self):
+        """per layer the 24 tensors in kind order, then token embedding,
+        position embedding, final LayerNorm weight and bias (oracle order)"""
+        out = [self.tensor_ptr(l, k) for l in range(self.cfg.n_layers) for k in range(WH_LAYER_KINDS)]
+        out += [self.tensor_ptr(-1, k) for k in (WH_TOKEN_EMBD, WH_POS_EMBD, WH_FINAL_LN_W, WH_FINAL_LN_B)]
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().oa_whisper_weights_free(self.ptr)
+            self.ptr = None
+
+
+class WhisperModel:
+    def __init__(self, weights: WhisperWeights, backend):
+        self.cfg = weights.cfg
+        self.ptr = lib().oa_whisper_model_create(backend, weights.ptr)
+        if not self.ptr:
+            raise RuntimeError("whisper model upload failed")
+
+    def session(self) -> "WhisperSession":
+        return WhisperSession(self)
+
+    def free(self):
+        if self.ptr:
+            lib().oa_whisper_model_free(self.ptr)
+            self.ptr = None
+
+
+class WhisperSession:
+    """Batch-1 Whisper decode: cross K/V from encoder states, then greedy steps."""
+
+    def __init__(self, model: WhisperModel):
+        self.model = model
+        self.ptr = lib().oa_whisper_session_create(model.ptr)
+        if not self.ptr:
+            raise RuntimeError("whisper session allocation failed")
+
+    @staticmethod
+    def _check(st: int, what: str):
+        if st != 0:
+            raise RuntimeError(f"{what} failed with ggml status {st}")
+
+    def set_encoder(self, enc: np.ndarray):
+        enc = np.ascontiguousarray(enc, dtype=np.float32)
+        self._check(lib().oa_whisper_set_encoder(self.ptr, enc.ctypes.data), "cross K/V precompute")
+
+    def step(self, token: int, want_logits: bool = False):
+        top1 = C.c_int32(0)
+        logits = np.zeros(self.model.cfg.vocab, np.float32) if want_logits else None
+        self._check(lib().oa_whisper_decode_step(self.ptr, int(token), C.byref(top1),
+                                                 logits.ctypes.data if want_logits else None), "whisper step")
+        return (top1.value, logits) if want_logits else top1.value
+
+    def generate(self, first: int, n_steps: int):
+        out = np.zeros(n_steps, np.int32)
+        ms = np.zeros(n_steps, np.float64)
+        self._check(lib().oa_whisper_generate(self.ptr, int(first), n_steps, out.ctypes.data, ms.ctypes.data),
+                    "whisper generate")
+        return out, ms
+
+    def read_cross(self, layer: int):
+        c = self.model.cfg
+        k = np.zeros((c.n_frames, c.d_model), np.uint16)
+        v = np.zeros((c.n_frames, c.d_model), np.uint16)
+        self._check(lib().oa_whisper_read_cross(self.ptr, layer, k.ctypes.data, v.ctypes.data), "read_cross")
+        return k, v
+
+    def decode_graph(self):
+        return lib().oa_whisper_decode_graph(self.ptr)
+
+    def position(self) -> int:
+        return lib().oa_whisper_session_position(self.ptr)
+
+    def free(self):
+        if self.ptr:
+            lib().oa_whisper_session_free(self.ptr)
+            self.ptr = None
+
+
+def whisper_inputs(shape: dict, n_prompt: int = 4, seed: int = 91):
+    """seeded N(0,1) encoder states [n_frames, d] and prompt token ids"""
+    enc = g.synth_normal(seed, 3000, shape["n_frames"] * shape["d_model"]).reshape(shape["n_frames"], shape["d_model"])
+    prompt = np.zeros(n_prompt, np.int32)
+    g.base().oa_synth_uniform_i32(seed, 3001, n_prompt, shape["vocab"], prompt.ctypes.data)
+    return enc, prompt
 
 
 def detect_degenerate_ngram(tokens, max_ngram: int = 8):

@@ -263,3 +263,44 @@ class QwenRefBatch:
                                     logits.ctypes.data if want_logits else None, self.fidelity, self.threads)
         self.pos += 1
         return (top1, logits) if want_logits else top1
+
+
+class WhisperDims(C.Structure):
+    _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("ffn", C.c_int),
+                ("vocab", C.c_int), ("max_positions", C.c_int), ("n_frames", C.c_int), ("ln_eps", C.c_float)]
+
+
+class WhisperRef:
+    """CPU reference of the Whisper decoder (batch 1) over host weight bytes:
+    cross K/V precompute from encoder states, then one token per step."""
+
+    def __init__(self, cfg, pointer_table, fa_fidelity: int = 4, threads: int = 0):
+        L = lib()
+        L.ref_whisper_cross_kv.restype = None
+        L.ref_whisper_cross_kv.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]
+        L.ref_whisper_step.restype = C.c_int32
+        L.ref_whisper_step.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_int32, C.c_int, C.c_void_p, C.c_int, C.c_int]
+        self.dims = WhisperDims(cfg.d_model, cfg.n_layers, cfg.n_head, cfg.ffn, cfg.vocab, cfg.max_positions,
+                                cfg.n_frames, cfg.ln_eps)
+        self.table = (C.c_void_p * len(pointer_table))(*pointer_table)
+        self.fidelity, self.threads = fa_fidelity, threads
+        n = cfg.n_layers
+        self.k = [np.zeros((cfg.max_positions, cfg.d_model), np.uint16) for _ in range(n)]
+        self.v = [np.zeros((cfg.max_positions, cfg.d_model), np.uint16) for _ in range(n)]
+        self.ck = [np.zeros((cfg.n_frames, cfg.d_model), np.uint16) for _ in range(n)]
+        self.cv = [np.zeros((cfg.n_frames, cfg.d_model), np.uint16) for _ in range(n)]
+        arr = lambda xs: (C.c_void_p * n)(*[a.ctypes.data for a in xs])
+        self.kp, self.vp, self.ckp, self.cvp = arr(self.k), arr(self.v), arr(self.ck), arr(self.cv)
+        self.pos = 0
+
+    def set_encoder(self, enc: np.ndarray):
+        enc = np.ascontiguousarray(enc, dtype=np.float32)
+        lib().ref_whisper_cross_kv(C.byref(self.dims), self.table, enc.ctypes.data, self.ckp, self.cvp, self.threads)
+
+    def step(self, token: int):
+        logits = np.zeros(self.dims.vocab, np.float32)
+        top1 = lib().ref_whisper_step(C.byref(self.dims), self.table, self.kp, self.vp, self.ckp, self.cvp,
+                                      int(token), self.pos, logits.ctypes.data, self.fidelity, self.threads)
+        self.pos += 1
+        return int(top1), logits

@@ -213,3 +213,130 @@ void ref_qwen_decode_batch(const ref_qwen_dims * m, const void * const * t, uint
     free(lg);
     free(mask);
 }
+
+/* ------------------------------------------------------------ Whisper -- */
+
+/*
+ * Whisper decoder step, batch 1 (models/whisper/ggml_decoder_graph.rs):
+ * reusable one-token graph :3869-4052, self attention :4557-5044, cross
+ * attention :5106-5340, MLP :5342-5392, LayerNorm :5953-6010, linear with
+ * bias :5446-5490, cross K/V precompute :5780-5805.
+ * Pointer table: per layer OA_WH_LAYER_KINDS (24) entries in the order of
+ * oa_whisper_tensor_kind, then token embedding (Q8_0), position embedding
+ * (f32), final LayerNorm weight and bias.
+ */
+typedef struct {
+    int d_model, n_layers, n_head, ffn, vocab, max_positions, n_frames;
+    float ln_eps;
+} ref_whisper_dims;
+
+enum {
+    W_SELF_LN_W = 0, W_SELF_LN_B, W_SELF_Q, W_SELF_Q_B, W_SELF_K, W_SELF_V, W_SELF_V_B, W_SELF_O, W_SELF_O_B,
+    W_CROSS_LN_W, W_CROSS_LN_B, W_CROSS_Q, W_CROSS_Q_B, W_CROSS_K, W_CROSS_V, W_CROSS_V_B, W_CROSS_O, W_CROSS_O_B,
+    W_MLP_LN_W, W_MLP_LN_B, W_FC1, W_FC1_B, W_FC2, W_FC2_B, W_PER_LAYER
+};
+
+static const void * wp(const void * const * t, int layer, int kind) { return t[layer * W_PER_LAYER + kind]; }
+static const void * wg(const ref_whisper_dims * m, const void * const * t, int i) {
+    return t[m->n_layers * W_PER_LAYER + i];
+}
+
+/* apply_affine_layer_norm: norm, then * w, then + b (separate f32 ops) */
+static void wh_layer_norm(const float * x, float * y, int n, const float * w, const float * b, float eps) {
+    ref_norm(x, y, n, 1, eps);
+    for (int i = 0; i < n; i++) y[i] = y[i] * w[i];
+    for (int i = 0; i < n; i++) y[i] = y[i] + b[i];
+}
+
+/* mul_mat then + bias (when given) */
+static void wh_linear(const void * w, int rows, int k, const float * x, const float * b, float * y, int threads) {
+    ref_mul_mat(REF_Q8_0, w, ref_row_size(REF_Q8_0, k), rows, k, x, k, 1, y, rows, threads);
+    if (b)
+        for (int i = 0; i < rows; i++) y[i] = y[i] + b[i];
+}
+
+/* cross K/V for every layer: K = Wk enc, V = Wv enc + bv, f16 [n_frames][d] */
+void ref_whisper_cross_kv(const ref_whisper_dims * m, const void * const * t, const float * enc,
+                          uint16_t * const * ck, uint16_t * const * cv, int threads) {
+    const int d = m->d_model, F = m->n_frames;
+    float * k = (float *) malloc(sizeof(float) * (size_t) F * d);
+    for (int l = 0; l < m->n_layers; l++) {
+        ref_mul_mat(REF_Q8_0, wp(t, l, W_CROSS_K), ref_row_size(REF_Q8_0, d), d, d, enc, d, F, k, d, threads);
+        ref_fp32_to_fp16_row(k, ck[l], (int64_t) F * d);
+        ref_mul_mat(REF_Q8_0, wp(t, l, W_CROSS_V), ref_row_size(REF_Q8_0, d), d, d, enc, d, F, k, d, threads);
+        const float * bv = (const float *) wp(t, l, W_CROSS_V_B);
+        for (int f = 0; f < F; f++)
+            for (int i = 0; i < d; i++) k[(size_t) f * d + i] = k[(size_t) f * d + i] + bv[i];
+        ref_fp32_to_fp16_row(k, cv[l], (int64_t) F * d);
+    }
+    free(k);
+}
+
+/*
+ * One token at position pos. kc/vc: per layer self K/V f16 [max_positions][d]
+ * (row = position, all heads); ck/cv: per layer cross K/V f16 [n_frames][d].
+ * Writes this position's K/V rows, attends over the full span with the
+ * fixed-span mask (masked positions are skipped), fills logits [vocab] when
+ * non-null and returns the first-max top-1.
+ */
+int32_t ref_whisper_step(const ref_whisper_dims * m, const void * const * t, uint16_t * const * kc,
+                         uint16_t * const * vc, uint16_t * const * ck, uint16_t * const * cv, int32_t token, int pos,
+                         float * logits, int fa_fidelity, int threads) {
+    const int d = m->d_model, H = m->n_head, hd = d / H, mp = m->max_positions;
+    float * x = (float *) malloc(sizeof(float) * d);
+    float * nrm = (float *) malloc(sizeof(float) * d);
+    float * q = (float *) malloc(sizeof(float) * d);
+    float * k = (float *) malloc(sizeof(float) * d);
+    float * v = (float *) malloc(sizeof(float) * d);
+    float * att = (float *) malloc(sizeof(float) * d);
+    float * o = (float *) malloc(sizeof(float) * d);
+    float * h = (float *) malloc(sizeof(float) * m->ffn);
+    uint16_t * mask = (uint16_t *) malloc(sizeof(uint16_t) * mp);
+    for (int j = 0; j < mp; j++) mask[j] = j <= pos ? 0 : 0xFC00;
+    /* token + learned position embedding */
+    ref_dequantize_row_q8_0((const ref_block_q8_0 *) ((const char *) wg(m, t, 0) + (size_t) token * ref_row_size(REF_Q8_0, d)),
+                            x, d);
+    const float * pe = (const float *) wg(m, t, 1) + (size_t) pos * d;
+    for (int i = 0; i < d; i++) x[i] = x[i] + pe[i];
+    const float scale = 1.0f / sqrtf((float) hd);
+    for (int l = 0; l < m->n_layers; l++) {
+        /* self attention */
+        wh_layer_norm(x, nrm, d, (const float *) wp(t, l, W_SELF_LN_W), (const float *) wp(t, l, W_SELF_LN_B), m->ln_eps);
+        wh_linear(wp(t, l, W_SELF_Q), d, d, nrm, (const float *) wp(t, l, W_SELF_Q_B), q, threads);
+        wh_linear(wp(t, l, W_SELF_K), d, d, nrm, NULL, k, threads);
+        wh_linear(wp(t, l, W_SELF_V), d, d, nrm, (const float *) wp(t, l, W_SELF_V_B), v, threads);
+        ref_fp32_to_fp16_row(k, kc[l] + (size_t) pos * d, d);
+        ref_fp32_to_fp16_row(v, vc[l] + (size_t) pos * d, d);
+        ref_flash_attn_ext(q, d, hd, kc[l], vc[l], hd, d, mask, mp, att, hd, 1, H, H, mp, scale, fa_fidelity, threads);
+        wh_linear(wp(t, l, W_SELF_O), d, d, att, (const float *) wp(t, l, W_SELF_O_B), o, threads);
+        for (int i = 0; i < d; i++) x[i] = o[i] + x[i];
+        /* cross attention */
+        wh_layer_norm(x, nrm, d, (const float *) wp(t, l, W_CROSS_LN_W), (const float *) wp(t, l, W_CROSS_LN_B), m->ln_eps);
+        wh_linear(wp(t, l, W_CROSS_Q), d, d, nrm, (const float *) wp(t, l, W_CROSS_Q_B), q, threads);
+        ref_flash_attn_ext(q, d, hd, ck[l], cv[l], hd, d, NULL, 0, att, hd, 1, H, H, m->n_frames, scale, fa_fidelity,
+                           threads);
+        wh_linear(wp(t, l, W_CROSS_O), d, d, att, (const float *) wp(t, l, W_CROSS_O_B), o, threads);
+        for (int i = 0; i < d; i++) x[i] = o[i] + x[i];
+        /* MLP */
+        wh_layer_norm(x, nrm, d, (const float *) wp(t, l, W_MLP_LN_W), (const float *) wp(t, l, W_MLP_LN_B), m->ln_eps);
+        wh_linear(wp(t, l, W_FC1), m->ffn, d, nrm, (const float *) wp(t, l, W_FC1_B), h, threads);
+        for (int i = 0; i < m->ffn; i++) h[i] = ref_gelu(h[i]);
+        wh_linear(wp(t, l, W_FC2), d, m->ffn, h, (const float *) wp(t, l, W_FC2_B), o, threads);
+        for (int i = 0; i < d; i++) x[i] = o[i] + x[i];
+    }
+    wh_layer_norm(x, nrm, d, (const float *) wg(m, t, 2), (const float *) wg(m, t, 3), m->ln_eps);
+    float * lg = logits ? logits : (float *) malloc(sizeof(float) * m->vocab);
+    ref_mul_mat(REF_Q8_0, wg(m, t, 0), ref_row_size(REF_Q8_0, d), m->vocab, d, nrm, d, 1, lg, m->vocab, threads);
+    const int32_t top1 = ref_argmax_first(lg, m->vocab);
+    if (!logits) free(lg);
+    free(x);
+    free(nrm);
+    free(q);
+    free(k);
+    free(v);
+    free(att);
+    free(o);
+    free(h);
+    free(mask);
+    return top1;
+}

@@ -120,3 +120,36 @@ def test_qwen3_06b_q4_K_batch8_first_64_steps(gpu, ref):
     print("qwen3-0.6b q4_K b8", flush=True)
     run_pair(gpu, ref, D.QWEN3_06B, g.Q4_K, 8, prefix=375, prompt=8, steps=64, max_pos=1024, seed=1234,
              check_logits=True)
+
+
+def test_whisper_tiny_q8_0_first_64_steps(gpu, ref):
+    """Whisper-tiny-shaped decoder, Q8_0, 1500 N(0,1) encoder frames, batch 1:
+    cross K/V bit for bit, then 4 prompt tokens and 64 greedy steps token for
+    token with the logits checked every step"""
+    print("whisper-tiny q8_0 b1", flush=True)
+    shape = D.WHISPER_TINY
+    w = D.WhisperWeights(seed=4321, **shape)
+    model = D.WhisperModel(w, gpu.backend)
+    sess = model.session()
+    enc, prompt = D.whisper_inputs(shape, n_prompt=4, seed=91)
+    sess.set_encoder(enc)
+    r = ref.WhisperRef(w.cfg, w.pointer_table(), fa_fidelity=4)
+    r.set_encoder(enc)
+    for layer in range(shape["n_layers"]):
+        k, v = sess.read_cross(layer)
+        assert np.array_equal(k, r.ck[layer]) and np.array_equal(v, r.cv[layer]), f"cross K/V layer {layer}"
+    max_dl = 0.0
+    tok_d = tok_r = None
+    for i, t in enumerate(list(prompt) + [None] * 64):
+        t_d = int(t) if t is not None else tok_d
+        t_r = int(t) if t is not None else tok_r
+        tok_d, lg_d = sess.step(t_d, want_logits=True)
+        tok_r, lg_r = r.step(t_r)
+        max_dl = max(max_dl, float(np.abs(lg_d - lg_r).max()))
+        assert tok_d == tok_r, f"step {i}: gpu {tok_d} != cpu {tok_r}"
+    print(f"  max |dlogit| {max_dl:.2e}")
+    assert max_dl < 1e-2
+    # the self K cache of the last layer holds the reference's rows
+    sess.free()
+    model.free()
+    w.free()

@@ -371,3 +371,31 @@ def test_flash_attn_chunked_mode(ref, n_kv, holes):
         v2[:, a:b] = np.float16(np.nan)
     got2 = ref.flash_attn(q, k2.view(np.uint16), v2.view(np.uint16), mask.view(np.uint16), scale, fidelity=4)
     assert np.array_equal(got, got2)
+
+
+def test_whisper_cross_kv_matches_brute_force(ref):
+    """the oracle's cross K/V precompute (K = Wk enc, V = Wv enc + bv, f16)
+    against an f64 product of the dequantized weight with the Q8_0-quantized
+    encoder states, on a reduced shape"""
+    from openasr_amd import decoders as D
+    shape = dict(D.WHISPER_TINY, vocab=512, n_frames=96, n_layers=1)
+    w = D.WhisperWeights(seed=5, **shape)
+    enc = RNG.standard_normal((shape["n_frames"], shape["d_model"])).astype(np.float32)
+    r = ref.WhisperRef(w.cfg, w.pointer_table())
+    r.set_encoder(enc)
+    d = shape["d_model"]
+    tbl = w.pointer_table()
+    import ctypes as C
+    nbytes = d * ref.row_size(ref.Q8_0, d)
+    wk = np.ctypeslib.as_array((C.c_uint8 * nbytes).from_address(tbl[13]))
+    wv = np.ctypeslib.as_array((C.c_uint8 * nbytes).from_address(tbl[14]))
+    bv = np.ctypeslib.as_array((C.c_float * d).from_address(tbl[15])).astype(np.float64)
+    xq = np.stack([ref.dequantize(ref.Q8_0, ref.quantize_act(ref.Q8_0, enc[f:f + 1]), d) for f in range(len(enc))])
+    for wq, bias, got in ((wk, None, r.ck[0]), (wv, bv, r.cv[0])):
+        W = ref.dequantize(ref.Q8_0, wq, d * d).reshape(d, d).astype(np.float64)
+        want = xq.reshape(len(enc), d).astype(np.float64) @ W.T
+        if bias is not None:
+            want = want + bias
+        g16 = got.view(np.float16).astype(np.float64)
+        assert np.abs(g16 - want).max() <= 1e-3 * np.abs(want).max() + 1e-6
+    w.free()
