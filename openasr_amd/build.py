@@ -66,7 +66,7 @@ def build_base(fp: str) -> Path:
 def build_models() -> Path:
     out = LIB / "libopenasr-models.so"
     srcs = sorted(str(p) for p in (PKG / "decoders").glob("*.cpp"))
-    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", f"-I{INCLUDE}", *srcs, "-o", str(out),
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", f"-I{INCLUDE}", *srcs, "-o", str(out),
           f"-L{LIB}", "-lggml-base", "-Wl,-rpath,$ORIGIN"])
     return out
 

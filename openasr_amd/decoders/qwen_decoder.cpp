@@ -45,15 +45,23 @@ std::vector<uint8_t> synth_matrix(int wtype, uint64_t seed, const std::vector<st
     for (auto & p : parts) rows += p.second;
     const size_t rs = ggml_row_size((ggml_type) wtype, k);
     std::vector<uint8_t> out((size_t) rows * rs);
-    const int64_t slab = 1024;
-    std::vector<float> buf((size_t) (slab * k));
+    // slabs of rows are independent (the generator is counter-based and the
+    // quantizers work row by row), so they are filled in parallel
+    const int64_t slab = 256;
     int64_t row0 = 0;
     for (auto & p : parts) {
-        for (int64_t r = 0; r < p.second; r += slab) {
-            const int64_t n = std::min(slab, p.second - r);
-            oa_synth_normal(seed, p.first, r * k, n * k, 0.0f, 0.02f, buf.data());
-            ggml_quantize_chunk((ggml_type) wtype, buf.data(), out.data() + (size_t) (row0 + r) * rs, 0, n, k,
-                                nullptr);
+        const int64_t n_slabs = (p.second + slab - 1) / slab;
+#pragma omp parallel
+        {
+            std::vector<float> buf((size_t) (slab * k));  // one per thread, reused across slabs
+#pragma omp for schedule(dynamic, 1)
+            for (int64_t si = 0; si < n_slabs; si++) {
+                const int64_t r = si * slab;
+                const int64_t n = std::min(slab, p.second - r);
+                oa_synth_normal(seed, p.first, r * k, n * k, 0.0f, 0.02f, buf.data());
+                ggml_quantize_chunk((ggml_type) wtype, buf.data(), out.data() + (size_t) (row0 + r) * rs, 0, n, k,
+                                    nullptr);
+            }
         }
         row0 += p.second;
     }

@@ -10,6 +10,7 @@
  */
 #include "ggml_cpu_ref.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -190,14 +191,29 @@ void ref_dequantize_row_q8_0(const ref_block_q8_0 * x, float * y, int64_t k) {
     }
 }
 
+/* horizontal sum of eight int32 lanes (integer: order-free) */
+static inline int hsum_i32x8(__m256i v) {
+    __m128i s = _mm_add_epi32(_mm256_castsi256_si128(v), _mm256_extracti128_si256(v, 1));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0x4E));
+    s = _mm_add_epi32(s, _mm_shuffle_epi32(s, 0xB1));
+    return _mm_cvtsi128_si32(s);
+}
+
 /* vec_dot_q8_0_q8_0: per block an exact integer dot, scaled by d_x*d_y;
  * block terms summed in f64 and rounded once (see vec_dot_q4_K_q8_K) */
 float ref_vec_dot_q8_0_q8_0(int64_t n, const ref_block_q8_0 * x, const ref_block_q8_0 * y) {
     const int64_t nb = n / REF_QK8_0;
     double sum = 0.0;
     for (int64_t i = 0; i < nb; i++) {
-        int sumi = 0;
-        for (int j = 0; j < REF_QK8_0; j++) sumi += (int) x[i].qs[j] * (int) y[i].qs[j];
+        /* the integer dot in AVX2: int8 widened to int16, pair products
+         * summed to int32 (exact for every int8 value) */
+        const __m256i xv = _mm256_loadu_si256((const __m256i *) x[i].qs);
+        const __m256i yv = _mm256_loadu_si256((const __m256i *) y[i].qs);
+        const __m256i p0 = _mm256_madd_epi16(_mm256_cvtepi8_epi16(_mm256_castsi256_si128(xv)),
+                                             _mm256_cvtepi8_epi16(_mm256_castsi256_si128(yv)));
+        const __m256i p1 = _mm256_madd_epi16(_mm256_cvtepi8_epi16(_mm256_extracti128_si256(xv, 1)),
+                                             _mm256_cvtepi8_epi16(_mm256_extracti128_si256(yv, 1)));
+        const int sumi = hsum_i32x8(_mm256_add_epi32(p0, p1));
         /* d_x*d_y of two halves is exact in f32; the block term is exact in f64 */
         const float dd = ref_fp16_to_fp32(x[i].d) * ref_fp16_to_fp32(y[i].d);
         sum += (double) sumi * (double) dd;
@@ -401,17 +417,25 @@ float ref_vec_dot_q4_K_q8_K(int64_t n, const ref_block_q4_K * x, const ref_block
         for (int j = 0; j < 8; j++) ref_get_scale_min_k4(j, x[i].scales, &sc[j], &mn[j]);
         int msum = 0;
         for (int j = 0; j < 16; j++) msum += (int) y[i].bsums[j] * (int) mn[j / 2];
-        int isum = 0;
+        /* isum = sum_c sc[2c] * <lo nibbles, q8[64c..+32]> + sc[2c+1] * <hi
+         * nibbles, q8[64c+32..+32]>, in AVX2: unsigned nibble x int8 pairs
+         * (|pair| <= 2*15*128, no int16 saturation), then x the 6-bit scale
+         * into int32 lanes; exact integer arithmetic */
         const uint8_t * q4 = x[i].qs;
         const int8_t * q8 = y[i].qs;
+        const __m256i m4 = _mm256_set1_epi8(0x0F);
+        __m256i acc = _mm256_setzero_si256();
         for (int c = 0; c < 4; c++) {
-            int s_lo = 0, s_hi = 0;
-            for (int l = 0; l < 32; l++) {
-                s_lo += (int) (q4[32 * c + l] & 0xF) * (int) q8[64 * c + l];
-                s_hi += (int) (q4[32 * c + l] >> 4) * (int) q8[64 * c + 32 + l];
-            }
-            isum += s_lo * sc[2 * c] + s_hi * sc[2 * c + 1];
+            const __m256i q4v = _mm256_loadu_si256((const __m256i *) (q4 + 32 * c));
+            const __m256i lo = _mm256_and_si256(q4v, m4);
+            const __m256i hi = _mm256_and_si256(_mm256_srli_epi16(q4v, 4), m4);
+            const __m256i y0 = _mm256_loadu_si256((const __m256i *) (q8 + 64 * c));
+            const __m256i y1 = _mm256_loadu_si256((const __m256i *) (q8 + 64 * c + 32));
+            acc = _mm256_add_epi32(acc, _mm256_madd_epi16(_mm256_maddubs_epi16(lo, y0), _mm256_set1_epi16(sc[2 * c])));
+            acc = _mm256_add_epi32(acc,
+                                   _mm256_madd_epi16(_mm256_maddubs_epi16(hi, y1), _mm256_set1_epi16(sc[2 * c + 1])));
         }
+        const int isum = hsum_i32x8(acc);
         const double d = (double) ref_fp16_to_fp32(x[i].d) * (double) y[i].d;
         const double dmin = (double) ref_fp16_to_fp32(x[i].dmin) * (double) y[i].d;
         sum += d * (double) isum - dmin * (double) msum;
@@ -618,6 +642,103 @@ int32_t ref_argmax_first(const float * x, int64_t n) {
 
 /* ----------------------------------------------------- flash attention -- */
 
+/* s[j] = sum_d (double) (k_j[d] * q[d]) for up to four positions j, each
+ * summed in dim order (the f32 products are exact roundings of the f16
+ * operands' products; F16C converts f16 exactly). Four positions are in
+ * flight so the dependent f64 adds of one sum overlap the others'. */
+static void fa_dot4(const uint16_t * k, int64_t kv_stride_pos, const float * qf, int64_t D, int n, double * s) {
+    float tt[512][4];
+    for (int j = 0; j < 4; j++) {
+        if (j >= n) {
+            for (int64_t d = 0; d < D; d++) tt[d][j] = 0.0f;
+            continue;
+        }
+        const uint16_t * kr = k + j * kv_stride_pos;
+        for (int64_t d = 0; d < D; d += 8) {
+            float pr[8];
+            _mm256_storeu_ps(pr, _mm256_mul_ps(_mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) (kr + d))),
+                                               _mm256_loadu_ps(qf + d)));
+            for (int e = 0; e < 8; e++) tt[d + e][j] = pr[e];
+        }
+    }
+    __m256d a = _mm256_setzero_pd();
+    for (int64_t d = 0; d < D; d++) a = _mm256_add_pd(a, _mm256_cvtps_pd(_mm_loadu_ps(tt[d])));
+    _mm256_storeu_pd(s, a);
+}
+
+/* fidelity 4 for one (query, head): fixed 64-position KV chunks, each with
+ * its own max m_c, p = exp(s - m_c), f64 sums l_c and a_c; the chunks are
+ * combined in order with w = exp(m_c - M), M = max m_c. Masked (-inf)
+ * positions contribute nothing. Scores are formed once and kept. */
+static void fa_chunked_one(const uint16_t * qh, const uint16_t * k, const uint16_t * v, int64_t kv_stride_pos,
+                           const uint16_t * mask, float * o, int64_t D, int64_t n_kv, float scale) {
+    const int64_t C = 64, n_chunks = (n_kv + C - 1) / C;
+    if (n_chunks > 1024) abort(); /* spans beyond 65536 positions are not modelled */
+    if (D % 8 != 0 || D > 512) abort();
+    float qf[512];
+    for (int64_t d = 0; d < D; d++) qf[d] = ref_fp16_to_fp32(qh[d]);
+    float * sc = (float *) malloc((size_t) (n_kv > 0 ? n_kv : 1) * sizeof(float));
+    float mcs[1024];
+    float M = -INFINITY;
+    for (int64_t c = 0; c < n_chunks; c++) {
+        float mc = -INFINITY;
+        const int64_t e = n_kv < (c + 1) * C ? n_kv : (c + 1) * C;
+        for (int64_t i0 = c * C; i0 < e; i0 += 4) {
+            const int n = e - i0 < 4 ? (int) (e - i0) : 4;
+            float mv[4];
+            int live = 0;
+            for (int j = 0; j < n; j++) {
+                mv[j] = mask ? ref_fp16_to_fp32(mask[i0 + j]) : 0.0f;
+                live |= mv[j] != -INFINITY;
+            }
+            double a[4] = {0.0, 0.0, 0.0, 0.0};
+            if (live) fa_dot4(k + i0 * kv_stride_pos, kv_stride_pos, qf, D, n, a);
+            for (int j = 0; j < n; j++) {
+                if (mv[j] == -INFINITY) {
+                    sc[i0 + j] = -INFINITY;
+                    continue;
+                }
+                const float s = (float) a[j] * scale + mv[j];
+                sc[i0 + j] = s;
+                mc = s > mc ? s : mc;
+            }
+        }
+        mcs[c] = mc;
+        M = mc > M ? mc : M;
+    }
+    double L = 0.0;
+    double O[512], acc[512];
+    for (int64_t d = 0; d < D; d++) O[d] = 0.0;
+    for (int64_t c = 0; c < n_chunks && M != -INFINITY; c++) {
+        if (mcs[c] == -INFINITY) continue;
+        const float w = ref_expf_det(mcs[c] - M);
+        if (w == 0.0f) continue;
+        double l = 0.0;
+        for (int64_t d = 0; d < D; d++) acc[d] = 0.0;
+        const int64_t e = n_kv < (c + 1) * C ? n_kv : (c + 1) * C;
+        for (int64_t ic = c * C; ic < e; ic++) {
+            if (sc[ic] == -INFINITY) continue;
+            const float p = ref_expf_det(sc[ic] - mcs[c]);
+            l += (double) p;
+            if (p == 0.0f) continue;
+            /* acc[d] += p * v[d], per d in position order (f32 x f32 exact in f64) */
+            const uint16_t * vr = v + ic * kv_stride_pos;
+            const __m256d p4 = _mm256_set1_pd((double) p);
+            for (int64_t d = 0; d < D; d += 8) {
+                const __m256 vf = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) (vr + d)));
+                const __m256d lo = _mm256_mul_pd(p4, _mm256_cvtps_pd(_mm256_castps256_ps128(vf)));
+                const __m256d hi = _mm256_mul_pd(p4, _mm256_cvtps_pd(_mm256_extractf128_ps(vf, 1)));
+                _mm256_storeu_pd(acc + d, _mm256_add_pd(_mm256_loadu_pd(acc + d), lo));
+                _mm256_storeu_pd(acc + d + 4, _mm256_add_pd(_mm256_loadu_pd(acc + d + 4), hi));
+            }
+        }
+        L += (double) w * l;
+        for (int64_t d = 0; d < D; d++) O[d] += (double) w * acc[d];
+    }
+    for (int64_t d = 0; d < D; d++) o[d] = L == 0.0 ? 0.0f : (float) (O[d] / L);
+    free(sc);
+}
+
 /* ggml_compute_forward_flash_attn_ext_f16_one_chunk restated: sequential
  * online softmax over KV positions, masked (-inf) positions skipped. */
 void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -648,53 +769,8 @@ void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_
             }
             float * o = out + (iq * Hq + h) * D;
             if (fidelity == 4) {
-                /* chunked: fixed 64-position KV chunks, each with its own max
-                 * m_c, p = exp(s - m_c), f64 sums l_c and a_c; the chunks are
-                 * combined in order with w = exp(m_c - M), M = max m_c */
-                const int64_t C = 64, n_chunks = (n_kv + C - 1) / C;
-                float mcs[1024];
-                if (n_chunks > 1024) abort(); /* spans beyond 65536 positions are not modelled */
-                float M = -INFINITY;
-                for (int64_t c = 0; c < n_chunks; c++) {
-                    float mc = -INFINITY;
-                    for (int64_t ic = c * C; ic < n_kv && ic < (c + 1) * C; ic++) {
-                        const float mv = mask ? ref_fp16_to_fp32(mask[iq * mask_stride + ic]) : 0.0f;
-                        if (mv == -INFINITY) continue;
-                        const uint16_t * kr = k + kvh * kv_stride_head + ic * kv_stride_pos;
-                        double a = 0.0;
-                        for (int64_t d = 0; d < D; d++) a += (double) (ref_fp16_to_fp32(kr[d]) * ref_fp16_to_fp32(qh[d]));
-                        const float s = (float) a * scale + mv;
-                        mc = s > mc ? s : mc;
-                    }
-                    mcs[c] = mc;
-                    M = mc > M ? mc : M;
-                }
-                double L = 0.0;
-                double O[512];
-                for (int64_t d = 0; d < D; d++) O[d] = 0.0;
-                for (int64_t c = 0; c < n_chunks && M != -INFINITY; c++) {
-                    if (mcs[c] == -INFINITY) continue;
-                    const float w = ref_expf_det(mcs[c] - M);
-                    if (w == 0.0f) continue;
-                    double l = 0.0, acc[512];
-                    for (int64_t d = 0; d < D; d++) acc[d] = 0.0;
-                    for (int64_t ic = c * C; ic < n_kv && ic < (c + 1) * C; ic++) {
-                        const float mv = mask ? ref_fp16_to_fp32(mask[iq * mask_stride + ic]) : 0.0f;
-                        if (mv == -INFINITY) continue;
-                        const uint16_t * kr = k + kvh * kv_stride_head + ic * kv_stride_pos;
-                        const uint16_t * vr = v + kvh * kv_stride_head + ic * kv_stride_pos;
-                        double a = 0.0;
-                        for (int64_t d = 0; d < D; d++) a += (double) (ref_fp16_to_fp32(kr[d]) * ref_fp16_to_fp32(qh[d]));
-                        const float s = (float) a * scale + mv;
-                        const float p = ref_expf_det(s - mcs[c]);
-                        l += (double) p;
-                        if (p == 0.0f) continue;
-                        for (int64_t d = 0; d < D; d++) acc[d] += (double) p * (double) ref_fp16_to_fp32(vr[d]);
-                    }
-                    L += (double) w * l;
-                    for (int64_t d = 0; d < D; d++) O[d] += (double) w * acc[d];
-                }
-                for (int64_t d = 0; d < D; d++) o[d] = L == 0.0 ? 0.0f : (float) (O[d] / L);
+                fa_chunked_one(qh, k + kvh * kv_stride_head, v + kvh * kv_stride_head, kv_stride_pos,
+                               mask ? mask + iq * mask_stride : NULL, o, D, n_kv, scale);
                 continue;
             }
             if (fidelity == 3) {

@@ -153,3 +153,59 @@ def test_whisper_tiny_q8_0_first_64_steps(gpu, ref):
     sess.free()
     model.free()
     w.free()
+
+
+def test_qwen3_17b_q4_K_batch8_long_context(gpu, ref):
+    """Qwen3-1.7B-shaped Q4_K decoder at batch 8, 4096-position KV cache per
+    sequence, 3000-position N(0,1) prefixes plus 8 prompt tokens.
+
+    Prefill (chunked 256 positions at a time on the device): the oracle
+    recomputes layers 0 and 1 of one sequence over all 3008 positions in one
+    pass, and both layers' K/V must match bit for bit (the second layer's
+    depends on the first's attention over the whole prefix). Decode: the
+    oracle's batched step starts from the device's KV caches after prefill,
+    and both run 64 greedy steps of all eight sequences: token IDs identical,
+    logits within 1e-2 at every step."""
+    import types
+    wl = D.WORKLOADS["qwen3-1.7b-q4_K-b8"]
+    print(f"{wl.name}: prefill {wl.n_seq} x {wl.prefix}+{wl.prompt}", flush=True)
+    w = D.QwenWeights(wl.wtype, seed=1234, **wl.shape)
+    model = D.QwenModel(w, gpu.backend)
+    sess = model.session(wl.n_seq, wl.max_positions)
+    emb, prompt = D.workload_inputs(wl, seed=77)
+    sess.prefill_embeddings(emb)
+    cur = sess.prefill_tokens(prompt)
+    n_pos = wl.prefix + wl.prompt
+    assert all(sess.position(s) == n_pos for s in range(wl.n_seq))
+
+    s = 5
+    two = types.SimpleNamespace(**{f: getattr(w.cfg, f) for f, _ in w.cfg._fields_})
+    two.n_layers = 2
+    r2 = ref.QwenRef(two, w.pointer_table(), wl.max_positions)
+    r2.forward(np.concatenate([emb[s], r2.embed(prompt[s])]))
+    for layer in range(2):
+        k, v = sess.read_kv(layer, s)
+        assert np.array_equal(k[:, :n_pos], r2.k[layer][:, :n_pos]), f"prefill K layer {layer}"
+        assert np.array_equal(v[:, :n_pos], r2.v[layer][:, :n_pos]), f"prefill V layer {layer}"
+    del r2
+    print("  prefill K/V of layers 0-1 bit-exact", flush=True)
+
+    rb = ref.QwenRefBatch(w.cfg, w.pointer_table(), wl.max_positions, wl.n_seq)
+    for q in range(wl.n_seq):
+        for layer in range(wl.shape["n_layers"]):
+            k, v = sess.read_kv(layer, q)
+            rb.k[q][layer][...] = k
+            rb.v[q][layer][...] = v
+        rb.pos[q] = n_pos
+    cur_d = cur_r = np.asarray(cur, np.int32)
+    max_dl = 0.0
+    for i in range(64):
+        cur_d, lg_d = sess.step(cur_d, want_logits=True)
+        cur_r, lg_r = rb.step(cur_r, want_logits=True)
+        max_dl = max(max_dl, float(np.abs(lg_d - lg_r).max()))
+        assert np.array_equal(cur_d, cur_r), f"step {i}: gpu {cur_d} != cpu {cur_r}"
+    print(f"  64 batched steps token-exact, max |dlogit| {max_dl:.2e}", flush=True)
+    assert max_dl < 1e-2
+    sess.free()
+    model.free()
+    w.free()
