@@ -9,7 +9,9 @@ decode step of all eight sequences through the persistent decode graph
 The timed region is K consecutive greedy steps (each step is a synchronous
 graph compute, so the region is bracketed by device synchronisation).
 
-Also reported (same run): the Qwen3-0.6B Q8_0 batch-1 decode rate, per-kernel
+Also reported (same run): the Qwen3-0.6B Q8_0 batch-1 decode rate, the
+Qwen3-1.7B Q4_K batch-8 rate after 3000-position prefixes (4096-position KV),
+the Whisper-tiny Q8_0 batch-1 rate over 1500 cross frames, per-kernel
 times of one decode step from HIP events on the backend's own stream, the
 roofline fraction of the dominant kernel (the quantized GEMV), and the CPU
 oracle's batched decode rate on the host cores from the same KV state.
@@ -47,6 +49,8 @@ def parse():
     p.add_argument("--workload", default="qwen3-0.6b-q4_K-b8")
     p.add_argument("--no-b1", action="store_true", help="skip the batch-1 Q8_0 side measurement")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--no-whisper", action="store_true", help="skip the Whisper-tiny batch-1 side measurement")
+    p.add_argument("--no-long", action="store_true", help="skip the Qwen3-1.7B long-context side measurement")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile-iters", type=int, default=20)
     p.add_argument("--sweep", action="store_true", help="per-kernel sweep of mul_mat and flash_attn_ext shapes")
@@ -139,6 +143,55 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
     model.free()
     w.free()
     return result
+
+
+def run_whisper(n_tokens: int, cpu_seconds: float):
+    """Whisper-tiny-shaped Q8_0 decoder at batch 1: cross K/V precompute from
+    1500 N(0,1) encoder frames, 4 prompt tokens, then `n_tokens` greedy steps
+    through the persistent step graph; the CPU oracle's step timed beside it."""
+    from openasr_amd import decoders as D
+    from openasr_amd import ggml as g
+
+    plugin = g.plugin()
+    shape = D.WHISPER_TINY
+    w = D.WhisperWeights(seed=4321, **shape)
+    model = D.WhisperModel(w, plugin.backend)
+    sess = model.session()
+    enc, prompt = D.whisper_inputs(shape, n_prompt=4, seed=91)
+    sess.set_encoder(enc)  # builds and warms the encoder graph
+    t0 = time.perf_counter()
+    sess.set_encoder(enc)
+    cross_ms = (time.perf_counter() - t0) * 1e3
+    tok = 0
+    for t in prompt:
+        tok = sess.step(int(t))
+    n_tokens = min(n_tokens, shape["max_positions"] - len(prompt) - 1)
+    t0 = time.perf_counter()
+    out, step_ms = sess.generate(tok, n_tokens)
+    elapsed = time.perf_counter() - t0
+    tok_s = n_tokens / elapsed
+    log(f"[bench] whisper-tiny q8_0 b1: cross K/V {cross_ms:.2f} ms, {n_tokens} greedy steps {elapsed * 1e3 / n_tokens:.3f} "
+        f"ms/step = {tok_s:.1f} tokens/s")
+    res = {"tokens_per_s": round(tok_s, 1), "ms_per_step": round(elapsed * 1e3 / n_tokens, 4), "steps": n_tokens,
+           "cross_kv_ms": round(cross_ms, 3), "cpu_tokens_per_s": None}
+    if cpu_seconds > 0:
+        from oracle import ref
+        threads = os.cpu_count() or 1
+        r = ref.WhisperRef(w.cfg, w.pointer_table(), threads=threads)
+        r.set_encoder(enc)
+        cur, n = int(prompt[0]), 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < cpu_seconds and n < shape["max_positions"] - 1:
+            cur, _ = r.step(cur)
+            n += 1
+        dt = time.perf_counter() - t0
+        res["cpu_tokens_per_s"] = round(n / dt, 2)
+        res["cpu_threads"] = threads
+        log(f"[bench] whisper cpu oracle: {n} steps in {dt:.1f}s on {threads} threads = {n / dt:.1f} tokens/s")
+    sess.free()
+    model.free()
+    w.free()
+    return res
 
 
 def cpu_baseline(w, wl, sess, tokens, seconds: float):
@@ -322,6 +375,15 @@ def main() -> int:
         r1 = run_workload("qwen3-0.6b-q8_0-b1", min(a.steps, 128), a.warmup, a.profile_iters, False, 0)
         b1 = {"tokens_per_s": round(r1["tok_s"], 1), "ms_per_step": round(r1["ms_per_step"], 4),
               "mul_mat_q8_0_gbs": round(r1["gemv_gbs"], 1)}
+    long = None
+    if not a.no_long and a.workload != "qwen3-1.7b-q4_K-b8":
+        rl = run_workload("qwen3-1.7b-q4_K-b8", min(a.steps, 64), a.warmup, max(4, a.profile_iters // 4), False, 0)
+        long = {"tokens_per_s": round(rl["tok_s"], 1), "ms_per_step": round(rl["ms_per_step"], 4),
+                "prefill_positions": rl["n_prefill"], "prefill_ms": round(rl["prefill_ms"], 1),
+                "mul_mat_q4_K_gbs": round(rl["gemv_gbs"], 1)}
+    whisper = None
+    if not a.no_whisper:
+        whisper = run_whisper(224, 0 if a.no_cpu else min(5.0, a.cpu_seconds))
     frac = main_r["gemv_gbs"] / HBM_PEAK_GBS
     # measured HBM bytes per GEMV launch (rocprofv3 FETCH_SIZE / WRITE_SIZE
     # runs of `bench.py --traffic-probe`, summarised by openasr_amd.pmc)
@@ -357,6 +419,8 @@ def main() -> int:
         "eager_step_ms": round(main_r["eager_step_ms"], 4),
         "kernels": main_r["breakdown"],
         "batch1_q8_0": b1,
+        "qwen3_1.7b_q4_K_b8_kv4096": long,
+        "whisper_tiny_q8_0_b1": whisper,
     }
     print(json.dumps(out), flush=True)
     return 0
