@@ -19,6 +19,13 @@
 // matrices are a few MB, so the whole matrix is in flight at once; the kernel
 // is latency-bound by construction, not issue-bound.
 //
+// Activation prologue (optional): the workgroup reads the f32 activations,
+// normalises them when the graph puts a norm in front of the MUL_MAT, and
+// quantizes them into LDS; the main loop then reads its A operands from LDS.
+// The first unit's weight loads are issued before the prologue, so the HBM
+// round trip of the weights overlaps it, and the norm / quantize launches
+// that would otherwise precede the GEMV disappear.
+//
 // Q4_K B-operand loads: lane (row r, group g) reads 8 bytes of nibbles at
 // qs + 32c + 8g for c = 0..3, which hold elements 8g..8g+7 of sub-block 2c
 // (low nibbles) and of sub-block 2c+1 (high nibbles); the A operand takes the
@@ -30,6 +37,7 @@
 // nn/decoder.rs:2107-2145) -- the same two f32 roundings as the unfused ops.
 #include "../mi355x_common.h"
 #include "../ops.h"
+#include "../quant_dev.h"
 
 namespace mi355x {
 
@@ -51,7 +59,291 @@ struct gemv_args {
     int64_t dst_nb1;
     const char * res;  // optional residual, same layout as dst
     int64_t res_nb1;
+    gemv_prologue pro;
 };
+
+// prologue modes (template parameter)
+constexpr int kProNone = 0;      // pre-quantized activations in global memory
+constexpr int kProQuant = 1;     // quantize f32 activations into LDS
+constexpr int kProNorm = 2;      // normalise (* w), then quantize into LDS
+constexpr int kProNormBias = 3;  // normalise, * w, + b, then quantize into LDS
+constexpr int kPadQ = 16;        // bytes of padding per staged column (LDS banks)
+
+// Staging layout: a job is one 256-element span (column j / nspan, span
+// j % nspan) held by one DPP row of 16 lanes, 16 consecutive elements per
+// lane (lane li of the row: elements 16 li .. 16 li + 15). A wave works on a
+// group of four jobs at once (one per row); wave w takes groups w, w + nw, ...
+// The normalising prologue keeps kNormGroups groups per wave in registers
+// across its statistics pass (launches give it one wave per group).
+constexpr int kNormGroups = 1;
+
+// LDS carve of the staged activations of nc columns
+struct gemv_lds {
+    int64_t q_stride;  // bytes between staged columns of quants
+    int64_t d_stride;  // floats between columns of scales
+    int64_t ss_stride;  // int16 between columns of 32-element sums
+    int64_t q_off, d_off, ss_off, part_off, stat_off, total;
+};
+
+__host__ __device__ inline int64_t round16(int64_t v) { return (v + 15) & ~(int64_t) 15; }
+
+__host__ __device__ inline gemv_lds gemv_lds_layout(int wtype, int64_t K, int nc) {
+    gemv_lds L;
+    const int64_t nspan = (K + 255) / 256;
+    L.q_stride = K + kPadQ;
+    L.d_stride = wtype == GGML_TYPE_Q4_K ? K / 256 : K / 32;
+    L.ss_stride = wtype == GGML_TYPE_Q4_K ? K / 32 : 0;
+    L.q_off = 0;
+    L.d_off = round16(L.q_off + nc * L.q_stride);
+    L.ss_off = round16(L.d_off + nc * L.d_stride * 4);
+    L.part_off = round16(L.ss_off + nc * L.ss_stride * 2);
+    L.stat_off = round16(L.part_off + 2 * nc * nspan * 8);
+    L.total = round16(L.stat_off + nc * 8);
+    return L;
+}
+
+// DPP moves inside a row of 16 lanes (VALU operations, no LDS traffic):
+// xor 1 and xor 2 within quads, rotations by 4 and 8 across the row
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppRor4 = 0x124, kDppRor8 = 0x128;
+
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+    return __int_as_float(dpp_i<CTRL>(__float_as_int(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+    return __hiloint2double(dpp_i<CTRL>(__double2hiint(v)), dpp_i<CTRL>(__double2loint(v)));
+}
+
+// f64 sum over the 16 lanes of a row (lane 0's value is the one used)
+__device__ __forceinline__ double row16_sum(double v) {
+    v += dpp_d<kDppXor1>(v);
+    v += dpp_d<kDppXor2>(v);
+    v += dpp_d<kDppRor4>(v);
+    v += dpp_d<kDppRor8>(v);
+    return v;
+}
+
+// signed value of largest magnitude over the row, first element on ties
+template <int CTRL>
+__device__ __forceinline__ void row16_best_step(float & ab, float & best, int & idx) {
+    const float oab = dpp_f<CTRL>(ab), obest = dpp_f<CTRL>(best);
+    const int oidx = dpp_i<CTRL>(idx);
+    if (oab > ab || (oab == ab && oidx < idx)) {
+        ab = oab;
+        best = obest;
+        idx = oidx;
+    }
+}
+
+__device__ __forceinline__ float elem16(const float4 (&x)[4], int t) {
+    const float4 & v = x[t >> 2];
+    return (t & 3) == 0 ? v.x : (t & 3) == 1 ? v.y : (t & 3) == 2 ? v.z : v.w;
+}
+
+// Quantize one row's span into LDS. Q8_K (quantize_row_q8_K_ref): the
+// signed value of largest magnitude, first one on ties, sets iscale =
+// -127/max, quants min(127, rne(iscale x)), d = 1/iscale, sums of each 32
+// quants (two lanes). Q8_0 (x86 ggml-cpu rule): per 32 elements (two lanes)
+// d = amax/127 stored as f16, quants rne(x * 127/amax). Same arithmetic as
+// quantize_q8_K_wave / quantize_q8_0_group.
+template <int WT>
+__device__ __forceinline__ void stage_quantize(const float4 (&x)[4], bool live, int col, int sp, int li, int64_t K,
+                                               const gemv_lds & L, char * smem) {
+    int8_t * s_q = (int8_t *) (smem + L.q_off);
+    float * s_d = (float *) (smem + L.d_off);
+    int16_t * s_ss = (int16_t *) (smem + L.ss_off);
+    const int64_t e = (int64_t) sp * 256 + 16 * li;  // first element of this lane
+    int qv[16];
+    if constexpr (WT == GGML_TYPE_Q4_K) {
+        float best = x[0].x, ab = fabsf(x[0].x);
+        int idx = 16 * li;
+#pragma unroll
+        for (int t = 1; t < 16; t++) {
+            const float v = elem16(x, t);
+            if (fabsf(v) > ab) {
+                ab = fabsf(v);
+                best = v;
+                idx = 16 * li + t;
+            }
+        }
+        row16_best_step<kDppXor1>(ab, best, idx);
+        row16_best_step<kDppXor2>(ab, best, idx);
+        row16_best_step<kDppRor4>(ab, best, idx);
+        row16_best_step<kDppRor8>(ab, best, idx);
+        const float iscale = ab == 0.0f ? 0.0f : -127.0f / best;
+        int ssum = 0;
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            qv[t] = ab == 0.0f ? 0 : min(127, __float2int_rn(iscale * elem16(x, t)));
+            ssum += qv[t];
+        }
+        ssum += dpp_i<kDppXor1>(ssum);
+        if (live) {
+            if ((li & 1) == 0) s_ss[col * L.ss_stride + e / 32] = (int16_t) ssum;
+            if (li == 0) s_d[col * L.d_stride + sp] = ab == 0.0f ? 0.0f : 1.0f / iscale;
+        }
+    } else {
+        float amax = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 16; t++) amax = fmaxf(amax, fabsf(elem16(x, t)));
+        amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
+        const float dd = amax / 127.0f;
+        const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+#pragma unroll
+        for (int t = 0; t < 16; t++) qv[t] = __float2int_rn(elem16(x, t) * id);
+        live = live && e < K;  // Q8_0 spans may end early; whole lane pairs drop out
+        if (live && (li & 1) == 0) s_d[col * L.d_stride + e / 32] = round_to_half(dd);
+    }
+    if (live) {
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            w[j] = (uint32_t) (qv[4 * j] & 0xFF) | ((uint32_t) (qv[4 * j + 1] & 0xFF) << 8) |
+                   ((uint32_t) (qv[4 * j + 2] & 0xFF) << 16) | ((uint32_t) (qv[4 * j + 3] & 0xFF) << 24);
+        }
+        *(uint4 *) (s_q + col * L.q_stride + e) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+}
+
+// load this lane's 16 elements of job `job` (zeros outside the job range)
+__device__ __forceinline__ bool stage_load(const gemv_args & a, int n0, int jobs, int nspan, int job, int li,
+                                           float4 (&x)[4]) {
+    const int col = job / nspan, sp = job - col * nspan;
+    const int64_t e = (int64_t) sp * 256 + 16 * li;
+    const bool ok = job < jobs && e < a.K;
+    // clamped address, unconditional load: keeps the loads of a group in flight together
+    const float * src = (const float *) ((const char *) a.pro.x + (int64_t) (n0 + (ok ? col : 0)) * a.pro.x_nb1) +
+                        (ok ? e : 0);
+#pragma unroll
+    for (int j = 0; j < 4; j++) x[j] = ((const float4 *) src)[j];
+    if (!ok) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    return ok;
+}
+
+// quantize-only staging: each wave streams its groups, one group's loads in flight at a time
+template <int WT>
+__device__ __forceinline__ void gemv_stage_quant(const gemv_args & a, int n0, int nc, char * smem) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int row = lane >> 4, li = lane & 15;
+    const int64_t K = a.K;
+    const int nspan = (int) ((K + 255) / 256);
+    const int jobs = nc * nspan;
+    const int groups = (jobs + 3) / 4;
+    const gemv_lds L = gemv_lds_layout(WT, K, nc);
+    for (int gi = wave; gi < groups; gi += 2 * nw) {
+        // two groups per iteration, both loads issued before either is quantized
+        float4 x0[4], x1[4];
+        const int j0 = 4 * gi + row, j1 = 4 * (gi + nw) + row;
+        const bool ok0 = stage_load(a, n0, jobs, nspan, j0, li, x0);
+        const bool ok1 = stage_load(a, n0, jobs, nspan, j1, li, x1);
+        stage_quantize<WT>(x0, ok0, j0 / nspan, j0 % nspan, li, K, L, smem);
+        if (gi + nw < groups) stage_quantize<WT>(x1, ok1, j1 / nspan, j1 % nspan, li, K, L, smem);
+    }
+    __syncthreads();
+}
+
+// normalising staging: the statistics are f64 sums of the elements (layer
+// norm) and of the centred squares -- per lane in element order, over the
+// row by DPP, per column over the spans in order -- then
+// mean = sum / K, scale = 1 / sqrt(var + eps); the normalised value is
+// ((x - mean) * scale) * w (+ b), the roundings of NORM / RMS_NORM, MUL, ADD
+template <int WT, bool BIAS>
+__device__ __forceinline__ void gemv_stage_norm(const gemv_args & a, int n0, int nc, char * smem) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int row = lane >> 4, li = lane & 15;
+    const int64_t K = a.K;
+    const int nspan = (int) ((K + 255) / 256);
+    const int jobs = nc * nspan;
+    const gemv_lds L = gemv_lds_layout(WT, K, nc);
+    double * s_part = (double *) (smem + L.part_off);
+    float2 * s_stat = (float2 *) (smem + L.stat_off);
+    const gemv_prologue & p = a.pro;
+    float4 x[kNormGroups][4], w[kNormGroups][4], b[BIAS ? kNormGroups : 1][4];
+    bool ok[kNormGroups];
+#pragma unroll
+    for (int k = 0; k < kNormGroups; k++) {
+        const int job = 4 * (wave + nw * k) + row;
+        ok[k] = stage_load(a, n0, jobs, nspan, job, li, x[k]);
+        const int64_t e = ok[k] ? (int64_t) (job % nspan) * 256 + 16 * li : 0;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            w[k][j] = p.w ? *(const float4 *) (p.w + e + 4 * j) : make_float4(1.f, 1.f, 1.f, 1.f);
+            if constexpr (BIAS) b[k][j] = *(const float4 *) (p.b + e + 4 * j);
+        }
+    }
+    const double n = (double) K;
+    if (p.norm == 1) {
+#pragma unroll
+        for (int k = 0; k < kNormGroups; k++) {
+            double s = 0.0;
+#pragma unroll
+            for (int t = 0; t < 16; t++) s += (double) elem16(x[k], t);
+            s = row16_sum(s);
+            const int job = 4 * (wave + nw * k) + row;
+            if (li == 0 && job < jobs) s_part[job] = s;
+        }
+        __syncthreads();
+        if ((int) threadIdx.x < nc) {
+            double t = 0.0;
+            for (int sp = 0; sp < nspan; sp++) t += s_part[threadIdx.x * nspan + sp];
+            s_stat[threadIdx.x].x = (float) (t / n);
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < kNormGroups; k++) {
+        const int job = 4 * (wave + nw * k) + row;
+        const float mean = p.norm == 1 && ok[k] ? s_stat[job / nspan].x : 0.0f;
+        double s2 = 0.0;
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const float v = ok[k] ? elem16(x[k], t) - mean : 0.0f;
+            s2 += (double) (v * v);
+        }
+        s2 = row16_sum(s2);
+        if (li == 0 && job < jobs) s_part[jobs + job] = s2;
+    }
+    __syncthreads();
+    if ((int) threadIdx.x < nc) {
+        double t2 = 0.0;
+        for (int sp = 0; sp < nspan; sp++) t2 += s_part[jobs + threadIdx.x * nspan + sp];
+        const float var = (float) (t2 / n);
+        s_stat[threadIdx.x].y = 1.0f / sqrtf(var + p.eps);
+        if (p.norm != 1) s_stat[threadIdx.x].x = 0.0f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kNormGroups; k++) {
+        const int job = 4 * (wave + nw * k) + row;
+        if (4 * (wave + nw * k) >= jobs) break;  // uniform: no row of the wave has a job
+        const int col = ok[k] ? job / nspan : 0;
+        const float2 st = s_stat[col];
+        float4 v[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            v[j].x = ((x[k][j].x - st.x) * st.y) * w[k][j].x;
+            v[j].y = ((x[k][j].y - st.x) * st.y) * w[k][j].y;
+            v[j].z = ((x[k][j].z - st.x) * st.y) * w[k][j].z;
+            v[j].w = ((x[k][j].w - st.x) * st.y) * w[k][j].w;
+            if constexpr (BIAS) {
+                v[j].x += b[k][j].x;
+                v[j].y += b[k][j].y;
+                v[j].z += b[k][j].z;
+                v[j].w += b[k][j].w;
+            }
+        }
+        stage_quantize<WT>(v, ok[k], col, job % nspan, li, K, L, smem);
+    }
+    __syncthreads();
+}
 
 // per-lane scale / min of sub-blocks 0..7 of one Q4_K super-block header
 __device__ __forceinline__ void q4k_scales(const uint4 & hdr, int * sc, int * mn) {
@@ -107,8 +399,10 @@ __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4
 }
 
 // waves of the workgroup take super-blocks round-robin (wave w: sb = w,
-// w + nw, ...); each super-block's loads are issued together
+// w + nw, ...); each super-block's weight loads are issued one unit ahead
+template <int PRO>
 __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
+    extern __shared__ __align__(16) char smem[];
     __shared__ double s_red[16][64][4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int half = a.W2 ? nw / 2 : nw;
@@ -117,28 +411,60 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
     const int r = lane & 15, g = lane >> 4;
     const int64_t tile = blockIdx.x;
     const int n0 = (int) blockIdx.y * 16;
+    const int nc = min(16, a.N - n0);
     const int64_t nsb = a.K / 256;
     const int64_t row = tile * 16 + r;
     const char * wrow = (second ? a.W2 : a.W) + row * a.row_bytes;
-    const bool a_ok = n0 + r < a.N;  // this lane's A-operand column
-    const int8_t * acol = a.aq + (int64_t) (n0 + r) * a.K;
-    double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int64_t sb = wv; sb < nsb; sb += half) {
+    uint4 hdr = make_uint4(0, 0, 0, 0);
+    long q[4] = {0, 0, 0, 0};
+    int64_t sb = wv;
+    if (sb < nsb) {
         const char * blk = wrow + sb * 144;
-        const uint4 hdr = *(const uint4 *) blk;
-        long q[4], af[8];
-        float ad[4];
-        uint4 ss[4];
+        hdr = *(const uint4 *) blk;
 #pragma unroll
         for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
+    }
+    // activation operands: LDS after the prologue, else the global buffers
+    const int8_t * aq;
+    const float * adp;
+    const int16_t * asp;
+    int64_t q_stride, d_stride, ss_stride;
+    int c0;  // column index of the chunk's first column in the operand arrays
+    if constexpr (PRO != kProNone) {
+        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q4_K>(a, n0, nc, smem);
+        else gemv_stage_norm<GGML_TYPE_Q4_K, PRO == kProNormBias>(a, n0, nc, smem);
+        const gemv_lds L = gemv_lds_layout(GGML_TYPE_Q4_K, a.K, nc);
+        aq = (const int8_t *) (smem + L.q_off);
+        adp = (const float *) (smem + L.d_off);
+        asp = (const int16_t *) (smem + L.ss_off);
+        q_stride = L.q_stride;
+        d_stride = L.d_stride;
+        ss_stride = L.ss_stride;
+        c0 = 0;
+    } else {
+        aq = a.aq;
+        adp = a.ad;
+        asp = a.ass;
+        q_stride = a.K;
+        d_stride = nsb;
+        ss_stride = a.K / 32;
+        c0 = n0;
+    }
+    const bool a_ok = r < nc;  // this lane's A-operand column
+    const int8_t * acol = aq + (int64_t) (c0 + (a_ok ? r : 0)) * q_stride;
+    double acc[4] = {0.0, 0.0, 0.0, 0.0};
+    for (; sb < nsb; sb += half) {
+        long af[8];
+        float ad[4];
+        uint4 ss[4];
 #pragma unroll
         for (int j = 0; j < 8; j++) af[j] = a_ok ? *(const long *) (acol + sb * 256 + 32 * j + 8 * g) : 0;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int n = n0 + 4 * g + i;
-            const bool ok = n < a.N;
-            ad[i] = ok ? a.ad[(int64_t) n * nsb + sb] : 0.0f;
-            ss[i] = ok ? *(const uint4 *) (a.ass + ((int64_t) n * nsb + sb) * 8) : make_uint4(0, 0, 0, 0);
+            const int n = 4 * g + i;
+            const bool ok = n < nc;
+            ad[i] = ok ? adp[(int64_t) (c0 + n) * d_stride + sb] : 0.0f;
+            ss[i] = ok ? *(const uint4 *) (asp + (int64_t) (c0 + n) * ss_stride + sb * 8) : make_uint4(0, 0, 0, 0);
         }
         int sc[8], mn[8];
         q4k_scales(hdr, sc, mn);
@@ -148,13 +474,20 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
             const long lo = q[c] & 0x0F0F0F0F0F0F0F0FL;
             const long hi = (q[c] >> 4) & 0x0F0F0F0F0F0F0F0FL;
             const v4i z = {0, 0, 0, 0};
-            const v4i c0 = mfma_i8(af[2 * c], lo, z);
-            const v4i c1 = mfma_i8(af[2 * c + 1], hi, z);
+            const v4i c0v = mfma_i8(af[2 * c], lo, z);
+            const v4i c1v = mfma_i8(af[2 * c + 1], hi, z);
 #pragma unroll
-            for (int i = 0; i < 4; i++) isum[i] += sc[2 * c] * c0[i] + sc[2 * c + 1] * c1[i];
+            for (int i = 0; i < 4; i++) isum[i] += sc[2 * c] * c0v[i] + sc[2 * c + 1] * c1v[i];
         }
         const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
         const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
+        // the next unit's weights go out before this unit's f64 epilogue
+        if (sb + half < nsb) {
+            const char * blk = wrow + (sb + half) * 144;
+            hdr = *(const uint4 *) blk;
+#pragma unroll
+            for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
+        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t w4[4] = {ss[i].x, ss[i].y, ss[i].z, ss[i].w};
@@ -175,9 +508,12 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
 
 // Q8_0 weights in the row-split layout [K quants][K/32 f16 scales]; the waves
 // take groups of 8 blocks round-robin, each group's loads issued together
+// (the first group's weights before the prologue)
 constexpr int kQ8Group = 8;
 
+template <int PRO>
 __global__ __launch_bounds__(1024) void k_gemv_q8_0(gemv_args a) {
+    extern __shared__ __align__(16) char smem[];
     __shared__ double s_red[16][64][4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int half = a.W2 ? nw / 2 : nw;
@@ -186,33 +522,70 @@ __global__ __launch_bounds__(1024) void k_gemv_q8_0(gemv_args a) {
     const int r = lane & 15, g = lane >> 4;
     const int64_t tile = blockIdx.x;
     const int n0 = (int) blockIdx.y * 16;
+    const int nc = min(16, a.N - n0);
     const int64_t nblk = a.K / 32;
     const int64_t row = tile * 16 + r;
     const char * wrow = (second ? a.W2 : a.W) + row * a.row_bytes;
     const uint16_t * wsc = (const uint16_t *) (wrow + a.K);
-    const bool a_ok = n0 + r < a.N;
-    const int8_t * acol = a.aq + (int64_t) (n0 + r) * a.K;
+    long q[kQ8Group];
+    uint16_t ds[kQ8Group];
+    int64_t b0 = (int64_t) wv * kQ8Group;
+#pragma unroll
+    for (int u = 0; u < kQ8Group; u++) {
+        const int64_t b = b0 + u;
+        const bool ok = b < nblk;
+        q[u] = ok ? *(const long *) (wrow + b * 32 + 8 * g) : 0;
+        ds[u] = ok ? wsc[b] : 0;
+    }
+    const int8_t * aq;
+    const float * adp;
+    int64_t q_stride, d_stride;
+    int c0;
+    if constexpr (PRO != kProNone) {
+        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q8_0>(a, n0, nc, smem);
+        else gemv_stage_norm<GGML_TYPE_Q8_0, PRO == kProNormBias>(a, n0, nc, smem);
+        const gemv_lds L = gemv_lds_layout(GGML_TYPE_Q8_0, a.K, nc);
+        aq = (const int8_t *) (smem + L.q_off);
+        adp = (const float *) (smem + L.d_off);
+        q_stride = L.q_stride;
+        d_stride = L.d_stride;
+        c0 = 0;
+    } else {
+        aq = a.aq;
+        adp = a.ad;
+        q_stride = a.K;
+        d_stride = nblk;
+        c0 = n0;
+    }
+    const bool a_ok = r < nc;
+    const int8_t * acol = aq + (int64_t) (c0 + (a_ok ? r : 0)) * q_stride;
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
-    for (int64_t b0 = (int64_t) wv * kQ8Group; b0 < nblk; b0 += (int64_t) half * kQ8Group) {
-        long q[kQ8Group], af[kQ8Group];
-        uint16_t ds[kQ8Group];
+    const int64_t first = b0;
+    for (; b0 < nblk; b0 += (int64_t) half * kQ8Group) {
+        if (b0 != first) {
+#pragma unroll
+            for (int u = 0; u < kQ8Group; u++) {
+                const int64_t b = b0 + u;
+                const bool ok = b < nblk;
+                q[u] = ok ? *(const long *) (wrow + b * 32 + 8 * g) : 0;
+                ds[u] = ok ? wsc[b] : 0;
+            }
+        }
+        long af[kQ8Group];
         float4 ad[4][kQ8Group / 4];
 #pragma unroll
         for (int u = 0; u < kQ8Group; u++) {
             const int64_t b = b0 + u;
-            const bool ok = b < nblk;
-            q[u] = ok ? *(const long *) (wrow + b * 32 + 8 * g) : 0;
-            af[u] = ok && a_ok ? *(const long *) (acol + b * 32 + 8 * g) : 0;
-            ds[u] = ok ? wsc[b] : 0;
+            af[u] = b < nblk && a_ok ? *(const long *) (acol + b * 32 + 8 * g) : 0;
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int n = n0 + 4 * g + i;
+            const int n = 4 * g + i;
 #pragma unroll
             for (int v = 0; v < kQ8Group / 4; v++) {
                 const int64_t b = b0 + 4 * v;
-                ad[i][v] = n < a.N && b < nblk ? *(const float4 *) (a.ad + (int64_t) n * nblk + b)
-                                               : make_float4(0.f, 0.f, 0.f, 0.f);
+                ad[i][v] = n < nc && b < nblk ? *(const float4 *) (adp + (int64_t) (c0 + n) * d_stride + b)
+                                              : make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
 #pragma unroll
@@ -241,9 +614,60 @@ bool gemv_mfma_supported(int wtype, int64_t M, int64_t K) {
     return false;
 }
 
+namespace {
+
+int64_t gemv_units(int wtype, int64_t K) { return wtype == GGML_TYPE_Q4_K ? K / 256 : (K / 32 + kQ8Group - 1) / kQ8Group; }
+
+// waves of a launch: one per unit up to 16 (8 per matrix with W2); with a
+// prologue, up to one staging group (four spans) per wave as well -- every
+// wave stages, W2's included
+int gemv_waves(int wtype, int64_t K, int64_t N, bool dual, int pro) {
+    const int64_t units = gemv_units(wtype, K);
+    const int64_t per = dual ? 8 : 16;
+    const int64_t mats = dual ? 2 : 1;
+    int64_t w = units < per ? units : per;
+    if (pro != kProNone) {
+        const int64_t nc = N < 16 ? N : 16;
+        const int64_t groups = (nc * ((K + 255) / 256) + 3) / 4;
+        const int64_t need = groups < 16 ? groups : 16;
+        const int64_t wm = (need + mats - 1) / mats;
+        if (w < wm) w = wm;
+    }
+    return (int) (w * mats);
+}
+
+template <int PRO>
+void launch_kernel(int wtype, const dim3 & grid, const dim3 & block, size_t lds, hipStream_t stream,
+                   const gemv_args & a) {
+    if (lds > 48 * 1024) {
+        // staged columns beyond the default dynamic-LDS limit: raise it once per kernel
+        static bool raised[2] = {false, false};
+        const int idx = wtype == GGML_TYPE_Q4_K ? 0 : 1;
+        if (!raised[idx]) {
+            const void * fn = wtype == GGML_TYPE_Q4_K ? (const void *) k_gemv_q4_K<PRO> : (const void *) k_gemv_q8_0<PRO>;
+            MI_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 32768));
+            raised[idx] = true;
+        }
+    }
+    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_gemv_q4_K<PRO>, grid, block, lds, stream, a);
+    else hipLaunchKernelGGL(k_gemv_q8_0<PRO>, grid, block, lds, stream, a);
+}
+
+}  // namespace
+
+bool gemv_prologue_supported(int wtype, int64_t M, int64_t K, int64_t N, bool norm) {
+    if (!gemv_mfma_supported(wtype, M, K) || N < 1) return false;
+    const int64_t nc = N < 16 ? N : 16;
+    const int64_t groups = (nc * ((K + 255) / 256) + 3) / 4;
+    // the normalising prologue holds at most kNormGroups groups per wave, 16 waves
+    if (norm && groups > 16 * kNormGroups) return false;
+    // LDS: the staged columns plus the 32 KB reduction buffer within 160 KB
+    return gemv_lds_layout(wtype, K, (int) nc).total + 32768 <= 160 * 1024;
+}
+
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const char * res,
-                      int64_t res_nb1, const char * W2) {
+                      int64_t res_nb1, const char * W2, const gemv_prologue * pro) {
     (void) n_cu;
     gemv_args a;
     a.W = W;
@@ -259,12 +683,17 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
     a.dst_nb1 = dst_nb1;
     a.res = res;
     a.res_nb1 = res_nb1;
+    const int mode = !pro ? kProNone : pro->norm < 0 ? kProQuant : pro->b ? kProNormBias : kProNorm;
+    if (pro) a.pro = *pro;
     const dim3 grid((unsigned) (M / 16), (unsigned) ((N + 15) / 16));
-    const int64_t units = wtype == GGML_TYPE_Q4_K ? K / 256 : (K / 32 + kQ8Group - 1) / kQ8Group;
-    const int64_t per = W2 ? 8 : 16;  // waves per matrix
-    const unsigned waves = (unsigned) ((units < per ? units : per) * (W2 ? 2 : 1));
-    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_gemv_q4_K, grid, dim3(64 * waves), 0, stream, a);
-    else hipLaunchKernelGGL(k_gemv_q8_0, grid, dim3(64 * waves), 0, stream, a);
+    const dim3 block(64 * gemv_waves(wtype, K, N, W2 != nullptr, mode));
+    const size_t lds = mode == kProNone ? 0 : (size_t) gemv_lds_layout(wtype, K, (int) (N < 16 ? N : 16)).total;
+    switch (mode) {
+        case kProNone: launch_kernel<kProNone>(wtype, grid, block, lds, stream, a); break;
+        case kProQuant: launch_kernel<kProQuant>(wtype, grid, block, lds, stream, a); break;
+        case kProNorm: launch_kernel<kProNorm>(wtype, grid, block, lds, stream, a); break;
+        default: launch_kernel<kProNormBias>(wtype, grid, block, lds, stream, a); break;
+    }
 }
 
 }  // namespace mi355x

@@ -21,6 +21,7 @@
 #include <cstring>
 #include <unordered_map>
 
+#include "ggml_host.h"
 #include "ops.h"
 
 namespace mi355x {
@@ -255,6 +256,61 @@ struct planner {
         return false;
     }
 
+    // norms whose launch is skipped: the GEMVs consuming their output
+    // normalise and quantize in their activation prologue (norm output -> it)
+    std::unordered_map<const ggml_tensor *, gemv_prologue> pro_norm;
+
+    // at most this many 16-row tiles take a prologue: every workgroup stages
+    // the activations itself, so the redundant staging grows with the grid
+    static constexpr int64_t kProMaxTiles = 512;
+
+    static bool use_mmq(int wtype, int64_t M, int64_t K, int64_t N) {
+        return mmq_supported(wtype, M, K) && N > 16 && (N > 64 || M >= 8192);
+    }
+
+    // the MUL_MAT c (quantized weights, activations of K x N) runs as an MFMA
+    // GEMV that can take an activation prologue
+    bool prologue_gemv(const ggml_tensor * c, bool norm) const {
+        const ggml_tensor * w = c->src[0];
+        const int64_t K = w->ne[0], M = w->ne[1];
+        const int64_t N = c->src[1]->ne[1] * c->src[1]->ne[2] * c->src[1]->ne[3];
+        return !use_mmq(w->type, M, K, N) && gemv_mfma_supported(w->type, M, K) && M / 16 <= kProMaxTiles &&
+               gemv_prologue_supported(w->type, M, K, N, norm);
+    }
+
+    static bool aligned16(const void * p) { return ((uintptr_t) p & 15) == 0; }
+
+    // an f32 view whose columns the prologue can read: unit stride, columns
+    // at a uniform 16-byte-aligned stride
+    static bool prologue_view(const tview & v) {
+        if (v.nb[0] != 4 || !aligned16(v.data) || v.nb[1] % 16 != 0) return false;
+        if (v.ne[2] > 1 && v.nb[2] != v.nb[1] * v.ne[1]) return false;
+        if (v.ne[3] > 1 && v.nb[3] != v.nb[2] * v.ne[2]) return false;
+        return true;
+    }
+
+    // bytes [lo, hi) a view spans
+    static void view_span(const tview & v, int64_t elem, uintptr_t & lo, uintptr_t & hi) {
+        int64_t last = elem;
+        for (int d = 0; d < 4; d++) last += (v.ne[d] - 1) * v.nb[d];
+        lo = (uintptr_t) v.data;
+        hi = lo + (uintptr_t) last;
+    }
+
+    // no node between positions i and j (inclusive) that may run writes into
+    // the bytes of view v
+    bool untouched_until(const tview & v, int i, int j) const {
+        uintptr_t lo, hi;
+        view_span(v, 4, lo, hi);
+        for (int k = i + 1; k <= j && k < cg->n_nodes; k++) {
+            const ggml_tensor * n = cg->nodes[k];
+            if (is_view_op(n->op) || n->op == GGML_OP_NONE || !n->data) continue;
+            const uintptr_t a = (uintptr_t) n->data, b = a + ggml_nbytes(n);
+            if (a < hi && lo < b) return false;
+        }
+        return true;
+    }
+
     bool plan();
     bool plan_mul_mat(int i, const ggml_tensor * t);
     // t is available before node i runs: a leaf, or a node planned earlier
@@ -283,15 +339,32 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         const int64_t row_bytes = (int64_t) w->nb[1];
         act_need = std::max(act_need, act_bytes(wtype, K, N));
         const bool reuse = act_src == x && act_wtype == wtype;
-        act_src = x;
-        act_wtype = wtype;
         backend_state * b = be;
         const int ncu = n_cu;
         char * dst = (char *) t->data;
         int64_t dst_nb1 = (int64_t) t->nb[1];
         // the tile GEMM once the columns outgrow a few GEMV chunks (earlier for tall matrices)
-        const bool wide = mmq_supported(wtype, M, K) && N > 16 && (N > 64 || M >= 8192);
+        const bool wide = use_mmq(wtype, M, K, N);
         const bool mfma = !wide && gemv_mfma_supported(wtype, M, K);
+        // activation prologue: the norm in front (planned by plan_norm), or
+        // the quantization of f32 activations no earlier step quantized
+        bool has_pro = false;
+        gemv_prologue pro;
+        auto pn = pro_norm.find(x);
+        if (pn != pro_norm.end()) {
+            if (!mfma || !prologue_gemv(t, true)) return fail(t, "normalising prologue on a launch that cannot take it");
+            pro = pn->second;
+            has_pro = true;
+        } else if (!reuse && mfma && x->type == GGML_TYPE_F32 && prologue_view(xv) && prologue_gemv(t, false)) {
+            pro.x = (const float *) xv.data;
+            pro.x_nb1 = xv.nb[1];
+            has_pro = true;
+        }
+        if (!has_pro) {
+            // the act region now holds x's quantization
+            act_src = x;
+            act_wtype = wtype;
+        }
         // SwiGLU: MUL_MAT(gate, x) -> SILU -> MUL with MUL_MAT(up, x) of the
         // same shape becomes one launch over both matrices
         const char * W2 = nullptr;
@@ -334,7 +407,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 produced = add;
             }
         }
-        if (!reuse) {
+        if (!reuse && !has_pro) {
             add_step(
                 [=](hipStream_t s) {
                     act_buffers act = act_carve(wtype, act_base(b), K, N);
@@ -347,7 +420,8 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 act_buffers act = act_carve(wtype, act_base(b), K, N);
                 if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
                 else if (mfma)
-                    launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1, W2);
+                    launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1, W2,
+                                     has_pro ? &pro : nullptr);
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
             produced, W2 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")
@@ -451,6 +525,31 @@ bool planner::plan_norm(int i, const ggml_tensor * t) {
     // when only quantized MUL_MATs read the result, the norm kernel also
     // writes their quantized activations (they then skip their quantize step)
     int qt = quant_consumers(out, i + 1);
+    if (qt >= 0 && !(out->flags & GGML_TENSOR_FLAG_OUTPUT) && prologue_view(av) && av.ne[0] == out->ne[0] &&
+        (!hw || aligned16(wt->data)) && (!hb || aligned16(bt->data))) {
+        // every consumer a prologue GEMV, and the norm's input still intact
+        // when the last of them runs
+        bool ok = true;
+        int last = i;
+        for (int j = i + 1; j < cg->n_nodes && ok; j++) {
+            const ggml_tensor * c = cg->nodes[j];
+            if (c->op == GGML_OP_MUL_MAT && c->src[1] == out) {
+                ok = prologue_gemv(c, true);
+                last = j;
+            }
+        }
+        if (ok && last > i && untouched_until(av, i, last)) {
+            gemv_prologue p;
+            p.x = (const float *) av.data;
+            p.x_nb1 = av.nb[1];
+            p.w = hw ? (const float *) wt->data : nullptr;
+            p.b = hb ? (const float *) bt->data : nullptr;
+            p.eps = eps;
+            p.norm = mode;
+            pro_norm[out] = p;
+            return true;
+        }
+    }
     if (qt >= 0 && !norm_rows_supported(dv, av, hw ? &wv : nullptr, hb ? &bv : nullptr)) qt = -1;
     const int64_t K = out->ne[0], N = out->ne[1] * out->ne[2] * out->ne[3];
     if (qt >= 0) act_need = std::max(act_need, act_bytes(qt, K, N));
@@ -733,8 +832,8 @@ enum ggml_status map_error(hipError_t e) {
 
 void release_graph_cache(backend_state * be) {
     for (cache_entry & c : be->cache) {
-        if (c.exec) hipGraphExecDestroy(c.exec);
-        if (c.graph) hipGraphDestroy(c.graph);
+        if (c.exec) (void) hipGraphExecDestroy(c.exec);
+        if (c.graph) (void) hipGraphDestroy(c.graph);
     }
     be->cache.clear();
 }
@@ -754,8 +853,8 @@ static cache_entry * new_entry(backend_state * be, uint64_t key) {
             if (be->cache[i].last_use < be->cache[victim].last_use) victim = i;
         }
         cache_entry & v = be->cache[victim];
-        if (v.exec) hipGraphExecDestroy(v.exec);
-        if (v.graph) hipGraphDestroy(v.graph);
+        if (v.exec) (void) hipGraphExecDestroy(v.exec);
+        if (v.graph) (void) hipGraphDestroy(v.graph);
         be->cache.erase(be->cache.begin() + (long) victim);
     }
     cache_entry e;

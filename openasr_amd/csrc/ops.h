@@ -22,13 +22,32 @@ act_buffers act_carve(int wtype, char * base, int64_t K, int64_t ncols);
 void launch_mmv(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                 int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
 
+// Activation prologue of the MFMA GEMV: instead of reading pre-quantized
+// activations, every workgroup reads the f32 activations x (column stride
+// x_nb1 bytes), optionally normalises each column (RMS_NORM or NORM, then
+// * w, + b -- the ops the graph applies before the MUL_MAT) and quantizes
+// them into LDS with the same arithmetic as the stand-alone norm and
+// quantize kernels.
+struct gemv_prologue {
+    const float * x = nullptr;
+    int64_t x_nb1 = 0;
+    const float * w = nullptr;
+    const float * b = nullptr;
+    float eps = 0.0f;
+    int norm = -1;  // -1: quantize only; 0: RMS norm; 1: layer norm
+};
+
 // MFMA GEMV for the decode step (16-column chunks), M % 16 == 0; res (same
 // column layout as dst, stride res_nb1) is added to the result when non-null;
-// with W2 (same shape and type as W) the result is silu(W x) * (W2 x)
+// with W2 (same shape and type as W) the result is silu(W x) * (W2 x). With a
+// prologue, act is not read.
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K);
+// whether a launch of this shape can take the activation prologue
+bool gemv_prologue_supported(int wtype, int64_t M, int64_t K, int64_t N, bool norm);
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu,
-                      const char * res = nullptr, int64_t res_nb1 = 0, const char * W2 = nullptr);
+                      const char * res = nullptr, int64_t res_nb1 = 0, const char * W2 = nullptr,
+                      const gemv_prologue * pro = nullptr);
 
 // MFMA int8 GEMM for wider N (prefill)
 bool mmq_supported(int wtype, int64_t M, int64_t K);

@@ -75,6 +75,50 @@ def test_mul_mat_quantized(ggml, gpu, ref, wname, m, k, n):
     G.free()
 
 
+NORM_MM_CASES = [
+    # norm, weights, M, K, N
+    ("rms", "q4_K", 4096, 1024, 8), ("rms", "q4_K", 4096, 2048, 8), ("rms", "q4_K", 1024, 1024, 13),
+    ("rms", "q4_K", 3072, 1024, 20), ("rms", "q8_0", 4096, 1024, 1), ("rms", "q8_0", 1024, 1024, 8),
+    ("layer", "q8_0", 384, 384, 1), ("layer", "q8_0", 1536, 384, 3), ("layer", "q4_K", 1024, 1024, 2),
+]
+
+
+@pytest.mark.parametrize("norm,wname,m,k,n", NORM_MM_CASES)
+def test_norm_then_mul_mat_prologue(ggml, gpu, ref, norm, wname, m, k, n):
+    """RMS_NORM / NORM -> MUL(w) (-> ADD(b)) -> two MUL_MATs reading the
+    normalised activations: the norm launch is folded into both GEMVs'
+    activation prologue (no norm step in the plan), results bit-exact"""
+    wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
+    print(f"{norm}_norm -> mul_mat {wname} M={m} K={k} N={n}", flush=True)
+    x = (RNG.standard_normal((n, k)) * 1.5 + 0.3).astype(np.float32)
+    wn = RNG.standard_normal(k).astype(np.float32)
+    bn = RNG.standard_normal(k).astype(np.float32) * 0.1
+    wq1 = ggml.quantize(wt, ggml.synth_normal(12, m + k, m * k, 0.0, 0.02).reshape(m, k))
+    wq2 = ggml.quantize(wt, ggml.synth_normal(13, m + k, m * k, 0.0, 0.02).reshape(m, k))
+    G = ggml.Graph()
+    X = G.new(ggml.F32, k, n)
+    WN = G.new(ggml.F32, k, weight=True)
+    BN = G.new(ggml.F32, k, weight=True)
+    W1 = G.new(wt, k, m, weight=True)
+    W2 = G.new(wt, k, m, weight=True)
+    if norm == "rms":
+        h = G.lib.ggml_mul(G.ctx, G.lib.ggml_rms_norm(G.ctx, X, 1e-6), WN)
+    else:
+        h = G.lib.ggml_add(G.ctx, G.lib.ggml_mul(G.ctx, G.lib.ggml_norm(G.ctx, X, 1e-5), WN), BN)
+    Y = G.lib.ggml_add(G.ctx, G.lib.ggml_mul_mat(G.ctx, W1, h), G.lib.ggml_mul_mat(G.ctx, W2, h))
+    run(ggml, gpu, G, Y)
+    for T, v in ((X, x), (WN, wn), (BN, bn), (W1, wq1), (W2, wq2)):
+        G.set(T, v)
+    assert G.compute(gpu.backend) == 0
+    y = G.get(Y).reshape(n, m)
+    hn = (ref.rms_norm(x, 1e-6) * wn) if norm == "rms" else (ref.norm(x, 1e-5) * wn + bn)
+    want = ref.mul_mat(wt, wq1, m, k, hn) + ref.mul_mat(wt, wq2, m, k, hn)
+    assert_same_bits(y, want)
+    labels = [lab.split(":")[0] for lab, _ in gpu.profile(G.gf, 1)]
+    assert not any("norm" in lab or "quantize" in lab for lab in labels), labels
+    G.free()
+
+
 def test_mul_mat_lm_head_full_size(ggml, gpu, ref):
     """151936 x 1024 Q4_K at batch 8, the largest decode GEMV of the Qwen3-0.6B shape"""
     m, k, n = 151936, 1024, 8
