@@ -370,22 +370,54 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
     }
 }
 
+// RMS norm * w, then NEOX RoPE at position p, of one 128-element row held by
+// a wave (lane l: elements l and l + 64) -- k_rms_norm_rope128's sequence
+__device__ __forceinline__ void as_norm_rope(const float * x, const float * w, float eps, float p, float theta_scale,
+                                             float freq_scale, float attn_factor, int lane, float & y0, float & y1) {
+    const float x0 = x[lane], x1 = x[lane + 64];
+    const float w0 = w[lane], w1 = w[lane + 64];
+    const double s2 = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
+    const float var = (float) (s2 / 128.0);
+    const float scale = 1.0f / sqrtf(var + eps);
+    const float v0 = (x0 * scale) * w0, v1 = (x1 * scale) * w1;
+    float theta = p;
+    for (int k = 0; k < lane; k++) theta *= theta_scale;
+    float sn, c;
+    sincosf_det(freq_scale * theta, sn, c);
+    c *= attn_factor;
+    sn *= attn_factor;
+    y0 = v0 * c - v1 * sn;
+    y1 = v0 * sn + v1 * c;
+}
+
 // Decode form (one query position): one wave per (chunk, query head,
 // sequence). For the scores lane p owns KV position p of the chunk (its whole
 // K row, the query broadcast from LDS); for P*V lane l owns dims D/64*l.. of
 // every position, the chunk's p values broadcast lane by lane. After the
-// mask, K and V are requested in one burst. Every sum runs in the CPU reference's order
-// (dimensions, then positions) and the p*v products are exact in f64, so
-// fused multiply-adds change nothing: the chunk partials are bit-identical. The query heads of one kv head
-// read the same K/V rows at the same time, so the second read comes from
-// cache. Waves share nothing: wave-local LDS, no workgroup barriers.
-template <int D>
-__global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __restrict__ part_m,
+// mask, K and V are requested in one burst. Every sum runs in the CPU
+// reference's order (dimensions, then positions) and the p*v products are
+// exact in f64, so fused multiply-adds change nothing: the chunk partials are
+// bit-identical. The query heads of one kv head read the same K/V rows at the
+// same time, so the second read comes from cache. Waves share nothing:
+// wave-local LDS, no workgroup barriers.
+//
+// STEP (decode step, D = 128): the wave also derives its inputs from the
+// fused QKV projection -- the query row's RMS norm * w and NEOX RoPE (the
+// arithmetic of k_rms_norm_rope128), and, in the chunk holding this step's
+// position, the new K row (same) and V row, which replace that cache row in
+// the wave's registers; the first query head's wave also writes them into the
+// f16 caches (SET_ROWS). No other wave reads the new row from the cache in
+// this launch, so the write needs no ordering.
+template <int D, bool STEP>
+__global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float * __restrict__ part_m,
                                                       double * __restrict__ part_l, double * __restrict__ part_acc) {
     constexpr int DL = D / 64;
     constexpr int KU = D / 8;  // 16-byte pieces of a K row
+    static_assert(!STEP || D == 128, "the step form handles 128-wide heads");
     __shared__ __align__(16) float s_q[4][D];
     __shared__ uint4 s_k[4][kFaChunk][KU + 1];  // one padded row per position: conflict-free row reads
+    __shared__ __align__(16) uint16_t s_vnew[STEP ? 4 : 1][D];
+    const fattn_args & a = st.fa;
     const int lane = (int) threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane((int) threadIdx.x >> 6);
     const int64_t item = (int64_t) blockIdx.x * 4 + wave;
@@ -406,7 +438,20 @@ __global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __re
     const int pos = c * kFaChunk + lane;
 
     // the query (f16-rounded) and the mask first
-    {
+    int jn = -1;  // STEP: the chunk row of this step's position, if in this chunk
+    int64_t r_new = -1;
+    if constexpr (STEP) {
+        const char * ip = st.idx + (int64_t) (kvh % st.idx_ne1) * st.idx_nb1 + (int64_t) (seq % st.idx_ne2) * st.idx_nb2;
+        r_new = st.idx_i64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
+        const float p = (float) st.pos[seq];
+        float y0, y1;
+        as_norm_rope((const float *) (st.qsrc + (int64_t) head * st.q_nb1 + (int64_t) seq * st.q_nb2), st.qw, st.q_eps,
+                     p, st.theta_scale, st.freq_scale, st.attn_factor, lane, y0, y1);
+        s_q[wave][lane] = round_to_half(y0);
+        s_q[wave][lane + 64] = round_to_half(y1);
+        const int64_t j = r_new - (int64_t) c * kFaChunk;
+        jn = j >= 0 && j < clen ? (int) j : -1;
+    } else {
         const float * qp = (const float *) (a.q + (int64_t) head * a.q_nb2 + (int64_t) seq * a.q_nb3);
         for (int d = lane; d < D; d += 64) s_q[wave][d] = round_to_half(qp[d]);
     }
@@ -421,7 +466,12 @@ __global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __re
             part_m[prow * nc + c] = -INFINITY;
             part_l[prow * nc + c] = 0.0;
         }
-        return;
+        if constexpr (STEP) {
+            // the cache row is written even when no query attends to it
+            if (jn < 0 || hh != 0) return;
+        } else {
+            return;
+        }
     }
     // K in wave-wide contiguous pieces (each load instruction covers whole
     // rows), transposed through LDS so that lane p gets row p. Positions past
@@ -449,12 +499,48 @@ __global__ __launch_bounds__(256) void k_fattn_decode(fattn_args a, float * __re
         if (DL == 2) vr[j] = *(const uint32_t *) (vb + off);
         else vr[j] = (uint32_t) *(const uint16_t *) (vb + off);
     }
+    if constexpr (STEP) {
+        if (jn >= 0) {
+            // this step's K / V rows: K replaces the LDS row jn (after the
+            // transposing stores above, in program order within the wave), V
+            // goes through LDS to the dims layout
+            float y0, y1;
+            as_norm_rope((const float *) (st.ksrc + (int64_t) kvh * st.k_nb1 + (int64_t) seq * st.k_nb2), st.kw,
+                         st.k_eps, (float) st.pos[seq], st.theta_scale, st.freq_scale, st.attn_factor, lane, y0, y1);
+            const uint16_t k0 = float_to_half_bits(y0), k1 = float_to_half_bits(y1);
+            const float * vsp = (const float *) (st.vsrc + (int64_t) kvh * st.v_nb1 + (int64_t) seq * st.v_nb2);
+            const uint16_t v0 = float_to_half_bits(vsp[lane]), v1 = float_to_half_bits(vsp[lane + 64]);
+            uint16_t * krow = (uint16_t *) &s_k[wave][jn][0];
+            krow[lane] = k0;
+            krow[lane + 64] = k1;
+            s_vnew[wave][lane] = v0;
+            s_vnew[wave][lane + 64] = v1;
+            if (hh == 0 && r_new < st.kc_rows) {
+                uint16_t * kd = (uint16_t *) (st.kc + r_new * st.kc_nb1 + (int64_t) kvh * st.kc_nb2 + (int64_t) seq * st.kc_nb3);
+                kd[lane] = k0;
+                kd[lane + 64] = k1;
+            }
+            if (hh == 0 && r_new < st.vc_rows) {
+                uint16_t * vd = (uint16_t *) (st.vc + r_new * st.vc_nb1 + (int64_t) kvh * st.vc_nb2 + (int64_t) seq * st.vc_nb3);
+                vd[lane] = v0;
+                vd[lane + 64] = v1;
+            }
+        }
+        if (__ballot(live) == 0) return;  // a fully masked chunk only had the cache row to write
+    }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     uint4 kr[KU];
 #pragma unroll
     for (int u = 0; u < KU; u++) kr[u] = s_k[wave][lane][u];
+    if constexpr (STEP) {
+        if (jn >= 0) {
+            const uint32_t vn = *(const uint32_t *) &s_vnew[wave][lane * DL];
+#pragma unroll
+            for (int j = 0; j < kFaChunk; j++) vr[j] = j == jn ? vn : vr[j];
+        }
+    }
 
     // scores: lane = position; products of two halves are exact in f32
     double sc = 0.0;
@@ -598,6 +684,32 @@ void fattn_plan(fattn_args & a, int n_cu) {
     else a.split = fits && tiles < 2LL * n_cu ? 1 : 0;
 }
 
+bool attn_step_supported(const fattn_args & a) {
+    return a.d == 128 && a.n_q == 1 && a.split == 2 && fattn_supported(a.d, a.hq, a.hkv);
+}
+
+size_t attn_step_scratch_bytes(const fattn_args & a) { return fattn_scratch_bytes(a); }
+
+void launch_attn_step(const attn_step_args & st, void * scratch, hipStream_t s) {
+    const fattn_args & a = st.fa;
+    const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
+    float * pm = (float *) scratch;
+    char * p = (char *) (pm + prows);
+    p = (char *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
+    double * pl = (double *) p;
+    double * pa = pl + prows;
+    const int64_t items = (int64_t) a.n_chunks * a.hq * a.n_seq;
+    hipLaunchKernelGGL((k_fattn_decode<128, true>), dim3((unsigned) ((items + 3) / 4)), dim3(256), 0, s, st, pm, pl, pa);
+    const dim3 cgrid(1u, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
+    float * out = st.out;
+    switch (a.rows) {
+        case 1: hipLaunchKernelGGL((k_fattn_combine<128, 1>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out); break;
+        case 2: hipLaunchKernelGGL((k_fattn_combine<128, 2>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out); break;
+        case 4: hipLaunchKernelGGL((k_fattn_combine<128, 4>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out); break;
+        default: hipLaunchKernelGGL((k_fattn_combine<128, 8>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out); break;
+    }
+}
+
 bool fattn_supported(int d, int hq, int hkv) {
     if (d != 64 && d != 128) return false;
     if (hkv <= 0 || hq % hkv != 0) return false;
@@ -619,7 +731,10 @@ static void launch_fa(const fattn_args & a, void * scratch, float * out, hipStre
         double * pa = pl + prows;
         if (a.split == 2) {
             const int64_t items = (int64_t) a.n_chunks * a.hq * a.n_seq;
-            hipLaunchKernelGGL((k_fattn_decode<D>), dim3((unsigned) ((items + 3) / 4)), dim3(256), 0, s, a, pm, pl, pa);
+            attn_step_args st{};
+            st.fa = a;
+            hipLaunchKernelGGL((k_fattn_decode<D, false>), dim3((unsigned) ((items + 3) / 4)), dim3(256), 0, s, st, pm,
+                               pl, pa);
         } else {
             const dim3 grid((unsigned) a.n_chunks, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
             hipLaunchKernelGGL((k_fattn_split<D, R>), grid, dim3(kFaThreads), 0, s, a, pm, pl, pa);

@@ -325,6 +325,9 @@ struct planner {
     bool plan_unary(int i, const ggml_tensor * t);
     bool plan_binary(const ggml_tensor * t);
     bool plan_fattn(int i, const ggml_tensor * t);
+    bool make_fattn(const ggml_tensor * t, fattn_args & a);
+    void fattn_quant_out(int i, const ggml_tensor * t, fattn_args & a, const ggml_tensor *& view);
+    bool plan_attn_step(int i, const ggml_tensor * t);
 };
 
 bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
@@ -460,6 +463,7 @@ bool planner::norm_rope_match(int i, const ggml_tensor * t, norm_rope_job & job,
 }
 
 bool planner::plan_norm(int i, const ggml_tensor * t) {
+    if (plan_attn_step(i, t)) return true;
     {
         norm_rope_job j0, j1;
         const ggml_tensor *mul0, *rope0, *mul1, *rope1;
@@ -608,9 +612,9 @@ bool planner::plan_binary(const ggml_tensor * t) {
     return true;
 }
 
-bool planner::plan_fattn(int i, const ggml_tensor * t) {
+bool planner::make_fattn(const ggml_tensor * t, fattn_args & a) {
     const ggml_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2], *m = t->src[3];
-    fattn_args a{};
+    a = fattn_args{};
     a.q = (const char *) q->data;
     a.k = (const char *) k->data;
     a.v = (const char *) v->data;
@@ -645,11 +649,14 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
     if (((uintptr_t) a.k | (uintptr_t) a.v) % 16 != 0) return fail(t, "K/V not 16-byte aligned");
     fattn_plan(a, n_cu);
     if (!fattn_fits(a)) return fail(t, "KV span longer than the kernel's chunk table");
+    return true;
+}
 
-    // the output projection consumes the output through a contiguous reshape:
-    // let the attention kernel quantize it for that MUL_MAT
+// the output projection consumes the output through a contiguous reshape:
+// let the attention kernel quantize it for that MUL_MAT
+void planner::fattn_quant_out(int i, const ggml_tensor * t, fattn_args & a, const ggml_tensor *& view) {
     const int g = a.hq / a.hkv;
-    const ggml_tensor * view = sole_consumer(t, i + 1);
+    view = sole_consumer(t, i + 1);
     const ggml_tensor * mm = nullptr;
     if (view && (view->op == GGML_OP_RESHAPE || view->op == GGML_OP_VIEW) && view->view_src == t &&
         view->view_offs == 0 && is_contiguous(view) && view->ne[0] == (int64_t) a.d * a.hq) {
@@ -665,12 +672,19 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
             a.act = act_buffers{nullptr, nullptr, nullptr};
         }
     }
+}
+
+bool planner::plan_fattn(int i, const ggml_tensor * t) {
+    fattn_args a;
+    if (!make_fattn(t, a)) return false;
+    const ggml_tensor * view = nullptr;
+    fattn_quant_out(i, t, a, view);
     gen_need = std::max(gen_need, fattn_scratch_bytes(a));
     backend_state * b = be;
     float * out = (float *) t->data;
     const int64_t qK = (int64_t) a.d * a.hq, qN = (int64_t) a.n_q * a.n_seq;
     add_step(
-[=](hipStream_t s) {
+        [=](hipStream_t s) {
             fattn_args la = a;
             if (la.qtype >= 0) la.act = act_carve(la.qtype, act_base(b), qK, qN);
             launch_fattn(la, gen_base(b), out, s);
@@ -679,6 +693,157 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
     if (a.qtype >= 0) {
         act_src = view;
         act_wtype = a.qtype;
+    }
+    return true;
+}
+
+// The decode-step attention of nn/decoder.rs:1937-2105 as one launch: the
+// query / key rows' RMS_NORM -> MUL(w) -> ROPE (node t and the key rows' norm
+// after it), the K and V SET_ROWS into the caches and the FLASH_ATTN_EXT over
+// them, when nothing else reads the intermediate results and no other node
+// runs in between. Falls back (false, nothing planned) on any other shape.
+bool planner::plan_attn_step(int i, const ggml_tensor * t) {
+    norm_rope_job j0, j1;
+    const ggml_tensor *mul0, *rope0, *mul1 = nullptr, *rope1 = nullptr;
+    if (!norm_rope_match(i, t, j0, mul0, rope0)) return false;
+    const ggml_tensor * t1 = nullptr;
+    int i1 = -1;
+    for (int j = i + 1; j < cg->n_nodes; j++) {
+        const ggml_tensor * n = cg->nodes[j];
+        if (is_view_op(n->op) || bypass.count(n) || deferred.count(n) || n == mul0 || n == rope0) continue;
+        t1 = n;
+        i1 = j;
+        break;
+    }
+    if (!t1 || !norm_rope_match(i1, t1, j1, mul1, rope1)) return false;
+    if (j0.theta_scale != j1.theta_scale || j0.freq_scale != j1.freq_scale || j0.attn_factor != j1.attn_factor ||
+        j0.pos != j1.pos)
+        return false;
+    // the attention reading the query rows
+    const ggml_tensor * F = nullptr;
+    int iF = -1;
+    for (int j = i1 + 1; j < cg->n_nodes; j++) {
+        const ggml_tensor * n = cg->nodes[j];
+        if (n->op == GGML_OP_FLASH_ATTN_EXT && root_of(n->src[0]) == rope0) {
+            F = n;
+            iF = j;
+            break;
+        }
+    }
+    if (!F || !supports_op(be->dev, F)) return false;
+    const ggml_tensor *sk = F->src[1], *sv = F->src[2];
+    if (sk->op != GGML_OP_SET_ROWS || sv->op != GGML_OP_SET_ROWS || sk->src[1] != sv->src[1]) return false;
+    if (sk->type != GGML_TYPE_F16 || sv->type != GGML_TYPE_F16 || root_of(sk->src[0]) != rope1) return false;
+    const ggml_tensor *qv = F->src[0], *kn = sk->src[0], *vn = sv->src[0], *idx = sk->src[1];
+    // rope outputs [128, heads, n_seq]; the attention / set_rows views
+    // [128, 1, heads, n_seq] over them
+    auto head_view = [](const ggml_tensor * v, const ggml_tensor * r) {
+        return v->data == r->data && r->ne[3] == 1 && v->ne[0] == 128 && v->ne[1] == 1 && v->ne[2] == r->ne[1] &&
+               v->ne[3] == r->ne[2] && v->nb[0] == 4 && v->nb[2] == r->nb[1] && v->nb[3] == r->nb[2];
+    };
+    if (!head_view(qv, rope0) || !head_view(kn, rope1)) return false;
+    if (vn->type != GGML_TYPE_F32 || vn->ne[0] != 128 || vn->ne[1] != 1 || vn->ne[2] != kn->ne[2] ||
+        vn->ne[3] != kn->ne[3])
+        return false;
+    if (sk->ne[2] != kn->ne[2] || sk->ne[3] != kn->ne[3] || sv->ne[2] != vn->ne[2] || sv->ne[3] != vn->ne[3])
+        return false;
+    if (idx->ne[0] < 1 || idx->ne[3] != 1) return false;
+    if (j0.a.ne[3] != 1 || j1.a.ne[3] != 1 || j0.a.nb[0] != 4 || j1.a.nb[0] != 4) return false;
+    fattn_args fa;
+    if (!make_fattn(F, fa)) return false;
+    if (!attn_step_supported(fa) || F->src[1] != sk || F->src[2] != sv) return false;
+    // nothing else runs between the first norm and the attention, and nothing
+    // outside the fused nodes reads their intermediate results
+    const ggml_tensor * fused[] = {t, mul0, rope0, t1, mul1, rope1, sk, sv, F};
+    auto in_fused = [&](const ggml_tensor * n) {
+        for (const ggml_tensor * f : fused)
+            if (n == f) return true;
+        return false;
+    };
+    for (int j = i + 1; j <= iF; j++) {
+        const ggml_tensor * n = cg->nodes[j];
+        if (is_view_op(n->op) || bypass.count(n) || in_fused(n)) continue;
+        return false;
+    }
+    for (int j = i + 1; j < cg->n_nodes; j++) {
+        const ggml_tensor * n = cg->nodes[j];
+        if (is_view_op(n->op) || in_fused(n)) continue;
+        for (int k = 0; k < GGML_MAX_SRC; k++) {
+            const ggml_tensor * x = n->src[k];
+            if (!x) continue;
+            for (const ggml_tensor * f : fused) {
+                if (f == F) continue;
+                if (x == f || (root_of(x) == f && f != sk && f != sv)) return false;
+            }
+        }
+    }
+    for (const ggml_tensor * f : fused) {
+        if (f != F && (f->flags & GGML_TENSOR_FLAG_OUTPUT)) return false;
+    }
+    // the kernel's output must not overlap what it reads (the projection rows)
+    const tview vsrc = view_of(vn);
+    {
+        uintptr_t lo, hi, olo = (uintptr_t) F->data, ohi = olo + ggml_nbytes(F);
+        const tview * reads[] = {&j0.a, &j1.a, &vsrc};
+        for (const tview * v : reads) {
+            view_span(*v, 4, lo, hi);
+            if (lo < ohi && olo < hi) return false;
+        }
+    }
+    attn_step_args as{};
+    const ggml_tensor * oview = nullptr;
+    fattn_quant_out(iF, F, fa, oview);
+    as.fa = fa;
+    as.qsrc = j0.a.data;
+    as.q_nb1 = j0.a.nb[1];
+    as.q_nb2 = j0.a.nb[2];
+    as.ksrc = j1.a.data;
+    as.k_nb1 = j1.a.nb[1];
+    as.k_nb2 = j1.a.nb[2];
+    as.vsrc = vsrc.data;
+    as.v_nb1 = vsrc.nb[2];
+    as.v_nb2 = vsrc.nb[3];
+    as.qw = j0.w;
+    as.kw = j1.w;
+    as.q_eps = j0.eps;
+    as.k_eps = j1.eps;
+    as.pos = j0.pos;
+    as.theta_scale = j0.theta_scale;
+    as.freq_scale = j0.freq_scale;
+    as.attn_factor = j0.attn_factor;
+    as.idx = (const char *) idx->data;
+    as.idx_nb1 = idx->nb[1];
+    as.idx_nb2 = idx->nb[2];
+    as.idx_ne1 = (int) idx->ne[1];
+    as.idx_ne2 = (int) idx->ne[2];
+    as.idx_i64 = idx->type == GGML_TYPE_I64;
+    as.kc = (char *) sk->data;
+    as.kc_nb1 = sk->nb[1];
+    as.kc_nb2 = sk->nb[2];
+    as.kc_nb3 = sk->nb[3];
+    as.kc_rows = sk->ne[1];
+    as.vc = (char *) sv->data;
+    as.vc_nb1 = sv->nb[1];
+    as.vc_nb2 = sv->nb[2];
+    as.vc_nb3 = sv->nb[3];
+    as.vc_rows = sv->ne[1];
+    as.out = (float *) F->data;
+    for (const ggml_tensor * f : fused) {
+        if (f != t) deferred[f] = f;
+    }
+    gen_need = std::max(gen_need, attn_step_scratch_bytes(fa));
+    backend_state * b = be;
+    const int64_t qK = (int64_t) fa.d * fa.hq, qN = (int64_t) fa.n_q * fa.n_seq;
+    add_step(
+        [=](hipStream_t s) {
+            attn_step_args la = as;
+            if (la.fa.qtype >= 0) la.fa.act = act_carve(la.fa.qtype, act_base(b), qK, qN);
+            launch_attn_step(la, gen_base(b), s);
+        },
+        F, "attn_step");
+    if (fa.qtype >= 0) {
+        act_src = oview;
+        act_wtype = fa.qtype;
     }
     return true;
 }
@@ -910,7 +1075,7 @@ enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg) {
         std::fprintf(stderr, "mi355x: graph capture failed (%s); running eagerly\n", hipGetErrorString(e));
         (void) hipGetLastError();
         if (ce->graph) {
-            hipGraphDestroy(ce->graph);
+            (void) hipGraphDestroy(ce->graph);
             ce->graph = nullptr;
         }
         ce->exec = nullptr;
@@ -920,7 +1085,7 @@ enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg) {
     be->last_observation = GGML_BACKEND_GRAPH_CANCEL_OBSERVATION_SUBMISSION_CHECKPOINT;
     for (step & s : p.steps) {
         if (be->abort_cb && be->abort_cb(be->abort_data)) {
-            hipStreamSynchronize(be->stream);
+            (void) hipStreamSynchronize(be->stream);
             return GGML_STATUS_ABORTED;
         }
         s.run(be->stream);

@@ -81,6 +81,39 @@ struct fattn_args {
     int qtype;
     act_buffers act;
 };
+// One decode step of attention (D = 128): per-head RMS norm * w and NEOX
+// RoPE of the step's new query and key rows (taken from the fused QKV
+// projection), the new K/V rows written into the f16 caches at the set_rows
+// index, and attention over the cached span by 64-position chunks (the
+// flash_attn_ext definition: chunk launch + combine launch). Output: the
+// attention rows (and optionally their quantized activations for the output
+// projection, fa.qtype / fa.act).
+struct attn_step_args {
+    fattn_args fa;  // cache reads (k, v, strides), mask, scale, shapes; fa.q unused
+    const char * qsrc;  // new query row of head h, sequence s: qsrc + h * q_nb1 + s * q_nb2 (f32)
+    int64_t q_nb1, q_nb2;
+    const char * ksrc;
+    int64_t k_nb1, k_nb2;
+    const char * vsrc;
+    int64_t v_nb1, v_nb2;
+    const float * qw;  // QK-norm weights [128]
+    const float * kw;
+    float q_eps, k_eps;
+    const int32_t * pos;  // RoPE position of sequence s: pos[s]
+    float theta_scale, freq_scale, attn_factor;
+    const char * idx;  // set_rows index: row of (head h, sequence s) = idx[0, h % ne1, s % ne2]
+    int64_t idx_nb1, idx_nb2;
+    int idx_ne1, idx_ne2, idx_i64;
+    char * kc;  // K / V caches written (f16), [128, rows, hkv, n_seq] strides
+    int64_t kc_nb1, kc_nb2, kc_nb3, kc_rows;
+    char * vc;
+    int64_t vc_nb1, vc_nb2, vc_nb3, vc_rows;
+    float * out;  // [128, hq, 1, n_seq]
+};
+bool attn_step_supported(const fattn_args & a);
+size_t attn_step_scratch_bytes(const fattn_args & a);
+void launch_attn_step(const attn_step_args & a, void * scratch, hipStream_t stream);
+
 bool fattn_supported(int d, int hq, int hkv);
 void fattn_plan(fattn_args & a, int n_cu);
 bool fattn_fits(const fattn_args & a);
