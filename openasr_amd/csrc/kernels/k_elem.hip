@@ -377,6 +377,22 @@ __global__ __launch_bounds__(256) void k_rms_norm_rope128(norm_rope_job j0, norm
     y[lane + 64] = v0 * sn + v1 * c;
 }
 
+__global__ __launch_bounds__(64) void k_rope_table(float2 * table, const int32_t * pos, float theta_scale,
+                                                   float freq_scale, float attn_factor) {
+    const int lane = (int) threadIdx.x, seq = (int) blockIdx.x;
+    float theta = (float) pos[seq];
+    for (int k = 0; k < lane; k++) theta *= theta_scale;
+    float sn, c;
+    sincosf_det(freq_scale * theta, sn, c);
+    table[seq * 64 + lane] = make_float2(c * attn_factor, sn * attn_factor);
+}
+
+void launch_rope_table(float2 * table, const int32_t * pos, int n_seq, float theta_scale, float freq_scale,
+                       float attn_factor, hipStream_t s) {
+    hipLaunchKernelGGL(k_rope_table, dim3((unsigned) n_seq), dim3(64), 0, s, table, pos, theta_scale, freq_scale,
+                       attn_factor);
+}
+
 void launch_rms_norm_rope128(const norm_rope_job & j0, const norm_rope_job * j1, hipStream_t s) {
     const int64_t rows = j1 && j1->rows > j0.rows ? j1->rows : j0.rows;
     hipLaunchKernelGGL(k_rms_norm_rope128, dim3((unsigned) ((rows + 3) / 4), j1 ? 2u : 1u), dim3(256), 0, s, j0,

@@ -370,24 +370,17 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
     }
 }
 
-// RMS norm * w, then NEOX RoPE at position p, of one 128-element row held by
-// a wave (lane l: elements l and l + 64) -- k_rms_norm_rope128's sequence
-__device__ __forceinline__ void as_norm_rope(const float * x, const float * w, float eps, float p, float theta_scale,
-                                             float freq_scale, float attn_factor, int lane, float & y0, float & y1) {
-    const float x0 = x[lane], x1 = x[lane + 64];
-    const float w0 = w[lane], w1 = w[lane + 64];
+// RMS norm * w, then NEOX RoPE by a (cos, sin) pair, of one 128-element row
+// held by a wave (lane l: elements l and l + 64, rotation index l) -- the
+// arithmetic of k_rms_norm_rope128 with the angle from the rope table
+__device__ __forceinline__ void as_norm_rope(float x0, float x1, float w0, float w1, float2 cs, float eps, float & y0,
+                                             float & y1) {
     const double s2 = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
     const float var = (float) (s2 / 128.0);
     const float scale = 1.0f / sqrtf(var + eps);
     const float v0 = (x0 * scale) * w0, v1 = (x1 * scale) * w1;
-    float theta = p;
-    for (int k = 0; k < lane; k++) theta *= theta_scale;
-    float sn, c;
-    sincosf_det(freq_scale * theta, sn, c);
-    c *= attn_factor;
-    sn *= attn_factor;
-    y0 = v0 * c - v1 * sn;
-    y1 = v0 * sn + v1 * c;
+    y0 = v0 * cs.x - v1 * cs.y;
+    y1 = v0 * cs.y + v1 * cs.x;
 }
 
 // Decode form (one query position): one wave per (chunk, query head,
@@ -437,16 +430,24 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     const int64_t prow = hs;  // partial row: tile (seq, kvh) row head % g
     const int pos = c * kFaChunk + lane;
 
-    // the query (f16-rounded) and the mask first
+    // the query (f16-rounded) and the mask first; in the step form every
+    // independent input is requested before any is used
     int jn = -1;  // STEP: the chunk row of this step's position, if in this chunk
     int64_t r_new = -1;
+    float mv = -INFINITY;
     if constexpr (STEP) {
         const char * ip = st.idx + (int64_t) (kvh % st.idx_ne1) * st.idx_nb1 + (int64_t) (seq % st.idx_ne2) * st.idx_nb2;
+        const float * qx = (const float *) (st.qsrc + (int64_t) head * st.q_nb1 + (int64_t) seq * st.q_nb2);
+        const float x0 = qx[lane], x1 = qx[lane + 64];
+        const float w0 = st.qw[lane], w1 = st.qw[lane + 64];
+        const float2 cs = st.rope[seq * 64 + lane];
+        if (lane < clen) {
+            mv = 0.0f;
+            if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
+        }
         r_new = st.idx_i64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
-        const float p = (float) st.pos[seq];
         float y0, y1;
-        as_norm_rope((const float *) (st.qsrc + (int64_t) head * st.q_nb1 + (int64_t) seq * st.q_nb2), st.qw, st.q_eps,
-                     p, st.theta_scale, st.freq_scale, st.attn_factor, lane, y0, y1);
+        as_norm_rope(x0, x1, w0, w1, cs, st.q_eps, y0, y1);
         s_q[wave][lane] = round_to_half(y0);
         s_q[wave][lane + 64] = round_to_half(y1);
         const int64_t j = r_new - (int64_t) c * kFaChunk;
@@ -454,11 +455,10 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     } else {
         const float * qp = (const float *) (a.q + (int64_t) head * a.q_nb2 + (int64_t) seq * a.q_nb3);
         for (int d = lane; d < D; d += 64) s_q[wave][d] = round_to_half(qp[d]);
-    }
-    float mv = -INFINITY;
-    if (lane < clen) {
-        mv = 0.0f;
-        if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
+        if (lane < clen) {
+            mv = 0.0f;
+            if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
+        }
     }
     const bool live = mv != -INFINITY;
     if (__ballot(live) == 0) {
@@ -504,9 +504,10 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
             // this step's K / V rows: K replaces the LDS row jn (after the
             // transposing stores above, in program order within the wave), V
             // goes through LDS to the dims layout
+            const float * kx = (const float *) (st.ksrc + (int64_t) kvh * st.k_nb1 + (int64_t) seq * st.k_nb2);
             float y0, y1;
-            as_norm_rope((const float *) (st.ksrc + (int64_t) kvh * st.k_nb1 + (int64_t) seq * st.k_nb2), st.kw,
-                         st.k_eps, (float) st.pos[seq], st.theta_scale, st.freq_scale, st.attn_factor, lane, y0, y1);
+            as_norm_rope(kx[lane], kx[lane + 64], st.kw[lane], st.kw[lane + 64], st.rope[seq * 64 + lane], st.k_eps, y0,
+                         y1);
             const uint16_t k0 = float_to_half_bits(y0), k1 = float_to_half_bits(y1);
             const float * vsp = (const float *) (st.vsrc + (int64_t) kvh * st.v_nb1 + (int64_t) seq * st.v_nb2);
             const uint16_t v0 = float_to_half_bits(vsp[lane]), v1 = float_to_half_bits(vsp[lane + 64]);

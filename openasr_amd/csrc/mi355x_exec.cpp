@@ -33,7 +33,11 @@ size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // scratch arena: [activation region][general region]
 char * act_base(const backend_state * be) { return be->scratch; }
-char * gen_base(const backend_state * be) { return be->scratch + be->gen_off; }
+// the general region starts with the decode step's rope table (kept for the
+// whole graph); the rest is per-launch scratch
+constexpr size_t kRopeTableBytes = 64 * 1024;
+char * rope_base(const backend_state * be) { return be->scratch + be->gen_off; }
+char * gen_base(const backend_state * be) { return be->scratch + be->gen_off + kRopeTableBytes; }
 
 bool is_view_op(enum ggml_op op) {
     return op == GGML_OP_NONE || op == GGML_OP_RESHAPE || op == GGML_OP_VIEW || op == GGML_OP_PERMUTE ||
@@ -259,6 +263,13 @@ struct planner {
     // norms whose launch is skipped: the GEMVs consuming their output
     // normalise and quantize in their activation prologue (norm output -> it)
     std::unordered_map<const ggml_tensor *, gemv_prologue> pro_norm;
+
+    // the rope table the scratch holds at this point of the plan
+    struct rope_key {
+        const int32_t * pos = nullptr;
+        int n_seq = 0;
+        float theta_scale = 0, freq_scale = 0, attn_factor = 0;
+    } rope_cur;
 
     // at most this many 16-row tiles take a prologue: every workgroup stages
     // the activations itself, so the redundant staging grows with the grid
@@ -828,15 +839,32 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     as.vc_nb3 = sv->nb[3];
     as.vc_rows = sv->ne[1];
     as.out = (float *) F->data;
+    if (fa.n_seq * 64 * sizeof(float2) > kRopeTableBytes) return false;
     for (const ggml_tensor * f : fused) {
         if (f != t) deferred[f] = f;
     }
     gen_need = std::max(gen_need, attn_step_scratch_bytes(fa));
     backend_state * b = be;
+    // the rotation table of this step's positions, once per graph (again if
+    // another layer rotates differently)
     const int64_t qK = (int64_t) fa.d * fa.hq, qN = (int64_t) fa.n_q * fa.n_seq;
+    const int n_seq = fa.n_seq;
+    if (rope_cur.pos != j0.pos || rope_cur.n_seq != n_seq || rope_cur.theta_scale != j0.theta_scale ||
+        rope_cur.freq_scale != j0.freq_scale || rope_cur.attn_factor != j0.attn_factor) {
+        rope_cur.pos = j0.pos;
+        rope_cur.n_seq = n_seq;
+        rope_cur.theta_scale = j0.theta_scale;
+        rope_cur.freq_scale = j0.freq_scale;
+        rope_cur.attn_factor = j0.attn_factor;
+        const rope_key rk = rope_cur;
+        add_step([=](hipStream_t s) {
+            launch_rope_table((float2 *) rope_base(b), rk.pos, rk.n_seq, rk.theta_scale, rk.freq_scale, rk.attn_factor, s);
+        }, F, "rope_table");
+    }
     add_step(
         [=](hipStream_t s) {
             attn_step_args la = as;
+            la.rope = (const float2 *) rope_base(b);
             if (la.fa.qtype >= 0) la.fa.act = act_carve(la.fa.qtype, act_base(b), qK, qN);
             launch_attn_step(la, gen_base(b), s);
         },
@@ -969,7 +997,7 @@ bool planner::plan() {
 
 bool ensure_scratch(backend_state * be, size_t act_need, size_t gen_need) {
     act_need = align_up(act_need, kAlign);
-    gen_need = align_up(gen_need, kAlign);
+    gen_need = align_up(gen_need + kRopeTableBytes, kAlign);
     if (be->scratch && act_need <= be->gen_off && be->gen_off + gen_need <= be->scratch_cap) return true;
     release_graph_cache(be);
     if (be->scratch) MI_CHECK(hipFree(be->scratch));

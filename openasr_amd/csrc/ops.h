@@ -109,7 +109,14 @@ struct attn_step_args {
     char * vc;
     int64_t vc_nb1, vc_nb2, vc_nb3, vc_rows;
     float * out;  // [128, hq, 1, n_seq]
+    const float2 * rope;  // per sequence the 64 (cos, sin) pairs of its position (launch_rope_table)
 };
+// (cos, sin) of the NEOX rotation angles of 128-wide rows at each sequence's
+// position: table[s][i] for rotation index i < 64, the arithmetic of
+// k_rms_norm_rope128 (theta_i = p * theta_scale^i built by repeated
+// multiplication, deterministic sincos, times attn_factor)
+void launch_rope_table(float2 * table, const int32_t * pos, int n_seq, float theta_scale, float freq_scale,
+                       float attn_factor, hipStream_t s);
 bool attn_step_supported(const fattn_args & a);
 size_t attn_step_scratch_bytes(const fattn_args & a);
 void launch_attn_step(const attn_step_args & a, void * scratch, hipStream_t stream);
