@@ -362,8 +362,23 @@ __device__ __forceinline__ void q4k_scales(const uint4 & hdr, int * sc, int * mn
 // matrix; the epilogue then writes silu(W x) * (W2 x) -- the SwiGLU gate of
 // nn/ffn.rs:64-91 with the same roundings as MUL_MAT, SILU and MUL apart.
 // A residual, when given, is added to the rounded product.
+// the residual values wave 0 adds in the epilogue, requested at kernel start
+__device__ __forceinline__ void gemv_res_prefetch(const gemv_args & a, int64_t row, int n0, float (&res)[4]) {
+    const int g = (threadIdx.x & 63) >> 4;
+    if (!a.res) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) res[i] = 0.0f;
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int n = n0 + 4 * g + i;
+        res[i] = *(const float *) (a.res + (int64_t) (n < a.N ? n : n0) * a.res_nb1 + row * 4);
+    }
+}
+
 __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4], double (*s_red)[64][4], int64_t row,
-                                            int n0, int half) {
+                                            int n0, int half, const float (&res)[4]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int g = lane >> 4;
     double acc2[4] = {0.0, 0.0, 0.0, 0.0};
@@ -392,16 +407,17 @@ __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4
                 const float u = (float) acc2[i];
                 v = (v / (1.0f + expf_det(-v))) * u;
             }
-            if (a.res) v = *(const float *) (a.res + (int64_t) n * a.res_nb1 + row * 4) + v;
+            if (a.res) v = res[i] + v;
             *(float *) (a.dst + (int64_t) n * a.dst_nb1 + row * 4) = v;
         }
     }
 }
 
 // waves of the workgroup take super-blocks round-robin (wave w: sb = w,
-// w + nw, ...); each super-block's weight loads are issued one unit ahead
-template <int PRO>
-__global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
+// w + nw, ...); the first unit's weights are requested at kernel start, each
+// next unit's at the end of the current one
+template <int PRO, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
     extern __shared__ __align__(16) char smem[];
     __shared__ double s_red[16][64][4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -415,15 +431,18 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
     const int64_t nsb = a.K / 256;
     const int64_t row = tile * 16 + r;
     const char * wrow = (second ? a.W2 : a.W) + row * a.row_bytes;
-    uint4 hdr = make_uint4(0, 0, 0, 0);
-    long q[4] = {0, 0, 0, 0};
+    uint4 hdr;
+    long q[4];
     int64_t sb = wv;
-    if (sb < nsb) {
-        const char * blk = wrow + sb * 144;
+    {
+        // waves without a unit (staging helpers) read unit 0 and never use it
+        const char * blk = wrow + (sb < nsb ? sb : 0) * 144;
         hdr = *(const uint4 *) blk;
 #pragma unroll
         for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
     }
+    float res[4];
+    gemv_res_prefetch(a, row, n0, res);
     // activation operands: LDS after the prologue, else the global buffers
     const int8_t * aq;
     const float * adp;
@@ -457,14 +476,24 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
         long af[8];
         float ad[4];
         uint4 ss[4];
+        // every load unconditional (clamped to column 0 of the chunk, which
+        // always exists) and masked afterwards: no load waits behind a branch
 #pragma unroll
-        for (int j = 0; j < 8; j++) af[j] = a_ok ? *(const long *) (acol + sb * 256 + 32 * j + 8 * g) : 0;
+        for (int j = 0; j < 8; j++) af[j] = *(const long *) (acol + sb * 256 + 32 * j + 8 * g);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = 4 * g + i;
-            const bool ok = n < nc;
-            ad[i] = ok ? adp[(int64_t) (c0 + n) * d_stride + sb] : 0.0f;
-            ss[i] = ok ? *(const uint4 *) (asp + (int64_t) (c0 + n) * ss_stride + sb * 8) : make_uint4(0, 0, 0, 0);
+            const int nn = n < nc ? n : 0;
+            ad[i] = adp[(int64_t) (c0 + nn) * d_stride + sb];
+            ss[i] = *(const uint4 *) (asp + (int64_t) (c0 + nn) * ss_stride + sb * 8);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++) af[j] = a_ok ? af[j] : 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const bool ok = 4 * g + i < nc;
+            ad[i] = ok ? ad[i] : 0.0f;
+            ss[i] = ok ? ss[i] : make_uint4(0, 0, 0, 0);
         }
         int sc[8], mn[8];
         q4k_scales(hdr, sc, mn);
@@ -481,13 +510,6 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
         }
         const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
         const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
-        // the next unit's weights go out before this unit's f64 epilogue
-        if (sb + half < nsb) {
-            const char * blk = wrow + (sb + half) * 144;
-            hdr = *(const uint4 *) blk;
-#pragma unroll
-            for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
-        }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t w4[4] = {ss[i].x, ss[i].y, ss[i].z, ss[i].w};
@@ -502,8 +524,15 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
             const double dmin = (double) dmw * da;
             acc[i] += d * (double) isum[i] - dmin * (double) msum;
         }
+        // the next unit's weights
+        if (sb + half < nsb) {
+            const char * blk = wrow + (sb + half) * 144;
+            hdr = *(const uint4 *) blk;
+#pragma unroll
+            for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
+        }
     }
-    gemv_finish(a, acc, s_red, row, n0, half);
+    gemv_finish(a, acc, s_red, row, n0, half, res);
 }
 
 // Q8_0 weights in the row-split layout [K quants][K/32 f16 scales]; the waves
@@ -511,8 +540,8 @@ __global__ __launch_bounds__(1024) void k_gemv_q4_K(gemv_args a) {
 // (the first group's weights before the prologue)
 constexpr int kQ8Group = 8;
 
-template <int PRO>
-__global__ __launch_bounds__(1024) void k_gemv_q8_0(gemv_args a) {
+template <int PRO, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
     extern __shared__ __align__(16) char smem[];
     __shared__ double s_red[16][64][4];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -532,11 +561,12 @@ __global__ __launch_bounds__(1024) void k_gemv_q8_0(gemv_args a) {
     int64_t b0 = (int64_t) wv * kQ8Group;
 #pragma unroll
     for (int u = 0; u < kQ8Group; u++) {
-        const int64_t b = b0 + u;
-        const bool ok = b < nblk;
-        q[u] = ok ? *(const long *) (wrow + b * 32 + 8 * g) : 0;
-        ds[u] = ok ? wsc[b] : 0;
+        const int64_t b = b0 + u < nblk ? b0 + u : 0;  // clamped; past-the-end blocks are never used
+        q[u] = *(const long *) (wrow + b * 32 + 8 * g);
+        ds[u] = wsc[b];
     }
+    float res[4];
+    gemv_res_prefetch(a, row, n0, res);
     const int8_t * aq;
     const float * adp;
     int64_t q_stride, d_stride;
@@ -565,27 +595,36 @@ __global__ __launch_bounds__(1024) void k_gemv_q8_0(gemv_args a) {
         if (b0 != first) {
 #pragma unroll
             for (int u = 0; u < kQ8Group; u++) {
-                const int64_t b = b0 + u;
-                const bool ok = b < nblk;
-                q[u] = ok ? *(const long *) (wrow + b * 32 + 8 * g) : 0;
-                ds[u] = ok ? wsc[b] : 0;
+                const int64_t b = b0 + u < nblk ? b0 + u : 0;
+                q[u] = *(const long *) (wrow + b * 32 + 8 * g);
+                ds[u] = wsc[b];
             }
         }
+        // unconditional clamped loads, masked afterwards (no load behind a branch)
         long af[kQ8Group];
         float4 ad[4][kQ8Group / 4];
 #pragma unroll
         for (int u = 0; u < kQ8Group; u++) {
-            const int64_t b = b0 + u;
-            af[u] = b < nblk && a_ok ? *(const long *) (acol + b * 32 + 8 * g) : 0;
+            const int64_t b = b0 + u < nblk ? b0 + u : 0;
+            af[u] = *(const long *) (acol + b * 32 + 8 * g);
         }
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = 4 * g + i;
+            const int nn = n < nc ? n : 0;
 #pragma unroll
             for (int v = 0; v < kQ8Group / 4; v++) {
-                const int64_t b = b0 + 4 * v;
-                ad[i][v] = n < nc && b < nblk ? *(const float4 *) (adp + (int64_t) (c0 + n) * d_stride + b)
-                                              : make_float4(0.f, 0.f, 0.f, 0.f);
+                const int64_t b = b0 + 4 * v < nblk ? b0 + 4 * v : 0;
+                ad[i][v] = *(const float4 *) (adp + (int64_t) (c0 + nn) * d_stride + b);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kQ8Group; u++) af[u] = a_ok ? af[u] : 0;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            if (4 * g + i >= nc) {
+#pragma unroll
+                for (int v = 0; v < kQ8Group / 4; v++) ad[i][v] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
 #pragma unroll
@@ -604,7 +643,7 @@ __global__ __launch_bounds__(1024) void k_gemv_q8_0(gemv_args a) {
             }
         }
     }
-    gemv_finish(a, acc, s_red, row, n0, half);
+    gemv_finish(a, acc, s_red, row, n0, half, res);
 }
 
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K) {
@@ -636,21 +675,30 @@ int gemv_waves(int wtype, int64_t K, int64_t N, bool dual, int pro) {
     return (int) (w * mats);
 }
 
-template <int PRO>
-void launch_kernel(int wtype, const dim3 & grid, const dim3 & block, size_t lds, hipStream_t stream,
-                   const gemv_args & a) {
+// kernels compiled for at most 8 waves get twice the registers per lane
+template <int PRO, int MAXW>
+void launch_kernel_w(int wtype, const dim3 & grid, const dim3 & block, size_t lds, hipStream_t stream,
+                     const gemv_args & a) {
     if (lds > 48 * 1024) {
         // staged columns beyond the default dynamic-LDS limit: raise it once per kernel
         static bool raised[2] = {false, false};
         const int idx = wtype == GGML_TYPE_Q4_K ? 0 : 1;
         if (!raised[idx]) {
-            const void * fn = wtype == GGML_TYPE_Q4_K ? (const void *) k_gemv_q4_K<PRO> : (const void *) k_gemv_q8_0<PRO>;
+            const void * fn = wtype == GGML_TYPE_Q4_K ? (const void *) k_gemv_q4_K<PRO, MAXW>
+                                                      : (const void *) k_gemv_q8_0<PRO, MAXW>;
             MI_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 32768));
             raised[idx] = true;
         }
     }
-    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_gemv_q4_K<PRO>, grid, block, lds, stream, a);
-    else hipLaunchKernelGGL(k_gemv_q8_0<PRO>, grid, block, lds, stream, a);
+    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL((k_gemv_q4_K<PRO, MAXW>), grid, block, lds, stream, a);
+    else hipLaunchKernelGGL((k_gemv_q8_0<PRO, MAXW>), grid, block, lds, stream, a);
+}
+
+template <int PRO>
+void launch_kernel(int wtype, const dim3 & grid, const dim3 & block, size_t lds, hipStream_t stream,
+                   const gemv_args & a) {
+    if (block.x <= 512) launch_kernel_w<PRO, 8>(wtype, grid, block, lds, stream, a);
+    else launch_kernel_w<PRO, 16>(wtype, grid, block, lds, stream, a);
 }
 
 }  // namespace
