@@ -558,17 +558,32 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     const float sv = live ? (float) sc * a.scale + mv : -INFINITY;
     const float m = wave_max(sv);
     const float p = sv == -INFINITY ? 0.0f : expf_det(sv - m);
-    // P * V: lane = dims; the sum of p in position order alongside
+    // P * V: lane = dims; the sum of p in position order alongside. p_j is
+    // broadcast as an f64 through two scalar registers. Masked positions
+    // (which may hold anything in the cache, even NaN) are skipped by a
+    // scalar test of the live-position mask; a live position (finite V) with
+    // p = 0 adds exactly nothing (acc + 0 * v = acc), as the reference's skip
+    // of p = 0 does, so the whole-chunk-live case runs without any test.
+    const double pd = (double) p;
+    const uint64_t live_bits = __ballot(live);
     double acc[DL], l = 0.0;
 #pragma unroll
     for (int i = 0; i < DL; i++) acc[i] = 0.0;
+    auto pv_step = [&](int j) {
+        const int lo = __builtin_amdgcn_readlane(__double2loint(pd), j);
+        const int hi = __builtin_amdgcn_readlane(__double2hiint(pd), j);
+        const double pj = __hiloint2double(hi, lo);
+        l += pj;
+        acc[0] = fma(pj, (double) half_bits_to_float((uint16_t) (vr[j] & 0xFFFF)), acc[0]);
+        if (DL == 2) acc[DL - 1] = fma(pj, (double) half_bits_to_float((uint16_t) (vr[j] >> 16)), acc[DL - 1]);
+    };
+    if (live_bits == ~0ull) {
 #pragma unroll
-    for (int j = 0; j < kFaChunk; j++) {
-        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
-        l += (double) pj;
-        if (pj != 0.0f) {  // masked slots may hold anything, even NaN
-            acc[0] = fma((double) pj, (double) half_bits_to_float((uint16_t) (vr[j] & 0xFFFF)), acc[0]);
-            if (DL == 2) acc[DL - 1] = fma((double) pj, (double) half_bits_to_float((uint16_t) (vr[j] >> 16)), acc[DL - 1]);
+        for (int j = 0; j < kFaChunk; j++) pv_step(j);
+    } else {
+#pragma unroll
+        for (int j = 0; j < kFaChunk; j++) {
+            if ((live_bits >> j) & 1) pv_step(j);
         }
     }
     double * pa = part_acc + (prow * nc + c) * D + lane * DL;

@@ -26,6 +26,9 @@
 // round trip of the weights overlaps it, and the norm / quantize launches
 // that would otherwise precede the GEMV disappear.
 //
+// The scale products are 24-bit multiplies: |MFMA sum| <= 32 * 127 * 15 and
+// |32-element sum| <= 32 * 127, scales and mins 6-bit, all within 24 bits.
+//
 // Q4_K B-operand loads: lane (row r, group g) reads 8 bytes of nibbles at
 // qs + 32c + 8g for c = 0..3, which hold elements 8g..8g+7 of sub-block 2c
 // (low nibbles) and of sub-block 2c+1 (high nibbles); the A operand takes the
@@ -506,7 +509,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
             const v4i c0v = mfma_i8(af[2 * c], lo, z);
             const v4i c1v = mfma_i8(af[2 * c + 1], hi, z);
 #pragma unroll
-            for (int i = 0; i < 4; i++) isum[i] += sc[2 * c] * c0v[i] + sc[2 * c + 1] * c1v[i];
+            for (int i = 0; i < 4; i++) isum[i] += __mul24(sc[2 * c], c0v[i]) + __mul24(sc[2 * c + 1], c1v[i]);
         }
         const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
         const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
@@ -516,8 +519,8 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
             int msum = 0;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                msum += mn[2 * j] * (int) (int16_t) (w4[j] & 0xFFFF);
-                msum += mn[2 * j + 1] * (int) (int16_t) (w4[j] >> 16);
+                msum += __mul24(mn[2 * j], (int) (int16_t) (w4[j] & 0xFFFF));
+                msum += __mul24(mn[2 * j + 1], (int) (int16_t) (w4[j] >> 16));
             }
             const double da = (double) ad[i];
             const double d = (double) dw * da;

@@ -123,14 +123,14 @@ __global__ __launch_bounds__(256) void k_mmq_q4_K(mmq_args a) {
                 const v4i c0 = mfma_i8_mmq(a0, lo, z);
                 const v4i c1 = mfma_i8_mmq(a1, hi, z);
 #pragma unroll
-                for (int i = 0; i < 4; i++) isum[i] += sc[2 * c] * c0[i] + sc[2 * c + 1] * c1[i];
+                for (int i = 0; i < 4; i++) isum[i] += __mul24(sc[2 * c], c0[i]) + __mul24(sc[2 * c + 1], c1[i]);
             }
 #pragma unroll
             for (int i = 0; i < 4; i++) {
                 const int n = grp * 16 + 4 * g + i;
                 int msum = 0;
 #pragma unroll
-                for (int j = 0; j < 8; j++) msum += mn[j] * (int) s_ss[n][j];
+                for (int j = 0; j < 8; j++) msum += __mul24(mn[j], (int) s_ss[n][j]);  // 6 x 13 bits
                 const double da = (double) s_d[n];
                 const double d = (double) dw * da;
                 const double dmin = (double) dmw * da;
