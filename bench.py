@@ -73,7 +73,8 @@ def weight_bytes(cfg, wtype) -> dict:
     return out
 
 
-def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cpu: bool, cpu_seconds: float):
+def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cpu: bool, cpu_seconds: float,
+                 cpu_variants: bool = True):
     from openasr_amd import decoders as D
     from openasr_amd import ggml as g
 
@@ -135,7 +136,7 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
 
     cpu = None
     if want_cpu:
-        cpu = cpu_baseline(w, wl, sess, out[-1], cpu_seconds)
+        cpu = cpu_baseline(w, wl, sess, out[-1], cpu_seconds, variants=cpu_variants)
     result = dict(tok_s=tok_s, ms_per_step=elapsed * 1e3 / steps, steps=steps, prefill_ms=prefill_s * 1e3,
                   n_prefill=n_prefill, gemv_ms=gemv_ms, gemv_launches=gemv_n, gemv_gbs=gemv_gbs,
                   weight_bytes=alg_bytes, eager_step_ms=eager_ms, breakdown=breakdown, cpu=cpu)
@@ -194,7 +195,38 @@ def run_whisper(n_tokens: int, cpu_seconds: float):
     return res
 
 
-def cpu_baseline(w, wl, sess, tokens, seconds: float):
+def measured_copy_gbs(reps: int = 20) -> float:
+    """HBM bandwidth a plain device copy reaches through the backend: a 1 GiB
+    f32 CONT (read 1 GiB + write 1 GiB per compute), timed over graph replays"""
+    from openasr_amd import ggml as g
+
+    plugin = g.plugin()
+    n = 256 << 20  # floats
+    G = g.Graph(n_tensors=8, graph_size=16)
+    src = G.new(g.F32, n)
+    dst = G.lib.ggml_cont(G.ctx, G.lib.ggml_reshape_2d(G.ctx, src, 1 << 20, 256))
+    G.build(dst)
+    G.allocate(plugin.buft)
+    G.set(src, np.zeros(n, np.float32))
+    sec = _timed_graph(G, plugin.backend, reps)
+    G.free()
+    gbs = 2 * 4 * n / sec / 1e9
+    log(f"[bench] device copy 1 GiB -> 1 GiB: {sec * 1e3:.3f} ms = {gbs:.0f} GB/s")
+    return gbs
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(w, wl, sess, tokens, seconds: float, variants: bool = True):
     """The CPU oracle's batched decode step (oracle/ref_decoder.c, the checker)
     on the host cores, continuing from the device's KV state: a bounded sample
     of the same workload, timed for ~`seconds`."""
@@ -208,18 +240,34 @@ def cpu_baseline(w, wl, sess, tokens, seconds: float):
             r.k[s][layer][...] = k
             r.v[s][layer][...] = v
         r.pos[s] = sess.position(s)
+    start = int(r.pos.min())
     cur = np.asarray(tokens, np.int32)
-    n = 0
-    t0 = time.perf_counter()
-    while time.perf_counter() - t0 < seconds and r.pos.max() < wl.max_positions - 1:
-        cur = r.step(cur)
-        n += 1
-    dt = time.perf_counter() - t0
-    val = wl.n_seq * n / dt
+
+    def timed(th: int, budget: float):
+        r.threads = th
+        nonlocal cur
+        n = 0
+        t0 = time.perf_counter()
+        while time.perf_counter() - t0 < budget and r.pos.max() < wl.max_positions - 1:
+            cur = r.step(cur)
+            n += 1
+        dt = time.perf_counter() - t0
+        return n, dt, wl.n_seq * n / max(dt, 1e-9)
+
+    n, dt, val = timed(threads, seconds)
     log(f"[bench] cpu oracle: {n} batched decode steps in {dt:.1f}s on {threads} threads = {val:.2f} tokens/s")
-    return {"value": round(val, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{n} batched decode steps of {wl.name} (oracle ref_qwen_decode_batch, {threads} OpenMP "
-                      f"threads) continuing from the device KV state at position {int(r.pos.min()) - n}"}
+    res = {"value": round(val, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
+           "sample": f"{n} batched decode steps of {wl.name} (oracle ref_qwen_decode_batch, {threads} OpenMP "
+                     f"threads) continuing from the device KV state at position {start}",
+           "cpu": cpu_model()}
+    if variants:
+        # the reference's decoder thread policy (available / 2, at least 2) and one thread, shorter samples
+        half = max(2, threads // 2)
+        _, _, val2 = timed(half, seconds / 3)
+        _, _, val1 = timed(1, seconds / 3)
+        log(f"[bench] cpu oracle: {val2:.2f} tokens/s on {half} threads, {val1:.2f} tokens/s on 1 thread")
+        res.update(tokens_per_s_half_threads=round(val2, 3), half_threads=half, tokens_per_s_1_thread=round(val1, 3))
+    return res
 
 
 # ------------------------------------------------------------ kernel sweep --
@@ -372,9 +420,11 @@ def main() -> int:
     main_r = run_workload(a.workload, a.steps, a.warmup, a.profile_iters, not a.no_cpu, a.cpu_seconds)
     b1 = None
     if not a.no_b1 and a.workload != "qwen3-0.6b-q8_0-b1":
-        r1 = run_workload("qwen3-0.6b-q8_0-b1", min(a.steps, 128), a.warmup, a.profile_iters, False, 0)
+        r1 = run_workload("qwen3-0.6b-q8_0-b1", min(a.steps, 128), a.warmup, a.profile_iters, not a.no_cpu,
+                          min(4.0, a.cpu_seconds), cpu_variants=False)
         b1 = {"tokens_per_s": round(r1["tok_s"], 1), "ms_per_step": round(r1["ms_per_step"], 4),
-              "mul_mat_q8_0_gbs": round(r1["gemv_gbs"], 1)}
+              "mul_mat_q8_0_gbs": round(r1["gemv_gbs"], 1),
+              "cpu_tokens_per_s": r1["cpu"]["value"] if r1["cpu"] else None}
     long = None
     if not a.no_long and a.workload != "qwen3-1.7b-q4_K-b8":
         rl = run_workload("qwen3-1.7b-q4_K-b8", min(a.steps, 64), a.warmup, max(4, a.profile_iters // 4), False, 0)
@@ -384,6 +434,7 @@ def main() -> int:
     whisper = None
     if not a.no_whisper:
         whisper = run_whisper(224, 0 if a.no_cpu else min(5.0, a.cpu_seconds))
+    copy_gbs = measured_copy_gbs()
     frac = main_r["gemv_gbs"] / HBM_PEAK_GBS
     # measured HBM bytes per GEMV launch (rocprofv3 FETCH_SIZE / WRITE_SIZE
     # runs of `bench.py --traffic-probe`, summarised by openasr_amd.pmc)
@@ -408,7 +459,7 @@ def main() -> int:
                    "head_dim 128, ffn 3072, vocab 151936)", "global_batch": 8, "seq_len": 1024,
                    "prefill_positions": main_r["n_prefill"], "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(main_r["gemv_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(frac, 4), "traffic": traffic,
+                     "frac": round(frac, 4), "traffic": traffic, "copy_gbs_measured": round(copy_gbs, 1),
                      "alg_bytes_per_launch": round(main_r["weight_bytes"] / max(1, main_r["gemv_launches"]), 1),
                      "launches": main_r["gemv_launches"],
                      "kernel": "k_gemv_q4_K: the quantized GEMV launches of one decode step (per layer QKV, "

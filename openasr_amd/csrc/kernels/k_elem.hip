@@ -7,6 +7,8 @@
 // argmax. All are HBM- or latency-bound; each is one pass over its data.
 #include "../mi355x_common.h"
 #include "../ops.h"
+
+#include <algorithm>
 #include "../quant_dev.h"
 
 namespace mi355x {
@@ -578,8 +580,47 @@ __global__ void k_copy(tview d, int dtype, tview a, int atype, int64_t n) {
     }
 }
 
+// dense copies: 16 bytes per lane per iteration, grid-stride (same type), or
+// four f32 -> four f16 (RNE) per lane
+__global__ __launch_bounds__(256) void k_copy_dense(const uint4 * __restrict__ src, uint4 * __restrict__ dst,
+                                                    int64_t n16) {
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n16; i += (int64_t) gridDim.x * blockDim.x)
+        dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(256) void k_copy_f32_f16_dense(const float4 * __restrict__ src, uint2 * __restrict__ dst,
+                                                            int64_t n4) {
+    for (int64_t i = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t) gridDim.x * blockDim.x) {
+        const float4 v = src[i];
+        dst[i] = make_uint2((uint32_t) float_to_half_bits(v.x) | ((uint32_t) float_to_half_bits(v.y) << 16),
+                            (uint32_t) float_to_half_bits(v.z) | ((uint32_t) float_to_half_bits(v.w) << 16));
+    }
+}
+
+static bool dense(const tview & v, int64_t esize) {
+    return v.nb[0] == esize && v.nb[1] == v.ne[0] * v.nb[0] && v.nb[2] == v.ne[1] * v.nb[1] &&
+           v.nb[3] == v.ne[2] * v.nb[2];
+}
+
 void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStream_t s, int n_cu) {
     const int64_t n = a.ne[0] * a.ne[1] * a.ne[2] * a.ne[3];
+    const int64_t asz = atype == GGML_TYPE_F16 ? 2 : 4, dsz = dtype == GGML_TYPE_F16 ? 2 : 4;
+    const bool aligned = ((uintptr_t) a.data | (uintptr_t) d.data) % 16 == 0;
+    if (aligned && dense(a, asz) && dense(d, dsz)) {
+        const int64_t blocks = 1024 * (int64_t) n_cu;  // one 16-byte piece per lane up to 256 Mi pieces
+        if (atype == dtype && (n * asz) % 16 == 0) {
+            const int64_t n16 = n * asz / 16;
+            hipLaunchKernelGGL(k_copy_dense, dim3((unsigned) std::min<int64_t>(blocks, (n16 + 255) / 256)), dim3(256),
+                               0, s, (const uint4 *) a.data, (uint4 *) d.data, n16);
+            return;
+        }
+        if (atype == GGML_TYPE_F32 && dtype == GGML_TYPE_F16 && n % 4 == 0 && (uintptr_t) d.data % 8 == 0) {
+            const int64_t n4 = n / 4;
+            hipLaunchKernelGGL(k_copy_f32_f16_dense, dim3((unsigned) std::min<int64_t>(blocks, (n4 + 255) / 256)),
+                               dim3(256), 0, s, (const float4 *) a.data, (uint2 *) d.data, n4);
+            return;
+        }
+    }
     hipLaunchKernelGGL(k_copy, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, dtype, a, atype, n);
 }
 

@@ -1,7 +1,7 @@
 """Summaries of rocprofv3 hardware-counter runs of the decode benchmark.
 
 `python bench.py --traffic-probe` is a fixed short program: a 256 MiB f32
-copy through the backend (k_copy reads and writes exactly 256 MiB), then two
+copy through the backend (the copy kernel reads and writes exactly 256 MiB), then two
 eager decode steps. Run it twice under `rocprofv3 --pmc FETCH_SIZE` and
 `rocprofv3 --pmc WRITE_SIZE` (one counter per run, `--output-format csv`),
 then
@@ -50,10 +50,12 @@ def _per_dispatch(rows):
 
 
 def _copy_scale(disp, bytes_moved: int) -> float:
-    vals = [v for k, g, v in disp.values() if k == "k_copy" and g >= (1 << 20)]
+    """bytes moved / counter value of the calibration copy (the largest copy
+    dispatch of the run: the 256 MiB one)"""
+    vals = [v for k, g, v in disp.values() if k.startswith("k_copy")]
     if not vals:
         raise RuntimeError("the calibration copy is missing from the counter run")
-    return bytes_moved / (vals[0] * 1024.0)
+    return bytes_moved / (max(vals) * 1024.0)
 
 
 def _last_step(disp):
