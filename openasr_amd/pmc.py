@@ -107,19 +107,39 @@ def summarize(fetch_dir: str, write_dir: str, workload: str | None = None) -> di
     return out
 
 
+def markdown(s: dict) -> str:
+    """the per-step GEMV figure and the per-kernel table of a summary"""
+    d = s["decode_step"]
+    lines = [f"Scale factors (bytes moved / counter bytes on the copy): FETCH_SIZE x {s['fetch_scale']:.4f}, "
+             f"WRITE_SIZE x {s['write_scale']:.4f}.", "",
+             "Last decode step, quantized GEMV launches only:", "",
+             "| launches | HBM bytes (scaled FETCH+WRITE) | algorithmic bytes | ratio |", "|---|---|---|---|"]
+    if "gemv_algorithmic_bytes" in d:
+        lines.append(f"| {d['gemv_launches']} | {d['gemv_hbm_bytes'] / 1e6:.1f} MB "
+                     f"({d['gemv_hbm_bytes_per_launch'] / 1e6:.3f} MB / launch) | "
+                     f"{d['gemv_algorithmic_bytes'] / 1e6:.1f} MB ({d['gemv_algorithmic_bytes_per_launch'] / 1e6:.3f} "
+                     f"MB / launch) | {d['traffic_over_algorithmic']:.3f} |")
+    lines += ["", "Per kernel (all dispatches of the probe, prefill included; grid in threads):", "",
+              "| kernel[grid] | dispatches | FETCH MB / dispatch | WRITE MB / dispatch |", "|---|---|---|---|"]
+    for k, v in s["kernels"].items():
+        lines.append(f"| {k} | {v['dispatches']} | {v['fetch_bytes_avg'] / 1e6:.3f} | {v['write_bytes_avg'] / 1e6:.3f} |")
+    return "\n".join(lines)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("fetch_dir")
     ap.add_argument("write_dir")
     ap.add_argument("--workload", default=None)
     ap.add_argument("--out", default=None)
+    ap.add_argument("--md", action="store_true", help="print the markdown tables instead of the JSON")
     a = ap.parse_args()
     s = summarize(a.fetch_dir, a.write_dir, a.workload)
     text = json.dumps(s, indent=1)
     if a.out:
         with open(a.out, "w") as f:
             f.write(text + "\n")
-    print(text)
+    print(markdown(s) if a.md else text)
     return 0
 
 

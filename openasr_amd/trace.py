@@ -1,0 +1,85 @@
+"""Per-kernel summary of one decode step from a rocprofv3 kernel trace of
+`bench.py` (HIP-graph capture off, so every launch is a traced dispatch):
+
+    OPENASR_MI355X_HIP_GRAPHS=0 rocprofv3 --kernel-trace --stats --output-format csv \\
+        -d prof_bench -o run -- python3 bench.py --no-cpu --no-long --no-whisper \\
+        --steps 16 --warmup 2 --profile-iters 4
+    python -m openasr_amd.trace prof_bench/run_kernel_trace.csv
+
+Decode steps are the launches between consecutive `k_argmax_final`
+dispatches; the two workloads of the run (Qwen3-0.6B Q4_K batch 8, then Q8_0
+batch 1) are told apart by the gap between them. Eight timed steps of each are
+averaged (the first three argmax dispatches of a workload belong to prefill
+and warmup).
+"""
+
+from __future__ import annotations
+
+import argparse
+import collections
+import csv
+import os
+import sys
+
+
+def _steps(rows, which: int, n: int = 8):
+    idx = [i for i, r in enumerate(rows) if "k_argmax_final" in r["Kernel_Name"]]
+    groups = [[idx[0]]]
+    for a, b in zip(idx, idx[1:]):
+        if int(rows[b]["Start_Timestamp"]) - int(rows[a]["End_Timestamp"]) > 200e6:
+            groups.append([])
+        groups[-1].append(b)
+    g = groups[which]
+    a, b = g[3], g[3 + n]
+    return rows[a + 1:b + 1], n
+
+
+def table(trace: str, which: int, workload: str) -> str:
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    from openasr_amd import decoders as D
+    from openasr_amd import ggml as g
+    from openasr_amd.pmc import gemv_algorithmic_bytes
+
+    with open(trace, newline="") as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    win, n = _steps(rows, which)
+    st = collections.defaultdict(list)
+    for r in win:
+        name = r["Kernel_Name"].split("(")[0].replace("void ", "").replace("mi355x::", "")
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        st[(name, grid, int(r["Workgroup_Size_X"]))].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    lines = ["| kernel | grid (threads) | workgroup | launches / step | avg us | min us | us / step |",
+             "|---|---|---|---|---|---|---|"]
+    tot = gemv = gemv_n = 0
+    for k, v in sorted(st.items(), key=lambda kv: -sum(kv[1])):
+        tot += sum(v)
+        if k[0].startswith("k_gemv") or k[0].startswith("k_mmv"):
+            gemv += sum(v)
+            gemv_n += len(v)
+        lines.append(f"| {k[0]} | {k[1]} | {k[2]} | {len(v) / n:.0f} | {sum(v) / len(v) / 1e3:.2f} | "
+                     f"{min(v) / 1e3:.2f} | {sum(v) / n / 1e3:.1f} |")
+    wl = D.WORKLOADS[workload]
+    alg, _ = gemv_algorithmic_bytes(wl.shape, wl.wtype == g.Q4_K, wl.n_seq)
+    gemv_us = gemv / n / 1e3
+    span = (int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / n / 1e3
+    lines += ["", f"Kernel time per decode step: {tot / n / 1e3:.1f} us over {len(win) / n:.0f} launches "
+                  f"(first start to last end {span:.1f} us with eager launches and profiler overhead).",
+              f"Quantized GEMV launches per step: {gemv_n / n:.0f}, {gemv_us:.1f} us; algorithmic bytes "
+              f"{alg / 1e6:.1f} MB (weights + int8 activations + f32 outputs) -> {alg / (gemv_us * 1e-6) / 1e9:.0f} GB/s "
+              f"= {alg / (gemv_us * 1e-6) / 1e9 / 8000:.1%} of 8 TB/s; average GEMV launch {gemv_us / (gemv_n / n):.2f} us."]
+    return "\n".join(lines)
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("trace")
+    a = ap.parse_args()
+    print("## Q4_K weights, batch 8\n")
+    print(table(a.trace, 0, "qwen3-0.6b-q4_K-b8"))
+    print("\n## Q8_0 weights, batch 1\n")
+    print(table(a.trace, 1, "qwen3-0.6b-q8_0-b1"))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
