@@ -4,18 +4,19 @@
 //
 // The result is defined chunk-wise over fixed 64-position KV chunks, the
 // same on every launch shape:
-//   per chunk c   s = f32(sum_f64(f16(q) * k)) * scale + mask   (masked
+//   per chunk c   for each live (unmasked) position, in f32:
+//                   s = fma-chain_d(k[d], f16(q)[d]) * scale + mask
+//                 (the chain runs over the dims in order from 0; masked
 //                 positions are skipped outright, as ggml-cpu does)
-//                 m_c = max s, p = exp(s - m_c), l_c = sum_f64 p,
-//                 a_c = sum_f64 p * v
-//   combine       M = max m_c; for c in order: w = exp(m_c - M),
+//                 m_c = max s, p = exp(s - m_c); over the live positions in
+//                 order, l_c = l_c + p and a_c = fma(p, v, a_c) in f32
+//   combine       M = max m_c; for c in order, in f64: w = exp(m_c - M),
 //                 L += w * l_c, O += w * a_c; out = f32(O / L)
-// Products of two halves are exact in f32 and of a float and a half exact in
-// f64, so the chunk sums do not depend on how positions are spread over
-// lanes; the combine runs in chunk order. The CPU reference evaluates the
-// same definition (oracle fidelity 4).
+// Every chain is sequential in one thread, so each launch form below gives
+// the same bits. The CPU reference evaluates the same definition (oracle
+// fidelity 5).
 //
-// Two launch forms compute it:
+// Three launch forms compute it:
 //   decode one wave per (chunk, query head, sequence) for a single query
 //          position: mask first, then the chunk's K and V, no barriers;
 //          partials to scratch, combined by a second launch.
@@ -23,13 +24,16 @@
 //          the chunk's mask first and skips a fully masked chunk without
 //          touching K/V (the graph always passes the full fixed span,
 //          nn/decoder.rs:1295-1301), then issues all of its K and V loads at
-//          once; partials go to scratch and a second launch combines them
-//          per tile. Used for decode, where tiles alone cannot fill the chip.
+//          once into LDS; partials go to scratch and a second launch combines
+//          them per tile.
 //   full   one workgroup per (kv head, sequence, query tile) walks every
 //          chunk twice (chunk maxima, then sums). Used for prefill.
-// Both can quantize their output straight into the activation layout of the
-// MUL_MAT that consumes it (the attention output projection), since a tile
-// holds all query heads of one kv head: g*D consecutive elements of a column.
+// In split and full, lane p of each wave takes position p for the scores
+// (wave w the tile rows w, w + 4, ...) and each thread one row's run of dims
+// for P * V. Both can quantize their output straight into the activation
+// layout of the MUL_MAT that consumes it (the attention output projection),
+// since a tile holds all query heads of one kv head: g*D consecutive
+// elements of a column.
 #include "../mi355x_common.h"
 #include "../ops.h"
 #include "../quant_dev.h"
@@ -65,13 +69,13 @@ __device__ __forceinline__ int64_t fa_orow(const fattn_args & a, const fa_tile &
 
 template <int D, int R>
 struct alignas(16) fa_smem {
-    float q[R][D];           // f16-rounded queries; after the combine, the output rows
-    float s[R][kFaChunk];    // scores, then p
-    float mask[R][kFaChunk]; // per query position of the tile
+    uint4 k[kFaChunk][D / 8 + 1];  // the chunk's K rows, padded: conflict-free row reads
+    uint4 v[kFaChunk][D / 8];      // the chunk's V rows
+    float q[R][D];                 // f16-rounded queries; after the combine, the output rows
+    float s[R][kFaChunk];          // scores, then p
+    float mask[R][kFaChunk];       // per query position of the tile
+    uint64_t live[R];              // live positions of the chunk per row
     float m[R];
-    double l[R];
-    double red[4][R][D];
-    float w[R];
 };
 
 __device__ __forceinline__ void unpack8(const uint4 & u, float * f) {
@@ -81,6 +85,24 @@ __device__ __forceinline__ void unpack8(const uint4 & u, float * f) {
         f[2 * i] = half_bits_to_float((uint16_t) (w[i] & 0xFFFF));
         f[2 * i + 1] = half_bits_to_float((uint16_t) (w[i] >> 16));
     }
+}
+
+// the score chain of one position: acc = fma(k[d], q[d], acc) over the dims
+// in order, from 0, in f32 (k is f16, so the compiler may read it in place)
+template <int D>
+__device__ __forceinline__ float fa_dot(const uint4 (&kr)[D / 8], const float * q) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < D / 8; u++) {
+        float kf[8];
+        unpack8(kr[u], kf);
+        const float4 q0 = *(const float4 *) (q + 8 * u);
+        const float4 q1 = *(const float4 *) (q + 8 * u + 4);
+        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc = fmaf(kf[i], qv[i], acc);
+    }
+    return acc;
 }
 
 // mask of chunk c for the tile's query positions; true if any entry is live
@@ -105,28 +127,38 @@ __device__ __forceinline__ bool fa_load_mask(const fattn_args & a, const fa_tile
     return __syncthreads_or(live) != 0;
 }
 
-// K: thread t holds position t/4, dims (t%4)*D/4 .. +D/4
-template <int D>
-__device__ __forceinline__ void fa_load_k(const fattn_args & a, const fa_tile & t, int c, uint4 (&kr)[D / 32]) {
+// the chunk's K (and V) rows into registers, all requested at once: thread t
+// takes the 16-byte pieces t, t + 256, ... of the row-major chunk. Rows past
+// the span repeat the chunk's last row (in bounds; such positions are masked).
+template <int D, bool WITH_V>
+struct fa_kv_regs {
+    static constexpr int NP = kFaChunk * D / 8 / kFaThreads;
+    uint4 k[NP];
+    uint4 v[WITH_V ? NP : 1];
+};
+
+template <int D, bool WITH_V>
+__device__ __forceinline__ void fa_load_kv(const fattn_args & a, const fa_tile & t, int c, fa_kv_regs<D, WITH_V> & r) {
+    constexpr int RP = D / 8;
     const int clen = min(kFaChunk, a.n_kv - c * kFaChunk);
-    const int p = (int) threadIdx.x >> 2, sk = (int) threadIdx.x & 3;
-    const char * kb = a.k + (int64_t) t.kvh * a.k_nb2 + (int64_t) t.kv_seq * a.k_nb3 +
-                      (int64_t) (c * kFaChunk + p) * a.k_nb1 + sk * (D / 4) * 2;
+    const char * kb = a.k + (int64_t) t.kvh * a.k_nb2 + (int64_t) t.kv_seq * a.k_nb3 + (int64_t) c * kFaChunk * a.k_nb1;
+    const char * vb = a.v + (int64_t) t.kvh * a.v_nb2 + (int64_t) t.kv_seq * a.v_nb3 + (int64_t) c * kFaChunk * a.v_nb1;
 #pragma unroll
-    for (int u = 0; u < D / 32; u++) kr[u] = p < clen ? *(const uint4 *) (kb + 16 * u) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < fa_kv_regs<D, WITH_V>::NP; i++) {
+        const int piece = (int) threadIdx.x + i * kFaThreads, row = min(piece / RP, clen - 1), col = piece % RP;
+        r.k[i] = *(const uint4 *) (kb + (int64_t) row * a.k_nb1 + 16 * col);
+        if constexpr (WITH_V) r.v[i] = *(const uint4 *) (vb + (int64_t) row * a.v_nb1 + 16 * col);
+    }
 }
 
-// V: thread t holds dims (t % (D/8))*8 .. +8 of positions t/(D/8) + NPG*j
-template <int D>
-__device__ __forceinline__ void fa_load_v(const fattn_args & a, const fa_tile & t, int c, uint4 (&vr)[D / 32]) {
-    constexpr int DS = D / 8, NPG = kFaThreads / DS;
-    const int clen = min(kFaChunk, a.n_kv - c * kFaChunk);
-    const int ds = (int) threadIdx.x % DS, pg = (int) threadIdx.x / DS;
-    const char * vb = a.v + (int64_t) t.kvh * a.v_nb2 + (int64_t) t.kv_seq * a.v_nb3 + ds * 16;
+template <int D, int R, bool WITH_V>
+__device__ __forceinline__ void fa_store_kv(const fa_kv_regs<D, WITH_V> & r, fa_smem<D, R> & sm) {
+    constexpr int RP = D / 8;
 #pragma unroll
-    for (int j = 0; j < D / 32; j++) {
-        const int p = pg + NPG * j;
-        vr[j] = p < clen ? *(const uint4 *) (vb + (int64_t) (c * kFaChunk + p) * a.v_nb1) : make_uint4(0, 0, 0, 0);
+    for (int i = 0; i < fa_kv_regs<D, WITH_V>::NP; i++) {
+        const int piece = (int) threadIdx.x + i * kFaThreads;
+        sm.k[piece / RP][piece % RP] = r.k[i];
+        if constexpr (WITH_V) sm.v[piece / RP][piece % RP] = r.v[i];
     }
 }
 
@@ -140,105 +172,80 @@ __device__ __forceinline__ void fa_load_q(const fattn_args & a, const fa_tile & 
     }
 }
 
-// scores of the chunk into sm.s (needs sm.q and sm.mask; caller syncs after)
+// scores of the chunk into sm.s: lane p of every wave takes position p (its
+// K row from LDS), wave w the rows w, w + 4, ... (needs sm.k, sm.q, sm.mask;
+// the caller syncs after)
 template <int D, int R>
-__device__ __forceinline__ void fa_scores(const fattn_args & a, const fa_tile & t, const uint4 (&kr)[D / 32],
-                                          fa_smem<D, R> & sm) {
-    const int p = (int) threadIdx.x >> 2, sk = (int) threadIdx.x & 3;
-    float kf[D / 4];
+__device__ __forceinline__ void fa_scores(const fattn_args & a, const fa_tile & t, fa_smem<D, R> & sm) {
+    const int p = (int) threadIdx.x & 63, wave = (int) threadIdx.x >> 6;
+    if (wave >= t.nrows) return;
+    uint4 kr[D / 8];
 #pragma unroll
-    for (int u = 0; u < D / 32; u++) unpack8(kr[u], kf + 8 * u);
-#pragma unroll
-    for (int r = 0; r < R; r++) {
-        if (r < t.nrows) {
-            const float * qr = &sm.q[r][sk * (D / 4)];
-            double acc = 0.0;
-#pragma unroll
-            for (int i = 0; i < D / 4; i++) acc += (double) (kf[i] * qr[i]);  // exact products
-            acc += __shfl_xor(acc, 1);
-            acc += __shfl_xor(acc, 2);
-            if (sk == 0) {
-                const float mv = sm.mask[r / t.g][p];
-                sm.s[r][p] = mv == -INFINITY ? -INFINITY : (float) acc * a.scale + mv;
-            }
-        }
+    for (int u = 0; u < D / 8; u++) kr[u] = sm.k[p][u];
+    for (int r = wave; r < t.nrows; r += 4) {
+        const float acc = fa_dot<D>(kr, &sm.q[r][0]);
+        const float mv = sm.mask[r / t.g][p];
+        sm.s[r][p] = mv == -INFINITY ? -INFINITY : acc * a.scale + mv;
     }
 }
 
-// chunk maximum m_c, p = exp(s - m_c) in place, l_c; one wave per row
-template <int D, int R>
+// chunk maximum m_c and (WITH_P) p = exp(s - m_c) in place and the live
+// positions; one wave per row
+template <int D, int R, bool WITH_P>
 __device__ __forceinline__ void fa_softmax_chunk(const fa_tile & t, fa_smem<D, R> & sm) {
     const int lane = (int) threadIdx.x & 63, wave = (int) threadIdx.x >> 6;
     for (int r = wave; r < t.nrows; r += 4) {
         const float s = sm.s[r][lane];
         const float m = wave_max(s);
-        const float p = s == -INFINITY ? 0.0f : expf_det(s - m);
-        sm.s[r][lane] = p;
-        const double l = wave_sum_d((double) p);
+        const bool live = s != -INFINITY;
+        if constexpr (WITH_P) sm.s[r][lane] = live ? expf_det(s - m) : 0.0f;
+        const uint64_t bits = __ballot(live);
         if (lane == 0) {
             sm.m[r] = m;
-            sm.l[r] = l;
+            sm.live[r] = bits;
         }
     }
 }
 
-// a_c = sum p * v into sm.red (per wave; the caller sums the four waves in
-// order); caller syncs after
-template <int D, int R>
-__device__ __forceinline__ void fa_pv(const fa_tile & t, const uint4 (&vr)[D / 32], fa_smem<D, R> & sm) {
-    constexpr int DS = D / 8, NPG = kFaThreads / DS;
-    const int lane = (int) threadIdx.x & 63, wave = (int) threadIdx.x >> 6;
-    const int ds = (int) threadIdx.x % DS, pg = (int) threadIdx.x / DS;
-    double acc[R][8];
+// P * V of one row's dims [d0, d0 + DPT): the live positions in order,
+// l = l + p and acc = fma(p, v, acc) in f32 (needs sm.s, sm.v, sm.live)
+template <int D, int R, int DPT>
+__device__ __forceinline__ void fa_pv_row(const fa_smem<D, R> & sm, int r, int d0, float (&acc)[DPT], float & l) {
+    const uint64_t live = sm.live[r];
+    const uint16_t * vb = (const uint16_t *) &sm.v[0][0] + d0;
 #pragma unroll
-    for (int r = 0; r < R; r++)
+    for (int i = 0; i < DPT; i++) acc[i] = 0.0f;
+    l = 0.0f;
+    for (int j = 0; j < kFaChunk; j++) {
+        if ((live >> j) & 1) {
+            const float p = sm.s[r][j];
+            l = l + p;
+            const uint16_t * vr = vb + j * D;
 #pragma unroll
-        for (int i = 0; i < 8; i++) acc[r][i] = 0.0;
-#pragma unroll
-    for (int j = 0; j < D / 32; j++) {
-        const int p = pg + NPG * j;
-        float vf[8];
-        unpack8(vr[j], vf);
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            const float pr = r < t.nrows ? sm.s[r][p] : 0.0f;
-            if (pr != 0.0f) {  // masked slots may hold anything, even NaN
-#pragma unroll
-                for (int i = 0; i < 8; i++) acc[r][i] += (double) pr * (double) vf[i];  // exact products
-            }
+            for (int i = 0; i < DPT; i++) acc[i] = fmaf(p, half_bits_to_float(vr[i]), acc[i]);
         }
     }
-#pragma unroll
-    for (int off = DS; off < 64; off <<= 1) {
-#pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) acc[r][i] += __shfl_xor(acc[r][i], off);
-    }
-    if (lane < DS) {
-#pragma unroll
-        for (int r = 0; r < R; r++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) sm.red[wave][r][ds * 8 + i] = acc[r][i];
-    }
 }
 
+// dims per thread of the P * V step: every (row, dim) of the tile has one thread
 template <int D, int R>
-__device__ __forceinline__ double fa_red_sum(const fa_smem<D, R> & sm, int r, int d) {
-    return ((sm.red[0][r][d] + sm.red[1][r][d]) + sm.red[2][r][d]) + sm.red[3][r][d];
-}
+struct fa_pv_shape {
+    static constexpr int DPT = R * D >= 2 * kFaThreads ? R * D / kFaThreads : 1;
+    static constexpr int TPR = D / DPT;  // threads per row
+};
 
-// output rows are in sm.q; quantize the tile's column segments for the next
-// MUL_MAT (Q8_K for Q4_K weights, Q8_0 for Q8_0 weights)
-template <int D, int R>
-__device__ __forceinline__ void fa_quantize_out(const fattn_args & a, const fa_tile & t, fa_smem<D, R> & sm) {
+// the tile's output rows are in LDS (row r at rows + r * D); quantize its
+// column segments for the next MUL_MAT (Q8_K for Q4_K weights, Q8_0 for Q8_0
+// weights)
+template <int D>
+__device__ __forceinline__ void fa_quantize_out(const fattn_args & a, const fa_tile & t, const float * rows) {
     const int lane = (int) threadIdx.x & 63, wave = (int) threadIdx.x >> 6;
     const int seg = t.g * D;
     const int64_t K = (int64_t) a.hq * D;
     const int64_t e0 = (int64_t) t.kvh * seg;
     for (int tql = 0; tql < t.ntq; tql++) {
         const int64_t col = (int64_t) t.seq * a.n_q + t.tq0 + tql;
-        const float * row = &sm.q[tql * t.g][0];
+        const float * row = rows + (int64_t) tql * t.g * D;
         for (int piece = wave; piece * 256 < seg; piece += 4) {
             const int e = piece * 256 + lane * 4;
             const float4 v = e < seg ? *(const float4 *) (row + e) : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -260,63 +267,73 @@ __device__ __forceinline__ void fa_quantize_out(const fattn_args & a, const fa_t
 
 template <int D, int R>
 __global__ __launch_bounds__(kFaThreads) void k_fattn_split(fattn_args a, float * __restrict__ part_m,
-                                                            double * __restrict__ part_l,
-                                                            double * __restrict__ part_acc) {
+                                                            float * __restrict__ part_l,
+                                                            float * __restrict__ part_acc) {
     __shared__ fa_smem<D, R> sm;
+    using PV = fa_pv_shape<D, R>;
     const fa_tile t = fa_tile_of(a);
     const int c = (int) blockIdx.x, tid = (int) threadIdx.x;
     const int64_t prow = (int64_t) t.gti * R;  // partial row of tile row 0
 
     if (fa_load_mask<D, R>(a, t, c, sm)) {
-        uint4 kr[D / 32], vr[D / 32];
-        fa_load_k<D>(a, t, c, kr);
-        fa_load_v<D>(a, t, c, vr);
+        fa_kv_regs<D, true> kv;
+        fa_load_kv<D, true>(a, t, c, kv);
         fa_load_q<D, R>(a, t, sm);
+        fa_store_kv<D, R, true>(kv, sm);
         __syncthreads();
-        fa_scores<D, R>(a, t, kr, sm);
+        fa_scores<D, R>(a, t, sm);
         __syncthreads();
-        fa_softmax_chunk<D, R>(t, sm);
+        fa_softmax_chunk<D, R, true>(t, sm);
         __syncthreads();
-        fa_pv<D, R>(t, vr, sm);
-        __syncthreads();
-        for (int idx = tid; idx < t.nrows * D; idx += kFaThreads) {
-            const int r = idx / D, d = idx % D;
-            part_acc[((prow + r) * a.n_chunks + c) * D + d] = fa_red_sum<D, R>(sm, r, d);
-        }
-        if (tid < t.nrows) {
-            part_m[(prow + tid) * a.n_chunks + c] = sm.m[tid];
-            part_l[(prow + tid) * a.n_chunks + c] = sm.l[tid];
+        const int r = tid / PV::TPR, d0 = (tid % PV::TPR) * PV::DPT;
+        if (r < t.nrows) {
+            float acc[PV::DPT], l;
+            fa_pv_row<D, R, PV::DPT>(sm, r, d0, acc, l);
+            float * pa = part_acc + ((prow + r) * a.n_chunks + c) * D + d0;
+#pragma unroll
+            for (int i = 0; i < PV::DPT; i++) pa[i] = acc[i];
+            if (d0 == 0) {
+                part_m[(prow + r) * a.n_chunks + c] = sm.m[r];
+                part_l[(prow + r) * a.n_chunks + c] = l;
+            }
         }
     } else if (tid < t.nrows) {
         part_m[(prow + tid) * a.n_chunks + c] = -INFINITY;
-        part_l[(prow + tid) * a.n_chunks + c] = 0.0;
+        part_l[(prow + tid) * a.n_chunks + c] = 0.0f;
     }
 }
 
-// combine of the split forms: one workgroup per tile, chunks in order
-template <int D, int R>
+// combine of the split forms: one workgroup per tile, chunks in order, in
+// f64. Each thread owns output elements of the tile; its partials for up to
+// CB chunks are requested together with the chunk maxima and sums, so a span
+// of up to CB chunks costs one memory round trip. The loads are unconditional
+// (chunk index clamped to the span, row 0 for a thread without an element).
+template <int D, int R, int CB0>
 __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, const float * __restrict__ part_m,
-                                                              const double * __restrict__ part_l,
-                                                              const double * __restrict__ part_acc,
+                                                              const float * __restrict__ part_l,
+                                                              const float * __restrict__ part_acc,
                                                               float * __restrict__ out) {
-    __shared__ fa_smem<D, R> sm;
-    __shared__ double s_L[R];
+    constexpr int NE = (R * D + kFaThreads - 1) / kFaThreads;  // output elements per thread
+    constexpr int CB = CB0 < 64 / NE ? CB0 : 64 / NE;          // chunks per batch of loads
+    __shared__ __align__(16) float s_out[R][D];
     __shared__ double s_w[R][kFaMaxChunks];
     __shared__ double s_l[R][kFaMaxChunks];
     const fa_tile t = fa_tile_of(a);
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t prow = (int64_t) t.gti * R;
     const int nc = a.n_chunks;
-    // every partial is requested before any is used: one memory round trip
-    // (when each thread owns at most one output element)
-    constexpr int NE = (R * D + kFaThreads - 1) / kFaThreads;
-    double pv[16];
-    const bool small = NE == 1 && nc <= 16;
-    if (small) {
-        const int r = tid / D, d = tid % D;
+    int er[NE], ed[NE];
+    bool ev[NE];
+    float pv[NE][CB];
 #pragma unroll
-        for (int k = 0; k < 16; k++)
-            pv[k] = tid < t.nrows * D && k < nc ? part_acc[((prow + r) * nc + k) * D + d] : 0.0;
+    for (int e = 0; e < NE; e++) {
+        const int idx = tid + e * kFaThreads;
+        ev[e] = idx < t.nrows * D;
+        er[e] = ev[e] ? idx / D : 0;
+        ed[e] = idx % D;
+        const float * pa = part_acc + (prow + er[e]) * nc * D + ed[e];
+#pragma unroll
+        for (int k = 0; k < CB; k++) pv[e][k] = pa[(int64_t) min(k, nc - 1) * D];
     }
     for (int r = wave; r < t.nrows; r += 4) {
         float M = -INFINITY;
@@ -325,48 +342,39 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
         for (int i = lane; i < nc; i += 64) {
             const float mc = part_m[(prow + r) * nc + i];
             s_w[r][i] = mc == -INFINITY ? 0.0 : (double) expf_det(mc - M);
-            s_l[r][i] = part_l[(prow + r) * nc + i];
+            s_l[r][i] = (double) part_l[(prow + r) * nc + i];
         }
-    }
-    __syncthreads();
-    if (tid < t.nrows) {
-        double L = 0.0;
-        for (int i = 0; i < nc; i++) {
-            if (s_w[tid][i] != 0.0) L += s_w[tid][i] * s_l[tid][i];
-        }
-        s_L[tid] = L;
     }
     __syncthreads();
 #pragma unroll
     for (int e = 0; e < NE; e++) {
-        const int idx = tid + e * kFaThreads;
-        if (idx >= t.nrows * D) continue;
-        const int r = idx / D, d = idx % D;
-        double O = 0.0;
-        if (small) {
+        if (!ev[e]) continue;
+        const int r = er[e];
+        double L = 0.0, O = 0.0;  // two chains, each in chunk order
+        for (int c0 = 0; c0 < nc; c0 += CB) {
+            if (c0 > 0) {
+                const float * pa = part_acc + ((prow + r) * nc + c0) * D + ed[e];
 #pragma unroll
-            for (int k = 0; k < 16; k++) {
-                if (k < nc && s_w[r][k] != 0.0) O += s_w[r][k] * pv[k];
+                for (int k = 0; k < CB; k++) pv[e][k] = pa[(int64_t) (min(c0 + k, nc - 1) - c0) * D];
             }
-        } else {
-            const double * pa = part_acc + (prow + r) * nc * D + d;
-            for (int c0 = 0; c0 < nc; c0 += 16) {
-                double v[16];
+            // a chunk with w = 0 adds +0, which leaves a sum that starts at +0
+            // unchanged, as skipping it would (its partials may be stale)
 #pragma unroll
-                for (int k = 0; k < 16; k++) v[k] = c0 + k < nc ? pa[(int64_t) (c0 + k) * D] : 0.0;
-#pragma unroll
-                for (int k = 0; k < 16; k++) {
-                    if (c0 + k < nc && s_w[r][c0 + k] != 0.0) O += s_w[r][c0 + k] * v[k];
-                }
+            for (int k = 0; k < CB; k++) {
+                if (c0 + k >= nc) break;
+                const double w = s_w[r][c0 + k];
+                const double tl = w * s_l[r][c0 + k], to = w * (double) pv[e][k];
+                L += w != 0.0 ? tl : 0.0;
+                O += w != 0.0 ? to : 0.0;
             }
         }
-        const float o = s_L[r] == 0.0 ? 0.0f : (float) (O / s_L[r]);
-        out[fa_orow(a, t, r) * D + d] = o;
-        sm.q[r][d] = o;
+        const float o = L == 0.0 ? 0.0f : (float) (O / L);
+        out[fa_orow(a, t, r) * D + ed[e]] = o;
+        s_out[r][ed[e]] = o;
     }
     if (a.qtype >= 0) {
         __syncthreads();
-        fa_quantize_out<D, R>(a, t, sm);
+        fa_quantize_out<D>(a, t, &s_out[0][0]);
     }
 }
 
@@ -387,12 +395,11 @@ __device__ __forceinline__ void as_norm_rope(float x0, float x1, float w0, float
 // sequence). For the scores lane p owns KV position p of the chunk (its whole
 // K row, the query broadcast from LDS); for P*V lane l owns dims D/64*l.. of
 // every position, the chunk's p values broadcast lane by lane. After the
-// mask, K and V are requested in one burst. Every sum runs in the CPU
-// reference's order (dimensions, then positions) and the p*v products are
-// exact in f64, so fused multiply-adds change nothing: the chunk partials are
-// bit-identical. The query heads of one kv head read the same K/V rows at the
-// same time, so the second read comes from cache. Waves share nothing:
-// wave-local LDS, no workgroup barriers.
+// mask, K and V are requested in one burst. Each score chain runs over the
+// dims in order in one lane, and each P*V chain over the positions in order
+// in one lane, as the definition has them. The query heads of one kv head
+// read the same K/V rows at the same time, so the second read comes from
+// cache. Waves share nothing: wave-local LDS, no workgroup barriers.
 //
 // STEP (decode step, D = 128): the wave also derives its inputs from the
 // fused QKV projection -- the query row's RMS norm * w and NEOX RoPE (the
@@ -403,7 +410,7 @@ __device__ __forceinline__ void as_norm_rope(float x0, float x1, float w0, float
 // this launch, so the write needs no ordering.
 template <int D, bool STEP>
 __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float * __restrict__ part_m,
-                                                      double * __restrict__ part_l, double * __restrict__ part_acc) {
+                                                      float * __restrict__ part_l, float * __restrict__ part_acc) {
     constexpr int DL = D / 64;
     constexpr int KU = D / 8;  // 16-byte pieces of a K row
     static_assert(!STEP || D == 128, "the step form handles 128-wide heads");
@@ -417,11 +424,16 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     const int nc = a.n_chunks;
     if (item >= (int64_t) nc * a.hq * a.n_seq) return;
     // the g query heads of one kv head are adjacent waves of a workgroup, so
-    // the second read of a chunk's K/V rows hits the CU's caches
+    // the second read of a chunk's K/V rows hits the CU's caches. The chunk
+    // index varies slowest: workgroups go to the XCDs round-robin, and the
+    // masked tail of the span (whole chunks of it) then falls on the last
+    // workgroups of the grid, spread over every XCD, instead of on the same
+    // few XCDs for every kv head.
     const int g = a.hq / a.hkv;
+    const int64_t nkt = (int64_t) a.hkv * a.n_seq;
     const int hh = (int) (item % g);
-    const int c = (int) ((item / g) % nc);
-    const int kt = (int) (item / ((int64_t) g * nc));  // seq * hkv + kvh
+    const int kt = (int) ((item / g) % nkt);  // seq * hkv + kvh
+    const int c = (int) (item / (g * nkt));
     const int kvh = kt % a.hkv, seq = kt / a.hkv;
     const int head = kvh * g + hh;
     const int hs = seq * a.hq + head;
@@ -464,7 +476,7 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     if (__ballot(live) == 0) {
         if (lane == 0) {
             part_m[prow * nc + c] = -INFINITY;
-            part_l[prow * nc + c] = 0.0;
+            part_l[prow * nc + c] = 0.0f;
         }
         if constexpr (STEP) {
             // the cache row is written even when no query attends to it
@@ -543,39 +555,25 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
         }
     }
 
-    // scores: lane = position; products of two halves are exact in f32
-    double sc = 0.0;
-#pragma unroll
-    for (int u = 0; u < D / 8; u++) {
-        float kf[8];
-        unpack8(kr[u], kf);
-        const float4 q0 = *(const float4 *) &s_q[wave][8 * u];
-        const float4 q1 = *(const float4 *) &s_q[wave][8 * u + 4];
-        const float qv[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-#pragma unroll
-        for (int i = 0; i < 8; i++) sc += (double) (kf[i] * qv[i]);
-    }
-    const float sv = live ? (float) sc * a.scale + mv : -INFINITY;
+    // scores: lane = position, the f32 fma chain over the dims in order
+    const float sc = fa_dot<D>(kr, &s_q[wave][0]);
+    const float sv = live ? sc * a.scale + mv : -INFINITY;
     const float m = wave_max(sv);
     const float p = sv == -INFINITY ? 0.0f : expf_det(sv - m);
-    // P * V: lane = dims; the sum of p in position order alongside. p_j is
-    // broadcast as an f64 through two scalar registers. Masked positions
-    // (which may hold anything in the cache, even NaN) are skipped by a
-    // scalar test of the live-position mask; a live position (finite V) with
-    // p = 0 adds exactly nothing (acc + 0 * v = acc), as the reference's skip
-    // of p = 0 does, so the whole-chunk-live case runs without any test.
-    const double pd = (double) p;
+    // P * V: lane = dims; l = l + p and acc = fma(p, v, acc) over the live
+    // positions in order, p_j broadcast through a scalar register. Masked
+    // positions (which may hold anything in the cache, even NaN) are skipped
+    // by a scalar test of the live-position mask; with every position live
+    // the loop runs without a test.
     const uint64_t live_bits = __ballot(live);
-    double acc[DL], l = 0.0;
+    float acc[DL], l = 0.0f;
 #pragma unroll
-    for (int i = 0; i < DL; i++) acc[i] = 0.0;
+    for (int i = 0; i < DL; i++) acc[i] = 0.0f;
     auto pv_step = [&](int j) {
-        const int lo = __builtin_amdgcn_readlane(__double2loint(pd), j);
-        const int hi = __builtin_amdgcn_readlane(__double2hiint(pd), j);
-        const double pj = __hiloint2double(hi, lo);
-        l += pj;
-        acc[0] = fma(pj, (double) half_bits_to_float((uint16_t) (vr[j] & 0xFFFF)), acc[0]);
-        if (DL == 2) acc[DL - 1] = fma(pj, (double) half_bits_to_float((uint16_t) (vr[j] >> 16)), acc[DL - 1]);
+        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
+        l = l + pj;
+        acc[0] = fmaf(pj, half_bits_to_float((uint16_t) (vr[j] & 0xFFFF)), acc[0]);
+        if (DL == 2) acc[DL - 1] = fmaf(pj, half_bits_to_float((uint16_t) (vr[j] >> 16)), acc[DL - 1]);
     };
     if (live_bits == ~0ull) {
 #pragma unroll
@@ -586,7 +584,7 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
             if ((live_bits >> j) & 1) pv_step(j);
         }
     }
-    double * pa = part_acc + (prow * nc + c) * D + lane * DL;
+    float * pa = part_acc + (prow * nc + c) * D + lane * DL;
 #pragma unroll
     for (int i = 0; i < DL; i++) pa[i] = acc[i];
     if (lane == 0) {
@@ -599,80 +597,74 @@ template <int D, int R>
 __global__ __launch_bounds__(kFaThreads) void k_fattn_full(fattn_args a, float * __restrict__ out) {
     __shared__ fa_smem<D, R> sm;
     __shared__ float s_mc[R][kFaMaxChunks];
-    __shared__ float s_M[R];
-    __shared__ double s_L[R];
-    constexpr int NE = (R * D + kFaThreads - 1) / kFaThreads;
+    using PV = fa_pv_shape<D, R>;
     const fa_tile t = fa_tile_of(a);
     const int tid = (int) threadIdx.x;
+    const int r = tid / PV::TPR, d0 = (tid % PV::TPR) * PV::DPT;  // this thread's output row and dims
+    const bool owner = r < t.nrows;
 
     fa_load_q<D, R>(a, t, sm);
     // pass 1: chunk maxima
     for (int c = 0; c < a.n_chunks; c++) {
         const bool live = fa_load_mask<D, R>(a, t, c, sm);
         if (live) {
-            uint4 kr[D / 32];
-            fa_load_k<D>(a, t, c, kr);
-            fa_scores<D, R>(a, t, kr, sm);
+            fa_kv_regs<D, false> kv;
+            fa_load_kv<D, false>(a, t, c, kv);
+            fa_store_kv<D, R, false>(kv, sm);
             __syncthreads();
-            fa_softmax_chunk<D, R>(t, sm);
+            fa_scores<D, R>(a, t, sm);
+            __syncthreads();
+            fa_softmax_chunk<D, R, false>(t, sm);
             __syncthreads();
         }
         if (tid < t.nrows) s_mc[tid][c] = live ? sm.m[tid] : -INFINITY;
         __syncthreads();
     }
-    if (tid < t.nrows) {
-        float M = -INFINITY;
-        for (int c = 0; c < a.n_chunks; c++) M = fmaxf(M, s_mc[tid][c]);
-        s_M[tid] = M;
-        s_L[tid] = 0.0;
+    float M = -INFINITY;
+    if (owner) {
+        for (int c = 0; c < a.n_chunks; c++) M = fmaxf(M, s_mc[r][c]);
     }
-    __syncthreads();
-    // pass 2: chunk sums combined in chunk order
-    double O[NE];
+    // pass 2: chunk sums combined in chunk order, in f64
+    double O[PV::DPT], L = 0.0;
 #pragma unroll
-    for (int e = 0; e < NE; e++) O[e] = 0.0;
+    for (int i = 0; i < PV::DPT; i++) O[i] = 0.0;
     for (int c = 0; c < a.n_chunks; c++) {
         int any = 0;
-        for (int r = 0; r < t.nrows; r++) any |= s_mc[r][c] != -INFINITY;
+        for (int rr = 0; rr < t.nrows; rr++) any |= s_mc[rr][c] != -INFINITY;
         if (!any) continue;  // uniform
         fa_load_mask<D, R>(a, t, c, sm);
-        uint4 kr[D / 32], vr[D / 32];
-        fa_load_k<D>(a, t, c, kr);
-        fa_load_v<D>(a, t, c, vr);
-        fa_scores<D, R>(a, t, kr, sm);
+        fa_kv_regs<D, true> kv;
+        fa_load_kv<D, true>(a, t, c, kv);
+        fa_store_kv<D, R, true>(kv, sm);
         __syncthreads();
-        fa_softmax_chunk<D, R>(t, sm);
-        if (tid < t.nrows) {
-            const float mc = s_mc[tid][c];
-            sm.w[tid] = mc == -INFINITY ? 0.0f : expf_det(mc - s_M[tid]);
-        }
+        fa_scores<D, R>(a, t, sm);
         __syncthreads();
-        fa_pv<D, R>(t, vr, sm);
+        fa_softmax_chunk<D, R, true>(t, sm);
         __syncthreads();
-        if (tid < t.nrows && sm.w[tid] != 0.0f) s_L[tid] += (double) sm.w[tid] * sm.l[tid];
+        if (owner) {
+            const float mc = s_mc[r][c];
+            const float w = mc == -INFINITY ? 0.0f : expf_det(mc - M);
+            if (w != 0.0f) {
+                float acc[PV::DPT], l;
+                fa_pv_row<D, R, PV::DPT>(sm, r, d0, acc, l);
+                L += (double) w * (double) l;
 #pragma unroll
-        for (int e = 0; e < NE; e++) {
-            const int idx = tid + e * kFaThreads;
-            if (idx < t.nrows * D) {
-                const int r = idx / D, d = idx % D;
-                if (sm.w[r] != 0.0f) O[e] += (double) sm.w[r] * fa_red_sum<D, R>(sm, r, d);
+                for (int i = 0; i < PV::DPT; i++) O[i] += (double) w * (double) acc[i];
             }
         }
         __syncthreads();
     }
+    if (owner) {
 #pragma unroll
-    for (int e = 0; e < NE; e++) {
-        const int idx = tid + e * kFaThreads;
-        if (idx < t.nrows * D) {
-            const int r = idx / D, d = idx % D;
-            const float o = s_L[r] == 0.0 ? 0.0f : (float) (O[e] / s_L[r]);
-            out[fa_orow(a, t, r) * D + d] = o;
-            sm.q[r][d] = o;
+        for (int i = 0; i < PV::DPT; i++) {
+            const float o = L == 0.0 ? 0.0f : (float) (O[i] / L);
+            out[fa_orow(a, t, r) * D + d0 + i] = o;
+            sm.q[r][d0 + i] = o;
         }
     }
     if (a.qtype >= 0) {
         __syncthreads();
-        fa_quantize_out<D, R>(a, t, sm);
+        fa_quantize_out<D>(a, t, &sm.q[0][0]);
     }
 }
 
@@ -683,7 +675,7 @@ static int64_t fa_tiles(const fattn_args & a) { return (int64_t) a.hkv * a.n_seq
 size_t fattn_scratch_bytes(const fattn_args & a) {
     if (!a.split) return 0;
     const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
-    return (size_t) prows * (sizeof(float) + sizeof(double) + (size_t) a.d * sizeof(double)) + 1024;
+    return (size_t) prows * (2 + (size_t) a.d) * sizeof(float) + 1024;
 }
 
 void fattn_plan(fattn_args & a, int n_cu) {
@@ -693,11 +685,19 @@ void fattn_plan(fattn_args & a, int n_cu) {
     a.q_tiles = (a.n_q + a.tq - 1) / a.tq;
     a.n_chunks = (a.n_kv + kFaChunk - 1) / kFaChunk;
     const int64_t tiles = fa_tiles(a);
-    const int64_t part_bytes = tiles * a.rows * a.n_chunks * (12 + 8 * (int64_t) a.d);
+    const int64_t part_bytes = tiles * a.rows * a.n_chunks * (8 + 4 * (int64_t) a.d);
     // split the KV span over workgroups when the tiles alone leave CUs idle
     const bool fits = a.n_chunks <= kFaMaxChunks && part_bytes <= (256LL << 20);
     if (fits && a.tq == 1) a.split = 2;  // wave per (chunk, query head)
     else a.split = fits && tiles < 2LL * n_cu ? 1 : 0;
+}
+
+template <int D, int R>
+static void launch_combine(const fattn_args & a, const float * pm, const float * pl, const float * pa, float * out,
+                           hipStream_t s) {
+    const dim3 grid(1u, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
+    if (a.n_chunks <= 16) hipLaunchKernelGGL((k_fattn_combine<D, R, 16>), grid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out);
+    else hipLaunchKernelGGL((k_fattn_combine<D, R, 64>), grid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out);
 }
 
 bool attn_step_supported(const fattn_args & a) {
@@ -710,19 +710,17 @@ void launch_attn_step(const attn_step_args & st, void * scratch, hipStream_t s) 
     const fattn_args & a = st.fa;
     const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
     float * pm = (float *) scratch;
-    char * p = (char *) (pm + prows);
-    p = (char *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
-    double * pl = (double *) p;
-    double * pa = pl + prows;
+    float * pl = pm + prows;
+    char * p = (char *) (pl + prows);
+    float * pa = (float *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
     const int64_t items = (int64_t) a.n_chunks * a.hq * a.n_seq;
     hipLaunchKernelGGL((k_fattn_decode<128, true>), dim3((unsigned) ((items + 3) / 4)), dim3(256), 0, s, st, pm, pl, pa);
-    const dim3 cgrid(1u, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
     float * out = st.out;
     switch (a.rows) {
-        case 1: hipLaunchKernelGGL((k_fattn_combine<128, 1>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out); break;
-        case 2: hipLaunchKernelGGL((k_fattn_combine<128, 2>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out); break;
-        case 4: hipLaunchKernelGGL((k_fattn_combine<128, 4>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out); break;
-        default: hipLaunchKernelGGL((k_fattn_combine<128, 8>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out); break;
+        case 1: launch_combine<128, 1>(a, pm, pl, pa, out, s); break;
+        case 2: launch_combine<128, 2>(a, pm, pl, pa, out, s); break;
+        case 4: launch_combine<128, 4>(a, pm, pl, pa, out, s); break;
+        default: launch_combine<128, 8>(a, pm, pl, pa, out, s); break;
     }
 }
 
@@ -741,10 +739,9 @@ static void launch_fa(const fattn_args & a, void * scratch, float * out, hipStre
     if (a.split) {
         const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
         float * pm = (float *) scratch;
-        char * p = (char *) (pm + prows);
-        p = (char *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
-        double * pl = (double *) p;
-        double * pa = pl + prows;
+        float * pl = pm + prows;
+        char * p = (char *) (pl + prows);
+        float * pa = (float *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
         if (a.split == 2) {
             const int64_t items = (int64_t) a.n_chunks * a.hq * a.n_seq;
             attn_step_args st{};
@@ -755,8 +752,7 @@ static void launch_fa(const fattn_args & a, void * scratch, float * out, hipStre
             const dim3 grid((unsigned) a.n_chunks, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
             hipLaunchKernelGGL((k_fattn_split<D, R>), grid, dim3(kFaThreads), 0, s, a, pm, pl, pa);
         }
-        const dim3 cgrid(1u, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
-        hipLaunchKernelGGL((k_fattn_combine<D, R>), cgrid, dim3(kFaThreads), 0, s, a, pm, pl, pa, out);
+        launch_combine<D, R>(a, pm, pl, pa, out, s);
     } else {
         const dim3 grid(1u, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
         hipLaunchKernelGGL((k_fattn_full<D, R>), grid, dim3(kFaThreads), 0, s, a, out);

@@ -739,6 +739,101 @@ static void fa_chunked_one(const uint16_t * qh, const uint16_t * k, const uint16
     free(sc);
 }
 
+/* s[j] for up to eight positions j: one f32 fused multiply-add chain per
+ * position over the dims in order, acc = fma(k_j[d], q[d], acc) from 0 (F16C
+ * converts f16 exactly; each vector lane carries one position's chain, so
+ * the vector form gives the scalar chain's bits). */
+static void fa5_dot8(const uint16_t * k, int64_t kv_stride_pos, const float * qf, int64_t D, int n, float * s) {
+    float tt[512][8];
+    for (int j = 0; j < 8; j++) {
+        if (j >= n) {
+            for (int64_t d = 0; d < D; d++) tt[d][j] = 0.0f;
+            continue;
+        }
+        const uint16_t * kr = k + j * kv_stride_pos;
+        for (int64_t d = 0; d < D; d += 8) {
+            float pr[8];
+            _mm256_storeu_ps(pr, _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) (kr + d))));
+            for (int e = 0; e < 8; e++) tt[d + e][j] = pr[e];
+        }
+    }
+    __m256 a = _mm256_setzero_ps();
+    for (int64_t d = 0; d < D; d++) a = _mm256_fmadd_ps(_mm256_loadu_ps(tt[d]), _mm256_set1_ps(qf[d]), a);
+    _mm256_storeu_ps(s, a);
+}
+
+/* fidelity 5 for one (query, head): fixed 64-position KV chunks; per live
+ * (unmasked) position the score is the f32 fma chain over dims times scale
+ * plus the mask value; per chunk m_c = max s, p = exp(s - m_c), and in
+ * position order l_c = l_c + p and a_c[d] = fma(p, v[d], a_c[d]) in f32
+ * (every live position, p = 0 included); masked positions are skipped. The
+ * chunks are combined in order in f64 with w = exp(m_c - M), M = max m_c:
+ * L += w * l_c, O += w * a_c, out = O / L rounded once. */
+static void fa_chunked5_one(const uint16_t * qh, const uint16_t * k, const uint16_t * v, int64_t kv_stride_pos,
+                            const uint16_t * mask, float * o, int64_t D, int64_t n_kv, float scale) {
+    const int64_t C = 64, n_chunks = (n_kv + C - 1) / C;
+    if (n_chunks > 1024) abort(); /* spans beyond 65536 positions are not modelled */
+    if (D % 8 != 0 || D > 512) abort();
+    float qf[512];
+    for (int64_t d = 0; d < D; d++) qf[d] = ref_fp16_to_fp32(qh[d]);
+    float * sc = (float *) malloc((size_t) (n_kv > 0 ? n_kv : 1) * sizeof(float));
+    float mcs[1024];
+    float M = -INFINITY;
+    for (int64_t c = 0; c < n_chunks; c++) {
+        float mc = -INFINITY;
+        const int64_t e = n_kv < (c + 1) * C ? n_kv : (c + 1) * C;
+        for (int64_t i0 = c * C; i0 < e; i0 += 8) {
+            const int n = e - i0 < 8 ? (int) (e - i0) : 8;
+            float mv[8];
+            int live = 0;
+            for (int j = 0; j < n; j++) {
+                mv[j] = mask ? ref_fp16_to_fp32(mask[i0 + j]) : 0.0f;
+                live |= mv[j] != -INFINITY;
+            }
+            float a[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+            if (live) fa5_dot8(k + i0 * kv_stride_pos, kv_stride_pos, qf, D, n, a);
+            for (int j = 0; j < n; j++) {
+                if (mv[j] == -INFINITY) {
+                    sc[i0 + j] = -INFINITY;
+                    continue;
+                }
+                const float s = a[j] * scale + mv[j];
+                sc[i0 + j] = s;
+                mc = s > mc ? s : mc;
+            }
+        }
+        mcs[c] = mc;
+        M = mc > M ? mc : M;
+    }
+    double L = 0.0;
+    double O[512];
+    float acc[512];
+    for (int64_t d = 0; d < D; d++) O[d] = 0.0;
+    for (int64_t c = 0; c < n_chunks && M != -INFINITY; c++) {
+        if (mcs[c] == -INFINITY) continue;
+        const float w = ref_expf_det(mcs[c] - M);
+        if (w == 0.0f) continue;
+        float l = 0.0f;
+        for (int64_t d = 0; d < D; d++) acc[d] = 0.0f;
+        const int64_t e = n_kv < (c + 1) * C ? n_kv : (c + 1) * C;
+        for (int64_t ic = c * C; ic < e; ic++) {
+            if (sc[ic] == -INFINITY) continue;
+            const float p = ref_expf_det(sc[ic] - mcs[c]);
+            l = l + p;
+            const uint16_t * vr = v + ic * kv_stride_pos;
+            const __m256 p8 = _mm256_set1_ps(p);
+            for (int64_t d = 0; d < D; d += 8) {
+                const __m256 vf = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) (vr + d)));
+                _mm256_storeu_ps(acc + d, _mm256_fmadd_ps(p8, vf, _mm256_loadu_ps(acc + d)));
+            }
+        }
+        L += (double) w * (double) l;
+        for (int64_t d = 0; d < D; d++) O[d] += (double) w * (double) acc[d];
+    }
+    for (int64_t d = 0; d < D; d++) o[d] = L == 0.0 ? 0.0f : (float) (O[d] / L);
+    free(sc);
+}
+
 /* ggml_compute_forward_flash_attn_ext_f16_one_chunk restated: sequential
  * online softmax over KV positions, masked (-inf) positions skipped. */
 void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -768,6 +863,11 @@ void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_
                 acc32[d] = 0.0f;
             }
             float * o = out + (iq * Hq + h) * D;
+            if (fidelity == 5) {
+                fa_chunked5_one(qh, k + kvh * kv_stride_head, v + kvh * kv_stride_head, kv_stride_pos,
+                                mask ? mask + iq * mask_stride : NULL, o, D, n_kv, scale);
+                continue;
+            }
             if (fidelity == 4) {
                 fa_chunked_one(qh, k + kvh * kv_stride_head, v + kvh * kv_stride_head, kv_stride_pos,
                                mask ? mask + iq * mask_stride : NULL, o, D, n_kv, scale);

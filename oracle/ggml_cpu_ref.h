@@ -115,12 +115,15 @@ int32_t ref_argmax_first(const float * x, int64_t n);
  * accumulates V in f32; fidelity=0 keeps Q in f32 and accumulates in f32;
  * fidelity=3 rounds Q to f16, takes the global max first and accumulates
  * p = exp(s - max), the sum and p*V in f64, rounding once.
- * fidelity=4 (the device's definition) rounds Q to f16 and splits the span
- * into fixed 64-position chunks: per chunk the max m_c, p = exp(s - m_c) and
- * the f64 sums l_c = sum p, a_c = sum p*V; then M = max m_c and, in chunk
- * order, w = exp(m_c - M), L += w*l_c, O += w*a_c; out = O/L rounded once.
- * Chunk sums of exact products do not depend on the order positions are
- * visited in, so any split of the chunks over workers gives these bits.
+ * fidelity=4 rounds Q to f16 and splits the span into fixed 64-position
+ * chunks: per chunk the max m_c, p = exp(s - m_c) and the f64 sums
+ * l_c = sum p, a_c = sum p*V; then M = max m_c and, in chunk order,
+ * w = exp(m_c - M), L += w*l_c, O += w*a_c; out = O/L rounded once.
+ * fidelity=5 (the device's definition) has the chunks of fidelity 4 with
+ * f32 arithmetic in a fixed order inside a chunk: each score is the f32 fma
+ * chain over dims in order (times scale, plus the mask value), l_c = l_c + p
+ * and a_c = fma(p, V, a_c) in f32 over the chunk's live positions in order;
+ * the chunk combine is fidelity 4's, in f64.
  */
 void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_head,
                         const uint16_t * k, const uint16_t * v, int64_t kv_stride_head,

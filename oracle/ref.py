@@ -164,7 +164,9 @@ def flash_attn(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16: np.ndarr
     fidelity 1: ggml-cpu numerics (f16 Q, f16 V accumulator); 2: f16 Q, f32
     online accumulation; 0: f32 throughout; 3: f16 Q, two-pass f64 sums over
     the whole span; 4: f16 Q, fixed 64-position chunks with their own maxima
-    and f64 sums, combined in chunk order (the device's definition). Returns
+    and f64 sums, combined in chunk order; 5: the chunks of 4 with f32 fma
+    chains in a fixed order inside each chunk (scores over dims, p*V over
+    positions) and the f64 chunk combine (the device's definition). Returns
     [n_q, Hq, D] f32."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     k16 = np.ascontiguousarray(k16, dtype=np.uint16)
@@ -191,7 +193,7 @@ class QwenRef:
     """CPU reference of one Qwen3 decoder sequence over host weight bytes
     (a pointer table into the same buffers the device was loaded from)."""
 
-    def __init__(self, cfg, pointer_table, max_pos: int, fa_fidelity: int = 4, threads: int = 0):
+    def __init__(self, cfg, pointer_table, max_pos: int, fa_fidelity: int = 5, threads: int = 0):
         L = lib()
         L.ref_qwen_forward.restype = C.c_int32
         L.ref_qwen_forward.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
@@ -235,7 +237,7 @@ class QwenRefBatch:
     """CPU reference of a batched decode step over n_seq sequences (weights
     streamed once per step), continuing from given KV caches."""
 
-    def __init__(self, cfg, pointer_table, max_pos: int, n_seq: int, fa_fidelity: int = 4, threads: int = 0):
+    def __init__(self, cfg, pointer_table, max_pos: int, n_seq: int, fa_fidelity: int = 5, threads: int = 0):
         L = lib()
         L.ref_qwen_decode_batch.restype = None
         L.ref_qwen_decode_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
@@ -274,7 +276,7 @@ class WhisperRef:
     """CPU reference of the Whisper decoder (batch 1) over host weight bytes:
     cross K/V precompute from encoder states, then one token per step."""
 
-    def __init__(self, cfg, pointer_table, fa_fidelity: int = 4, threads: int = 0):
+    def __init__(self, cfg, pointer_table, fa_fidelity: int = 5, threads: int = 0):
         L = lib()
         L.ref_whisper_cross_kv.restype = None
         L.ref_whisper_cross_kv.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int]

@@ -78,6 +78,8 @@ def fixtures() -> dict[str, np.ndarray]:
     f["fa_mask"] = fm.view(np.uint16)
     f["fa_out"] = np.stack([ref.flash_attn(q[s:s + 1], kk[s], vv[s], fm[s:s + 1].view(np.uint16), 0.125,
                                            fidelity=4) for s in range(2)])
+    f["fa5_out"] = np.stack([ref.flash_attn(q[s:s + 1], kk[s], vv[s], fm[s:s + 1].view(np.uint16), 0.125,
+                                            fidelity=5) for s in range(2)])
     return f
 
 

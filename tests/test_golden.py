@@ -44,6 +44,7 @@ def test_row_ops(ref, fx):
 
 
 def test_flash_attn(ref, fx):
-    out = np.stack([ref.flash_attn(fx["fa_q"][s:s + 1], fx["fa_k"][s], fx["fa_v"][s], fx["fa_mask"][s:s + 1], 0.125,
-                                   fidelity=4) for s in range(2)])
-    same(out, fx["fa_out"])
+    for fid, key in ((4, "fa_out"), (5, "fa5_out")):
+        out = np.stack([ref.flash_attn(fx["fa_q"][s:s + 1], fx["fa_k"][s], fx["fa_v"][s], fx["fa_mask"][s:s + 1],
+                                       0.125, fidelity=fid) for s in range(2)])
+        same(out, fx[key])

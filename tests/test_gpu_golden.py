@@ -83,5 +83,5 @@ def test_flash_attn_fixture(ggml, gpu, fx):
     G.set(M, m)
     assert G.compute(gpu.backend) == 0
     out = G.get(O).reshape(n_seq, 1, hq, d)
-    assert np.array_equal(bits(out), bits(fx["fa_out"]))
+    assert np.array_equal(bits(out), bits(fx["fa5_out"]))
     G.free()

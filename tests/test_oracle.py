@@ -8,6 +8,7 @@ in the un-vendored openasr-ggml fork), so these are the pins.
 """
 
 import math
+from fractions import Fraction
 
 import numpy as np
 import pytest
@@ -371,6 +372,111 @@ def test_flash_attn_chunked_mode(ref, n_kv, holes):
         v2[:, a:b] = np.float16(np.nan)
     got2 = ref.flash_attn(q, k2.view(np.uint16), v2.view(np.uint16), mask.view(np.uint16), scale, fidelity=4)
     assert np.array_equal(got, got2)
+
+
+@pytest.mark.parametrize("n_kv,holes", [(1, []), (64, []), (65, []), (300, [(30, 130)]), (1000, [(0, 200), (640, 700)])])
+def test_flash_attn_f32_chunked_mode(ref, n_kv, holes):
+    """fidelity 5 (the chunks of fidelity 4 with f32 chains inside a chunk)
+    against the f64 textbook and fidelity 4; garbage under the mask changes
+    nothing; a lone live position returns its V row exactly"""
+    n_q, hq, hkv, d = 2, 4, 2, 128
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((n_q, n_kv), np.float16)
+    for a, b in holes:
+        mask[:, a:b] = -np.inf
+    scale = 1 / math.sqrt(d)
+    qh = q.astype(np.float16).astype(np.float32)
+    want = textbook_attention(qh, k, v, mask, scale, hq // hkv)
+    got = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, fidelity=5)
+    assert np.abs(got - want).max() < 2e-6 * max(1.0, np.abs(want).max())
+    f4 = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, fidelity=4)
+    assert np.abs(got - f4).max() < 2e-6 * max(1.0, np.abs(want).max())
+    k2, v2 = k.copy(), v.copy()
+    for a, b in holes:
+        k2[:, a:b] = np.float16(60000)
+        v2[:, a:b] = np.float16(np.nan)
+    got2 = ref.flash_attn(q, k2.view(np.uint16), v2.view(np.uint16), mask.view(np.uint16), scale, fidelity=5)
+    assert np.array_equal(got, got2)
+    one = np.full((1, n_kv), -np.inf, np.float16)
+    one[0, n_kv // 2] = 0
+    lone = ref.flash_attn(q[:1], k.view(np.uint16), v.view(np.uint16), one.view(np.uint16), scale, fidelity=5)
+    for h in range(hq):
+        assert np.array_equal(lone[0, h], v[h // (hq // hkv), n_kv // 2].astype(np.float32))
+
+
+def _round_f32(x: Fraction) -> float:
+    """a rational rounded to the nearest float32 (ties to even), exactly"""
+    if x == 0:
+        return 0.0
+    sign = -1 if x < 0 else 1
+    a = abs(x)
+    e = a.numerator.bit_length() - a.denominator.bit_length()
+    if Fraction(2) ** e > a:
+        e -= 1
+    e = max(e, -126)  # below that, the subnormal quantum 2**-149
+    quantum = Fraction(2) ** (e - 23)
+    m = a / quantum
+    n = m.numerator // m.denominator
+    rem = m - n
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and n % 2 == 1):
+        n += 1
+    return sign * float(n * quantum)
+
+
+def _fma32(a: float, b: float, c: float) -> float:
+    return _round_f32(Fraction(a) * Fraction(b) + Fraction(c))
+
+
+def test_flash_attn_f32_chunked_mode_brute_force(ref):
+    """fidelity 5 bit for bit against a scalar restatement with exact
+    rational fused multiply-adds (one rounding each): score chains over the
+    dims in order, p*V chains and the sum of p over the live positions in
+    order, the chunk combine in f64. Two chunks, masked holes in both."""
+    L = ref.lib()
+    n_q, hq, hkv, n_kv, d = 2, 2, 1, 70, 16
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((n_q, n_kv), np.float16)
+    mask[0, 5:9] = -np.inf
+    mask[1, 60:66] = -np.inf
+    mask[1, 0] = np.float16(-1.5)
+    scale = np.float32(0.3)
+    got = ref.flash_attn(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), float(scale), fidelity=5)
+    qh = q.astype(np.float16).astype(np.float32)
+    kf, vf = k.astype(np.float32), v.astype(np.float32)
+    for i in range(n_q):
+        for h in range(hq):
+            chunks = []
+            for c0 in range(0, n_kv, 64):
+                live = [j for j in range(c0, min(n_kv, c0 + 64)) if mask[i, j] != -np.inf]
+                s = {}
+                for j in live:
+                    acc = 0.0
+                    for t in range(d):
+                        acc = _fma32(float(kf[0, j, t]), float(qh[i, h, t]), acc)
+                    s[j] = np.float32(np.float32(acc) * scale) + np.float32(mask[i, j])
+                mc = max(s.values()) if live else -np.inf
+                l, a = np.float32(0), [0.0] * d
+                for j in live:
+                    p = np.float32(L.ref_expf_det(float(np.float32(s[j] - mc))))
+                    l = np.float32(l + p)
+                    a = [_fma32(float(p), float(vf[0, j, t]), a[t]) for t in range(d)]
+                chunks.append((mc, l, a))
+            M = max(c[0] for c in chunks)
+            Ls, O = 0.0, [0.0] * d
+            for mc, l, a in chunks:
+                if mc == -np.inf:
+                    continue
+                w = np.float32(L.ref_expf_det(float(np.float32(mc - M))))
+                if w == 0:
+                    continue
+                Ls += float(w) * float(l)
+                O = [O[t] + float(w) * a[t] for t in range(d)]
+            want = np.array([0.0 if Ls == 0 else O[t] / Ls for t in range(d)], np.float32)
+            assert np.array_equal(got[i, h], want), (i, h)
 
 
 def test_whisper_cross_kv_matches_brute_force(ref):
