@@ -18,6 +18,7 @@
 #include <string>
 #include <vector>
 
+#include "ggml_backend_memory.h"
 #include "ggml_host.h"
 #include "ggml_mi355x.h"
 #include "mi355x_exec.h"
@@ -85,6 +86,7 @@ static void buf_free(ggml_backend_buffer_t buffer) {
     buffer_ctx * c = (buffer_ctx *) buffer->context;
     MI_CHECK(hipSetDevice(c->dev->hip_id));
     MI_CHECK(hipFree(c->base));
+    ledger_sub(c->dev, c->size, false);
     delete c;
 }
 
@@ -197,9 +199,11 @@ static ggml_backend_buffer_t buft_alloc_buffer(ggml_backend_buffer_type_t buft, 
     const size_t alloc = std::max<size_t>(size, 256);
     if (hipMalloc(&p, alloc) != hipSuccess) {
         (void) hipGetLastError();
+        ledger_failure(dev);
         std::fprintf(stderr, "mi355x: cannot allocate %zu bytes on %s\n", size, dev->name.c_str());
         return nullptr;
     }
+    ledger_add(dev, alloc, false);
     buffer_ctx * c = new buffer_ctx{dev, (char *) p, alloc};
     return ggml_backend_buffer_init(buft, kBufferIface, c, size);
 }
@@ -224,8 +228,7 @@ static const char * be_get_name(ggml_backend_t backend) {
 static void be_free(ggml_backend_t backend) {
     backend_state * be = (backend_state *) backend->context;
     MI_CHECK(hipSetDevice(be->dev->hip_id));
-    release_graph_cache(be);
-    if (be->scratch) MI_CHECK(hipFree(be->scratch));
+    release_scratch(be);
     MI_CHECK(hipStreamDestroy(be->stream));
     delete be;
 }
@@ -248,7 +251,11 @@ static void be_synchronize(ggml_backend_t backend) {
 }
 
 static enum ggml_status be_graph_compute(ggml_backend_t backend, struct ggml_cgraph * cgraph) {
-    return graph_compute((backend_state *) backend->context, cgraph);
+    backend_state * be = (backend_state *) backend->context;
+    const enum ggml_status st = graph_compute(be, cgraph);
+    be->last_status = (int) st;
+    if (st != GGML_STATUS_SUCCESS) be->last_native_error = (int64_t) g_last_error;
+    return st;
 }
 
 static const ggml_backend_i kBackendIface = {
@@ -398,7 +405,10 @@ static void init_devices() {
         std::snprintf(pci, sizeof(pci), "%04x:%02x:%02x.0", p.pciDomainID, p.pciBusID, p.pciDeviceID);
         dev->pci_id = pci;
         MI_CHECK(hipSetDevice(i));
+        hipUUID uuid;
+        if (hipDeviceGetUuid(&uuid, i) == hipSuccess) std::memcpy(dev->uuid, uuid.bytes, 16);
         MI_CHECK(hipMalloc((void **) &dev->gelu_table, table.size() * 2));
+        ledger_add(dev, table.size() * 2, false);
         MI_CHECK(hipMemcpy(dev->gelu_table, table.data(), table.size() * 2, hipMemcpyHostToDevice));
         dev->buft.iface = kBuftIface;
         dev->buft.device = &dev->dev;
@@ -435,11 +445,24 @@ static void * reg_get_proc_address(ggml_backend_reg_t, const char * name) {
     if (std::strcmp(name, "ggml_backend_device_pci_vendor_id") == 0) return (void *) pci_vendor_id;
     if (std::strcmp(name, "ggml_backend_mi355x_profile_graph") == 0) return (void *) ggml_backend_mi355x_profile_graph;
     if (std::strcmp(name, "ggml_backend_mi355x_set_hip_graphs") == 0) return (void *) ggml_backend_mi355x_set_hip_graphs;
+    if (std::strcmp(name, "ggml_backend_memory_get_api_v1") == 0) return (void *) ggml_backend_memory_get_api_v1;
     return nullptr;
 }
 
 static const ggml_backend_reg_i kRegIface = {reg_get_name, reg_get_device_count, reg_get_device,
                                              reg_get_proc_address};
+
+device_state * device_of(ggml_backend_dev_t d) {
+    return d && d->iface.get_name == dev_get_name ? (device_state *) d->context : nullptr;
+}
+
+device_state * device_of_buft(ggml_backend_buffer_type_t buft) {
+    return buft && buft->iface.get_name == buft_get_name ? (device_state *) buft->context : nullptr;
+}
+
+backend_state * backend_of(ggml_backend_t backend) {
+    return backend && backend->iface.get_name == be_get_name ? (backend_state *) backend->context : nullptr;
+}
 
 }  // namespace mi355x
 

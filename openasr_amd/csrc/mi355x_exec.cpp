@@ -995,21 +995,27 @@ bool planner::plan() {
     return true;
 }
 
-bool ensure_scratch(backend_state * be, size_t act_need, size_t gen_need) {
+// the arena: two equal halves (activation region, general region), at least
+// 32 MiB each
+size_t arena_half(size_t act_need, size_t gen_need) {
     act_need = align_up(act_need, kAlign);
     gen_need = align_up(gen_need + kRopeTableBytes, kAlign);
-    if (be->scratch && act_need <= be->gen_off && be->gen_off + gen_need <= be->scratch_cap) return true;
-    release_graph_cache(be);
-    if (be->scratch) MI_CHECK(hipFree(be->scratch));
-    be->scratch = nullptr;
-    be->scratch_cap = 0;
-    const size_t half = std::max<size_t>(std::max(act_need, gen_need), 32u << 20);
+    return std::max<size_t>(std::max(act_need, gen_need), 32u << 20);
+}
+
+bool ensure_scratch(backend_state * be, size_t act_need, size_t gen_need) {
+    const size_t half = arena_half(act_need, gen_need);
+    if (be->scratch && half <= be->gen_off) return true;
+    release_scratch(be);
     if (hipMalloc((void **) &be->scratch, 2 * half) != hipSuccess) {
+        (void) hipGetLastError();
         be->scratch = nullptr;
+        ledger_failure(be->dev);
         return false;
     }
     be->scratch_cap = 2 * half;
     be->gen_off = half;
+    ledger_add(be->dev, be->scratch_cap, true);
     return true;
 }
 
@@ -1022,6 +1028,50 @@ enum ggml_status map_error(hipError_t e) {
 }
 
 }  // namespace
+
+void ledger_add(device_state * dev, uint64_t bytes, bool workspace) {
+    std::lock_guard<std::mutex> lk(dev->mem_mu);
+    (workspace ? dev->workspace_bytes : dev->live_bytes) += bytes;
+    dev->high_water = std::max(dev->high_water, dev->live_bytes + dev->workspace_bytes);
+    dev->alloc_count++;
+    dev->generation++;
+}
+
+void ledger_sub(device_state * dev, uint64_t bytes, bool workspace) {
+    std::lock_guard<std::mutex> lk(dev->mem_mu);
+    uint64_t & v = workspace ? dev->workspace_bytes : dev->live_bytes;
+    v -= std::min(v, bytes);
+    dev->generation++;
+}
+
+void ledger_failure(device_state * dev) {
+    std::lock_guard<std::mutex> lk(dev->mem_mu);
+    dev->alloc_failures++;
+}
+
+void release_scratch(backend_state * be) {
+    release_graph_cache(be);
+    if (be->scratch) {
+        MI_CHECK(hipFree(be->scratch));
+        ledger_sub(be->dev, be->scratch_cap, true);
+    }
+    be->scratch = nullptr;
+    be->scratch_cap = 0;
+    be->gen_off = 0;
+}
+
+bool graph_arena_bytes(backend_state * be, ggml_cgraph * cg, size_t * bytes) {
+    planner p(be, cg);
+    if (!p.plan()) return false;
+    *bytes = 2 * arena_half(p.act_need, p.gen_need);
+    return true;
+}
+
+bool reserve_graph_arena(backend_state * be, ggml_cgraph * cg) {
+    MI_CHECK(hipSetDevice(be->dev->hip_id));
+    planner p(be, cg);
+    return p.plan() && ensure_scratch(be, p.act_need, p.gen_need);
+}
 
 void release_graph_cache(backend_state * be) {
     for (cache_entry & c : be->cache) {

@@ -1,7 +1,9 @@
 // mi355x_exec.h -- device / backend state and the graph executor interface.
 #pragma once
 
+#include <cstdint>
 #include <functional>
+#include <mutex>
 #include <string>
 #include <vector>
 
@@ -20,9 +22,29 @@ struct device_state {
     std::string arch;
     uint16_t * gelu_table = nullptr;  // device copy of the f16 GELU table
     int wall_clock_khz = 100000;      // constant-rate device clock (hipDeviceAttributeWallClockRate)
+    uint8_t uuid[16] = {};            // hipDeviceGetUuid
     ggml_backend_device dev{};
     ggml_backend_buffer_type buft{};
+    // allocation ledger of the memory ABI: every device allocation the plugin
+    // makes on this device (buffers, executor arenas, its own tables)
+    std::mutex mem_mu;
+    uint64_t live_bytes = 0;       // buffers and tables
+    uint64_t workspace_bytes = 0;  // executor scratch arenas
+    uint64_t high_water = 0;       // largest live + workspace seen
+    uint64_t alloc_count = 0, alloc_failures = 0;
+    uint64_t generation = 1;       // advances with every allocation and release
 };
+
+// this plugin's objects behind ggml handles (null for another backend's)
+device_state * device_of(ggml_backend_dev_t d);
+device_state * device_of_buft(ggml_backend_buffer_type_t buft);
+struct backend_state;
+backend_state * backend_of(ggml_backend_t backend);
+
+// ledger updates (thread-safe)
+void ledger_add(device_state * dev, uint64_t bytes, bool workspace);
+void ledger_sub(device_state * dev, uint64_t bytes, bool workspace);
+void ledger_failure(device_state * dev);
 
 // one planned launch: a closure that enqueues kernels on a stream
 struct step {
@@ -52,12 +74,23 @@ struct backend_state {
     void * abort_data = nullptr;
     int last_observation = 0;
     bool poisoned = false;
+    bool quarantined = false;          // by the memory ABI's quarantine call
+    uint64_t quarantine_generation = 0;
+    int last_status = 0;               // ggml_status of the last graph_compute
+    int64_t last_native_error = 0;     // hipError_t behind it
     ggml_guid guid{};
     ggml_backend backend{};
     std::string name;
 };
 
 enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg);
+
+// executor scratch arena: the bytes running `cg` needs (false if the graph
+// cannot be planned), growing the arena to it, and releasing it (with the
+// HIP-graph cache that points into it)
+bool graph_arena_bytes(backend_state * be, ggml_cgraph * cg, size_t * bytes);
+bool reserve_graph_arena(backend_state * be, ggml_cgraph * cg);
+void release_scratch(backend_state * be);
 bool supports_op(const device_state * dev, const ggml_tensor * op);
 void release_graph_cache(backend_state * be);
 

@@ -140,6 +140,7 @@ def base() -> C.CDLL:
     _sig(lib, "ggml_backend_buffer_set_usage", None, C.c_void_p, i)
     _sig(lib, "ggml_backend_buffer_clear", None, C.c_void_p, C.c_uint8)
     _sig(lib, "ggml_backend_buffer_get_size", sz, C.c_void_p)
+    _sig(lib, "ggml_backend_buft_alloc_buffer", C.c_void_p, C.c_void_p, sz)
     _sig(lib, "ggml_backend_buft_name", C.c_char_p, C.c_void_p)
     _sig(lib, "ggml_backend_buft_get_alignment", sz, C.c_void_p)
     _sig(lib, "ggml_backend_name", C.c_char_p, C.c_void_p)
@@ -328,6 +329,168 @@ class Graph:
             self.free()
         except Exception:
             pass
+
+
+# ------------------------------------------------------ memory ABI v1 -----
+# ctypes mirror of include/ggml_backend_memory.h (the host's #[repr(C)]
+# structs, crates/openasr-core/src/ggml_runtime/ffi.rs:144-332) and a thin
+# wrapper that drives it the way backend_memory.rs:140-330 does: resolve the
+# registry proc, check size / version / required entries, and call every
+# list-returning function twice (count, then fill).
+
+MEM_DOMAIN_DEVICE_LOCAL = 1
+MEM_REQUEST_BUFFER, MEM_REQUEST_HOST_IMPORT, MEM_REQUEST_GRAPH_PRIVATE, MEM_REQUEST_TRANSFER = 1, 2, 3, 4
+MEM_QUOTE_PROVISIONAL = 1 << 0
+MEM_QUOTE_OPAQUE_DRIVER_COSTS = 1 << 2
+MEM_STATS_BUDGET_UNAVAILABLE = 1 << 0
+MEM_CLAIM_EXACT, MEM_CLAIM_CONSERVATIVE_UPPER, MEM_CLAIM_PROVISIONAL = 1 << 0, 1 << 1, 1 << 6
+MEM_HEALTHY, MEM_DEGRADED, MEM_QUARANTINED, MEM_DEVICE_LOST = 0, 1, 2, 3
+
+
+class mem_domain_id(C.Structure):
+    _fields_ = [("physical_device_uuid", C.c_uint8 * 16), ("heap_index", C.c_uint32), ("kind", C.c_uint32)]
+
+
+class mem_domain(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("flags", C.c_uint32), ("id", mem_domain_id), ("name", C.c_char * 48)]
+
+
+class mem_request(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("kind", C.c_uint32), ("flags", C.c_uint32), ("usage", C.c_uint32),
+                ("request_id", C.c_uint64), ("backend", C.c_void_p), ("peer_backend", C.c_void_p),
+                ("buft", C.c_void_p), ("graph", C.c_void_p), ("host_ptr", C.c_void_p),
+                ("requested_bytes", C.c_uint64), ("currently_allocated_bytes", C.c_uint64),
+                ("max_tensor_bytes", C.c_uint64)]
+
+
+class mem_claim(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("flags", C.c_uint32), ("request_id", C.c_uint64),
+                ("domain", mem_domain_id), ("payload_requested_bytes", C.c_uint64),
+                ("committed_before_bytes", C.c_uint64), ("committed_after_upper_bytes", C.c_uint64),
+                ("commit_peak_extra_upper_bytes", C.c_uint64), ("resident_after_upper_bytes", C.c_uint64),
+                ("retained_after_use_upper_bytes", C.c_uint64), ("releasable_after_use_upper_bytes", C.c_uint64)]
+
+
+class mem_quote(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("flags", C.c_uint32), ("residual_flags", C.c_uint32),
+                ("residual_request_count", C.c_uint32), ("provisional_requested_upper_bytes", C.c_uint64),
+                ("stats_generation", C.c_uint64), ("quote_token", C.c_uint64), ("request_fingerprint", C.c_uint64)]
+
+
+class mem_stats(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("flags", C.c_uint32), ("domain", mem_domain_id),
+                ("generation", C.c_uint64), ("timestamp_monotonic_ns", C.c_uint64), ("total_bytes", C.c_uint64),
+                ("budget_bytes", C.c_uint64), ("device_used_bytes", C.c_uint64), ("device_free_bytes", C.c_uint64),
+                ("backend_owned_live_bytes", C.c_uint64), ("backend_owned_cached_bytes", C.c_uint64),
+                ("backend_owned_workspace_bytes", C.c_uint64), ("backend_owned_high_water_bytes", C.c_uint64),
+                ("allocation_count", C.c_uint64), ("allocation_failure_count", C.c_uint64),
+                ("health", C.c_uint32), ("last_ggml_status", C.c_int32), ("last_native_error", C.c_int64),
+                ("quarantine_generation", C.c_uint64)]
+
+
+class mem_quarantine(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("flags", C.c_uint32), ("reason", C.c_uint32),
+                ("ggml_status", C.c_int32), ("native_error", C.c_int64), ("message", C.c_char * 96)]
+
+
+_U32P = C.POINTER(C.c_uint32)
+MEM_GET_DOMAINS = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(mem_domain), _U32P)
+MEM_QUOTE = C.CFUNCTYPE(C.c_int, C.POINTER(mem_request), C.c_uint32, C.POINTER(mem_quote), C.POINTER(mem_claim),
+                        _U32P)
+MEM_RESERVE = C.CFUNCTYPE(C.c_int, C.POINTER(mem_request), C.c_uint32, C.POINTER(mem_quote), C.POINTER(mem_claim),
+                          _U32P)
+MEM_GET_STATS = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_void_p, C.POINTER(mem_stats), _U32P)
+MEM_TRIM = C.CFUNCTYPE(C.c_int, C.c_void_p, C.c_uint64)
+MEM_QUARANTINE = C.CFUNCTYPE(C.c_int, C.c_void_p, C.POINTER(mem_quarantine))
+
+
+class mem_api(C.Structure):
+    _fields_ = [("struct_size", C.c_uint32), ("abi_version", C.c_uint32), ("capabilities", C.c_uint64),
+                ("get_domains", MEM_GET_DOMAINS), ("quote", MEM_QUOTE), ("reserve_private", MEM_RESERVE),
+                ("get_stats", MEM_GET_STATS), ("trim", MEM_TRIM), ("quarantine", MEM_QUARANTINE)]
+
+
+MEM_API_GET = C.CFUNCTYPE(C.POINTER(mem_api))
+
+
+class MemoryStatusError(RuntimeError):
+    def __init__(self, operation: str, status: int):
+        super().__init__(f"memory ABI {operation} returned ggml status {status}")
+        self.operation, self.status = operation, status
+
+
+def _check(operation: str, status: int) -> None:
+    if status != 0:
+        raise MemoryStatusError(operation, status)
+
+
+def _array(cls, n: int):
+    arr = (cls * max(n, 1))()
+    for x in arr:
+        x.struct_size = C.sizeof(cls)
+    return arr
+
+
+class MemoryApi:
+    """The v1 table of one backend, resolved through its registry."""
+
+    def __init__(self, reg, device, backend):
+        proc = base().ggml_backend_reg_get_proc_address(reg, b"ggml_backend_memory_get_api_v1")
+        if not proc:
+            raise RuntimeError("memory ABI unavailable")
+        api = MEM_API_GET(proc)()
+        if not api:
+            raise RuntimeError("memory ABI unavailable")
+        self.raw = api.contents
+        if (self.raw.struct_size < C.sizeof(mem_api) or self.raw.abi_version != 1
+                or not all((self.raw.get_domains, self.raw.quote, self.raw.reserve_private, self.raw.get_stats))):
+            raise RuntimeError("memory ABI incompatible")
+        self.device, self.backend = device, backend
+
+    def domains(self):
+        n = C.c_uint32(0)
+        _check("domains/count", self.raw.get_domains(self.device, None, C.byref(n)))
+        arr, cap = _array(mem_domain, n.value), C.c_uint32(n.value)
+        _check("domains", self.raw.get_domains(self.device, arr, C.byref(cap)))
+        return list(arr)[:cap.value]
+
+    def quote(self, requests):
+        reqs = (mem_request * max(len(requests), 1))(*requests)
+        q = mem_quote(struct_size=C.sizeof(mem_quote))
+        n = C.c_uint32(0)
+        _check("quote/count", self.raw.quote(reqs, len(requests), C.byref(q), None, C.byref(n)))
+        claims, cap = _array(mem_claim, n.value), C.c_uint32(n.value)
+        _check("quote", self.raw.quote(reqs, len(requests), C.byref(q), claims, C.byref(cap)))
+        return q, list(claims)[:cap.value]
+
+    def reserve_private(self, requests, q):
+        reqs = (mem_request * max(len(requests), 1))(*requests)
+        n = C.c_uint32(0)
+        _check("reserve_private/count", self.raw.reserve_private(reqs, len(requests), C.byref(q), None, C.byref(n)))
+        claims, cap = _array(mem_claim, n.value), C.c_uint32(n.value)
+        _check("reserve_private", self.raw.reserve_private(reqs, len(requests), C.byref(q), claims, C.byref(cap)))
+        return list(claims)[:cap.value]
+
+    def stats(self):
+        n = C.c_uint32(0)
+        _check("stats/count", self.raw.get_stats(self.device, self.backend, None, C.byref(n)))
+        arr, cap = _array(mem_stats, n.value), C.c_uint32(n.value)
+        _check("stats", self.raw.get_stats(self.device, self.backend, arr, C.byref(cap)))
+        return list(arr)[:cap.value]
+
+    def trim(self, flags: int = 0) -> None:
+        _check("trim", self.raw.trim(self.backend, flags))
+
+    def quarantine(self, reason: int, status: int, message: bytes) -> None:
+        q = mem_quarantine(struct_size=C.sizeof(mem_quarantine), reason=reason, ggml_status=status, message=message)
+        _check("quarantine", self.raw.quarantine(self.backend, C.byref(q)))
+
+
+def mem_request_of(kind: int, backend=None, buft=None, graph=None, requested: int = 0, current: int = 0,
+                   request_id: int = 0, usage: int = 0) -> mem_request:
+    return mem_request(struct_size=C.sizeof(mem_request), kind=kind, usage=usage, request_id=request_id,
+                       backend=backend, buft=buft, graph=graph, requested_bytes=requested,
+                       currently_allocated_bytes=current)
 
 
 # --------------------------------------------------------------- helpers ---

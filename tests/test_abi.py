@@ -70,3 +70,60 @@ def test_verified_loader_rejects_wrong_attestation(ggml):
     assert not lib.ggml_backend_load_verified_v3_utf8(path, None, 0, fp, b"cuda", b"gfx950", b"")
     assert not lib.ggml_backend_load_verified_v3_utf8(path, None, 0, fp, b"hip", b"gfx1200", b"")
     assert not lib.ggml_backend_load_verified_v3_utf8(b"/nonexistent/plugin.so", None, 0, fp, b"hip", b"", b"")
+
+
+MEM_STRUCTS = {
+    "mem_domain_id": "ggml_backend_memory_domain_id_v1",
+    "mem_domain": "ggml_backend_memory_domain_v1",
+    "mem_request": "ggml_backend_memory_request_v1",
+    "mem_claim": "ggml_backend_memory_claim_v1",
+    "mem_quote": "ggml_backend_memory_quote_v1",
+    "mem_stats": "ggml_backend_memory_stats_v1",
+    "mem_quarantine": "ggml_backend_memory_quarantine_v1",
+    "mem_api": "ggml_backend_memory_api_v1",
+}
+
+
+def test_memory_abi_layouts_match_header(ggml, tmp_path):
+    """every field offset and struct size of include/ggml_backend_memory.h
+    (compiled by gcc) equals the ctypes mirror the tests drive it with"""
+    import subprocess
+    lines = ['#include <stdio.h>', '#include <stddef.h>', '#include "ggml_backend_memory.h"', "int main(void) {"]
+    for py, c in MEM_STRUCTS.items():
+        lines.append(f'printf("{py} %zu\\n", sizeof({c}));')
+        for fname, _ in getattr(ggml, py)._fields_:
+            lines.append(f'printf("{py}.{fname} %zu\\n", offsetof({c}, {fname}));')
+    lines.append("return 0; }")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c11", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                        check=True).stdout.splitlines())
+    for py in MEM_STRUCTS:
+        cls = getattr(ggml, py)
+        assert int(got[py]) == C.sizeof(cls), py
+        for fname, _ in cls._fields_:
+            assert int(got[f"{py}.{fname}"]) == getattr(cls, fname).offset, (py, fname)
+
+
+def test_memory_abi_table_without_a_device(ggml):
+    """the registry proc and the direct export give the same v1 table with
+    every entry set (the host's acceptance test, backend_memory.rs:174-184)"""
+    lib = C.CDLL(str(ggml.PLUGIN_PATH))
+    assert not [n for n in declared("ggml_backend_memory.h") if not hasattr(lib, n)]
+    lib.ggml_backend_init.restype = C.c_void_p
+    reg = lib.ggml_backend_init()
+    assert reg
+    proc = ggml.base().ggml_backend_reg_get_proc_address(reg, b"ggml_backend_memory_get_api_v1")
+    lib.ggml_backend_memory_get_api_v1.restype = C.c_void_p
+    assert proc and C.cast(proc, C.c_void_p).value == C.cast(lib.ggml_backend_memory_get_api_v1, C.c_void_p).value
+    api = ggml.MEM_API_GET(proc)().contents
+    assert api.struct_size == C.sizeof(ggml.mem_api) and api.abi_version == 1
+    for f in ("get_domains", "quote", "reserve_private", "get_stats", "trim", "quarantine"):
+        assert getattr(api, f), f
+    # calls on handles that are not this plugin's fail instead of crashing
+    n = C.c_uint32(0)
+    assert api.get_domains(None, None, C.byref(n)) != 0
+    assert api.get_stats(None, None, None, C.byref(n)) != 0
+    assert api.trim(None, 0) != 0
