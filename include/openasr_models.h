@@ -38,6 +38,7 @@ typedef struct {
     float rms_eps;
     int wtype; /* GGML_TYPE_Q8_0 or GGML_TYPE_Q4_K for every matrix and the tied embedding */
     uint64_t seed;
+    int out_wtype; /* type of a separate output projection (runtime packs with output.weight), else unused */
 } oa_qwen_config;
 
 enum oa_qwen_tensor_kind {
@@ -51,14 +52,53 @@ enum oa_qwen_tensor_kind {
     OA_QWEN_FFN_NORM,       /* f32 [d_model] */
     OA_QWEN_GATE,           /* wtype, ffn rows of d_model */
     OA_QWEN_UP,             /* wtype, ffn rows of d_model */
-    OA_QWEN_DOWN            /* wtype, d_model rows of ffn */
+    OA_QWEN_DOWN,           /* wtype, d_model rows of ffn */
+    OA_QWEN_OUTPUT          /* out_wtype [vocab rows of d_model]: a separate output projection, NULL when tied */
 };
 
 typedef struct oa_qwen_weights oa_qwen_weights;
+
+/*
+ * GGUF runtime-pack reader (v2/v3, the `.oasr` v1 payload:
+ * docs/format/OASR_PACKAGE_CONTRACT_V1.md). The file is mapped read-only;
+ * tensor data are views into the mapping, valid until oa_gguf_close. The
+ * reserved OASR magic and unknown magics are refused, as are malformed
+ * headers, out-of-file or misaligned tensor ranges and duplicate names
+ * (the fork's gguf_init_from_file + ggml_runtime/gguf_tensor_data.rs).
+ */
+typedef struct oa_gguf oa_gguf;
+oa_gguf * oa_gguf_open(const char * path, char * err, size_t err_cap);
+void oa_gguf_close(oa_gguf * g);
+uint32_t oa_gguf_version(const oa_gguf * g);
+size_t oa_gguf_alignment(const oa_gguf * g);
+int64_t oa_gguf_n_tensors(const oa_gguf * g);
+int64_t oa_gguf_n_kv(const oa_gguf * g);
+int64_t oa_gguf_find_tensor(const oa_gguf * g, const char * name); /* -1 when absent */
+const char * oa_gguf_tensor_name(const oa_gguf * g, int64_t i);
+/* type and ne[4] of tensor i; returns n_dims, -1 for a bad index */
+int oa_gguf_tensor_info(const oa_gguf * g, int64_t i, int * type, int64_t ne[4]);
+const void * oa_gguf_tensor_data(const oa_gguf * g, int64_t i, size_t * nbytes);
+int oa_gguf_kv_type(const oa_gguf * g, const char * key); /* GGUF value type, -1 when absent */
+const char * oa_gguf_get_str(const oa_gguf * g, const char * key);
+bool oa_gguf_get_i64(const oa_gguf * g, const char * key, int64_t * out);  /* any integer type */
+bool oa_gguf_get_f64(const oa_gguf * g, const char * key, double * out);   /* float or integer */
 typedef struct oa_qwen_model oa_qwen_model;
 typedef struct oa_qwen_session oa_qwen_session;
 
 oa_qwen_weights * oa_qwen_weights_synthesize(const oa_qwen_config * cfg);
+/* Weights of a qwen3-asr runtime pack (.oasr v1 = GGUF): hparams from the
+ * qwen3-asr.llm.* keys (arch/hparams.rs:52-58), tensors blk.N.{attn_norm,
+ * attn_q, attn_k, attn_v, attn_output, attn_q_norm, attn_k_norm, ffn_norm,
+ * ffn_gate, ffn_up, ffn_down}.weight, token_embd.weight, output_norm.weight
+ * and an optional output.weight (models/qwen/decoder_contract.rs:686-705,
+ * 764-769). The matrices stay views into the file mapping (q|k|v are joined
+ * into the fused projection, llm_transformer.rs:6505-6555); every matrix must
+ * be Q8_0 or Q4_K, all of one type. RoPE theta 1e6 unless the pack carries
+ * qwen3-asr.llm.rope_theta; RMS epsilon 1e-6. NULL with a message on any
+ * missing or mis-shaped tensor or key. */
+oa_qwen_weights * oa_qwen_weights_load_gguf(const char * path, char * err, size_t err_cap);
+/* the configuration the weights describe */
+void oa_qwen_weights_config(const oa_qwen_weights * w, oa_qwen_config * out);
 void oa_qwen_weights_free(oa_qwen_weights * w);
 /* host bytes of one tensor (layer ignored for TOKEN_EMBD / OUTPUT_NORM) */
 const void * oa_qwen_weights_tensor(const oa_qwen_weights * w, int layer, int kind, size_t * nbytes);

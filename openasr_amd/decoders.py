@@ -18,7 +18,7 @@ MODELS_PATH = g.LIB_DIR / "libopenasr-models.so"
 class QwenConfig(C.Structure):
     _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("n_kv_head", C.c_int),
                 ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("rope_theta", C.c_float),
-                ("rms_eps", C.c_float), ("wtype", C.c_int), ("seed", C.c_uint64)]
+                ("rms_eps", C.c_float), ("wtype", C.c_int), ("seed", C.c_uint64), ("out_wtype", C.c_int)]
 
 
 class WhisperConfig(C.Structure):
@@ -38,7 +38,7 @@ QWEN3_06B = dict(d_model=1024, n_layers=28, n_head=16, n_kv_head=8, head_dim=128
 QWEN3_17B = dict(d_model=2048, n_layers=28, n_head=16, n_kv_head=8, head_dim=128, ffn=6144, vocab=151936)
 
 # tensor kinds (enum oa_qwen_tensor_kind)
-(TOKEN_EMBD, OUTPUT_NORM, ATTN_NORM, QKV, Q_NORM, K_NORM, O, FFN_NORM, GATE, UP, DOWN) = range(11)
+(TOKEN_EMBD, OUTPUT_NORM, ATTN_NORM, QKV, Q_NORM, K_NORM, O, FFN_NORM, GATE, UP, DOWN, OUTPUT) = range(12)
 LAYER_KINDS = (ATTN_NORM, QKV, Q_NORM, K_NORM, O, FFN_NORM, GATE, UP, DOWN)
 
 _lib = None
@@ -60,6 +60,23 @@ def lib() -> C.CDLL:
         fn.argtypes = list(args)
 
     s("oa_qwen_weights_synthesize", vp, C.POINTER(QwenConfig))
+    s("oa_qwen_weights_load_gguf", vp, C.c_char_p, C.c_char_p, C.c_size_t)
+    s("oa_qwen_weights_config", None, vp, C.POINTER(QwenConfig))
+    i64 = C.c_int64
+    s("oa_gguf_open", vp, C.c_char_p, C.c_char_p, C.c_size_t)
+    s("oa_gguf_close", None, vp)
+    s("oa_gguf_version", C.c_uint32, vp)
+    s("oa_gguf_alignment", C.c_size_t, vp)
+    s("oa_gguf_n_tensors", i64, vp)
+    s("oa_gguf_n_kv", i64, vp)
+    s("oa_gguf_find_tensor", i64, vp, C.c_char_p)
+    s("oa_gguf_tensor_name", C.c_char_p, vp, i64)
+    s("oa_gguf_tensor_info", i, vp, i64, C.POINTER(C.c_int), C.POINTER(i64))
+    s("oa_gguf_tensor_data", vp, vp, i64, C.POINTER(C.c_size_t))
+    s("oa_gguf_kv_type", i, vp, C.c_char_p)
+    s("oa_gguf_get_str", C.c_char_p, vp, C.c_char_p)
+    s("oa_gguf_get_i64", C.c_bool, vp, C.c_char_p, C.POINTER(i64))
+    s("oa_gguf_get_f64", C.c_bool, vp, C.c_char_p, C.POINTER(C.c_double))
     s("oa_qwen_weights_free", None, vp)
     s("oa_qwen_weights_tensor", vp, vp, i, i, C.POINTER(C.c_size_t))
     s("oa_qwen_model_create", vp, vp, vp)
@@ -92,7 +109,8 @@ def lib() -> C.CDLL:
 
 
 class QwenWeights:
-    """Host copy of a synthesised Qwen3-shaped decoder (quantized bytes)."""
+    """Host bytes of a Qwen3-shaped decoder: synthesised (seeded N(0, 0.02),
+    quantized), or views into a mapped qwen3-asr runtime pack (load_gguf)."""
 
     def __init__(self, wtype: int, seed: int = 1234, rope_theta: float = 1e6, rms_eps: float = 1e-6, **shape):
         self.cfg = QwenConfig(rope_theta=rope_theta, rms_eps=rms_eps, wtype=wtype, seed=seed, **shape)
@@ -100,17 +118,37 @@ class QwenWeights:
         if not self.ptr:
             raise RuntimeError("weight synthesis failed")
 
+    @classmethod
+    def load_gguf(cls, path) -> "QwenWeights":
+        err = C.create_string_buffer(512)
+        ptr = lib().oa_qwen_weights_load_gguf(str(path).encode(), err, len(err))
+        if not ptr:
+            raise ValueError(f"{path}: {err.value.decode()}")
+        self = cls.__new__(cls)
+        self.ptr = ptr
+        self.cfg = QwenConfig()
+        lib().oa_qwen_weights_config(ptr, C.byref(self.cfg))
+        return self
+
+    def array(self, layer: int, kind: int) -> np.ndarray:
+        """a copy of one tensor's host bytes (uint8)"""
+        p, n = self.tensor(layer, kind)
+        if not p:
+            return None
+        return np.ctypeslib.as_array((C.c_uint8 * n).from_address(p)).copy()
+
     def tensor(self, layer: int, kind: int) -> tuple[int, int]:
         n = C.c_size_t(0)
         p = lib().oa_qwen_weights_tensor(self.ptr, layer, kind, C.byref(n))
         return p, n.value
 
     def pointer_table(self) -> list[int]:
-        """[tok_embd, out_norm, per layer: attn_norm, qkv, q_norm, k_norm, o, ffn_norm, gate, up, down]"""
+        """[tok_embd, out_norm, per layer: attn_norm, qkv, q_norm, k_norm, o, ffn_norm, gate, up, down,
+        then the separate output projection or None when tied]"""
         t = [self.tensor(-1, TOKEN_EMBD)[0], self.tensor(-1, OUTPUT_NORM)[0]]
         for layer in range(self.cfg.n_layers):
             t += [self.tensor(layer, k)[0] for k in LAYER_KINDS]
-        return t
+        return t + [self.tensor(-1, OUTPUT)[0]]
 
     def free(self):
         if self.ptr:

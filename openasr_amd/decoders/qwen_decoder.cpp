@@ -31,9 +31,30 @@ namespace {
 
 constexpr int kPrefillChunk = 256;  // llm_transformer.rs:60
 
+// weight bytes: owned (synthesised, or assembled such as the fused QKV) or
+// a view into a mapped runtime pack
+struct blob {
+    std::vector<uint8_t> own;
+    const uint8_t * view = nullptr;
+    size_t n = 0;
+    blob & operator=(std::vector<uint8_t> && v) {
+        own = std::move(v);
+        view = nullptr;
+        n = 0;
+        return *this;
+    }
+    void set_view(const void * p, size_t bytes) {
+        own.clear();
+        view = (const uint8_t *) p;
+        n = bytes;
+    }
+    const uint8_t * data() const { return view ? view : own.data(); }
+    size_t size() const { return view ? n : own.size(); }
+};
+
 struct qlayer_host {
     std::vector<float> attn_norm, q_norm, k_norm, ffn_norm;
-    std::vector<uint8_t> qkv, o, gate, up, down;
+    blob qkv, o, gate, up, down;
 };
 
 uint64_t stream_id(int layer, int kind, int part) { return (uint64_t) (layer + 1) * 1000 + (uint64_t) kind * 10 + part; }
@@ -72,9 +93,12 @@ std::vector<uint8_t> synth_matrix(int wtype, uint64_t seed, const std::vector<st
 
 struct oa_qwen_weights {
     oa_qwen_config cfg;
-    std::vector<uint8_t> tok_embd;
+    blob tok_embd;
+    blob lm_head;  // empty: the output projection is tied to tok_embd
     std::vector<float> out_norm;
     std::vector<qlayer_host> layers;
+    oa_gguf * src = nullptr;  // the mapped pack the views point into
+    ~oa_qwen_weights() { oa_gguf_close(src); }
 };
 
 struct qlayer_dev {
@@ -87,6 +111,7 @@ struct oa_qwen_model {
     ggml_context * ctx;
     ggml_backend_buffer_t buf;
     ggml_tensor *tok_embd, *out_norm;
+    ggml_tensor * lm_head;  // tok_embd when tied
     std::vector<qlayer_dev> layers;
 };
 
@@ -224,7 +249,7 @@ bool build_step(oa_qwen_session * s, step_graph & g, int T, bool emb) {
                                              (size_t) (T - 1) * c.d_model * sizeof(float)));
     }
     ggml_tensor * normed = rms_norm_mul(g.ctx, last, m->out_norm, c.rms_eps);
-    g.logits = ggml_mul_mat(g.ctx, m->tok_embd, normed);
+    g.logits = ggml_mul_mat(g.ctx, m->lm_head, normed);
     g.top1 = ggml_argmax_first(g.ctx, g.logits);
     ggml_set_output(g.logits);
     ggml_set_output(g.top1);
@@ -307,7 +332,7 @@ oa_qwen_weights * oa_qwen_weights_synthesize(const oa_qwen_config * cfg) {
 void oa_qwen_weights_free(oa_qwen_weights * w) { delete w; }
 
 const void * oa_qwen_weights_tensor(const oa_qwen_weights * w, int layer, int kind, size_t * nbytes) {
-    auto ret_u8 = [&](const std::vector<uint8_t> & v) -> const void * {
+    auto ret_u8 = [&](const blob & v) -> const void * {
         if (nbytes) *nbytes = v.size();
         return v.data();
     };
@@ -316,6 +341,7 @@ const void * oa_qwen_weights_tensor(const oa_qwen_weights * w, int layer, int ki
         return v.data();
     };
     if (kind == OA_QWEN_TOKEN_EMBD) return ret_u8(w->tok_embd);
+    if (kind == OA_QWEN_OUTPUT) return w->lm_head.size() ? ret_u8(w->lm_head) : nullptr;
     if (kind == OA_QWEN_OUTPUT_NORM) return ret_f(w->out_norm);
     if (layer < 0 || layer >= (int) w->layers.size()) return nullptr;
     const qlayer_host & L = w->layers[(size_t) layer];
@@ -343,6 +369,8 @@ oa_qwen_model * oa_qwen_model_create(ggml_backend_t backend, const oa_qwen_weigh
     const ggml_type wt = (ggml_type) c.wtype;
     const int q_w = c.n_head * c.head_dim, kv_w = c.n_kv_head * c.head_dim;
     m->tok_embd = ggml_new_tensor_2d(m->ctx, wt, c.d_model, c.vocab);
+    m->lm_head = w->lm_head.size() ? ggml_new_tensor_2d(m->ctx, (ggml_type) c.out_wtype, c.d_model, c.vocab)
+                                   : m->tok_embd;
     m->out_norm = ggml_new_tensor_1d(m->ctx, GGML_TYPE_F32, c.d_model);
     m->layers.resize((size_t) c.n_layers);
     for (int l = 0; l < c.n_layers; l++) {
@@ -366,6 +394,7 @@ oa_qwen_model * oa_qwen_model_create(ggml_backend_t backend, const oa_qwen_weigh
     ggml_backend_buffer_set_usage(m->buf, GGML_BACKEND_BUFFER_USAGE_WEIGHTS);
     auto up = [](ggml_tensor * t, const void * data, size_t n) { ggml_backend_tensor_set(t, data, 0, n); };
     up(m->tok_embd, w->tok_embd.data(), w->tok_embd.size());
+    if (m->lm_head != m->tok_embd) up(m->lm_head, w->lm_head.data(), w->lm_head.size());
     up(m->out_norm, w->out_norm.data(), w->out_norm.size() * 4);
     for (int l = 0; l < c.n_layers; l++) {
         const qlayer_host & H = w->layers[(size_t) l];
@@ -510,3 +539,155 @@ int oa_detect_degenerate_ngram(const int32_t * tokens, int len, int max_ngram, i
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------- runtime packs ----
+
+namespace {
+
+struct pack_reader {
+    oa_gguf * g;
+    std::string err;
+
+    bool fail(const std::string & msg) {
+        if (err.empty()) err = msg;
+        return false;
+    }
+    bool key_i(const char * key, int & out) {
+        int64_t v = 0;
+        if (!oa_gguf_get_i64(g, key, &v)) return fail(std::string("missing or non-integer key ") + key);
+        if (v <= 0 || v > (1 << 30)) return fail(std::string("key ") + key + " out of range");
+        out = (int) v;
+        return true;
+    }
+    // tensor `name` of type in `types` with ne = (ne0, ne1); returns its index
+    int64_t tensor(const std::string & name, int64_t ne0, int64_t ne1, std::initializer_list<int> types, int & type) {
+        const int64_t i = oa_gguf_find_tensor(g, name.c_str());
+        if (i < 0) {
+            fail("missing tensor " + name);
+            return -1;
+        }
+        int64_t ne[4];
+        const int nd = oa_gguf_tensor_info(g, i, &type, ne);
+        if (ne[0] != ne0 || ne[1] != ne1 || ne[2] != 1 || ne[3] != 1 || nd > 2) {
+            fail("tensor " + name + " has shape [" + std::to_string(ne[0]) + ", " + std::to_string(ne[1]) +
+                 "], expected [" + std::to_string(ne0) + ", " + std::to_string(ne1) + "]");
+            return -1;
+        }
+        bool ok = false;
+        for (int t : types) ok |= t == type;
+        if (!ok) {
+            fail("tensor " + name + " has unsupported type " + std::string(ggml_type_name((ggml_type) type)));
+            return -1;
+        }
+        return i;
+    }
+    bool vec(const std::string & name, int64_t n, std::vector<float> & out) {
+        int type = 0;
+        const int64_t i = tensor(name, n, 1, {GGML_TYPE_F32}, type);
+        if (i < 0) return false;
+        size_t nb = 0;
+        const float * p = (const float *) oa_gguf_tensor_data(g, i, &nb);
+        out.assign(p, p + n);
+        return true;
+    }
+    bool mat(const std::string & name, int64_t k, int64_t rows, int wtype, blob & out) {
+        int type = 0;
+        const int64_t i = tensor(name, k, rows, {GGML_TYPE_Q8_0, GGML_TYPE_Q4_K}, type);
+        if (i < 0) return false;
+        if (type != wtype) return fail("tensor " + name + " is " + ggml_type_name((ggml_type) type) +
+                                       ", the pack's matrices are " + ggml_type_name((ggml_type) wtype));
+        size_t nb = 0;
+        const void * p = oa_gguf_tensor_data(g, i, &nb);
+        out.set_view(p, nb);
+        return true;
+    }
+};
+
+}  // namespace
+
+extern "C" oa_qwen_weights * oa_qwen_weights_load_gguf(const char * path, char * err, size_t err_cap) {
+    auto report = [&](const std::string & msg) -> oa_qwen_weights * {
+        if (err && err_cap) std::snprintf(err, err_cap, "%s", msg.c_str());
+        return nullptr;
+    };
+    char gerr[256] = {0};
+    oa_gguf * g = oa_gguf_open(path, gerr, sizeof(gerr));
+    if (!g) return report(gerr);
+    oa_qwen_weights * w = new oa_qwen_weights;
+    w->src = g;
+    pack_reader r{g, {}};
+    auto bad = [&](const std::string & msg) {
+        delete w;
+        return report(msg);
+    };
+    // OpenASR package metadata (oasr_metadata.rs:15-28): present keys must be valid
+    if (const char * v = oa_gguf_get_str(g, "openasr.package.version"); v && std::strcmp(v, "1") != 0)
+        return bad(std::string("unsupported openasr.package.version ") + v);
+    if (oa_gguf_kv_type(g, "openasr.package.version") >= 0 && !oa_gguf_get_str(g, "openasr.package.version"))
+        return bad("openasr.package.version is not a string");
+    if (const char * a = oa_gguf_get_str(g, "general.architecture"); a && std::strcmp(a, "qwen3-asr") != 0)
+        return bad(std::string("general.architecture is ") + a + ", not qwen3-asr");
+    oa_qwen_config & c = w->cfg;
+    c = oa_qwen_config{};
+    if (!r.key_i("qwen3-asr.llm.n_layers", c.n_layers) || !r.key_i("qwen3-asr.llm.d_model", c.d_model) ||
+        !r.key_i("qwen3-asr.llm.n_heads", c.n_head) || !r.key_i("qwen3-asr.llm.n_kv_heads", c.n_kv_head) ||
+        !r.key_i("qwen3-asr.llm.head_dim", c.head_dim) || !r.key_i("qwen3-asr.llm.vocab_size", c.vocab))
+        return bad(r.err);
+    if (c.n_head % c.n_kv_head != 0) return bad("n_heads is not a multiple of n_kv_heads");
+    double theta = 1e6;
+    if (oa_gguf_kv_type(g, "qwen3-asr.llm.rope_theta") >= 0 && !oa_gguf_get_f64(g, "qwen3-asr.llm.rope_theta", &theta))
+        return bad("qwen3-asr.llm.rope_theta is not a number");
+    c.rope_theta = (float) theta;
+    c.rms_eps = 1e-6f;
+    // matrix type and FFN width from the first layer's gate projection
+    const int64_t gi = oa_gguf_find_tensor(g, "blk.0.ffn_gate.weight");
+    if (gi < 0) return bad("missing tensor blk.0.ffn_gate.weight");
+    int64_t ne[4];
+    oa_gguf_tensor_info(g, gi, &c.wtype, ne);
+    if (c.wtype != GGML_TYPE_Q8_0 && c.wtype != GGML_TYPE_Q4_K)
+        return bad(std::string("matrices are ") + ggml_type_name((ggml_type) c.wtype) + ", not Q8_0 or Q4_K");
+    c.ffn = (int) ne[1];
+    const int q_w = c.n_head * c.head_dim, kv_w = c.n_kv_head * c.head_dim;
+    if (!r.mat("token_embd.weight", c.d_model, c.vocab, c.wtype, w->tok_embd) ||
+        !r.vec("output_norm.weight", c.d_model, w->out_norm))
+        return bad(r.err);
+    if (oa_gguf_find_tensor(g, "output.weight") >= 0) {
+        int ot = 0;
+        const int64_t oi = r.tensor("output.weight", c.d_model, c.vocab, {GGML_TYPE_Q8_0, GGML_TYPE_Q4_K}, ot);
+        if (oi < 0) return bad(r.err);
+        size_t nb = 0;
+        const void * p = oa_gguf_tensor_data(g, oi, &nb);
+        // byte-identical to the embedding: tied after all
+        if (ot != c.wtype || nb != w->tok_embd.size() || std::memcmp(p, w->tok_embd.data(), nb) != 0) {
+            w->lm_head.set_view(p, nb);
+            c.out_wtype = ot;
+        }
+    }
+    w->layers.resize((size_t) c.n_layers);
+    for (int l = 0; l < c.n_layers; l++) {
+        qlayer_host & L = w->layers[(size_t) l];
+        const std::string p = "blk." + std::to_string(l) + ".";
+        blob q, k, v;
+        if (!r.vec(p + "attn_norm.weight", c.d_model, L.attn_norm) ||
+            !r.vec(p + "attn_q_norm.weight", c.head_dim, L.q_norm) ||
+            !r.vec(p + "attn_k_norm.weight", c.head_dim, L.k_norm) ||
+            !r.vec(p + "ffn_norm.weight", c.d_model, L.ffn_norm) ||
+            !r.mat(p + "attn_q.weight", c.d_model, q_w, c.wtype, q) ||
+            !r.mat(p + "attn_k.weight", c.d_model, kv_w, c.wtype, k) ||
+            !r.mat(p + "attn_v.weight", c.d_model, kv_w, c.wtype, v) ||
+            !r.mat(p + "attn_output.weight", q_w, c.d_model, c.wtype, L.o) ||
+            !r.mat(p + "ffn_gate.weight", c.d_model, c.ffn, c.wtype, L.gate) ||
+            !r.mat(p + "ffn_up.weight", c.d_model, c.ffn, c.wtype, L.up) ||
+            !r.mat(p + "ffn_down.weight", c.ffn, c.d_model, c.wtype, L.down))
+            return bad(r.err);
+        // the fused projection: rows of q, then k, then v (llm_transformer.rs:6505-6555)
+        std::vector<uint8_t> qkv(q.size() + k.size() + v.size());
+        std::memcpy(qkv.data(), q.data(), q.size());
+        std::memcpy(qkv.data() + q.size(), k.data(), k.size());
+        std::memcpy(qkv.data() + q.size() + k.size(), v.data(), v.size());
+        L.qkv = std::move(qkv);
+    }
+    return w;
+}
+
+extern "C" void oa_qwen_weights_config(const oa_qwen_weights * w, oa_qwen_config * out) { *out = w->cfg; }

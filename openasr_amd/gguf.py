@@ -1,0 +1,127 @@
+"""GGUF (v3) writer for OpenASR runtime packs (`.oasr` v1 = standard GGUF
+bytes, docs/format/OASR_PACKAGE_CONTRACT_V1.md), the producer side of the
+pack reader in libopenasr-models.so (oa_gguf_open). Mirrors what the
+reference's pack writer emits (crates/openasr-core/src/ggml_runtime/
+gguf_write.rs): typed metadata, tensor infos, then every tensor's bytes at the
+pack's alignment.
+
+`export_qwen_pack` writes a qwen3-asr LLM pack from decoder weights: the
+hparam keys of arch/hparams.rs:52-58 and the tensor names of
+models/qwen/decoder_contract.rs:686-705, 764-769, with the fused q|k|v
+projection split back into attn_q / attn_k / attn_v.
+"""
+
+from __future__ import annotations
+
+import struct
+from pathlib import Path
+
+import numpy as np
+
+GGUF_MAGIC = b"GGUF"
+GGUF_VERSION = 3
+(U8, I8, U16, I16, U32, I32, F32, BOOL, STR, ARR, U64, I64, F64) = range(13)
+_SCALAR = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", BOOL: "<?", U64: "<Q",
+           I64: "<q", F64: "<d"}
+
+
+def _str(s: str | bytes) -> bytes:
+    b = s.encode() if isinstance(s, str) else s
+    return struct.pack("<Q", len(b)) + b
+
+
+def _value(vtype: int, v) -> bytes:
+    if vtype == STR:
+        return _str(v)
+    if vtype == ARR:
+        etype, items = v
+        out = struct.pack("<IQ", etype, len(items))
+        return out + b"".join(_value(etype, x) for x in items)
+    return struct.pack(_SCALAR[vtype], v)
+
+
+class GGUFWriter:
+    """Collects metadata and tensors, then writes the file in one pass."""
+
+    def __init__(self, alignment: int = 32):
+        if alignment <= 0 or alignment & (alignment - 1):
+            raise ValueError("alignment must be a power of two")
+        self.alignment = alignment
+        self.kv: list[tuple[str, int, object]] = []
+        self.tensors: list[tuple[str, int, tuple[int, ...], bytes]] = []
+        if alignment != 32:
+            self.add("general.alignment", U32, alignment)
+
+    def add(self, key: str, vtype: int, value) -> None:
+        self.kv.append((key, vtype, value))
+
+    def add_tensor(self, name: str, ggml_type: int, ne: tuple[int, ...], data: bytes | np.ndarray) -> None:
+        """ne in ggml order (ne[0] = row length); data = the tensor's bytes"""
+        raw = data.tobytes() if isinstance(data, np.ndarray) else bytes(data)
+        self.tensors.append((name, ggml_type, tuple(int(x) for x in ne), raw))
+
+    def write(self, path) -> None:
+        head = bytearray()
+        head += GGUF_MAGIC + struct.pack("<IQQ", GGUF_VERSION, len(self.tensors), len(self.kv))
+        for key, vtype, value in self.kv:
+            head += _str(key) + struct.pack("<I", vtype) + _value(vtype, value)
+        offsets = []
+        off = 0
+        for name, gtype, ne, raw in self.tensors:
+            offsets.append(off)
+            head += _str(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", x) for x in ne)
+            head += struct.pack("<IQ", gtype, off)
+            off = (off + len(raw) + self.alignment - 1) // self.alignment * self.alignment
+        pad = (-len(head)) % self.alignment
+        with open(path, "wb") as f:
+            f.write(head)
+            f.write(b"\0" * pad)
+            for (name, gtype, ne, raw), o in zip(self.tensors, offsets):
+                f.write(raw)
+                f.write(b"\0" * ((-len(raw)) % self.alignment))
+
+
+def export_qwen_pack(weights, path, with_output: bool = False, extra_kv: dict | None = None,
+                     alignment: int = 32) -> Path:
+    """Write `weights` (openasr_amd.decoders.QwenWeights) as a qwen3-asr pack.
+    with_output: also write output.weight (a copy of the tied embedding)."""
+    from . import decoders as D
+
+    c = weights.cfg
+    w = GGUFWriter(alignment)
+    w.add("general.architecture", STR, "qwen3-asr")
+    w.add("openasr.package.version", STR, "1")
+    w.add("openasr.model.family", STR, "qwen3-asr")
+    w.add("openasr.model.architecture", STR, "qwen3-asr")
+    for key, val in (("n_layers", c.n_layers), ("d_model", c.d_model), ("n_heads", c.n_head),
+                     ("n_kv_heads", c.n_kv_head), ("head_dim", c.head_dim), ("vocab_size", c.vocab)):
+        w.add(f"qwen3-asr.llm.{key}", U32, val)
+    w.add("qwen3-asr.llm.max_pos", U32, 4096)
+    if c.rope_theta != 1e6:
+        w.add("qwen3-asr.llm.rope_theta", F32, c.rope_theta)
+    for key, (vtype, val) in (extra_kv or {}).items():
+        w.add(key, vtype, val)
+    wt = c.wtype
+    q_w, kv_w = c.n_head * c.head_dim, c.n_kv_head * c.head_dim
+    emb = weights.array(-1, D.TOKEN_EMBD)
+    w.add_tensor("token_embd.weight", wt, (c.d_model, c.vocab), emb)
+    w.add_tensor("output_norm.weight", 0, (c.d_model,), weights.array(-1, D.OUTPUT_NORM))
+    if with_output:
+        w.add_tensor("output.weight", wt, (c.d_model, c.vocab), emb)
+    for layer in range(c.n_layers):
+        p = f"blk.{layer}."
+        qkv = weights.array(layer, D.QKV)
+        row = len(qkv) // (q_w + 2 * kv_w)
+        w.add_tensor(p + "attn_norm.weight", 0, (c.d_model,), weights.array(layer, D.ATTN_NORM))
+        w.add_tensor(p + "attn_q.weight", wt, (c.d_model, q_w), qkv[:q_w * row])
+        w.add_tensor(p + "attn_k.weight", wt, (c.d_model, kv_w), qkv[q_w * row:(q_w + kv_w) * row])
+        w.add_tensor(p + "attn_v.weight", wt, (c.d_model, kv_w), qkv[(q_w + kv_w) * row:])
+        w.add_tensor(p + "attn_q_norm.weight", 0, (c.head_dim,), weights.array(layer, D.Q_NORM))
+        w.add_tensor(p + "attn_k_norm.weight", 0, (c.head_dim,), weights.array(layer, D.K_NORM))
+        w.add_tensor(p + "attn_output.weight", wt, (q_w, c.d_model), weights.array(layer, D.O))
+        w.add_tensor(p + "ffn_norm.weight", 0, (c.d_model,), weights.array(layer, D.FFN_NORM))
+        w.add_tensor(p + "ffn_gate.weight", wt, (c.d_model, c.ffn), weights.array(layer, D.GATE))
+        w.add_tensor(p + "ffn_up.weight", wt, (c.d_model, c.ffn), weights.array(layer, D.UP))
+        w.add_tensor(p + "ffn_down.weight", wt, (c.ffn, c.d_model), weights.array(layer, D.DOWN))
+    w.write(path)
+    return Path(path)

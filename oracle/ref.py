@@ -186,7 +186,7 @@ def flash_attn(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16: np.ndarr
 class QwenDims(C.Structure):
     _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("n_kv_head", C.c_int),
                 ("head_dim", C.c_int), ("ffn", C.c_int), ("vocab", C.c_int), ("wtype", C.c_int),
-                ("rope_theta", C.c_float), ("rms_eps", C.c_float)]
+                ("rope_theta", C.c_float), ("rms_eps", C.c_float), ("out_wtype", C.c_int)]
 
 
 class QwenRef:
@@ -201,7 +201,7 @@ class QwenRef:
         L.ref_qwen_embed.restype = None
         L.ref_qwen_embed.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p]
         self.dims = QwenDims(cfg.d_model, cfg.n_layers, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.ffn, cfg.vocab,
-                             cfg.wtype, cfg.rope_theta, cfg.rms_eps)
+                             cfg.wtype, cfg.rope_theta, cfg.rms_eps, getattr(cfg, "out_wtype", 0))
         self.table = (C.c_void_p * len(pointer_table))(*pointer_table)
         self.max_pos = max_pos
         self.fidelity = fa_fidelity
@@ -243,7 +243,7 @@ class QwenRefBatch:
         L.ref_qwen_decode_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
                                             C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int, C.c_int]
         self.dims = QwenDims(cfg.d_model, cfg.n_layers, cfg.n_head, cfg.n_kv_head, cfg.head_dim, cfg.ffn, cfg.vocab,
-                             cfg.wtype, cfg.rope_theta, cfg.rms_eps)
+                             cfg.wtype, cfg.rope_theta, cfg.rms_eps, getattr(cfg, "out_wtype", 0))
         self.table = (C.c_void_p * len(pointer_table))(*pointer_table)
         self.max_pos, self.n_seq, self.fidelity, self.threads = max_pos, n_seq, fa_fidelity, threads
         shape = (cfg.n_kv_head, max_pos, cfg.head_dim)

@@ -19,11 +19,21 @@
 typedef struct {
     int d_model, n_layers, n_head, n_kv_head, head_dim, ffn, vocab, wtype;
     float rope_theta, rms_eps;
+    int out_wtype; /* type of a separate output projection */
 } ref_qwen_dims;
 
 /* pointer table: [tok_embd, out_norm, then per layer attn_norm, qkv, q_norm,
- * k_norm, o, ffn_norm, gate, up, down] */
+ * k_norm, o, ffn_norm, gate, up, down, then the output projection or NULL
+ * when it is tied to tok_embd] */
 enum { T_EMBD = 0, T_OUT_NORM = 1, T_LAYER0 = 2, T_PER_LAYER = 9 };
+
+/* the logits projection: a separate output.weight, else the tied embedding
+ * (llm_transformer.rs:2096-2115) */
+static const void * lm_head(const ref_qwen_dims * m, const void * const * t, int * type) {
+    const void * o = t[T_LAYER0 + m->n_layers * T_PER_LAYER];
+    *type = o ? m->out_wtype : m->wtype;
+    return o ? o : t[T_EMBD];
+}
 
 static const void * tp(const void * const * t, int layer, int idx) { return t[T_LAYER0 + layer * T_PER_LAYER + idx]; }
 
@@ -114,7 +124,9 @@ int32_t ref_qwen_forward(const ref_qwen_dims * m, const void * const * t, uint16
         float * last = x + (size_t) (T - 1) * d;
         ref_rms_norm(last, nrm, d, 1, m->rms_eps);
         mul_row_weight(nrm, (const float *) t[T_OUT_NORM], 1, d);
-        ref_mul_mat(m->wtype, t[T_EMBD], rs_d, m->vocab, d, nrm, d, 1, logits, m->vocab, threads);
+        int lt;
+        const void * lw = lm_head(m, t, &lt);
+        ref_mul_mat(lt, lw, ref_row_size(lt, d), m->vocab, d, nrm, d, 1, logits, m->vocab, threads);
         top1 = ref_argmax_first(logits, m->vocab);
     }
     free(x);
@@ -196,7 +208,9 @@ void ref_qwen_decode_batch(const ref_qwen_dims * m, const void * const * t, uint
     }
     ref_rms_norm(x, nrm, d, N, m->rms_eps);
     mul_row_weight(nrm, (const float *) t[T_OUT_NORM], N, d);
-    ref_mul_mat(m->wtype, t[T_EMBD], rs_d, m->vocab, d, nrm, d, N, lg, m->vocab, threads);
+    int lt;
+    const void * lw = lm_head(m, t, &lt);
+    ref_mul_mat(lt, lw, ref_row_size(lt, d), m->vocab, d, nrm, d, N, lg, m->vocab, threads);
     for (int i = 0; i < N; i++) {
         top1[i] = ref_argmax_first(lg + (size_t) i * m->vocab, m->vocab);
         if (logits) memcpy(logits + (size_t) i * m->vocab, lg + (size_t) i * m->vocab, sizeof(float) * m->vocab);

@@ -26,8 +26,8 @@ pytestmark = pytest.mark.gpu
 TINY = dict(d_model=256, n_layers=2, n_head=4, n_kv_head=2, head_dim=64, ffn=512, vocab=1000)
 
 
-def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed=7, check_logits=True):
-    w = D.QwenWeights(wtype, seed=seed, **shape)
+def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed=7, check_logits=True, weights=None):
+    w = weights or D.QwenWeights(wtype, seed=seed, **shape)
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(n_seq, max_pos)
     wl = D.QwenWorkload("test", shape, wtype, n_seq, prefix, prompt, steps, max_pos)
@@ -74,7 +74,8 @@ def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed
     assert np.abs(rk - gk).max() <= 2e-2 * np.abs(rk).max()
     sess.free()
     model.free()
-    w.free()
+    if weights is None:
+        w.free()
     return gpu_tokens
 
 
@@ -181,7 +182,8 @@ def test_qwen3_17b_q4_K_batch8_long_context(gpu, ref):
     s = 5
     two = types.SimpleNamespace(**{f: getattr(w.cfg, f) for f, _ in w.cfg._fields_})
     two.n_layers = 2
-    r2 = ref.QwenRef(two, w.pointer_table(), wl.max_positions)
+    tbl = w.pointer_table()
+    r2 = ref.QwenRef(two, tbl[:2 + 2 * 9] + tbl[-1:], wl.max_positions)  # layers 0-1, then the output projection
     r2.forward(np.concatenate([emb[s], r2.embed(prompt[s])]))
     for layer in range(2):
         k, v = sess.read_kv(layer, s)
@@ -208,4 +210,59 @@ def test_qwen3_17b_q4_K_batch8_long_context(gpu, ref):
     assert max_dl < 1e-2
     sess.free()
     model.free()
+    w.free()
+
+
+def test_runtime_pack_decodes_like_synthesized(gpu, ref, tmp_path):
+    """a qwen3-asr runtime pack (GGUF, q/k/v split, views into the mapping)
+    loads into the device and decodes the same tokens as the weights it was
+    written from, token-exact against the oracle"""
+    from openasr_amd import gguf
+    print("runtime pack: tied output", flush=True)
+    shape = dict(TINY, vocab=4096)
+    w = D.QwenWeights(g.Q4_K, seed=21, **shape)
+    path = gguf.export_qwen_pack(w, tmp_path / "tiny.oasr", with_output=True)
+    packed = D.QwenWeights.load_gguf(path)
+    a = run_pair(gpu, ref, shape, g.Q4_K, 2, prefix=100, prompt=4, steps=16, max_pos=256, seed=21, weights=w)
+    b = run_pair(gpu, ref, shape, g.Q4_K, 2, prefix=100, prompt=4, steps=16, max_pos=256, seed=21, weights=packed)
+    assert np.array_equal(a, b)
+    packed.free()
+    w.free()
+
+
+def test_runtime_pack_separate_output(gpu, ref, tmp_path):
+    """a pack whose output.weight differs from the embedding (Q8_0 over Q4_K
+    matrices): the device projects logits with it, token-exact against the
+    oracle given the same projection"""
+    from openasr_amd import gguf
+    print("runtime pack: separate Q8_0 output", flush=True)
+    shape = dict(TINY, vocab=4096)
+    w = D.QwenWeights(g.Q4_K, seed=31, **shape)
+    other = D.QwenWeights(g.Q8_0, seed=32, **shape)
+    base = gguf.export_qwen_pack(w, tmp_path / "base.oasr")
+    # same pack plus a distinct output projection
+    wr = gguf.GGUFWriter()
+    L = D.lib()
+    import ctypes as C
+    err = C.create_string_buffer(256)
+    h = L.oa_gguf_open(str(base).encode(), err, 256)
+    assert h, err.value
+    for key in ("n_layers", "d_model", "n_heads", "n_kv_heads", "head_dim", "vocab_size"):
+        v = C.c_int64(0)
+        assert L.oa_gguf_get_i64(h, f"qwen3-asr.llm.{key}".encode(), C.byref(v))
+        wr.add(f"qwen3-asr.llm.{key}", gguf.U32, v.value)
+    for i in range(L.oa_gguf_n_tensors(h)):
+        t, ne, n = C.c_int(0), (C.c_int64 * 4)(), C.c_size_t(0)
+        nd = L.oa_gguf_tensor_info(h, i, C.byref(t), ne)
+        p = L.oa_gguf_tensor_data(h, i, C.byref(n))
+        data = bytes((C.c_uint8 * n.value).from_address(p))
+        wr.add_tensor(L.oa_gguf_tensor_name(h, i).decode(), t.value, tuple(ne)[:nd], data)
+    L.oa_gguf_close(h)
+    wr.add_tensor("output.weight", g.Q8_0, (shape["d_model"], shape["vocab"]), other.array(-1, D.TOKEN_EMBD))
+    wr.write(tmp_path / "untied.oasr")
+    packed = D.QwenWeights.load_gguf(tmp_path / "untied.oasr")
+    assert packed.cfg.out_wtype == g.Q8_0
+    run_pair(gpu, ref, shape, g.Q4_K, 2, prefix=100, prompt=4, steps=16, max_pos=256, seed=31, weights=packed)
+    packed.free()
+    other.free()
     w.free()
