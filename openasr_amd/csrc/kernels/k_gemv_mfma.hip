@@ -348,15 +348,58 @@ __device__ __forceinline__ void gemv_stage_norm(const gemv_args & a, int n0, int
     __syncthreads();
 }
 
-// per-lane scale / min of sub-blocks 0..7 of one Q4_K super-block header
-__device__ __forceinline__ void q4k_scales(const uint4 & hdr, int * sc, int * mn) {
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// the A operand of the min correction: the 32-element sums of sub-blocks g
+// and g + 4 (g = lane / 16) of the lane's activation column, as floats
+__device__ __forceinline__ void q4k_ssum_operand(const int16_t * col_ss, bool ok, int g, float (&ssa)[2]) {
+    const int s0 = col_ss[g], s1 = col_ss[g + 4];
+    ssa[0] = ok ? (float) s0 : 0.0f;
+    ssa[1] = ok ? (float) s1 : 0.0f;
+}
+
+// one Q4_K super-block of a 16-row tile against four activation columns per
+// lane: integer MFMA sums per sub-block, scaled by the 6-bit scales (exact
+// 24-bit products), then d * isum - dmin * msum added to acc in f64. The min
+// correction msum = sum over sub-blocks of min(row) * ssum(column) runs on
+// two f32 MFMAs (16x16x4, sub-blocks g and g + 4 of lane group g): every
+// product is below 2^18 and every partial sum below 2^21, so the f32 result
+// is the exact integer.
+__device__ __forceinline__ void q4k_unit(const uint4 & hdr, const long (&q)[4], const long (&af)[8],
+                                         const float (&ad)[4], const float (&ssa)[2], double (&acc)[4]) {
+    const int g = (threadIdx.x & 63) >> 4;
     const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;  // bytes 0-3, 4-7, 8-11 of scales[12]
+    // B operand of the min correction: this row's mins of sub-blocks g and g + 4
+    const float m0 = (float) ((s1 >> (8 * g)) & 63);
+    const float m1 = (float) (((s2 >> (8 * g + 4)) & 0xF) | (((s1 >> (8 * g + 6)) & 3) << 4));
+    const v4f z = {0.f, 0.f, 0.f, 0.f};
+    const v4f mlo = __builtin_amdgcn_mfma_f32_16x16x4f32(ssa[0], m0, z, 0, 0, 0);
+    const v4f msum = __builtin_amdgcn_mfma_f32_16x16x4f32(ssa[1], m1, mlo, 0, 0, 0);
+    int sc[8];
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         sc[j] = (s0 >> (8 * j)) & 63;
-        mn[j] = (s1 >> (8 * j)) & 63;
         sc[j + 4] = ((s2 >> (8 * j)) & 0xF) | (((s0 >> (8 * j + 6)) & 3) << 4);
-        mn[j + 4] = ((s2 >> (8 * j + 4)) & 0xF) | (((s1 >> (8 * j + 6)) & 3) << 4);
+    }
+    int isum[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+        const long lo = q[c] & 0x0F0F0F0F0F0F0F0FL;
+        const long hi = (q[c] >> 4) & 0x0F0F0F0F0F0F0F0FL;
+        const v4i zi = {0, 0, 0, 0};
+        const v4i c0v = mfma_i8(af[2 * c], lo, zi);
+        const v4i c1v = mfma_i8(af[2 * c + 1], hi, zi);
+#pragma unroll
+        for (int i = 0; i < 4; i++) isum[i] += __mul24(sc[2 * c], c0v[i]) + __mul24(sc[2 * c + 1], c1v[i]);
+    }
+    const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
+    const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const double da = (double) ad[i];
+        const double d = (double) dw * da;
+        const double dmin = (double) dmw * da;
+        acc[i] += d * (double) isum[i] - dmin * (double) msum[i];
     }
 }
 
@@ -477,8 +520,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
     double acc[4] = {0.0, 0.0, 0.0, 0.0};
     for (; sb < nsb; sb += half) {
         long af[8];
-        float ad[4];
-        uint4 ss[4];
+        float ad[4], ssa[2];
         // every load unconditional (clamped to column 0 of the chunk, which
         // always exists) and masked afterwards: no load waits behind a branch
 #pragma unroll
@@ -488,45 +530,13 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
             const int n = 4 * g + i;
             const int nn = n < nc ? n : 0;
             ad[i] = adp[(int64_t) (c0 + nn) * d_stride + sb];
-            ss[i] = *(const uint4 *) (asp + (int64_t) (c0 + nn) * ss_stride + sb * 8);
         }
+        q4k_ssum_operand(asp + (int64_t) (c0 + (a_ok ? r : 0)) * ss_stride + sb * 8, a_ok, g, ssa);
 #pragma unroll
         for (int j = 0; j < 8; j++) af[j] = a_ok ? af[j] : 0;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const bool ok = 4 * g + i < nc;
-            ad[i] = ok ? ad[i] : 0.0f;
-            ss[i] = ok ? ss[i] : make_uint4(0, 0, 0, 0);
-        }
-        int sc[8], mn[8];
-        q4k_scales(hdr, sc, mn);
-        int isum[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const long lo = q[c] & 0x0F0F0F0F0F0F0F0FL;
-            const long hi = (q[c] >> 4) & 0x0F0F0F0F0F0F0F0FL;
-            const v4i z = {0, 0, 0, 0};
-            const v4i c0v = mfma_i8(af[2 * c], lo, z);
-            const v4i c1v = mfma_i8(af[2 * c + 1], hi, z);
-#pragma unroll
-            for (int i = 0; i < 4; i++) isum[i] += __mul24(sc[2 * c], c0v[i]) + __mul24(sc[2 * c + 1], c1v[i]);
-        }
-        const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
-        const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t w4[4] = {ss[i].x, ss[i].y, ss[i].z, ss[i].w};
-            int msum = 0;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                msum += __mul24(mn[2 * j], (int) (int16_t) (w4[j] & 0xFFFF));
-                msum += __mul24(mn[2 * j + 1], (int) (int16_t) (w4[j] >> 16));
-            }
-            const double da = (double) ad[i];
-            const double d = (double) dw * da;
-            const double dmin = (double) dmw * da;
-            acc[i] += d * (double) isum[i] - dmin * (double) msum;
-        }
+        for (int i = 0; i < 4; i++) ad[i] = 4 * g + i < nc ? ad[i] : 0.0f;
+        q4k_unit(hdr, q, af, ad, ssa, acc);
         // the next unit's weights
         if (sb + half < nsb) {
             const char * blk = wrow + (sb + half) * 144;
@@ -542,6 +552,29 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
 // take groups of 8 blocks round-robin, each group's loads issued together
 // (the first group's weights before the prologue)
 constexpr int kQ8Group = 8;
+
+// the first nb (<= kQ8Group) blocks of a group of a 16-row tile against four
+// activation columns per lane: one MFMA per block, each integer sum times
+// d_w * d_a added to acc in f64
+__device__ __forceinline__ void q8_0_unit(const long (&q)[kQ8Group], const uint16_t (&ds)[kQ8Group],
+                                          const long (&af)[kQ8Group], const float4 (&ad)[4][kQ8Group / 4], int nb,
+                                          double (&acc)[4]) {
+#pragma unroll
+    for (int u = 0; u < kQ8Group; u++) {
+        if (u < nb) {
+            const v4i z = {0, 0, 0, 0};
+            const v4i cc = mfma_i8(af[u], q[u], z);
+            const float dw = half_bits_to_float(ds[u]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 d4 = ad[i][u / 4];
+                const float da = (u & 3) == 0 ? d4.x : (u & 3) == 1 ? d4.y : (u & 3) == 2 ? d4.z : d4.w;
+                // d_w * d_a of two halves is exact in f32, the term exact in f64
+                acc[i] += (double) cc[i] * (double) (dw * da);
+            }
+        }
+    }
+}
 
 template <int PRO, int MAXW>
 __global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
@@ -630,23 +663,139 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
                 for (int v = 0; v < kQ8Group / 4; v++) ad[i][v] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
         }
+        q8_0_unit(q, ds, af, ad, (int) (nblk - b0 < kQ8Group ? nblk - b0 : kQ8Group), acc);
+    }
+    gemv_finish(a, acc, s_red, row, n0, half, res);
+}
+
+// Streaming form for tall matrices with pre-quantized activations (the
+// vocabulary projection: thousands of tiles, one unit per wave). A workgroup
+// of U waves (U = units of a row) keeps wave w's activation operands -- those
+// of unit w, the same for every tile -- in registers and walks batches of
+// kStreamTiles consecutive tiles, batch k + 1's weights requested before
+// batch k's arithmetic. Each wave puts its unit's term of every tile of the
+// batch in LDS; after one barrier wave j sums tile j's terms in wave order
+// (the order of gemv_finish) and stores the rows.
+constexpr int kStreamTiles = 4;
+
+template <int WT> struct stream_w;
+template <> struct stream_w<GGML_TYPE_Q4_K> {
+    uint4 hdr;
+    long q[4];
+};
+template <> struct stream_w<GGML_TYPE_Q8_0> {
+    long q[kQ8Group];
+    uint16_t ds[kQ8Group];
+};
+
+// unit `u` of the rows of tiles base .. base + kStreamTiles - 1 (tiles past
+// the end read tile 0, which always exists; their values are never stored)
+template <int WT>
+__device__ __forceinline__ void stream_load(const gemv_args & a, int64_t base, int u, int r, int g,
+                                            stream_w<WT> (&w)[kStreamTiles]) {
+    const int64_t ntiles = a.M / 16;
 #pragma unroll
-        for (int u = 0; u < kQ8Group; u++) {
-            if (b0 + u < nblk) {
-                const v4i z = {0, 0, 0, 0};
-                const v4i cc = mfma_i8(af[u], q[u], z);
-                const float dw = half_bits_to_float(ds[u]);
+    for (int j = 0; j < kStreamTiles; j++) {
+        const int64_t tile = base + j < ntiles ? base + j : 0;
+        const char * wrow = a.W + (tile * 16 + r) * a.row_bytes;
+        if constexpr (WT == GGML_TYPE_Q4_K) {
+            const char * blk = wrow + (int64_t) u * 144;
+            w[j].hdr = *(const uint4 *) blk;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float4 d4 = ad[i][u / 4];
-                    const float da = (u & 3) == 0 ? d4.x : (u & 3) == 1 ? d4.y : (u & 3) == 2 ? d4.z : d4.w;
-                    // d_w * d_a of two halves is exact in f32, the term exact in f64
-                    acc[i] += (double) cc[i] * (double) (dw * da);
-                }
+            for (int c = 0; c < 4; c++) w[j].q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
+        } else {
+            const uint16_t * wsc = (const uint16_t *) (wrow + a.K);
+            const int64_t b0 = (int64_t) u * kQ8Group;
+#pragma unroll
+            for (int v = 0; v < kQ8Group; v++) {
+                w[j].q[v] = *(const long *) (wrow + (b0 + v) * 32 + 8 * g);
+                w[j].ds[v] = wsc[b0 + v];
             }
         }
     }
-    gemv_finish(a, acc, s_red, row, n0, half, res);
+}
+
+template <int WT>
+__global__ __launch_bounds__(512) void k_gemv_stream(gemv_args a) {
+    extern __shared__ __align__(16) char smem[];
+    double (*s_part)[64][4] = (double (*)[64][4]) smem;  // [tile of the batch * nw + wave][lane]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int n0 = (int) blockIdx.y * 16;
+    const int nc = min(16, a.N - n0);
+    const int64_t ntiles = a.M / 16;
+    const int64_t step = (int64_t) gridDim.x * kStreamTiles;
+    int64_t base = (int64_t) blockIdx.x * kStreamTiles;
+    stream_w<WT> cur[kStreamTiles], nxt[kStreamTiles];
+    stream_load<WT>(a, base, wave, r, g, cur);
+    // this wave's activation operands (unit `wave`), clamped loads masked afterwards
+    const bool a_ok = r < nc;
+    const int8_t * acol = a.aq + (int64_t) (n0 + (a_ok ? r : 0)) * a.K;
+    long af[8];
+    float ad4[4], ssa[2];
+    float4 ad8[4][kQ8Group / 4];
+    if constexpr (WT == GGML_TYPE_Q4_K) {
+        const int64_t sb = wave, nsb = a.K / 256;
+#pragma unroll
+        for (int j = 0; j < 8; j++) af[j] = *(const long *) (acol + sb * 256 + 32 * j + 8 * g);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = 4 * g + i;
+            const int nn = n < nc ? n : 0;
+            ad4[i] = a.ad[(int64_t) (n0 + nn) * nsb + sb];
+        }
+        q4k_ssum_operand(a.ass + (int64_t) (n0 + (a_ok ? r : 0)) * (a.K / 32) + sb * 8, a_ok, g, ssa);
+#pragma unroll
+        for (int i = 0; i < 4; i++) ad4[i] = 4 * g + i < nc ? ad4[i] : 0.0f;
+    } else {
+        const int64_t b0 = (int64_t) wave * kQ8Group, nblk = a.K / 32;
+#pragma unroll
+        for (int u = 0; u < kQ8Group; u++) af[u] = *(const long *) (acol + (b0 + u) * 32 + 8 * g);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = 4 * g + i;
+            const int nn = n < nc ? n : 0;
+#pragma unroll
+            for (int v = 0; v < kQ8Group / 4; v++) {
+                ad8[i][v] = *(const float4 *) (a.ad + (int64_t) (n0 + nn) * nblk + b0 + 4 * v);
+                if (n >= nc) ad8[i][v] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) af[j] = a_ok ? af[j] : 0;
+    for (; base < ntiles; base += step) {
+        if (base + step < ntiles) stream_load<WT>(a, base + step, wave, r, g, nxt);
+#pragma unroll
+        for (int j = 0; j < kStreamTiles; j++) {
+            double acc[4] = {0.0, 0.0, 0.0, 0.0};
+            if constexpr (WT == GGML_TYPE_Q4_K) q4k_unit(cur[j].hdr, cur[j].q, af, ad4, ssa, acc);
+            else q8_0_unit(cur[j].q, cur[j].ds, af, ad8, kQ8Group, acc);
+#pragma unroll
+            for (int i = 0; i < 4; i++) s_part[j * nw + wave][lane][i] = acc[i];
+        }
+        __syncthreads();
+        for (int j = wave; j < kStreamTiles; j += nw) {
+            const int64_t tile = base + j;
+            if (tile < ntiles) {
+                double v[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) v[i] = s_part[j * nw][lane][i];
+                for (int w = 1; w < nw; w++) {
+#pragma unroll
+                    for (int i = 0; i < 4; i++) v[i] += s_part[j * nw + w][lane][i];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const int n = n0 + 4 * g + i;
+                    if (n < a.N) *(float *) (a.dst + (int64_t) n * a.dst_nb1 + (tile * 16 + r) * 4) = (float) v[i];
+                }
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < kStreamTiles; j++) cur[j] = nxt[j];
+    }
 }
 
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K) {
@@ -659,6 +808,16 @@ bool gemv_mfma_supported(int wtype, int64_t M, int64_t K) {
 namespace {
 
 int64_t gemv_units(int wtype, int64_t K) { return wtype == GGML_TYPE_Q4_K ? K / 256 : (K / 32 + kQ8Group - 1) / kQ8Group; }
+
+// the streaming form: pre-quantized activations, one matrix, no residual, at
+// most 8 full units a row (the LDS of a batch stays within 64 KB), and enough
+// tiles that every CU walks several batches
+bool gemv_stream_eligible(int wtype, int64_t M, int64_t K, int mode, bool dual, bool res, int n_cu) {
+    if (mode != kProNone || dual || res || n_cu <= 0) return false;
+    if (wtype == GGML_TYPE_Q8_0 && (K / 32) % kQ8Group != 0) return false;
+    const int64_t units = gemv_units(wtype, K);
+    return units >= 1 && units <= 8 && M / 16 >= 8LL * n_cu;
+}
 
 // waves of a launch: one per unit up to 16 (8 per matrix with W2); with a
 // prologue, up to one staging group (four spans) per wave as well -- every
@@ -719,7 +878,6 @@ bool gemv_prologue_supported(int wtype, int64_t M, int64_t K, int64_t N, bool no
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const char * res,
                       int64_t res_nb1, const char * W2, const gemv_prologue * pro) {
-    (void) n_cu;
     gemv_args a;
     a.W = W;
     a.W2 = W2;
@@ -736,6 +894,26 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
     a.res_nb1 = res_nb1;
     const int mode = !pro ? kProNone : pro->norm < 0 ? kProQuant : pro->b ? kProNormBias : kProNorm;
     if (pro) a.pro = *pro;
+    if (gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu)) {
+        // tall matrix: a persistent grid of two workgroups per CU walks the tiles
+        const int64_t units = gemv_units(wtype, K);
+        const int64_t batches = (M / 16 + kStreamTiles - 1) / kStreamTiles;
+        const int64_t wgs = batches < 2LL * n_cu ? batches : 2LL * n_cu;
+        const dim3 grid((unsigned) wgs, (unsigned) ((N + 15) / 16));
+        const size_t lds = (size_t) kStreamTiles * units * 64 * 4 * sizeof(double);
+        const void * fn = wtype == GGML_TYPE_Q4_K ? (const void *) k_gemv_stream<GGML_TYPE_Q4_K>
+                                                  : (const void *) k_gemv_stream<GGML_TYPE_Q8_0>;
+        static bool raised[2] = {false, false};
+        bool & done = raised[wtype == GGML_TYPE_Q4_K ? 0 : 1];
+        if (lds > 48 * 1024 && !done) {
+            MI_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+            done = true;
+        }
+        if (wtype == GGML_TYPE_Q4_K)
+            hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q4_K>), grid, dim3(64 * units), lds, stream, a);
+        else hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q8_0>), grid, dim3(64 * units), lds, stream, a);
+        return;
+    }
     const dim3 grid((unsigned) (M / 16), (unsigned) ((N + 15) / 16));
     const dim3 block(64 * gemv_waves(wtype, K, N, W2 != nullptr, mode));
     const size_t lds = mode == kProNone ? 0 : (size_t) gemv_lds_layout(wtype, K, (int) (N < 16 ? N : 16)).total;

@@ -119,14 +119,25 @@ def test_norm_then_mul_mat_prologue(ggml, gpu, ref, norm, wname, m, k, n):
     G.free()
 
 
-def test_mul_mat_lm_head_full_size(ggml, gpu, ref):
-    """151936 x 1024 Q4_K at batch 8, the largest decode GEMV of the Qwen3-0.6B shape"""
-    m, k, n = 151936, 1024, 8
+TALL_CASES = [
+    # weights, M, K, N: the vocabulary projections of the Qwen3 shapes, and a
+    # tile count that leaves a partial batch, at K = 2048 (eight waves)
+    ("q4_K", 151936, 1024, 8), ("q8_0", 151936, 1024, 1), ("q4_K", 151936, 1024, 16),
+    ("q4_K", 32784, 2048, 3), ("q8_0", 32784, 2048, 8),
+]
+
+
+@pytest.mark.parametrize("wname,m,k,n", TALL_CASES)
+def test_mul_mat_lm_head_full_size(ggml, gpu, ref, wname, m, k, n):
+    """tall decode GEMVs (the streaming launch walks batches of tiles),
+    bit-exact, same argmax"""
+    wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
+    print(f"tall mul_mat {wname} M={m} K={k} N={n}", flush=True)
     w = ggml.synth_normal(5, 99, m * k, 0.0, 0.02).reshape(m, k)
-    wq = ggml.quantize(ggml.Q4_K, w)
+    wq = ggml.quantize(wt, w)
     x = RNG.standard_normal((n, k)).astype(np.float32)
     G = ggml.Graph()
-    W = G.new(ggml.Q4_K, k, m, weight=True)
+    W = G.new(wt, k, m, weight=True)
     X = G.new(ggml.F32, k, n)
     Y = G.lib.ggml_mul_mat(G.ctx, W, X)
     run(ggml, gpu, G, Y)
@@ -134,7 +145,7 @@ def test_mul_mat_lm_head_full_size(ggml, gpu, ref):
     G.set(X, x)
     assert G.compute(gpu.backend) == 0
     y = G.get(Y).reshape(n, m)
-    want = ref.mul_mat(ggml.Q4_K, wq, m, k, x)
+    want = ref.mul_mat(wt, wq, m, k, x)
     assert_same_bits(y, want)
     assert np.array_equal(y.argmax(1), want.argmax(1))
     G.free()
