@@ -675,8 +675,12 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
 // kStreamTiles consecutive tiles, batch k + 1's weights requested before
 // batch k's arithmetic. Each wave puts its unit's term of every tile of the
 // batch in LDS; after one barrier wave j sums tile j's terms in wave order
-// (the order of gemv_finish) and stores the rows.
-constexpr int kStreamTiles = 4;
+// (the order of gemv_finish) and stores the rows. The LDS of consecutive
+// batches alternates, so one barrier a batch suffices: a wave writes a
+// buffer again only after the next batch's barrier, which every wave reaches
+// after its reads of that buffer.
+constexpr int kStreamTiles = 2;
+constexpr int kStreamWgPerCu = 4;
 
 template <int WT> struct stream_w;
 template <> struct stream_w<GGML_TYPE_Q4_K> {
@@ -764,15 +768,16 @@ __global__ __launch_bounds__(512) void k_gemv_stream(gemv_args a) {
     }
 #pragma unroll
     for (int j = 0; j < 8; j++) af[j] = a_ok ? af[j] : 0;
-    for (; base < ntiles; base += step) {
+    for (int par = 0; base < ntiles; base += step, par ^= 1) {
         if (base + step < ntiles) stream_load<WT>(a, base + step, wave, r, g, nxt);
+        double (*sp)[64][4] = s_part + par * kStreamTiles * nw;
 #pragma unroll
         for (int j = 0; j < kStreamTiles; j++) {
             double acc[4] = {0.0, 0.0, 0.0, 0.0};
             if constexpr (WT == GGML_TYPE_Q4_K) q4k_unit(cur[j].hdr, cur[j].q, af, ad4, ssa, acc);
             else q8_0_unit(cur[j].q, cur[j].ds, af, ad8, kQ8Group, acc);
 #pragma unroll
-            for (int i = 0; i < 4; i++) s_part[j * nw + wave][lane][i] = acc[i];
+            for (int i = 0; i < 4; i++) sp[j * nw + wave][lane][i] = acc[i];
         }
         __syncthreads();
         for (int j = wave; j < kStreamTiles; j += nw) {
@@ -780,10 +785,10 @@ __global__ __launch_bounds__(512) void k_gemv_stream(gemv_args a) {
             if (tile < ntiles) {
                 double v[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = s_part[j * nw][lane][i];
+                for (int i = 0; i < 4; i++) v[i] = sp[j * nw][lane][i];
                 for (int w = 1; w < nw; w++) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++) v[i] += s_part[j * nw + w][lane][i];
+                    for (int i = 0; i < 4; i++) v[i] += sp[j * nw + w][lane][i];
                 }
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
@@ -792,7 +797,6 @@ __global__ __launch_bounds__(512) void k_gemv_stream(gemv_args a) {
                 }
             }
         }
-        __syncthreads();
 #pragma unroll
         for (int j = 0; j < kStreamTiles; j++) cur[j] = nxt[j];
     }
@@ -810,7 +814,7 @@ namespace {
 int64_t gemv_units(int wtype, int64_t K) { return wtype == GGML_TYPE_Q4_K ? K / 256 : (K / 32 + kQ8Group - 1) / kQ8Group; }
 
 // the streaming form: pre-quantized activations, one matrix, no residual, at
-// most 8 full units a row (the LDS of a batch stays within 64 KB), and enough
+// most 8 full units a row (the LDS of two batches stays within 64 KB), and enough
 // tiles that every CU walks several batches
 bool gemv_stream_eligible(int wtype, int64_t M, int64_t K, int mode, bool dual, bool res, int n_cu) {
     if (mode != kProNone || dual || res || n_cu <= 0) return false;
@@ -895,12 +899,12 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
     const int mode = !pro ? kProNone : pro->norm < 0 ? kProQuant : pro->b ? kProNormBias : kProNorm;
     if (pro) a.pro = *pro;
     if (gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu)) {
-        // tall matrix: a persistent grid of two workgroups per CU walks the tiles
+        // tall matrix: a persistent grid of kStreamWgPerCu workgroups per CU walks the tiles
         const int64_t units = gemv_units(wtype, K);
         const int64_t batches = (M / 16 + kStreamTiles - 1) / kStreamTiles;
-        const int64_t wgs = batches < 2LL * n_cu ? batches : 2LL * n_cu;
-        const dim3 grid((unsigned) wgs, (unsigned) ((N + 15) / 16));
-        const size_t lds = (size_t) kStreamTiles * units * 64 * 4 * sizeof(double);
+        const int64_t cap = (int64_t) kStreamWgPerCu * n_cu;
+        const dim3 grid((unsigned) (batches < cap ? batches : cap), (unsigned) ((N + 15) / 16));
+        const size_t lds = 2 * (size_t) kStreamTiles * units * 64 * 4 * sizeof(double);
         const void * fn = wtype == GGML_TYPE_Q4_K ? (const void *) k_gemv_stream<GGML_TYPE_Q4_K>
                                                   : (const void *) k_gemv_stream<GGML_TYPE_Q8_0>;
         static bool raised[2] = {false, false};
