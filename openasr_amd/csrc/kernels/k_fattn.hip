@@ -443,10 +443,14 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     const int pos = c * kFaChunk + lane;
 
     // the query (f16-rounded) and the mask first; in the step form every
-    // independent input is requested before any is used
+    // independent input is requested before any is used, and the query's
+    // norm and rotation wait until the chunk's K/V loads are in flight
     int jn = -1;  // STEP: the chunk row of this step's position, if in this chunk
     int64_t r_new = -1;
     float mv = -INFINITY;
+    // STEP: the query's inputs, normalised and rotated once the K/V loads are in flight
+    float qx0 = 0.0f, qx1 = 0.0f, qw0 = 0.0f, qw1 = 0.0f;
+    float2 qcs = make_float2(0.0f, 0.0f);
     if constexpr (STEP) {
         const char * ip = st.idx + (int64_t) (kvh % st.idx_ne1) * st.idx_nb1 + (int64_t) (seq % st.idx_ne2) * st.idx_nb2;
         const float * qx = (const float *) (st.qsrc + (int64_t) head * st.q_nb1 + (int64_t) seq * st.q_nb2);
@@ -458,10 +462,11 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
             if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
         }
         r_new = st.idx_i64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
-        float y0, y1;
-        as_norm_rope(x0, x1, w0, w1, cs, st.q_eps, y0, y1);
-        s_q[wave][lane] = round_to_half(y0);
-        s_q[wave][lane + 64] = round_to_half(y1);
+        qx0 = x0;
+        qx1 = x1;
+        qw0 = w0;
+        qw1 = w1;
+        qcs = cs;
         const int64_t j = r_new - (int64_t) c * kFaChunk;
         jn = j >= 0 && j < clen ? (int) j : -1;
     } else {
@@ -512,6 +517,10 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
         else vr[j] = (uint32_t) *(const uint16_t *) (vb + off);
     }
     if constexpr (STEP) {
+        float y0, y1;
+        as_norm_rope(qx0, qx1, qw0, qw1, qcs, st.q_eps, y0, y1);
+        s_q[wave][lane] = round_to_half(y0);
+        s_q[wave][lane + 64] = round_to_half(y1);
         if (jn >= 0) {
             // this step's K / V rows: K replaces the LDS row jn (after the
             // transposing stores above, in program order within the wave), V
