@@ -58,6 +58,7 @@ struct gemv_args {
     const float * ad;
     const int16_t * ass;  // Q8_K 32-element sums
     int N;                // activation columns
+    int cw;               // columns a workgroup takes (16, fewer to spread a short matrix's prologue)
     char * dst;
     int64_t dst_nb1;
     const char * res;  // optional residual, same layout as dst
@@ -424,7 +425,7 @@ __device__ __forceinline__ void gemv_res_prefetch(const gemv_args & a, int64_t r
 }
 
 __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4], double (*s_red)[64][4], int64_t row,
-                                            int n0, int half, const float (&res)[4]) {
+                                            int n0, int nc, int half, const float (&res)[4]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int g = lane >> 4;
     double acc2[4] = {0.0, 0.0, 0.0, 0.0};
@@ -447,7 +448,7 @@ __device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         const int n = n0 + 4 * g + i;
-        if (n < a.N) {
+        if (4 * g + i < nc) {  // the workgroup's columns (nc <= N - n0)
             float v = (float) acc[i];
             if (a.W2) {
                 const float u = (float) acc2[i];
@@ -472,8 +473,8 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
     const int wv = wave - (second ? half : 0);
     const int r = lane & 15, g = lane >> 4;
     const int64_t tile = blockIdx.x;
-    const int n0 = (int) blockIdx.y * 16;
-    const int nc = min(16, a.N - n0);
+    const int n0 = (int) blockIdx.y * a.cw;
+    const int nc = min(a.cw, a.N - n0);
     const int64_t nsb = a.K / 256;
     const int64_t row = tile * 16 + r;
     const char * wrow = (second ? a.W2 : a.W) + row * a.row_bytes;
@@ -545,7 +546,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
             for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
         }
     }
-    gemv_finish(a, acc, s_red, row, n0, half, res);
+    gemv_finish(a, acc, s_red, row, n0, nc, half, res);
 }
 
 // Q8_0 weights in the row-split layout [K quants][K/32 f16 scales]; the waves
@@ -586,8 +587,8 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
     const int wv = wave - (second ? half : 0);
     const int r = lane & 15, g = lane >> 4;
     const int64_t tile = blockIdx.x;
-    const int n0 = (int) blockIdx.y * 16;
-    const int nc = min(16, a.N - n0);
+    const int n0 = (int) blockIdx.y * a.cw;
+    const int nc = min(a.cw, a.N - n0);
     const int64_t nblk = a.K / 32;
     const int64_t row = tile * 16 + r;
     const char * wrow = (second ? a.W2 : a.W) + row * a.row_bytes;
@@ -665,7 +666,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
         }
         q8_0_unit(q, ds, af, ad, (int) (nblk - b0 < kQ8Group ? nblk - b0 : kQ8Group), acc);
     }
-    gemv_finish(a, acc, s_red, row, n0, half, res);
+    gemv_finish(a, acc, s_red, row, n0, nc, half, res);
 }
 
 // Streaming form for tall matrices with pre-quantized activations (the
@@ -841,6 +842,29 @@ int gemv_waves(int wtype, int64_t K, int64_t N, bool dual, int pro) {
     return (int) (w * mats);
 }
 
+// columns a workgroup takes with a prologue: 16, or half as many, again,
+// while the workgroups still run in one round -- the column chunks of a tile
+// stage their activations in parallel and re-read the tile's weights from
+// L2. A split that gives a wave at most one staging group keeps one
+// workgroup a CU; while a wave still has more, a round may hold as many
+// workgroups as fit a CU at 16 waves (short matrices: the down projection).
+int gemv_cols(int wtype, int64_t M, int64_t K, int64_t N, bool dual, int mode, int n_cu) {
+    int cw = (int) (N < 16 ? N : 16);
+    if (mode == kProNone) return 16;
+    const int64_t nspan = (K + 255) / 256;
+    while (cw > 1) {
+        const int64_t groups = (cw * nspan + 3) / 4;
+        const int64_t waves = gemv_waves(wtype, K, cw, dual, mode);
+        const int half = (cw + 1) / 2;
+        const int64_t wgs = (M / 16) * ((N + half - 1) / half);
+        const int64_t per_cu = 16 / gemv_waves(wtype, K, half, dual, mode);
+        const int64_t round = (int64_t) n_cu * (groups > waves && per_cu > 1 ? per_cu : 1);
+        if (wgs > round) break;
+        cw = half;
+    }
+    return cw;
+}
+
 // kernels compiled for at most 8 waves get twice the registers per lane
 template <int PRO, int MAXW>
 void launch_kernel_w(int wtype, const dim3 & grid, const dim3 & block, size_t lds, hipStream_t stream,
@@ -898,6 +922,7 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
     a.res_nb1 = res_nb1;
     const int mode = !pro ? kProNone : pro->norm < 0 ? kProQuant : pro->b ? kProNormBias : kProNorm;
     if (pro) a.pro = *pro;
+    a.cw = 16;
     if (gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu)) {
         // tall matrix: a persistent grid of kStreamWgPerCu workgroups per CU walks the tiles
         const int64_t units = gemv_units(wtype, K);
@@ -918,9 +943,10 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
         else hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q8_0>), grid, dim3(64 * units), lds, stream, a);
         return;
     }
-    const dim3 grid((unsigned) (M / 16), (unsigned) ((N + 15) / 16));
-    const dim3 block(64 * gemv_waves(wtype, K, N, W2 != nullptr, mode));
-    const size_t lds = mode == kProNone ? 0 : (size_t) gemv_lds_layout(wtype, K, (int) (N < 16 ? N : 16)).total;
+    a.cw = gemv_cols(wtype, M, K, N, W2 != nullptr, mode, n_cu);
+    const dim3 grid((unsigned) (M / 16), (unsigned) ((N + a.cw - 1) / a.cw));
+    const dim3 block(64 * gemv_waves(wtype, K, a.cw, W2 != nullptr, mode));
+    const size_t lds = mode == kProNone ? 0 : (size_t) gemv_lds_layout(wtype, K, (int) (N < a.cw ? N : a.cw)).total;
     switch (mode) {
         case kProNone: launch_kernel<kProNone>(wtype, grid, block, lds, stream, a); break;
         case kProQuant: launch_kernel<kProQuant>(wtype, grid, block, lds, stream, a); break;
