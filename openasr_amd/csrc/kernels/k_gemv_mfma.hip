@@ -842,23 +842,24 @@ int gemv_waves(int wtype, int64_t K, int64_t N, bool dual, int pro) {
     return (int) (w * mats);
 }
 
-// columns a workgroup takes with a prologue: 16, or half as many, again,
-// while the workgroups still run in one round -- the column chunks of a tile
-// stage their activations in parallel and re-read the tile's weights from
-// L2. A split that gives a wave at most one staging group keeps one
-// workgroup a CU; while a wave still has more, a round may hold as many
-// workgroups as fit a CU at 16 waves (short matrices: the down projection).
+// columns a workgroup takes: 16, or half as many, again, while the
+// workgroups still run in one round -- the column chunks of a short matrix's
+// tile then load (and, with a prologue, stage) their activations in parallel
+// and re-read the tile's weights from L2. One workgroup a CU is the round,
+// except while a prologue still gives a wave more than one staging group:
+// then as many workgroups as fit a CU at 16 waves (the down projection).
 int gemv_cols(int wtype, int64_t M, int64_t K, int64_t N, bool dual, int mode, int n_cu) {
     int cw = (int) (N < 16 ? N : 16);
-    if (mode == kProNone) return 16;
     const int64_t nspan = (K + 255) / 256;
     while (cw > 1) {
-        const int64_t groups = (cw * nspan + 3) / 4;
-        const int64_t waves = gemv_waves(wtype, K, cw, dual, mode);
         const int half = (cw + 1) / 2;
         const int64_t wgs = (M / 16) * ((N + half - 1) / half);
-        const int64_t per_cu = 16 / gemv_waves(wtype, K, half, dual, mode);
-        const int64_t round = (int64_t) n_cu * (groups > waves && per_cu > 1 ? per_cu : 1);
+        int64_t round = n_cu;
+        if (mode != kProNone) {
+            const int64_t groups = (cw * nspan + 3) / 4;
+            const int64_t per_cu = 16 / gemv_waves(wtype, K, half, dual, mode);
+            if (groups > gemv_waves(wtype, K, cw, dual, mode) && per_cu > 1) round *= per_cu;
+        }
         if (wgs > round) break;
         cw = half;
     }
