@@ -22,7 +22,7 @@ import os
 import sys
 
 
-def _steps(rows, which: int, n: int = 8):
+def _steps(rows, which: int, n: int = 8, tail: bool = False):
     idx = [i for i, r in enumerate(rows) if "k_argmax_final" in r["Kernel_Name"]]
     groups = [[idx[0]]]
     for a, b in zip(idx, idx[1:]):
@@ -30,11 +30,12 @@ def _steps(rows, which: int, n: int = 8):
             groups.append([])
         groups[-1].append(b)
     g = groups[which]
-    a, b = g[3], g[3 + n]
+    # tail: the workload's last steps (a long prefill ends in many argmax dispatches of its own)
+    a, b = (g[-1 - n], g[-1]) if tail else (g[3], g[3 + n])
     return rows[a + 1:b + 1], n
 
 
-def table(trace: str, which: int, workload: str) -> str:
+def table(trace: str, which: int, workload: str, tail: bool = False) -> str:
     sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
     from openasr_amd import decoders as D
     from openasr_amd import ggml as g
@@ -42,10 +43,12 @@ def table(trace: str, which: int, workload: str) -> str:
 
     with open(trace, newline="") as f:
         rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
-    win, n = _steps(rows, which)
+    win, n = _steps(rows, which, tail=tail)
     st = collections.defaultdict(list)
     for r in win:
         name = r["Kernel_Name"].split("(")[0].replace("void ", "").replace("mi355x::", "")
+        if name == "k_spin":  # the profiler's queue-filling spin, not part of a step
+            continue
         grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
         st[(name, grid, int(r["Workgroup_Size_X"]))].append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
     lines = ["| kernel | grid (threads) | workgroup | launches / step | avg us | min us | us / step |",
@@ -73,7 +76,12 @@ def table(trace: str, which: int, workload: str) -> str:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("trace")
+    ap.add_argument("--only", default=None, help="the trace holds this one workload (bench.py --workload W --no-b1)")
     a = ap.parse_args()
+    if a.only:
+        print(f"## {a.only}\n")
+        print(table(a.trace, 0, a.only, tail=True))
+        return 0
     print("## Q4_K weights, batch 8\n")
     print(table(a.trace, 0, "qwen3-0.6b-q4_K-b8"))
     print("\n## Q8_0 weights, batch 1\n")
