@@ -4,27 +4,34 @@
 //
 // A workgroup computes a 64-row x 64-column output tile: each of its four
 // waves owns 16 weight rows and all 64 columns (four 16-column MFMA groups),
-// so every weight fragment a wave loads feeds four v_mfma_i32_16x16x32_i8.
-// The activations of the current 256-element K slice (quants, scales and
-// 32-element sums of 64 columns) are staged once per slice in LDS and shared
-// by the four waves. The operand orientation is the GEMV's (activations A,
-// weight tile B: one weight row and four columns per lane), and each lane
-// walks K in order, so the f64 block sums are formed exactly as the CPU
-// reference forms them.
+// so every weight fragment a wave loads feeds four column groups. K is walked
+// in 256-element slices. A slice's activations (quants, scales and, for Q4_K,
+// the 32-element sums of the 64 columns) are staged in LDS, double-buffered:
+// right after a slice's barrier the workgroup requests the next slice's
+// activations and weights into registers, computes the current slice from
+// LDS, and stores the next slice into the other buffer at the top of the
+// next iteration -- one barrier a slice, the next slice's loads in flight
+// under this slice's arithmetic. A buffer is written again only after the
+// following barrier, which every wave reaches after its reads of it.
+//
+// The arithmetic of a block unit is the GEMV's (mfma_units.h) and each lane
+// walks K in order, so the f64 block sums are the ones the CPU reference
+// forms and the bits equal the GEMV's.
+//
+// Tiles are dealt to the XCDs in contiguous runs (workgroup i runs on XCD
+// i % 8): XCD x takes tiles [x P, (x + 1) P), the column blocks of a row tile
+// adjacent, so a weight tile is fetched into one XCD's L2 and read there by
+// all of its column blocks.
 #include "../mi355x_common.h"
 #include "../ops.h"
+#include "../mfma_units.h"
 
 namespace mi355x {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-__device__ __forceinline__ v4i mfma_i8_mmq(long a, long b, v4i c) {
-    return __builtin_amdgcn_mfma_i32_16x16x32_i8(a, b, c, 0, 0, 0);
-}
 
 constexpr int kMmqRows = 64;
 constexpr int kMmqCols = 64;
 constexpr int kMmqPad = 16;  // bytes of padding per staged column (LDS banks)
+constexpr int kMmqXcds = 8;
 
 struct mmq_args {
     const char * W;
@@ -35,24 +42,187 @@ struct mmq_args {
     int N;
     char * dst;
     int64_t dst_nb1;
+    int64_t col_blocks, tiles, per_xcd;
 };
 
-// stage 256 quants of each of the tile's columns (K slice ks) into LDS
-__device__ __forceinline__ void mmq_stage_q(const mmq_args & a, int n0, int ncol, int64_t ks,
-                                            int8_t (*s_q)[256 + kMmqPad]) {
-    for (int idx = (int) threadIdx.x; idx < kMmqCols * 16; idx += 256) {
-        const int col = idx / 16, piece = idx % 16;
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (col < ncol) {
-            const int8_t * src = a.aq + (int64_t) (n0 + col) * a.K + ks * 256 + piece * 16;
-            if (ks * 256 + piece * 16 < a.K) v = *(const uint4 *) src;
+// the activations of one K slice of the tile's 64 columns
+struct mmq_slice {
+    int8_t q[kMmqCols][256 + kMmqPad];
+    float d[8][kMmqCols];     // Q4_K: [0][col] the super-block scale; Q8_0: [block][col]
+    int16_t ss[kMmqCols][8];  // Q4_K: the 32-element sums
+};
+
+// this thread's share of a slice, held in registers between its request and
+// its store into LDS
+struct mmq_act {
+    uint4 q[4];
+    float d[4];
+    uint4 ss;
+};
+
+template <int WT>
+__device__ __forceinline__ void mmq_act_load(const mmq_args & a, int n0, int ncol, int64_t ks, mmq_act & r) {
+    const int t = (int) threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int idx = t + 256 * u, col = idx >> 4, piece = idx & 15;
+        const int64_t kk = ks * 256 + piece * 16;
+        const bool ok = col < ncol && kk < a.K;
+        // clamped address, unconditional load: masked when stored
+        r.q[u] = *(const uint4 *) (a.aq + (int64_t) (n0 + (ok ? col : 0)) * a.K + (ok ? kk : 0));
+    }
+    if constexpr (WT == GGML_TYPE_Q4_K) {
+        const int64_t nsb = a.K / 256;
+        const int col = t < ncol ? t : 0;
+        if (t < kMmqCols) {
+            r.d[0] = a.ad[(int64_t) (n0 + col) * nsb + ks];
+            r.ss = *(const uint4 *) (a.ass + ((int64_t) (n0 + col) * nsb + ks) * 8);
         }
-        *(uint4 *) &s_q[col][piece * 16] = v;
+    } else {
+        const int64_t nblk = a.K / 32;
+        const int col = (t >> 1) < ncol ? (t >> 1) : 0, h = t & 1;
+        if (t < 2 * kMmqCols) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int64_t b = ks * 8 + 4 * h + j;
+                r.d[j] = a.ad[(int64_t) (n0 + col) * nblk + (b < nblk ? b : nblk - 1)];
+            }
+        }
     }
 }
 
-__device__ __forceinline__ void mmq_store(const mmq_args & a, double (&acc)[4][4], int64_t row, int n0) {
-    const int g = (threadIdx.x & 63) >> 4;
+template <int WT>
+__device__ __forceinline__ void mmq_act_store(const mmq_args & a, int ncol, int64_t ks, const mmq_act & r,
+                                              mmq_slice & S) {
+    const int t = (int) threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < 4; u++) {
+        const int idx = t + 256 * u, col = idx >> 4, piece = idx & 15;
+        const bool ok = col < ncol && ks * 256 + piece * 16 < a.K;
+        *(uint4 *) &S.q[col][piece * 16] = ok ? r.q[u] : make_uint4(0, 0, 0, 0);
+    }
+    if constexpr (WT == GGML_TYPE_Q4_K) {
+        if (t < kMmqCols) {
+            const bool ok = t < ncol;
+            S.d[0][t] = ok ? r.d[0] : 0.0f;
+            *(uint4 *) &S.ss[t][0] = ok ? r.ss : make_uint4(0, 0, 0, 0);
+        }
+    } else {
+        const int64_t nblk = a.K / 32;
+        if (t < 2 * kMmqCols) {
+            const int col = t >> 1, h = t & 1;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const bool ok = col < ncol && ks * 8 + 4 * h + j < nblk;
+                S.d[4 * h + j][col] = ok ? r.d[j] : 0.0f;
+            }
+        }
+    }
+}
+
+// this lane's weights of one slice: Q4_K one super-block of its row, Q8_0
+// eight blocks (past the end of K: the row's last block, never used)
+struct mmq_w4 {
+    uint4 hdr;
+    long q[4];
+};
+struct mmq_w8 {
+    long q[kQ8Group];
+    uint16_t ds[kQ8Group];
+};
+
+__device__ __forceinline__ void mmq_w_load(const mmq_args & a, const char * wrow, int64_t ks, int g, mmq_w4 & w) {
+    const char * blk = wrow + ks * 144;
+    w.hdr = *(const uint4 *) blk;
+#pragma unroll
+    for (int c = 0; c < 4; c++) w.q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
+}
+
+__device__ __forceinline__ void mmq_w_load(const mmq_args & a, const char * wrow, int64_t ks, int g, mmq_w8 & w) {
+    const int64_t nblk = a.K / 32;
+    const uint16_t * wsc = (const uint16_t *) (wrow + a.K);
+#pragma unroll
+    for (int bb = 0; bb < kQ8Group; bb++) {
+        const int64_t b = ks * 8 + bb < nblk ? ks * 8 + bb : nblk - 1;
+        w.q[bb] = *(const long *) (wrow + b * 32 + 8 * g);
+        w.ds[bb] = wsc[b];
+    }
+}
+
+__device__ __forceinline__ void mmq_compute(const mmq_args & a, const mmq_slice & S, const mmq_w4 & w, int64_t ks,
+                                            int r, int g, double (&acc)[4][4]) {
+    (void) ks;
+#pragma unroll
+    for (int grp = 0; grp < 4; grp++) {
+        const int8_t * acol = &S.q[grp * 16 + r][0];
+        long af[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) af[j] = *(const long *) (acol + 32 * j + 8 * g);
+        const float4 d4 = *(const float4 *) &S.d[0][grp * 16 + 4 * g];
+        const float ad[4] = {d4.x, d4.y, d4.z, d4.w};
+        float ssa[2];
+        q4k_ssum_operand(&S.ss[grp * 16 + r][0], true, g, ssa);  // columns past N were staged as zeros
+        q4k_unit(w.hdr, w.q, af, ad, ssa, acc[grp]);
+    }
+}
+
+__device__ __forceinline__ void mmq_compute(const mmq_args & a, const mmq_slice & S, const mmq_w8 & w, int64_t ks,
+                                            int r, int g, double (&acc)[4][4]) {
+    const int64_t nblk = a.K / 32;
+    const int nb = (int) (nblk - ks * 8 < kQ8Group ? nblk - ks * 8 : kQ8Group);
+    // block by block (each (row, column) sum still takes its blocks in order),
+    // the column groups inner: a block's weights and scale serve four groups
+#pragma unroll
+    for (int u = 0; u < kQ8Group; u++) {
+        if (u >= nb) break;
+#pragma unroll
+        for (int grp = 0; grp < 4; grp++) {
+            const long af = *(const long *) (&S.q[grp * 16 + r][32 * u + 8 * g]);
+            const float4 d4 = *(const float4 *) &S.d[u][grp * 16 + 4 * g];
+            const float da[4] = {d4.x, d4.y, d4.z, d4.w};
+            q8_0_block(af, w.q[u], w.ds[u], da, acc[grp]);
+        }
+    }
+}
+
+template <int WT>
+__global__ __launch_bounds__(256) void k_mmq(mmq_args a) {
+    __shared__ __align__(16) mmq_slice s_buf[2];
+    using wregs = typename std::conditional<WT == GGML_TYPE_Q4_K, mmq_w4, mmq_w8>::type;
+    // contiguous runs of tiles per XCD
+    const int64_t id = blockIdx.x;
+    const int64_t t = (id % kMmqXcds) * a.per_xcd + id / kMmqXcds;
+    if (t >= a.tiles) return;  // before any barrier: the whole workgroup leaves
+    const int64_t row_tile = t / a.col_blocks, col_block = t % a.col_blocks;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t row = row_tile * kMmqRows + wave * 16 + r;
+    const bool row_ok = row_tile * kMmqRows + wave * 16 < a.M;  // uniform per wave
+    const int n0 = (int) (col_block * kMmqCols);
+    const int ncol = min(kMmqCols, a.N - n0);
+    const int64_t nks = (a.K + 255) / 256;
+    const char * wrow = a.W + (row_ok ? row : 0) * a.row_bytes;
+    double acc[4][4];
+#pragma unroll
+    for (int grp = 0; grp < 4; grp++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) acc[grp][i] = 0.0;
+    mmq_act act;
+    wregs wn;
+    mmq_act_load<WT>(a, n0, ncol, 0, act);
+    mmq_w_load(a, wrow, 0, g, wn);
+    for (int64_t ks = 0; ks < nks; ks++) {
+        mmq_slice & S = s_buf[ks & 1];
+        mmq_act_store<WT>(a, ncol, ks, act, S);
+        const wregs w = wn;
+        __syncthreads();
+        if (ks + 1 < nks) {
+            mmq_act_load<WT>(a, n0, ncol, ks + 1, act);
+            mmq_w_load(a, wrow, ks + 1, g, wn);
+        }
+        if (row_ok) mmq_compute(a, S, w, ks, r, g, acc);
+    }
+    if (!row_ok) return;
 #pragma unroll
     for (int grp = 0; grp < 4; grp++) {
 #pragma unroll
@@ -61,142 +231,6 @@ __device__ __forceinline__ void mmq_store(const mmq_args & a, double (&acc)[4][4
             if (n < a.N) *(float *) (a.dst + (int64_t) n * a.dst_nb1 + row * 4) = (float) acc[grp][i];
         }
     }
-}
-
-__global__ __launch_bounds__(256) void k_mmq_q4_K(mmq_args a) {
-    __shared__ __align__(16) int8_t s_q[kMmqCols][256 + kMmqPad];
-    __shared__ float s_d[kMmqCols];
-    __shared__ __align__(16) int16_t s_ss[kMmqCols][8];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int64_t row = (int64_t) blockIdx.x * kMmqRows + wave * 16 + r;
-    const bool row_ok = (int64_t) blockIdx.x * kMmqRows + wave * 16 < a.M;  // uniform per wave
-    const int n0 = (int) blockIdx.y * kMmqCols;
-    const int ncol = min(kMmqCols, a.N - n0);
-    const int64_t nsb = a.K / 256;
-    const char * wrow = a.W + (row_ok ? row : 0) * a.row_bytes;
-    double acc[4][4];
-#pragma unroll
-    for (int grp = 0; grp < 4; grp++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[grp][i] = 0.0;
-    for (int64_t sb = 0; sb < nsb; sb++) {
-        __syncthreads();  // the previous slice's LDS reads are done
-        mmq_stage_q(a, n0, ncol, sb, s_q);
-        if (threadIdx.x < kMmqCols) {
-            const int col = threadIdx.x;
-            s_d[col] = col < ncol ? a.ad[(int64_t) (n0 + col) * nsb + sb] : 0.0f;
-            *(uint4 *) s_ss[col] =
-                col < ncol ? *(const uint4 *) (a.ass + ((int64_t) (n0 + col) * nsb + sb) * 8) : make_uint4(0, 0, 0, 0);
-        }
-        const char * blk = wrow + sb * 144;
-        const uint4 hdr = *(const uint4 *) blk;
-        long q[4];
-#pragma unroll
-        for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
-        __syncthreads();
-        if (!row_ok) continue;
-        int sc[8], mn[8];
-        {
-            const uint32_t s0 = hdr.y, s1 = hdr.z, s2 = hdr.w;
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                sc[j] = (s0 >> (8 * j)) & 63;
-                mn[j] = (s1 >> (8 * j)) & 63;
-                sc[j + 4] = ((s2 >> (8 * j)) & 0xF) | (((s0 >> (8 * j + 6)) & 3) << 4);
-                mn[j + 4] = ((s2 >> (8 * j + 4)) & 0xF) | (((s1 >> (8 * j + 6)) & 3) << 4);
-            }
-        }
-        const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
-        const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
-#pragma unroll
-        for (int grp = 0; grp < 4; grp++) {
-            const int8_t * acol = &s_q[grp * 16 + r][0];
-            int isum[4] = {0, 0, 0, 0};
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const long lo = q[c] & 0x0F0F0F0F0F0F0F0FL;
-                const long hi = (q[c] >> 4) & 0x0F0F0F0F0F0F0F0FL;
-                const long a0 = *(const long *) (acol + 64 * c + 8 * g);
-                const long a1 = *(const long *) (acol + 64 * c + 32 + 8 * g);
-                const v4i z = {0, 0, 0, 0};
-                const v4i c0 = mfma_i8_mmq(a0, lo, z);
-                const v4i c1 = mfma_i8_mmq(a1, hi, z);
-#pragma unroll
-                for (int i = 0; i < 4; i++) isum[i] += __mul24(sc[2 * c], c0[i]) + __mul24(sc[2 * c + 1], c1[i]);
-            }
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const int n = grp * 16 + 4 * g + i;
-                int msum = 0;
-#pragma unroll
-                for (int j = 0; j < 8; j++) msum += __mul24(mn[j], (int) s_ss[n][j]);  // 6 x 13 bits
-                const double da = (double) s_d[n];
-                const double d = (double) dw * da;
-                const double dmin = (double) dmw * da;
-                acc[grp][i] += d * (double) isum[i] - dmin * (double) msum;
-            }
-        }
-    }
-    if (row_ok) mmq_store(a, acc, row, n0);
-}
-
-// Q8_0 weights in the row-split layout [K quants][K/32 f16 scales]; K is
-// walked in 256-element slices of eight blocks (the last may be partial)
-__global__ __launch_bounds__(256) void k_mmq_q8_0(mmq_args a) {
-    __shared__ __align__(16) int8_t s_q[kMmqCols][256 + kMmqPad];
-    __shared__ float s_d[kMmqCols][8];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int r = lane & 15, g = lane >> 4;
-    const int64_t row = (int64_t) blockIdx.x * kMmqRows + wave * 16 + r;
-    const bool row_ok = (int64_t) blockIdx.x * kMmqRows + wave * 16 < a.M;
-    const int n0 = (int) blockIdx.y * kMmqCols;
-    const int ncol = min(kMmqCols, a.N - n0);
-    const int64_t nblk = a.K / 32;
-    const int64_t nks = (a.K + 255) / 256;
-    const char * wrow = a.W + (row_ok ? row : 0) * a.row_bytes;
-    const uint16_t * wsc = (const uint16_t *) (wrow + a.K);
-    double acc[4][4];
-#pragma unroll
-    for (int grp = 0; grp < 4; grp++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) acc[grp][i] = 0.0;
-    for (int64_t ks = 0; ks < nks; ks++) {
-        const int nb = (int) min((int64_t) 8, nblk - ks * 8);
-        __syncthreads();
-        mmq_stage_q(a, n0, ncol, ks, s_q);
-        for (int idx = (int) threadIdx.x; idx < kMmqCols * 8; idx += 256) {
-            const int col = idx / 8, bb = idx % 8;
-            s_d[col][bb] = col < ncol && bb < nb ? a.ad[(int64_t) (n0 + col) * nblk + ks * 8 + bb] : 0.0f;
-        }
-        long q[8];
-        uint16_t ds[8];
-#pragma unroll
-        for (int bb = 0; bb < 8; bb++) {
-            q[bb] = bb < nb ? *(const long *) (wrow + (ks * 8 + bb) * 32 + 8 * g) : 0;
-            ds[bb] = bb < nb ? wsc[ks * 8 + bb] : 0;
-        }
-        __syncthreads();
-        if (!row_ok) continue;
-#pragma unroll
-        for (int bb = 0; bb < 8; bb++) {
-            if (bb >= nb) break;
-            const float dw = half_bits_to_float(ds[bb]);
-#pragma unroll
-            for (int grp = 0; grp < 4; grp++) {
-                const long av = *(const long *) (&s_q[grp * 16 + r][32 * bb + 8 * g]);
-                const v4i z = {0, 0, 0, 0};
-                const v4i cc = mfma_i8_mmq(av, q[bb], z);
-#pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const int n = grp * 16 + 4 * g + i;
-                    // d_w * d_a of two halves is exact in f32, the term exact in f64
-                    acc[grp][i] += (double) cc[i] * (double) (dw * s_d[n][bb]);
-                }
-            }
-        }
-    }
-    if (row_ok) mmq_store(a, acc, row, n0);
 }
 
 bool mmq_supported(int wtype, int64_t M, int64_t K) {
@@ -220,9 +254,12 @@ void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t
     a.N = (int) N;
     a.dst = dst;
     a.dst_nb1 = dst_nb1;
-    const dim3 grid((unsigned) ((M + kMmqRows - 1) / kMmqRows), (unsigned) ((N + kMmqCols - 1) / kMmqCols));
-    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_mmq_q4_K, grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(k_mmq_q8_0, grid, dim3(256), 0, stream, a);
+    a.col_blocks = (N + kMmqCols - 1) / kMmqCols;
+    a.tiles = ((M + kMmqRows - 1) / kMmqRows) * a.col_blocks;
+    a.per_xcd = (a.tiles + kMmqXcds - 1) / kMmqXcds;
+    const dim3 grid((unsigned) (a.per_xcd * kMmqXcds));
+    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_mmq<GGML_TYPE_Q4_K>, grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(k_mmq<GGML_TYPE_Q8_0>, grid, dim3(256), 0, stream, a);
 }
 
 }  // namespace mi355x
