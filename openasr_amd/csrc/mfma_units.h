@@ -77,14 +77,15 @@ __device__ __forceinline__ void q4k_unit(const uint4 & hdr, const long (&q)[4], 
 constexpr int kQ8Group = 8;
 
 // one Q8_0 block of a 16-row tile against four activation columns per lane:
-// the MFMA's integer sum times d_w * d_a (two halves: exact in f32), the
-// term exact in f64, added to acc
+// the MFMA's integer sum (|sum| < 2^19) times d_w * d_a (two halves: 22
+// significant bits, exact in f32) is exact in f64, so one fused multiply-add
+// rounds acc + term exactly as the separate product and sum do
 __device__ __forceinline__ void q8_0_block(long af, long q, uint16_t ds, const float (&da)[4], double (&acc)[4]) {
     const v4i z = {0, 0, 0, 0};
     const v4i cc = mfma_i8(af, q, z);
     const float dw = half_bits_to_float(ds);
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] += (double) cc[i] * (double) (dw * da[i]);
+    for (int i = 0; i < 4; i++) acc[i] = fma((double) cc[i], (double) (dw * da[i]), acc[i]);
 }
 
 // the first nb (<= kQ8Group) blocks of a group, in order
