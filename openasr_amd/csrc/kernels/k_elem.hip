@@ -689,8 +689,21 @@ __global__ __launch_bounds__(256) void k_argmax_part(tview a, uint64_t * keys, i
     const int64_t n = a.ne[0];
     const int64_t i0 = (int64_t) chunk * kArgmaxChunk;
     const int64_t i1 = i0 + kArgmaxChunk < n ? i0 + kArgmaxChunk : n;
+    // every load of the thread requested before the first key (clamped
+    // index, masked); the launch is 256 threads, kArgmaxChunk / 256 each
+    constexpr int kPer = kArgmaxChunk / 256;
+    float v[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+        const int64_t i = i0 + threadIdx.x + 256 * u;
+        v[u] = x[i < i1 ? i : i0];
+    }
     uint64_t best = 0;
-    for (int64_t i = i0 + threadIdx.x; i < i1; i += blockDim.x) best = max_u64(best, argmax_key(x[i], (uint32_t) i, first));
+#pragma unroll
+    for (int u = 0; u < kPer; u++) {
+        const int64_t i = i0 + threadIdx.x + 256 * u;
+        if (i < i1) best = max_u64(best, argmax_key(v[u], (uint32_t) i, first));
+    }
     for (int off = 32; off > 0; off >>= 1) {
         const uint64_t o = ((uint64_t) __shfl_xor((unsigned) (best >> 32), off) << 32) |
                            (uint64_t) __shfl_xor((unsigned) best, off);
