@@ -185,6 +185,19 @@ oa_whisper_weights * oa_whisper_weights_synthesize(const oa_whisper_config * cfg
 void oa_whisper_weights_free(oa_whisper_weights * w);
 const void * oa_whisper_weights_tensor(const oa_whisper_weights * w, int layer, int kind, size_t * nbytes);
 
+/* A whisper runtime pack (.oasr v1, GGUF v2/v3): hparams whisper.decoder.{block_count,
+ * embedding_length, attention.head_count, context_length}, whisper.vocab_size and
+ * whisper.encoder.context_length (models/whisper/runtime_contract.rs:180-230);
+ * decoder tensors decoder.token_embedding.weight (Q8_0, tied output projection),
+ * decoder.positional_embedding (F32), decoder.layer_norm.{weight,bias} and per layer
+ * decoder.layers.N.{self_attn,cross_attn}.{q,k,v,out}_proj.* (k without bias),
+ * {self_attn,encoder_attn,final}_layer_norm.*, fc1.*, fc2.* (ggml_tensor_binding.rs:135-210),
+ * matrices Q8_0. Matrices stay views into the read-only mapping (released with
+ * the weights). NULL and a message in err on any missing key or tensor, wrong
+ * shape or type. */
+oa_whisper_weights * oa_whisper_weights_load_gguf(const char * path, char * err, size_t err_cap);
+void oa_whisper_weights_config(const oa_whisper_weights * w, oa_whisper_config * out);
+
 oa_whisper_model * oa_whisper_model_create(ggml_backend_t backend, const oa_whisper_weights * w);
 void oa_whisper_model_free(oa_whisper_model * m);
 

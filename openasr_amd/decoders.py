@@ -31,6 +31,10 @@ class WhisperConfig(C.Structure):
 # 448 learned positions, 1500 encoder frames
 WHISPER_TINY = dict(d_model=384, n_layers=4, n_head=6, ffn=1536, vocab=51865, max_positions=448, n_frames=1500)
 WH_LAYER_KINDS = 24
+# per-layer tensor kinds (oa_whisper_tensor_kind)
+(WH_SELF_LN_W, WH_SELF_LN_B, WH_SELF_Q, WH_SELF_Q_B, WH_SELF_K, WH_SELF_V, WH_SELF_V_B, WH_SELF_O, WH_SELF_O_B,
+ WH_CROSS_LN_W, WH_CROSS_LN_B, WH_CROSS_Q, WH_CROSS_Q_B, WH_CROSS_K, WH_CROSS_V, WH_CROSS_V_B, WH_CROSS_O,
+ WH_CROSS_O_B, WH_MLP_LN_W, WH_MLP_LN_B, WH_FC1, WH_FC1_B, WH_FC2, WH_FC2_B) = range(WH_LAYER_KINDS)
 WH_TOKEN_EMBD, WH_POS_EMBD, WH_FINAL_LN_W, WH_FINAL_LN_B = 100, 101, 102, 103
 
 # Qwen3-0.6B / 1.7B shapes (hidden, layers, heads, kv heads, head_dim, ffn, vocab)
@@ -90,6 +94,8 @@ def lib() -> C.CDLL:
     s("oa_whisper_weights_synthesize", vp, C.POINTER(WhisperConfig))
     s("oa_whisper_weights_free", None, vp)
     s("oa_whisper_weights_tensor", vp, vp, i, i, C.POINTER(C.c_size_t))
+    s("oa_whisper_weights_load_gguf", vp, C.c_char_p, C.c_char_p, C.c_size_t)
+    s("oa_whisper_weights_config", None, vp, C.POINTER(WhisperConfig))
     s("oa_whisper_model_create", vp, vp, vp)
     s("oa_whisper_model_free", None, vp)
     s("oa_whisper_session_create", vp, vp)
@@ -243,7 +249,8 @@ class QwenSession:
 
 
 class WhisperWeights:
-    """Synthesised Whisper decoder weights (host bytes, Q8_0 matrices)."""
+    """Whisper decoder weights (host bytes, Q8_0 matrices): synthesised, or
+    views into a mapped whisper runtime pack (load_gguf)."""
 
     def __init__(self, seed: int = 1234, ln_eps: float = 1e-5, **shape):
         self.cfg = WhisperConfig(shape["d_model"], shape["n_layers"], shape["n_head"], shape["ffn"], shape["vocab"],
@@ -252,12 +259,32 @@ class WhisperWeights:
         if not self.ptr:
             raise RuntimeError("whisper weight synthesis failed")
 
+    @classmethod
+    def load_gguf(cls, path) -> "WhisperWeights":
+        err = C.create_string_buffer(512)
+        ptr = lib().oa_whisper_weights_load_gguf(str(path).encode(), err, len(err))
+        if not ptr:
+            raise ValueError(f"{path}: {err.value.decode()}")
+        self = cls.__new__(cls)
+        self.ptr = ptr
+        self.cfg = WhisperConfig()
+        lib().oa_whisper_weights_config(ptr, C.byref(self.cfg))
+        return self
+
     def tensor_ptr(self, layer: int, kind: int) -> int:
         n = C.c_size_t(0)
         p = lib().oa_whisper_weights_tensor(self.ptr, layer, kind, C.byref(n))
         if not p:
             raise KeyError((layer, kind))
         return p
+
+    def array(self, layer: int, kind: int) -> np.ndarray:
+        """a copy of one tensor's host bytes (uint8)"""
+        n = C.c_size_t(0)
+        p = lib().oa_whisper_weights_tensor(self.ptr, layer, kind, C.byref(n))
+        if not p:
+            raise KeyError((layer, kind))
+        return np.ctypeslib.as_array((C.c_uint8 * n.value).from_address(p)).copy()
 
     def pointer_table(self):
         """per layer the 24 tensors in kind order, then token embedding,

@@ -17,6 +17,10 @@
 
 #include "ggml_host.h"
 #include "openasr_models.h"
+#include "pack_reader.h"
+
+using oa_pack::blob;
+using oa_pack::pack_reader;
 
 extern "C" void oa_synth_normal(uint64_t seed, uint64_t stream, int64_t first, int64_t n, float mean, float std_dev,
                                 float * out);
@@ -51,11 +55,13 @@ bool is_matrix(int kind) {
 
 struct oa_whisper_weights {
     oa_whisper_config cfg;
-    std::vector<uint8_t> tok_embd;
+    blob tok_embd;  // synthesised, or a view into a mapped runtime pack
     std::vector<float> pos_embd, final_w, final_b;
     // per layer, indexed by oa_whisper_tensor_kind
-    std::vector<std::vector<std::vector<uint8_t>>> mats;
+    std::vector<std::vector<blob>> mats;
     std::vector<std::vector<std::vector<float>>> vecs;
+    oa_gguf * src = nullptr;  // the mapped pack the views point into
+    ~oa_whisper_weights() { oa_gguf_close(src); }
 };
 
 struct oa_whisper_model {
@@ -183,7 +189,7 @@ oa_whisper_weights * oa_whisper_weights_synthesize(const oa_whisper_config * cfg
     w->pos_embd = wh_vector(c.seed, wh_stream(-1, OA_WH_POS_EMBD), (int64_t) c.max_positions * d, 0.0f, 0.02f);
     w->final_w = wh_vector(c.seed, wh_stream(-1, OA_WH_FINAL_LN_W), d, 1.0f, 0.05f);
     w->final_b = wh_vector(c.seed, wh_stream(-1, OA_WH_FINAL_LN_B), d, 0.0f, 0.02f);
-    w->mats.assign((size_t) c.n_layers, std::vector<std::vector<uint8_t>>(OA_WH_LAYER_KINDS));
+    w->mats.assign((size_t) c.n_layers, std::vector<blob>(OA_WH_LAYER_KINDS));
     w->vecs.assign((size_t) c.n_layers, std::vector<std::vector<float>>(OA_WH_LAYER_KINDS));
     for (int l = 0; l < c.n_layers; l++) {
         for (int kind = 0; kind < OA_WH_LAYER_KINDS; kind++) {
@@ -205,7 +211,7 @@ oa_whisper_weights * oa_whisper_weights_synthesize(const oa_whisper_config * cfg
 void oa_whisper_weights_free(oa_whisper_weights * w) { delete w; }
 
 const void * oa_whisper_weights_tensor(const oa_whisper_weights * w, int layer, int kind, size_t * nbytes) {
-    auto u8 = [&](const std::vector<uint8_t> & v) -> const void * {
+    auto u8 = [&](const blob & v) -> const void * {
         if (nbytes) *nbytes = v.size();
         return v.data();
     };
@@ -223,6 +229,90 @@ const void * oa_whisper_weights_tensor(const oa_whisper_weights * w, int layer, 
     if (layer < 0 || layer >= w->cfg.n_layers || kind < 0 || kind >= OA_WH_LAYER_KINDS) return nullptr;
     return is_matrix(kind) ? u8(w->mats[(size_t) layer][(size_t) kind]) : f(w->vecs[(size_t) layer][(size_t) kind]);
 }
+
+// A whisper runtime pack (.oasr v1 = GGUF): hparams under whisper.* (the
+// keys of models/whisper/runtime_contract.rs:180-230), decoder tensors under
+// the names of models/whisper/ggml_tensor_binding.rs:135-210, matrices Q8_0
+// bound as views into the mapping, vectors and the positional table copied.
+oa_whisper_weights * oa_whisper_weights_load_gguf(const char * path, char * err, size_t err_cap) {
+    auto report = [&](const std::string & msg) -> oa_whisper_weights * {
+        if (err && err_cap) std::snprintf(err, err_cap, "%s", msg.c_str());
+        return nullptr;
+    };
+    char gerr[256] = {0};
+    oa_gguf * g = oa_gguf_open(path, gerr, sizeof(gerr));
+    if (!g) return report(gerr);
+    oa_whisper_weights * w = new oa_whisper_weights;
+    w->src = g;
+    pack_reader r{g, {}};
+    auto bad = [&](const std::string & msg) {
+        delete w;
+        return report(msg);
+    };
+    if (const char * v = oa_gguf_get_str(g, "openasr.package.version"); v && std::strcmp(v, "1") != 0)
+        return bad(std::string("unsupported openasr.package.version ") + v);
+    if (const char * a = oa_gguf_get_str(g, "general.architecture"); a && std::strcmp(a, "whisper") != 0)
+        return bad(std::string("general.architecture is ") + a + ", not whisper");
+    oa_whisper_config & c = w->cfg;
+    c = oa_whisper_config{};
+    if (!r.key_i("whisper.decoder.block_count", c.n_layers) || !r.key_i("whisper.decoder.embedding_length", c.d_model) ||
+        !r.key_i("whisper.decoder.attention.head_count", c.n_head) ||
+        !r.key_i("whisper.decoder.context_length", c.max_positions) || !r.key_i("whisper.vocab_size", c.vocab) ||
+        !r.key_i("whisper.encoder.context_length", c.n_frames))
+        return bad(r.err);
+    if (c.d_model % c.n_head != 0) return bad("embedding_length is not a multiple of head_count");
+    if (c.d_model % 32 != 0) return bad("embedding_length is not a multiple of the Q8_0 block");
+    c.ln_eps = 1e-5f;
+    c.seed = 0;
+    const int64_t fi = oa_gguf_find_tensor(g, "decoder.layers.0.fc1.weight");
+    if (fi < 0) return bad("missing tensor decoder.layers.0.fc1.weight");
+    int ft = 0;
+    int64_t ne[4];
+    oa_gguf_tensor_info(g, fi, &ft, ne);
+    c.ffn = (int) ne[1];
+    const int d = c.d_model;
+    if (!r.mat("decoder.token_embedding.weight", d, c.vocab, GGML_TYPE_Q8_0, w->tok_embd) ||
+        !r.vec("decoder.positional_embedding", d, w->pos_embd, c.max_positions) ||
+        !r.vec("decoder.layer_norm.weight", d, w->final_w) || !r.vec("decoder.layer_norm.bias", d, w->final_b))
+        return bad(r.err);
+    w->mats.assign((size_t) c.n_layers, std::vector<blob>(OA_WH_LAYER_KINDS));
+    w->vecs.assign((size_t) c.n_layers, std::vector<std::vector<float>>(OA_WH_LAYER_KINDS));
+    static const struct {
+        int kind;
+        const char * name;
+    } names[] = {
+        {OA_WH_SELF_LN_W, "self_attn_layer_norm.weight"}, {OA_WH_SELF_LN_B, "self_attn_layer_norm.bias"},
+        {OA_WH_SELF_Q, "self_attn.q_proj.weight"},        {OA_WH_SELF_Q_B, "self_attn.q_proj.bias"},
+        {OA_WH_SELF_K, "self_attn.k_proj.weight"},        {OA_WH_SELF_V, "self_attn.v_proj.weight"},
+        {OA_WH_SELF_V_B, "self_attn.v_proj.bias"},        {OA_WH_SELF_O, "self_attn.out_proj.weight"},
+        {OA_WH_SELF_O_B, "self_attn.out_proj.bias"},      {OA_WH_CROSS_LN_W, "encoder_attn_layer_norm.weight"},
+        {OA_WH_CROSS_LN_B, "encoder_attn_layer_norm.bias"}, {OA_WH_CROSS_Q, "cross_attn.q_proj.weight"},
+        {OA_WH_CROSS_Q_B, "cross_attn.q_proj.bias"},      {OA_WH_CROSS_K, "cross_attn.k_proj.weight"},
+        {OA_WH_CROSS_V, "cross_attn.v_proj.weight"},      {OA_WH_CROSS_V_B, "cross_attn.v_proj.bias"},
+        {OA_WH_CROSS_O, "cross_attn.out_proj.weight"},    {OA_WH_CROSS_O_B, "cross_attn.out_proj.bias"},
+        {OA_WH_MLP_LN_W, "final_layer_norm.weight"},      {OA_WH_MLP_LN_B, "final_layer_norm.bias"},
+        {OA_WH_FC1, "fc1.weight"},                        {OA_WH_FC1_B, "fc1.bias"},
+        {OA_WH_FC2, "fc2.weight"},                        {OA_WH_FC2_B, "fc2.bias"},
+    };
+    for (int l = 0; l < c.n_layers; l++) {
+        const std::string p = "decoder.layers." + std::to_string(l) + ".";
+        for (const auto & n : names) {
+            const int kind = n.kind;
+            bool ok;
+            if (is_matrix(kind)) {
+                const int64_t rows = kind == OA_WH_FC1 ? c.ffn : d;
+                const int64_t k = kind == OA_WH_FC2 ? c.ffn : d;
+                ok = r.mat(p + n.name, k, rows, GGML_TYPE_Q8_0, w->mats[(size_t) l][(size_t) kind]);
+            } else {
+                ok = r.vec(p + n.name, kind == OA_WH_FC1_B ? c.ffn : d, w->vecs[(size_t) l][(size_t) kind]);
+            }
+            if (!ok) return bad(r.err);
+        }
+    }
+    return w;
+}
+
+void oa_whisper_weights_config(const oa_whisper_weights * w, oa_whisper_config * out) { *out = w->cfg; }
 
 oa_whisper_model * oa_whisper_model_create(ggml_backend_t backend, const oa_whisper_weights * w) {
     const oa_whisper_config & c = w->cfg;

@@ -8,7 +8,10 @@ pack's alignment.
 `export_qwen_pack` writes a qwen3-asr LLM pack from decoder weights: the
 hparam keys of arch/hparams.rs:52-58 and the tensor names of
 models/qwen/decoder_contract.rs:686-705, 764-769, with the fused q|k|v
-projection split back into attn_q / attn_k / attn_v.
+projection split back into attn_q / attn_k / attn_v. `export_whisper_pack`
+writes the decoder part of a whisper pack: the keys of
+models/whisper/runtime_contract.rs:180-230 and the tensor names of
+models/whisper/ggml_tensor_binding.rs:135-210.
 """
 
 from __future__ import annotations
@@ -123,5 +126,64 @@ def export_qwen_pack(weights, path, with_output: bool = False, extra_kv: dict | 
         w.add_tensor(p + "ffn_gate.weight", wt, (c.d_model, c.ffn), weights.array(layer, D.GATE))
         w.add_tensor(p + "ffn_up.weight", wt, (c.d_model, c.ffn), weights.array(layer, D.UP))
         w.add_tensor(p + "ffn_down.weight", wt, (c.ffn, c.d_model), weights.array(layer, D.DOWN))
+    w.write(path)
+    return Path(path)
+
+
+# per-layer whisper decoder tensors: (kind in openasr_amd.decoders, name after "decoder.layers.N.")
+WHISPER_LAYER_NAMES = [
+    ("WH_SELF_LN_W", "self_attn_layer_norm.weight"), ("WH_SELF_LN_B", "self_attn_layer_norm.bias"),
+    ("WH_SELF_Q", "self_attn.q_proj.weight"), ("WH_SELF_Q_B", "self_attn.q_proj.bias"),
+    ("WH_SELF_K", "self_attn.k_proj.weight"), ("WH_SELF_V", "self_attn.v_proj.weight"),
+    ("WH_SELF_V_B", "self_attn.v_proj.bias"), ("WH_SELF_O", "self_attn.out_proj.weight"),
+    ("WH_SELF_O_B", "self_attn.out_proj.bias"), ("WH_CROSS_LN_W", "encoder_attn_layer_norm.weight"),
+    ("WH_CROSS_LN_B", "encoder_attn_layer_norm.bias"), ("WH_CROSS_Q", "cross_attn.q_proj.weight"),
+    ("WH_CROSS_Q_B", "cross_attn.q_proj.bias"), ("WH_CROSS_K", "cross_attn.k_proj.weight"),
+    ("WH_CROSS_V", "cross_attn.v_proj.weight"), ("WH_CROSS_V_B", "cross_attn.v_proj.bias"),
+    ("WH_CROSS_O", "cross_attn.out_proj.weight"), ("WH_CROSS_O_B", "cross_attn.out_proj.bias"),
+    ("WH_MLP_LN_W", "final_layer_norm.weight"), ("WH_MLP_LN_B", "final_layer_norm.bias"),
+    ("WH_FC1", "fc1.weight"), ("WH_FC1_B", "fc1.bias"), ("WH_FC2", "fc2.weight"), ("WH_FC2_B", "fc2.bias"),
+]
+
+
+def export_whisper_pack(weights, path, extra_kv: dict | None = None, alignment: int = 32, skip: tuple = ()) -> Path:
+    """Write `weights` (openasr_amd.decoders.WhisperWeights) as a whisper pack
+    (decoder tensors; the encoder's are not part of the decode path). `skip`:
+    tensor names left out (tests of the loader's checks)."""
+    from . import decoders as D
+
+    c = weights.cfg
+    w = GGUFWriter(alignment)
+    w.add("general.architecture", STR, "whisper")
+    w.add("openasr.package.version", STR, "1")
+    for key, val in (("whisper.decoder.block_count", c.n_layers), ("whisper.decoder.embedding_length", c.d_model),
+                     ("whisper.decoder.attention.head_count", c.n_head),
+                     ("whisper.decoder.context_length", c.max_positions), ("whisper.vocab_size", c.vocab),
+                     ("whisper.encoder.context_length", c.n_frames)):
+        w.add(key, U32, val)
+    for key, (vtype, val) in (extra_kv or {}).items():
+        w.add(key, vtype, val)
+    Q8_0 = 8
+    d = c.d_model
+
+    def put(name, gtype, ne, data):
+        if name not in skip:
+            w.add_tensor(name, gtype, ne, data)
+
+    put("decoder.token_embedding.weight", Q8_0, (d, c.vocab), weights.array(-1, D.WH_TOKEN_EMBD))
+    put("decoder.positional_embedding", 0, (d, c.max_positions), weights.array(-1, D.WH_POS_EMBD))
+    put("decoder.layer_norm.weight", 0, (d,), weights.array(-1, D.WH_FINAL_LN_W))
+    put("decoder.layer_norm.bias", 0, (d,), weights.array(-1, D.WH_FINAL_LN_B))
+    for layer in range(c.n_layers):
+        for kind_name, name in WHISPER_LAYER_NAMES:
+            kind = getattr(D, kind_name)
+            data = weights.array(layer, kind)
+            if name.endswith(".bias") or "layer_norm" in name:
+                ne = (c.ffn if kind == D.WH_FC1_B else d,)
+                gtype = 0
+            else:
+                ne = (c.ffn if kind == D.WH_FC2 else d, c.ffn if kind == D.WH_FC1 else d)
+                gtype = Q8_0
+            put(f"decoder.layers.{layer}.{name}", gtype, ne, data)
     w.write(path)
     return Path(path)

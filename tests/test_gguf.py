@@ -258,3 +258,57 @@ def test_qwen_pack_errors(tmp_path, case, needle):
     wr.write(tmp_path / "bad.oasr")
     with pytest.raises(ValueError, match=needle):
         D.QwenWeights.load_gguf(tmp_path / "bad.oasr")
+
+
+WH_SHAPE = dict(d_model=64, n_layers=2, n_head=2, ffn=128, vocab=96, max_positions=16, n_frames=12)
+
+
+def test_whisper_pack_round_trip(tmp_path):
+    w = D.WhisperWeights(seed=7, **WH_SHAPE)
+    path = gguf.export_whisper_pack(w, tmp_path / "wh.oasr")
+    w2 = D.WhisperWeights.load_gguf(path)
+    for f, _ in D.WhisperConfig._fields_:
+        if f != "seed":
+            assert getattr(w2.cfg, f) == pytest.approx(getattr(w.cfg, f)), f
+    for layer in range(WH_SHAPE["n_layers"]):
+        for k in range(D.WH_LAYER_KINDS):
+            assert np.array_equal(w.array(layer, k), w2.array(layer, k)), (layer, k)
+    for k in (D.WH_TOKEN_EMBD, D.WH_POS_EMBD, D.WH_FINAL_LN_W, D.WH_FINAL_LN_B):
+        assert np.array_equal(w.array(-1, k), w2.array(-1, k)), k
+    w2.free()
+    w.free()
+
+
+@pytest.mark.parametrize("case,needle", [
+    ("missing_tensor", "missing tensor decoder.layers.1.cross_attn.v_proj.bias"),
+    ("missing_key", "whisper.encoder.context_length"),
+    ("wrong_arch", "not whisper"),
+    ("wrong_type", "decoder.layers.0.fc1.weight has unsupported type"),
+])
+def test_whisper_pack_errors(tmp_path, case, needle):
+    w = D.WhisperWeights(seed=7, **WH_SHAPE)
+    path = gguf.export_whisper_pack(w, tmp_path / "ok.oasr")
+    g, _ = open_pack(path)
+    L = D.lib()
+    wr = gguf.GGUFWriter()
+    wr.add("general.architecture", gguf.STR, "qwen3-asr" if case == "wrong_arch" else "whisper")
+    for key in ("whisper.decoder.block_count", "whisper.decoder.embedding_length", "whisper.decoder.attention.head_count",
+                "whisper.decoder.context_length", "whisper.vocab_size", "whisper.encoder.context_length"):
+        if case == "missing_key" and key == "whisper.encoder.context_length":
+            continue
+        iv = C.c_int64(0)
+        L.oa_gguf_get_i64(g, key.encode(), C.byref(iv))
+        wr.add(key, gguf.U32, iv.value)
+    for i in range(L.oa_gguf_n_tensors(g)):
+        n = L.oa_gguf_tensor_name(g, i).decode()
+        if case == "missing_tensor" and n == "decoder.layers.1.cross_attn.v_proj.bias":
+            continue
+        t, ne, data = tensor(g, n)
+        if case == "wrong_type" and n == "decoder.layers.0.fc1.weight":
+            t, data = G.F32, np.zeros(int(np.prod(ne)), np.float32)
+        wr.add_tensor(n, t, tuple(ne), data)
+    L.oa_gguf_close(g)
+    wr.write(tmp_path / "bad.oasr")
+    with pytest.raises(ValueError, match=needle):
+        D.WhisperWeights.load_gguf(tmp_path / "bad.oasr")
+    w.free()

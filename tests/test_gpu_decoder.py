@@ -156,6 +156,43 @@ def test_whisper_tiny_q8_0_first_64_steps(gpu, ref):
     w.free()
 
 
+def test_whisper_runtime_pack_decodes_like_synthesized(gpu, tmp_path):
+    """Whisper-tiny weights written as a whisper runtime pack and bound from
+    the mapping: cross K/V and 32 greedy steps (tokens and logits) bit for
+    bit equal to the same weights uploaded from host arrays"""
+    from openasr_amd import gguf
+    print("whisper-tiny runtime pack", flush=True)
+    shape = D.WHISPER_TINY
+    w = D.WhisperWeights(seed=4321, **shape)
+    path = gguf.export_whisper_pack(w, tmp_path / "whisper-tiny.oasr")
+    wp = D.WhisperWeights.load_gguf(path)
+    assert (wp.cfg.d_model, wp.cfg.n_layers, wp.cfg.ffn, wp.cfg.vocab) == (w.cfg.d_model, w.cfg.n_layers, w.cfg.ffn,
+                                                                           w.cfg.vocab)
+    enc, prompt = D.whisper_inputs(shape, n_prompt=4, seed=91)
+    runs = []
+    for weights in (w, wp):
+        model = D.WhisperModel(weights, gpu.backend)
+        sess = model.session()
+        sess.set_encoder(enc)
+        cross = [sess.read_cross(layer) for layer in range(shape["n_layers"])]
+        toks, logits = [], []
+        tok = None
+        for t in list(prompt) + [None] * 32:
+            tok, lg = sess.step(int(t) if t is not None else tok, want_logits=True)
+            toks.append(tok)
+            logits.append(lg)
+        runs.append((cross, toks, np.stack(logits)))
+        sess.free()
+        model.free()
+    (c0, t0, l0), (c1, t1, l1) = runs
+    for (k0, v0), (k1, v1) in zip(c0, c1):
+        assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+    assert t0 == t1
+    assert np.array_equal(l0.view(np.int32), l1.view(np.int32))
+    wp.free()
+    w.free()
+
+
 def test_qwen3_17b_q4_K_batch8_long_context(gpu, ref):
     """Qwen3-1.7B-shaped Q4_K decoder at batch 8, 4096-position KV cache per
     sequence, 3000-position N(0,1) prefixes plus 8 prompt tokens.
