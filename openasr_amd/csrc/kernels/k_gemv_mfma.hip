@@ -718,6 +718,121 @@ __global__ __launch_bounds__(512) void k_gemv_stream(gemv_args a) {
     }
 }
 
+// Single-column form (batch 1, Q8_0 weights). At N = 1 the MFMA tile spends
+// 15 of its 16 columns on padding and a short matrix gives few workgroups.
+// Here a wave owns one weight row and walks K 1024 elements a pass: lane l
+// takes 16 quants (half a block) against the column's 16 activation quants
+// with four v_dot4_i32_i8, the two halves of a block add exactly (DPP), the
+// even lane adds the block term isum * (d_w * d_a) -- exact in f64, one fused
+// multiply-add -- to its f64 partial, and the row is the f64 sum of the
+// partials (the CPU reference sums the same exact terms wide, so any order
+// gives its bits). Workgroups of WV waves of R rows each; with a norm or
+// quantize in front each workgroup stages the column itself, its weight
+// pieces already requested.
+constexpr int kG1Waves = 4;
+constexpr int kG1MaxPasses = 8;  // K <= 8192
+
+template <int PRO, int WV, int R>
+__global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
+    extern __shared__ __align__(16) char smem[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row0 = ((int64_t) blockIdx.x * WV + wave) * R;  // this wave's R rows
+    const bool wave_ok = row0 < a.M;                                 // uniform per wave
+    const int64_t K = a.K;
+    const int passes = (int) ((K + 1023) / 1024);
+    uint4 wq[R][kG1MaxPasses], wq2[R][kG1MaxPasses];
+    uint16_t ws[R][kG1MaxPasses], ws2[R][kG1MaxPasses];
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const int64_t rr = row0 + j < a.M ? row0 + j : 0;  // clamped, never stored
+        const char * wrow = a.W + rr * a.row_bytes;
+        const char * wrow2 = a.W2 ? a.W2 + rr * a.row_bytes : nullptr;
+#pragma unroll
+        for (int p = 0; p < kG1MaxPasses; p++) {
+            if (p < passes) {
+                const int64_t e = (int64_t) p * 1024 + 16 * lane;
+                const int64_t ec = e < K ? e : 0;  // clamped, masked below
+                wq[j][p] = *(const uint4 *) (wrow + ec);
+                ws[j][p] = ((const uint16_t *) (wrow + K))[ec / 32];
+                if (wrow2) {
+                    wq2[j][p] = *(const uint4 *) (wrow2 + ec);
+                    ws2[j][p] = ((const uint16_t *) (wrow2 + K))[ec / 32];
+                }
+            }
+        }
+    }
+    float res[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        res[j] = 0.0f;
+        if (a.res && lane == 0) res[j] = *(const float *) (a.res + (row0 + j < a.M ? row0 + j : 0) * 4);
+    }
+    const int8_t * aq;
+    const float * adp;
+    if constexpr (PRO != kProNone) {
+        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q8_0>(a, 0, 1, smem);
+        else gemv_stage_norm<GGML_TYPE_Q8_0, PRO == kProNormBias>(a, 0, 1, smem);
+        const gemv_lds L = gemv_lds_layout(GGML_TYPE_Q8_0, K, 1);
+        aq = (const int8_t *) (smem + L.q_off);
+        adp = (const float *) (smem + L.d_off);
+    } else {
+        aq = a.aq;
+        adp = a.ad;
+    }
+    if (!wave_ok) return;  // after the prologue's barriers
+    double acc[R], acc2[R];
+#pragma unroll
+    for (int j = 0; j < R; j++) acc[j] = acc2[j] = 0.0;
+#pragma unroll
+    for (int p = 0; p < kG1MaxPasses; p++) {
+        if (p < passes) {
+            const int64_t e = (int64_t) p * 1024 + 16 * lane;
+            const bool ok = e < K;
+            const int64_t ec = ok ? e : 0;
+            const uint4 av = *(const uint4 *) (aq + ec);
+            const float da = adp[ec / 32];
+            auto term = [&](const uint4 & w, uint16_t sc, double & s) {
+                int h = dot4_i8((int) w.x, (int) av.x, 0);
+                h = dot4_i8((int) w.y, (int) av.y, h);
+                h = dot4_i8((int) w.z, (int) av.z, h);
+                h = dot4_i8((int) w.w, (int) av.w, h);
+                h = ok ? h : 0;
+                const int isum = h + dpp_i<kDppXor1>(h);  // the block's two halves, exact
+                // |isum| < 2^19 and d_w * d_a has 22 significant bits: the product is exact
+                if ((lane & 1) == 0 && ok) s = fma((double) isum, (double) (half_bits_to_float(sc) * da), s);
+            };
+#pragma unroll
+            for (int j = 0; j < R; j++) {
+                term(wq[j][p], ws[j][p], acc[j]);
+                if (a.W2) term(wq2[j][p], ws2[j][p], acc2[j]);
+            }
+        }
+    }
+    auto wave_total = [&](double v) {
+        v = row16_sum(v);
+        double t = 0.0;
+#pragma unroll
+        for (int q = 0; q < 4; q++)
+            t += __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), 16 * q),
+                                  __builtin_amdgcn_readlane(__double2loint(v), 16 * q));
+        return t;
+    };
+#pragma unroll
+    for (int j = 0; j < R; j++) {
+        const double sum = wave_total(acc[j]);
+        const double sum2 = a.W2 ? wave_total(acc2[j]) : 0.0;
+        if (lane == 0 && row0 + j < a.M) {
+            float v = (float) sum;
+            if (a.W2) {
+                const float u = (float) sum2;
+                v = (v / (1.0f + expf_det(-v))) * u;
+            }
+            if (a.res) v = res[j] + v;
+            *(float *) (a.dst + (row0 + j) * 4) = v;
+        }
+    }
+}
+
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K) {
     if (M % 16 != 0) return false;
     if (wtype == GGML_TYPE_Q4_K) return K % 256 == 0;
@@ -839,6 +954,32 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
     const int mode = !pro ? kProNone : pro->norm < 0 ? kProQuant : pro->b ? kProNormBias : kProNorm;
     if (pro) a.pro = *pro;
     a.cw = 16;
+    if (wtype == GGML_TYPE_Q8_0 && N == 1 && K <= 1024LL * kG1MaxPasses &&
+        (mode != kProNorm && mode != kProNormBias ? true : (K + 255) / 256 <= 4LL * kG1Waves * kNormGroups) &&
+        !gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu)) {
+        // one column: v_dot4 on the VALU, a wave per row (two for tall
+        // matrices with a prologue: fewer workgroups repeat the staging)
+        const bool tall = mode != kProNone && M >= 2048;
+        const int rows_wg = kG1Waves * (tall ? 2 : 1);
+        const dim3 grid((unsigned) ((M + rows_wg - 1) / rows_wg)), block(64 * kG1Waves);
+        const size_t lds = mode == kProNone ? 0 : (size_t) gemv_lds_layout(wtype, K, 1).total;
+        auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, lds, stream, a); };
+        if (tall) {
+            switch (mode) {
+                case kProQuant: go(k_gemv1_q8_0<kProQuant, kG1Waves, 2>); break;
+                case kProNorm: go(k_gemv1_q8_0<kProNorm, kG1Waves, 2>); break;
+                default: go(k_gemv1_q8_0<kProNormBias, kG1Waves, 2>); break;
+            }
+        } else {
+            switch (mode) {
+                case kProNone: go(k_gemv1_q8_0<kProNone, kG1Waves, 1>); break;
+                case kProQuant: go(k_gemv1_q8_0<kProQuant, kG1Waves, 1>); break;
+                case kProNorm: go(k_gemv1_q8_0<kProNorm, kG1Waves, 1>); break;
+                default: go(k_gemv1_q8_0<kProNormBias, kG1Waves, 1>); break;
+            }
+        }
+        return;
+    }
     if (gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu)) {
         // tall matrix: a persistent grid of kStreamWgPerCu workgroups per CU walks the tiles
         const int64_t units = gemv_units(wtype, K);
