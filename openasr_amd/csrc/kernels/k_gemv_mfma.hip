@@ -848,7 +848,7 @@ int64_t gemv_units(int wtype, int64_t K) { return wtype == GGML_TYPE_Q4_K ? K / 
 // most 8 full units a row (the LDS of two batches stays within 64 KB), and enough
 // tiles that every CU walks several batches
 bool gemv_stream_eligible(int wtype, int64_t M, int64_t K, int mode, bool dual, bool res, int n_cu) {
-    if (mode != kProNone || dual || res || n_cu <= 0) return false;
+    if (mode != kProNone || dual || res || n_cu <= 0 || M % 16 != 0) return false;
     if (wtype == GGML_TYPE_Q8_0 && (K / 32) % kQ8Group != 0) return false;
     const int64_t units = gemv_units(wtype, K);
     return units >= 1 && units <= 8 && M / 16 >= 8LL * n_cu;
@@ -978,6 +978,10 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
                 default: go(k_gemv1_q8_0<kProNormBias, kG1Waves, 1>); break;
             }
         }
+        return;
+    }
+    if (M % 16 != 0) {  // the tile forms need whole 16-row tiles (gemv_mfma_supported)
+        note_hip_error(hipErrorInvalidValue);
         return;
     }
     if (gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu)) {

@@ -50,6 +50,8 @@ MM_CASES = [
     ("q4_K", 1024, 3072), ("q4_K", 4096, 2048), ("q4_K", 2048, 6144),
     # M not a multiple of the tile GEMM's 64 rows (its last row tile has idle waves)
     ("q4_K", 1040, 512), ("q8_0", 1040, 384),
+    # rows off the 16-row tile (a vocabulary of 51865: the single-column form at N = 1)
+    ("q8_0", 1000, 384),
 ]
 
 
