@@ -959,7 +959,7 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
         !gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu)) {
         // one column: v_dot4 on the VALU, a wave per row (two for tall
         // matrices with a prologue: fewer workgroups repeat the staging)
-        const bool tall = mode != kProNone && M >= 2048;
+        const bool tall = mode != kProNone && M >= 2048 && !W2;  // a SwiGLU pair already has two rows a wave
         const int rows_wg = kG1Waves * (tall ? 2 : 1);
         const dim3 grid((unsigned) ((M + rows_wg - 1) / rows_wg)), block(64 * kG1Waves);
         const size_t lds = mode == kProNone ? 0 : (size_t) gemv_lds_layout(wtype, K, 1).total;
