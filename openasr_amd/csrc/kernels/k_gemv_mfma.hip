@@ -59,6 +59,7 @@ struct gemv_args {
     const char * res;  // optional residual, same layout as dst
     int64_t res_nb1;
     gemv_prologue pro;
+    gemv_epilogue epi;  // single-column form only
 };
 
 // prologue modes (template parameter)
@@ -761,11 +762,13 @@ __global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
             }
         }
     }
-    float res[R];
+    float res[R], res2[R];
 #pragma unroll
     for (int j = 0; j < R; j++) {
-        res[j] = 0.0f;
-        if (a.res && lane == 0) res[j] = *(const float *) (a.res + (row0 + j < a.M ? row0 + j : 0) * 4);
+        const int64_t rr = row0 + j < a.M ? row0 + j : 0;
+        res[j] = res2[j] = 0.0f;
+        if (a.res && lane == 0) res[j] = *(const float *) (a.res + rr * 4);
+        if (a.epi.res2 && lane == 0) res2[j] = *(const float *) (a.epi.res2 + rr * 4);
     }
     const int8_t * aq;
     const float * adp;
@@ -828,9 +831,16 @@ __global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
                 v = (v / (1.0f + expf_det(-v))) * u;
             }
             if (a.res) v = res[j] + v;
+            if (a.epi.res2) v = res2[j] + v;
+            if (a.epi.gelu) v = half_bits_to_float(a.epi.gelu[float_to_half_bits(v)]);
             *(float *) (a.dst + (row0 + j) * 4) = v;
         }
     }
+}
+
+bool gemv_single_column(int wtype, int64_t K, int64_t N, bool norm) {
+    if (wtype != GGML_TYPE_Q8_0 || N != 1 || K % 32 != 0 || K > 1024LL * kG1MaxPasses) return false;
+    return !norm || (K + 255) / 256 <= 4LL * kG1Waves * kNormGroups;  // one staging group a wave
 }
 
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K) {
@@ -936,7 +946,7 @@ bool gemv_prologue_supported(int wtype, int64_t M, int64_t K, int64_t N, bool no
 
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const char * res,
-                      int64_t res_nb1, const char * W2, const gemv_prologue * pro) {
+                      int64_t res_nb1, const char * W2, const gemv_prologue * pro, const gemv_epilogue & epi) {
     gemv_args a;
     a.W = W;
     a.W2 = W2;
@@ -951,12 +961,17 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
     a.dst_nb1 = dst_nb1;
     a.res = res;
     a.res_nb1 = res_nb1;
+    a.epi = epi;
     const int mode = !pro ? kProNone : pro->norm < 0 ? kProQuant : pro->b ? kProNormBias : kProNorm;
     if (pro) a.pro = *pro;
     a.cw = 16;
-    if (wtype == GGML_TYPE_Q8_0 && N == 1 && K <= 1024LL * kG1MaxPasses &&
-        (mode != kProNorm && mode != kProNormBias ? true : (K + 255) / 256 <= 4LL * kG1Waves * kNormGroups) &&
-        !gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu)) {
+    const bool single = gemv_single_column(wtype, K, N, mode == kProNorm || mode == kProNormBias) &&
+                        !gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu);
+    if ((epi.res2 || epi.gelu) && !single) {  // only the single-column form has these epilogues
+        note_hip_error(hipErrorInvalidValue);
+        return;
+    }
+    if (single) {
         // one column: v_dot4 on the VALU, a wave per row (two for tall
         // matrices with a prologue: fewer workgroups repeat the staging)
         const bool tall = mode != kProNone && M >= 2048 && !W2;  // a SwiGLU pair already has two rows a wave

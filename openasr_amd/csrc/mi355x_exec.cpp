@@ -421,6 +421,33 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 produced = add;
             }
         }
+        // one column of Q8_0 weights: a second ADD (bias, then residual) or a
+        // GELU after the first also folds into the single-column epilogue
+        gemv_epilogue epi;
+        if (res && mfma && gemv_single_column(wtype, K, N, has_pro && pro.norm >= 0)) {
+            const ggml_tensor * nx = sole_consumer(produced, i + 1);
+            if (nx && nx->op == GGML_OP_ADD && nx->type == GGML_TYPE_F32 && is_contiguous(nx)) {
+                const ggml_tensor * o = nx->src[0] == produced ? nx->src[1] : nx->src[0];
+                bool same = o != produced && o->type == GGML_TYPE_F32 && o->nb[0] == 4 && columns_foldable(o);
+                for (int d = 0; d < 4 && same; d++) same = o->ne[d] == t->ne[d] && nx->ne[d] == t->ne[d];
+                if (same && ready_before(o, i)) {
+                    epi.res2 = (const char *) o->data;
+                    dst = (char *) nx->data;
+                    deferred[nx] = nx;
+                    produced = nx;
+                }
+            } else if (nx && nx->op == GGML_OP_UNARY && nx->op_params[0] == GGML_UNARY_OP_GELU &&
+                       nx->src[0] == produced && nx->type == GGML_TYPE_F32 && is_contiguous(nx)) {
+                bool same = true;
+                for (int d = 0; d < 4 && same; d++) same = nx->ne[d] == t->ne[d];
+                if (same) {
+                    epi.gelu = be->dev->gelu_table;
+                    dst = (char *) nx->data;
+                    deferred[nx] = nx;
+                    produced = nx;
+                }
+            }
+        }
         if (!reuse && !has_pro) {
             add_step(
                 [=](hipStream_t s) {
@@ -435,7 +462,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
                 else if (mfma)
                     launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1, W2,
-                                     has_pro ? &pro : nullptr);
+                                     has_pro ? &pro : nullptr, epi);
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
             produced, W2 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")

@@ -44,10 +44,23 @@ struct gemv_prologue {
 bool gemv_mfma_supported(int wtype, int64_t M, int64_t K);
 // whether a launch of this shape can take the activation prologue
 bool gemv_prologue_supported(int wtype, int64_t M, int64_t K, int64_t N, bool norm);
+// Further epilogue of a one-column Q8_0 launch (the single-column form),
+// after the residual: a second addend of the output's shape (the bias, then
+// the residual: two roundings as the unfused ADDs), or GELU through ggml's f16
+// table.
+// the single-column form takes a launch of one column of Q8_0 weights (K
+// within its passes; with a normalising prologue, K within its waves' groups)
+bool gemv_single_column(int wtype, int64_t K, int64_t N, bool norm);
+
+struct gemv_epilogue {
+    const char * res2 = nullptr;
+    const uint16_t * gelu = nullptr;
+};
+
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu,
                       const char * res = nullptr, int64_t res_nb1 = 0, const char * W2 = nullptr,
-                      const gemv_prologue * pro = nullptr);
+                      const gemv_prologue * pro = nullptr, const gemv_epilogue & epi = gemv_epilogue());
 
 // MFMA int8 GEMM for wider N (prefill)
 bool mmq_supported(int wtype, int64_t M, int64_t K);

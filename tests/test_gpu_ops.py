@@ -341,6 +341,49 @@ def test_rope_neox_positions(ggml, gpu, ref):
     G.free()
 
 
+@pytest.mark.parametrize("d,k,ffn", [(384, 384, 1536), (1024, 2048, 1024)])
+def test_single_column_epilogues(ggml, gpu, ref, d, k, ffn):
+    """batch-1 Q8_0 MUL_MATs with their biases and activations folded into the
+    single-column epilogue: LayerNorm(x)·w + b -> MUL_MAT + bias -> GELU, and
+    MUL_MAT + bias + residual (two ADDs); bit-exact, no ADD or GELU launches"""
+    print(f"single-column epilogues d={d} k={k} ffn={ffn}", flush=True)
+    x = (RNG.standard_normal((1, k)) * 1.5).astype(np.float32)
+    wn = RNG.standard_normal(k).astype(np.float32)
+    bn = RNG.standard_normal(k).astype(np.float32) * 0.1
+    b1 = RNG.standard_normal(ffn).astype(np.float32) * 0.1
+    b2 = RNG.standard_normal(d).astype(np.float32) * 0.1
+    r = RNG.standard_normal((1, d)).astype(np.float32)
+    a = RNG.standard_normal((1, k)).astype(np.float32)
+    w1 = ggml.quantize(ggml.Q8_0, ggml.synth_normal(31, ffn + k, ffn * k, 0.0, 0.02).reshape(ffn, k))
+    w2 = ggml.quantize(ggml.Q8_0, ggml.synth_normal(32, d + k, d * k, 0.0, 0.02).reshape(d, k))
+    G = ggml.Graph()
+    X = G.new(ggml.F32, k, 1)
+    A = G.new(ggml.F32, k, 1)
+    R = G.new(ggml.F32, d, 1)
+    WN = G.new(ggml.F32, k, weight=True)
+    BN = G.new(ggml.F32, k, weight=True)
+    B1 = G.new(ggml.F32, ffn, weight=True)
+    B2 = G.new(ggml.F32, d, weight=True)
+    W1 = G.new(ggml.Q8_0, k, ffn, weight=True)
+    W2 = G.new(ggml.Q8_0, k, d, weight=True)
+    h = G.lib.ggml_add(G.ctx, G.lib.ggml_mul(G.ctx, G.lib.ggml_norm(G.ctx, X, 1e-5), WN), BN)
+    Y = G.lib.ggml_gelu(G.ctx, G.lib.ggml_add(G.ctx, G.lib.ggml_mul_mat(G.ctx, W1, h), B1))
+    Z = G.lib.ggml_add(G.ctx, G.lib.ggml_add(G.ctx, G.lib.ggml_mul_mat(G.ctx, W2, A), B2), R)
+    G.build(Y, Z)
+    G.allocate(gpu.buft)
+    for T, v in ((X, x), (A, a), (R, r), (WN, wn), (BN, bn), (B1, b1), (B2, b2), (W1, w1), (W2, w2)):
+        G.set(T, v)
+    assert G.compute(gpu.backend) == 0
+    hn = ref.norm(x, 1e-5) * wn + bn
+    want_y = ref.gelu(ref.mul_mat(ggml.Q8_0, w1, ffn, k, hn) + b1)
+    want_z = (ref.mul_mat(ggml.Q8_0, w2, d, k, a) + b2) + r
+    assert_same_bits(G.get(Y).reshape(1, ffn), want_y)
+    assert_same_bits(G.get(Z).reshape(1, d), want_z)
+    labels = [lab.split(":")[0] for lab, _ in gpu.profile(G.gf, 1)]
+    assert "binary" not in labels and "unary" not in labels, labels
+    G.free()
+
+
 def test_silu_mul_and_gelu(ggml, gpu, ref):
     g = RNG.standard_normal((4, 3072)).astype(np.float32) * 3
     u = RNG.standard_normal((4, 3072)).astype(np.float32)
