@@ -132,6 +132,7 @@ struct mmq_w8 {
 };
 
 __device__ __forceinline__ void mmq_w_load(const mmq_args & a, const char * wrow, int64_t ks, int g, mmq_w4 & w) {
+    (void) a;
     const char * blk = wrow + ks * 144;
     w.hdr = *(const uint4 *) blk;
 #pragma unroll
@@ -151,6 +152,7 @@ __device__ __forceinline__ void mmq_w_load(const mmq_args & a, const char * wrow
 
 __device__ __forceinline__ void mmq_compute(const mmq_args & a, const mmq_slice & S, const mmq_w4 & w, int64_t ks,
                                             int r, int g, double (&acc)[4][4]) {
+    (void) a;
     (void) ks;
 #pragma unroll
     for (int grp = 0; grp < 4; grp++) {
