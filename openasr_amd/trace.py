@@ -61,8 +61,17 @@ def table(trace: str, which: int, workload: str, tail: bool = False) -> str:
             gemv_n += len(v)
         lines.append(f"| {k[0]} | {k[1]} | {k[2]} | {len(v) / n:.0f} | {sum(v) / len(v) / 1e3:.2f} | "
                      f"{min(v) / 1e3:.2f} | {sum(v) / n / 1e3:.1f} |")
-    wl = D.WORKLOADS[workload]
-    alg, _ = gemv_algorithmic_bytes(wl.shape, wl.wtype == g.Q4_K, wl.n_seq)
+    if workload == "whisper-tiny-q8_0-b1":
+        # Q8_0 decoder matrices read per step: self q, k, v, o and cross q, o
+        # (the cross K/V projections run once per utterance), fc1, fc2, and
+        # the tied output projection; int8 activations in, f32 outputs out
+        sh = D.WHISPER_TINY
+        d, f, L = sh["d_model"], sh["ffn"], sh["n_layers"]
+        mats = [(d, d)] * (6 * L) + [(f, d), (d, f)] * L + [(sh["vocab"], d)]
+        alg = sum(m * k * 1.0625 + k + 4 * m for m, k in mats)
+    else:
+        wl = D.WORKLOADS[workload]
+        alg, _ = gemv_algorithmic_bytes(wl.shape, wl.wtype == g.Q4_K, wl.n_seq)
     gemv_us = gemv / n / 1e3
     span = (int(win[-1]["End_Timestamp"]) - int(win[0]["Start_Timestamp"])) / n / 1e3
     lines += ["", f"Kernel time per decode step: {tot / n / 1e3:.1f} us over {len(win) / n:.0f} launches "
@@ -76,7 +85,9 @@ def table(trace: str, which: int, workload: str, tail: bool = False) -> str:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("trace")
-    ap.add_argument("--only", default=None, help="the trace holds this one workload (bench.py --workload W --no-b1)")
+    ap.add_argument("--only", default=None,
+                    help="summarise the last steps of the trace as this workload (a WORKLOADS name, or "
+                         "whisper-tiny-q8_0-b1 for the Whisper leg that ends a bench.py run)")
     a = ap.parse_args()
     if a.only:
         print(f"## {a.only}\n")
