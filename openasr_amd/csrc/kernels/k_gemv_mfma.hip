@@ -60,6 +60,11 @@ struct gemv_args {
     int64_t res_nb1;
     gemv_prologue pro;
     gemv_epilogue epi;  // single-column form only
+    // single-column form: matrices after the first, their workgroups following
+    // the first's (sub_wg0[s] = the first workgroup of matrix s + 1)
+    int nsub;
+    gemv_sub sub[kGemvMaxSubs];
+    int64_t sub_wg0[kGemvMaxSubs];
 };
 
 // prologue modes (template parameter)
@@ -737,16 +742,27 @@ template <int PRO, int WV, int R>
 __global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
     extern __shared__ __align__(16) char smem[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t row0 = ((int64_t) blockIdx.x * WV + wave) * R;  // this wave's R rows
-    const bool wave_ok = row0 < a.M;                                 // uniform per wave
+    // which matrix of the launch this workgroup serves (constant indices:
+    // the argument block stays in scalar registers)
+    const char * Wm = a.W;
+    int64_t M = a.M, blk = blockIdx.x;
+    char * dst = a.dst;
+    const char * resp = a.res;
+    if (a.nsub > 1 && (int64_t) blockIdx.x >= a.sub_wg0[1]) {
+        Wm = a.sub[1].W, M = a.sub[1].M, dst = a.sub[1].dst, resp = a.sub[1].res, blk -= a.sub_wg0[1];
+    } else if (a.nsub > 0 && (int64_t) blockIdx.x >= a.sub_wg0[0]) {
+        Wm = a.sub[0].W, M = a.sub[0].M, dst = a.sub[0].dst, resp = a.sub[0].res, blk -= a.sub_wg0[0];
+    }
+    const int64_t row0 = (blk * WV + wave) * R;  // this wave's R rows
+    const bool wave_ok = row0 < M;                // uniform per wave
     const int64_t K = a.K;
     const int passes = (int) ((K + 1023) / 1024);
     uint4 wq[R][kG1MaxPasses], wq2[R][kG1MaxPasses];
     uint16_t ws[R][kG1MaxPasses], ws2[R][kG1MaxPasses];
 #pragma unroll
     for (int j = 0; j < R; j++) {
-        const int64_t rr = row0 + j < a.M ? row0 + j : 0;  // clamped, never stored
-        const char * wrow = a.W + rr * a.row_bytes;
+        const int64_t rr = row0 + j < M ? row0 + j : 0;  // clamped, never stored
+        const char * wrow = Wm + rr * a.row_bytes;
         const char * wrow2 = a.W2 ? a.W2 + rr * a.row_bytes : nullptr;
 #pragma unroll
         for (int p = 0; p < kG1MaxPasses; p++) {
@@ -765,9 +781,9 @@ __global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
     float res[R], res2[R];
 #pragma unroll
     for (int j = 0; j < R; j++) {
-        const int64_t rr = row0 + j < a.M ? row0 + j : 0;
+        const int64_t rr = row0 + j < M ? row0 + j : 0;
         res[j] = res2[j] = 0.0f;
-        if (a.res && lane == 0) res[j] = *(const float *) (a.res + rr * 4);
+        if (resp && lane == 0) res[j] = *(const float *) (resp + rr * 4);
         if (a.epi.res2 && lane == 0) res2[j] = *(const float *) (a.epi.res2 + rr * 4);
     }
     const int8_t * aq;
@@ -824,16 +840,16 @@ __global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
     for (int j = 0; j < R; j++) {
         const double sum = wave_total(acc[j]);
         const double sum2 = a.W2 ? wave_total(acc2[j]) : 0.0;
-        if (lane == 0 && row0 + j < a.M) {
+        if (lane == 0 && row0 + j < M) {
             float v = (float) sum;
             if (a.W2) {
                 const float u = (float) sum2;
                 v = (v / (1.0f + expf_det(-v))) * u;
             }
-            if (a.res) v = res[j] + v;
+            if (resp) v = res[j] + v;
             if (a.epi.res2) v = res2[j] + v;
             if (a.epi.gelu) v = half_bits_to_float(a.epi.gelu[float_to_half_bits(v)]);
-            *(float *) (a.dst + (row0 + j) * 4) = v;
+            *(float *) (dst + (row0 + j) * 4) = v;
         }
     }
 }
@@ -946,7 +962,8 @@ bool gemv_prologue_supported(int wtype, int64_t M, int64_t K, int64_t N, bool no
 
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const char * res,
-                      int64_t res_nb1, const char * W2, const gemv_prologue * pro, const gemv_epilogue & epi) {
+                      int64_t res_nb1, const char * W2, const gemv_prologue * pro, const gemv_epilogue & epi,
+                      const gemv_sub * subs, int nsub) {
     gemv_args a;
     a.W = W;
     a.W2 = W2;
@@ -962,21 +979,34 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
     a.res = res;
     a.res_nb1 = res_nb1;
     a.epi = epi;
+    a.nsub = 0;
     const int mode = !pro ? kProNone : pro->norm < 0 ? kProQuant : pro->b ? kProNormBias : kProNorm;
     if (pro) a.pro = *pro;
     a.cw = 16;
     const bool single = gemv_single_column(wtype, K, N, mode == kProNorm || mode == kProNormBias) &&
                         !gemv_stream_eligible(wtype, M, K, mode, W2 != nullptr, res != nullptr, n_cu);
-    if ((epi.res2 || epi.gelu) && !single) {  // only the single-column form has these epilogues
+    if ((epi.res2 || epi.gelu || nsub > 0) && !single) {  // only the single-column form has these
         note_hip_error(hipErrorInvalidValue);
         return;
     }
     if (single) {
         // one column: v_dot4 on the VALU, a wave per row (two for tall
         // matrices with a prologue: fewer workgroups repeat the staging)
-        const bool tall = mode != kProNone && M >= 2048 && !W2;  // a SwiGLU pair already has two rows a wave
+        const bool tall = mode != kProNone && M >= 2048 && !W2 && nsub == 0;  // a SwiGLU pair already has two rows a wave
         const int rows_wg = kG1Waves * (tall ? 2 : 1);
-        const dim3 grid((unsigned) ((M + rows_wg - 1) / rows_wg)), block(64 * kG1Waves);
+        int64_t wgs = (M + rows_wg - 1) / rows_wg;
+        if (nsub > kGemvMaxSubs || W2 || epi.res2 || epi.gelu) nsub = nsub > 0 ? -1 : 0;
+        if (nsub < 0) {  // further matrices only beside a plain first one
+            note_hip_error(hipErrorInvalidValue);
+            return;
+        }
+        for (int q = 0; q < nsub; q++) {
+            a.sub[q] = subs[q];
+            a.sub_wg0[q] = wgs;
+            wgs += (subs[q].M + rows_wg - 1) / rows_wg;
+        }
+        a.nsub = nsub;
+        const dim3 grid((unsigned) wgs), block(64 * kG1Waves);
         const size_t lds = mode == kProNone ? 0 : (size_t) gemv_lds_layout(wtype, K, 1).total;
         auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, block, lds, stream, a); };
         if (tall) {

@@ -448,6 +448,40 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 }
             }
         }
+        // sibling MUL_MATs of the same normalised column (Whisper's q, k, v
+        // projections, each maybe with a bias ADD) join a one-column launch,
+        // as long as nothing but they and their folded ADDs lie between
+        std::vector<gemv_sub> subs;
+        if (pn != pro_norm.end() && mfma && !W2 && !epi.res2 && !epi.gelu &&
+            gemv_single_column(wtype, K, N, pro.norm >= 0)) {
+            for (int j = i + 1; j < cg->n_nodes && (int) subs.size() < kGemvMaxSubs; j++) {
+                const ggml_tensor * u = cg->nodes[j];
+                if (is_view_op(u->op) || deferred.count(u)) continue;
+                const ggml_tensor * uw = u->src[0];
+                if (u->op != GGML_OP_MUL_MAT || u->src[1] != x || uw->type != wtype || uw->ne[0] != K ||
+                    uw->ne[2] != 1 || uw->ne[3] != 1 || u->type != GGML_TYPE_F32 || !is_contiguous(u) ||
+                    u->ne[1] * u->ne[2] * u->ne[3] != 1)
+                    break;
+                gemv_sub sb;
+                sb.W = (const char *) uw->data;
+                sb.M = uw->ne[1];
+                sb.dst = (char *) u->data;
+                if ((int64_t) uw->nb[1] != row_bytes) break;
+                deferred[u] = u;
+                const ggml_tensor * ua = sole_consumer(u, j + 1);
+                if (ua && ua->op == GGML_OP_ADD && ua->type == GGML_TYPE_F32 && is_contiguous(ua)) {
+                    const ggml_tensor * o = ua->src[0] == u ? ua->src[1] : ua->src[0];
+                    bool same = o != u && o->type == GGML_TYPE_F32 && o->nb[0] == 4 && columns_foldable(o);
+                    for (int d = 0; d < 4 && same; d++) same = o->ne[d] == u->ne[d] && ua->ne[d] == u->ne[d];
+                    if (same && ready_before(o, i)) {
+                        sb.res = (const char *) o->data;
+                        sb.dst = (char *) ua->data;
+                        deferred[ua] = ua;
+                    }
+                }
+                subs.push_back(sb);
+            }
+        }
         if (!reuse && !has_pro) {
             add_step(
                 [=](hipStream_t s) {
@@ -462,7 +496,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
                 else if (mfma)
                     launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1, W2,
-                                     has_pro ? &pro : nullptr, epi);
+                                     has_pro ? &pro : nullptr, epi, subs.data(), (int) subs.size());
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
             produced, W2 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")

@@ -57,10 +57,22 @@ struct gemv_epilogue {
     const uint16_t * gelu = nullptr;
 };
 
+// Further matrices of a one-column launch with a normalising prologue: sibling
+// MUL_MATs of the same normalised input (Whisper's q, k, v projections), each
+// with its own rows, output and optional residual (a folded bias).
+struct gemv_sub {
+    const char * W = nullptr;
+    int64_t M = 0;
+    char * dst = nullptr;
+    const char * res = nullptr;
+};
+constexpr int kGemvMaxSubs = 2;
+
 void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                       int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu,
                       const char * res = nullptr, int64_t res_nb1 = 0, const char * W2 = nullptr,
-                      const gemv_prologue * pro = nullptr, const gemv_epilogue & epi = gemv_epilogue());
+                      const gemv_prologue * pro = nullptr, const gemv_epilogue & epi = gemv_epilogue(),
+                      const gemv_sub * subs = nullptr, int nsub = 0);
 
 // MFMA int8 GEMM for wider N (prefill)
 bool mmq_supported(int wtype, int64_t M, int64_t K);

@@ -384,6 +384,39 @@ def test_single_column_epilogues(ggml, gpu, ref, d, k, ffn):
     G.free()
 
 
+def test_single_column_sibling_projections(ggml, gpu, ref):
+    """LayerNorm(x)·w + b feeding three Q8_0 MUL_MATs at batch 1 (q and v with
+    a bias ADD, k without; Whisper's self-attention projections): one launch,
+    bit-exact"""
+    d = 384
+    x = (RNG.standard_normal((1, d)) * 1.5).astype(np.float32)
+    wn = RNG.standard_normal(d).astype(np.float32)
+    bn = RNG.standard_normal(d).astype(np.float32) * 0.1
+    bq = RNG.standard_normal(d).astype(np.float32) * 0.1
+    bv = RNG.standard_normal(d).astype(np.float32) * 0.1
+    ws = [ggml.quantize(ggml.Q8_0, ggml.synth_normal(40 + i, d, d * d, 0.0, 0.02).reshape(d, d)) for i in range(3)]
+    G = ggml.Graph()
+    X = G.new(ggml.F32, d, 1)
+    WN, BN, BQ, BV = (G.new(ggml.F32, d, weight=True) for _ in range(4))
+    WQ, WK, WV = (G.new(ggml.Q8_0, d, d, weight=True) for _ in range(3))
+    h = G.lib.ggml_add(G.ctx, G.lib.ggml_mul(G.ctx, G.lib.ggml_norm(G.ctx, X, 1e-5), WN), BN)
+    Q = G.lib.ggml_add(G.ctx, G.lib.ggml_mul_mat(G.ctx, WQ, h), BQ)
+    Kt = G.lib.ggml_mul_mat(G.ctx, WK, h)
+    V = G.lib.ggml_add(G.ctx, G.lib.ggml_mul_mat(G.ctx, WV, h), BV)
+    G.build(Q, Kt, V)
+    G.allocate(gpu.buft)
+    for T, v in ((X, x), (WN, wn), (BN, bn), (BQ, bq), (BV, bv), (WQ, ws[0]), (WK, ws[1]), (WV, ws[2])):
+        G.set(T, v)
+    assert G.compute(gpu.backend) == 0
+    hn = ref.norm(x, 1e-5) * wn + bn
+    assert_same_bits(G.get(Q).reshape(1, d), ref.mul_mat(ggml.Q8_0, ws[0], d, d, hn) + bq)
+    assert_same_bits(G.get(Kt).reshape(1, d), ref.mul_mat(ggml.Q8_0, ws[1], d, d, hn))
+    assert_same_bits(G.get(V).reshape(1, d), ref.mul_mat(ggml.Q8_0, ws[2], d, d, hn) + bv)
+    labels = [lab.split(":")[0] for lab, _ in gpu.profile(G.gf, 1)]
+    assert sum(lab.startswith("mul_mat") for lab in labels) == 1 and "binary" not in labels, labels
+    G.free()
+
+
 def test_silu_mul_and_gelu(ggml, gpu, ref):
     g = RNG.standard_normal((4, 3072)).astype(np.float32) * 3
     u = RNG.standard_normal((4, 3072)).astype(np.float32)
