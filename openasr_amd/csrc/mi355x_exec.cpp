@@ -449,25 +449,45 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             }
         }
         // sibling MUL_MATs of the same normalised column (Whisper's q, k, v
-        // projections, each maybe with a bias ADD) join a one-column launch,
-        // as long as nothing but they and their folded ADDs lie between
+        // projections, each maybe with a bias ADD) join a one-column launch.
+        // A sibling's result is then written before the nodes that lie
+        // between (a few, e.g. the previous projection's reshape and copy),
+        // so none of them may read or write its bytes.
         std::vector<gemv_sub> subs;
         if (pn != pro_norm.end() && mfma && !W2 && !epi.res2 && !epi.gelu &&
             gemv_single_column(wtype, K, N, pro.norm >= 0)) {
-            for (int j = i + 1; j < cg->n_nodes && (int) subs.size() < kGemvMaxSubs; j++) {
+            std::vector<const ggml_tensor *> between;
+            auto overlaps = [](const ggml_tensor * a, const ggml_tensor * b) {
+                if (!a || !b || !a->data || !b->data) return false;
+                const uintptr_t a0 = (uintptr_t) a->data, a1 = a0 + ggml_nbytes(a);
+                const uintptr_t b0 = (uintptr_t) b->data, b1 = b0 + ggml_nbytes(b);
+                return a0 < b1 && b0 < a1;
+            };
+            auto clear_of = [&](const ggml_tensor * out) {
+                for (const ggml_tensor * n : between) {
+                    if (overlaps(n, out)) return false;
+                    for (int k = 0; k < GGML_MAX_SRC; k++)
+                        if (overlaps(n->src[k], out)) return false;
+                }
+                return true;
+            };
+            for (int j = i + 1; j < cg->n_nodes && j <= i + 16 && (int) subs.size() < kGemvMaxSubs; j++) {
                 const ggml_tensor * u = cg->nodes[j];
                 if (is_view_op(u->op) || deferred.count(u)) continue;
                 const ggml_tensor * uw = u->src[0];
-                if (u->op != GGML_OP_MUL_MAT || u->src[1] != x || uw->type != wtype || uw->ne[0] != K ||
-                    uw->ne[2] != 1 || uw->ne[3] != 1 || u->type != GGML_TYPE_F32 || !is_contiguous(u) ||
-                    u->ne[1] * u->ne[2] * u->ne[3] != 1)
-                    break;
+                const bool sibling = u->op == GGML_OP_MUL_MAT && u->src[1] == x && uw->type == wtype &&
+                                     uw->ne[0] == K && uw->ne[2] == 1 && uw->ne[3] == 1 &&
+                                     (int64_t) uw->nb[1] == row_bytes && u->type == GGML_TYPE_F32 && is_contiguous(u) &&
+                                     u->ne[1] * u->ne[2] * u->ne[3] == 1;
+                if (!sibling) {
+                    between.push_back(u);
+                    continue;
+                }
                 gemv_sub sb;
                 sb.W = (const char *) uw->data;
                 sb.M = uw->ne[1];
                 sb.dst = (char *) u->data;
-                if ((int64_t) uw->nb[1] != row_bytes) break;
-                deferred[u] = u;
+                const ggml_tensor * out = u;
                 const ggml_tensor * ua = sole_consumer(u, j + 1);
                 if (ua && ua->op == GGML_OP_ADD && ua->type == GGML_TYPE_F32 && is_contiguous(ua)) {
                     const ggml_tensor * o = ua->src[0] == u ? ua->src[1] : ua->src[0];
@@ -476,9 +496,12 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                     if (same && ready_before(o, i)) {
                         sb.res = (const char *) o->data;
                         sb.dst = (char *) ua->data;
-                        deferred[ua] = ua;
+                        out = ua;
                     }
                 }
+                if (!clear_of(out)) break;
+                deferred[u] = u;
+                if (out != u) deferred[out] = out;
                 subs.push_back(sb);
             }
         }
