@@ -98,6 +98,9 @@ struct ggml_tensor * ggml_set_rows(struct ggml_context * ctx, struct ggml_tensor
                                    struct ggml_tensor * c);
 struct ggml_tensor * ggml_argmax(struct ggml_context * ctx, struct ggml_tensor * a);
 struct ggml_tensor * ggml_argmax_first(struct ggml_context * ctx, struct ggml_tensor * a);
+/* ffi.rs:915-925 (ggml_conv_2d = im2col + mul_mat), cpu_graph.rs:5191-5246 */
+struct ggml_tensor * ggml_im2col(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int s0,
+                                 int s1, int p0, int p1, int d0, int d1, bool is_2D, enum ggml_type dst_type);
 struct ggml_tensor * ggml_soft_max(struct ggml_context * ctx, struct ggml_tensor * a);
 struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * mask,
                                        float scale, float max_bias);

@@ -1066,6 +1066,28 @@ bool planner::plan() {
                     t, "argmax");
                 break;
             }
+            case GGML_OP_IM2COL: {
+                const ggml_tensor * kr = t->src[0];
+                const tview bv = make_view(t->src[1]);
+                const bool two_d = t->op_params[6] != 0;
+                im2col_args a{};
+                a.total = t->ne[0] * t->ne[1] * t->ne[2] * t->ne[3];
+                a.K = t->ne[0], a.OW = t->ne[1];
+                a.KW = (int) kr->ne[0], a.KH = two_d ? (int) kr->ne[1] : 1;
+                a.s0 = t->op_params[0], a.s1 = t->op_params[1], a.p0 = t->op_params[2], a.p1 = t->op_params[3];
+                a.d0 = t->op_params[4], a.d1 = t->op_params[5];
+                a.IW = bv.ne[0];
+                if (two_d) {
+                    a.OH = t->ne[2], a.IH = bv.ne[1], a.nb_h = bv.nb[1], a.nb_c = bv.nb[2], a.nb_n = bv.nb[3];
+                } else {
+                    a.OH = 1, a.IH = 1, a.nb_h = 0, a.nb_c = bv.nb[1], a.nb_n = bv.nb[2];
+                }
+                void * d = t->data;
+                const int f16 = t->type == GGML_TYPE_F16;
+                const char * src = bv.data;
+                add_step([=](hipStream_t s) { launch_im2col(d, f16, src, a, s); }, t, "im2col");
+                break;
+            }
             case GGML_OP_FLASH_ATTN_EXT:
                 if (!plan_fattn(i, t)) return false;
                 continue;
@@ -1384,6 +1406,15 @@ bool supports_op(const device_state * dev, const ggml_tensor * t) {
         case GGML_OP_ARGMAX:
         case GGML_OP_ARGMAX_FIRST:
             return f32(t->src[0]) && rows_contiguous(t->src[0], 4) && t->type == GGML_TYPE_I32;
+        case GGML_OP_IM2COL: {
+            const ggml_tensor *kr = t->src[0], *b = t->src[1];
+            if (!kr || !b || !f32(b) || b->nb[0] != 4 || !is_contiguous(t)) return false;
+            if (t->type != GGML_TYPE_F16 && t->type != GGML_TYPE_F32) return false;
+            const bool two_d = t->op_params[6] != 0;
+            const int64_t K = two_d ? kr->ne[0] * kr->ne[1] * kr->ne[2] : kr->ne[0] * kr->ne[1];
+            return t->ne[0] == K && (!two_d || b->nb[1] == 4 * b->ne[0]) && t->ne[1] >= 1 &&
+                   t->op_params[0] > 0 && t->op_params[4] > 0 && (!two_d || (t->op_params[1] > 0 && t->op_params[5] > 0));
+        }
         case GGML_OP_CPY:
         case GGML_OP_CONT:
         case GGML_OP_DUP: {

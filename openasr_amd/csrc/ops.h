@@ -185,6 +185,15 @@ void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStre
 void launch_soft_max(const tview & d, const tview & a, const tview * mask, float scale, hipStream_t s);
 size_t argmax_scratch_bytes(int64_t ne0, int64_t rows);
 void launch_argmax(const tview & a, int32_t * out, int first, void * scratch, hipStream_t s);
+
+// GGML_OP_IM2COL over a contiguous result [K = IC*KH*KW, OW, OH, N] (1-D: KH =
+// OH = 1). Input element (n, ic, ih, iw) is f32 at n*nb_n + ic*nb_c + ih*nb_h +
+// 4*iw bytes.
+struct im2col_args {
+    int64_t total, K, OW, OH, IW, IH, nb_n, nb_c, nb_h;
+    int KW, KH, s0, s1, p0, p1, d0, d1;
+};
+void launch_im2col(void * dst, int dst_f16, const char * src, const im2col_args & a, hipStream_t s);
 bool norm_supported(int64_t ne0);
 // a one-wave kernel that returns after `us` microseconds of device wall clock
 void launch_spin_us(double us, int wall_clock_khz, hipStream_t s);

@@ -482,6 +482,43 @@ struct ggml_tensor * ggml_argmax_first(struct ggml_context * ctx, struct ggml_te
     return argmax_op(ctx, a, GGML_OP_ARGMAX_FIRST);
 }
 
+// Output length of a strided, padded, dilated convolution along one axis.
+static int64_t conv_out_len(int64_t in, int64_t k, int s, int p, int d) { return (in + 2 * p - d * (k - 1) - 1) / s + 1; }
+
+// Column matrix of a convolution (the first half of ggml_conv_2d / conv_1d,
+// used by nn/conv.rs:82-110 for the Qwen audio encoder's stem). `a` is the
+// kernel [KW, KH, IC, OC] (2-D) or [K, IC, OC] (1-D), read for its shape only;
+// `b` the input [IW, IH, IC, N] or [IW, IC, N]. The result row for output
+// pixel (n, oh, ow) holds IC*KH*KW taps, ic-major then kh then kw, zero where
+// the tap falls into padding. op_params = {s0, s1, p0, p1, d0, d1, is_2D}.
+struct ggml_tensor * ggml_im2col(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int s0,
+                                 int s1, int p0, int p1, int d0, int d1, bool is_2D, enum ggml_type dst_type) {
+    GB_REQUIRE(s0 > 0 && d0 > 0 && p0 >= 0 && (!is_2D || (s1 > 0 && d1 > 0 && p1 >= 0)),
+               "im2col: bad stride/padding/dilation");
+    GB_REQUIRE(dst_type == GGML_TYPE_F16 || dst_type == GGML_TYPE_F32, "im2col: result must be f16 or f32");
+    int64_t ne[4];
+    if (is_2D) {
+        GB_REQUIRE(a->ne[2] == b->ne[2], "im2col: kernel and input channel counts differ");
+        const int64_t oh = conv_out_len(b->ne[1], a->ne[1], s1, p1, d1);
+        const int64_t ow = conv_out_len(b->ne[0], a->ne[0], s0, p0, d0);
+        GB_REQUIRE(oh > 0 && ow > 0, "im2col: kernel larger than padded input");
+        ne[0] = a->ne[2] * a->ne[1] * a->ne[0], ne[1] = ow, ne[2] = oh, ne[3] = b->ne[3];
+    } else {
+        GB_REQUIRE(a->ne[1] == b->ne[1] && b->ne[3] == 1, "im2col: kernel and input channel counts differ");
+        const int64_t ow = conv_out_len(b->ne[0], a->ne[0], s0, p0, d0);
+        GB_REQUIRE(ow > 0, "im2col: kernel larger than padded input");
+        ne[0] = a->ne[1] * a->ne[0], ne[1] = ow, ne[2] = b->ne[2], ne[3] = 1;
+    }
+    ggml_tensor * r = new_tensor_impl(ctx, dst_type, 4, ne, nullptr, 0);
+    if (!r) return nullptr;
+    const int32_t params[7] = {s0, s1, p0, p1, d0, d1, is_2D ? 1 : 0};
+    set_op_params(r, params, sizeof(params));
+    r->op = GGML_OP_IM2COL;
+    r->src[0] = a;
+    r->src[1] = b;
+    return r;
+}
+
 struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * mask,
                                        float scale, float max_bias) {
     GB_REQUIRE(ggml_is_contiguous(a), "soft_max: input must be contiguous");

@@ -306,3 +306,28 @@ class WhisperRef:
                                       int(token), self.pos, logits.ctypes.data, self.fidelity, self.threads)
         self.pos += 1
         return int(top1), logits
+
+
+def im2col(x: np.ndarray, kw: int, kh: int, s0: int, s1: int, p0: int, p1: int, d0: int, d1: int,
+           is_2d: bool = True) -> np.ndarray:
+    """ggml's IM2COL (f32 columns; the f16 result is these rounded to nearest
+    even), the first half of ggml_conv_2d used by nn/conv.rs:82-110 /
+    cpu_graph.rs:5191-5246 (the ggml-cpu kernel lives in the absent
+    openasr-ggml fork; this restates ggml's published definition).
+    x: [N, IC, IH, IW] (2-D) or [N, IC, IW] (1-D). Returns [N, OH, OW, IC*KH*KW]
+    (1-D: [N, OW, IC*KW]); tap (ic, a, b) of output (oh, ow) reads input
+    (oh*s1 + a*d1 - p1, ow*s0 + b*d0 - p0), zero outside the input."""
+    if not is_2d:
+        x, kh, s1, p1, d1 = x[:, :, None, :], 1, 1, 0, 1
+    n, ic, ih, iw = x.shape
+    oh = (ih + 2 * p1 - d1 * (kh - 1) - 1) // s1 + 1
+    ow = (iw + 2 * p0 - d0 * (kw - 1) - 1) // s0 + 1
+    out = np.zeros((n, oh, ow, ic, kh, kw), np.float32)
+    for a in range(kh):
+        rows = np.arange(oh) * s1 + a * d1 - p1
+        for b in range(kw):
+            cols = np.arange(ow) * s0 + b * d0 - p0
+            inside = ((rows >= 0) & (rows < ih))[:, None] & ((cols >= 0) & (cols < iw))[None, :]
+            g = x[:, :, np.clip(rows, 0, ih - 1)][:, :, :, np.clip(cols, 0, iw - 1)]
+            out[..., a, b] = np.where(inside[None, None], g, np.float32(0)).transpose(0, 2, 3, 1)
+    return out.reshape(n, oh, ow, ic * kh * kw) if is_2d else out.reshape(n, ow, ic * kw)

@@ -544,3 +544,77 @@ def test_abort_callback_and_graph_replay(ggml, gpu, ref):
                                                      C.byref(cap))
     assert st == 0 and cap.mechanism == 1 and cap.observation_granularity == 1
     G.free()
+
+
+IM2COL_CASES = [
+    # ic, ih, iw, n, kh, kw, s0, s1, p0, p1, d0, d1, f16
+    (1, 128, 100, 1, 3, 3, 2, 2, 1, 1, 1, 1, True),  # encoder stem conv1 over a 128-bin mel chunk
+    (64, 64, 50, 1, 3, 3, 2, 2, 1, 1, 1, 1, True),  # conv2-shaped, fewer channels
+    (3, 9, 11, 2, 2, 3, 1, 2, 2, 0, 2, 1, False),  # every parameter different per axis
+]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("ic,ih,iw,n,kh,kw,s0,s1,p0,p1,d0,d1,f16", IM2COL_CASES)
+def test_im2col(ggml, gpu, ref, ic, ih, iw, n, kh, kw, s0, s1, p0, p1, d0, d1, f16):
+    x = RNG.standard_normal((n, ic, ih, iw)).astype(np.float32)
+    G = ggml.Graph()
+    Kt = G.new(ggml.F16 if f16 else ggml.F32, kw, kh, ic, 8)
+    X = G.new(ggml.F32, iw, ih, ic, n)
+    T = G.lib.ggml_im2col(G.ctx, Kt, X, s0, s1, p0, p1, d0, d1, True, ggml.F16 if f16 else ggml.F32)
+    G.build(T)
+    G.allocate(gpu.buft)
+    G.set(X, x)
+    assert G.compute(gpu.backend) == 0
+    want = ref.im2col(x, kw, kh, s0, s1, p0, p1, d0, d1)
+    if f16:
+        got = G.get(T, np.uint16).reshape(want.shape)
+        assert np.array_equal(got, want.astype(np.float16).view(np.uint16))
+    else:
+        assert np.array_equal(G.get(T).reshape(want.shape).view(np.uint32), want.view(np.uint32))
+    G.free()
+
+
+@pytest.mark.gpu
+def test_im2col_1d(ggml, gpu, ref):
+    x = RNG.standard_normal((3, 4, 50)).astype(np.float32)
+    G = ggml.Graph()
+    Kt = G.new(ggml.F16, 3, 4, 8)
+    X = G.new(ggml.F32, 50, 4, 3)
+    T = G.lib.ggml_im2col(G.ctx, Kt, X, 2, 0, 1, 0, 1, 0, False, ggml.F16)
+    G.build(T)
+    G.allocate(gpu.buft)
+    G.set(X, x)
+    assert G.compute(gpu.backend) == 0
+    want = ref.im2col(x, 3, 0, 2, 0, 1, 0, 1, 0, is_2d=False)
+    assert np.array_equal(G.get(T, np.uint16).reshape(want.shape), want.astype(np.float16).view(np.uint16))
+    G.free()
+
+
+@pytest.mark.gpu
+def test_conv_2d_f32_kernel_chain(ggml, gpu, ref):
+    """ggml_conv_2d with an f32 kernel as nn/conv.rs:82-110 builds it: IM2COL
+    -> MUL_MAT(columns, kernel rows) -> reshape/permute/cont to [OW, OH, OC, N],
+    against an f64 convolution"""
+    n, ic, ih, iw, oc = 1, 4, 30, 26, 16
+    x = RNG.standard_normal((n, ic, ih, iw)).astype(np.float32)
+    w = RNG.standard_normal((oc, ic, 3, 3)).astype(np.float32)
+    G = ggml.Graph()
+    Kt = G.new(ggml.F32, 3, 3, ic, oc)
+    X = G.new(ggml.F32, iw, ih, ic, n)
+    cols = G.lib.ggml_im2col(G.ctx, Kt, X, 2, 2, 1, 1, 1, 1, True, ggml.F32)
+    ct = ggml.tensor(cols)
+    kdim, ow, oh = ct.ne[0], ct.ne[1], ct.ne[2]
+    mm = G.lib.ggml_mul_mat(G.ctx, G.lib.ggml_reshape_2d(G.ctx, cols, kdim, ow * oh * n),
+                            G.lib.ggml_reshape_2d(G.ctx, Kt, kdim, oc))
+    y = G.lib.ggml_cont(G.ctx, G.lib.ggml_permute(G.ctx, G.lib.ggml_reshape_4d(G.ctx, mm, ow, oh, n, oc), 0, 1, 3, 2))
+    G.build(y)
+    G.allocate(gpu.buft)
+    G.set(X, x)
+    G.set(Kt, w)
+    assert G.compute(gpu.backend) == 0
+    cols_ref = ref.im2col(x, 3, 3, 2, 2, 1, 1, 1, 1).astype(np.float64)
+    want = (cols_ref @ w.reshape(oc, -1).T.astype(np.float64)).transpose(0, 3, 1, 2)  # [N, OC, OH, OW]
+    got = G.get(y).reshape(n, oc, oh, ow)
+    assert rel_err(got, want) <= 2e-3
+    G.free()
