@@ -200,6 +200,8 @@ ggml_backend_reg_t ggml_backend_dev_backend_reg(ggml_backend_dev_t dev);
 ggml_backend_t ggml_backend_dev_init(ggml_backend_dev_t dev, const char * params);
 ggml_backend_buffer_type_t ggml_backend_dev_buffer_type(ggml_backend_dev_t dev);
 ggml_backend_buffer_type_t ggml_backend_dev_host_buffer_type(ggml_backend_dev_t dev);
+/* plain host memory (ggml-base's CPU buffer type) */
+ggml_backend_buffer_type_t ggml_backend_cpu_buffer_type(void);
 ggml_backend_buffer_t ggml_backend_dev_buffer_from_host_ptr(ggml_backend_dev_t dev, void * ptr, size_t size,
                                                             size_t max_tensor_size);
 bool ggml_backend_dev_supports_op(ggml_backend_dev_t dev, const struct ggml_tensor * op);

@@ -26,8 +26,9 @@
  *                                            (docs/design/graph-cancellation.md:9-35)
  *   "ggml_backend_get_cancel_observation" -- observation boundary of the last compute
  *   "ggml_backend_device_pci_vendor_id"   -- 0x1002 (backend.rs:1678-1694)
- *   "ggml_backend_mi355x_profile_graph", "ggml_backend_mi355x_set_hip_graphs"
- *                                         -- the two functions below
+ *   "ggml_backend_mi355x_profile_graph", "ggml_backend_mi355x_set_hip_graphs",
+ *   "ggml_backend_mi355x_refuse_next_launch"
+ *                                         -- the three functions below
  */
 #ifndef OPENASR_GGML_MI355X_H
 #define OPENASR_GGML_MI355X_H
@@ -61,6 +62,13 @@ int ggml_backend_mi355x_profile_graph(ggml_backend_t backend, struct ggml_cgraph
 /* Turn HIP-graph capture of repeated graphs on or off (default on; the
  * environment variable OPENASR_MI355X_HIP_GRAPHS=0 also turns it off). */
 void ggml_backend_mi355x_set_hip_graphs(ggml_backend_t backend, bool enabled);
+
+/* Test seam: the first launch of the backend's next graph_compute is refused
+ * on the host (as a launcher refuses a shape it cannot run) and no kernel of
+ * it runs; that compute then fails closed with GGML_STATUS_FAILED and caches
+ * no HIP graph. It plays the role of the host's injected compute status
+ * (crates/openasr-core/src/ggml_runtime/cpu_graph.rs:7926-7947). */
+void ggml_backend_mi355x_refuse_next_launch(ggml_backend_t backend);
 
 #ifdef __cplusplus
 }

@@ -30,8 +30,16 @@
 
 namespace mi355x {
 
-static hipError_t g_last_error = hipSuccess;
-void note_hip_error(hipError_t err) { g_last_error = err; }
+static thread_local std::atomic<int> * tl_error_sink = nullptr;
+
+void note_hip_error(hipError_t err) {
+    if (err == hipSuccess || !tl_error_sink) return;
+    int expected = 0;
+    tl_error_sink->compare_exchange_strong(expected, (int) err);
+}
+
+error_scope::error_scope(std::atomic<int> * sink) : prev_(tl_error_sink) { tl_error_sink = sink; }
+error_scope::~error_scope() { tl_error_sink = prev_; }
 
 struct registry_ctx {
     std::once_flag once;
@@ -84,6 +92,7 @@ struct buffer_ctx {
 
 static void buf_free(ggml_backend_buffer_t buffer) {
     buffer_ctx * c = (buffer_ctx *) buffer->context;
+    error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
     MI_CHECK(hipFree(c->base));
     ledger_sub(c->dev, c->size, false);
@@ -98,10 +107,21 @@ static enum ggml_status buf_init_tensor(ggml_backend_buffer_t buffer, struct ggm
     return GGML_STATUS_SUCCESS;
 }
 
+static void buf_set_tensor(ggml_backend_buffer_t buffer, struct ggml_tensor * t, const void * data, size_t offset,
+                           size_t size);
+
 static void buf_memset_tensor(ggml_backend_buffer_t buffer, struct ggml_tensor * t, uint8_t value, size_t offset,
                               size_t size) {
     buffer_ctx * c = (buffer_ctx *) buffer->context;
+    error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
+    if (t->type == GGML_TYPE_Q8_0) {
+        // stored row-split on the device: ggml-layout bytes go through the
+        // same row conversion as set_tensor
+        std::vector<uint8_t> bytes(size, value);
+        buf_set_tensor(buffer, t, bytes.data(), offset, size);
+        return;
+    }
     MI_CHECK(hipMemset((char *) t->data + offset, value, size));
 }
 
@@ -118,6 +138,7 @@ static bool q8_0_rows(const ggml_tensor * t, size_t offset, size_t size, int64_t
 static void buf_set_tensor(ggml_backend_buffer_t buffer, struct ggml_tensor * t, const void * data, size_t offset,
                            size_t size) {
     buffer_ctx * c = (buffer_ctx *) buffer->context;
+    error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
     if (t->type != GGML_TYPE_Q8_0) {
         MI_CHECK(hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice));
@@ -145,6 +166,7 @@ static void buf_set_tensor(ggml_backend_buffer_t buffer, struct ggml_tensor * t,
 static void buf_get_tensor(ggml_backend_buffer_t buffer, const struct ggml_tensor * t, void * data, size_t offset,
                            size_t size) {
     buffer_ctx * c = (buffer_ctx *) buffer->context;
+    error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
     if (t->type != GGML_TYPE_Q8_0) {
         MI_CHECK(hipMemcpy(data, (const char *) t->data + offset, size, hipMemcpyDeviceToHost));
@@ -170,6 +192,7 @@ static bool buf_cpy_tensor(ggml_backend_buffer_t buffer, const struct ggml_tenso
     ggml_backend_buffer_t sb = src->view_src ? src->view_src->buffer : src->buffer;
     if (!sb || sb->buft->iface.get_name != buft_get_name) return false;
     buffer_ctx * c = (buffer_ctx *) buffer->context;
+    error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
     MI_CHECK(hipMemcpy(dst->data, src->data, ggml_nbytes(src), hipMemcpyDeviceToDevice));
     return true;
@@ -177,6 +200,7 @@ static bool buf_cpy_tensor(ggml_backend_buffer_t buffer, const struct ggml_tenso
 
 static void buf_clear(ggml_backend_buffer_t buffer, uint8_t value) {
     buffer_ctx * c = (buffer_ctx *) buffer->context;
+    error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
     MI_CHECK(hipMemset(c->base, value, c->size));
 }
@@ -254,7 +278,6 @@ static enum ggml_status be_graph_compute(ggml_backend_t backend, struct ggml_cgr
     backend_state * be = (backend_state *) backend->context;
     const enum ggml_status st = graph_compute(be, cgraph);
     be->last_status = (int) st;
-    if (st != GGML_STATUS_SUCCESS) be->last_native_error = (int64_t) g_last_error;
     return st;
 }
 
@@ -445,6 +468,8 @@ static void * reg_get_proc_address(ggml_backend_reg_t, const char * name) {
     if (std::strcmp(name, "ggml_backend_device_pci_vendor_id") == 0) return (void *) pci_vendor_id;
     if (std::strcmp(name, "ggml_backend_mi355x_profile_graph") == 0) return (void *) ggml_backend_mi355x_profile_graph;
     if (std::strcmp(name, "ggml_backend_mi355x_set_hip_graphs") == 0) return (void *) ggml_backend_mi355x_set_hip_graphs;
+    if (std::strcmp(name, "ggml_backend_mi355x_refuse_next_launch") == 0)
+        return (void *) ggml_backend_mi355x_refuse_next_launch;
     if (std::strcmp(name, "ggml_backend_memory_get_api_v1") == 0) return (void *) ggml_backend_memory_get_api_v1;
     return nullptr;
 }
@@ -534,6 +559,11 @@ void ggml_backend_mi355x_set_hip_graphs(ggml_backend_t backend, bool enabled) {
     backend_state * be = (backend_state *) backend->context;
     be->use_graphs = enabled;
     if (!enabled) release_graph_cache(be);
+}
+
+void ggml_backend_mi355x_refuse_next_launch(ggml_backend_t backend) {
+    if (!ggml_backend_is_mi355x(backend)) return;
+    ((backend_state *) backend->context)->fail_next_launch = true;
 }
 
 int ggml_backend_mi355x_device_count(void) { return (int) ggml_backend_mi355x_reg()->iface.get_device_count(nullptr); }

@@ -19,7 +19,9 @@
 
 #include <cmath>
 #include <cstring>
+#include <memory>
 #include <unordered_map>
+#include <unordered_set>
 
 #include "ggml_host.h"
 #include "ops.h"
@@ -138,6 +140,42 @@ uint64_t graph_key(const ggml_cgraph * cg) {
     return h;
 }
 
+// byte range [lo, hi) of a tensor's data (its view extent)
+struct span {
+    uintptr_t lo = 0, hi = 0;
+};
+
+span span_of(const ggml_tensor * x) {
+    span s;
+    if (!x || !x->data) return s;
+    s.lo = (uintptr_t) x->data;
+    s.hi = s.lo + ggml_nbytes(x);
+    return s;
+}
+
+span span_of(const tview & v, int64_t elem) {
+    span s;
+    s.lo = (uintptr_t) v.data;
+    int64_t last = elem;
+    for (int d = 0; d < 4; d++) last += (v.ne[d] - 1) * v.nb[d];
+    s.hi = s.lo + (uintptr_t) last;
+    return s;
+}
+
+bool overlap(span a, span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; }
+
+// A launch at graph position i that also does the work of later nodes (a
+// folded residual ADD, the SwiGLU pair, sibling projections) writes their
+// results before the nodes in between run, and reads their inputs early.
+struct hoist {
+    std::vector<const ggml_tensor *> nodes;  // later nodes whose work the launch does
+    std::vector<span> reads;                 // everything the launch reads
+    std::vector<span> writes;                // everything it writes
+    // (written, read) tensor pairs one lane reads then writes element by
+    // element: they may coincide exactly (an in-place residual), not overlap
+    std::vector<std::pair<const ggml_tensor *, const ggml_tensor *>> inplace;
+};
+
 struct planner {
     backend_state * be;
     const ggml_cgraph * cg;
@@ -151,12 +189,23 @@ struct planner {
     std::string error;
     int n_cu;
 
-    explicit planner(backend_state * b, const ggml_cgraph * g) : be(b), cg(g), n_cu(b->dev->n_cu) {}
+    // fusions a previous planning pass found unsafe under the graph's
+    // allocation (see validate): CONTs that must be materialised, unary
+    // nodes that must run at their own position
+    std::unordered_set<const ggml_tensor *> no_bypass, no_defer;
+    int cur = -1;  // graph position being planned
+
+    planner(backend_state * b, const ggml_cgraph * g, const std::unordered_set<const ggml_tensor *> & nb = {},
+            const std::unordered_set<const ggml_tensor *> & nd = {})
+        : be(b), cg(g), n_cu(b->dev->n_cu), no_bypass(nb), no_defer(nd) {}
 
     std::unordered_map<const ggml_tensor *, int> index;  // node -> position in the graph
     // CONT nodes whose copy is skipped: consumers read the CONT's strided
     // source directly (CONT -> its source)
     std::unordered_map<const ggml_tensor *, const ggml_tensor *> bypass;
+    std::unordered_map<const ggml_tensor *, int> bypass_last;  // bypassed CONT -> position of its last reader
+    // unary nodes evaluated inside a later consumer: (node, consumer position)
+    std::vector<std::pair<const ggml_tensor *, int>> deferred_unary;
 
     static const ggml_tensor * root_of(const ggml_tensor * x) { return x->view_src ? x->view_src : x; }
 
@@ -176,10 +225,12 @@ struct planner {
         for (int i = 0; i < cg->n_nodes; i++) {
             const ggml_tensor * c = cg->nodes[i];
             if (c->op != GGML_OP_CONT || c->type != GGML_TYPE_F32 || (c->flags & GGML_TENSOR_FLAG_OUTPUT)) continue;
+            if (no_bypass.count(c)) continue;
             const ggml_tensor * s = c->src[0];
             if (s->type != GGML_TYPE_F32 || s->nb[0] != 4 || s->ne[2] != 1 || s->ne[3] != 1) continue;
             if (s->nb[1] % 4 != 0) continue;
             bool ok = true, any = false;
+            int last = i;
             for (int j = i + 1; j < cg->n_nodes && ok; j++) {
                 const ggml_tensor * n = cg->nodes[j];
                 for (int k = 0; k < GGML_MAX_SRC && ok; k++) {
@@ -187,6 +238,7 @@ struct planner {
                     if (!x || root_of(x) != c) continue;
                     if (is_view_op(n->op)) continue;  // metadata; its readers are checked themselves
                     any = true;
+                    last = j;
                     const bool reader = n->op == GGML_OP_RMS_NORM || n->op == GGML_OP_NORM || n->op == GGML_OP_ROPE ||
                                         (n->op == GGML_OP_SET_ROWS && k == 0) ||
                                         ((n->op == GGML_OP_CPY || n->op == GGML_OP_CONT) && k == 0) ||
@@ -196,7 +248,10 @@ struct planner {
                     ok = reader && remap_through_cont(x, c, s, v);
                 }
             }
-            if (ok && any) bypass[c] = s;
+            if (ok && any) {
+                bypass[c] = s;
+                bypass_last[c] = last;
+            }
         }
     }
 
@@ -245,13 +300,24 @@ struct planner {
         return wt;
     }
 
-    void add_step(std::function<void(hipStream_t)> fn, const ggml_tensor * node, const char * label) {
+    // a launch at the current position writing `writes` (default: the bytes of `node`)
+    // (a list holding only nullptr: the step writes no graph tensor, only scratch)
+    void add_step(std::function<void(hipStream_t)> fn, const ggml_tensor * node, const char * label,
+                  std::vector<const ggml_tensor *> writes = {}) {
         step s;
         s.run = std::move(fn);
         s.node = node;
         s.label = label;
+        s.pos = cur;
+        if (writes.size() == 0) writes = {node};
+        for (const ggml_tensor * w : writes) {
+            const span sp = span_of(w);
+            if (sp.lo < sp.hi) s.writes.push_back({sp.lo, sp.hi});
+        }
         steps.push_back(std::move(s));
     }
+
+    bool validate();
 
     bool fail(const ggml_tensor * t, const char * why) {
         char buf[256];
@@ -263,6 +329,7 @@ struct planner {
     // norms whose launch is skipped: the GEMVs consuming their output
     // normalise and quantize in their activation prologue (norm output -> it)
     std::unordered_map<const ggml_tensor *, gemv_prologue> pro_norm;
+    std::unordered_map<const ggml_tensor *, span> pro_norm_in;  // the bytes such a prologue reads
 
     // the rope table the scratch holds at this point of the plan
     struct rope_key {
@@ -324,6 +391,7 @@ struct planner {
 
     bool plan();
     bool plan_mul_mat(int i, const ggml_tensor * t);
+    bool hoist_ok(int i, const hoist & h) const;
     // t is available before node i runs: a leaf, or a node planned earlier
     bool ready_before(const ggml_tensor * t, int i) const {
         while (t->view_src) t = t->view_src;
@@ -341,6 +409,68 @@ struct planner {
     bool plan_attn_step(int i, const ggml_tensor * t);
 };
 
+// May the launch at position i do the work described by h? Its own writes
+// must not overlap what it reads (other workgroups of the launch may still
+// be reading), except an exact in-place residual, nor each other; and every
+// node between i and the last node it absorbs, which now runs after the
+// launch although it ran before some of that work, must neither read what the
+// launch writes nor write what it reads or writes. A node whose evaluation is
+// deferred into a consumer is taken to read its sources too.
+bool planner::hoist_ok(int i, const hoist & h) const {
+    auto exact_inplace = [&](span w, span r) {
+        for (const auto & pr : h.inplace) {
+            const span a = span_of(pr.first), b = span_of(pr.second);
+            if (a.lo == w.lo && a.hi == w.hi && b.lo == r.lo && b.hi == r.hi && a.lo == b.lo &&
+                pr.first->nb[1] == pr.second->nb[1] && pr.first->nb[2] == pr.second->nb[2] &&
+                pr.first->nb[3] == pr.second->nb[3])
+                return true;
+        }
+        return false;
+    };
+    for (size_t a = 0; a < h.writes.size(); a++) {
+        for (const span & r : h.reads)
+            if (overlap(h.writes[a], r) && !exact_inplace(h.writes[a], r)) return false;
+        for (size_t b = a + 1; b < h.writes.size(); b++)
+            if (overlap(h.writes[a], h.writes[b])) return false;
+    }
+    int jmax = i;
+    for (const ggml_tensor * n : h.nodes) {
+        auto it = index.find(n);
+        if (it != index.end()) jmax = std::max(jmax, it->second);
+    }
+    auto absorbed = [&](const ggml_tensor * n) {
+        for (const ggml_tensor * x : h.nodes)
+            if (x == n) return true;
+        return false;
+    };
+    auto reads_written = [&](const ggml_tensor * x) {
+        const span sx = span_of(x);
+        for (const span & w : h.writes)
+            if (overlap(sx, w)) return true;
+        return false;
+    };
+    for (int k = i + 1; k <= jmax && k < cg->n_nodes; k++) {
+        const ggml_tensor * n = cg->nodes[k];
+        if (is_view_op(n->op) || absorbed(n)) continue;
+        const span nw = span_of(n);
+        for (const span & r : h.reads)
+            if (overlap(nw, r)) return false;
+        for (const span & w : h.writes)
+            if (overlap(nw, w)) return false;
+        for (int q = 0; q < GGML_MAX_SRC; q++) {
+            const ggml_tensor * x = n->src[q];
+            if (!x) continue;
+            if (reads_written(x)) return false;
+            if (deferred.count(x) || deferred.count(root_of(x))) {
+                const ggml_tensor * d = deferred.count(x) ? x : root_of(x);
+                for (int q2 = 0; q2 < GGML_MAX_SRC; q2++)
+                    if (d->src[q2] && reads_written(d->src[q2])) return false;
+            }
+        }
+    }
+    return true;
+}
+
 bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
     const ggml_tensor * w = t->src[0];
     const ggml_tensor * x = t->src[1];
@@ -355,8 +485,6 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         const bool reuse = act_src == x && act_wtype == wtype;
         backend_state * b = be;
         const int ncu = n_cu;
-        char * dst = (char *) t->data;
-        int64_t dst_nb1 = (int64_t) t->nb[1];
         // the tile GEMM once the columns outgrow a few GEMV chunks (earlier for tall matrices)
         const bool wide = use_mmq(wtype, M, K, N);
         const bool mfma = !wide && gemv_mfma_supported(wtype, M, K);
@@ -364,44 +492,67 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         // the quantization of f32 activations no earlier step quantized
         bool has_pro = false;
         gemv_prologue pro;
+        span pro_in;  // the f32 activations the prologue reads
         auto pn = pro_norm.find(x);
         if (pn != pro_norm.end()) {
             if (!mfma || !prologue_gemv(t, true)) return fail(t, "normalising prologue on a launch that cannot take it");
             pro = pn->second;
             has_pro = true;
+            pro_in = pro_norm_in[x];
         } else if (!reuse && mfma && x->type == GGML_TYPE_F32 && prologue_view(xv) && prologue_gemv(t, false)) {
             pro.x = (const float *) xv.data;
             pro.x_nb1 = xv.nb[1];
             has_pro = true;
+            pro_in = span_of(xv, 4);
         }
         if (!has_pro) {
             // the act region now holds x's quantization
             act_src = x;
             act_wtype = wtype;
         }
+        // what the plain launch reads and writes; each fold below is taken
+        // only if the launch with it still passes hoist_ok
+        hoist h;
+        h.reads.push_back(span_of(w));
+        if (has_pro) h.reads.push_back(pro_in);
+        h.writes.push_back(span_of(t));
+        if (!hoist_ok(i, h)) return fail(t, "MUL_MAT output overlaps its own input");
+        char * dst = (char *) t->data;
+        int64_t dst_nb1 = (int64_t) t->nb[1];
+        const ggml_tensor * produced = t;  // the last node the GEMV step writes
+        // the launch writing `out` instead of `produced`, absorbing `nodes`
+        // and reading `extra` (in place of `inplace_with`, if given)
+        auto try_fold = [&](std::initializer_list<const ggml_tensor *> nodes, const ggml_tensor * out,
+                            std::initializer_list<const ggml_tensor *> extra, const ggml_tensor * inplace_with) {
+            hoist h2 = h;
+            for (const ggml_tensor * n : nodes) h2.nodes.push_back(n);
+            h2.writes[0] = span_of(out);
+            for (const ggml_tensor * e : extra) h2.reads.push_back(span_of(e));
+            if (inplace_with) h2.inplace.push_back({out, inplace_with});
+            if (!hoist_ok(i, h2)) return false;
+            h = h2;
+            return true;
+        };
         // SwiGLU: MUL_MAT(gate, x) -> SILU -> MUL with MUL_MAT(up, x) of the
         // same shape becomes one launch over both matrices
         const char * W2 = nullptr;
-        const ggml_tensor * produced = t;  // the last node the GEMV step writes
         const ggml_tensor * silu = mfma ? sole_consumer(t, i + 1) : nullptr;
         if (silu && silu->op == GGML_OP_UNARY && silu->op_params[0] == GGML_UNARY_OP_SILU && silu->src[0] == t) {
-            const ggml_tensor * h = sole_consumer(silu, i + 1);
+            const ggml_tensor * hm = sole_consumer(silu, i + 1);
             const ggml_tensor * u = nullptr;
-            if (h && h->op == GGML_OP_MUL && (h->src[0] == silu || h->src[1] == silu)) {
-                u = h->src[0] == silu ? h->src[1] : h->src[0];
+            if (hm && hm->op == GGML_OP_MUL && (hm->src[0] == silu || hm->src[1] == silu)) {
+                u = hm->src[0] == silu ? hm->src[1] : hm->src[0];
             }
             bool ok = u && u->op == GGML_OP_MUL_MAT && u->src[1] == x && u->src[0]->type == wtype &&
                       u->src[0]->ne[0] == K && u->src[0]->ne[1] == M && u->src[0]->nb[1] == w->nb[1] &&
-                      sole_consumer(u, i + 1) == h && supports_op(be->dev, u) && is_contiguous(h);
-            for (int d = 0; d < 4 && ok; d++) ok = h->ne[d] == t->ne[d] && u->ne[d] == t->ne[d];
-            if (ok) {
+                      sole_consumer(u, i + 1) == hm && supports_op(be->dev, u) && is_contiguous(hm) &&
+                      ready_before(u->src[0], i);
+            for (int d = 0; d < 4 && ok; d++) ok = hm->ne[d] == t->ne[d] && u->ne[d] == t->ne[d];
+            if (ok && try_fold({silu, u, hm}, hm, {u->src[0]}, nullptr)) {
                 W2 = (const char *) u->src[0]->data;
-                dst = (char *) h->data;
-                dst_nb1 = (int64_t) h->nb[1];
-                deferred[silu] = silu;
-                deferred[u] = u;
-                deferred[h] = h;
-                produced = h;
+                dst = (char *) hm->data;
+                dst_nb1 = (int64_t) hm->nb[1];
+                produced = hm;
             }
         }
         // a following residual ADD of the same shape folds into the epilogue
@@ -412,12 +563,11 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             const ggml_tensor * o = add->src[0] == t ? add->src[1] : add->src[0];
             bool same = o != t && o->type == GGML_TYPE_F32 && o->nb[0] == 4 && columns_foldable(o);
             for (int d = 0; d < 4 && same; d++) same = o->ne[d] == t->ne[d] && add->ne[d] == t->ne[d];
-            if (same && ready_before(o, i)) {
+            if (same && ready_before(o, i) && try_fold({add}, add, {o}, o)) {
                 res = (const char *) o->data;
                 res_nb1 = (int64_t) o->nb[1];
                 dst = (char *) add->data;
                 dst_nb1 = (int64_t) add->nb[1];
-                deferred[add] = add;
                 produced = add;
             }
         }
@@ -430,47 +580,28 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 const ggml_tensor * o = nx->src[0] == produced ? nx->src[1] : nx->src[0];
                 bool same = o != produced && o->type == GGML_TYPE_F32 && o->nb[0] == 4 && columns_foldable(o);
                 for (int d = 0; d < 4 && same; d++) same = o->ne[d] == t->ne[d] && nx->ne[d] == t->ne[d];
-                if (same && ready_before(o, i)) {
+                if (same && ready_before(o, i) && try_fold({nx}, nx, {o}, o)) {
                     epi.res2 = (const char *) o->data;
                     dst = (char *) nx->data;
-                    deferred[nx] = nx;
                     produced = nx;
                 }
             } else if (nx && nx->op == GGML_OP_UNARY && nx->op_params[0] == GGML_UNARY_OP_GELU &&
                        nx->src[0] == produced && nx->type == GGML_TYPE_F32 && is_contiguous(nx)) {
                 bool same = true;
                 for (int d = 0; d < 4 && same; d++) same = nx->ne[d] == t->ne[d];
-                if (same) {
+                if (same && try_fold({nx}, nx, {}, nullptr)) {
                     epi.gelu = be->dev->gelu_table;
                     dst = (char *) nx->data;
-                    deferred[nx] = nx;
                     produced = nx;
                 }
             }
         }
         // sibling MUL_MATs of the same normalised column (Whisper's q, k, v
-        // projections, each maybe with a bias ADD) join a one-column launch.
-        // A sibling's result is then written before the nodes that lie
-        // between (a few, e.g. the previous projection's reshape and copy),
-        // so none of them may read or write its bytes.
+        // projections, each maybe with a bias ADD) join a one-column launch;
+        // each is taken only if the launch with it passes hoist_ok
         std::vector<gemv_sub> subs;
         if (pn != pro_norm.end() && mfma && !W2 && !epi.res2 && !epi.gelu &&
             gemv_single_column(wtype, K, N, pro.norm >= 0)) {
-            std::vector<const ggml_tensor *> between;
-            auto overlaps = [](const ggml_tensor * a, const ggml_tensor * b) {
-                if (!a || !b || !a->data || !b->data) return false;
-                const uintptr_t a0 = (uintptr_t) a->data, a1 = a0 + ggml_nbytes(a);
-                const uintptr_t b0 = (uintptr_t) b->data, b1 = b0 + ggml_nbytes(b);
-                return a0 < b1 && b0 < a1;
-            };
-            auto clear_of = [&](const ggml_tensor * out) {
-                for (const ggml_tensor * n : between) {
-                    if (overlaps(n, out)) return false;
-                    for (int k = 0; k < GGML_MAX_SRC; k++)
-                        if (overlaps(n->src[k], out)) return false;
-                }
-                return true;
-            };
             for (int j = i + 1; j < cg->n_nodes && j <= i + 16 && (int) subs.size() < kGemvMaxSubs; j++) {
                 const ggml_tensor * u = cg->nodes[j];
                 if (is_view_op(u->op) || deferred.count(u)) continue;
@@ -478,15 +609,15 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 const bool sibling = u->op == GGML_OP_MUL_MAT && u->src[1] == x && uw->type == wtype &&
                                      uw->ne[0] == K && uw->ne[2] == 1 && uw->ne[3] == 1 &&
                                      (int64_t) uw->nb[1] == row_bytes && u->type == GGML_TYPE_F32 && is_contiguous(u) &&
-                                     u->ne[1] * u->ne[2] * u->ne[3] == 1;
-                if (!sibling) {
-                    between.push_back(u);
-                    continue;
-                }
+                                     u->ne[1] * u->ne[2] * u->ne[3] == 1 && ready_before(uw, i);
+                if (!sibling) continue;
                 gemv_sub sb;
                 sb.W = (const char *) uw->data;
                 sb.M = uw->ne[1];
                 sb.dst = (char *) u->data;
+                hoist h2 = h;
+                h2.nodes.push_back(u);
+                h2.reads.push_back(span_of(uw));
                 const ggml_tensor * out = u;
                 const ggml_tensor * ua = sole_consumer(u, j + 1);
                 if (ua && ua->op == GGML_OP_ADD && ua->type == GGML_TYPE_F32 && is_contiguous(ua)) {
@@ -494,16 +625,32 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                     bool same = o != u && o->type == GGML_TYPE_F32 && o->nb[0] == 4 && columns_foldable(o);
                     for (int d = 0; d < 4 && same; d++) same = o->ne[d] == u->ne[d] && ua->ne[d] == u->ne[d];
                     if (same && ready_before(o, i)) {
-                        sb.res = (const char *) o->data;
-                        sb.dst = (char *) ua->data;
-                        out = ua;
+                        hoist h3 = h2;
+                        h3.nodes.push_back(ua);
+                        h3.reads.push_back(span_of(o));
+                        h3.writes.push_back(span_of(ua));
+                        h3.inplace.push_back({ua, o});
+                        if (hoist_ok(i, h3)) {
+                            sb.res = (const char *) o->data;
+                            sb.dst = (char *) ua->data;
+                            out = ua;
+                            h2 = h3;
+                        }
                     }
                 }
-                if (!clear_of(out)) break;
-                deferred[u] = u;
-                if (out != u) deferred[out] = out;
+                if (out == u) {
+                    h2.writes.push_back(span_of(u));
+                    if (!hoist_ok(i, h2)) break;
+                }
+                h = h2;
                 subs.push_back(sb);
             }
+        }
+        for (const ggml_tensor * n : h.nodes) deferred[n] = n;
+        std::vector<const ggml_tensor *> outs = {produced};
+        for (const ggml_tensor * n : h.nodes) {
+            for (const gemv_sub & sb : subs)
+                if ((const char *) n->data == sb.dst) outs.push_back(n);
         }
         if (!reuse && !has_pro) {
             add_step(
@@ -511,7 +658,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                     act_buffers act = act_carve(wtype, act_base(b), K, N);
                     launch_quantize_act(xv, wtype, act, s);
                 },
-                t, wtype == GGML_TYPE_Q8_0 ? "quantize_q8_0" : "quantize_q8_K");
+                t, wtype == GGML_TYPE_Q8_0 ? "quantize_q8_0" : "quantize_q8_K", {nullptr});
         }
         add_step(
             [=](hipStream_t s) {
@@ -523,7 +670,8 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
             produced, W2 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")
-                             : (wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K"));
+                             : (wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K"),
+            outs);
         return true;
     }
     const tview dv = make_view(t);
@@ -587,7 +735,8 @@ bool planner::plan_norm(int i, const ggml_tensor * t) {
                 deferred[t1] = t1;
                 deferred[mul1] = mul1;
                 deferred[rope1] = rope1;
-                add_step([=](hipStream_t s) { launch_rms_norm_rope128(j0, &j1, s); }, rope1, "rms_norm_rope");
+                add_step([=](hipStream_t s) { launch_rms_norm_rope128(j0, &j1, s); }, rope1, "rms_norm_rope",
+                         {rope0, rope1});
             } else {
                 add_step([=](hipStream_t s) { launch_rms_norm_rope128(j0, nullptr, s); }, rope0, "rms_norm_rope");
             }
@@ -646,6 +795,7 @@ bool planner::plan_norm(int i, const ggml_tensor * t) {
             p.eps = eps;
             p.norm = mode;
             pro_norm[out] = p;
+            pro_norm_in[out] = span_of(av, 4);
             return true;
         }
     }
@@ -670,7 +820,7 @@ bool planner::plan_norm(int i, const ggml_tensor * t) {
 bool planner::plan_unary(int i, const ggml_tensor * t) {
     const int uop = t->op_params[0];
     const int ncu = n_cu;
-    if (uop == GGML_UNARY_OP_SILU) {
+    if (uop == GGML_UNARY_OP_SILU && !no_defer.count(t)) {
         const ggml_tensor * mul = sole_consumer(t, i + 1);
         if (mul && mul->op == GGML_OP_MUL && (mul->src[0] == t || mul->src[1] == t)) {
             const ggml_tensor * other = mul->src[0] == t ? mul->src[1] : mul->src[0];
@@ -679,6 +829,7 @@ bool planner::plan_unary(int i, const ggml_tensor * t) {
             if (same_shape) {
                 // the SiLU is evaluated inside the multiply, at the multiply's position
                 deferred[t] = mul;
+                deferred_unary.push_back({t, index.at(mul)});
                 return true;
             }
         }
@@ -943,7 +1094,7 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
         const rope_key rk = rope_cur;
         add_step([=](hipStream_t s) {
             launch_rope_table((float2 *) rope_base(b), rk.pos, rk.n_seq, rk.theta_scale, rk.freq_scale, rk.attn_factor, s);
-        }, F, "rope_table");
+        }, F, "rope_table", {nullptr});
     }
     add_step(
         [=](hipStream_t s) {
@@ -952,7 +1103,7 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
             if (la.fa.qtype >= 0) la.fa.act = act_carve(la.fa.qtype, act_base(b), qK, qN);
             launch_attn_step(la, gen_base(b), s);
         },
-        F, "attn_step");
+        F, "attn_step", {F, sk, sv});
     if (fa.qtype >= 0) {
         act_src = oview;
         act_wtype = fa.qtype;
@@ -960,11 +1111,49 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     return true;
 }
 
+// The plan moves reads later than the graph has them in two places: a
+// bypassed CONT's readers read its source at their own positions, and a
+// deferred unary node reads its source at its consumer's position. Under an
+// allocator that reuses dead blocks, a launch between may already have
+// written those bytes. Such a fusion is recorded in no_bypass / no_defer and
+// validate returns false, and the caller plans again without it.
+bool planner::validate() {
+    bool ok = true;
+    auto written_between = [&](span src, int from, int to, bool allow_exact_at_to) {
+        for (const step & st : steps) {
+            if (st.pos <= from || st.pos > to) continue;
+            for (const auto & w : st.writes) {
+                const span ws{w.first, w.second};
+                if (!overlap(ws, src)) continue;
+                if (allow_exact_at_to && st.pos == to && ws.lo == src.lo && ws.hi == src.hi) continue;
+                return true;
+            }
+        }
+        return false;
+    };
+    for (const auto & bp : bypass) {
+        const ggml_tensor * c = bp.first;
+        const tview sv = make_view(bp.second);
+        if (written_between(span_of(sv, 4), index.at(c), bypass_last.at(c), false)) {
+            no_bypass.insert(c);
+            ok = false;
+        }
+    }
+    for (const auto & du : deferred_unary) {
+        if (written_between(span_of(du.first->src[0]), index.at(du.first), du.second, true)) {
+            no_defer.insert(du.first);
+            ok = false;
+        }
+    }
+    return ok;
+}
+
 bool planner::plan() {
     count_uses();
     find_bypass();
     for (int i = 0; i < cg->n_nodes; i++) {
         const ggml_tensor * t = cg->nodes[i];
+        cur = i;
         if (is_view_op(t->op)) continue;
         if (!supports_op(be->dev, t)) return fail(t, "unsupported op or layout");
         if (bypass.count(t)) continue;  // readers take the CONT's source directly
@@ -1023,7 +1212,7 @@ bool planner::plan() {
                     const int dtype2 = t2->type;
                     deferred[t2] = t2;
                     add_step([=](hipStream_t s) { launch_set_rows(dv, dtype, sv, iv, i64, s, ncu, &dv2, dtype2, &sv2); },
-                             t2, "set_rows");
+                             t2, "set_rows", {t, t2});
                 } else {
                     add_step([=](hipStream_t s) { launch_set_rows(dv, dtype, sv, iv, i64, s, ncu); }, t, "set_rows");
                 }
@@ -1101,6 +1290,23 @@ bool planner::plan() {
     return true;
 }
 
+// plan cg, and plan again without the fusions validate() finds unsafe under
+// the graph's allocation (each pass removes at least one; they are few)
+std::unique_ptr<planner> make_plan(backend_state * be, const ggml_cgraph * cg, bool & ok) {
+    std::unordered_set<const ggml_tensor *> nb, nd;
+    for (int pass = 0; pass < 64; pass++) {
+        auto p = std::make_unique<planner>(be, cg, nb, nd);
+        ok = p->plan();
+        if (!ok || p->validate()) return p;
+        nb = p->no_bypass;
+        nd = p->no_defer;
+    }
+    auto p = std::make_unique<planner>(be, cg, nb, nd);
+    ok = p->plan() && p->validate();
+    if (!ok && p->error.empty()) p->error = "no safe plan for this allocation";
+    return p;
+}
+
 // the arena: two equal halves (activation region, general region), at least
 // 32 MiB each
 size_t arena_half(size_t act_need, size_t gen_need) {
@@ -1167,16 +1373,18 @@ void release_scratch(backend_state * be) {
 }
 
 bool graph_arena_bytes(backend_state * be, ggml_cgraph * cg, size_t * bytes) {
-    planner p(be, cg);
-    if (!p.plan()) return false;
-    *bytes = 2 * arena_half(p.act_need, p.gen_need);
+    bool ok;
+    auto p = make_plan(be, cg, ok);
+    if (!ok) return false;
+    *bytes = 2 * arena_half(p->act_need, p->gen_need);
     return true;
 }
 
 bool reserve_graph_arena(backend_state * be, ggml_cgraph * cg) {
     MI_CHECK(hipSetDevice(be->dev->hip_id));
-    planner p(be, cg);
-    return p.plan() && ensure_scratch(be, p.act_need, p.gen_need);
+    bool ok;
+    auto p = make_plan(be, cg, ok);
+    return ok && ensure_scratch(be, p->act_need, p->gen_need);
 }
 
 void release_graph_cache(backend_state * be) {
@@ -1212,26 +1420,56 @@ static cache_entry * new_entry(backend_state * be, uint64_t key) {
     return &be->cache.back();
 }
 
+// the status of a compute that failed with HIP error e; a device-fatal one
+// poisons the backend (the host then leaks and never reuses it,
+// cpu_graph.rs:7880-7924)
+static enum ggml_status fail_with(backend_state * be, hipError_t e, const char * what) {
+    std::fprintf(stderr, "mi355x: %s: %s\n", what, hipGetErrorString(e));
+    be->last_native_error = (int64_t) e;
+    const enum ggml_status st = map_error(e);
+    if (st == GGML_STATUS_DEVICE_LOST) be->poisoned = true;
+    return st;
+}
+
+// run the planned steps on the backend stream; the test seam refuses the
+// first one the way a launcher refuses (noted error, nothing enqueued)
+static void run_steps(backend_state * be, std::vector<step> & steps, size_t first, size_t last) {
+    for (size_t k = first; k < last; k++) {
+        if (be->fail_next_launch) {
+            be->fail_next_launch = false;
+            note_hip_error(hipErrorInvalidValue);
+            continue;
+        }
+        steps[k].run(be->stream);
+    }
+}
+
 enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg) {
     if (be->poisoned) return GGML_STATUS_BACKEND_POISONED;
+    be->last_native_error = 0;
+    // a transfer into this device that failed since the last compute: the
+    // graph would read what it failed to write
+    const int te = be->dev->transfer_error.exchange(0);
+    if (te != 0) return fail_with(be, (hipError_t) te, "an earlier tensor transfer failed");
+    be->launch_error.store(0);
+    error_scope scope(&be->launch_error);
     MI_CHECK(hipSetDevice(be->dev->hip_id));
     const uint64_t key = graph_key(cg);
     cache_entry * ce = find_entry(be, key);
     be->use_clock++;
-    if (ce && ce->exec && !be->abort_cb) {
+    if (ce && ce->exec && !be->abort_cb && !be->fail_next_launch) {
         ce->last_use = be->use_clock;
         be->last_observation = GGML_BACKEND_GRAPH_CANCEL_OBSERVATION_GRAPH_COMPLETION;
         hipError_t e = hipGraphLaunch(ce->exec, be->stream);
         if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
-        if (e != hipSuccess) {
-            std::fprintf(stderr, "mi355x: graph replay failed: %s\n", hipGetErrorString(e));
-            be->poisoned = map_error(e) == GGML_STATUS_DEVICE_LOST;
-        }
-        return map_error(e);
+        if (e != hipSuccess) return fail_with(be, e, "graph replay failed");
+        return GGML_STATUS_SUCCESS;
     }
 
-    planner p(be, cg);
-    if (!p.plan()) {
+    bool planned;
+    auto pp = make_plan(be, cg, planned);
+    planner & p = *pp;
+    if (!planned) {
         std::fprintf(stderr, "mi355x: cannot plan graph: %s\n", p.error.c_str());
         return GGML_STATUS_FAILED;
     }
@@ -1241,20 +1479,38 @@ enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg) {
     ce->last_use = be->use_clock;
     ce->seen++;
 
+    if (ce->exec) {
+        // a cached graph exists but this compute runs the plan (the test seam
+        // is armed): the plan is captured afresh below or runs eagerly
+        (void) hipGraphExecDestroy(ce->exec);
+        (void) hipGraphDestroy(ce->graph);
+        ce->exec = nullptr;
+        ce->graph = nullptr;
+    }
     const bool capture = be->use_graphs && !be->abort_cb && ce->seen >= 2;
     if (capture) {
         hipError_t e = hipStreamBeginCapture(be->stream, hipStreamCaptureModeThreadLocal);
         if (e == hipSuccess) {
-            for (step & s : p.steps) s.run(be->stream);
+            run_steps(be, p.steps, 0, p.steps.size());
             e = hipStreamEndCapture(be->stream, &ce->graph);
+        }
+        if (e == hipSuccess && be->launch_error.load() != 0) {
+            // a launch was refused while capturing: the graph lacks it and
+            // must never be replayed
+            (void) hipGraphDestroy(ce->graph);
+            ce->graph = nullptr;
+            std::fprintf(stderr, "mi355x: a launch was refused: %s\n",
+                         hipGetErrorString((hipError_t) be->launch_error.load()));
+            be->last_native_error = be->launch_error.load();
+            return GGML_STATUS_FAILED;
         }
         if (e == hipSuccess) e = hipGraphInstantiate(&ce->exec, ce->graph, nullptr, nullptr, 0);
         if (e == hipSuccess) {
             be->last_observation = GGML_BACKEND_GRAPH_CANCEL_OBSERVATION_GRAPH_COMPLETION;
             e = hipGraphLaunch(ce->exec, be->stream);
             if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
-            if (e != hipSuccess) be->poisoned = map_error(e) == GGML_STATUS_DEVICE_LOST;
-            return map_error(e);
+            if (e != hipSuccess) return fail_with(be, e, "graph launch failed");
+            return GGML_STATUS_SUCCESS;
         }
         std::fprintf(stderr, "mi355x: graph capture failed (%s); running eagerly\n", hipGetErrorString(e));
         (void) hipGetLastError();
@@ -1264,30 +1520,37 @@ enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg) {
         }
         ce->exec = nullptr;
         be->use_graphs = false;
+        be->launch_error.store(0);
     }
 
     be->last_observation = GGML_BACKEND_GRAPH_CANCEL_OBSERVATION_SUBMISSION_CHECKPOINT;
-    for (step & s : p.steps) {
+    for (size_t k = 0; k < p.steps.size(); k++) {
         if (be->abort_cb && be->abort_cb(be->abort_data)) {
             (void) hipStreamSynchronize(be->stream);
             return GGML_STATUS_ABORTED;
         }
-        s.run(be->stream);
+        run_steps(be, p.steps, k, k + 1);
     }
     hipError_t e = hipGetLastError();
     if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
-    if (e != hipSuccess) {
-        std::fprintf(stderr, "mi355x: graph execution failed: %s\n", hipGetErrorString(e));
-        be->poisoned = map_error(e) == GGML_STATUS_DEVICE_LOST;
+    if (e != hipSuccess) return fail_with(be, e, "graph execution failed");
+    if (be->launch_error.load() != 0) {
+        // the kernels that did launch have finished (synchronized above)
+        std::fprintf(stderr, "mi355x: a launch was refused: %s\n",
+                     hipGetErrorString((hipError_t) be->launch_error.load()));
+        be->last_native_error = be->launch_error.load();
+        return GGML_STATUS_FAILED;
     }
-    return map_error(e);
+    return GGML_STATUS_SUCCESS;
 }
 
 int profile_graph(backend_state * be, ggml_cgraph * cg, int iters, float * step_ms, int max_steps, char * labels,
                   int label_cap) {
     MI_CHECK(hipSetDevice(be->dev->hip_id));
-    planner p(be, cg);
-    if (!p.plan()) {
+    bool planned;
+    auto pp = make_plan(be, cg, planned);
+    planner & p = *pp;
+    if (!planned) {
         std::fprintf(stderr, "mi355x: cannot plan graph: %s\n", p.error.c_str());
         return -1;
     }

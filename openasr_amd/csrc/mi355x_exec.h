@@ -1,6 +1,7 @@
 // mi355x_exec.h -- device / backend state and the graph executor interface.
 #pragma once
 
+#include <atomic>
 #include <cstdint>
 #include <functional>
 #include <mutex>
@@ -33,6 +34,24 @@ struct device_state {
     uint64_t high_water = 0;       // largest live + workspace seen
     uint64_t alloc_count = 0, alloc_failures = 0;
     uint64_t generation = 1;       // advances with every allocation and release
+    // first HIP error of a tensor transfer (set/get/memset/copy/clear) since
+    // the last graph_compute on this device; that compute consumes it and
+    // fails with it
+    std::atomic<int> transfer_error{0};
+};
+
+// Errors noted while an error_scope is active on the calling thread go to
+// its sink (the first one is kept): a backend's launch_error while it plans,
+// captures or launches a graph, the device's transfer_error inside a buffer
+// operation. Scopes nest; the innermost one receives the error.
+struct error_scope {
+    explicit error_scope(std::atomic<int> * sink);
+    ~error_scope();
+    error_scope(const error_scope &) = delete;
+    error_scope & operator=(const error_scope &) = delete;
+
+  private:
+    std::atomic<int> * prev_;
 };
 
 // this plugin's objects behind ggml handles (null for another backend's)
@@ -51,6 +70,8 @@ struct step {
     std::function<void(hipStream_t)> run;
     const ggml_tensor * node;  // the last graph node this step produces
     std::string label;
+    int pos = -1;  // graph position of the node being planned when the step was made (where it runs)
+    std::vector<std::pair<uintptr_t, uintptr_t>> writes;  // byte ranges [lo, hi) the step writes
 };
 
 struct cache_entry {
@@ -78,6 +99,8 @@ struct backend_state {
     uint64_t quarantine_generation = 0;
     int last_status = 0;               // ggml_status of the last graph_compute
     int64_t last_native_error = 0;     // hipError_t behind it
+    std::atomic<int> launch_error{0};  // first error noted during the current graph_compute
+    bool fail_next_launch = false;     // test seam: the next compute's first launch is refused
     ggml_guid guid{};
     ggml_backend backend{};
     std::string name;

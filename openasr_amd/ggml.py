@@ -170,6 +170,8 @@ def base() -> C.CDLL:
     _sig(lib, "ggml_gallocr_new", C.c_void_p, C.c_void_p)
     _sig(lib, "ggml_gallocr_free", None, C.c_void_p)
     _sig(lib, "ggml_gallocr_alloc_graph", C.c_bool, C.c_void_p, C.c_void_p)
+    _sig(lib, "ggml_gallocr_get_buffer_size", sz, C.c_void_p, i)
+    _sig(lib, "ggml_backend_cpu_buffer_type", C.c_void_p)
     _sig(lib, "oa_synth_normal", None, C.c_uint64, C.c_uint64, i64, i64, f, f, C.c_void_p)
     _sig(lib, "oa_synth_uniform_i32", None, C.c_uint64, C.c_uint64, i64, C.c_int32, C.c_void_p)
     _base = lib

@@ -16,6 +16,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
+#include <unordered_map>
 #include <vector>
 
 #ifndef OPENASR_HOST_ABI_FINGERPRINT
@@ -519,6 +520,51 @@ void ggml_backend_unload(ggml_backend_reg_t reg) {
     (void) handle;
 }
 
+// ------------------------------------------------------ host buffer type --
+// Plain host memory (ggml-base's CPU buffer type): what a graph allocated
+// without a device runs in, e.g. to inspect an allocation plan on a machine
+// with no GPU.
+
+namespace {
+
+void hostbuf_free(ggml_backend_buffer_t b) {
+    std::free(b->context);
+}
+void * hostbuf_base(ggml_backend_buffer_t b) { return b->context; }
+void hostbuf_memset(ggml_backend_buffer_t, struct ggml_tensor * t, uint8_t v, size_t off, size_t n) {
+    std::memset((char *) t->data + off, v, n);
+}
+void hostbuf_set(ggml_backend_buffer_t, struct ggml_tensor * t, const void * d, size_t off, size_t n) {
+    std::memcpy((char *) t->data + off, d, n);
+}
+void hostbuf_get(ggml_backend_buffer_t, const struct ggml_tensor * t, void * d, size_t off, size_t n) {
+    std::memcpy(d, (const char *) t->data + off, n);
+}
+void hostbuf_clear(ggml_backend_buffer_t b, uint8_t v) { std::memset(b->context, v, b->size); }
+
+const char * hostbuft_name(ggml_backend_buffer_type_t) { return "CPU"; }
+ggml_backend_buffer_t hostbuft_alloc(ggml_backend_buffer_type_t buft, size_t size) {
+    const size_t n = align_up(size ? size : 64, 64);
+    void * p = std::aligned_alloc(64, n);
+    if (!p) return nullptr;
+    static const ggml_backend_buffer_i iface = {hostbuf_free, hostbuf_base, nullptr, hostbuf_memset,
+                                                hostbuf_set, hostbuf_get, nullptr, hostbuf_clear, nullptr};
+    return ggml_backend_buffer_init(buft, iface, p, size);
+}
+size_t hostbuft_align(ggml_backend_buffer_type_t) { return 64; }
+size_t hostbuft_max(ggml_backend_buffer_type_t) { return SIZE_MAX; }
+size_t hostbuft_alloc_size(ggml_backend_buffer_type_t, const struct ggml_tensor * t) { return ggml_nbytes(t); }
+bool hostbuft_is_host(ggml_backend_buffer_type_t) { return true; }
+
+}  // namespace
+
+ggml_backend_buffer_type_t ggml_backend_cpu_buffer_type(void) {
+    static ggml_backend_buffer_type buft = {
+        {hostbuft_name, hostbuft_alloc, hostbuft_align, hostbuft_max, hostbuft_alloc_size, hostbuft_is_host},
+        nullptr, nullptr};
+    return &buft;
+}
+
 // -------------------------------------------------------- graph allocator --
 
 struct ggml_gallocr {
@@ -544,41 +590,228 @@ size_t ggml_gallocr_get_buffer_size(ggml_gallocr_t galloc, int buffer_id) {
     return galloc->buffer ? ggml_backend_buffer_get_size(galloc->buffer) : 0;
 }
 
-// Every graph tensor without storage gets its own slot in one buffer (no
-// lifetime-based reuse: an MI355X holds 288 GB and the decoder graphs here
-// need at most a few GB of intermediates). The buffer is kept and reused
-// while the next graph fits.
-bool ggml_gallocr_alloc_graph(ggml_gallocr_t galloc, struct ggml_cgraph * graph) {
-    const size_t align = ggml_backend_buft_get_alignment(galloc->buft);
-    std::vector<ggml_tensor *> todo;
-    auto consider = [&](ggml_tensor * t) {
-        if (t && t->data == nullptr && t->view_src == nullptr) {
-            for (ggml_tensor * seen : todo) {
-                if (seen == t) return;
-            }
-            todo.push_back(t);
-        }
-    };
-    for (int i = 0; i < graph->n_leafs; i++) consider(graph->leafs[i]);
-    for (int i = 0; i < graph->n_nodes; i++) {
-        for (int s = 0; s < GGML_MAX_SRC; s++) consider(graph->nodes[i]->src[s]);
-        // a view node whose base is not a graph node (set_rows into a cache
-        // tensor of the same context) still needs the base to have storage
-        consider(graph->nodes[i]->view_src);
-        consider(graph->nodes[i]);
+// Graph allocation by lifetime, as ggml-alloc does it (the allocator the
+// host's graph runner uses, reached through ggml_gallocr_alloc_graph,
+// crates/openasr-core/src/ggml_runtime/ffi.rs): every node counts its
+// consumers and the views of it; inputs are placed first and live for the
+// whole graph; each node then takes a block, or -- when its op can run in
+// place and a source of the same layout has no other consumer and no view --
+// that source's block; a source's block returns to the free list when its
+// last consumer has been placed (outputs and inputs are never freed). Blocks
+// are carved best-fit from one buffer whose size is the high-water mark of
+// the walk; adjacent free blocks merge.
+namespace {
+
+bool op_can_inplace(enum ggml_op op) {
+    switch (op) {
+        case GGML_OP_SCALE:
+        case GGML_OP_ADD:
+        case GGML_OP_SUB:
+        case GGML_OP_MUL:
+        case GGML_OP_DIV:
+        case GGML_OP_UNARY:
+        case GGML_OP_ROPE:
+        case GGML_OP_RMS_NORM:
+        case GGML_OP_SOFT_MAX:
+            return true;
+        default:
+            return false;
     }
-    size_t total = 0;
-    for (ggml_tensor * t : todo) total += align_up(ggml_backend_buft_get_alloc_size(galloc->buft, t), align);
-    if (total == 0) total = align;
+}
+
+bool same_layout(const ggml_tensor * a, const ggml_tensor * b) {
+    if (a->type != b->type) return false;
+    for (int d = 0; d < GGML_MAX_DIMS; d++)
+        if (a->ne[d] != b->ne[d] || a->nb[d] != b->nb[d]) return false;
+    return true;
+}
+
+struct block_pool {
+    struct blk {
+        size_t off, size;
+    };
+    std::vector<blk> free_list;  // sorted by offset, disjoint, merged
+    size_t top = 0;              // end of the highest block ever used
+
+    size_t alloc(size_t size) {
+        int best = -1;
+        for (int k = 0; k < (int) free_list.size(); k++) {
+            if (free_list[(size_t) k].size >= size &&
+                (best < 0 || free_list[(size_t) k].size < free_list[(size_t) best].size))
+                best = k;
+        }
+        if (best >= 0) {
+            blk & b = free_list[(size_t) best];
+            const size_t off = b.off;
+            b.off += size;
+            b.size -= size;
+            if (b.size == 0) free_list.erase(free_list.begin() + best);
+            return off;
+        }
+        // grow: a free block at the end is extended
+        if (!free_list.empty() && free_list.back().off + free_list.back().size == top) {
+            const size_t off = free_list.back().off;
+            top = off + size;
+            free_list.pop_back();
+            return off;
+        }
+        const size_t off = top;
+        top += size;
+        return off;
+    }
+
+    void release(size_t off, size_t size) {
+        size_t k = 0;
+        while (k < free_list.size() && free_list[k].off < off) k++;
+        free_list.insert(free_list.begin() + (long) k, blk{off, size});
+        if (k + 1 < free_list.size() && free_list[k].off + free_list[k].size == free_list[k + 1].off) {
+            free_list[k].size += free_list[k + 1].size;
+            free_list.erase(free_list.begin() + (long) k + 1);
+        }
+        if (k > 0 && free_list[k - 1].off + free_list[k - 1].size == free_list[k].off) {
+            free_list[k - 1].size += free_list[k].size;
+            free_list.erase(free_list.begin() + (long) k);
+        }
+    }
+};
+
+struct galloc_plan {
+    struct info {
+        int n_children = 0, n_views = 0;
+        bool own = false;        // placed by this allocator
+        bool pinned = false;     // an output, or the base of an output view: never freed or taken over
+        bool allocated = false;  // holds a block that will be freed at last use
+        size_t off = 0, size = 0;
+    };
+    std::unordered_map<const ggml_tensor *, info> tab;
+    std::vector<ggml_tensor *> order;  // tensors placed, in placement order
+    block_pool pool;
+    size_t align = 256;
+    ggml_backend_buffer_type_t buft = nullptr;
+
+    info & at(const ggml_tensor * t) { return tab[t]; }
+
+    void place(ggml_tensor * t) {
+        info & in = at(t);
+        if (in.own || t->data || t->view_src) return;
+        in.own = true;
+        in.size = align_up(ggml_backend_buft_get_alloc_size(buft, t), align);
+        if (in.size == 0) in.size = align;
+        order.push_back(t);
+        if (op_can_inplace(t->op) && !(t->flags & GGML_TENSOR_FLAG_INPUT)) {
+            for (int s = 0; s < GGML_MAX_SRC; s++) {
+                ggml_tensor * p = t->src[s];
+                if (!p) continue;
+                const bool view = p->view_src != nullptr;
+                ggml_tensor * base = view ? p->view_src : p;
+                info & pb = at(base);
+                info & pi = at(p);
+                if (!pb.own || !pb.allocated) continue;
+                if ((base->flags & (GGML_TENSOR_FLAG_OUTPUT | GGML_TENSOR_FLAG_INPUT)) ||
+                    (p->flags & GGML_TENSOR_FLAG_OUTPUT) || pb.pinned)
+                    continue;
+                if (!same_layout(t, p) || pi.n_children != 1 || pi.n_views != 0) continue;
+                if (view && (pb.n_views != 1 || pb.n_children != 0 || p->view_offs != 0)) continue;
+                if (pb.size < in.size) continue;
+                // take over the source's block
+                in.off = pb.off;
+                in.size = pb.size;
+                in.allocated = true;
+                pb.allocated = false;
+                return;
+            }
+        }
+        in.off = pool.alloc(in.size);
+        in.allocated = true;
+    }
+
+    void release_if_dead(const ggml_tensor * t) {
+        info & in = at(t);
+        if (!in.own || !in.allocated) return;
+        if (in.n_children != 0 || in.n_views != 0) return;
+        if ((t->flags & (GGML_TENSOR_FLAG_OUTPUT | GGML_TENSOR_FLAG_INPUT)) || in.pinned) return;
+        pool.release(in.off, in.size);
+        in.allocated = false;
+    }
+
+    void run(ggml_cgraph * g) {
+        for (int i = 0; i < g->n_nodes; i++) {
+            ggml_tensor * n = g->nodes[i];
+            if (n->view_src) {
+                at(n->view_src).n_views++;
+                if (n->flags & GGML_TENSOR_FLAG_OUTPUT) at(n->view_src).pinned = true;
+            }
+            for (int s = 0; s < GGML_MAX_SRC; s++)
+                if (n->src[s]) at(n->src[s]).n_children++;
+        }
+        // inputs first: they hold what the host sets before the compute
+        for (int i = 0; i < g->n_leafs; i++)
+            if (g->leafs[i]->flags & GGML_TENSOR_FLAG_INPUT) place(g->leafs[i]);
+        for (int i = 0; i < g->n_nodes; i++) {
+            ggml_tensor * n = g->nodes[i];
+            if (n->flags & GGML_TENSOR_FLAG_INPUT) place(n);
+            for (int s = 0; s < GGML_MAX_SRC; s++)
+                if (n->src[s] && (n->src[s]->flags & GGML_TENSOR_FLAG_INPUT)) place(n->src[s]);
+        }
+        for (int i = 0; i < g->n_nodes; i++) {
+            ggml_tensor * n = g->nodes[i];
+            // sources not placed yet (leafs: constants of the graph) live on
+            for (int s = 0; s < GGML_MAX_SRC; s++) {
+                ggml_tensor * p = n->src[s];
+                if (p && !p->data && !p->view_src && !at(p).own) {
+                    place(p);
+                    at(p).allocated = false;  // never freed
+                }
+            }
+            if (n->view_src && !n->view_src->data && !at(n->view_src).own) {
+                place(n->view_src);
+                at(n->view_src).allocated = false;
+            }
+            place(n);
+            for (int s = 0; s < GGML_MAX_SRC; s++) {
+                ggml_tensor * p = n->src[s];
+                if (!p) continue;
+                info & pi = at(p);
+                pi.n_children--;
+                if (pi.n_children != 0 || pi.n_views != 0) continue;
+                if (p->view_src) {
+                    info & vb = at(p->view_src);
+                    vb.n_views--;
+                    release_if_dead(p->view_src);
+                } else {
+                    release_if_dead(p);
+                }
+            }
+        }
+        // leafs the nodes never read (kept by the host for later graphs)
+        for (int i = 0; i < g->n_leafs; i++) {
+            ggml_tensor * l = g->leafs[i];
+            if (!l->data && !l->view_src && !at(l).own) {
+                place(l);
+                at(l).allocated = false;
+            }
+        }
+    }
+};
+
+}  // namespace
+
+bool ggml_gallocr_alloc_graph(ggml_gallocr_t galloc, struct ggml_cgraph * graph) {
+    galloc_plan plan;
+    plan.align = ggml_backend_buft_get_alignment(galloc->buft);
+    plan.buft = galloc->buft;
+    plan.run(graph);
+    size_t total = align_up(plan.pool.top, plan.align);
+    if (total == 0) total = plan.align;
     if (!galloc->buffer || ggml_backend_buffer_get_size(galloc->buffer) < total) {
         ggml_backend_buffer_free(galloc->buffer);
         galloc->buffer = ggml_backend_buft_alloc_buffer(galloc->buft, total);
         if (!galloc->buffer) return false;
         ggml_backend_buffer_set_usage(galloc->buffer, GGML_BACKEND_BUFFER_USAGE_COMPUTE);
     }
-    ggml_tallocr ta = ggml_tallocr_new(galloc->buffer);
-    for (ggml_tensor * t : todo) {
-        if (ggml_tallocr_alloc(&ta, t) != 0) return false;
+    char * base = (char *) ggml_backend_buffer_get_base(galloc->buffer);
+    for (ggml_tensor * t : plan.order) {
+        if (ggml_backend_tensor_alloc(galloc->buffer, t, base + plan.at(t).off) != 0) return false;
     }
     auto init_view = [](ggml_tensor * t) {
         if (t && t->view_src && t->data == nullptr && t->view_src->data) ggml_backend_view_init(t);

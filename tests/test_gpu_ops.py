@@ -618,3 +618,55 @@ def test_conv_2d_f32_kernel_chain(ggml, gpu, ref):
     got = G.get(y).reshape(n, oc, oh, ow)
     assert rel_err(got, want) <= 2e-3
     G.free()
+
+
+def test_refused_launch_fails_closed(ggml, gpu, ref):
+    """A launch refused on the host (the plugin's test seam plays a launcher
+    that refuses a shape) fails the compute with GGML_STATUS_FAILED -- in the
+    eager first compute and in the compute that captures the HIP graph -- and
+    no graph missing that launch is ever replayed: the computes after it
+    capture again and give the right result."""
+    import ctypes as C
+    refuse = gpu.cdll.ggml_backend_mi355x_refuse_next_launch
+    refuse.restype, refuse.argtypes = None, [C.c_void_p]
+    m, k = 1024, 1024
+    wq = ggml.quantize(ggml.Q8_0, ggml.synth_normal(3, 1, m * k, 0, 0.02).reshape(m, k))
+    G = ggml.Graph()
+    W = G.new(ggml.Q8_0, k, m, weight=True)
+    X = G.new(ggml.F32, k, 1)
+    Y = G.lib.ggml_add(G.ctx, G.lib.ggml_mul_mat(G.ctx, W, X), X)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    statuses = []
+    for it in range(6):
+        x = RNG.standard_normal((1, k)).astype(np.float32)
+        G.set(X, x)
+        G.set(Y, np.full((1, m), np.nan, np.float32))
+        if it in (0, 1, 4):  # eager, capturing, and a compute after a graph was cached
+            refuse(gpu.backend)
+        st = G.compute(gpu.backend)
+        statuses.append(st)
+        y = G.get(Y).reshape(1, m)
+        if st == 0:
+            assert_same_bits(y, ref.mul_mat(ggml.Q8_0, wq, m, k, x) + x)
+    assert statuses == [-1, -1, 0, 0, -1, 0], statuses
+    G.free()
+
+
+def test_failed_transfer_fails_next_compute(ggml, gpu):
+    """A tensor transfer the plugin refuses (a Q8_0 tensor whose rows are not
+    packed) is not lost: the next graph_compute on the device fails with
+    GGML_STATUS_EXECUTION_FAILED instead of running on what the transfer
+    failed to write, and the compute after that succeeds."""
+    G = ggml.Graph()
+    W = G.new(ggml.Q8_0, 64, 4, weight=True)
+    X = G.new(ggml.F32, 64, 1)
+    Y = G.lib.ggml_mul_mat(G.ctx, W, X)
+    run(ggml, gpu, G, Y)
+    # a view of W whose rows are 34 bytes wider than packed: set_tensor refuses it
+    V = G.lib.ggml_view_2d(G.wctx, W, 32, 2, 2 * 34, 0)
+    G.lib.ggml_backend_tensor_set(V, np.zeros(4 * 34 // 2, np.uint8).ctypes.data, 0, 2 * 34)
+    G.set(X, np.ones((1, 64), np.float32))
+    assert G.compute(gpu.backend) == 2
+    assert G.compute(gpu.backend) == 0
+    G.free()
