@@ -193,6 +193,10 @@ struct planner {
     // allocation (see validate): CONTs that must be materialised, unary
     // nodes that must run at their own position
     std::unordered_set<const ggml_tensor *> no_bypass, no_defer;
+    // nodes whose result is consumed only in a form a fused launch wrote to
+    // scratch (the attention output quantized for the output projection):
+    // their own bytes are never written, so nothing else may read them
+    std::unordered_set<const ggml_tensor *> unwritten;
     int cur = -1;  // graph position being planned
 
     planner(backend_state * b, const ggml_cgraph * g, const std::unordered_set<const ggml_tensor *> & nb = {},
@@ -483,6 +487,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         const int64_t row_bytes = (int64_t) w->nb[1];
         act_need = std::max(act_need, act_bytes(wtype, K, N));
         const bool reuse = act_src == x && act_wtype == wtype;
+        if (!reuse && unwritten.count(root_of(x))) return fail(t, "reads an output a fused launch never wrote");
         backend_state * b = be;
         const int ncu = n_cu;
         // the tile GEMM once the columns outgrow a few GEMV chunks (earlier for tall matrices)
@@ -1026,9 +1031,17 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     for (const ggml_tensor * f : fused) {
         if (f != F && (f->flags & GGML_TENSOR_FLAG_OUTPUT)) return false;
     }
-    // the kernel's output must not overlap what it reads (the projection rows)
     const tview vsrc = view_of(vn);
-    {
+    attn_step_args as{};
+    const ggml_tensor * oview = nullptr;
+    fattn_quant_out(iF, F, fa, oview);
+    // When the output projection consumes the quantized output this launch
+    // writes, nothing reads the f32 output: it goes to scratch, not to F's
+    // bytes (which an allocator may well have placed over the projection
+    // rows this launch reads). Any other reader of F then fails the plan.
+    const bool f32_unread = fa.qtype >= 0 && !(F->flags & GGML_TENSOR_FLAG_OUTPUT);
+    if (!f32_unread) {
+        // the kernel's output must not overlap what it reads (the projection rows)
         uintptr_t lo, hi, olo = (uintptr_t) F->data, ohi = olo + ggml_nbytes(F);
         const tview * reads[] = {&j0.a, &j1.a, &vsrc};
         for (const tview * v : reads) {
@@ -1036,9 +1049,6 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
             if (lo < ohi && olo < hi) return false;
         }
     }
-    attn_step_args as{};
-    const ggml_tensor * oview = nullptr;
-    fattn_quant_out(iF, F, fa, oview);
     as.fa = fa;
     as.qsrc = j0.a.data;
     as.q_nb1 = j0.a.nb[1];
@@ -1073,12 +1083,14 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     as.vc_nb2 = sv->nb[2];
     as.vc_nb3 = sv->nb[3];
     as.vc_rows = sv->ne[1];
-    as.out = (float *) F->data;
+    as.out = f32_unread ? nullptr : (float *) F->data;  // (nullptr: scratch, set at launch)
     if (fa.n_seq * 64 * sizeof(float2) > kRopeTableBytes) return false;
     for (const ggml_tensor * f : fused) {
         if (f != t) deferred[f] = f;
     }
-    gen_need = std::max(gen_need, attn_step_scratch_bytes(fa));
+    const size_t out_off = align_up(attn_step_scratch_bytes(fa), kAlign);
+    gen_need = std::max(gen_need, out_off + (f32_unread ? (size_t) ggml_nbytes(F) : 0));
+    if (f32_unread) unwritten.insert(F);
     backend_state * b = be;
     // the rotation table of this step's positions, once per graph (again if
     // another layer rotates differently)
@@ -1101,9 +1113,10 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
             attn_step_args la = as;
             la.rope = (const float2 *) rope_base(b);
             if (la.fa.qtype >= 0) la.fa.act = act_carve(la.fa.qtype, act_base(b), qK, qN);
+            if (!la.out) la.out = (float *) (gen_base(b) + out_off);
             launch_attn_step(la, gen_base(b), s);
         },
-        F, "attn_step", {F, sk, sv});
+        F, "attn_step", f32_unread ? std::vector<const ggml_tensor *>{sk, sv} : std::vector<const ggml_tensor *>{F, sk, sv});
     if (fa.qtype >= 0) {
         act_src = oview;
         act_wtype = fa.qtype;
@@ -1156,6 +1169,11 @@ bool planner::plan() {
         cur = i;
         if (is_view_op(t->op)) continue;
         if (!supports_op(be->dev, t)) return fail(t, "unsupported op or layout");
+        if (t->op != GGML_OP_MUL_MAT && !deferred.count(t)) {
+            for (int k = 0; k < GGML_MAX_SRC; k++)
+                if (t->src[k] && unwritten.count(root_of(t->src[k])))
+                    return fail(t, "reads an output a fused launch never wrote");
+        }
         if (bypass.count(t)) continue;  // readers take the CONT's source directly
         auto dit = deferred.find(t);
         if (dit != deferred.end() && dit->second == t) continue;  // produced by a fused predecessor
