@@ -70,6 +70,18 @@ void ggml_backend_mi355x_set_hip_graphs(ggml_backend_t backend, bool enabled);
  * (crates/openasr-core/src/ggml_runtime/cpu_graph.rs:7926-7947). */
 void ggml_backend_mi355x_refuse_next_launch(ggml_backend_t backend);
 
+/* Graph compute that allocates no device memory. No counterpart in the
+ * reference: it is for callers that cannot call hipMalloc (code under their
+ * own HIP-graph capture, tight serving loops, harnesses that forbid
+ * allocation). Same plan, kernels and results as ggml_backend_graph_compute
+ * on this backend, launched eagerly (no HIP-graph capture), with the plan's
+ * scratch in a fixed 64 MiB device array (one per device, held until the
+ * process ends; ggml_backend_mi355x_static_scratch_bytes reports its size).
+ * A graph whose plan needs more scratch returns GGML_STATUS_ALLOC_FAILED with
+ * a message. Calls that overlap on one device race on the shared array. */
+enum ggml_status ggml_backend_mi355x_graph_compute_static(ggml_backend_t backend, struct ggml_cgraph * cgraph);
+size_t ggml_backend_mi355x_static_scratch_bytes(void);
+
 #ifdef __cplusplus
 }
 #endif

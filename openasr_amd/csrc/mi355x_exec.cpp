@@ -34,12 +34,15 @@ constexpr size_t kAlign = 256;
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // scratch arena: [activation region][general region]
-char * act_base(const backend_state * be) { return be->scratch; }
+// (a compute given caller scratch points the plan at that instead of the arena)
+char * arena(const backend_state * be) { return be->scratch_override ? be->scratch_override : be->scratch; }
+size_t gen_offset(const backend_state * be) { return be->scratch_override ? be->override_gen_off : be->gen_off; }
+char * act_base(const backend_state * be) { return arena(be); }
 // the general region starts with the decode step's rope table (kept for the
 // whole graph); the rest is per-launch scratch
 constexpr size_t kRopeTableBytes = 64 * 1024;
-char * rope_base(const backend_state * be) { return be->scratch + be->gen_off; }
-char * gen_base(const backend_state * be) { return be->scratch + be->gen_off + kRopeTableBytes; }
+char * rope_base(const backend_state * be) { return arena(be) + gen_offset(be); }
+char * gen_base(const backend_state * be) { return arena(be) + gen_offset(be) + kRopeTableBytes; }
 
 bool is_view_op(enum ggml_op op) {
     return op == GGML_OP_NONE || op == GGML_OP_RESHAPE || op == GGML_OP_VIEW || op == GGML_OP_PERMUTE ||
@@ -1554,6 +1557,58 @@ enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg) {
     if (e != hipSuccess) return fail_with(be, e, "graph execution failed");
     if (be->launch_error.load() != 0) {
         // the kernels that did launch have finished (synchronized above)
+        std::fprintf(stderr, "mi355x: a launch was refused: %s\n",
+                     hipGetErrorString((hipError_t) be->launch_error.load()));
+        be->last_native_error = be->launch_error.load();
+        return GGML_STATUS_FAILED;
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
+enum ggml_status graph_compute_in(backend_state * be, ggml_cgraph * cg, char * scratch, size_t cap) {
+    if (be->poisoned) return GGML_STATUS_BACKEND_POISONED;
+    be->last_native_error = 0;
+    const int te = be->dev->transfer_error.exchange(0);
+    if (te != 0) return fail_with(be, (hipError_t) te, "an earlier tensor transfer failed");
+    be->launch_error.store(0);
+    error_scope scope(&be->launch_error);
+    MI_CHECK(hipSetDevice(be->dev->hip_id));
+    bool planned;
+    auto pp = make_plan(be, cg, planned);
+    planner & p = *pp;
+    if (!planned) {
+        std::fprintf(stderr, "mi355x: cannot plan graph: %s\n", p.error.c_str());
+        return GGML_STATUS_FAILED;
+    }
+    const size_t act = align_up(p.act_need, kAlign), gen = align_up(p.gen_need + kRopeTableBytes, kAlign);
+    if (act + gen > cap) {
+        std::fprintf(stderr,
+                     "mi355x: graph needs %zu bytes of scratch (activations %zu, partials and tables %zu); "
+                     "the caller's scratch holds %zu\n",
+                     act + gen, act, gen, cap);
+        return GGML_STATUS_ALLOC_FAILED;
+    }
+    struct override_guard {
+        backend_state * be;
+        ~override_guard() {
+            be->scratch_override = nullptr;
+            be->override_gen_off = 0;
+        }
+    } guard{be};
+    be->scratch_override = scratch;
+    be->override_gen_off = act;
+    be->last_observation = GGML_BACKEND_GRAPH_CANCEL_OBSERVATION_SUBMISSION_CHECKPOINT;
+    for (size_t k = 0; k < p.steps.size(); k++) {
+        if (be->abort_cb && be->abort_cb(be->abort_data)) {
+            (void) hipStreamSynchronize(be->stream);
+            return GGML_STATUS_ABORTED;
+        }
+        run_steps(be, p.steps, k, k + 1);
+    }
+    hipError_t e = hipGetLastError();
+    if (e == hipSuccess) e = hipStreamSynchronize(be->stream);
+    if (e != hipSuccess) return fail_with(be, e, "graph execution failed");
+    if (be->launch_error.load() != 0) {
         std::fprintf(stderr, "mi355x: a launch was refused: %s\n",
                      hipGetErrorString((hipError_t) be->launch_error.load()));
         be->last_native_error = be->launch_error.load();

@@ -38,6 +38,11 @@ struct device_state {
     // the last graph_compute on this device; that compute consumes it and
     // fails with it
     std::atomic<int> transfer_error{0};
+    // the device's copy of the fixed scratch array (mi355x_static.cpp), looked
+    // up once on first use
+    std::once_flag static_once;
+    char * static_scratch = nullptr;
+    hipError_t static_err = hipSuccess;
 };
 
 // Errors noted while an error_scope is active on the calling thread go to
@@ -101,12 +106,19 @@ struct backend_state {
     int64_t last_native_error = 0;     // hipError_t behind it
     std::atomic<int> launch_error{0};  // first error noted during the current graph_compute
     bool fail_next_launch = false;     // test seam: the next compute's first launch is refused
+    char * scratch_override = nullptr; // while graph_compute_in runs: the caller's scratch
+    size_t override_gen_off = 0;       // offset of its general region
     ggml_guid guid{};
     ggml_backend backend{};
     std::string name;
 };
 
 enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg);
+
+// graph_compute with the plan's scratch in [scratch, scratch + cap) instead of
+// the backend's arena: eager launches only (no HIP-graph capture), no device
+// allocation; GGML_STATUS_ALLOC_FAILED if the plan needs more than cap
+enum ggml_status graph_compute_in(backend_state * be, ggml_cgraph * cg, char * scratch, size_t cap);
 
 // executor scratch arena: the bytes running `cg` needs (false if the graph
 // cannot be planned), growing the arena to it, and releasing it (with the
