@@ -215,7 +215,11 @@ __device__ __forceinline__ void stage_quantize(const float4 (&x)[4], bool live, 
     }
 }
 
-// load this lane's 16 elements of job `job` (zeros outside the job range)
+// load this lane's 16 elements of job `job`; false outside the job range,
+// where the values (element 0 of the chunk's first column) are not used: the
+// users mask them, and the lanes that reduce together (a DPP row for Q8_K, a
+// lane pair for Q8_0) are all in range or all out, so no reduction sees them.
+// Masking here would make the load be waited for at once.
 __device__ __forceinline__ bool stage_load(const gemv_args & a, int n0, int jobs, int nspan, int job, int li,
                                            float4 (&x)[4]) {
     const int col = job / nspan, sp = job - col * nspan;
@@ -226,16 +230,15 @@ __device__ __forceinline__ bool stage_load(const gemv_args & a, int n0, int jobs
                         (ok ? e : 0);
 #pragma unroll
     for (int j = 0; j < 4; j++) x[j] = ((const float4 *) src)[j];
-    if (!ok) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) x[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-    }
     return ok;
 }
 
-// quantize-only staging: each wave streams its groups, one group's loads in flight at a time
-template <int WT>
-__device__ __forceinline__ void gemv_stage_quant(const gemv_args & a, int n0, int nc, char * smem) {
+// quantize-only staging: each wave streams its groups, two groups' loads in
+// flight at a time. The first two groups are requested before `issue` runs
+// (the caller's weight loads): loads return in issue order, so activations
+// requested first never wait behind the weights' HBM round trip.
+template <int WT, typename F>
+__device__ __forceinline__ void gemv_stage_quant(const gemv_args & a, int n0, int nc, char * smem, F && issue) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int row = lane >> 4, li = lane & 15;
     const int64_t K = a.K;
@@ -243,12 +246,19 @@ __device__ __forceinline__ void gemv_stage_quant(const gemv_args & a, int n0, in
     const int jobs = nc * nspan;
     const int groups = (jobs + 3) / 4;
     const gemv_lds L = gemv_lds_layout(WT, K, nc);
-    for (int gi = wave; gi < groups; gi += 2 * nw) {
-        // two groups per iteration, both loads issued before either is quantized
-        float4 x0[4], x1[4];
+    float4 x0[4], x1[4];
+    int gi = wave;
+    // clamped, unconditional loads (a job past the end reads element 0)
+    bool ok0 = stage_load(a, n0, jobs, nspan, 4 * gi + row, li, x0);
+    bool ok1 = stage_load(a, n0, jobs, nspan, 4 * (gi + nw) + row, li, x1);
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the caller's
+    issue();
+    for (; gi < groups; gi += 2 * nw) {
         const int j0 = 4 * gi + row, j1 = 4 * (gi + nw) + row;
-        const bool ok0 = stage_load(a, n0, jobs, nspan, j0, li, x0);
-        const bool ok1 = stage_load(a, n0, jobs, nspan, j1, li, x1);
+        if (gi != wave) {
+            ok0 = stage_load(a, n0, jobs, nspan, j0, li, x0);
+            ok1 = stage_load(a, n0, jobs, nspan, j1, li, x1);
+        }
         stage_quantize<WT>(x0, ok0, j0 / nspan, j0 % nspan, li, K, L, smem);
         if (gi + nw < groups) stage_quantize<WT>(x1, ok1, j1 / nspan, j1 % nspan, li, K, L, smem);
     }
@@ -260,8 +270,8 @@ __device__ __forceinline__ void gemv_stage_quant(const gemv_args & a, int n0, in
 // row by DPP, per column over the spans in order -- then
 // mean = sum / K, scale = 1 / sqrt(var + eps); the normalised value is
 // ((x - mean) * scale) * w (+ b), the roundings of NORM / RMS_NORM, MUL, ADD
-template <int WT, bool BIAS>
-__device__ __forceinline__ void gemv_stage_norm(const gemv_args & a, int n0, int nc, char * smem) {
+template <int WT, bool BIAS, typename F>
+__device__ __forceinline__ void gemv_stage_norm(const gemv_args & a, int n0, int nc, char * smem, F && issue) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const int row = lane >> 4, li = lane & 15;
     const int64_t K = a.K;
@@ -284,13 +294,15 @@ __device__ __forceinline__ void gemv_stage_norm(const gemv_args & a, int n0, int
             if constexpr (BIAS) b[k][j] = *(const float4 *) (p.b + e + 4 * j);
         }
     }
+    __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the caller's
+    issue();  // the caller's weight loads, behind the activations
     const double n = (double) K;
     if (p.norm == 1) {
 #pragma unroll
         for (int k = 0; k < kNormGroups; k++) {
             double s = 0.0;
 #pragma unroll
-            for (int t = 0; t < 16; t++) s += (double) elem16(x[k], t);
+            for (int t = 0; t < 16; t++) s += ok[k] ? (double) elem16(x[k], t) : 0.0;
             s = row16_sum(s);
             const int job = 4 * (wave + nw * k) + row;
             if (li == 0 && job < jobs) s_part[job] = s;
@@ -350,59 +362,66 @@ __device__ __forceinline__ void gemv_stage_norm(const gemv_args & a, int n0, int
     __syncthreads();
 }
 
-// wave partials summed in wave order by wave 0, then stored. Waves
-// [0, half) hold W's partials, waves [half, nw) W2's when there is a second
-// matrix; the epilogue then writes silu(W x) * (W2 x) -- the SwiGLU gate of
-// nn/ffn.rs:64-91 with the same roundings as MUL_MAT, SILU and MUL apart.
-// A residual, when given, is added to the rounded product.
-// the residual values wave 0 adds in the epilogue, requested at kernel start
-__device__ __forceinline__ void gemv_res_prefetch(const gemv_args & a, int64_t row, int n0, float (&res)[4]) {
-    const int g = (threadIdx.x & 63) >> 4;
-    if (!a.res) {
+// Split-K finish. Every wave puts its partials in LDS; after one barrier
+// each thread takes outputs o = tid, tid + 64 nw, ... of the tile (row o % 16,
+// column o / 16) and sums that output's partials in wave order -- waves
+// [0, half) hold W's, waves [half, nw) W2's when there is a second matrix,
+// whose epilogue then writes silu(W x) * (W2 x), the SwiGLU gate of
+// nn/ffn.rs:64-91 with the roundings of MUL_MAT, SILU and MUL apart. A
+// residual, when given, is added to the rounded product. The sums run in the
+// order a single wave would have added them, so the bits do not depend on
+// which thread finishes an output.
+constexpr int kFinishPerThread = 4;  // 16 x 16 outputs over at least one wave
+
+// the residual of this thread's outputs, requested early. The loads are
+// unconditional (clamped; without a residual they read the output tensor and
+// the value is not used): a load behind a branch would make every later wait
+// count it as outstanding on both paths.
+__device__ __forceinline__ void gemv_res_prefetch(const gemv_args & a, int64_t tile, int n0, int nc,
+                                                  float (&res)[kFinishPerThread]) {
+    const int nt = (int) blockDim.x;
+    const char * base = a.res ? a.res : a.dst;
+    const int64_t nb1 = a.res ? a.res_nb1 : a.dst_nb1;
 #pragma unroll
-        for (int i = 0; i < 4; i++) res[i] = 0.0f;
-        return;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int n = n0 + 4 * g + i;
-        res[i] = *(const float *) (a.res + (int64_t) (n < a.N ? n : n0) * a.res_nb1 + row * 4);
+    for (int k = 0; k < kFinishPerThread; k++) {
+        int o = (int) threadIdx.x + k * nt;
+        o = o < 16 * nc ? o : 0;
+        res[k] = *(const float *) (base + (int64_t) (n0 + (o >> 4)) * nb1 + (tile * 16 + (o & 15)) * 4);
     }
 }
 
-__device__ __forceinline__ void gemv_finish(const gemv_args & a, double (&acc)[4], double (*s_red)[64][4], int64_t row,
-                                            int n0, int nc, int half, const float (&res)[4]) {
+__device__ __forceinline__ void gemv_finish(const gemv_args & a, const double (&acc)[4], double (*s_red)[64][4],
+                                            int64_t tile, int n0, int nc, int half, const float (&res)[kFinishPerThread]) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int g = lane >> 4;
-    double acc2[4] = {0.0, 0.0, 0.0, 0.0};
-    if (nw > 1) {
-        if (wave > 0) {
 #pragma unroll
-            for (int i = 0; i < 4; i++) s_red[wave][lane][i] = acc[i];
+    for (int i = 0; i < 4; i++) s_red[wave][lane][i] = acc[i];
+    __syncthreads();
+    const int nt = 64 * nw;
+#pragma unroll
+    for (int k = 0; k < kFinishPerThread; k++) {
+        const int o = (int) threadIdx.x + k * nt;
+        if (o >= 16 * nc) break;
+        const int r = o & 15, n = o >> 4;
+        const int sl = r + 16 * (n >> 2), si = n & 3;  // the MFMA lane and slot holding (row r, column n)
+        double v = s_red[0][sl][si];
+#pragma unroll
+        for (int w = 1; w < 16; w++) {
+            const double pw = s_red[w][sl][si];  // in bounds for every w; added only for w < half
+            v = w < half ? v + pw : v;
         }
-        __syncthreads();
-        if (wave != 0) return;
-        for (int w = 1; w < half; w++) {
+        float f = (float) v;
+        if (a.W2) {
+            double v2 = 0.0;
 #pragma unroll
-            for (int i = 0; i < 4; i++) acc[i] += s_red[w][lane][i];
-        }
-        for (int w = half; w < nw; w++) {
-#pragma unroll
-            for (int i = 0; i < 4; i++) acc2[i] += s_red[w][lane][i];
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int n = n0 + 4 * g + i;
-        if (4 * g + i < nc) {  // the workgroup's columns (nc <= N - n0)
-            float v = (float) acc[i];
-            if (a.W2) {
-                const float u = (float) acc2[i];
-                v = (v / (1.0f + expf_det(-v))) * u;
+            for (int w = 1; w < 16; w++) {
+                const double pw = s_red[w][sl][si];
+                v2 = w >= half && w < nw ? v2 + pw : v2;
             }
-            if (a.res) v = res[i] + v;
-            *(float *) (a.dst + (int64_t) n * a.dst_nb1 + row * 4) = v;
+            const float u = (float) v2;
+            f = (f / (1.0f + expf_det(-f))) * u;
         }
+        if (a.res) f = res[k] + f;
+        *(float *) (a.dst + (int64_t) (n0 + n) * a.dst_nb1 + (tile * 16 + r) * 4) = f;
     }
 }
 
@@ -427,15 +446,17 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
     uint4 hdr;
     long q[4];
     int64_t sb = wv;
-    {
+    float res[kFinishPerThread];
+    // the first unit's weights and the residual; with a prologue they are
+    // requested right after the activations the prologue waits for
+    auto issue = [&]() {
+        gemv_res_prefetch(a, tile, n0, nc, res);
         // waves without a unit (staging helpers) read unit 0 and never use it
         const char * blk = wrow + (sb < nsb ? sb : 0) * 144;
         hdr = *(const uint4 *) blk;
 #pragma unroll
         for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
-    }
-    float res[4];
-    gemv_res_prefetch(a, row, n0, res);
+    };
     // activation operands: LDS after the prologue, else the global buffers
     const int8_t * aq;
     const float * adp;
@@ -443,8 +464,8 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
     int64_t q_stride, d_stride, ss_stride;
     int c0;  // column index of the chunk's first column in the operand arrays
     if constexpr (PRO != kProNone) {
-        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q4_K>(a, n0, nc, smem);
-        else gemv_stage_norm<GGML_TYPE_Q4_K, PRO == kProNormBias>(a, n0, nc, smem);
+        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q4_K>(a, n0, nc, smem, issue);
+        else gemv_stage_norm<GGML_TYPE_Q4_K, PRO == kProNormBias>(a, n0, nc, smem, issue);
         const gemv_lds L = gemv_lds_layout(GGML_TYPE_Q4_K, a.K, nc);
         aq = (const int8_t *) (smem + L.q_off);
         adp = (const float *) (smem + L.d_off);
@@ -454,6 +475,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
         ss_stride = L.ss_stride;
         c0 = 0;
     } else {
+        issue();
         aq = a.aq;
         adp = a.ad;
         asp = a.ass;
@@ -492,7 +514,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
             for (int c = 0; c < 4; c++) q[c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
         }
     }
-    gemv_finish(a, acc, s_red, row, n0, nc, half, res);
+    gemv_finish(a, acc, s_red, tile, n0, nc, half, res);
 }
 
 // Q8_0 weights in the row-split layout [K quants][K/32 f16 scales]; the waves
@@ -517,21 +539,24 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
     long q[kQ8Group];
     uint16_t ds[kQ8Group];
     int64_t b0 = (int64_t) wv * kQ8Group;
+    float res[kFinishPerThread];
+    // the first group's weights and the residual, behind the prologue's activations
+    auto issue = [&]() {
+        gemv_res_prefetch(a, tile, n0, nc, res);
 #pragma unroll
-    for (int u = 0; u < kQ8Group; u++) {
-        const int64_t b = b0 + u < nblk ? b0 + u : 0;  // clamped; past-the-end blocks are never used
-        q[u] = *(const long *) (wrow + b * 32 + 8 * g);
-        ds[u] = wsc[b];
-    }
-    float res[4];
-    gemv_res_prefetch(a, row, n0, res);
+        for (int u = 0; u < kQ8Group; u++) {
+            const int64_t b = b0 + u < nblk ? b0 + u : 0;  // clamped; past-the-end blocks are never used
+            q[u] = *(const long *) (wrow + b * 32 + 8 * g);
+            ds[u] = wsc[b];
+        }
+    };
     const int8_t * aq;
     const float * adp;
     int64_t q_stride, d_stride;
     int c0;
     if constexpr (PRO != kProNone) {
-        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q8_0>(a, n0, nc, smem);
-        else gemv_stage_norm<GGML_TYPE_Q8_0, PRO == kProNormBias>(a, n0, nc, smem);
+        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q8_0>(a, n0, nc, smem, issue);
+        else gemv_stage_norm<GGML_TYPE_Q8_0, PRO == kProNormBias>(a, n0, nc, smem, issue);
         const gemv_lds L = gemv_lds_layout(GGML_TYPE_Q8_0, a.K, nc);
         aq = (const int8_t *) (smem + L.q_off);
         adp = (const float *) (smem + L.d_off);
@@ -539,6 +564,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
         d_stride = L.d_stride;
         c0 = 0;
     } else {
+        issue();
         aq = a.aq;
         adp = a.ad;
         q_stride = a.K;
@@ -587,7 +613,7 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q8_0(gemv_args a) {
         }
         q8_0_unit(q, ds, af, ad, (int) (nblk - b0 < kQ8Group ? nblk - b0 : kQ8Group), acc);
     }
-    gemv_finish(a, acc, s_red, row, n0, nc, half, res);
+    gemv_finish(a, acc, s_red, tile, n0, nc, half, res);
 }
 
 // Streaming form for tall matrices with pre-quantized activations (the
@@ -759,42 +785,47 @@ __global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
     const int passes = (int) ((K + 1023) / 1024);
     uint4 wq[R][kG1MaxPasses], wq2[R][kG1MaxPasses];
     uint16_t ws[R][kG1MaxPasses], ws2[R][kG1MaxPasses];
+    float res[R], res2[R];
+    // the rows' weights and residuals; with a prologue they are requested
+    // right after the column the prologue waits for (loads return in order)
+    auto issue = [&]() {
 #pragma unroll
-    for (int j = 0; j < R; j++) {
-        const int64_t rr = row0 + j < M ? row0 + j : 0;  // clamped, never stored
-        const char * wrow = Wm + rr * a.row_bytes;
-        const char * wrow2 = a.W2 ? a.W2 + rr * a.row_bytes : nullptr;
+        for (int j = 0; j < R; j++) {
+            const int64_t rr = row0 + j < M ? row0 + j : 0;  // clamped, never stored
+            const char * wrow = Wm + rr * a.row_bytes;
+            const char * wrow2 = a.W2 ? a.W2 + rr * a.row_bytes : nullptr;
 #pragma unroll
-        for (int p = 0; p < kG1MaxPasses; p++) {
-            if (p < passes) {
-                const int64_t e = (int64_t) p * 1024 + 16 * lane;
-                const int64_t ec = e < K ? e : 0;  // clamped, masked below
-                wq[j][p] = *(const uint4 *) (wrow + ec);
-                ws[j][p] = ((const uint16_t *) (wrow + K))[ec / 32];
-                if (wrow2) {
-                    wq2[j][p] = *(const uint4 *) (wrow2 + ec);
-                    ws2[j][p] = ((const uint16_t *) (wrow2 + K))[ec / 32];
+            for (int p = 0; p < kG1MaxPasses; p++) {
+                if (p < passes) {
+                    const int64_t e = (int64_t) p * 1024 + 16 * lane;
+                    const int64_t ec = e < K ? e : 0;  // clamped, masked below
+                    wq[j][p] = *(const uint4 *) (wrow + ec);
+                    ws[j][p] = ((const uint16_t *) (wrow + K))[ec / 32];
+                    if (wrow2) {
+                        wq2[j][p] = *(const uint4 *) (wrow2 + ec);
+                        ws2[j][p] = ((const uint16_t *) (wrow2 + K))[ec / 32];
+                    }
                 }
             }
         }
-    }
-    float res[R], res2[R];
 #pragma unroll
-    for (int j = 0; j < R; j++) {
-        const int64_t rr = row0 + j < M ? row0 + j : 0;
-        res[j] = res2[j] = 0.0f;
-        if (resp && lane == 0) res[j] = *(const float *) (resp + rr * 4);
-        if (a.epi.res2 && lane == 0) res2[j] = *(const float *) (a.epi.res2 + rr * 4);
-    }
+        for (int j = 0; j < R; j++) {
+            const int64_t rr = row0 + j < M ? row0 + j : 0;
+            res[j] = res2[j] = 0.0f;
+            if (resp && lane == 0) res[j] = *(const float *) (resp + rr * 4);
+            if (a.epi.res2 && lane == 0) res2[j] = *(const float *) (a.epi.res2 + rr * 4);
+        }
+    };
     const int8_t * aq;
     const float * adp;
     if constexpr (PRO != kProNone) {
-        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q8_0>(a, 0, 1, smem);
-        else gemv_stage_norm<GGML_TYPE_Q8_0, PRO == kProNormBias>(a, 0, 1, smem);
+        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q8_0>(a, 0, 1, smem, issue);
+        else gemv_stage_norm<GGML_TYPE_Q8_0, PRO == kProNormBias>(a, 0, 1, smem, issue);
         const gemv_lds L = gemv_lds_layout(GGML_TYPE_Q8_0, K, 1);
         aq = (const int8_t *) (smem + L.q_off);
         adp = (const float *) (smem + L.d_off);
     } else {
+        issue();
         aq = a.aq;
         adp = a.ad;
     }
