@@ -322,6 +322,19 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t prow = (int64_t) t.gti * R;
     const int nc = a.n_chunks;
+    // the chunk maxima and sums of this wave's row first (clamped loads: up to
+    // kFaMaxChunks / 64 per lane), then every partial this thread combines, so
+    // that the weights are computed while the partials are still in flight
+    constexpr int MPL = kFaMaxChunks / 64;
+    const int r_w = wave < t.nrows ? wave : 0;  // rows >= 4 handled below
+    float mreg[MPL], lreg[MPL];
+#pragma unroll
+    for (int q = 0; q < MPL; q++) {
+        const int i = lane + 64 * q;
+        const int ic = i < nc ? i : 0;
+        mreg[q] = part_m[(prow + r_w) * nc + ic];
+        lreg[q] = part_l[(prow + r_w) * nc + ic];
+    }
     int er[NE], ed[NE];
     bool ev[NE];
     float pv[NE][CB];
@@ -336,13 +349,26 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
         for (int k = 0; k < CB; k++) pv[e][k] = pa[(int64_t) min(k, nc - 1) * D];
     }
     for (int r = wave; r < t.nrows; r += 4) {
+        if (r != r_w) {  // a wave with a second row (tiles of more than 4 rows) loads it now
+#pragma unroll
+            for (int q = 0; q < MPL; q++) {
+                const int i = lane + 64 * q;
+                const int ic = i < nc ? i : 0;
+                mreg[q] = part_m[(prow + r) * nc + ic];
+                lreg[q] = part_l[(prow + r) * nc + ic];
+            }
+        }
         float M = -INFINITY;
-        for (int i = lane; i < nc; i += 64) M = fmaxf(M, part_m[(prow + r) * nc + i]);
+#pragma unroll
+        for (int q = 0; q < MPL; q++) M = lane + 64 * q < nc ? fmaxf(M, mreg[q]) : M;
         M = wave_max(M);
-        for (int i = lane; i < nc; i += 64) {
-            const float mc = part_m[(prow + r) * nc + i];
-            s_w[r][i] = mc == -INFINITY ? 0.0 : (double) expf_det(mc - M);
-            s_l[r][i] = (double) part_l[(prow + r) * nc + i];
+#pragma unroll
+        for (int q = 0; q < MPL; q++) {
+            const int i = lane + 64 * q;
+            if (i < nc) {
+                s_w[r][i] = mreg[q] == -INFINITY ? 0.0 : (double) expf_det(mreg[q] - M);
+                s_l[r][i] = (double) lreg[q];
+            }
         }
     }
     __syncthreads();
@@ -451,12 +477,23 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     // STEP: the query's inputs, normalised and rotated once the K/V loads are in flight
     float qx0 = 0.0f, qx1 = 0.0f, qw0 = 0.0f, qw1 = 0.0f;
     float2 qcs = make_float2(0.0f, 0.0f);
+    // STEP: the new K / V row's inputs, requested with the query's (every wave:
+    // which one holds this step's position is known only with the index)
+    float kx0 = 0.0f, kx1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f;
     if constexpr (STEP) {
         const char * ip = st.idx + (int64_t) (kvh % st.idx_ne1) * st.idx_nb1 + (int64_t) (seq % st.idx_ne2) * st.idx_nb2;
         const float * qx = (const float *) (st.qsrc + (int64_t) head * st.q_nb1 + (int64_t) seq * st.q_nb2);
         const float x0 = qx[lane], x1 = qx[lane + 64];
         const float w0 = st.qw[lane], w1 = st.qw[lane + 64];
         const float2 cs = st.rope[seq * 64 + lane];
+        const float * kxp = (const float *) (st.ksrc + (int64_t) kvh * st.k_nb1 + (int64_t) seq * st.k_nb2);
+        kx0 = kxp[lane];
+        kx1 = kxp[lane + 64];
+        kw0 = st.kw[lane];
+        kw1 = st.kw[lane + 64];
+        const float * vxp = (const float *) (st.vsrc + (int64_t) kvh * st.v_nb1 + (int64_t) seq * st.v_nb2);
+        vx0 = vxp[lane];
+        vx1 = vxp[lane + 64];
         if (lane < clen) {
             mv = 0.0f;
             if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
@@ -525,13 +562,10 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
             // this step's K / V rows: K replaces the LDS row jn (after the
             // transposing stores above, in program order within the wave), V
             // goes through LDS to the dims layout
-            const float * kx = (const float *) (st.ksrc + (int64_t) kvh * st.k_nb1 + (int64_t) seq * st.k_nb2);
             float y0, y1;
-            as_norm_rope(kx[lane], kx[lane + 64], st.kw[lane], st.kw[lane + 64], st.rope[seq * 64 + lane], st.k_eps, y0,
-                         y1);
+            as_norm_rope(kx0, kx1, kw0, kw1, qcs, st.k_eps, y0, y1);
             const uint16_t k0 = float_to_half_bits(y0), k1 = float_to_half_bits(y1);
-            const float * vsp = (const float *) (st.vsrc + (int64_t) kvh * st.v_nb1 + (int64_t) seq * st.v_nb2);
-            const uint16_t v0 = float_to_half_bits(vsp[lane]), v1 = float_to_half_bits(vsp[lane + 64]);
+            const uint16_t v0 = float_to_half_bits(vx0), v1 = float_to_half_bits(vx1);
             uint16_t * krow = (uint16_t *) &s_k[wave][jn][0];
             krow[lane] = k0;
             krow[lane + 64] = k1;
