@@ -134,10 +134,15 @@ int oa_qwen_read_kv(const oa_qwen_session * s, int layer, int seq, uint16_t * k_
 struct ggml_cgraph * oa_qwen_decode_graph(oa_qwen_session * s);
 
 /* Degenerate n-gram guard (seq2seq_greedy_decode.rs:569-605): smallest n in
- * 1..max_ngram whose trailing n-gram repeats at least 8 (n=1), 6 (n=2) or 4
- * (n>=3) times back to back. Returns the length to keep (truncating the run
- * to one occurrence), or -1 when no loop is detected. */
-int oa_detect_degenerate_ngram(const int32_t * tokens, int len, int max_ngram, int * ngram_len, int * repeats);
+ * 1..max_ngram whose trailing n-gram repeats at least bounds[n - 1] times
+ * back to back (the reference's max_consecutive_repeats(n) function as a
+ * table; a bound of 0 disables that length). bounds == NULL selects the
+ * shipped tiers, default_max_consecutive_ngram_repeats (:51-58): 8 for n=1,
+ * 6 for n=2, 4 for n>=3. Returns the length to keep (the run truncated to one
+ * occurrence: len - (repeats - 1) * n), or -1 when no loop is detected (also
+ * for max_ngram 0 or an empty tail). */
+int oa_detect_degenerate_ngram(const int32_t * tokens, int len, int max_ngram, const int * bounds, int * ngram_len,
+                               int * repeats);
 
 /*
  * Whisper decoder (models/whisper/ggml_decoder_graph.rs): reusable one-token

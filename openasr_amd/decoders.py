@@ -108,7 +108,7 @@ def lib() -> C.CDLL:
     s("oa_whisper_decode_graph", vp, vp)
     s("oa_qwen_generate", i, vp, vp, i, vp, vp)
     s("oa_qwen_read_kv", i, vp, i, i, vp, vp)
-    s("oa_detect_degenerate_ngram", i, vp, i, i, vp, vp)
+    s("oa_detect_degenerate_ngram", i, vp, i, i, vp, vp, vp)
     s("oa_qwen_decode_graph", vp, vp)
     _lib = L
     return L
@@ -374,10 +374,17 @@ def whisper_inputs(shape: dict, n_prompt: int = 4, seed: int = 91):
     return enc, prompt
 
 
-def detect_degenerate_ngram(tokens, max_ngram: int = 8):
+def detect_degenerate_ngram(tokens, max_ngram: int = 8, bound=None):
+    """(keep_len, ngram_len, repeats) when the tail ends in a loop, else None.
+    bound: a function of the cycle length (the reference's
+    max_consecutive_repeats), or None for the shipped 8/6/4 tiers."""
     t = np.ascontiguousarray(tokens, dtype=np.int32)
     n, r = C.c_int(0), C.c_int(0)
-    keep = lib().oa_detect_degenerate_ngram(t.ctypes.data, len(t), max_ngram, C.byref(n), C.byref(r))
+    table = None
+    if bound is not None and max_ngram > 0:
+        table = np.array([bound(k) for k in range(1, max_ngram + 1)], np.int32)
+    keep = lib().oa_detect_degenerate_ngram(t.ctypes.data if t.size else None, len(t), max_ngram,
+                                            table.ctypes.data if table is not None else None, C.byref(n), C.byref(r))
     return None if keep < 0 else (keep, n.value, r.value)
 
 

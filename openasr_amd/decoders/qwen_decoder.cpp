@@ -505,13 +505,18 @@ int oa_qwen_read_kv(const oa_qwen_session * s, int layer, int seq, uint16_t * k_
 
 struct ggml_cgraph * oa_qwen_decode_graph(oa_qwen_session * s) { return s->decode.gf; }
 
-int oa_detect_degenerate_ngram(const int32_t * tokens, int len, int max_ngram, int * ngram_len, int * repeats) {
+int oa_detect_degenerate_ngram(const int32_t * tokens, int len, int max_ngram, const int * bounds, int * ngram_len,
+                               int * repeats) {
+    if (!tokens || len <= 0) return -1;
     for (int n = 1; n <= max_ngram; n++) {
-        const int bound = n == 1 ? 8 : (n == 2 ? 6 : 4);
-        if (len < n * bound) continue;
+        // the bound for this cycle length: the caller's, else the shipped
+        // tiers (seq2seq_greedy_decode.rs:51-58); 0 disables this length
+        const int bound = bounds ? bounds[n - 1] : (n == 1 ? 8 : (n == 2 ? 6 : 4));
+        if (bound <= 0) continue;
+        if ((int64_t) len < (int64_t) n * bound) continue;
         const int32_t * tail = tokens + len - n;
         int r = 1;
-        while ((r + 1) * n <= len && std::memcmp(tokens + len - (r + 1) * n, tail, (size_t) n * 4) == 0) r++;
+        while ((int64_t) (r + 1) * n <= len && std::memcmp(tokens + len - (r + 1) * n, tail, (size_t) n * 4) == 0) r++;
         if (r >= bound) {
             if (ngram_len) *ngram_len = n;
             if (repeats) *repeats = r;
