@@ -133,21 +133,50 @@ __device__ __forceinline__ double row16_sum(double v) {
     return v;
 }
 
-// signed value of largest magnitude over the row, first element on ties
-template <int CTRL>
-__device__ __forceinline__ void row16_best_step(float & ab, float & best, int & idx) {
-    const float oab = dpp_f<CTRL>(ab), obest = dpp_f<CTRL>(best);
-    const int oidx = dpp_i<CTRL>(idx);
-    if (oab > ab || (oab == ab && oidx < idx)) {
-        ab = oab;
-        best = obest;
-        idx = oidx;
-    }
+// f32 max / min over the 16 lanes of a row (every lane gets the result)
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp_f<kDppXor1>(v));
+    v = fmaxf(v, dpp_f<kDppXor2>(v));
+    v = fmaxf(v, dpp_f<kDppRor4>(v));
+    return fmaxf(v, dpp_f<kDppRor8>(v));
+}
+__device__ __forceinline__ float row16_min(float v) {
+    v = fminf(v, dpp_f<kDppXor1>(v));
+    v = fminf(v, dpp_f<kDppXor2>(v));
+    v = fminf(v, dpp_f<kDppRor4>(v));
+    return fminf(v, dpp_f<kDppRor8>(v));
+}
+__device__ __forceinline__ int row16_min_i(int v) {
+    v = min(v, dpp_i<kDppXor1>(v));
+    v = min(v, dpp_i<kDppXor2>(v));
+    v = min(v, dpp_i<kDppRor4>(v));
+    return min(v, dpp_i<kDppRor8>(v));
 }
 
 __device__ __forceinline__ float elem16(const float4 (&x)[4], int t) {
     const float4 & v = x[t >> 2];
     return (t & 3) == 0 ? v.x : (t & 3) == 1 ? v.y : (t & 3) == 2 ? v.z : v.w;
+}
+
+// Round-to-nearest-even of y (|y| < 2^22) by adding 1.5 * 2^23: the sum's
+// low mantissa bits are the integer in two's complement (ggml's nearest_int
+// does exactly this), so the low byte of the sum's bits is the int8 quant.
+constexpr float kRneMagic = 12582912.0f;
+
+// the low bytes of four such sums packed into one word, element a lowest
+__device__ __forceinline__ uint32_t pack_low_bytes(float a, float b, float c, float d) {
+    const uint32_t lo = __builtin_amdgcn_perm(__float_as_uint(b), __float_as_uint(a), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(__float_as_uint(d), __float_as_uint(c), 0x04000c0cu);
+    return lo | hi;
+}
+
+// quants of 16 elements times s, packed four to a word
+__device__ __forceinline__ void quant16(const float4 (&x)[4], float s, uint32_t (&w)[4]) {
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        w[j] = pack_low_bytes(s * x[j].x + kRneMagic, s * x[j].y + kRneMagic, s * x[j].z + kRneMagic,
+                              s * x[j].w + kRneMagic);
+    }
 }
 
 // Quantize one row's span into LDS. Q8_K (quantize_row_q8_K_ref): the
@@ -156,6 +185,12 @@ __device__ __forceinline__ float elem16(const float4 (&x)[4], int t) {
 // quants (two lanes). Q8_0 (x86 ggml-cpu rule): per 32 elements (two lanes)
 // d = amax/127 stored as f16, quants rne(x * 127/amax). Same arithmetic as
 // quantize_q8_K_wave / quantize_q8_0_group.
+//
+// The Q8_K maximum comes from the row's signed max and min: when only one of
+// +amax / -amax occurs it is the value of largest magnitude whatever its
+// position, so the first-on-ties search runs only for a row holding both.
+// |iscale x| <= 127 (1 + 2^-24)^2 < 127.5, so the min(127, .) never binds
+// and the quant is the rounded product alone.
 template <int WT>
 __device__ __forceinline__ void stage_quantize(const float4 (&x)[4], bool live, int col, int sp, int li, int64_t K,
                                                const gemv_lds & L, char * smem) {
@@ -163,34 +198,39 @@ __device__ __forceinline__ void stage_quantize(const float4 (&x)[4], bool live, 
     float * s_d = (float *) (smem + L.d_off);
     int16_t * s_ss = (int16_t *) (smem + L.ss_off);
     const int64_t e = (int64_t) sp * 256 + 16 * li;  // first element of this lane
-    int qv[16];
+    uint32_t w[4];
     if constexpr (WT == GGML_TYPE_Q4_K) {
-        float best = x[0].x, ab = fabsf(x[0].x);
-        int idx = 16 * li;
+        float hi = x[0].x, lo = x[0].x;
 #pragma unroll
         for (int t = 1; t < 16; t++) {
-            const float v = elem16(x, t);
-            if (fabsf(v) > ab) {
-                ab = fabsf(v);
-                best = v;
-                idx = 16 * li + t;
-            }
+            hi = fmaxf(hi, elem16(x, t));
+            lo = fminf(lo, elem16(x, t));
         }
-        row16_best_step<kDppXor1>(ab, best, idx);
-        row16_best_step<kDppXor2>(ab, best, idx);
-        row16_best_step<kDppRor4>(ab, best, idx);
-        row16_best_step<kDppRor8>(ab, best, idx);
-        const float iscale = ab == 0.0f ? 0.0f : -127.0f / best;
+        hi = row16_max(hi);
+        lo = row16_min(lo);
+        const float amax = fmaxf(hi, -lo);
+        float best = hi >= -lo ? hi : lo;
+        if (hi == -lo && amax != 0.0f) {
+            // both signs reach amax (uniform over the row): the first such
+            // element in order decides; key = 2 * index + sign
+            int key = 0x7fffffff;
+#pragma unroll
+            for (int t = 15; t >= 0; t--) {
+                const float v = elem16(x, t);
+                if (fabsf(v) == amax) key = 2 * (16 * li + t) + (v < 0.0f ? 1 : 0);
+            }
+            key = row16_min_i(key);
+            best = (key & 1) ? lo : hi;
+        }
+        const float iscale = amax == 0.0f ? 0.0f : -127.0f / best;
+        quant16(x, iscale, w);
         int ssum = 0;
 #pragma unroll
-        for (int t = 0; t < 16; t++) {
-            qv[t] = ab == 0.0f ? 0 : min(127, __float2int_rn(iscale * elem16(x, t)));
-            ssum += qv[t];
-        }
+        for (int j = 0; j < 4; j++) ssum = __builtin_amdgcn_sdot4((int) w[j], 0x01010101, ssum, false);
         ssum += dpp_i<kDppXor1>(ssum);
         if (live) {
             if ((li & 1) == 0) s_ss[col * L.ss_stride + e / 32] = (int16_t) ssum;
-            if (li == 0) s_d[col * L.d_stride + sp] = ab == 0.0f ? 0.0f : 1.0f / iscale;
+            if (li == 0) s_d[col * L.d_stride + sp] = amax == 0.0f ? 0.0f : 1.0f / iscale;
         }
     } else {
         float amax = 0.0f;
@@ -199,20 +239,11 @@ __device__ __forceinline__ void stage_quantize(const float4 (&x)[4], bool live, 
         amax = fmaxf(amax, dpp_f<kDppXor1>(amax));
         const float dd = amax / 127.0f;
         const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
-#pragma unroll
-        for (int t = 0; t < 16; t++) qv[t] = __float2int_rn(elem16(x, t) * id);
+        quant16(x, id, w);
         live = live && e < K;  // Q8_0 spans may end early; whole lane pairs drop out
         if (live && (li & 1) == 0) s_d[col * L.d_stride + e / 32] = round_to_half(dd);
     }
-    if (live) {
-        uint32_t w[4];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            w[j] = (uint32_t) (qv[4 * j] & 0xFF) | ((uint32_t) (qv[4 * j + 1] & 0xFF) << 8) |
-                   ((uint32_t) (qv[4 * j + 2] & 0xFF) << 16) | ((uint32_t) (qv[4 * j + 3] & 0xFF) << 24);
-        }
-        *(uint4 *) (s_q + col * L.q_stride + e) = make_uint4(w[0], w[1], w[2], w[3]);
-    }
+    if (live) *(uint4 *) (s_q + col * L.q_stride + e) = make_uint4(w[0], w[1], w[2], w[3]);
 }
 
 // load this lane's 16 elements of job `job`; false outside the job range,
@@ -344,12 +375,21 @@ __device__ __forceinline__ void gemv_stage_norm(const gemv_args & a, int n0, int
         const int col = ok[k] ? job / nspan : 0;
         const float2 st = s_stat[col];
         float4 v[4];
+        // RMS norm: x - 0 == x bit for bit, so the subtraction is skipped
+        const float4 * xs = x[k];
+        float4 xc[4];
+        if (p.norm == 1) {
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                xc[j] = make_float4(x[k][j].x - st.x, x[k][j].y - st.x, x[k][j].z - st.x, x[k][j].w - st.x);
+            xs = xc;
+        }
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            v[j].x = ((x[k][j].x - st.x) * st.y) * w[k][j].x;
-            v[j].y = ((x[k][j].y - st.x) * st.y) * w[k][j].y;
-            v[j].z = ((x[k][j].z - st.x) * st.y) * w[k][j].z;
-            v[j].w = ((x[k][j].w - st.x) * st.y) * w[k][j].w;
+            v[j].x = (xs[j].x * st.y) * w[k][j].x;
+            v[j].y = (xs[j].y * st.y) * w[k][j].y;
+            v[j].z = (xs[j].z * st.y) * w[k][j].z;
+            v[j].w = (xs[j].w * st.y) * w[k][j].w;
             if constexpr (BIAS) {
                 v[j].x += b[k][j].x;
                 v[j].y += b[k][j].y;

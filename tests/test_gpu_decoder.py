@@ -66,12 +66,12 @@ def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed
           f"min top1-top2 margin {min_margin:.3e}")
     if check_logits:
         assert max_dl < 1e-2
-    # the device KV cache holds what the reference wrote
-    k, v = sess.read_kv(shape["n_layers"] - 1, n_seq - 1)
+    # the device KV cache holds exactly what the reference wrote, every layer
     n = sess.position(n_seq - 1)
-    rk = r.k[-1][:, :n].view(np.float16).astype(np.float32)
-    gk = k[:, :n].view(np.float16).astype(np.float32)
-    assert np.abs(rk - gk).max() <= 2e-2 * np.abs(rk).max()
+    for layer in range(shape["n_layers"]):
+        k, v = sess.read_kv(layer, n_seq - 1)
+        assert np.array_equal(k[:, :n], r.k[layer][:, :n]), f"K cache layer {layer}"
+        assert np.array_equal(v[:, :n], r.v[layer][:, :n]), f"V cache layer {layer}"
     sess.free()
     model.free()
     if weights is None:
@@ -245,6 +245,36 @@ def test_qwen3_17b_q4_K_batch8_long_context(gpu, ref):
         assert np.array_equal(cur_d, cur_r), f"step {i}: gpu {cur_d} != cpu {cur_r}"
     print(f"  64 batched steps token-exact, max |dlogit| {max_dl:.2e}", flush=True)
     assert max_dl < 1e-2
+    sess.free()
+    model.free()
+    w.free()
+
+
+def test_qwen3_17b_q4_K_prefill_all_layers(gpu, ref):
+    """Qwen3-1.7B-shaped Q4_K at batch 8 with a 600-position prefix (three
+    256-position prefill chunks, the last partial) plus 8 prompt tokens: the
+    K/V rows of all 28 layers of one sequence equal a full-depth oracle
+    forward over the 608 positions bit for bit, and so does the first token"""
+    wl = D.WORKLOADS["qwen3-1.7b-q4_K-b8"]
+    prefix, prompt_len = 600, 8
+    print(f"{wl.name}: prefill {wl.n_seq} x {prefix}+{prompt_len}, all layers", flush=True)
+    w = D.QwenWeights(wl.wtype, seed=1234, **wl.shape)
+    model = D.QwenModel(w, gpu.backend)
+    sess = model.session(wl.n_seq, wl.max_positions)
+    short = D.QwenWorkload("short", wl.shape, wl.wtype, wl.n_seq, prefix, prompt_len, 0, wl.max_positions)
+    emb, prompt = D.workload_inputs(short, seed=78)
+    sess.prefill_embeddings(emb)
+    first = sess.prefill_tokens(prompt)
+    n_pos = prefix + prompt_len
+    s = 3
+    r = ref.QwenRef(w.cfg, w.pointer_table(), wl.max_positions)
+    t, _ = r.forward(np.concatenate([emb[s], r.embed(prompt[s])]))
+    assert t == first[s]
+    for layer in range(wl.shape["n_layers"]):
+        k, v = sess.read_kv(layer, s)
+        assert np.array_equal(k[:, :n_pos], r.k[layer][:, :n_pos]), f"prefill K layer {layer}"
+        assert np.array_equal(v[:, :n_pos], r.v[layer][:, :n_pos]), f"prefill V layer {layer}"
+    print("  prefill K/V of all 28 layers bit-exact", flush=True)
     sess.free()
     model.free()
     w.free()

@@ -155,6 +155,101 @@ def test_mul_mat_lm_head_full_size(ggml, gpu, ref, wname, m, k, n):
     G.free()
 
 
+SWEEP_CASES = [
+    # the kernel-sweep points: every M x K at N = 512 in both formats, and the
+    # vocabulary projection at N = 1, 8, 64 and 512
+    *[(w, m, k, 512) for w in ("q8_0", "q4_K") for m, k in ((1024, 1024), (3072, 1024), (1024, 3072))],
+    ("q4_K", 151936, 1024, 1), ("q8_0", 151936, 1024, 8), ("q4_K", 151936, 1024, 64), ("q8_0", 151936, 1024, 64),
+    ("q4_K", 151936, 1024, 512), ("q8_0", 151936, 1024, 512),
+]
+
+
+@pytest.mark.parametrize("wname,m,k,n", SWEEP_CASES)
+def test_mul_mat_sweep_points(ggml, gpu, ref, wname, m, k, n):
+    """the mul_mat sweep's shapes at the column counts the other tests leave
+    out, bit-exact against the oracle, same argmax per column"""
+    wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
+    print(f"sweep mul_mat {wname} M={m} K={k} N={n}", flush=True)
+    wq = ggml.quantize(wt, ggml.synth_normal(7, m + 3 * k, m * k, 0.0, 0.02).reshape(m, k))
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    G = ggml.Graph()
+    W = G.new(wt, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    Y = G.lib.ggml_mul_mat(G.ctx, W, X)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    G.set(X, x)
+    assert G.compute(gpu.backend) == 0
+    y = G.get(Y).reshape(n, m)
+    want = ref.mul_mat(wt, wq, m, k, x)
+    assert_same_bits(y, want)
+    assert np.array_equal(y.argmax(1), want.argmax(1))
+    G.free()
+
+
+def quantizer_edge_activations(n, k, seed):
+    """activation columns whose 256-element blocks hit the quantizers' edge
+    cases: +A and -A both at the block maximum (the first in element order
+    sets the Q8_K sign; pairs in one lane, in neighbouring lanes, across the
+    block, either sign first), all-zero blocks, a single non-zero element,
+    values exactly at 127/A multiples, and tiny magnitudes"""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, k)).astype(np.float32)
+    pairs = [(3, 9), (9, 3), (15, 16), (16, 15), (0, 255), (255, 0), (40, 41), (130, 7)]
+    for c in range(n):
+        for b in range(k // 256):
+            blk = x[c, 256 * b:256 * (b + 1)]
+            kind = (c * 7 + b) % 11
+            if kind < len(pairs):
+                i, j = pairs[kind]
+                a = np.float32(4.0 + kind)
+                blk[i], blk[j] = a, -a
+                blk[(i + 100) % 256] = a if kind % 2 else -a  # a third copy after both
+            elif kind == 8:
+                blk[:] = 0.0
+            elif kind == 9:
+                blk[:] = 0.0
+                blk[(c * 31 + b) % 256] = -0.75
+            else:
+                blk *= np.float32(1e-30)
+    x[0, :32] = np.arange(-16, 16, dtype=np.float32) * np.float32(127.0 / 16.0)
+    return x
+
+
+@pytest.mark.parametrize("wname,m,k,n,norm", [
+    ("q4_K", 1024, 1024, 8, False), ("q4_K", 1024, 3072, 8, False), ("q4_K", 4096, 1024, 8, True),
+    ("q4_K", 1024, 2048, 1, False), ("q8_0", 1024, 1024, 8, False), ("q8_0", 1024, 1024, 1, False),
+    ("q8_0", 4096, 1024, 1, True),
+])
+def test_mul_mat_activation_quantizer_edges(ggml, gpu, ref, wname, m, k, n, norm):
+    """the GEMVs' in-LDS activation quantizer (plain and behind an RMS norm
+    with unit weights, which keeps +-A ties exact) on the blocks of
+    quantizer_edge_activations, bit-exact against the oracle"""
+    wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
+    print(f"quantizer edges {wname} M={m} K={k} N={n} norm={norm}", flush=True)
+    wq = ggml.quantize(wt, ggml.synth_normal(14, m + k, m * k, 0.0, 0.02).reshape(m, k))
+    x = quantizer_edge_activations(n, k, seed=m + k + n)
+    if norm:  # keep every column's norm away from zero
+        x[:, -1] = np.float32(3.0)
+    G = ggml.Graph()
+    W = G.new(wt, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    WN = G.new(ggml.F32, k, weight=True)
+    h = G.lib.ggml_mul(G.ctx, G.lib.ggml_rms_norm(G.ctx, X, 1e-6), WN) if norm else X
+    Y = G.lib.ggml_mul_mat(G.ctx, W, h)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    G.set(X, x)
+    if norm:
+        G.set(WN, np.ones(k, np.float32))
+    assert G.compute(gpu.backend) == 0
+    y = G.get(Y).reshape(n, m)
+    xin = ref.rms_norm(x, 1e-6) * np.ones(k, np.float32) if norm else x
+    want = ref.mul_mat(wt, wq, m, k, xin)
+    assert_same_bits(y, want)
+    G.free()
+
+
 def test_mul_mat_f16_weights(ggml, gpu, ref):
     m, k, n = 96, 128, 5
     w = RNG.standard_normal((m, k)).astype(np.float16)
@@ -178,7 +273,7 @@ FA_CASES = [
     # d, hq, hkv, n_kv, n_q, n_seq
     (128, 16, 8, 512, 1, 1), (128, 16, 8, 1024, 1, 8), (128, 16, 8, 2048, 1, 1), (128, 16, 8, 8192, 1, 1),
     (128, 16, 8, 512, 64, 1), (128, 16, 8, 2048, 64, 2), (64, 6, 6, 448, 1, 1), (64, 6, 6, 1500, 1, 1),
-    (64, 6, 6, 1500, 1, 3),
+    (64, 6, 6, 1500, 1, 3), (128, 16, 8, 8192, 64, 1),
 ]
 
 
