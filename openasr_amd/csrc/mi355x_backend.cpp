@@ -94,6 +94,7 @@ static void buf_free(ggml_backend_buffer_t buffer) {
     buffer_ctx * c = (buffer_ctx *) buffer->context;
     error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
+    flush_uploads(c->dev, nullptr, true);  // queued writes into this buffer land before it is freed
     MI_CHECK(hipFree(c->base));
     ledger_sub(c->dev, c->size, false);
     delete c;
@@ -115,6 +116,7 @@ static void buf_memset_tensor(ggml_backend_buffer_t buffer, struct ggml_tensor *
     buffer_ctx * c = (buffer_ctx *) buffer->context;
     error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
+    flush_uploads(c->dev, nullptr, true);
     if (t->type == GGML_TYPE_Q8_0) {
         // stored row-split on the device: ggml-layout bytes go through the
         // same row conversion as set_tensor
@@ -141,9 +143,13 @@ static void buf_set_tensor(ggml_backend_buffer_t buffer, struct ggml_tensor * t,
     error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
     if (t->type != GGML_TYPE_Q8_0) {
+        // small writes wait in pinned memory for the next device use
+        if (stage_upload(c->dev, (char *) t->data + offset, data, size)) return;
+        flush_uploads(c->dev, nullptr, true);
         MI_CHECK(hipMemcpy((char *) t->data + offset, data, size, hipMemcpyHostToDevice));
         return;
     }
+    flush_uploads(c->dev, nullptr, true);
     int64_t r0, r1;
     size_t rb;
     if (!q8_0_rows(t, offset, size, r0, r1, rb)) {
@@ -168,6 +174,7 @@ static void buf_get_tensor(ggml_backend_buffer_t buffer, const struct ggml_tenso
     buffer_ctx * c = (buffer_ctx *) buffer->context;
     error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
+    flush_uploads(c->dev, nullptr, true);
     if (t->type != GGML_TYPE_Q8_0) {
         MI_CHECK(hipMemcpy(data, (const char *) t->data + offset, size, hipMemcpyDeviceToHost));
         return;
@@ -194,6 +201,7 @@ static bool buf_cpy_tensor(ggml_backend_buffer_t buffer, const struct ggml_tenso
     buffer_ctx * c = (buffer_ctx *) buffer->context;
     error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
+    flush_uploads(c->dev, nullptr, true);
     MI_CHECK(hipMemcpy(dst->data, src->data, ggml_nbytes(src), hipMemcpyDeviceToDevice));
     return true;
 }
@@ -202,6 +210,7 @@ static void buf_clear(ggml_backend_buffer_t buffer, uint8_t value) {
     buffer_ctx * c = (buffer_ctx *) buffer->context;
     error_scope scope(&c->dev->transfer_error);
     MI_CHECK(hipSetDevice(c->dev->hip_id));
+    flush_uploads(c->dev, nullptr, true);
     MI_CHECK(hipMemset(c->base, value, c->size));
 }
 
@@ -271,6 +280,8 @@ static void be_get_tensor_async(ggml_backend_t backend, const struct ggml_tensor
 
 static void be_synchronize(ggml_backend_t backend) {
     backend_state * be = (backend_state *) backend->context;
+    MI_CHECK(hipSetDevice(be->dev->hip_id));
+    flush_uploads(be->dev, be->stream, false);
     MI_CHECK(hipStreamSynchronize(be->stream));
 }
 

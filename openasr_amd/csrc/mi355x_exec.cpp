@@ -1475,6 +1475,7 @@ enum ggml_status graph_compute(backend_state * be, ggml_cgraph * cg) {
     be->launch_error.store(0);
     error_scope scope(&be->launch_error);
     MI_CHECK(hipSetDevice(be->dev->hip_id));
+    flush_uploads(be->dev, be->stream, false);  // queued input writes land ahead of the graph
     const uint64_t key = graph_key(cg);
     cache_entry * ce = find_entry(be, key);
     be->use_clock++;
@@ -1573,6 +1574,7 @@ enum ggml_status graph_compute_in(backend_state * be, ggml_cgraph * cg, char * s
     be->launch_error.store(0);
     error_scope scope(&be->launch_error);
     MI_CHECK(hipSetDevice(be->dev->hip_id));
+    flush_uploads(be->dev, be->stream, false);  // queued input writes land ahead of the graph
     bool planned;
     auto pp = make_plan(be, cg, planned);
     planner & p = *pp;
@@ -1620,6 +1622,7 @@ enum ggml_status graph_compute_in(backend_state * be, ggml_cgraph * cg, char * s
 int profile_graph(backend_state * be, ggml_cgraph * cg, int iters, float * step_ms, int max_steps, char * labels,
                   int label_cap) {
     MI_CHECK(hipSetDevice(be->dev->hip_id));
+    flush_uploads(be->dev, nullptr, true);
     bool planned;
     auto pp = make_plan(be, cg, planned);
     planner & p = *pp;

@@ -10,8 +10,21 @@
 
 #include "ggml_abi.h"
 #include "mi355x_common.h"
+#include "ops.h"
 
 namespace mi355x {
+
+// small host uploads waiting in pinned memory (mi355x_upload.cpp)
+struct upload_queue {
+    std::mutex mu;
+    char * pinned = nullptr;  // two halves of kUploadHalf bytes, hipHostMalloc'd
+    bool tried = false;       // allocation attempted (on failure uploads stay synchronous)
+    int cur = 0;              // the half new uploads go to
+    size_t used = 0;
+    std::vector<upload_entry> pending;
+    hipEvent_t done[2] = {nullptr, nullptr};  // recorded after the launch that read each half
+    bool busy[2] = {false, false};
+};
 
 struct device_state {
     int hip_id = -1;
@@ -43,7 +56,19 @@ struct device_state {
     std::once_flag static_once;
     char * static_scratch = nullptr;
     hipError_t static_err = hipSuccess;
+    upload_queue uploads;
 };
+
+// Staged uploads. stage_upload copies n bytes for dst into pinned memory
+// and queues them (false: not staged -- too large, or no pinned memory --
+// and the caller copies synchronously). flush_uploads applies everything
+// queued, on stream s (null: the null stream), before any device work that
+// may read it; with wait it returns once the writes are done. Every buffer
+// operation and every compute on the device flushes first, so the queue is
+// invisible to the host except in time.
+bool stage_upload(device_state * dev, char * dst, const void * src, size_t n);
+void flush_uploads(device_state * dev, hipStream_t s, bool wait);
+void release_uploads(device_state * dev);
 
 // Errors noted while an error_scope is active on the calling thread go to
 // its sink (the first one is kept): a backend's launch_error while it plans,

@@ -198,6 +198,21 @@ bool norm_supported(int64_t ne0);
 // a one-wave kernel that returns after `us` microseconds of device wall clock
 void launch_spin_us(double us, int wall_clock_khz, hipStream_t s);
 
+// Staged host uploads: small tensor writes are copied into pinned host
+// memory and applied on the device in one launch when the device is next
+// used (entry i: bytes [off, off + n) of the pinned area to dst)
+struct upload_entry {
+    char * dst;
+    uint32_t off, n;
+};
+constexpr int kUploadBatch = 16;  // entries per apply launch
+struct upload_batch {
+    const char * src;  // the pinned area (device-accessible host memory)
+    int n;
+    upload_entry e[kUploadBatch];
+};
+void launch_apply_uploads(const upload_batch & b, hipStream_t s);
+
 // Q8_0 layout conversion between ggml's interleaved blocks and the row-split
 // device layout (host side, used by set/get_tensor)
 void q8_0_to_split_rows(const uint8_t * src, uint8_t * dst, int64_t rows, int64_t k);

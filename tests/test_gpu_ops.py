@@ -765,3 +765,49 @@ def test_failed_transfer_fails_next_compute(ggml, gpu):
     assert G.compute(gpu.backend) == 2
     assert G.compute(gpu.backend) == 0
     G.free()
+
+
+def test_staged_uploads_keep_write_order(ggml, gpu):
+    """Small tensor writes wait in pinned host memory and land at the next
+    device use. Overlapping partial writes land in call order, a read sees
+    every write before it, more writes than one apply launch takes all land
+    (4-byte pieces at 4-byte offsets: the unaligned path), a write too large
+    to stage lands after the staged ones before it, and a compute sees the
+    writes queued just before it."""
+    G = ggml.Graph()
+    L = G.lib
+    n = 131072  # 512 KB: a whole-tensor write takes the synchronous path
+    X = G.new(ggml.F32, n)
+    Y = L.ggml_scale(G.ctx, X, 2.0)
+    run(ggml, gpu, G, Y)
+
+    def put(arr, elem_off):
+        arr = np.ascontiguousarray(arr, np.float32)
+        assert L.ggml_backend_tensor_set(X, arr.ctypes.data, 4 * elem_off, arr.nbytes) == 0
+
+    base = RNG.standard_normal(n).astype(np.float32)
+    G.set(X, base)
+    want = base.copy()
+    put(np.full(100, 7.0), 100)
+    put(np.full(50, -3.0), 150)
+    want[100:200] = 7.0
+    want[150:200] = -3.0
+    assert np.array_equal(G.get(X).reshape(-1), want)
+    for i in range(100):
+        put([1000.0 + i], 1000 + 3 * i)
+        want[1000 + 3 * i] = 1000.0 + i
+    assert G.compute(gpu.backend) == 0
+    assert np.array_equal(G.get(Y).reshape(-1), want * 2.0)
+    # staged, then a synchronous whole-tensor write: the large one wins
+    put(np.full(64, 5.0), 0)
+    big = RNG.standard_normal(n).astype(np.float32)
+    G.set(X, big)
+    assert np.array_equal(G.get(X).reshape(-1), big)
+    # staged writes right before a compute
+    put(np.full(16, 9.0), 4096)
+    big[4096:4112] = 9.0
+    assert G.compute(gpu.backend) == 0
+    assert np.array_equal(G.get(Y).reshape(-1), big * 2.0)
+    # a staged write into a buffer that is then freed
+    put(np.full(8, 1.0), 0)
+    G.free()
