@@ -51,6 +51,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-whisper", action="store_true", help="skip the Whisper-tiny batch-1 side measurement")
     p.add_argument("--no-long", action="store_true", help="skip the Qwen3-1.7B long-context side measurement")
+    p.add_argument("--no-full", action="store_true",
+                   help="skip the side lines that time each workload's whole greedy decode")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
     p.add_argument("--profile-iters", type=int, default=20)
     p.add_argument("--sweep", action="store_true", help="per-kernel sweep of mul_mat and flash_attn_ext shapes")
@@ -74,7 +76,7 @@ def weight_bytes(cfg, wtype) -> dict:
 
 
 def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cpu: bool, cpu_seconds: float,
-                 cpu_variants: bool = True):
+                 cpu_variants: bool = True, full_run: bool = False):
     from openasr_amd import decoders as D
     from openasr_amd import ggml as g
 
@@ -97,12 +99,15 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
     steps = min(steps, wl.max_positions - wl.prefix - wl.prompt - warmup)
     out, _ = sess.generate(first, warmup)
     cur = out[-1] if warmup else first
+    # the step at position p writes KV row p and attends over rows 0..p
+    pos0 = sess.position(0)
     t0 = time.perf_counter()
     out, step_ms = sess.generate(cur, steps)
     elapsed = time.perf_counter() - t0
     tok_s = wl.n_seq * steps / elapsed
-    log(f"[bench] {steps} decode steps: {elapsed * 1e3 / steps:.3f} ms/step, {tok_s:.1f} tokens/s "
-        f"(median step {np.median(step_ms):.3f} ms)")
+    timed_positions = [pos0, pos0 + steps - 1]
+    log(f"[bench] {steps} decode steps at positions {timed_positions[0]}-{timed_positions[1]}: "
+        f"{elapsed * 1e3 / steps:.3f} ms/step, {tok_s:.1f} tokens/s (median step {np.median(step_ms):.3f} ms)")
 
     # per-launch-group times of one decode step: HIP events on the backend stream around each group,
     # the groups queued behind a short spin so they run back to back
@@ -137,9 +142,27 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
     cpu = None
     if want_cpu:
         cpu = cpu_baseline(w, wl, sess, out[-1], cpu_seconds, variants=cpu_variants)
+    full = None
+    if full_run:
+        # the workload's whole greedy decode from a fresh prefill, every step timed
+        sess.free()
+        sess = model.session(wl.n_seq, wl.max_positions)
+        sess.prefill_embeddings(emb)
+        first = sess.prefill_tokens(prompt)
+        p0 = sess.position(0)
+        n = min(wl.decode, wl.max_positions - p0)
+        t0 = time.perf_counter()
+        _, fms = sess.generate(first, n)
+        dt = time.perf_counter() - t0
+        full = {"steps": n, "positions": [p0, p0 + n - 1], "tokens_per_s": round(wl.n_seq * n / dt, 1),
+                "ms_per_step": round(dt * 1e3 / n, 4), "first_step_ms": round(float(fms[0]), 4),
+                "last_step_ms": round(float(fms[-1]), 4)}
+        log(f"[bench] {name} full decode: {n} steps at positions {p0}-{p0 + n - 1}, {dt * 1e3 / n:.3f} ms/step, "
+            f"{full['tokens_per_s']:.1f} tokens/s (first step {fms[0]:.3f} ms, last {fms[-1]:.3f} ms)")
     result = dict(tok_s=tok_s, ms_per_step=elapsed * 1e3 / steps, steps=steps, prefill_ms=prefill_s * 1e3,
                   n_prefill=n_prefill, gemv_ms=gemv_ms, gemv_launches=gemv_n, gemv_gbs=gemv_gbs,
-                  weight_bytes=alg_bytes, eager_step_ms=eager_ms, breakdown=breakdown, cpu=cpu)
+                  weight_bytes=alg_bytes, eager_step_ms=eager_ms, breakdown=breakdown, cpu=cpu,
+                  timed_positions=timed_positions, full=full)
     sess.free()
     model.free()
     w.free()
@@ -167,6 +190,7 @@ def run_whisper(n_tokens: int, cpu_seconds: float):
     for t in prompt:
         tok = sess.step(int(t))
     n_tokens = min(n_tokens, shape["max_positions"] - len(prompt) - 1)
+    p0 = sess.position()
     t0 = time.perf_counter()
     out, step_ms = sess.generate(tok, n_tokens)
     elapsed = time.perf_counter() - t0
@@ -174,10 +198,11 @@ def run_whisper(n_tokens: int, cpu_seconds: float):
     log(f"[bench] whisper-tiny q8_0 b1: cross K/V {cross_ms:.2f} ms, {n_tokens} greedy steps {elapsed * 1e3 / n_tokens:.3f} "
         f"ms/step = {tok_s:.1f} tokens/s")
     res = {"tokens_per_s": round(tok_s, 1), "ms_per_step": round(elapsed * 1e3 / n_tokens, 4), "steps": n_tokens,
+           "positions": [p0, p0 + n_tokens - 1],
            "cross_kv_ms": round(cross_ms, 3), "cpu_tokens_per_s": None}
     if cpu_seconds > 0:
         from oracle import ref
-        threads = os.cpu_count() or 1
+        threads = usable_cpus()
         r = ref.WhisperRef(w.cfg, w.pointer_table(), threads=threads)
         r.set_encoder(enc)
         cur, n = int(prompt[0]), 0
@@ -215,15 +240,53 @@ def measured_copy_gbs(reps: int = 20) -> float:
     return gbs
 
 
+def usable_cpus() -> int:
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
+
+
 def cpu_model() -> str:
+    return cpu_description()["model"]
+
+
+def cpu_description() -> dict:
+    """host CPU as /proc/cpuinfo gives it: model name, physical cores (distinct
+    (physical id, core id) pairs), logical CPUs, the SIMD ISA flags the
+    oracle's kernels can use, and the cores this process may run on"""
+    model, flags, cores, logical = "unknown", set(), set(), 0
+    phys = core = None
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                key, _, val = line.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "processor":
+                    logical += 1
+                elif key == "model name":
+                    model = val
+                elif key == "flags":
+                    flags = set(val.split())
+                elif key == "physical id":
+                    phys = val
+                elif key == "core id":
+                    core = val
+                elif not key and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None:
+            cores.add((phys, core))
     except OSError:
         pass
-    return "unknown"
+    isa = [f for f in ("sse4_2", "avx", "avx2", "fma", "f16c", "avx512f", "avx512bw", "avx512vl", "avx512_vnni",
+                       "avx512_bf16", "avx_vnni", "amx_tile", "amx_int8") if f in flags]
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = logical
+    return {"model": model, "physical_cores": len(cores) or None, "logical_cpus": logical, "isa": isa,
+            "usable_cpus": affinity}
 
 
 def cpu_baseline(w, wl, sess, tokens, seconds: float, variants: bool = True):
@@ -232,7 +295,7 @@ def cpu_baseline(w, wl, sess, tokens, seconds: float, variants: bool = True):
     of the same workload, timed for ~`seconds`."""
     from oracle import ref
 
-    threads = os.cpu_count() or 1
+    threads = usable_cpus()
     r = ref.QwenRefBatch(w.cfg, w.pointer_table(), wl.max_positions, wl.n_seq, threads=threads)
     for s in range(wl.n_seq):
         for layer in range(wl.shape["n_layers"]):
@@ -259,7 +322,7 @@ def cpu_baseline(w, wl, sess, tokens, seconds: float, variants: bool = True):
     res = {"value": round(val, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
            "sample": f"{n} batched decode steps of {wl.name} (oracle ref_qwen_decode_batch, {threads} OpenMP "
                      f"threads) continuing from the device KV state at position {start}",
-           "cpu": cpu_model()}
+           "cpu": cpu_model(), "host": cpu_description()}
     if variants:
         # the reference's decoder thread policy (available / 2, at least 2) and one thread, shorter samples
         half = max(2, threads // 2)
@@ -417,14 +480,15 @@ def main() -> int:
     from openasr_amd import ggml as g
 
     log(f"[bench] backend {g.plugin().name}")
-    main_r = run_workload(a.workload, a.steps, a.warmup, a.profile_iters, not a.no_cpu, a.cpu_seconds)
+    main_r = run_workload(a.workload, a.steps, a.warmup, a.profile_iters, not a.no_cpu, a.cpu_seconds,
+                          full_run=not a.no_full)
     b1 = None
     if not a.no_b1 and a.workload != "qwen3-0.6b-q8_0-b1":
         r1 = run_workload("qwen3-0.6b-q8_0-b1", min(a.steps, 128), a.warmup, a.profile_iters, not a.no_cpu,
-                          min(4.0, a.cpu_seconds), cpu_variants=False)
+                          min(4.0, a.cpu_seconds), cpu_variants=False, full_run=not a.no_full)
         b1 = {"tokens_per_s": round(r1["tok_s"], 1), "ms_per_step": round(r1["ms_per_step"], 4),
-              "mul_mat_q8_0_gbs": round(r1["gemv_gbs"], 1),
-              "cpu_tokens_per_s": r1["cpu"]["value"] if r1["cpu"] else None}
+              "timed_positions": r1["timed_positions"], "mul_mat_q8_0_gbs": round(r1["gemv_gbs"], 1),
+              "cpu_tokens_per_s": r1["cpu"]["value"] if r1["cpu"] else None, "full_decode": r1["full"]}
     long = None
     if not a.no_long and a.workload != "qwen3-1.7b-q4_K-b8":
         rl = run_workload("qwen3-1.7b-q4_K-b8", min(a.steps, 64), a.warmup, max(4, a.profile_iters // 4), False, 0)
@@ -438,10 +502,13 @@ def main() -> int:
     frac = main_r["gemv_gbs"] / HBM_PEAK_GBS
     # measured HBM bytes per GEMV launch (rocprofv3 FETCH_SIZE / WRITE_SIZE
     # runs of `bench.py --traffic-probe`, summarised by openasr_amd.pmc)
-    traffic = None
+    traffic, traffic_source = None, None
     tpath = ROOT / "profiles" / f"gemv_traffic_{a.workload}.json"
     if tpath.exists():
-        traffic = round(json.loads(tpath.read_text())["decode_step"]["gemv_hbm_bytes_per_launch"], 1)
+        tj = json.loads(tpath.read_text())
+        traffic = round(tj["decode_step"]["gemv_hbm_bytes_per_launch"], 1)
+        traffic_source = (f"not measured in this run: profiles/{tpath.name} (rocprofv3 FETCH_SIZE and WRITE_SIZE "
+                          f"passes of bench.py --traffic-probe) at commit {tj.get('commit', 'unrecorded')}")
     out = {
         "metric": "decode tokens/sec @ batch 8 (Qwen3-0.6B-shaped Q4_K decoder); quantized mul_mat HBM GB/s as % of peak",
         "value": round(main_r["tok_s"], 1),
@@ -459,13 +526,16 @@ def main() -> int:
                    "head_dim 128, ffn 3072, vocab 151936)", "global_batch": 8, "seq_len": 1024,
                    "prefill_positions": main_r["n_prefill"], "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(main_r["gemv_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(frac, 4), "traffic": traffic, "copy_gbs_measured": round(copy_gbs, 1),
+                     "frac": round(frac, 4), "traffic": traffic, "traffic_source": traffic_source,
+                     "copy_gbs_measured": round(copy_gbs, 1),
                      "alg_bytes_per_launch": round(main_r["weight_bytes"] / max(1, main_r["gemv_launches"]), 1),
                      "launches": main_r["gemv_launches"],
                      "kernel": "k_gemv_q4_K: the quantized GEMV launches of one decode step (per layer QKV, "
                                "o-proj+residual, gate+up SwiGLU, down+residual; lm_head), algorithmic bytes "
                                "(weights + int8 activations + f32 outputs) / summed launch time"},
         "cpu_baseline": main_r["cpu"],
+        "timed_positions": main_r["timed_positions"],
+        "full_decode": main_r["full"],
         "prefill_ms": round(main_r["prefill_ms"], 2),
         "eager_step_ms": round(main_r["eager_step_ms"], 4),
         "kernels": main_r["breakdown"],

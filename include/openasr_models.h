@@ -110,6 +110,15 @@ oa_qwen_session * oa_qwen_session_create(oa_qwen_model * m, int n_seq, int max_p
 void oa_qwen_session_free(oa_qwen_session * s);
 int oa_qwen_session_position(const oa_qwen_session * s, int seq);
 
+/* Greedy top-1 head of the session's step graphs: 0 (default) ARGMAX_FIRST
+ * over the logits; 1 the reversed-row graph of the whole-decoder fused
+ * logits head (cpu_graph.rs:3772-3810, llm_transformer.rs:2096-2130) --
+ * GET_ROWS by vocab - 1 .. 0 (through a transposed copy for more than one
+ * sequence), CONT, then ggml's last-max ARGMAX, the result r mapped to
+ * vocab - 1 - r; a result outside the vocabulary fails the step. Both give
+ * the first of equal maxima. Takes effect on the next step. */
+void oa_qwen_session_set_reversed_top1(oa_qwen_session * s, int enable);
+
 /* Prefill T positions of every sequence (chunked internally at 256) from
  * hidden inputs [n_seq][T][d_model] (an audio-embedding prefix) or token ids
  * [n_seq][T]. top1_out (optional, [n_seq]) gets the first-max argmax of the

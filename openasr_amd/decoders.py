@@ -88,6 +88,7 @@ def lib() -> C.CDLL:
     s("oa_qwen_session_create", vp, vp, i, i)
     s("oa_qwen_session_free", None, vp)
     s("oa_qwen_session_position", i, vp, i)
+    s("oa_qwen_session_set_reversed_top1", None, vp, i)
     s("oa_qwen_prefill_embeddings", i, vp, vp, i, vp)
     s("oa_qwen_prefill_tokens", i, vp, vp, i, vp)
     s("oa_qwen_decode_step", i, vp, vp, vp, vp)
@@ -241,6 +242,10 @@ class QwenSession:
 
     def position(self, seq: int = 0) -> int:
         return lib().oa_qwen_session_position(self.ptr, seq)
+
+    def set_reversed_top1(self, enable: bool = True):
+        """greedy top-1 through the reversed-row GET_ROWS + ARGMAX graph"""
+        lib().oa_qwen_session_set_reversed_top1(self.ptr, int(enable))
 
     def free(self):
         if self.ptr:

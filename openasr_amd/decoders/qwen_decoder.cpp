@@ -122,11 +122,33 @@ struct oa_qwen_session {
     std::vector<int> n_past;  // per sequence
     step_graph decode;
     std::vector<uint16_t> mask_host;
+    // greedy top-1 through the reversed-row graph (cpu_graph.rs:3772-3810)
+    // instead of ARGMAX_FIRST; rev_idx holds vocab - 1 .. 0
+    bool reversed_top1 = false;
+    ggml_tensor * rev_idx = nullptr;
 };
 
 namespace {
 
 const ggml_fp16_t kNegInf = 0xFC00;
+
+// Greedy top-1 with first-max ties from ggml's ARGMAX, which keeps the last
+// of equal maxima: every logits row is reversed by GET_ROWS (one element per
+// row for a single column, the transposed matrix's rows otherwise), then
+// ARGMAX; the caller maps a result r to vocab - 1 - r
+// (cpu_graph.rs:3772-3810, llm_transformer.rs:2096-2115).
+ggml_tensor * top1_reversed(ggml_context * ctx, ggml_tensor * logits, ggml_tensor * rev) {
+    const int64_t V = logits->ne[0], n = logits->ne[1];
+    ggml_tensor * r;
+    if (n == 1) {
+        r = ggml_get_rows(ctx, ggml_reshape_2d(ctx, logits, 1, V), rev);
+        r = ggml_reshape_2d(ctx, ggml_cont(ctx, r), V, 1);
+    } else {
+        ggml_tensor * tr = ggml_cont(ctx, ggml_transpose(ctx, logits));  // [n, V]
+        r = ggml_cont(ctx, ggml_transpose(ctx, ggml_get_rows(ctx, tr, rev)));
+    }
+    return ggml_argmax(ctx, r);
+}
 
 ggml_tensor * rms_norm_mul(ggml_context * ctx, ggml_tensor * x, ggml_tensor * w, float eps) {
     return ggml_mul(ctx, ggml_rms_norm(ctx, x, eps), w);  // nn/norm.rs:39-56
@@ -233,7 +255,7 @@ bool build_step(oa_qwen_session * s, step_graph & g, int T, bool emb) {
     }
     ggml_tensor * normed = rms_norm_mul(g.ctx, last, m->out_norm, c.rms_eps);
     g.logits = ggml_mul_mat(g.ctx, m->lm_head, normed);
-    g.top1 = ggml_argmax_first(g.ctx, g.logits);
+    g.top1 = s->reversed_top1 ? top1_reversed(g.ctx, g.logits, s->rev_idx) : ggml_argmax_first(g.ctx, g.logits);
     ggml_set_output(g.logits);
     ggml_set_output(g.top1);
     g.gf = ggml_new_graph_custom(g.ctx, (size_t) c.n_layers * 64 + 256, false);
@@ -261,6 +283,19 @@ void set_step_inputs(oa_qwen_session * s, step_graph & g, int T) {
     ggml_backend_tensor_set(g.mask, mask.data(), 0, mask.size() * 2);
 }
 
+// the step's greedy tokens; a reversed-row result r is vocab - 1 - r, and a
+// value outside the vocabulary fails the step (llm_transformer.rs:2117-2130)
+int read_top1(const oa_qwen_session * s, const step_graph & g, int32_t * out) {
+    ggml_backend_tensor_get(g.top1, out, 0, (size_t) s->n_seq * sizeof(int32_t));
+    if (!s->reversed_top1) return GGML_STATUS_SUCCESS;
+    const int V = s->m->cfg.vocab;
+    for (int q = 0; q < s->n_seq; q++) {
+        if (out[q] < 0 || out[q] >= V) return GGML_STATUS_FAILED;
+        out[q] = V - 1 - out[q];
+    }
+    return GGML_STATUS_SUCCESS;
+}
+
 int run_chunk(oa_qwen_session * s, const void * input, bool emb, int T, int32_t * top1_out) {
     step_graph g;
     if (!build_step(s, g, T, emb)) {
@@ -272,12 +307,13 @@ int run_chunk(oa_qwen_session * s, const void * input, bool emb, int T, int32_t 
     else ggml_backend_tensor_set(g.tokens, input, 0, (size_t) T * s->n_seq * sizeof(int32_t));
     set_step_inputs(s, g, T);
     const int st = ggml_backend_graph_compute(s->m->backend, g.gf);
+    int ret = st;
     if (st == GGML_STATUS_SUCCESS) {
         for (int q = 0; q < s->n_seq; q++) s->n_past[(size_t) q] += T;
-        if (top1_out) ggml_backend_tensor_get(g.top1, top1_out, 0, (size_t) s->n_seq * sizeof(int32_t));
+        if (top1_out) ret = read_top1(s, g, top1_out);
     }
     g.release();
-    return st;
+    return ret;
 }
 
 }  // namespace
@@ -415,6 +451,7 @@ oa_qwen_session * oa_qwen_session_create(oa_qwen_model * m, int n_seq, int max_p
         s->k_cache.push_back(ggml_new_tensor_4d(s->kv_ctx, GGML_TYPE_F16, c.head_dim, max_positions, c.n_kv_head, n_seq));
         s->v_cache.push_back(ggml_new_tensor_4d(s->kv_ctx, GGML_TYPE_F16, c.head_dim, max_positions, c.n_kv_head, n_seq));
     }
+    s->rev_idx = ggml_new_tensor_1d(s->kv_ctx, GGML_TYPE_I32, c.vocab);
     s->kv_buf = ggml_backend_alloc_ctx_tensors_from_buft(s->kv_ctx, ggml_backend_get_default_buffer_type(m->backend));
     if (!s->kv_buf) {
         ggml_free(s->kv_ctx);
@@ -422,6 +459,9 @@ oa_qwen_session * oa_qwen_session_create(oa_qwen_model * m, int n_seq, int max_p
         return nullptr;
     }
     ggml_backend_buffer_clear(s->kv_buf, 0);  // unwritten slots stay zero (nn/decoder.rs:2407-2416)
+    std::vector<int32_t> rev((size_t) c.vocab);
+    for (int i = 0; i < c.vocab; i++) rev[(size_t) i] = c.vocab - 1 - i;
+    ggml_backend_tensor_set(s->rev_idx, rev.data(), 0, rev.size() * sizeof(int32_t));
     return s;
 }
 
@@ -434,6 +474,12 @@ void oa_qwen_session_free(oa_qwen_session * s) {
 }
 
 int oa_qwen_session_position(const oa_qwen_session * s, int seq) { return s->n_past[(size_t) seq]; }
+
+void oa_qwen_session_set_reversed_top1(oa_qwen_session * s, int enable) {
+    if (s->reversed_top1 == (enable != 0)) return;
+    s->reversed_top1 = enable != 0;
+    s->decode.release();  // rebuilt with the other head on the next step
+}
 
 int oa_qwen_prefill_embeddings(oa_qwen_session * s, const float * emb, int T, int32_t * top1_out) {
     const int d = s->m->cfg.d_model, n_seq = s->n_seq;
@@ -477,7 +523,10 @@ int oa_qwen_decode_step(oa_qwen_session * s, const int32_t * tokens, int32_t * t
     const int st = ggml_backend_graph_compute(s->m->backend, g.gf);
     if (st != GGML_STATUS_SUCCESS) return st;
     for (int q = 0; q < s->n_seq; q++) s->n_past[(size_t) q] += 1;
-    if (top1_out) ggml_backend_tensor_get(g.top1, top1_out, 0, (size_t) s->n_seq * 4);
+    if (top1_out) {
+        const int rt = read_top1(s, g, top1_out);
+        if (rt != GGML_STATUS_SUCCESS) return rt;
+    }
     if (logits_out) ggml_backend_tensor_get(g.logits, logits_out, 0, (size_t) s->n_seq * s->m->cfg.vocab * 4);
     return GGML_STATUS_SUCCESS;
 }

@@ -26,10 +26,13 @@ pytestmark = pytest.mark.gpu
 TINY = dict(d_model=256, n_layers=2, n_head=4, n_kv_head=2, head_dim=64, ffn=512, vocab=1000)
 
 
-def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed=7, check_logits=True, weights=None):
+def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed=7, check_logits=True, weights=None,
+             reversed_top1=False):
     w = weights or D.QwenWeights(wtype, seed=seed, **shape)
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(n_seq, max_pos)
+    if reversed_top1:
+        sess.set_reversed_top1(True)
     wl = D.QwenWorkload("test", shape, wtype, n_seq, prefix, prompt, steps, max_pos)
     emb, toks = D.workload_inputs(wl, seed=seed + 1)
     t0 = time.time()
@@ -87,6 +90,15 @@ def test_tiny_decoder_token_exact(gpu, ref, wname, n_seq):
     run_pair(gpu, ref, TINY, wt, n_seq, prefix=300, prompt=5, steps=24, max_pos=512)
 
 
+@pytest.mark.parametrize("n_seq", [1, 3])
+def test_tiny_decoder_reversed_top1_head(gpu, ref, n_seq):
+    """the step graphs with the reference's reversed-row top-1 head (GET_ROWS
+    by vocab - 1 .. 0, CONT, last-max ARGMAX; cpu_graph.rs:3772-3810): token
+    for token the oracle's first-max greedy decode"""
+    print(f"tiny qwen reversed top-1 n_seq={n_seq}", flush=True)
+    run_pair(gpu, ref, TINY, g.Q4_K, n_seq, prefix=200, prompt=5, steps=24, max_pos=512, reversed_top1=True)
+
+
 def test_batched_equals_serial(gpu):
     """n_seq=3 in one graph == three n_seq=1 sessions (nn/decoder.rs:3412-3520 invariant)"""
     w = D.QwenWeights(g.Q4_K, seed=3, **TINY)
@@ -114,6 +126,15 @@ def test_qwen3_06b_q8_0_batch1_first_64_steps(gpu, ref):
     """Qwen3-0.6B shape, Q8_0, 375-position N(0,1) prefix + 8 prompt tokens, batch 1"""
     print("qwen3-0.6b q8_0 b1", flush=True)
     run_pair(gpu, ref, D.QWEN3_06B, g.Q8_0, 1, prefix=375, prompt=8, steps=64, max_pos=1024, seed=1234)
+
+
+def test_qwen3_06b_q8_0_batch1_reversed_top1_first_64_steps(gpu, ref):
+    """the batch-1 configuration through the reference's whole-decoder fused
+    logits head (reversed GET_ROWS + CONT + ARGMAX, llm_transformer.rs:
+    2096-2130): 64 greedy steps token for token against the oracle"""
+    print("qwen3-0.6b q8_0 b1, reversed top-1 head", flush=True)
+    run_pair(gpu, ref, D.QWEN3_06B, g.Q8_0, 1, prefix=375, prompt=8, steps=64, max_pos=1024, seed=1234,
+             reversed_top1=True)
 
 
 def test_qwen3_06b_q4_K_batch8_first_64_steps(gpu, ref):

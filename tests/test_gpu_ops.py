@@ -811,3 +811,42 @@ def test_staged_uploads_keep_write_order(ggml, gpu):
     # a staged write into a buffer that is then freed
     put(np.full(8, 1.0), 0)
     G.free()
+
+
+@pytest.mark.parametrize("n", [1, 3])
+def test_reversed_row_top1_keeps_the_first_max(ggml, gpu, n):
+    """the reversed-row top-1 graph (cpu_graph.rs:3772-3810) on logits with
+    exact ties: GET_ROWS by V - 1 .. 0 (a one-element row per logit for one
+    column, rows of the transposed matrix otherwise), CONT, ggml's last-max
+    ARGMAX, then V - 1 - r is the FIRST of the equal maxima; plain ARGMAX on
+    the same logits gives the last"""
+    V = 151936
+    G = ggml.Graph()
+    L = G.lib
+    X = G.new(ggml.F32, V, n)
+    R = G.new(ggml.I32, V)
+    if n == 1:
+        r = L.ggml_get_rows(G.ctx, L.ggml_reshape_2d(G.ctx, X, 1, V), R)
+        r = L.ggml_reshape_2d(G.ctx, L.ggml_cont(G.ctx, r), V, 1)
+    else:
+        tr = L.ggml_cont(G.ctx, L.ggml_transpose(G.ctx, X))
+        r = L.ggml_cont(G.ctx, L.ggml_transpose(G.ctx, L.ggml_get_rows(G.ctx, tr, R)))
+    top = L.ggml_argmax(G.ctx, r)
+    last = L.ggml_argmax(G.ctx, X)
+    G.build(top, last)
+    G.allocate(gpu.buft)
+    x = RNG.standard_normal((n, V)).astype(np.float32)
+    firsts = []
+    for c in range(n):
+        idx = np.sort(RNG.choice(V, 4, replace=False))
+        x[c, idx] = 9.0  # four equal maxima
+        firsts.append(idx)
+    G.set(X, x)
+    G.set(R, np.arange(V - 1, -1, -1, dtype=np.int32))
+    assert G.compute(gpu.backend) == 0
+    got = G.get(top, np.int32).reshape(-1)
+    got_last = G.get(last, np.int32).reshape(-1)
+    for c in range(n):
+        assert V - 1 - got[c] == firsts[c][0]
+        assert got_last[c] == firsts[c][-1]
+    G.free()
