@@ -417,6 +417,41 @@ __device__ __forceinline__ void as_norm_rope(float x0, float x1, float w0, float
     y1 = v0 * cs.y + v1 * cs.x;
 }
 
+// The decode wave's K and V requests for one chunk; rows past the span
+// repeat the last one. K goes straight to LDS (global_load_lds, 16 bytes a
+// lane): instruction u fills slots u*64 .. u*64+63 of the wave's area, slot
+// t holding piece (t % KU) ^ (row & 7) of row t / KU -- swizzled, so that
+// the transposed reads (lane p: the pieces of row p) hit distinct banks. V
+// goes to registers, lane = its dims of every position.
+__device__ __forceinline__ int fa_kslot(int row, int piece, int KU) { return row * KU + (piece ^ (row & 7)); }
+
+template <int D>
+__device__ __forceinline__ void fa_issue_kv(const char * kc, const char * vb, int64_t k_nb1, int vs, int loff, int clen,
+                                            int lane, uint4 * s_kw, uint32_t (&vr)[kFaChunk]) {
+    constexpr int KU = D / 8, DL = D / 64;
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        const int t = u * 64 + lane, row = t / KU, piece = (t % KU) ^ (row & 7);
+        const char * src = kc + (int64_t) min(row, clen - 1) * k_nb1 + 16 * piece;
+        __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *) src,
+                                         (void __attribute__((address_space(3))) *) (s_kw + u * 64), 16, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < kFaChunk; j++) {
+        const int off = (j < clen ? j : clen - 1) * vs + loff;
+        if (DL == 2) vr[j] = *(const uint32_t *) (vb + off);
+        else vr[j] = (uint32_t) *(const uint16_t *) (vb + off);
+    }
+}
+
+// s_waitcnt with only a vector-memory bound: at most n (< 64) requests of this
+// wave outstanding (gfx9 encoding: vmcnt in bits 3:0 and 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
 // Decode form (one query position): one wave per (chunk, query head,
 // sequence). For the scores lane p owns KV position p of the chunk (its whole
 // K row, the query broadcast from LDS); for P*V lane l owns dims D/64*l.. of
@@ -441,7 +476,7 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     constexpr int KU = D / 8;  // 16-byte pieces of a K row
     static_assert(!STEP || D == 128, "the step form handles 128-wide heads");
     __shared__ __align__(16) float s_q[4][D];
-    __shared__ uint4 s_k[4][kFaChunk][KU + 1];  // one padded row per position: conflict-free row reads
+    __shared__ uint4 s_k[4][kFaChunk * KU];  // per wave the chunk's K rows, swizzled (fa_kslot)
     __shared__ __align__(16) uint16_t s_vnew[STEP ? 4 : 1][D];
     const fattn_args & a = st.fa;
     const int lane = (int) threadIdx.x & 63;
@@ -527,48 +562,33 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
             return;
         }
     }
-    // K in wave-wide contiguous pieces (each load instruction covers whole
-    // rows), transposed through LDS so that lane p gets row p. Positions past
-    // the span read the chunk's last valid row (always in bounds, loads stay
-    // unconditional); they are masked.
+    // K (into LDS, for the transposed reads: lane p gets row p) and V (lane =
+    // dims of every position) in one burst. Positions past the span read the
+    // chunk's last valid row (always in bounds, loads stay unconditional);
+    // they are masked.
     const char * kc = a.k + (int64_t) kvh * a.k_nb2 + (int64_t) kv_seq * a.k_nb3 + (int64_t) c * kFaChunk * a.k_nb1;
     const char * vb = a.v + (int64_t) kvh * a.v_nb2 + (int64_t) kv_seq * a.v_nb3 + (int64_t) c * kFaChunk * a.v_nb1;
     const int vs = (int) a.v_nb1, loff = lane * DL * 2;
-    uint4 kl[KU];
-#pragma unroll
-    for (int u = 0; u < KU; u++) {
-        const int t = u * 64 + lane, row = t / KU, col = t % KU;
-        kl[u] = *(const uint4 *) (kc + (int64_t) min(row, clen - 1) * a.k_nb1 + 16 * col);
-    }
-#pragma unroll
-    for (int u = 0; u < KU; u++) {
-        const int t = u * 64 + lane;
-        s_k[wave][t / KU][t % KU] = kl[u];
-    }
-    // V in the same burst (lane = dims of every position)
     uint32_t vr[kFaChunk];
-#pragma unroll
-    for (int j = 0; j < kFaChunk; j++) {
-        const int off = (j < clen ? j : clen - 1) * vs + loff;
-        if (DL == 2) vr[j] = *(const uint32_t *) (vb + off);
-        else vr[j] = (uint32_t) *(const uint16_t *) (vb + off);
-    }
+    fa_issue_kv<D>(kc, vb, a.k_nb1, vs, loff, clen, lane, &s_k[wave][0], vr);
     if constexpr (STEP) {
         float y0, y1;
         as_norm_rope(qx0, qx1, qw0, qw1, qcs, st.q_eps, y0, y1);
         s_q[wave][lane] = round_to_half(y0);
         s_q[wave][lane + 64] = round_to_half(y1);
         if (jn >= 0) {
-            // this step's K / V rows: K replaces the LDS row jn (after the
-            // transposing stores above, in program order within the wave), V
-            // goes through LDS to the dims layout
+            // this step's K / V rows: K replaces the LDS row jn once the
+            // chunk's K has landed (its requests precede the 64 V requests, so
+            // at most 63 outstanding means every K request is done), V goes
+            // through LDS to the dims layout
             float y0, y1;
             as_norm_rope(kx0, kx1, kw0, kw1, qcs, st.k_eps, y0, y1);
             const uint16_t k0 = float_to_half_bits(y0), k1 = float_to_half_bits(y1);
             const uint16_t v0 = float_to_half_bits(vx0), v1 = float_to_half_bits(vx1);
-            uint16_t * krow = (uint16_t *) &s_k[wave][jn][0];
-            krow[lane] = k0;
-            krow[lane + 64] = k1;
+            uint16_t * krow = (uint16_t *) &s_k[wave][0];
+            wait_vmcnt<63>();
+            krow[fa_kslot(jn, lane >> 3, KU) * 8 + (lane & 7)] = k0;
+            krow[fa_kslot(jn, (lane + 64) >> 3, KU) * 8 + (lane & 7)] = k1;
             s_vnew[wave][lane] = v0;
             s_vnew[wave][lane + 64] = v1;
             if (hh == 0 && r_new < st.kc_rows) {
@@ -584,12 +604,13 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
         }
         if (__ballot(live) == 0) return;  // a fully masked chunk only had the cache row to write
     }
+    wait_vmcnt<63>();  // the K requests (ahead of the V ones) have landed
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     uint4 kr[KU];
 #pragma unroll
-    for (int u = 0; u < KU; u++) kr[u] = s_k[wave][lane][u];
+    for (int u = 0; u < KU; u++) kr[u] = s_k[wave][fa_kslot(lane, u, KU)];
     if constexpr (STEP) {
         if (jn >= 0) {
             const uint32_t vn = *(const uint32_t *) &s_vnew[wave][lane * DL];
