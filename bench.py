@@ -57,6 +57,9 @@ def parse():
     p.add_argument("--profile-iters", type=int, default=20)
     p.add_argument("--sweep", action="store_true", help="per-kernel sweep of mul_mat and flash_attn_ext shapes")
     p.add_argument("--sweep-reps", type=int, default=20)
+    p.add_argument("--mfma-probe", action="store_true",
+                   help="a short fixed program for hardware-counter runs of the wide kernels: mul_mat "
+                        "151936x1024 at N=512 (Q4_K, Q8_0) and flash_attn_ext over 8192 positions with 64 queries")
     p.add_argument("--traffic-probe", action="store_true",
                    help="fixed short program for rocprofv3 --pmc runs (copy calibration + two decode steps)")
     return p.parse_args()
@@ -467,10 +470,29 @@ def run_traffic_probe(workload: str) -> int:
     return 0
 
 
+def run_mfma_probe() -> int:
+    """the prefill-shaped kernels once each (a few computes of one-copy
+    graphs), for `rocprofv3 --pmc` runs: the tile GEMM at the vocabulary
+    projection's shape and the wide attention"""
+    from openasr_amd import ggml as g
+
+    plugin = g.plugin()
+    global ROTATE_BYTES
+    ROTATE_BYTES = 1  # one copy of each operand
+    for wtype in (g.Q4_K, g.Q8_0):
+        r = sweep_mul_mat(plugin, g, 151936, 1024, wtype, 512, 2)
+        log(f"[probe] mul_mat {r['type']} 151936x1024 N=512: {r['us']:.1f} us, {r['tops']:.1f} TOP/s")
+    r = sweep_fattn(plugin, g, 8192, 64, 2)
+    log(f"[probe] flash_attn_ext kv 8192 x 64 queries: {r['us']:.1f} us, {r['tflops']:.2f} TFLOP/s")
+    return 0
+
+
 def main() -> int:
     a = parse()
     if a.sweep:
         return run_sweep(a.sweep_reps)
+    if a.mfma_probe:
+        return run_mfma_probe()
     if a.traffic_probe:
         return run_traffic_probe(a.workload)
     if a.gpus != 1:

@@ -35,6 +35,10 @@ HIP_FLAGS = [
     # results must not depend on whether the compiler fuses a*b+c: the CPU
     # reference evaluates every expression with separate roundings
     "-ffp-contract=off",
+    # MFMA results in ordinary VGPRs: the integer sums are scaled by VALU
+    # code right after each MFMA, and results in AGPRs would cost a
+    # v_accvgpr_read per value first
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wno-unused-result",
 ]
 

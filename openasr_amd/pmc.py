@@ -12,6 +12,11 @@ scales each counter by what it reads for the copy (bytes moved / counter
 value) and reports HBM bytes per dispatch by kernel, and for the last decode
 step the bytes the quantized GEMV launches moved against their algorithmic
 bytes (weights + int8 activations + f32 outputs).
+
+    python -m openasr_amd.pmc --counters RUN_DIR [--only NAME]
+
+tabulates a run with several counters (e.g. the MFMA and VALU busy metrics
+over `bench.py --mfma-probe`): per kernel and grid, the mean per dispatch.
 """
 
 from __future__ import annotations
@@ -126,7 +131,41 @@ def markdown(s: dict) -> str:
     return "\n".join(lines)
 
 
+def counters(run_dir: str) -> dict:
+    """per kernel[grid] the mean per dispatch of every counter of a
+    multi-counter run (one row per counter per dispatch in the CSV)"""
+    per = defaultdict(dict)
+    names = {}
+    for r in _rows(run_dir):
+        i = int(r["Dispatch_Id"])
+        per[i][r["Counter_Name"]] = float(r["Counter_Value"])
+        names[i] = f"{_short(r['Kernel_Name'])}[{r['Grid_Size']}]"
+    kern = defaultdict(lambda: defaultdict(list))
+    for i, cs in per.items():
+        for c, v in cs.items():
+            kern[names[i]][c].append(v)
+    return {k: {"dispatches": len(next(iter(cs.values()))), **{c: sum(v) / len(v) for c, v in sorted(cs.items())}}
+            for k, cs in sorted(kern.items())}
+
+
+def counters_markdown(s: dict, only: str | None = None) -> str:
+    keys = sorted({c for v in s.values() for c in v if c != "dispatches"})
+    lines = ["| kernel[grid] | dispatches | " + " | ".join(keys) + " |", "|---" * (len(keys) + 2) + "|"]
+    for k, v in s.items():
+        if only and only not in k:
+            continue
+        lines.append(f"| {k} | {v['dispatches']} | " + " | ".join(f"{v.get(c, float('nan')):.4g}" for c in keys) + " |")
+    return "\n".join(lines)
+
+
 def main() -> int:
+    if len(sys.argv) > 1 and sys.argv[1] == "--counters":
+        ap = argparse.ArgumentParser()
+        ap.add_argument("--counters", dest="run_dir", required=True)
+        ap.add_argument("--only", default=None, help="kernels whose name contains this")
+        a = ap.parse_args()
+        print(counters_markdown(counters(a.run_dir), a.only))
+        return 0
     ap = argparse.ArgumentParser()
     ap.add_argument("fetch_dir")
     ap.add_argument("write_dir")
