@@ -174,6 +174,9 @@ typedef struct {
     int n_frames;      /* encoder frames the cross attention reads */
     float ln_eps;
     uint64_t seed;
+    /* FFN activation between fc1 and fc2 of the shared seq2seq block
+     * (nn/decoder.rs:1125-1138): 0 GELU (Whisper), 1 RELU, 2 GELU_ERF, 3 SILU */
+    int ffn_act;
 } oa_whisper_config;
 
 enum oa_whisper_tensor_kind {

@@ -121,6 +121,26 @@ __device__ __forceinline__ float expf_det(float x) {
     return (float) ldexp(p, (int) k);
 }
 
+// erf(x) as a fixed sequence of IEEE double operations rounded once to f32:
+// the Maclaurin series 2/sqrt(pi) sum_n (-1)^n x^(2n+1) / (n! (2n+1)), 64
+// terms, for |x| < 4 (the largest term there is ~1e5, so the double sum is
+// good to ~1e-10 absolute, far inside half an f32 ulp); +-1 beyond, where the
+// exact value rounds to +-1 in f32. The CPU reference runs the same sequence.
+__device__ __forceinline__ float erff_det(float x) {
+    if (x != x) return x;
+    const double xd = (double) x;
+    if (xd >= 4.0) return 1.0f;
+    if (xd <= -4.0) return -1.0f;
+    const double x2 = xd * xd;
+    double term = xd, sum = xd;
+#pragma unroll
+    for (int n = 1; n < 64; n++) {
+        term = term * (-x2) * (1.0 / (double) n);
+        sum = sum + term * (1.0 / (double) (2 * n + 1));
+    }
+    return (float) (sum * 1.1283791670955125739);
+}
+
 __device__ __forceinline__ void sincosf_det(float x, float & s_out, float & c_out) {
     const double xd = (double) x;
     const double k = rint(xd * 0.63661977236758134308);

@@ -24,7 +24,11 @@ class QwenConfig(C.Structure):
 class WhisperConfig(C.Structure):
     _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("ffn", C.c_int),
                 ("vocab", C.c_int), ("max_positions", C.c_int), ("n_frames", C.c_int), ("ln_eps", C.c_float),
-                ("seed", C.c_uint64)]
+                ("seed", C.c_uint64), ("ffn_act", C.c_int)]
+
+
+# FFN activations of the shared seq2seq block (oa_whisper_config.ffn_act)
+FFN_GELU, FFN_RELU, FFN_GELU_ERF, FFN_SILU = 0, 1, 2, 3
 
 
 # Whisper-tiny decoder shape: d_model 384, 4 layers, 6 heads of 64, FFN 1536, vocab 51865,
@@ -257,9 +261,9 @@ class WhisperWeights:
     """Whisper decoder weights (host bytes, Q8_0 matrices): synthesised, or
     views into a mapped whisper runtime pack (load_gguf)."""
 
-    def __init__(self, seed: int = 1234, ln_eps: float = 1e-5, **shape):
+    def __init__(self, seed: int = 1234, ln_eps: float = 1e-5, ffn_act: int = FFN_GELU, **shape):
         self.cfg = WhisperConfig(shape["d_model"], shape["n_layers"], shape["n_head"], shape["ffn"], shape["vocab"],
-                                 shape["max_positions"], shape["n_frames"], ln_eps, seed)
+                                 shape["max_positions"], shape["n_frames"], ln_eps, seed, ffn_act)
         self.ptr = lib().oa_whisper_weights_synthesize(C.byref(self.cfg))
         if not self.ptr:
             raise RuntimeError("whisper weight synthesis failed")

@@ -162,7 +162,13 @@ bool build_decode(oa_whisper_session * s, wh_graph & g) {
         state = ggml_add(ctx, linear(ctx, L[OA_WH_CROSS_O], ctx_cross, L[OA_WH_CROSS_O_B]), state);
         // MLP (:5342-5392)
         nrm = layer_norm(ctx, state, L[OA_WH_MLP_LN_W], L[OA_WH_MLP_LN_B], c.ln_eps);
-        ggml_tensor * h = ggml_gelu(ctx, linear(ctx, L[OA_WH_FC1], nrm, L[OA_WH_FC1_B]));
+        ggml_tensor * h = linear(ctx, L[OA_WH_FC1], nrm, L[OA_WH_FC1_B]);
+        switch (c.ffn_act) {  // nn/decoder.rs:1125-1138
+            case 1: h = ggml_relu(ctx, h); break;
+            case 2: h = ggml_gelu_erf(ctx, h); break;
+            case 3: h = ggml_silu(ctx, h); break;
+            default: h = ggml_gelu(ctx, h); break;
+        }
         state = ggml_add(ctx, linear(ctx, L[OA_WH_FC2], h, L[OA_WH_FC2_B]), state);
     }
     ggml_tensor * nrm = layer_norm(ctx, state, m->final_w, m->final_b, c.ln_eps);

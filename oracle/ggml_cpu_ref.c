@@ -548,6 +548,30 @@ void ref_norm(const float * x, float * y, int64_t ne0, int64_t rows, float eps) 
 
 float ref_silu(float x) { return x / (1.0f + ref_expf_det(-x)); }
 
+/* erf as a fixed sequence of double operations rounded once: the Maclaurin
+ * series 2/sqrt(pi) sum_n (-1)^n x^(2n+1) / (n! (2n+1)), 64 terms, for
+ * |x| < 4, +-1 beyond (where erf rounds to +-1 in f32). ggml-cpu's GELU_ERF
+ * (ggml_vec_gelu_erf_f32) calls libm erff, which is not reproducible across
+ * devices; this sequence is, and it is pinned against math.erf. */
+float ref_erff_det(float x) {
+    if (x != x) return x;
+    const double xd = (double) x;
+    if (xd >= 4.0) return 1.0f;
+    if (xd <= -4.0) return -1.0f;
+    const double x2 = xd * xd;
+    double term = xd, sum = xd;
+    for (int n = 1; n < 64; n++) {
+        term = term * (-x2) * (1.0 / (double) n);
+        sum = sum + term * (1.0 / (double) (2 * n + 1));
+    }
+    return (float) (sum * 1.1283791670955125739);
+}
+
+/* ggml_vec_gelu_erf_f32: 0.5 x (1 + erf(x / sqrt 2)) in f32 */
+float ref_gelu_erf(float x) { return 0.5f * x * (1.0f + ref_erff_det(x * 0.70710678118654752440f)); }
+
+float ref_relu(float x) { return x > 0.0f ? x : 0.0f; }
+
 float ref_gelu_f32(float x) {
     const float c = 0.79788456080286535587989211986876f; /* sqrt(2/pi) */
     return 0.5f * x * (1.0f + tanhf(c * x * (1.0f + 0.044715f * x * x)));

@@ -54,6 +54,9 @@ def lib() -> C.CDLL:
     s("ref_argmax_last", C.c_int32, vp, i64)
     s("ref_argmax_first", C.c_int32, vp, i64)
     s("ref_expf_det", f, f)
+    s("ref_erff_det", f, f)
+    s("ref_gelu_erf", f, f)
+    s("ref_relu", f, f)
     s("ref_sincosf_det", None, f, vp, vp)
     s("ref_flash_attn_ext", None, vp, i64, i64, vp, vp, i64, i64, vp, i64, vp, i64, i64, i64, i64, i64, f, i, i)
     _lib = L
@@ -269,7 +272,8 @@ class QwenRefBatch:
 
 class WhisperDims(C.Structure):
     _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("ffn", C.c_int),
-                ("vocab", C.c_int), ("max_positions", C.c_int), ("n_frames", C.c_int), ("ln_eps", C.c_float)]
+                ("vocab", C.c_int), ("max_positions", C.c_int), ("n_frames", C.c_int), ("ln_eps", C.c_float),
+                ("ffn_act", C.c_int)]
 
 
 class WhisperRef:
@@ -284,7 +288,7 @@ class WhisperRef:
         L.ref_whisper_step.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
                                        C.c_int32, C.c_int, C.c_void_p, C.c_int, C.c_int]
         self.dims = WhisperDims(cfg.d_model, cfg.n_layers, cfg.n_head, cfg.ffn, cfg.vocab, cfg.max_positions,
-                                cfg.n_frames, cfg.ln_eps)
+                                cfg.n_frames, cfg.ln_eps, getattr(cfg, "ffn_act", 0))
         self.table = (C.c_void_p * len(pointer_table))(*pointer_table)
         self.fidelity, self.threads = fa_fidelity, threads
         n = cfg.n_layers

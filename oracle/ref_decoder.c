@@ -242,7 +242,17 @@ void ref_qwen_decode_batch(const ref_qwen_dims * m, const void * const * t, uint
 typedef struct {
     int d_model, n_layers, n_head, ffn, vocab, max_positions, n_frames;
     float ln_eps;
+    int ffn_act; /* FFN activation (nn/decoder.rs:1125-1138): 0 GELU, 1 RELU, 2 GELU_ERF, 3 SILU */
 } ref_whisper_dims;
+
+static float wh_act(int act, float x) {
+    switch (act) {
+        case 1: return ref_relu(x);
+        case 2: return ref_gelu_erf(x);
+        case 3: return ref_silu(x);
+        default: return ref_gelu(x);
+    }
+}
 
 enum {
     W_SELF_LN_W = 0, W_SELF_LN_B, W_SELF_Q, W_SELF_Q_B, W_SELF_K, W_SELF_V, W_SELF_V_B, W_SELF_O, W_SELF_O_B,
@@ -334,7 +344,7 @@ int32_t ref_whisper_step(const ref_whisper_dims * m, const void * const * t, uin
         /* MLP */
         wh_layer_norm(x, nrm, d, (const float *) wp(t, l, W_MLP_LN_W), (const float *) wp(t, l, W_MLP_LN_B), m->ln_eps);
         wh_linear(wp(t, l, W_FC1), m->ffn, d, nrm, (const float *) wp(t, l, W_FC1_B), h, threads);
-        for (int i = 0; i < m->ffn; i++) h[i] = ref_gelu(h[i]);
+        for (int i = 0; i < m->ffn; i++) h[i] = wh_act(m->ffn_act, h[i]);
         wh_linear(wp(t, l, W_FC2), d, m->ffn, h, (const float *) wp(t, l, W_FC2_B), o, threads);
         for (int i = 0; i < d; i++) x[i] = o[i] + x[i];
     }

@@ -177,6 +177,38 @@ def test_whisper_tiny_q8_0_first_64_steps(gpu, ref):
     w.free()
 
 
+@pytest.mark.parametrize("ffn_act", [D.FFN_RELU, D.FFN_GELU_ERF, D.FFN_SILU])
+def test_seq2seq_block_ffn_activations(gpu, ref, ffn_act):
+    """the shared seq2seq block with the other FFN activations of
+    nn/decoder.rs:1125-1138 (RELU, GELU_ERF, SILU) on a Whisper-tiny-shaped
+    decoder (2 layers, 4096-token vocabulary, 200 encoder frames): 4 prompt
+    tokens and 24 greedy steps token for token against the oracle, logits
+    within 1e-2"""
+    print(f"seq2seq ffn activation {ffn_act}", flush=True)
+    shape = dict(D.WHISPER_TINY, n_layers=2, vocab=4096, n_frames=200)
+    w = D.WhisperWeights(seed=77 + ffn_act, ffn_act=ffn_act, **shape)
+    model = D.WhisperModel(w, gpu.backend)
+    sess = model.session()
+    enc, prompt = D.whisper_inputs(shape, n_prompt=4, seed=92)
+    sess.set_encoder(enc)
+    r = ref.WhisperRef(w.cfg, w.pointer_table(), fa_fidelity=5)
+    r.set_encoder(enc)
+    max_dl = 0.0
+    tok_d = tok_r = None
+    for i, t in enumerate(list(prompt) + [None] * 24):
+        t_d = int(t) if t is not None else tok_d
+        t_r = int(t) if t is not None else tok_r
+        tok_d, lg_d = sess.step(t_d, want_logits=True)
+        tok_r, lg_r = r.step(t_r)
+        max_dl = max(max_dl, float(np.abs(lg_d - lg_r).max()))
+        assert tok_d == tok_r, f"step {i}: gpu {tok_d} != cpu {tok_r}"
+    print(f"  max |dlogit| {max_dl:.2e}")
+    assert max_dl < 1e-2
+    sess.free()
+    model.free()
+    w.free()
+
+
 def test_whisper_runtime_pack_decodes_like_synthesized(gpu, tmp_path):
     """Whisper-tiny weights written as a whisper runtime pack and bound from
     the mapping: cross K/V and 32 greedy steps (tokens and logits) bit for

@@ -530,6 +530,25 @@ def test_silu_mul_and_gelu(ggml, gpu, ref):
     G.free()
 
 
+def test_relu_and_gelu_erf(ggml, gpu, ref):
+    """RELU and GELU_ERF (erf by the fixed double series both sides run) bit
+    for bit, over the range where erf bends and past its +-4 saturation"""
+    x = np.concatenate([np.linspace(-9, 9, 4096), RNG.standard_normal(4096) * 3]).astype(np.float32).reshape(2, 4096)
+    G = ggml.Graph()
+    X = G.new(ggml.F32, 4096, 2)
+    R = G.lib.ggml_relu(G.ctx, X)
+    E = G.lib.ggml_gelu_erf(G.ctx, X)
+    G.build(R, E)
+    G.allocate(gpu.buft)
+    G.set(X, x)
+    assert G.compute(gpu.backend) == 0
+    L = ref.lib()
+    want_e = np.array([L.ref_gelu_erf(float(v)) for v in x.reshape(-1)], np.float32).reshape(2, 4096)
+    assert np.array_equal(G.get(R).reshape(2, 4096), np.maximum(x, 0))
+    assert np.array_equal(G.get(E).reshape(2, 4096).view(np.uint32), want_e.view(np.uint32))
+    G.free()
+
+
 def test_set_rows_batched_kv_write(ggml, gpu):
     """f32 -> f16 rows into a [128, maxpos, 8, n_seq] cache at per-sequence rows"""
     d, maxpos, hkv, n_seq = 128, 64, 8, 4
@@ -849,4 +868,56 @@ def test_reversed_row_top1_keeps_the_first_max(ggml, gpu, n):
     for c in range(n):
         assert V - 1 - got[c] == firsts[c][0]
         assert got_last[c] == firsts[c][-1]
+    G.free()
+
+
+@pytest.mark.parametrize("n_q,n_seq", [(1, 2), (8, 1)])
+def test_naive_masked_attention_chain(ggml, gpu, ref, n_q, n_seq):
+    """the unfused attention the host emits with flash attention off
+    (nn/decoder.rs:2147-2200): scores = MUL_MAT(K f16 [128, kv, 8, s],
+    Q f32 [128, n_q, 16, s]) with the GQA broadcast of MUL_MAT's batch dims,
+    SOFT_MAX_EXT(mask [kv, n_q, 1, s], scale), V^T by CONT(TRANSPOSE), the
+    context MUL_MAT, then PERMUTE(0, 2, 1, 3) + CONT. Checked against the
+    oracle's ops composed slice by slice (f16 rows x f16-rounded activations,
+    summed in f64) within 2e-3, and against the flash_attn_ext result"""
+    d, hq, hkv, n_kv = 128, 16, 8, 512
+    print(f"naive attention chain n_q={n_q} n_seq={n_seq}", flush=True)
+    q = RNG.standard_normal((n_seq, hq, n_q, d)).astype(np.float32)
+    k = RNG.standard_normal((n_seq, hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((n_seq, hkv, n_kv, d)).astype(np.float16)
+    valid = [n_kv - 37 * s for s in range(n_seq)]
+    mask = np.full((n_seq, n_q, n_kv), -np.inf, np.float16)
+    for s in range(n_seq):
+        for i in range(n_q):
+            mask[s, i, :valid[s] - n_q + i + 1] = 0
+    scale = 1.0 / math.sqrt(d)
+    G = ggml.Graph()
+    L = G.lib
+    Q = G.new(ggml.F32, d, n_q, hq, n_seq)
+    K = G.new(ggml.F16, d, n_kv, hkv, n_seq)
+    V = G.new(ggml.F16, d, n_kv, hkv, n_seq)
+    M = G.new(ggml.F16, n_kv, n_q, 1, n_seq)
+    scores = L.ggml_mul_mat(G.ctx, K, Q)
+    probs = L.ggml_soft_max_ext(G.ctx, scores, M, scale, 0.0)
+    vt = L.ggml_cont(G.ctx, L.ggml_transpose(G.ctx, V))
+    att = L.ggml_cont(G.ctx, L.ggml_permute(G.ctx, L.ggml_mul_mat(G.ctx, vt, probs), 0, 2, 1, 3))
+    FA = L.ggml_flash_attn_ext(G.ctx, Q, K, V, M, scale, 0.0, 0.0)
+    G.build(att, FA)
+    G.allocate(gpu.buft)
+    G.set(Q, q)
+    G.set(K, k.view(np.uint16))
+    G.set(V, v.view(np.uint16))
+    G.set(M, mask.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    got = G.get(att).reshape(n_seq, n_q, hq, d)
+    fa = G.get(FA).reshape(n_seq, n_q, hq, d)
+    g = hq // hkv
+    for s in range(n_seq):
+        for h in range(hq):
+            kh, vh = k[s, h // g], v[s, h // g]
+            sc = ref.mul_mat(ref.F16, kh.view(np.uint16), n_kv, d, q[s, h])           # [n_q, n_kv]
+            p = ref.soft_max_ext(sc, mask[s].view(np.uint16), scale)
+            ctx = ref.mul_mat(ref.F16, np.ascontiguousarray(vh.T).view(np.uint16), d, n_kv, p)  # [n_q, d]
+            assert rel_err(got[s, :, h], ctx) < 2e-3, (s, h)
+    assert rel_err(got, fa) < 2e-3
     G.free()

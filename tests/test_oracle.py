@@ -505,3 +505,27 @@ def test_whisper_cross_kv_matches_brute_force(ref):
         g16 = got.view(np.float16).astype(np.float64)
         assert np.abs(g16 - want).max() <= 1e-3 * np.abs(want).max() + 1e-6
     w.free()
+
+
+def test_erf_det_within_one_ulp_of_math_erf(ref):
+    """the deterministic erf (fixed double series) against math.erf rounded to
+    f32: within one f32 ulp everywhere, equal for the vast majority, odd,
+    saturating to +-1 where erf rounds there"""
+    L = ref.lib()
+    xs = np.concatenate([np.linspace(-5, 5, 20001), RNG.standard_normal(5000) * 2.0,
+                         [0.0, -0.0, 1e-30, 3.9, 3.99, 4.0, -4.0, 1e-8]]).astype(np.float32)
+    got = np.array([L.ref_erff_det(float(x)) for x in xs], np.float32)
+    want = np.array([math.erf(float(x)) for x in xs], np.float32)
+    d = ulp_dist(got, want)
+    assert d.max() <= 1
+    assert (d == 0).mean() > 0.99
+    assert all(L.ref_erff_det(float(x)) == -L.ref_erff_det(float(-x)) for x in xs[:2000])
+    assert L.ref_erff_det(5.0) == 1.0 and L.ref_erff_det(-7.5) == -1.0
+
+
+def test_gelu_erf_and_relu_closed_forms(ref):
+    L = ref.lib()
+    for x in np.linspace(-6, 6, 1201).astype(np.float32):
+        want = 0.5 * float(x) * (1.0 + math.erf(float(x) / math.sqrt(2.0)))
+        assert abs(L.ref_gelu_erf(float(x)) - want) <= 2e-7 * max(1.0, abs(want))
+        assert L.ref_relu(float(x)) == (float(x) if x > 0 else 0.0)

@@ -297,11 +297,12 @@ class TinyWhisper:
     """A Whisper-shaped decoder from seeded numpy arrays (Q8_0 matrices),
     d 128, 2 heads of 64, FFN 256, 16 positions, 40 encoder frames."""
 
-    def __init__(self, ref, seed, n_layers=2, d=128, H=2, ffn=256, vocab=200, max_positions=16, n_frames=40):
+    def __init__(self, ref, seed, n_layers=2, d=128, H=2, ffn=256, vocab=200, max_positions=16, n_frames=40,
+                 ffn_act=0):
         self.ref = ref
         rng = np.random.default_rng(seed)
         self.cfg = SimpleNamespace(d_model=d, n_layers=n_layers, n_head=H, ffn=ffn, vocab=vocab,
-                                   max_positions=max_positions, n_frames=n_frames, ln_eps=1e-5)
+                                   max_positions=max_positions, n_frames=n_frames, ln_eps=1e-5, ffn_act=ffn_act)
 
         def mat(rows, k, scale=None):
             x = rng.standard_normal((rows, k)) * (scale if scale is not None else k ** -0.5)
@@ -353,6 +354,19 @@ def gelu64(x):
     return np.where(x <= -10, 0.0, np.where(x >= 10, x, f16_round(g(f16_round(x)))))
 
 
+def act64(act, x):
+    """the seq2seq FFN activations (nn/decoder.rs:1125-1138) in f64: GELU
+    through ggml's f16 table, RELU, GELU_ERF, SILU"""
+    if act == 1:
+        return np.maximum(x, 0.0)
+    if act == 2:
+        from math import erf
+        return 0.5 * x * (1.0 + np.vectorize(erf)(x / np.sqrt(2.0)))
+    if act == 3:
+        return silu64(x)
+    return gelu64(x)
+
+
 def whisper64(M, enc, tokens, bug=None):
     """logits [T, vocab] of the tokens at positions 0..T-1"""
     ref, c = M.ref, M.cfg
@@ -384,17 +398,22 @@ def whisper64(M, enc, tokens, bug=None):
         x = x + lin(L["cross_o"], d, d, a.reshape(T, d), L["cross_o_b"])
         n = ln64(x, L["mlp_ln_w"], lnb("mlp_ln_b"), c.ln_eps)
         h = lin(L["fc1"], ffn, d, n, L["fc1_b"])
-        h = h if bug == "no_gelu" else gelu64(h)
+        act = getattr(c, "ffn_act", 0)
+        if bug == "wrong_activation":
+            act = (act + 1) % 4
+        h = h if bug == "no_gelu" else act64(act, h)
         x = x + lin(L["fc2"], d, ffn, h, L["fc2_b"])
     n = ln64(x, M.fin_w, 0.0 if bug == "ln_without_bias" else M.fin_b, c.ln_eps)
     return mm64(ref, ref.Q8_0, M.tok, c.vocab, d, n)
 
 
-WHISPER_BUGS = ("residual_from_normed", "ln_without_bias", "cross_reads_self_cache", "no_gelu")
+WHISPER_BUGS = ("residual_from_normed", "ln_without_bias", "cross_reads_self_cache", "no_gelu", "wrong_activation")
 
 
-def test_whisper_oracle_matches_f64_restatement(ref):
-    M = TinyWhisper(ref, seed=21)
+@pytest.mark.parametrize("ffn_act", [0, 1, 2, 3])
+def test_whisper_oracle_matches_f64_restatement(ref, ffn_act):
+    """the seq2seq block with each FFN activation (0 GELU, 1 RELU, 2 GELU_ERF, 3 SILU)"""
+    M = TinyWhisper(ref, seed=21, ffn_act=ffn_act)
     enc = f32(np.random.default_rng(6).standard_normal((M.cfg.n_frames, M.cfg.d_model)))
     r = M.oracle(enc)
     tokens = [3, 150, 150, 9, 77]
