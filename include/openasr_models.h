@@ -231,6 +231,32 @@ int oa_whisper_generate(oa_whisper_session * s, int32_t first_token, int n_steps
 int oa_whisper_read_cross(const oa_whisper_session * s, int layer, uint16_t * k_out, uint16_t * v_out);
 struct ggml_cgraph * oa_whisper_decode_graph(oa_whisper_session * s);
 
+/* ---- pack storage policy (crates/openasr-core/src/models/pack_quant.rs) ---- */
+
+/* requested pack rung, enum PackQuant (pack_quant.rs:25-32) */
+enum oa_pack_quant { OA_PACK_FP16 = 0, OA_PACK_Q8_0 = 1, OA_PACK_Q3_K = 2, OA_PACK_Q4_K = 3 };
+/* a tensor's mathematical role, enum TensorRole (pack_quant.rs:51-62) */
+enum oa_tensor_role {
+    OA_ROLE_ACOUSTIC_ENCODER_MATRIX = 0,
+    OA_ROLE_TEXT_DECODER_MATRIX = 1,
+    OA_ROLE_EMBEDDING_TABLE = 2,
+    OA_ROLE_OUTPUT_PROJECTION = 3,
+    OA_ROLE_PRECISION_CRITICAL_MATRIX = 4,
+    OA_ROLE_NON_QUANTIZABLE = 5,
+};
+/* which dimension is ggml's ne0, enum QuantizedAxis (pack_quant.rs:64-68) */
+enum oa_quantized_axis { OA_AXIS_FIRST = 0, OA_AXIS_LAST = 1 };
+
+/* classify_quant_tensor_role (pack_quant.rs:179-213): the ggml type the
+ * writer stores the tensor as (GGML_TYPE_Q8_0 / Q3_K / Q4_K), -1 for "keep
+ * the rung's non-quantized representation" (the reference's None), -2 for
+ * an argument out of range. */
+int oa_classify_quant_tensor_role(const uint64_t * dims, int n_dims, int quantization, int role, int axis);
+/* TensorQuantizationContract::target_write_type (pack_quant.rs:127-147) for
+ * a resolved role and axis: only rank-2 tensors are block-quantized. Same
+ * returns. */
+int oa_quant_target_write_type(const uint64_t * dims, int n_dims, int quantization, int role, int axis);
+
 #ifdef __cplusplus
 }
 #endif

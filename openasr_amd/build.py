@@ -62,7 +62,9 @@ def _run(cmd: list[str]) -> None:
 def build_base(fp: str) -> Path:
     out = LIB / "libggml-base.so"
     srcs = sorted(str(p) for p in (PKG / "host").glob("*.cpp"))
-    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", f"-I{INCLUDE}",
+    # no contraction of a * b + c: the weight quantizers reproduce ggml-base's
+    # float operation order bit for bit
+    _run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", "-fopenmp", "-ffp-contract=off", f"-I{INCLUDE}",
           f'-DOPENASR_HOST_ABI_FINGERPRINT="{fp}"', *srcs, "-o", str(out), "-ldl"])
     return out
 

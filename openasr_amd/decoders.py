@@ -114,6 +114,8 @@ def lib() -> C.CDLL:
     s("oa_qwen_generate", i, vp, vp, i, vp, vp)
     s("oa_qwen_read_kv", i, vp, i, i, vp, vp)
     s("oa_detect_degenerate_ngram", i, vp, i, i, vp, vp, vp)
+    s("oa_classify_quant_tensor_role", i, vp, i, i, i, i)
+    s("oa_quant_target_write_type", i, vp, i, i, i, i)
     s("oa_qwen_decode_graph", vp, vp)
     _lib = L
     return L
@@ -125,6 +127,19 @@ class QwenWeights:
 
     def __init__(self, wtype: int, seed: int = 1234, rope_theta: float = 1e6, rms_eps: float = 1e-6, **shape):
         self.cfg = QwenConfig(rope_theta=rope_theta, rms_eps=rms_eps, wtype=wtype, seed=seed, **shape)
+        # every matrix must be stored as the pack writer's policy stores it
+        # for this rung (a Q4_K pack keeps Q8_0 where ne0 % 256 != 0)
+        c = self.cfg
+        q_w = c.n_head * c.head_dim
+        for name, dims, role in (("token_embd", (c.d_model, c.vocab), ROLE_EMBEDDING_TABLE),
+                                 ("attn_q/k/v", (c.d_model, q_w), ROLE_TEXT_DECODER_MATRIX),
+                                 ("attn_output", (q_w, c.d_model), ROLE_TEXT_DECODER_MATRIX),
+                                 ("ffn_gate/up", (c.d_model, c.ffn), ROLE_TEXT_DECODER_MATRIX),
+                                 ("ffn_down", (c.ffn, c.d_model), ROLE_TEXT_DECODER_MATRIX)):
+            got = target_write_type(dims, pack_rung(wtype), role)
+            if got != wtype:
+                raise ValueError(f"{name} {dims}: a {PACK_LABELS[pack_rung(wtype)]} pack stores it as ggml type "
+                                 f"{got}, not {wtype}")
         self.ptr = lib().oa_qwen_weights_synthesize(C.byref(self.cfg))
         if not self.ptr:
             raise RuntimeError("weight synthesis failed")
@@ -395,6 +410,45 @@ def detect_degenerate_ngram(tokens, max_ngram: int = 8, bound=None):
     keep = lib().oa_detect_degenerate_ngram(t.ctypes.data if t.size else None, len(t), max_ngram,
                                             table.ctypes.data if table is not None else None, C.byref(n), C.byref(r))
     return None if keep < 0 else (keep, n.value, r.value)
+
+
+# pack storage policy (crates/openasr-core/src/models/pack_quant.rs):
+# requested rungs, tensor roles, quantized axes
+PACK_FP16, PACK_Q8_0, PACK_Q3_K, PACK_Q4_K = range(4)
+(ROLE_ACOUSTIC_ENCODER_MATRIX, ROLE_TEXT_DECODER_MATRIX, ROLE_EMBEDDING_TABLE, ROLE_OUTPUT_PROJECTION,
+ ROLE_PRECISION_CRITICAL_MATRIX, ROLE_NON_QUANTIZABLE) = range(6)
+AXIS_FIRST, AXIS_LAST = range(2)
+PACK_LABELS = {PACK_FP16: "fp16", PACK_Q8_0: "q8_0", PACK_Q3_K: "q3_k", PACK_Q4_K: "q4_k"}
+GGML_Q3_K = 11
+
+
+def _policy(fn, dims, quantization: int, role: int, axis: int):
+    d = np.ascontiguousarray(dims, dtype=np.uint64)
+    r = fn(d.ctypes.data if d.size else None, int(d.size), quantization, role, axis)
+    if r == -2:
+        raise ValueError(f"pack policy: argument out of range (quantization {quantization}, role {role}, axis {axis})")
+    return None if r < 0 else r
+
+
+def classify_quant_tensor_role(dims, quantization: int, role: int, axis: int = AXIS_FIRST):
+    """classify_quant_tensor_role (pack_quant.rs:179-213): the ggml type a
+    tensor of this role and shape is written as for the requested rung, or
+    None (kept in the rung's non-quantized representation)."""
+    return _policy(lib().oa_classify_quant_tensor_role, dims, quantization, role, axis)
+
+
+def target_write_type(dims, quantization: int, role: int, axis: int = AXIS_FIRST):
+    """target_write_type (pack_quant.rs:127-147) for a resolved role: only
+    rank-2 tensors are block-quantized. role None (a contract with no
+    acoustic encoder) writes nothing quantized."""
+    if role is None:
+        return None
+    return _policy(lib().oa_quant_target_write_type, dims, quantization, role, axis)
+
+
+def pack_rung(wtype: int) -> int:
+    """the pack rung that asks for weights of ggml type wtype"""
+    return {g.Q8_0: PACK_Q8_0, g.Q4_K: PACK_Q4_K}[wtype]
 
 
 @dataclass

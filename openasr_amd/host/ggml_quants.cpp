@@ -4,11 +4,12 @@
 // importance matrix), and the f16 conversions.
 //
 // Q8_0 follows ggml-base's reference rule (d = amax/127, quants rounded half
-// away from zero). Q4_K packs eight 32-weight sub-blocks with 6-bit scales
-// and mins under f16 super-block scales (the ggml-common.h block_q4_K
-// layout); the per-sub-block (scale, min) is a least-squares fit over a grid
-// of candidate step sizes. Kernel parity does not depend on which Q4_K bytes
-// a quantizer picks: host and device consume the same bytes.
+// away from zero); Q4_K is ggml-base's quantize_row_q4_K_ref (eight 32-weight
+// sub-blocks with 6-bit scales and mins under f16 super-block scales, the
+// ggml-common.h block_q4_K layout). The ggml fork (pinned revision
+// 0db3a287511085fb1564fea3f86839f9e40ca39e, model-registry/catalog.public.json:3941)
+// is not part of the reference tree: both are restated from ggml's published
+// algorithms.
 
 #include <cmath>
 #include <cstdint>
@@ -63,75 +64,101 @@ void quantize_row_q8_0(const float * x, uint8_t * y, int64_t k) {
     }
 }
 
-// least-squares (step, offset) for one 32-weight sub-block: x ~ step*q - offset, q in 0..15
-void fit_sub_block(const float * x, float & step, float & offset) {
-    float lo = x[0], hi = x[0];
-    for (int i = 1; i < 32; i++) {
-        lo = std::fmin(lo, x[i]);
-        hi = std::fmax(hi, x[i]);
+// Q4_K: the super-block quantizer ggml_quantize_chunk runs for a NULL
+// importance matrix (quantize_row_q4_K_ref, ggml-quants.c of the pinned
+// ggml revision), in float arithmetic in ggml's operation order. Per
+// 32-weight sub-block, a weighted fit x ~ step * q + low (low <= 0, q in
+// 0..15; weights rms + |x|): a first fit from the value range, then 21
+// candidate inverse steps (14 + 0.1 i) / range, each rounding q and solving
+// the weighted least squares for (step, low) -- low clamped to 0 with the
+// step refitted -- the first strictly better weighted squared error
+// replacing the current fit.
+struct sub_fit {
+    float step, neg_low;
+};
+
+sub_fit fit_sub_block(const float * x, const float * w, uint8_t * q) {
+    constexpr int n = 32, qmax = 15, steps = 20;
+    float lo = x[0], hi = x[0], sw = 0.0f, swx = 0.0f;
+    for (int i = 0; i < n; i++) {
+        lo = x[i] < lo ? x[i] : lo;
+        hi = x[i] > hi ? x[i] : hi;
+        sw += w[i];
+        swx += w[i] * x[i];
     }
-    lo = std::fmin(lo, 0.0f);
-    if (hi <= lo) {
-        step = 0.0f;
-        offset = -lo;
-        return;
+    lo = lo > 0.0f ? 0.0f : lo;
+    if (hi == lo) {
+        std::memset(q, 0, n);
+        return {0.0f, -lo};
     }
-    double best_err = INFINITY;
-    float bs = (hi - lo) / 15.0f, bo = -lo;
-    for (int t = -10; t <= 10; t++) {
-        const float inv = (15.0f + 0.1f * (float) t) / (hi - lo);
-        int q[32];
-        double sq = 0, sx = 0, sqq = 0, sqx = 0;
-        for (int i = 0; i < 32; i++) {
-            int v = rne(inv * (x[i] - lo));
-            v = v < 0 ? 0 : (v > 15 ? 15 : v);
-            q[i] = v;
-            sq += v;
-            sx += x[i];
-            sqq += (double) v * v;
-            sqx += (double) v * x[i];
+    auto clamp_q = [](int v) { return (uint8_t) (v < 0 ? 0 : (v > qmax ? qmax : v)); };
+    float inv = (float) qmax / (hi - lo);
+    float step = 1.0f / inv;
+    float err_best = 0.0f;
+    for (int i = 0; i < n; i++) {
+        q[i] = clamp_q(rne(inv * (x[i] - lo)));
+        const float e = step * (float) q[i] + lo - x[i];
+        err_best += w[i] * (e * e);
+    }
+    uint8_t cand[n];
+    for (int t = 0; t <= steps; t++) {
+        inv = (-1.0f + 0.1f * (float) t + (float) qmax) / (hi - lo);
+        float swq = 0.0f, swqq = 0.0f, swqx = 0.0f;
+        for (int i = 0; i < n; i++) {
+            cand[i] = clamp_q(rne(inv * (x[i] - lo)));
+            const float wq = w[i] * (float) cand[i];
+            swq += wq;
+            swqq += wq * (float) cand[i];
+            swqx += wq * x[i];
         }
-        const double det = 32.0 * sqq - sq * sq;
-        if (det <= 0) continue;
-        double s = (32.0 * sqx - sq * sx) / det;
-        double m = (sx - s * sq) / 32.0;  // x ~ s*q + m with m <= 0
-        if (m > 0) {
-            m = 0;
-            s = sqq > 0 ? sqx / sqq : 0;
+        const float det = sw * swqq - swq * swq;
+        if (!(det > 0.0f)) continue;
+        float s = (sw * swqx - swx * swq) / det;
+        float low = (swqq * swx - swq * swqx) / det;
+        if (low > 0.0f) {
+            low = 0.0f;
+            s = swqx / swqq;
         }
-        if (s <= 0) continue;
-        double err = 0;
-        for (int i = 0; i < 32; i++) {
-            const double e = s * q[i] + m - x[i];
-            err += e * e;
+        float err = 0.0f;
+        for (int i = 0; i < n; i++) {
+            const float e = s * (float) cand[i] + low - x[i];
+            err += w[i] * (e * e);
         }
-        if (err < best_err) {
-            best_err = err;
-            bs = (float) s;
-            bo = (float) -m;
+        if (err < err_best) {
+            std::memcpy(q, cand, n);
+            err_best = err;
+            step = s;
+            lo = low;
         }
     }
-    step = bs;
-    offset = bo;
+    return {step, -lo};
 }
 
 void quantize_row_q4_K(const float * x, uint8_t * y, int64_t k) {
     for (int64_t sb = 0; sb < k / 256; sb++) {
         const float * xb = x + 256 * sb;
         uint8_t * o = y + 144 * sb;
-        float step[8], off[8], max_step = 0.0f, max_off = 0.0f;
+        uint8_t q[256];
+        sub_fit f[8];
+        float max_step = 0.0f, max_off = 0.0f;
         for (int j = 0; j < 8; j++) {
-            fit_sub_block(xb + 32 * j, step[j], off[j]);
-            max_step = std::fmax(max_step, step[j]);
-            max_off = std::fmax(max_off, off[j]);
+            const float * xs = xb + 32 * j;
+            float sq = 0.0f;
+            for (int l = 0; l < 32; l++) sq += xs[l] * xs[l];
+            const float rms = std::sqrt(sq / 32.0f);
+            float w[32];
+            for (int l = 0; l < 32; l++) w[l] = rms + std::fabs(xs[l]);
+            f[j] = fit_sub_block(xs, w, q + 32 * j);
+            max_step = f[j].step > max_step ? f[j].step : max_step;
+            max_off = f[j].neg_low > max_off ? f[j].neg_low : max_off;
         }
         const float is = max_step > 0 ? 63.0f / max_step : 0.0f;
         const float io = max_off > 0 ? 63.0f / max_off : 0.0f;
         uint8_t ls[8], lm[8];
         for (int j = 0; j < 8; j++) {
-            const int a = rne(is * step[j]), b = rne(io * off[j]);
-            ls[j] = (uint8_t) (a < 0 ? 0 : (a > 63 ? 63 : a));
-            lm[j] = (uint8_t) (b < 0 ? 0 : (b > 63 ? 63 : b));
+            const int a = rne(is * f[j].step), b = rne(io * f[j].neg_low);
+            ls[j] = (uint8_t) (a > 63 ? 63 : a);
+            lm[j] = (uint8_t) (b > 63 ? 63 : b);
         }
         uint8_t * sc = o + 4;
         for (int j = 0; j < 4; j++) {
@@ -143,16 +170,14 @@ void quantize_row_q4_K(const float * x, uint8_t * y, int64_t k) {
         std::memcpy(o, &dh, 2);
         std::memcpy(o + 2, &mh, 2);
         const float d = f16_to_f32(dh), dmin = f16_to_f32(mh);
-        uint8_t q[256];
+        // requantize against the coded step and offset; a sub-block whose
+        // coded step is 0 keeps the fit's q
         for (int j = 0; j < 8; j++) {
-            const float dd = d * ls[j], dm = dmin * lm[j];
+            const float dd = d * (float) ls[j], dm = dmin * (float) lm[j];
+            if (dd == 0.0f) continue;
             for (int l = 0; l < 32; l++) {
-                int v = 0;
-                if (dd != 0.0f) {
-                    v = rne((xb[32 * j + l] + dm) / dd);
-                    v = v < 0 ? 0 : (v > 15 ? 15 : v);
-                }
-                q[32 * j + l] = (uint8_t) v;
+                const int v = rne((xb[32 * j + l] + dm) / dd);
+                q[32 * j + l] = (uint8_t) (v < 0 ? 0 : (v > 15 ? 15 : v));
             }
         }
         uint8_t * qs = o + 16;

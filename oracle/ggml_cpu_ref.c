@@ -253,79 +253,113 @@ void ref_dequantize_row_q4_K(const ref_block_q4_K * x, float * y, int64_t k) {
     }
 }
 
-/* Least-squares fit of x ~ s*l - mn over a small grid of candidate inverse
- * scales (the shape of ggml's make_qkx2_quants search, restated without its
- * importance weights). Returns s >= 0 and mn >= 0. The exact Q4_K quantizer
- * search does not affect kernel parity: CPU and GPU consume the same bytes. */
-static void fit_subblock_q4(const float * x, int n, float * s_out, float * mn_out) {
-    float lo = x[0], hi = x[0];
-    for (int i = 1; i < n; i++) {
-        lo = x[i] < lo ? x[i] : lo;
-        hi = x[i] > hi ? x[i] : hi;
+/* ggml's Q4_K weight quantizer, quantize_row_q4_K_ref of ggml-quants.c at
+ * the fork's pinned revision (0db3a287511085fb1564fea3f86839f9e40ca39e,
+ * model-registry/catalog.public.json:3941), which ggml_quantize_chunk runs
+ * for a NULL importance matrix (gguf_write.rs:579-588). The fork is absent
+ * from the reference tree; this restates ggml's published algorithm, in
+ * float arithmetic in ggml's operation order:
+ *  - each 32-weight sub-block is fitted as x ~ scale * L + min (min <= 0,
+ *    L in 0..15) by make_qkx2_quants: weights av + |x| (av the sub-block's
+ *    RMS); a first fit from the range, then 21 candidate inverse scales
+ *    (14 + 0.1 is) / (max - min), each giving L and a weighted least-squares
+ *    (scale, min) (min clamped to 0 with the scale refitted), the candidate
+ *    of smallest weighted squared error replacing the first fit only when
+ *    strictly smaller;
+ *  - scales and -mins are coded in 6 bits against the block's largest
+ *    (d = max_scale / 63, dmin = max_min / 63 as f16);
+ *  - the weights are requantized against the coded values; a sub-block
+ *    whose coded scale is 0 keeps the search's L. */
+static int q4k_nearest(float v) { return nearest_even(v); }  /* ggml nearest_int: v + 1.5*2^23 */
+
+static float q4k_fit(const float * x, const float * w, uint8_t * L, float * neg_min) {
+    enum { n = 32, nmax = 15, nstep = 20 };
+    const float rmin = -1.0f, rdelta = 0.1f;
+    uint8_t aux[32];
+    float lo = x[0], hi = x[0], sw = 0.0f, sx = 0.0f;
+    for (int i = 0; i < n; i++) {
+        if (x[i] < lo) lo = x[i];
+        if (x[i] > hi) hi = x[i];
+        sw += w[i];
+        sx += w[i] * x[i];
     }
     if (lo > 0.0f) lo = 0.0f;
-    if (hi <= lo) {
-        *s_out = 0.0f;
-        *mn_out = -lo;
-        return;
+    if (hi == lo) {
+        memset(L, 0, n);
+        *neg_min = -lo;
+        return 0.0f;
     }
-    float best_s = (hi - lo) / 15.0f, best_min = lo, best_err = INFINITY;
-    for (int t = -10; t <= 10; t++) {
-        const float iscale = (15.0f + 0.1f * (float) t) / (hi - lo);
-        double sl = 0, sx = 0, sll = 0, slx = 0;
-        int lq[32];
+    float iscale = (float) nmax / (hi - lo);
+    float scale = 1.0f / iscale;
+    float best = 0.0f;
+    for (int i = 0; i < n; i++) {
+        int l = q4k_nearest(iscale * (x[i] - lo));
+        l = l < 0 ? 0 : (l > nmax ? nmax : l);
+        L[i] = (uint8_t) l;
+        const float e = scale * (float) l + lo - x[i];
+        best += w[i] * (e * e);
+    }
+    for (int is = 0; is <= nstep; is++) {
+        iscale = (rmin + rdelta * (float) is + (float) nmax) / (hi - lo);
+        float sl = 0.0f, sl2 = 0.0f, sxl = 0.0f;
         for (int i = 0; i < n; i++) {
-            int l = nearest_even(iscale * (x[i] - lo));
-            l = l < 0 ? 0 : (l > 15 ? 15 : l);
-            lq[i] = l;
-            sl += l;
-            sx += x[i];
-            sll += (double) l * l;
-            slx += (double) l * x[i];
+            int l = q4k_nearest(iscale * (x[i] - lo));
+            l = l < 0 ? 0 : (l > nmax ? nmax : l);
+            aux[i] = (uint8_t) l;
+            const float wl = w[i] * (float) l;
+            sl += wl;
+            sl2 += wl * (float) l;
+            sxl += wl * x[i];
         }
-        const double det = n * sll - sl * sl;
-        if (det <= 0) continue;
-        double s = (n * slx - sl * sx) / det;
-        double mn = (sx - s * sl) / n;
-        if (mn > 0) {
-            mn = 0;
-            s = sll > 0 ? slx / sll : 0;
+        const float det = sw * sl2 - sl * sl;
+        if (!(det > 0.0f)) continue;
+        float s = (sw * sxl - sx * sl) / det;
+        float m = (sl2 * sx - sl * sxl) / det;
+        if (m > 0.0f) {
+            m = 0.0f;
+            s = sxl / sl2;
         }
-        if (s <= 0) continue;
-        double err = 0;
+        float err = 0.0f;
         for (int i = 0; i < n; i++) {
-            const double e = s * lq[i] + mn - x[i];
-            err += e * e;
+            const float e = s * (float) aux[i] + m - x[i];
+            err += w[i] * (e * e);
         }
-        if (err < best_err) {
-            best_err = (float) err;
-            best_s = (float) s;
-            best_min = (float) mn;
+        if (err < best) {
+            memcpy(L, aux, n);
+            best = err;
+            scale = s;
+            lo = m;
         }
     }
-    *s_out = best_s;
-    *mn_out = -best_min;
+    *neg_min = -lo;
+    return scale;
 }
 
 void ref_quantize_row_q4_K(const float * x, ref_block_q4_K * y, int64_t k) {
     const int64_t nb = k / REF_QK_K;
     for (int64_t i = 0; i < nb; i++) {
         const float * xb = x + i * REF_QK_K;
-        float scales[8], mins[8];
+        uint8_t L[REF_QK_K];
+        float scales[8], mins[8], wt[32];
         float max_scale = 0.0f, max_min = 0.0f;
         for (int j = 0; j < 8; j++) {
-            fit_subblock_q4(xb + 32 * j, 32, &scales[j], &mins[j]);
-            max_scale = scales[j] > max_scale ? scales[j] : max_scale;
-            max_min = mins[j] > max_min ? mins[j] : max_min;
+            const float * xs = xb + 32 * j;
+            float ss = 0.0f;
+            for (int l = 0; l < 32; l++) ss += xs[l] * xs[l];
+            const float av = sqrtf(ss / 32.0f);
+            for (int l = 0; l < 32; l++) wt[l] = av + fabsf(xs[l]);
+            scales[j] = q4k_fit(xs, wt, L + 32 * j, &mins[j]);
+            if (scales[j] > max_scale) max_scale = scales[j];
+            if (mins[j] > max_min) max_min = mins[j];
         }
         const float inv_scale = max_scale > 0 ? 63.0f / max_scale : 0.0f;
         const float inv_min = max_min > 0 ? 63.0f / max_min : 0.0f;
         uint8_t ls[8], lm[8];
         for (int j = 0; j < 8; j++) {
-            int a = nearest_even(inv_scale * scales[j]);
-            int b = nearest_even(inv_min * mins[j]);
-            ls[j] = (uint8_t) (a > 63 ? 63 : (a < 0 ? 0 : a));
-            lm[j] = (uint8_t) (b > 63 ? 63 : (b < 0 ? 0 : b));
+            const int a = q4k_nearest(inv_scale * scales[j]);
+            const int b = q4k_nearest(inv_min * mins[j]);
+            ls[j] = (uint8_t) (a > 63 ? 63 : a);
+            lm[j] = (uint8_t) (b > 63 ? 63 : b);
         }
         memset(y[i].scales, 0, 12);
         for (int j = 0; j < 4; j++) {
@@ -337,19 +371,15 @@ void ref_quantize_row_q4_K(const float * x, ref_block_q4_K * y, int64_t k) {
         y[i].dmin = ref_fp32_to_fp16(max_min / 63.0f);
         const float d = ref_fp16_to_fp32(y[i].d);
         const float dmin = ref_fp16_to_fp32(y[i].dmin);
-        uint8_t L[REF_QK_K];
         for (int j = 0; j < 8; j++) {
             uint8_t sc, m;
             ref_get_scale_min_k4(j, y[i].scales, &sc, &m);
-            const float dd = d * sc;
-            const float dm = dmin * m;
+            const float dd = d * (float) sc;
+            if (dd == 0.0f) continue;  /* keeps the search's L */
+            const float dm = dmin * (float) m;
             for (int l = 0; l < 32; l++) {
-                int q = 0;
-                if (dd != 0.0f) {
-                    q = nearest_even((xb[32 * j + l] + dm) / dd);
-                    q = q < 0 ? 0 : (q > 15 ? 15 : q);
-                }
-                L[32 * j + l] = (uint8_t) q;
+                int q = q4k_nearest((xb[32 * j + l] + dm) / dd);
+                L[32 * j + l] = (uint8_t) (q < 0 ? 0 : (q > 15 ? 15 : q));
             }
         }
         for (int c = 0; c < 4; c++) {

@@ -44,6 +44,18 @@ def test_plugin_exports_every_declared_symbol(ggml):
     assert not missing, missing
 
 
+def test_models_library_exports_every_declared_symbol():
+    from openasr_amd import decoders as D
+
+    lib = D.lib()
+    names = declared("openasr_models.h")
+    for required in ("oa_qwen_decode_step", "oa_detect_degenerate_ngram", "oa_classify_quant_tensor_role",
+                     "oa_whisper_decode_step"):
+        assert required in names
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
 def test_plugin_imports_ggml_base_not_registry(ggml):
     import subprocess
     out = subprocess.run(["readelf", "-d", str(ggml.PLUGIN_PATH)], capture_output=True, text=True).stdout

@@ -118,6 +118,62 @@ def test_q4_K_quantizer_roundtrip(ref):
     assert np.all(err <= rng / 15.0 * 0.75 + 1e-6)
 
 
+def test_q4_K_quantizer_recovers_an_exact_grid(ref):
+    """Weights on an exact Q4_K grid, x = (k_j q - n_j) 2^-12 with 6-bit step
+    codes k_j and min codes n_j (63 among each) and every sub-block spanning
+    q = 0..15: any fit that keeps an exact solution must code d = dmin =
+    2^-12, scales k, mins n and quants q -- the bytes the independent packer
+    writes. Pins the 6-bit coding against the largest scale, the f16 super
+    scales, the requantization and the packing, whatever the search's
+    candidate order."""
+    for trial in range(4):
+        k = RNG.integers(1, 64, 8)
+        n = RNG.integers(0, 64, 8)
+        k[RNG.integers(0, 8)] = 63
+        n[RNG.integers(0, 8)] = 63
+        q = RNG.integers(0, 16, 256)
+        for j in range(8):
+            pos = RNG.choice(32, 2, replace=False)
+            q[32 * j + pos[0]], q[32 * j + pos[1]] = 0, 15
+        x = np.array([(k[i // 32] * q[i] - n[i // 32]) * 2.0 ** -12 for i in range(256)], np.float32)
+        want = pack_q4_K(np.float16(2.0 ** -12), np.float16(2.0 ** -12), k, n, q)
+        got = ref.quantize_weights(ref.Q4_K, x.reshape(1, -1))
+        assert np.array_equal(got, want), trial
+
+
+def test_q4_K_quantizer_closed_forms(ref):
+    """An all-zero block codes to zero bytes; a constant positive block c is
+    the top quant of step c/15 (min 0), a constant negative block the offset
+    alone (step 0): both dequantize to c within the f16 super scale's
+    rounding (|c| / 945 a normal f16, so that rounding is relative)."""
+    assert not ref.quantize_weights(ref.Q4_K, np.zeros((1, 256), np.float32)).any()
+    for c in (0.37, 0.09, -0.52, -0.2):
+        x = np.full((1, 256), c, np.float32)
+        blk = ref.quantize_weights(ref.Q4_K, x)
+        y = ref.dequantize(ref.Q4_K, blk, 256)
+        assert np.allclose(y, c, rtol=2 ** -10, atol=0), c
+        qs = blk[16:]
+        if c > 0:
+            assert np.all(qs == 0xFF), c  # quant 15 in both nibbles
+        else:
+            assert not qs.any(), c
+
+
+def test_q4_K_quantizer_host_and_oracle_agree(ref, ggml):
+    """ggml_quantize_chunk of the host library (the bytes packs and the
+    device consume) and the oracle's restatement of the same quantizer give
+    the same bytes on N(0, s) rows, mixed-magnitude sub-blocks, blocks with
+    one outlier, constant and subnormal blocks."""
+    rows = [RNG.standard_normal(1024) * s for s in (0.02, 1.0, 300.0)]
+    mixed = RNG.standard_normal(1024) * np.repeat(10.0 ** RNG.uniform(-4, 1, 32), 32)
+    outlier = RNG.standard_normal(1024) * 0.01
+    outlier[::97] = 3.0
+    rows += [mixed, outlier, np.full(1024, 0.25), np.full(1024, -1e-3),
+             RNG.standard_normal(1024) * 1e-40, np.abs(RNG.standard_normal(1024))]
+    x = np.stack(rows).astype(np.float32)
+    assert np.array_equal(ggml.quantize(ggml.Q4_K, x), ref.quantize_weights(ref.Q4_K, x))
+
+
 # ----------------------------------------------------------------- Q8_K --
 
 def test_q8_K_known_answer_and_invariants(ref):
