@@ -78,6 +78,32 @@ def weight_bytes(cfg, wtype) -> dict:
     return out
 
 
+def workload_text(name: str) -> dict:
+    """the metric, dtype, data and model fields of the bench line, from the
+    workload's own shape, weight type and batch"""
+    from openasr_amd import decoders as D
+    from openasr_amd import ggml as g
+
+    wl = D.WORKLOADS[name]
+    sh = wl.shape
+    size = {1024: "0.6B", 2048: "1.7B"}.get(sh["d_model"], f"d{sh['d_model']}")
+    wt = {g.Q4_K: ("Q4_K", "q4_K weights x q8_K activations (int8 dot, f64 block sums)"),
+          g.Q8_0: ("Q8_0", "q8_0 weights x q8_0 activations (int8 dot, f64 block sums)")}[wl.wtype]
+    return {
+        "metric": f"decode tokens/sec @ batch {wl.n_seq} (Qwen3-{size}-shaped {wt[0]} decoder); "
+                  "quantized mul_mat HBM GB/s as % of peak",
+        "dtype": f"{wt[1]}, f16 KV, f32 activations",
+        "data": f"synthetic: random-init N(0,0.02) weights quantized to {wt[0]}, seeded N(0,1) "
+                f"{wl.prefix}-position prefixes",
+        "model": f"qwen3-{size.lower()}-shaped (hidden {sh['d_model']}, {sh['n_layers']} layers, "
+                 f"{sh['n_head']}/{sh['n_kv_head']} heads, head_dim {sh['head_dim']}, ffn {sh['ffn']}, "
+                 f"vocab {sh['vocab']})",
+        "batch": wl.n_seq,
+        "seq_len": wl.max_positions,
+        "kernel": "k_gemv_q4_K" if wl.wtype == g.Q4_K else ("k_gemv1_q8_0" if wl.n_seq == 1 else "k_gemv_q8_0"),
+    }
+
+
 def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cpu: bool, cpu_seconds: float,
                  cpu_variants: bool = True, full_run: bool = False):
     from openasr_amd import decoders as D
@@ -531,8 +557,9 @@ def main() -> int:
         traffic = round(tj["decode_step"]["gemv_hbm_bytes_per_launch"], 1)
         traffic_source = (f"not measured in this run: profiles/{tpath.name} (rocprofv3 FETCH_SIZE and WRITE_SIZE "
                           f"passes of bench.py --traffic-probe) at commit {tj.get('commit', 'unrecorded')}")
+    main_wl_text = workload_text(a.workload)
     out = {
-        "metric": "decode tokens/sec @ batch 8 (Qwen3-0.6B-shaped Q4_K decoder); quantized mul_mat HBM GB/s as % of peak",
+        "metric": main_wl_text["metric"],
         "value": round(main_r["tok_s"], 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -542,17 +569,17 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_K weights x q8_K activations (int8 dot, f64 block sums), f16 KV, f32 activations",
-        "data": "synthetic: random-init N(0,0.02) weights quantized to Q4_K, seeded N(0,1) 375-position prefixes",
-        "config": {"workload": a.workload, "model": "qwen3-0.6b-shaped (hidden 1024, 28 layers, 16/8 heads, "
-                   "head_dim 128, ffn 3072, vocab 151936)", "global_batch": 8, "seq_len": 1024,
-                   "prefill_positions": main_r["n_prefill"], "parallelism": "single-gpu"},
+        "dtype": main_wl_text["dtype"],
+        "data": main_wl_text["data"],
+        "config": {"workload": a.workload, "model": main_wl_text["model"], "global_batch": main_wl_text["batch"],
+                   "seq_len": main_wl_text["seq_len"], "prefill_positions": main_r["n_prefill"],
+                   "parallelism": "single-gpu"},
         "roofline": {"bound": "hbm", "achieved": round(main_r["gemv_gbs"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(frac, 4), "traffic": traffic, "traffic_source": traffic_source,
                      "copy_gbs_measured": round(copy_gbs, 1),
                      "alg_bytes_per_launch": round(main_r["weight_bytes"] / max(1, main_r["gemv_launches"]), 1),
                      "launches": main_r["gemv_launches"],
-                     "kernel": "k_gemv_q4_K: the quantized GEMV launches of one decode step (per layer QKV, "
+                     "kernel": f"{main_wl_text['kernel']}: the quantized GEMV launches of one decode step (per layer QKV, "
                                "o-proj+residual, gate+up SwiGLU, down+residual; lm_head), algorithmic bytes "
                                "(weights + int8 activations + f32 outputs) / summed launch time"},
         "cpu_baseline": main_r["cpu"],

@@ -9,37 +9,46 @@
 
 namespace mi355x {
 
-// one workgroup per entry; 16-byte pieces when the entry is 16-byte aligned
-// (each thread requests up to four pieces before it stores any), bytes otherwise
+namespace {
+
+// bytes one workgroup copies: one 16-byte piece per thread, so every read of
+// host memory is in flight at once and a launch costs one PCIe round trip
+// whatever the entry sizes (a 64 KB mask is 16 workgroups, not 16 dependent
+// passes of one)
+constexpr uint32_t kChunk = 256 * 16;
+
+__host__ __device__ inline uint32_t entry_chunks(uint32_t n) { return n == 0 ? 1u : (n + kChunk - 1) / kChunk; }
+
+}  // namespace
+
+// the workgroups of entry k follow those of entries 0..k-1; 16-byte pieces
+// when the entry is 16-byte aligned, bytes otherwise
 __global__ __launch_bounds__(256) void k_apply_uploads(upload_batch b) {
-    const upload_entry e = b.e[blockIdx.x];
+    uint32_t blk = blockIdx.x;
+    int k = 0;
+    for (; k < b.n - 1; k++) {
+        const uint32_t c = entry_chunks(b.e[k].n);
+        if (blk < c) break;
+        blk -= c;
+    }
+    const upload_entry e = b.e[k];
     const char * src = b.src + e.off;
-    const int tid = (int) threadIdx.x;
+    const uint32_t lo = blk * kChunk;
+    const uint32_t hi = min(e.n, lo + kChunk);
+    const uint32_t tid = threadIdx.x;
     if ((((uintptr_t) e.dst) | (uintptr_t) src | e.n) % 16 == 0) {
-        const uint32_t n16 = e.n / 16;
-        const uint4 * s4 = (const uint4 *) src;
-        uint4 * d4 = (uint4 *) e.dst;
-        for (uint32_t base = 0; base < n16; base += 4 * 256) {
-            uint4 v[4];
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t i = base + (uint32_t) (k * 256 + tid);
-                if (i < n16) v[k] = s4[i];
-            }
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const uint32_t i = base + (uint32_t) (k * 256 + tid);
-                if (i < n16) d4[i] = v[k];
-            }
-        }
+        const uint32_t i = lo + tid * 16;
+        if (i < hi) *(uint4 *) (e.dst + i) = *(const uint4 *) (src + i);
     } else {
-        for (uint32_t i = (uint32_t) tid; i < e.n; i += 256) e.dst[i] = src[i];
+        for (uint32_t i = lo + tid; i < hi; i += 256) e.dst[i] = src[i];
     }
 }
 
 void launch_apply_uploads(const upload_batch & b, hipStream_t s) {
     if (b.n <= 0) return;
-    hipLaunchKernelGGL(k_apply_uploads, dim3((unsigned) b.n), dim3(256), 0, s, b);
+    uint32_t blocks = 0;
+    for (int k = 0; k < b.n; k++) blocks += entry_chunks(b.e[k].n);
+    hipLaunchKernelGGL(k_apply_uploads, dim3(blocks), dim3(256), 0, s, b);
     note_hip_error(hipGetLastError());
 }
 

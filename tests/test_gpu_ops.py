@@ -792,7 +792,8 @@ def test_staged_uploads_keep_write_order(ggml, gpu):
     every write before it, more writes than one apply launch takes all land
     (4-byte pieces at 4-byte offsets: the unaligned path), a write too large
     to stage lands after the staged ones before it, and a compute sees the
-    writes queued just before it."""
+    writes queued just before it, and writes larger than one apply
+    workgroup's piece land whole."""
     G = ggml.Graph()
     L = G.lib
     n = 131072  # 512 KB: a whole-tensor write takes the synchronous path
@@ -825,6 +826,15 @@ def test_staged_uploads_keep_write_order(ggml, gpu):
     # staged writes right before a compute
     put(np.full(16, 9.0), 4096)
     big[4096:4112] = 9.0
+    assert G.compute(gpu.backend) == 0
+    assert np.array_equal(G.get(Y).reshape(-1), big * 2.0)
+    # writes that span several apply workgroups in one launch: 100 KB aligned
+    # (16-byte pieces), 9996 bytes at a 4-byte offset (the byte path), and a
+    # one-piece write between them
+    for arr, off in ((RNG.standard_normal(25600), 8192), (np.full(4, 3.0), 36000),
+                     (RNG.standard_normal(2499), 40001)):
+        put(arr, off)
+        big[off:off + len(arr)] = arr
     assert G.compute(gpu.backend) == 0
     assert np.array_equal(G.get(Y).reshape(-1), big * 2.0)
     # a staged write into a buffer that is then freed
