@@ -372,31 +372,46 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
         }
     }
     __syncthreads();
+    // per element two chains (L, O), each in chunk order; every batch of
+    // chunks requests the partials of all this thread's elements before any
+    // is added, so a span of nc chunks costs nc / CB round trips, not NE times
+    // as many
+    double L[NE], O[NE];
 #pragma unroll
     for (int e = 0; e < NE; e++) {
-        if (!ev[e]) continue;
-        const int r = er[e];
-        double L = 0.0, O = 0.0;  // two chains, each in chunk order
-        for (int c0 = 0; c0 < nc; c0 += CB) {
-            if (c0 > 0) {
-                const float * pa = part_acc + ((prow + r) * nc + c0) * D + ed[e];
+        L[e] = 0.0;
+        O[e] = 0.0;
+    }
+    for (int c0 = 0; c0 < nc; c0 += CB) {
+        if (c0 > 0) {
+#pragma unroll
+            for (int e = 0; e < NE; e++) {
+                const float * pa = part_acc + ((prow + er[e]) * nc + c0) * D + ed[e];
 #pragma unroll
                 for (int k = 0; k < CB; k++) pv[e][k] = pa[(int64_t) (min(c0 + k, nc - 1) - c0) * D];
             }
-            // a chunk with w = 0 adds +0, which leaves a sum that starts at +0
-            // unchanged, as skipping it would (its partials may be stale)
+        }
+        // a chunk with w = 0 adds +0, which leaves a sum that starts at +0
+        // unchanged, as skipping it would (its partials may be stale)
+#pragma unroll
+        for (int e = 0; e < NE; e++) {
+            const int r = er[e];
 #pragma unroll
             for (int k = 0; k < CB; k++) {
                 if (c0 + k >= nc) break;
                 const double w = s_w[r][c0 + k];
                 const double tl = w * s_l[r][c0 + k], to = w * (double) pv[e][k];
-                L += w != 0.0 ? tl : 0.0;
-                O += w != 0.0 ? to : 0.0;
+                L[e] += w != 0.0 ? tl : 0.0;
+                O[e] += w != 0.0 ? to : 0.0;
             }
         }
-        const float o = L == 0.0 ? 0.0f : (float) (O / L);
-        out[fa_orow(a, t, r) * D + ed[e]] = o;
-        s_out[r][ed[e]] = o;
+    }
+#pragma unroll
+    for (int e = 0; e < NE; e++) {
+        if (!ev[e]) continue;
+        const float o = L[e] == 0.0 ? 0.0f : (float) (O[e] / L[e]);
+        out[fa_orow(a, t, er[e]) * D + ed[e]] = o;
+        s_out[er[e]][ed[e]] = o;
     }
     if (a.qtype >= 0) {
         __syncthreads();

@@ -172,8 +172,11 @@ def main() -> int:
     ap.add_argument("--workload", default=None)
     ap.add_argument("--out", default=None)
     ap.add_argument("--md", action="store_true", help="print the markdown tables instead of the JSON")
+    ap.add_argument("--commit", default=None, help="the commit the counter runs were taken at (recorded in the JSON)")
     a = ap.parse_args()
     s = summarize(a.fetch_dir, a.write_dir, a.workload)
+    if a.commit:
+        s["commit"] = a.commit
     text = json.dumps(s, indent=1)
     if a.out:
         with open(a.out, "w") as f:

@@ -90,6 +90,24 @@ def test_tiny_decoder_token_exact(gpu, ref, wname, n_seq):
     run_pair(gpu, ref, TINY, wt, n_seq, prefix=300, prompt=5, steps=24, max_pos=512)
 
 
+HEAD128 = dict(d_model=256, n_layers=2, n_head=4, n_kv_head=2, head_dim=128, ffn=512, vocab=1000)
+MHA128 = dict(d_model=256, n_layers=2, n_head=2, n_kv_head=2, head_dim=128, ffn=512, vocab=1000)
+
+
+@pytest.mark.parametrize("name,shape,n_seq,prefix", [
+    ("chunk 8 goes live at position 512", HEAD128, 3, 490),
+    ("every chunk of the 1024-position arena live", HEAD128, 2, 978),
+    ("one query head per kv head", MHA128, 2, 490),
+])
+def test_attention_step_spans_of_the_arena(gpu, ref, name, shape, n_seq, prefix):
+    """decode steps of 128-wide heads over a 1024-position arena (16
+    64-position chunks) at positions where the chunks past the first eight
+    go live, up to the arena's last row, with two query heads per kv head and
+    with one: token-exact, KV caches bit-exact"""
+    print(f"attention step spans: {name}", flush=True)
+    run_pair(gpu, ref, shape, g.Q4_K, n_seq, prefix=prefix, prompt=5, steps=40, max_pos=1024)
+
+
 @pytest.mark.parametrize("n_seq", [1, 3])
 def test_tiny_decoder_reversed_top1_head(gpu, ref, n_seq):
     """the step graphs with the reference's reversed-row top-1 head (GET_ROWS
