@@ -1,0 +1,206 @@
+// k_gemm_float.hip -- GGML_OP_MUL_MAT with float weights (F16 or F32 src0)
+// over many columns, on the matrix cores: the dense projections and the
+// convolution GEMM of the audio encoders (crates/openasr-core/src/nn/conv.rs:
+// 82-110, nn/encoder.rs:678-870, models/qwen/audio_encoder.rs:520-668) and
+// the score / context products of the unfused attention chain
+// (nn/decoder.rs:2154-2200). Call site of the op:
+// crates/openasr-core/src/ggml_runtime/cpu_graph.rs:3652-3686.
+//
+// Operand types follow ggml-cpu's vec_dot_type rule: an F16 src0 takes its
+// columns rounded to f16 (f16 x f16 products, exact in f32, summed in f32 on
+// v_mfma_f32_16x16x32_f16); an F32 src0 takes f32 columns (an F16 src1 is
+// widened) on v_mfma_f32_16x16x4f32. The sums are f32 in the matrix core's
+// order: the result is within float tolerance of the reference, not bit
+// for bit (the CPU's own SIMD reduction order differs by ISA as well).
+//
+// Tiling: a workgroup of four waves owns a 64 (rows of src0) x 64 (columns)
+// output tile and walks K in 32-wide slabs staged through LDS, the next
+// slab's global loads in flight while the current one is multiplied. The
+// columns are the MFMA A operand and the weight rows the B operand, so each
+// lane ends with one output row (lane % 16) of four columns, and a store of
+// the tile writes 64-byte runs of consecutive rows.
+#include <type_traits>
+
+#include "../mi355x_common.h"
+#include "../ops.h"
+
+namespace mi355x {
+
+namespace {
+
+constexpr int kGfBM = 64, kGfBN = 64, kGfBK = 32;
+constexpr int kGfThreads = 256;
+
+typedef float gf_v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 gf_v8h __attribute__((ext_vector_type(8)));
+
+// element k of a row of type f16 (t16) or f32, as float
+__device__ __forceinline__ float gf_elem(const char * row, int64_t k, bool t16) {
+    return t16 ? half_bits_to_float(((const uint16_t *) row)[k]) : ((const float *) row)[k];
+}
+
+// eight consecutive elements k0 .. k0 + 7 of a row (zero past K), as floats;
+// vec: the row and k0 are 16-byte aligned for this type (one or two vector loads)
+__device__ __forceinline__ void gf_load8(const char * row, int64_t k0, int64_t K, bool t16, bool vec, bool live,
+                                         float (&v)[8]) {
+    if (live && vec && k0 + 8 <= K) {
+        if (t16) {
+            const uint4 w = *(const uint4 *) (row + 2 * k0);
+            const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                v[2 * i] = half_bits_to_float((uint16_t) (u[i] & 0xFFFF));
+                v[2 * i + 1] = half_bits_to_float((uint16_t) (u[i] >> 16));
+            }
+        } else {
+            const float4 a = *(const float4 *) (row + 4 * k0), b = *(const float4 *) (row + 4 * k0 + 16);
+            v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) v[i] = live && k0 + i < K ? gf_elem(row, k0 + i, t16) : 0.0f;
+}
+
+}  // namespace
+
+// F16 = true: f16 operands (an F16 src0), else f32 operands
+template <bool F16>
+__global__ __launch_bounds__(kGfThreads) void k_gemm_float(gemm_float_args g) {
+    constexpr int PADE = F16 ? 8 : 4;  // row padding of the LDS slabs, in elements
+    using T = typename std::conditional<F16, _Float16, float>::type;
+    __shared__ __align__(16) T sa[kGfBM][kGfBK + PADE];  // weight rows x k
+    __shared__ __align__(16) T sb[kGfBN][kGfBK + PADE];  // columns x k
+    const int tid = (int) threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t m0 = (int64_t) blockIdx.x * kGfBM, n0 = (int64_t) blockIdx.y * kGfBN;
+    const int i2 = (int) blockIdx.z % g.ne2, i3 = (int) blockIdx.z / g.ne2;
+    const char * abase = g.a + (int64_t) (i2 / g.r2) * g.a_nb2 + (int64_t) (i3 / g.r3) * g.a_nb3;
+    const char * bbase = g.b + (int64_t) i2 * g.b_nb2 + (int64_t) i3 * g.b_nb3;
+    char * dbase = g.d + (int64_t) i2 * g.d_nb2 + (int64_t) i3 * g.d_nb3;
+
+    // staging: thread t loads row / column t / 4, elements 8 (t % 4) .. + 7 of the slab
+    const int srow = tid >> 2, sk = (tid & 3) * 8;
+    const bool a_live = m0 + srow < g.M, b_live = n0 + srow < g.N;
+    const char * arow = abase + (a_live ? m0 + srow : 0) * g.a_nb1;
+    const char * brow = bbase + (b_live ? n0 + srow : 0) * g.b_nb1;
+    float av[8], bv[8];
+    gf_load8(arow, sk, g.K, g.a_f16, g.a_vec, a_live, av);
+    gf_load8(brow, sk, g.K, g.b_f16, g.b_vec, b_live, bv);
+
+    // wave w: rows (w & 1) * 32 .. + 31, columns (w >> 1) * 32 .. + 31 of the tile
+    const int wr = (wave & 1) * 32, wc = (wave >> 1) * 32;
+    gf_v4f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = gf_v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int64_t k0 = 0; k0 < g.K; k0 += kGfBK) {
+        // the slab into LDS (columns rounded to f16 for an F16 src0, as
+        // ggml-cpu converts src1 to the weight's vec_dot type)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            sa[srow][sk + i] = (T) av[i];
+            sb[srow][sk + i] = F16 ? (T) round_to_half(bv[i]) : (T) bv[i];
+        }
+        __syncthreads();
+        // the next slab's loads, in flight under this slab's MFMAs
+        if (k0 + kGfBK < g.K) {
+            gf_load8(arow, k0 + kGfBK + sk, g.K, g.a_f16, g.a_vec, a_live, av);
+            gf_load8(brow, k0 + kGfBK + sk, g.K, g.b_f16, g.b_vec, b_live, bv);
+        }
+        const int r16 = lane & 15, kg = lane >> 4;
+        if constexpr (F16) {
+            // A: column wc + 16 j + r16, k 8 kg .. + 7; B: row wr + 16 i + r16, same k
+            gf_v8h bo[2], ao[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) bo[j] = *(const gf_v8h *) &sb[wc + 16 * j + r16][8 * kg];
+#pragma unroll
+            for (int i = 0; i < 2; i++) ao[i] = *(const gf_v8h *) &sa[wr + 16 * i + r16][8 * kg];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bo[j], ao[i], acc[i][j], 0, 0, 0);
+        } else {
+#pragma unroll
+            for (int kk = 0; kk < kGfBK; kk += 4) {
+                float bo[2], ao[2];
+#pragma unroll
+                for (int j = 0; j < 2; j++) bo[j] = sb[wc + 16 * j + r16][kk + kg];
+#pragma unroll
+                for (int i = 0; i < 2; i++) ao[i] = sa[wr + 16 * i + r16][kk + kg];
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < 2; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bo[j], ao[i], acc[i][j], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+    }
+
+    // lane: row wr + 16 i + (lane % 16), columns wc + 16 j + 4 (lane / 16) + v
+    const int r16 = lane & 15, cg = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int64_t m = m0 + wr + 16 * i + r16;
+        if (m >= g.M) continue;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int64_t n = n0 + wc + 16 * j + 4 * cg + v;
+                if (n < g.N) ((float *) (dbase + n * g.d_nb1))[m] = acc[i][j][v];
+            }
+        }
+    }
+}
+
+bool gemm_float_supported(const tview & d, const tview & a, int atype, const tview & b, int btype) {
+    const int ea = atype == GGML_TYPE_F16 ? 2 : 4, eb = btype == GGML_TYPE_F16 ? 2 : 4;
+    if (atype != GGML_TYPE_F16 && atype != GGML_TYPE_F32) return false;
+    if (btype != GGML_TYPE_F16 && btype != GGML_TYPE_F32) return false;
+    if (a.nb[0] != ea || b.nb[0] != eb || d.nb[0] != 4) return false;
+    if (a.ne[0] != b.ne[0] || d.ne[0] != a.ne[1] || d.ne[1] != b.ne[1]) return false;
+    if (d.ne[2] != b.ne[2] || d.ne[3] != b.ne[3] || d.ne[2] % a.ne[2] != 0 || d.ne[3] % a.ne[3] != 0) return false;
+    // the matrix cores pay off once a 64 x 64 tile is mostly live
+    return d.ne[0] >= 16 && d.ne[1] >= 16 && d.ne[2] * d.ne[3] <= 65535 &&
+           (d.ne[0] + kGfBM - 1) / kGfBM <= 0x7fffffff && (d.ne[1] + kGfBN - 1) / kGfBN <= 65535;
+}
+
+void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s) {
+    gemm_float_args g{};
+    g.a = a.data;
+    g.a_nb1 = a.nb[1];
+    g.a_nb2 = a.nb[2];
+    g.a_nb3 = a.nb[3];
+    g.a_f16 = atype == GGML_TYPE_F16;
+    g.b = b.data;
+    g.b_nb1 = b.nb[1];
+    g.b_nb2 = b.nb[2];
+    g.b_nb3 = b.nb[3];
+    g.b_f16 = btype == GGML_TYPE_F16;
+    g.d = d.data;
+    g.d_nb1 = d.nb[1];
+    g.d_nb2 = d.nb[2];
+    g.d_nb3 = d.nb[3];
+    g.M = d.ne[0];
+    g.N = d.ne[1];
+    g.K = a.ne[0];
+    g.ne2 = (int) d.ne[2];
+    g.ne3 = (int) d.ne[3];
+    g.r2 = (int) (d.ne[2] / a.ne[2]);
+    g.r3 = (int) (d.ne[3] / a.ne[3]);
+    // 16-byte vector loads where every row start is 16-byte aligned
+    g.a_vec = ((uintptr_t) a.data | (uintptr_t) a.nb[1] | (uintptr_t) a.nb[2] | (uintptr_t) a.nb[3]) % 16 == 0;
+    g.b_vec = ((uintptr_t) b.data | (uintptr_t) b.nb[1] | (uintptr_t) b.nb[2] | (uintptr_t) b.nb[3]) % 16 == 0;
+    const dim3 grid((unsigned) ((g.M + kGfBM - 1) / kGfBM), (unsigned) ((g.N + kGfBN - 1) / kGfBN),
+                    (unsigned) (g.ne2 * g.ne3));
+    if (g.a_f16) hipLaunchKernelGGL(k_gemm_float<true>, grid, dim3(kGfThreads), 0, s, g);
+    else hipLaunchKernelGGL(k_gemm_float<false>, grid, dim3(kGfThreads), 0, s, g);
+    note_hip_error(hipGetLastError());
+}
+
+}  // namespace mi355x

@@ -684,8 +684,14 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
     }
     const tview dv = make_view(t);
     const tview wv = make_view(w);
-    const int atype = w->type;
+    const int atype = w->type, btype = x->type;
     act_src = nullptr;
+    if (gemm_float_supported(dv, wv, atype, xv, btype)) {
+        add_step([=](hipStream_t s) { launch_gemm_float(dv, wv, atype, xv, btype, s); }, t,
+                 atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32");
+        return true;
+    }
+    if (btype != GGML_TYPE_F32) return fail(t, "f16 columns outside the matrix-core GEMM");
     add_step([=](hipStream_t s) { launch_mul_mat_float(dv, wv, atype, xv, s); }, t, "mul_mat_float");
     return true;
 }
@@ -899,8 +905,10 @@ bool planner::make_fattn(const ggml_tensor * t, fattn_args & a) {
     a.rk3 = (int) (q->ne[3] / k->ne[3]);
     a.scale = op_f32(t, 0);
     a.qtype = -1;
-    // K and V rows are read as 16-byte vectors
-    if (((uintptr_t) a.k | (uintptr_t) a.v) % 16 != 0) return fail(t, "K/V not 16-byte aligned");
+    // f16 K and V rows are read as 16-byte vectors (f32 ones are converted
+    // into aligned scratch by plan_fattn)
+    if ((k->type == GGML_TYPE_F16 && (uintptr_t) a.k % 16 != 0) || (v->type == GGML_TYPE_F16 && (uintptr_t) a.v % 16 != 0))
+        return fail(t, "K/V not 16-byte aligned");
     fattn_plan(a, n_cu);
     if (!fattn_fits(a)) return fail(t, "KV span longer than the kernel's chunk table");
     return true;
@@ -933,15 +941,47 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
     if (!make_fattn(t, a)) return false;
     const ggml_tensor * view = nullptr;
     fattn_quant_out(i, t, a, view);
-    gen_need = std::max(gen_need, fattn_scratch_bytes(a));
+    // f32 K / V: rounded to contiguous f16 copies in scratch after the
+    // partials -- the f16 definition over f16-rounded K / V, the conversion
+    // ggml's GPU backends make as well
+    const ggml_tensor *k = t->src[1], *v = t->src[2];
+    const size_t part = (fattn_scratch_bytes(a) + 255) & ~(size_t) 255;
+    const bool k32 = k->type == GGML_TYPE_F32, v32 = v->type == GGML_TYPE_F32;
+    const size_t kbytes = k32 ? ((size_t) ggml_nelements(k) * 2 + 255) & ~(size_t) 255 : 0;
+    const size_t vbytes = v32 ? ((size_t) ggml_nelements(v) * 2 + 255) & ~(size_t) 255 : 0;
+    gen_need = std::max(gen_need, part + kbytes + vbytes);
+    const tview kv = make_view(k), vv = make_view(v);
     backend_state * b = be;
+    const int ncu = n_cu;
     float * out = (float *) t->data;
     const int64_t qK = (int64_t) a.d * a.hq, qN = (int64_t) a.n_q * a.n_seq;
     add_step(
         [=](hipStream_t s) {
             fattn_args la = a;
             if (la.qtype >= 0) la.act = act_carve(la.qtype, act_base(b), qK, qN);
-            launch_fattn(la, gen_base(b), out, s);
+            // contiguous f16 [ne0, ne1, ne2, ne3] copy of an f32 operand
+            auto to_f16 = [&](const tview & src, char * dst, int64_t & nb1, int64_t & nb2, int64_t & nb3) {
+                tview d = src;
+                d.data = dst;
+                d.nb[0] = 2;
+                d.nb[1] = 2 * d.ne[0];
+                d.nb[2] = d.nb[1] * d.ne[1];
+                d.nb[3] = d.nb[2] * d.ne[2];
+                launch_copy(d, GGML_TYPE_F16, src, GGML_TYPE_F32, s, ncu);
+                nb1 = d.nb[1];
+                nb2 = d.nb[2];
+                nb3 = d.nb[3];
+            };
+            char * g = gen_base(b);
+            if (k32) {
+                to_f16(kv, g + part, la.k_nb1, la.k_nb2, la.k_nb3);
+                la.k = g + part;
+            }
+            if (v32) {
+                to_f16(vv, g + part + kbytes, la.v_nb1, la.v_nb2, la.v_nb3);
+                la.v = g + part + kbytes;
+            }
+            launch_fattn(la, g, out, s);
         },
         t, "flash_attn_ext");
     if (a.qtype >= 0) {
@@ -1703,7 +1743,12 @@ bool supports_op(const device_state * dev, const ggml_tensor * t) {
                    norm_supported(t->ne[0]);
         case GGML_OP_MUL_MAT: {
             const ggml_tensor *w = t->src[0], *x = t->src[1];
-            if (!f32(t) || !f32(x) || !is_contiguous(t)) return false;
+            if (!f32(t) || !is_contiguous(t)) return false;
+            // f16 columns (an f16 convolution's IM2COL) only on the matrix-core GEMM
+            if (x->type == GGML_TYPE_F16)
+                return (w->type == GGML_TYPE_F16 || w->type == GGML_TYPE_F32) &&
+                       gemm_float_supported(make_view(t), make_view(w), w->type, make_view(x), x->type);
+            if (!f32(x)) return false;
             if (w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K) {
                 return w->ne[2] == 1 && w->ne[3] == 1 && is_contiguous(w) && columns_foldable(x) &&
                        (w->type != GGML_TYPE_Q4_K || w->ne[0] % 256 == 0) && w->ne[0] % 32 == 0;
@@ -1731,8 +1776,12 @@ bool supports_op(const device_state * dev, const ggml_tensor * t) {
         }
         case GGML_OP_FLASH_ATTN_EXT: {
             const ggml_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2], *m = t->src[3];
-            if (!f32(q) || k->type != GGML_TYPE_F16 || v->type != GGML_TYPE_F16) return false;
-            if (q->nb[0] != 4 || k->nb[0] != 2 || v->nb[0] != 2) return false;
+            // f32 K / V (strided views straight from the projections, as the
+            // encoders pass them) are rounded to contiguous f16 first
+            auto kv_ok = [](const ggml_tensor * x) {
+                return (x->type == GGML_TYPE_F16 && x->nb[0] == 2) || (x->type == GGML_TYPE_F32 && x->nb[0] == 4);
+            };
+            if (!f32(q) || q->nb[0] != 4 || !kv_ok(k) || !kv_ok(v)) return false;
             if (v->ne[0] != k->ne[0] || k->ne[2] != v->ne[2]) return false;
             if (op_f32(t, 1) != 0.0f || op_f32(t, 2) != 0.0f) return false;  // max_bias, softcap
             if (m && (m->type != GGML_TYPE_F16 || m->ne[2] != 1 || m->nb[0] != 2)) return false;

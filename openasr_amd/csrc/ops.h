@@ -82,6 +82,23 @@ void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t
 // float GEMM fallback (f16 / f32 src0)
 void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tview & b, hipStream_t s);
 
+// float-weight MUL_MAT on the matrix cores (k_gemm_float.hip): src0 a (F16 /
+// F32, rows contiguous) x src1 b (F32 / F16, rows contiguous) -> d (f32),
+// batch dims broadcast from a as ggml does (r2 = d.ne2 / a.ne2, r3)
+struct gemm_float_args {
+    const char * a;
+    int64_t a_nb1, a_nb2, a_nb3;
+    const char * b;
+    int64_t b_nb1, b_nb2, b_nb3;
+    char * d;
+    int64_t d_nb1, d_nb2, d_nb3;
+    int64_t M, N, K;
+    int ne2, ne3, r2, r3;
+    int a_f16, b_f16, a_vec, b_vec;
+};
+bool gemm_float_supported(const tview & d, const tview & a, int atype, const tview & b, int btype);
+void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s);
+
 struct fattn_args {
     const char * q;
     const char * k;

@@ -267,6 +267,48 @@ def test_mul_mat_f16_weights(ggml, gpu, ref):
     G.free()
 
 
+# weight type, column type, M (rows), K, N (columns), weight batch, column batch
+FLOAT_MM_CASES = [
+    ("f16", "f32", 1024, 1280, 375, (1, 1), (1, 1)),    # an encoder projection, f16 weights
+    ("f16", "f32", 1000, 4320, 97, (1, 1), (1, 1)),     # rows off the 64-row tile
+    ("f16", "f16", 480, 9, 1500, (1, 1), (1, 1)),       # first conv of an f16 stem (K = 3 x 3, unaligned rows)
+    ("f16", "f16", 480, 4320, 750, (1, 1), (1, 1)),     # later conv (K = 3 x 3 x 480)
+    ("f32", "f32", 896, 896, 300, (1, 1), (1, 1)),      # f32 encoder weights
+    ("f32", "f32", 1280, 5120, 64, (1, 1), (1, 1)),
+    ("f32", "f16", 64, 100, 33, (1, 1), (1, 1)),
+    ("f16", "f32", 100, 64, 40, (2, 1), (4, 2)),        # weight batch broadcast over column batches
+    ("f32", "f32", 333, 128, 17, (8, 1), (16, 1)),      # score-shaped: kv heads x query heads
+]
+
+
+@pytest.mark.parametrize("wt,xt,m,k,n,wb,xb", FLOAT_MM_CASES)
+def test_mul_mat_float_matrix_cores(ggml, gpu, wt, xt, m, k, n, wb, xb):
+    """float MUL_MAT on the matrix-core GEMM against an f64 product of the
+    same operands, the columns rounded to f16 for f16 weights (ggml-cpu's
+    vec_dot_type rule): f32 sums in the matrix core's order, within 1e-4 of
+    the largest output (the op tolerance is 2e-3)"""
+    print(f"float mul_mat {wt} x {xt} M={m} K={k} N={n} wb={wb} xb={xb}", flush=True)
+    wdt = np.float16 if wt == "f16" else np.float32
+    xdt = np.float16 if xt == "f16" else np.float32
+    w = RNG.standard_normal((wb[1], wb[0], m, k)).astype(wdt)
+    x = RNG.standard_normal((xb[1], xb[0], n, k)).astype(xdt)
+    G = ggml.Graph()
+    W = G.new(ggml.F16 if wt == "f16" else ggml.F32, k, m, wb[0], wb[1], weight=True)
+    X = G.new(ggml.F16 if xt == "f16" else ggml.F32, k, n, xb[0], xb[1])
+    Y = G.lib.ggml_mul_mat(G.ctx, W, X)
+    run(ggml, gpu, G, Y)
+    G.set(W, w.view(np.uint16) if wt == "f16" else w)
+    G.set(X, x.view(np.uint16) if xt == "f16" else x)
+    assert G.compute(gpu.backend) == 0
+    xr = x.astype(np.float16) if wt == "f16" else x
+    r2, r3 = xb[0] // wb[0], xb[1] // wb[1]
+    wf = np.repeat(np.repeat(w.astype(np.float64), r2, axis=1), r3, axis=0)
+    want = np.matmul(xr.astype(np.float64), wf.transpose(0, 1, 3, 2))  # [b3, b2, n, m]
+    got = G.get(Y).reshape(xb[1], xb[0], n, m)
+    assert rel_err(got, want) < 1e-4
+    G.free()
+
+
 # ----------------------------------------------------- flash attention --
 
 FA_CASES = [
@@ -275,6 +317,41 @@ FA_CASES = [
     (128, 16, 8, 512, 64, 1), (128, 16, 8, 2048, 64, 2), (64, 6, 6, 448, 1, 1), (64, 6, 6, 1500, 1, 1),
     (64, 6, 6, 1500, 1, 3), (128, 16, 8, 8192, 64, 1),
 ]
+
+
+@pytest.mark.parametrize("d,heads,t", [(64, 20, 750), (128, 8, 300), (64, 6, 100)])
+def test_flash_attn_ext_f32_kv_head_views(ggml, gpu, ref, d, heads, t):
+    """the encoders' self-attention (nn/encoder.rs:735-800): Q, K and V are
+    f32 projections [d * heads, t] viewed as heads (reshape [d, heads, t],
+    permute to [d, t, heads]) without a CONT, under an f16 block mask. The
+    f32 K / V are rounded to f16 (the conversion ggml's GPU backends make):
+    bit for bit the oracle's chunked attention over the f16-rounded K / V"""
+    print(f"flash_attn f32 K/V views D={d} heads={heads} t={t}", flush=True)
+    G = ggml.Graph()
+    L = G.lib
+    P = [G.new(ggml.F32, d * heads, t) for _ in range(3)]
+    M = G.new(ggml.F16, t, t)
+
+    def heads_view(x):
+        return L.ggml_permute(G.ctx, L.ggml_reshape_3d(G.ctx, x, d, heads, t), 0, 2, 1, 3)
+
+    scale = 1.0 / math.sqrt(d)
+    O = L.ggml_flash_attn_ext(G.ctx, heads_view(P[0]), heads_view(P[1]), heads_view(P[2]), M, scale, 0.0, 0.0)
+    run(ggml, gpu, G, O)
+    x = [RNG.standard_normal((t, heads, d)).astype(np.float32) for _ in range(3)]
+    for Pi, xi in zip(P, x):
+        G.set(Pi, xi)
+    # block-diagonal mask of 40-row windows, the chunked encoders' padding shape
+    blk = np.arange(t) // 40
+    mask = np.where(blk[:, None] == blk[None, :], 0.0, -np.inf).astype(np.float16)
+    G.set(M, mask.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    out = G.get(O).reshape(t, heads, d)  # ggml result [d, heads, t]
+    k16 = np.ascontiguousarray(x[1].transpose(1, 0, 2)).astype(np.float16)  # [heads, t, d]
+    v16 = np.ascontiguousarray(x[2].transpose(1, 0, 2)).astype(np.float16)
+    same = ref.flash_attn(x[0], k16.view(np.uint16), v16.view(np.uint16), mask.view(np.uint16), scale, fidelity=5)
+    assert_same_bits(out, same)
+    G.free()
 
 
 def attention_f64(q, k, v, mask, scale):
