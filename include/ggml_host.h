@@ -101,6 +101,18 @@ struct ggml_tensor * ggml_argmax_first(struct ggml_context * ctx, struct ggml_te
 /* ffi.rs:915-925 (ggml_conv_2d = im2col + mul_mat), cpu_graph.rs:5191-5246 */
 struct ggml_tensor * ggml_im2col(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int s0,
                                  int s1, int p0, int p1, int d0, int d1, bool is_2D, enum ggml_type dst_type);
+/* ffi.rs:915-925: kernel a [KW, KH, IC, OC] over input b [W, H, IC, N] ->
+ * [OW, OH, OC, N]; IM2COL in a's type, MUL_MAT of the columns by the kernel
+ * rows, then the channel-major permute and CONT */
+struct ggml_tensor * ggml_conv_2d(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int s0,
+                                  int s1, int p0, int p1, int d0, int d1);
+/* ffi.rs:686-687 (the sinusoidal position tables, nn/encoder.rs:580-590) */
+struct ggml_tensor * ggml_sin(struct ggml_context * ctx, struct ggml_tensor * a);
+struct ggml_tensor * ggml_cos(struct ggml_context * ctx, struct ggml_tensor * a);
+/* ffi.rs:724-729: a and b joined along dim */
+struct ggml_tensor * ggml_concat(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int dim);
+/* ffi.rs:812: a copy of a in another type (a CPY into a new tensor) */
+struct ggml_tensor * ggml_cast(struct ggml_context * ctx, struct ggml_tensor * a, enum ggml_type type);
 struct ggml_tensor * ggml_soft_max(struct ggml_context * ctx, struct ggml_tensor * a);
 struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * mask,
                                        float scale, float max_bias);

@@ -101,6 +101,12 @@ __device__ __forceinline__ float unary_apply(int op, float x, const uint16_t * g
         case GGML_UNARY_OP_EXP: return expf_det(x);
         case GGML_UNARY_OP_NEG: return -x;
         case GGML_UNARY_OP_ABS: return fabsf(x);
+        case kUnarySin:
+        case kUnaryCos: {
+            float sn, c;
+            sincosf_det(x, sn, c);
+            return op == kUnarySin ? sn : c;
+        }
         default: return x;
     }
 }
@@ -117,6 +123,30 @@ __global__ void k_unary(tview d, tview a, int op, const uint16_t * gelu_table, i
 void launch_unary(const tview & d, const tview & a, int op, const uint16_t * gelu_table, hipStream_t s, int n_cu) {
     const int64_t n = d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3];
     hipLaunchKernelGGL(k_unary, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, a, op, gelu_table, n);
+}
+
+// GGML_OP_CONCAT: d = a joined with b along dim (elements of esize bytes)
+__global__ void k_concat(tview d, tview a, tview b, int dim, int esize, int64_t n) {
+    for (int64_t idx = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; idx < n; idx += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i[4];
+        unravel(idx, d.ne, i[0], i[1], i[2], i[3]);
+        const char * src;
+        if (i[dim] < a.ne[dim]) {
+            src = a.data + offs4(a, i[0], i[1], i[2], i[3]);
+        } else {
+            i[dim] -= a.ne[dim];
+            src = b.data + offs4(b, i[0], i[1], i[2], i[3]);
+            i[dim] += a.ne[dim];
+        }
+        char * dst = d.data + offs4(d, i[0], i[1], i[2], i[3]);
+        if (esize == 4) *(uint32_t *) dst = *(const uint32_t *) src;
+        else *(uint16_t *) dst = *(const uint16_t *) src;
+    }
+}
+
+void launch_concat(const tview & d, const tview & a, const tview & b, int dim, int esize, hipStream_t s, int n_cu) {
+    const int64_t n = d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3];
+    hipLaunchKernelGGL(k_concat, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, a, b, dim, esize, n);
 }
 
 // SwiGLU tail fused: d = silu(g) * u (the gate activation and gate multiply

@@ -1233,6 +1233,20 @@ bool planner::plan() {
             case GGML_OP_UNARY:
                 plan_unary(i, t);
                 break;
+            case GGML_OP_SIN:
+            case GGML_OP_COS: {
+                const tview dv = make_view(t), av = make_view(t->src[0]);
+                const int code = t->op == GGML_OP_SIN ? kUnarySin : kUnaryCos;
+                add_step([=](hipStream_t s) { launch_unary(dv, av, code, nullptr, s, ncu); }, t,
+                         t->op == GGML_OP_SIN ? "sin" : "cos");
+                break;
+            }
+            case GGML_OP_CONCAT: {
+                const tview dv = make_view(t), av = view_of(t->src[0]), bv = view_of(t->src[1]);
+                const int dim = t->op_params[0], es = t->type == GGML_TYPE_F16 ? 2 : 4;
+                add_step([=](hipStream_t s) { launch_concat(dv, av, bv, dim, es, s, ncu); }, t, "concat");
+                break;
+            }
             case GGML_OP_ADD:
             case GGML_OP_SUB:
             case GGML_OP_MUL:
@@ -1736,6 +1750,14 @@ bool supports_op(const device_state * dev, const ggml_tensor * t) {
                                u == GGML_UNARY_OP_RELU || u == GGML_UNARY_OP_TANH || u == GGML_UNARY_OP_SIGMOID ||
                                u == GGML_UNARY_OP_EXP || u == GGML_UNARY_OP_NEG || u == GGML_UNARY_OP_ABS;
             return op_ok && f32(t) && f32(t->src[0]);
+        }
+        case GGML_OP_SIN:
+        case GGML_OP_COS:
+            return f32(t) && f32(t->src[0]);
+        case GGML_OP_CONCAT: {
+            const int ty = t->type, dim = t->op_params[0];
+            return (ty == GGML_TYPE_F32 || ty == GGML_TYPE_F16) && t->src[0]->type == ty && t->src[1]->type == ty &&
+                   dim >= 0 && dim < 4;
         }
         case GGML_OP_RMS_NORM:
         case GGML_OP_NORM:

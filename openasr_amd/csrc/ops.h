@@ -171,6 +171,10 @@ void launch_fattn(const fattn_args & a, void * scratch, float * out, hipStream_t
 
 void launch_binary(int op, const tview & d, const tview & a, const tview & b, hipStream_t s, int n_cu);
 void launch_scale(const tview & d, const tview & a, float sc, float bias, hipStream_t s, int n_cu);
+// launch_unary codes past ggml's unary ops: GGML_OP_SIN / GGML_OP_COS
+// (sincosf_det, the deterministic sine and cosine the CPU reference runs)
+constexpr int kUnarySin = 1001, kUnaryCos = 1002;
+void launch_concat(const tview & d, const tview & a, const tview & b, int dim, int esize, hipStream_t s, int n_cu);
 void launch_unary(const tview & d, const tview & a, int op, const uint16_t * gelu_table, hipStream_t s, int n_cu);
 void launch_silu_mul(const tview & d, const tview & g, const tview & u, hipStream_t s, int n_cu);
 // qtype/act: optionally also write the normalised rows as quantized

@@ -126,6 +126,11 @@ def base() -> C.CDLL:
     _sig(lib, "ggml_view_4d", T, CTX, T, i64, i64, i64, i64, sz, sz, sz, sz)
     _sig(lib, "ggml_permute", T, CTX, T, i, i, i, i)
     _sig(lib, "ggml_im2col", T, CTX, T, T, i, i, i, i, i, i, C.c_bool, i)
+    _sig(lib, "ggml_conv_2d", T, CTX, T, T, i, i, i, i, i, i)
+    for name in ("ggml_sin", "ggml_cos"):
+        _sig(lib, name, T, CTX, T)
+    _sig(lib, "ggml_concat", T, CTX, T, T, i)
+    _sig(lib, "ggml_cast", T, CTX, T, i)
     _sig(lib, "ggml_new_graph_custom", C.c_void_p, CTX, sz, C.c_bool)
     _sig(lib, "ggml_build_forward_expand", None, C.c_void_p, T)
     _sig(lib, "ggml_graph_n_nodes", i, C.c_void_p)

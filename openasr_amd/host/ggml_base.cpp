@@ -519,6 +519,20 @@ struct ggml_tensor * ggml_im2col(struct ggml_context * ctx, struct ggml_tensor *
     return r;
 }
 
+struct ggml_tensor * ggml_conv_2d(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int s0,
+                                  int s1, int p0, int p1, int d0, int d1) {
+    // columns [IC KH KW, OW, OH, N] in the kernel's type; the columns are the
+    // MUL_MAT's first operand and the kernel rows its second, so the product
+    // is [OW OH N, OC]
+    ggml_tensor * im = ggml_im2col(ctx, a, b, s0, s1, p0, p1, d0, d1, true, a->type);
+    if (!im) return nullptr;
+    ggml_tensor * r = ggml_mul_mat(ctx, ggml_reshape_2d(ctx, im, im->ne[0], im->ne[3] * im->ne[2] * im->ne[1]),
+                                   ggml_reshape_2d(ctx, a, a->ne[0] * a->ne[1] * a->ne[2], a->ne[3]));
+    if (!r) return nullptr;
+    r = ggml_reshape_4d(ctx, r, im->ne[1], im->ne[2], im->ne[3], a->ne[3]);  // [OW, OH, N, OC]
+    return ggml_cont(ctx, ggml_permute(ctx, r, 0, 1, 3, 2));                  // [OW, OH, OC, N]
+}
+
 struct ggml_tensor * ggml_soft_max_ext(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * mask,
                                        float scale, float max_bias) {
     GB_REQUIRE(ggml_is_contiguous(a), "soft_max: input must be contiguous");
@@ -598,6 +612,46 @@ struct ggml_tensor * ggml_cpy(struct ggml_context * ctx, struct ggml_tensor * a,
     ggml_tensor * r = view_tensor(ctx, b);
     if (!r) return nullptr;
     r->op = GGML_OP_CPY;
+    r->src[0] = a;
+    r->src[1] = b;
+    return r;
+}
+
+struct ggml_tensor * ggml_cast(struct ggml_context * ctx, struct ggml_tensor * a, enum ggml_type type) {
+    ggml_tensor * r = ggml_new_tensor(ctx, type, GGML_MAX_DIMS, a->ne);
+    if (!r) return nullptr;
+    r->op = GGML_OP_CPY;
+    r->src[0] = a;
+    r->src[1] = r;
+    return r;
+}
+
+static ggml_tensor * elementwise_op(ggml_context * ctx, ggml_tensor * a, enum ggml_op op) {
+    ggml_tensor * r = dup_tensor(ctx, a);
+    if (!r) return nullptr;
+    r->op = op;
+    r->src[0] = a;
+    return r;
+}
+
+struct ggml_tensor * ggml_sin(struct ggml_context * ctx, struct ggml_tensor * a) {
+    return elementwise_op(ctx, a, GGML_OP_SIN);
+}
+struct ggml_tensor * ggml_cos(struct ggml_context * ctx, struct ggml_tensor * a) {
+    return elementwise_op(ctx, a, GGML_OP_COS);
+}
+
+struct ggml_tensor * ggml_concat(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b, int dim) {
+    GB_REQUIRE(dim >= 0 && dim < GGML_MAX_DIMS && a->type == b->type, "concat: dim out of range or types differ");
+    int64_t ne[GGML_MAX_DIMS];
+    for (int d = 0; d < GGML_MAX_DIMS; d++) {
+        GB_REQUIRE(d == dim || a->ne[d] == b->ne[d], "concat: shapes differ off the joined dim");
+        ne[d] = d == dim ? a->ne[d] + b->ne[d] : a->ne[d];
+    }
+    ggml_tensor * r = ggml_new_tensor(ctx, a->type, GGML_MAX_DIMS, ne);
+    if (!r) return nullptr;
+    r->op_params[0] = dim;
+    r->op = GGML_OP_CONCAT;
     r->src[0] = a;
     r->src[1] = b;
     return r;

@@ -12,6 +12,7 @@ result and must be at least as accurate as ggml-cpu's numerics (whose V
 accumulator is f16).
 """
 
+import ctypes
 import math
 
 import numpy as np
@@ -808,6 +809,87 @@ def test_conv_2d_f32_kernel_chain(ggml, gpu, ref):
     want = (cols_ref @ w.reshape(oc, -1).T.astype(np.float64)).transpose(0, 3, 1, 2)  # [N, OC, OH, OW]
     got = G.get(y).reshape(n, oc, oh, ow)
     assert rel_err(got, want) <= 2e-3
+    G.free()
+
+
+def test_conv_2d_f16_kernel(ggml, gpu, ref):
+    """ggml_conv_2d with an f16 kernel (the Qwen audio encoder's conv stem,
+    models/qwen/audio_encoder.rs:520-550): f16 columns x f16 kernel rows on
+    the matrix-core GEMM, against an f64 convolution of the f16-rounded input
+    (f32 sums: within 1e-4 of the largest output)"""
+    n, ic, ih, iw, oc = 2, 8, 40, 24, 32
+    x = RNG.standard_normal((n, ic, ih, iw)).astype(np.float32)
+    w = (RNG.standard_normal((oc, ic, 3, 3)) * 0.2).astype(np.float16)
+    G = ggml.Graph()
+    Kt = G.new(ggml.F16, 3, 3, ic, oc, weight=True)
+    X = G.new(ggml.F32, iw, ih, ic, n)
+    y = G.lib.ggml_conv_2d(G.ctx, Kt, X, 2, 2, 1, 1, 1, 1)
+    yt = ggml.tensor(y)
+    ow, oh = yt.ne[0], yt.ne[1]
+    assert (yt.ne[2], yt.ne[3]) == (oc, n)
+    run(ggml, gpu, G, y)
+    G.set(X, x)
+    G.set(Kt, w.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    cols_ref = ref.im2col(x.astype(np.float16).astype(np.float32), 3, 3, 2, 2, 1, 1, 1, 1).astype(np.float64)
+    want = (cols_ref @ w.reshape(oc, -1).T.astype(np.float64)).transpose(0, 3, 1, 2)  # [N, OC, OH, OW]
+    got = G.get(y).reshape(n, oc, oh, ow)
+    assert rel_err(got, want) < 1e-4
+    G.free()
+
+
+def test_sinusoidal_position_table(ggml, gpu, ref):
+    """the encoders' sinusoidal positions (nn/encoder.rs:575-590): angles =
+    MUL_MAT(inverse timescales [1, half], positions [1, T]), SIN and COS of
+    them, CONCAT along dim 0 (half-split layout); SIN / COS are the
+    deterministic sincos both sides run (bit for bit), the angles an exact
+    f32 product (K = 1), CONCAT a copy; and a CAST of the table to f16"""
+    half, t = 64, 300
+    inv = np.exp(-np.log(10000.0) * np.arange(half) / (half - 1)).astype(np.float32)
+    pos = np.arange(t, dtype=np.float32)
+    G = ggml.Graph()
+    L = G.lib
+    Inv = G.new(ggml.F32, 1, half, weight=True)
+    Pos = G.new(ggml.F32, 1, t)
+    ang = L.ggml_mul_mat(G.ctx, Inv, Pos)  # [half, t]
+    table = L.ggml_concat(G.ctx, L.ggml_sin(G.ctx, ang), L.ggml_cos(G.ctx, ang), 0)  # [2 half, t]
+    t16 = L.ggml_cast(G.ctx, table, ggml.F16)
+    run(ggml, gpu, G, t16)
+    G.set(Inv, inv)
+    G.set(Pos, pos)
+    assert G.compute(gpu.backend) == 0
+    a = (pos[:, None] * inv[None, :]).astype(np.float32)  # [t, half], one exact-rounded product each
+    s = np.zeros_like(a)
+    c = np.zeros_like(a)
+    fs, fc = ctypes.c_float(), ctypes.c_float()
+    for idx, v in np.ndenumerate(a):
+        ref.lib().ref_sincosf_det(float(v), ctypes.byref(fs), ctypes.byref(fc))
+        s[idx], c[idx] = fs.value, fc.value
+    want = np.concatenate([s, c], axis=1)  # [t, 2 half]
+    got = G.get(table).reshape(t, 2 * half)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    assert np.array_equal(G.get(t16).reshape(t, 2 * half).view(np.uint16), want.astype(np.float16).view(np.uint16))
+    G.free()
+
+
+@pytest.mark.parametrize("dim", [0, 1, 2, 3])
+def test_concat_every_dim(ggml, gpu, dim):
+    """CONCAT along each dim, f32 and of a permuted (strided) second operand"""
+    shape_a = [6, 5, 4, 3]
+    shape_b = list(shape_a)
+    shape_b[dim] = 2
+    a = RNG.standard_normal(shape_a[::-1]).astype(np.float32)
+    b = RNG.standard_normal(shape_b[::-1]).astype(np.float32)
+    G = ggml.Graph()
+    A = G.new(ggml.F32, *shape_a)
+    B = G.new(ggml.F32, *shape_b)
+    C = G.lib.ggml_concat(G.ctx, A, B, dim)
+    run(ggml, gpu, G, C)
+    G.set(A, a)
+    G.set(B, b)
+    assert G.compute(gpu.backend) == 0
+    want = np.concatenate([a, b], axis=3 - dim)
+    assert np.array_equal(G.get(C).reshape(want.shape), want)
     G.free()
 
 
