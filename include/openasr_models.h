@@ -231,6 +231,57 @@ int oa_whisper_generate(oa_whisper_session * s, int32_t first_token, int n_steps
 int oa_whisper_read_cross(const oa_whisper_session * s, int layer, uint16_t * k_out, uint16_t * v_out);
 struct ggml_cgraph * oa_whisper_decode_graph(oa_whisper_session * s);
 
+/* ---- Qwen3-ASR audio encoder (crates/openasr-core/src/models/qwen/audio_encoder.rs) ----
+ * The prefix producer of the Qwen decoder, as the host builds its graph for a
+ * GPU backend (flash attention over strided head views): mel [n_mels][n_frames]
+ * packed into 100-frame chunks (:798-845), three 3x3 stride-2 GELU_ERF
+ * convolutions with f32 kernels (:510-552, nn/conv.rs:82-111), the channel
+ * permute and conv_out projection (:553-592), the sinusoidal position table
+ * added per chunk (:455-465, nn/encoder.rs:575-590), n_layers pre-norm
+ * encoder blocks over all chunks' rows with a zero f32 mask cast to f16
+ * (:1078-1110, nn/encoder.rs:678-870), ln_post, proj1 + GELU_ERF, proj2
+ * (:615-672). Output: [rows][out_dim] f32, rows = 13 per chunk
+ * (qwen3_audio_token_count_for_mel_frames, :859-867). */
+typedef struct oa_qwen_audio_config {
+    int n_mels;         /* mel bins (even, >= 8) */
+    int conv_channels;  /* channels of the three convolutions */
+    int d_model, n_heads, n_layers, ffn;
+    int out_dim;        /* the decoder's d_model */
+    int wtype;          /* 2-D projections: GGML_TYPE_F32, GGML_TYPE_F16 or GGML_TYPE_Q8_0 */
+    uint64_t seed;
+} oa_qwen_audio_config;
+
+enum oa_qwen_audio_tensor_kind {
+    /* per layer (layer >= 0); matrices [rows][K] of wtype, vectors f32 */
+    OA_QA_ATTN_NORM_W = 0, OA_QA_ATTN_NORM_B, OA_QA_Q, OA_QA_Q_B, OA_QA_K, OA_QA_K_B, OA_QA_V, OA_QA_V_B,
+    OA_QA_O, OA_QA_O_B, OA_QA_FFN_NORM_W, OA_QA_FFN_NORM_B, OA_QA_UP, OA_QA_UP_B, OA_QA_DOWN, OA_QA_DOWN_B,
+    OA_QA_LAYER_KINDS,
+    /* global (layer = -1): f32 conv kernels [OC][IC][3][3] (ggml [3, 3, IC, OC]) and biases */
+    OA_QA_CONV1_W = 100, OA_QA_CONV1_B, OA_QA_CONV2_W, OA_QA_CONV2_B, OA_QA_CONV3_W, OA_QA_CONV3_B,
+    OA_QA_CONV_OUT, OA_QA_CONV_OUT_B, /* matrix [d_model][conv_channels * freq bins] of wtype */
+    OA_QA_LN_POST_W, OA_QA_LN_POST_B,
+    OA_QA_PROJ1, OA_QA_PROJ1_B, /* [d_model][d_model] */
+    OA_QA_PROJ2, OA_QA_PROJ2_B, /* [out_dim][d_model] */
+    OA_QA_INV_TIMESCALES        /* f32 [d_model / 2]: exp(-ln(10000) i / (d_model / 2 - 1)) */
+};
+
+typedef struct oa_qwen_audio_weights oa_qwen_audio_weights;
+typedef struct oa_qwen_audio_encoder oa_qwen_audio_encoder;
+
+/* seeded N(0, 0.02) matrices quantized / rounded to wtype; NULL on a shape the
+ * type cannot hold (Q8_0 needs every K % 32 == 0) */
+oa_qwen_audio_weights * oa_qwen_audio_weights_synthesize(const oa_qwen_audio_config * cfg);
+void oa_qwen_audio_weights_free(oa_qwen_audio_weights * w);
+const void * oa_qwen_audio_weights_tensor(const oa_qwen_audio_weights * w, int layer, int kind, size_t * nbytes);
+/* rows the encoder emits for n_frames mel frames: 13 per started 100-frame chunk */
+int oa_qwen_audio_token_count(int n_frames);
+oa_qwen_audio_encoder * oa_qwen_audio_encoder_create(ggml_backend_t backend, const oa_qwen_audio_weights * w);
+void oa_qwen_audio_encoder_free(oa_qwen_audio_encoder * e);
+/* one encode: mel [n_mels][n_frames] f32 -> out [rows][out_dim] f32; ms (may be
+ * NULL) receives the compute's wall time. The graph is built on the first call
+ * for a chunk count and replayed after. Returns a ggml_status. */
+int oa_qwen_audio_encode(oa_qwen_audio_encoder * e, const float * mel, int n_frames, float * out, double * ms);
+
 /* ---- pack storage policy (crates/openasr-core/src/models/pack_quant.rs) ---- */
 
 /* requested pack rung, enum PackQuant (pack_quant.rs:25-32) */

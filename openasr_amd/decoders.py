@@ -27,6 +27,23 @@ class WhisperConfig(C.Structure):
                 ("seed", C.c_uint64), ("ffn_act", C.c_int)]
 
 
+class QwenAudioConfig(C.Structure):
+    _fields_ = [("n_mels", C.c_int), ("conv_channels", C.c_int), ("d_model", C.c_int), ("n_heads", C.c_int),
+                ("n_layers", C.c_int), ("ffn", C.c_int), ("out_dim", C.c_int), ("wtype", C.c_int),
+                ("seed", C.c_uint64)]
+
+
+# Qwen3-ASR audio encoder tensor kinds (enum oa_qwen_audio_tensor_kind)
+(QA_ATTN_NORM_W, QA_ATTN_NORM_B, QA_Q, QA_Q_B, QA_K, QA_K_B, QA_V, QA_V_B, QA_O, QA_O_B, QA_FFN_NORM_W,
+ QA_FFN_NORM_B, QA_UP, QA_UP_B, QA_DOWN, QA_DOWN_B) = range(16)
+QA_LAYER_KINDS = 16
+(QA_CONV1_W, QA_CONV1_B, QA_CONV2_W, QA_CONV2_B, QA_CONV3_W, QA_CONV3_B, QA_CONV_OUT, QA_CONV_OUT_B,
+ QA_LN_POST_W, QA_LN_POST_B, QA_PROJ1, QA_PROJ1_B, QA_PROJ2, QA_PROJ2_B, QA_INV_TIMESCALES) = range(100, 115)
+# an audio encoder of Qwen3-ASR-0.6B's shape: 128 mel bins, 480 conv channels,
+# 18 layers of d_model 896 (14 heads, FFN 3584), into a 1024-wide decoder
+QWEN3_06B_AUDIO = dict(n_mels=128, conv_channels=480, d_model=896, n_heads=14, n_layers=18, ffn=3584, out_dim=1024)
+
+
 # FFN activations of the shared seq2seq block (oa_whisper_config.ffn_act)
 FFN_GELU, FFN_RELU, FFN_GELU_ERF, FFN_SILU = 0, 1, 2, 3
 
@@ -114,6 +131,13 @@ def lib() -> C.CDLL:
     s("oa_qwen_generate", i, vp, vp, i, vp, vp)
     s("oa_qwen_read_kv", i, vp, i, i, vp, vp)
     s("oa_detect_degenerate_ngram", i, vp, i, i, vp, vp, vp)
+    s("oa_qwen_audio_weights_synthesize", vp, vp)
+    s("oa_qwen_audio_weights_free", None, vp)
+    s("oa_qwen_audio_weights_tensor", vp, vp, i, i, C.POINTER(C.c_size_t))
+    s("oa_qwen_audio_token_count", i, i)
+    s("oa_qwen_audio_encoder_create", vp, vp, vp)
+    s("oa_qwen_audio_encoder_free", None, vp)
+    s("oa_qwen_audio_encode", i, vp, vp, i, vp, C.POINTER(C.c_double))
     s("oa_classify_quant_tensor_role", i, vp, i, i, i, i)
     s("oa_quant_target_write_type", i, vp, i, i, i, i)
     s("oa_qwen_decode_graph", vp, vp)
@@ -410,6 +434,60 @@ def detect_degenerate_ngram(tokens, max_ngram: int = 8, bound=None):
     keep = lib().oa_detect_degenerate_ngram(t.ctypes.data if t.size else None, len(t), max_ngram,
                                             table.ctypes.data if table is not None else None, C.byref(n), C.byref(r))
     return None if keep < 0 else (keep, n.value, r.value)
+
+
+class QwenAudioWeights:
+    """Host bytes of a Qwen3-ASR-shaped audio encoder, synthesised (seeded
+    N(0, 0.02) projections of ggml type wtype, f32 conv kernels and vectors)."""
+
+    def __init__(self, wtype: int = g.F16, seed: int = 4242, **shape):
+        self.cfg = QwenAudioConfig(wtype=wtype, seed=seed, **shape)
+        self.ptr = lib().oa_qwen_audio_weights_synthesize(C.byref(self.cfg))
+        if not self.ptr:
+            raise ValueError(f"audio encoder weights: shape {shape} does not fit type {wtype}")
+
+    def array(self, layer: int, kind: int) -> np.ndarray:
+        """a copy of one tensor's bytes (uint8); layer -1 for the global tensors"""
+        n = C.c_size_t(0)
+        p = lib().oa_qwen_audio_weights_tensor(self.ptr, layer, kind, C.byref(n))
+        if not p:
+            return None
+        return np.ctypeslib.as_array((C.c_uint8 * n.value).from_address(p)).copy()
+
+    def free(self):
+        if self.ptr:
+            lib().oa_qwen_audio_weights_free(self.ptr)
+            self.ptr = None
+
+
+def qwen_audio_token_count(n_frames: int) -> int:
+    return int(lib().oa_qwen_audio_token_count(n_frames))
+
+
+class QwenAudioEncoder:
+    """The audio encoder graph on a backend (oa_qwen_audio_encoder_create)."""
+
+    def __init__(self, weights: QwenAudioWeights, backend):
+        self.cfg = weights.cfg
+        self.ptr = lib().oa_qwen_audio_encoder_create(backend, weights.ptr)
+        if not self.ptr:
+            raise RuntimeError("audio encoder: weight upload failed")
+
+    def encode(self, mel: np.ndarray):
+        """mel [n_mels, n_frames] -> (embeddings [rows, out_dim], compute ms)"""
+        mel = np.ascontiguousarray(mel, dtype=np.float32)
+        n_frames = mel.shape[1]
+        out = np.zeros((qwen_audio_token_count(n_frames), self.cfg.out_dim), np.float32)
+        ms = C.c_double(0.0)
+        st = lib().oa_qwen_audio_encode(self.ptr, mel.ctypes.data, n_frames, out.ctypes.data, C.byref(ms))
+        if st != 0:
+            raise RuntimeError(f"audio encode failed: status {st}")
+        return out, ms.value
+
+    def free(self):
+        if self.ptr:
+            lib().oa_qwen_audio_encoder_free(self.ptr)
+            self.ptr = None
 
 
 # pack storage policy (crates/openasr-core/src/models/pack_quant.rs):

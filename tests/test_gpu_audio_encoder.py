@@ -1,0 +1,79 @@
+"""The Qwen3-ASR audio encoder graph (the decoder's prefix producer,
+models/qwen/audio_encoder.rs) on the MI355X backend against the numpy
+restatement in oracle/audio_encoder.py on the same synthesised weights and
+seeded mel features.
+
+The encoder is a float path (f32 conv stem, f32 / f16 / Q8_0 projections on
+the matrix-core GEMM or the quantized tile GEMM, flash attention over f16
+K / V), with the reference rounding operands as the device and ggml do, so
+that what remains is the order of float sums. The bar is the op tolerance,
+2e-3 of the largest output, for f32 and f16 projections. With Q8_0
+projections every activation is requantized to int8 per 32-element block:
+an order-of-sum difference that moves an activation across a rounding
+boundary moves it by a whole quantization step, and the stack carries that
+on. The reference run twice with two summation orders (f64 and f32 BLAS)
+already differs by up to ~1e-2 of the largest output there, so the Q8_0 bar
+is 2e-2.
+"""
+
+import numpy as np
+import pytest
+
+from openasr_amd import decoders as D
+from openasr_amd import ggml as g
+
+SMALL = dict(n_mels=32, conv_channels=32, d_model=256, n_heads=4, n_layers=2, ffn=512, out_dim=96)
+
+
+def rel_err(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+def mel_input(n_mels, n_frames, seed):
+    return np.random.default_rng(seed).standard_normal((n_mels, n_frames)).astype(np.float32)
+
+
+def test_token_count_is_13_per_started_chunk():
+    """qwen3_audio_token_count_for_mel_frames (audio_encoder.rs:859-867): each
+    100-frame chunk (a partial tail padded) passes three stride-2 convs,
+    100 -> 50 -> 25 -> 13 rows"""
+    from oracle import audio_encoder as RA
+    for n, want in ((0, 0), (1, 13), (100, 13), (101, 26), (250, 39), (3000, 390)):
+        assert D.qwen_audio_token_count(n) == want == RA.token_count(n), n
+
+
+def test_weights_refuse_shapes_their_type_cannot_hold():
+    with pytest.raises(ValueError):
+        D.QwenAudioWeights(g.Q8_0, **dict(SMALL, ffn=500))  # Q8_0 needs K % 32 == 0
+    w = D.QwenAudioWeights(g.F16, **SMALL)
+    assert w.array(0, D.QA_Q).size == 256 * 256 * 2
+    assert w.array(-1, D.QA_CONV2_W).size == 32 * 32 * 9 * 4
+    assert w.array(-1, D.QA_CONV_OUT).size == 256 * 32 * 4 * 2  # 32 mel bins -> 4 after the stem
+    w.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("wname", ["f32", "f16", "q8_0"])
+def test_audio_encoder_matches_reference(gpu, wname):
+    """three mel chunks (the last one partial) through the whole encoder,
+    then a second input of the same chunk count (the graph replayed) and one
+    of another (rebuilt)"""
+    from oracle import audio_encoder as RA
+    wt = {"f32": g.F32, "f16": g.F16, "q8_0": g.Q8_0}[wname]
+    print(f"qwen audio encoder {wname}", flush=True)
+    w = D.QwenAudioWeights(wt, seed=77, **SMALL)
+    enc = D.QwenAudioEncoder(w, gpu.backend)
+    for n_frames, seed in ((250, 1), (270, 2), (100, 3)):
+        mel = mel_input(SMALL["n_mels"], n_frames, seed)
+        got, ms = enc.encode(mel)
+        want = RA.encode(w, mel)
+        err = rel_err(got, want)
+        spread = rel_err(RA.encode(w, mel, sums="f32"), want)
+        print(f"  frames {n_frames}: rows {got.shape[0]}, {ms:.2f} ms, rel err {err:.2e} "
+              f"(reference f32 vs f64 sums {spread:.2e})", flush=True)
+        assert got.shape == want.shape == (D.qwen_audio_token_count(n_frames), SMALL["out_dim"])
+        assert err < (2e-2 if wt == g.Q8_0 else 2e-3)
+    enc.free()
+    w.free()
