@@ -51,6 +51,9 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--no-whisper", action="store_true", help="skip the Whisper-tiny batch-1 side measurement")
     p.add_argument("--no-long", action="store_true", help="skip the Qwen3-1.7B long-context side measurement")
+    p.add_argument("--no-encoder", action="store_true", help="skip the Qwen3-ASR audio encoder side measurement")
+    p.add_argument("--encoder-only", action="store_true",
+                   help="run only the audio encoder side measurement (for kernel traces of it)")
     p.add_argument("--no-full", action="store_true",
                    help="skip the side lines that time each workload's whole greedy decode")
     p.add_argument("--cpu-seconds", type=float, default=12.0)
@@ -196,6 +199,59 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
     model.free()
     w.free()
     return result
+
+
+def encoder_flops(shape: dict, n_frames: int) -> float:
+    """algorithmic multiply-add work of one encode, x 2 (conv stem, projections,
+    attention scores and context)"""
+    chunks = -(-n_frames // 100)
+    c, d, f, L = shape["conv_channels"], shape["d_model"], shape["ffn"], shape["n_layers"]
+    sizes = [100]
+    mels = [shape["n_mels"]]
+    for _ in range(3):
+        sizes.append((sizes[-1] - 1) // 2 + 1)
+        mels.append((mels[-1] - 1) // 2 + 1)
+    rows = chunks * sizes[3]
+    macs = chunks * (sizes[1] * mels[1] * c * 9 + sizes[2] * mels[2] * c * c * 9 + sizes[3] * mels[3] * c * c * 9)
+    macs += rows * c * mels[3] * d                         # conv_out
+    macs += L * rows * (4 * d * d + 2 * d * f)             # q, k, v, o, up, down
+    macs += L * 2 * rows * rows * d                        # scores and context
+    macs += rows * d * d + rows * d * shape["out_dim"]     # proj1, proj2
+    return 2.0 * macs
+
+
+def run_audio_encoder(n_frames: int = 3000, reps: int = 10):
+    """Qwen3-ASR-0.6B-shaped audio encoder (18 layers of 896, 480 conv
+    channels, 128 mel bins) over n_frames seeded N(0,1) mel frames, with f16
+    projections (an fp16 pack) and Q8_0 ones (a quantized pack: the acoustic
+    encoder's Q8_0 floor): the encode's wall time over `reps` calls"""
+    from openasr_amd import decoders as D
+    from openasr_amd import ggml as g
+
+    plugin = g.plugin()
+    shape = D.QWEN3_06B_AUDIO
+    mel = np.random.default_rng(31).standard_normal((shape["n_mels"], n_frames)).astype(np.float32)
+    flops = encoder_flops(shape, n_frames)
+    res = {"workload": f"qwen3-asr-0.6b-shaped audio encoder, {n_frames} mel frames "
+                       f"({D.qwen_audio_token_count(n_frames)} rows)", "gflop": round(flops / 1e9, 2)}
+    for name, wt in (("f16", g.F16), ("q8_0", g.Q8_0)):
+        w = D.QwenAudioWeights(wt, seed=5, **shape)
+        enc = D.QwenAudioEncoder(w, plugin.backend)
+        enc.encode(mel)  # builds the graph
+        t0 = time.perf_counter()
+        times = []
+        for _ in range(reps):
+            _, ms = enc.encode(mel)
+            times.append(ms)
+        wall = (time.perf_counter() - t0) * 1e3 / reps
+        best = min(times)
+        res[name] = {"ms": round(float(np.median(times)), 3), "best_ms": round(best, 3),
+                     "wall_ms_with_io": round(wall, 3), "tflops": round(flops / (best * 1e-3) / 1e12, 2)}
+        log(f"[bench] audio encoder {name}: {np.median(times):.2f} ms/encode (best {best:.2f}), "
+            f"{flops / (best * 1e-3) / 1e12:.1f} TFLOP/s")
+        enc.free()
+        w.free()
+    return res
 
 
 def run_whisper(n_tokens: int, cpu_seconds: float):
@@ -528,6 +584,9 @@ def main() -> int:
     from openasr_amd import ggml as g
 
     log(f"[bench] backend {g.plugin().name}")
+    if a.encoder_only:
+        print(json.dumps({"audio_encoder": run_audio_encoder()}))
+        return 0
     main_r = run_workload(a.workload, a.steps, a.warmup, a.profile_iters, not a.no_cpu, a.cpu_seconds,
                           full_run=not a.no_full)
     b1 = None
@@ -543,6 +602,9 @@ def main() -> int:
         long = {"tokens_per_s": round(rl["tok_s"], 1), "ms_per_step": round(rl["ms_per_step"], 4),
                 "prefill_positions": rl["n_prefill"], "prefill_ms": round(rl["prefill_ms"], 1),
                 "mul_mat_q4_K_gbs": round(rl["gemv_gbs"], 1)}
+    encoder = None
+    if not a.no_encoder:
+        encoder = run_audio_encoder()
     whisper = None
     if not a.no_whisper:
         whisper = run_whisper(224, 0 if a.no_cpu else min(5.0, a.cpu_seconds))
@@ -591,6 +653,7 @@ def main() -> int:
         "batch1_q8_0": b1,
         "qwen3_1.7b_q4_K_b8_kv4096": long,
         "whisper_tiny_q8_0_b1": whisper,
+        "qwen3_asr_audio_encoder": encoder,
     }
     print(json.dumps(out), flush=True)
     return 0

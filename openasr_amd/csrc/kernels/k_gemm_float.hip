@@ -152,11 +152,27 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float(gemm_float_args g) {
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int64_t n = n0 + wc + 16 * j + 4 * cg + v;
-                if (n < g.N) ((float *) (dbase + n * g.d_nb1))[m] = acc[i][j][v];
+                if (n >= g.N) continue;
+                float o = acc[i][j][v];
+                if (g.epi.bias) o = o + g.epi.bias[m];
+                // the residual has the output's layout (contiguous, same batch offsets)
+                if (g.epi.res) o = o + ((const float *) ((const char *) g.epi.res + (dbase - g.d) + n * g.d_nb1))[m];
+                ((float *) (dbase + n * g.d_nb1))[m] = o;
             }
         }
     }
 }
+
+namespace {
+
+// one weight matrix for every batch and columns that continue across the
+// batch dims (as in dst): the batches are more columns of one product
+bool batches_are_columns(const tview & d, const tview & a, const tview & b) {
+    return a.ne[2] == 1 && a.ne[3] == 1 && b.nb[2] == b.nb[1] * b.ne[1] && b.nb[3] == b.nb[2] * b.ne[2] &&
+           d.nb[2] == d.nb[1] * d.ne[1] && d.nb[3] == d.nb[2] * d.ne[2];
+}
+
+}  // namespace
 
 bool gemm_float_supported(const tview & d, const tview & a, int atype, const tview & b, int btype) {
     const int ea = atype == GGML_TYPE_F16 ? 2 : 4, eb = btype == GGML_TYPE_F16 ? 2 : 4;
@@ -165,13 +181,27 @@ bool gemm_float_supported(const tview & d, const tview & a, int atype, const tvi
     if (a.nb[0] != ea || b.nb[0] != eb || d.nb[0] != 4) return false;
     if (a.ne[0] != b.ne[0] || d.ne[0] != a.ne[1] || d.ne[1] != b.ne[1]) return false;
     if (d.ne[2] != b.ne[2] || d.ne[3] != b.ne[3] || d.ne[2] % a.ne[2] != 0 || d.ne[3] % a.ne[3] != 0) return false;
-    // the matrix cores pay off once a 64 x 64 tile is mostly live
-    return d.ne[0] >= 16 && d.ne[1] >= 16 && d.ne[2] * d.ne[3] <= 65535 &&
-           (d.ne[0] + kGfBM - 1) / kGfBM <= 0x7fffffff && (d.ne[1] + kGfBN - 1) / kGfBN <= 65535;
+    const bool fold = batches_are_columns(d, a, b);
+    const int64_t n = fold ? d.ne[1] * d.ne[2] * d.ne[3] : d.ne[1], batches = fold ? 1 : d.ne[2] * d.ne[3];
+    // the matrix cores pay off once a 64 x 64 tile is mostly live, or a long
+    // K makes even a narrow tile cheaper than a wave per output
+    return d.ne[0] >= 16 && (n >= 16 || a.ne[0] >= 256) && batches <= 65535 && (n + kGfBN - 1) / kGfBN <= 65535;
 }
 
-void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s) {
+void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
+                       const gemm_float_epi & epi) {
+    if (batches_are_columns(d, a, b) && d.ne[2] * d.ne[3] > 1) {
+        tview d2 = d, b2 = b;
+        d2.ne[1] = d.ne[1] * d.ne[2] * d.ne[3];
+        b2.ne[1] = d2.ne[1];
+        d2.ne[2] = d2.ne[3] = b2.ne[2] = b2.ne[3] = 1;
+        d2.nb[2] = d2.nb[3] = d2.nb[1] * d2.ne[1];
+        b2.nb[2] = b2.nb[3] = b2.nb[1] * b2.ne[1];
+        launch_gemm_float(d2, a, atype, b2, btype, s, epi);
+        return;
+    }
     gemm_float_args g{};
+    g.epi = epi;
     g.a = a.data;
     g.a_nb1 = a.nb[1];
     g.a_nb2 = a.nb[2];

@@ -687,8 +687,53 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
     const int atype = w->type, btype = x->type;
     act_src = nullptr;
     if (gemm_float_supported(dv, wv, atype, xv, btype)) {
-        add_step([=](hipStream_t s) { launch_gemm_float(dv, wv, atype, xv, btype, s); }, t,
-                 atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32");
+        // the linear layers' bias ADD (a row of the output's width) and a
+        // residual ADD of the output's shape fold into the epilogue, with
+        // the two f32 roundings of the separate ops
+        hoist h;
+        h.reads.push_back(span_of(w));
+        h.reads.push_back(span_of(xv, btype == GGML_TYPE_F16 ? 2 : 4));
+        h.writes.push_back(span_of(t));
+        if (!hoist_ok(i, h)) return fail(t, "MUL_MAT output overlaps its own input");
+        const ggml_tensor * produced = t;
+        gemm_float_epi epi;
+        auto plain_f32 = [](const ggml_tensor * o) { return o->type == GGML_TYPE_F32 && is_contiguous(o); };
+        auto try_fold = [&](const ggml_tensor * node, const ggml_tensor * o, bool inplace) {
+            hoist h2 = h;
+            h2.nodes.push_back(node);
+            h2.writes[0] = span_of(node);
+            h2.reads.push_back(span_of(o));
+            if (inplace) h2.inplace.push_back({node, o});
+            if (!hoist_ok(i, h2)) return false;
+            h = h2;
+            return true;
+        };
+        const ggml_tensor * add = sole_consumer(t, i + 1);
+        if (add && add->op == GGML_OP_ADD && plain_f32(add) && is_contiguous(t)) {
+            const ggml_tensor * o = add->src[0] == t ? add->src[1] : add->src[0];
+            bool same = o != t;
+            for (int d = 0; d < 4 && same; d++) same = add->ne[d] == t->ne[d];
+            const bool row = same && plain_f32(o) && o->ne[0] == t->ne[0] && o->ne[1] * o->ne[2] * o->ne[3] == 1;
+            if (row && ready_before(o, i) && try_fold(add, o, false)) {
+                epi.bias = (const float *) o->data;
+                produced = add;
+                const ggml_tensor * add2 = sole_consumer(add, i + 1);
+                if (add2 && add2->op == GGML_OP_ADD && plain_f32(add2)) {
+                    const ggml_tensor * r = add2->src[0] == add ? add2->src[1] : add2->src[0];
+                    bool same2 = r != add && plain_f32(r);
+                    for (int d = 0; d < 4 && same2; d++) same2 = add2->ne[d] == t->ne[d] && r->ne[d] == t->ne[d];
+                    if (same2 && ready_before(r, i) && try_fold(add2, r, true)) {
+                        epi.res = (const float *) r->data;
+                        produced = add2;
+                    }
+                }
+            }
+        }
+        for (const ggml_tensor * n : h.nodes) deferred[n] = n;
+        tview ov = dv;
+        ov.data = (char *) produced->data;
+        add_step([=](hipStream_t s) { launch_gemm_float(ov, wv, atype, xv, btype, s, epi); }, produced,
+                 atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32", {produced});
         return true;
     }
     if (btype != GGML_TYPE_F32) return fail(t, "f16 columns outside the matrix-core GEMM");

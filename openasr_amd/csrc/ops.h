@@ -85,7 +85,14 @@ void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tvi
 // float-weight MUL_MAT on the matrix cores (k_gemm_float.hip): src0 a (F16 /
 // F32, rows contiguous) x src1 b (F32 / F16, rows contiguous) -> d (f32),
 // batch dims broadcast from a as ggml does (r2 = d.ne2 / a.ne2, r3)
+// optional epilogue: out = (acc + bias[row]) + res[row, col] (res laid out as
+// the output), the roundings of MUL_MAT, ADD, ADD apart
+struct gemm_float_epi {
+    const float * bias = nullptr;
+    const float * res = nullptr;
+};
 struct gemm_float_args {
+    gemm_float_epi epi;
     const char * a;
     int64_t a_nb1, a_nb2, a_nb3;
     const char * b;
@@ -97,7 +104,8 @@ struct gemm_float_args {
     int a_f16, b_f16, a_vec, b_vec;
 };
 bool gemm_float_supported(const tview & d, const tview & a, int atype, const tview & b, int btype);
-void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s);
+void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
+                       const gemm_float_epi & epi = gemm_float_epi());
 
 struct fattn_args {
     const char * q;

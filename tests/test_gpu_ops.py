@@ -279,6 +279,8 @@ FLOAT_MM_CASES = [
     ("f32", "f16", 64, 100, 33, (1, 1), (1, 1)),
     ("f16", "f32", 100, 64, 40, (2, 1), (4, 2)),        # weight batch broadcast over column batches
     ("f32", "f32", 333, 128, 17, (8, 1), (16, 1)),      # score-shaped: kv heads x query heads
+    ("f16", "f32", 256, 512, 13, (1, 1), (30, 1)),      # one matrix over 30 chunks of 13 columns (folded)
+    ("f32", "f32", 128, 512, 3, (1, 1), (1, 1)),        # three columns, a long K
 ]
 
 
@@ -809,6 +811,42 @@ def test_conv_2d_f32_kernel_chain(ggml, gpu, ref):
     want = (cols_ref @ w.reshape(oc, -1).T.astype(np.float64)).transpose(0, 3, 1, 2)  # [N, OC, OH, OW]
     got = G.get(y).reshape(n, oc, oh, ow)
     assert rel_err(got, want) <= 2e-3
+    G.free()
+
+
+@pytest.mark.parametrize("wt,residual", [("f16", True), ("f32", True), ("f16", False)])
+def test_float_mul_mat_bias_residual_epilogue(ggml, gpu, wt, residual):
+    """the encoders' linear layers (nn/encoder.rs:655-671) and residual ADD:
+    MUL_MAT -> ADD(bias row) -> ADD(residual) in one launch, with the f32
+    roundings of the three ops (within 1e-5 of an f64 product rounded as
+    the graph does); the intermediate nodes are never written"""
+    m, k, n = 200, 384, 90
+    wdt = np.float16 if wt == "f16" else np.float32
+    w = (RNG.standard_normal((m, k)) * 0.05).astype(wdt)
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    b = RNG.standard_normal(m).astype(np.float32)
+    r = RNG.standard_normal((n, m)).astype(np.float32)
+    G = ggml.Graph()
+    L = G.lib
+    W = G.new(ggml.F16 if wt == "f16" else ggml.F32, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    B = G.new(ggml.F32, m, weight=True)
+    R = G.new(ggml.F32, m, n)
+    Y = L.ggml_add(G.ctx, L.ggml_mul_mat(G.ctx, W, X), B)
+    if residual:
+        Y = L.ggml_add(G.ctx, Y, R)
+    run(ggml, gpu, G, Y)
+    G.set(W, w.view(np.uint16) if wt == "f16" else w)
+    G.set(X, x)
+    G.set(B, b)
+    if residual:
+        G.set(R, r)  # not part of the graph otherwise
+    assert G.compute(gpu.backend) == 0
+    xr = x.astype(np.float16) if wt == "f16" else x
+    want = (xr.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32) + b
+    if residual:
+        want = want + r
+    assert rel_err(G.get(Y).reshape(n, m), want) < 1e-5
     G.free()
 
 
