@@ -273,6 +273,16 @@ typedef struct oa_qwen_audio_encoder oa_qwen_audio_encoder;
 oa_qwen_audio_weights * oa_qwen_audio_weights_synthesize(const oa_qwen_audio_config * cfg);
 void oa_qwen_audio_weights_free(oa_qwen_audio_weights * w);
 const void * oa_qwen_audio_weights_tensor(const oa_qwen_audio_weights * w, int layer, int kind, size_t * nbytes);
+/* The encoder of a qwen3-asr runtime pack: keys qwen3-asr.n_mels,
+ * qwen3-asr.audio.{n_layers,d_model,n_heads}, qwen3-asr.llm.d_model (arch/hparams.rs:42-52);
+ * tensors audio.conv.{1,2,3}.{weight,bias}, audio.conv_out.weight (+ optional bias),
+ * audio.ln_post.*, audio.proj{1,2}.*, audio.blk.N.{attn_norm,attn_q,attn_k,attn_v,
+ * attn_out,ffn_norm,ffn_up,ffn_down}.{weight,bias} (models/qwen/tensor_names.rs:3-45);
+ * conv kernels, norms and biases F32 or F16 (widened to f32), projections all
+ * F32, F16 or Q8_0. The bytes are copied; the pack is closed on return. NULL
+ * and a message in err on a missing key or tensor, a wrong shape or type. */
+oa_qwen_audio_weights * oa_qwen_audio_weights_load_gguf(const char * path, char * err, size_t err_cap);
+void oa_qwen_audio_weights_config(const oa_qwen_audio_weights * w, oa_qwen_audio_config * out);
 /* rows the encoder emits for n_frames mel frames: 13 per started 100-frame chunk */
 int oa_qwen_audio_token_count(int n_frames);
 oa_qwen_audio_encoder * oa_qwen_audio_encoder_create(ggml_backend_t backend, const oa_qwen_audio_weights * w);

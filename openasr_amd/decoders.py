@@ -135,6 +135,8 @@ def lib() -> C.CDLL:
     s("oa_qwen_audio_weights_free", None, vp)
     s("oa_qwen_audio_weights_tensor", vp, vp, i, i, C.POINTER(C.c_size_t))
     s("oa_qwen_audio_token_count", i, i)
+    s("oa_qwen_audio_weights_load_gguf", vp, C.c_char_p, C.c_char_p, C.c_size_t)
+    s("oa_qwen_audio_weights_config", None, vp, C.POINTER(QwenAudioConfig))
     s("oa_qwen_audio_encoder_create", vp, vp, vp)
     s("oa_qwen_audio_encoder_free", None, vp)
     s("oa_qwen_audio_encode", i, vp, vp, i, vp, C.POINTER(C.c_double))
@@ -445,6 +447,19 @@ class QwenAudioWeights:
         self.ptr = lib().oa_qwen_audio_weights_synthesize(C.byref(self.cfg))
         if not self.ptr:
             raise ValueError(f"audio encoder weights: shape {shape} does not fit type {wtype}")
+
+    @classmethod
+    def load_gguf(cls, path) -> "QwenAudioWeights":
+        """the audio encoder of a qwen3-asr runtime pack (oa_qwen_audio_weights_load_gguf)"""
+        err = C.create_string_buffer(512)
+        ptr = lib().oa_qwen_audio_weights_load_gguf(str(path).encode(), err, len(err))
+        if not ptr:
+            raise ValueError(f"{path}: {err.value.decode()}")
+        self = cls.__new__(cls)
+        self.ptr = ptr
+        self.cfg = QwenAudioConfig()
+        lib().oa_qwen_audio_weights_config(ptr, C.byref(self.cfg))
+        return self
 
     def array(self, layer: int, kind: int) -> np.ndarray:
         """a copy of one tensor's bytes (uint8); layer -1 for the global tensors"""

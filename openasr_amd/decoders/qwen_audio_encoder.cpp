@@ -9,17 +9,21 @@
 //                                           nn/encoder.rs:654-870, nn/attn.rs:89-126,
 //                                           nn/norm.rs:10-31, nn/ffn.rs:22-50
 //   ln_post, proj1, GELU_ERF, proj2         audio_encoder.rs:615-672
-// The weights here are synthesised (seeded); the graph is the same op
-// sequence whatever their source.
+// The weights are synthesised (seeded) or read from a qwen3-asr runtime pack
+// (load_qwen3_audio_encoder_weights_from_reader, audio_encoder.rs:896-1050);
+// the graph is the same op sequence whatever their source.
 
 #include <chrono>
 #include <cmath>
+#include <cstdio>
 #include <cstring>
 #include <map>
+#include <string>
 #include <vector>
 
 #include "ggml_host.h"
 #include "openasr_models.h"
+#include "pack_reader.h"
 
 extern "C" void oa_synth_normal(uint64_t seed, uint64_t stream, int64_t first, int64_t n, float mean, float std_dev,
                                 float * out);
@@ -64,6 +68,7 @@ std::vector<uint8_t> bytes_of(const std::vector<float> & v) {
 struct oa_qwen_audio_weights {
     oa_qwen_audio_config cfg;
     int freq_bins;                                  // mel bins after the three convolutions
+    bool conv_out_bias = true;                      // optional in a pack (audio_encoder.rs:907-915)
     std::map<int, std::vector<uint8_t>> global;     // kind -> bytes
     std::vector<std::vector<std::vector<uint8_t>>> layers;  // [layer][kind]
 };
@@ -71,6 +76,7 @@ struct oa_qwen_audio_weights {
 struct oa_qwen_audio_encoder {
     oa_qwen_audio_config cfg;
     int freq_bins;
+    bool conv_out_bias;
     ggml_backend_t backend;
     ggml_context * ctx = nullptr;
     ggml_backend_buffer_t buf = nullptr;
@@ -160,7 +166,8 @@ bool build_graph(oa_qwen_audio_encoder * e, int chunks) {
     // [cof, F, C, chunks] -> [F, C, cof, chunks] -> [C F, cof, chunks]
     x = ggml_cont(ctx, ggml_permute(ctx, x, 2, 0, 1, 3));
     x = ggml_reshape_3d(ctx, x, (int64_t) c.conv_channels * e->freq_bins, cof, chunks);
-    x = ggml_add(ctx, ggml_mul_mat(ctx, e->g[OA_QA_CONV_OUT], x), e->g[OA_QA_CONV_OUT_B]);
+    x = ggml_mul_mat(ctx, e->g[OA_QA_CONV_OUT], x);
+    if (e->conv_out_bias) x = ggml_add(ctx, x, e->g[OA_QA_CONV_OUT_B]);
     x = ggml_add(ctx, x, posemb);
     x = ggml_reshape_2d(ctx, x, c.d_model, rows);
     // flash attention takes an f16 mask: the f32 one cast once per layer (nn/encoder.rs:794-800)
@@ -266,6 +273,7 @@ oa_qwen_audio_encoder * oa_qwen_audio_encoder_create(ggml_backend_t backend, con
     oa_qwen_audio_encoder * e = new oa_qwen_audio_encoder;
     e->cfg = c;
     e->freq_bins = w->freq_bins;
+    e->conv_out_bias = w->conv_out_bias;
     e->backend = backend;
     ggml_init_params ip = {ggml_tensor_overhead() * ((size_t) c.n_layers * OA_QA_LAYER_KINDS + 32), nullptr, true};
     e->ctx = ggml_init(ip);
@@ -306,7 +314,7 @@ oa_qwen_audio_encoder * oa_qwen_audio_encoder_create(ggml_backend_t backend, con
     for (auto & kv : e->g) {
         size_t n = 0;
         const void * src = oa_qwen_audio_weights_tensor(w, -1, kv.first, &n);
-        ggml_backend_tensor_set(kv.second, src, 0, n);
+        if (src) ggml_backend_tensor_set(kv.second, src, 0, n);
     }
     for (int l = 0; l < c.n_layers; l++) {
         for (int kind = 0; kind < OA_QA_LAYER_KINDS; kind++) {
@@ -361,5 +369,138 @@ int oa_qwen_audio_encode(oa_qwen_audio_encoder * e, const float * mel, int n_fra
     if (ms) *ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now() - t0).count();
     return GGML_STATUS_SUCCESS;
 }
+
+}  // extern "C"
+
+namespace {
+
+std::vector<uint8_t> f32_bytes_of(const void * p, int type, int64_t n) {
+    std::vector<float> v((size_t) n);
+    if (type == GGML_TYPE_F32) std::memcpy(v.data(), p, (size_t) n * 4);
+    else
+        for (int64_t i = 0; i < n; i++) v[(size_t) i] = ggml_fp16_to_fp32(((const ggml_fp16_t *) p)[i]);
+    return bytes_of(v);
+}
+
+}  // namespace
+
+extern "C" {
+
+// The names and checks of load_qwen3_audio_encoder_weights_from_reader
+// (audio_encoder.rs:896-1050; names models/qwen/tensor_names.rs:3-45; keys
+// arch/hparams.rs:42-52): float tensors (conv kernels, norms, biases) may be
+// F32 or F16 and are widened to f32, as load_tensor_f32 does; the 2-D
+// projections are bound in their stored type, one of F32 / F16 / Q8_0 for
+// all of them.
+oa_qwen_audio_weights * oa_qwen_audio_weights_load_gguf(const char * path, char * err, size_t err_cap) {
+    auto report = [&](const std::string & msg) -> oa_qwen_audio_weights * {
+        if (err && err_cap) std::snprintf(err, err_cap, "%s", msg.c_str());
+        return nullptr;
+    };
+    char gerr[256] = {0};
+    oa_gguf * g = oa_gguf_open(path, gerr, sizeof(gerr));
+    if (!g) return report(gerr);
+    oa_pack::pack_reader r{g, {}};
+    oa_qwen_audio_weights * w = new oa_qwen_audio_weights;
+    auto bad = [&](const std::string & msg) {
+        delete w;
+        oa_gguf_close(g);
+        return report(msg);
+    };
+    if (const char * a = oa_gguf_get_str(g, "general.architecture"); a && std::strcmp(a, "qwen3-asr") != 0)
+        return bad(std::string("general.architecture is ") + a + ", not qwen3-asr");
+    oa_qwen_audio_config & c = w->cfg;
+    c = oa_qwen_audio_config{};
+    if (!r.key_i("qwen3-asr.n_mels", c.n_mels) || !r.key_i("qwen3-asr.audio.n_layers", c.n_layers) ||
+        !r.key_i("qwen3-asr.audio.d_model", c.d_model) || !r.key_i("qwen3-asr.audio.n_heads", c.n_heads) ||
+        !r.key_i("qwen3-asr.llm.d_model", c.out_dim))
+        return bad(r.err);
+    if (c.d_model % c.n_heads != 0 || c.d_model % 2 != 0) return bad("audio.d_model is not an even multiple of audio.n_heads");
+    w->freq_bins = conv_out_len(conv_out_len(conv_out_len(c.n_mels)));
+    // rank-4 conv kernels [3, 3, IC, OC]
+    auto conv = [&](const char * name, int64_t ic, int64_t oc, int kind) {
+        const int64_t i = oa_gguf_find_tensor(g, name);
+        if (i < 0) return r.fail(std::string("missing tensor ") + name);
+        int type = 0;
+        int64_t ne[4];
+        oa_gguf_tensor_info(g, i, &type, ne);
+        if (ne[0] != 3 || ne[1] != 3 || ne[2] != ic || (oc > 0 && ne[3] != oc))
+            return r.fail(std::string("tensor ") + name + " is not a 3x3 kernel over the expected channels");
+        if (type != GGML_TYPE_F32 && type != GGML_TYPE_F16) return r.fail(std::string("tensor ") + name + " is not F32 or F16");
+        size_t nb = 0;
+        w->global[kind] = f32_bytes_of(oa_gguf_tensor_data(g, i, &nb), type, 9 * ic * ne[3]);
+        if (oc <= 0) c.conv_channels = (int) ne[3];
+        return true;
+    };
+    auto vecf = [&](const std::string & name, int64_t n, std::vector<uint8_t> & out) {
+        int type = 0;
+        const int64_t i = r.tensor(name, n, 1, {GGML_TYPE_F32, GGML_TYPE_F16}, type);
+        if (i < 0) return false;
+        size_t nb = 0;
+        out = f32_bytes_of(oa_gguf_tensor_data(g, i, &nb), type, n);
+        return true;
+    };
+    int wtype = -1;
+    auto mat = [&](const std::string & name, int64_t k, int64_t rows, std::vector<uint8_t> & out) {
+        int type = 0;
+        const int64_t i = r.tensor(name, k, rows, {GGML_TYPE_F32, GGML_TYPE_F16, GGML_TYPE_Q8_0}, type);
+        if (i < 0) return false;
+        if (wtype < 0) wtype = type;
+        if (type != wtype)
+            return r.fail("tensor " + name + " is " + ggml_type_name((ggml_type) type) + ", the encoder's projections are " +
+                          ggml_type_name((ggml_type) wtype));
+        size_t nb = 0;
+        const uint8_t * p = (const uint8_t *) oa_gguf_tensor_data(g, i, &nb);
+        out.assign(p, p + nb);
+        return true;
+    };
+    if (!conv("audio.conv.1.weight", 1, 0, OA_QA_CONV1_W)) return bad(r.err);
+    const int C = c.conv_channels, d = c.d_model;
+    if (!conv("audio.conv.2.weight", C, C, OA_QA_CONV2_W) || !conv("audio.conv.3.weight", C, C, OA_QA_CONV3_W) ||
+        !vecf("audio.conv.1.bias", C, w->global[OA_QA_CONV1_B]) || !vecf("audio.conv.2.bias", C, w->global[OA_QA_CONV2_B]) ||
+        !vecf("audio.conv.3.bias", C, w->global[OA_QA_CONV3_B]) ||
+        !mat("audio.conv_out.weight", (int64_t) C * w->freq_bins, d, w->global[OA_QA_CONV_OUT]) ||
+        !vecf("audio.ln_post.weight", d, w->global[OA_QA_LN_POST_W]) ||
+        !vecf("audio.ln_post.bias", d, w->global[OA_QA_LN_POST_B]) ||
+        !mat("audio.proj1.weight", d, d, w->global[OA_QA_PROJ1]) || !vecf("audio.proj1.bias", d, w->global[OA_QA_PROJ1_B]) ||
+        !mat("audio.proj2.weight", d, c.out_dim, w->global[OA_QA_PROJ2]) ||
+        !vecf("audio.proj2.bias", c.out_dim, w->global[OA_QA_PROJ2_B]))
+        return bad(r.err);
+    w->conv_out_bias = oa_gguf_find_tensor(g, "audio.conv_out.bias") >= 0;
+    if (w->conv_out_bias && !vecf("audio.conv_out.bias", d, w->global[OA_QA_CONV_OUT_B])) return bad(r.err);
+    w->layers.assign((size_t) c.n_layers, std::vector<std::vector<uint8_t>>(OA_QA_LAYER_KINDS));
+    for (int l = 0; l < c.n_layers; l++) {
+        auto & L = w->layers[(size_t) l];
+        const std::string p = "audio.blk." + std::to_string(l) + ".";
+        // the FFN width comes from ffn_up's rows
+        const int64_t up = oa_gguf_find_tensor(g, (p + "ffn_up.weight").c_str());
+        if (up < 0) return bad("missing tensor " + p + "ffn_up.weight");
+        int t = 0;
+        int64_t ne[4];
+        oa_gguf_tensor_info(g, up, &t, ne);
+        if (l == 0) c.ffn = (int) ne[1];
+        if (!vecf(p + "attn_norm.weight", d, L[OA_QA_ATTN_NORM_W]) || !vecf(p + "attn_norm.bias", d, L[OA_QA_ATTN_NORM_B]) ||
+            !mat(p + "attn_q.weight", d, d, L[OA_QA_Q]) || !vecf(p + "attn_q.bias", d, L[OA_QA_Q_B]) ||
+            !mat(p + "attn_k.weight", d, d, L[OA_QA_K]) || !vecf(p + "attn_k.bias", d, L[OA_QA_K_B]) ||
+            !mat(p + "attn_v.weight", d, d, L[OA_QA_V]) || !vecf(p + "attn_v.bias", d, L[OA_QA_V_B]) ||
+            !mat(p + "attn_out.weight", d, d, L[OA_QA_O]) || !vecf(p + "attn_out.bias", d, L[OA_QA_O_B]) ||
+            !vecf(p + "ffn_norm.weight", d, L[OA_QA_FFN_NORM_W]) || !vecf(p + "ffn_norm.bias", d, L[OA_QA_FFN_NORM_B]) ||
+            !mat(p + "ffn_up.weight", d, c.ffn, L[OA_QA_UP]) || !vecf(p + "ffn_up.bias", c.ffn, L[OA_QA_UP_B]) ||
+            !mat(p + "ffn_down.weight", c.ffn, d, L[OA_QA_DOWN]) || !vecf(p + "ffn_down.bias", d, L[OA_QA_DOWN_B]))
+            return bad(r.err);
+    }
+    c.wtype = wtype;
+    if (c.wtype == GGML_TYPE_Q8_0 && (((int64_t) C * w->freq_bins) % 32 || d % 32 || c.ffn % 32))
+        return bad("Q8_0 projections need every K % 32 == 0");
+    const int half = d / 2;
+    const float log_inc = std::log(10000.0f) / (float) (half - 1 > 1 ? half - 1 : 1);
+    std::vector<float> inv((size_t) half);
+    for (int i = 0; i < half; i++) inv[(size_t) i] = std::exp(-log_inc * (float) i);
+    w->global[OA_QA_INV_TIMESCALES] = bytes_of(inv);
+    oa_gguf_close(g);
+    return w;
+}
+
+void oa_qwen_audio_weights_config(const oa_qwen_audio_weights * w, oa_qwen_audio_config * out) { *out = w->cfg; }
 
 }  // extern "C"

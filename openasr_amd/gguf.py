@@ -130,6 +130,79 @@ def export_qwen_pack(weights, path, with_output: bool = False, extra_kv: dict | 
     return Path(path)
 
 
+# per-layer qwen3-asr audio encoder tensors (models/qwen/tensor_names.rs:23-45):
+# (kind in openasr_amd.decoders, name after "audio.blk.N.")
+QWEN_AUDIO_LAYER_NAMES = [
+    ("QA_ATTN_NORM_W", "attn_norm.weight"), ("QA_ATTN_NORM_B", "attn_norm.bias"), ("QA_Q", "attn_q.weight"),
+    ("QA_Q_B", "attn_q.bias"), ("QA_K", "attn_k.weight"), ("QA_K_B", "attn_k.bias"), ("QA_V", "attn_v.weight"),
+    ("QA_V_B", "attn_v.bias"), ("QA_O", "attn_out.weight"), ("QA_O_B", "attn_out.bias"),
+    ("QA_FFN_NORM_W", "ffn_norm.weight"), ("QA_FFN_NORM_B", "ffn_norm.bias"), ("QA_UP", "ffn_up.weight"),
+    ("QA_UP_B", "ffn_up.bias"), ("QA_DOWN", "ffn_down.weight"), ("QA_DOWN_B", "ffn_down.bias"),
+]
+
+
+def export_qwen_audio_pack(weights, path, skip: tuple = (), conv_f16: bool = False, extra_kv: dict | None = None,
+                           alignment: int = 32, replace: dict | None = None) -> Path:
+    """Write `weights` (openasr_amd.decoders.QwenAudioWeights) as the audio
+    encoder half of a qwen3-asr pack (tensor names models/qwen/tensor_names.rs,
+    keys arch/hparams.rs:42-52). conv_f16: store the conv kernels as F16 (the
+    loader widens them); skip: tensor names left out, replace: name ->
+    (ggml type, bytes) stored instead (tests of the loader)."""
+    from . import decoders as D
+
+    c = weights.cfg
+    w = GGUFWriter(alignment)
+    w.add("general.architecture", STR, "qwen3-asr")
+    w.add("openasr.package.version", STR, "1")
+    for key, val in (("n_mels", c.n_mels), ("audio.n_layers", c.n_layers), ("audio.d_model", c.d_model),
+                     ("audio.n_heads", c.n_heads), ("llm.d_model", c.out_dim)):
+        w.add(f"qwen3-asr.{key}", U32, val)
+    for key, (vtype, val) in (extra_kv or {}).items():
+        w.add(key, vtype, val)
+    fb = c.n_mels
+    for _ in range(3):
+        fb = (fb - 1) // 2 + 1
+    C_, d = c.conv_channels, c.d_model
+
+    def put(name, gtype, ne, data):
+        if name in (replace or {}):
+            gtype, data = replace[name]
+        if name not in skip:
+            w.add_tensor(name, gtype, ne, data)
+
+    for i, (kw, kb) in enumerate(((D.QA_CONV1_W, D.QA_CONV1_B), (D.QA_CONV2_W, D.QA_CONV2_B),
+                                  (D.QA_CONV3_W, D.QA_CONV3_B)), start=1):
+        ic = 1 if i == 1 else C_
+        kern = weights.array(-1, kw)
+        if conv_f16:
+            put(f"audio.conv.{i}.weight", 1, (3, 3, ic, C_), kern.view(np.float32).astype(np.float16))
+        else:
+            put(f"audio.conv.{i}.weight", 0, (3, 3, ic, C_), kern)
+        put(f"audio.conv.{i}.bias", 0, (C_,), weights.array(-1, kb))
+    wt = c.wtype
+    put("audio.conv_out.weight", wt, (C_ * fb, d), weights.array(-1, D.QA_CONV_OUT))
+    put("audio.conv_out.bias", 0, (d,), weights.array(-1, D.QA_CONV_OUT_B))
+    put("audio.ln_post.weight", 0, (d,), weights.array(-1, D.QA_LN_POST_W))
+    put("audio.ln_post.bias", 0, (d,), weights.array(-1, D.QA_LN_POST_B))
+    put("audio.proj1.weight", wt, (d, d), weights.array(-1, D.QA_PROJ1))
+    put("audio.proj1.bias", 0, (d,), weights.array(-1, D.QA_PROJ1_B))
+    put("audio.proj2.weight", wt, (d, c.out_dim), weights.array(-1, D.QA_PROJ2))
+    put("audio.proj2.bias", 0, (c.out_dim,), weights.array(-1, D.QA_PROJ2_B))
+    for layer in range(c.n_layers):
+        for kind_name, name in QWEN_AUDIO_LAYER_NAMES:
+            kind = getattr(D, kind_name)
+            data = weights.array(layer, kind)
+            if name.endswith(".bias") or "norm" in name:
+                ne = (c.ffn if kind == D.QA_UP_B else d,)
+                gtype = 0
+            else:
+                ne = (c.ffn if kind == D.QA_DOWN else d, c.ffn if kind == D.QA_UP else d)
+                gtype = wt
+            put(f"audio.blk.{layer}.{name}", gtype, ne, data)
+    w.write(path)
+    return Path(path)
+
+
 # per-layer whisper decoder tensors: (kind in openasr_amd.decoders, name after "decoder.layers.N.")
 WHISPER_LAYER_NAMES = [
     ("WH_SELF_LN_W", "self_attn_layer_norm.weight"), ("WH_SELF_LN_B", "self_attn_layer_norm.bias"),

@@ -54,6 +54,59 @@ def test_weights_refuse_shapes_their_type_cannot_hold():
     w.free()
 
 
+@pytest.mark.parametrize("wname", ["f16", "q8_0"])
+def test_runtime_pack_reads_back_tensor_for_tensor(tmp_path, wname):
+    """an audio encoder written into a qwen3-asr pack (f16 conv kernels, as
+    an fp16 pack stores them) loads back with the same configuration and
+    every tensor's bytes (the kernels widened back to the same f32 values)"""
+    from openasr_amd import gguf
+    wt = g.F16 if wname == "f16" else g.Q8_0
+    w = D.QwenAudioWeights(wt, seed=9, **SMALL)
+    path = gguf.export_qwen_audio_pack(w, tmp_path / "enc.oasr", conv_f16=True)
+    r = D.QwenAudioWeights.load_gguf(path)
+    for f in ("n_mels", "conv_channels", "d_model", "n_heads", "n_layers", "ffn", "out_dim", "wtype"):
+        assert getattr(r.cfg, f) == getattr(w.cfg, f), f
+    for kind in range(D.QA_CONV1_W, D.QA_INV_TIMESCALES + 1):
+        a, b = w.array(-1, kind), r.array(-1, kind)
+        if kind in (D.QA_CONV1_W, D.QA_CONV2_W, D.QA_CONV3_W):
+            a = a.view(np.float32).astype(np.float16).astype(np.float32).view(np.uint8)
+        assert np.array_equal(a, b), kind
+    for layer in range(SMALL["n_layers"]):
+        for kind in range(D.QA_LAYER_KINDS):
+            assert np.array_equal(w.array(layer, kind), r.array(layer, kind)), (layer, kind)
+    r.free()
+    w.free()
+
+
+@pytest.mark.parametrize("skip,msg", [
+    (("audio.blk.1.attn_k.bias",), "missing tensor audio.blk.1.attn_k.bias"),
+    (("audio.conv.2.weight",), "missing tensor audio.conv.2.weight"),
+    (("audio.ln_post.weight",), "missing tensor audio.ln_post.weight"),
+])
+def test_runtime_pack_refuses_a_missing_tensor(tmp_path, skip, msg):
+    from openasr_amd import gguf
+    w = D.QwenAudioWeights(g.F16, seed=9, **SMALL)
+    path = gguf.export_qwen_audio_pack(w, tmp_path / "enc.oasr", skip=skip)
+    with pytest.raises(ValueError, match=msg):
+        D.QwenAudioWeights.load_gguf(path)
+    w.free()
+
+
+def test_runtime_pack_refuses_mixed_projection_types(tmp_path):
+    """the encoder's projections share one storage type (all F16, or all
+    Q8_0 under the acoustic encoder's floor): an F16 pack with one Q8_0
+    matrix is refused by name"""
+    from openasr_amd import gguf
+    w16 = D.QwenAudioWeights(g.F16, seed=9, **SMALL)
+    w8 = D.QwenAudioWeights(g.Q8_0, seed=9, **SMALL)
+    path = gguf.export_qwen_audio_pack(w16, tmp_path / "enc.oasr",
+                                       replace={"audio.proj1.weight": (g.Q8_0, w8.array(-1, D.QA_PROJ1))})
+    with pytest.raises(ValueError, match="audio.proj1.weight is q8_0, the encoder's projections are f16"):
+        D.QwenAudioWeights.load_gguf(path)
+    w16.free()
+    w8.free()
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("wname", ["f32", "f16", "q8_0"])
 def test_audio_encoder_matches_reference(gpu, wname):
@@ -76,4 +129,25 @@ def test_audio_encoder_matches_reference(gpu, wname):
         assert got.shape == want.shape == (D.qwen_audio_token_count(n_frames), SMALL["out_dim"])
         assert err < (2e-2 if wt == g.Q8_0 else 2e-3)
     enc.free()
+    w.free()
+
+
+@pytest.mark.gpu
+def test_runtime_pack_encodes_like_synthesized(gpu, tmp_path):
+    """the encoder bound from a qwen3-asr pack (f32 conv kernels, F16
+    projections) gives the same bits as the synthesised weights it was
+    written from"""
+    from openasr_amd import gguf
+    w = D.QwenAudioWeights(g.F16, seed=13, **SMALL)
+    path = gguf.export_qwen_audio_pack(w, tmp_path / "enc.oasr")
+    r = D.QwenAudioWeights.load_gguf(path)
+    mel = mel_input(SMALL["n_mels"], 230, 4)
+    a = D.QwenAudioEncoder(w, gpu.backend)
+    b = D.QwenAudioEncoder(r, gpu.backend)
+    ya, _ = a.encode(mel)
+    yb, _ = b.encode(mel)
+    assert np.array_equal(ya, yb)
+    a.free()
+    b.free()
+    r.free()
     w.free()
