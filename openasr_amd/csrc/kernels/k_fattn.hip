@@ -105,6 +105,26 @@ __device__ __forceinline__ float fa_dot(const uint4 (&kr)[D / 8], const float * 
     return acc;
 }
 
+// the same chain with the query as f16 halves (its f16-rounded values), all
+// D/8 16-byte pieces requested before the first step: the chain then waits
+// on no LDS read (each step is one v_fma_mix_f32, both operands halves)
+template <int D>
+__device__ __forceinline__ float fa_dot_h(const uint4 (&kr)[D / 8], const uint4 * qh) {
+    uint4 qv[D / 8];
+#pragma unroll
+    for (int u = 0; u < D / 8; u++) qv[u] = qh[u];
+    float acc = 0.0f;
+#pragma unroll
+    for (int u = 0; u < D / 8; u++) {
+        float kf[8], qf[8];
+        unpack8(kr[u], kf);
+        unpack8(qv[u], qf);
+#pragma unroll
+        for (int i = 0; i < 8; i++) acc = fmaf(kf[i], qf[i], acc);
+    }
+    return acc;
+}
+
 // mask of chunk c for the tile's query positions; true if any entry is live
 template <int D, int R>
 __device__ __forceinline__ bool fa_load_mask(const fattn_args & a, const fa_tile & t, int c, fa_smem<D, R> & sm) {
@@ -490,7 +510,7 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     constexpr int DL = D / 64;
     constexpr int KU = D / 8;  // 16-byte pieces of a K row
     static_assert(!STEP || D == 128, "the step form handles 128-wide heads");
-    __shared__ __align__(16) float s_q[4][D];
+    __shared__ __align__(16) uint16_t s_q[4][D];  // per wave the query row, f16
     __shared__ uint4 s_k[4][kFaChunk * KU];  // per wave the chunk's K rows, swizzled (fa_kslot)
     __shared__ __align__(16) uint16_t s_vnew[STEP ? 4 : 1][D];
     const fattn_args & a = st.fa;
@@ -558,7 +578,7 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
         jn = j >= 0 && j < clen ? (int) j : -1;
     } else {
         const float * qp = (const float *) (a.q + (int64_t) head * a.q_nb2 + (int64_t) seq * a.q_nb3);
-        for (int d = lane; d < D; d += 64) s_q[wave][d] = round_to_half(qp[d]);
+        for (int d = lane; d < D; d += 64) s_q[wave][d] = float_to_half_bits(qp[d]);
         if (lane < clen) {
             mv = 0.0f;
             if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
@@ -589,8 +609,8 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     if constexpr (STEP) {
         float y0, y1;
         as_norm_rope(qx0, qx1, qw0, qw1, qcs, st.q_eps, y0, y1);
-        s_q[wave][lane] = round_to_half(y0);
-        s_q[wave][lane + 64] = round_to_half(y1);
+        s_q[wave][lane] = float_to_half_bits(y0);
+        s_q[wave][lane + 64] = float_to_half_bits(y1);
         if (jn >= 0) {
             // this step's K / V rows: K replaces the LDS row jn once the
             // chunk's K has landed (its requests precede the 64 V requests, so
@@ -635,7 +655,7 @@ __global__ __launch_bounds__(256) void k_fattn_decode(attn_step_args st, float *
     }
 
     // scores: lane = position, the f32 fma chain over the dims in order
-    const float sc = fa_dot<D>(kr, &s_q[wave][0]);
+    const float sc = fa_dot_h<D>(kr, (const uint4 *) &s_q[wave][0]);
     const float sv = live ? sc * a.scale + mv : -INFINITY;
     const float m = wave_max(sv);
     const float p = sv == -INFINITY ? 0.0f : expf_det(sv - m);
