@@ -448,6 +448,56 @@ def test_flash_attn_fully_masked_chunks_are_skipped_exactly(ggml, gpu, ref):
     G.free()
 
 
+# one sequence's decode attention straight into a Q8_0 output projection (+
+# residual): the attention's combine writes the projection's quantized
+# activations, the one-column projection reads them. Qwen3-0.6B shape at a
+# 1024-position arena with 450 live positions and at 4096 positions (64
+# chunks); Whisper-tiny self attention (448 positions) and cross attention
+# (1500, no mask).
+ATTN_PROJ_CASES = [(128, 16, 8, 1024, 450, 1024), (128, 16, 8, 4096, 3000, 1024), (64, 6, 6, 448, 37, 384),
+                   (64, 6, 6, 1500, None, 384)]
+
+
+@pytest.mark.parametrize("d,hq,hkv,n_kv,live,m", ATTN_PROJ_CASES)
+def test_attention_into_output_projection(ggml, gpu, ref, d, hq, hkv, n_kv, live, m):
+    print(f"attention -> o-proj D={d} Hq={hq} Hkv={hkv} kv={n_kv} live={live} M={m}", flush=True)
+    k_in = d * hq
+    q = RNG.standard_normal((hq, 1, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    wq = ggml.quantize(ggml.Q8_0, ggml.synth_normal(3, 1, m * k_in, 0, 0.02).reshape(m, k_in))
+    G = ggml.Graph()
+    Q = G.new(ggml.F32, d, 1, hq, 1)
+    K = G.new(ggml.F16, d, n_kv, hkv, 1)
+    V = G.new(ggml.F16, d, n_kv, hkv, 1)
+    M = None if live is None else G.new(ggml.F16, n_kv, 1, 1, 1)
+    W = G.new(ggml.Q8_0, k_in, m, weight=True)
+    X = G.new(ggml.F32, m, 1)
+    O = G.lib.ggml_flash_attn_ext(G.ctx, Q, K, V, M, 1 / math.sqrt(d), 0.0, 0.0)
+    R = G.lib.ggml_reshape_2d(G.ctx, O, k_in, 1)
+    Y = G.lib.ggml_add(G.ctx, G.lib.ggml_mul_mat(G.ctx, W, R), X)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    for it in range(3):  # the same graph again (captured, then replayed) on new inputs
+        q = RNG.standard_normal((hq, 1, d)).astype(np.float32)
+        x = RNG.standard_normal((1, m)).astype(np.float32)
+        mask = np.zeros((1, n_kv), np.float16)
+        if live is not None:
+            mask[0, live + it:] = -np.inf
+        G.set(Q, q)
+        G.set(K, k.view(np.uint16))
+        G.set(V, v.view(np.uint16))
+        G.set(X, x)
+        if M is not None:
+            G.set(M, mask.view(np.uint16))
+        assert G.compute(gpu.backend) == 0
+        att = ref.flash_attn(np.ascontiguousarray(q.transpose(1, 0, 2)), k.view(np.uint16), v.view(np.uint16),
+                             None if M is None else mask.view(np.uint16), 1 / math.sqrt(d), fidelity=5)
+        want = ref.mul_mat(ggml.Q8_0, wq, m, k_in, att.reshape(1, k_in)) + x
+        assert_same_bits(G.get(Y).reshape(1, m), want)
+    G.free()
+
+
 # ------------------------------------------------------------ row ops ---
 
 def test_rms_norm_mul_fused(ggml, gpu, ref):
