@@ -296,6 +296,27 @@ __device__ __forceinline__ void gemv_stage_quant(const gemv_args & a, int n0, in
     __syncthreads();
 }
 
+__device__ __forceinline__ double readlane_d(double v, int l) {
+    return __hiloint2double(__builtin_amdgcn_readlane(__double2hiint(v), l),
+                            __builtin_amdgcn_readlane(__double2loint(v), l));
+}
+
+// the sum over a column's spans, in span order from 0.0, when the column's
+// nspan spans are rows first .. first + nspan - 1 of this wave's group: each
+// row's row16_sum is read from its lane 0
+__device__ __forceinline__ double group_col_sum(double v, int first, int nspan) {
+    const double r0 = readlane_d(v, 0), r1 = readlane_d(v, 16), r2 = readlane_d(v, 32), r3 = readlane_d(v, 48);
+    double t = 0.0;
+#pragma unroll
+    for (int sp = 0; sp < 4; sp++) {
+        if (sp < nspan) {
+            const int q = first + sp;
+            t += q == 0 ? r0 : q == 1 ? r1 : q == 2 ? r2 : r3;
+        }
+    }
+    return t;
+}
+
 // normalising staging: the statistics are f64 sums of the elements (layer
 // norm) and of the centred squares -- per lane in element order, over the
 // row by DPP, per column over the spans in order -- then
@@ -328,6 +349,51 @@ __device__ __forceinline__ void gemv_stage_norm(const gemv_args & a, int n0, int
     __builtin_amdgcn_sched_barrier(0);  // keep the activation loads ahead of the caller's
     issue();  // the caller's weight loads, behind the activations
     const double n = (double) K;
+    if (kNormGroups == 1 && (nspan == 1 || nspan == 2 || nspan == 4)) {
+        // every column's spans lie in one wave's group (rows first ..
+        // first + nspan - 1): the statistics are summed inside the wave --
+        // the same sums in the same order -- with no LDS round trip and no
+        // barrier before the quantization
+        const int job = 4 * wave + row;
+        const int first = (row / nspan) * nspan;
+        float mean = 0.0f;
+        if (p.norm == 1) {
+            double s = 0.0;
+#pragma unroll
+            for (int t = 0; t < 16; t++) s += ok[0] ? (double) elem16(x[0], t) : 0.0;
+            mean = (float) (group_col_sum(row16_sum(s), first, nspan) / n);
+        }
+        double s2 = 0.0;
+#pragma unroll
+        for (int t = 0; t < 16; t++) {
+            const float v = ok[0] ? elem16(x[0], t) - mean : 0.0f;
+            s2 += (double) (v * v);
+        }
+        const float var = (float) (group_col_sum(row16_sum(s2), first, nspan) / n);
+        const float scale = 1.0f / sqrtf(var + p.eps);
+        if (4 * wave < jobs) {  // uniform: some row of the wave has a job
+            const int col = ok[0] ? job / nspan : 0;
+            float4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                float4 xs = x[0][j];
+                if (p.norm == 1) xs = make_float4(xs.x - mean, xs.y - mean, xs.z - mean, xs.w - mean);
+                v[j].x = (xs.x * scale) * w[0][j].x;
+                v[j].y = (xs.y * scale) * w[0][j].y;
+                v[j].z = (xs.z * scale) * w[0][j].z;
+                v[j].w = (xs.w * scale) * w[0][j].w;
+                if constexpr (BIAS) {
+                    v[j].x += b[0][j].x;
+                    v[j].y += b[0][j].y;
+                    v[j].z += b[0][j].z;
+                    v[j].w += b[0][j].w;
+                }
+            }
+            stage_quantize<WT>(v, ok[0], col, job % nspan, li, K, L, smem);
+        }
+        __syncthreads();
+        return;
+    }
     if (p.norm == 1) {
 #pragma unroll
         for (int k = 0; k < kNormGroups; k++) {
