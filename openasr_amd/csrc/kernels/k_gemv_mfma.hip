@@ -773,7 +773,8 @@ __device__ __forceinline__ void stream_load(const gemv_args & a, int64_t base, i
     }
 }
 
-template <int WT>
+// NCL: the columns a lane keeps (1 for a one-column launch, else 4)
+template <int WT, int NCL>
 __global__ __launch_bounds__(512) void k_gemv_stream(gemv_args a) {
     extern __shared__ __align__(16) char smem[];
     double (*s_part)[64][4] = (double (*)[64][4]) smem;  // [tile of the batch * nw + wave][lane]
@@ -828,10 +829,10 @@ __global__ __launch_bounds__(512) void k_gemv_stream(gemv_args a) {
 #pragma unroll
         for (int j = 0; j < kStreamTiles; j++) {
             double acc[4] = {0.0, 0.0, 0.0, 0.0};
-            if constexpr (WT == GGML_TYPE_Q4_K) q4k_unit(cur[j].hdr, cur[j].q, af, ad4, ssa, acc);
-            else q8_0_unit(cur[j].q, cur[j].ds, af, ad8, kQ8Group, acc);
+            if constexpr (WT == GGML_TYPE_Q4_K) q4k_unit<NCL>(cur[j].hdr, cur[j].q, af, ad4, ssa, acc);
+            else q8_0_unit<NCL>(cur[j].q, cur[j].ds, af, ad8, kQ8Group, acc);
 #pragma unroll
-            for (int i = 0; i < 4; i++) sp[j * nw + wave][lane][i] = acc[i];
+            for (int i = 0; i < NCL; i++) sp[j * nw + wave][lane][i] = acc[i];
         }
         __syncthreads();
         for (int j = wave; j < kStreamTiles; j += nw) {
@@ -839,13 +840,13 @@ __global__ __launch_bounds__(512) void k_gemv_stream(gemv_args a) {
             if (tile < ntiles) {
                 double v[4];
 #pragma unroll
-                for (int i = 0; i < 4; i++) v[i] = sp[j * nw][lane][i];
+                for (int i = 0; i < NCL; i++) v[i] = sp[j * nw][lane][i];
                 for (int w = 1; w < nw; w++) {
 #pragma unroll
-                    for (int i = 0; i < 4; i++) v[i] += sp[j * nw + w][lane][i];
+                    for (int i = 0; i < NCL; i++) v[i] += sp[j * nw + w][lane][i];
                 }
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
+                for (int i = 0; i < NCL; i++) {
                     const int n = n0 + 4 * g + i;
                     if (n < a.N) *(float *) (a.dst + (int64_t) n * a.dst_nb1 + (tile * 16 + r) * 4) = (float) v[i];
                 }
@@ -1173,17 +1174,24 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
         const int64_t cap = (int64_t) kStreamWgPerCu * n_cu;
         const dim3 grid((unsigned) (batches < cap ? batches : cap), (unsigned) ((N + 15) / 16));
         const size_t lds = 2 * (size_t) kStreamTiles * units * 64 * 4 * sizeof(double);
-        const void * fn = wtype == GGML_TYPE_Q4_K ? (const void *) k_gemv_stream<GGML_TYPE_Q4_K>
-                                                  : (const void *) k_gemv_stream<GGML_TYPE_Q8_0>;
-        static bool raised[2] = {false, false};
-        bool & done = raised[wtype == GGML_TYPE_Q4_K ? 0 : 1];
-        if (lds > 48 * 1024 && !done) {
-            MI_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
-            done = true;
+        const bool one = N == 1;  // one column: a lane keeps one of its four
+        const int which = (wtype == GGML_TYPE_Q4_K ? 0 : 2) + (one ? 1 : 0);
+        const void * fns[4] = {(const void *) k_gemv_stream<GGML_TYPE_Q4_K, 4>,
+                               (const void *) k_gemv_stream<GGML_TYPE_Q4_K, 1>,
+                               (const void *) k_gemv_stream<GGML_TYPE_Q8_0, 4>,
+                               (const void *) k_gemv_stream<GGML_TYPE_Q8_0, 1>};
+        static bool raised[4] = {false, false, false, false};
+        if (lds > 48 * 1024 && !raised[which]) {
+            MI_CHECK(hipFuncSetAttribute(fns[which], hipFuncAttributeMaxDynamicSharedMemorySize, 64 * 1024));
+            raised[which] = true;
         }
-        if (wtype == GGML_TYPE_Q4_K)
-            hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q4_K>), grid, dim3(64 * units), lds, stream, a);
-        else hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q8_0>), grid, dim3(64 * units), lds, stream, a);
+        const dim3 block(64 * units);
+        switch (which) {
+            case 0: hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q4_K, 4>), grid, block, lds, stream, a); break;
+            case 1: hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q4_K, 1>), grid, block, lds, stream, a); break;
+            case 2: hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q8_0, 4>), grid, block, lds, stream, a); break;
+            default: hipLaunchKernelGGL((k_gemv_stream<GGML_TYPE_Q8_0, 1>), grid, block, lds, stream, a); break;
+        }
         return;
     }
     a.cw = gemv_cols(wtype, M, K, N, W2 != nullptr, mode, n_cu);

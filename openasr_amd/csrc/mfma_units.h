@@ -33,7 +33,9 @@ __device__ __forceinline__ void q4k_ssum_operand(const int16_t * col_ss, bool ok
 // correction msum = sum over sub-blocks of min(row) * ssum(column) runs on
 // two f32 MFMAs (16x16x4, sub-blocks g and g + 4 of lane group g): every
 // product is below 2^18 and every partial sum below 2^21, so the f32 result
-// is the exact integer.
+// is the exact integer. NCL: the lane's columns in use (1 when the launch
+// has one column: lanes hold columns 4g + i, so only i = 0 can be live).
+template <int NCL = 4>
 __device__ __forceinline__ void q4k_unit(const uint4 & hdr, const long (&q)[4], const long (&af)[8],
                                          const float (&ad)[4], const float (&ssa)[2], double (&acc)[4]) {
     const int g = (threadIdx.x & 63) >> 4;
@@ -59,12 +61,12 @@ __device__ __forceinline__ void q4k_unit(const uint4 & hdr, const long (&q)[4], 
         const v4i c0v = mfma_i8(af[2 * c], lo, zi);
         const v4i c1v = mfma_i8(af[2 * c + 1], hi, zi);
 #pragma unroll
-        for (int i = 0; i < 4; i++) isum[i] += __mul24(sc[2 * c], c0v[i]) + __mul24(sc[2 * c + 1], c1v[i]);
+        for (int i = 0; i < NCL; i++) isum[i] += __mul24(sc[2 * c], c0v[i]) + __mul24(sc[2 * c + 1], c1v[i]);
     }
     const float dw = half_bits_to_float((uint16_t) (hdr.x & 0xFFFF));
     const float dmw = half_bits_to_float((uint16_t) (hdr.x >> 16));
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < NCL; i++) {
         const double da = (double) ad[i];
         const double d = (double) dw * da;
         const double dmin = (double) dmw * da;
@@ -79,16 +81,19 @@ constexpr int kQ8Group = 8;
 // one Q8_0 block of a 16-row tile against four activation columns per lane:
 // the MFMA's integer sum (|sum| < 2^19) times d_w * d_a (two halves: 22
 // significant bits, exact in f32) is exact in f64, so one fused multiply-add
-// rounds acc + term exactly as the separate product and sum do
+// rounds acc + term exactly as the separate product and sum do (NCL as for
+// q4k_unit)
+template <int NCL = 4>
 __device__ __forceinline__ void q8_0_block(long af, long q, uint16_t ds, const float (&da)[4], double (&acc)[4]) {
     const v4i z = {0, 0, 0, 0};
     const v4i cc = mfma_i8(af, q, z);
     const float dw = half_bits_to_float(ds);
 #pragma unroll
-    for (int i = 0; i < 4; i++) acc[i] = fma((double) cc[i], (double) (dw * da[i]), acc[i]);
+    for (int i = 0; i < NCL; i++) acc[i] = fma((double) cc[i], (double) (dw * da[i]), acc[i]);
 }
 
 // the first nb (<= kQ8Group) blocks of a group, in order
+template <int NCL = 4>
 __device__ __forceinline__ void q8_0_unit(const long (&q)[kQ8Group], const uint16_t (&ds)[kQ8Group],
                                           const long (&af)[kQ8Group], const float4 (&ad)[4][kQ8Group / 4], int nb,
                                           double (&acc)[4]) {
@@ -101,7 +106,7 @@ __device__ __forceinline__ void q8_0_unit(const long (&q)[kQ8Group], const uint1
                 const float4 d4 = ad[i][u / 4];
                 da[i] = (u & 3) == 0 ? d4.x : (u & 3) == 1 ? d4.y : (u & 3) == 2 ? d4.z : d4.w;
             }
-            q8_0_block(af[u], q[u], ds[u], da, acc);
+            q8_0_block<NCL>(af[u], q[u], ds[u], da, acc);
         }
     }
 }
