@@ -94,7 +94,7 @@ __device__ __forceinline__ float unary_apply(int op, float x, const uint16_t * g
             if (x >= 10.0f) return x;
             return half_bits_to_float(gelu_table[float_to_half_bits(x)]);
         }
-        case GGML_UNARY_OP_GELU_ERF: return 0.5f * x * (1.0f + erff_det(x * 0.70710678118654752440f));
+        case GGML_UNARY_OP_GELU_ERF: return gelu_erf_det(x);
         case GGML_UNARY_OP_RELU: return x > 0.0f ? x : 0.0f;
         case GGML_UNARY_OP_TANH: return tanhf(x);
         case GGML_UNARY_OP_SIGMOID: return 1.0f / (1.0f + expf_det(-x));

@@ -157,6 +157,7 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float(gemm_float_args g) {
                 if (g.epi.bias) o = o + g.epi.bias[m];
                 // the residual has the output's layout (contiguous, same batch offsets)
                 if (g.epi.res) o = o + ((const float *) ((const char *) g.epi.res + (dbase - g.d) + n * g.d_nb1))[m];
+                if (g.epi.gelu_erf) o = gelu_erf_det(o);
                 ((float *) (dbase + n * g.d_nb1))[m] = o;
             }
         }

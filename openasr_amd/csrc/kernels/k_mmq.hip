@@ -43,6 +43,7 @@ struct mmq_args {
     char * dst;
     int64_t dst_nb1;
     int64_t col_blocks, tiles, per_xcd;
+    gemm_float_epi epi;  // bias, residual (laid out as dst), GELU_ERF
 };
 
 // the activations of one K slice of the tile's 64 columns
@@ -230,7 +231,13 @@ __global__ __launch_bounds__(256) void k_mmq(mmq_args a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = n0 + grp * 16 + 4 * g + i;
-            if (n < a.N) *(float *) (a.dst + (int64_t) n * a.dst_nb1 + row * 4) = (float) acc[grp][i];
+            if (n < a.N) {
+                float v = (float) acc[grp][i];
+                if (a.epi.bias) v = v + a.epi.bias[row];
+                if (a.epi.res) v = v + *(const float *) ((const char *) a.epi.res + (int64_t) n * a.dst_nb1 + row * 4);
+                if (a.epi.gelu_erf) v = gelu_erf_det(v);
+                *(float *) (a.dst + (int64_t) n * a.dst_nb1 + row * 4) = v;
+            }
         }
     }
 }
@@ -243,9 +250,10 @@ bool mmq_supported(int wtype, int64_t M, int64_t K) {
 }
 
 void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
-                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu) {
+                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const gemm_float_epi & epi) {
     (void) n_cu;
     mmq_args a;
+    a.epi = epi;
     a.W = W;
     a.row_bytes = row_bytes;
     a.M = M;

@@ -141,6 +141,9 @@ __device__ __forceinline__ float erff_det(float x) {
     return (float) (sum * 1.1283791670955125739);
 }
 
+// GELU_ERF (ggml_vec_gelu_erf_f32): 0.5 x (1 + erf(x / sqrt 2)) in f32
+__device__ __forceinline__ float gelu_erf_det(float x) { return 0.5f * x * (1.0f + erff_det(x * 0.70710678118654752440f)); }
+
 __device__ __forceinline__ void sincosf_det(float x, float & s_out, float & c_out) {
     const double xd = (double) x;
     const double k = rint(xd * 0.63661977236758134308);

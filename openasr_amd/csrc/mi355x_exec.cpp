@@ -563,6 +563,47 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 produced = hm;
             }
         }
+        // the tile GEMM: a bias ADD (a row of the output's width), a residual
+        // ADD of the output's shape and a GELU_ERF fold into its epilogue,
+        // with the roundings of the separate ops
+        gemm_float_epi mepi;
+        if (wide && is_contiguous(t)) {
+            auto plain = [](const ggml_tensor * o) { return o->type == GGML_TYPE_F32 && is_contiguous(o); };
+            auto shaped = [&](const ggml_tensor * o) {
+                for (int d = 0; d < 4; d++)
+                    if (o->ne[d] != t->ne[d]) return false;
+                return true;
+            };
+            const ggml_tensor * add = sole_consumer(t, i + 1);
+            if (add && add->op == GGML_OP_ADD && plain(add) && shaped(add)) {
+                const ggml_tensor * o = add->src[0] == t ? add->src[1] : add->src[0];
+                const bool row = o != t && plain(o) && o->ne[0] == t->ne[0] && o->ne[1] * o->ne[2] * o->ne[3] == 1;
+                const bool full = o != t && plain(o) && shaped(o);
+                if (row && ready_before(o, i) && try_fold({add}, add, {o}, nullptr)) {
+                    mepi.bias = (const float *) o->data;
+                    produced = add;
+                } else if (full && ready_before(o, i) && try_fold({add}, add, {o}, o)) {
+                    mepi.res = (const float *) o->data;
+                    produced = add;
+                }
+            }
+            const ggml_tensor * nx = produced != t ? sole_consumer(produced, i + 1) : nullptr;
+            if (mepi.bias && nx && nx->op == GGML_OP_ADD && plain(nx) && shaped(nx)) {
+                const ggml_tensor * r = nx->src[0] == produced ? nx->src[1] : nx->src[0];
+                if (r != produced && plain(r) && shaped(r) && ready_before(r, i) && try_fold({nx}, nx, {r}, r)) {
+                    mepi.res = (const float *) r->data;
+                    produced = nx;
+                }
+            }
+            const ggml_tensor * u = sole_consumer(produced, i + 1);
+            if (u && u->op == GGML_OP_UNARY && u->op_params[0] == GGML_UNARY_OP_GELU_ERF && u->src[0] == produced &&
+                plain(u) && shaped(u) && try_fold({u}, u, {}, nullptr)) {
+                mepi.gelu_erf = true;
+                produced = u;
+            }
+            dst = (char *) produced->data;
+            dst_nb1 = (int64_t) produced->nb[1];
+        }
         // a following residual ADD of the same shape folds into the epilogue
         const char * res = nullptr;
         int64_t res_nb1 = 0;
@@ -671,7 +712,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         add_step(
             [=](hipStream_t s) {
                 act_buffers act = act_carve(wtype, act_base(b), K, N);
-                if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
+                if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, mepi);
                 else if (mfma)
                     launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1, W2,
                                      has_pro ? &pro : nullptr, epi, subs.data(), (int) subs.size());
@@ -727,6 +768,20 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                         produced = add2;
                     }
                 }
+            }
+        }
+        const ggml_tensor * ge = sole_consumer(produced, i + 1);
+        if (ge && ge->op == GGML_OP_UNARY && ge->op_params[0] == GGML_UNARY_OP_GELU_ERF && ge->src[0] == produced &&
+            plain_f32(ge) && is_contiguous(produced)) {
+            bool same = true;
+            for (int d = 0; d < 4 && same; d++) same = ge->ne[d] == t->ne[d];
+            hoist h2 = h;
+            h2.nodes.push_back(ge);
+            h2.writes[0] = span_of(ge);
+            if (same && hoist_ok(i, h2)) {
+                h = h2;
+                epi.gelu_erf = true;
+                produced = ge;
             }
         }
         for (const ggml_tensor * n : h.nodes) deferred[n] = n;

@@ -76,8 +76,9 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
 
 // MFMA int8 GEMM for wider N (prefill)
 bool mmq_supported(int wtype, int64_t M, int64_t K);
+struct gemm_float_epi;
 void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
-                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
+                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const gemm_float_epi & epi);
 
 // float GEMM fallback (f16 / f32 src0)
 void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tview & b, hipStream_t s);
@@ -86,10 +87,12 @@ void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tvi
 // F32, rows contiguous) x src1 b (F32 / F16, rows contiguous) -> d (f32),
 // batch dims broadcast from a as ggml does (r2 = d.ne2 / a.ne2, r3)
 // optional epilogue: out = (acc + bias[row]) + res[row, col] (res laid out as
-// the output), the roundings of MUL_MAT, ADD, ADD apart
+// the output), then GELU_ERF -- the roundings of MUL_MAT, ADD, ADD, GELU_ERF
+// apart
 struct gemm_float_epi {
     const float * bias = nullptr;
     const float * res = nullptr;
+    bool gelu_erf = false;
 };
 struct gemm_float_args {
     gemm_float_epi epi;

@@ -900,6 +900,48 @@ def test_float_mul_mat_bias_residual_epilogue(ggml, gpu, wt, residual):
     G.free()
 
 
+@pytest.mark.parametrize("wname,tail", [("q8_0", "bias_res"), ("q4_K", "bias_res"), ("q8_0", "bias_gelu"),
+                                        ("q4_K", "res"), ("q8_0", "gelu")])
+def test_tile_gemm_epilogue(ggml, gpu, ref, wname, tail):
+    """the quantized tile GEMM (N > 64: prefill, the audio encoder's
+    projections) with what follows it folded into its epilogue -- a bias ADD
+    (a row), a residual ADD (the output's shape), GELU_ERF -- bit for bit the
+    oracle's MUL_MAT and the separate ops' f32 roundings"""
+    wt = {"q8_0": ggml.Q8_0, "q4_K": ggml.Q4_K}[wname]
+    m, k, n = 320, 512, 150
+    wq = ggml.quantize(wt, ggml.synth_normal(5, 1, m * k, 0, 0.05).reshape(m, k))
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    b = RNG.standard_normal(m).astype(np.float32)
+    r = RNG.standard_normal((n, m)).astype(np.float32)
+    G = ggml.Graph()
+    L = G.lib
+    W = G.new(wt, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    B = G.new(ggml.F32, m, weight=True)
+    R = G.new(ggml.F32, m, n)
+    Y = L.ggml_mul_mat(G.ctx, W, X)
+    want = ref.mul_mat(wt, wq, m, k, x)
+    if "bias" in tail:
+        Y = L.ggml_add(G.ctx, Y, B)
+        want = want + b
+    if "res" in tail:
+        Y = L.ggml_add(G.ctx, R, Y)
+        want = r + want
+    if "gelu" in tail:
+        Y = L.ggml_gelu_erf(G.ctx, Y)
+        want = np.vectorize(lambda v: ref.lib().ref_gelu_erf(float(v)), otypes=[np.float32])(want)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    G.set(X, x)
+    if "bias" in tail:
+        G.set(B, b)
+    if "res" in tail:
+        G.set(R, r)
+    assert G.compute(gpu.backend) == 0
+    assert_same_bits(G.get(Y).reshape(n, m), want)
+    G.free()
+
+
 def test_conv_2d_f16_kernel(ggml, gpu, ref):
     """ggml_conv_2d with an f16 kernel (the Qwen audio encoder's conv stem,
     models/qwen/audio_encoder.rs:520-550): f16 columns x f16 kernel rows on
