@@ -29,6 +29,7 @@ namespace mi355x {
 namespace {
 
 constexpr int kGfBM = 64, kGfBN = 64, kGfBK = 32;
+constexpr int kGfDepth = 4;  // slabs in flight in the aligned form (even: slab s is in LDS buffer s % 2)
 constexpr int kGfThreads = 256;
 
 typedef float gf_v4f __attribute__((ext_vector_type(4)));
@@ -63,6 +64,199 @@ __device__ __forceinline__ void gf_load8(const char * row, int64_t k0, int64_t K
 }
 
 }  // namespace
+
+// the wave's 32 x 32 outputs (lane: row wr + 16 i + (lane % 16), columns wc
+// + 16 j + 4 (lane / 16) + v) through the epilogue into dst
+__device__ __forceinline__ void gf_store(const gemm_float_args & g, const gf_v4f (&acc)[2][2], int64_t m0, int64_t n0,
+                                         int wr, int wc, int lane, char * dbase) {
+    const int r16 = lane & 15, cg = lane >> 4;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int64_t m = m0 + wr + 16 * i + r16;
+        if (m >= g.M) continue;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int64_t n = n0 + wc + 16 * j + 4 * cg + v;
+                if (n >= g.N) continue;
+                float o = acc[i][j][v];
+                if (g.epi.bias) o = o + g.epi.bias[m];
+                // the residual has the output's layout (contiguous, same batch offsets)
+                if (g.epi.res) o = o + ((const float *) ((const char *) g.epi.res + (dbase - g.d) + n * g.d_nb1))[m];
+                if (g.epi.gelu_erf) o = gelu_erf_det(o);
+                ((float *) (dbase + n * g.d_nb1))[m] = o;
+            }
+        }
+    }
+}
+
+// one slab's MFMAs from LDS (sa, sb) into the wave's 32 x 32 outputs
+template <bool F16, typename T, int PADE>
+__device__ __forceinline__ void gf_mfma(const T (*sa)[kGfBK + PADE], const T (*sb)[kGfBK + PADE], int wr, int wc,
+                                        int lane, gf_v4f (&acc)[2][2]) {
+    const int r16 = lane & 15, kg = lane >> 4;
+    if constexpr (F16) {
+        // A: column wc + 16 j + r16, k 8 kg .. + 7; B: row wr + 16 i + r16, same k
+        gf_v8h bo[2], ao[2];
+#pragma unroll
+        for (int j = 0; j < 2; j++) bo[j] = *(const gf_v8h *) &sb[wc + 16 * j + r16][8 * kg];
+#pragma unroll
+        for (int i = 0; i < 2; i++) ao[i] = *(const gf_v8h *) &sa[wr + 16 * i + r16][8 * kg];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bo[j], ao[i], acc[i][j], 0, 0, 0);
+    } else {
+#pragma unroll
+        for (int kk = 0; kk < kGfBK; kk += 4) {
+            float bo[2], ao[2];
+#pragma unroll
+            for (int j = 0; j < 2; j++) bo[j] = sb[wc + 16 * j + r16][kk + kg];
+#pragma unroll
+            for (int i = 0; i < 2; i++) ao[i] = sa[wr + 16 * i + r16][kk + kg];
+#pragma unroll
+            for (int i = 0; i < 2; i++)
+#pragma unroll
+                for (int j = 0; j < 2; j++)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bo[j], ao[i], acc[i][j], 0, 0, 0);
+        }
+    }
+}
+
+// eight elements k0 .. k0 + 7 of a 16-byte aligned row of a K % 8 == 0
+// operand, raw (one 16-byte load for f16, two for f32) with whether they are
+// live (inside K and a live row). The load is always made (clamped to the
+// row start) and the mask applied only when the slab is staged: a load
+// behind a branch, or a value used right after its load, would make the step
+// wait for every load in flight.
+struct gf_raw {
+    uint4 r[2];
+    bool ok;
+};
+template <bool T16>
+__device__ __forceinline__ void gf_load_raw(const char * row, int64_t k0, int64_t K, bool live, gf_raw & v) {
+    v.ok = live && k0 < K;
+    const int64_t kc = v.ok ? k0 : 0;
+    if constexpr (T16) {
+        v.r[0] = *(const uint4 *) (row + 2 * kc);
+    } else {
+        v.r[0] = *(const uint4 *) (row + 4 * kc);
+        v.r[1] = *(const uint4 *) (row + 4 * kc + 16);
+    }
+}
+
+// a raw operand piece as eight f16 (T16 source: as is; f32: rounded to
+// nearest even) or eight f32 values, zeros when not live
+template <bool T16>
+__device__ __forceinline__ uint4 gf_as_f16(const gf_raw & v) {
+    if constexpr (T16) return v.ok ? v.r[0] : make_uint4(0, 0, 0, 0);
+    const uint32_t f[8] = {v.r[0].x, v.r[0].y, v.r[0].z, v.r[0].w, v.r[1].x, v.r[1].y, v.r[1].z, v.r[1].w};
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        w[i] = (uint32_t) float_to_half_bits(__uint_as_float(f[2 * i])) |
+               ((uint32_t) float_to_half_bits(__uint_as_float(f[2 * i + 1])) << 16);
+    return v.ok ? make_uint4(w[0], w[1], w[2], w[3]) : make_uint4(0, 0, 0, 0);
+}
+template <bool T16>
+__device__ __forceinline__ void gf_as_f32(const gf_raw & v, uint4 & lo, uint4 & hi) {
+    if constexpr (T16) {
+        const uint32_t u[4] = {v.r[0].x, v.r[0].y, v.r[0].z, v.r[0].w};
+        float f[8];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            f[2 * i] = half_bits_to_float((uint16_t) (u[i] & 0xFFFF));
+            f[2 * i + 1] = half_bits_to_float((uint16_t) (u[i] >> 16));
+        }
+        lo = make_uint4(__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]), __float_as_uint(f[3]));
+        hi = make_uint4(__float_as_uint(f[4]), __float_as_uint(f[5]), __float_as_uint(f[6]), __float_as_uint(f[7]));
+    } else {
+        lo = v.r[0];
+        hi = v.r[1];
+    }
+    if (!v.ok) lo = hi = make_uint4(0, 0, 0, 0);
+}
+
+// a slab's pieces into LDS (sa, sb): f16 operands for an F16 src0 (the
+// columns rounded to f16, as ggml-cpu converts src1 to the weight's
+// vec_dot type), else f32; one or two 16-byte stores a piece (the padded
+// rows stay 16-byte aligned)
+template <bool F16, bool BF16, typename T, int PADE>
+__device__ __forceinline__ void gf_stage_raw(const gf_raw & a, const gf_raw & b, int srow, int sk,
+                                             T (*sa)[kGfBK + PADE], T (*sb)[kGfBK + PADE]) {
+    if constexpr (F16) {
+        *(uint4 *) &sa[srow][sk] = gf_as_f16<true>(a);
+        *(uint4 *) &sb[srow][sk] = gf_as_f16<BF16>(b);
+    } else {
+        uint4 lo, hi;
+        gf_as_f32<false>(a, lo, hi);
+        *(uint4 *) &sa[srow][sk] = lo;
+        *(uint4 *) &sa[srow][sk + 4] = hi;
+        gf_as_f32<BF16>(b, lo, hi);
+        *(uint4 *) &sb[srow][sk] = lo;
+        *(uint4 *) &sb[srow][sk + 4] = hi;
+    }
+}
+
+// The aligned form (16-byte aligned rows of both operands, K % 8 == 0):
+// kGfDepth slabs in flight, slab j in register slot j % kGfDepth from its
+// request until it is staged, and the LDS double-buffered -- step s
+// multiplies slab s (buffer s % 2), stages slab s + 1 into the other buffer
+// and requests slab s + 1 + kGfDepth into the slot it left; one barrier a
+// step (a buffer is staged again only after the barrier that follows every
+// wave's reads of it). Every load is unconditional (past K: clamped, zeros),
+// so each step waits for its own slab only, not for all loads in flight. The
+// steps are padded to a multiple of kGfDepth; the extra slabs are zeros.
+template <bool F16, bool BF16>
+__global__ __launch_bounds__(kGfThreads) void k_gemm_float_v(gemm_float_args g) {
+    constexpr int PADE = F16 ? 8 : 4;
+    using T = typename std::conditional<F16, _Float16, float>::type;
+    __shared__ __align__(16) T sa[2][kGfBM][kGfBK + PADE];
+    __shared__ __align__(16) T sb[2][kGfBN][kGfBK + PADE];
+    const int tid = (int) threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int64_t m0 = (int64_t) blockIdx.x * kGfBM, n0 = (int64_t) blockIdx.y * kGfBN;
+    const int i2 = (int) blockIdx.z % g.ne2, i3 = (int) blockIdx.z / g.ne2;
+    const char * abase = g.a + (int64_t) (i2 / g.r2) * g.a_nb2 + (int64_t) (i3 / g.r3) * g.a_nb3;
+    const char * bbase = g.b + (int64_t) i2 * g.b_nb2 + (int64_t) i3 * g.b_nb3;
+    char * dbase = g.d + (int64_t) i2 * g.d_nb2 + (int64_t) i3 * g.d_nb3;
+    const int srow = tid >> 2, sk = (tid & 3) * 8;
+    const bool a_live = m0 + srow < g.M, b_live = n0 + srow < g.N;
+    const char * arow = abase + (a_live ? m0 + srow : 0) * g.a_nb1;
+    const char * brow = bbase + (b_live ? n0 + srow : 0) * g.b_nb1;
+    const int64_t S = ((g.K + kGfBK - 1) / kGfBK + kGfDepth - 1) / kGfDepth * kGfDepth;
+    gf_raw av[kGfDepth], bv[kGfDepth];
+#pragma unroll
+    for (int p = 0; p < kGfDepth; p++) {
+        gf_load_raw<F16>(arow, (int64_t) p * kGfBK + sk, g.K, a_live, av[p]);
+        gf_load_raw<BF16>(brow, (int64_t) p * kGfBK + sk, g.K, b_live, bv[p]);
+    }
+    gf_stage_raw<F16, BF16, T, PADE>(av[0], bv[0], srow, sk, sa[0], sb[0]);
+    gf_load_raw<F16>(arow, (int64_t) kGfDepth * kGfBK + sk, g.K, a_live, av[0]);
+    gf_load_raw<BF16>(brow, (int64_t) kGfDepth * kGfBK + sk, g.K, b_live, bv[0]);
+    __syncthreads();
+    // wave w: rows (w & 1) * 32 .. + 31, columns (w >> 1) * 32 .. + 31 of the tile
+    const int wr = (wave & 1) * 32, wc = (wave >> 1) * 32;
+    gf_v4f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = gf_v4f{0.f, 0.f, 0.f, 0.f};
+    for (int64_t s0 = 0; s0 < S; s0 += kGfDepth) {
+#pragma unroll
+        for (int p = 0; p < kGfDepth; p++) {
+            const int q = (p + 1) % kGfDepth;
+            gf_mfma<F16, T, PADE>(sa[p & 1], sb[p & 1], wr, wc, lane, acc);
+            gf_stage_raw<F16, BF16, T, PADE>(av[q], bv[q], srow, sk, sa[(p + 1) & 1], sb[(p + 1) & 1]);
+            const int64_t kn = (s0 + p + 1 + kGfDepth) * kGfBK + sk;
+            gf_load_raw<F16>(arow, kn, g.K, a_live, av[q]);
+            gf_load_raw<BF16>(brow, kn, g.K, b_live, bv[q]);
+            __syncthreads();
+        }
+    }
+    gf_store(g, acc, m0, n0, wr, wc, lane, dbase);
+}
 
 // F16 = true: f16 operands (an F16 src0), else f32 operands
 template <bool F16>
@@ -110,58 +304,11 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float(gemm_float_args g) {
             gf_load8(arow, k0 + kGfBK + sk, g.K, g.a_f16, g.a_vec, a_live, av);
             gf_load8(brow, k0 + kGfBK + sk, g.K, g.b_f16, g.b_vec, b_live, bv);
         }
-        const int r16 = lane & 15, kg = lane >> 4;
-        if constexpr (F16) {
-            // A: column wc + 16 j + r16, k 8 kg .. + 7; B: row wr + 16 i + r16, same k
-            gf_v8h bo[2], ao[2];
-#pragma unroll
-            for (int j = 0; j < 2; j++) bo[j] = *(const gf_v8h *) &sb[wc + 16 * j + r16][8 * kg];
-#pragma unroll
-            for (int i = 0; i < 2; i++) ao[i] = *(const gf_v8h *) &sa[wr + 16 * i + r16][8 * kg];
-#pragma unroll
-            for (int i = 0; i < 2; i++)
-#pragma unroll
-                for (int j = 0; j < 2; j++)
-                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(bo[j], ao[i], acc[i][j], 0, 0, 0);
-        } else {
-#pragma unroll
-            for (int kk = 0; kk < kGfBK; kk += 4) {
-                float bo[2], ao[2];
-#pragma unroll
-                for (int j = 0; j < 2; j++) bo[j] = sb[wc + 16 * j + r16][kk + kg];
-#pragma unroll
-                for (int i = 0; i < 2; i++) ao[i] = sa[wr + 16 * i + r16][kk + kg];
-#pragma unroll
-                for (int i = 0; i < 2; i++)
-#pragma unroll
-                    for (int j = 0; j < 2; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bo[j], ao[i], acc[i][j], 0, 0, 0);
-            }
-        }
+        gf_mfma<F16, T, PADE>(sa, sb, wr, wc, lane, acc);
         __syncthreads();
     }
 
-    // lane: row wr + 16 i + (lane % 16), columns wc + 16 j + 4 (lane / 16) + v
-    const int r16 = lane & 15, cg = lane >> 4;
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-        const int64_t m = m0 + wr + 16 * i + r16;
-        if (m >= g.M) continue;
-#pragma unroll
-        for (int j = 0; j < 2; j++) {
-#pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const int64_t n = n0 + wc + 16 * j + 4 * cg + v;
-                if (n >= g.N) continue;
-                float o = acc[i][j][v];
-                if (g.epi.bias) o = o + g.epi.bias[m];
-                // the residual has the output's layout (contiguous, same batch offsets)
-                if (g.epi.res) o = o + ((const float *) ((const char *) g.epi.res + (dbase - g.d) + n * g.d_nb1))[m];
-                if (g.epi.gelu_erf) o = gelu_erf_det(o);
-                ((float *) (dbase + n * g.d_nb1))[m] = o;
-            }
-        }
-    }
+    gf_store(g, acc, m0, n0, wr, wc, lane, dbase);
 }
 
 namespace {
@@ -229,7 +376,12 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
     g.b_vec = ((uintptr_t) b.data | (uintptr_t) b.nb[1] | (uintptr_t) b.nb[2] | (uintptr_t) b.nb[3]) % 16 == 0;
     const dim3 grid((unsigned) ((g.M + kGfBM - 1) / kGfBM), (unsigned) ((g.N + kGfBN - 1) / kGfBN),
                     (unsigned) (g.ne2 * g.ne3));
-    if (g.a_f16) hipLaunchKernelGGL(k_gemm_float<true>, grid, dim3(kGfThreads), 0, s, g);
+    if (g.a_vec && g.b_vec && g.K % 8 == 0) {
+        if (g.a_f16 && g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<true, true>), grid, dim3(kGfThreads), 0, s, g);
+        else if (g.a_f16) hipLaunchKernelGGL((k_gemm_float_v<true, false>), grid, dim3(kGfThreads), 0, s, g);
+        else if (g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<false, true>), grid, dim3(kGfThreads), 0, s, g);
+        else hipLaunchKernelGGL((k_gemm_float_v<false, false>), grid, dim3(kGfThreads), 0, s, g);
+    } else if (g.a_f16) hipLaunchKernelGGL(k_gemm_float<true>, grid, dim3(kGfThreads), 0, s, g);
     else hipLaunchKernelGGL(k_gemm_float<false>, grid, dim3(kGfThreads), 0, s, g);
     note_hip_error(hipGetLastError());
 }
