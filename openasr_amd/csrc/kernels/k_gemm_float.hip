@@ -82,10 +82,16 @@ __device__ __forceinline__ void gf_store(const gemm_float_args & g, const gf_v4f
                 if (n >= g.N) continue;
                 float o = acc[i][j][v];
                 if (g.epi.bias) o = o + g.epi.bias[m];
+                if (g.epi.bias_col) o = o + g.epi.bias_col[n];
                 // the residual has the output's layout (contiguous, same batch offsets)
                 if (g.epi.res) o = o + ((const float *) ((const char *) g.epi.res + (dbase - g.d) + n * g.d_nb1))[m];
                 if (g.epi.gelu_erf) o = gelu_erf_det(o);
-                ((float *) (dbase + n * g.d_nb1))[m] = o;
+                if (g.epi.perm_rows) {
+                    const int64_t pr = g.epi.perm_rows;
+                    ((float *) g.d)[m % pr + pr * n + pr * g.N * (m / pr)] = o;
+                } else {
+                    ((float *) (dbase + n * g.d_nb1))[m] = o;
+                }
             }
         }
     }

@@ -749,6 +749,58 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             h = h2;
             return true;
         };
+        // a convolution's tail (ggml_conv_2d: the column GEMM's result
+        // reshaped to [OW, OH, N, OC], PERMUTE(0, 1, 3, 2), CONT; then maybe
+        // an ADD of one bias value a channel and GELU_ERF): the GEMM writes
+        // the CONT's layout itself and adds the bias and the GELU in its
+        // epilogue, the roundings of the separate ops
+        const ggml_tensor * rs = sole_consumer(t, i + 1);
+        const ggml_tensor * pm = rs && rs->op == GGML_OP_RESHAPE && rs->view_src == t ? sole_consumer(rs, i + 1) : nullptr;
+        const ggml_tensor * ct = pm && pm->op == GGML_OP_PERMUTE && pm->src[0] == rs ? sole_consumer(pm, i + 1) : nullptr;
+        if (ct && ct->op == GGML_OP_CONT && ct->src[0] == pm && plain_f32(t) && plain_f32(ct) && t->ne[2] == 1 &&
+            t->ne[3] == 1) {
+            const int64_t OW = rs->ne[0], OH = rs->ne[1], NB = rs->ne[2], OC = rs->ne[3];
+            const bool perm = OW * OH * NB == t->ne[0] && OC == t->ne[1] && pm->ne[0] == OW && pm->ne[1] == OH &&
+                              pm->ne[2] == OC && pm->ne[3] == NB && pm->nb[0] == 4 && pm->nb[1] == 4 * OW &&
+                              pm->nb[2] == (size_t) t->nb[1] && pm->nb[3] == (size_t) (4 * OW * OH);
+            hoist h2 = h;
+            h2.nodes.push_back(ct);
+            h2.writes[0] = span_of(ct);
+            if (perm && hoist_ok(i, h2)) {
+                h = h2;
+                epi.perm_rows = OW * OH;
+                produced = ct;
+                const ggml_tensor * ad = sole_consumer(ct, i + 1);
+                if (ad && ad->op == GGML_OP_ADD && plain_f32(ad) && ad->src[0] == ct) {
+                    const ggml_tensor * b = ad->src[1];
+                    bool shaped = true;
+                    for (int d = 0; d < 4; d++) shaped = shaped && ad->ne[d] == ct->ne[d];
+                    if (shaped && plain_f32(b) && b->ne[0] == 1 && b->ne[1] == 1 && b->ne[2] == OC && b->ne[3] == 1 &&
+                        ready_before(b, i) && try_fold(ad, b, false)) {
+                        epi.bias_col = (const float *) b->data;
+                        produced = ad;
+                    }
+                }
+                const ggml_tensor * ge = sole_consumer(produced, i + 1);
+                if (ge && ge->op == GGML_OP_UNARY && ge->op_params[0] == GGML_UNARY_OP_GELU_ERF && ge->src[0] == produced &&
+                    plain_f32(ge)) {
+                    hoist h3 = h;
+                    h3.nodes.push_back(ge);
+                    h3.writes[0] = span_of(ge);
+                    if (hoist_ok(i, h3)) {
+                        h = h3;
+                        epi.gelu_erf = true;
+                        produced = ge;
+                    }
+                }
+                for (const ggml_tensor * n : h.nodes) deferred[n] = n;
+                tview ov = dv;
+                ov.data = (char *) produced->data;
+                add_step([=](hipStream_t s) { launch_gemm_float(ov, wv, atype, xv, btype, s, epi); }, produced,
+                         atype == GGML_TYPE_F16 ? "conv_gemm_f16" : "conv_gemm_f32", {produced});
+                return true;
+            }
+        }
         const ggml_tensor * add = sole_consumer(t, i + 1);
         if (add && add->op == GGML_OP_ADD && plain_f32(add) && is_contiguous(t)) {
             const ggml_tensor * o = add->src[0] == t ? add->src[1] : add->src[0];

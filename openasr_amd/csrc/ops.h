@@ -88,11 +88,16 @@ void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tvi
 // batch dims broadcast from a as ggml does (r2 = d.ne2 / a.ne2, r3)
 // optional epilogue: out = (acc + bias[row]) + res[row, col] (res laid out as
 // the output), then GELU_ERF -- the roundings of MUL_MAT, ADD, ADD, GELU_ERF
-// apart
+// apart. A convolution's column GEMM (k_gemm_float only) may instead add a
+// bias of one value a column (bias_col) and write its permuted layout: with
+// perm_rows = P, row m and column n go to element (m % P) + P n + P N (m / P)
+// of a contiguous output (ggml_conv_2d's PERMUTE(0, 1, 3, 2) + CONT)
 struct gemm_float_epi {
     const float * bias = nullptr;
     const float * res = nullptr;
     bool gelu_erf = false;
+    const float * bias_col = nullptr;
+    int64_t perm_rows = 0;
 };
 struct gemm_float_args {
     gemm_float_epi epi;

@@ -968,6 +968,45 @@ def test_conv_2d_f16_kernel(ggml, gpu, ref):
     G.free()
 
 
+@pytest.mark.parametrize("ic,tail", [(1, "bias_gelu"), (16, "bias_gelu"), (16, "bias"), (16, "gelu"), (16, "")])
+def test_conv_2d_tail_in_the_gemm(ggml, gpu, ref, ic, tail):
+    """an f32-kernel ggml_conv_2d followed by the conv stem's bias ADD (one
+    value a channel) and GELU_ERF (models/qwen/audio_encoder.rs:520-552):
+    the column GEMM writes the permuted layout itself with the bias and GELU
+    in its epilogue; against an f64 convolution, then the same f32 bias add
+    and the oracle's GELU_ERF (f32 sums: within 1e-5 of the largest output)"""
+    n, ih, iw, oc = 3, 32, 20, 24
+    x = RNG.standard_normal((n, ic, ih, iw)).astype(np.float32)
+    w = (RNG.standard_normal((oc, ic, 3, 3)) * 0.2).astype(np.float32)
+    b = RNG.standard_normal(oc).astype(np.float32)
+    G = ggml.Graph()
+    Kt = G.new(ggml.F32, 3, 3, ic, oc, weight=True)
+    X = G.new(ggml.F32, iw, ih, ic, n)
+    B = G.new(ggml.F32, 1, 1, oc, weight=True)
+    y = G.lib.ggml_conv_2d(G.ctx, Kt, X, 2, 2, 1, 1, 1, 1)
+    yt = ggml.tensor(y)
+    ow, oh = yt.ne[0], yt.ne[1]
+    if "bias" in tail:
+        y = G.lib.ggml_add(G.ctx, y, B)
+    if "gelu" in tail:
+        y = G.lib.ggml_gelu_erf(G.ctx, y)
+    run(ggml, gpu, G, y)
+    G.set(X, x)
+    G.set(Kt, w)
+    if "bias" in tail:
+        G.set(B, b)
+    assert G.compute(gpu.backend) == 0
+    cols_ref = ref.im2col(x, 3, 3, 2, 2, 1, 1, 1, 1).astype(np.float64)
+    want = (cols_ref @ w.reshape(oc, -1).T.astype(np.float64)).astype(np.float32).transpose(0, 3, 1, 2)
+    if "bias" in tail:
+        want = want + b[None, :, None, None]
+    if "gelu" in tail:
+        want = np.vectorize(lambda v: ref.lib().ref_gelu_erf(float(v)), otypes=[np.float32])(want)
+    got = G.get(y).reshape(n, oc, oh, ow)
+    assert rel_err(got, want) < 1e-5
+    G.free()
+
+
 def test_sinusoidal_position_table(ggml, gpu, ref):
     """the encoders' sinusoidal positions (nn/encoder.rs:575-590): angles =
     MUL_MAT(inverse timescales [1, half], positions [1, T]), SIN and COS of
