@@ -579,22 +579,42 @@ void ref_norm(const float * x, float * y, int64_t ne0, int64_t rows, float eps) 
 float ref_silu(float x) { return x / (1.0f + ref_expf_det(-x)); }
 
 /* erf as a fixed sequence of double operations rounded once: the Maclaurin
- * series 2/sqrt(pi) sum_n (-1)^n x^(2n+1) / (n! (2n+1)), 64 terms, for
- * |x| < 4, +-1 beyond (where erf rounds to +-1 in f32). ggml-cpu's GELU_ERF
- * (ggml_vec_gelu_erf_f32) calls libm erff, which is not reproducible across
- * devices; this sequence is, and it is pinned against math.erf. */
+ * series 2/sqrt(pi) x sum_{n < 64} a_n (x^2)^n with a_n = (-1)^n / (n!
+ * (2n+1)) rounded to the nearest double, evaluated by Horner's rule from n =
+ * 63 down (separate multiply and add), for |x| < 4; +-1 beyond (where erf
+ * rounds to +-1 in f32). ggml-cpu's GELU_ERF (ggml_vec_gelu_erf_f32) calls
+ * libm erff, which is not reproducible across devices; this sequence is, and
+ * it is pinned against math.erf. The device runs the same table and steps. */
+static const double kErfCoef[64] = {
+    0x1.0000000000000p+0, -0x1.5555555555555p-2, 0x1.999999999999ap-4, -0x1.8618618618618p-6,
+    0x1.2f684bda12f68p-8, -0x1.8d3018d3018d3p-11, 0x1.c01c01c01c01cp-14, -0x1.bbd779334ef0bp-17,
+    0x1.87a00187a0018p-20, -0x1.3777c55568ccdp-23, 0x1.c2e3054870b38p-27, -0x1.2b67310aa9f3ap-30,
+    0x1.6f448e13e85e1p-34, -0x1.a289ee7e40f74p-38, 0x1.bd577e658d020p-42, -0x1.bc6250fb14231p-46,
+    0x1.a173a167fba4dp-50, -0x1.7271cbe5863ecp-54, 0x1.377c2110f2083p-58, -0x1.f1b4073b34a68p-63,
+    0x1.7abd72258fb6ep-67, -0x1.13246abce1bddp-71, 0x1.7e6b81382cd42p-76, -0x1.fd6bebd65107ap-81,
+    0x1.45c0a838efe59p-85, -0x1.909c9de3a31c5p-90, 0x1.da7460554e5dbp-95, -0x1.0eef30fa10d2cp-99,
+    0x1.2ac65385f79acp-104, -0x1.3e81bb5701ac5p-109, 0x1.4899fcdef0a8dp-114, -0x1.486eea20c2656p-119,
+    0x1.3e53defc4e233p-124, -0x1.2b778acc3dedfp-129, 0x1.11ae81077a49ep-134, -0x1.e6597092ccbf0p-140,
+    0x1.a47767f2a3c32p-145, -0x1.61f30bc3acd1ap-150, 0x1.22521d98f98a9p-155, -0x1.d05cc9e3507c9p-161,
+    0x1.6a513f56f8a2fp-166, -0x1.13f85fc9e143ep-171, 0x1.9aa19d4d16643p-177, -0x1.2a8fa59ffec31p-182,
+    0x1.a8830736a5123p-188, -0x1.273d8edcec957p-193, 0x1.91ef82b367a95p-199, -0x1.0be5a4cd94283p-204,
+    0x1.5dd4c9219115ap-210, -0x1.bfb10e0f68c50p-216, 0x1.18d952ef00889p-221, -0x1.59982b2e94840p-227,
+    0x1.a13ec00b39f6fp-233, -0x1.ee6cefaa5a158p-239, 0x1.1f9dec94da5f8p-244, -0x1.48a6b3820b441p-250,
+    0x1.70f41ac13e2a1p-256, -0x1.970f1cb2ad53fp-262, 0x1.b97d90d3e603bp-268, -0x1.d6db2a7c68dcbp-274,
+    0x1.edf1e6e4658a9p-280, -0x1.fdcf88bbf71dbp-286, 0x1.02eb04e5f82f5p-291, -0x1.02e2bc1b5790ep-297,
+};
+
+double ref_erf_coef(int n) { return kErfCoef[n]; }
+
 float ref_erff_det(float x) {
     if (x != x) return x;
     const double xd = (double) x;
     if (xd >= 4.0) return 1.0f;
     if (xd <= -4.0) return -1.0f;
-    const double x2 = xd * xd;
-    double term = xd, sum = xd;
-    for (int n = 1; n < 64; n++) {
-        term = term * (-x2) * (1.0 / (double) n);
-        sum = sum + term * (1.0 / (double) (2 * n + 1));
-    }
-    return (float) (sum * 1.1283791670955125739);
+    const double t = xd * xd;
+    double p = kErfCoef[63];
+    for (int n = 62; n >= 0; n--) p = p * t + kErfCoef[n];
+    return (float) (xd * p * 1.1283791670955125739);
 }
 
 /* ggml_vec_gelu_erf_f32: 0.5 x (1 + erf(x / sqrt 2)) in f32 */

@@ -102,6 +102,7 @@ void ref_soft_max_ext(const float * x, const uint16_t * mask, float * y, int64_t
 int32_t ref_argmax_last(const float * x, int64_t n);
 float ref_expf_det(float x);
 float ref_erff_det(float x);
+double ref_erf_coef(int n); /* coefficient a_n (n < 64) of ref_erff_det's series */
 float ref_gelu_erf(float x); /* 0.5 x (1 + erf(x / sqrt 2)), erf by ref_erff_det */
 float ref_relu(float x);
 void ref_sincosf_det(float x, float * s_out, float * c_out);

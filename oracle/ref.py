@@ -55,6 +55,7 @@ def lib() -> C.CDLL:
     s("ref_argmax_first", C.c_int32, vp, i64)
     s("ref_expf_det", f, f)
     s("ref_erff_det", f, f)
+    s("ref_erf_coef", C.c_double, C.c_int)
     s("ref_gelu_erf", f, f)
     s("ref_relu", f, f)
     s("ref_sincosf_det", None, f, vp, vp)

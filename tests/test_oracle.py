@@ -563,10 +563,19 @@ def test_whisper_cross_kv_matches_brute_force(ref):
     w.free()
 
 
+def test_erf_det_coefficients_are_the_series_rounded(ref):
+    """the 64 coefficients of the deterministic erf are the Maclaurin series'
+    (-1)^n / (n! (2n+1)), each the nearest double to the exact rational"""
+    from fractions import Fraction
+    L = ref.lib()
+    for n in range(64):
+        assert L.ref_erf_coef(n) == float(Fraction((-1) ** n, math.factorial(n) * (2 * n + 1))), n
+
+
 def test_erf_det_within_one_ulp_of_math_erf(ref):
-    """the deterministic erf (fixed double series) against math.erf rounded to
-    f32: within one f32 ulp everywhere, equal for the vast majority, odd,
-    saturating to +-1 where erf rounds there"""
+    """the deterministic erf (the series by Horner's rule in double) against
+    math.erf rounded to f32: within one f32 ulp everywhere, equal for the vast
+    majority, odd, saturating to +-1 where erf rounds there"""
     L = ref.lib()
     xs = np.concatenate([np.linspace(-5, 5, 20001), RNG.standard_normal(5000) * 2.0,
                          [0.0, -0.0, 1e-30, 3.9, 3.99, 4.0, -4.0, 1e-8]]).astype(np.float32)
