@@ -19,6 +19,7 @@
 // columns are the MFMA A operand and the weight rows the B operand, so each
 // lane ends with one output row (lane % 16) of four columns, and a store of
 // the tile writes 64-byte runs of consecutive rows.
+#include <algorithm>
 #include <type_traits>
 
 #include "../mi355x_common.h"
@@ -65,10 +66,26 @@ __device__ __forceinline__ void gf_load8(const char * row, int64_t k0, int64_t K
 
 }  // namespace
 
+// the epilogue of output (m, n) with accumulated value o, into dst
+__device__ __forceinline__ void gf_epi_store(const gemm_float_args & g, float o, int64_t m, int64_t n, char * dbase) {
+    if (g.epi.bias) o = o + g.epi.bias[m];
+    if (g.epi.bias_col) o = o + g.epi.bias_col[n];
+    // the residual has the output's layout (contiguous, same batch offsets)
+    if (g.epi.res) o = o + ((const float *) ((const char *) g.epi.res + (dbase - g.d) + n * g.d_nb1))[m];
+    if (g.epi.gelu_erf) o = gelu_erf_det(o);
+    if (g.epi.perm_rows) {
+        const int64_t pr = g.epi.perm_rows;
+        ((float *) g.d)[m % pr + pr * n + pr * g.N * (m / pr)] = o;
+    } else {
+        ((float *) (dbase + n * g.d_nb1))[m] = o;
+    }
+}
+
 // the wave's 32 x 32 outputs (lane: row wr + 16 i + (lane % 16), columns wc
-// + 16 j + 4 (lane / 16) + v) through the epilogue into dst
+// + 16 j + 4 (lane / 16) + v) through the epilogue into dst, or as they are
+// into a split's partials (part: column-major M x N)
 __device__ __forceinline__ void gf_store(const gemm_float_args & g, const gf_v4f (&acc)[2][2], int64_t m0, int64_t n0,
-                                         int wr, int wc, int lane, char * dbase) {
+                                         int wr, int wc, int lane, char * dbase, float * part = nullptr) {
     const int r16 = lane & 15, cg = lane >> 4;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
@@ -80,18 +97,8 @@ __device__ __forceinline__ void gf_store(const gemm_float_args & g, const gf_v4f
             for (int v = 0; v < 4; v++) {
                 const int64_t n = n0 + wc + 16 * j + 4 * cg + v;
                 if (n >= g.N) continue;
-                float o = acc[i][j][v];
-                if (g.epi.bias) o = o + g.epi.bias[m];
-                if (g.epi.bias_col) o = o + g.epi.bias_col[n];
-                // the residual has the output's layout (contiguous, same batch offsets)
-                if (g.epi.res) o = o + ((const float *) ((const char *) g.epi.res + (dbase - g.d) + n * g.d_nb1))[m];
-                if (g.epi.gelu_erf) o = gelu_erf_det(o);
-                if (g.epi.perm_rows) {
-                    const int64_t pr = g.epi.perm_rows;
-                    ((float *) g.d)[m % pr + pr * n + pr * g.N * (m / pr)] = o;
-                } else {
-                    ((float *) (dbase + n * g.d_nb1))[m] = o;
-                }
+                if (part) part[n * g.M + m] = acc[i][j][v];
+                else gf_epi_store(g, acc[i][j][v], m, n, dbase);
             }
         }
     }
@@ -223,24 +230,28 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float_v(gemm_float_args g) 
     const int tid = (int) threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int64_t m0 = (int64_t) blockIdx.x * kGfBM, n0 = (int64_t) blockIdx.y * kGfBN;
-    const int i2 = (int) blockIdx.z % g.ne2, i3 = (int) blockIdx.z / g.ne2;
-    const char * abase = g.a + (int64_t) (i2 / g.r2) * g.a_nb2 + (int64_t) (i3 / g.r3) * g.a_nb3;
-    const char * bbase = g.b + (int64_t) i2 * g.b_nb2 + (int64_t) i3 * g.b_nb3;
+    // split: blockIdx.z is the split (one batch); else the batch
+    const int zb = g.splits > 1 ? 0 : (int) blockIdx.z, ks = g.splits > 1 ? (int) blockIdx.z : 0;
+    const int i2 = zb % g.ne2, i3 = zb / g.ne2;
+    const int64_t kb = (int64_t) ks * g.k_span;
+    const int64_t K = g.splits > 1 ? (g.K - kb < g.k_span ? g.K - kb : g.k_span) : g.K;
+    const char * abase = g.a + (int64_t) (i2 / g.r2) * g.a_nb2 + (int64_t) (i3 / g.r3) * g.a_nb3 + kb * (F16 ? 2 : 4);
+    const char * bbase = g.b + (int64_t) i2 * g.b_nb2 + (int64_t) i3 * g.b_nb3 + kb * (BF16 ? 2 : 4);
     char * dbase = g.d + (int64_t) i2 * g.d_nb2 + (int64_t) i3 * g.d_nb3;
     const int srow = tid >> 2, sk = (tid & 3) * 8;
     const bool a_live = m0 + srow < g.M, b_live = n0 + srow < g.N;
     const char * arow = abase + (a_live ? m0 + srow : 0) * g.a_nb1;
     const char * brow = bbase + (b_live ? n0 + srow : 0) * g.b_nb1;
-    const int64_t S = ((g.K + kGfBK - 1) / kGfBK + kGfDepth - 1) / kGfDepth * kGfDepth;
+    const int64_t S = ((K + kGfBK - 1) / kGfBK + kGfDepth - 1) / kGfDepth * kGfDepth;
     gf_raw av[kGfDepth], bv[kGfDepth];
 #pragma unroll
     for (int p = 0; p < kGfDepth; p++) {
-        gf_load_raw<F16>(arow, (int64_t) p * kGfBK + sk, g.K, a_live, av[p]);
-        gf_load_raw<BF16>(brow, (int64_t) p * kGfBK + sk, g.K, b_live, bv[p]);
+        gf_load_raw<F16>(arow, (int64_t) p * kGfBK + sk, K, a_live, av[p]);
+        gf_load_raw<BF16>(brow, (int64_t) p * kGfBK + sk, K, b_live, bv[p]);
     }
     gf_stage_raw<F16, BF16, T, PADE>(av[0], bv[0], srow, sk, sa[0], sb[0]);
-    gf_load_raw<F16>(arow, (int64_t) kGfDepth * kGfBK + sk, g.K, a_live, av[0]);
-    gf_load_raw<BF16>(brow, (int64_t) kGfDepth * kGfBK + sk, g.K, b_live, bv[0]);
+    gf_load_raw<F16>(arow, (int64_t) kGfDepth * kGfBK + sk, K, a_live, av[0]);
+    gf_load_raw<BF16>(brow, (int64_t) kGfDepth * kGfBK + sk, K, b_live, bv[0]);
     __syncthreads();
     // wave w: rows (w & 1) * 32 .. + 31, columns (w >> 1) * 32 .. + 31 of the tile
     const int wr = (wave & 1) * 32, wc = (wave >> 1) * 32;
@@ -256,12 +267,22 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float_v(gemm_float_args g) 
             gf_mfma<F16, T, PADE>(sa[p & 1], sb[p & 1], wr, wc, lane, acc);
             gf_stage_raw<F16, BF16, T, PADE>(av[q], bv[q], srow, sk, sa[(p + 1) & 1], sb[(p + 1) & 1]);
             const int64_t kn = (s0 + p + 1 + kGfDepth) * kGfBK + sk;
-            gf_load_raw<F16>(arow, kn, g.K, a_live, av[q]);
-            gf_load_raw<BF16>(brow, kn, g.K, b_live, bv[q]);
+            gf_load_raw<F16>(arow, kn, K, a_live, av[q]);
+            gf_load_raw<BF16>(brow, kn, K, b_live, bv[q]);
             __syncthreads();
         }
     }
-    gf_store(g, acc, m0, n0, wr, wc, lane, dbase);
+    gf_store(g, acc, m0, n0, wr, wc, lane, dbase, g.splits > 1 ? g.part + ks * g.M * g.N : nullptr);
+}
+
+// the splits' partials of each output added in split order, then the epilogue
+__global__ __launch_bounds__(256) void k_gemm_float_reduce(gemm_float_args g) {
+    const int64_t total = g.M * g.N;
+    for (int64_t i = (int64_t) blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t) gridDim.x * 256) {
+        float o = g.part[i];
+        for (int s = 1; s < g.splits; s++) o = o + g.part[s * total + i];
+        gf_epi_store(g, o, i % g.M, i / g.M, g.d);
+    }
 }
 
 // F16 = true: f16 operands (an F16 src0), else f32 operands
@@ -342,16 +363,53 @@ bool gemm_float_supported(const tview & d, const tview & a, int atype, const tvi
     return d.ne[0] >= 16 && (n >= 16 || a.ne[0] >= 256) && batches <= 65535 && (n + kGfBN - 1) / kGfBN <= 65535;
 }
 
+namespace {
+
+bool row_aligned(const tview & t) {
+    return ((uintptr_t) t.data | (uintptr_t) t.nb[1] | (uintptr_t) t.nb[2] | (uintptr_t) t.nb[3]) % 16 == 0;
+}
+
+// the product with batches that continue the columns folded into one batch
+void fold_batches(const tview & d, const tview & b, tview & d2, tview & b2) {
+    d2 = d, b2 = b;
+    d2.ne[1] = d.ne[1] * d.ne[2] * d.ne[3];
+    b2.ne[1] = d2.ne[1];
+    d2.ne[2] = d2.ne[3] = b2.ne[2] = b2.ne[3] = 1;
+    d2.nb[2] = d2.nb[3] = d2.nb[1] * d2.ne[1];
+    b2.nb[2] = b2.nb[3] = b2.nb[1] * b2.ne[1];
+}
+
+}  // namespace
+
+// Split K only where the aligned form runs one batch on fewer 64 x 64 tiles
+// than CUs: about two workgroups a CU, each with a whole number of kGfDepth
+// slab groups (the 896 x 390 projections of a 30 s audio encode: 98 tiles,
+// K = 896 in 4 splits, K = 3584 in 6).
+int gemm_float_splits(const tview & d, const tview & a, int atype, const tview & b, int btype, int n_cu) {
+    tview dd = d, bb = b;
+    if (batches_are_columns(d, a, b)) fold_batches(d, b, dd, bb);
+    if (dd.ne[2] * dd.ne[3] != 1) return 1;
+    const int64_t K = a.ne[0];
+    (void) atype, (void) btype;
+    if (!row_aligned(a) || !row_aligned(bb) || K % 8 != 0) return 1;
+    const int64_t tiles = (dd.ne[0] + kGfBM - 1) / kGfBM * ((dd.ne[1] + kGfBN - 1) / kGfBN);
+    const int64_t slabs = (K + kGfBK - 1) / kGfBK;
+    if (tiles >= n_cu || slabs < 2 * kGfDepth) return 1;
+    const int64_t want = (2 * n_cu + tiles - 1) / tiles;
+    const int64_t per = ((slabs + want - 1) / want + kGfDepth - 1) / kGfDepth * kGfDepth;
+    return (int) std::min<int64_t>((slabs + per - 1) / per, 16);
+}
+
+size_t gemm_float_split_bytes(const tview & d, int splits) {
+    return splits > 1 ? (size_t) splits * d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3] * sizeof(float) : 0;
+}
+
 void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
-                       const gemm_float_epi & epi) {
+                       const gemm_float_epi & epi, int splits, float * part) {
     if (batches_are_columns(d, a, b) && d.ne[2] * d.ne[3] > 1) {
-        tview d2 = d, b2 = b;
-        d2.ne[1] = d.ne[1] * d.ne[2] * d.ne[3];
-        b2.ne[1] = d2.ne[1];
-        d2.ne[2] = d2.ne[3] = b2.ne[2] = b2.ne[3] = 1;
-        d2.nb[2] = d2.nb[3] = d2.nb[1] * d2.ne[1];
-        b2.nb[2] = b2.nb[3] = b2.nb[1] * b2.ne[1];
-        launch_gemm_float(d2, a, atype, b2, btype, s, epi);
+        tview d2, b2;
+        fold_batches(d, b, d2, b2);
+        launch_gemm_float(d2, a, atype, b2, btype, s, epi, splits, part);
         return;
     }
     gemm_float_args g{};
@@ -378,15 +436,31 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
     g.r2 = (int) (d.ne[2] / a.ne[2]);
     g.r3 = (int) (d.ne[3] / a.ne[3]);
     // 16-byte vector loads where every row start is 16-byte aligned
-    g.a_vec = ((uintptr_t) a.data | (uintptr_t) a.nb[1] | (uintptr_t) a.nb[2] | (uintptr_t) a.nb[3]) % 16 == 0;
-    g.b_vec = ((uintptr_t) b.data | (uintptr_t) b.nb[1] | (uintptr_t) b.nb[2] | (uintptr_t) b.nb[3]) % 16 == 0;
+    g.a_vec = row_aligned(a);
+    g.b_vec = row_aligned(b);
+    g.splits = 1;
+    g.k_span = g.K;
+    g.part = nullptr;
+    const bool aligned = g.a_vec && g.b_vec && g.K % 8 == 0;
+    if (splits > 1 && part && aligned && g.ne2 * g.ne3 == 1) {
+        // every split but the last takes k_span (whole kGfDepth slab groups)
+        const int64_t slabs = (g.K + kGfBK - 1) / kGfBK;
+        const int64_t per = ((slabs + splits - 1) / splits + kGfDepth - 1) / kGfDepth * kGfDepth;
+        g.k_span = per * kGfBK;
+        g.splits = (int) ((slabs + per - 1) / per);
+        g.part = part;
+    }
     const dim3 grid((unsigned) ((g.M + kGfBM - 1) / kGfBM), (unsigned) ((g.N + kGfBN - 1) / kGfBN),
-                    (unsigned) (g.ne2 * g.ne3));
-    if (g.a_vec && g.b_vec && g.K % 8 == 0) {
+                    (unsigned) (g.splits > 1 ? g.splits : g.ne2 * g.ne3));
+    if (aligned) {
         if (g.a_f16 && g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<true, true>), grid, dim3(kGfThreads), 0, s, g);
         else if (g.a_f16) hipLaunchKernelGGL((k_gemm_float_v<true, false>), grid, dim3(kGfThreads), 0, s, g);
         else if (g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<false, true>), grid, dim3(kGfThreads), 0, s, g);
         else hipLaunchKernelGGL((k_gemm_float_v<false, false>), grid, dim3(kGfThreads), 0, s, g);
+        if (g.splits > 1) {
+            const int64_t blocks = std::min<int64_t>((g.M * g.N + 255) / 256, 4096);
+            hipLaunchKernelGGL(k_gemm_float_reduce, dim3((unsigned) blocks), dim3(256), 0, s, g);
+        }
     } else if (g.a_f16) hipLaunchKernelGGL(k_gemm_float<true>, grid, dim3(kGfThreads), 0, s, g);
     else hipLaunchKernelGGL(k_gemm_float<false>, grid, dim3(kGfThreads), 0, s, g);
     note_hip_error(hipGetLastError());

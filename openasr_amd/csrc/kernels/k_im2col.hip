@@ -1,10 +1,14 @@
 // GGML_OP_IM2COL: the column matrix of a 2-D (or 1-D) convolution, the
 // first half of ggml_conv_2d as the Qwen audio encoder's stem uses it
-// (nn/conv.rs:82-110, cpu_graph.rs:5191-5246). Pure index work: one lane per
-// output element, so the f16/f32 stores of consecutive lanes are contiguous;
-// the input gathers fall in the few rows a workgroup's outputs touch and are
-// served from L2. A tap in the padding is written as zero; an in-range tap is
-// copied (f32) or rounded to nearest-even (f16), bit-identical to ggml-cpu.
+// (nn/conv.rs:82-110, cpu_graph.rs:5191-5246). Pure index work, bound by the
+// column stores: a lane writes V consecutive elements of one column row (one
+// 16-byte f32 or 8-byte f16 store when K % 4 == 0), splitting its first flat
+// index once by multiply-and-shift division and stepping the taps of the
+// rest by carries; the input gathers fall in the few rows a workgroup's
+// outputs touch and are served from L2 (every tap's load is issued, clamped
+// into the image, and a tap in the padding selected to zero). An in-range
+// tap is copied (f32) or rounded to nearest-even (f16), bit-identical to
+// ggml-cpu.
 
 #include "../mi355x_common.h"
 #include "../ops.h"
@@ -12,6 +16,89 @@
 namespace mi355x {
 namespace {
 
+// n / d for n < 2^31: m = ceil(2^(31 + l) / d), l = ceil(log2 d), so that
+// m d - 2^(31 + l) < d <= 2^l and floor(n / d) = floor(n m / 2^(31 + l))
+// (Granlund & Montgomery, "Division by invariant integers using
+// multiplication", 1994, theorem 4.2 with N = 31); n m < 2^64.
+struct fast_div {
+    uint64_t m;
+    uint32_t d;
+    int sh;
+};
+
+fast_div make_fast_div(uint32_t d) {
+    int l = 0;
+    while ((1ull << l) < d) l++;
+    fast_div f;
+    f.d = d;
+    f.sh = 31 + l;
+    f.m = ((1ull << f.sh) + d - 1) / d;
+    return f;
+}
+
+__device__ __forceinline__ uint32_t div_by(uint32_t n, const fast_div & f) {
+    return (uint32_t) (((uint64_t) n * f.m) >> f.sh);
+}
+
+struct im2col_divs {
+    fast_div K, OW, OH, KW, KH;
+};
+
+template <typename DT>
+__device__ __forceinline__ void im2col_store(DT * p, const float (&v)[1]) {
+    *p = (DT) v[0];
+}
+__device__ __forceinline__ void im2col_store(float * p, const float (&v)[4]) {
+    *(float4 *) p = make_float4(v[0], v[1], v[2], v[3]);
+}
+__device__ __forceinline__ void im2col_store(_Float16 * p, const float (&v)[4]) {
+    const uint32_t lo = (uint32_t) float_to_half_bits(v[0]) | ((uint32_t) float_to_half_bits(v[1]) << 16);
+    const uint32_t hi = (uint32_t) float_to_half_bits(v[2]) | ((uint32_t) float_to_half_bits(v[3]) << 16);
+    *(uint2 *) p = make_uint2(lo, hi);
+}
+
+// total < 2^31 and K % V == 0: lane t writes elements V t .. V t + V - 1
+template <typename DT, int V>
+__global__ __launch_bounds__(256) void k_im2col_v(DT * __restrict__ dst, const char * __restrict__ src, im2col_args a,
+                                                  im2col_divs dv) {
+    const uint32_t nt = (uint32_t) (a.total / V);
+    const uint32_t stride = gridDim.x * 256u;
+    for (uint32_t t = blockIdx.x * 256u + threadIdx.x; t < nt; t += stride) {
+        const uint32_t i = t * V;
+        const uint32_t r = div_by(i, dv.K), k = i - r * dv.K.d;
+        const uint32_t r2 = div_by(r, dv.OW), ow = r - r2 * dv.OW.d;
+        const uint32_t n = div_by(r2, dv.OH), oh = r2 - n * dv.OH.d;
+        const uint32_t t2 = div_by(k, dv.KW);
+        int kw = (int) (k - t2 * dv.KW.d);
+        const uint32_t ic0 = div_by(t2, dv.KH);
+        int kh = (int) (t2 - ic0 * dv.KH.d);
+        int64_t ic = ic0;
+        const char * img = src + (int64_t) n * a.nb_n;
+        const int64_t iw0 = (int64_t) ow * a.s0 - a.p0, ih0 = (int64_t) oh * a.s1 - a.p1;
+        float raw[V];
+        bool in[V];
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            const int64_t iw = iw0 + (int64_t) kw * a.d0, ih = ih0 + (int64_t) kh * a.d1;
+            in[e] = iw >= 0 && iw < a.IW && ih >= 0 && ih < a.IH;
+            const int64_t cw = in[e] ? iw : 0, ch = in[e] ? ih : 0;
+            raw[e] = *(const float *) (img + ic * a.nb_c + ch * a.nb_h + cw * 4);
+            if (++kw == a.KW) {
+                kw = 0;
+                if (++kh == a.KH) {
+                    kh = 0;
+                    ic++;
+                }
+            }
+        }
+        float v[V];
+#pragma unroll
+        for (int e = 0; e < V; e++) v[e] = in[e] ? raw[e] : 0.0f;
+        im2col_store(dst + i, v);
+    }
+}
+
+// any size: one lane per element, 64-bit index arithmetic
 template <typename DT>
 __global__ __launch_bounds__(256) void k_im2col(DT * __restrict__ dst, const char * __restrict__ src, im2col_args a) {
     const int64_t stride = (int64_t) gridDim.x * 256;
@@ -35,15 +122,30 @@ __global__ __launch_bounds__(256) void k_im2col(DT * __restrict__ dst, const cha
     }
 }
 
+template <typename DT>
+void im2col_launch(DT * dst, const char * src, const im2col_args & a, hipStream_t s) {
+    constexpr int64_t kMaxBlocks = 65536;
+    if (a.total < (1LL << 31)) {
+        const im2col_divs dv{make_fast_div((uint32_t) a.K), make_fast_div((uint32_t) a.OW),
+                             make_fast_div((uint32_t) a.OH), make_fast_div((uint32_t) a.KW),
+                             make_fast_div((uint32_t) a.KH)};
+        const bool vec = a.K % 4 == 0 && (uintptr_t) dst % (4 * sizeof(DT)) == 0;
+        const int64_t nt = vec ? a.total / 4 : a.total;
+        const dim3 grid((unsigned) std::min<int64_t>((nt + 255) / 256, kMaxBlocks));
+        if (vec) hipLaunchKernelGGL((k_im2col_v<DT, 4>), grid, dim3(256), 0, s, dst, src, a, dv);
+        else hipLaunchKernelGGL((k_im2col_v<DT, 1>), grid, dim3(256), 0, s, dst, src, a, dv);
+    } else {
+        const dim3 grid((unsigned) std::min<int64_t>((a.total + 255) / 256, kMaxBlocks));
+        hipLaunchKernelGGL(k_im2col<DT>, grid, dim3(256), 0, s, dst, src, a);
+    }
+}
+
 }  // namespace
 
 void launch_im2col(void * dst, int dst_f16, const char * src, const im2col_args & a, hipStream_t s) {
     if (a.total <= 0) return;
-    const int64_t g = std::min<int64_t>((a.total + 255) / 256, 16384);
-    if (dst_f16)
-        hipLaunchKernelGGL(k_im2col<_Float16>, dim3((unsigned) g), dim3(256), 0, s, (_Float16 *) dst, src, a);
-    else
-        hipLaunchKernelGGL(k_im2col<float>, dim3((unsigned) g), dim3(256), 0, s, (float *) dst, src, a);
+    if (dst_f16) im2col_launch((_Float16 *) dst, src, a, s);
+    else im2col_launch((float *) dst, src, a, s);
 }
 
 }  // namespace mi355x

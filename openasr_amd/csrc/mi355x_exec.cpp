@@ -796,8 +796,14 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 for (const ggml_tensor * n : h.nodes) deferred[n] = n;
                 tview ov = dv;
                 ov.data = (char *) produced->data;
-                add_step([=](hipStream_t s) { launch_gemm_float(ov, wv, atype, xv, btype, s, epi); }, produced,
-                         atype == GGML_TYPE_F16 ? "conv_gemm_f16" : "conv_gemm_f32", {produced});
+                const int splits = gemm_float_splits(dv, wv, atype, xv, btype, n_cu);
+                gen_need = std::max(gen_need, gemm_float_split_bytes(dv, splits));
+                backend_state * b = be;
+                add_step(
+                    [=](hipStream_t s) {
+                        launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b));
+                    },
+                    produced, atype == GGML_TYPE_F16 ? "conv_gemm_f16" : "conv_gemm_f32", {produced});
                 return true;
             }
         }
@@ -839,8 +845,15 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         for (const ggml_tensor * n : h.nodes) deferred[n] = n;
         tview ov = dv;
         ov.data = (char *) produced->data;
-        add_step([=](hipStream_t s) { launch_gemm_float(ov, wv, atype, xv, btype, s, epi); }, produced,
-                 atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32", {produced});
+        // split K where the tiles leave CUs idle: partials in per-launch scratch
+        const int splits = gemm_float_splits(dv, wv, atype, xv, btype, n_cu);
+        gen_need = std::max(gen_need, gemm_float_split_bytes(dv, splits));
+        backend_state * b = be;
+        add_step(
+            [=](hipStream_t s) {
+                launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b));
+            },
+            produced, atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32", {produced});
         return true;
     }
     if (btype != GGML_TYPE_F32) return fail(t, "f16 columns outside the matrix-core GEMM");

@@ -110,10 +110,21 @@ struct gemm_float_args {
     int64_t M, N, K;
     int ne2, ne3, r2, r3;
     int a_f16, b_f16, a_vec, b_vec;
+    // split K: workgroup z = s sums k in [s k_span, (s + 1) k_span) into
+    // part + s M N (column-major M x N f32), a second launch adds the splits
+    // in order and applies the epilogue
+    int splits;
+    int64_t k_span;
+    float * part;
 };
 bool gemm_float_supported(const tview & d, const tview & a, int atype, const tview & b, int btype);
+// how many K splits a launch of this product takes on n_cu CUs (1: none;
+// more when its 64 x 64 tiles leave CUs idle), and the f32 partials scratch
+// they need
+int gemm_float_splits(const tview & d, const tview & a, int atype, const tview & b, int btype, int n_cu);
+size_t gemm_float_split_bytes(const tview & d, int splits);
 void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
-                       const gemm_float_epi & epi = gemm_float_epi());
+                       const gemm_float_epi & epi = gemm_float_epi(), int splits = 1, float * part = nullptr);
 
 struct fattn_args {
     const char * q;

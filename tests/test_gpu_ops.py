@@ -795,6 +795,8 @@ IM2COL_CASES = [
     (1, 128, 100, 1, 3, 3, 2, 2, 1, 1, 1, 1, True),  # encoder stem conv1 over a 128-bin mel chunk
     (64, 64, 50, 1, 3, 3, 2, 2, 1, 1, 1, 1, True),  # conv2-shaped, fewer channels
     (3, 9, 11, 2, 2, 3, 1, 2, 2, 0, 2, 1, False),  # every parameter different per axis
+    (4, 9, 11, 2, 2, 3, 1, 2, 2, 0, 2, 1, False),  # K % 4 == 0: four-element runs crossing channels
+    (5, 7, 6, 3, 2, 2, 2, 1, 1, 1, 1, 2, True),  # K % 4 == 0, f16 columns, three images
 ]
 
 
@@ -896,6 +898,36 @@ def test_float_mul_mat_bias_residual_epilogue(ggml, gpu, wt, residual):
     want = (xr.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32) + b
     if residual:
         want = want + r
+    assert rel_err(G.get(Y).reshape(n, m), want) < 1e-5
+    G.free()
+
+
+@pytest.mark.parametrize("wt,m,k,n", [("f16", 896, 3584, 390), ("f32", 256, 1000, 100), ("f16", 64, 4096, 16)])
+def test_float_mul_mat_split_k(ggml, gpu, ref, wt, m, k, n):
+    """float MUL_MAT with too few 64 x 64 tiles to fill the CUs (the audio
+    encoder's 896-row projections over 390 positions) splits K over
+    workgroups, a second launch adding the splits in order before the bias
+    ADD and GELU_ERF of the epilogue: within 1e-5 of an f64 product rounded
+    as the graph does (K = 1000 leaves a short last split)"""
+    print(f"float mul_mat split K {wt} M={m} K={k} N={n}", flush=True)
+    wdt = np.float16 if wt == "f16" else np.float32
+    w = (RNG.standard_normal((m, k)) * 0.03).astype(wdt)
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    b = RNG.standard_normal(m).astype(np.float32)
+    G = ggml.Graph()
+    L = G.lib
+    W = G.new(ggml.F16 if wt == "f16" else ggml.F32, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    B = G.new(ggml.F32, m, weight=True)
+    Y = L.ggml_gelu_erf(G.ctx, L.ggml_add(G.ctx, L.ggml_mul_mat(G.ctx, W, X), B))
+    run(ggml, gpu, G, Y)
+    G.set(W, w.view(np.uint16) if wt == "f16" else w)
+    G.set(X, x)
+    G.set(B, b)
+    assert G.compute(gpu.backend) == 0
+    xr = x.astype(np.float16) if wt == "f16" else x
+    pre = (xr.astype(np.float64) @ w.astype(np.float64).T).astype(np.float32) + b
+    want = np.vectorize(lambda v: ref.lib().ref_gelu_erf(float(v)), otypes=[np.float32])(pre)
     assert rel_err(G.get(Y).reshape(n, m), want) < 1e-5
     G.free()
 
