@@ -87,20 +87,59 @@ __device__ __forceinline__ void gf_epi_store(const gemm_float_args & g, float o,
 __device__ __forceinline__ void gf_store(const gemm_float_args & g, const gf_v4f (&acc)[2][2], int64_t m0, int64_t n0,
                                          int wr, int wc, int lane, char * dbase, float * part = nullptr) {
     const int r16 = lane & 15, cg = lane >> 4;
+    if (part || !g.epi.gelu_erf) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int64_t m = m0 + wr + 16 * i + r16;
+            if (m >= g.M) continue;
+#pragma unroll
+            for (int j = 0; j < 2; j++) {
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    const int64_t n = n0 + wc + 16 * j + 4 * cg + v;
+                    if (n >= g.N) continue;
+                    if (part) part[n * g.M + m] = acc[i][j][v];
+                    else gf_epi_store(g, acc[i][j][v], m, n, dbase);
+                }
+            }
+        }
+        return;
+    }
+    // with GELU_ERF: the lane's 16 values through the adds, then the 16
+    // GELUs together (interleaved chains), then the stores
+    gemm_float_epi e2 = g.epi;
+    e2.gelu_erf = false;
+    gemm_float_args g2 = g;
+    g2.epi = e2;
+    float o[16];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const int64_t m = m0 + wr + 16 * i + r16, n = n0 + wc + 16 * j + 4 * cg + v;
+                float x = acc[i][j][v];
+                if (m < g.M && n < g.N) {
+                    if (g.epi.bias) x = x + g.epi.bias[m];
+                    if (g.epi.bias_col) x = x + g.epi.bias_col[n];
+                    if (g.epi.res) x = x + ((const float *) ((const char *) g.epi.res + (dbase - g.d) + n * g.d_nb1))[m];
+                }
+                o[(i * 2 + j) * 4 + v] = x;
+            }
+    gelu_erf_det_n<16>(o);
+    g2.epi.bias = g2.epi.bias_col = g2.epi.res = nullptr;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int64_t m = m0 + wr + 16 * i + r16;
         if (m >= g.M) continue;
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
+        for (int j = 0; j < 2; j++)
 #pragma unroll
             for (int v = 0; v < 4; v++) {
                 const int64_t n = n0 + wc + 16 * j + 4 * cg + v;
-                if (n >= g.N) continue;
-                if (part) part[n * g.M + m] = acc[i][j][v];
-                else gf_epi_store(g, acc[i][j][v], m, n, dbase);
+                if (n < g.N) gf_epi_store(g2, o[(i * 2 + j) * 4 + v], m, n, dbase);
             }
-        }
     }
 }
 

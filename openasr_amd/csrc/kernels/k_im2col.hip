@@ -1,14 +1,19 @@
 // GGML_OP_IM2COL: the column matrix of a 2-D (or 1-D) convolution, the
 // first half of ggml_conv_2d as the Qwen audio encoder's stem uses it
-// (nn/conv.rs:82-110, cpu_graph.rs:5191-5246). Pure index work, bound by the
-// column stores: a lane writes V consecutive elements of one column row (one
-// 16-byte f32 or 8-byte f16 store when K % 4 == 0), splitting its first flat
-// index once by multiply-and-shift division and stepping the taps of the
-// rest by carries; the input gathers fall in the few rows a workgroup's
-// outputs touch and are served from L2 (every tap's load is issued, clamped
-// into the image, and a tap in the padding selected to zero). An in-range
-// tap is copied (f32) or rounded to nearest-even (f16), bit-identical to
-// ggml-cpu.
+// (nn/conv.rs:82-110, cpu_graph.rs:5191-5246). Pure index work, bound by
+// HBM. The line form: a workgroup takes one output line (image n, output row
+// oh: OW column rows) and a block of input channels, reads the KH input rows
+// the line's taps touch for those channels into LDS (consecutive lanes,
+// consecutive input elements) and writes each column row's run of
+// channels x taps (consecutive lanes, consecutive output elements; a 16-byte
+// f32 or 8-byte f16 store of four when the runs allow). The element form
+// (any shape): a lane writes V consecutive elements of one column row,
+// splitting its first flat index once by multiply-and-shift division and
+// stepping the taps by carries. A tap in the padding is written as zero; an
+// in-range tap is copied (f32) or rounded to nearest-even (f16),
+// bit-identical to ggml-cpu.
+
+#include <algorithm>
 
 #include "../mi355x_common.h"
 #include "../ops.h"
@@ -98,6 +103,66 @@ __global__ __launch_bounds__(256) void k_im2col_v(DT * __restrict__ dst, const c
     }
 }
 
+// The line form. Block b: line = b / nblk (n = line / OH, oh = line % OH),
+// channels c0 = (b % nblk) cb .. + cb - 1 (fewer in the last block). LDS:
+// tile[kh][c][iw], zeros for an input row outside the image. Output: row
+// line OW + ow, elements c0 KH KW + j for j < run = cbn KH KW.
+struct im2col_line {
+    int cb, nblk, ic;
+    fast_div run, taps, KW;  // run: cb KH KW (the full block's run); taps: KH KW
+};
+
+template <typename DT, int V>
+__global__ __launch_bounds__(256) void k_im2col_line(DT * __restrict__ dst, const char * __restrict__ src, im2col_args a,
+                                                     im2col_line L) {
+    extern __shared__ float tile[];
+    const int64_t line = blockIdx.x / L.nblk;
+    const int c0 = (int) (blockIdx.x % L.nblk) * L.cb;
+    const int cbn = L.ic - c0 < L.cb ? L.ic - c0 : L.cb;
+    const int64_t n = line / a.OH, oh = line % a.OH;
+    const int IW = (int) a.IW;
+    const char * img = src + n * a.nb_n;
+    // the taps' input rows into LDS
+    for (int e = threadIdx.x; e < a.KH * cbn * IW; e += 256) {
+        const int iw = e % IW, r = e / IW;
+        const int c = r % cbn, kh = r / cbn;
+        const int64_t ih = oh * a.s1 - a.p1 + (int64_t) kh * a.d1;
+        float v = 0.0f;
+        if (ih >= 0 && ih < a.IH) v = *(const float *) (img + (int64_t) (c0 + c) * a.nb_c + ih * a.nb_h + iw * 4);
+        tile[(kh * L.cb + c) * IW + iw] = v;
+    }
+    __syncthreads();
+    const uint32_t run = (uint32_t) cbn * L.taps.d;
+    const uint32_t total = (uint32_t) a.OW * run;
+    DT * out = dst + line * a.OW * a.K + (int64_t) c0 * L.taps.d;
+    for (uint32_t i = threadIdx.x * V; i < total; i += 256 * V) {
+        // run == the full block's run except in the last block: divide by it
+        const uint32_t ow = run == L.run.d ? div_by(i, L.run) : i / run;
+        const uint32_t j = i - ow * run;
+        uint32_t c = div_by(j, L.taps);
+        const uint32_t t = j - c * L.taps.d;
+        const uint32_t khu = div_by(t, L.KW);
+        int kh = (int) khu, kw = (int) (t - khu * L.KW.d);
+        const int64_t iw0 = (int64_t) ow * a.s0 - a.p0;
+        float v[V];
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            const int64_t iw = iw0 + (int64_t) kw * a.d0;
+            const bool in = iw >= 0 && iw < IW;
+            const float x = tile[(kh * L.cb + (int) c) * IW + (in ? (int) iw : 0)];
+            v[e] = in ? x : 0.0f;
+            if (++kw == a.KW) {
+                kw = 0;
+                if (++kh == a.KH) {
+                    kh = 0;
+                    c++;
+                }
+            }
+        }
+        im2col_store(out + (int64_t) ow * a.K + j, v);
+    }
+}
+
 // any size: one lane per element, 64-bit index arithmetic
 template <typename DT>
 __global__ __launch_bounds__(256) void k_im2col(DT * __restrict__ dst, const char * __restrict__ src, im2col_args a) {
@@ -122,9 +187,32 @@ __global__ __launch_bounds__(256) void k_im2col(DT * __restrict__ dst, const cha
     }
 }
 
+constexpr int kLineTileFloats = 8192;  // 32 KB of LDS a workgroup
+
 template <typename DT>
 void im2col_launch(DT * dst, const char * src, const im2col_args & a, hipStream_t s) {
     constexpr int64_t kMaxBlocks = 65536;
+    const int64_t taps = (int64_t) a.KH * a.KW, ic = a.K / taps;
+    const int64_t lines = (a.total / a.K) / a.OW;  // N OH
+    int64_t cb = kLineTileFloats / std::max<int64_t>(1, a.KH * a.IW);
+    if (cb >= 4) cb = cb / 4 * 4;
+    cb = std::min<int64_t>(cb, ic);
+    const int64_t nblk = cb > 0 ? (ic + cb - 1) / cb : 0;
+    if (a.total < (1LL << 31) && cb >= 1 && lines * nblk < (1LL << 31) && a.OW * cb * taps < (1LL << 31)) {
+        im2col_line L;
+        L.cb = (int) cb;
+        L.nblk = (int) nblk;
+        L.ic = (int) ic;
+        L.run = make_fast_div((uint32_t) (cb * taps));
+        L.taps = make_fast_div((uint32_t) taps);
+        L.KW = make_fast_div((uint32_t) a.KW);
+        const bool vec = a.K % 4 == 0 && (cb * taps) % 4 == 0 && (uintptr_t) dst % (4 * sizeof(DT)) == 0;
+        const size_t lds = (size_t) a.KH * cb * a.IW * sizeof(float);
+        const dim3 grid((unsigned) (lines * nblk));
+        if (vec) hipLaunchKernelGGL((k_im2col_line<DT, 4>), grid, dim3(256), lds, s, dst, src, a, L);
+        else hipLaunchKernelGGL((k_im2col_line<DT, 1>), grid, dim3(256), lds, s, dst, src, a, L);
+        return;
+    }
     if (a.total < (1LL << 31)) {
         const im2col_divs dv{make_fast_div((uint32_t) a.K), make_fast_div((uint32_t) a.OW),
                              make_fast_div((uint32_t) a.OH), make_fast_div((uint32_t) a.KW),

@@ -226,18 +226,28 @@ __global__ __launch_bounds__(256) void k_mmq(mmq_args a) {
         if (row_ok) mmq_compute(a, S, w, ks, r, g, acc);
     }
     if (!row_ok) return;
+    // the adds, then (GELU_ERF) the lane's 16 GELUs together, then the stores
+    float o[16];
 #pragma unroll
     for (int grp = 0; grp < 4; grp++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = n0 + grp * 16 + 4 * g + i;
+            float v = (float) acc[grp][i];
             if (n < a.N) {
-                float v = (float) acc[grp][i];
                 if (a.epi.bias) v = v + a.epi.bias[row];
                 if (a.epi.res) v = v + *(const float *) ((const char *) a.epi.res + (int64_t) n * a.dst_nb1 + row * 4);
-                if (a.epi.gelu_erf) v = gelu_erf_det(v);
-                *(float *) (a.dst + (int64_t) n * a.dst_nb1 + row * 4) = v;
             }
+            o[grp * 4 + i] = v;
+        }
+    }
+    if (a.epi.gelu_erf) gelu_erf_det_n<16>(o);
+#pragma unroll
+    for (int grp = 0; grp < 4; grp++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int n = n0 + grp * 16 + 4 * g + i;
+            if (n < a.N) *(float *) (a.dst + (int64_t) n * a.dst_nb1 + row * 4) = o[grp * 4 + i];
         }
     }
 }

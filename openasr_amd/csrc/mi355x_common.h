@@ -162,6 +162,35 @@ __device__ __forceinline__ float erff_det(float x) {
 // GELU_ERF (ggml_vec_gelu_erf_f32): 0.5 x (1 + erf(x / sqrt 2)) in f32
 __device__ __forceinline__ float gelu_erf_det(float x) { return 0.5f * x * (1.0f + erff_det(x * 0.70710678118654752440f)); }
 
+// gelu_erf_det of NV values at once: the same operations per value (so the
+// same bits), the NV Horner chains interleaved step by step so that a lane
+// has NV independent double operations in flight instead of one chain; the
+// series is evaluated for every value and the NaN / |x| >= 4 cases selected
+// after it (their series result is discarded)
+template <int NV>
+__device__ __forceinline__ void gelu_erf_det_n(float (&x)[NV]) {
+    double xd[NV], t[NV], p[NV];
+#pragma unroll
+    for (int e = 0; e < NV; e++) {
+        xd[e] = (double) (x[e] * 0.70710678118654752440f);
+        t[e] = xd[e] * xd[e];
+        p[e] = kErfCoef[63];
+    }
+#pragma unroll
+    for (int n = 62; n >= 0; n--)
+#pragma unroll
+        for (int e = 0; e < NV; e++) p[e] = p[e] * t[e] + kErfCoef[n];
+#pragma unroll
+    for (int e = 0; e < NV; e++) {
+        const float a = x[e] * 0.70710678118654752440f;
+        float er = (float) (xd[e] * p[e] * 1.1283791670955125739);
+        if (xd[e] >= 4.0) er = 1.0f;
+        if (xd[e] <= -4.0) er = -1.0f;
+        if (a != a) er = a;
+        x[e] = 0.5f * x[e] * (1.0f + er);
+    }
+}
+
 __device__ __forceinline__ void sincosf_det(float x, float & s_out, float & c_out) {
     const double xd = (double) x;
     const double k = rint(xd * 0.63661977236758134308);
