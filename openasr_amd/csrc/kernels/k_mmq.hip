@@ -4,7 +4,8 @@
 //
 // A workgroup computes a 64-row x 64-column output tile: each of its four
 // waves owns 16 weight rows and all 64 columns (four 16-column MFMA groups),
-// so every weight fragment a wave loads feeds four column groups. K is walked
+// so every weight fragment a wave loads feeds four column groups; where the
+// 64-column tiles would leave CUs idle, 32-column tiles (two groups). K is walked
 // in 256-element slices. A slice's activations (quants, scales and, for Q4_K,
 // the 32-element sums of the 64 columns) are staged in LDS, double-buffered:
 // right after a slice's barrier the workgroup requests the next slice's
@@ -61,11 +62,11 @@ struct mmq_act {
     uint4 ss;
 };
 
-template <int WT>
+template <int WT, int GRPS>
 __device__ __forceinline__ void mmq_act_load(const mmq_args & a, int n0, int ncol, int64_t ks, mmq_act & r) {
     const int t = (int) threadIdx.x;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < GRPS; u++) {
         const int idx = t + 256 * u, col = idx >> 4, piece = idx & 15;
         const int64_t kk = ks * 256 + piece * 16;
         const bool ok = col < ncol && kk < a.K;
@@ -75,14 +76,14 @@ __device__ __forceinline__ void mmq_act_load(const mmq_args & a, int n0, int nco
     if constexpr (WT == GGML_TYPE_Q4_K) {
         const int64_t nsb = a.K / 256;
         const int col = t < ncol ? t : 0;
-        if (t < kMmqCols) {
+        if (t < 16 * GRPS) {
             r.d[0] = a.ad[(int64_t) (n0 + col) * nsb + ks];
             r.ss = *(const uint4 *) (a.ass + ((int64_t) (n0 + col) * nsb + ks) * 8);
         }
     } else {
         const int64_t nblk = a.K / 32;
         const int col = (t >> 1) < ncol ? (t >> 1) : 0, h = t & 1;
-        if (t < 2 * kMmqCols) {
+        if (t < 32 * GRPS) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int64_t b = ks * 8 + 4 * h + j;
@@ -92,25 +93,25 @@ __device__ __forceinline__ void mmq_act_load(const mmq_args & a, int n0, int nco
     }
 }
 
-template <int WT>
+template <int WT, int GRPS>
 __device__ __forceinline__ void mmq_act_store(const mmq_args & a, int ncol, int64_t ks, const mmq_act & r,
                                               mmq_slice & S) {
     const int t = (int) threadIdx.x;
 #pragma unroll
-    for (int u = 0; u < 4; u++) {
+    for (int u = 0; u < GRPS; u++) {
         const int idx = t + 256 * u, col = idx >> 4, piece = idx & 15;
         const bool ok = col < ncol && ks * 256 + piece * 16 < a.K;
         *(uint4 *) &S.q[col][piece * 16] = ok ? r.q[u] : make_uint4(0, 0, 0, 0);
     }
     if constexpr (WT == GGML_TYPE_Q4_K) {
-        if (t < kMmqCols) {
+        if (t < 16 * GRPS) {
             const bool ok = t < ncol;
             S.d[0][t] = ok ? r.d[0] : 0.0f;
             *(uint4 *) &S.ss[t][0] = ok ? r.ss : make_uint4(0, 0, 0, 0);
         }
     } else {
         const int64_t nblk = a.K / 32;
-        if (t < 2 * kMmqCols) {
+        if (t < 32 * GRPS) {
             const int col = t >> 1, h = t & 1;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
@@ -151,12 +152,13 @@ __device__ __forceinline__ void mmq_w_load(const mmq_args & a, const char * wrow
     }
 }
 
+template <int GRPS>
 __device__ __forceinline__ void mmq_compute(const mmq_args & a, const mmq_slice & S, const mmq_w4 & w, int64_t ks,
                                             int r, int g, double (&acc)[4][4]) {
     (void) a;
     (void) ks;
 #pragma unroll
-    for (int grp = 0; grp < 4; grp++) {
+    for (int grp = 0; grp < GRPS; grp++) {
         const int8_t * acol = &S.q[grp * 16 + r][0];
         long af[8];
 #pragma unroll
@@ -169,6 +171,7 @@ __device__ __forceinline__ void mmq_compute(const mmq_args & a, const mmq_slice 
     }
 }
 
+template <int GRPS>
 __device__ __forceinline__ void mmq_compute(const mmq_args & a, const mmq_slice & S, const mmq_w8 & w, int64_t ks,
                                             int r, int g, double (&acc)[4][4]) {
     const int64_t nblk = a.K / 32;
@@ -179,7 +182,7 @@ __device__ __forceinline__ void mmq_compute(const mmq_args & a, const mmq_slice 
     for (int u = 0; u < kQ8Group; u++) {
         if (u >= nb) break;
 #pragma unroll
-        for (int grp = 0; grp < 4; grp++) {
+        for (int grp = 0; grp < GRPS; grp++) {
             const long af = *(const long *) (&S.q[grp * 16 + r][32 * u + 8 * g]);
             const float4 d4 = *(const float4 *) &S.d[u][grp * 16 + 4 * g];
             const float da[4] = {d4.x, d4.y, d4.z, d4.w};
@@ -188,7 +191,7 @@ __device__ __forceinline__ void mmq_compute(const mmq_args & a, const mmq_slice 
     }
 }
 
-template <int WT>
+template <int WT, int GRPS>
 __global__ __launch_bounds__(256) void k_mmq(mmq_args a) {
     __shared__ __align__(16) mmq_slice s_buf[2];
     using wregs = typename std::conditional<WT == GGML_TYPE_Q4_K, mmq_w4, mmq_w8>::type;
@@ -201,8 +204,8 @@ __global__ __launch_bounds__(256) void k_mmq(mmq_args a) {
     const int r = lane & 15, g = lane >> 4;
     const int64_t row = row_tile * kMmqRows + wave * 16 + r;
     const bool row_ok = row_tile * kMmqRows + wave * 16 < a.M;  // uniform per wave
-    const int n0 = (int) (col_block * kMmqCols);
-    const int ncol = min(kMmqCols, a.N - n0);
+    const int n0 = (int) (col_block * 16 * GRPS);
+    const int ncol = min(16 * GRPS, a.N - n0);
     const int64_t nks = (a.K + 255) / 256;
     const char * wrow = a.W + (row_ok ? row : 0) * a.row_bytes;
     double acc[4][4];
@@ -212,24 +215,24 @@ __global__ __launch_bounds__(256) void k_mmq(mmq_args a) {
         for (int i = 0; i < 4; i++) acc[grp][i] = 0.0;
     mmq_act act;
     wregs wn;
-    mmq_act_load<WT>(a, n0, ncol, 0, act);
+    mmq_act_load<WT, GRPS>(a, n0, ncol, 0, act);
     mmq_w_load(a, wrow, 0, g, wn);
     for (int64_t ks = 0; ks < nks; ks++) {
         mmq_slice & S = s_buf[ks & 1];
-        mmq_act_store<WT>(a, ncol, ks, act, S);
+        mmq_act_store<WT, GRPS>(a, ncol, ks, act, S);
         const wregs w = wn;
         __syncthreads();
         if (ks + 1 < nks) {
-            mmq_act_load<WT>(a, n0, ncol, ks + 1, act);
+            mmq_act_load<WT, GRPS>(a, n0, ncol, ks + 1, act);
             mmq_w_load(a, wrow, ks + 1, g, wn);
         }
-        if (row_ok) mmq_compute(a, S, w, ks, r, g, acc);
+        if (row_ok) mmq_compute<GRPS>(a, S, w, ks, r, g, acc);
     }
     if (!row_ok) return;
-    // the adds, then (GELU_ERF) the lane's 16 GELUs together, then the stores
-    float o[16];
+    // the adds, then (GELU_ERF) the lane's GELUs together, then the stores
+    float o[4 * GRPS];
 #pragma unroll
-    for (int grp = 0; grp < 4; grp++) {
+    for (int grp = 0; grp < GRPS; grp++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = n0 + grp * 16 + 4 * g + i;
@@ -241,9 +244,9 @@ __global__ __launch_bounds__(256) void k_mmq(mmq_args a) {
             o[grp * 4 + i] = v;
         }
     }
-    if (a.epi.gelu_erf) gelu_erf_det_n<16>(o);
+    if (a.epi.gelu_erf) gelu_erf_det_n<4 * GRPS>(o);
 #pragma unroll
-    for (int grp = 0; grp < 4; grp++) {
+    for (int grp = 0; grp < GRPS; grp++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int n = n0 + grp * 16 + 4 * g + i;
@@ -261,7 +264,6 @@ bool mmq_supported(int wtype, int64_t M, int64_t K) {
 
 void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                 int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const gemm_float_epi & epi) {
-    (void) n_cu;
     mmq_args a;
     a.epi = epi;
     a.W = W;
@@ -274,12 +276,22 @@ void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t
     a.N = (int) N;
     a.dst = dst;
     a.dst_nb1 = dst_nb1;
-    a.col_blocks = (N + kMmqCols - 1) / kMmqCols;
-    a.tiles = ((M + kMmqRows - 1) / kMmqRows) * a.col_blocks;
+    // 32-column tiles where 64-column tiles leave CUs idle (the audio
+    // encoder's 896-row projections over 390 positions: 98 -> 182 tiles)
+    const int64_t row_tiles = (M + kMmqRows - 1) / kMmqRows;
+    const bool narrow = N > 32 && row_tiles * ((N + kMmqCols - 1) / kMmqCols) < n_cu;
+    const int cols = narrow ? 32 : kMmqCols;
+    a.col_blocks = (N + cols - 1) / cols;
+    a.tiles = row_tiles * a.col_blocks;
     a.per_xcd = (a.tiles + kMmqXcds - 1) / kMmqXcds;
     const dim3 grid((unsigned) (a.per_xcd * kMmqXcds));
-    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_mmq<GGML_TYPE_Q4_K>, grid, dim3(256), 0, stream, a);
-    else hipLaunchKernelGGL(k_mmq<GGML_TYPE_Q8_0>, grid, dim3(256), 0, stream, a);
+    if (wtype == GGML_TYPE_Q4_K) {
+        if (narrow) hipLaunchKernelGGL((k_mmq<GGML_TYPE_Q4_K, 2>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((k_mmq<GGML_TYPE_Q4_K, 4>), grid, dim3(256), 0, stream, a);
+    } else {
+        if (narrow) hipLaunchKernelGGL((k_mmq<GGML_TYPE_Q8_0, 2>), grid, dim3(256), 0, stream, a);
+        else hipLaunchKernelGGL((k_mmq<GGML_TYPE_Q8_0, 4>), grid, dim3(256), 0, stream, a);
+    }
 }
 
 }  // namespace mi355x
