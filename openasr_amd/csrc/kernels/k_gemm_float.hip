@@ -268,7 +268,32 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float_v(gemm_float_args g) 
     __shared__ __align__(16) T sb[2][kGfBN][kGfBK + PADE];
     const int tid = (int) threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int64_t m0 = (int64_t) blockIdx.x * kGfBM, n0 = (int64_t) blockIdx.y * kGfBN;
+    int64_t m0 = (int64_t) blockIdx.x * kGfBM;
+    const int64_t n0 = (int64_t) blockIdx.y * kGfBN;
+    // sibling products: this tile's product (rows, weights, output, bias)
+    // (selects with constant indices: an index into the argument arrays
+    // would put the arguments in scratch memory)
+    static_assert(kGemmFloatMaxSubs == 2, "product selection below");
+    if (g.nsub > 0) {
+        int64_t base = 0, mend = g.sub_m0[1];
+        const char * sa = g.sub_a[0];
+        char * sd = g.sub_d[0];
+        const float * sbias = g.sub_bias[0];
+        if (m0 >= g.sub_m0[1]) {
+            base = g.sub_m0[1], mend = g.sub_m0[2];
+            sa = g.sub_a[1], sd = g.sub_d[1], sbias = g.sub_bias[1];
+        }
+        if (g.nsub >= 2 && m0 >= g.sub_m0[2]) {
+            base = g.sub_m0[2], mend = g.sub_m0[3];
+            sa = g.sub_a[2], sd = g.sub_d[2], sbias = g.sub_bias[2];
+        }
+        m0 -= base;
+        g.M = mend - base;
+        g.a = sa;
+        g.d = sd;
+        g.d_nb1 = g.M * 4;  // each product's output is contiguous
+        g.epi.bias = sbias;
+    }
     // split: blockIdx.z is the split (one batch); else the batch
     const int zb = g.splits > 1 ? 0 : (int) blockIdx.z, ks = g.splits > 1 ? (int) blockIdx.z : 0;
     const int i2 = zb % g.ne2, i3 = zb / g.ne2;
@@ -439,16 +464,21 @@ int gemm_float_splits(const tview & d, const tview & a, int atype, const tview &
     return (int) std::min<int64_t>((slabs + per - 1) / per, 16);
 }
 
+bool gemm_float_siblings_ok(const tview & d, const tview & a, const tview & b) {
+    return d.ne[2] * d.ne[3] == 1 && a.ne[2] * a.ne[3] == 1 && row_aligned(a) && row_aligned(b) && a.ne[0] % 8 == 0 &&
+           d.ne[0] % kGfBM == 0;
+}
+
 size_t gemm_float_split_bytes(const tview & d, int splits) {
     return splits > 1 ? (size_t) splits * d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3] * sizeof(float) : 0;
 }
 
 void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
-                       const gemm_float_epi & epi, int splits, float * part) {
+                       const gemm_float_epi & epi, int splits, float * part, const gemm_float_sub * subs, int nsub) {
     if (batches_are_columns(d, a, b) && d.ne[2] * d.ne[3] > 1) {
         tview d2, b2;
         fold_batches(d, b, d2, b2);
-        launch_gemm_float(d2, a, atype, b2, btype, s, epi, splits, part);
+        launch_gemm_float(d2, a, atype, b2, btype, s, epi, splits, part, subs, nsub);
         return;
     }
     gemm_float_args g{};
@@ -480,7 +510,42 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
     g.splits = 1;
     g.k_span = g.K;
     g.part = nullptr;
+    g.nsub = 0;
     const bool aligned = g.a_vec && g.b_vec && g.K % 8 == 0;
+    int64_t m_all = g.M;
+    if (nsub > 0 && aligned && g.ne2 * g.ne3 == 1 && g.M % kGfBM == 0 && nsub <= kGemmFloatMaxSubs) {
+        // sibling products: their row ranges follow the first product's
+        g.nsub = nsub;
+        g.sub_m0[0] = 0;
+        g.sub_a[0] = g.a;
+        g.sub_d[0] = g.d;
+        g.sub_bias[0] = epi.bias;
+        for (int i = 0; i < nsub; i++) {
+            g.sub_m0[i + 1] = m_all;
+            g.sub_a[i + 1] = subs[i].a;
+            g.sub_d[i + 1] = subs[i].d;
+            g.sub_bias[i + 1] = subs[i].bias;
+            m_all += subs[i].M;
+        }
+        g.sub_m0[nsub + 1] = m_all;
+        splits = 1;
+    } else if (nsub > 0) {
+        // not joinable here: each product on its own
+        launch_gemm_float(d, a, atype, b, btype, s, epi, splits, part);
+        for (int i = 0; i < nsub; i++) {
+            tview ai = a, di = d;
+            ai.data = (char *) subs[i].a;
+            ai.ne[1] = subs[i].M;
+            di.data = subs[i].d;
+            di.ne[0] = subs[i].M;
+            di.nb[1] = di.nb[0] * subs[i].M;
+            di.nb[2] = di.nb[3] = di.nb[1] * di.ne[1];
+            gemm_float_epi ei;
+            ei.bias = subs[i].bias;
+            launch_gemm_float(di, ai, atype, b, btype, s, ei);
+        }
+        return;
+    }
     if (splits > 1 && part && aligned && g.ne2 * g.ne3 == 1) {
         // every split but the last takes k_span (whole kGfDepth slab groups)
         const int64_t slabs = (g.K + kGfBK - 1) / kGfBK;
@@ -489,7 +554,7 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
         g.splits = (int) ((slabs + per - 1) / per);
         g.part = part;
     }
-    const dim3 grid((unsigned) ((g.M + kGfBM - 1) / kGfBM), (unsigned) ((g.N + kGfBN - 1) / kGfBN),
+    const dim3 grid((unsigned) ((m_all + kGfBM - 1) / kGfBM), (unsigned) ((g.N + kGfBN - 1) / kGfBN),
                     (unsigned) (g.splits > 1 ? g.splits : g.ne2 * g.ne3));
     if (aligned) {
         if (g.a_f16 && g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<true, true>), grid, dim3(kGfThreads), 0, s, g);

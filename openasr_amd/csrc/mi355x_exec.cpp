@@ -842,18 +842,73 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 produced = ge;
             }
         }
+        // sibling MUL_MATs of the same columns (an encoder block's q, k, v
+        // projections, each maybe with a bias ADD) join the launch as further
+        // row ranges; each is taken only if the launch with it passes hoist_ok
+        std::vector<gemm_float_sub> subs;
+        std::vector<const ggml_tensor *> sub_outs;
+        if (!epi.res && !epi.gelu_erf && gemm_float_siblings_ok(dv, wv, xv) && is_contiguous(t)) {
+            for (int j = i + 1; j < cg->n_nodes && j <= i + 16 && (int) subs.size() < kGemmFloatMaxSubs; j++) {
+                const ggml_tensor * u = cg->nodes[j];
+                if (is_view_op(u->op) || deferred.count(u)) continue;
+                const ggml_tensor * uw = u->src[0];
+                const bool sibling = u->op == GGML_OP_MUL_MAT && u->src[1] == x && uw->type == w->type &&
+                                     uw->ne[0] == w->ne[0] && uw->ne[2] == 1 && uw->ne[3] == 1 &&
+                                     uw->nb[1] == w->nb[1] && uw->nb[0] == w->nb[0] && uw->ne[1] % 64 == 0 &&
+                                     u->type == GGML_TYPE_F32 && is_contiguous(u) && u->ne[1] == t->ne[1] &&
+                                     u->ne[2] == 1 && u->ne[3] == 1 && ready_before(uw, i);
+                if (!sibling) continue;
+                gemm_float_sub sb;
+                sb.a = (const char *) uw->data;
+                sb.M = uw->ne[1];
+                sb.d = (char *) u->data;
+                hoist h2 = h;
+                h2.nodes.push_back(u);
+                h2.reads.push_back(span_of(uw));
+                const ggml_tensor * out = u;
+                const ggml_tensor * ua = sole_consumer(u, j + 1);
+                if (ua && ua->op == GGML_OP_ADD && plain_f32(ua)) {
+                    const ggml_tensor * o = ua->src[0] == u ? ua->src[1] : ua->src[0];
+                    bool same = o != u;
+                    for (int d = 0; d < 4 && same; d++) same = ua->ne[d] == u->ne[d];
+                    const bool row = same && plain_f32(o) && o->ne[0] == u->ne[0] && o->ne[1] * o->ne[2] * o->ne[3] == 1;
+                    if (row && ready_before(o, i)) {
+                        hoist h3 = h2;
+                        h3.nodes.push_back(ua);
+                        h3.reads.push_back(span_of(o));
+                        h3.writes.push_back(span_of(ua));
+                        if (hoist_ok(i, h3)) {
+                            sb.bias = (const float *) o->data;
+                            sb.d = (char *) ua->data;
+                            out = ua;
+                            h2 = h3;
+                        }
+                    }
+                }
+                if (out == u) {
+                    h2.writes.push_back(span_of(u));
+                    if (!hoist_ok(i, h2)) break;
+                }
+                h = h2;
+                subs.push_back(sb);
+                sub_outs.push_back(out);
+            }
+        }
         for (const ggml_tensor * n : h.nodes) deferred[n] = n;
         tview ov = dv;
         ov.data = (char *) produced->data;
         // split K where the tiles leave CUs idle: partials in per-launch scratch
-        const int splits = gemm_float_splits(dv, wv, atype, xv, btype, n_cu);
+        const int splits = subs.empty() ? gemm_float_splits(dv, wv, atype, xv, btype, n_cu) : 1;
         gen_need = std::max(gen_need, gemm_float_split_bytes(dv, splits));
         backend_state * b = be;
+        std::vector<const ggml_tensor *> outs = {produced};
+        outs.insert(outs.end(), sub_outs.begin(), sub_outs.end());
         add_step(
             [=](hipStream_t s) {
-                launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b));
+                launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b),
+                                  subs.empty() ? nullptr : subs.data(), (int) subs.size());
             },
-            produced, atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32", {produced});
+            produced, atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32", outs);
         return true;
     }
     if (btype != GGML_TYPE_F32) return fail(t, "f16 columns outside the matrix-core GEMM");

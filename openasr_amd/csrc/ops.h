@@ -99,6 +99,7 @@ struct gemm_float_epi {
     const float * bias_col = nullptr;
     int64_t perm_rows = 0;
 };
+constexpr int kGemmFloatMaxSubs = 2;
 struct gemm_float_args {
     gemm_float_epi epi;
     const char * a;
@@ -116,6 +117,24 @@ struct gemm_float_args {
     int splits;
     int64_t k_span;
     float * part;
+    // sibling products of the same columns in one launch (aligned form, no
+    // split): rows [sub_m0[i], sub_m0[i + 1]) of the launch are product i,
+    // with weights sub_a[i], contiguous output sub_d[i] and bias sub_bias[i]
+    // (product 0 is a / d / epi.bias); every sub_m0 is a multiple of 64
+    int nsub;
+    int64_t sub_m0[kGemmFloatMaxSubs + 2];
+    const char * sub_a[kGemmFloatMaxSubs + 1];
+    char * sub_d[kGemmFloatMaxSubs + 1];
+    const float * sub_bias[kGemmFloatMaxSubs + 1];
+};
+// a further product of a sibling launch: weights a (same type, K and row
+// stride as the first), output d (f32, contiguous, the first's column count),
+// optional bias of one value a row
+struct gemm_float_sub {
+    const char * a = nullptr;
+    int64_t M = 0;
+    char * d = nullptr;
+    const float * bias = nullptr;
 };
 bool gemm_float_supported(const tview & d, const tview & a, int atype, const tview & b, int btype);
 // how many K splits a launch of this product takes on n_cu CUs (1: none;
@@ -124,7 +143,11 @@ bool gemm_float_supported(const tview & d, const tview & a, int atype, const tvi
 int gemm_float_splits(const tview & d, const tview & a, int atype, const tview & b, int btype, int n_cu);
 size_t gemm_float_split_bytes(const tview & d, int splits);
 void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
-                       const gemm_float_epi & epi = gemm_float_epi(), int splits = 1, float * part = nullptr);
+                       const gemm_float_epi & epi = gemm_float_epi(), int splits = 1, float * part = nullptr,
+                       const gemm_float_sub * subs = nullptr, int nsub = 0);
+// whether sibling products can join a launch of this product (aligned rows,
+// K % 8 == 0, one batch, M a multiple of 64)
+bool gemm_float_siblings_ok(const tview & d, const tview & a, const tview & b);
 
 struct fattn_args {
     const char * q;

@@ -642,6 +642,43 @@ def test_single_column_sibling_projections(ggml, gpu, ref):
     G.free()
 
 
+@pytest.mark.parametrize("wt", ["f16", "f32"])
+def test_float_sibling_projections(ggml, gpu, wt):
+    """three float MUL_MATs of the same columns (an encoder block's q, k, v
+    projections over 390 positions; q and v with a bias ADD, k without, row
+    counts 128 / 192 / 64): one matrix-core launch, each product within 1e-5
+    of an f64 product rounded as the graph does"""
+    k, n, ms = 256, 390, (128, 192, 64)
+    wdt = np.float16 if wt == "f16" else np.float32
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    ws = [(RNG.standard_normal((m, k)) * 0.05).astype(wdt) for m in ms]
+    bq = RNG.standard_normal(ms[0]).astype(np.float32)
+    bv = RNG.standard_normal(ms[2]).astype(np.float32)
+    G = ggml.Graph()
+    L = G.lib
+    X = G.new(ggml.F32, k, n)
+    Ws = [G.new(ggml.F16 if wt == "f16" else ggml.F32, k, m, weight=True) for m in ms]
+    BQ, BV = G.new(ggml.F32, ms[0], weight=True), G.new(ggml.F32, ms[2], weight=True)
+    Q = L.ggml_add(G.ctx, L.ggml_mul_mat(G.ctx, Ws[0], X), BQ)
+    Kt = L.ggml_mul_mat(G.ctx, Ws[1], X)
+    V = L.ggml_add(G.ctx, L.ggml_mul_mat(G.ctx, Ws[2], X), BV)
+    G.build(Q, Kt, V)
+    G.allocate(gpu.buft)
+    for T, v in ((X, x), (BQ, bq), (BV, bv)):
+        G.set(T, v)
+    for T, w in zip(Ws, ws):
+        G.set(T, w.view(np.uint16) if wt == "f16" else w)
+    assert G.compute(gpu.backend) == 0
+    xr = (x.astype(np.float16) if wt == "f16" else x).astype(np.float64)
+    want = [(xr @ w.astype(np.float64).T).astype(np.float32) for w in ws]
+    assert rel_err(G.get(Q).reshape(n, ms[0]), want[0] + bq) < 1e-5
+    assert rel_err(G.get(Kt).reshape(n, ms[1]), want[1]) < 1e-5
+    assert rel_err(G.get(V).reshape(n, ms[2]), want[2] + bv) < 1e-5
+    labels = [lab.split(":")[0] for lab, _ in gpu.profile(G.gf, 1)]
+    assert sum(lab.startswith("mul_mat") for lab in labels) == 1 and "binary" not in labels, labels
+    G.free()
+
+
 def test_silu_mul_and_gelu(ggml, gpu, ref):
     g = RNG.standard_normal((4, 3072)).astype(np.float32) * 3
     u = RNG.standard_normal((4, 3072)).astype(np.float32)
