@@ -45,6 +45,13 @@ struct mmq_args {
     int64_t dst_nb1;
     int64_t col_blocks, tiles, per_xcd;
     gemm_float_epi epi;  // bias, residual (laid out as dst), GELU_ERF
+    // sibling products of the same activations (rows [sub_m0[i],
+    // sub_m0[i + 1]) are product i: weights, contiguous output, bias)
+    int nsub;
+    int64_t sub_m0[kGemmFloatMaxSubs + 2];
+    const char * sub_W[kGemmFloatMaxSubs + 1];
+    char * sub_dst[kGemmFloatMaxSubs + 1];
+    const float * sub_bias[kGemmFloatMaxSubs + 1];
 };
 
 // the activations of one K slice of the tile's 64 columns
@@ -199,7 +206,32 @@ __global__ __launch_bounds__(256) void k_mmq(mmq_args a) {
     const int64_t id = blockIdx.x;
     const int64_t t = (id % kMmqXcds) * a.per_xcd + id / kMmqXcds;
     if (t >= a.tiles) return;  // before any barrier: the whole workgroup leaves
-    const int64_t row_tile = t / a.col_blocks, col_block = t % a.col_blocks;
+    int64_t row_tile = t / a.col_blocks;
+    const int64_t col_block = t % a.col_blocks;
+    // sibling products: this tile's product, selected with constant indices
+    // (an index into the argument arrays would put them in scratch memory)
+    static_assert(kGemmFloatMaxSubs == 2, "product selection below");
+    if (a.nsub > 0) {
+        const int64_t r0 = row_tile * kMmqRows;
+        int64_t base = 0, mend = a.sub_m0[1];
+        const char * sw = a.sub_W[0];
+        char * sd = a.sub_dst[0];
+        const float * sb = a.sub_bias[0];
+        if (r0 >= a.sub_m0[1]) {
+            base = a.sub_m0[1], mend = a.sub_m0[2];
+            sw = a.sub_W[1], sd = a.sub_dst[1], sb = a.sub_bias[1];
+        }
+        if (a.nsub >= 2 && r0 >= a.sub_m0[2]) {
+            base = a.sub_m0[2], mend = a.sub_m0[3];
+            sw = a.sub_W[2], sd = a.sub_dst[2], sb = a.sub_bias[2];
+        }
+        row_tile -= base / kMmqRows;
+        a.M = mend - base;
+        a.W = sw;
+        a.dst = sd;
+        a.dst_nb1 = a.M * 4;  // each product's output is contiguous
+        a.epi.bias = sb;
+    }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r = lane & 15, g = lane >> 4;
     const int64_t row = row_tile * kMmqRows + wave * 16 + r;
@@ -263,8 +295,35 @@ bool mmq_supported(int wtype, int64_t M, int64_t K) {
 }
 
 void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
-                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const gemm_float_epi & epi) {
+                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const gemm_float_epi & epi,
+                const gemm_float_sub * subs, int nsub) {
     mmq_args a;
+    a.nsub = 0;
+    int64_t m_all = M;
+    if (nsub > 0 && nsub <= kGemmFloatMaxSubs && M % kMmqRows == 0 && !epi.res && !epi.gelu_erf) {
+        a.nsub = nsub;
+        a.sub_m0[0] = 0;
+        a.sub_W[0] = W;
+        a.sub_dst[0] = dst;
+        a.sub_bias[0] = epi.bias;
+        for (int i = 0; i < nsub; i++) {
+            a.sub_m0[i + 1] = m_all;
+            a.sub_W[i + 1] = subs[i].a;
+            a.sub_dst[i + 1] = subs[i].d;
+            a.sub_bias[i + 1] = subs[i].bias;
+            m_all += subs[i].M;
+        }
+        a.sub_m0[nsub + 1] = m_all;
+    } else if (nsub > 0) {
+        // not joinable: each product on its own
+        launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, stream, n_cu, epi);
+        for (int i = 0; i < nsub; i++) {
+            gemm_float_epi ei;
+            ei.bias = subs[i].bias;
+            launch_mmq(wtype, subs[i].a, row_bytes, subs[i].M, K, act, N, subs[i].d, subs[i].M * 4, stream, n_cu, ei);
+        }
+        return;
+    }
     a.epi = epi;
     a.W = W;
     a.row_bytes = row_bytes;
@@ -278,7 +337,7 @@ void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t
     a.dst_nb1 = dst_nb1;
     // 32-column tiles where 64-column tiles leave CUs idle (the audio
     // encoder's 896-row projections over 390 positions: 98 -> 182 tiles)
-    const int64_t row_tiles = (M + kMmqRows - 1) / kMmqRows;
+    const int64_t row_tiles = (m_all + kMmqRows - 1) / kMmqRows;
     const bool narrow = N > 32 && row_tiles * ((N + kMmqCols - 1) / kMmqCols) < n_cu;
     const int cols = narrow ? 32 : kMmqCols;
     a.col_blocks = (N + cols - 1) / cols;

@@ -604,6 +604,60 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             dst = (char *) produced->data;
             dst_nb1 = (int64_t) produced->nb[1];
         }
+        // sibling MUL_MATs of the same activations (an encoder block's q, k, v
+        // projections, each maybe with a bias ADD) join the tile GEMM launch
+        // as further row ranges; each is taken only if the launch with it
+        // passes hoist_ok
+        std::vector<gemm_float_sub> msubs;
+        std::vector<const ggml_tensor *> msub_outs;
+        if (wide && is_contiguous(t) && !mepi.res && !mepi.gelu_erf && M % 64 == 0 && N == t->ne[1]) {
+            for (int j = i + 1; j < cg->n_nodes && j <= i + 16 && (int) msubs.size() < kGemmFloatMaxSubs; j++) {
+                const ggml_tensor * u = cg->nodes[j];
+                if (is_view_op(u->op) || deferred.count(u)) continue;
+                const ggml_tensor * uw = u->src[0];
+                const bool sibling = u->op == GGML_OP_MUL_MAT && u->src[1] == x && uw->type == wtype &&
+                                     uw->ne[0] == K && uw->ne[2] == 1 && uw->ne[3] == 1 &&
+                                     (int64_t) uw->nb[1] == row_bytes && uw->ne[1] % 64 == 0 &&
+                                     u->type == GGML_TYPE_F32 && is_contiguous(u) && u->ne[1] == N && u->ne[2] == 1 &&
+                                     u->ne[3] == 1 && ready_before(uw, i);
+                if (!sibling) continue;
+                gemm_float_sub sb;
+                sb.a = (const char *) uw->data;
+                sb.M = uw->ne[1];
+                sb.d = (char *) u->data;
+                hoist h2 = h;
+                h2.nodes.push_back(u);
+                h2.reads.push_back(span_of(uw));
+                const ggml_tensor * out = u;
+                const ggml_tensor * ua = sole_consumer(u, j + 1);
+                if (ua && ua->op == GGML_OP_ADD && ua->type == GGML_TYPE_F32 && is_contiguous(ua)) {
+                    const ggml_tensor * o = ua->src[0] == u ? ua->src[1] : ua->src[0];
+                    bool same = o != u;
+                    for (int d = 0; d < 4 && same; d++) same = ua->ne[d] == u->ne[d];
+                    const bool row = same && o->type == GGML_TYPE_F32 && is_contiguous(o) && o->ne[0] == u->ne[0] &&
+                                     o->ne[1] * o->ne[2] * o->ne[3] == 1;
+                    if (row && ready_before(o, i)) {
+                        hoist h3 = h2;
+                        h3.nodes.push_back(ua);
+                        h3.reads.push_back(span_of(o));
+                        h3.writes.push_back(span_of(ua));
+                        if (hoist_ok(i, h3)) {
+                            sb.bias = (const float *) o->data;
+                            sb.d = (char *) ua->data;
+                            out = ua;
+                            h2 = h3;
+                        }
+                    }
+                }
+                if (out == u) {
+                    h2.writes.push_back(span_of(u));
+                    if (!hoist_ok(i, h2)) break;
+                }
+                h = h2;
+                msubs.push_back(sb);
+                msub_outs.push_back(out);
+            }
+        }
         // a following residual ADD of the same shape folds into the epilogue
         const char * res = nullptr;
         int64_t res_nb1 = 0;
@@ -701,6 +755,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             for (const gemv_sub & sb : subs)
                 if ((const char *) n->data == sb.dst) outs.push_back(n);
         }
+        outs.insert(outs.end(), msub_outs.begin(), msub_outs.end());
         if (!reuse && !has_pro) {
             add_step(
                 [=](hipStream_t s) {
@@ -712,7 +767,9 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         add_step(
             [=](hipStream_t s) {
                 act_buffers act = act_carve(wtype, act_base(b), K, N);
-                if (wide) launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, mepi);
+                if (wide)
+                    launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, mepi,
+                               msubs.empty() ? nullptr : msubs.data(), (int) msubs.size());
                 else if (mfma)
                     launch_gemv_mfma(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, res, res_nb1, W2,
                                      has_pro ? &pro : nullptr, epi, subs.data(), (int) subs.size());

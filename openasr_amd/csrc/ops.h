@@ -77,8 +77,13 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
 // MFMA int8 GEMM for wider N (prefill)
 bool mmq_supported(int wtype, int64_t M, int64_t K);
 struct gemm_float_epi;
+struct gemm_float_sub;
+// subs: sibling products of the same activations in one launch (weights of
+// the same type, K and row stride; contiguous outputs of N columns; each
+// product's rows a multiple of 64; only a bias in the epilogue)
 void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
-                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const gemm_float_epi & epi);
+                int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const gemm_float_epi & epi,
+                const gemm_float_sub * subs = nullptr, int nsub = 0);
 
 // float GEMM fallback (f16 / f32 src0)
 void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tview & b, hipStream_t s);

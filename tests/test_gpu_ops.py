@@ -679,6 +679,38 @@ def test_float_sibling_projections(ggml, gpu, wt):
     G.free()
 
 
+@pytest.mark.parametrize("wname", ["q8_0", "q4_K"])
+def test_tile_gemm_sibling_projections(ggml, gpu, ref, wname):
+    """three quantized MUL_MATs of the same 390 columns (an encoder block's
+    q, k, v projections; q and v with a bias ADD, k without; row counts
+    128 / 192 / 64): one tile-GEMM launch, bit for bit the oracle"""
+    wt = {"q8_0": ggml.Q8_0, "q4_K": ggml.Q4_K}[wname]
+    k, n, ms = 512, 390, (128, 192, 64)
+    x = RNG.standard_normal((n, k)).astype(np.float32)
+    ws = [ggml.quantize(wt, ggml.synth_normal(60 + i, 1, m * k, 0, 0.05).reshape(m, k)) for i, m in enumerate(ms)]
+    bq = RNG.standard_normal(ms[0]).astype(np.float32)
+    bv = RNG.standard_normal(ms[2]).astype(np.float32)
+    G = ggml.Graph()
+    L = G.lib
+    X = G.new(ggml.F32, k, n)
+    Ws = [G.new(wt, k, m, weight=True) for m in ms]
+    BQ, BV = G.new(ggml.F32, ms[0], weight=True), G.new(ggml.F32, ms[2], weight=True)
+    Q = L.ggml_add(G.ctx, L.ggml_mul_mat(G.ctx, Ws[0], X), BQ)
+    Kt = L.ggml_mul_mat(G.ctx, Ws[1], X)
+    V = L.ggml_add(G.ctx, L.ggml_mul_mat(G.ctx, Ws[2], X), BV)
+    G.build(Q, Kt, V)
+    G.allocate(gpu.buft)
+    for T, v in [(X, x), (BQ, bq), (BV, bv)] + list(zip(Ws, ws)):
+        G.set(T, v)
+    assert G.compute(gpu.backend) == 0
+    assert_same_bits(G.get(Q).reshape(n, ms[0]), ref.mul_mat(wt, ws[0], ms[0], k, x) + bq)
+    assert_same_bits(G.get(Kt).reshape(n, ms[1]), ref.mul_mat(wt, ws[1], ms[1], k, x))
+    assert_same_bits(G.get(V).reshape(n, ms[2]), ref.mul_mat(wt, ws[2], ms[2], k, x) + bv)
+    labels = [lab.split(":")[0] for lab, _ in gpu.profile(G.gf, 1)]
+    assert sum(lab.startswith("mul_mat") for lab in labels) == 1 and "binary" not in labels, labels
+    G.free()
+
+
 def test_silu_mul_and_gelu(ggml, gpu, ref):
     g = RNG.standard_normal((4, 3072)).astype(np.float32) * 3
     u = RNG.standard_normal((4, 3072)).astype(np.float32)
