@@ -82,13 +82,62 @@ def table(trace: str, which: int, workload: str, tail: bool = False) -> str:
     return "\n".join(lines)
 
 
+def encoder_tables(trace: str, reps: int = 10) -> str:
+    """Per-kernel summary of the audio encoder from a trace of `bench.py
+    --encoder-only` (HIP-graph capture off): an encode starts at its first
+    IM2COL (the stem's three convolutions each run one, conv1's first); the
+    run holds an f16 leg, then a Q8_0 leg, of 1 + `reps` encodes each, and
+    the last `reps` of each leg are averaged."""
+    with open(trace, newline="") as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    starts, n_im = [], 0
+    for i, r in enumerate(rows):
+        if "im2col" in r["Kernel_Name"]:
+            if n_im % 3 == 0:
+                starts.append(i)
+            n_im += 1
+    if len(starts) != 2 * (reps + 1):
+        raise SystemExit(f"expected {2 * (reps + 1)} encodes, found {len(starts)}")
+    starts.append(len(rows))
+    out = []
+    for leg, name in enumerate(("F16 projections", "Q8_0 projections")):
+        agg = collections.defaultdict(list)
+        first = leg * (reps + 1) + 1
+        for e in range(first, first + reps):
+            enc = rows[starts[e]:starts[e + 1]]
+            for r in enc:
+                kname = r["Kernel_Name"].replace("(anonymous namespace)::", "")
+                key = (kname.split("(")[0].replace("void ", "").replace("mi355x::", ""),
+                       r["Grid_Size_X"], r["Grid_Size_Y"], r["Grid_Size_Z"], r["Workgroup_Size_X"])
+                agg[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+        lines = [f"## {name}", "", "| kernel | grid (threads x, y, z) | workgroup | launches / encode | avg us | us / encode |",
+                 "|---|---|---|---|---|---|"]
+        total = 0.0
+        for (k, gx, gy, gz, wg), v in sorted(agg.items(), key=lambda kv: -sum(kv[1])):
+            per = sum(v) / reps
+            total += per
+            if per >= 20.0:
+                lines.append(f"| {k} | {gx} x {gy} x {gz} | {wg} | {len(v) / reps:g} | {sum(v) / len(v):.2f} | {per:.1f} |")
+        n_launch = sum(len(v) for v in agg.values()) / reps
+        lines.append("")
+        lines.append(f"Kernel time per encode: {total / 1e3:.3f} ms over {n_launch:g} launches "
+                     "(kernels under 20 us an encode not listed).")
+        out.append("\n".join(lines))
+    return "\n\n".join(out)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("trace")
+    ap.add_argument("--encoder", action="store_true",
+                    help="summarise a trace of bench.py --encoder-only (the two audio encoder legs)")
     ap.add_argument("--only", default=None,
                     help="summarise the last steps of the trace as this workload (a WORKLOADS name, or "
                          "whisper-tiny-q8_0-b1 for the Whisper leg that ends a bench.py run)")
     a = ap.parse_args()
+    if a.encoder:
+        print(encoder_tables(a.trace))
+        return 0
     if a.only:
         print(f"## {a.only}\n")
         print(table(a.trace, 0, a.only, tail=True))
