@@ -592,7 +592,7 @@ void launch_get_rows(const tview & dst, const tview & src, int stype, const tvie
 
 // element-order copy between any two layouts of equal element count, with
 // f32 <-> f16 conversion (CPY, CONT, DUP)
-__global__ void k_copy(tview d, int dtype, tview a, int atype, int64_t n) {
+__device__ __forceinline__ void copy_elems(const tview & d, int dtype, const tview & a, int atype, int64_t n) {
     for (int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
         int64_t i0, i1, i2, i3;
         unravel(t, a.ne, i0, i1, i2, i3);
@@ -608,6 +608,14 @@ __global__ void k_copy(tview d, int dtype, tview a, int atype, int64_t n) {
         if (dtype == GGML_TYPE_F16) *(uint16_t *) op = float_to_half_bits(v);
         else *(float *) op = v;
     }
+}
+
+__global__ void k_copy(tview d, int dtype, tview a, int atype, int64_t n) { copy_elems(d, dtype, a, atype, n); }
+
+// two such copies of n elements each in one launch (blockIdx.y: which)
+__global__ void k_copy_pair(tview d0, tview a0, tview d1, tview a1, int dtype, int atype, int64_t n) {
+    if (blockIdx.y == 0) copy_elems(d0, dtype, a0, atype, n);
+    else copy_elems(d1, dtype, a1, atype, n);
 }
 
 // dense copies: 16 bytes per lane per iteration, grid-stride (same type), or
@@ -652,6 +660,17 @@ void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStre
         }
     }
     hipLaunchKernelGGL(k_copy, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, dtype, a, atype, n);
+}
+
+void launch_copy_pair(const tview & d0, const tview & a0, const tview & d1, const tview & a1, int dtype, int atype,
+                      hipStream_t s, int n_cu) {
+    const int64_t n = a0.ne[0] * a0.ne[1] * a0.ne[2] * a0.ne[3];
+    if (n != a1.ne[0] * a1.ne[1] * a1.ne[2] * a1.ne[3]) {
+        launch_copy(d0, dtype, a0, atype, s, n_cu);
+        launch_copy(d1, dtype, a1, atype, s, n_cu);
+        return;
+    }
+    hipLaunchKernelGGL(k_copy_pair, dim3(grid_for(n, 256, n_cu), 2), dim3(256), 0, s, d0, a0, d1, a1, dtype, atype, n);
 }
 
 // ------------------------------------------------------------ soft_max ---

@@ -1237,26 +1237,42 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
             fattn_args la = a;
             if (la.qtype >= 0) la.act = act_carve(la.qtype, act_base(b), qK, qN);
             // contiguous f16 [ne0, ne1, ne2, ne3] copy of an f32 operand
-            auto to_f16 = [&](const tview & src, char * dst, int64_t & nb1, int64_t & nb2, int64_t & nb3) {
+            auto f16_dense = [](const tview & src, char * dst) {
                 tview d = src;
                 d.data = dst;
                 d.nb[0] = 2;
                 d.nb[1] = 2 * d.ne[0];
                 d.nb[2] = d.nb[1] * d.ne[1];
                 d.nb[3] = d.nb[2] * d.ne[2];
+                return d;
+            };
+            auto dense_f32 = [](const tview & v) {
+                return v.nb[0] == 4 && v.nb[1] == 4 * v.ne[0] && v.nb[2] == v.nb[1] * v.ne[1] &&
+                       v.nb[3] == v.nb[2] * v.ne[2];
+            };
+            auto to_f16 = [&](const tview & src, char * dst, int64_t & nb1, int64_t & nb2, int64_t & nb3) {
+                const tview d = f16_dense(src, dst);
                 launch_copy(d, GGML_TYPE_F16, src, GGML_TYPE_F32, s, ncu);
                 nb1 = d.nb[1];
                 nb2 = d.nb[2];
                 nb3 = d.nb[3];
             };
             char * g = gen_base(b);
-            if (k32) {
-                to_f16(kv, g + part, la.k_nb1, la.k_nb2, la.k_nb3);
-                la.k = g + part;
-            }
-            if (v32) {
-                to_f16(vv, g + part + kbytes, la.v_nb1, la.v_nb2, la.v_nb3);
-                la.v = g + part + kbytes;
+            if (k32 && v32 && !dense_f32(kv) && !dense_f32(vv)) {
+                // both strided head views: one launch for the two
+                tview dk = f16_dense(kv, g + part), dvw = f16_dense(vv, g + part + kbytes);
+                launch_copy_pair(dk, kv, dvw, vv, GGML_TYPE_F16, GGML_TYPE_F32, s, ncu);
+                la.k = g + part, la.k_nb1 = dk.nb[1], la.k_nb2 = dk.nb[2], la.k_nb3 = dk.nb[3];
+                la.v = g + part + kbytes, la.v_nb1 = dvw.nb[1], la.v_nb2 = dvw.nb[2], la.v_nb3 = dvw.nb[3];
+            } else {
+                if (k32) {
+                    to_f16(kv, g + part, la.k_nb1, la.k_nb2, la.k_nb3);
+                    la.k = g + part;
+                }
+                if (v32) {
+                    to_f16(vv, g + part + kbytes, la.v_nb1, la.v_nb2, la.v_nb3);
+                    la.v = g + part + kbytes;
+                }
             }
             launch_fattn(la, g, out, s);
         },

@@ -258,6 +258,9 @@ norm_rope_job make_norm_rope_job(const tview & d, const tview & a, float eps, co
 void launch_rms_norm_rope128(const norm_rope_job & j0, const norm_rope_job * j1, hipStream_t s);
 void launch_get_rows(const tview & dst, const tview & src, int stype, const tview & idx, hipStream_t s, int n_cu);
 void launch_copy(const tview & d, int dtype, const tview & a, int atype, hipStream_t s, int n_cu);
+// two copies of equal element count (same types) in one launch
+void launch_copy_pair(const tview & d0, const tview & a0, const tview & d1, const tview & a1, int dtype, int atype,
+                      hipStream_t s, int n_cu);
 void launch_soft_max(const tview & d, const tview & a, const tview * mask, float scale, hipStream_t s);
 size_t argmax_scratch_bytes(int64_t ne0, int64_t rows);
 void launch_argmax(const tview & a, int32_t * out, int first, void * scratch, hipStream_t s);
