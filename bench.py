@@ -7,7 +7,9 @@ an f16 KV cache sized for 1024 positions per sequence. One "step" is one
 decode step of all eight sequences through the persistent decode graph
 (28 layers + batched lm_head + first-max top-1), inputs resident in HBM.
 The timed region is K consecutive greedy steps (each step is a synchronous
-graph compute, so the region is bracketed by device synchronisation).
+graph compute, so the region is bracketed by device synchronisation),
+centred on the mean position of the workload's 512-token decode (untimed
+steps, at least the warmup, decode the tokens before it).
 
 Also reported (same run): the Qwen3-0.6B Q8_0 batch-1 decode rate, the
 Qwen3-1.7B Q4_K batch-8 rate after 3000-position prefixes (4096-position KV),
@@ -128,10 +130,19 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
     n_prefill = wl.n_seq * (wl.prefix + wl.prompt)
     log(f"[bench] prefill {n_prefill} positions in {prefill_s * 1e3:.1f} ms")
 
-    steps = min(steps, wl.max_positions - wl.prefix - wl.prompt - warmup)
-    out, _ = sess.generate(first, warmup)
-    cur = out[-1] if warmup else first
-    # the step at position p writes KV row p and attends over rows 0..p
+    # The workload's greedy decode runs at positions p_first .. p_first +
+    # decode - 1 (the step at position p writes KV row p and attends over rows
+    # 0..p, so the step time grows with p). The timed steps are centred on
+    # the workload's mean position, so their rate is the whole decode's rate:
+    # the untimed steps before them (at least `warmup`) decode the tokens
+    # that precede that span.
+    p_first = wl.prefix + wl.prompt
+    steps = min(steps, wl.max_positions - p_first - warmup)
+    centre = p_first + (wl.decode - 1) / 2
+    lead = max(warmup, int(round(centre - (steps - 1) / 2)) - p_first)
+    lead = min(lead, wl.max_positions - p_first - steps)
+    out, _ = sess.generate(first, lead)
+    cur = out[-1] if lead else first
     pos0 = sess.position(0)
     t0 = time.perf_counter()
     out, step_ms = sess.generate(cur, steps)
@@ -191,10 +202,23 @@ def run_workload(name: str, steps: int, warmup: int, profile_iters: int, want_cp
                 "last_step_ms": round(float(fms[-1]), 4)}
         log(f"[bench] {name} full decode: {n} steps at positions {p0}-{p0 + n - 1}, {dt * 1e3 / n:.3f} ms/step, "
             f"{full['tokens_per_s']:.1f} tokens/s (first step {fms[0]:.3f} ms, last {fms[-1]:.3f} ms)")
+    # the whole step's algorithmic bytes at the timed positions: every weight
+    # once, each sequence's attended K/V rows (0..p, f16), the GEMV
+    # activations; over the measured step time
+    kv_row = wl.shape["n_layers"] * 2 * kv_w * 2
+    kv_bytes = wl.n_seq * kv_row * float(np.mean([p + 1 for p in range(pos0, pos0 + steps)]))
+    step_bytes = sum(wb.values()) + act_bytes + kv_bytes
+    step_gbs = step_bytes / (elapsed / steps) / 1e9
+    whole_step = {"alg_bytes": round(step_bytes), "weight_bytes": round(sum(wb.values())),
+                  "kv_bytes": round(kv_bytes), "activation_bytes": act_bytes, "achieved": round(step_gbs, 1),
+                  "frac": round(step_gbs / HBM_PEAK_GBS, 4)}
+    log(f"[bench] whole step: {step_bytes / 1e6:.1f} MB (weights {sum(wb.values()) / 1e6:.1f}, attended KV "
+        f"{kv_bytes / 1e6:.1f}, activations {act_bytes / 1e6:.1f}) per {elapsed * 1e3 / steps:.3f} ms = "
+        f"{step_gbs:.0f} GB/s = {step_gbs / HBM_PEAK_GBS:.1%} of HBM peak")
     result = dict(tok_s=tok_s, ms_per_step=elapsed * 1e3 / steps, steps=steps, prefill_ms=prefill_s * 1e3,
                   n_prefill=n_prefill, gemv_ms=gemv_ms, gemv_launches=gemv_n, gemv_gbs=gemv_gbs,
                   weight_bytes=alg_bytes, eager_step_ms=eager_ms, breakdown=breakdown, cpu=cpu,
-                  timed_positions=timed_positions, full=full)
+                  timed_positions=timed_positions, full=full, untimed_steps=lead, whole_step=whole_step)
     sess.free()
     model.free()
     w.free()
@@ -641,11 +665,13 @@ def main() -> int:
                      "copy_gbs_measured": round(copy_gbs, 1),
                      "alg_bytes_per_launch": round(main_r["weight_bytes"] / max(1, main_r["gemv_launches"]), 1),
                      "launches": main_r["gemv_launches"],
+                     "whole_step": main_r["whole_step"],
                      "kernel": f"{main_wl_text['kernel']}: the quantized GEMV launches of one decode step (per layer QKV, "
                                "o-proj+residual, gate+up SwiGLU, down+residual; lm_head), algorithmic bytes "
                                "(weights + int8 activations + f32 outputs) / summed launch time"},
         "cpu_baseline": main_r["cpu"],
         "timed_positions": main_r["timed_positions"],
+        "untimed_steps_before": main_r["untimed_steps"],
         "full_decode": main_r["full"],
         "prefill_ms": round(main_r["prefill_ms"], 2),
         "eager_step_ms": round(main_r["eager_step_ms"], 4),

@@ -97,16 +97,6 @@ def build_plugin(fp: str) -> Path:
     return out
 
 
-def build_probes() -> list[Path]:
-    """Stand-alone measurement programs (csrc/probe/*.hip -> lib/<name>)."""
-    outs = []
-    for src in sorted((PKG / "csrc" / "probe").glob("*.hip")):
-        out = LIB / src.stem
-        _run([HIPCC, *HIP_FLAGS, "-x", "hip", str(src), "-o", str(out)])
-        outs.append(out)
-    return outs
-
-
 def build_oracle() -> Path:
     out_dir = ORACLE / "build"
     out_dir.mkdir(exist_ok=True)
@@ -125,8 +115,6 @@ def build_all(plugin: bool = True) -> dict[str, Path]:
     built["models"] = build_models()
     if plugin:
         built["plugin"] = build_plugin(fp)
-        for p in build_probes():
-            built[p.name] = p
     return built
 
 

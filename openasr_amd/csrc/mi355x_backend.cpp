@@ -443,6 +443,10 @@ static void init_devices() {
         if (hipDeviceGetUuid(&uuid, i) == hipSuccess) std::memcpy(dev->uuid, uuid.bytes, 16);
         MI_CHECK(hipMalloc((void **) &dev->gelu_table, table.size() * 2));
         ledger_add(dev, table.size() * 2, false);
+        // the fixed scratch array of the allocation-free compute is device
+        // memory the plugin holds on every device until the process ends
+        // (mapped with the code object, not by hipMalloc)
+        ledger_add(dev, static_scratch_bytes(), false);
         MI_CHECK(hipMemcpy(dev->gelu_table, table.data(), table.size() * 2, hipMemcpyHostToDevice));
         dev->buft.iface = kBuftIface;
         dev->buft.device = &dev->dev;

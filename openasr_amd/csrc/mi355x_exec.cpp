@@ -200,11 +200,24 @@ struct planner {
     // scratch (the attention output quantized for the output projection):
     // their own bytes are never written, so nothing else may read them
     std::unordered_set<const ggml_tensor *> unwritten;
+    // attention outputs that must be written after all: a reader found one
+    // unwritten, and the graph is planned again without that diversion
+    std::unordered_set<const ggml_tensor *> no_divert;
+    bool replan = false;
+    bool reads_unwritten(const ggml_tensor * t, const ggml_tensor * x) {
+        const ggml_tensor * r = root_of(x);
+        if (!unwritten.count(r)) return false;
+        no_divert.insert(r);
+        replan = true;
+        fail(t, "reads an output a fused launch never wrote");
+        return true;
+    }
     int cur = -1;  // graph position being planned
 
     planner(backend_state * b, const ggml_cgraph * g, const std::unordered_set<const ggml_tensor *> & nb = {},
-            const std::unordered_set<const ggml_tensor *> & nd = {})
-        : be(b), cg(g), n_cu(b->dev->n_cu), no_bypass(nb), no_defer(nd) {}
+            const std::unordered_set<const ggml_tensor *> & nd = {},
+            const std::unordered_set<const ggml_tensor *> & nv = {})
+        : be(b), cg(g), n_cu(b->dev->n_cu), no_bypass(nb), no_defer(nd), no_divert(nv) {}
 
     std::unordered_map<const ggml_tensor *, int> index;  // node -> position in the graph
     // CONT nodes whose copy is skipped: consumers read the CONT's strided
@@ -490,7 +503,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         const int64_t row_bytes = (int64_t) w->nb[1];
         act_need = std::max(act_need, act_bytes(wtype, K, N));
         const bool reuse = act_src == x && act_wtype == wtype;
-        if (!reuse && unwritten.count(root_of(x))) return fail(t, "reads an output a fused launch never wrote");
+        if (!reuse && reads_unwritten(t, x)) return false;
         backend_state * b = be;
         const int ncu = n_cu;
         // the tile GEMM once the columns outgrow a few GEMV chunks (earlier for tall matrices)
@@ -913,7 +926,8 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                                      uw->ne[0] == w->ne[0] && uw->ne[2] == 1 && uw->ne[3] == 1 &&
                                      uw->nb[1] == w->nb[1] && uw->nb[0] == w->nb[0] && uw->ne[1] % 64 == 0 &&
                                      u->type == GGML_TYPE_F32 && is_contiguous(u) && u->ne[1] == t->ne[1] &&
-                                     u->ne[2] == 1 && u->ne[3] == 1 && ready_before(uw, i);
+                                     u->ne[2] == 1 && u->ne[3] == 1 && ready_before(uw, i) &&
+                                     aligned16(uw->data);  // its rows take the same 16-byte loads
                 if (!sibling) continue;
                 gemm_float_sub sb;
                 sb.a = (const char *) uw->data;
@@ -1375,7 +1389,7 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     // writes, nothing reads the f32 output: it goes to scratch, not to F's
     // bytes (which an allocator may well have placed over the projection
     // rows this launch reads). Any other reader of F then fails the plan.
-    const bool f32_unread = fa.qtype >= 0 && !(F->flags & GGML_TENSOR_FLAG_OUTPUT);
+    const bool f32_unread = fa.qtype >= 0 && !(F->flags & GGML_TENSOR_FLAG_OUTPUT) && !no_divert.count(F);
     if (!f32_unread) {
         // the kernel's output must not overlap what it reads (the projection rows)
         uintptr_t lo, hi, olo = (uintptr_t) F->data, ohi = olo + ggml_nbytes(F);
@@ -1507,8 +1521,7 @@ bool planner::plan() {
         if (!supports_op(be->dev, t)) return fail(t, "unsupported op or layout");
         if (t->op != GGML_OP_MUL_MAT && !deferred.count(t)) {
             for (int k = 0; k < GGML_MAX_SRC; k++)
-                if (t->src[k] && unwritten.count(root_of(t->src[k])))
-                    return fail(t, "reads an output a fused launch never wrote");
+                if (t->src[k] && reads_unwritten(t, t->src[k])) return false;
         }
         if (bypass.count(t)) continue;  // readers take the CONT's source directly
         auto dit = deferred.find(t);
@@ -1661,15 +1674,17 @@ bool planner::plan() {
 // plan cg, and plan again without the fusions validate() finds unsafe under
 // the graph's allocation (each pass removes at least one; they are few)
 std::unique_ptr<planner> make_plan(backend_state * be, const ggml_cgraph * cg, bool & ok) {
-    std::unordered_set<const ggml_tensor *> nb, nd;
+    std::unordered_set<const ggml_tensor *> nb, nd, nv;
     for (int pass = 0; pass < 64; pass++) {
-        auto p = std::make_unique<planner>(be, cg, nb, nd);
+        auto p = std::make_unique<planner>(be, cg, nb, nd, nv);
         ok = p->plan();
-        if (!ok || p->validate()) return p;
+        if (!ok && !p->replan) return p;
+        if (ok && p->validate()) return p;
         nb = p->no_bypass;
         nd = p->no_defer;
+        nv = p->no_divert;
     }
-    auto p = std::make_unique<planner>(be, cg, nb, nd);
+    auto p = std::make_unique<planner>(be, cg, nb, nd, nv);
     ok = p->plan() && p->validate();
     if (!ok && p->error.empty()) p->error = "no safe plan for this allocation";
     return p;

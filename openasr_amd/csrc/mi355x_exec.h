@@ -94,6 +94,8 @@ backend_state * backend_of(ggml_backend_t backend);
 void ledger_add(device_state * dev, uint64_t bytes, bool workspace);
 void ledger_sub(device_state * dev, uint64_t bytes, bool workspace);
 void ledger_failure(device_state * dev);
+// size of the fixed scratch array every device holds (mi355x_static.cpp)
+size_t static_scratch_bytes();
 
 // one planned launch: a closure that enqueues kernels on a stream
 struct step {

@@ -43,6 +43,8 @@ static char * device_scratch(device_state * dev) {
     return dev->static_scratch;
 }
 
+size_t static_scratch_bytes() { return kStaticScratchBytes; }
+
 }  // namespace mi355x
 
 using namespace mi355x;

@@ -127,7 +127,11 @@ def test_audio_encoder_matches_reference(gpu, wname):
         print(f"  frames {n_frames}: rows {got.shape[0]}, {ms:.2f} ms, rel err {err:.2e} "
               f"(reference f32 vs f64 sums {spread:.2e})", flush=True)
         assert got.shape == want.shape == (D.qwen_audio_token_count(n_frames), SMALL["out_dim"])
-        assert err < (2e-2 if wt == g.Q8_0 else 2e-3)
+        # each projection type is held to its own precision: the f32 path
+        # measures ~1e-6 (an f32 path that rounded an operand to f16 would
+        # show ~3e-4), f16 ~3e-4, and Q8_0 moves by whole activation
+        # quantization steps where a sum lands near an int8 rounding boundary
+        assert err < {"f32": 1e-5, "f16": 2e-3, "q8_0": 2e-2}[wname]
     enc.free()
     w.free()
 

@@ -42,7 +42,13 @@ def test_stats_are_consistent_and_stable(ggml, mem):
     assert a.total_bytes > 200 * (1 << 30) and a.budget_bytes == a.total_bytes
     assert a.device_used_bytes + a.device_free_bytes == a.total_bytes
     assert a.health == ggml.MEM_HEALTHY
-    assert a.backend_owned_live_bytes > 0  # at least the plugin's GELU table
+    # at least the plugin's GELU table and the fixed scratch array of the
+    # allocation-free compute, which every device holds until the process ends
+    fn = ggml.plugin().cdll.ggml_backend_mi355x_static_scratch_bytes
+    fn.restype = C.c_size_t
+    static = fn()
+    assert static == 64 * MiB
+    assert a.backend_owned_live_bytes >= static + 65536 * 2
     assert a.backend_owned_high_water_bytes >= a.backend_owned_live_bytes + a.backend_owned_workspace_bytes
     assert bytes(a.domain.physical_device_uuid) == bytes(mem.domains()[0].id.physical_device_uuid)
 

@@ -4,7 +4,8 @@ graphs and inputs, bit for bit: a graph whose plan uses every kind of scratch
 (the tile GEMM's quantized activations, the decode attention's chunk
 partials, argmax partials), computed twice in a row, the second time with
 smaller inputs (fewer columns, a shorter KV span), so the second call runs on
-an array that still holds the first call's contents."""
+an array that still holds the first call's contents. The device's allocation
+ledger (memory ABI v1) must not move across a call."""
 
 import ctypes as C
 
@@ -57,8 +58,15 @@ def test_static_compute_matches_graph_compute(ggml, gpu):
         G, outs = build(ggml, gpu, n, kv, seed)
         for t in outs:  # poison the outputs: every value must be written
             G.set(t, np.full(G.get(t).shape, -1, G.get(t).dtype))
+        mem = ggml.MemoryApi(gpu.reg, gpu.dev, gpu.backend)
+        s0 = mem.stats()[0]
         assert lib.ggml_backend_mi355x_graph_compute_static(gpu.backend, G.gf) == 0
         got = outputs(G, outs)
+        # the call allocated nothing: the device ledger did not move
+        s1 = mem.stats()[0]
+        assert s1.allocation_count == s0.allocation_count and s1.generation == s0.generation
+        assert s1.backend_owned_workspace_bytes == s0.backend_owned_workspace_bytes
+        assert s1.backend_owned_live_bytes == s0.backend_owned_live_bytes
         assert G.compute(gpu.backend) == 0
         want = outputs(G, outs)
         for g, w_ in zip(got, want):
