@@ -119,6 +119,21 @@ int oa_qwen_session_position(const oa_qwen_session * s, int seq);
  * the first of equal maxima. Takes effect on the next step. */
 void oa_qwen_session_set_reversed_top1(oa_qwen_session * s, int enable);
 
+/* The step graphs the unmodified host builds on a discrete-GPU HIP backend
+ * (enable = 1): native GQA is Unsupported there
+ * (ggml_runtime/cpu_graph.rs:736-757), so each layer expands K and V to the
+ * query heads with RESHAPE / REPEAT / RESHAPE (expand_attention_kv,
+ * nn/decoder.rs:1799-1841); prefill chunks of more than two positions over
+ * a span of more than 32 take the unfused attention chain
+ * (llm_naive_masked_attention, nn/decoder.rs:2154-2200;
+ * llm_transformer.rs:7864-7877) with GGML_PREC_F32 on its two products
+ * (cpu_graph.rs:157-165, 202-228); prefill runs in chunks of at most
+ * prefill_chunk positions, odd widths above one trimmed by one
+ * (llm_transformer.rs:7903-7911). One sequence only, as the host refuses
+ * more on this lane (llm_transformer.rs:2444-2450): another n_seq returns
+ * GGML_STATUS_FAILED. Takes effect on the next step. */
+int oa_qwen_session_set_hip_lane(oa_qwen_session * s, int enable, int prefill_chunk);
+
 /* Prefill T positions of every sequence (chunked internally at 256) from
  * hidden inputs [n_seq][T][d_model] (an audio-embedding prefix) or token ids
  * [n_seq][T]. top1_out (optional, [n_seq]) gets the first-max argmax of the

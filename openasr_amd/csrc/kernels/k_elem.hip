@@ -673,6 +673,25 @@ void launch_copy_pair(const tview & d0, const tview & a0, const tview & d1, cons
     hipLaunchKernelGGL(k_copy_pair, dim3(grid_for(n, 256, n_cu), 2), dim3(256), 0, s, d0, a0, d1, a1, dtype, atype, n);
 }
 
+// -------------------------------------------------------------- repeat ---
+
+// ggml_repeat: dst[i] = src[i mod src.ne] per dim, elements of esize bytes
+__global__ void k_repeat(tview d, tview a, int esize, int64_t n) {
+    for (int64_t t = (int64_t) blockIdx.x * blockDim.x + threadIdx.x; t < n; t += (int64_t) gridDim.x * blockDim.x) {
+        int64_t i0, i1, i2, i3;
+        unravel(t, d.ne, i0, i1, i2, i3);
+        const char * ip = a.data + offs4(a, i0 % a.ne[0], i1 % a.ne[1], i2 % a.ne[2], i3 % a.ne[3]);
+        char * op = d.data + offs4(d, i0, i1, i2, i3);
+        if (esize == 4) *(uint32_t *) op = *(const uint32_t *) ip;
+        else *(uint16_t *) op = *(const uint16_t *) ip;
+    }
+}
+
+void launch_repeat(const tview & d, const tview & src, int esize, hipStream_t s, int n_cu) {
+    const int64_t n = d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3];
+    hipLaunchKernelGGL(k_repeat, dim3(grid_for(n, 256, n_cu)), dim3(256), 0, s, d, src, esize, n);
+}
+
 // ------------------------------------------------------------ soft_max ---
 
 // ggml_compute_forward_soft_max_f32, max_bias 0: y = softmax(x*scale + mask)

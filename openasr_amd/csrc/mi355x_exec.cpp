@@ -167,6 +167,26 @@ span span_of(const tview & v, int64_t elem) {
 
 bool overlap(span a, span b) { return a.lo < a.hi && b.lo < b.hi && a.lo < b.hi && b.lo < a.hi; }
 
+// The GQA expansion of expand_attention_kv (nn/decoder.rs:1799-1841): x is
+// the [D, T, g * H, 1] reshape of R = REPEAT [D, T, g, H] of S [D, T, 1, H],
+// so head h of x is head h / g of S -- the broadcast FLASH_ATTN_EXT and
+// MUL_MAT make natively. Gives R and S seen as [D, T, H, 1].
+bool match_gqa(const ggml_tensor * x, const ggml_tensor *& rep, tview & folded) {
+    const ggml_tensor * r = x->view_src ? x->view_src : x;
+    if (r->op != GGML_OP_REPEAT || x == r || x->op != GGML_OP_RESHAPE || x->data != r->data) return false;
+    const ggml_tensor * s = r->src[0];
+    if (!s || s->type != r->type || !is_contiguous(x) || !is_contiguous(r)) return false;
+    if (x->ne[0] != r->ne[0] || x->ne[1] != r->ne[1] || x->ne[2] != r->ne[2] * r->ne[3] || x->ne[3] != 1) return false;
+    if (s->ne[0] != r->ne[0] || s->ne[1] != r->ne[1] || s->ne[2] != 1 || s->ne[3] != r->ne[3]) return false;
+    rep = r;
+    folded = make_view(s);
+    folded.ne[2] = s->ne[3];
+    folded.ne[3] = 1;
+    folded.nb[2] = s->nb[3];
+    folded.nb[3] = s->nb[3] * s->ne[3];
+    return true;
+}
+
 // A launch at graph position i that also does the work of later nodes (a
 // folded residual ADD, the SwiGLU pair, sibling projections) writes their
 // results before the nodes in between run, and reads their inputs early.
@@ -177,6 +197,12 @@ struct hoist {
     // (written, read) tensor pairs one lane reads then writes element by
     // element: they may coincide exactly (an in-place residual), not overlap
     std::vector<std::pair<const ggml_tensor *, const ggml_tensor *>> inplace;
+};
+
+// fusions a previous planning pass found unsafe under the graph's
+// allocation, or that a reader could not take (see validate and replan)
+struct plan_exclusions {
+    std::unordered_set<const ggml_tensor *> no_bypass, no_defer, no_divert, no_fold, no_naive;
 };
 
 struct planner {
@@ -192,9 +218,8 @@ struct planner {
     std::string error;
     int n_cu;
 
-    // fusions a previous planning pass found unsafe under the graph's
-    // allocation (see validate): CONTs that must be materialised, unary
-    // nodes that must run at their own position
+    // CONTs that must be materialised, unary nodes that must run at their
+    // own position (validate)
     std::unordered_set<const ggml_tensor *> no_bypass, no_defer;
     // nodes whose result is consumed only in a form a fused launch wrote to
     // scratch (the attention output quantized for the output projection):
@@ -203,7 +228,39 @@ struct planner {
     // attention outputs that must be written after all: a reader found one
     // unwritten, and the graph is planned again without that diversion
     std::unordered_set<const ggml_tensor *> no_divert;
+    // REPEATs to materialise, unfused attention chains to run op by op
+    std::unordered_set<const ggml_tensor *> no_fold, no_naive;
     bool replan = false;
+    plan_exclusions exclusions() const { return {no_bypass, no_defer, no_divert, no_fold, no_naive}; }
+
+    // GQA expansions (match_gqa) every reader of which reads the source's kv
+    // heads instead: the REPEAT is not launched
+    std::unordered_set<const ggml_tensor *> gqa_skip;
+    // x read through a skipped REPEAT: the view of its source
+    bool gqa_fold(const ggml_tensor * x, tview & v) const {
+        const ggml_tensor * r = nullptr;
+        return match_gqa(x, r, v) && gqa_skip.count(r);
+    }
+    // The unfused attention chain (nn/decoder.rs:2154-2200) as one launch at
+    // its output CONT: the scores MUL_MAT S, the SOFT_MAX P, the V^T CONT VT
+    // and the context MUL_MAT C are not launched on their own.
+    struct naive_job {
+        const ggml_tensor *S = nullptr, *P = nullptr, *VT = nullptr, *C = nullptr, *O = nullptr;
+        naive_attn_args a{};
+        std::vector<std::pair<span, int>> reads;  // what the launch reads, and where the graph read it
+    };
+    std::unordered_map<const ggml_tensor *, naive_job> naive_jobs;  // by output CONT
+    std::unordered_set<const ggml_tensor *> naive_nodes;            // S, P, VT, C of the jobs
+    void find_naive();
+    void find_gqa_skip();
+    bool plan_naive(int i, const ggml_tensor * t);
+    struct fold_read {
+        const ggml_tensor * rep;
+        span src;       // the expansion's source
+        int from, to;   // the REPEAT's position, its last reader's
+    };
+    std::vector<fold_read> fold_reads;
+    bool naive_dropped = false;
     bool reads_unwritten(const ggml_tensor * t, const ggml_tensor * x) {
         const ggml_tensor * r = root_of(x);
         if (!unwritten.count(r)) return false;
@@ -214,10 +271,9 @@ struct planner {
     }
     int cur = -1;  // graph position being planned
 
-    planner(backend_state * b, const ggml_cgraph * g, const std::unordered_set<const ggml_tensor *> & nb = {},
-            const std::unordered_set<const ggml_tensor *> & nd = {},
-            const std::unordered_set<const ggml_tensor *> & nv = {})
-        : be(b), cg(g), n_cu(b->dev->n_cu), no_bypass(nb), no_defer(nd), no_divert(nv) {}
+    planner(backend_state * b, const ggml_cgraph * g, const plan_exclusions & x = {})
+        : be(b), cg(g), n_cu(b->dev->n_cu), no_bypass(x.no_bypass), no_defer(x.no_defer), no_divert(x.no_divert),
+          no_fold(x.no_fold), no_naive(x.no_naive) {}
 
     std::unordered_map<const ggml_tensor *, int> index;  // node -> position in the graph
     // CONT nodes whose copy is skipped: consumers read the CONT's strided
@@ -429,7 +485,143 @@ struct planner {
     bool plan_attn_step(int i, const ggml_tensor * t);
 };
 
-// May the launch at position i do the work described by h? Its own writes
+// The unfused attention chains of the graph (llm_naive_masked_attention,
+// nn/decoder.rs:2154-2200): SOFT_MAX_EXT P over S = MUL_MAT(K, Q), read only
+// by C = MUL_MAT(CONT(TRANSPOSE(V)), P), read only through PERMUTE(0, 2, 1, 3)
+// by the output CONT O; K and V f16 rows (the caches, or their GQA
+// expansions), Q f32. Each becomes one k_attn_naive launch at O.
+void planner::find_naive() {
+    for (int iP = 0; iP < cg->n_nodes; iP++) {
+        const ggml_tensor * P = cg->nodes[iP];
+        if (P->op != GGML_OP_SOFT_MAX || P->type != GGML_TYPE_F32 || op_f32(P, 1) != 0.0f) continue;
+        const ggml_tensor *S = P->src[0], *M = P->src[1];
+        if (!S || S->op != GGML_OP_MUL_MAT || !single_use(S) || !single_use(P)) continue;
+        const ggml_tensor *Kx = S->src[0], *Q = S->src[1];
+        if (Kx->type != GGML_TYPE_F16 || Q->type != GGML_TYPE_F32 || Q->nb[0] != 4) continue;
+        const ggml_tensor * C = sole_consumer(P, iP + 1);
+        if (!C || C->op != GGML_OP_MUL_MAT || C->src[1] != P || C->type != GGML_TYPE_F32 || !single_use(C)) continue;
+        const ggml_tensor * VT = C->src[0];
+        if (VT->op != GGML_OP_CONT || VT->type != GGML_TYPE_F16 || !single_use(VT) || !is_contiguous(VT)) continue;
+        const ggml_tensor * TR = VT->src[0];
+        if (TR->op != GGML_OP_TRANSPOSE || !single_use(TR)) continue;
+        const ggml_tensor * Vx = TR->src[0];
+        if (Vx->type != GGML_TYPE_F16) continue;
+        const ggml_tensor * PM = sole_consumer(C, index.at(C) + 1);
+        if (!PM || PM->op != GGML_OP_PERMUTE || !single_use(PM)) continue;
+        const ggml_tensor * O = sole_consumer(PM, index.at(PM) + 1);
+        if (!O || O->op != GGML_OP_CONT || O->type != GGML_TYPE_F32 || !is_contiguous(O) || no_naive.count(O)) continue;
+        if ((S->flags | P->flags | VT->flags | C->flags) & GGML_TENSOR_FLAG_OUTPUT) continue;
+        const int64_t D = Q->ne[0], nq = Q->ne[1], Hq = Q->ne[2], ns = Q->ne[3];
+        // K and V as the launch reads them: the source of a GQA expansion
+        // (query head h reads kv head h / g), or the operand itself
+        tview kv = make_view(Kx), vv = make_view(Vx);
+        const ggml_tensor *rk = nullptr, *rv = nullptr;
+        tview fk, fv;
+        const bool kf = match_gqa(Kx, rk, fk) && !no_fold.count(rk);
+        const bool vf = match_gqa(Vx, rv, fv) && !no_fold.count(rv);
+        if (kf != vf) continue;
+        if (kf) kv = fk, vv = fv;
+        const int64_t T = kv.ne[1], Hk = kv.ne[2];
+        bool ok = kv.ne[0] == D && vv.ne[0] == D && vv.ne[1] == T && vv.ne[2] == Hk && vv.ne[3] == kv.ne[3] &&
+                  kv.nb[0] == 2 && vv.nb[0] == 2 && Hk > 0 && Hq % Hk == 0 && kv.ne[3] > 0 && ns % kv.ne[3] == 0;
+        ok = ok && S->ne[0] == T && S->ne[1] == nq && S->ne[2] == Hq && S->ne[3] == ns;
+        ok = ok && C->ne[0] == D && C->ne[1] == nq && C->ne[2] == Hq && C->ne[3] == ns;
+        ok = ok && TR->ne[0] == Vx->ne[1] && TR->ne[1] == Vx->ne[0] && TR->nb[0] == Vx->nb[1] && TR->nb[1] == Vx->nb[0];
+        ok = ok && PM->ne[0] == D && PM->ne[1] == Hq && PM->ne[2] == nq && PM->ne[3] == ns && PM->nb[0] == C->nb[0] &&
+             PM->nb[1] == C->nb[2] && PM->nb[2] == C->nb[1] && PM->nb[3] == C->nb[3] && PM->data == C->data;
+        for (int d = 0; d < 4 && ok; d++) ok = O->ne[d] == PM->ne[d];
+        ok = ok && ((uintptr_t) kv.data % 16 == 0) && kv.nb[1] % 16 == 0 && ((uintptr_t) vv.data % 16 == 0) &&
+             vv.nb[1] % 16 == 0 && attn_naive_supported((int) D, (int) Hq, (int) Hk, T);
+        if (M) ok = ok && M->type == GGML_TYPE_F16 && M->ne[0] >= T && M->ne[1] >= nq && M->nb[0] == 2;
+        if (!ok) continue;
+        naive_job j;
+        j.S = S, j.P = P, j.VT = VT, j.C = C, j.O = O;
+        naive_attn_args & a = j.a;
+        a.q = (const char *) Q->data;
+        a.q_nb1 = Q->nb[1], a.q_nb2 = Q->nb[2], a.q_nb3 = Q->nb[3];
+        a.k = kv.data;
+        a.k_nb1 = kv.nb[1], a.k_nb2 = kv.nb[2], a.k_nb3 = kv.nb[3];
+        a.v = vv.data;
+        a.v_nb1 = vv.nb[1], a.v_nb2 = vv.nb[2], a.v_nb3 = vv.nb[3];
+        a.mask = M ? (const char *) M->data : nullptr;
+        if (M) {
+            a.m_nb1 = M->nb[1], a.m_nb2 = M->nb[2], a.m_nb3 = M->nb[3];
+            a.m_ne2 = (int) M->ne[2], a.m_ne3 = (int) M->ne[3];
+        } else {
+            a.m_ne2 = a.m_ne3 = 1;
+        }
+        a.d = (int) D, a.hq = (int) Hq, a.hkv = (int) Hk, a.n_q = (int) nq, a.n_kv = (int) T, a.n_seq = (int) ns;
+        a.rk3 = (int) (ns / kv.ne[3]);
+        a.scale = op_f32(P, 0);
+        a.q_f32 = S->op_params[0] == GGML_PREC_F32;
+        a.p_f32 = C->op_params[0] == GGML_PREC_F32;
+        a.out = (float *) O->data;
+        // what the launch at O reads, and where the graph read it
+        j.reads.push_back({span_of(kv, 2), index.at(S)});
+        j.reads.push_back({span_of(make_view(Q), 4), index.at(S)});
+        j.reads.push_back({span_of(vv, 2), index.at(VT)});
+        if (M) j.reads.push_back({span_of(M), index.at(P)});
+        naive_jobs[O] = j;
+        for (const ggml_tensor * n : {S, P, VT, C}) naive_nodes.insert(n);
+    }
+}
+
+// REPEATs every reader of which folds them (match_gqa): a FLASH_ATTN_EXT's
+// K or V, or a fused attention chain's scores product and V^T copy. Their
+// readers read the source instead, so the REPEAT is not launched.
+void planner::find_gqa_skip() {
+    for (int i = 0; i < cg->n_nodes; i++) {
+        const ggml_tensor * r = cg->nodes[i];
+        if (r->op != GGML_OP_REPEAT || no_fold.count(r) || (r->flags & GGML_TENSOR_FLAG_OUTPUT)) continue;
+        bool ok = true, any = false;
+        for (int j = i + 1; j < cg->n_nodes && ok; j++) {
+            const ggml_tensor * n = cg->nodes[j];
+            if (is_view_op(n->op)) continue;
+            for (int k = 0; k < GGML_MAX_SRC && ok; k++) {
+                const ggml_tensor * x = n->src[k];
+                if (!x || root_of(x) != r) continue;
+                any = true;
+                const ggml_tensor * rr = nullptr;
+                tview v;
+                const bool fold = match_gqa(x, rr, v);
+                if (n->op == GGML_OP_FLASH_ATTN_EXT && (k == 1 || k == 2) && fold && x->type == GGML_TYPE_F16) continue;
+                if (naive_nodes.count(n) && ((n->op == GGML_OP_MUL_MAT && k == 0 && fold) || n->op == GGML_OP_CONT)) continue;
+                ok = false;
+            }
+        }
+        if (ok && any) {
+            gqa_skip.insert(r);
+            // the readers read the source where the REPEAT read it
+            int last = i;
+            for (int j = i + 1; j < cg->n_nodes; j++) {
+                for (int k = 0; k < GGML_MAX_SRC; k++)
+                    if (cg->nodes[j]->src[k] && root_of(cg->nodes[j]->src[k]) == r) last = j;
+            }
+            fold_reads.push_back({r, span_of(r->src[0]), i, last});
+        }
+    }
+    // a fused chain whose K / V expansion is still launched reads the
+    // expanded operands; if only one of the two folds, the chain runs op by op
+    for (auto it = naive_jobs.begin(); it != naive_jobs.end();) {
+        const naive_job & j = it->second;
+        const ggml_tensor * Vx = j.VT->src[0]->src[0];
+        tview fk, fv;
+        const bool kf = gqa_fold(j.S->src[0], fk), vf = gqa_fold(Vx, fv);
+        const ggml_tensor *rk = nullptr, *rv = nullptr;
+        tview t0;
+        const bool kr = match_gqa(j.S->src[0], rk, t0), vr = match_gqa(Vx, rv, t0);
+        if (kf == kr && vf == vr) {
+            ++it;
+            continue;
+        }
+        for (const ggml_tensor * n : {j.S, j.P, j.VT, j.C}) naive_nodes.erase(n);
+        no_naive.insert(it->first);
+        naive_dropped = true;
+        it = naive_jobs.erase(it);
+    }
+}
+
+// May the launch at position i do the work described by h? Its own writes// May the launch at position i do the work described by h? Its own writes
 // must not overlap what it reads (other workgroups of the launch may still
 // be reading), except an exact in-place residual, nor each other; and every
 // node between i and the last node it absorbs, which now runs after the
@@ -1165,35 +1357,42 @@ bool planner::plan_binary(const ggml_tensor * t) {
 
 bool planner::make_fattn(const ggml_tensor * t, fattn_args & a) {
     const ggml_tensor *q = t->src[0], *k = t->src[1], *v = t->src[2], *m = t->src[3];
+    // K and V behind GQA expansions that are not launched: the sources'
+    // kv heads (query head h reads head h / (hq / hkv), the kernel's rule)
+    tview kv = make_view(k), vv = make_view(v);
+    const bool kf = gqa_fold(k, kv), vf = gqa_fold(v, vv);
+    if (kf != vf) return fail(t, "only one of K and V is a folded GQA expansion");
     a = fattn_args{};
     a.q = (const char *) q->data;
-    a.k = (const char *) k->data;
-    a.v = (const char *) v->data;
+    a.k = kv.data;
+    a.v = vv.data;
     a.mask = m ? (const char *) m->data : nullptr;
     a.q_nb1 = q->nb[1];
     a.q_nb2 = q->nb[2];
     a.q_nb3 = q->nb[3];
-    a.k_nb1 = k->nb[1];
-    a.k_nb2 = k->nb[2];
-    a.k_nb3 = k->nb[3];
-    a.v_nb1 = v->nb[1];
-    a.v_nb2 = v->nb[2];
-    a.v_nb3 = v->nb[3];
+    a.k_nb1 = kv.nb[1];
+    a.k_nb2 = kv.nb[2];
+    a.k_nb3 = kv.nb[3];
+    a.v_nb1 = vv.nb[1];
+    a.v_nb2 = vv.nb[2];
+    a.v_nb3 = vv.nb[3];
     if (m) {
         a.m_nb1 = m->nb[1];
         a.m_nb2 = m->nb[2];
         a.m_nb3 = m->nb[3];
         a.m_ne2 = (int) m->ne[2];
         a.m_ne3 = (int) m->ne[3];
-        if (m->ne[0] < k->ne[1] || m->ne[1] < q->ne[1]) return fail(t, "mask smaller than the attention span");
+        if (m->ne[0] < kv.ne[1] || m->ne[1] < q->ne[1]) return fail(t, "mask smaller than the attention span");
     }
     a.d = (int) q->ne[0];
     a.n_q = (int) q->ne[1];
     a.hq = (int) q->ne[2];
     a.n_seq = (int) q->ne[3];
-    a.n_kv = (int) k->ne[1];
-    a.hkv = (int) k->ne[2];
-    a.rk3 = (int) (q->ne[3] / k->ne[3]);
+    a.n_kv = (int) kv.ne[1];
+    a.hkv = (int) kv.ne[2];
+    if (a.hkv <= 0 || a.hq % a.hkv != 0 || vv.ne[2] != kv.ne[2] || vv.ne[1] != kv.ne[1])
+        return fail(t, "K / V heads do not divide the query heads");
+    a.rk3 = (int) (q->ne[3] / kv.ne[3]);
     a.scale = op_f32(t, 0);
     a.qtype = -1;
     // f16 K and V rows are read as 16-byte vectors (f32 ones are converted
@@ -1311,7 +1510,8 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     int i1 = -1;
     for (int j = i + 1; j < cg->n_nodes; j++) {
         const ggml_tensor * n = cg->nodes[j];
-        if (is_view_op(n->op) || bypass.count(n) || deferred.count(n) || n == mul0 || n == rope0) continue;
+        if (is_view_op(n->op) || bypass.count(n) || deferred.count(n) || gqa_skip.count(n) || n == mul0 || n == rope0)
+            continue;
         t1 = n;
         i1 = j;
         break;
@@ -1332,7 +1532,23 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
         }
     }
     if (!F || !supports_op(be->dev, F)) return false;
-    const ggml_tensor *sk = F->src[1], *sv = F->src[2];
+    // the cache write an attention operand reads: the SET_ROWS itself, or
+    // through a GQA expansion that is not launched (its source a reshape of
+    // the SET_ROWS with the write's own layout)
+    auto set_rows_of = [&](const ggml_tensor * x) -> const ggml_tensor * {
+        if (x->op == GGML_OP_SET_ROWS) return x;
+        tview v;
+        if (!gqa_fold(x, v)) return nullptr;
+        const ggml_tensor * src = (x->view_src ? x->view_src : x)->src[0];
+        if (src->op != GGML_OP_RESHAPE && src->op != GGML_OP_VIEW) return nullptr;
+        const ggml_tensor * sr = src->src[0];
+        if (!sr || sr->op != GGML_OP_SET_ROWS || sr->data != v.data || sr->ne[3] != 1 || v.ne[1] != sr->ne[1] ||
+            v.ne[2] != sr->ne[2] || v.nb[1] != (int64_t) sr->nb[1] || v.nb[2] != (int64_t) sr->nb[2])
+            return nullptr;
+        return sr;
+    };
+    const ggml_tensor *sk = set_rows_of(F->src[1]), *sv = set_rows_of(F->src[2]);
+    if (!sk || !sv) return false;
     if (sk->op != GGML_OP_SET_ROWS || sv->op != GGML_OP_SET_ROWS || sk->src[1] != sv->src[1]) return false;
     if (sk->type != GGML_TYPE_F16 || sv->type != GGML_TYPE_F16 || root_of(sk->src[0]) != rope1) return false;
     const ggml_tensor *qv = F->src[0], *kn = sk->src[0], *vn = sv->src[0], *idx = sk->src[1];
@@ -1352,7 +1568,7 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     if (j0.a.ne[3] != 1 || j1.a.ne[3] != 1 || j0.a.nb[0] != 4 || j1.a.nb[0] != 4) return false;
     fattn_args fa;
     if (!make_fattn(F, fa)) return false;
-    if (!attn_step_supported(fa) || F->src[1] != sk || F->src[2] != sv) return false;
+    if (!attn_step_supported(fa)) return false;
     // nothing else runs between the first norm and the attention, and nothing
     // outside the fused nodes reads their intermediate results
     const ggml_tensor * fused[] = {t, mul0, rope0, t1, mul1, rope1, sk, sv, F};
@@ -1363,12 +1579,12 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     };
     for (int j = i + 1; j <= iF; j++) {
         const ggml_tensor * n = cg->nodes[j];
-        if (is_view_op(n->op) || bypass.count(n) || in_fused(n)) continue;
+        if (is_view_op(n->op) || bypass.count(n) || in_fused(n) || gqa_skip.count(n)) continue;
         return false;
     }
     for (int j = i + 1; j < cg->n_nodes; j++) {
         const ggml_tensor * n = cg->nodes[j];
-        if (is_view_op(n->op) || in_fused(n)) continue;
+        if (is_view_op(n->op) || in_fused(n) || gqa_skip.count(n)) continue;
         for (int k = 0; k < GGML_MAX_SRC; k++) {
             const ggml_tensor * x = n->src[k];
             if (!x) continue;
@@ -1474,6 +1690,39 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
     return true;
 }
 
+// One launch for a fused attention chain (find_naive), at its output CONT.
+// If the output's bytes overlap what the launch reads (an allocator may
+// place it over the query rows, which are dead after the scores product),
+// the launch writes to scratch and a copy moves the rows.
+bool planner::plan_naive(int i, const ggml_tensor * t) {
+    (void) i;
+    const naive_job & j = naive_jobs.at(t);
+    const naive_attn_args a = j.a;
+    const span o = span_of(t);
+    bool clash = false;
+    for (const auto & r : j.reads) clash = clash || overlap(o, r.first);
+    const size_t work = attn_naive_scratch_bytes(a);
+    const size_t out_off = align_up(work, kAlign);
+    gen_need = std::max(gen_need, out_off + (clash ? (size_t) ggml_nbytes(t) : 0));
+    const tview dv = make_view(t);
+    backend_state * b = be;
+    const int ncu = n_cu;
+    add_step(
+        [=](hipStream_t s) {
+            naive_attn_args la = a;
+            char * g = gen_base(b);
+            if (clash) la.out = (float *) (g + out_off);
+            launch_attn_naive(la, (float *) g, s);
+            if (clash) {
+                tview sv = dv;
+                sv.data = g + out_off;
+                launch_copy(dv, GGML_TYPE_F32, sv, GGML_TYPE_F32, s, ncu);
+            }
+        },
+        t, "attn_naive");
+    return true;
+}
+
 // The plan moves reads later than the graph has them in two places: a
 // bypassed CONT's readers read its source at their own positions, and a
 // deferred unary node reads its source at its consumer's position. Under an
@@ -1508,12 +1757,39 @@ bool planner::validate() {
             ok = false;
         }
     }
+    // an expansion not launched: its readers read the source later than the
+    // REPEAT would have
+    for (const fold_read & fr : fold_reads) {
+        if (written_between(fr.src, fr.from, fr.to - 1, false)) {
+            no_fold.insert(fr.rep);
+            ok = false;
+        }
+    }
+    // a fused attention chain reads its operands at its output's position
+    for (const auto & nj : naive_jobs) {
+        const int at = index.at(nj.first);
+        for (const auto & r : nj.second.reads) {
+            if (written_between(r.first, r.second, at - 1, false)) {
+                no_naive.insert(nj.first);
+                ok = false;
+                break;
+            }
+        }
+    }
     return ok;
 }
 
 bool planner::plan() {
     count_uses();
     find_bypass();
+    find_naive();
+    find_gqa_skip();
+    if (naive_dropped) {
+        // a chain dropped after the expansions were decided: decide again without it
+        replan = true;
+        error = "an attention chain's K and V expansions fold differently";
+        return false;
+    }
     for (int i = 0; i < cg->n_nodes; i++) {
         const ggml_tensor * t = cg->nodes[i];
         cur = i;
@@ -1522,6 +1798,17 @@ bool planner::plan() {
         if (t->op != GGML_OP_MUL_MAT && !deferred.count(t)) {
             for (int k = 0; k < GGML_MAX_SRC; k++)
                 if (t->src[k] && reads_unwritten(t, t->src[k])) return false;
+        }
+        if (gqa_skip.count(t) || naive_nodes.count(t)) continue;  // read through its source / part of a fused chain
+        // a read of an expansion that is not launched must fold into the reader
+        for (int k = 0; k < GGML_MAX_SRC; k++) {
+            const ggml_tensor * x = t->src[k];
+            if (!x || !gqa_skip.count(root_of(x))) continue;
+            tview v;
+            if (t->op == GGML_OP_FLASH_ATTN_EXT && (k == 1 || k == 2) && gqa_fold(x, v)) continue;
+            no_fold.insert(root_of(x));
+            replan = true;
+            return fail(t, "reads a GQA expansion that is not launched");
         }
         if (bypass.count(t)) continue;  // readers take the CONT's source directly
         auto dit = deferred.find(t);
@@ -1605,9 +1892,19 @@ bool planner::plan() {
                 add_step([=](hipStream_t s) { launch_get_rows(dv, sv, stype, iv, s, ncu); }, t, "get_rows");
                 break;
             }
+            case GGML_OP_REPEAT: {
+                const tview dv = make_view(t), sv = view_of(t->src[0]);
+                const int es = (int) ggml_type_size(t->type);
+                add_step([=](hipStream_t s) { launch_repeat(dv, sv, es, s, ncu); }, t, "repeat");
+                break;
+            }
             case GGML_OP_CPY:
             case GGML_OP_CONT:
             case GGML_OP_DUP: {
+                if (naive_jobs.count(t)) {
+                    if (!plan_naive(i, t)) return false;
+                    continue;
+                }
                 const ggml_tensor * dst = t;
                 const tview dv = make_view(dst), av = view_of(t->src[0]);
                 const int dtype = dst->type, atype = t->src[0]->type;
@@ -1674,17 +1971,15 @@ bool planner::plan() {
 // plan cg, and plan again without the fusions validate() finds unsafe under
 // the graph's allocation (each pass removes at least one; they are few)
 std::unique_ptr<planner> make_plan(backend_state * be, const ggml_cgraph * cg, bool & ok) {
-    std::unordered_set<const ggml_tensor *> nb, nd, nv;
+    plan_exclusions x;
     for (int pass = 0; pass < 64; pass++) {
-        auto p = std::make_unique<planner>(be, cg, nb, nd, nv);
+        auto p = std::make_unique<planner>(be, cg, x);
         ok = p->plan();
         if (!ok && !p->replan) return p;
         if (ok && p->validate()) return p;
-        nb = p->no_bypass;
-        nd = p->no_defer;
-        nv = p->no_divert;
+        x = p->exclusions();
     }
-    auto p = std::make_unique<planner>(be, cg, nb, nd, nv);
+    auto p = std::make_unique<planner>(be, cg, x);
     ok = p->plan() && p->validate();
     if (!ok && p->error.empty()) p->error = "no safe plan for this allocation";
     return p;
@@ -2139,6 +2434,16 @@ bool supports_op(const device_state * dev, const ggml_tensor * t) {
             const int a = t->src[0]->type, d = t->type;
             auto ok = [](int ty) { return ty == GGML_TYPE_F32 || ty == GGML_TYPE_F16; };
             return (ok(a) && ok(d)) || (a == GGML_TYPE_I32 && d == GGML_TYPE_I32);
+        }
+        case GGML_OP_REPEAT: {
+            // the GQA K/V expansion (nn/decoder.rs:1799-1841) and any other
+            // tiling of 2- or 4-byte elements
+            const ggml_tensor * a = t->src[0];
+            const bool ty = a->type == t->type && (t->type == GGML_TYPE_F32 || t->type == GGML_TYPE_F16 ||
+                                                   t->type == GGML_TYPE_I32);
+            bool tiles = true;
+            for (int d = 0; d < 4; d++) tiles = tiles && a->ne[d] > 0 && t->ne[d] % a->ne[d] == 0;
+            return ty && tiles;
         }
         default:
             return false;

@@ -178,6 +178,40 @@ struct fattn_args {
     int qtype;
     act_buffers act;
 };
+// The unfused attention chain of the discrete-GPU prefill (MUL_MAT(K, Q) ->
+// SOFT_MAX_EXT -> MUL_MAT(CONT(V^T), P) -> PERMUTE/CONT) as one launch, in
+// the fixed order k_attn_naive.hip defines. Q f32 [d, n_q, hq, n_seq]
+// (strided), K / V f16 [d, n_kv, hkv, n_seq / rk3] rows (16-byte aligned),
+// mask f16 [>= n_kv, >= n_q, m_ne2, m_ne3] or null; out f32 [d, hq, n_q,
+// n_seq] contiguous. q_f32 / p_f32: GGML_PREC_F32 on the score / context
+// product (the operand stays f32), else it is rounded to f16.
+constexpr int kNaMaxChunks = 128;  // spans of up to 8192 positions
+struct naive_attn_args {
+    const char * q;
+    const char * k;
+    const char * v;
+    const char * mask;
+    int64_t q_nb1, q_nb2, q_nb3;
+    int64_t k_nb1, k_nb2, k_nb3;
+    int64_t v_nb1, v_nb2, v_nb3;
+    int64_t m_nb1, m_nb2, m_nb3;
+    int m_ne2, m_ne3;
+    int d, hq, hkv, n_q, n_kv, n_seq, rk3;
+    float scale;
+    int q_f32, p_f32;
+    float * out;
+    // set by the launcher
+    int qt;        // queries a workgroup owns (16 / (hq / hkv))
+    float * work;  // per workgroup 16 rows x the span rounded to 64, f32
+};
+bool attn_naive_supported(int d, int hq, int hkv, int64_t n_kv);
+size_t attn_naive_scratch_bytes(const naive_attn_args & a);
+void launch_attn_naive(const naive_attn_args & a, float * work, hipStream_t s);
+
+// REPEAT: dst [ne] filled from src with every index taken modulo src's
+// extent in that dim (elements of esize bytes)
+void launch_repeat(const tview & d, const tview & src, int esize, hipStream_t s, int n_cu);
+
 // One decode step of attention (D = 128): per-head RMS norm * w and NEOX
 // RoPE of the step's new query and key rows (taken from the fused QKV
 // projection), the new K/V rows written into the f16 caches at the set_rows

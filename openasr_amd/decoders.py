@@ -110,6 +110,7 @@ def lib() -> C.CDLL:
     s("oa_qwen_session_free", None, vp)
     s("oa_qwen_session_position", i, vp, i)
     s("oa_qwen_session_set_reversed_top1", None, vp, i)
+    s("oa_qwen_session_set_hip_lane", i, vp, i, i)
     s("oa_qwen_prefill_embeddings", i, vp, vp, i, vp)
     s("oa_qwen_prefill_tokens", i, vp, vp, i, vp)
     s("oa_qwen_decode_step", i, vp, vp, vp, vp)
@@ -291,6 +292,13 @@ class QwenSession:
     def set_reversed_top1(self, enable: bool = True):
         """greedy top-1 through the reversed-row GET_ROWS + ARGMAX graph"""
         lib().oa_qwen_session_set_reversed_top1(self.ptr, int(enable))
+
+    def set_hip_lane(self, enable: bool = True, prefill_chunk: int = 256):
+        """step graphs as the unmodified host builds them on a discrete-GPU
+        HIP backend: REPEAT-expanded K/V (expand_attention_kv), the unfused
+        attention chain for prefill chunks of more than two positions, even
+        prefill chunks of at most prefill_chunk positions (one sequence)"""
+        self._check(lib().oa_qwen_session_set_hip_lane(self.ptr, int(enable), int(prefill_chunk)), "set_hip_lane")
 
     def free(self):
         if self.ptr:

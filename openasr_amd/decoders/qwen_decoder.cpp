@@ -9,6 +9,13 @@
 //   fixed-span KV mask             nn/decoder.rs:2431-2463
 //   reusable decode graph          models/qwen/llm_transformer.rs:5169-5320
 //   fused logits + first-max top1  llm_transformer.rs:2096-2115
+//   HIP-lane graph (a session option): expand_attention_kv
+//   nn/decoder.rs:1799-1841 (native GQA Unsupported on HIP,
+//   ggml_runtime/cpu_graph.rs:736-757), llm_naive_masked_attention
+//   nn/decoder.rs:2154-2200 for prefill chunks of more than two queries over
+//   a span of more than 32 positions (llm_transformer.rs:7864-7877), its
+//   products at GGML_PREC_F32 (cpu_graph.rs:157-165, 202-228), even prefill
+//   widths (llm_transformer.rs:3186-3198, 7903-7911)
 // The batched logits head (one lm_head GEMV over every sequence, then a
 // first-max argmax) replaces the reference's per-slot logits graphs
 // (models/qwen/batched_decode.rs:961-975); its output is the same token.
@@ -126,6 +133,12 @@ struct oa_qwen_session {
     // instead of ARGMAX_FIRST; rev_idx holds vocab - 1 .. 0
     bool reversed_top1 = false;
     ggml_tensor * rev_idx = nullptr;
+    // the graph the host builds on a discrete-GPU HIP backend (one sequence):
+    // K/V expanded to the query heads by REPEAT, the unfused attention chain
+    // for wide prefill chunks, chunks of at most prefill_chunk positions
+    // trimmed to even widths
+    bool hip_lane = false;
+    int prefill_chunk = kPrefillChunk;
 };
 
 namespace {
@@ -157,7 +170,7 @@ ggml_tensor * rms_norm_mul(ggml_context * ctx, ggml_tensor * x, ggml_tensor * w,
 // llm_layer for token_count tokens of n_seq sequences (nn/decoder.rs:1850-2145)
 ggml_tensor * llm_layer(ggml_context * ctx, const oa_qwen_config & c, const qlayer_dev & L, ggml_tensor * hidden,
                         ggml_tensor * k_hist, ggml_tensor * v_hist, ggml_tensor * rows, ggml_tensor * pos,
-                        ggml_tensor * mask, int T, int n_seq, int max_pos) {
+                        ggml_tensor * mask, int T, int n_seq, int max_pos, bool hip_lane) {
     const int hd = c.head_dim, q_w = c.n_head * hd, kv_w = c.n_kv_head * hd;
     const int tokens = T * n_seq;
     ggml_tensor * normed = rms_norm_mul(ctx, hidden, L.attn_norm, c.rms_eps);
@@ -202,8 +215,31 @@ ggml_tensor * llm_layer(ggml_context * ctx, const oa_qwen_config & c, const qlay
     // write this step's K/V into the resident cache, attend over the full span
     ggml_tensor * k_full = ggml_set_rows(ctx, k_hist, k_new, rows);
     ggml_tensor * v_full = ggml_set_rows(ctx, v_hist, v_new, rows);
-    ggml_tensor * att = ggml_flash_attn_ext(ctx, q_fa, k_full, v_full, mask, 1.0f / std::sqrt((float) hd), 0.0f, 0.0f);
-    ggml_flash_attn_ext_set_prec(att, GGML_PREC_DEFAULT);
+    const int g = c.n_head / c.n_kv_head;
+    if (hip_lane && n_seq == 1 && g > 1) {
+        // expand_attention_kv: each kv head repeated for its query heads
+        k_full = ggml_reshape_4d(ctx, k_full, hd, max_pos, 1, c.n_kv_head);
+        v_full = ggml_reshape_4d(ctx, v_full, hd, max_pos, 1, c.n_kv_head);
+        k_full = ggml_repeat_4d(ctx, k_full, hd, max_pos, g, c.n_kv_head);
+        v_full = ggml_repeat_4d(ctx, v_full, hd, max_pos, g, c.n_kv_head);
+        k_full = ggml_reshape_3d(ctx, k_full, hd, max_pos, c.n_head);
+        v_full = ggml_reshape_3d(ctx, v_full, hd, max_pos, c.n_head);
+    }
+    const float scale = 1.0f / std::sqrt((float) hd);
+    ggml_tensor * att;
+    if (hip_lane && T > 2 && max_pos > 32) {
+        // llm_naive_masked_attention: scores, masked softmax, V^T, context
+        ggml_tensor * scores = ggml_mul_mat(ctx, k_full, q_fa);
+        ggml_mul_mat_set_prec(scores, GGML_PREC_F32);
+        ggml_tensor * probs = ggml_soft_max_ext(ctx, scores, mask, scale, 0.0f);
+        ggml_tensor * v_t = ggml_cont(ctx, ggml_transpose(ctx, v_full));
+        ggml_tensor * ctx_rows = ggml_mul_mat(ctx, v_t, probs);
+        ggml_mul_mat_set_prec(ctx_rows, GGML_PREC_F32);
+        att = ggml_cont(ctx, ggml_permute(ctx, ctx_rows, 0, 2, 1, 3));
+    } else {
+        att = ggml_flash_attn_ext(ctx, q_fa, k_full, v_full, mask, scale, 0.0f, 0.0f);
+        ggml_flash_attn_ext_set_prec(att, GGML_PREC_DEFAULT);
+    }
     att = ggml_reshape_2d(ctx, att, q_w, tokens);
     ggml_tensor * post_attn = ggml_add(ctx, hidden, ggml_mul_mat(ctx, L.o, att));
     // SwiGLU FFN with residual (nn/ffn.rs:64-91)
@@ -246,7 +282,7 @@ bool build_step(oa_qwen_session * s, step_graph & g, int T, bool emb) {
     ggml_set_input(g.mask);
     for (int l = 0; l < c.n_layers; l++) {
         state = llm_layer(g.ctx, c, m->layers[(size_t) l], state, s->k_cache[(size_t) l], s->v_cache[(size_t) l],
-                          g.rows, g.pos, g.mask, T, n_seq, s->max_pos);
+                          g.rows, g.pos, g.mask, T, n_seq, s->max_pos, s->hip_lane);
     }
     ggml_tensor * last = state;
     if (T > 1) {  // the last position of each sequence
@@ -475,16 +511,35 @@ void oa_qwen_session_free(oa_qwen_session * s) {
 
 int oa_qwen_session_position(const oa_qwen_session * s, int seq) { return s->n_past[(size_t) seq]; }
 
+int oa_qwen_session_set_hip_lane(oa_qwen_session * s, int enable, int prefill_chunk) {
+    // the host refuses more than one sequence on this lane
+    // (llm_transformer.rs:2444-2450)
+    if (enable && (s->n_seq != 1 || prefill_chunk < 1)) return GGML_STATUS_FAILED;
+    s->hip_lane = enable != 0;
+    s->prefill_chunk = enable ? prefill_chunk : kPrefillChunk;
+    s->decode.release();  // rebuilt with the lane's graph on the next step
+    return GGML_STATUS_SUCCESS;
+}
+
 void oa_qwen_session_set_reversed_top1(oa_qwen_session * s, int enable) {
     if (s->reversed_top1 == (enable != 0)) return;
     s->reversed_top1 = enable != 0;
     s->decode.release();  // rebuilt with the other head on the next step
 }
 
+// width of the next prefill chunk: at most the session's chunk; on the HIP
+// lane an odd width above one is trimmed by one, so every multi-token chunk
+// is even and a final single token follows (even_prefill_chunk_len,
+// llm_transformer.rs:7903-7911)
+static int chunk_width(const oa_qwen_session * s, int remaining) {
+    const int w = std::min(s->hip_lane ? s->prefill_chunk : kPrefillChunk, remaining);
+    return s->hip_lane && w > 1 && w % 2 == 1 ? w - 1 : w;
+}
+
 int oa_qwen_prefill_embeddings(oa_qwen_session * s, const float * emb, int T, int32_t * top1_out) {
     const int d = s->m->cfg.d_model, n_seq = s->n_seq;
-    for (int t0 = 0; t0 < T; t0 += kPrefillChunk) {
-        const int n = std::min(kPrefillChunk, T - t0);
+    for (int t0 = 0, n = 0; t0 < T; t0 += n) {
+        n = chunk_width(s, T - t0);
         std::vector<float> chunk((size_t) n * n_seq * d);
         for (int q = 0; q < n_seq; q++) {
             std::memcpy(chunk.data() + (size_t) q * n * d, emb + ((size_t) q * T + t0) * d, (size_t) n * d * 4);
@@ -497,8 +552,8 @@ int oa_qwen_prefill_embeddings(oa_qwen_session * s, const float * emb, int T, in
 
 int oa_qwen_prefill_tokens(oa_qwen_session * s, const int32_t * tokens, int T, int32_t * top1_out) {
     const int n_seq = s->n_seq;
-    for (int t0 = 0; t0 < T; t0 += kPrefillChunk) {
-        const int n = std::min(kPrefillChunk, T - t0);
+    for (int t0 = 0, n = 0; t0 < T; t0 += n) {
+        n = chunk_width(s, T - t0);
         std::vector<int32_t> chunk((size_t) n * n_seq);
         for (int q = 0; q < n_seq; q++) {
             std::memcpy(chunk.data() + (size_t) q * n, tokens + (size_t) q * T + t0, (size_t) n * 4);

@@ -120,6 +120,8 @@ def base() -> C.CDLL:
     _sig(lib, "ggml_reshape_2d", T, CTX, T, i64, i64)
     _sig(lib, "ggml_reshape_3d", T, CTX, T, i64, i64, i64)
     _sig(lib, "ggml_reshape_4d", T, CTX, T, i64, i64, i64, i64)
+    _sig(lib, "ggml_repeat", T, CTX, T, T)
+    _sig(lib, "ggml_repeat_4d", T, CTX, T, i64, i64, i64, i64)
     _sig(lib, "ggml_view_1d", T, CTX, T, i64, sz)
     _sig(lib, "ggml_view_2d", T, CTX, T, i64, i64, sz, sz)
     _sig(lib, "ggml_view_3d", T, CTX, T, i64, i64, i64, sz, sz, sz)

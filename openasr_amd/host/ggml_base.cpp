@@ -657,6 +657,31 @@ struct ggml_tensor * ggml_concat(struct ggml_context * ctx, struct ggml_tensor *
     return r;
 }
 
+// REPEAT: b's shape filled with copies of a (every dim of b a multiple of
+// a's), dst[i] = a[i mod a.ne] per dim
+struct ggml_tensor * ggml_repeat(struct ggml_context * ctx, struct ggml_tensor * a, struct ggml_tensor * b) {
+    GB_REQUIRE(ggml_can_repeat(a, b), "repeat: b's shape is not a multiple of a's");
+    ggml_tensor * r = ggml_new_tensor(ctx, a->type, GGML_MAX_DIMS, b->ne);
+    if (!r) return nullptr;
+    r->op = GGML_OP_REPEAT;
+    r->src[0] = a;
+    return r;
+}
+
+// REPEAT to an explicit shape (the GQA K/V expansion, nn/decoder.rs:1799-1841)
+struct ggml_tensor * ggml_repeat_4d(struct ggml_context * ctx, struct ggml_tensor * a, int64_t ne0, int64_t ne1,
+                                    int64_t ne2, int64_t ne3) {
+    const bool empty = ggml_nelements(a) == 0;
+    GB_REQUIRE(empty || (a->ne[0] > 0 && a->ne[1] > 0 && a->ne[2] > 0 && a->ne[3] > 0 && ne0 % a->ne[0] == 0 &&
+                         ne1 % a->ne[1] == 0 && ne2 % a->ne[2] == 0 && ne3 % a->ne[3] == 0),
+               "repeat_4d: the shape is not a multiple of the source's");
+    ggml_tensor * r = ggml_new_tensor_4d(ctx, a->type, ne0, ne1, ne2, ne3);
+    if (!r) return nullptr;
+    r->op = GGML_OP_REPEAT;
+    r->src[0] = a;
+    return r;
+}
+
 struct ggml_tensor * ggml_cont(struct ggml_context * ctx, struct ggml_tensor * a) {
     ggml_tensor * r = dup_tensor(ctx, a);
     if (!r) return nullptr;

@@ -908,6 +908,104 @@ static void fa_chunked5_one(const uint16_t * qh, const uint16_t * k, const uint1
     free(sc);
 }
 
+/* The unfused attention chain of llm_naive_masked_attention
+ * (crates/openasr-core/src/nn/decoder.rs:2154-2200), the attention the host
+ * emits on a discrete GPU for prefill chunks of more than two queries over a
+ * span of more than 32 positions (models/qwen/llm_transformer.rs:7864-7877):
+ *   S = MUL_MAT(K, Q)                  per (position t, query, head)
+ *   P = SOFT_MAX_EXT(S, mask, scale)   over the positions of a row
+ *   O = MUL_MAT(CONT(TRANSPOSE(V)), P), PERMUTE(0, 2, 1, 3), CONT
+ * GQA is MUL_MAT's batch broadcast: query head h reads kv head h / (Hq/Hkv),
+ * which is also what the REPEAT-expanded K/V of expand_attention_kv
+ * (nn/decoder.rs:1799-1841) hold. prec_f32: the GGML_PREC_F32 the host sets
+ * on both products for an F16 src0 with an F32 src1 on CUDA/HIP backends
+ * (ggml_runtime/cpu_graph.rs:157-165, 202-228, 3638-3686): Q and P stay f32;
+ * without it they are rounded to f16, as ggml-cpu converts src1 to an F16
+ * src0's vec_dot type. The arithmetic is defined as:
+ *   score: one f32 fused multiply-add chain over the dims in order,
+ *          acc = fma(k[d], q[d], acc) from +0; then s = acc * scale + mask
+ *          (two roundings, soft_max's scale then mask add); a masked (-inf)
+ *          position is -inf without its dot;
+ *   softmax: M = max s; e = exp(s - M) (the deterministic exp); the f64 sum
+ *          of e over each 64-position chunk by a pairwise tree (level k adds
+ *          neighbouring sums of 2^k positions, positions past the span add
+ *          +0), then of the chunk sums in chunk order from 0;
+ *          P = e * (float) (1 / sum);
+ *   context: out[d] = fma(P[t], v[t][d], out[d]) over t in order from +0
+ *          (terms with P = 0 are skipped: they leave a sum that is never -0
+ *          unchanged).
+ * out: [n_q][Hq][D], the CONT of the permuted context. */
+void ref_naive_attention(const float * q, int64_t q_stride_tok, int64_t q_stride_head, const uint16_t * k,
+                         const uint16_t * v, int64_t kv_stride_head, int64_t kv_stride_pos, const uint16_t * mask,
+                         int64_t mask_stride, float * out, int64_t D, int64_t n_q, int64_t Hq, int64_t Hkv,
+                         int64_t n_kv, float scale, int prec_f32, int n_threads) {
+    const int64_t group = Hq / Hkv, C = 64;
+    if (D % 8 != 0 || D > 512) abort();
+#ifdef _OPENMP
+    if (n_threads <= 0) n_threads = omp_get_max_threads();
+#else
+    (void) n_threads;
+#endif
+#pragma omp parallel for collapse(2) num_threads(n_threads) schedule(static)
+    for (int64_t iq = 0; iq < n_q; iq++) {
+        for (int64_t h = 0; h < Hq; h++) {
+            const int64_t kvh = h / group;
+            const uint16_t * kb = k + kvh * kv_stride_head;
+            const uint16_t * vb = v + kvh * kv_stride_head;
+            const uint16_t * mr = mask ? mask + iq * mask_stride : NULL;
+            const float * qr = q + iq * q_stride_tok + h * q_stride_head;
+            float qf[512];
+            for (int64_t d = 0; d < D; d++) qf[d] = prec_f32 ? qr[d] : ref_fp16_to_fp32(ref_fp32_to_fp16(qr[d]));
+            float * sc = (float *) malloc((size_t) (n_kv > 0 ? n_kv : 1) * sizeof(float));
+            float M = -INFINITY;
+            for (int64_t i0 = 0; i0 < n_kv; i0 += 8) {
+                const int n = n_kv - i0 < 8 ? (int) (n_kv - i0) : 8;
+                float mv[8];
+                int live = 0;
+                for (int j = 0; j < n; j++) {
+                    mv[j] = mr ? ref_fp16_to_fp32(mr[i0 + j]) : 0.0f;
+                    live |= mv[j] != -INFINITY;
+                }
+                float a[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+                if (live) fa5_dot8(kb + i0 * kv_stride_pos, kv_stride_pos, qf, D, n, a);
+                for (int j = 0; j < n; j++) {
+                    sc[i0 + j] = mv[j] == -INFINITY ? -INFINITY : a[j] * scale + mv[j];
+                    M = sc[i0 + j] > M ? sc[i0 + j] : M;
+                }
+            }
+            double sum = 0.0;
+            for (int64_t c0 = 0; c0 < n_kv; c0 += C) {
+                double tree[64];
+                for (int64_t j = 0; j < C; j++) {
+                    const int64_t t = c0 + j;
+                    if (t < n_kv) sc[t] = ref_expf_det(sc[t] - M);
+                    tree[j] = t < n_kv ? (double) sc[t] : 0.0;
+                }
+                for (int64_t w = 1; w < C; w <<= 1)
+                    for (int64_t j = 0; j < C; j += 2 * w) tree[j] = tree[j] + tree[j + w];
+                sum += tree[0];
+            }
+            const float inv = (float) (1.0 / sum);
+            float acc[512];
+            for (int64_t d = 0; d < D; d++) acc[d] = 0.0f;
+            for (int64_t t = 0; t < n_kv; t++) {
+                float p = sc[t] * inv;
+                if (!prec_f32) p = ref_fp16_to_fp32(ref_fp32_to_fp16(p));
+                if (p == 0.0f) continue;
+                const uint16_t * vr = vb + t * kv_stride_pos;
+                const __m256 p8 = _mm256_set1_ps(p);
+                for (int64_t d = 0; d < D; d += 8) {
+                    const __m256 vf = _mm256_cvtph_ps(_mm_loadu_si128((const __m128i *) (vr + d)));
+                    _mm256_storeu_ps(acc + d, _mm256_fmadd_ps(p8, vf, _mm256_loadu_ps(acc + d)));
+                }
+            }
+            float * o = out + (iq * Hq + h) * D;
+            for (int64_t d = 0; d < D; d++) o[d] = acc[d];
+            free(sc);
+        }
+    }
+}
+
 /* ggml_compute_forward_flash_attn_ext_f16_one_chunk restated: sequential
  * online softmax over KV positions, masked (-inf) positions skipped. */
 void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_head,
@@ -916,6 +1014,12 @@ void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_
                         float * out, int64_t D, int64_t n_q, int64_t Hq, int64_t Hkv, int64_t n_kv,
                         float scale, int fidelity, int n_threads) {
     const int64_t group = Hq / Hkv;
+    if (fidelity == 6 || fidelity == 7) {
+        /* the unfused chain in place of the fused op (6: GGML_PREC_F32) */
+        ref_naive_attention(q, q_stride_tok, q_stride_head, k, v, kv_stride_head, kv_stride_pos, mask, mask_stride,
+                            out, D, n_q, Hq, Hkv, n_kv, scale, fidelity == 6, n_threads);
+        return;
+    }
 #ifdef _OPENMP
     if (n_threads <= 0) n_threads = omp_get_max_threads();
 #else

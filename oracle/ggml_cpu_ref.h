@@ -128,12 +128,26 @@ int32_t ref_argmax_first(const float * x, int64_t n);
  * chain over dims in order (times scale, plus the mask value), l_c = l_c + p
  * and a_c = fma(p, V, a_c) in f32 over the chunk's live positions in order;
  * the chunk combine is fidelity 4's, in f64.
+ * fidelity=6 and 7 compute the unfused chain the host emits in its place
+ * (ref_naive_attention; 6 with GGML_PREC_F32 on its products, 7 without).
  */
 void ref_flash_attn_ext(const float * q, int64_t q_stride_tok, int64_t q_stride_head,
                         const uint16_t * k, const uint16_t * v, int64_t kv_stride_head,
                         int64_t kv_stride_pos, const uint16_t * mask, int64_t mask_stride,
                         float * out, int64_t D, int64_t n_q, int64_t Hq, int64_t Hkv, int64_t n_kv,
                         float scale, int fidelity, int n_threads);
+
+/*
+ * llm_naive_masked_attention (nn/decoder.rs:2154-2200): MUL_MAT(K, Q) ->
+ * SOFT_MAX_EXT(mask, scale) -> MUL_MAT(CONT(V^T), P) -> PERMUTE/CONT, same
+ * layouts as ref_flash_attn_ext; prec_f32: GGML_PREC_F32 on both products
+ * (Q and P kept f32), else Q and P rounded to f16. The order of every sum is
+ * fixed (see the definition in ggml_cpu_ref.c).
+ */
+void ref_naive_attention(const float * q, int64_t q_stride_tok, int64_t q_stride_head, const uint16_t * k,
+                         const uint16_t * v, int64_t kv_stride_head, int64_t kv_stride_pos, const uint16_t * mask,
+                         int64_t mask_stride, float * out, int64_t D, int64_t n_q, int64_t Hq, int64_t Hkv,
+                         int64_t n_kv, float scale, int prec_f32, int n_threads);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,7 @@ def lib() -> C.CDLL:
     s("ref_relu", f, f)
     s("ref_sincosf_det", None, f, vp, vp)
     s("ref_flash_attn_ext", None, vp, i64, i64, vp, vp, i64, i64, vp, i64, vp, i64, i64, i64, i64, i64, f, i, i)
+    s("ref_naive_attention", None, vp, i64, i64, vp, vp, i64, i64, vp, i64, vp, i64, i64, i64, i64, i64, f, i, i)
     _lib = L
     return L
 
@@ -185,6 +186,25 @@ def flash_attn(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16: np.ndarr
     return out
 
 
+def naive_attention(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16: np.ndarray | None, scale: float,
+                    prec_f32: bool = True, threads: int = 0) -> np.ndarray:
+    """The unfused attention chain (MUL_MAT(K, Q) -> SOFT_MAX_EXT -> MUL_MAT of
+    V^T by P -> PERMUTE/CONT, nn/decoder.rs:2154-2200) in the oracle's fixed
+    order; layouts as flash_attn. prec_f32: GGML_PREC_F32 on both products
+    (Q and P kept f32), else both rounded to f16. Returns [n_q, Hq, D] f32."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k16 = np.ascontiguousarray(k16, dtype=np.uint16)
+    v16 = np.ascontiguousarray(v16, dtype=np.uint16)
+    n_q, hq, d = q.shape
+    hkv, n_kv, _ = k16.shape
+    out = np.zeros((n_q, hq, d), dtype=np.float32)
+    m = None if mask16 is None else np.ascontiguousarray(mask16, dtype=np.uint16)
+    lib().ref_naive_attention(_p(q), hq * d, d, _p(k16), _p(v16), n_kv * d, d, None if m is None else _p(m),
+                              0 if m is None else m.shape[-1], _p(out), d, n_q, hq, hkv, n_kv, scale,
+                              int(bool(prec_f32)), threads)
+    return out
+
+
 # ------------------------------------------------------------ decoders ---
 
 class QwenDims(C.Structure):
@@ -235,6 +255,28 @@ class QwenRef:
 
     def step(self, token: int):
         return self.forward(self.embed([token]))
+
+    def prefill_hip_lane(self, x: np.ndarray, chunk: int):
+        """x [T, d] through the chunks of the unmodified host's HIP-lane
+        prefill (even widths of at most `chunk`, an odd width above one
+        trimmed by one, llm_transformer.rs:7903-7911): the unfused attention
+        chain with GGML_PREC_F32 (fidelity 6) for chunks of more than two
+        positions over a span of more than 32 (llm_transformer.rs:7864-7877),
+        the flash attention definition otherwise. Returns the last chunk's
+        (top1, logits)."""
+        t0, res = 0, None
+        keep = self.fidelity
+        try:
+            while t0 < len(x):
+                w = min(chunk, len(x) - t0)
+                if w > 1 and w % 2:
+                    w -= 1
+                self.fidelity = 6 if w > 2 and self.max_pos > 32 else keep
+                res = self.forward(x[t0:t0 + w])
+                t0 += w
+        finally:
+            self.fidelity = keep
+        return res
 
 
 class QwenRefBatch:

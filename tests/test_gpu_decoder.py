@@ -27,12 +27,17 @@ TINY = dict(d_model=256, n_layers=2, n_head=4, n_kv_head=2, head_dim=64, ffn=512
 
 
 def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed=7, check_logits=True, weights=None,
-             reversed_top1=False):
+             reversed_top1=False, hip_lane=None):
+    """hip_lane: a prefill chunk width to run the graphs the unmodified host
+    builds on its HIP lane (REPEAT-expanded K/V, the unfused attention chain
+    for wide prefill chunks), the oracle prefilling in the same chunks"""
     w = weights or D.QwenWeights(wtype, seed=seed, **shape)
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(n_seq, max_pos)
     if reversed_top1:
         sess.set_reversed_top1(True)
+    if hip_lane:
+        sess.set_hip_lane(True, hip_lane)
     wl = D.QwenWorkload("test", shape, wtype, n_seq, prefix, prompt, steps, max_pos)
     emb, toks = D.workload_inputs(wl, seed=seed + 1)
     t0 = time.time()
@@ -53,9 +58,14 @@ def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed
     max_dl, min_margin = 0.0, np.inf
     for s in range(n_seq):
         r = ref.QwenRef(w.cfg, table, max_pos, fa_fidelity=5)
-        if prefix:
-            r.forward(emb[s])
-        t, lg = r.forward(r.embed(toks[s]))
+        if hip_lane:
+            if prefix:
+                r.prefill_hip_lane(emb[s], hip_lane)
+            t, lg = r.prefill_hip_lane(r.embed(toks[s]), hip_lane)
+        else:
+            if prefix:
+                r.forward(emb[s])
+            t, lg = r.forward(r.embed(toks[s]))
         assert t == gpu_tokens[0, s], f"seq {s}: first token after prefill differs"
         for i in range(steps):
             t, lg = r.step(t)
@@ -117,6 +127,32 @@ def test_tiny_decoder_reversed_top1_head(gpu, ref, n_seq):
     run_pair(gpu, ref, TINY, g.Q4_K, n_seq, prefix=200, prompt=5, steps=24, max_pos=512, reversed_top1=True)
 
 
+@pytest.mark.parametrize("chunk", [256, 8])
+@pytest.mark.parametrize("wname", ["q8_0", "q4_K"])
+def test_tiny_decoder_hip_lane_graph(gpu, ref, wname, chunk):
+    """the graphs the unmodified host builds on its HIP lane at one sequence
+    (expand_attention_kv's REPEAT, the unfused attention chain for prefill
+    chunks of more than two positions, even chunk widths ending in a
+    one-position step): token-exact and KV-exact against the oracle
+    prefilling in the same chunks"""
+    wt = g.Q8_0 if wname == "q8_0" else g.Q4_K
+    print(f"tiny qwen hip lane {wname} chunk {chunk}", flush=True)
+    run_pair(gpu, ref, HEAD128, wt, 1, prefix=301, prompt=5, steps=24, max_pos=512, hip_lane=chunk)
+
+
+def test_hip_lane_refuses_batches(gpu):
+    """the host refuses more than one sequence on the HIP lane
+    (llm_transformer.rs:2444-2450); the session option does as well"""
+    w = D.QwenWeights(g.Q8_0, seed=3, **TINY)
+    model = D.QwenModel(w, gpu.backend)
+    sess = model.session(2, 64)
+    with pytest.raises(RuntimeError):
+        sess.set_hip_lane(True, 8)
+    sess.free()
+    model.free()
+    w.free()
+
+
 def test_batched_equals_serial(gpu):
     """n_seq=3 in one graph == three n_seq=1 sessions (nn/decoder.rs:3412-3520 invariant)"""
     w = D.QwenWeights(g.Q4_K, seed=3, **TINY)
@@ -144,6 +180,18 @@ def test_qwen3_06b_q8_0_batch1_first_64_steps(gpu, ref):
     """Qwen3-0.6B shape, Q8_0, 375-position N(0,1) prefix + 8 prompt tokens, batch 1"""
     print("qwen3-0.6b q8_0 b1", flush=True)
     run_pair(gpu, ref, D.QWEN3_06B, g.Q8_0, 1, prefix=375, prompt=8, steps=64, max_pos=1024, seed=1234)
+
+
+@pytest.mark.parametrize("chunk", [256, 8])
+def test_qwen3_06b_q8_0_batch1_hip_lane_first_64_steps(gpu, ref, chunk):
+    """the batch-1 configuration (Qwen3-0.6B shape, Q8_0, 375-position prefix
+    + 8 prompt tokens) through the graphs the unmodified host builds on its
+    HIP lane: prefill in even chunks of at most `chunk` positions over the
+    unfused attention chain, REPEAT-expanded K/V in every layer of every
+    step; 64 greedy steps token for token against the oracle, logits < 1e-2"""
+    print(f"qwen3-0.6b q8_0 b1, hip lane, prefill chunk {chunk}", flush=True)
+    run_pair(gpu, ref, D.QWEN3_06B, g.Q8_0, 1, prefix=375, prompt=8, steps=64, max_pos=1024, seed=1234,
+             hip_lane=chunk)
 
 
 def test_qwen3_06b_q8_0_batch1_reversed_top1_first_64_steps(gpu, ref):

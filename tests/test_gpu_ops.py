@@ -1360,3 +1360,140 @@ def test_naive_masked_attention_chain(ggml, gpu, ref, n_q, n_seq):
             assert rel_err(got[s, :, h], ctx) < 2e-3, (s, h)
     assert rel_err(got, fa) < 2e-3
     G.free()
+
+
+# ------------------------------------------- the HIP lane's GQA expansion --
+
+def hip_lane_kv(L, G, K, V, d, n_kv, hq, hkv):
+    """expand_attention_kv (nn/decoder.rs:1799-1841): RESHAPE [d, kv, 1, hkv],
+    REPEAT [d, kv, g, hkv], RESHAPE [d, kv, hq]"""
+    g = hq // hkv
+    out = []
+    for X in (K, V):
+        X = L.ggml_reshape_4d(G.ctx, X, d, n_kv, 1, hkv)
+        X = L.ggml_repeat_4d(G.ctx, X, d, n_kv, g, hkv)
+        out.append(L.ggml_reshape_3d(G.ctx, X, d, n_kv, hq))
+    return out
+
+
+def causal_mask(n_q, n_kv, live):
+    """query i at position live - n_q + i sees positions 0 .. that one"""
+    mask = np.full((n_q, n_kv), -np.inf, np.float16)
+    for i in range(n_q):
+        mask[i, :live - n_q + i + 1] = 0
+    return mask
+
+
+def plan_labels(gpu, G):
+    return [lab.split(":", 1)[0] for lab, _ in gpu.profile(G.gf, 1)]
+
+
+@pytest.mark.parametrize("n_kv,live", [(1024, 383), (1024, 1024), (4096, 3008)])
+@pytest.mark.parametrize("n_q", [8, 256])
+@pytest.mark.parametrize("prec_f32", [True, False])
+def test_naive_chain_over_repeat_expanded_kv(ggml, gpu, ref, n_kv, live, n_q, prec_f32):
+    """the prefill attention of the unmodified host's HIP lane: K/V of the
+    f16 caches expanded to the 16 query heads by RESHAPE / REPEAT / RESHAPE,
+    the unfused chain (nn/decoder.rs:2154-2200) over the whole span under the
+    causal mask, with GGML_PREC_F32 on both products as the host sets it for
+    a ROCm backend (cpu_graph.rs:157-165) or without. One launch: no REPEAT,
+    no scores or V^T in memory; bit for bit the oracle's chain"""
+    d, hq, hkv = 128, 16, 8
+    print(f"naive chain over expanded K/V: kv {n_kv} live {live} n_q {n_q} prec_f32 {prec_f32}", flush=True)
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = causal_mask(n_q, n_kv, live)
+    scale = 1.0 / math.sqrt(d)
+    G = ggml.Graph()
+    L = G.lib
+    Qs = G.new(ggml.F32, d, hq, n_q)  # the rotated query rows, [d, heads, tokens]
+    K = G.new(ggml.F16, d, n_kv, hkv, 1)
+    V = G.new(ggml.F16, d, n_kv, hkv, 1)
+    M = G.new(ggml.F16, n_kv, n_q, 1, 1)
+    Q = L.ggml_permute(G.ctx, L.ggml_reshape_4d(G.ctx, Qs, d, hq, n_q, 1), 0, 2, 1, 3)
+    Kx, Vx = hip_lane_kv(L, G, K, V, d, n_kv, hq, hkv)
+    scores = L.ggml_mul_mat(G.ctx, Kx, Q)
+    probs = L.ggml_soft_max_ext(G.ctx, scores, M, scale, 0.0)
+    vt = L.ggml_cont(G.ctx, L.ggml_transpose(G.ctx, Vx))
+    cx = L.ggml_mul_mat(G.ctx, vt, probs)
+    if prec_f32:
+        L.ggml_mul_mat_set_prec(scores, ggml.GGML_PREC_F32)
+        L.ggml_mul_mat_set_prec(cx, ggml.GGML_PREC_F32)
+    att = L.ggml_cont(G.ctx, L.ggml_permute(G.ctx, cx, 0, 2, 1, 3))
+    G.build(att)
+    G.allocate(gpu.buft)
+    G.set(Qs, q)
+    G.set(K, k.view(np.uint16))
+    G.set(V, v.view(np.uint16))
+    G.set(M, mask.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    got = G.get(att).reshape(n_q, hq, d)
+    want = ref.naive_attention(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale,
+                               prec_f32=prec_f32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rel_err(got, want)
+    # replayed (captured) computes give the same bits
+    assert G.compute(gpu.backend) == 0 and G.compute(gpu.backend) == 0
+    assert np.array_equal(G.get(att).reshape(n_q, hq, d).view(np.uint32), want.view(np.uint32))
+    labels = plan_labels(gpu, G)
+    assert "attn_naive" in labels and "repeat" not in labels, labels
+    assert not any(l.startswith("mul_mat") or l in ("soft_max", "copy") for l in labels), labels
+    G.free()
+
+
+@pytest.mark.parametrize("n_q", [1, 64])
+def test_flash_attn_ext_over_repeat_expanded_kv(ggml, gpu, n_q):
+    """FLASH_ATTN_EXT reading REPEAT-expanded K/V (the HIP lane's decode
+    attention) gives the bits of the same attention over the caches
+    themselves (native GQA), and the expansion is never launched"""
+    d, hq, hkv, n_kv, live = 128, 16, 8, 1024, 700
+    print(f"flash_attn_ext over expanded K/V n_q={n_q}", flush=True)
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = causal_mask(n_q, n_kv, live)
+    scale = 1.0 / math.sqrt(d)
+    outs = []
+    for expand in (False, True):
+        G = ggml.Graph()
+        L = G.lib
+        Qs = G.new(ggml.F32, d, hq, n_q)
+        K = G.new(ggml.F16, d, n_kv, hkv, 1)
+        V = G.new(ggml.F16, d, n_kv, hkv, 1)
+        M = G.new(ggml.F16, n_kv, n_q, 1, 1)
+        Q = L.ggml_permute(G.ctx, L.ggml_reshape_4d(G.ctx, Qs, d, hq, n_q, 1), 0, 2, 1, 3)
+        Kx, Vx = hip_lane_kv(L, G, K, V, d, n_kv, hq, hkv) if expand else (K, V)
+        O = L.ggml_flash_attn_ext(G.ctx, Q, Kx, Vx, M, scale, 0.0, 0.0)
+        G.build(O)
+        G.allocate(gpu.buft)
+        G.set(Qs, q)
+        G.set(K, k.view(np.uint16))
+        G.set(V, v.view(np.uint16))
+        G.set(M, mask.view(np.uint16))
+        assert G.compute(gpu.backend) == 0
+        outs.append(G.get(O).copy())
+        if expand:
+            assert "repeat" not in plan_labels(gpu, G)
+        G.free()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("tname", ["f32", "f16"])
+def test_repeat_materialised(ggml, gpu, tname):
+    """a REPEAT that is a graph output is launched: every dim tiled, equal to
+    numpy's tile of the source"""
+    typ, dt = (ggml.F32, np.float32) if tname == "f32" else (ggml.F16, np.float16)
+    print(f"repeat {tname}", flush=True)
+    x = RNG.standard_normal((2, 1, 3, 5)).astype(dt)  # [ne3, ne2, ne1, ne0]
+    G = ggml.Graph()
+    X = G.new(typ, 5, 3, 1, 2)
+    R = G.lib.ggml_repeat_4d(G.ctx, X, 10, 6, 4, 2)
+    G.build(R)
+    G.allocate(gpu.buft)
+    G.set(X, x if typ == ggml.F32 else x.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    got = G.get(R)
+    got = got if typ == ggml.F32 else got.view(np.float16)
+    assert np.array_equal(got.reshape(2, 4, 6, 10), np.tile(x, (1, 4, 2, 2)))
+    assert "repeat" in plan_labels(gpu, G)
+    G.free()

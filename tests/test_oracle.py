@@ -535,6 +535,121 @@ def test_flash_attn_f32_chunked_mode_brute_force(ref):
             assert np.array_equal(got[i, h], want), (i, h)
 
 
+@pytest.mark.parametrize("n_kv,holes", [(1, []), (64, []), (65, []), (300, [(30, 130)]),
+                                        (1000, [(0, 200), (640, 700)])])
+@pytest.mark.parametrize("prec_f32", [True, False])
+def test_naive_attention_against_textbook(ref, n_kv, holes, prec_f32):
+    """the unfused attention chain (MUL_MAT(K, Q) -> SOFT_MAX_EXT -> MUL_MAT of
+    V^T by P, nn/decoder.rs:2154-2200) against the f64 textbook: within f32
+    rounding with GGML_PREC_F32 (Q and P kept f32), within the f16 rounding
+    of Q and P without it; GQA by the batch broadcast equals explicitly
+    repeated K/V (what expand_attention_kv builds) bit for bit; garbage under
+    the mask changes nothing; a lone live position returns its V row"""
+    n_q, hq, hkv, d = 2, 4, 2, 128
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((n_q, n_kv), np.float16)
+    for a, b in holes:
+        mask[:, a:b] = -np.inf
+    scale = 1 / math.sqrt(d)
+    qq = q if prec_f32 else q.astype(np.float16).astype(np.float32)
+    want = textbook_attention(qq, k, v, mask, scale, hq // hkv)
+    got = ref.naive_attention(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), scale, prec_f32)
+    bar = 2e-6 if prec_f32 else 1e-3
+    assert np.abs(got - want).max() < bar * max(1.0, np.abs(want).max())
+    g = hq // hkv
+    kr, vr = np.repeat(k, g, axis=0), np.repeat(v, g, axis=0)
+    rep = ref.naive_attention(q, kr.view(np.uint16), vr.view(np.uint16), mask.view(np.uint16), scale, prec_f32)
+    assert np.array_equal(got.view(np.uint32), rep.view(np.uint32))
+    k2, v2 = k.copy(), v.copy()
+    for a, b in holes:
+        k2[:, a:b] = np.float16(60000)
+        v2[:, a:b] = np.float16(np.nan)
+    got2 = ref.naive_attention(q, k2.view(np.uint16), v2.view(np.uint16), mask.view(np.uint16), scale, prec_f32)
+    assert np.array_equal(got.view(np.uint32), got2.view(np.uint32))
+    one = np.full((1, n_kv), -np.inf, np.float16)
+    one[0, n_kv // 2] = 0
+    lone = ref.naive_attention(q[:1], k.view(np.uint16), v.view(np.uint16), one.view(np.uint16), scale, prec_f32)
+    for h in range(hq):
+        assert np.array_equal(lone[0, h], v[h // g, n_kv // 2].astype(np.float32))
+
+
+def _pairwise(xs):
+    """a 64-entry list summed by the pairwise tree (level k adds neighbouring
+    sums of 2^k entries), in f64"""
+    xs = list(xs)
+    w = 1
+    while w < len(xs):
+        for j in range(0, len(xs), 2 * w):
+            xs[j] = xs[j] + xs[j + w]
+        w *= 2
+    return xs[0]
+
+
+@pytest.mark.parametrize("prec_f32", [True, False])
+def test_naive_attention_brute_force(ref, prec_f32):
+    """the chain's fixed order, bit for bit, against a scalar restatement with
+    exact rational fused multiply-adds (one rounding each): score chains over
+    the dims in order, then * scale + mask; exp(s - max); the f64 sum of each
+    64-position chunk by the pairwise tree, the chunk sums in order; P = e *
+    (1 / sum) in f32 (rounded to f16 without GGML_PREC_F32); context chains
+    over the positions in order. Two chunks, masked holes, a row whose first
+    position carries a finite mask value. A planted mistake differs: with
+    GGML_PREC_F32 an unfused score chain (product, then add: two roundings;
+    without it the f16 operands' products are exact and the two agree), and
+    without it P left unrounded."""
+    L = ref.lib()
+    n_q, hq, hkv, n_kv, d = 2, 2, 1, 70, 16
+    q = RNG.standard_normal((n_q, hq, d)).astype(np.float32)
+    k = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((n_q, n_kv), np.float16)
+    mask[0, 5:9] = -np.inf
+    mask[1, 60:66] = -np.inf
+    mask[1, 0] = np.float16(-1.5)
+    scale = np.float32(0.3)
+    got = ref.naive_attention(q, k.view(np.uint16), v.view(np.uint16), mask.view(np.uint16), float(scale), prec_f32)
+    kf, vf = k.astype(np.float32), v.astype(np.float32)
+    planted_differs = False
+    for i in range(n_q):
+        for h in range(hq):
+            qv = q[i, h] if prec_f32 else q[i, h].astype(np.float16).astype(np.float32)
+            s, s_unfused = {}, {}
+            for j in range(n_kv):
+                if mask[i, j] == -np.inf:
+                    continue
+                acc, acc2 = 0.0, np.float32(0)
+                for t in range(d):
+                    acc = _fma32(float(kf[0, j, t]), float(qv[t]), acc)
+                    acc2 = np.float32(acc2 + np.float32(kf[0, j, t] * qv[t]))
+                s[j] = np.float32(np.float32(acc) * scale) + np.float32(mask[i, j])
+                s_unfused[j] = np.float32(acc2 * scale) + np.float32(mask[i, j])
+            planted_differs |= any(s[j] != s_unfused[j] for j in s)
+            M = max(s.values())
+            e = [np.float32(L.ref_expf_det(float(np.float32(s[j] - M)))) if j in s else np.float32(0)
+                 for j in range(n_kv)]
+            total = 0.0
+            for c0 in range(0, n_kv, 64):
+                total = total + _pairwise([float(e[j]) if j < n_kv else 0.0 for j in range(c0, c0 + 64)])
+            inv = np.float32(1.0 / total)
+            out, out_p32 = [0.0] * d, [0.0] * d
+            for j in range(n_kv):
+                p = np.float32(e[j] * inv)
+                if p != 0:
+                    out_p32 = [_fma32(float(p), float(vf[0, j, t]), out_p32[t]) for t in range(d)]
+                if not prec_f32:
+                    p = np.float32(np.float16(p))
+                if p == 0:
+                    continue
+                out = [_fma32(float(p), float(vf[0, j, t]), out[t]) for t in range(d)]
+            want = np.array(out, np.float32)
+            assert np.array_equal(got[i, h].view(np.uint32), want.view(np.uint32)), (i, h)
+            if not prec_f32:
+                planted_differs |= not np.array_equal(np.array(out_p32, np.float32), want)
+    assert planted_differs
+
+
 def test_whisper_cross_kv_matches_brute_force(ref):
     """the oracle's cross K/V precompute (K = Wk enc, V = Wv enc + bv, f16)
     against an f64 product of the dequantized weight with the Q8_0-quantized
