@@ -399,46 +399,62 @@ def cpu_description() -> dict:
 
 
 def cpu_baseline(w, wl, sess, tokens, seconds: float, variants: bool = True):
-    """The CPU oracle's batched decode step (oracle/ref_decoder.c, the checker)
-    on the host cores, continuing from the device's KV state: a bounded sample
-    of the same workload, timed for ~`seconds`."""
+    """The CPU baseline: the batched decode step of the same workload on the
+    host cores, continuing from the device's KV state, for a bounded sample of
+    ~`seconds`. The timed leg is the ggml-cpu-class restatement
+    (oracle/cpu_fast.c: int8 block dots in SIMD registers -- AVX-512 VNNI
+    where the host has it -- with f32 block accumulation, ggml-cpu's f16 V
+    accumulator, rows split over the threads) on every usable core, then on
+    the reference's decoder thread policy (available / 2, at least 2,
+    ggml_runtime/cpu_graph.rs:511-524) and on one thread. The oracle's own
+    step (f64 block sums, the checker) is timed beside it for reference."""
     from oracle import ref
 
     threads = usable_cpus()
-    r = ref.QwenRefBatch(w.cfg, w.pointer_table(), wl.max_positions, wl.n_seq, threads=threads)
-    for s in range(wl.n_seq):
-        for layer in range(wl.shape["n_layers"]):
-            k, v = sess.read_kv(layer, s)
-            r.k[s][layer][...] = k
-            r.v[s][layer][...] = v
-        r.pos[s] = sess.position(s)
-    start = int(r.pos.min())
-    cur = np.asarray(tokens, np.int32)
+    legs = {"fast": ref.QwenFastBatch(w.cfg, w.pointer_table(), wl.max_positions, wl.n_seq, threads=threads),
+            "oracle": ref.QwenRefBatch(w.cfg, w.pointer_table(), wl.max_positions, wl.n_seq, threads=threads)}
+    for r in legs.values():
+        for s in range(wl.n_seq):
+            for layer in range(wl.shape["n_layers"]):
+                k, v = sess.read_kv(layer, s)
+                r.k[s][layer][...] = k
+                r.v[s][layer][...] = v
+            r.pos[s] = sess.position(s)
+    start = int(legs["fast"].pos.min())
+    cur = {name: np.asarray(tokens, np.int32) for name in legs}
 
-    def timed(th: int, budget: float):
+    def timed(name: str, th: int, budget: float):
+        r = legs[name]
         r.threads = th
-        nonlocal cur
         n = 0
         t0 = time.perf_counter()
         while time.perf_counter() - t0 < budget and r.pos.max() < wl.max_positions - 1:
-            cur = r.step(cur)
+            cur[name] = r.step(cur[name])
             n += 1
         dt = time.perf_counter() - t0
         return n, dt, wl.n_seq * n / max(dt, 1e-9)
 
-    n, dt, val = timed(threads, seconds)
-    log(f"[bench] cpu oracle: {n} batched decode steps in {dt:.1f}s on {threads} threads = {val:.2f} tokens/s")
+    n, dt, val = timed("fast", threads, seconds)
+    isa = "AVX-512 VNNI" if ref.fast_uses_vnni() else "AVX2"
+    log(f"[bench] cpu ggml-cpu-class restatement ({isa}): {n} batched decode steps in {dt:.1f}s on {threads} threads "
+        f"= {val:.2f} tokens/s")
     res = {"value": round(val, 3), "unit": "tokens/s", "cores": threads, "kind": "port",
-           "sample": f"{n} batched decode steps of {wl.name} (oracle ref_qwen_decode_batch, {threads} OpenMP "
-                     f"threads) continuing from the device KV state at position {start}",
+           "label": "ggml-cpu-class restatement",
+           "sample": f"{n} batched decode steps of {wl.name} (oracle/cpu_fast.c fast_qwen_decode_batch: {isa} int8 "
+                     f"block dots with f32 block sums, f16 V accumulator, {threads} OpenMP threads) continuing from "
+                     f"the device KV state at position {start}",
            "cpu": cpu_model(), "host": cpu_description()}
     if variants:
-        # the reference's decoder thread policy (available / 2, at least 2) and one thread, shorter samples
         half = max(2, threads // 2)
-        _, _, val2 = timed(half, seconds / 3)
-        _, _, val1 = timed(1, seconds / 3)
-        log(f"[bench] cpu oracle: {val2:.2f} tokens/s on {half} threads, {val1:.2f} tokens/s on 1 thread")
+        _, _, val2 = timed("fast", half, seconds / 3)
+        _, _, val1 = timed("fast", 1, seconds / 3)
+        log(f"[bench] cpu ggml-cpu-class restatement: {val2:.2f} tokens/s on {half} threads, {val1:.2f} tokens/s on "
+            "1 thread")
         res.update(tokens_per_s_half_threads=round(val2, 3), half_threads=half, tokens_per_s_1_thread=round(val1, 3))
+    no, dto, valo = timed("oracle", threads, seconds / 3)
+    log(f"[bench] cpu oracle (checker, f64 block sums): {no} steps in {dto:.1f}s on {threads} threads = {valo:.2f} "
+        "tokens/s")
+    res["oracle_tokens_per_s"] = round(valo, 3)
     return res
 
 

@@ -313,6 +313,69 @@ class QwenRefBatch:
         return (top1, logits) if want_logits else top1
 
 
+class QwenFastBatch(QwenRefBatch):
+    """The benchmark's CPU baseline leg (oracle/cpu_fast.c): the same batched
+    decode step with ggml-cpu's arithmetic classes on the host ISA (VNNI or
+    AVX2 int8 block dots with f32 accumulation, f16 V accumulator in
+    attention). Not the checker: tests/test_cpu_fast.py holds it to the
+    oracle within float tolerance."""
+
+    def __init__(self, cfg, pointer_table, max_pos: int, n_seq: int, threads: int = 0):
+        super().__init__(cfg, pointer_table, max_pos, n_seq, threads=threads)
+        L = lib()
+        L.fast_qwen_decode_batch.restype = None
+        L.fast_qwen_decode_batch.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_int, C.c_void_p,
+                                             C.c_void_p, C.c_int, C.c_void_p, C.c_void_p, C.c_int]
+
+    def step(self, tokens, want_logits: bool = False):
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        top1 = np.zeros(self.n_seq, np.int32)
+        logits = np.zeros((self.n_seq, self.dims.vocab), np.float32) if want_logits else None
+        pos = np.ascontiguousarray(self.pos, dtype=np.int32)
+        lib().fast_qwen_decode_batch(C.byref(self.dims), self.table, self.kp, self.vp, self.max_pos,
+                                     tokens.ctypes.data, pos.ctypes.data, self.n_seq, top1.ctypes.data,
+                                     logits.ctypes.data if want_logits else None, self.threads)
+        self.pos += 1
+        return (top1, logits) if want_logits else top1
+
+
+def fast_uses_vnni() -> bool:
+    L = lib()
+    L.fast_cpu_uses_vnni.restype = C.c_int
+    return bool(L.fast_cpu_uses_vnni())
+
+
+def fast_mul_mat(wtype: int, w_bytes: np.ndarray, m: int, k: int, x: np.ndarray, threads: int = 0) -> np.ndarray:
+    """the baseline leg's MUL_MAT: [n, m] f32 from weights of wtype and x [n, k]"""
+    L = lib()
+    L.fast_mul_mat.restype = None
+    i64 = C.c_int64
+    L.fast_mul_mat.argtypes = [C.c_int, C.c_void_p, C.c_size_t, i64, i64, C.c_void_p, i64, i64, C.c_void_p, i64,
+                               C.c_int]
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w_bytes = np.ascontiguousarray(w_bytes)
+    n = x.shape[0]
+    out = np.zeros((n, m), np.float32)
+    L.fast_mul_mat(wtype, w_bytes.ctypes.data, row_size(wtype, k), m, k, x.ctypes.data, k, n, out.ctypes.data, m,
+                   threads)
+    return out
+
+
+def fast_attn_one(q: np.ndarray, k16: np.ndarray, v16: np.ndarray, mask16, scale: float) -> np.ndarray:
+    """the baseline leg's decode attention for one query row: q [D] f32, k16 /
+    v16 [n_kv, D] f16 bits, mask16 [n_kv] f16 bits or None"""
+    L = lib()
+    L.fast_attn_one.restype = None
+    L.fast_attn_one.argtypes = [C.c_void_p] * 4 + [C.c_int64, C.c_int64, C.c_float, C.c_void_p]
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k16 = np.ascontiguousarray(k16, dtype=np.uint16)
+    v16 = np.ascontiguousarray(v16, dtype=np.uint16)
+    m = None if mask16 is None else np.ascontiguousarray(mask16, dtype=np.uint16)
+    out = np.zeros(q.shape[-1], np.float32)
+    L.fast_attn_one(_p(q), _p(k16), _p(v16), None if m is None else _p(m), k16.shape[0], q.shape[-1], scale, _p(out))
+    return out
+
+
 class WhisperDims(C.Structure):
     _fields_ = [("d_model", C.c_int), ("n_layers", C.c_int), ("n_head", C.c_int), ("ffn", C.c_int),
                 ("vocab", C.c_int), ("max_positions", C.c_int), ("n_frames", C.c_int), ("ln_eps", C.c_float),
