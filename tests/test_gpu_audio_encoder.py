@@ -137,6 +137,31 @@ def test_audio_encoder_matches_reference(gpu, wname):
 
 
 @pytest.mark.gpu
+@pytest.mark.parametrize("wname", ["f32", "f16", "q8_0"])
+def test_full_size_audio_encoder_matches_reference(gpu, wname):
+    """the Qwen3-ASR-0.6B-shaped encoder the bench times (18 layers of 896,
+    14 heads, FFN 3584, 128 mel bins, 480 conv channels, 1024 outputs) over
+    three chunks, the last one partial, against the checker (pinned against
+    an independent textbook encoder in tests/test_oracle_audio_encoder.py),
+    each projection type to its bar"""
+    from oracle import audio_encoder as RA
+    wt = {"f32": g.F32, "f16": g.F16, "q8_0": g.Q8_0}[wname]
+    print(f"full-size qwen audio encoder {wname}", flush=True)
+    shape = D.QWEN3_06B_AUDIO
+    w = D.QwenAudioWeights(wt, seed=21, **shape)
+    enc = D.QwenAudioEncoder(w, gpu.backend)
+    mel = mel_input(shape["n_mels"], 250, 8)
+    got, ms = enc.encode(mel)
+    want = RA.encode(w, mel)
+    err = rel_err(got, want)
+    print(f"  rows {got.shape[0]}, {ms:.2f} ms, rel err {err:.2e}", flush=True)
+    assert got.shape == want.shape == (39, shape["out_dim"])
+    assert err < {"f32": 1e-5, "f16": 2e-3, "q8_0": 2e-2}[wname]
+    enc.free()
+    w.free()
+
+
+@pytest.mark.gpu
 def test_runtime_pack_encodes_like_synthesized(gpu, tmp_path):
     """the encoder bound from a qwen3-asr pack (f32 conv kernels, F16
     projections) gives the same bits as the synthesised weights it was
