@@ -421,10 +421,15 @@ def cpu_baseline(w, wl, sess, tokens, seconds: float, variants: bool = True):
                 r.v[s][layer][...] = v
             r.pos[s] = sess.position(s)
     start = int(legs["fast"].pos.min())
+    pos0 = {name: r.pos.copy() for name, r in legs.items()}
     cur = {name: np.asarray(tokens, np.int32) for name in legs}
 
     def timed(name: str, th: int, budget: float):
+        # every sample starts at the device's position (the cache rows past it
+        # are rewritten), so each thread count decodes the same span
         r = legs[name]
+        r.pos[...] = pos0[name]
+        cur[name] = np.asarray(tokens, np.int32)
         r.threads = th
         n = 0
         t0 = time.perf_counter()
