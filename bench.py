@@ -505,7 +505,7 @@ def sweep_mul_mat(plugin, g, M, K, wtype, N, reps):
                 tops=2.0 * M * K * N / dt / 1e12)
 
 
-def sweep_fattn(plugin, g, n_kv, n_q, reps, d=128, hq=16, hkv=8):
+def sweep_fattn(plugin, g, n_kv, n_q, reps, d=128, hq=16, hkv=8, prec=0):
     kv_bytes = 2 * n_kv * hkv * d * 2
     copies = max(1, min(256, int(ROTATE_BYTES // kv_bytes)))
     rng = np.random.default_rng(7)
@@ -521,6 +521,8 @@ def sweep_fattn(plugin, g, n_kv, n_q, reps, d=128, hq=16, hkv=8):
     Ks = [G.new(g.F16, d, n_kv, hkv, 1, weight=True) for _ in range(copies)]
     Vs = [G.new(g.F16, d, n_kv, hkv, 1, weight=True) for _ in range(copies)]
     outs = [G.lib.ggml_flash_attn_ext(G.ctx, Q, Ks[i], Vs[i], Mk, 1.0 / np.sqrt(d), 0.0, 0.0) for i in range(copies)]
+    for o in outs:
+        G.lib.ggml_flash_attn_ext_set_prec(o, prec)
     G.build(*outs)
     G.allocate(plugin.buft)
     for i in range(copies):
@@ -531,7 +533,8 @@ def sweep_fattn(plugin, g, n_kv, n_q, reps, d=128, hq=16, hkv=8):
     dt = _timed_graph(G, plugin.backend, reps) / copies
     G.free()
     alg = kv_bytes + 2 * hq * n_q * d * 4 + n_q * n_kv * 2
-    return dict(op="flash_attn_ext", D=d, hq=hq, hkv=hkv, n_kv=n_kv, n_q=n_q, copies=copies, us=dt * 1e6,
+    return dict(op="flash_attn_ext", prec="f32" if prec == g.GGML_PREC_F32 else "default", D=d, hq=hq, hkv=hkv,
+                n_kv=n_kv, n_q=n_q, copies=copies, us=dt * 1e6,
                 gbs=alg / dt / 1e9, frac_hbm=alg / dt / 1e9 / HBM_PEAK_GBS,
                 tflops=4.0 * hq * n_q * n_kv * d / dt / 1e12)
 
@@ -539,7 +542,8 @@ def sweep_fattn(plugin, g, n_kv, n_q, reps, d=128, hq=16, hkv=8):
 def run_sweep(reps: int) -> int:
     """mul_mat on Q8_0/Q4_K weights M x K in {1024^2, 3072x1024, 1024x3072,
     151936x1024} for N in {1, 8, 64, 512}, and flash_attn_ext (16 query /
-    8 kv heads, D 128, f16 KV of {512, 2048, 8192} positions, q_len {1, 64}).
+    8 kv heads, D 128, f16 KV of {512, 2048, 8192} positions, q_len {1, 64,
+    256}; several queries at both precision contracts).
     Operands are rotated over copies totalling more than the 256 MB cache, so
     the rates are HBM rates. One JSON line per case."""
     from openasr_amd import ggml as g
@@ -553,10 +557,11 @@ def run_sweep(reps: int) -> int:
                     f"{r['gbs']:8.1f} GB/s ({r['frac_hbm']:.1%} HBM)  {r['tops']:7.2f} TOP/s")
                 print(json.dumps(r), flush=True)
     for n_kv in (512, 2048, 8192):
-        for n_q in (1, 64):
-            r = sweep_fattn(plugin, g, n_kv, n_q, reps)
-            log(f"[sweep] flash_attn_ext kv={n_kv:<5} q={n_q:<3} {r['us']:9.2f} us  {r['gbs']:8.1f} GB/s "
-                f"({r['frac_hbm']:.1%} HBM)  {r['tflops']:7.2f} TFLOP/s")
+        for n_q, prec in ((1, g.GGML_PREC_DEFAULT), (64, g.GGML_PREC_DEFAULT), (64, g.GGML_PREC_F32),
+                          (256, g.GGML_PREC_DEFAULT), (256, g.GGML_PREC_F32)):
+            r = sweep_fattn(plugin, g, n_kv, n_q, reps, prec=prec)
+            log(f"[sweep] flash_attn_ext {r['prec']:>7} kv={n_kv:<5} q={n_q:<3} {r['us']:9.2f} us  "
+                f"{r['gbs']:8.1f} GB/s ({r['frac_hbm']:.1%} HBM)  {r['tflops']:7.2f} TFLOP/s")
             print(json.dumps(r), flush=True)
     return 0
 

@@ -134,6 +134,17 @@ void oa_qwen_session_set_reversed_top1(oa_qwen_session * s, int enable);
  * GGML_STATUS_FAILED. Takes effect on the next step. */
 int oa_qwen_session_set_hip_lane(oa_qwen_session * s, int enable, int prefill_chunk);
 
+/* The precision contract of the self-attention's FLASH_ATTN_EXT
+ * (set_flash_attention_precision, models/qwen/llm_transformer.rs:3044-3053;
+ * GgmlFlashAttentionPrecision, ggml_runtime/cpu_graph.rs:122-155):
+ * GGML_PREC_DEFAULT (the default, what the ASR decoder builds) lets the
+ * backend take its fastest validated form -- prefill chunks on the matrix
+ * cores within float tolerance; GGML_PREC_F32 (what the forced aligner
+ * selects, forced_aligner_runtime.rs:622) keeps every attention in the
+ * exact chunked form. Decode steps (one query) are exact under both. Other
+ * values return GGML_STATUS_FAILED. Takes effect on the next step. */
+int oa_qwen_session_set_flash_attention_precision(oa_qwen_session * s, int precision);
+
 /* Prefill T positions of every sequence (chunked internally at 256) from
  * hidden inputs [n_seq][T][d_model] (an audio-embedding prefix) or token ids
  * [n_seq][T]. top1_out (optional, [n_seq]) gets the first-max argmax of the
@@ -306,6 +317,14 @@ void oa_qwen_audio_encoder_free(oa_qwen_audio_encoder * e);
  * NULL) receives the compute's wall time. The graph is built on the first call
  * for a chunk count and replayed after. Returns a ggml_status. */
 int oa_qwen_audio_encode(oa_qwen_audio_encoder * e, const float * mel, int n_frames, float * out, double * ms);
+/* The self-attention's FLASH_ATTN_EXT precision. The reference's encoder
+ * always builds GGML_PREC_DEFAULT (flash_attn_ext, cpu_graph.rs:4120-4142;
+ * nn/encoder.rs:784-793), this shim's default too: the matrix-core form
+ * within float tolerance. GGML_PREC_F32 keeps the exact chunked form; this
+ * switch has no counterpart in the reference and is there for exact
+ * comparisons. Other values return GGML_STATUS_FAILED; the next encode
+ * rebuilds the graph. */
+int oa_qwen_audio_encoder_set_flash_attention_precision(oa_qwen_audio_encoder * e, int precision);
 
 /* ---- pack storage policy (crates/openasr-core/src/models/pack_quant.rs) ---- */
 

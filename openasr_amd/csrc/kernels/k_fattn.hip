@@ -785,6 +785,7 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_full(fattn_args a, float *
 static int64_t fa_tiles(const fattn_args & a) { return (int64_t) a.hkv * a.n_seq * a.q_tiles; }
 
 size_t fattn_scratch_bytes(const fattn_args & a) {
+    if (a.mfma) return fattn_mfma_scratch_bytes(a);
     if (!a.split) return 0;
     const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
     return (size_t) prows * (2 + (size_t) a.d) * sizeof(float) + 1024;
@@ -803,7 +804,7 @@ void fattn_plan(fattn_args & a, int n_cu) {
     // 686 tiles: 93 -> ~60 us a layer) gain from the split up to several
     // tiles a CU; 128-wide causal prefill chunks (1024 tiles) lose from it
     const bool fits = a.n_chunks <= kFaMaxChunks && part_bytes <= (256LL << 20);
-    if (fits && a.tq == 1) a.split = 2;  // wave per (chunk, query head)
+    if (fits && a.n_q == 1) a.split = 2;  // wave per (chunk, query head) of the one query
     else a.split = fits && tiles < (a.d == 64 ? 8LL : 2LL) * n_cu ? 1 : 0;
 }
 
@@ -886,6 +887,10 @@ static void launch_fa_d(const fattn_args & a, void * scratch, float * out, hipSt
 }
 
 void launch_fattn(const fattn_args & a, void * scratch, float * out, hipStream_t stream) {
+    if (a.mfma) {
+        launch_fattn_mfma(a, scratch, out, stream);
+        return;
+    }
     if (a.d == 128) launch_fa_d<128>(a, scratch, out, stream);
     else launch_fa_d<64>(a, scratch, out, stream);
 }

@@ -1400,7 +1400,11 @@ bool planner::make_fattn(const ggml_tensor * t, fattn_args & a) {
     if ((k->type == GGML_TYPE_F16 && (uintptr_t) a.k % 16 != 0) || (v->type == GGML_TYPE_F16 && (uintptr_t) a.v % 16 != 0))
         return fail(t, "K/V not 16-byte aligned");
     fattn_plan(a, n_cu);
-    if (!fattn_fits(a)) return fail(t, "KV span longer than the kernel's chunk table");
+    // more than one query at the default precision (op_params[3], the
+    // host's flash-attention precision contract): the matrix-core form
+    a.mfma = t->op_params[3] != GGML_PREC_F32 && fattn_mfma_supported(a);
+    if (a.mfma) fattn_mfma_plan(a, n_cu);
+    if (!a.mfma && !fattn_fits(a)) return fail(t, "KV span longer than the kernel's chunk table");
     return true;
 }
 
@@ -1430,7 +1434,7 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
     fattn_args a;
     if (!make_fattn(t, a)) return false;
     const ggml_tensor * view = nullptr;
-    fattn_quant_out(i, t, a, view);
+    if (!a.mfma) fattn_quant_out(i, t, a, view);
     // f32 K / V: rounded to contiguous f16 copies in scratch after the
     // partials -- the f16 definition over f16-rounded K / V, the conversion
     // ggml's GPU backends make as well
@@ -1489,7 +1493,7 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
             }
             launch_fattn(la, g, out, s);
         },
-        t, "flash_attn_ext");
+        t, a.mfma ? "flash_attn_mfma" : "flash_attn_ext");
     if (a.qtype >= 0) {
         act_src = view;
         act_wtype = a.qtype;

@@ -177,7 +177,16 @@ struct fattn_args {
     // -1 none, GGML_TYPE_Q8_0 or GGML_TYPE_Q4_K (Q8_K activations)
     int qtype;
     act_buffers act;
+    // more than one query at the default precision: the matrix-core form
+    // (k_fattn_mfma.hip, float tolerance) instead of the chunked definition
+    int mfma;
+    int mfma_split;  // KV splits of the matrix-core form (partials + combine when > 1)
 };
+// whether the matrix-core form takes this attention (n_q > 1, D 64 / 128)
+bool fattn_mfma_supported(const fattn_args & a);
+void fattn_mfma_plan(fattn_args & a, int n_cu);
+size_t fattn_mfma_scratch_bytes(const fattn_args & a);
+void launch_fattn_mfma(const fattn_args & a, void * scratch, float * out, hipStream_t s);
 // The unfused attention chain of the discrete-GPU prefill (MUL_MAT(K, Q) ->
 // SOFT_MAX_EXT -> MUL_MAT(CONT(V^T), P) -> PERMUTE/CONT) as one launch, in
 // the fixed order k_attn_naive.hip defines. Q f32 [d, n_q, hq, n_seq]

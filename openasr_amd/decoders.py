@@ -110,6 +110,7 @@ def lib() -> C.CDLL:
     s("oa_qwen_session_free", None, vp)
     s("oa_qwen_session_position", i, vp, i)
     s("oa_qwen_session_set_reversed_top1", None, vp, i)
+    s("oa_qwen_session_set_flash_attention_precision", i, vp, i)
     s("oa_qwen_session_set_hip_lane", i, vp, i, i)
     s("oa_qwen_prefill_embeddings", i, vp, vp, i, vp)
     s("oa_qwen_prefill_tokens", i, vp, vp, i, vp)
@@ -141,6 +142,7 @@ def lib() -> C.CDLL:
     s("oa_qwen_audio_encoder_create", vp, vp, vp)
     s("oa_qwen_audio_encoder_free", None, vp)
     s("oa_qwen_audio_encode", i, vp, vp, i, vp, C.POINTER(C.c_double))
+    s("oa_qwen_audio_encoder_set_flash_attention_precision", i, vp, i)
     s("oa_classify_quant_tensor_role", i, vp, i, i, i, i)
     s("oa_quant_target_write_type", i, vp, i, i, i, i)
     s("oa_qwen_decode_graph", vp, vp)
@@ -288,6 +290,14 @@ class QwenSession:
 
     def position(self, seq: int = 0) -> int:
         return lib().oa_qwen_session_position(self.ptr, seq)
+
+    def set_flash_attention_precision(self, precision: int):
+        """the self-attention's contract (set_flash_attention_precision,
+        llm_transformer.rs:3044-3053): GGML_PREC_DEFAULT runs prefill chunks
+        on the matrix cores within float tolerance, GGML_PREC_F32 keeps the
+        exact chunked form; decode steps are exact under both"""
+        self._check(lib().oa_qwen_session_set_flash_attention_precision(self.ptr, int(precision)),
+                    "set_flash_attention_precision")
 
     def set_reversed_top1(self, enable: bool = True):
         """greedy top-1 through the reversed-row GET_ROWS + ARGMAX graph"""
@@ -506,6 +516,12 @@ class QwenAudioEncoder:
         if st != 0:
             raise RuntimeError(f"audio encode failed: status {st}")
         return out, ms.value
+
+    def set_flash_attention_precision(self, precision: int):
+        """GGML_PREC_DEFAULT (as the reference builds the encoder) or
+        GGML_PREC_F32 (the exact chunked attention)"""
+        if lib().oa_qwen_audio_encoder_set_flash_attention_precision(self.ptr, int(precision)) != 0:
+            raise ValueError(f"unknown flash-attention precision {precision}")
 
     def free(self):
         if self.ptr:

@@ -82,6 +82,9 @@ struct oa_qwen_audio_encoder {
     ggml_backend_buffer_t buf = nullptr;
     std::map<int, ggml_tensor *> g;                // global weights
     std::vector<std::vector<ggml_tensor *>> L;     // [layer][kind]
+    // the self-attention's flash-attention precision (GGML_PREC_DEFAULT as
+    // the reference builds it, or GGML_PREC_F32)
+    int fa_prec = GGML_PREC_DEFAULT;
     // the graph of the last chunk count
     int graph_chunks = 0;
     ggml_context * gctx = nullptr;
@@ -118,7 +121,8 @@ ggml_tensor * heads_view(ggml_context * ctx, ggml_tensor * x, int hd, int heads,
 
 // transformer_layer (nn/encoder.rs:678-870) with flash attention and GELU_ERF
 ggml_tensor * encoder_layer(ggml_context * ctx, ggml_tensor * x, ggml_tensor * mask16,
-                            const std::vector<ggml_tensor *> & W, const oa_qwen_audio_config & c, int rows) {
+                            const std::vector<ggml_tensor *> & W, const oa_qwen_audio_config & c, int rows,
+                            int fa_prec) {
     const int hd = c.d_model / c.n_heads;
     ggml_tensor * residual = x;
     ggml_tensor * h = layer_norm(ctx, x, W[OA_QA_ATTN_NORM_W], W[OA_QA_ATTN_NORM_B]);
@@ -129,6 +133,7 @@ ggml_tensor * encoder_layer(ggml_context * ctx, ggml_tensor * x, ggml_tensor * m
     ggml_tensor * att = ggml_flash_attn_ext(ctx, heads_view(ctx, q, hd, c.n_heads, rows),
                                             heads_view(ctx, k, hd, c.n_heads, rows),
                                             heads_view(ctx, v, hd, c.n_heads, rows), mask16, scale, 0.0f, 0.0f);
+    ggml_flash_attn_ext_set_prec(att, (ggml_prec) fa_prec);
     att = ggml_reshape_2d(ctx, att, (int64_t) hd * c.n_heads, rows);
     x = ggml_add(ctx, linear(ctx, W[OA_QA_O], att, W[OA_QA_O_B]), residual);
     // FFN (nn/ffn.rs:22-50): up, GELU_ERF, down, residual
@@ -173,7 +178,7 @@ bool build_graph(oa_qwen_audio_encoder * e, int chunks) {
     // flash attention takes an f16 mask: the f32 one cast once per layer (nn/encoder.rs:794-800)
     for (int l = 0; l < c.n_layers; l++) {
         ggml_tensor * mask16 = ggml_cast(ctx, e->mask, GGML_TYPE_F16);
-        x = encoder_layer(ctx, x, mask16, e->L[(size_t) l], c, rows);
+        x = encoder_layer(ctx, x, mask16, e->L[(size_t) l], c, rows, e->fa_prec);
     }
     x = layer_norm(ctx, x, e->g[OA_QA_LN_POST_W], e->g[OA_QA_LN_POST_B]);
     x = ggml_gelu_erf(ctx, linear(ctx, e->g[OA_QA_PROJ1], x, e->g[OA_QA_PROJ1_B]));
@@ -332,6 +337,15 @@ void oa_qwen_audio_encoder_free(oa_qwen_audio_encoder * e) {
     ggml_backend_buffer_free(e->buf);
     ggml_free(e->ctx);
     delete e;
+}
+
+int oa_qwen_audio_encoder_set_flash_attention_precision(oa_qwen_audio_encoder * e, int precision) {
+    if (precision != GGML_PREC_DEFAULT && precision != GGML_PREC_F32) return GGML_STATUS_FAILED;
+    if (precision != e->fa_prec) {
+        e->fa_prec = precision;
+        e->release_graph();
+    }
+    return GGML_STATUS_SUCCESS;
 }
 
 int oa_qwen_audio_encode(oa_qwen_audio_encoder * e, const float * mel, int n_frames, float * out, double * ms) {

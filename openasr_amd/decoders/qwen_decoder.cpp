@@ -139,6 +139,9 @@ struct oa_qwen_session {
     // trimmed to even widths
     bool hip_lane = false;
     int prefill_chunk = kPrefillChunk;
+    // the self-attention's flash-attention precision contract
+    // (set_flash_attention_precision, llm_transformer.rs:3044-3053)
+    int fa_prec = GGML_PREC_DEFAULT;
 };
 
 namespace {
@@ -170,7 +173,7 @@ ggml_tensor * rms_norm_mul(ggml_context * ctx, ggml_tensor * x, ggml_tensor * w,
 // llm_layer for token_count tokens of n_seq sequences (nn/decoder.rs:1850-2145)
 ggml_tensor * llm_layer(ggml_context * ctx, const oa_qwen_config & c, const qlayer_dev & L, ggml_tensor * hidden,
                         ggml_tensor * k_hist, ggml_tensor * v_hist, ggml_tensor * rows, ggml_tensor * pos,
-                        ggml_tensor * mask, int T, int n_seq, int max_pos, bool hip_lane) {
+                        ggml_tensor * mask, int T, int n_seq, int max_pos, bool hip_lane, int fa_prec) {
     const int hd = c.head_dim, q_w = c.n_head * hd, kv_w = c.n_kv_head * hd;
     const int tokens = T * n_seq;
     ggml_tensor * normed = rms_norm_mul(ctx, hidden, L.attn_norm, c.rms_eps);
@@ -238,7 +241,7 @@ ggml_tensor * llm_layer(ggml_context * ctx, const oa_qwen_config & c, const qlay
         att = ggml_cont(ctx, ggml_permute(ctx, ctx_rows, 0, 2, 1, 3));
     } else {
         att = ggml_flash_attn_ext(ctx, q_fa, k_full, v_full, mask, scale, 0.0f, 0.0f);
-        ggml_flash_attn_ext_set_prec(att, GGML_PREC_DEFAULT);
+        ggml_flash_attn_ext_set_prec(att, (ggml_prec) fa_prec);
     }
     att = ggml_reshape_2d(ctx, att, q_w, tokens);
     ggml_tensor * post_attn = ggml_add(ctx, hidden, ggml_mul_mat(ctx, L.o, att));
@@ -282,7 +285,7 @@ bool build_step(oa_qwen_session * s, step_graph & g, int T, bool emb) {
     ggml_set_input(g.mask);
     for (int l = 0; l < c.n_layers; l++) {
         state = llm_layer(g.ctx, c, m->layers[(size_t) l], state, s->k_cache[(size_t) l], s->v_cache[(size_t) l],
-                          g.rows, g.pos, g.mask, T, n_seq, s->max_pos, s->hip_lane);
+                          g.rows, g.pos, g.mask, T, n_seq, s->max_pos, s->hip_lane, s->fa_prec);
     }
     ggml_tensor * last = state;
     if (T > 1) {  // the last position of each sequence
@@ -518,6 +521,13 @@ int oa_qwen_session_set_hip_lane(oa_qwen_session * s, int enable, int prefill_ch
     s->hip_lane = enable != 0;
     s->prefill_chunk = enable ? prefill_chunk : kPrefillChunk;
     s->decode.release();  // rebuilt with the lane's graph on the next step
+    return GGML_STATUS_SUCCESS;
+}
+
+int oa_qwen_session_set_flash_attention_precision(oa_qwen_session * s, int precision) {
+    if (precision != GGML_PREC_DEFAULT && precision != GGML_PREC_F32) return GGML_STATUS_FAILED;
+    s->fa_prec = precision;
+    s->decode.release();  // no graph built under the other contract survives
     return GGML_STATUS_SUCCESS;
 }
 

@@ -118,6 +118,7 @@ def test_audio_encoder_matches_reference(gpu, wname):
     print(f"qwen audio encoder {wname}", flush=True)
     w = D.QwenAudioWeights(wt, seed=77, **SMALL)
     enc = D.QwenAudioEncoder(w, gpu.backend)
+    enc.set_flash_attention_precision(g.GGML_PREC_F32)  # the exact attention: the projections' bars
     for n_frames, seed in ((250, 1), (270, 2), (100, 3)):
         mel = mel_input(SMALL["n_mels"], n_frames, seed)
         got, ms = enc.encode(mel)
@@ -150,6 +151,7 @@ def test_full_size_audio_encoder_matches_reference(gpu, wname):
     shape = D.QWEN3_06B_AUDIO
     w = D.QwenAudioWeights(wt, seed=21, **shape)
     enc = D.QwenAudioEncoder(w, gpu.backend)
+    enc.set_flash_attention_precision(g.GGML_PREC_F32)
     mel = mel_input(shape["n_mels"], 250, 8)
     got, ms = enc.encode(mel)
     want = RA.encode(w, mel)
@@ -166,6 +168,33 @@ def test_full_size_audio_encoder_matches_reference(gpu, wname):
     else:
         # an f32 path that rounded an operand to f16 would show ~5e-4
         assert err < {"f32": 5e-5, "f16": 2e-3}[wname]
+    enc.free()
+    w.free()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("size", ["small", "full"])
+def test_audio_encoder_default_precision(gpu, size):
+    """the encoder as the reference builds it (flash attention at
+    GGML_PREC_DEFAULT, cpu_graph.rs:4120-4142): the attention on the matrix
+    cores (P rounded to f16 for P V) with f32 projections, within the op
+    tolerance 2e-3 of the checker; the exact contract on the same encoder
+    moves by less"""
+    from oracle import audio_encoder as RA
+    shape = SMALL if size == "small" else D.QWEN3_06B_AUDIO
+    print(f"qwen audio encoder {size}, f32 projections, default-precision attention", flush=True)
+    w = D.QwenAudioWeights(g.F32, seed=23, **shape)
+    enc = D.QwenAudioEncoder(w, gpu.backend)
+    mel = mel_input(shape["n_mels"], 250, 9)
+    want = RA.encode(w, mel)
+    got, ms = enc.encode(mel)
+    err = rel_err(got, want)
+    enc.set_flash_attention_precision(g.GGML_PREC_F32)
+    exact, ms32 = enc.encode(mel)
+    err32 = rel_err(exact, want)
+    print(f"  default {ms:.2f} ms, rel err {err:.2e}; exact attention {ms32:.2f} ms, rel err {err32:.2e}",
+          flush=True)
+    assert err < 2e-3 and err32 <= err
     enc.free()
     w.free()
 

@@ -30,10 +30,13 @@ def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed
              reversed_top1=False, hip_lane=None):
     """hip_lane: a prefill chunk width to run the graphs the unmodified host
     builds on its HIP lane (REPEAT-expanded K/V, the unfused attention chain
-    for wide prefill chunks), the oracle prefilling in the same chunks"""
+    for wide prefill chunks), the oracle prefilling in the same chunks.
+    Prefill attention under GGML_PREC_F32 (the exact chunked form): every
+    step is compared bit for bit"""
     w = weights or D.QwenWeights(wtype, seed=seed, **shape)
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(n_seq, max_pos)
+    sess.set_flash_attention_precision(g.GGML_PREC_F32)
     if reversed_top1:
         sess.set_reversed_top1(True)
     if hip_lane:
@@ -154,7 +157,9 @@ def test_hip_lane_refuses_batches(gpu):
 
 
 def test_batched_equals_serial(gpu):
-    """n_seq=3 in one graph == three n_seq=1 sessions (nn/decoder.rs:3412-3520 invariant)"""
+    """n_seq=3 in one graph == three n_seq=1 sessions (nn/decoder.rs:3412-3520
+    invariant), at the default attention precision: the matrix-core prefill
+    plans each sequence's work alike batched or alone"""
     w = D.QwenWeights(g.Q4_K, seed=3, **TINY)
     model = D.QwenModel(w, gpu.backend)
     wl = D.QwenWorkload("t", TINY, g.Q4_K, 3, 40, 4, 12, 128)
@@ -192,6 +197,89 @@ def test_qwen3_06b_q8_0_batch1_hip_lane_first_64_steps(gpu, ref, chunk):
     print(f"qwen3-0.6b q8_0 b1, hip lane, prefill chunk {chunk}", flush=True)
     run_pair(gpu, ref, D.QWEN3_06B, g.Q8_0, 1, prefix=375, prompt=8, steps=64, max_pos=1024, seed=1234,
              hip_lane=chunk)
+
+
+def seed_from_device(r, sess, seq, n_pos, n_layers):
+    """the oracle continues from the device's KV caches after prefill"""
+    for layer in range(n_layers):
+        k, v = sess.read_kv(layer, seq)
+        r.k[layer][...] = k
+        r.v[layer][...] = v
+    r.pos = n_pos
+
+
+@pytest.mark.parametrize("wname,n_seq", [("q8_0", 1), ("q4_K", 8)])
+def test_qwen3_06b_default_precision_prefill(gpu, ref, wname, n_seq):
+    """the ASR decoder's own contract (GGML_PREC_DEFAULT, what
+    llm_transformer.rs builds for transcription): 375-position prefixes + 8
+    prompt tokens prefilled with the attention on the matrix cores. The K/V
+    caches of every layer stay as close to the exact chunked form's (the
+    oracle, fidelity 5) as ggml-cpu's own f16-accumulator attention keeps
+    them (fidelity 1): within twice that distance, or 5e-2 of the largest
+    entry; the first token agrees wherever the oracle's top-1 margin exceeds
+    twice the ggml-cpu numerics' logit distance. Then the oracle continues
+    from the device's caches: 64 greedy decode steps token for token, logits
+    < 1e-2 (one query a step: exact under either contract)."""
+    wt = g.Q8_0 if wname == "q8_0" else g.Q4_K
+    print(f"qwen3-0.6b {wname} b{n_seq}, default-precision prefill", flush=True)
+    shape, max_pos, n_pos = D.QWEN3_06B, 1024, 383
+    w = D.QwenWeights(wt, seed=1234, **shape)
+    model = D.QwenModel(w, gpu.backend)
+    sess = model.session(n_seq, max_pos)
+    wl = D.QwenWorkload("t", shape, wt, n_seq, 375, 8, 64, max_pos)
+    emb, toks = D.workload_inputs(wl, seed=1235)
+    sess.prefill_embeddings(emb)
+    first = sess.prefill_tokens(toks)
+    table = w.pointer_table()
+    seqs = [0] if n_seq == 1 else [0, n_seq - 1]
+
+    def f16(a):
+        return a[:, :n_pos].view(np.float16).astype(np.float64)
+
+    for s in seqs:
+        exact = ref.QwenRef(w.cfg, table, max_pos, fa_fidelity=5)
+        exact.forward(emb[s])
+        t5, lg5 = exact.forward(exact.embed(toks[s]))
+        cpu = ref.QwenRef(w.cfg, table, max_pos, fa_fidelity=1)
+        cpu.forward(emb[s])
+        t1, lg1 = cpu.forward(cpu.embed(toks[s]))
+        spread = float(np.abs(lg1 - lg5).max())
+        top2 = np.sort(lg5)[-2:]
+        margin = float(top2[1] - top2[0])
+        kv_err = kv_spread = 0.0
+        for L in range(shape["n_layers"]):
+            k_dev, v_dev = sess.read_kv(L, s)
+            for dev, ex, cp in ((k_dev, exact.k[L], cpu.k[L]), (v_dev, exact.v[L], cpu.v[L])):
+                top = np.abs(f16(ex)).max()
+                kv_err = max(kv_err, float(np.abs(f16(dev) - f16(ex)).max() / top))
+                kv_spread = max(kv_spread, float(np.abs(f16(cp) - f16(ex)).max() / top))
+        print(f"  seq {s}: first token dev {first[s]} exact {t5} ggml-cpu numerics {t1}; top-1 margin "
+              f"{margin:.3e}, ggml-cpu numerics' logit distance {spread:.3e}; K/V caches vs exact: dev "
+              f"{kv_err:.3e}, ggml-cpu numerics {kv_spread:.3e}", flush=True)
+        assert kv_err <= max(2 * kv_spread, 5e-2)
+        if margin > 2 * spread:
+            assert first[s] == t5
+    # decode from the device's caches: exact
+    cur = first
+    dev_toks, dev_logits = [], []
+    for _ in range(64):
+        cur, lg = sess.step(cur, want_logits=True)
+        dev_toks.append(cur.copy())
+        dev_logits.append(lg)
+    max_dl = 0.0
+    for s in seqs:
+        r = ref.QwenRef(w.cfg, table, max_pos, fa_fidelity=5)
+        seed_from_device(r, sess, s, n_pos, shape["n_layers"])
+        t = int(first[s])
+        for i in range(64):
+            t, lg = r.step(t)
+            max_dl = max(max_dl, float(np.abs(dev_logits[i][s] - lg).max()))
+            assert t == dev_toks[i][s], f"seq {s} step {i}: cpu {t} != gpu {dev_toks[i][s]}"
+    print(f"  64 decode steps from the device caches token-exact, max |dlogit| {max_dl:.2e}", flush=True)
+    assert max_dl < 1e-2
+    sess.free()
+    model.free()
+    w.free()
 
 
 def test_qwen3_06b_q8_0_batch1_reversed_top1_first_64_steps(gpu, ref):
@@ -329,6 +417,7 @@ def test_qwen3_17b_q4_K_batch8_long_context(gpu, ref):
     w = D.QwenWeights(wl.wtype, seed=1234, **wl.shape)
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(wl.n_seq, wl.max_positions)
+    sess.set_flash_attention_precision(g.GGML_PREC_F32)
     emb, prompt = D.workload_inputs(wl, seed=77)
     sess.prefill_embeddings(emb)
     cur = sess.prefill_tokens(prompt)
@@ -380,6 +469,7 @@ def test_qwen3_17b_q4_K_prefill_all_layers(gpu, ref):
     w = D.QwenWeights(wl.wtype, seed=1234, **wl.shape)
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(wl.n_seq, wl.max_positions)
+    sess.set_flash_attention_precision(g.GGML_PREC_F32)
     short = D.QwenWorkload("short", wl.shape, wl.wtype, wl.n_seq, prefix, prompt_len, 0, wl.max_positions)
     emb, prompt = D.workload_inputs(short, seed=78)
     sess.prefill_embeddings(emb)

@@ -322,14 +322,17 @@ FA_CASES = [
 ]
 
 
+@pytest.mark.parametrize("prec", ["f32", "default"])
 @pytest.mark.parametrize("d,heads,t", [(64, 20, 750), (128, 8, 300), (64, 6, 100)])
-def test_flash_attn_ext_f32_kv_head_views(ggml, gpu, ref, d, heads, t):
+def test_flash_attn_ext_f32_kv_head_views(ggml, gpu, ref, d, heads, t, prec):
     """the encoders' self-attention (nn/encoder.rs:735-800): Q, K and V are
     f32 projections [d * heads, t] viewed as heads (reshape [d, heads, t],
     permute to [d, t, heads]) without a CONT, under an f16 block mask. The
-    f32 K / V are rounded to f16 (the conversion ggml's GPU backends make):
-    bit for bit the oracle's chunked attention over the f16-rounded K / V"""
-    print(f"flash_attn f32 K/V views D={d} heads={heads} t={t}", flush=True)
+    f32 K / V are rounded to f16 (the conversion ggml's GPU backends make).
+    GGML_PREC_F32: bit for bit the oracle's chunked attention over the
+    f16-rounded K / V; the default precision (the matrix-core form): within
+    2e-3 of the f64 textbook attention over the same operands"""
+    print(f"flash_attn f32 K/V views D={d} heads={heads} t={t} prec={prec}", flush=True)
     G = ggml.Graph()
     L = G.lib
     P = [G.new(ggml.F32, d * heads, t) for _ in range(3)]
@@ -340,6 +343,8 @@ def test_flash_attn_ext_f32_kv_head_views(ggml, gpu, ref, d, heads, t):
 
     scale = 1.0 / math.sqrt(d)
     O = L.ggml_flash_attn_ext(G.ctx, heads_view(P[0]), heads_view(P[1]), heads_view(P[2]), M, scale, 0.0, 0.0)
+    if prec == "f32":
+        L.ggml_flash_attn_ext_set_prec(O, ggml.GGML_PREC_F32)
     run(ggml, gpu, G, O)
     x = [RNG.standard_normal((t, heads, d)).astype(np.float32) for _ in range(3)]
     for Pi, xi in zip(P, x):
@@ -352,8 +357,16 @@ def test_flash_attn_ext_f32_kv_head_views(ggml, gpu, ref, d, heads, t):
     out = G.get(O).reshape(t, heads, d)  # ggml result [d, heads, t]
     k16 = np.ascontiguousarray(x[1].transpose(1, 0, 2)).astype(np.float16)  # [heads, t, d]
     v16 = np.ascontiguousarray(x[2].transpose(1, 0, 2)).astype(np.float16)
-    same = ref.flash_attn(x[0], k16.view(np.uint16), v16.view(np.uint16), mask.view(np.uint16), scale, fidelity=5)
-    assert_same_bits(out, same)
+    if prec == "f32":
+        same = ref.flash_attn(x[0], k16.view(np.uint16), v16.view(np.uint16), mask.view(np.uint16), scale,
+                              fidelity=5)
+        assert_same_bits(out, same)
+    else:
+        exact = attention_f64(x[0].astype(np.float16).astype(np.float32), k16, v16, mask, scale)
+        err = rel_err(out, exact)
+        print(f"  matrix-core form vs f64 textbook: {err:.2e}")
+        assert err < 2e-3
+        assert "flash_attn_mfma" in plan_labels(gpu, G)
     G.free()
 
 
@@ -390,6 +403,8 @@ def test_flash_attn_ext(ggml, gpu, ref, d, hq, hkv, n_kv, n_q, n_seq):
     M = None if cross else G.new(ggml.F16, n_kv, n_q, 1, n_seq)
     scale = 1.0 / math.sqrt(d)
     O = G.lib.ggml_flash_attn_ext(G.ctx, Q, K, V, M, scale, 0.0, 0.0)
+    if n_q > 1:  # several queries: the full-precision contract keeps the chunked definition
+        G.lib.ggml_flash_attn_ext_set_prec(O, ggml.GGML_PREC_F32)
     run(ggml, gpu, G, O)
     G.set(Q, q)
     G.set(K, k.view(np.uint16))
@@ -445,6 +460,80 @@ def test_flash_attn_fully_masked_chunks_are_skipped_exactly(ggml, gpu, ref):
                           1 / math.sqrt(d), fidelity=5)[0]
     assert np.isfinite(out).all()
     assert_same_bits(out, want)
+    G.free()
+
+
+# the matrix-core form (several queries at the default precision): d, hq,
+# hkv, n_kv, n_q, n_seq, mask kind. Qwen3-0.6B prefill chunks over 512 ..
+# 8192 positions (the few-query shapes split the span over workgroups), a
+# partial query block and partial last tile, two sequences with their own
+# spans, GQA 4 and 8, the encoders' full attention (D 64, one head a kv head)
+# under a block mask, Whisper cross attention (no mask), three sequences of
+# 200-query chunks over 4096 positions.
+FA_MFMA_CASES = [
+    (128, 16, 8, 512, 64, 1, "causal"), (128, 16, 8, 2048, 64, 2, "causal"), (128, 16, 8, 8192, 64, 1, "causal"),
+    (128, 16, 8, 2048, 256, 1, "causal"), (128, 16, 8, 1000, 37, 1, "causal"), (128, 32, 8, 1024, 70, 1, "causal"),
+    (128, 16, 2, 600, 20, 1, "causal"), (64, 20, 20, 750, 750, 1, "block"), (64, 6, 6, 1500, 100, 1, None),
+    (128, 16, 8, 4096, 200, 3, "causal"),
+]
+
+
+@pytest.mark.parametrize("d,hq,hkv,n_kv,n_q,n_seq,mkind", FA_MFMA_CASES)
+def test_flash_attn_ext_matrix_cores(ggml, gpu, ref, d, hq, hkv, n_kv, n_q, n_seq, mkind):
+    """several queries at the default precision run on the matrix cores (f16
+    Q K^T and P V, f32 sums and online softmax): within 2e-3 of the f64
+    textbook attention over the f16-rounded operands, printed beside the
+    ggml-cpu numerics' error; the same graph under GGML_PREC_F32 runs the
+    chunked definition, bit for bit the oracle"""
+    print(f"flash_attn mfma D={d} Hq={hq} Hkv={hkv} kv={n_kv} nq={n_q} seq={n_seq} mask={mkind}", flush=True)
+    q = RNG.standard_normal((n_seq, hq, n_q, d)).astype(np.float32)
+    k = RNG.standard_normal((n_seq, hkv, n_kv, d)).astype(np.float16)
+    v = RNG.standard_normal((n_seq, hkv, n_kv, d)).astype(np.float16)
+    mask = np.zeros((n_seq, n_q, n_kv), np.float16)
+    for s in range(n_seq):
+        if mkind == "causal":
+            mask[s] = causal_mask(n_q, n_kv, n_kv - 64 * s)
+        elif mkind == "block":
+            blk_q, blk_k = np.arange(n_q) // 100, np.arange(n_kv) // 100
+            mask[s] = np.where(blk_q[:, None] == blk_k[None, :], 0.0, -np.inf)
+    G = ggml.Graph()
+    Q = G.new(ggml.F32, d, n_q, hq, n_seq)
+    K = G.new(ggml.F16, d, n_kv, hkv, n_seq)
+    V = G.new(ggml.F16, d, n_kv, hkv, n_seq)
+    M = None if mkind is None else G.new(ggml.F16, n_kv, n_q, 1, n_seq)
+    scale = 1.0 / math.sqrt(d)
+    O = G.lib.ggml_flash_attn_ext(G.ctx, Q, K, V, M, scale, 0.0, 0.0)
+    O32 = G.lib.ggml_flash_attn_ext(G.ctx, Q, K, V, M, scale, 0.0, 0.0)
+    G.lib.ggml_flash_attn_ext_set_prec(O32, ggml.GGML_PREC_F32)
+    G.build(O, O32)
+    G.allocate(gpu.buft)
+    G.set(Q, q)
+    G.set(K, k.view(np.uint16))
+    G.set(V, v.view(np.uint16))
+    if M is not None:
+        G.set(M, mask.view(np.uint16))
+    assert G.compute(gpu.backend) == 0
+    labels = plan_labels(gpu, G)
+    assert "flash_attn_mfma" in labels and "flash_attn_ext" in labels, labels
+    out = G.get(O).reshape(n_seq, n_q, hq, d)
+    out32 = G.get(O32).reshape(n_seq, n_q, hq, d)
+    for s in range(n_seq):
+        qs = np.ascontiguousarray(q[s].transpose(1, 0, 2))  # [n_q, hq, d]
+        q16 = qs.astype(np.float16).astype(np.float32)
+        ms = None if M is None else mask[s]
+        exact = attention_f64(q16, k[s], v[s], ms, scale)
+        mbits = None if ms is None else ms.view(np.uint16)
+        same = ref.flash_attn(qs, k[s].view(np.uint16), v[s].view(np.uint16), mbits, scale, fidelity=5)
+        assert_same_bits(out32[s], same)
+        cpu = ref.flash_attn(qs, k[s].view(np.uint16), v[s].view(np.uint16), mbits, scale, fidelity=1)
+        err, e_cpu = rel_err(out[s], exact), rel_err(cpu, exact)
+        print(f"  seq {s}: matrix-core form vs f64 {err:.2e}, ggml-cpu numerics vs f64 {e_cpu:.2e}")
+        assert err < 2e-3
+        assert np.isfinite(out[s]).all()
+    # replays of the captured graph give the same bits
+    first = out.copy()
+    assert G.compute(gpu.backend) == 0
+    assert np.array_equal(G.get(O).reshape(first.shape).view(np.uint32), first.view(np.uint32))
     G.free()
 
 
