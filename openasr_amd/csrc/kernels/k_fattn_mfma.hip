@@ -8,23 +8,25 @@
 // (decode) steps keep the exact chunked form of k_fattn.hip.
 //
 // Arithmetic (float tolerance, the ggml GPU backends' flash attention): the
-// query rows rounded to f16, S = Q K^T on v_mfma_f32_16x16x32_f16 (f16
-// products, f32 sums), S * scale + mask, an online softmax over 64-position
-// tiles in f32 (running max m, sum l, the output rescaled by exp(m_old -
-// m_new)), P rounded to f16 for P V on the same MFMA, out = O / l (0 for a
-// row with no live position).
+// query rows rounded to f16, S^T = K Q^T on v_mfma_f32_16x16x32_f16 (f16
+// products, f32 sums), S * scale * log2(e) + mask * log2(e) in f32, an
+// online softmax over 64-position tiles in f32 with exp2 (running max m, sum
+// l, the output rescaled by 2^(m_old - m_new)), P rounded to f16 for
+// O^T = V^T P^T on the same MFMA, out = O / l (0 for a row with no open
+// position).
 //
 // Work: a workgroup of four waves owns 64 rows -- 64 / g queries times the
 // g query heads of one kv head of one sequence -- so each K/V tile is read
-// once for g heads; wave w owns rows 16 w .. 16 w + 15 (the MFMA's M). Per
-// 64-position tile: K rows staged in LDS (rows padded: the score MFMA's
-// B-operand reads of 16 rows hit distinct banks), V staged transposed
-// ([dim][position], the P V MFMA's B operand contiguous), tiles masked for
-// every row of the workgroup skipped. MFMA operand layouts (16x16x32):
-// A lane l = row l % 16, k 8 (l / 16) .. + 7; B lane l = k 8 (l / 16) .. + 7,
-// column l % 16; result lane l = rows 4 (l / 16) .. + 3, column l % 16. The
-// score result's row layout is the P V result's, so the softmax rescale is
-// lane-local; P goes through LDS to the A layout.
+// once for g heads; wave w owns rows 16 w .. 16 w + 15. MFMA operand layouts
+// (16x16x32): A lane l = row l % 16, k 8 (l / 16) .. + 7; B lane l = k
+// 8 (l / 16) .. + 7, column l % 16; result lane l = rows 4 (l / 16) .. + 3,
+// column l % 16. The scores are computed transposed (rows = positions,
+// columns = the wave's rows), so a lane holds 16 positions of one row: the
+// softmax is lane-local but for two cross-lane steps, and its P values are
+// the lane's own B operand of the P V product (the k slots ordered to match,
+// V^T read in that order) -- P never goes through LDS. Per 64-position tile:
+// K rows staged in LDS (rows padded against bank conflicts), V staged
+// transposed ([dim][position]), the mask as f32.
 #include <algorithm>
 #include <cmath>
 
@@ -46,32 +48,6 @@ typedef float fm_f4 __attribute__((ext_vector_type(4)));
 typedef uint32_t fm_u4 __attribute__((ext_vector_type(4)));  // 16 bytes (a native vector: copies stay in registers)
 
 __device__ __forceinline__ fm_h8 fm_load8(const _Float16 * p) { return *(const fm_h8 *) p; }
-
-// max / sum over the 16 lanes of a lane group (lanes 16 k .. 16 k + 15, a
-// DPP row) by data-parallel-primitive moves inside the row: partner lanes
-// i ^ 1, i ^ 2 (quad permutations), then 7 - i within eight, 15 - i within
-// sixteen (half mirror, mirror). Every lane ends with the same value (each
-// step combines two equal-shaped partials, and max / + commute).
-template <int CTRL>
-__device__ __forceinline__ float fm_dpp(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
-constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
-constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
-constexpr int kDppHalfMirror = 0x141;
-constexpr int kDppMirror = 0x140;
-__device__ __forceinline__ float fm_max16(float v) {
-    v = fmaxf(v, fm_dpp<kDppXor1>(v));
-    v = fmaxf(v, fm_dpp<kDppXor2>(v));
-    v = fmaxf(v, fm_dpp<kDppHalfMirror>(v));
-    return fmaxf(v, fm_dpp<kDppMirror>(v));
-}
-__device__ __forceinline__ float fm_sum16(float v) {
-    v += fm_dpp<kDppXor1>(v);
-    v += fm_dpp<kDppXor2>(v);
-    v += fm_dpp<kDppHalfMirror>(v);
-    return v + fm_dpp<kDppMirror>(v);
-}
 
 // Mask entries pos .. pos + 7 of one mask row (f16 bits), in two steps so
 // that a thread's loads issue back to back and are waited for only where the
@@ -140,8 +116,7 @@ __global__ __launch_bounds__(kFmThreads) void k_fattn_mfma(fattn_args a, float *
     static_assert(KLD >= 1 && VLD >= 1 && MLD >= 1, "staging split");
     __shared__ __align__(16) _Float16 s_k[kFmTile][KP];
     __shared__ __align__(16) _Float16 s_vt[D][VP];
-    __shared__ __align__(16) _Float16 s_p[4][16][VP];
-    __shared__ __align__(16) uint16_t s_m[kFmRows][VP];
+    __shared__ __align__(16) float s_m[kFmRows][kFmTile + 4];  // mask x log2(e), -inf kept
     __shared__ uint32_t s_open[kFmMaxSpan / 32];
     const int tid = (int) threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = a.hq / a.hkv, qpw = kFmRows / g;  // queries a workgroup
@@ -247,20 +222,19 @@ __global__ __launch_bounds__(kFmThreads) void k_fattn_mfma(fattn_args a, float *
         return t;
     };
 
+    // scores are taken to base-2 exponent units in f32 (exp2 on the softmax
+    // side): s = S * scale * log2(e) + mask * log2(e)
+    const float qscale = a.scale * 1.4426950408889634f;
     fm_h8 qa[KS];
 #pragma unroll
     for (int kk = 0; kk < KS; kk++) {
 #pragma unroll
         for (int j = 0; j < 8; j++) qa[kk][j] = q_live ? (_Float16) qv[kk][j] : (_Float16) 0.0f;
     }
-    // the result rows of this lane: 16 wave + 4 lg + v
-    float m[4], l[4];
+    // this lane's row (query / head pair): 16 wave + l16; its running max,
+    // sum and O^T columns (dims 16 ct + 4 lg + i)
+    float m = -INFINITY, l = 0.0f;
     fm_f4 o[NT];
-#pragma unroll
-    for (int v = 0; v < 4; v++) {
-        m[v] = -INFINITY;
-        l[v] = 0.0f;
-    }
 #pragma unroll
     for (int ct = 0; ct < NT; ct++) o[ct] = fm_f4{0.f, 0.f, 0.f, 0.f};
 
@@ -289,8 +263,25 @@ __global__ __launch_bounds__(kFmThreads) void k_fattn_mfma(fattn_args a, float *
 #pragma unroll
         for (int i = 0; i < MLD; i++) {
             const int e = tid + i * kFmThreads, ql = e >> 3, c = e & 7;
-            const fm_u4 dead = fm_u4{0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u};
-            if (ql < qpw) *(fm_u4 *) &s_m[ql][8 * c] = ql < nq_live ? fm_mask_fix(mr[i], tile * kFmTile + 8 * c, a.n_kv) : dead;
+            if (ql >= qpw) continue;
+            const fm_u4 mh = ql < nq_live ? fm_mask_fix(mr[i], tile * kFmTile + 8 * c, a.n_kv)
+                                          : fm_u4{0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u, 0xFC00FC00u};
+            fm_f4 lo, hi;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t w = mh[j];
+                const float e0 = half_bits_to_float((uint16_t) (w & 0xFFFFu)), e1 = half_bits_to_float((uint16_t) (w >> 16));
+                const float f0 = e0 * 1.4426950408889634f, f1 = e1 * 1.4426950408889634f;
+                if (j < 2) {
+                    lo[2 * j] = f0;
+                    lo[2 * j + 1] = f1;
+                } else {
+                    hi[2 * j - 4] = f0;
+                    hi[2 * j - 3] = f1;
+                }
+            }
+            *(fm_f4 *) &s_m[ql][8 * c] = lo;
+            *(fm_f4 *) &s_m[ql][8 * c + 4] = hi;
         }
     };
 
@@ -302,8 +293,9 @@ __global__ __launch_bounds__(kFmThreads) void k_fattn_mfma(fattn_args a, float *
         __syncthreads();
         const int nxt = next_open(tile + 1);
         if (nxt < t_end) issue(nxt);
-        // S = Q K^T for the wave's 16 rows and the tile's 64 positions
-        // (k steps outer: four independent accumulations in flight)
+        // S^T = K Q^T for the tile's 64 positions and the wave's 16 rows:
+        // lane (lg, l16) gets positions 16 t + 4 lg + i of row l16 (k steps
+        // outer: four independent accumulations in flight)
         fm_f4 sc[4];
 #pragma unroll
         for (int t = 0; t < 4; t++) sc[t] = fm_f4{0.f, 0.f, 0.f, 0.f};
@@ -313,64 +305,62 @@ __global__ __launch_bounds__(kFmThreads) void k_fattn_mfma(fattn_args a, float *
 #pragma unroll
             for (int t = 0; t < 4; t++) kb[t] = fm_load8(&s_k[16 * t + l16][32 * kk + 8 * lg]);
 #pragma unroll
-            for (int t = 0; t < 4; t++) sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[kk], kb[t], sc[t], 0, 0, 0);
+            for (int t = 0; t < 4; t++) sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kb[t], qa[kk], sc[t], 0, 0, 0);
         }
-        // scale, mask, online softmax per row (a row's 64 values: 4 in this
-        // lane, the rest in the other 15 lanes of its group); the four rows
-        // of a lane go through each step together
-        float s[4][4], mn[4], alpha[4], ps[4];
+        // mask and online softmax of the lane's row: 16 of its 64 values in
+        // the lane, the rest in lanes l16 + 16, + 32, + 48
+        const int ql = (16 * wave + l16) / g;
+        float sv[4][4], mx = -INFINITY;
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int ql = (16 * wave + 4 * lg + v) / g;
-            mn[v] = -INFINITY;
+        for (int t = 0; t < 4; t++) {
+            const fm_f4 mk = *(const fm_f4 *) &s_m[ql][16 * t + 4 * lg];
 #pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const uint16_t mh = s_m[ql][16 * t + l16];
-                s[v][t] = mh == kFmNegInf ? -INFINITY : sc[t][v] * a.scale + half_bits_to_float(mh);
-                mn[v] = fmaxf(mn[v], s[v][t]);
+            for (int i = 0; i < 4; i++) {
+                sv[t][i] = mk[i] == -INFINITY ? -INFINITY : fmaf(sc[t][i], qscale, mk[i]);
+                mx = fmaxf(mx, sv[t][i]);
             }
         }
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mn = fmaxf(m, mx);
+        const float base = mn == -INFINITY ? 0.0f : mn;  // a row with nothing open yet
+        const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m - base);
+        // P^T in registers as the P V product's B operand: k slot 8 lg + j of
+        // step kk holds position 32 kk + 16 (j / 4) + 4 lg + j % 4 -- this
+        // lane's own values; V^T is read in the same order
+        fm_h8 pb[kFmTile / 32];
+        float ps = 0.0f;
 #pragma unroll
-        for (int v = 0; v < 4; v++) mn[v] = fmaxf(m[v], fm_max16(mn[v]));
+        for (int t = 0; t < 4; t++) {
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const float base = mn[v] == -INFINITY ? 0.0f : mn[v];  // a row with nothing open yet
-            alpha[v] = m[v] == -INFINITY ? 0.0f : __expf(m[v] - base);
-            ps[v] = 0.0f;
-#pragma unroll
-            for (int t = 0; t < 4; t++) {
-                const float pv = s[v][t] == -INFINITY ? 0.0f : __expf(s[v][t] - base);
+            for (int i = 0; i < 4; i++) {
+                const float pv = sv[t][i] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(sv[t][i] - base);
                 const _Float16 ph = (_Float16) pv;
-                ps[v] += (float) ph;
-                s_p[wave][4 * lg + v][16 * t + l16] = ph;
+                ps += (float) ph;
+                pb[t >> 1][4 * (t & 1) + i] = ph;
             }
         }
-#pragma unroll
-        for (int v = 0; v < 4; v++) {
-            l[v] = l[v] * alpha[v] + fm_sum16(ps[v]);
-            m[v] = mn[v];
-        }
+        ps += __shfl_xor(ps, 16);
+        ps += __shfl_xor(ps, 32);
+        l = l * alpha + ps;
+        m = mn;
         // rescale the accumulators only when some row's maximum moved
-        if (__any(alpha[0] != 1.0f || alpha[1] != 1.0f || alpha[2] != 1.0f || alpha[3] != 1.0f)) {
+        if (__any(alpha != 1.0f)) {
 #pragma unroll
-            for (int ct = 0; ct < NT; ct++) {
-#pragma unroll
-                for (int v = 0; v < 4; v++) o[ct][v] *= alpha[v];
-            }
+            for (int ct = 0; ct < NT; ct++) o[ct] *= alpha;
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        // O += P V
-        fm_h8 pa[kFmTile / 32];
-#pragma unroll
-        for (int kk = 0; kk < kFmTile / 32; kk++) pa[kk] = fm_load8(&s_p[wave][l16][32 * kk + 8 * lg]);
+        // O^T += V^T P^T: A lane (lg, l16) = dim 16 ct + l16 at the k slots'
+        // positions, two 4-position runs of V^T
 #pragma unroll
         for (int kk = 0; kk < kFmTile / 32; kk++) {
 #pragma unroll
-            for (int ct = 0; ct < NT; ct++)
-                o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[kk], fm_load8(&s_vt[16 * ct + l16][32 * kk + 8 * lg]),
-                                                               o[ct], 0, 0, 0);
+            for (int ct = 0; ct < NT; ct++) {
+                const _Float16 * vrow = &s_vt[16 * ct + l16][32 * kk + 4 * lg];
+                typedef _Float16 fm_h4 __attribute__((ext_vector_type(4)));
+                const fm_h4 v0 = *(const fm_h4 *) vrow, v1 = *(const fm_h4 *) (vrow + 16);
+                const fm_h8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb[kk], o[ct], 0, 0, 0);
+            }
         }
         tile = nxt;
     }
@@ -378,28 +368,22 @@ __global__ __launch_bounds__(kFmThreads) void k_fattn_mfma(fattn_args a, float *
         // partials of split z: O unnormalised, then (m, l), per workgroup row
         const int64_t blk = (int64_t) hs * q_blocks + qb;
         const int64_t all_rows = (int64_t) n_blk * kFmRows;
+        const int64_t pr = (blk * a.mfma_split + z) * kFmRows + 16 * wave + l16;
 #pragma unroll
-        for (int v = 0; v < 4; v++) {
-            const int64_t pr = (blk * a.mfma_split + z) * kFmRows + 16 * wave + 4 * lg + v;
-#pragma unroll
-            for (int ct = 0; ct < NT; ct++) part[pr * D + 16 * ct + l16] = o[ct][v];
-            if (l16 == 0) {
-                part[all_rows * D + 2 * pr] = m[v];
-                part[all_rows * D + 2 * pr + 1] = l[v];
-            }
+        for (int ct = 0; ct < NT; ct++) *(fm_f4 *) &part[pr * D + 16 * ct + 4 * lg] = o[ct];
+        if (lg == 0) {
+            part[all_rows * D + 2 * pr] = m;
+            part[all_rows * D + 2 * pr + 1] = l;
         }
         return;
     }
     // out = O / l, ggml's [D, hq, n_q, n_seq] layout
+    const int r = 16 * wave + l16, i = q0 + r / g;
+    if (i >= a.n_q) return;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float * op = out + (((int64_t) seq * a.n_q + i) * a.hq + kvh * g + r % g) * D;
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-        const int r = 16 * wave + 4 * lg + v, i = q0 + r / g;
-        if (i >= a.n_q) continue;
-        const float inv = l[v] > 0.0f ? 1.0f / l[v] : 0.0f;
-        float * op = out + (((int64_t) seq * a.n_q + i) * a.hq + kvh * g + r % g) * D;
-#pragma unroll
-        for (int ct = 0; ct < NT; ct++) op[16 * ct + l16] = o[ct][v] * inv;
-    }
+    for (int ct = 0; ct < NT; ct++) *(fm_f4 *) &op[16 * ct + 4 * lg] = o[ct] * inv;
 }
 
 // the splits of a workgroup row: M = max m_s, L = sum l_s exp(m_s - M),
@@ -431,7 +415,7 @@ __global__ __launch_bounds__(kFmThreads) void k_fattn_mfma_combine(fattn_args a,
             const int64_t pr = (blk * ns + z) * kFmRows + r;
             const float ms = ml[2 * pr];
             if (ms == -INFINITY) continue;
-            const float w = __expf(ms - mx);
+            const float w = __builtin_amdgcn_exp2f(ms - mx);  // maxima in base-2 exponent units
             L += ml[2 * pr + 1] * w;
             acc += part[pr * D + dim] * w;
         }
