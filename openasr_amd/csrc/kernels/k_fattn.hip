@@ -471,6 +471,10 @@ __device__ __forceinline__ void fa_issue_kv(const char * kc, const char * vb, in
         __builtin_amdgcn_global_load_lds((const void __attribute__((address_space(1))) *) src,
                                          (void __attribute__((address_space(3))) *) (s_kw + u * 64), 16, 0, 0);
     }
+    // every K request is issued ahead of every V request: the callers' "at
+    // most 63 outstanding" waits rely on that order, which the scheduler must
+    // not change
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < kFaChunk; j++) {
         const int off = (j < clen ? j : clen - 1) * vs + loff;
