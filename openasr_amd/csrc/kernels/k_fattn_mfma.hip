@@ -55,14 +55,22 @@ __device__ __forceinline__ fm_h8 fm_load8(const _Float16 * p) { return *(const f
 // per kernel): 0 no mask (zeros); 1 16-byte rows -- the aligned 16-byte
 // piece at pos, or the last piece holding an entry below n_kv when pos is
 // past it (an aligned 16-byte piece holding a valid entry lies in that
-// entry's page); 2 other rows -- eight 2-byte loads, indexes clamped below
-// n_kv. fm_mask_fix: positions at or past n_kv become -inf.
+// entry's page); 3 4-byte rows -- four word loads the same way; 2 other
+// rows -- eight 2-byte loads, indexes clamped below n_kv. fm_mask_fix:
+// positions at or past n_kv become -inf.
 template <int MM>
 __device__ __forceinline__ fm_u4 fm_mask_load(const uint16_t * row, int pos, int n_kv) {
     if constexpr (MM == 0) {
         return fm_u4{0, 0, 0, 0};
     } else if constexpr (MM == 1) {
         return *(const fm_u4 *) (row + min(pos, (n_kv - 1) & ~7));
+    } else if constexpr (MM == 3) {
+        // 4-byte rows: four word loads, clamped to the last word holding an
+        // entry below n_kv (pos is even; a word holding a valid entry lies in
+        // that entry's page)
+        const uint32_t * w = (const uint32_t *) row;
+        const int wi = pos >> 1, wl = (n_kv - 1) >> 1;
+        return fm_u4{w[min(wi, wl)], w[min(wi + 1, wl)], w[min(wi + 2, wl)], w[min(wi + 3, wl)]};
     } else {
         uint32_t h[8];
 #pragma unroll
@@ -407,17 +415,36 @@ __global__ __launch_bounds__(kFmThreads) void k_fattn_mfma_combine(fattn_args a,
     const int ns = a.mfma_split;
     const int64_t all_rows = n_blk * ns * kFmRows;
     const float * ml = part + all_rows * D;
+    // batches of kB splits: every load of a batch is requested before any is
+    // used (indexes clamped to the last split, the extra terms masked), so a
+    // batch costs one memory round trip
+    constexpr int kB = 16;
     float mx = -INFINITY;
-    for (int z = 0; z < ns; z++) mx = fmaxf(mx, ml[2 * ((blk * ns + z) * kFmRows + r)]);
+    for (int z0 = 0; z0 < ns; z0 += kB) {
+        float mz[kB];
+#pragma unroll
+        for (int k = 0; k < kB; k++) mz[k] = ml[2 * ((blk * ns + min(z0 + k, ns - 1)) * kFmRows + r)];
+#pragma unroll
+        for (int k = 0; k < kB; k++) mx = z0 + k < ns ? fmaxf(mx, mz[k]) : mx;
+    }
     float L = 0.0f, acc = 0.0f;
     if (mx != -INFINITY) {
-        for (int z = 0; z < ns; z++) {
-            const int64_t pr = (blk * ns + z) * kFmRows + r;
-            const float ms = ml[2 * pr];
-            if (ms == -INFINITY) continue;
-            const float w = __builtin_amdgcn_exp2f(ms - mx);  // maxima in base-2 exponent units
-            L += ml[2 * pr + 1] * w;
-            acc += part[pr * D + dim] * w;
+        for (int z0 = 0; z0 < ns; z0 += kB) {
+            float mz[kB], lz[kB], oz[kB];
+#pragma unroll
+            for (int k = 0; k < kB; k++) {
+                const int64_t pr = (blk * ns + min(z0 + k, ns - 1)) * kFmRows + r;
+                mz[k] = ml[2 * pr];
+                lz[k] = ml[2 * pr + 1];
+                oz[k] = part[pr * D + dim];
+            }
+#pragma unroll
+            for (int k = 0; k < kB; k++) {
+                if (z0 + k >= ns || mz[k] == -INFINITY) continue;
+                const float w = __builtin_amdgcn_exp2f(mz[k] - mx);  // maxima in base-2 exponent units
+                L += lz[k] * w;
+                acc += oz[k] * w;
+            }
         }
     }
     out[(((int64_t) seq * a.n_q + i) * a.hq + head) * D + dim] = L > 0.0f ? acc / L : 0.0f;
@@ -463,15 +490,18 @@ void launch_fattn_mfma(const fattn_args & a, void * scratch, float * out, hipStr
     const int qb = fm_q_blocks(a);
     const dim3 grid((unsigned) (qb * a.hkv * a.n_seq * std::max(1, a.mfma_split)));
     float * part = (float *) scratch;
-    const int mm = !a.mask ? 0 : (((uintptr_t) a.mask | (uintptr_t) a.m_nb1 | (uintptr_t) a.m_nb3) & 15) == 0 ? 1 : 2;
+    const uintptr_t mal = (uintptr_t) a.mask | (uintptr_t) a.m_nb1 | (uintptr_t) a.m_nb3;
+    const int mm = !a.mask ? 0 : (mal & 15) == 0 ? 1 : (mal & 3) == 0 ? 3 : 2;
     auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, dim3(kFmThreads), 0, s, a, out, part); };
     if (a.d == 128) {
         if (mm == 0) go(k_fattn_mfma<128, 0>);
         else if (mm == 1) go(k_fattn_mfma<128, 1>);
+        else if (mm == 3) go(k_fattn_mfma<128, 3>);
         else go(k_fattn_mfma<128, 2>);
     } else {
         if (mm == 0) go(k_fattn_mfma<64, 0>);
         else if (mm == 1) go(k_fattn_mfma<64, 1>);
+        else if (mm == 3) go(k_fattn_mfma<64, 3>);
         else go(k_fattn_mfma<64, 2>);
     }
     note_hip_error(hipGetLastError());
