@@ -17,7 +17,8 @@
 // fidelity 5).
 //
 // Three launch forms compute it:
-//   decode one wave per (chunk, query head, sequence) for a single query
+//   decode one wave per (chunk, kv head, sequence) and query head (or
+//          pair of the kv head's query heads) for a single query
 //          position: mask first, then the chunk's K and V, no barriers;
 //          partials to scratch, combined by a second launch.
 //   split  one workgroup per (chunk, kv head, sequence, query tile): loads
@@ -491,88 +492,172 @@ __device__ __forceinline__ void wait_vmcnt() {
     __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
 }
 
-// The decode form's item (chunk c, sequence s, kv head k, query head hh of
-// the kv head's g) of workgroup b: item = u * g + hh with unit u = c * nkt +
-// s * hkv + k. Workgroups are dealt to the 8 XCDs round-robin (b % 8); the g
-// heads of a unit are XCD b % 8's consecutive workgroups b, b + 8, ..., and
-// consecutive units go to consecutive XCDs, so the masked tail of the span
-// (the last chunks, the last units) spreads over every XCD. A grid of
-// fa_decode_grid(items, g) workgroups covers every item once.
+// The decode form's item of workgroup b: a unit (chunk c, sequence s, kv
+// head k) and one group hg of G query heads of the kv head's g (ng = g / G
+// groups): item = u * ng + hg with unit u = c * nkt + s * hkv + k (or, for
+// G = 2, u = (s * hkv + k) * n_chunks + c). Workgroups are dealt to the 8
+// XCDs round-robin (b % 8); the ng groups of a unit are XCD b % 8's
+// consecutive workgroups b, b + 8, ..., whose L2 serves the second read of
+// the chunk's K/V rows, and consecutive units go to consecutive XCDs, so the
+// masked tail of the span spreads over every XCD. A grid of
+// fa_decode_grid(items, ng) workgroups covers every item once.
 constexpr int kFaXcds = 8;
-__device__ __forceinline__ int64_t fa_decode_item(int64_t b, int g) {
+__device__ __forceinline__ int64_t fa_decode_item(int64_t b, int ng) {
     const int64_t r = b / kFaXcds;
-    return ((r / g) * kFaXcds + b % kFaXcds) * g + r % g;
+    return ((r / ng) * kFaXcds + b % kFaXcds) * ng + r % ng;
 }
-static int64_t fa_decode_grid(int64_t items, int g) {
-    const int64_t blk = (int64_t) kFaXcds * g;
+static int64_t fa_decode_grid(int64_t items, int ng) {
+    const int64_t blk = (int64_t) kFaXcds * ng;
     return (items + blk - 1) / blk * blk;
 }
+// query heads per decode wave (fattn_args::dheads): one, or two whose chains
+// share each K piece; more would not fit the wave's registers next to the K
+// row and the chunk's V
+// The mask of the decode wave's position (lane < clen), -inf past the span.
+// The load is unconditional (a null mask reads the K cache's first half and
+// ignores it; lanes past the span read the chunk's last position): a branch
+// around it would leave the first loads' completion unknown where the paths
+// join, and the compiler would then wait for every later request there.
+__device__ __forceinline__ float fa_decode_mask(const fattn_args & a, int seq, int pos, int clen, int lane) {
+    const int pc = pos - lane + min(lane, clen - 1);
+    const uint16_t * mp = a.mask ? (const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3) + pc
+                                 : (const uint16_t *) a.k;
+    const uint16_t raw = *mp;
+    return lane < clen ? (a.mask ? half_bits_to_float(raw) : 0.0f) : -INFINITY;
+}
 
-// Decode form (one query position): one wave -- a workgroup of its own --
-// per (chunk, query head, sequence). For the scores lane p owns KV position p of the chunk (its whole
-// K row, the query broadcast from LDS); for P*V lane l owns dims D/64*l.. of
-// every position, the chunk's p values broadcast lane by lane. After the
-// mask, K and V are requested in one burst. Each score chain runs over the
-// dims in order in one lane, and each P*V chain over the positions in order
-// in one lane, as the definition has them. A workgroup of one wave takes a
-// CU's load and LDS bandwidth to itself where four queued behind each other
-// (batch 1: 9.8 -> 8.7 us a launch); the g query heads of one kv head are
-// workgroups b, b + 8, ... -- the same XCD, whose L2 serves the second read
-// of the chunk's K/V rows (fa_decode_item).
+// STEP: the wave holding this step's position (jn >= 0) writes the new K / V
+// rows into the f16 caches (SET_ROWS). Called last: stores issued after the
+// K/V burst whose data registers were then reused would make the compiler
+// wait for every request of the burst.
+__device__ __forceinline__ void fa_decode_set_rows(const attn_step_args & st, int jn, int64_t r_new, int kvh, int seq,
+                                                   int lane, uint16_t k0, uint16_t k1, uint16_t v0, uint16_t v1) {
+    if (jn < 0) return;
+    if (r_new < st.kc_rows) {
+        uint16_t * kd = (uint16_t *) (st.kc + r_new * st.kc_nb1 + (int64_t) kvh * st.kc_nb2 + (int64_t) seq * st.kc_nb3);
+        kd[lane] = k0;
+        kd[lane + 64] = k1;
+    }
+    if (r_new < st.vc_rows) {
+        uint16_t * vd = (uint16_t *) (st.vc + r_new * st.vc_nb1 + (int64_t) kvh * st.vc_nb2 + (int64_t) seq * st.vc_nb3);
+        vd[lane] = v0;
+        vd[lane + 64] = v1;
+    }
+}
+
+// The G score chains of one position (lane = position): for each query head
+// h of the kv head, acc_h = fma(k[d], q_h[d], acc_h) over the dims in order
+// from 0, in f32. One K piece feeds the G chains, which advance together; the
+// queries are f16 halves in LDS (their f16-rounded values), so each step is
+// one v_fma_mix_f32. The query pieces are read two 8-dim steps ahead of their
+// use: held all at once they would take 4 * D / 8 registers a head.
+template <int D, int G>
+__device__ __forceinline__ void fa_dot_hg(const uint4 (&kr)[D / 8], const uint16_t (*sq)[D], float (&sc)[G]) {
+    constexpr int KU = D / 8;
+    uint4 q0[G], q1[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        sc[h] = 0.0f;
+        q0[h] = *(const uint4 *) &sq[h][0];
+        q1[h] = *(const uint4 *) &sq[h][8];
+    }
+#pragma unroll
+    for (int u = 0; u < KU; u++) {
+        uint4 q2[G];
+#pragma unroll
+        for (int h = 0; h < G; h++) q2[h] = *(const uint4 *) &sq[h][8 * (u + 2 < KU ? u + 2 : KU - 1)];
+        // the reads above stay here: hoisted, every piece would be live at once
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            // each head converts the K halves inside its own fused
+            // multiply-adds (v_fma_mix_f32): shared, the converted row would
+            // take D registers
+            uint4 kx = kr[u];
+            if (h > 0) asm volatile("" : "+v"(kx.x), "+v"(kx.y), "+v"(kx.z), "+v"(kx.w));
+            float kf[8], qf[8];
+            unpack8(kx, kf);
+            unpack8(q0[h], qf);
+#pragma unroll
+            for (int i = 0; i < 8; i++) sc[h] = fmaf(kf[i], qf[i], sc[h]);
+            q0[h] = q1[h];
+            q1[h] = q2[h];
+        }
+    }
+}
+
+// Decode form (one query position): one wave -- a workgroup of its own -- per
+// (chunk, kv head, sequence) and group of G query heads of the kv head, so a
+// kv head's K/V rows are requested once per G heads. For the scores lane p owns KV position p of the
+// chunk (its whole K row, each query broadcast from LDS); for P*V lane l owns
+// dims D/64*l.. of every position, the chunk's p values broadcast lane by
+// lane. After the mask, K and V are requested in one burst. Each score chain
+// runs over the dims in order in one lane, and each P*V chain over the
+// positions in order in one lane, as the definition has them. A workgroup of
+// one wave takes a CU's load and LDS bandwidth to itself where four queued
+// behind each other (batch 1: 9.8 -> 8.7 us a launch).
 //
 // STEP (decode step, D = 128): the wave also derives its inputs from the
-// fused QKV projection -- the query row's RMS norm * w and NEOX RoPE (the
+// fused QKV projection -- each query row's RMS norm * w and NEOX RoPE (the
 // arithmetic of k_rms_norm_rope128), and, in the chunk holding this step's
 // position, the new K row (same) and V row, which replace that cache row in
-// the wave's registers; the first query head's wave also writes them into the
-// f16 caches (SET_ROWS). No other wave reads the new row from the cache in
-// this launch, so the write needs no ordering.
-template <int D, bool STEP>
+// the wave's registers; that wave also writes them into the f16 caches
+// (SET_ROWS, after its outputs). No other wave reads the new row from the
+// cache in this launch, so the write needs no ordering.
+template <int D, bool STEP, int G>
 __global__ __launch_bounds__(64) void k_fattn_decode(attn_step_args st, float * __restrict__ part_m,
                                                      float * __restrict__ part_l, float * __restrict__ part_acc) {
     constexpr int DL = D / 64;
     constexpr int KU = D / 8;  // 16-byte pieces of a K row
     static_assert(!STEP || D == 128, "the step form handles 128-wide heads");
-    __shared__ __align__(16) uint16_t s_q[1][D];    // the query row, f16
-    __shared__ uint4 s_k[1][kFaChunk * KU];         // the chunk's K rows, swizzled (fa_kslot)
-    __shared__ __align__(16) uint16_t s_vnew[1][D];  // STEP: the new V row
+    __shared__ __align__(16) uint16_t s_q[G][D];  // the query rows, f16
+    __shared__ uint4 s_k[kFaChunk * KU];          // the chunk's K rows, swizzled (fa_kslot)
+    __shared__ __align__(16) uint16_t s_vnew[D];  // STEP: the new V row
     const fattn_args & a = st.fa;
     const int lane = (int) threadIdx.x & 63;
-    constexpr int wave = 0;
     const int nc = a.n_chunks;
-    const int g = a.hq / a.hkv;
-    const int64_t item = fa_decode_item(blockIdx.x, g);
-    if (item >= (int64_t) nc * a.hq * a.n_seq) return;  // the grid's padding
     const int64_t nkt = (int64_t) a.hkv * a.n_seq;
-    const int hh = (int) (item % g);
-    const int kt = (int) ((item / g) % nkt);  // seq * hkv + kvh
-    const int c = (int) (item / (g * nkt));
+    const int g = a.hq / a.hkv, ng = g / G;
+    const int64_t item = fa_decode_item(blockIdx.x, ng);
+    if (item >= (int64_t) nc * nkt * ng) return;  // the grid's padding
+    const int64_t unit = item / ng;
+    // G = 2 (waves in several rounds): chunk-minor units, so waves resident
+    // together stream neighbouring 16 KB K / V blocks rather than blocks 1 MB
+    // apart (1.7B, 3000 positions: 2.44 -> 2.40 ms a step); G = 1 (one round):
+    // chunk-major (0.6B, 640 positions: 1.24 -> 1.22 ms)
+    const int c = (int) (G == 2 ? unit % nc : unit / nkt);
+    const int kt = (int) (G == 2 ? unit / nc : unit % nkt);  // seq * hkv + kvh
     const int kvh = kt % a.hkv, seq = kt / a.hkv;
-    const int head = kvh * g + hh;
-    const int hs = seq * a.hq + head;
+    const int head0 = kvh * g + (int) (item % ng) * G;
     const int kv_seq = seq / a.rk3;
     const int clen = min(kFaChunk, a.n_kv - c * kFaChunk);
-    const int64_t prow = hs;  // partial row: tile (seq, kvh) row head % g
+    const int64_t prow0 = (int64_t) seq * a.hq + head0;  // partial rows prow0 + h
     const int pos = c * kFaChunk + lane;
 
-    // the query (f16-rounded) and the mask first; in the step form every
-    // independent input is requested before any is used, and the query's
+    // the queries (f16-rounded) and the mask first; in the step form every
+    // independent input is requested before any is used, and the queries'
     // norm and rotation wait until the chunk's K/V loads are in flight
     int jn = -1;  // STEP: the chunk row of this step's position, if in this chunk
     int64_t r_new = -1;
     float mv = -INFINITY;
-    // STEP: the query's inputs, normalised and rotated once the K/V loads are in flight
-    float qx0 = 0.0f, qx1 = 0.0f, qw0 = 0.0f, qw1 = 0.0f;
+    // STEP: the queries' inputs, normalised and rotated once the K/V loads are in flight
+    float qx0[G], qx1[G], qw0 = 0.0f, qw1 = 0.0f;
     float2 qcs = make_float2(0.0f, 0.0f);
-    // STEP: the new K / V row's inputs, requested with the query's (every wave:
+    // STEP: the new K / V row's inputs, requested with the queries' (every wave:
     // which one holds this step's position is known only with the index)
     float kx0 = 0.0f, kx1 = 0.0f, kw0 = 0.0f, kw1 = 0.0f, vx0 = 0.0f, vx1 = 0.0f;
+    uint16_t knew0 = 0, knew1 = 0, vnew0 = 0, vnew1 = 0;  // STEP: the new rows, f16
     if constexpr (STEP) {
         const char * ip = st.idx + (int64_t) (kvh % st.idx_ne1) * st.idx_nb1 + (int64_t) (seq % st.idx_ne2) * st.idx_nb2;
-        const float * qx = (const float *) (st.qsrc + (int64_t) head * st.q_nb1 + (int64_t) seq * st.q_nb2);
-        const float x0 = qx[lane], x1 = qx[lane + 64];
-        const float w0 = st.qw[lane], w1 = st.qw[lane + 64];
-        const float2 cs = st.rope[seq * 64 + lane];
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float * qx = (const float *) (st.qsrc + (int64_t) (head0 + h) * st.q_nb1 + (int64_t) seq * st.q_nb2);
+            qx0[h] = qx[lane];
+            qx1[h] = qx[lane + 64];
+        }
+        qw0 = st.qw[lane];
+        qw1 = st.qw[lane + 64];
+        qcs = st.rope[seq * 64 + lane];
         const float * kxp = (const float *) (st.ksrc + (int64_t) kvh * st.k_nb1 + (int64_t) seq * st.k_nb2);
         kx0 = kxp[lane];
         kx1 = kxp[lane + 64];
@@ -581,35 +666,31 @@ __global__ __launch_bounds__(64) void k_fattn_decode(attn_step_args st, float * 
         const float * vxp = (const float *) (st.vsrc + (int64_t) kvh * st.v_nb1 + (int64_t) seq * st.v_nb2);
         vx0 = vxp[lane];
         vx1 = vxp[lane + 64];
-        if (lane < clen) {
-            mv = 0.0f;
-            if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
-        }
-        r_new = st.idx_i64 ? *(const int64_t *) ip : (int64_t) *(const int32_t *) ip;
-        qx0 = x0;
-        qx1 = x1;
-        qw0 = w0;
-        qw1 = w1;
-        qcs = cs;
+        mv = fa_decode_mask(a, seq, pos, clen, lane);
+        // the index as one or two 32-bit words, both requested whatever its
+        // type (a branch here would make the compiler wait for every request
+        // of the K/V burst before the queries' norm)
+        const uint32_t lo = *(const uint32_t *) ip, hi = *(const uint32_t *) (ip + (st.idx_i64 ? 4 : 0));
+        r_new = st.idx_i64 ? (int64_t) (((uint64_t) hi << 32) | lo) : (int64_t) (int32_t) lo;
         const int64_t j = r_new - (int64_t) c * kFaChunk;
         jn = j >= 0 && j < clen ? (int) j : -1;
     } else {
-        const float * qp = (const float *) (a.q + (int64_t) head * a.q_nb2 + (int64_t) seq * a.q_nb3);
-        for (int d = lane; d < D; d += 64) s_q[wave][d] = float_to_half_bits(qp[d]);
-        if (lane < clen) {
-            mv = 0.0f;
-            if (a.mask) mv = half_bits_to_float(((const uint16_t *) (a.mask + (int64_t) (seq % a.m_ne3) * a.m_nb3))[pos]);
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float * qp = (const float *) (a.q + (int64_t) (head0 + h) * a.q_nb2 + (int64_t) seq * a.q_nb3);
+            for (int d = lane; d < D; d += 64) s_q[h][d] = float_to_half_bits(qp[d]);
         }
+        mv = fa_decode_mask(a, seq, pos, clen, lane);
     }
     const bool live = mv != -INFINITY;
     if (__ballot(live) == 0) {
-        if (lane == 0) {
-            part_m[prow * nc + c] = -INFINITY;
-            part_l[prow * nc + c] = 0.0f;
+        if (lane < G) {
+            part_m[(prow0 + lane) * nc + c] = -INFINITY;
+            part_l[(prow0 + lane) * nc + c] = 0.0f;
         }
         if constexpr (STEP) {
             // the cache row is written even when no query attends to it
-            if (jn < 0 || hh != 0) return;
+            if (jn < 0) return;
         } else {
             return;
         }
@@ -622,12 +703,15 @@ __global__ __launch_bounds__(64) void k_fattn_decode(attn_step_args st, float * 
     const char * vb = a.v + (int64_t) kvh * a.v_nb2 + (int64_t) kv_seq * a.v_nb3 + (int64_t) c * kFaChunk * a.v_nb1;
     const int vs = (int) a.v_nb1, loff = lane * DL * 2;
     uint32_t vr[kFaChunk];
-    fa_issue_kv<D>(kc, vb, a.k_nb1, vs, loff, clen, lane, &s_k[wave][0], vr);
+    fa_issue_kv<D>(kc, vb, a.k_nb1, vs, loff, clen, lane, &s_k[0], vr);
     if constexpr (STEP) {
-        float y0, y1;
-        as_norm_rope(qx0, qx1, qw0, qw1, qcs, st.q_eps, y0, y1);
-        s_q[wave][lane] = float_to_half_bits(y0);
-        s_q[wave][lane + 64] = float_to_half_bits(y1);
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            float y0, y1;
+            as_norm_rope(qx0[h], qx1[h], qw0, qw1, qcs, st.q_eps, y0, y1);
+            s_q[h][lane] = float_to_half_bits(y0);
+            s_q[h][lane + 64] = float_to_half_bits(y1);
+        }
         if (jn >= 0) {
             // this step's K / V rows: K replaces the LDS row jn once the
             // chunk's K has landed (its requests precede the 64 V requests, so
@@ -635,26 +719,21 @@ __global__ __launch_bounds__(64) void k_fattn_decode(attn_step_args st, float * 
             // through LDS to the dims layout
             float y0, y1;
             as_norm_rope(kx0, kx1, kw0, kw1, qcs, st.k_eps, y0, y1);
-            const uint16_t k0 = float_to_half_bits(y0), k1 = float_to_half_bits(y1);
-            const uint16_t v0 = float_to_half_bits(vx0), v1 = float_to_half_bits(vx1);
-            uint16_t * krow = (uint16_t *) &s_k[wave][0];
+            knew0 = float_to_half_bits(y0);
+            knew1 = float_to_half_bits(y1);
+            vnew0 = float_to_half_bits(vx0);
+            vnew1 = float_to_half_bits(vx1);
+            uint16_t * krow = (uint16_t *) &s_k[0];
             wait_vmcnt<63>();
-            krow[fa_kslot(jn, lane >> 3, KU) * 8 + (lane & 7)] = k0;
-            krow[fa_kslot(jn, (lane + 64) >> 3, KU) * 8 + (lane & 7)] = k1;
-            s_vnew[wave][lane] = v0;
-            s_vnew[wave][lane + 64] = v1;
-            if (hh == 0 && r_new < st.kc_rows) {
-                uint16_t * kd = (uint16_t *) (st.kc + r_new * st.kc_nb1 + (int64_t) kvh * st.kc_nb2 + (int64_t) seq * st.kc_nb3);
-                kd[lane] = k0;
-                kd[lane + 64] = k1;
-            }
-            if (hh == 0 && r_new < st.vc_rows) {
-                uint16_t * vd = (uint16_t *) (st.vc + r_new * st.vc_nb1 + (int64_t) kvh * st.vc_nb2 + (int64_t) seq * st.vc_nb3);
-                vd[lane] = v0;
-                vd[lane + 64] = v1;
-            }
+            krow[fa_kslot(jn, lane >> 3, KU) * 8 + (lane & 7)] = knew0;
+            krow[fa_kslot(jn, (lane + 64) >> 3, KU) * 8 + (lane & 7)] = knew1;
+            s_vnew[lane] = vnew0;
+            s_vnew[lane + 64] = vnew1;
         }
-        if (__ballot(live) == 0) return;  // a fully masked chunk only had the cache row to write
+        if (__ballot(live) == 0) {  // a fully masked chunk only has the cache row to write
+            fa_decode_set_rows(st, jn, r_new, kvh, seq, lane, knew0, knew1, vnew0, vnew1);
+            return;
+        }
     }
     wait_vmcnt<63>();  // the K requests (ahead of the V ones) have landed
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -662,34 +741,47 @@ __global__ __launch_bounds__(64) void k_fattn_decode(attn_step_args st, float * 
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     uint4 kr[KU];
 #pragma unroll
-    for (int u = 0; u < KU; u++) kr[u] = s_k[wave][fa_kslot(lane, u, KU)];
+    for (int u = 0; u < KU; u++) kr[u] = s_k[fa_kslot(lane, u, KU)];
     if constexpr (STEP) {
         if (jn >= 0) {
-            const uint32_t vn = *(const uint32_t *) &s_vnew[wave][lane * DL];
+            const uint32_t vn = *(const uint32_t *) &s_vnew[lane * DL];
 #pragma unroll
             for (int j = 0; j < kFaChunk; j++) vr[j] = j == jn ? vn : vr[j];
         }
     }
 
-    // scores: lane = position, the f32 fma chain over the dims in order
-    const float sc = fa_dot_h<D>(kr, (const uint4 *) &s_q[wave][0]);
-    const float sv = live ? sc * a.scale + mv : -INFINITY;
-    const float m = wave_max(sv);
-    const float p = sv == -INFINITY ? 0.0f : expf_det(sv - m);
-    // P * V: lane = dims; l = l + p and acc = fma(p, v, acc) over the live
-    // positions in order, p_j broadcast through a scalar register. Masked
-    // positions (which may hold anything in the cache, even NaN) are skipped
-    // by a scalar test of the live-position mask; with every position live
-    // the loop runs without a test.
-    const uint64_t live_bits = __ballot(live);
-    float acc[DL], l = 0.0f;
+    // scores: lane = position, per query head the f32 fma chain over the dims in order
+    float sc[G], p[G], m[G];
+    fa_dot_hg<D, G>(kr, s_q, sc);
 #pragma unroll
-    for (int i = 0; i < DL; i++) acc[i] = 0.0f;
+    for (int h = 0; h < G; h++) {
+        const float sv = live ? sc[h] * a.scale + mv : -INFINITY;
+        m[h] = wave_max(sv);
+        p[h] = sv == -INFINITY ? 0.0f : expf_det(sv - m[h]);
+    }
+    // P * V: lane = dims; per head l = l + p and acc = fma(p, v, acc) over the
+    // live positions in order, p_j broadcast through a scalar register.
+    // Masked positions (which may hold anything in the cache, even NaN) are
+    // skipped by a scalar test of the live-position mask; with every position
+    // live the loop runs without a test.
+    const uint64_t live_bits = __ballot(live);
+    float acc[G][DL], l[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) {
+        l[h] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < DL; i++) acc[h][i] = 0.0f;
+    }
     auto pv_step = [&](int j) {
-        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
-        l = l + pj;
-        acc[0] = fmaf(pj, half_bits_to_float((uint16_t) (vr[j] & 0xFFFF)), acc[0]);
-        if (DL == 2) acc[DL - 1] = fmaf(pj, half_bits_to_float((uint16_t) (vr[j] >> 16)), acc[DL - 1]);
+        const float v0 = half_bits_to_float((uint16_t) (vr[j] & 0xFFFF));
+        const float v1 = DL == 2 ? half_bits_to_float((uint16_t) (vr[j] >> 16)) : 0.0f;
+#pragma unroll
+        for (int h = 0; h < G; h++) {
+            const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p[h]), j));
+            l[h] = l[h] + pj;
+            acc[h][0] = fmaf(pj, v0, acc[h][0]);
+            if (DL == 2) acc[h][DL - 1] = fmaf(pj, v1, acc[h][DL - 1]);
+        }
     };
     if (live_bits == ~0ull) {
 #pragma unroll
@@ -700,13 +792,17 @@ __global__ __launch_bounds__(64) void k_fattn_decode(attn_step_args st, float * 
             if ((live_bits >> j) & 1) pv_step(j);
         }
     }
-    float * pa = part_acc + (prow * nc + c) * D + lane * DL;
 #pragma unroll
-    for (int i = 0; i < DL; i++) pa[i] = acc[i];
-    if (lane == 0) {
-        part_m[prow * nc + c] = m;
-        part_l[prow * nc + c] = l;
+    for (int h = 0; h < G; h++) {
+        float * pa = part_acc + ((prow0 + h) * nc + c) * D + lane * DL;
+#pragma unroll
+        for (int i = 0; i < DL; i++) pa[i] = acc[h][i];
+        if (lane == 0) {
+            part_m[(prow0 + h) * nc + c] = m[h];
+            part_l[(prow0 + h) * nc + c] = l[h];
+        }
     }
+    if constexpr (STEP) fa_decode_set_rows(st, jn, r_new, kvh, seq, lane, knew0, knew1, vnew0, vnew1);
 }
 
 template <int D, int R>
@@ -808,8 +904,14 @@ void fattn_plan(fattn_args & a, int n_cu) {
     // 686 tiles: 93 -> ~60 us a layer) gain from the split up to several
     // tiles a CU; 128-wide causal prefill chunks (1024 tiles) lose from it
     const bool fits = a.n_chunks <= kFaMaxChunks && part_bytes <= (256LL << 20);
-    if (fits && a.n_q == 1) a.split = 2;  // wave per (chunk, query head) of the one query
+    if (fits && a.n_q == 1) a.split = 2;  // wave per (chunk, kv head, query head group) of the one query
     else a.split = fits && tiles < (a.d == 64 ? 8LL : 2LL) * n_cu ? 1 : 0;
+    // decode waves: one per query head while they all fit the CUs at once
+    // (eight a CU: the LDS and registers of one allow that many); past that,
+    // one wave takes two heads from one K/V read, halving the rounds of waves
+    // behind each other
+    const int64_t units = (int64_t) a.n_chunks * a.hkv * a.n_seq;
+    a.dheads = g >= 2 && units * g > 8LL * n_cu ? 2 : 1;
 }
 
 template <int D, int R>
@@ -826,6 +928,23 @@ bool attn_step_supported(const fattn_args & a) {
 
 size_t attn_step_scratch_bytes(const fattn_args & a) { return fattn_scratch_bytes(a); }
 
+// one query position: rows = g query heads of a kv head, one decode wave per
+// (chunk, kv head, sequence) for all of them
+template <int R>
+static void launch_attn_step_g(const attn_step_args & st, float * pm, float * pl, float * pa, hipStream_t s) {
+    const fattn_args & a = st.fa;
+    const int64_t units = (int64_t) a.n_chunks * a.hkv * a.n_seq;
+    if (R >= 2 && a.dheads == 2) {
+        constexpr int G = R >= 2 ? 2 : 1;
+        hipLaunchKernelGGL((k_fattn_decode<128, true, G>), dim3((unsigned) fa_decode_grid(units * (R / G), R / G)),
+                           dim3(64), 0, s, st, pm, pl, pa);
+    } else {
+        hipLaunchKernelGGL((k_fattn_decode<128, true, 1>), dim3((unsigned) fa_decode_grid(units * R, R)), dim3(64), 0,
+                           s, st, pm, pl, pa);
+    }
+    launch_combine<128, R>(a, pm, pl, pa, st.out, s);
+}
+
 void launch_attn_step(const attn_step_args & st, void * scratch, hipStream_t s) {
     const fattn_args & a = st.fa;
     const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
@@ -833,15 +952,11 @@ void launch_attn_step(const attn_step_args & st, void * scratch, hipStream_t s) 
     float * pl = pm + prows;
     char * p = (char *) (pl + prows);
     float * pa = (float *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
-    const int64_t items = (int64_t) a.n_chunks * a.hq * a.n_seq;
-    hipLaunchKernelGGL((k_fattn_decode<128, true>), dim3((unsigned) fa_decode_grid(items, a.hq / a.hkv)), dim3(64), 0, s, st,
-                       pm, pl, pa);
-    float * out = st.out;
     switch (a.rows) {
-        case 1: launch_combine<128, 1>(a, pm, pl, pa, out, s); break;
-        case 2: launch_combine<128, 2>(a, pm, pl, pa, out, s); break;
-        case 4: launch_combine<128, 4>(a, pm, pl, pa, out, s); break;
-        default: launch_combine<128, 8>(a, pm, pl, pa, out, s); break;
+        case 1: launch_attn_step_g<1>(st, pm, pl, pa, s); break;
+        case 2: launch_attn_step_g<2>(st, pm, pl, pa, s); break;
+        case 4: launch_attn_step_g<4>(st, pm, pl, pa, s); break;
+        default: launch_attn_step_g<8>(st, pm, pl, pa, s); break;
     }
 }
 
@@ -864,11 +979,18 @@ static void launch_fa(const fattn_args & a, void * scratch, float * out, hipStre
         char * p = (char *) (pl + prows);
         float * pa = (float *) (((uintptr_t) p + 255) & ~(uintptr_t) 255);
         if (a.split == 2) {
-            const int64_t items = (int64_t) a.n_chunks * a.hq * a.n_seq;
+            // one query position: the tile rows are the g query heads (R = g)
+            const int64_t units = (int64_t) a.n_chunks * a.hkv * a.n_seq;
             attn_step_args st{};
             st.fa = a;
-            hipLaunchKernelGGL((k_fattn_decode<D, false>), dim3((unsigned) fa_decode_grid(items, a.hq / a.hkv)), dim3(64),
-                               0, s, st, pm, pl, pa);
+            if (R >= 2 && a.dheads == 2) {
+                constexpr int G = R >= 2 ? 2 : 1;
+                hipLaunchKernelGGL((k_fattn_decode<D, false, G>), dim3((unsigned) fa_decode_grid(units * (R / G), R / G)),
+                                   dim3(64), 0, s, st, pm, pl, pa);
+            } else {
+                hipLaunchKernelGGL((k_fattn_decode<D, false, 1>), dim3((unsigned) fa_decode_grid(units * R, R)), dim3(64),
+                                   0, s, st, pm, pl, pa);
+            }
         } else {
             const dim3 grid((unsigned) a.n_chunks, (unsigned) (a.hkv * a.n_seq), (unsigned) a.q_tiles);
             hipLaunchKernelGGL((k_fattn_split<D, R>), grid, dim3(kFaThreads), 0, s, a, pm, pl, pa);

@@ -173,6 +173,7 @@ struct fattn_args {
     int n_chunks;  // 64-position KV chunks
     int split;     // 0: one workgroup per tile; 1: chunks over workgroups; 2: one wave per chunk
                    // (1 and 2 write partials that a combine launch reduces)
+    int dheads;    // split 2: query heads per decode wave (1, or 2 sharing each K/V read)
     // optional quantization of the output for the consuming MUL_MAT:
     // -1 none, GGML_TYPE_Q8_0 or GGML_TYPE_Q4_K (Q8_K activations)
     int qtype;
