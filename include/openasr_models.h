@@ -138,11 +138,12 @@ int oa_qwen_session_set_hip_lane(oa_qwen_session * s, int enable, int prefill_ch
  * (set_flash_attention_precision, models/qwen/llm_transformer.rs:3044-3053;
  * GgmlFlashAttentionPrecision, ggml_runtime/cpu_graph.rs:122-155):
  * GGML_PREC_DEFAULT (the default, what the ASR decoder builds) lets the
- * backend take its fastest validated form -- prefill chunks on the matrix
- * cores within float tolerance; GGML_PREC_F32 (what the forced aligner
- * selects, forced_aligner_runtime.rs:622) keeps every attention in the
- * exact chunked form. Decode steps (one query) are exact under both. Other
- * values return GGML_STATUS_FAILED. Takes effect on the next step. */
+ * backend take its fastest validated form within float tolerance -- prefill
+ * chunks on the matrix cores, decode steps one workgroup per (sequence, kv
+ * head) with the combine in the launch; GGML_PREC_F32 (what the forced
+ * aligner selects, forced_aligner_runtime.rs:622) keeps every attention in
+ * the exact chunked form. Other values return GGML_STATUS_FAILED. Takes
+ * effect on the next step. */
 int oa_qwen_session_set_flash_attention_precision(oa_qwen_session * s, int precision);
 
 /* Prefill T positions of every sequence (chunked internally at 256) from
@@ -255,6 +256,13 @@ int oa_whisper_generate(oa_whisper_session * s, int32_t first_token, int n_steps
                         double * step_ms);
 /* the layer's cross K / V caches, f16 [n_frames][d_model] */
 int oa_whisper_read_cross(const oa_whisper_session * s, int layer, uint16_t * k_out, uint16_t * v_out);
+/* The precision contract of the decoder's self and cross FLASH_ATTN_EXT
+ * (flash_attention_precision of the seq2seq decoder graphs, nn/decoder.rs:
+ * 3064-3728): GGML_PREC_DEFAULT (the default) runs the single-query
+ * workgroup form within float tolerance, GGML_PREC_F32 the exact chunked
+ * form. Other values return GGML_STATUS_FAILED. Takes effect on the next
+ * step. */
+int oa_whisper_session_set_flash_attention_precision(oa_whisper_session * s, int precision);
 struct ggml_cgraph * oa_whisper_decode_graph(oa_whisper_session * s);
 
 /* ---- Qwen3-ASR audio encoder (crates/openasr-core/src/models/qwen/audio_encoder.rs) ----

@@ -35,9 +35,12 @@
 // layout of the MUL_MAT that consumes it (the attention output projection),
 // since a tile holds all query heads of one kv head: g*D consecutive
 // elements of a column.
+#include <type_traits>
+
 #include "../mi355x_common.h"
 #include "../ops.h"
 #include "../quant_dev.h"
+#include "../fattn_dev.h"
 
 namespace mi355x {
 
@@ -46,9 +49,6 @@ constexpr int kFaChunk = 64;
 constexpr int kFaMaxChunks = 256;  // 16384 KV positions
 constexpr int kFaMaxRows = 8;      // query rows (positions x heads of one kv head) per tile
 
-struct fa_tile {
-    int kvh, seq, g, tq0, ntq, nrows, kv_seq, gti;
-};
 
 __device__ __forceinline__ fa_tile fa_tile_of(const fattn_args & a) {
     fa_tile t;
@@ -255,37 +255,6 @@ struct fa_pv_shape {
     static constexpr int TPR = D / DPT;  // threads per row
 };
 
-// the tile's output rows are in LDS (row r at rows + r * D); quantize its
-// column segments for the next MUL_MAT (Q8_K for Q4_K weights, Q8_0 for Q8_0
-// weights)
-template <int D>
-__device__ __forceinline__ void fa_quantize_out(const fattn_args & a, const fa_tile & t, const float * rows) {
-    const int lane = (int) threadIdx.x & 63, wave = (int) threadIdx.x >> 6;
-    const int seg = t.g * D;
-    const int64_t K = (int64_t) a.hq * D;
-    const int64_t e0 = (int64_t) t.kvh * seg;
-    for (int tql = 0; tql < t.ntq; tql++) {
-        const int64_t col = (int64_t) t.seq * a.n_q + t.tq0 + tql;
-        const float * row = rows + (int64_t) tql * t.g * D;
-        for (int piece = wave; piece * 256 < seg; piece += 4) {
-            const int e = piece * 256 + lane * 4;
-            const float4 v = e < seg ? *(const float4 *) (row + e) : make_float4(0.f, 0.f, 0.f, 0.f);
-            if (a.qtype == GGML_TYPE_Q4_K) {
-                const q8_K_lane o = quantize_q8_K_wave(v, lane);
-                *(char4 *) (a.act.q + col * K + e0 + e) = o.q;
-                if ((lane & 7) == 0) a.act.ssum[col * (K / 32) + (e0 + e) / 32] = (int16_t) o.ssum;
-                if (lane == 0) a.act.d[col * (K / 256) + (e0 + piece * 256) / 256] = o.d;
-            } else {
-                const q8_0_lane o = quantize_q8_0_group(v);
-                if (e < seg) {
-                    *(char4 *) (a.act.q + col * K + e0 + e) = o.q;
-                    if ((lane & 7) == 0) a.act.d[col * (K / 32) + (e0 + e) / 32] = o.d;
-                }
-            }
-        }
-    }
-}
-
 template <int D, int R>
 __global__ __launch_bounds__(kFaThreads) void k_fattn_split(fattn_args a, float * __restrict__ part_m,
                                                             float * __restrict__ part_l,
@@ -440,19 +409,6 @@ __global__ __launch_bounds__(kFaThreads) void k_fattn_combine(fattn_args a, cons
     }
 }
 
-// RMS norm * w, then NEOX RoPE by a (cos, sin) pair, of one 128-element row
-// held by a wave (lane l: elements l and l + 64, rotation index l) -- the
-// arithmetic of k_rms_norm_rope128 with the angle from the rope table
-__device__ __forceinline__ void as_norm_rope(float x0, float x1, float w0, float w1, float2 cs, float eps, float & y0,
-                                             float & y1) {
-    const double s2 = wave_sum_d((double) (x0 * x0) + (double) (x1 * x1));
-    const float var = (float) (s2 / 128.0);
-    const float scale = 1.0f / sqrtf(var + eps);
-    const float v0 = (x0 * scale) * w0, v1 = (x1 * scale) * w1;
-    y0 = v0 * cs.x - v1 * cs.y;
-    y1 = v0 * cs.y + v1 * cs.x;
-}
-
 // The decode wave's K and V requests for one chunk; rows past the span
 // repeat the last one. K goes straight to LDS (global_load_lds, 16 bytes a
 // lane): instruction u fills slots u*64 .. u*64+63 of the wave's area, slot
@@ -524,25 +480,6 @@ __device__ __forceinline__ float fa_decode_mask(const fattn_args & a, int seq, i
                                  : (const uint16_t *) a.k;
     const uint16_t raw = *mp;
     return lane < clen ? (a.mask ? half_bits_to_float(raw) : 0.0f) : -INFINITY;
-}
-
-// STEP: the wave holding this step's position (jn >= 0) writes the new K / V
-// rows into the f16 caches (SET_ROWS). Called last: stores issued after the
-// K/V burst whose data registers were then reused would make the compiler
-// wait for every request of the burst.
-__device__ __forceinline__ void fa_decode_set_rows(const attn_step_args & st, int jn, int64_t r_new, int kvh, int seq,
-                                                   int lane, uint16_t k0, uint16_t k1, uint16_t v0, uint16_t v1) {
-    if (jn < 0) return;
-    if (r_new < st.kc_rows) {
-        uint16_t * kd = (uint16_t *) (st.kc + r_new * st.kc_nb1 + (int64_t) kvh * st.kc_nb2 + (int64_t) seq * st.kc_nb3);
-        kd[lane] = k0;
-        kd[lane + 64] = k1;
-    }
-    if (r_new < st.vc_rows) {
-        uint16_t * vd = (uint16_t *) (st.vc + r_new * st.vc_nb1 + (int64_t) kvh * st.vc_nb2 + (int64_t) seq * st.vc_nb3);
-        vd[lane] = v0;
-        vd[lane + 64] = v1;
-    }
 }
 
 // The G score chains of one position (lane = position): for each query head
@@ -886,6 +823,7 @@ static int64_t fa_tiles(const fattn_args & a) { return (int64_t) a.hkv * a.n_seq
 
 size_t fattn_scratch_bytes(const fattn_args & a) {
     if (a.mfma) return fattn_mfma_scratch_bytes(a);
+    if (a.dec) return fattn_dec_scratch_bytes(a);
     if (!a.split) return 0;
     const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
     return (size_t) prows * (2 + (size_t) a.d) * sizeof(float) + 1024;
@@ -923,10 +861,26 @@ static void launch_combine(const fattn_args & a, const float * pm, const float *
 }
 
 bool attn_step_supported(const fattn_args & a) {
+    if (a.dec) return a.d == 128;  // the default-precision workgroup form
     return a.d == 128 && a.n_q == 1 && a.split == 2 && fattn_supported(a.d, a.hq, a.hkv);
 }
 
 size_t attn_step_scratch_bytes(const fattn_args & a) { return fattn_scratch_bytes(a); }
+
+void launch_fattn_combine(const fattn_args & a, const float * pm, const float * pl, const float * pa, float * out,
+                          hipStream_t s) {
+    auto go = [&](auto d) {
+        constexpr int D = decltype(d)::value;
+        switch (a.rows) {
+            case 1: launch_combine<D, 1>(a, pm, pl, pa, out, s); break;
+            case 2: launch_combine<D, 2>(a, pm, pl, pa, out, s); break;
+            case 4: launch_combine<D, 4>(a, pm, pl, pa, out, s); break;
+            default: launch_combine<D, 8>(a, pm, pl, pa, out, s); break;
+        }
+    };
+    if (a.d == 128) go(std::integral_constant<int, 128>{});
+    else go(std::integral_constant<int, 64>{});
+}
 
 // one query position: rows = g query heads of a kv head, one decode wave per
 // (chunk, kv head, sequence) for all of them
@@ -947,6 +901,10 @@ static void launch_attn_step_g(const attn_step_args & st, float * pm, float * pl
 
 void launch_attn_step(const attn_step_args & st, void * scratch, hipStream_t s) {
     const fattn_args & a = st.fa;
+    if (a.dec) {
+        launch_fattn_dec(st, true, st.out, scratch, s);
+        return;
+    }
     const int64_t prows = fa_tiles(a) * a.rows * a.n_chunks;
     float * pm = (float *) scratch;
     float * pl = pm + prows;
@@ -1015,6 +973,12 @@ static void launch_fa_d(const fattn_args & a, void * scratch, float * out, hipSt
 void launch_fattn(const fattn_args & a, void * scratch, float * out, hipStream_t stream) {
     if (a.mfma) {
         launch_fattn_mfma(a, scratch, out, stream);
+        return;
+    }
+    if (a.dec) {
+        attn_step_args st{};
+        st.fa = a;
+        launch_fattn_dec(st, false, out, scratch, stream);
         return;
     }
     if (a.d == 128) launch_fa_d<128>(a, scratch, out, stream);

@@ -1404,7 +1404,11 @@ bool planner::make_fattn(const ggml_tensor * t, fattn_args & a) {
     // host's flash-attention precision contract): the matrix-core form
     a.mfma = t->op_params[3] != GGML_PREC_F32 && fattn_mfma_supported(a);
     if (a.mfma) fattn_mfma_plan(a, n_cu);
-    if (!a.mfma && !fattn_fits(a)) return fail(t, "KV span longer than the kernel's chunk table");
+    // one query at the default precision: one workgroup per (sequence, kv
+    // head, KV split), the waves merged in the launch (k_fattn_dec.hip),
+    // where that form is the faster one
+    if (!a.mfma && t->op_params[3] != GGML_PREC_F32 && fattn_dec_supported(a)) fattn_dec_plan(a, n_cu);
+    if (!a.mfma && !a.dec && !fattn_fits(a)) return fail(t, "KV span longer than the kernel's chunk table");
     return true;
 }
 
@@ -1493,7 +1497,7 @@ bool planner::plan_fattn(int i, const ggml_tensor * t) {
             }
             launch_fattn(la, g, out, s);
         },
-        t, a.mfma ? "flash_attn_mfma" : "flash_attn_ext");
+        t, a.mfma ? "flash_attn_mfma" : a.dec ? "flash_attn_dec" : "flash_attn_ext");
     if (a.qtype >= 0) {
         act_src = view;
         act_wtype = a.qtype;
@@ -1686,7 +1690,8 @@ bool planner::plan_attn_step(int i, const ggml_tensor * t) {
             if (!la.out) la.out = (float *) (gen_base(b) + out_off);
             launch_attn_step(la, gen_base(b), s);
         },
-        F, "attn_step", f32_unread ? std::vector<const ggml_tensor *>{sk, sv} : std::vector<const ggml_tensor *>{F, sk, sv});
+        F, fa.dec ? "attn_step_dec" : "attn_step",
+        f32_unread ? std::vector<const ggml_tensor *>{sk, sv} : std::vector<const ggml_tensor *>{F, sk, sv});
     if (fa.qtype >= 0) {
         act_src = oview;
         act_wtype = fa.qtype;

@@ -182,12 +182,29 @@ struct fattn_args {
     // (k_fattn_mfma.hip, float tolerance) instead of the chunked definition
     int mfma;
     int mfma_split;  // KV splits of the matrix-core form (partials + combine when > 1)
+    // one query at the default precision: the workgroup form (k_fattn_dec.hip,
+    // float tolerance); its KV splits (0: not used; > 1: partials + combine)
+    int dec;
 };
 // whether the matrix-core form takes this attention (n_q > 1, D 64 / 128)
 bool fattn_mfma_supported(const fattn_args & a);
 void fattn_mfma_plan(fattn_args & a, int n_cu);
 size_t fattn_mfma_scratch_bytes(const fattn_args & a);
 void launch_fattn_mfma(const fattn_args & a, void * scratch, float * out, hipStream_t s);
+struct attn_step_args;
+// whether the single-query workgroup form takes this attention (n_q = 1,
+// D 64 / 128, 1, 2 or 4 query heads a kv head)
+bool fattn_dec_supported(const fattn_args & a);
+// a.dec: the KV splits where the workgroup form is the faster one, else 0
+void fattn_dec_plan(fattn_args & a, int n_cu);
+size_t fattn_dec_scratch_bytes(const fattn_args & a);
+// step: the fused decode step (st's QK-norm, RoPE, new K / V rows and cache
+// writes; D 128); otherwise a plain FLASH_ATTN_EXT over st.fa into out
+void launch_fattn_dec(const attn_step_args & st, bool step, float * out, void * scratch, hipStream_t s);
+// the combine launch of the split forms over partials laid out per (tile
+// row, partial) -- a.n_chunks partials a row, a.rows rows a tile
+void launch_fattn_combine(const fattn_args & a, const float * pm, const float * pl, const float * pa, float * out,
+                          hipStream_t s);
 // The unfused attention chain of the discrete-GPU prefill (MUL_MAT(K, Q) ->
 // SOFT_MAX_EXT -> MUL_MAT(CONT(V^T), P) -> PERMUTE/CONT) as one launch, in
 // the fixed order k_attn_naive.hip defines. Q f32 [d, n_q, hq, n_seq]

@@ -130,6 +130,7 @@ def lib() -> C.CDLL:
     s("oa_whisper_generate", i, vp, C.c_int32, i, vp, vp)
     s("oa_whisper_read_cross", i, vp, i, vp, vp)
     s("oa_whisper_decode_graph", vp, vp)
+    s("oa_whisper_session_set_flash_attention_precision", i, vp, i)
     s("oa_qwen_generate", i, vp, vp, i, vp, vp)
     s("oa_qwen_read_kv", i, vp, i, i, vp, vp)
     s("oa_detect_degenerate_ngram", i, vp, i, i, vp, vp, vp)
@@ -424,6 +425,14 @@ class WhisperSession:
 
     def decode_graph(self):
         return lib().oa_whisper_decode_graph(self.ptr)
+
+    def set_flash_attention_precision(self, precision: int):
+        """the self and cross attention's contract (the seq2seq decoder
+        graphs' flash_attention_precision, nn/decoder.rs:3064-3728):
+        GGML_PREC_DEFAULT (the default) or GGML_PREC_F32 (the exact chunked
+        form)"""
+        self._check(lib().oa_whisper_session_set_flash_attention_precision(self.ptr, int(precision)),
+                    "set_flash_attention_precision")
 
     def position(self) -> int:
         return lib().oa_whisper_session_position(self.ptr)

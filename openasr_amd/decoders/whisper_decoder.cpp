@@ -93,6 +93,7 @@ struct wh_graph {
 struct oa_whisper_session {
     oa_whisper_model * m;
     int n_past = 0;
+    int fa_prec = GGML_PREC_DEFAULT;  // the attentions' precision contract
     ggml_context * kv_ctx = nullptr;
     ggml_backend_buffer_t kv_buf = nullptr;
     std::vector<ggml_tensor *> k_self, v_self, k_cross, v_cross;  // per layer, f16 [d_model, positions|frames]
@@ -150,6 +151,7 @@ bool build_decode(oa_whisper_session * s, wh_graph & g) {
         ggml_tensor * kc = ggml_view_3d(ctx, k_written, hd, mp, H, row_stride, head_stride, 0);
         ggml_tensor * vc = ggml_view_3d(ctx, v_written, hd, mp, H, row_stride, head_stride, 0);
         ggml_tensor * ctx_self = ggml_flash_attn_ext(ctx, heads_view(ctx, q, hd, H, 1), kc, vc, g.mask, scale, 0.0f, 0.0f);
+        ggml_flash_attn_ext_set_prec(ctx_self, (ggml_prec) s->fa_prec);
         ctx_self = ggml_reshape_2d(ctx, ctx_self, d, 1);
         state = ggml_add(ctx, linear(ctx, L[OA_WH_SELF_O], ctx_self, L[OA_WH_SELF_O_B]), state);
         // cross attention (:5106-5340) over the precomputed f16 cross K/V, no mask
@@ -158,6 +160,7 @@ bool build_decode(oa_whisper_session * s, wh_graph & g) {
         ggml_tensor * ck = ggml_view_3d(ctx, s->k_cross[(size_t) l], hd, c.n_frames, H, row_stride, head_stride, 0);
         ggml_tensor * cv = ggml_view_3d(ctx, s->v_cross[(size_t) l], hd, c.n_frames, H, row_stride, head_stride, 0);
         ggml_tensor * ctx_cross = ggml_flash_attn_ext(ctx, heads_view(ctx, q, hd, H, 1), ck, cv, nullptr, scale, 0.0f, 0.0f);
+        ggml_flash_attn_ext_set_prec(ctx_cross, (ggml_prec) s->fa_prec);
         ctx_cross = ggml_reshape_2d(ctx, ctx_cross, d, 1);
         state = ggml_add(ctx, linear(ctx, L[OA_WH_CROSS_O], ctx_cross, L[OA_WH_CROSS_O_B]), state);
         // MLP (:5342-5392)
@@ -404,6 +407,15 @@ void oa_whisper_session_free(oa_whisper_session * s) {
 }
 
 int oa_whisper_session_position(const oa_whisper_session * s) { return s->n_past; }
+
+int oa_whisper_session_set_flash_attention_precision(oa_whisper_session * s, int precision) {
+    if (precision != GGML_PREC_DEFAULT && precision != GGML_PREC_F32) return GGML_STATUS_FAILED;
+    if (precision != s->fa_prec) {
+        s->fa_prec = precision;
+        s->decode.release();  // rebuilt under the new contract on the next step
+    }
+    return GGML_STATUS_SUCCESS;
+}
 
 int oa_whisper_set_encoder(oa_whisper_session * s, const float * enc) {
     const oa_whisper_model * m = s->m;

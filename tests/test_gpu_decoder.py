@@ -208,6 +208,33 @@ def seed_from_device(r, sess, seq, n_pos, n_layers):
     r.pos = n_pos
 
 
+def check_teacher_forced(what, exact_step, cpu_step, fed, dev):
+    """dev: the device's (top-1, logits) of consecutive steps, step i fed
+    token fed[i]. The exact oracle (fidelity 5) and ggml-cpu's attention
+    numerics (fidelity 1) are fed the same tokens. The device's logits must
+    stay as close to the exact form's as ggml-cpu's own numerics do (twice
+    that distance, or 1e-2), and the top-1 must agree wherever the exact
+    top-1 margin exceeds twice the step's logit distance"""
+    max_dl = max_d1 = 0.0
+    checked = 0
+    per_step = []
+    for i, ((tok, lg), t) in enumerate(zip(dev, fed)):
+        t5, lg5 = exact_step(int(t))
+        _, lg1 = cpu_step(int(t))
+        dl = float(np.abs(lg - lg5).max())
+        d1 = float(np.abs(lg1 - lg5).max())
+        per_step.append(dl)
+        max_dl, max_d1 = max(max_dl, dl), max(max_d1, d1)
+        top2 = np.sort(lg5)[-2:]
+        if top2[1] - top2[0] > 2 * dl:
+            checked += 1
+            assert t5 == tok, f"{what} step {i}: cpu {t5} != gpu {tok}"
+    print(f"  {what}: {len(dev)} default-precision steps, max |dlogit| {max_dl:.2e} (first steps "
+          f"{', '.join(f'{x:.1e}' for x in per_step[:4])}), ggml-cpu numerics {max_d1:.2e}, top-1 checked at "
+          f"{checked} of {len(dev)} steps", flush=True)
+    assert max_dl <= max(2 * max_d1, 1e-2)
+
+
 @pytest.mark.parametrize("wname,n_seq", [("q8_0", 1), ("q4_K", 8)])
 def test_qwen3_06b_default_precision_prefill(gpu, ref, wname, n_seq):
     """the ASR decoder's own contract (GGML_PREC_DEFAULT, what
@@ -217,9 +244,13 @@ def test_qwen3_06b_default_precision_prefill(gpu, ref, wname, n_seq):
     oracle, fidelity 5) as ggml-cpu's own f16-accumulator attention keeps
     them (fidelity 1): within twice that distance, or 5e-2 of the largest
     entry; the first token agrees wherever the oracle's top-1 margin exceeds
-    twice the ggml-cpu numerics' logit distance. Then the oracle continues
-    from the device's caches: 64 greedy decode steps token for token, logits
-    < 1e-2 (one query a step: exact under either contract)."""
+    twice the ggml-cpu numerics' logit distance. Then 64 greedy decode steps
+    at the default precision (the single-query workgroup form), the oracle
+    (exact chunked attention) continuing from the device's caches and fed the
+    device's tokens: the device's logits stay as close to the exact form's as
+    ggml-cpu's own attention numerics (fidelity 1, fed the same tokens) do --
+    within twice that distance, or 1e-2 -- and the top-1 agrees wherever the
+    oracle's top-1 margin exceeds twice the step's logit distance."""
     wt = g.Q8_0 if wname == "q8_0" else g.Q4_K
     print(f"qwen3-0.6b {wname} b{n_seq}, default-precision prefill", flush=True)
     shape, max_pos, n_pos = D.QWEN3_06B, 1024, 383
@@ -259,24 +290,76 @@ def test_qwen3_06b_default_precision_prefill(gpu, ref, wname, n_seq):
         assert kv_err <= max(2 * kv_spread, 5e-2)
         if margin > 2 * spread:
             assert first[s] == t5
-    # decode from the device's caches: exact
+    # decode at the default precision from the device's caches, the oracle
+    # fed the device's tokens
     cur = first
     dev_toks, dev_logits = [], []
     for _ in range(64):
         cur, lg = sess.step(cur, want_logits=True)
         dev_toks.append(cur.copy())
         dev_logits.append(lg)
-    max_dl = 0.0
     for s in seqs:
+        exact = ref.QwenRef(w.cfg, table, max_pos, fa_fidelity=5)
+        cpu = ref.QwenRef(w.cfg, table, max_pos, fa_fidelity=1)
+        seed_from_device(exact, sess, s, n_pos, shape["n_layers"])
+        seed_from_device(cpu, sess, s, n_pos, shape["n_layers"])
+        fed = [int(first[s])] + [int(dev_toks[i][s]) for i in range(63)]
+        check_teacher_forced(f"seq {s}", exact.step, cpu.step, fed,
+                             [(int(dev_toks[i][s]), dev_logits[i][s]) for i in range(64)])
+    sess.free()
+    model.free()
+    w.free()
+
+
+@pytest.mark.parametrize("n_seq,max_pos,prefix", [(8, 4096, 1100), (2, 512, 300)])
+def test_default_precision_step_workgroup_form(gpu, ref, n_seq, max_pos, prefix):
+    """the fused decode step at the default precision in the single-query
+    workgroup form (128-wide heads, two query heads a kv head): at batch 8
+    over a 4096-position arena (four KV splits merged by the combine launch,
+    the step's row in the second split) and at batch 2 over 512 positions
+    (one split, finished and quantized for the output projection in the
+    launch). The oracle, seeded with the device's caches after prefill and
+    fed the device's tokens, is matched as closely as ggml-cpu's own
+    attention numerics match it (check_teacher_forced's bars), and every
+    step's layer-0 K / V rows (a function of the token alone) land in the
+    caches bit for bit"""
+    shape = dict(d_model=256, n_layers=2, n_head=16, n_kv_head=8, head_dim=128, ffn=512, vocab=1000)
+    prompt, steps = 4, 24
+    print(f"default-precision step, workgroup form: {n_seq} x {max_pos} positions", flush=True)
+    w = D.QwenWeights(g.Q8_0, seed=17, **shape)
+    model = D.QwenModel(w, gpu.backend)
+    sess = model.session(n_seq, max_pos)
+    wl = D.QwenWorkload("t", shape, g.Q8_0, n_seq, prefix, prompt, steps, max_pos)
+    emb, toks = D.workload_inputs(wl, seed=18)
+    sess.prefill_embeddings(emb)
+    first = sess.prefill_tokens(toks)
+    n_pos = prefix + prompt
+    table = w.pointer_table()
+    refs = []
+    for s in range(n_seq):
         r = ref.QwenRef(w.cfg, table, max_pos, fa_fidelity=5)
         seed_from_device(r, sess, s, n_pos, shape["n_layers"])
-        t = int(first[s])
-        for i in range(64):
-            t, lg = r.step(t)
-            max_dl = max(max_dl, float(np.abs(dev_logits[i][s] - lg).max()))
-            assert t == dev_toks[i][s], f"seq {s} step {i}: cpu {t} != gpu {dev_toks[i][s]}"
-    print(f"  64 decode steps from the device caches token-exact, max |dlogit| {max_dl:.2e}", flush=True)
-    assert max_dl < 1e-2
+        refs.append(r)
+    cpus = []
+    for s in range(n_seq):
+        r = ref.QwenRef(w.cfg, table, max_pos, fa_fidelity=1)
+        seed_from_device(r, sess, s, n_pos, shape["n_layers"])
+        cpus.append(r)
+    cur = first
+    dev = []
+    for i in range(steps):
+        cur, lg = sess.step(cur, want_logits=True)
+        dev.append((cur.copy(), lg))
+    for s in range(n_seq):
+        fed = [int(first[s])] + [int(t[s]) for t, _ in dev[:-1]]
+        check_teacher_forced(f"seq {s}", refs[s].step, cpus[s].step, fed, [(int(t[s]), lg[s]) for t, lg in dev])
+    for s in range(n_seq):
+        k, v = sess.read_kv(0, s)
+        rows = slice(n_pos, n_pos + steps)
+        assert np.array_equal(k[:, rows], refs[s].k[0][:, rows]), f"seq {s}: layer-0 K rows of the steps"
+        assert np.array_equal(v[:, rows], refs[s].v[0][:, rows]), f"seq {s}: layer-0 V rows of the steps"
+    labels = [lab.split(":", 1)[0] for lab, _ in gpu.profile(sess.decode_graph(), 1)]
+    assert "attn_step_dec" in labels, labels
     sess.free()
     model.free()
     w.free()
@@ -307,6 +390,7 @@ def test_whisper_tiny_q8_0_first_64_steps(gpu, ref):
     w = D.WhisperWeights(seed=4321, **shape)
     model = D.WhisperModel(w, gpu.backend)
     sess = model.session()
+    sess.set_flash_attention_precision(g.GGML_PREC_F32)  # the exact chunked attention
     enc, prompt = D.whisper_inputs(shape, n_prompt=4, seed=91)
     sess.set_encoder(enc)
     r = ref.WhisperRef(w.cfg, w.pointer_table(), fa_fidelity=5)
@@ -331,6 +415,34 @@ def test_whisper_tiny_q8_0_first_64_steps(gpu, ref):
     w.free()
 
 
+def test_whisper_tiny_default_precision_decode(gpu, ref):
+    """the decoder's own contract (GGML_PREC_DEFAULT on the self and cross
+    attention: the single-query workgroup form): 4 prompt tokens and 64
+    greedy steps; the exact oracle and ggml-cpu's attention numerics fed the
+    device's tokens (check_teacher_forced's bars)"""
+    print("whisper-tiny q8_0 b1, default precision", flush=True)
+    shape = D.WHISPER_TINY
+    w = D.WhisperWeights(seed=4321, **shape)
+    model = D.WhisperModel(w, gpu.backend)
+    sess = model.session()
+    enc, prompt = D.whisper_inputs(shape, n_prompt=4, seed=91)
+    sess.set_encoder(enc)
+    exact = ref.WhisperRef(w.cfg, w.pointer_table(), fa_fidelity=5)
+    cpu = ref.WhisperRef(w.cfg, w.pointer_table(), fa_fidelity=1)
+    exact.set_encoder(enc)
+    cpu.set_encoder(enc)
+    fed, dev = [], []
+    tok = None
+    for t in list(prompt) + [None] * 64:  # the prompt forced, then greedy
+        fed.append(int(t) if t is not None else tok)
+        tok, lg = sess.step(fed[-1], want_logits=True)
+        dev.append((tok, lg))
+    check_teacher_forced("whisper", exact.step, cpu.step, fed, dev)
+    sess.free()
+    model.free()
+    w.free()
+
+
 @pytest.mark.parametrize("ffn_act", [D.FFN_RELU, D.FFN_GELU_ERF, D.FFN_SILU])
 def test_seq2seq_block_ffn_activations(gpu, ref, ffn_act):
     """the shared seq2seq block with the other FFN activations of
@@ -343,6 +455,7 @@ def test_seq2seq_block_ffn_activations(gpu, ref, ffn_act):
     w = D.WhisperWeights(seed=77 + ffn_act, ffn_act=ffn_act, **shape)
     model = D.WhisperModel(w, gpu.backend)
     sess = model.session()
+    sess.set_flash_attention_precision(g.GGML_PREC_F32)  # the exact chunked attention
     enc, prompt = D.whisper_inputs(shape, n_prompt=4, seed=92)
     sess.set_encoder(enc)
     r = ref.WhisperRef(w.cfg, w.pointer_table(), fa_fidelity=5)

@@ -75,6 +75,7 @@ def test_flash_attn_fixture(ggml, gpu, fx):
     V = G.new(ggml.F16, d, n_kv, hkv, n_seq)
     M = G.new(ggml.F16, n_kv, 1, 1, n_seq)
     O = G.lib.ggml_flash_attn_ext(G.ctx, Q, K, V, M, 0.125, 0.0, 0.0)
+    G.lib.ggml_flash_attn_ext_set_prec(O, ggml.GGML_PREC_F32)  # the exact chunked definition
     G.build(O)
     G.allocate(gpu.buft)
     G.set(Q, q)
