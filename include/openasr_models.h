@@ -146,6 +146,15 @@ int oa_qwen_session_set_hip_lane(oa_qwen_session * s, int enable, int prefill_ch
  * effect on the next step. */
 int oa_qwen_session_set_flash_attention_precision(oa_qwen_session * s, int precision);
 
+/* The precision of the quantized projections' MUL_MATs (the graph's
+ * mul_mat_with_precision, ggml_runtime/cpu_graph.rs:3622-3631; the decoder
+ * builds them at GgmlMatmulPrecision::Default): GGML_PREC_DEFAULT (the
+ * default) lets wide prefill products run on the f16 matrix cores within
+ * float tolerance; GGML_PREC_F32 keeps every product in the exact integer
+ * form. Decode-size products are exact under both. Other values return
+ * GGML_STATUS_FAILED. Takes effect on the next step. */
+int oa_qwen_session_set_matmul_precision(oa_qwen_session * s, int precision);
+
 /* Prefill T positions of every sequence (chunked internally at 256) from
  * hidden inputs [n_seq][T][d_model] (an audio-embedding prefix) or token ids
  * [n_seq][T]. top1_out (optional, [n_seq]) gets the first-max argmax of the

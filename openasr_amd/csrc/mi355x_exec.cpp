@@ -821,6 +821,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 if (is_view_op(u->op) || deferred.count(u)) continue;
                 const ggml_tensor * uw = u->src[0];
                 const bool sibling = u->op == GGML_OP_MUL_MAT && u->src[1] == x && uw->type == wtype &&
+                                     u->op_params[0] == t->op_params[0] &&
                                      uw->ne[0] == K && uw->ne[2] == 1 && uw->ne[3] == 1 &&
                                      (int64_t) uw->nb[1] == row_bytes && uw->ne[1] % 64 == 0 &&
                                      u->type == GGML_TYPE_F32 && is_contiguous(u) && u->ne[1] == N && u->ne[2] == 1 &&
@@ -863,6 +864,13 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 msub_outs.push_back(out);
             }
         }
+        // the default precision (the graph's contract, op_params[0]) with
+        // enough tiles and 16-byte weight rows: the f16 matrix-core form
+        // (k_mmq_f16.hip, float tolerance)
+        bool mmq16 = wide && t->op_params[0] != GGML_PREC_F32 && mmq_f16_supported(wtype, M, K, N, n_cu) &&
+                     row_bytes % 16 == 0 && aligned16(W);
+        for (const gemm_float_sub & sb : msubs) mmq16 = mmq16 && aligned16(sb.a);
+        if (mmq16) gen_need = std::max(gen_need, mmq_f16_scratch_bytes(K, N));
         // a following residual ADD of the same shape folds into the epilogue
         const char * res = nullptr;
         int64_t res_nb1 = 0;
@@ -915,6 +923,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 if (is_view_op(u->op) || deferred.count(u)) continue;
                 const ggml_tensor * uw = u->src[0];
                 const bool sibling = u->op == GGML_OP_MUL_MAT && u->src[1] == x && uw->type == wtype &&
+                                     u->op_params[0] == t->op_params[0] &&
                                      uw->ne[0] == K && uw->ne[2] == 1 && uw->ne[3] == 1 &&
                                      (int64_t) uw->nb[1] == row_bytes && u->type == GGML_TYPE_F32 && is_contiguous(u) &&
                                      u->ne[1] * u->ne[2] * u->ne[3] == 1 && ready_before(uw, i);
@@ -972,7 +981,10 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         add_step(
             [=](hipStream_t s) {
                 act_buffers act = act_carve(wtype, act_base(b), K, N);
-                if (wide)
+                if (mmq16)
+                    launch_mmq_f16(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, gen_base(b), s, mepi,
+                                   msubs.empty() ? nullptr : msubs.data(), (int) msubs.size());
+                else if (wide)
                     launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, mepi,
                                msubs.empty() ? nullptr : msubs.data(), (int) msubs.size());
                 else if (mfma)
@@ -980,8 +992,9 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                                      has_pro ? &pro : nullptr, epi, subs.data(), (int) subs.size());
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
-            produced, W2 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")
-                             : (wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K"),
+            produced, W2     ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")
+                      : mmq16 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_f16_q8_0" : "mul_mat_f16_q4_K")
+                              : (wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K"),
             outs);
         return true;
     }

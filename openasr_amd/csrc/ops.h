@@ -85,6 +85,17 @@ void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t
                 int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu, const gemm_float_epi & epi,
                 const gemm_float_sub * subs = nullptr, int nsub = 0);
 
+// the same product at the default precision on the f16 matrix cores
+// (k_mmq_f16.hip, float tolerance): where it takes the product (enough
+// 128 x 128 tiles), the general scratch it needs (the activations
+// dequantized to f16), and the launch (subs joined when every product's rows
+// are a multiple of 128)
+bool mmq_f16_supported(int wtype, int64_t M, int64_t K, int64_t N, int n_cu);
+size_t mmq_f16_scratch_bytes(int64_t K, int64_t N);
+void launch_mmq_f16(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
+                    int64_t N, char * dst, int64_t dst_nb1, void * scratch, hipStream_t stream,
+                    const gemm_float_epi & epi, const gemm_float_sub * subs = nullptr, int nsub = 0);
+
 // float GEMM fallback (f16 / f32 src0)
 void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tview & b, hipStream_t s);
 

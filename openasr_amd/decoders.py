@@ -111,6 +111,7 @@ def lib() -> C.CDLL:
     s("oa_qwen_session_position", i, vp, i)
     s("oa_qwen_session_set_reversed_top1", None, vp, i)
     s("oa_qwen_session_set_flash_attention_precision", i, vp, i)
+    s("oa_qwen_session_set_matmul_precision", i, vp, i)
     s("oa_qwen_session_set_hip_lane", i, vp, i, i)
     s("oa_qwen_prefill_embeddings", i, vp, vp, i, vp)
     s("oa_qwen_prefill_tokens", i, vp, vp, i, vp)
@@ -295,10 +296,18 @@ class QwenSession:
     def set_flash_attention_precision(self, precision: int):
         """the self-attention's contract (set_flash_attention_precision,
         llm_transformer.rs:3044-3053): GGML_PREC_DEFAULT runs prefill chunks
-        on the matrix cores within float tolerance, GGML_PREC_F32 keeps the
-        exact chunked form; decode steps are exact under both"""
+        on the matrix cores and, where it is planned, the decode step in the
+        single-query workgroup form, within float tolerance; GGML_PREC_F32
+        keeps the exact chunked form"""
         self._check(lib().oa_qwen_session_set_flash_attention_precision(self.ptr, int(precision)),
                     "set_flash_attention_precision")
+
+    def set_matmul_precision(self, precision: int):
+        """the quantized projections' MUL_MAT precision (the graph's
+        mul_mat_with_precision, cpu_graph.rs:3622-3631): GGML_PREC_DEFAULT
+        runs wide prefill products on the f16 matrix cores within float
+        tolerance, GGML_PREC_F32 keeps every product exact"""
+        self._check(lib().oa_qwen_session_set_matmul_precision(self.ptr, int(precision)), "set_matmul_precision")
 
     def set_reversed_top1(self, enable: bool = True):
         """greedy top-1 through the reversed-row GET_ROWS + ARGMAX graph"""

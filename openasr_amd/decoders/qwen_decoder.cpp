@@ -142,6 +142,9 @@ struct oa_qwen_session {
     // the self-attention's flash-attention precision contract
     // (set_flash_attention_precision, llm_transformer.rs:3044-3053)
     int fa_prec = GGML_PREC_DEFAULT;
+    // the quantized projections' MUL_MAT precision (mul_mat_with_precision,
+    // cpu_graph.rs:3622-3631): the graph builds them at the default
+    int mm_prec = GGML_PREC_DEFAULT;
 };
 
 namespace {
@@ -170,15 +173,23 @@ ggml_tensor * rms_norm_mul(ggml_context * ctx, ggml_tensor * x, ggml_tensor * w,
     return ggml_mul(ctx, ggml_rms_norm(ctx, x, eps), w);  // nn/norm.rs:39-56
 }
 
+// a quantized projection at the session's MUL_MAT precision
+ggml_tensor * proj(ggml_context * ctx, ggml_tensor * w, ggml_tensor * x, int mm_prec) {
+    ggml_tensor * y = ggml_mul_mat(ctx, w, x);
+    if (mm_prec == GGML_PREC_F32) ggml_mul_mat_set_prec(y, GGML_PREC_F32);
+    return y;
+}
+
 // llm_layer for token_count tokens of n_seq sequences (nn/decoder.rs:1850-2145)
 ggml_tensor * llm_layer(ggml_context * ctx, const oa_qwen_config & c, const qlayer_dev & L, ggml_tensor * hidden,
                         ggml_tensor * k_hist, ggml_tensor * v_hist, ggml_tensor * rows, ggml_tensor * pos,
-                        ggml_tensor * mask, int T, int n_seq, int max_pos, bool hip_lane, int fa_prec) {
+                        ggml_tensor * mask, int T, int n_seq, int max_pos, bool hip_lane, int fa_prec,
+                        int mm_prec) {
     const int hd = c.head_dim, q_w = c.n_head * hd, kv_w = c.n_kv_head * hd;
     const int tokens = T * n_seq;
     ggml_tensor * normed = rms_norm_mul(ctx, hidden, L.attn_norm, c.rms_eps);
     // fused [q|k|v] projection then f32 column views (nn/decoder.rs:1722-1789)
-    ggml_tensor * qkv = ggml_mul_mat(ctx, L.qkv, normed);
+    ggml_tensor * qkv = proj(ctx, L.qkv, normed, mm_prec);
     const size_t col = (size_t) (q_w + 2 * kv_w) * sizeof(float);
     ggml_tensor * q = ggml_view_2d(ctx, qkv, q_w, tokens, col, 0);
     ggml_tensor * k = ggml_view_2d(ctx, qkv, kv_w, tokens, col, (size_t) q_w * sizeof(float));
@@ -244,12 +255,12 @@ ggml_tensor * llm_layer(ggml_context * ctx, const oa_qwen_config & c, const qlay
         ggml_flash_attn_ext_set_prec(att, (ggml_prec) fa_prec);
     }
     att = ggml_reshape_2d(ctx, att, q_w, tokens);
-    ggml_tensor * post_attn = ggml_add(ctx, hidden, ggml_mul_mat(ctx, L.o, att));
+    ggml_tensor * post_attn = ggml_add(ctx, hidden, proj(ctx, L.o, att, mm_prec));
     // SwiGLU FFN with residual (nn/ffn.rs:64-91)
     ggml_tensor * ffn_in = rms_norm_mul(ctx, post_attn, L.ffn_norm, c.rms_eps);
-    ggml_tensor * gate = ggml_silu(ctx, ggml_mul_mat(ctx, L.gate, ffn_in));
-    ggml_tensor * up = ggml_mul_mat(ctx, L.up, ffn_in);
-    ggml_tensor * down = ggml_mul_mat(ctx, L.down, ggml_mul(ctx, gate, up));
+    ggml_tensor * gate = ggml_silu(ctx, proj(ctx, L.gate, ffn_in, mm_prec));
+    ggml_tensor * up = proj(ctx, L.up, ffn_in, mm_prec);
+    ggml_tensor * down = proj(ctx, L.down, ggml_mul(ctx, gate, up), mm_prec);
     return ggml_add(ctx, down, post_attn);
 }
 
@@ -285,7 +296,7 @@ bool build_step(oa_qwen_session * s, step_graph & g, int T, bool emb) {
     ggml_set_input(g.mask);
     for (int l = 0; l < c.n_layers; l++) {
         state = llm_layer(g.ctx, c, m->layers[(size_t) l], state, s->k_cache[(size_t) l], s->v_cache[(size_t) l],
-                          g.rows, g.pos, g.mask, T, n_seq, s->max_pos, s->hip_lane, s->fa_prec);
+                          g.rows, g.pos, g.mask, T, n_seq, s->max_pos, s->hip_lane, s->fa_prec, s->mm_prec);
     }
     ggml_tensor * last = state;
     if (T > 1) {  // the last position of each sequence
@@ -293,7 +304,7 @@ bool build_step(oa_qwen_session * s, step_graph & g, int T, bool emb) {
                                              (size_t) (T - 1) * c.d_model * sizeof(float)));
     }
     ggml_tensor * normed = rms_norm_mul(g.ctx, last, m->out_norm, c.rms_eps);
-    g.logits = ggml_mul_mat(g.ctx, m->lm_head, normed);
+    g.logits = proj(g.ctx, m->lm_head, normed, s->mm_prec);
     g.top1 = s->reversed_top1 ? top1_reversed(g.ctx, g.logits, s->rev_idx) : ggml_argmax_first(g.ctx, g.logits);
     ggml_set_output(g.logits);
     ggml_set_output(g.top1);
@@ -527,6 +538,13 @@ int oa_qwen_session_set_hip_lane(oa_qwen_session * s, int enable, int prefill_ch
 int oa_qwen_session_set_flash_attention_precision(oa_qwen_session * s, int precision) {
     if (precision != GGML_PREC_DEFAULT && precision != GGML_PREC_F32) return GGML_STATUS_FAILED;
     s->fa_prec = precision;
+    s->decode.release();  // no graph built under the other contract survives
+    return GGML_STATUS_SUCCESS;
+}
+
+int oa_qwen_session_set_matmul_precision(oa_qwen_session * s, int precision) {
+    if (precision != GGML_PREC_DEFAULT && precision != GGML_PREC_F32) return GGML_STATUS_FAILED;
+    s->mm_prec = precision;
     s->decode.release();  // no graph built under the other contract survives
     return GGML_STATUS_SUCCESS;
 }

@@ -31,12 +31,13 @@ def run_pair(gpu, ref, shape, wtype, n_seq, prefix, prompt, steps, max_pos, seed
     """hip_lane: a prefill chunk width to run the graphs the unmodified host
     builds on its HIP lane (REPEAT-expanded K/V, the unfused attention chain
     for wide prefill chunks), the oracle prefilling in the same chunks.
-    Prefill attention under GGML_PREC_F32 (the exact chunked form): every
-    step is compared bit for bit"""
+    Prefill attention and projections under GGML_PREC_F32 (the exact forms):
+    every step is compared bit for bit"""
     w = weights or D.QwenWeights(wtype, seed=seed, **shape)
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(n_seq, max_pos)
     sess.set_flash_attention_precision(g.GGML_PREC_F32)
+    sess.set_matmul_precision(g.GGML_PREC_F32)
     if reversed_top1:
         sess.set_reversed_top1(True)
     if hip_lane:
@@ -531,6 +532,7 @@ def test_qwen3_17b_q4_K_batch8_long_context(gpu, ref):
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(wl.n_seq, wl.max_positions)
     sess.set_flash_attention_precision(g.GGML_PREC_F32)
+    sess.set_matmul_precision(g.GGML_PREC_F32)
     emb, prompt = D.workload_inputs(wl, seed=77)
     sess.prefill_embeddings(emb)
     cur = sess.prefill_tokens(prompt)
@@ -583,6 +585,7 @@ def test_qwen3_17b_q4_K_prefill_all_layers(gpu, ref):
     model = D.QwenModel(w, gpu.backend)
     sess = model.session(wl.n_seq, wl.max_positions)
     sess.set_flash_attention_precision(g.GGML_PREC_F32)
+    sess.set_matmul_precision(g.GGML_PREC_F32)
     short = D.QwenWorkload("short", wl.shape, wl.wtype, wl.n_seq, prefix, prompt_len, 0, wl.max_positions)
     emb, prompt = D.workload_inputs(short, seed=78)
     sess.prefill_embeddings(emb)

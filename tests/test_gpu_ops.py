@@ -168,7 +168,9 @@ SWEEP_CASES = [
 @pytest.mark.parametrize("wname,m,k,n", SWEEP_CASES)
 def test_mul_mat_sweep_points(ggml, gpu, ref, wname, m, k, n):
     """the mul_mat sweep's shapes at the column counts the other tests leave
-    out, bit-exact against the oracle, same argmax per column"""
+    out, under GGML_PREC_F32 (the exact forms; wide products at the default
+    precision run on the f16 matrix cores, tested below): bit-exact against
+    the oracle, same argmax per column"""
     wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
     print(f"sweep mul_mat {wname} M={m} K={k} N={n}", flush=True)
     wq = ggml.quantize(wt, ggml.synth_normal(7, m + 3 * k, m * k, 0.0, 0.02).reshape(m, k))
@@ -177,6 +179,7 @@ def test_mul_mat_sweep_points(ggml, gpu, ref, wname, m, k, n):
     W = G.new(wt, k, m, weight=True)
     X = G.new(ggml.F32, k, n)
     Y = G.lib.ggml_mul_mat(G.ctx, W, X)
+    G.lib.ggml_mul_mat_set_prec(Y, ggml.GGML_PREC_F32)
     run(ggml, gpu, G, Y)
     G.set(W, wq)
     G.set(X, x)
@@ -185,6 +188,79 @@ def test_mul_mat_sweep_points(ggml, gpu, ref, wname, m, k, n):
     want = ref.mul_mat(wt, wq, m, k, x)
     assert_same_bits(y, want)
     assert np.array_equal(y.argmax(1), want.argmax(1))
+    G.free()
+
+
+# the f16 matrix-core tile GEMM (quantized weights, wide columns, the
+# default precision): weights, M, K, N, epilogue. The vocabulary projection
+# at 512 columns and at 300 (a partial column tile) in both formats; the
+# Qwen3-0.6B QKV and the Qwen3-1.7B down projection (with its residual) of a
+# batch-8 prefill chunk; a Q8_0 projection with bias and GELU_ERF; rows off
+# the 128-row tile with 96 columns and a bias.
+MMQ16_CASES = [
+    ("q4_K", 151936, 1024, 512, None), ("q8_0", 151936, 1024, 512, None), ("q4_K", 151936, 1024, 300, None),
+    ("q4_K", 4096, 1024, 2048, None), ("q4_K", 2048, 6144, 2048, "res"), ("q8_0", 3072, 1024, 2048, "bias_gelu"),
+    ("q4_K", 32784, 2048, 96, "bias"),
+]
+
+
+@pytest.mark.parametrize("wname,m,k,n,tail", MMQ16_CASES)
+def test_mul_mat_f16_matrix_cores(ggml, gpu, ref, wname, m, k, n, tail):
+    """a quantized MUL_MAT over wide columns at the default precision runs on
+    the f16 matrix cores (activations quantized as for the exact path, then
+    both operands dequantized to f16, f32 sums): within 2e-3 of the oracle's
+    exact product (with the epilogue's adds and GELU_ERF), same argmax in
+    every column where the oracle's top-2 margin exceeds the error; graph
+    replays give the same bits"""
+    wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
+    print(f"f16 tile gemm {wname} M={m} K={k} N={n} tail={tail}", flush=True)
+    wq = ggml.quantize(wt, ggml.synth_normal(8, m + k, m * k, 0.0, 0.02).reshape(m, k))
+    rng = np.random.default_rng(m + n)
+    x = rng.standard_normal((n, k)).astype(np.float32)
+    b = rng.standard_normal(m).astype(np.float32)
+    r = rng.standard_normal((n, m)).astype(np.float32)
+    G = ggml.Graph()
+    L = G.lib
+    W = G.new(wt, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    B = G.new(ggml.F32, m, weight=True)
+    R = G.new(ggml.F32, m, n)
+    Y = L.ggml_mul_mat(G.ctx, W, X)
+    want = ref.mul_mat(wt, wq, m, k, x)
+    if tail and "bias" in tail:
+        Y = L.ggml_add(G.ctx, Y, B)
+        want = want + b
+    if tail and "res" in tail:
+        Y = L.ggml_add(G.ctx, R, Y)
+        want = want + r
+    if tail and "gelu" in tail:
+        from scipy.special import erf  # the exact GELU_ERF: the 2e-3 bar dwarfs its rounding
+        Y = L.ggml_gelu_erf(G.ctx, Y)
+        w64 = want.astype(np.float64)
+        want = 0.5 * w64 * (1.0 + erf(w64 / math.sqrt(2.0)))
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    G.set(X, x)
+    if tail and "bias" in tail:
+        G.set(B, b)
+    if tail and "res" in tail:
+        G.set(R, r)
+    assert G.compute(gpu.backend) == 0
+    labels = plan_labels(gpu, G)
+    assert f"mul_mat_f16_{wname}" in labels, labels
+    y = G.get(Y).reshape(n, m)
+    err = rel_err(y, want)
+    print(f"  vs the exact product: {err:.2e}", flush=True)
+    assert err < 2e-3
+    assert np.isfinite(y).all()
+    if tail is None:
+        top2 = np.sort(want, axis=1)[:, -2:]
+        clear = top2[:, 1] - top2[:, 0] > 2 * err * np.abs(want).max()
+        assert np.array_equal(y.argmax(1)[clear], want.argmax(1)[clear])
+    first = y.copy()
+    for _ in range(2):  # captured, then replayed
+        assert G.compute(gpu.backend) == 0
+        assert np.array_equal(G.get(Y).reshape(n, m).view(np.uint32), first.view(np.uint32))
     G.free()
 
 
