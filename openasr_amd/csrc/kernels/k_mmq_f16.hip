@@ -120,7 +120,7 @@ __device__ __forceinline__ uint4 hq_int8(uint32_t w0, uint32_t w1, hh2 s) {
 // its store: weights of row r = t / 2, half h = t % 2 (Q4_K: the 16 bytes
 // holding sub-blocks 2c and 2c + 1 at elements 16 h .. 16 h + 15, plus the
 // super-block header; Q8_0: the 32 quants of block 2 s + h and its scale);
-// activations of column t / 2, elements 32 h .. 32 h + 31 of the step. Only
+// activations: 16-byte piece t % 8 of columns t / 8 + 32 i (i = 0 .. 3). Only
 // 16-byte members: a narrower one leaves padding that keeps the struct in
 // scratch memory.
 struct hq_regs {
@@ -143,12 +143,15 @@ __device__ __forceinline__ void hq_load(const mmqh_args & a, const char * wrow, 
         r.w1 = *(const uint4 *) (wrow + bk * 32 + 16);
         r.hdr = make_uint4(((const uint16_t *) (wrow + a.K))[bk], 0, 0, 0);
     }
-    const int col = min(n0 + (t >> 1), a.N - 1);
-    const uint4 * xp = (const uint4 *) (a.x16 + (int64_t) col * a.K + k0 + 32 * h);
-    r.x0 = xp[0];
-    r.x1 = xp[1];
-    r.x2 = xp[2];
-    r.x3 = xp[3];
+    // activations: piece q = t + 256 i (i = 0 .. 3) is 16-byte piece q % 8 of
+    // column q / 8, so eight consecutive lanes read one column's whole 128
+    // bytes of the step
+    const uint16_t * xs = a.x16 + k0 + 8 * (t & 7);
+    auto xcol = [&](int i) { return (int64_t) min(n0 + (t >> 3) + 32 * i, a.N - 1) * a.K; };
+    r.x0 = *(const uint4 *) (xs + xcol(0));
+    r.x1 = *(const uint4 *) (xs + xcol(1));
+    r.x2 = *(const uint4 *) (xs + xcol(2));
+    r.x3 = *(const uint4 *) (xs + xcol(3));
 }
 
 template <int WT>
@@ -197,10 +200,11 @@ __device__ __forceinline__ void hq_store(const hq_regs & r, int64_t k0, uint16_t
         *hq_slot(sw, row, 4 * h + 2) = hq_int8(r.w1.x, r.w1.y, s);
         *hq_slot(sw, row, 4 * h + 3) = hq_int8(r.w1.z, r.w1.w, s);
     }
-    *hq_slot(sx, row, 4 * h) = r.x0;
-    *hq_slot(sx, row, 4 * h + 1) = r.x1;
-    *hq_slot(sx, row, 4 * h + 2) = r.x2;
-    *hq_slot(sx, row, 4 * h + 3) = r.x3;
+    const int xc = t >> 3, xp = t & 7;
+    *hq_slot(sx, xc, xp) = r.x0;
+    *hq_slot(sx, xc + 32, xp) = r.x1;
+    *hq_slot(sx, xc + 64, xp) = r.x2;
+    *hq_slot(sx, xc + 96, xp) = r.x3;
 }
 
 template <int WT>
