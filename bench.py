@@ -480,7 +480,7 @@ def _timed_graph(G, backend, reps: int) -> float:
     return (time.perf_counter() - t0) / reps
 
 
-def sweep_mul_mat(plugin, g, M, K, wtype, N, reps):
+def sweep_mul_mat(plugin, g, M, K, wtype, N, reps, prec=0):
     bpw = 144 / 256 if wtype == g.Q4_K else 34 / 32
     wbytes = M * K * bpw
     copies = max(1, min(2048, int(ROTATE_BYTES // wbytes)))
@@ -492,6 +492,8 @@ def sweep_mul_mat(plugin, g, M, K, wtype, N, reps):
     X = G.new(g.F32, K, N)
     Ws = [G.new(wtype, K, M, weight=True) for _ in range(copies)]
     outs = [G.lib.ggml_mul_mat(G.ctx, W, X) for W in Ws]
+    for o in outs:
+        G.lib.ggml_mul_mat_set_prec(o, prec)
     G.build(*outs)
     G.allocate(plugin.buft)
     for W in Ws:
@@ -500,7 +502,8 @@ def sweep_mul_mat(plugin, g, M, K, wtype, N, reps):
     dt = _timed_graph(G, plugin.backend, reps) / copies
     G.free()
     alg = wbytes + (K * N if N <= 16 else 4 * K * N) + 4 * M * N
-    return dict(op="mul_mat", type=g.TYPE_NAMES[wtype], M=M, K=K, N=N, copies=copies, us=dt * 1e6,
+    return dict(op="mul_mat", type=g.TYPE_NAMES[wtype], prec="f32" if prec == g.GGML_PREC_F32 else "default",
+                M=M, K=K, N=N, copies=copies, us=dt * 1e6,
                 gbs=alg / dt / 1e9, frac_hbm=alg / dt / 1e9 / HBM_PEAK_GBS,
                 tops=2.0 * M * K * N / dt / 1e12)
 
@@ -541,7 +544,8 @@ def sweep_fattn(plugin, g, n_kv, n_q, reps, d=128, hq=16, hkv=8, prec=0):
 
 def run_sweep(reps: int) -> int:
     """mul_mat on Q8_0/Q4_K weights M x K in {1024^2, 3072x1024, 1024x3072,
-    151936x1024} for N in {1, 8, 64, 512}, and flash_attn_ext (16 query /
+    151936x1024} for N in {1, 8, 64, 512} and the batch-8 prefill products
+    (N = 2048), wide ones at both precisions, and flash_attn_ext (16 query /
     8 kv heads, D 128, f16 KV of {512, 2048, 8192} positions, q_len {1, 64,
     256}; several queries at both precision contracts).
     Operands are rotated over copies totalling more than the 256 MB cache, so
@@ -550,10 +554,16 @@ def run_sweep(reps: int) -> int:
 
     plugin = g.plugin()
     for wtype in (g.Q8_0, g.Q4_K):
-        for M, K in ((1024, 1024), (3072, 1024), (1024, 3072), (151936, 1024)):
-            for N in (1, 8, 64, 512):
-                r = sweep_mul_mat(plugin, g, M, K, wtype, N, reps)
-                log(f"[sweep] mul_mat {r['type']:>4} {M:>6}x{K:<5} N={N:<4} {r['us']:9.2f} us  "
+        shapes = [(M, K, N) for M, K in ((1024, 1024), (3072, 1024), (1024, 3072), (151936, 1024))
+                  for N in (1, 8, 64, 512)]
+        # the prefill products of the Qwen3-0.6B / 1.7B batch-8 chunks (2048 columns)
+        shapes += [(4096, 1024, 2048), (3072, 1024, 2048), (2048, 6144, 2048), (6144, 2048, 2048)]
+        for M, K, N in shapes:
+            # wide products at both precision contracts (the default takes the
+            # f16 matrix-core form where planned)
+            for prec in ((g.GGML_PREC_DEFAULT, g.GGML_PREC_F32) if N > 16 else (g.GGML_PREC_DEFAULT,)):
+                r = sweep_mul_mat(plugin, g, M, K, wtype, N, reps, prec=prec)
+                log(f"[sweep] mul_mat {r['type']:>4} {r['prec']:>7} {M:>6}x{K:<5} N={N:<4} {r['us']:9.2f} us  "
                     f"{r['gbs']:8.1f} GB/s ({r['frac_hbm']:.1%} HBM)  {r['tops']:7.2f} TOP/s")
                 print(json.dumps(r), flush=True)
     for n_kv in (512, 2048, 8192):
@@ -605,17 +615,20 @@ def run_traffic_probe(workload: str) -> int:
 def run_mfma_probe() -> int:
     """the prefill-shaped kernels once each (a few computes of one-copy
     graphs), for `rocprofv3 --pmc` runs: the tile GEMM at the vocabulary
-    projection's shape and the wide attention"""
+    projection's shape and the wide attention, at the default precision (the
+    f16 matrix-core forms) and then under GGML_PREC_F32 (the exact forms)"""
     from openasr_amd import ggml as g
 
     plugin = g.plugin()
     global ROTATE_BYTES
     ROTATE_BYTES = 1  # one copy of each operand
-    for wtype in (g.Q4_K, g.Q8_0):
-        r = sweep_mul_mat(plugin, g, 151936, 1024, wtype, 512, 2)
-        log(f"[probe] mul_mat {r['type']} 151936x1024 N=512: {r['us']:.1f} us, {r['tops']:.1f} TOP/s")
-    r = sweep_fattn(plugin, g, 8192, 64, 2)
-    log(f"[probe] flash_attn_ext kv 8192 x 64 queries: {r['us']:.1f} us, {r['tflops']:.2f} TFLOP/s")
+    for prec in (g.GGML_PREC_DEFAULT, g.GGML_PREC_F32):
+        for wtype in (g.Q4_K, g.Q8_0):
+            r = sweep_mul_mat(plugin, g, 151936, 1024, wtype, 512, 2, prec=prec)
+            log(f"[probe] mul_mat {r['type']} {r['prec']} 151936x1024 N=512: {r['us']:.1f} us, "
+                f"{r['tops']:.1f} TOP/s")
+        r = sweep_fattn(plugin, g, 8192, 64, 2, prec=prec)
+        log(f"[probe] flash_attn_ext {r['prec']} kv 8192 x 64 queries: {r['us']:.1f} us, {r['tflops']:.2f} TFLOP/s")
     return 0
 
 

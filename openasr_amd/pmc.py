@@ -45,6 +45,7 @@ def _rows(d: str):
 
 
 def _short(name: str) -> str:
+    name = name.replace("(anonymous namespace)::", "")
     return name.split("(")[0].replace("void ", "").replace("mi355x::", "")
 
 

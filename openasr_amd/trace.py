@@ -22,6 +22,13 @@ import os
 import sys
 
 
+def short_name(kernel: str) -> str:
+    """a kernel's name without its namespaces and argument list (kernels in an
+    anonymous namespace carry "(anonymous namespace)::" before the name)"""
+    k = kernel.replace("(anonymous namespace)::", "")
+    return k.split("(")[0].replace("void ", "").replace("mi355x::", "")
+
+
 def _steps(rows, which: int, n: int = 8, tail: bool = False):
     idx = [i for i, r in enumerate(rows) if "k_argmax_final" in r["Kernel_Name"]]
     groups = [[idx[0]]]
@@ -46,7 +53,7 @@ def table(trace: str, which: int, workload: str, tail: bool = False) -> str:
     win, n = _steps(rows, which, tail=tail)
     st = collections.defaultdict(list)
     for r in win:
-        name = r["Kernel_Name"].split("(")[0].replace("void ", "").replace("mi355x::", "")
+        name = short_name(r["Kernel_Name"])
         if name == "k_spin":  # the profiler's queue-filling spin, not part of a step
             continue
         grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
@@ -107,7 +114,7 @@ def encoder_tables(trace: str, reps: int = 10) -> str:
             enc = rows[starts[e]:starts[e + 1]]
             for r in enc:
                 kname = r["Kernel_Name"].replace("(anonymous namespace)::", "")
-                key = (kname.split("(")[0].replace("void ", "").replace("mi355x::", ""),
+                key = (short_name(kname),
                        r["Grid_Size_X"], r["Grid_Size_Y"], r["Grid_Size_Z"], r["Workgroup_Size_X"])
                 agg[key].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
         lines = [f"## {name}", "", "| kernel | grid (threads x, y, z) | workgroup | launches / encode | avg us | us / encode |",
