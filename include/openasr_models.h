@@ -146,9 +146,10 @@ int oa_qwen_session_set_hip_lane(oa_qwen_session * s, int enable, int prefill_ch
  * effect on the next step. */
 int oa_qwen_session_set_flash_attention_precision(oa_qwen_session * s, int precision);
 
-/* The precision of the quantized projections' MUL_MATs (the graph's
- * mul_mat_with_precision, ggml_runtime/cpu_graph.rs:3622-3631; the decoder
- * builds them at GgmlMatmulPrecision::Default): GGML_PREC_DEFAULT (the
+/* The precision of the quantized projections' MUL_MATs (GgmlMatmulPrecision,
+ * ggml_runtime/cpu_graph.rs:142-146; mul_mat / mul_mat_impl :3615-3685 set
+ * GGML_PREC_F32 only on request, and the decoder's projections,
+ * nn/decoder.rs:1621, take the plain mul_mat): GGML_PREC_DEFAULT (the
  * default) lets wide prefill products run on the f16 matrix cores within
  * float tolerance; GGML_PREC_F32 keeps every product in the exact integer
  * form. Decode-size products are exact under both. Other values return

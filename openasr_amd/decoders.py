@@ -304,7 +304,7 @@ class QwenSession:
 
     def set_matmul_precision(self, precision: int):
         """the quantized projections' MUL_MAT precision (the graph's
-        mul_mat_with_precision, cpu_graph.rs:3622-3631): GGML_PREC_DEFAULT
+        GgmlMatmulPrecision, cpu_graph.rs:142-146, 3624-3685): GGML_PREC_DEFAULT
         runs wide prefill products on the f16 matrix cores within float
         tolerance, GGML_PREC_F32 keeps every product exact"""
         self._check(lib().oa_qwen_session_set_matmul_precision(self.ptr, int(precision)), "set_matmul_precision")

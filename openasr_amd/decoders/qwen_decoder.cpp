@@ -142,8 +142,9 @@ struct oa_qwen_session {
     // the self-attention's flash-attention precision contract
     // (set_flash_attention_precision, llm_transformer.rs:3044-3053)
     int fa_prec = GGML_PREC_DEFAULT;
-    // the quantized projections' MUL_MAT precision (mul_mat_with_precision,
-    // cpu_graph.rs:3622-3631): the graph builds them at the default
+    // the quantized projections' MUL_MAT precision (GgmlMatmulPrecision,
+    // cpu_graph.rs:142-146, 3624-3685): the decoder's projections take the
+    // plain mul_mat (nn/decoder.rs:1621), i.e. the default
     int mm_prec = GGML_PREC_DEFAULT;
 };
 

@@ -196,11 +196,11 @@ def test_mul_mat_sweep_points(ggml, gpu, ref, wname, m, k, n):
 # at 512 columns and at 300 (a partial column tile) in both formats; the
 # Qwen3-0.6B QKV and the Qwen3-1.7B down projection (with its residual) of a
 # batch-8 prefill chunk; a Q8_0 projection with bias and GELU_ERF; rows off
-# the 128-row tile with 96 columns and a bias.
+# the 128-row tile with 160 columns and a bias (Q4_K) or 96 (Q8_0).
 MMQ16_CASES = [
     ("q4_K", 151936, 1024, 512, None), ("q8_0", 151936, 1024, 512, None), ("q4_K", 151936, 1024, 300, None),
     ("q4_K", 4096, 1024, 2048, None), ("q4_K", 2048, 6144, 2048, "res"), ("q8_0", 3072, 1024, 2048, "bias_gelu"),
-    ("q4_K", 32784, 2048, 96, "bias"),
+    ("q4_K", 32784, 2048, 160, "bias"), ("q8_0", 32784, 2048, 96, None),
 ]
 
 
