@@ -266,6 +266,9 @@ int oa_whisper_generate(oa_whisper_session * s, int32_t first_token, int n_steps
                         double * step_ms);
 /* the layer's cross K / V caches, f16 [n_frames][d_model] */
 int oa_whisper_read_cross(const oa_whisper_session * s, int layer, uint16_t * k_out, uint16_t * v_out);
+/* the layer's self-attention K / V caches, f16 [max_positions][d_model] (row
+ * p written by the step at position p) */
+int oa_whisper_read_self(const oa_whisper_session * s, int layer, uint16_t * k_out, uint16_t * v_out);
 /* The precision contract of the decoder's self and cross FLASH_ATTN_EXT
  * (flash_attention_precision of the seq2seq decoder graphs, nn/decoder.rs:
  * 3064-3728): GGML_PREC_DEFAULT (the default) runs the single-query

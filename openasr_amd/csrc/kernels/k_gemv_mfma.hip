@@ -881,10 +881,21 @@ __global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
     int64_t M = a.M, blk = blockIdx.x;
     char * dst = a.dst;
     const char * resp = a.res;
+    int si = -1;  // the sibling matrix this workgroup serves, if any
     if (a.nsub > 1 && (int64_t) blockIdx.x >= a.sub_wg0[1]) {
         Wm = a.sub[1].W, M = a.sub[1].M, dst = a.sub[1].dst, resp = a.sub[1].res, blk -= a.sub_wg0[1];
+        si = 1;
     } else if (a.nsub > 0 && (int64_t) blockIdx.x >= a.sub_wg0[0]) {
         Wm = a.sub[0].W, M = a.sub[0].M, dst = a.sub[0].dst, resp = a.sub[0].res, blk -= a.sub_wg0[0];
+        si = 0;
+    }
+    // a sibling's SET_ROWS: the cache row its column also goes to (null: none
+    // or an index out of range)
+    uint16_t * crow = nullptr;
+    if (si >= 0 && a.sub[si].rows_dst) {
+        const gemv_sub & sb = a.sub[si];
+        const int64_t r = sb.rows_i64 ? *(const int64_t *) sb.rows_idx : (int64_t) *(const int32_t *) sb.rows_idx;
+        crow = r >= 0 && r < sb.rows_n ? (uint16_t *) (sb.rows_dst + r * sb.rows_nb1) : nullptr;
     }
     const int64_t row0 = (blk * WV + wave) * R;  // this wave's R rows
     const bool wave_ok = row0 < M;                // uniform per wave
@@ -987,7 +998,8 @@ __global__ __launch_bounds__(64 * WV) void k_gemv1_q8_0(gemv_args a) {
             if (resp) v = res[j] + v;
             if (a.epi.res2) v = res2[j] + v;
             if (a.epi.gelu) v = half_bits_to_float(a.epi.gelu[float_to_half_bits(v)]);
-            *(float *) (dst + (row0 + j) * 4) = v;
+            if (dst) *(float *) (dst + (row0 + j) * 4) = v;  // null: a sibling with only its cache row
+            if (crow) crow[row0 + j] = float_to_half_bits(v);
         }
     }
 }

@@ -18,6 +18,8 @@
 #include "mi355x_exec.h"
 
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <unordered_map>
@@ -390,7 +392,22 @@ struct planner {
             const span sp = span_of(w);
             if (sp.lo < sp.hi) s.writes.push_back({sp.lo, sp.hi});
         }
+        if (plan_trace()) {
+            std::fprintf(stderr, "mi355x plan: step %zu at node %d %s", steps.size(), cur, label);
+            for (const ggml_tensor * w : writes)
+                if (w) std::fprintf(stderr, " [%s %s]", ggml_op_name(w->op), w->name);
+            std::fprintf(stderr, "\n");
+        }
         steps.push_back(std::move(s));
+    }
+    // OPENASR_MI355X_PLAN_TRACE=1: each planned launch on stderr (its label,
+    // the graph position it runs at, the nodes it writes)
+    static bool plan_trace() {
+        static const bool on = [] {
+            const char * e = std::getenv("OPENASR_MI355X_PLAN_TRACE");
+            return e && e[0] == '1';
+        }();
+        return on;
     }
 
     bool validate();
@@ -913,9 +930,16 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             }
         }
         // sibling MUL_MATs of the same normalised column (Whisper's q, k, v
-        // projections, each maybe with a bias ADD) join a one-column launch;
-        // each is taken only if the launch with it passes hoist_ok
+        // projections, each maybe with a bias ADD) join a one-column launch.
+        // A sibling whose column only goes (through its RESHAPE to one row)
+        // to a SET_ROWS into an f16 cache writes the cache row itself
+        // (Whisper's self-attention K / V rows, the rounding of the separate
+        // op) and not the f32 column. Each sibling is taken in the first of
+        // these forms whose launch passes hoist_ok: bias and cache row, bias,
+        // cache row, neither.
         std::vector<gemv_sub> subs;
+        std::vector<const ggml_tensor *> sub_outs;  // the siblings' f32 columns the launch writes
+        std::vector<const ggml_tensor *> row_outs;  // SET_ROWS the launch performs
         if (pn != pro_norm.end() && mfma && !W2 && !epi.res2 && !epi.gelu &&
             gemv_single_column(wtype, K, N, pro.norm >= 0)) {
             for (int j = i + 1; j < cg->n_nodes && j <= i + 16 && (int) subs.size() < kGemvMaxSubs; j++) {
@@ -928,48 +952,75 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                                      (int64_t) uw->nb[1] == row_bytes && u->type == GGML_TYPE_F32 && is_contiguous(u) &&
                                      u->ne[1] * u->ne[2] * u->ne[3] == 1 && ready_before(uw, i);
                 if (!sibling) continue;
-                gemv_sub sb;
-                sb.W = (const char *) uw->data;
-                sb.M = uw->ne[1];
-                sb.dst = (char *) u->data;
-                hoist h2 = h;
-                h2.nodes.push_back(u);
-                h2.reads.push_back(span_of(uw));
-                const ggml_tensor * out = u;
+                // the bias ADD (a tensor of the column's shape)
                 const ggml_tensor * ua = sole_consumer(u, j + 1);
+                const ggml_tensor * bias = nullptr;
                 if (ua && ua->op == GGML_OP_ADD && ua->type == GGML_TYPE_F32 && is_contiguous(ua)) {
                     const ggml_tensor * o = ua->src[0] == u ? ua->src[1] : ua->src[0];
                     bool same = o != u && o->type == GGML_TYPE_F32 && o->nb[0] == 4 && columns_foldable(o);
                     for (int d = 0; d < 4 && same; d++) same = o->ne[d] == u->ne[d] && ua->ne[d] == u->ne[d];
-                    if (same && ready_before(o, i)) {
-                        hoist h3 = h2;
-                        h3.nodes.push_back(ua);
-                        h3.reads.push_back(span_of(o));
-                        h3.writes.push_back(span_of(ua));
-                        h3.inplace.push_back({ua, o});
-                        if (hoist_ok(i, h3)) {
-                            sb.res = (const char *) o->data;
-                            sb.dst = (char *) ua->data;
-                            out = ua;
-                            h2 = h3;
-                        }
+                    if (same && ready_before(o, i)) bias = o;
+                }
+                // the cache row the column goes to
+                auto set_rows_of = [&](const ggml_tensor * out) -> const ggml_tensor * {
+                    const ggml_tensor * rs = sole_consumer(out, j + 1);
+                    if (!rs || rs->op != GGML_OP_RESHAPE || rs->src[0] != out || rs->ne[0] != uw->ne[1] ||
+                        rs->ne[1] != 1 || rs->ne[2] != 1 || rs->ne[3] != 1)
+                        return nullptr;
+                    const ggml_tensor * sr = sole_consumer(rs, j + 1);
+                    if (!sr || sr->op != GGML_OP_SET_ROWS || sr->src[0] != rs || sr->type != GGML_TYPE_F16 ||
+                        sr->nb[0] != 2 || sr->ne[0] != uw->ne[1] || sr->ne[2] != 1 || sr->ne[3] != 1)
+                        return nullptr;
+                    const ggml_tensor * ix = sr->src[1];
+                    if (ggml_nelements(ix) != 1 || (ix->type != GGML_TYPE_I32 && ix->type != GGML_TYPE_I64) ||
+                        !ready_before(ix, i) || !supports_op(be->dev, sr))
+                        return nullptr;
+                    return sr;
+                };
+                auto attempt = [&](bool with_bias, bool with_rows) {
+                    const ggml_tensor * out = with_bias ? ua : u;
+                    const ggml_tensor * sr = with_rows ? set_rows_of(out) : nullptr;
+                    if ((with_bias && !bias) || (with_rows && !sr)) return false;
+                    hoist h2 = h;
+                    h2.nodes.push_back(u);
+                    h2.reads.push_back(span_of(uw));
+                    gemv_sub sb;
+                    sb.W = (const char *) uw->data;
+                    sb.M = uw->ne[1];
+                    if (with_bias) {
+                        h2.nodes.push_back(ua);
+                        h2.reads.push_back(span_of(bias));
+                        sb.res = (const char *) bias->data;
                     }
-                }
-                if (out == u) {
-                    h2.writes.push_back(span_of(u));
-                    if (!hoist_ok(i, h2)) break;
-                }
-                h = h2;
-                subs.push_back(sb);
+                    if (sr) {
+                        h2.nodes.push_back(sr);
+                        h2.reads.push_back(span_of(sr->src[1]));
+                        h2.writes.push_back(span_of(sr));
+                        sb.rows_dst = (char *) sr->data;
+                        sb.rows_idx = (const char *) sr->src[1]->data;
+                        sb.rows_i64 = sr->src[1]->type == GGML_TYPE_I64;
+                        sb.rows_nb1 = (int64_t) sr->nb[1];
+                        sb.rows_n = sr->ne[1];
+                    } else {
+                        h2.writes.push_back(span_of(out));
+                        if (with_bias) h2.inplace.push_back({ua, bias});
+                        sb.dst = (char *) out->data;
+                    }
+                    if (!hoist_ok(i, h2)) return false;
+                    h = h2;
+                    subs.push_back(sb);
+                    if (sr) row_outs.push_back(sr);
+                    else sub_outs.push_back(out);
+                    return true;
+                };
+                if (!attempt(true, true) && !attempt(true, false) && !attempt(false, true) && !attempt(false, false)) break;
             }
         }
         for (const ggml_tensor * n : h.nodes) deferred[n] = n;
         std::vector<const ggml_tensor *> outs = {produced};
-        for (const ggml_tensor * n : h.nodes) {
-            for (const gemv_sub & sb : subs)
-                if ((const char *) n->data == sb.dst) outs.push_back(n);
-        }
+        outs.insert(outs.end(), sub_outs.begin(), sub_outs.end());
         outs.insert(outs.end(), msub_outs.begin(), msub_outs.end());
+        outs.insert(outs.end(), row_outs.begin(), row_outs.end());
         if (!reuse && !has_pro) {
             add_step(
                 [=](hipStream_t s) {

@@ -65,6 +65,13 @@ struct gemv_sub {
     int64_t M = 0;
     char * dst = nullptr;
     const char * res = nullptr;
+    // optional SET_ROWS of the result column into an f16 cache: element m
+    // to rows_dst + r * rows_nb1 + 2 m with r = rows_idx[0] (I32, or I64 when
+    // rows_i64), skipped unless 0 <= r < rows_n (Whisper's self-attention K / V)
+    char * rows_dst = nullptr;
+    const char * rows_idx = nullptr;
+    int rows_i64 = 0;
+    int64_t rows_nb1 = 0, rows_n = 0;
 };
 constexpr int kGemvMaxSubs = 2;
 

@@ -130,6 +130,7 @@ def lib() -> C.CDLL:
     s("oa_whisper_decode_step", i, vp, C.c_int32, vp, vp)
     s("oa_whisper_generate", i, vp, C.c_int32, i, vp, vp)
     s("oa_whisper_read_cross", i, vp, i, vp, vp)
+    s("oa_whisper_read_self", i, vp, i, vp, vp)
     s("oa_whisper_decode_graph", vp, vp)
     s("oa_whisper_session_set_flash_attention_precision", i, vp, i)
     s("oa_qwen_generate", i, vp, vp, i, vp, vp)
@@ -430,6 +431,14 @@ class WhisperSession:
         k = np.zeros((c.n_frames, c.d_model), np.uint16)
         v = np.zeros((c.n_frames, c.d_model), np.uint16)
         self._check(lib().oa_whisper_read_cross(self.ptr, layer, k.ctypes.data, v.ctypes.data), "read_cross")
+        return k, v
+
+    def read_self(self, layer: int):
+        """the layer's self-attention K / V caches, f16 bits [max_positions, d_model]"""
+        c = self.model.cfg
+        k = np.zeros((c.max_positions, c.d_model), np.uint16)
+        v = np.zeros((c.max_positions, c.d_model), np.uint16)
+        self._check(lib().oa_whisper_read_self(self.ptr, layer, k.ctypes.data, v.ctypes.data), "read_self")
         return k, v
 
     def decode_graph(self):

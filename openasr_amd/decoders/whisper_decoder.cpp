@@ -491,6 +491,15 @@ int oa_whisper_read_cross(const oa_whisper_session * s, int layer, uint16_t * k_
     return 0;
 }
 
+int oa_whisper_read_self(const oa_whisper_session * s, int layer, uint16_t * k_out, uint16_t * v_out) {
+    const oa_whisper_config & c = s->m->cfg;
+    if (layer < 0 || layer >= c.n_layers) return 1;
+    const size_t n = (size_t) c.d_model * c.max_positions * 2;
+    if (k_out && ggml_backend_tensor_get(s->k_self[(size_t) layer], k_out, 0, n)) return 1;
+    if (v_out && ggml_backend_tensor_get(s->v_self[(size_t) layer], v_out, 0, n)) return 1;
+    return 0;
+}
+
 struct ggml_cgraph * oa_whisper_decode_graph(oa_whisper_session * s) { return s->decode.gf; }
 
 }  // extern "C"

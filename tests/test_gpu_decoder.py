@@ -410,7 +410,14 @@ def test_whisper_tiny_q8_0_first_64_steps(gpu, ref):
         assert tok_d == tok_r, f"step {i}: gpu {tok_d} != cpu {tok_r}"
     print(f"  max |dlogit| {max_dl:.2e}")
     assert max_dl < 1e-2
-    # the self K cache of the last layer holds the reference's rows
+    # the self K / V caches hold the oracle's rows (written by the q/k/v
+    # projection launch itself where the planner folds the SET_ROWS)
+    n = len(prompt) + 64
+    for layer in range(shape["n_layers"]):
+        k, v = sess.read_self(layer)
+        assert np.array_equal(k[:n], r.k[layer][:n]) and np.array_equal(v[:n], r.v[layer][:n]), f"self K/V {layer}"
+    labels = [lab.split(":", 1)[0] for lab, _ in gpu.profile(sess.decode_graph(), 1)]
+    assert "set_rows" not in labels, labels
     sess.free()
     model.free()
     w.free()

@@ -394,7 +394,7 @@ FA_CASES = [
     # d, hq, hkv, n_kv, n_q, n_seq
     (128, 16, 8, 512, 1, 1), (128, 16, 8, 1024, 1, 8), (128, 16, 8, 2048, 1, 1), (128, 16, 8, 8192, 1, 1),
     (128, 16, 8, 512, 64, 1), (128, 16, 8, 2048, 64, 2), (64, 6, 6, 448, 1, 1), (64, 6, 6, 1500, 1, 1),
-    (64, 6, 6, 1500, 1, 3), (128, 16, 8, 8192, 64, 1),
+    (64, 6, 6, 1500, 1, 3), (128, 16, 8, 8192, 64, 1), (128, 32, 8, 256, 1, 2), (64, 16, 2, 192, 1, 1),
 ]
 
 
@@ -506,6 +506,10 @@ def test_flash_attn_ext(ggml, gpu, ref, d, hq, hkv, n_kv, n_q, n_seq):
         print(f"  seq {s}: gpu vs f64 {e_gpu:.2e}, ggml-cpu numerics vs f64 {e_cpu:.2e}, "
               f"gpu vs ggml-cpu numerics {rel_err(out[s], cpu):.2e}")
         assert e_gpu < 2e-5 and e_gpu <= e_cpu
+    # again, captured and replayed: the same bits every time
+    for _ in range(3):
+        assert G.compute(gpu.backend) == 0
+        assert_same_bits(G.get(O).reshape(n_seq, n_q, hq, d), out)
     G.free()
 
 
