@@ -623,6 +623,116 @@ __global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K(gemv_args a) {
     gemv_finish(a, acc, s_red, tile, n0, nc, half, res);
 }
 
+// k_gemv_q4_K with TPW = 2 16-row tiles a workgroup, for launches where one
+// tile a workgroup would take the CUs more than one round (the Qwen3-1.7B
+// gate/up pair: 384 tiles of 16 waves, one workgroup a CU): the tiles share
+// the staged activations and each unit's activation operands, their weights
+// are requested together, and each tile's outputs are summed and stored in
+// turn. No residual (the launcher keeps such products on k_gemv_q4_K).
+template <int PRO, int MAXW>
+__global__ __launch_bounds__(64 * MAXW) void k_gemv_q4_K_pair(gemv_args a) {
+    constexpr int TPW = 2;
+    extern __shared__ __align__(16) char smem[];
+    __shared__ double s_red[16][64][4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int half = a.W2 ? nw / 2 : nw;
+    const int second = wave >= half;
+    const int wv = wave - (second ? half : 0);
+    const int r = lane & 15, g = lane >> 4;
+    const int64_t tile0 = (int64_t) blockIdx.x * TPW;
+    const int64_t ntile = a.M / 16;
+    const int n0 = (int) blockIdx.y * a.cw;
+    const int nc = min(a.cw, a.N - n0);
+    const int64_t nsb = a.K / 256;
+    const char * wrow[TPW];
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        const int64_t tt = tile0 + t < ntile ? tile0 + t : tile0;  // a missing tile reads the first, never stored
+        wrow[t] = (second ? a.W2 : a.W) + (tt * 16 + r) * a.row_bytes;
+    }
+    uint4 hdr[TPW];
+    long q[TPW][4];
+    int64_t sb = wv;
+    const float res[kFinishPerThread] = {0.0f, 0.0f, 0.0f, 0.0f};  // no residual
+    // the first unit's weights of tile t; with a prologue tile 0's are
+    // requested right after the activations the prologue waits for, tile 1's
+    // once the prologue's registers are free
+    auto issue_tile = [&](int t) {
+        // waves without a unit (staging helpers) read unit 0 and never use it
+        const char * blk = wrow[t] + (sb < nsb ? sb : 0) * 144;
+        hdr[t] = *(const uint4 *) blk;
+#pragma unroll
+        for (int c = 0; c < 4; c++) q[t][c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
+    };
+    auto issue = [&]() { issue_tile(0); };
+    // activation operands: LDS after the prologue, else the global buffers
+    const int8_t * aq;
+    const float * adp;
+    const int16_t * asp;
+    int64_t q_stride, d_stride, ss_stride;
+    int c0;  // column index of the chunk's first column in the operand arrays
+    if constexpr (PRO != kProNone) {
+        if constexpr (PRO == kProQuant) gemv_stage_quant<GGML_TYPE_Q4_K>(a, n0, nc, smem, issue);
+        else gemv_stage_norm<GGML_TYPE_Q4_K, PRO == kProNormBias>(a, n0, nc, smem, issue);
+        const gemv_lds L = gemv_lds_layout(GGML_TYPE_Q4_K, a.K, nc);
+        aq = (const int8_t *) (smem + L.q_off);
+        adp = (const float *) (smem + L.d_off);
+        asp = (const int16_t *) (smem + L.ss_off);
+        q_stride = L.q_stride;
+        d_stride = L.d_stride;
+        ss_stride = L.ss_stride;
+        c0 = 0;
+    } else {
+        issue();
+        aq = a.aq;
+        adp = a.ad;
+        asp = a.ass;
+        q_stride = a.K;
+        d_stride = nsb;
+        ss_stride = a.K / 32;
+        c0 = n0;
+    }
+    issue_tile(1);
+    const bool a_ok = r < nc;  // this lane's A-operand column
+    const int8_t * acol = aq + (int64_t) (c0 + (a_ok ? r : 0)) * q_stride;
+    // the tiles one after the other (tile 1's first weights in flight
+    // meanwhile), so only one tile's sums are live at a time
+#pragma unroll
+    for (int t = 0; t < TPW; t++) {
+        if (tile0 + t >= ntile) break;  // uniform
+        double acc[4] = {0.0, 0.0, 0.0, 0.0};
+        for (int64_t u = wv; u < nsb; u += half) {
+            long af[8];
+            float ad[4], ssa[2];
+            // every load unconditional (clamped to column 0 of the chunk,
+            // which always exists) and masked afterwards
+#pragma unroll
+            for (int j = 0; j < 8; j++) af[j] = *(const long *) (acol + u * 256 + 32 * j + 8 * g);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int n = 4 * g + i;
+                const int nn = n < nc ? n : 0;
+                ad[i] = adp[(int64_t) (c0 + nn) * d_stride + u];
+            }
+            q4k_ssum_operand(asp + (int64_t) (c0 + (a_ok ? r : 0)) * ss_stride + u * 8, a_ok, g, ssa);
+#pragma unroll
+            for (int j = 0; j < 8; j++) af[j] = a_ok ? af[j] : 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) ad[i] = 4 * g + i < nc ? ad[i] : 0.0f;
+            q4k_unit(hdr[t], q[t], af, ad, ssa, acc);
+            // the tile's next unit
+            if (u + half < nsb) {
+                const char * blk = wrow[t] + (u + half) * 144;
+                hdr[t] = *(const uint4 *) blk;
+#pragma unroll
+                for (int c = 0; c < 4; c++) q[t][c] = *(const long *) (blk + 16 + 32 * c + 8 * g);
+            }
+        }
+        if (t > 0) __syncthreads();  // the previous tile's sums have been read from s_red
+        gemv_finish(a, acc, s_red, tile0 + t, n0, nc, half, res);
+    }
+}
+
 // Q8_0 weights in the row-split layout [K quants][K/32 f16 scales]; the waves
 // take groups of 8 blocks round-robin, each group's loads issued together
 // (the first group's weights before the prologue)
@@ -1073,29 +1183,38 @@ int gemv_cols(int wtype, int64_t M, int64_t K, int64_t N, bool dual, int mode, i
 }
 
 // kernels compiled for at most 8 waves get twice the registers per lane
-template <int PRO, int MAXW>
+template <int PRO, int MAXW, int TPW>
 void launch_kernel_w(int wtype, const dim3 & grid, const dim3 & block, size_t lds, hipStream_t stream,
                      const gemv_args & a) {
+    static_assert(TPW == 1 || TPW == 2, "tiles a workgroup");
+    const void * fn = wtype != GGML_TYPE_Q4_K ? (const void *) k_gemv_q8_0<PRO, MAXW>
+                      : TPW == 2               ? (const void *) k_gemv_q4_K_pair<PRO, MAXW>
+                                               : (const void *) k_gemv_q4_K<PRO, MAXW>;
     if (lds > 48 * 1024) {
         // staged columns beyond the default dynamic-LDS limit: raise it once per kernel
-        static bool raised[2] = {false, false};
+        static bool raised[2] = {false, false};  // per instantiation: Q4_K, Q8_0
         const int idx = wtype == GGML_TYPE_Q4_K ? 0 : 1;
         if (!raised[idx]) {
-            const void * fn = wtype == GGML_TYPE_Q4_K ? (const void *) k_gemv_q4_K<PRO, MAXW>
-                                                      : (const void *) k_gemv_q8_0<PRO, MAXW>;
             MI_CHECK(hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024 - 32768));
             raised[idx] = true;
         }
     }
-    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL((k_gemv_q4_K<PRO, MAXW>), grid, block, lds, stream, a);
-    else hipLaunchKernelGGL((k_gemv_q8_0<PRO, MAXW>), grid, block, lds, stream, a);
+    if (wtype != GGML_TYPE_Q4_K) hipLaunchKernelGGL((k_gemv_q8_0<PRO, MAXW>), grid, block, lds, stream, a);
+    else if (TPW == 2) hipLaunchKernelGGL((k_gemv_q4_K_pair<PRO, MAXW>), grid, block, lds, stream, a);
+    else hipLaunchKernelGGL((k_gemv_q4_K<PRO, MAXW>), grid, block, lds, stream, a);
 }
 
+// tpw: 16-row tiles a workgroup (2 only for Q4_K)
 template <int PRO>
 void launch_kernel(int wtype, const dim3 & grid, const dim3 & block, size_t lds, hipStream_t stream,
-                   const gemv_args & a) {
-    if (block.x <= 512) launch_kernel_w<PRO, 8>(wtype, grid, block, lds, stream, a);
-    else launch_kernel_w<PRO, 16>(wtype, grid, block, lds, stream, a);
+                   const gemv_args & a, int tpw) {
+    if (block.x <= 512) {
+        if (tpw == 2) launch_kernel_w<PRO, 8, 2>(wtype, grid, block, lds, stream, a);
+        else launch_kernel_w<PRO, 8, 1>(wtype, grid, block, lds, stream, a);
+    } else {
+        if (tpw == 2) launch_kernel_w<PRO, 16, 2>(wtype, grid, block, lds, stream, a);
+        else launch_kernel_w<PRO, 16, 1>(wtype, grid, block, lds, stream, a);
+    }
 }
 
 }  // namespace
@@ -1207,14 +1326,22 @@ void launch_gemv_mfma(int wtype, const char * W, int64_t row_bytes, int64_t M, i
         return;
     }
     a.cw = gemv_cols(wtype, M, K, N, W2 != nullptr, mode, n_cu);
-    const dim3 grid((unsigned) (M / 16), (unsigned) ((N + a.cw - 1) / a.cw));
-    const dim3 block(64 * gemv_waves(wtype, K, a.cw, W2 != nullptr, mode));
+    const int waves = gemv_waves(wtype, K, a.cw, W2 != nullptr, mode);
+    const int64_t chunks = (N + a.cw - 1) / a.cw;
+    // Q4_K without a residual: two tiles a workgroup where one a workgroup
+    // would take the CUs more than one round (16 / waves workgroups fit a CU;
+    // the Qwen3-1.7B gate/up pair, 384 tiles of 16 waves)
+    const int tpw = wtype == GGML_TYPE_Q4_K && !res && (M / 16) % 2 == 0 &&
+                            (M / 16) * chunks > (int64_t) n_cu * (16 / waves)
+                        ? 2 : 1;
+    const dim3 grid((unsigned) (M / 16 / tpw), (unsigned) chunks);
+    const dim3 block(64 * waves);
     const size_t lds = mode == kProNone ? 0 : (size_t) gemv_lds_layout(wtype, K, (int) (N < a.cw ? N : a.cw)).total;
     switch (mode) {
-        case kProNone: launch_kernel<kProNone>(wtype, grid, block, lds, stream, a); break;
-        case kProQuant: launch_kernel<kProQuant>(wtype, grid, block, lds, stream, a); break;
-        case kProNorm: launch_kernel<kProNorm>(wtype, grid, block, lds, stream, a); break;
-        default: launch_kernel<kProNormBias>(wtype, grid, block, lds, stream, a); break;
+        case kProNone: launch_kernel<kProNone>(wtype, grid, block, lds, stream, a, tpw); break;
+        case kProQuant: launch_kernel<kProQuant>(wtype, grid, block, lds, stream, a, tpw); break;
+        case kProNorm: launch_kernel<kProNorm>(wtype, grid, block, lds, stream, a, tpw); break;
+        default: launch_kernel<kProNormBias>(wtype, grid, block, lds, stream, a, tpw); break;
     }
 }
 

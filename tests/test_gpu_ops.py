@@ -49,6 +49,8 @@ MM_CASES = [
     ("q8_0", 64, 256), ("q8_0", 1024, 1024), ("q8_0", 3072, 1024), ("q8_0", 1024, 3072), ("q8_0", 384, 384),
     ("q8_0", 1536, 384), ("q8_0", 384, 1536), ("q4_K", 64, 256), ("q4_K", 1024, 1024), ("q4_K", 3072, 1024),
     ("q4_K", 1024, 3072), ("q4_K", 4096, 2048), ("q4_K", 2048, 6144),
+    # 384 row tiles at 8 columns: two tiles a workgroup (one round of the CUs)
+    ("q4_K", 6144, 2048),
     # M not a multiple of the tile GEMM's 64 rows (its last row tile has idle waves)
     ("q4_K", 1040, 512), ("q8_0", 1040, 384),
     # rows off the 16-row tile (a vocabulary of 51865: the single-column form at N = 1)
