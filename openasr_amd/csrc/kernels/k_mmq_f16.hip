@@ -27,8 +27,10 @@
 // weights and activations are requested into registers while the previous
 // step is multiplied, then dequantized into the other of two LDS buffers
 // (16-byte pieces XOR-swizzled by row: conflict-free fragment reads, 64 KB
-// of LDS a workgroup, two workgroups a CU); one barrier a
-// step. Wave (wr, wc) multiplies the 64 x 64 quarter (wr: rows, wc:
+// of LDS a workgroup); one barrier a
+// step (174 VGPRs + 88 AGPRs: one workgroup a CU; held to two a CU, 256
+// registers a lane, the compiler fits without spills but the GEMM measured
+// 1-5 % slower). Wave (wr, wc) multiplies the 64 x 64 quarter (wr: rows, wc:
 // columns) as 4 x 4 blocks of 16 x 16: the activations are the MFMA A
 // operand (lane l: column l % 16, k 8 (l / 16) .. + 7), the weights the B
 // operand, so lane l ends with weight row l % 16 of four consecutive
@@ -63,6 +65,7 @@ typedef float hf4 __attribute__((ext_vector_type(4)));
 
 struct mmqh_args {
     const char * W;
+    const char * W2;  // SwiGLU form: the up matrix (W the gate), same shape
     int64_t row_bytes, M, K;
     const uint16_t * x16;  // the dequantized activations, f16 [N][K]
     int N;
@@ -207,7 +210,11 @@ __device__ __forceinline__ void hq_store(const hq_regs & r, int64_t k0, uint16_t
     *hq_slot(sx, xc + 96, xp) = r.x3;
 }
 
-template <int WT>
+// SWI (the SwiGLU pair, MUL(SILU(W x), W2 x)): a tile holds 64 gate rows
+// (tile rows 0 .. 63) and the same 64 rows of the up matrix (64 .. 127); the
+// up waves hand their sums to the gate waves through LDS, which store
+// silu(g) * u for the 64 rows -- the roundings of MUL_MAT, SILU and MUL apart.
+template <int WT, bool SWI>
 __global__ __launch_bounds__(kHThreads) void k_mmq_f16(mmqh_args a) {
     __shared__ __align__(16) uint16_t s_w[2][kHM][kHRow];
     __shared__ __align__(16) uint16_t s_x[2][kHN][kHRow];
@@ -241,11 +248,13 @@ __global__ __launch_bounds__(kHThreads) void k_mmq_f16(mmqh_args a) {
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wr = wave & 1, wc = wave >> 1;
-    const int64_t m0 = row_tile * kHM;
+    const int64_t m0 = row_tile * (SWI ? kHM / 2 : kHM);  // the tile's first output row
     const int n0 = (int) (col_block * kHN);
     // this thread's staging row (rows past M repeat the last one; their
     // outputs are not stored)
-    const char * wrow = a.W + min(m0 + (threadIdx.x >> 1), a.M - 1) * a.row_bytes;
+    const int sr = (int) (threadIdx.x >> 1);
+    const char * wrow = SWI ? (sr < kHM / 2 ? a.W : a.W2) + min(m0 + (sr & (kHM / 2 - 1)), a.M - 1) * a.row_bytes
+                            : a.W + min(m0 + sr, a.M - 1) * a.row_bytes;
     const int64_t nsteps = a.K / kHK;
     hf4 acc[4][4];
 #pragma unroll
@@ -295,6 +304,37 @@ __global__ __launch_bounds__(kHThreads) void k_mmq_f16(mmqh_args a) {
         hq_store<WT>(ra, kstep(s + 2), s_w[0], s_x[0]);
         hq_load<WT>(a, wrow, n0, kstep(s + 4), ra);
         __syncthreads();
+    }
+    if constexpr (SWI) {
+        // the up waves' sums through the staging buffers (free after the
+        // loop's last barrier): lane, block (i, j) of wave column wc
+        hf4 * s_up = (hf4 *) &s_w[0][0][0];
+        static_assert(sizeof(s_w) >= 2 * 16 * 64 * sizeof(hf4), "staging buffers hold the up sums");
+        if (wr == 1) {
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) s_up[(wc * 16 + 4 * i + j) * 64 + lane] = acc[i][j];
+        }
+        __syncthreads();
+        if (wr == 0) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int64_t m = m0 + 16 * j + fr;
+                if (m >= a.M) continue;
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const hf4 up = s_up[(wc * 16 + 4 * i + j) * 64 + lane];
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const int n = n0 + wc * 64 + 16 * i + 4 * (lane >> 4) + v;
+                        const float g = acc[i][j][v];
+                        if (n < a.N) *(float *) (a.dst + (int64_t) n * a.dst_nb1 + m * 4) = (g / (1.0f + expf_det(-g))) * up[v];
+                    }
+                }
+            }
+        }
+        return;
     }
     // lane: weight row m0 + 64 wr + 16 j + lane % 16 of columns n0 + 64 wc +
     // 16 i + 4 (lane / 16) + v; the adds, then (GELU_ERF) the lane's values
@@ -373,7 +413,7 @@ size_t mmq_f16_scratch_bytes(int64_t K, int64_t N) { return (size_t) (K * N * 2 
 
 void launch_mmq_f16(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                     int64_t N, char * dst, int64_t dst_nb1, void * scratch, hipStream_t stream,
-                    const gemm_float_epi & epi, const gemm_float_sub * subs, int nsub) {
+                    const gemm_float_epi & epi, const gemm_float_sub * subs, int nsub, const char * W2) {
     uint16_t * x16 = (uint16_t *) scratch;
     const int64_t n8 = K * N / 8;
     if (wtype == GGML_TYPE_Q4_K)
@@ -382,7 +422,26 @@ void launch_mmq_f16(int wtype, const char * W, int64_t row_bytes, int64_t M, int
     else
         hipLaunchKernelGGL(k_act_f16<GGML_TYPE_Q8_0>, dim3((unsigned) ((n8 + 255) / 256)), dim3(256), 0, stream, act, K,
                            N, x16);
+    if (W2) {
+        // the SwiGLU pair: 64 output rows a tile, no epilogue adds or siblings
+        if (nsub != 0 || epi.bias || epi.res || epi.gelu_erf || M % (kHM / 2) != 0) {
+            note_hip_error(hipErrorInvalidValue);
+            return;
+        }
+        mmqh_args b = mmqh_args{};
+        b.W = W, b.W2 = W2, b.row_bytes = row_bytes, b.M = M, b.K = K, b.x16 = x16, b.N = (int) N, b.dst = dst;
+        b.dst_nb1 = dst_nb1;
+        b.nsub = 0;
+        b.col_blocks = (N + kHN - 1) / kHN;
+        b.tiles = M / (kHM / 2) * b.col_blocks;
+        b.per_xcd = (b.tiles + kHXcds - 1) / kHXcds;
+        const dim3 grid((unsigned) (b.per_xcd * kHXcds));
+        if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL((k_mmq_f16<GGML_TYPE_Q4_K, true>), grid, dim3(kHThreads), 0, stream, b);
+        else hipLaunchKernelGGL((k_mmq_f16<GGML_TYPE_Q8_0, true>), grid, dim3(kHThreads), 0, stream, b);
+        return;
+    }
     mmqh_args a;
+    a.W2 = nullptr;
     a.nsub = 0;
     int64_t m_all = M;
     bool joined = nsub == 0;
@@ -404,8 +463,9 @@ void launch_mmq_f16(int wtype, const char * W, int64_t row_bytes, int64_t M, int
             b.tiles = (m + kHM - 1) / kHM * b.col_blocks;
             b.per_xcd = (b.tiles + kHXcds - 1) / kHXcds;
             const dim3 grid((unsigned) (b.per_xcd * kHXcds));
-            if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_mmq_f16<GGML_TYPE_Q4_K>, grid, dim3(kHThreads), 0, stream, b);
-            else hipLaunchKernelGGL(k_mmq_f16<GGML_TYPE_Q8_0>, grid, dim3(kHThreads), 0, stream, b);
+            if (wtype == GGML_TYPE_Q4_K)
+                hipLaunchKernelGGL((k_mmq_f16<GGML_TYPE_Q4_K, false>), grid, dim3(kHThreads), 0, stream, b);
+            else hipLaunchKernelGGL((k_mmq_f16<GGML_TYPE_Q8_0, false>), grid, dim3(kHThreads), 0, stream, b);
         };
         one(W, M, dst, dst_nb1, epi);
         for (int i = 0; i < nsub; i++) {
@@ -443,8 +503,8 @@ void launch_mmq_f16(int wtype, const char * W, int64_t row_bytes, int64_t M, int
     a.tiles = (m_all + kHM - 1) / kHM * a.col_blocks;
     a.per_xcd = (a.tiles + kHXcds - 1) / kHXcds;
     const dim3 grid((unsigned) (a.per_xcd * kHXcds));
-    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL(k_mmq_f16<GGML_TYPE_Q4_K>, grid, dim3(kHThreads), 0, stream, a);
-    else hipLaunchKernelGGL(k_mmq_f16<GGML_TYPE_Q8_0>, grid, dim3(kHThreads), 0, stream, a);
+    if (wtype == GGML_TYPE_Q4_K) hipLaunchKernelGGL((k_mmq_f16<GGML_TYPE_Q4_K, false>), grid, dim3(kHThreads), 0, stream, a);
+    else hipLaunchKernelGGL((k_mmq_f16<GGML_TYPE_Q8_0, false>), grid, dim3(kHThreads), 0, stream, a);
 }
 
 }  // namespace mi355x

@@ -763,10 +763,16 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             h = h2;
             return true;
         };
+        // the default precision (the graph's contract, op_params[0]) with
+        // enough tiles and 16-byte weight rows: the f16 matrix-core form
+        // (k_mmq_f16.hip, float tolerance)
+        const bool mmq16_ok = wide && t->op_params[0] != GGML_PREC_F32 && mmq_f16_supported(wtype, M, K, N, n_cu) &&
+                              row_bytes % 16 == 0 && aligned16(W);
         // SwiGLU: MUL_MAT(gate, x) -> SILU -> MUL with MUL_MAT(up, x) of the
-        // same shape becomes one launch over both matrices
+        // same shape becomes one launch over both matrices (the GEMV, or the
+        // f16 tile GEMM for 64-row multiples)
         const char * W2 = nullptr;
-        const ggml_tensor * silu = mfma ? sole_consumer(t, i + 1) : nullptr;
+        const ggml_tensor * silu = mfma || (mmq16_ok && M % 64 == 0) ? sole_consumer(t, i + 1) : nullptr;
         if (silu && silu->op == GGML_OP_UNARY && silu->op_params[0] == GGML_UNARY_OP_SILU && silu->src[0] == t) {
             const ggml_tensor * hm = sole_consumer(silu, i + 1);
             const ggml_tensor * u = nullptr;
@@ -776,7 +782,8 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
             bool ok = u && u->op == GGML_OP_MUL_MAT && u->src[1] == x && u->src[0]->type == wtype &&
                       u->src[0]->ne[0] == K && u->src[0]->ne[1] == M && u->src[0]->nb[1] == w->nb[1] &&
                       sole_consumer(u, i + 1) == hm && supports_op(be->dev, u) && is_contiguous(hm) &&
-                      ready_before(u->src[0], i);
+                      ready_before(u->src[0], i) && u->op_params[0] == t->op_params[0] &&
+                      (mfma || aligned16(u->src[0]->data));
             for (int d = 0; d < 4 && ok; d++) ok = hm->ne[d] == t->ne[d] && u->ne[d] == t->ne[d];
             if (ok && try_fold({silu, u, hm}, hm, {u->src[0]}, nullptr)) {
                 W2 = (const char *) u->src[0]->data;
@@ -789,7 +796,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         // ADD of the output's shape and a GELU_ERF fold into its epilogue,
         // with the roundings of the separate ops
         gemm_float_epi mepi;
-        if (wide && is_contiguous(t)) {
+        if (wide && !W2 && is_contiguous(t)) {
             auto plain = [](const ggml_tensor * o) { return o->type == GGML_TYPE_F32 && is_contiguous(o); };
             auto shaped = [&](const ggml_tensor * o) {
                 for (int d = 0; d < 4; d++)
@@ -832,7 +839,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         // passes hoist_ok
         std::vector<gemm_float_sub> msubs;
         std::vector<const ggml_tensor *> msub_outs;
-        if (wide && is_contiguous(t) && !mepi.res && !mepi.gelu_erf && M % 64 == 0 && N == t->ne[1]) {
+        if (wide && !W2 && is_contiguous(t) && !mepi.res && !mepi.gelu_erf && M % 64 == 0 && N == t->ne[1]) {
             for (int j = i + 1; j < cg->n_nodes && j <= i + 16 && (int) msubs.size() < kGemmFloatMaxSubs; j++) {
                 const ggml_tensor * u = cg->nodes[j];
                 if (is_view_op(u->op) || deferred.count(u)) continue;
@@ -881,11 +888,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 msub_outs.push_back(out);
             }
         }
-        // the default precision (the graph's contract, op_params[0]) with
-        // enough tiles and 16-byte weight rows: the f16 matrix-core form
-        // (k_mmq_f16.hip, float tolerance)
-        bool mmq16 = wide && t->op_params[0] != GGML_PREC_F32 && mmq_f16_supported(wtype, M, K, N, n_cu) &&
-                     row_bytes % 16 == 0 && aligned16(W);
+        bool mmq16 = mmq16_ok;
         for (const gemm_float_sub & sb : msubs) mmq16 = mmq16 && aligned16(sb.a);
         if (mmq16) gen_need = std::max(gen_need, mmq_f16_scratch_bytes(K, N));
         // a following residual ADD of the same shape folds into the epilogue
@@ -1034,7 +1037,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 act_buffers act = act_carve(wtype, act_base(b), K, N);
                 if (mmq16)
                     launch_mmq_f16(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, gen_base(b), s, mepi,
-                                   msubs.empty() ? nullptr : msubs.data(), (int) msubs.size());
+                                   msubs.empty() ? nullptr : msubs.data(), (int) msubs.size(), W2);
                 else if (wide)
                     launch_mmq(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu, mepi,
                                msubs.empty() ? nullptr : msubs.data(), (int) msubs.size());
@@ -1043,8 +1046,9 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                                      has_pro ? &pro : nullptr, epi, subs.data(), (int) subs.size());
                 else launch_mmv(wtype, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
             },
-            produced, W2     ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")
-                      : mmq16 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_f16_q8_0" : "mul_mat_f16_q4_K")
+            produced, W2 && mmq16 ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_f16_q8_0" : "mul_mat_swiglu_f16_q4_K")
+                      : W2      ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_swiglu_q8_0" : "mul_mat_swiglu_q4_K")
+                      : mmq16   ? (wtype == GGML_TYPE_Q8_0 ? "mul_mat_f16_q8_0" : "mul_mat_f16_q4_K")
                               : (wtype == GGML_TYPE_Q8_0 ? "mul_mat_q8_0" : "mul_mat_q4_K"),
             outs);
         return true;

@@ -99,9 +99,12 @@ void launch_mmq(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t
 // are a multiple of 128)
 bool mmq_f16_supported(int wtype, int64_t M, int64_t K, int64_t N, int n_cu);
 size_t mmq_f16_scratch_bytes(int64_t K, int64_t N);
+// W2: the SwiGLU pair -- dst = silu(W x) * (W2 x), W2 of W's shape, M a
+// multiple of 64, no epilogue adds and no subs
 void launch_mmq_f16(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                     int64_t N, char * dst, int64_t dst_nb1, void * scratch, hipStream_t stream,
-                    const gemm_float_epi & epi, const gemm_float_sub * subs = nullptr, int nsub = 0);
+                    const gemm_float_epi & epi, const gemm_float_sub * subs = nullptr, int nsub = 0,
+                    const char * W2 = nullptr);
 
 // float GEMM fallback (f16 / f32 src0)
 void launch_mul_mat_float(const tview & d, const tview & a, int atype, const tview & b, hipStream_t s);

@@ -266,6 +266,56 @@ def test_mul_mat_f16_matrix_cores(ggml, gpu, ref, wname, m, k, n, tail):
     G.free()
 
 
+@pytest.mark.parametrize("wname,m,k,n", [("q4_K", 6144, 2048, 1024), ("q4_K", 3072, 1024, 2048),
+                                         ("q8_0", 3072, 1024, 1408), ("q4_K", 3008, 1024, 1300)])
+def test_mul_mat_swiglu_f16_matrix_cores(ggml, gpu, ref, wname, m, k, n):
+    """the prefill FFN gate: MUL(SILU(MUL_MAT(gate, x)), MUL_MAT(up, x)) at
+    the default precision is one f16 tile GEMM launch (a tile's 64 gate rows
+    and the same 64 up rows, combined in its epilogue): within 2e-3 of
+    silu(exact gate product) * exact up product from the oracle, graph
+    replays bit-identical; under GGML_PREC_F32 the products stay exact and
+    the graph bit for bit the oracle's"""
+    wt = ggml.Q8_0 if wname == "q8_0" else ggml.Q4_K
+    print(f"f16 swiglu {wname} M={m} K={k} N={n}", flush=True)
+    wg = ggml.quantize(wt, ggml.synth_normal(11, m + k, m * k, 0.0, 0.02).reshape(m, k))
+    wu = ggml.quantize(wt, ggml.synth_normal(12, m + k, m * k, 0.0, 0.02).reshape(m, k))
+    x = np.random.default_rng(m + k + n).standard_normal((n, k)).astype(np.float32)
+    gate, up = ref.mul_mat(wt, wg, m, k, x), ref.mul_mat(wt, wu, m, k, x)
+    for prec in (None, ggml.GGML_PREC_F32):
+        G = ggml.Graph()
+        L = G.lib
+        Wg = G.new(wt, k, m, weight=True)
+        Wu = G.new(wt, k, m, weight=True)
+        X = G.new(ggml.F32, k, n)
+        Pg, Pu = L.ggml_mul_mat(G.ctx, Wg, X), L.ggml_mul_mat(G.ctx, Wu, X)
+        if prec is not None:
+            L.ggml_mul_mat_set_prec(Pg, prec)
+            L.ggml_mul_mat_set_prec(Pu, prec)
+        Y = L.ggml_mul(G.ctx, L.ggml_silu(G.ctx, Pg), Pu)
+        run(ggml, gpu, G, Y)
+        G.set(Wg, wg)
+        G.set(Wu, wu)
+        G.set(X, x)
+        assert G.compute(gpu.backend) == 0
+        labels = plan_labels(gpu, G)
+        y = G.get(Y).reshape(n, m)
+        if prec is None:
+            assert f"mul_mat_swiglu_f16_{wname}" in labels, labels
+            g64 = gate.astype(np.float64)
+            want = g64 / (1.0 + np.exp(-g64)) * up.astype(np.float64)
+            err = rel_err(y, want)
+            print(f"  vs the exact products: {err:.2e}", flush=True)
+            assert err < 2e-3 and np.isfinite(y).all()
+        else:
+            assert not any("f16" in lab for lab in labels), labels
+            assert_same_bits(y, ref.silu(gate) * up)
+        first = y.copy()
+        for _ in range(2):  # captured, then replayed
+            assert G.compute(gpu.backend) == 0
+            assert np.array_equal(G.get(Y).reshape(n, m).view(np.uint32), first.view(np.uint32))
+        G.free()
+
+
 def quantizer_edge_activations(n, k, seed):
     """activation columns whose 256-element blocks hit the quantizers' edge
     cases: +A and -A both at the block maximum (the first in element order
