@@ -251,6 +251,30 @@ __device__ __forceinline__ void gf_stage_raw(const gf_raw & a, const gf_raw & b,
     }
 }
 
+// X3 staging: eight f32 elements (zeros when not live) as bf16 hi (rounded to
+// nearest even) and lo = bf16(x - hi): hi + lo carries ~17 of the 24 bits
+typedef __bf16 gf_v8b __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ void gf_split8(const gf_raw & v, uint4 & hi, uint4 & lo) {
+    const uint32_t f[8] = {v.r[0].x, v.r[0].y, v.r[0].z, v.r[0].w, v.r[1].x, v.r[1].y, v.r[1].z, v.r[1].w};
+    uint32_t h[4], l[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint32_t hb[2], lb[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const float x = v.ok ? __uint_as_float(f[2 * i + e]) : 0.0f;
+            const __bf16 xh = (__bf16) x;
+            const __bf16 xl = (__bf16) (x - (float) xh);
+            hb[e] = __builtin_bit_cast(uint16_t, xh);
+            lb[e] = __builtin_bit_cast(uint16_t, xl);
+        }
+        h[i] = hb[0] | (hb[1] << 16);
+        l[i] = lb[0] | (lb[1] << 16);
+    }
+    hi = make_uint4(h[0], h[1], h[2], h[3]);
+    lo = make_uint4(l[0], l[1], l[2], l[3]);
+}
+
 // The aligned form (16-byte aligned rows of both operands, K % 8 == 0):
 // kGfDepth slabs in flight, slab j in register slot j % kGfDepth from its
 // request until it is staged, and the LDS double-buffered -- step s
@@ -333,6 +357,118 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float_v(gemm_float_args g) 
             const int64_t kn = (s0 + p + 1 + kGfDepth) * kGfBK + sk;
             gf_load_raw<F16>(arow, kn, K, a_live, av[q]);
             gf_load_raw<BF16>(brow, kn, K, b_live, bv[q]);
+            __syncthreads();
+        }
+    }
+    gf_store(g, acc, m0, n0, wr, wc, lane, dbase, g.splits > 1 ? g.part + ks * g.M * g.N : nullptr);
+}
+
+// The aligned form for an F32 x F32 product at the default precision (x3):
+// the same tiles, slabs in flight and barriers as k_gemm_float_v, the slab
+// staged as bf16 hi / lo halves of each f32 element and each 16 x 16 block
+// advanced by three bf16 MFMAs a 32-wide slab (lo hi, hi lo, then hi hi; the
+// lo lo term, ~2^-16 of the product, dropped) instead of eight f32 ones.
+template <int PADE>
+__device__ __forceinline__ void gf_mfma_x3(const uint16_t (*sah)[kGfBK + PADE], const uint16_t (*sal)[kGfBK + PADE],
+                                           const uint16_t (*sbh)[kGfBK + PADE], const uint16_t (*sbl)[kGfBK + PADE],
+                                           int wr, int wc, int lane, gf_v4f (&acc)[2][2]) {
+    const int r16 = lane & 15, kg = lane >> 4;
+    gf_v8b bh[2], bl[2], ah[2], al[2];
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        bh[j] = *(const gf_v8b *) &sbh[wc + 16 * j + r16][8 * kg];
+        bl[j] = *(const gf_v8b *) &sbl[wc + 16 * j + r16][8 * kg];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        ah[i] = *(const gf_v8b *) &sah[wr + 16 * i + r16][8 * kg];
+        al[i] = *(const gf_v8b *) &sal[wr + 16 * i + r16][8 * kg];
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bl[j], ah[i], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[j], al[i], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bh[j], ah[i], acc[i][j], 0, 0, 0);
+        }
+}
+
+__global__ __launch_bounds__(kGfThreads) void k_gemm_float_x3(gemm_float_args g) {
+    constexpr int PADE = 8;
+    __shared__ __align__(16) uint16_t sah[2][kGfBM][kGfBK + PADE], sal[2][kGfBM][kGfBK + PADE];
+    __shared__ __align__(16) uint16_t sbh[2][kGfBN][kGfBK + PADE], sbl[2][kGfBN][kGfBK + PADE];
+    const int tid = (int) threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    int64_t m0 = (int64_t) blockIdx.x * kGfBM;
+    const int64_t n0 = (int64_t) blockIdx.y * kGfBN;
+    static_assert(kGemmFloatMaxSubs == 2, "product selection below");
+    if (g.nsub > 0) {
+        int64_t base = 0, mend = g.sub_m0[1];
+        const char * sa = g.sub_a[0];
+        char * sd = g.sub_d[0];
+        const float * sbias = g.sub_bias[0];
+        if (m0 >= g.sub_m0[1]) {
+            base = g.sub_m0[1], mend = g.sub_m0[2];
+            sa = g.sub_a[1], sd = g.sub_d[1], sbias = g.sub_bias[1];
+        }
+        if (g.nsub >= 2 && m0 >= g.sub_m0[2]) {
+            base = g.sub_m0[2], mend = g.sub_m0[3];
+            sa = g.sub_a[2], sd = g.sub_d[2], sbias = g.sub_bias[2];
+        }
+        m0 -= base;
+        g.M = mend - base;
+        g.a = sa;
+        g.d = sd;
+        g.d_nb1 = g.M * 4;
+        g.epi.bias = sbias;
+    }
+    const int zb = g.splits > 1 ? 0 : (int) blockIdx.z, ks = g.splits > 1 ? (int) blockIdx.z : 0;
+    const int i2 = zb % g.ne2, i3 = zb / g.ne2;
+    const int64_t kb = (int64_t) ks * g.k_span;
+    const int64_t K = g.splits > 1 ? (g.K - kb < g.k_span ? g.K - kb : g.k_span) : g.K;
+    const char * abase = g.a + (int64_t) (i2 / g.r2) * g.a_nb2 + (int64_t) (i3 / g.r3) * g.a_nb3 + kb * 4;
+    const char * bbase = g.b + (int64_t) i2 * g.b_nb2 + (int64_t) i3 * g.b_nb3 + kb * 4;
+    char * dbase = g.d + (int64_t) i2 * g.d_nb2 + (int64_t) i3 * g.d_nb3;
+    const int srow = tid >> 2, sk = (tid & 3) * 8;
+    const bool a_live = m0 + srow < g.M, b_live = n0 + srow < g.N;
+    const char * arow = abase + (a_live ? m0 + srow : 0) * g.a_nb1;
+    const char * brow = bbase + (b_live ? n0 + srow : 0) * g.b_nb1;
+    const int64_t S = ((K + kGfBK - 1) / kGfBK + kGfDepth - 1) / kGfDepth * kGfDepth;
+    auto stage = [&](const gf_raw & a, const gf_raw & b, int buf) {
+        uint4 hi, lo;
+        gf_split8(a, hi, lo);
+        *(uint4 *) &sah[buf][srow][sk] = hi;
+        *(uint4 *) &sal[buf][srow][sk] = lo;
+        gf_split8(b, hi, lo);
+        *(uint4 *) &sbh[buf][srow][sk] = hi;
+        *(uint4 *) &sbl[buf][srow][sk] = lo;
+    };
+    gf_raw av[kGfDepth], bv[kGfDepth];
+#pragma unroll
+    for (int p = 0; p < kGfDepth; p++) {
+        gf_load_raw<false>(arow, (int64_t) p * kGfBK + sk, K, a_live, av[p]);
+        gf_load_raw<false>(brow, (int64_t) p * kGfBK + sk, K, b_live, bv[p]);
+    }
+    stage(av[0], bv[0], 0);
+    gf_load_raw<false>(arow, (int64_t) kGfDepth * kGfBK + sk, K, a_live, av[0]);
+    gf_load_raw<false>(brow, (int64_t) kGfDepth * kGfBK + sk, K, b_live, bv[0]);
+    __syncthreads();
+    const int wr = (wave & 1) * 32, wc = (wave >> 1) * 32;
+    gf_v4f acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = gf_v4f{0.f, 0.f, 0.f, 0.f};
+    for (int64_t s0 = 0; s0 < S; s0 += kGfDepth) {
+#pragma unroll
+        for (int p = 0; p < kGfDepth; p++) {
+            const int q = (p + 1) % kGfDepth;
+            gf_mfma_x3<PADE>(sah[p & 1], sal[p & 1], sbh[p & 1], sbl[p & 1], wr, wc, lane, acc);
+            stage(av[q], bv[q], (p + 1) & 1);
+            const int64_t kn = (s0 + p + 1 + kGfDepth) * kGfBK + sk;
+            gf_load_raw<false>(arow, kn, K, a_live, av[q]);
+            gf_load_raw<false>(brow, kn, K, b_live, bv[q]);
             __syncthreads();
         }
     }
@@ -474,11 +610,12 @@ size_t gemm_float_split_bytes(const tview & d, int splits) {
 }
 
 void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
-                       const gemm_float_epi & epi, int splits, float * part, const gemm_float_sub * subs, int nsub) {
+                       const gemm_float_epi & epi, int splits, float * part, const gemm_float_sub * subs, int nsub,
+                       bool x3) {
     if (batches_are_columns(d, a, b) && d.ne[2] * d.ne[3] > 1) {
         tview d2, b2;
         fold_batches(d, b, d2, b2);
-        launch_gemm_float(d2, a, atype, b2, btype, s, epi, splits, part, subs, nsub);
+        launch_gemm_float(d2, a, atype, b2, btype, s, epi, splits, part, subs, nsub, x3);
         return;
     }
     gemm_float_args g{};
@@ -531,7 +668,7 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
         splits = 1;
     } else if (nsub > 0) {
         // not joinable here: each product on its own
-        launch_gemm_float(d, a, atype, b, btype, s, epi, splits, part);
+        launch_gemm_float(d, a, atype, b, btype, s, epi, splits, part, nullptr, 0, x3);
         for (int i = 0; i < nsub; i++) {
             tview ai = a, di = d;
             ai.data = (char *) subs[i].a;
@@ -542,7 +679,7 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
             di.nb[2] = di.nb[3] = di.nb[1] * di.ne[1];
             gemm_float_epi ei;
             ei.bias = subs[i].bias;
-            launch_gemm_float(di, ai, atype, b, btype, s, ei);
+            launch_gemm_float(di, ai, atype, b, btype, s, ei, 1, nullptr, nullptr, 0, x3);
         }
         return;
     }
@@ -560,6 +697,7 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
         if (g.a_f16 && g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<true, true>), grid, dim3(kGfThreads), 0, s, g);
         else if (g.a_f16) hipLaunchKernelGGL((k_gemm_float_v<true, false>), grid, dim3(kGfThreads), 0, s, g);
         else if (g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<false, true>), grid, dim3(kGfThreads), 0, s, g);
+        else if (x3) hipLaunchKernelGGL(k_gemm_float_x3, grid, dim3(kGfThreads), 0, s, g);
         else hipLaunchKernelGGL((k_gemm_float_v<false, false>), grid, dim3(kGfThreads), 0, s, g);
         if (g.splits > 1) {
             const int64_t blocks = std::min<int64_t>((g.M * g.N + 255) / 256, 4096);

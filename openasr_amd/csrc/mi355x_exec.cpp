@@ -1129,9 +1129,11 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 const int splits = gemm_float_splits(dv, wv, atype, xv, btype, n_cu);
                 gen_need = std::max(gen_need, gemm_float_split_bytes(dv, splits));
                 backend_state * b = be;
+                const bool x3 = t->op_params[0] != GGML_PREC_F32 && atype == GGML_TYPE_F32 && btype == GGML_TYPE_F32;
                 add_step(
                     [=](hipStream_t s) {
-                        launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b));
+                        launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b), nullptr, 0,
+                                          x3);
                     },
                     produced, atype == GGML_TYPE_F16 ? "conv_gemm_f16" : "conv_gemm_f32", {produced});
                 return true;
@@ -1234,10 +1236,13 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         backend_state * b = be;
         std::vector<const ggml_tensor *> outs = {produced};
         outs.insert(outs.end(), sub_outs.begin(), sub_outs.end());
+        // F32 x F32 at the default precision (the graph's contract): the
+        // bf16 hi / lo form on the matrix cores (float tolerance)
+        const bool x3 = t->op_params[0] != GGML_PREC_F32 && atype == GGML_TYPE_F32 && btype == GGML_TYPE_F32;
         add_step(
             [=](hipStream_t s) {
                 launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b),
-                                  subs.empty() ? nullptr : subs.data(), (int) subs.size());
+                                  subs.empty() ? nullptr : subs.data(), (int) subs.size(), x3);
             },
             produced, atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32", outs);
         return true;

@@ -168,9 +168,13 @@ bool gemm_float_supported(const tview & d, const tview & a, int atype, const tvi
 // they need
 int gemm_float_splits(const tview & d, const tview & a, int atype, const tview & b, int btype, int n_cu);
 size_t gemm_float_split_bytes(const tview & d, int splits);
+// x3: an F32 x F32 product at the default precision (the graph's contract,
+// float tolerance) on the bf16 matrix cores -- each f32 operand element split
+// into bf16 hi + lo, three bf16 products a term (hi hi + hi lo + lo hi,
+// ~1e-5 relative) -- where the aligned form runs it; else f32 products
 void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
                        const gemm_float_epi & epi = gemm_float_epi(), int splits = 1, float * part = nullptr,
-                       const gemm_float_sub * subs = nullptr, int nsub = 0);
+                       const gemm_float_sub * subs = nullptr, int nsub = 0, bool x3 = false);
 // whether sibling products can join a launch of this product (aligned rows,
 // K % 8 == 0, one batch, M a multiple of 64)
 bool gemm_float_siblings_ok(const tview & d, const tview & a, const tview & b);
