@@ -394,6 +394,10 @@ __device__ __forceinline__ void gf_mfma_x3(const uint16_t (*sah)[kGfBK + PADE], 
         }
 }
 
+// ASPLIT: src0 already holds the hi / lo halves (im2col_args::split: each
+// 8-element group of a row as 8 bf16 hi then 8 lo, the bytes its 8 f32 would
+// take), staged as loaded
+template <bool ASPLIT>
 __global__ __launch_bounds__(kGfThreads) void k_gemm_float_x3(gemm_float_args g) {
     constexpr int PADE = 8;
     __shared__ __align__(16) uint16_t sah[2][kGfBM][kGfBK + PADE], sal[2][kGfBM][kGfBK + PADE];
@@ -437,7 +441,12 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float_x3(gemm_float_args g)
     const int64_t S = ((K + kGfBK - 1) / kGfBK + kGfDepth - 1) / kGfDepth * kGfDepth;
     auto stage = [&](const gf_raw & a, const gf_raw & b, int buf) {
         uint4 hi, lo;
-        gf_split8(a, hi, lo);
+        if constexpr (ASPLIT) {
+            hi = a.ok ? a.r[0] : make_uint4(0, 0, 0, 0);
+            lo = a.ok ? a.r[1] : make_uint4(0, 0, 0, 0);
+        } else {
+            gf_split8(a, hi, lo);
+        }
         *(uint4 *) &sah[buf][srow][sk] = hi;
         *(uint4 *) &sal[buf][srow][sk] = lo;
         gf_split8(b, hi, lo);
@@ -609,13 +618,22 @@ size_t gemm_float_split_bytes(const tview & d, int splits) {
     return splits > 1 ? (size_t) splits * d.ne[0] * d.ne[1] * d.ne[2] * d.ne[3] * sizeof(float) : 0;
 }
 
+bool gemm_float_x3_aligned(const tview & a, const tview & b) {
+    return row_aligned(a) && row_aligned(b) && a.ne[0] % 8 == 0;
+}
+
 void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
                        const gemm_float_epi & epi, int splits, float * part, const gemm_float_sub * subs, int nsub,
-                       bool x3) {
+                       bool x3, bool a_split) {
+    if (a_split && (!x3 || atype != GGML_TYPE_F32 || btype != GGML_TYPE_F32 || nsub > 0 ||
+                    !gemm_float_x3_aligned(a, b))) {
+        note_hip_error(hipErrorInvalidValue);  // only the aligned bf16 form reads the split layout
+        return;
+    }
     if (batches_are_columns(d, a, b) && d.ne[2] * d.ne[3] > 1) {
         tview d2, b2;
         fold_batches(d, b, d2, b2);
-        launch_gemm_float(d2, a, atype, b2, btype, s, epi, splits, part, subs, nsub, x3);
+        launch_gemm_float(d2, a, atype, b2, btype, s, epi, splits, part, subs, nsub, x3, a_split);
         return;
     }
     gemm_float_args g{};
@@ -697,7 +715,8 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
         if (g.a_f16 && g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<true, true>), grid, dim3(kGfThreads), 0, s, g);
         else if (g.a_f16) hipLaunchKernelGGL((k_gemm_float_v<true, false>), grid, dim3(kGfThreads), 0, s, g);
         else if (g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<false, true>), grid, dim3(kGfThreads), 0, s, g);
-        else if (x3) hipLaunchKernelGGL(k_gemm_float_x3, grid, dim3(kGfThreads), 0, s, g);
+        else if (x3 && a_split) hipLaunchKernelGGL(k_gemm_float_x3<true>, grid, dim3(kGfThreads), 0, s, g);
+        else if (x3) hipLaunchKernelGGL(k_gemm_float_x3<false>, grid, dim3(kGfThreads), 0, s, g);
         else hipLaunchKernelGGL((k_gemm_float_v<false, false>), grid, dim3(kGfThreads), 0, s, g);
         if (g.splits > 1) {
             const int64_t blocks = std::min<int64_t>((g.M * g.N + 255) / 256, 4096);

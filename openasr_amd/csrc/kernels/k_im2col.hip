@@ -14,6 +14,7 @@
 // bit-identical to ggml-cpu.
 
 #include <algorithm>
+#include <type_traits>
 
 #include "../mi355x_common.h"
 #include "../ops.h"
@@ -62,6 +63,41 @@ __device__ __forceinline__ void im2col_store(_Float16 * p, const float (&v)[4]) 
     *(uint2 *) p = make_uint2(lo, hi);
 }
 
+// the split layout (im2col_args::split): flat element f of the column matrix
+// (K % 8 == 0, so a row starts a group) goes to bf16 hi at byte 32 (f / 8) +
+// 2 (f % 8) and lo 16 bytes further; V = 4 values start on a 4-element boundary
+template <int V>
+__device__ __forceinline__ void im2col_split_store(float * dst, int64_t f, const float (&v)[V]) {
+    uint16_t h[V], l[V];
+#pragma unroll
+    for (int e = 0; e < V; e++) {
+        const __bf16 xh = (__bf16) v[e];
+        h[e] = __builtin_bit_cast(uint16_t, xh);
+        l[e] = __builtin_bit_cast(uint16_t, (__bf16) (v[e] - (float) xh));
+    }
+    char * p = (char *) dst + (f >> 3) * 32 + (f & 7) * 2;
+    if constexpr (V == 4) {
+        *(uint2 *) p = make_uint2(h[0] | ((uint32_t) h[1] << 16), h[2] | ((uint32_t) h[3] << 16));
+        *(uint2 *) (p + 16) = make_uint2(l[0] | ((uint32_t) l[1] << 16), l[2] | ((uint32_t) l[3] << 16));
+    } else {
+#pragma unroll
+        for (int e = 0; e < V; e++) {
+            ((uint16_t *) p)[e] = h[e];
+            ((uint16_t *) (p + 16))[e] = l[e];
+        }
+    }
+}
+template <typename DT, int V>
+__device__ __forceinline__ void im2col_put(DT * dst, int64_t f, const float (&v)[V], bool split) {
+    if constexpr (std::is_same<DT, float>::value) {
+        if (split) {
+            im2col_split_store<V>(dst, f, v);
+            return;
+        }
+    }
+    im2col_store(dst + f, v);
+}
+
 // total < 2^31 and K % V == 0: lane t writes elements V t .. V t + V - 1
 template <typename DT, int V>
 __global__ __launch_bounds__(256) void k_im2col_v(DT * __restrict__ dst, const char * __restrict__ src, im2col_args a,
@@ -99,7 +135,7 @@ __global__ __launch_bounds__(256) void k_im2col_v(DT * __restrict__ dst, const c
         float v[V];
 #pragma unroll
         for (int e = 0; e < V; e++) v[e] = in[e] ? raw[e] : 0.0f;
-        im2col_store(dst + i, v);
+        im2col_put<DT, V>(dst, i, v, a.split);
     }
 }
 
@@ -134,7 +170,7 @@ __global__ __launch_bounds__(256) void k_im2col_line(DT * __restrict__ dst, cons
     __syncthreads();
     const uint32_t run = (uint32_t) cbn * L.taps.d;
     const uint32_t total = (uint32_t) a.OW * run;
-    DT * out = dst + line * a.OW * a.K + (int64_t) c0 * L.taps.d;
+    const int64_t out0 = line * a.OW * a.K + (int64_t) c0 * L.taps.d;  // flat index of the line's first element
     for (uint32_t i = threadIdx.x * V; i < total; i += 256 * V) {
         // run == the full block's run except in the last block: divide by it
         const uint32_t ow = run == L.run.d ? div_by(i, L.run) : i / run;
@@ -159,7 +195,7 @@ __global__ __launch_bounds__(256) void k_im2col_line(DT * __restrict__ dst, cons
                 }
             }
         }
-        im2col_store(out + (int64_t) ow * a.K + j, v);
+        im2col_put<DT, V>(dst, out0 + (int64_t) ow * a.K + j, v, a.split);
     }
 }
 
@@ -180,10 +216,10 @@ __global__ __launch_bounds__(256) void k_im2col(DT * __restrict__ dst, const cha
         const int64_t ic = t / a.KH;
         const int64_t iw = ow * a.s0 + (int64_t) kw * a.d0 - a.p0;
         const int64_t ih = oh * a.s1 + (int64_t) kh * a.d1 - a.p1;
-        float v = 0.0f;
+        float v[1] = {0.0f};
         if (iw >= 0 && iw < a.IW && ih >= 0 && ih < a.IH)
-            v = *(const float *) (src + n * a.nb_n + ic * a.nb_c + ih * a.nb_h + iw * 4);
-        dst[i] = (DT) v;
+            v[0] = *(const float *) (src + n * a.nb_n + ic * a.nb_c + ih * a.nb_h + iw * 4);
+        im2col_put<DT, 1>(dst, i, v, a.split);
     }
 }
 
@@ -232,6 +268,10 @@ void im2col_launch(DT * dst, const char * src, const im2col_args & a, hipStream_
 
 void launch_im2col(void * dst, int dst_f16, const char * src, const im2col_args & a, hipStream_t s) {
     if (a.total <= 0) return;
+    if (a.split && (dst_f16 || a.K % 8 != 0 || (uintptr_t) dst % 16 != 0)) {
+        note_hip_error(hipErrorInvalidValue);
+        return;
+    }
     if (dst_f16) im2col_launch((_Float16 *) dst, src, a, s);
     else im2col_launch((float *) dst, src, a, s);
 }

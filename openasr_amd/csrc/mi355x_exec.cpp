@@ -253,6 +253,9 @@ struct planner {
     };
     std::unordered_map<const ggml_tensor *, naive_job> naive_jobs;  // by output CONT
     std::unordered_set<const ggml_tensor *> naive_nodes;            // S, P, VT, C of the jobs
+    // IM2COL results written in the bf16 hi / lo layout for their column
+    // GEMM (im2col_args::split), which reads them as such
+    std::unordered_set<const ggml_tensor *> split_cols;
     void find_naive();
     void find_gqa_skip();
     bool plan_naive(int i, const ggml_tensor * t);
@@ -1057,6 +1060,9 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
     const tview wv = make_view(w);
     const int atype = w->type, btype = x->type;
     act_src = nullptr;
+    // src0 an IM2COL result in the split layout (planned with it, see the
+    // IM2COL case): only the bf16 form of this launch reads it
+    const bool a_split = split_cols.count(root_of(w)) > 0;
     if (gemm_float_supported(dv, wv, atype, xv, btype)) {
         // the linear layers' bias ADD (a row of the output's width) and a
         // residual ADD of the output's shape fold into the epilogue, with
@@ -1133,7 +1139,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
                 add_step(
                     [=](hipStream_t s) {
                         launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b), nullptr, 0,
-                                          x3);
+                                          x3, a_split);
                     },
                     produced, atype == GGML_TYPE_F16 ? "conv_gemm_f16" : "conv_gemm_f32", {produced});
                 return true;
@@ -1179,7 +1185,7 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         // row ranges; each is taken only if the launch with it passes hoist_ok
         std::vector<gemm_float_sub> subs;
         std::vector<const ggml_tensor *> sub_outs;
-        if (!epi.res && !epi.gelu_erf && gemm_float_siblings_ok(dv, wv, xv) && is_contiguous(t)) {
+        if (!a_split && !epi.res && !epi.gelu_erf && gemm_float_siblings_ok(dv, wv, xv) && is_contiguous(t)) {
             for (int j = i + 1; j < cg->n_nodes && j <= i + 16 && (int) subs.size() < kGemmFloatMaxSubs; j++) {
                 const ggml_tensor * u = cg->nodes[j];
                 if (is_view_op(u->op) || deferred.count(u)) continue;
@@ -1242,11 +1248,12 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
         add_step(
             [=](hipStream_t s) {
                 launch_gemm_float(ov, wv, atype, xv, btype, s, epi, splits, (float *) gen_base(b),
-                                  subs.empty() ? nullptr : subs.data(), (int) subs.size(), x3);
+                                  subs.empty() ? nullptr : subs.data(), (int) subs.size(), x3, a_split);
             },
             produced, atype == GGML_TYPE_F16 ? "mul_mat_f16" : "mul_mat_f32", outs);
         return true;
     }
+    if (a_split) return fail(t, "split column matrix outside its bf16 GEMM");
     if (btype != GGML_TYPE_F32) return fail(t, "f16 columns outside the matrix-core GEMM");
     add_step([=](hipStream_t s) { launch_mul_mat_float(dv, wv, atype, xv, s); }, t, "mul_mat_float");
     return true;
@@ -2034,6 +2041,22 @@ bool planner::plan() {
                 void * d = t->data;
                 const int f16 = t->type == GGML_TYPE_F16;
                 const char * src = bv.data;
+                // read only (through its RESHAPE) as src0 of an F32 x F32
+                // column GEMM at the default precision that runs in the
+                // aligned bf16 form: written as that form's hi / lo operand
+                const ggml_tensor * rs = sole_consumer(t, i + 1);
+                const ggml_tensor * mm = rs && rs->op == GGML_OP_RESHAPE && rs->view_src == t ? sole_consumer(rs, i + 1)
+                                                                                               : nullptr;
+                if (!f16 && t->ne[0] % 8 == 0 && (uintptr_t) d % 16 == 0 && mm && mm->op == GGML_OP_MUL_MAT &&
+                    mm->src[0] == rs && mm->src[1] != rs && mm->op_params[0] != GGML_PREC_F32 &&
+                    mm->src[1]->type == GGML_TYPE_F32 && mm->type == GGML_TYPE_F32 && supports_op(be->dev, mm)) {
+                    const tview rv = make_view(rs), xv2 = make_view(mm->src[1]), mv = make_view(mm);
+                    if (gemm_float_supported(mv, rv, GGML_TYPE_F32, xv2, GGML_TYPE_F32) &&
+                        gemm_float_x3_aligned(rv, xv2)) {
+                        a.split = 1;
+                        split_cols.insert(t);
+                    }
+                }
                 add_step([=](hipStream_t s) { launch_im2col(d, f16, src, a, s); }, t, "im2col");
                 break;
             }

@@ -171,10 +171,16 @@ size_t gemm_float_split_bytes(const tview & d, int splits);
 // x3: an F32 x F32 product at the default precision (the graph's contract,
 // float tolerance) on the bf16 matrix cores -- each f32 operand element split
 // into bf16 hi + lo, three bf16 products a term (hi hi + hi lo + lo hi,
-// ~1e-5 relative) -- where the aligned form runs it; else f32 products
+// ~1e-5 relative) -- where the aligned form runs it; else f32 products.
+// a_split: src0 holds the split layout IM2COL writes (im2col_args::split);
+// only the aligned x3 form reads it, any other launch fails
 void launch_gemm_float(const tview & d, const tview & a, int atype, const tview & b, int btype, hipStream_t s,
                        const gemm_float_epi & epi = gemm_float_epi(), int splits = 1, float * part = nullptr,
-                       const gemm_float_sub * subs = nullptr, int nsub = 0, bool x3 = false);
+                       const gemm_float_sub * subs = nullptr, int nsub = 0, bool x3 = false,
+                       bool a_split = false);
+// whether launch_gemm_float runs this F32 x F32 product in the aligned bf16
+// form (x3), the one that reads an a_split operand
+bool gemm_float_x3_aligned(const tview & a, const tview & b);
 // whether sibling products can join a launch of this product (aligned rows,
 // K % 8 == 0, one batch, M a multiple of 64)
 bool gemm_float_siblings_ok(const tview & d, const tview & a, const tview & b);
@@ -357,6 +363,11 @@ void launch_argmax(const tview & a, int32_t * out, int first, void * scratch, hi
 struct im2col_args {
     int64_t total, K, OW, OH, IW, IH, nb_n, nb_c, nb_h;
     int KW, KH, s0, s1, p0, p1, d0, d1;
+    // f32 dst only, K % 8 == 0: each 8-element group of a row written as its
+    // 8 bf16 hi halves then 8 lo halves (x = hi + lo + ~2^-17 x; 32 bytes, the
+    // group's f32 size) -- the operand layout of the column GEMM's bf16 form
+    // (launch_gemm_float, a_split), its only reader
+    int split;
 };
 void launch_im2col(void * dst, int dst_f16, const char * src, const im2col_args & a, hipStream_t s);
 bool norm_supported(int64_t ne0);
