@@ -404,8 +404,13 @@ __global__ __launch_bounds__(kGfThreads) void k_gemm_float_x3(gemm_float_args g)
     __shared__ __align__(16) uint16_t sbh[2][kGfBN][kGfBK + PADE], sbl[2][kGfBN][kGfBK + PADE];
     const int tid = (int) threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    int64_t m0 = (int64_t) blockIdx.x * kGfBM;
-    const int64_t n0 = (int64_t) blockIdx.y * kGfBN;
+    // the tile: contiguous runs of tiles a XCD, a row tile's column tiles
+    // adjacent (dispatched together, so the row tile's columns are fetched
+    // into one L2)
+    const int64_t t = (int64_t) (blockIdx.x % 8) * g.per_xcd + blockIdx.x / 8;
+    if (t >= g.tiles) return;  // the grid's padding, before any barrier
+    int64_t m0 = t / g.col_blocks * kGfBM;
+    const int64_t n0 = t % g.col_blocks * kGfBN;
     static_assert(kGemmFloatMaxSubs == 2, "product selection below");
     if (g.nsub > 0) {
         int64_t base = 0, mend = g.sub_m0[1];
@@ -715,8 +720,15 @@ void launch_gemm_float(const tview & d, const tview & a, int atype, const tview 
         if (g.a_f16 && g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<true, true>), grid, dim3(kGfThreads), 0, s, g);
         else if (g.a_f16) hipLaunchKernelGGL((k_gemm_float_v<true, false>), grid, dim3(kGfThreads), 0, s, g);
         else if (g.b_f16) hipLaunchKernelGGL((k_gemm_float_v<false, true>), grid, dim3(kGfThreads), 0, s, g);
-        else if (x3 && a_split) hipLaunchKernelGGL(k_gemm_float_x3<true>, grid, dim3(kGfThreads), 0, s, g);
-        else if (x3) hipLaunchKernelGGL(k_gemm_float_x3<false>, grid, dim3(kGfThreads), 0, s, g);
+        else if (x3) {
+            // one dim of tiles, dealt to the XCDs in contiguous runs
+            g.tiles = (int64_t) grid.x * grid.y;
+            g.col_blocks = grid.y;
+            g.per_xcd = (g.tiles + 7) / 8;
+            const dim3 g1((unsigned) (g.per_xcd * 8), 1u, grid.z);
+            if (a_split) hipLaunchKernelGGL(k_gemm_float_x3<true>, g1, dim3(kGfThreads), 0, s, g);
+            else hipLaunchKernelGGL(k_gemm_float_x3<false>, g1, dim3(kGfThreads), 0, s, g);
+        }
         else hipLaunchKernelGGL((k_gemm_float_v<false, false>), grid, dim3(kGfThreads), 0, s, g);
         if (g.splits > 1) {
             const int64_t blocks = std::min<int64_t>((g.M * g.N + 255) / 256, 4096);

@@ -137,6 +137,10 @@ struct gemm_float_args {
     int64_t M, N, K;
     int ne2, ne3, r2, r3;
     int a_f16, b_f16, a_vec, b_vec;
+    // the bf16 form's tile order: workgroup i (of the x dim) on XCD i % 8
+    // takes tile (i % 8) per_xcd + i / 8 (none from tiles on), tile t = row
+    // tile t / col_blocks, column tile t % col_blocks
+    int64_t tiles, col_blocks, per_xcd;
     // split K: workgroup z = s sums k in [s k_span, (s + 1) k_span) into
     // part + s M N (column-major M x N f32), a second launch adds the splits
     // in order and applies the epilogue
