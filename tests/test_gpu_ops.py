@@ -412,8 +412,12 @@ FLOAT_MM_CASES = [
 ]
 
 
-@pytest.mark.parametrize("prec", ["default", "f32"])
-@pytest.mark.parametrize("wt,xt,m,k,n,wb,xb", FLOAT_MM_CASES)
+# every case at the default precision; the F32 x F32 ones under GGML_PREC_F32 too
+FLOAT_MM_PREC_CASES = [c + ("default",) for c in FLOAT_MM_CASES] + \
+    [c + ("f32",) for c in FLOAT_MM_CASES if c[:2] == ("f32", "f32")]
+
+
+@pytest.mark.parametrize("wt,xt,m,k,n,wb,xb,prec", FLOAT_MM_PREC_CASES)
 def test_mul_mat_float_matrix_cores(ggml, gpu, wt, xt, m, k, n, wb, xb, prec):
     """float MUL_MAT on the matrix-core GEMM against an f64 product of the
     same operands, the columns rounded to f16 for f16 weights (ggml-cpu's
@@ -421,8 +425,6 @@ def test_mul_mat_float_matrix_cores(ggml, gpu, wt, xt, m, k, n, wb, xb, prec):
     the largest output (the op tolerance is 2e-3). An F32 x F32 product at
     the default precision runs as three bf16 products of hi / lo operand
     halves (~1e-5); under GGML_PREC_F32 on f32 products"""
-    if prec == "f32" and (wt, xt) != ("f32", "f32"):
-        pytest.skip("the precision contract changes only F32 x F32 products")
     print(f"float mul_mat {wt} x {xt} M={m} K={k} N={n} wb={wb} xb={xb} prec={prec}", flush=True)
     wdt = np.float16 if wt == "f16" else np.float32
     xdt = np.float16 if xt == "f16" else np.float32
