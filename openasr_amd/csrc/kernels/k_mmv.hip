@@ -146,6 +146,76 @@ __global__ __launch_bounds__(256) void k_mmv_q4_K(const char * __restrict__ W, i
     }
 }
 
+// Q3_K weights (ggml layout, 110-byte super-blocks: hmask[32], qs[64],
+// scales[12], f16 d; rows only 2-byte aligned). A chunk is one 32-weight
+// group g = 4h + j of a super-block: weights 128h + 32j + l (l < 32) with
+// quants ((qs[32h + l] >> 2j) & 3) - 4, the 4 dropped where bit 4h + j of
+// hmask[l] is set, scaled by 6-bit scales 8h + 2j (l < 16) and 8h + 2j + 1,
+// each stored plus 32. Used by ggml-cpu's MUL_MAT for the host's q3_k pack
+// policy (models/pack_quant.rs:205-207).
+__device__ __forceinline__ uint32_t ld32_a2(const char * p) {
+    const uint16_t * h = (const uint16_t *) p;
+    return (uint32_t) h[0] | ((uint32_t) h[1] << 16);
+}
+__device__ __forceinline__ int q3_K_scale(const uint8_t * sc, int i) {
+    const int lo = (sc[i % 8] >> (4 * (i / 8))) & 0xF;
+    const int hi = (sc[8 + i % 4] >> (2 * (i / 4))) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+template <int NC>
+__global__ __launch_bounds__(256) void k_mmv_q3_K(const char * __restrict__ W, int64_t row_bytes, int64_t M,
+                                                  int64_t K, const int8_t * __restrict__ aq,
+                                                  const float * __restrict__ ad, char * __restrict__ dst,
+                                                  int64_t dst_nb1, int lpr_log2, int cpl) {
+    const int lane = threadIdx.x & 63;
+    const int LPR = 1 << lpr_log2;
+    const int li = lane & (LPR - 1);
+    const int teams_per_wave = 64 >> lpr_log2;
+    const int64_t team = ((int64_t) blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6)) * teams_per_wave +
+                         (lane >> lpr_log2);
+    const int64_t team_stride = (int64_t) gridDim.x * (blockDim.x >> 6) * teams_per_wave;
+    const int64_t nsb = K / 256;
+    for (int64_t row = team; row < M; row += team_stride) {
+        const char * wr = W + row * row_bytes;
+        double acc[NC];
+#pragma unroll
+        for (int n = 0; n < NC; n++) acc[n] = 0.0;
+        for (int c = 0; c < cpl; c++) {
+            const int ci = li + c * LPR;
+            const int sb = ci >> 3, g = ci & 7, h = g >> 2, j = g & 3;
+            const char * blk = wr + (int64_t) sb * 110;
+            // the 32 signed quants as eight words of four int8: two low bits
+            // plus 0xFC (-4) in bytes whose hmask bit is clear (at most
+            // 3 + 0xFC, no carry between bytes)
+            int q[8];
+#pragma unroll
+            for (int w = 0; w < 8; w++) {
+                const uint32_t lo = (ld32_a2(blk + 32 + 32 * h + 4 * w) >> (2 * j)) & 0x03030303u;
+                const uint32_t hb = (ld32_a2(blk + 4 * w) >> (4 * h + j)) & 0x01010101u;
+                q[w] = (int) (lo + (hb ^ 0x01010101u) * 0xFCu);
+            }
+            const int s0 = q3_K_scale((const uint8_t *) (blk + 96), 8 * h + 2 * j);
+            const int s1 = q3_K_scale((const uint8_t *) (blk + 96), 8 * h + 2 * j + 1);
+            const float dw = half_bits_to_float(*(const uint16_t *) (blk + 108));
+            const int64_t e0 = (int64_t) sb * 256 + 128 * h + 32 * j;
+#pragma unroll
+            for (int n = 0; n < NC; n++) {
+                const int8_t * acol = aq + n * K + e0;
+                const int isum = dot16(make_int4(q[0], q[1], q[2], q[3]), *(const int4 *) acol) * s0 +
+                                 dot16(make_int4(q[4], q[5], q[6], q[7]), *(const int4 *) (acol + 16)) * s1;
+                acc[n] += ((double) dw * (double) ad[n * nsb + sb]) * (double) isum;
+            }
+        }
+#pragma unroll
+        for (int n = 0; n < NC; n++) {
+            double v = acc[n];
+            for (int off = LPR / 2; off > 0; off >>= 1) v += __shfl_xor(v, off);
+            if (li == 0) *(float *) (dst + n * dst_nb1 + row * 4) = (float) v;
+        }
+    }
+}
+
 // Split the row's chunks over a power-of-two team so each lane owns a whole
 // number of chunks: chunks = LPR * CPL with LPR = min(64, largest power of
 // two dividing chunks).
@@ -159,7 +229,7 @@ static void pick_team(int64_t chunks, int & lpr_log2, int & cpl) {
 template <int NC>
 static void mmv_dispatch(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K,
                          const act_buffers & act, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu) {
-    const int64_t chunks = wtype == GGML_TYPE_Q8_0 ? K / 16 : K / 64;
+    const int64_t chunks = wtype == GGML_TYPE_Q8_0 ? K / 16 : wtype == GGML_TYPE_Q3_K ? K / 32 : K / 64;
     int lpr_log2, cpl;
     pick_team(chunks, lpr_log2, cpl);
     const int64_t teams = M;
@@ -169,6 +239,9 @@ static void mmv_dispatch(int wtype, const char * W, int64_t row_bytes, int64_t M
     if (blocks > cap) blocks = cap;
     if (wtype == GGML_TYPE_Q8_0) {
         hipLaunchKernelGGL(k_mmv_q8_0<NC>, dim3((unsigned) blocks), dim3(256), 0, stream, W, row_bytes, M, K, act.q,
+                           act.d, dst, dst_nb1, lpr_log2, cpl);
+    } else if (wtype == GGML_TYPE_Q3_K) {
+        hipLaunchKernelGGL(k_mmv_q3_K<NC>, dim3((unsigned) blocks), dim3(256), 0, stream, W, row_bytes, M, K, act.q,
                            act.d, dst, dst_nb1, lpr_log2, cpl);
     } else {
         hipLaunchKernelGGL(k_mmv_q4_K<NC>, dim3((unsigned) blocks), dim3(256), 0, stream, W, row_bytes, M, K, act.q,

@@ -70,6 +70,7 @@ bool is_contiguous(const ggml_tensor * t) {
         case GGML_TYPE_I32: expect = 4; break;
         case GGML_TYPE_Q8_0: expect = 34; blck = 32; break;
         case GGML_TYPE_Q4_K: expect = 144; blck = 256; break;
+        case GGML_TYPE_Q3_K: expect = 110; blck = 256; break;
         default: return false;
     }
     if (t->ne[0] % blck) return false;
@@ -707,6 +708,43 @@ bool planner::plan_mul_mat(int i, const ggml_tensor * t) {
     const ggml_tensor * w = t->src[0];
     const ggml_tensor * x = t->src[1];
     const tview xv = make_view(x);
+    if (w->type == GGML_TYPE_Q3_K) {
+        // Q3_K weights (the host's q3_k pack policy, pack_quant.rs:205-207):
+        // the columns quantized to Q8_K as for Q4_K, then the row-team GEMV
+        // (eight columns a launch), exact block sums; no folds
+        const int64_t K = w->ne[0], M = w->ne[1];
+        const int64_t N = x->ne[1] * x->ne[2] * x->ne[3];
+        const char * W = (const char *) w->data;
+        const int64_t row_bytes = (int64_t) w->nb[1];
+        act_need = std::max(act_need, act_bytes(GGML_TYPE_Q3_K, K, N));
+        const bool reuse = act_src == x && act_wtype == GGML_TYPE_Q3_K;
+        if (!reuse && reads_unwritten(t, x)) return false;
+        hoist h;
+        h.reads.push_back(span_of(w));
+        h.writes.push_back(span_of(t));
+        if (!hoist_ok(i, h)) return fail(t, "MUL_MAT output overlaps its own input");
+        act_src = x;
+        act_wtype = GGML_TYPE_Q3_K;
+        backend_state * b = be;
+        const int ncu = n_cu;
+        char * dst = (char *) t->data;
+        const int64_t dst_nb1 = (int64_t) t->nb[1];
+        if (!reuse) {
+            add_step(
+                [=](hipStream_t s) {
+                    act_buffers act = act_carve(GGML_TYPE_Q3_K, act_base(b), K, N);
+                    launch_quantize_act(xv, GGML_TYPE_Q3_K, act, s);
+                },
+                t, "quantize_q8_K", {nullptr});
+        }
+        add_step(
+            [=](hipStream_t s) {
+                act_buffers act = act_carve(GGML_TYPE_Q3_K, act_base(b), K, N);
+                launch_mmv(GGML_TYPE_Q3_K, W, row_bytes, M, K, act, N, dst, dst_nb1, s, ncu);
+            },
+            t, "mul_mat_q3_K");
+        return true;
+    }
     if (w->type == GGML_TYPE_Q8_0 || w->type == GGML_TYPE_Q4_K) {
         const int wtype = w->type;
         const int64_t K = w->ne[0], M = w->ne[1];
@@ -2483,6 +2521,9 @@ bool supports_op(const device_state * dev, const ggml_tensor * t) {
                 return w->ne[2] == 1 && w->ne[3] == 1 && is_contiguous(w) && columns_foldable(x) &&
                        (w->type != GGML_TYPE_Q4_K || w->ne[0] % 256 == 0) && w->ne[0] % 32 == 0;
             }
+            if (w->type == GGML_TYPE_Q3_K)
+                return w->ne[2] == 1 && w->ne[3] == 1 && is_contiguous(w) && columns_foldable(x) &&
+                       w->ne[0] % 256 == 0;
             return w->type == GGML_TYPE_F16 || w->type == GGML_TYPE_F32;
         }
         case GGML_OP_GET_ROWS: {

@@ -18,7 +18,7 @@ void launch_quantize_act(const tview & src, int wtype, const act_buffers & out, 
 size_t act_bytes(int wtype, int64_t K, int64_t ncols);
 act_buffers act_carve(int wtype, char * base, int64_t K, int64_t ncols);
 
-// GEMV on Q8_0 (row-split) / Q4_K weights for N columns, dst column stride dst_nb1 bytes
+// GEMV on Q8_0 (row-split) / Q4_K / Q3_K weights for N columns, dst column stride dst_nb1 bytes
 void launch_mmv(int wtype, const char * W, int64_t row_bytes, int64_t M, int64_t K, const act_buffers & act,
                 int64_t N, char * dst, int64_t dst_nb1, hipStream_t stream, int n_cu);
 

@@ -26,8 +26,8 @@ GGML_MAX_DIMS = 4
 GGML_MAX_SRC = 10
 
 # element types (ffi.rs:343-351)
-F32, F16, Q4_0, Q8_0, Q4_K, Q8_K, I32, I64 = 0, 1, 2, 8, 12, 15, 26, 27
-TYPE_NAMES = {F32: "f32", F16: "f16", Q8_0: "q8_0", Q4_K: "q4_K", I32: "i32"}
+F32, F16, Q4_0, Q8_0, Q3_K, Q4_K, Q8_K, I32, I64 = 0, 1, 2, 8, 11, 12, 15, 26, 27
+TYPE_NAMES = {F32: "f32", F16: "f16", Q8_0: "q8_0", Q3_K: "q3_K", Q4_K: "q4_K", I32: "i32"}
 
 GGML_ROPE_TYPE_NEOX = 2
 GGML_PREC_DEFAULT, GGML_PREC_F32 = 0, 10

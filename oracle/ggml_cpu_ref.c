@@ -473,6 +473,61 @@ float ref_vec_dot_q4_K_q8_K(int64_t n, const ref_block_q4_K * x, const ref_block
     return (float) sum;
 }
 
+/* ---------------------------------------------------------------- Q3_K -- */
+/* The Q3_K weight format, written by the host's pack writer for decoder
+ * matrices under the q3_k pack policy (models/pack_quant.rs:205-207, through
+ * ggml_quantize_chunk, ggml_runtime/gguf_write.rs:579-588) and multiplied by
+ * ggml-cpu's MUL_MAT against Q8_K activations. ggml-base's published layout
+ * (block_q3_K, dequantize_row_q3_K, vec_dot_q3_K_q8_K of the fork's pinned
+ * revision 0db3a287): weight e = 128h + 32j + l of a super-block (h < 2,
+ * j < 4, l < 32) is d * (scale[8h + 2j + l/16] - 32) * q with
+ * q = ((qs[32h + l] >> 2j) & 3) - (hmask[l] bit 4h + j ? 0 : 4). */
+
+/* 6-bit scale i of 16: the low four bits are nibble i/8 of byte i%8, the
+ * high two bits are bits 2(i/4)..+1 of byte 8 + i%4 */
+int ref_q3_K_scale(const uint8_t * scales, int i) {
+    const int lo = (scales[i % 8] >> (4 * (i / 8))) & 0xF;
+    const int hi = (scales[8 + i % 4] >> (2 * (i / 4))) & 3;
+    return (lo | (hi << 4)) - 32;
+}
+
+static inline int q3_K_quant(const ref_block_q3_K * b, int e) {
+    const int h = e / 128, j = (e % 128) / 32, l = e % 32;
+    const int q = (b->qs[32 * h + l] >> (2 * j)) & 3;
+    return q - ((b->hmask[l] >> (4 * h + j)) & 1 ? 0 : 4);
+}
+
+void ref_dequantize_row_q3_K(const ref_block_q3_K * x, float * y, int64_t k) {
+    const int64_t nb = k / REF_QK_K;
+    for (int64_t i = 0; i < nb; i++) {
+        const float d = ref_fp16_to_fp32(x[i].d);
+        for (int e = 0; e < REF_QK_K; e++) {
+            const float dl = d * (float) ref_q3_K_scale(x[i].scales, e / 16);
+            y[i * REF_QK_K + e] = dl * (float) q3_K_quant(&x[i], e);
+        }
+    }
+}
+
+/* vec_dot_q3_K_q8_K: per super-block isum = sum over the sixteen 16-weight
+ * groups of (scale - 32) * <q, q8>, an exact integer; the term
+ * d_x * d_y * isum is exact in f64 and the terms are summed in f64, rounding
+ * to f32 once (ggml-cpu sums them in ISA-dependent f32 lanes; the wide sum
+ * makes the value independent of the order, as for Q4_K) */
+float ref_vec_dot_q3_K_q8_K(int64_t n, const ref_block_q3_K * x, const ref_block_q8_K * y) {
+    const int64_t nb = n / REF_QK_K;
+    double sum = 0.0;
+    for (int64_t i = 0; i < nb; i++) {
+        int64_t isum = 0;
+        for (int g = 0; g < 16; g++) {
+            int s = 0;
+            for (int l = 0; l < 16; l++) s += q3_K_quant(&x[i], 16 * g + l) * (int) y[i].qs[16 * g + l];
+            isum += (int64_t) ref_q3_K_scale(x[i].scales, g) * s;
+        }
+        sum += (double) ref_fp16_to_fp32(x[i].d) * (double) y[i].d * (double) isum;
+    }
+    return (float) sum;
+}
+
 /* ggml_vec_dot_f16: products of two halves are exact in f32; summed wide */
 float ref_vec_dot_f16(int64_t n, const uint16_t * x, const uint16_t * y) {
     double s = 0.0;
@@ -486,6 +541,7 @@ size_t ref_row_size(int type, int64_t ne0) {
         case REF_F16: return (size_t) ne0 * 2;
         case REF_Q8_0: return (size_t) (ne0 / REF_QK8_0) * sizeof(ref_block_q8_0);
         case REF_Q4_K: return (size_t) (ne0 / REF_QK_K) * sizeof(ref_block_q4_K);
+        case REF_Q3_K: return (size_t) (ne0 / REF_QK_K) * sizeof(ref_block_q3_K);
         case REF_Q8_K: return (size_t) (ne0 / REF_QK_K) * sizeof(ref_block_q8_K);
         default: return 0;
     }
@@ -504,7 +560,9 @@ void ref_mul_mat(int wtype, const void * w, size_t row_bytes, int64_t m, int64_t
     /* every column is converted to the weight's vec_dot type once, then each
      * weight row is streamed once against all columns (ggml-cpu's "convert
      * src1 first" rule; the loop order only changes speed, not results) */
-    const int vtype = wtype == REF_Q8_0 ? REF_Q8_0 : (wtype == REF_Q4_K ? REF_Q8_K : (wtype == REF_F16 ? REF_F16 : REF_F32));
+    const int vtype = wtype == REF_Q8_0 ? REF_Q8_0
+                      : (wtype == REF_Q4_K || wtype == REF_Q3_K) ? REF_Q8_K
+                      : (wtype == REF_F16 ? REF_F16 : REF_F32);
     const size_t qrow = vtype == REF_F32 ? (size_t) k * 4 : ref_row_size(vtype, k);
     char * xq = (char *) malloc(qrow * (size_t) (n > 0 ? n : 1));
 #pragma omp parallel for num_threads(n_threads) schedule(static)
@@ -524,6 +582,8 @@ void ref_mul_mat(int wtype, const void * w, size_t row_bytes, int64_t m, int64_t
             float v;
             if (vtype == REF_Q8_0) {
                 v = ref_vec_dot_q8_0_q8_0(k, (const ref_block_q8_0 *) wr, (const ref_block_q8_0 *) xc);
+            } else if (wtype == REF_Q3_K) {
+                v = ref_vec_dot_q3_K_q8_K(k, (const ref_block_q3_K *) wr, (const ref_block_q8_K *) xc);
             } else if (vtype == REF_Q8_K) {
                 v = ref_vec_dot_q4_K_q8_K(k, (const ref_block_q4_K *) wr, (const ref_block_q8_K *) xc);
             } else if (vtype == REF_F16) {

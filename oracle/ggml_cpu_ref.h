@@ -48,13 +48,20 @@ typedef struct {
 } ref_block_q4_K; /* 144 bytes */
 
 typedef struct {
+    uint8_t hmask[REF_QK_K / 8]; /* third bit of each quant, clear = minus 4 */
+    uint8_t qs[REF_QK_K / 4];    /* two low bits of each quant */
+    uint8_t scales[12];          /* sixteen 6-bit scales, stored minus 32 */
+    uint16_t d;
+} ref_block_q3_K; /* 110 bytes */
+
+typedef struct {
     float d;
     int8_t qs[REF_QK_K];
     int16_t bsums[REF_QK_K / 16];
 } ref_block_q8_K; /* 292 bytes */
 
 /* element-type codes, as ggml numbers them */
-enum { REF_F32 = 0, REF_F16 = 1, REF_Q8_0 = 8, REF_Q4_K = 12, REF_Q8_K = 15 };
+enum { REF_F32 = 0, REF_F16 = 1, REF_Q8_0 = 8, REF_Q3_K = 11, REF_Q4_K = 12, REF_Q8_K = 15 };
 
 uint16_t ref_fp32_to_fp16(float f);
 float ref_fp16_to_fp32(uint16_t h);
@@ -70,11 +77,14 @@ void ref_quantize_row_q8_K(const float * x, ref_block_q8_K * y, int64_t k);
 
 void ref_dequantize_row_q8_0(const ref_block_q8_0 * x, float * y, int64_t k);
 void ref_dequantize_row_q4_K(const ref_block_q4_K * x, float * y, int64_t k);
+void ref_dequantize_row_q3_K(const ref_block_q3_K * x, float * y, int64_t k);
+int ref_q3_K_scale(const uint8_t * scales, int i);
 void ref_dequantize_row_q8_K(const ref_block_q8_K * x, float * y, int64_t k);
 void ref_get_scale_min_k4(int j, const uint8_t * q, uint8_t * d, uint8_t * m);
 
 float ref_vec_dot_q8_0_q8_0(int64_t n, const ref_block_q8_0 * x, const ref_block_q8_0 * y);
 float ref_vec_dot_q4_K_q8_K(int64_t n, const ref_block_q4_K * x, const ref_block_q8_K * y);
+float ref_vec_dot_q3_K_q8_K(int64_t n, const ref_block_q3_K * x, const ref_block_q8_K * y);
 float ref_vec_dot_f16(int64_t n, const uint16_t * x, const uint16_t * y);
 
 size_t ref_row_size(int type, int64_t ne0);

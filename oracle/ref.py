@@ -13,8 +13,8 @@ import numpy as np
 
 LIB_PATH = Path(__file__).resolve().parent / "build" / "libggml_cpu_ref.so"
 
-F32, F16, Q8_0, Q4_K, Q8_K = 0, 1, 8, 12, 15
-BLOCK = {Q8_0: (32, 34), Q4_K: (256, 144), Q8_K: (256, 292)}
+F32, F16, Q8_0, Q3_K, Q4_K, Q8_K = 0, 1, 8, 11, 12, 15
+BLOCK = {Q8_0: (32, 34), Q3_K: (256, 110), Q4_K: (256, 144), Q8_K: (256, 292)}
 
 _lib = None
 
@@ -37,10 +37,12 @@ def lib() -> C.CDLL:
     s("ref_fp16_to_fp32", f, C.c_uint16)
     for n in ("ref_quantize_row_q8_0_weights", "ref_quantize_row_q4_K", "ref_quantize_row_q8_0_act",
               "ref_quantize_row_q8_K", "ref_dequantize_row_q8_0", "ref_dequantize_row_q4_K",
-              "ref_dequantize_row_q8_K"):
+              "ref_dequantize_row_q8_K", "ref_dequantize_row_q3_K"):
         s(n, None, vp, vp, i64)
     s("ref_vec_dot_q8_0_q8_0", f, i64, vp, vp)
     s("ref_vec_dot_q4_K_q8_K", f, i64, vp, vp)
+    s("ref_vec_dot_q3_K_q8_K", f, i64, vp, vp)
+    s("ref_q3_K_scale", i, vp, i)
     s("ref_vec_dot_f16", f, i64, vp, vp)
     s("ref_row_size", C.c_size_t, i, i64)
     s("ref_mul_mat", None, i, vp, C.c_size_t, i64, i64, vp, i64, i64, vp, i64, i)
@@ -94,7 +96,7 @@ def quantize_act(typ: int, x: np.ndarray) -> np.ndarray:
 def dequantize(typ: int, q: np.ndarray, n: int) -> np.ndarray:
     out = np.zeros(n, dtype=np.float32)
     fn = {Q8_0: lib().ref_dequantize_row_q8_0, Q4_K: lib().ref_dequantize_row_q4_K,
-          Q8_K: lib().ref_dequantize_row_q8_K}[typ]
+          Q8_K: lib().ref_dequantize_row_q8_K, Q3_K: lib().ref_dequantize_row_q3_K}[typ]
     q = np.ascontiguousarray(q)
     fn(_p(q), _p(out), n)
     return out
@@ -106,7 +108,7 @@ def mul_mat(wtype: int, w: np.ndarray, m: int, k: int, x: np.ndarray, threads: i
     x = np.ascontiguousarray(x, dtype=np.float32)
     n = x.shape[0]
     dst = np.zeros((n, m), dtype=np.float32)
-    rb = row_size(wtype, k) if wtype in (Q8_0, Q4_K) else (2 * k if wtype == F16 else 4 * k)
+    rb = row_size(wtype, k) if wtype in (Q8_0, Q3_K, Q4_K) else (2 * k if wtype == F16 else 4 * k)
     lib().ref_mul_mat(wtype, _p(w), rb, m, k, _p(x), k, n, _p(dst), m, threads)
     return dst
 

@@ -82,6 +82,34 @@ def test_mul_mat_quantized(ggml, gpu, ref, wname, m, k, n):
     G.free()
 
 
+@pytest.mark.parametrize("m,k", [(64, 256), (1024, 1024), (3072, 1024), (1000, 3072)])
+@pytest.mark.parametrize("n", [1, 3, 8, 13])
+def test_mul_mat_q3_K(ggml, gpu, ref, m, k, n):
+    """MUL_MAT on Q3_K weights (the host's q3_k pack policy): the row-team
+    GEMV over Q8_K columns, bit for bit the oracle's; the blocks come from
+    random bytes with finite f16 scales (every such block is a valid Q3_K
+    block), since nothing here writes Q3_K weights"""
+    print(f"mul_mat q3_K M={m} K={k} N={n}", flush=True)
+    rng = np.random.default_rng(m + 7 * k + n)
+    nb = m * k // 256
+    wq = rng.integers(0, 256, (nb, 110), dtype=np.uint8)
+    wq[:, 108:110] = np.float16(rng.uniform(0.001, 0.01, nb)).view(np.uint8).reshape(nb, 2)
+    wq = wq.reshape(-1)
+    x = rng.standard_normal((n, k)).astype(np.float32)
+    G = ggml.Graph()
+    W = G.new(ggml.Q3_K, k, m, weight=True)
+    X = G.new(ggml.F32, k, n)
+    Y = G.lib.ggml_mul_mat(G.ctx, W, X)
+    run(ggml, gpu, G, Y)
+    G.set(W, wq)
+    G.set(X, x)
+    for _ in range(2):
+        assert G.compute(gpu.backend) == 0
+        y = G.get(Y).reshape(n, m)
+        assert_same_bits(y, ref.mul_mat(ref.Q3_K, wq, m, k, x))
+    G.free()
+
+
 NORM_MM_CASES = [
     # norm, weights, M, K, N
     ("rms", "q4_K", 4096, 1024, 8), ("rms", "q4_K", 4096, 2048, 8), ("rms", "q4_K", 1024, 1024, 13),

@@ -709,3 +709,81 @@ def test_gelu_erf_and_relu_closed_forms(ref):
         want = 0.5 * float(x) * (1.0 + math.erf(float(x) / math.sqrt(2.0)))
         assert abs(L.ref_gelu_erf(float(x)) - want) <= 2e-7 * max(1.0, abs(want))
         assert L.ref_relu(float(x)) == (float(x) if x > 0 else 0.0)
+
+
+def pack_q3_K(d16, scales, quants):
+    """a Q3_K super-block written from its published layout by an
+    independent packer: scales (16 values in -32..31) coded as 6-bit values
+    + 32 split into low nibbles (bytes 0..7) and high bit pairs (bytes
+    8..11), quants (256 values in -4..3) split into two low bits in qs and
+    the third bit in hmask (set for q >= 0)"""
+    c = [s + 32 for s in scales]
+    sb = bytearray(12)
+    for i in range(16):
+        sb[i % 8] |= (c[i] & 0xF) << (4 * (i // 8))
+        sb[8 + i % 4] |= (c[i] >> 4) << (2 * (i // 4))
+    hm, qs = bytearray(32), bytearray(64)
+    for e, q in enumerate(quants):
+        h, j, l = e // 128, (e % 128) // 32, e % 32
+        u = q + 4  # 0..7: bit 2 is the hmask bit, bits 0..1 go to qs
+        qs[32 * h + l] |= (u & 3) << (2 * j)
+        hm[l] |= (u >> 2) << (4 * h + j)
+    return bytes(hm) + bytes(qs) + bytes(sb) + np.uint16(d16).tobytes()
+
+
+def test_q3_K_dequant_known_answer(ref):
+    """the oracle's Q3_K decoding inverts the independent packer: every
+    scale index and quant position comes back (a transposed index, a wrong
+    bit of hmask or a dropped -32 / -4 offset fails)"""
+    rng = np.random.default_rng(3)
+    for trial in range(6):
+        scales = rng.integers(-32, 32, 16).tolist()
+        quants = rng.integers(-4, 4, 256).tolist()
+        if trial == 0:
+            scales, quants = list(range(-32, 32, 4)), [(e % 8) - 4 for e in range(256)]
+        d16 = int(np.float16(0.5 + trial).view(np.uint16))
+        blk = np.frombuffer(pack_q3_K(d16, scales, quants), dtype=np.uint8)
+        assert blk.size == 110
+        for i in range(16):
+            assert ref.lib().ref_q3_K_scale(ref._p(np.ascontiguousarray(blk[96:108])), i) == scales[i]
+        y = ref.dequantize(ref.Q3_K, blk, 256)
+        d = np.float32(np.float16(0.5 + trial))
+        want = np.array([np.float32(d * np.float32(scales[e // 16])) * np.float32(quants[e]) for e in range(256)],
+                        dtype=np.float32)
+        np.testing.assert_array_equal(y, want)
+
+
+def test_vec_dot_q3_K_equals_f64_dot_of_dequantized(ref):
+    """the Q3_K x Q8_K dot equals the f64 dot of the two dequantized rows
+    (the Q8_K side dequantizes through f32 products, hence the tolerance)"""
+    rng = np.random.default_rng(33)
+    k = 1024
+    blocks = b"".join(pack_q3_K(int(np.float16(rng.uniform(0.01, 0.1)).view(np.uint16)),
+                                rng.integers(-32, 32, 16).tolist(), rng.integers(-4, 4, 256).tolist())
+                      for _ in range(k // 256))
+    w = np.frombuffer(blocks, dtype=np.uint8).copy()
+    for t in range(4):
+        x = rng.standard_normal(k).astype(np.float32)
+        xq = ref.quantize_act(ref.Q8_K, x)
+        got = ref.lib().ref_vec_dot_q3_K_q8_K(k, ref._p(w), ref._p(xq))
+        wd = ref.dequantize(ref.Q3_K, w, k).astype(np.float64)
+        xd = ref.dequantize(ref.Q8_K, xq, k).astype(np.float64)
+        assert got == pytest.approx(np.dot(wd, xd), rel=2e-5, abs=2e-5)
+
+
+def test_mul_mat_q3_K_brute_force(ref):
+    """MUL_MAT on Q3_K weights: every column equals the per-row dot"""
+    rng = np.random.default_rng(34)
+    m, k, n = 5, 512, 3
+    w = np.frombuffer(b"".join(pack_q3_K(int(np.float16(rng.uniform(0.01, 0.1)).view(np.uint16)),
+                                         rng.integers(-32, 32, 16).tolist(), rng.integers(-4, 4, 256).tolist())
+                               for _ in range(m * k // 256)), dtype=np.uint8).copy()
+    x = rng.standard_normal((n, k)).astype(np.float32)
+    y = ref.mul_mat(ref.Q3_K, w, m, k, x)
+    rb = ref.row_size(ref.Q3_K, k)
+    assert rb == k // 256 * 110
+    for c in range(n):
+        xq = ref.quantize_act(ref.Q8_K, x[c])
+        for r in range(m):
+            wr = np.ascontiguousarray(w[r * rb:(r + 1) * rb])
+            assert y[c, r] == np.float32(ref.lib().ref_vec_dot_q3_K_q8_K(k, ref._p(wr), ref._p(xq)))
